@@ -1,0 +1,106 @@
+"""ctypes binding of the C ABI in include/cnhip.h (libcnhip.so).
+
+The library is loaded from cppnet_amd/_lib/.  There is no fallback: if the
+HIP library is missing, importing the op wrappers raises, so nothing can run
+silently on a CPU path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import re
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+LIBDIR = PKG / "_lib"
+HEADER = PKG.parent / "include" / "cnhip.h"
+
+i64 = C.c_int64
+f32 = C.c_float
+vp = C.c_void_p
+i32 = C.c_int
+
+# name -> (restype, argtypes)
+SIGNATURES: dict[str, tuple] = {
+    "cnhip_last_error": (C.c_char_p, []),
+    "cnhip_version": (C.c_char_p, []),
+    "cnhip_device_count": (i32, []),
+    "cnhip_set_device": (i32, [i32]),
+    "cnhip_malloc": (i32, [C.POINTER(vp), C.c_size_t]),
+    "cnhip_free": (i32, [vp]),
+    "cnhip_memcpy_async": (i32, [vp, vp, C.c_size_t, i32, vp]),
+    "cnhip_memset_async": (i32, [vp, i32, C.c_size_t, vp]),
+    "cnhip_stream_create": (i32, [C.POINTER(vp)]),
+    "cnhip_stream_destroy": (i32, [vp]),
+    "cnhip_stream_synchronize": (i32, [vp]),
+    "cnhip_device_synchronize": (i32, []),
+    "cnhip_event_create": (i32, [C.POINTER(vp)]),
+    "cnhip_event_destroy": (i32, [vp]),
+    "cnhip_event_record": (i32, [vp, vp]),
+    "cnhip_event_elapsed_ms": (i32, [C.POINTER(f32), vp, vp]),
+    "cnhip_gemm_f32": (i32, [i32, i32, i64, i64, i64, f32, vp, i64, vp, i64, f32, vp, i64, vp,
+                             i32, vp]),
+    "cnhip_linear_forward": (i32, [vp, vp, vp, vp, i64, i64, i64, vp]),
+    "cnhip_linear_backward": (i32, [vp, vp, vp, vp, vp, vp, i64, i64, i64, i32, i32, vp]),
+    "cnhip_column_sum": (i32, [vp, vp, i64, i64, i32, vp]),
+    "cnhip_relu_forward": (i32, [vp, vp, i64, vp]),
+    "cnhip_relu_backward": (i32, [vp, vp, vp, i64, vp]),
+    "cnhip_sigmoid_forward": (i32, [vp, vp, i64, vp]),
+    "cnhip_sigmoid_backward": (i32, [vp, vp, vp, i64, vp]),
+    "cnhip_tanh_forward": (i32, [vp, vp, i64, vp]),
+    "cnhip_tanh_backward": (i32, [vp, vp, vp, i64, vp]),
+    "cnhip_bce_forward": (i32, [vp, vp, vp, i64, i32, vp]),
+    "cnhip_bce_backward": (i32, [vp, vp, vp, i64, i32, vp]),
+    "cnhip_mse_forward": (i32, [vp, vp, vp, i64, i32, vp]),
+    "cnhip_mse_backward": (i32, [vp, vp, vp, i64, i32, vp]),
+    "cnhip_softmax_ce_forward": (i32, [vp, vp, vp, vp, i64, i64, i32, vp]),
+    "cnhip_softmax_ce_backward": (i32, [vp, vp, vp, i64, i64, i32, vp]),
+    "cnhip_adam_step": (i32, [vp, vp, vp, vp, i64, f32, f32, f32, f32, f32, f32, vp]),
+    "cnhip_adam_step_multi": (i32, [i32, C.POINTER(vp), C.POINTER(vp), C.POINTER(vp),
+                                    C.POINTER(vp), C.POINTER(i64), C.POINTER(f32),
+                                    C.POINTER(f32), f32, f32, f32, f32, vp]),
+}
+
+
+class CnhipError(RuntimeError):
+    """Non-zero status from the HIP library; the message is cnhip_last_error()."""
+
+
+_lib = None
+
+
+def header_symbols(header: Path = HEADER) -> list[str]:
+    """Function names declared in a C header (used by the export test)."""
+    text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(cn[a-z]*_[a-z0-9_]+)\s*\(", text)))
+
+
+def lib_path() -> Path:
+    return LIBDIR / "libcnhip.so"
+
+
+def load() -> C.CDLL:
+    """Load libcnhip.so (raises if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    path = lib_path()
+    if not path.exists():
+        raise ImportError(f"{path} is missing: run `python -m cppnet_amd.build` first "
+                          "(there is no CPU fallback)")
+    lib = C.CDLL(str(path), mode=C.RTLD_GLOBAL)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def check(status: int) -> None:
+    if status != 0:
+        msg = load().cnhip_last_error().decode(errors="replace")
+        raise CnhipError(f"cnhip status {status}: {msg}")
+
+
+def call(name: str, *args) -> None:
+    check(getattr(load(), name)(*args))

@@ -1,0 +1,65 @@
+// Shared helpers of the HIP library: status/error plumbing and launch checks.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "cnhip.h"
+
+namespace cnhip {
+
+// Records the message returned by cnhip_last_error() for this host thread.
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+
+inline hipStream_t as_stream(cnhip_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Checks the launch that was just enqueued.
+inline int check_launch(const char* where) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("%s: kernel launch failed: %s", where, hipGetErrorString(e));
+    return CNHIP_EHIP;
+  }
+  return CNHIP_OK;
+}
+
+inline int check_hip(hipError_t e, const char* where) {
+  if (e != hipSuccess) {
+    set_error("%s: %s", where, hipGetErrorString(e));
+    return e == hipErrorOutOfMemory ? CNHIP_ENOMEM : CNHIP_EHIP;
+  }
+  return CNHIP_OK;
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Grid size for a grid-stride elementwise kernel: enough waves to fill the
+// 256 CUs (8 XCDs x 32) several times over without launching one block per
+// element for very large n.
+inline unsigned elementwise_grid(int64_t work_items, int block) {
+  int64_t blocks = (work_items + block - 1) / block;
+  const int64_t cap = 256 * 32;  // 32 blocks per CU
+  if (blocks > cap) blocks = cap;
+  if (blocks < 1) blocks = 1;
+  return static_cast<unsigned>(blocks);
+}
+
+}  // namespace cnhip
+
+#define CNHIP_REQUIRE(cond, ...)           \
+  do {                                     \
+    if (!(cond)) {                         \
+      ::cnhip::set_error(__VA_ARGS__);     \
+      return CNHIP_EINVAL;                 \
+    }                                      \
+  } while (0)
+
+#define CNHIP_TRY(expr)               \
+  do {                                \
+    int _st = (expr);                 \
+    if (_st != CNHIP_OK) return _st;  \
+  } while (0)

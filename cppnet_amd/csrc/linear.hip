@@ -1,0 +1,106 @@
+// Linear layer entry points and the bias-gradient column reduction.
+//
+// ref: Linear::forward_gpu / backward_gpu, src/CppNet/layers/linear.cpp:456-539
+// and the cpu-eigen semantics they must match, linear.cpp:218-234, 335-358:
+//   Y  = X W + b
+//   dW += X^T dY      db += sum_batch dY      dX = dY W^T
+#include <hip/hip_runtime.h>
+
+#include "common.hpp"
+
+namespace cnhip {
+
+int gemm_f32(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float alpha,
+             const float* A, int64_t lda, const float* B, int64_t ldb, float beta, float* C,
+             int64_t ldc, const float* bias, int epilogue, hipStream_t st, const char* who);
+
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// One wavefront per column of a ColMajor [rows, cols] matrix; a column is
+// contiguous, so each lane streams float4s and the wave reduces with DPP/
+// shuffles.  The summation order is fixed, so results are deterministic.
+__global__ void __launch_bounds__(256) column_sum_kernel(const float* __restrict__ in,
+                                                         float* __restrict__ out, int64_t rows,
+                                                         int64_t cols, int accumulate, int vec) {
+  const int lane = threadIdx.x & 63;
+  const int64_t col = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (col >= cols) return;
+  const float* p = in + rows * col;
+  float s = 0.f;
+  if (vec) {
+    const int64_t n4 = rows >> 2;
+    for (int64_t i = lane; i < n4; i += 64) {
+      const f32x4 v = reinterpret_cast<const f32x4*>(p)[i];
+      s += (v[0] + v[1]) + (v[2] + v[3]);
+    }
+  } else {
+    for (int64_t i = lane; i < rows; i += 64) s += p[i];
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+  if (lane == 0) out[col] = accumulate ? out[col] + s : s;
+}
+
+}  // namespace
+
+int column_sum(const float* in, float* out, int64_t rows, int64_t cols, int accumulate,
+               hipStream_t st, const char* who) {
+  CNHIP_REQUIRE(rows >= 0 && cols >= 0, "%s: negative size", who);
+  if (cols == 0) return CNHIP_OK;
+  CNHIP_REQUIRE(out != nullptr, "%s: out is NULL", who);
+  CNHIP_REQUIRE(rows == 0 || in != nullptr, "%s: in is NULL", who);
+  const int vec = (rows % 4 == 0) && aligned16(in);
+  hipLaunchKernelGGL(column_sum_kernel, dim3((unsigned)((cols + 3) / 4)), dim3(256), 0, st, in, out,
+                     rows, cols, accumulate, vec);
+  return check_launch(who);
+}
+
+}  // namespace cnhip
+
+extern "C" {
+
+int cnhip_column_sum(const float* in, float* out, int64_t rows, int64_t cols, int accumulate,
+                     cnhip_stream_t stream) {
+  return cnhip::column_sum(in, out, rows, cols, accumulate, cnhip::as_stream(stream),
+                           "cnhip_column_sum");
+}
+
+int cnhip_linear_forward(const float* X, const float* W, const float* b, float* Y, int64_t batch,
+                         int64_t in_features, int64_t out_features, cnhip_stream_t stream) {
+  CNHIP_REQUIRE(batch >= 0 && in_features > 0 && out_features > 0,
+                "cnhip_linear_forward: bad shape batch=%lld in=%lld out=%lld", (long long)batch,
+                (long long)in_features, (long long)out_features);
+  // Y[B,O] = X[B,I] * W[I,O]  (+ b)
+  return cnhip::gemm_f32(0, 0, batch, out_features, in_features, 1.f, X, batch, W, in_features,
+                         0.f, Y, batch, b, CNHIP_EPI_NONE, cnhip::as_stream(stream),
+                         "cnhip_linear_forward");
+}
+
+int cnhip_linear_backward(const float* X, const float* W, const float* dY, float* grad_W,
+                          float* grad_b, float* dX, int64_t batch, int64_t in_features,
+                          int64_t out_features, int trainable, int accumulate,
+                          cnhip_stream_t stream) {
+  const char* who = "cnhip_linear_backward";
+  CNHIP_REQUIRE(batch >= 0 && in_features > 0 && out_features > 0,
+                "%s: bad shape batch=%lld in=%lld out=%lld", who, (long long)batch,
+                (long long)in_features, (long long)out_features);
+  hipStream_t st = cnhip::as_stream(stream);
+  const float beta = accumulate ? 1.f : 0.f;
+  if (trainable) {
+    CNHIP_REQUIRE(grad_W != nullptr, "%s: trainable layer needs grad_W", who);
+    // dW[I,O] (+)= X^T[I,B] * dY[B,O]
+    CNHIP_TRY(cnhip::gemm_f32(1, 0, in_features, out_features, batch, 1.f, X, batch, dY, batch,
+                              beta, grad_W, in_features, nullptr, CNHIP_EPI_NONE, st, who));
+    if (grad_b) CNHIP_TRY(cnhip::column_sum(dY, grad_b, batch, out_features, accumulate, st, who));
+  }
+  if (dX) {
+    // dX[B,I] = dY[B,O] * W^T[O,I]
+    CNHIP_TRY(cnhip::gemm_f32(0, 1, batch, in_features, out_features, 1.f, dY, batch, W,
+                              in_features, 0.f, dX, batch, nullptr, CNHIP_EPI_NONE, st, who));
+  }
+  return CNHIP_OK;
+}
+
+}  // extern "C"

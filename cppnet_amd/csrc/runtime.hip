@@ -1,0 +1,124 @@
+// Runtime services of the C ABI: errors, devices, memory, streams, events.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+
+#include "common.hpp"
+
+namespace cnhip {
+
+static thread_local char g_last_error[1024] = "";
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+}
+
+}  // namespace cnhip
+
+using cnhip::as_stream;
+using cnhip::check_hip;
+
+extern "C" {
+
+const char* cnhip_last_error(void) { return cnhip::g_last_error; }
+
+const char* cnhip_version(void) { return "cnhip 0.1 gfx950"; }
+
+int cnhip_device_count(void) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  return n;
+}
+
+int cnhip_set_device(int device) { return check_hip(hipSetDevice(device), "cnhip_set_device"); }
+
+int cnhip_malloc(void** ptr, size_t bytes) {
+  CNHIP_REQUIRE(ptr != nullptr, "cnhip_malloc: ptr is NULL");
+  *ptr = nullptr;
+  if (bytes == 0) return CNHIP_OK;
+  return check_hip(hipMalloc(ptr, bytes), "cnhip_malloc");
+}
+
+int cnhip_free(void* ptr) {
+  if (ptr == nullptr) return CNHIP_OK;
+  return check_hip(hipFree(ptr), "cnhip_free");
+}
+
+int cnhip_memcpy_async(void* dst, const void* src, size_t bytes, int kind,
+                       cnhip_stream_t stream) {
+  if (bytes == 0) return CNHIP_OK;
+  CNHIP_REQUIRE(dst && src, "cnhip_memcpy_async: NULL pointer");
+  hipMemcpyKind k;
+  switch (kind) {
+    case 0: k = hipMemcpyHostToDevice; break;
+    case 1: k = hipMemcpyDeviceToHost; break;
+    case 2: k = hipMemcpyDeviceToDevice; break;
+    default: cnhip::set_error("cnhip_memcpy_async: bad kind %d", kind); return CNHIP_EINVAL;
+  }
+  return check_hip(hipMemcpyAsync(dst, src, bytes, k, as_stream(stream)), "cnhip_memcpy_async");
+}
+
+int cnhip_memset_async(void* dst, int value, size_t bytes, cnhip_stream_t stream) {
+  if (bytes == 0) return CNHIP_OK;
+  CNHIP_REQUIRE(dst, "cnhip_memset_async: NULL pointer");
+  return check_hip(hipMemsetAsync(dst, value, bytes, as_stream(stream)), "cnhip_memset_async");
+}
+
+int cnhip_stream_create(cnhip_stream_t* stream) {
+  CNHIP_REQUIRE(stream, "cnhip_stream_create: NULL out pointer");
+  hipStream_t s = nullptr;
+  // Default priority only: streams of mixed priorities are not used here.
+  int st = check_hip(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "cnhip_stream_create");
+  *stream = reinterpret_cast<cnhip_stream_t>(s);
+  return st;
+}
+
+int cnhip_stream_destroy(cnhip_stream_t stream) {
+  if (!stream) return CNHIP_OK;
+  return check_hip(hipStreamDestroy(as_stream(stream)), "cnhip_stream_destroy");
+}
+
+int cnhip_stream_synchronize(cnhip_stream_t stream) {
+  return check_hip(hipStreamSynchronize(as_stream(stream)), "cnhip_stream_synchronize");
+}
+
+int cnhip_device_synchronize(void) {
+  return check_hip(hipDeviceSynchronize(), "cnhip_device_synchronize");
+}
+
+int cnhip_event_create(void** event) {
+  CNHIP_REQUIRE(event, "cnhip_event_create: NULL out pointer");
+  hipEvent_t e = nullptr;
+  int st = check_hip(hipEventCreate(&e), "cnhip_event_create");
+  *event = reinterpret_cast<void*>(e);
+  return st;
+}
+
+int cnhip_event_destroy(void* event) {
+  if (!event) return CNHIP_OK;
+  return check_hip(hipEventDestroy(reinterpret_cast<hipEvent_t>(event)), "cnhip_event_destroy");
+}
+
+int cnhip_event_record(void* event, cnhip_stream_t stream) {
+  CNHIP_REQUIRE(event, "cnhip_event_record: NULL event");
+  return check_hip(hipEventRecord(reinterpret_cast<hipEvent_t>(event), as_stream(stream)),
+                   "cnhip_event_record");
+}
+
+int cnhip_event_elapsed_ms(float* ms, void* start, void* stop) {
+  CNHIP_REQUIRE(ms && start && stop, "cnhip_event_elapsed_ms: NULL argument");
+  CNHIP_TRY(check_hip(hipEventSynchronize(reinterpret_cast<hipEvent_t>(stop)),
+                      "cnhip_event_elapsed_ms"));
+  return check_hip(hipEventElapsedTime(ms, reinterpret_cast<hipEvent_t>(start),
+                                       reinterpret_cast<hipEvent_t>(stop)),
+                   "cnhip_event_elapsed_ms");
+}
+
+}  // extern "C"

@@ -1,0 +1,132 @@
+"""Thin torch-tensor front end to the C ABI (include/cnhip.h).
+
+Tensors are device tensors holding Eigen ColMajor data: a CppNet
+``[rows, cols]`` matrix is a flat (or any contiguous) float32 tensor of
+rows*cols values with the row index fastest.  torch is used only for device
+memory and the current stream; every computation is a HIP kernel of
+libcnhip.so.  Entry points raise CnhipError (with cnhip_last_error()) on a
+non-zero status and refuse host tensors.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _capi
+
+MEAN, SUM = 0, 1
+_REDUCTIONS = {"mean": MEAN, "sum": SUM}
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _p(t: torch.Tensor | None, name: str = "tensor") -> int | None:
+    if t is None:
+        return None
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise TypeError(f"{name}: expected a device tensor (the HIP path has no host fallback)")
+    if t.dtype not in (torch.float32, torch.int32):
+        raise TypeError(f"{name}: expected float32/int32, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name}: expected a contiguous tensor")
+    return t.data_ptr()
+
+
+def _red(reduction: str | int) -> int:
+    if isinstance(reduction, int):
+        return reduction
+    if reduction not in _REDUCTIONS:
+        raise ValueError(f'reduction must be "mean" or "sum", got {reduction!r}')
+    return _REDUCTIONS[reduction]
+
+
+def gemm(trans_a: bool, trans_b: bool, M: int, N: int, K: int, A, lda: int, B, ldb: int, C,
+         ldc: int, alpha: float = 1.0, beta: float = 0.0, bias=None, relu: bool = False) -> None:
+    _capi.call("cnhip_gemm_f32", int(trans_a), int(trans_b), M, N, K, alpha, _p(A, "A"), lda,
+               _p(B, "B"), ldb, beta, _p(C, "C"), ldc, _p(bias, "bias"), 1 if relu else 0,
+               _stream())
+
+
+def linear_forward(X, W, b, Y, batch: int, in_features: int, out_features: int) -> None:
+    _capi.call("cnhip_linear_forward", _p(X, "X"), _p(W, "W"), _p(b, "b"), _p(Y, "Y"), batch,
+               in_features, out_features, _stream())
+
+
+def linear_backward(X, W, dY, grad_W, grad_b, dX, batch: int, in_features: int,
+                    out_features: int, trainable: bool = True, accumulate: bool = True) -> None:
+    _capi.call("cnhip_linear_backward", _p(X, "X"), _p(W, "W"), _p(dY, "dY"),
+               _p(grad_W, "grad_W"), _p(grad_b, "grad_b"), _p(dX, "dX"), batch, in_features,
+               out_features, int(trainable), int(accumulate), _stream())
+
+
+def column_sum(x, out, rows: int, cols: int, accumulate: bool = False) -> None:
+    _capi.call("cnhip_column_sum", _p(x), _p(out), rows, cols, int(accumulate), _stream())
+
+
+def _unary(name: str, x, y) -> None:
+    _capi.call(name, _p(x, "x"), _p(y, "y"), x.numel(), _stream())
+
+
+def _binary(name: str, y, dy, dx) -> None:
+    if not (y.numel() == dy.numel() == dx.numel()):
+        raise ValueError(f"{name}: size mismatch")
+    _capi.call(name, _p(y, "y"), _p(dy, "dy"), _p(dx, "dx"), y.numel(), _stream())
+
+
+def relu_forward(x, y): _unary("cnhip_relu_forward", x, y)
+def relu_backward(y, dy, dx): _binary("cnhip_relu_backward", y, dy, dx)
+def sigmoid_forward(x, y): _unary("cnhip_sigmoid_forward", x, y)
+def sigmoid_backward(y, dy, dx): _binary("cnhip_sigmoid_backward", y, dy, dx)
+def tanh_forward(x, y): _unary("cnhip_tanh_forward", x, y)
+def tanh_backward(y, dy, dx): _binary("cnhip_tanh_backward", y, dy, dx)
+
+
+def bce_forward(pred, target, loss, reduction="mean") -> None:
+    _capi.call("cnhip_bce_forward", _p(pred), _p(target), _p(loss), pred.numel(),
+               _red(reduction), _stream())
+
+
+def bce_backward(pred, target, grad, reduction="mean") -> None:
+    _capi.call("cnhip_bce_backward", _p(pred), _p(target), _p(grad), pred.numel(),
+               _red(reduction), _stream())
+
+
+def mse_forward(pred, target, loss, reduction="mean") -> None:
+    _capi.call("cnhip_mse_forward", _p(pred), _p(target), _p(loss), pred.numel(),
+               _red(reduction), _stream())
+
+
+def mse_backward(pred, target, grad, reduction="mean") -> None:
+    _capi.call("cnhip_mse_backward", _p(pred), _p(target), _p(grad), pred.numel(),
+               _red(reduction), _stream())
+
+
+def softmax_ce_forward(logits, targets, softmax_out, loss, batch: int, classes: int,
+                       reduction="mean") -> None:
+    _capi.call("cnhip_softmax_ce_forward", _p(logits), _p(targets), _p(softmax_out), _p(loss),
+               batch, classes, _red(reduction), _stream())
+
+
+def softmax_ce_backward(softmax, targets, grad, batch: int, classes: int,
+                        reduction="mean") -> None:
+    _capi.call("cnhip_softmax_ce_backward", _p(softmax), _p(targets), _p(grad), batch, classes,
+               _red(reduction), _stream())
+
+
+def adam_step(W, g, m, v, lr: float, beta1: float, beta2: float, eps: float, bc1: float,
+              bc2: float) -> None:
+    _capi.call("cnhip_adam_step", _p(W), _p(g), _p(m), _p(v), W.numel(), lr, beta1, beta2, eps,
+               bc1, bc2, _stream())
+
+
+def adam_step_multi(params: list, lr: float, beta1: float, beta2: float, eps: float) -> None:
+    """params: list of (W, g, m, v, bc1, bc2) device-tensor tuples."""
+    import ctypes as C
+    n = len(params)
+    arr = lambda idx: (C.c_void_p * n)(*[_p(p[idx]) for p in params])
+    sizes = (C.c_int64 * n)(*[p[0].numel() for p in params])
+    bc1 = (C.c_float * n)(*[p[4] for p in params])
+    bc2 = (C.c_float * n)(*[p[5] for p in params])
+    _capi.call("cnhip_adam_step_multi", n, arr(0), arr(1), arr(2), arr(3), sizes, bc1, bc2, lr,
+               beta1, beta2, eps, _stream())

@@ -1,0 +1,172 @@
+/*
+ * cnhip.h — C ABI of the MI355X (gfx950) training backend for CppNet.
+ *
+ * Every entry point takes device pointers, element counts / shapes and a
+ * stream handle (NULL = the default stream), enqueues its kernels and returns
+ * a status code.  Nothing here synchronises the device unless the comment
+ * says so.  On a non-zero status, cnhip_last_error() returns a message that
+ * names the entry point and the failed condition.
+ *
+ * Layout: every tensor is Eigen ColMajor, exactly as the reference stores it
+ * (first index fastest):
+ *   2-D [R,C]        (r,c)     -> r + R*c
+ *   3-D [B,S,D]      (b,s,d)   -> b + B*(s + S*d)
+ *   4-D [N,C,H,W]    (n,c,h,w) -> n + N*(c + C*(h + H*w))
+ * so a [batch, features] matrix is batch-contiguous.
+ *
+ * Citations "ref: file:line" name the reference function (under
+ * LoqmanSamani/CppNet) whose "gpu" branch the entry point replaces.
+ */
+#ifndef CNHIP_H
+#define CNHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* cnhip_stream_t; /* a hipStream_t; NULL = default stream */
+
+/* ---- status codes ------------------------------------------------------ */
+#define CNHIP_OK              0
+#define CNHIP_EINVAL          1  /* bad argument (shape, null pointer, enum) */
+#define CNHIP_EHIP            2  /* HIP runtime error (launch, copy, device) */
+#define CNHIP_ENOMEM          3  /* device allocation failed */
+#define CNHIP_EUNSUPPORTED    4  /* valid but not supported here */
+
+/* ---- runtime ----------------------------------------------------------- */
+/* Message for the last non-zero status returned on this host thread. */
+const char* cnhip_last_error(void);
+/* Library version string, e.g. "cnhip 0.1 gfx950". */
+const char* cnhip_version(void);
+/* Number of visible HIP devices (0 when none); never fails. */
+int cnhip_device_count(void);
+/* Select the current device for this host thread. */
+int cnhip_set_device(int device);
+/* hipMalloc / hipFree / copies / fill; the runtime services the C++ host
+ * layer uses (ref: the cudaMalloc/cudaMemcpy calls spread through every
+ * "gpu" branch, e.g. src/CppNet/layers/linear.cpp:420-454). */
+int cnhip_malloc(void** ptr, size_t bytes);
+int cnhip_free(void* ptr);
+/* kind: 0 host->device, 1 device->host, 2 device->device */
+int cnhip_memcpy_async(void* dst, const void* src, size_t bytes, int kind,
+                       cnhip_stream_t stream);
+int cnhip_memset_async(void* dst, int value, size_t bytes, cnhip_stream_t stream);
+int cnhip_stream_create(cnhip_stream_t* stream);
+int cnhip_stream_destroy(cnhip_stream_t stream);
+int cnhip_stream_synchronize(cnhip_stream_t stream);
+int cnhip_device_synchronize(void);
+/* Events for timing on the stream the kernels run on. */
+int cnhip_event_create(void** event);
+int cnhip_event_destroy(void* event);
+int cnhip_event_record(void* event, cnhip_stream_t stream);
+int cnhip_event_elapsed_ms(float* ms, void* start, void* stop); /* syncs stop */
+
+/* ---- GEMM ---------------------------------------------------------------
+ * ColMajor  C[M,N] = alpha * op(A)[M,K] * op(B)[K,N] + beta * C  (+ bias[n])
+ *   trans_a == 0: A(m,k) = A[m + lda*k];  trans_a == 1: A(m,k) = A[k + lda*m]
+ *   trans_b == 0: B(k,n) = B[k + ldb*n];  trans_b == 1: B(k,n) = B[n + ldb*k]
+ * beta == 0 never reads C.  bias may be NULL.  epilogue: 0 none, 1 ReLU
+ * applied after bias.  fp32 in, fp32 MFMA (v_mfma_f32_32x32x2f32), fp32 out.
+ * ref: src/CppNet/kernels/gpu/matmul.cu:16-71 (NN), matmul_grad_input.cu:14-68
+ * (NT), matmul_grad_weight.cu:14-69 (TN), add_bias.cu:13-22 (bias epilogue). */
+#define CNHIP_EPI_NONE 0
+#define CNHIP_EPI_RELU 1
+int cnhip_gemm_f32(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K,
+                   float alpha, const float* A, int64_t lda,
+                   const float* B, int64_t ldb, float beta,
+                   float* C, int64_t ldc, const float* bias, int epilogue,
+                   cnhip_stream_t stream);
+
+/* ---- Linear ------------------------------------------------------------ */
+/* Y[B,O] = X[B,I] * W[I,O] + b[O]   (b may be NULL)
+ * ref: Linear::forward_gpu, src/CppNet/layers/linear.cpp:456-500 */
+int cnhip_linear_forward(const float* X, const float* W, const float* b,
+                         float* Y, int64_t batch, int64_t in_features,
+                         int64_t out_features, cnhip_stream_t stream);
+/* grad_W[I,O] += X^T dY ; grad_b[O] += colsum(dY)   (when trainable; grad_b
+ * skipped when NULL) ; dX[B,I] = dY W^T (skipped when dX is NULL).
+ * accumulate: 1 adds into grad_W/grad_b (the cpu-eigen semantics,
+ * linear.cpp:346-352), 0 overwrites them.
+ * ref: Linear::backward_gpu, src/CppNet/layers/linear.cpp:502-539 and
+ * Linear::backward_eigen, linear.cpp:335-358 */
+int cnhip_linear_backward(const float* X, const float* W, const float* dY,
+                          float* grad_W, float* grad_b, float* dX,
+                          int64_t batch, int64_t in_features,
+                          int64_t out_features, int trainable, int accumulate,
+                          cnhip_stream_t stream);
+/* out[j] (+)= sum_r in[r + rows*j]   — column sums of a ColMajor [rows,cols]
+ * ref: src/CppNet/kernels/gpu/bias_grad.cu:12-46 */
+int cnhip_column_sum(const float* in, float* out, int64_t rows, int64_t cols,
+                     int accumulate, cnhip_stream_t stream);
+
+/* ---- activations (elementwise over n values) -------------------------- */
+/* ReLU: y = max(x,0); dx = dy * (y > 0)   (mask from the cached OUTPUT)
+ * ref: relu.cu:14-23, relu_grad.cu:11-19; ReLU::forward/backward
+ * src/CppNet/activations/relu.cpp:97-225 */
+int cnhip_relu_forward(const float* x, float* y, int64_t n, cnhip_stream_t stream);
+int cnhip_relu_backward(const float* y, const float* dy, float* dx, int64_t n,
+                        cnhip_stream_t stream);
+/* Sigmoid: y = 1/(1+exp(-clamp(x,-500,500))); dx = dy*y*(1-y)
+ * ref: sigmoid.cu:13-23, sigmoid_grad.cu:11-20; sigmoid.cpp:97-231 */
+int cnhip_sigmoid_forward(const float* x, float* y, int64_t n, cnhip_stream_t stream);
+int cnhip_sigmoid_backward(const float* y, const float* dy, float* dx, int64_t n,
+                           cnhip_stream_t stream);
+/* Tanh: y = tanh(x); dx = dy*(1-y^2)
+ * ref: tanh_activation.cu:13-21, tanh_activation_grad.cu:11-20; tanh.cpp:136-219 */
+int cnhip_tanh_forward(const float* x, float* y, int64_t n, cnhip_stream_t stream);
+int cnhip_tanh_backward(const float* y, const float* dy, float* dx, int64_t n,
+                        cnhip_stream_t stream);
+
+/* ---- losses ------------------------------------------------------------
+ * reduction: 0 "mean", 1 "sum".  loss points to ONE device float.      */
+#define CNHIP_REDUCE_MEAN 0
+#define CNHIP_REDUCE_SUM  1
+/* BinaryCrossEntropy on n = rows*cols values; p clipped to [1e-7, 1-1e-7].
+ * grad = (p-t)/(p(1-p)) [/n for mean]
+ * ref: BinaryCrossEntropy::forward/backward binary_cross_entropy.cpp:143-225 */
+int cnhip_bce_forward(const float* pred, const float* target, float* loss,
+                      int64_t n, int reduction, cnhip_stream_t stream);
+int cnhip_bce_backward(const float* pred, const float* target, float* grad,
+                       int64_t n, int reduction, cnhip_stream_t stream);
+/* MSE: loss = sum (p-t)^2 [/n]; grad = 2(p-t) [/n]
+ * ref: MSE::forward/backward src/CppNet/losses/mse.cpp:102-161 */
+int cnhip_mse_forward(const float* pred, const float* target, float* loss,
+                      int64_t n, int reduction, cnhip_stream_t stream);
+int cnhip_mse_backward(const float* pred, const float* target, float* grad,
+                       int64_t n, int reduction, cnhip_stream_t stream);
+/* SoftmaxCrossEntropy over ColMajor logits/targets [batch, classes].
+ * forward writes the row softmax into softmax_out (the reference's
+ * softmax_cache_) and the loss; backward: grad = (softmax - t) [/batch].
+ * ref: SoftmaxCrossEntropy::forward/backward softmax_cross_entropy.cpp:118-195 */
+int cnhip_softmax_ce_forward(const float* logits, const float* targets,
+                             float* softmax_out, float* loss, int64_t batch,
+                             int64_t classes, int reduction, cnhip_stream_t stream);
+int cnhip_softmax_ce_backward(const float* softmax, const float* targets,
+                              float* grad, int64_t batch, int64_t classes,
+                              int reduction, cnhip_stream_t stream);
+
+/* ---- optimizer ---------------------------------------------------------
+ * Adam, one tensor: m = b1 m + (1-b1) g ; v = b2 v + (1-b2) g^2 ;
+ * W -= lr * (m/bc1) / (sqrt(v/bc2) + eps), bc1/bc2 = 1 - beta^t computed by
+ * the caller in float (adam.cpp:121-122).
+ * ref: adam_step.cu:10-25; Adam::update src/CppNet/optimizers/adam.cpp:98-133 */
+int cnhip_adam_step(float* W, const float* g, float* m, float* v, int64_t n,
+                    float lr, float beta1, float beta2, float eps,
+                    float bc1, float bc2, cnhip_stream_t stream);
+/* The same update over several tensors in ONE launch; tensor i is
+ * (W[i], g[i], m[i], v[i], n[i]) with its own bias corrections bc1[i],
+ * bc2[i] (the per-key t of the reference).  Host arrays of length count
+ * (count <= 64).  ref: as cnhip_adam_step, applied per Layer::step call. */
+int cnhip_adam_step_multi(int count, float* const* W, const float* const* g,
+                          float* const* m, float* const* v, const int64_t* n,
+                          const float* bc1, const float* bc2, float lr,
+                          float beta1, float beta2, float eps,
+                          cnhip_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* CNHIP_H */

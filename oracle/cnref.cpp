@@ -1,0 +1,214 @@
+// CPU oracle for the CppNet "cpu-eigen" semantics — TEST INFRASTRUCTURE ONLY
+// (loaded by tests/, smoke() and bench.py's cpu_baseline leg; never by the
+// product).  See cnref.h for conventions.  Reference paths are relative to
+// the LoqmanSamani/CppNet tree.
+#include "cnref.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+namespace {
+int g_threads = 1;
+}
+
+extern "C" {
+
+void cnref_set_threads(int n) { g_threads = n < 1 ? 1 : n; }
+int cnref_get_threads(void) { return g_threads; }
+
+// ---------------------------------------------------------------------------
+// GEMM.  op(A) is first materialised M-contiguous and op(B) K-contiguous;
+// each column n of the product is then accumulated as a sequence of axpys in
+// ascending k, so element (m,n) is the fp32 sum  ((0 + a0 b0) + a1 b1) + ...
+// This is the contraction Eigen performs for X.contract(W) in
+// Linear::forward_eigen (linear.cpp:224) and backward_eigen (346-357), up to
+// Eigen's blocking of the k loop.
+void cnref_gemm_f32(int ta, int tb, int64_t M, int64_t N, int64_t K, float alpha, const float* A,
+                    int64_t lda, const float* B, int64_t ldb, float beta, float* C, int64_t ldc,
+                    const float* bias, int epi) {
+  if (M <= 0 || N <= 0) return;
+  std::vector<float> Am((size_t)M * (size_t)std::max<int64_t>(K, 1));
+  std::vector<float> Bk((size_t)std::max<int64_t>(K, 1) * (size_t)N);
+  for (int64_t k = 0; k < K; ++k)
+    for (int64_t m = 0; m < M; ++m) Am[m + M * k] = ta ? A[k + lda * m] : A[m + lda * k];
+  for (int64_t n = 0; n < N; ++n)
+    for (int64_t k = 0; k < K; ++k) Bk[k + K * n] = tb ? B[n + ldb * k] : B[k + ldb * n];
+
+  const int64_t KB = 128;  // k-panel kept in cache; order within a column is unchanged
+  std::vector<float> acc((size_t)M * (size_t)N, 0.f);
+  for (int64_t k0 = 0; k0 < K; k0 += KB) {
+    const int64_t k1 = std::min(K, k0 + KB);
+#pragma omp parallel for num_threads(g_threads) schedule(static)
+    for (int64_t n = 0; n < N; ++n) {
+      float* c = acc.data() + M * n;
+      for (int64_t k = k0; k < k1; ++k) {
+        const float b = Bk[k + K * n];
+        const float* a = Am.data() + M * k;
+        for (int64_t m = 0; m < M; ++m) c[m] += a[m] * b;
+      }
+    }
+  }
+  for (int64_t n = 0; n < N; ++n)
+    for (int64_t m = 0; m < M; ++m) {
+      float v = alpha * acc[m + M * n];
+      if (beta != 0.f) v += beta * C[m + ldc * n];
+      if (bias) v += bias[n];
+      if (epi == 1) v = std::max(v, 0.f);
+      C[m + ldc * n] = v;
+    }
+}
+
+// Linear::forward_eigen (linear.cpp:218-234): output = X.contract(W) then
+// + bias broadcast along the batch.
+void cnref_linear_forward(const float* X, const float* W, const float* b, float* Y, int64_t B,
+                          int64_t I, int64_t O) {
+  cnref_gemm_f32(0, 0, B, O, I, 1.f, X, B, W, I, 0.f, Y, B, b, 0);
+}
+
+// Sum over the batch (rows) of a ColMajor [rows, cols] matrix; the
+// grad_biases_ += grad_output.sum({0}) of linear.cpp:350-352.
+void cnref_column_sum(const float* in, float* out, int64_t rows, int64_t cols, int accumulate) {
+  for (int64_t c = 0; c < cols; ++c) {
+    float s = 0.f;
+    for (int64_t r = 0; r < rows; ++r) s += in[r + rows * c];
+    out[c] = accumulate ? out[c] + s : s;
+  }
+}
+
+// Linear::backward_eigen (linear.cpp:335-358):
+//   if trainable: grad_W += X^T dY ; grad_b += sum_batch dY
+//   grad_input = dY W^T   (always, linear.cpp:357)
+// accumulate=0 overwrites grad_W / grad_b instead (used for the other layers'
+// zero-then-compute convention and for isolated op tests).
+void cnref_linear_backward(const float* X, const float* W, const float* dY, float* gW, float* gb,
+                           float* dX, int64_t B, int64_t I, int64_t O, int trainable,
+                           int accumulate) {
+  if (trainable) {
+    cnref_gemm_f32(1, 0, I, O, B, 1.f, X, B, dY, B, accumulate ? 1.f : 0.f, gW, I, nullptr, 0);
+    if (gb) cnref_column_sum(dY, gb, B, O, accumulate);
+  }
+  if (dX) cnref_gemm_f32(0, 1, B, I, O, 1.f, dY, B, W, I, 0.f, dX, B, nullptr, 0);
+}
+
+// ReLU::forward cpu-eigen: cwiseMax(0) (relu.cpp:116-119)
+void cnref_relu_forward(const float* x, float* y, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) y[i] = std::max(x[i], 0.0f);
+}
+// ReLU::backward cpu-eigen: grad * select(out > 0, 1, 0) (relu.cpp:176-182)
+void cnref_relu_backward(const float* y, const float* dy, float* dx, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) dx[i] = dy[i] * (y[i] > 0.0f ? 1.0f : 0.0f);
+}
+// Sigmoid::forward cpu-eigen (sigmoid.cpp:123-128)
+void cnref_sigmoid_forward(const float* x, float* y, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) {
+    const float c = std::max(-500.0f, std::min(500.0f, x[i]));
+    y[i] = 1.0f / (1.0f + std::exp(-c));
+  }
+}
+// Sigmoid::backward cpu-eigen: grad * (s * (1 - s)) (sigmoid.cpp:190-194)
+void cnref_sigmoid_backward(const float* y, const float* dy, float* dx, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) dx[i] = dy[i] * (y[i] * (1.0f - y[i]));
+}
+// Tanh::forward (tanh.cpp:100-134, cpu-eigen: .tanh())
+void cnref_tanh_forward(const float* x, float* y, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) y[i] = std::tanh(x[i]);
+}
+// Tanh::backward cpu-eigen: grad * (1 - t*t) (tanh.cpp:151-155)
+void cnref_tanh_backward(const float* y, const float* dy, float* dx, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) dx[i] = dy[i] * (1.0f - y[i] * y[i]);
+}
+
+// BinaryCrossEntropy::forward (binary_cross_entropy.cpp:143-184).  Targets
+// are validated to {0,1} by the caller side (validate_inputs, 101-131).
+float cnref_bce_forward(const float* p, const float* t, int64_t n, int reduction) {
+  float total = 0.0f;
+  for (int64_t i = 0; i < n; ++i) {
+    const float pc = std::max(1e-7f, std::min(p[i], 1.0f - 1e-7f));
+    const float tv = t[i];
+    total += -(tv * std::log(pc) + (1.0f - tv) * std::log(1.0f - pc));
+  }
+  return reduction == 1 ? total : total / (float)n;
+}
+// BinaryCrossEntropy::backward (binary_cross_entropy.cpp:186-225): the
+// denominator p*(1.0-p) is evaluated in double (the literal 1.0), the
+// quotient narrowed to float, then divided by n in float for "mean".
+void cnref_bce_backward(const float* p, const float* t, float* g, int64_t n, int reduction) {
+  for (int64_t i = 0; i < n; ++i) {
+    const float pc = std::max(1e-7f, std::min(p[i], 1.0f - 1e-7f));
+    float gv = (pc - t[i]) / (pc * (1.0 - pc));
+    if (reduction == 0) gv /= (float)n;
+    g[i] = gv;
+  }
+}
+// MSE::forward (mse.cpp:102-130)
+float cnref_mse_forward(const float* p, const float* t, int64_t n, int reduction) {
+  float s = 0.0f;
+  for (int64_t i = 0; i < n; ++i) {
+    const float d = p[i] - t[i];
+    s += d * d;
+  }
+  return reduction == 0 ? s / (float)n : s;
+}
+// MSE::backward (mse.cpp:132-161): scale = 2/n for mean
+void cnref_mse_backward(const float* p, const float* t, float* g, int64_t n, int reduction) {
+  const float scale = reduction == 0 ? 2.0f / (float)n : 2.0f;
+  for (int64_t i = 0; i < n; ++i) g[i] = scale * (p[i] - t[i]);
+}
+// SoftmaxCrossEntropy::forward (softmax_cross_entropy.cpp:118-157), ColMajor
+// [B, C].  The cached softmax is exp(z - max) / sum_exp; the loss uses
+// log(sum_exp + 1e-12) and is divided by the batch size for "mean".
+float cnref_softmax_ce_forward(const float* z, const float* t, float* sm, int64_t B, int64_t C,
+                               int reduction) {
+  float total = 0.0f;
+  for (int64_t b = 0; b < B; ++b) {
+    float mx = z[b];
+    for (int64_t c = 1; c < C; ++c) mx = std::max(mx, z[b + B * c]);
+    float se = 0.0f;
+    for (int64_t c = 0; c < C; ++c) {
+      sm[b + B * c] = std::exp(z[b + B * c] - mx);
+      se += sm[b + B * c];
+    }
+    const float ls = std::log(se + 1e-12f);
+    for (int64_t c = 0; c < C; ++c) {
+      sm[b + B * c] /= se;
+      total -= t[b + B * c] * ((z[b + B * c] - mx) - ls);
+    }
+  }
+  return reduction == 0 ? total / (float)B : total;
+}
+// SoftmaxCrossEntropy::backward (softmax_cross_entropy.cpp:159-195):
+// (softmax - t) * (1/B) for mean.
+void cnref_softmax_ce_backward(const float* sm, const float* t, float* g, int64_t B, int64_t C,
+                               int reduction) {
+  const float inv = 1.0f / (float)B;
+  for (int64_t i = 0; i < B * C; ++i) {
+    float v = sm[i] - t[i];
+    if (reduction == 0) v *= inv;
+    g[i] = v;
+  }
+}
+
+// Adam::update (adam.cpp:98-133), per element in order.
+void cnref_adam_step(float* W, const float* g, float* m, float* v, int64_t n, float lr, float b1,
+                     float b2, float eps, float bc1, float bc2) {
+  for (int64_t i = 0; i < n; ++i) {
+    m[i] = b1 * m[i] + (1.0f - b1) * g[i];
+    v[i] = b2 * v[i] + (1.0f - b2) * g[i] * g[i];
+    const float mh = m[i] / bc1;
+    const float vh = v[i] / bc2;
+    W[i] -= lr * mh / (std::sqrt(vh) + eps);
+  }
+}
+
+// adam.cpp:121-122: 1.0f - std::pow(beta, static_cast<float>(t))
+float cnref_bias_correction(float beta, int t) {
+  return 1.0f - std::pow(beta, static_cast<float>(t));
+}
+
+}  // extern "C"

@@ -1,0 +1,67 @@
+/*
+ * cnref.h — CPU oracle for the CppNet "cpu-eigen" training semantics.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library restates, in plain C++17 loops,
+ * what the reference computes on its "cpu-eigen" device (Eigen3 is absent
+ * from this image, so the reference itself cannot be compiled here).  Only
+ * tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load
+ * it, and only as the checker or the timed CPU baseline; the product path
+ * (cppnet_amd) never links, loads or calls it.
+ *
+ * Layout is Eigen ColMajor throughout (first index fastest), as in the
+ * reference.  Every function cites the reference file:line it restates.
+ * Sums run in ascending index order in fp32 unless stated otherwise; the
+ * library is compiled without FMA contraction so each operation rounds once.
+ */
+#ifndef CNREF_H
+#define CNREF_H
+#include <stdint.h>
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+void cnref_set_threads(int n);
+int  cnref_get_threads(void);
+
+/* ColMajor C[M,N] = alpha*op(A)*op(B) + beta*C (+bias[n]) (relu if epi==1);
+ * same operand conventions as cnhip_gemm_f32.  beta==0 does not read C. */
+void cnref_gemm_f32(int ta, int tb, int64_t M, int64_t N, int64_t K, float alpha,
+                    const float* A, int64_t lda, const float* B, int64_t ldb, float beta,
+                    float* C, int64_t ldc, const float* bias, int epi);
+
+/* Linear (linear.cpp:218-234 forward_eigen; 335-358 backward_eigen) */
+void cnref_linear_forward(const float* X, const float* W, const float* b, float* Y,
+                          int64_t B, int64_t I, int64_t O);
+void cnref_linear_backward(const float* X, const float* W, const float* dY, float* gW,
+                           float* gb, float* dX, int64_t B, int64_t I, int64_t O,
+                           int trainable, int accumulate);
+void cnref_column_sum(const float* in, float* out, int64_t rows, int64_t cols, int accumulate);
+
+/* Activations (relu.cpp:97-225; sigmoid.cpp:97-231; tanh.cpp:136-219) */
+void cnref_relu_forward(const float* x, float* y, int64_t n);
+void cnref_relu_backward(const float* y, const float* dy, float* dx, int64_t n);
+void cnref_sigmoid_forward(const float* x, float* y, int64_t n);
+void cnref_sigmoid_backward(const float* y, const float* dy, float* dx, int64_t n);
+void cnref_tanh_forward(const float* x, float* y, int64_t n);
+void cnref_tanh_backward(const float* y, const float* dy, float* dx, int64_t n);
+
+/* Losses; reduction 0 = mean, 1 = sum */
+float cnref_bce_forward(const float* p, const float* t, int64_t n, int reduction);
+void  cnref_bce_backward(const float* p, const float* t, float* g, int64_t n, int reduction);
+float cnref_mse_forward(const float* p, const float* t, int64_t n, int reduction);
+void  cnref_mse_backward(const float* p, const float* t, float* g, int64_t n, int reduction);
+float cnref_softmax_ce_forward(const float* z, const float* t, float* sm, int64_t B,
+                               int64_t C, int reduction);
+void  cnref_softmax_ce_backward(const float* sm, const float* t, float* g, int64_t B,
+                                int64_t C, int reduction);
+
+/* Adam, one tensor, caller-computed bias corrections (adam.cpp:98-133) */
+void cnref_adam_step(float* W, const float* g, float* m, float* v, int64_t n, float lr,
+                     float b1, float b2, float eps, float bc1, float bc2);
+/* bias correction exactly as the reference: 1 - pow(beta, float(t)) in float */
+float cnref_bias_correction(float beta, int t);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,116 @@
+"""Writes tests/golden/known_answers.json.
+
+The fixtures are the known-answer vectors that the reference's own test suite
+(LoqmanSamani/CppNet, tests/) asserts for the ops on the hot path, transcribed
+as data: inputs, expected outputs, the reference's tolerance and the test
+file:line they come from.  Matrices are given logically, row by row
+(``[[row0...], [row1...]]``), exactly as the reference's ``setValues`` calls
+write them; tests convert to Eigen ColMajor memory order.
+
+Where the reference only asserts a sign or an inequality, the entry states
+that predicate ("check") and, when the mathematics fixes the exact value, the
+exact value as well ("exact", derived by hand in the "derivation" field).
+
+Run:  python tests/golden/make_golden.py
+"""
+import json
+import math
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+
+
+def sig(x):
+    return 1.0 / (1.0 + math.exp(-x))
+
+
+def softmax(row):
+    m = max(row)
+    e = [math.exp(v - m) for v in row]
+    s = sum(e)
+    return [v / s for v in e]
+
+
+CASES = [
+    # ---- Linear ------------------------------------------------------------
+    dict(op="linear_forward", source="tests/layers/test_linear.cpp:108-129",
+         X=[[3.0, 4.0]], W=[[1.0, 0.0], [0.0, 1.0]], b=[0.5, -0.5],
+         expected=[[3.5, 3.5]], tol=1e-4),
+    dict(op="linear_forward", source="tests/kernels/test_matmul_gpu.cu:69-90",
+         X=[[1.0, 2.0, 3.0], [4.0, 5.0, 6.0]],
+         W=[[1.0, 0.0, 0.0], [0.0, 1.0, 0.0], [0.0, 0.0, 1.0]], b=None,
+         expected=[[1.0, 2.0, 3.0], [4.0, 5.0, 6.0]], tol=1e-3),
+    dict(op="linear_forward", source="tests/kernels/test_matmul_gpu.cu:92-109",
+         X=[[3.0, 4.0]], W=[[1.0, 0.0], [0.0, 1.0]], b=[0.5, -0.5],
+         expected=[[3.5, 3.5]], tol=1e-3),
+    # ---- ReLU ----------------------------------------------------------------
+    dict(op="relu_backward", source="tests/activations/test_relu.cpp:100-118",
+         X=[[-1.0, 2.0, -3.0], [4.0, -5.0, 0.0]], dY=[[1.0, 1.0, 1.0], [1.0, 1.0, 1.0]],
+         check="zero where input <= 0, positive where input > 0",
+         exact=[[0.0, 1.0, 0.0], [1.0, 0.0, 0.0]],
+         derivation="mask = (relu(x) > 0); dx = dy * mask; relu(0) = 0 so x = 0 is gated",
+         tol=1e-6),
+    # ---- Sigmoid -------------------------------------------------------------
+    dict(op="sigmoid_forward", source="tests/activations/test_sigmoid.cpp:79-89",
+         X=[[-2.0, -1.0, 1.0, 2.0]], expected=[[sig(-2.0), sig(-1.0), sig(1.0), sig(2.0)]],
+         tol=1e-5),
+    dict(op="sigmoid_forward", source="tests/activations/test_sigmoid.cpp:92-110",
+         X=[[50.0, -50.0]], expected=[[1.0, 0.0]], tol=1e-5),
+    dict(op="sigmoid_backward", source="tests/activations/test_sigmoid.cpp:131-148",
+         X=[[-1.0, 0.0, 1.0]], dY=[[1.0, 1.0, 1.0]],
+         expected=[[sig(-1.0) * (1 - sig(-1.0)), 0.25, sig(1.0) * (1 - sig(1.0))]], tol=1e-5),
+    # ---- BinaryCrossEntropy --------------------------------------------------
+    dict(op="bce_forward", source="tests/losses/test_binary_cross_entropy.cpp:97-109",
+         P=[[0.5]], T=[[1.0]], expected=-math.log(0.5), tol=0.05),
+    dict(op="bce_forward", source="tests/losses/test_binary_cross_entropy.cpp:47-58",
+         P=[[0.999, 0.001, 0.999]], T=[[1.0, 0.0, 1.0]], check="loss < 0.01",
+         exact=-math.log(0.999), derivation="each term is -log(0.999); mean of three equal terms",
+         tol=1e-6),
+    dict(op="bce_forward", source="tests/losses/test_binary_cross_entropy.cpp:61-72",
+         P=[[0.01, 0.99]], T=[[1.0, 0.0]], check="loss > 1",
+         exact=-math.log(0.01), derivation="each term is -log(0.01)", tol=1e-5),
+    dict(op="bce_backward", source="tests/losses/test_binary_cross_entropy.cpp:144-157",
+         P=[[0.5]], T=[[1.0]], check="grad < 0",
+         exact=[[-2.0]], derivation="(0.5-1)/(0.5*0.5)/1 = -2", tol=1e-6),
+    # ---- MSE -----------------------------------------------------------------
+    dict(op="mse_forward", source="tests/losses/test_mse.cpp:74-86",
+         P=[[0.0, 0.0, 0.0]], T=[[1.0, 2.0, 3.0]], expected=14.0 / 3.0, tol=0.1),
+    dict(op="mse_forward", source="tests/losses/test_mse.cpp:47-57",
+         P=[[1.0, 2.0, 3.0], [4.0, 5.0, 6.0]], T=[[1.0, 2.0, 3.0], [4.0, 5.0, 6.0]],
+         expected=0.0, tol=1e-6),
+    dict(op="mse_backward", source="tests/losses/test_mse.cpp:132-145",
+         P=[[5.0, 10.0]], T=[[1.0, 1.0]], check="grad > 0",
+         exact=[[2.0 * 4.0 / 2.0, 2.0 * 9.0 / 2.0]], derivation="2*(p-t)/n with n = 2",
+         tol=1e-6),
+    # ---- SoftmaxCrossEntropy -------------------------------------------------
+    dict(op="softmax_ce_forward", source="tests/losses/test_softmax_cross_entropy.cpp:32-40",
+         Z=[[10.0, -10.0, -10.0]], T=[[1.0, 0.0, 0.0]], check="loss < 0.1",
+         exact=-math.log(softmax([10.0, -10.0, -10.0])[0]),
+         derivation="-log softmax_0", tol=1e-6),
+    dict(op="softmax_ce_forward", source="tests/losses/test_softmax_cross_entropy.cpp:42-50",
+         Z=[[-10.0, 10.0, -10.0]], T=[[1.0, 0.0, 0.0]], check="loss > 10",
+         exact=-math.log(softmax([-10.0, 10.0, -10.0])[0]),
+         derivation="-log softmax_0 = 20 + log(1 + 2 e^-20)", tol=1e-4),
+    dict(op="softmax_ce_backward", source="tests/losses/test_softmax_cross_entropy.cpp:77-90",
+         Z=[[1.0, 2.0, 3.0]], T=[[0.0, 0.0, 1.0]], expected=[[0.0900, 0.2447, -0.3348]],
+         exact=[[a - b for a, b in zip(softmax([1.0, 2.0, 3.0]), [0.0, 0.0, 1.0])]],
+         derivation="softmax - target over a batch of 1", tol=0.02),
+    # ---- Adam ----------------------------------------------------------------
+    dict(op="adam_first_step", source="src/CppNet/optimizers/adam.cpp:98-133",
+         W=[1.0, -2.0, 0.5, 3.0], G=[0.1, -0.3, 2.0, -1e-3],
+         lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8,
+         exact=[w - 1e-3 * g / (abs(g) + 1e-8)
+                for w, g in zip([1.0, -2.0, 0.5, 3.0], [0.1, -0.3, 2.0, -1e-3])],
+         derivation="t=1: m/bc1 = g and v/bc2 = g^2, so W1 = W0 - lr*g/(|g|+eps)", tol=1e-6),
+]
+
+
+def main():
+    out = HERE / "known_answers.json"
+    out.write_text(json.dumps({"convention": "matrices logical row-major, as setValues",
+                               "cases": CASES}, indent=1) + "\n")
+    print("wrote", out, len(CASES), "cases")
+
+
+if __name__ == "__main__":
+    main()

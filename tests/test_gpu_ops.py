@@ -1,0 +1,266 @@
+"""GPU parity of the C-ABI ops against the CPU oracle (same seeded inputs).
+
+Tolerances: fp32 results within rel 1e-4 / abs 1e-5 of
+the oracle, elementwise |gpu - ref| <= 1e-5 + 1e-4*|ref|.  Adam is checked
+bit-exact: the kernel evaluates the reference's operation sequence without
+contraction, and fp32 division/sqrt are correctly rounded on both sides.
+"""
+import numpy as np
+import pytest
+import torch
+
+from cppnet_amd import ops
+from oracle_lib import close, fp
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-4, 1e-5
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def rnd(rng, n, scale=1.0):
+    return (rng.standard_normal(n) * scale).astype(np.float32)
+
+
+def _gemm_case(oracle, ta, tb, M, N, K, beta, with_bias, relu, pad, seed):
+    rng = np.random.default_rng(seed)
+    lda = (K if ta else M) + pad
+    ldb = (N if tb else K) + pad
+    ldc = M + pad
+    A = rnd(rng, max(1, lda * (M if ta else K)))
+    B = rnd(rng, max(1, ldb * (K if tb else N)))
+    C = rnd(rng, ldc * N)
+    bias = rnd(rng, N) if with_bias else None
+    Cd = dev(C)
+    ops.gemm(ta, tb, M, N, K, dev(A), lda, dev(B), ldb, Cd, ldc, alpha=1.0, beta=beta,
+             bias=None if bias is None else dev(bias), relu=relu)
+    want = C.copy()
+    oracle.cnref_gemm_f32(ta, tb, M, N, K, 1.0, fp(A), lda, fp(B), ldb, beta, fp(want), ldc,
+                          fp(bias), 1 if relu else 0)
+    got = host(Cd)
+    ok, msg = close(got, want, RTOL, ATOL)
+    assert ok, f"gemm ta={ta} tb={tb} M={M} N={N} K={K}: {msg}"
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1), (1, 1)])
+@pytest.mark.parametrize("M,N,K", [(128, 128, 16), (256, 384, 512), (130, 70, 33), (1, 1, 1),
+                                   (5, 300, 7), (300, 10, 700), (64, 3, 2000), (512, 512, 10)])
+def test_gemm_vs_oracle(gpu, oracle, ta, tb, M, N, K):
+    print(f"[gemm] ta={ta} tb={tb} M={M} N={N} K={K}", flush=True)
+    _gemm_case(oracle, ta, tb, M, N, K, beta=0.0, with_bias=False, relu=False, pad=0, seed=M + N + K)
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1)])
+def test_gemm_epilogues_and_strides(gpu, oracle, ta, tb):
+    print(f"[gemm-epi] ta={ta} tb={tb}", flush=True)
+    _gemm_case(oracle, ta, tb, 200, 150, 96, beta=1.0, with_bias=True, relu=True, pad=3, seed=11)
+    _gemm_case(oracle, ta, tb, 129, 257, 300, beta=0.5, with_bias=True, relu=False, pad=1, seed=12)
+
+
+def test_gemm_k_zero_scales_c(gpu, oracle):
+    _gemm_case(oracle, 0, 0, 40, 30, 0, beta=1.0, with_bias=True, relu=False, pad=0, seed=3)
+
+
+@pytest.mark.parametrize("B,I,O", [(512, 30, 64), (512, 64, 1), (256, 1024, 256), (33, 17, 5)])
+@pytest.mark.parametrize("trainable", [1, 0])
+def test_linear_vs_oracle(gpu, oracle, B, I, O, trainable):
+    print(f"[linear] B={B} I={I} O={O} trainable={trainable}", flush=True)
+    rng = np.random.default_rng(B * 7 + I + O)
+    X, W, b = rnd(rng, B * I), rnd(rng, I * O, 0.1), rnd(rng, O)
+    dY = rnd(rng, B * O, 0.01)
+    gW0, gb0 = rnd(rng, I * O, 1e-3), rnd(rng, O, 1e-3)
+    Y = torch.empty(B * O, device="cuda")
+    ops.linear_forward(dev(X), dev(W), dev(b), Y, B, I, O)
+    gW, gb, dX = dev(gW0), dev(gb0), torch.empty(B * I, device="cuda")
+    ops.linear_backward(dev(X), dev(W), dev(dY), gW, gb, dX, B, I, O, trainable=bool(trainable),
+                        accumulate=True)
+    rY = np.zeros(B * O, np.float32)
+    oracle.cnref_linear_forward(fp(X), fp(W), fp(b), fp(rY), B, I, O)
+    rgW, rgb, rdX = gW0.copy(), gb0.copy(), np.zeros(B * I, np.float32)
+    oracle.cnref_linear_backward(fp(X), fp(W), fp(dY), fp(rgW), fp(rgb), fp(rdX), B, I, O,
+                                 trainable, 1)
+    for got, want, name in [(host(Y), rY, "Y"), (host(gW), rgW, "grad_W"),
+                            (host(gb), rgb, "grad_b"), (host(dX), rdX, "dX")]:
+        ok, msg = close(got, want, RTOL, ATOL)
+        assert ok, f"{name}: {msg}"
+
+
+def test_linear_accumulates_over_two_backwards(gpu, oracle):
+    B, I, O = 64, 40, 24
+    rng = np.random.default_rng(2)
+    X, W, dY = rnd(rng, B * I), rnd(rng, I * O), rnd(rng, B * O)
+    gW, gb = torch.zeros(I * O, device="cuda"), torch.zeros(O, device="cuda")
+    for _ in range(2):
+        ops.linear_backward(dev(X), dev(W), dev(dY), gW, gb, None, B, I, O)
+    rgW, rgb = np.zeros(I * O, np.float32), np.zeros(O, np.float32)
+    for _ in range(2):
+        oracle.cnref_linear_backward(fp(X), fp(W), fp(dY), fp(rgW), fp(rgb), None, B, I, O, 1, 1)
+    assert close(host(gW), rgW, RTOL, ATOL)[0] and close(host(gb), rgb, RTOL, ATOL)[0]
+
+
+@pytest.mark.parametrize("rows,cols", [(4096, 37), (7, 3), (1, 5), (1000, 1)])
+def test_column_sum(gpu, oracle, rows, cols):
+    rng = np.random.default_rng(rows + cols)
+    a = rnd(rng, rows * cols)
+    out0 = rnd(rng, cols)
+    out = dev(out0)
+    ops.column_sum(dev(a), out, rows, cols, accumulate=True)
+    want = out0.copy()
+    oracle.cnref_column_sum(fp(a), fp(want), rows, cols, 1)
+    ok, msg = close(host(out), want, RTOL, ATOL)
+    assert ok, msg
+
+
+@pytest.mark.parametrize("name", ["relu", "sigmoid", "tanh"])
+@pytest.mark.parametrize("n", [1, 3, 4, 1001, 4096 * 64])
+def test_activation_vs_oracle(gpu, oracle, name, n):
+    rng = np.random.default_rng(n)
+    x = rnd(rng, n, 4.0)
+    if n > 3:
+        x[:3] = [0.0, 700.0, -700.0]
+    dy = rnd(rng, n)
+    y, dx = torch.empty(n, device="cuda"), torch.empty(n, device="cuda")
+    getattr(ops, f"{name}_forward")(dev(x), y)
+    getattr(ops, f"{name}_backward")(y, dev(dy), dx)
+    ry, rdx = np.zeros(n, np.float32), np.zeros(n, np.float32)
+    getattr(oracle, f"cnref_{name}_forward")(fp(x), fp(ry), n)
+    # the backward is checked on the GPU's own forward output, so a 1-ulp
+    # difference in exp/tanh does not leak into the derivative check
+    y_h = host(y)
+    getattr(oracle, f"cnref_{name}_backward")(fp(y_h), fp(dy), fp(rdx), n)
+    ok, msg = close(y_h, ry, RTOL, ATOL)
+    assert ok, f"{name} forward: {msg}"
+    got_dx = host(dx)
+    if name == "relu":
+        np.testing.assert_array_equal(got_dx, rdx)
+        np.testing.assert_array_equal(y_h, ry)
+    ok, msg = close(got_dx, rdx, RTOL, ATOL)
+    assert ok, f"{name} backward: {msg}"
+
+
+@pytest.mark.parametrize("n", [1, 512, 10000])
+@pytest.mark.parametrize("reduction", ["mean", "sum"])
+def test_bce_vs_oracle(gpu, oracle, n, reduction):
+    rng = np.random.default_rng(n)
+    p = rng.uniform(0.0, 1.0, n).astype(np.float32)
+    p[: min(n, 2)] = [0.0, 1.0][: min(n, 2)]
+    t = (rng.uniform(size=n) < 0.5).astype(np.float32)
+    loss, g = torch.empty(1, device="cuda"), torch.empty(n, device="cuda")
+    ops.bce_forward(dev(p), dev(t), loss, reduction)
+    ops.bce_backward(dev(p), dev(t), g, reduction)
+    r = 0 if reduction == "mean" else 1
+    want = oracle.cnref_bce_forward(fp(p), fp(t), n, r)
+    rg = np.zeros(n, np.float32)
+    oracle.cnref_bce_backward(fp(p), fp(t), fp(rg), n, r)
+    ok, msg = close(host(loss), [want], RTOL, ATOL)
+    assert ok, msg
+    ok, msg = close(host(g), rg, RTOL, ATOL)
+    assert ok, msg
+
+
+@pytest.mark.parametrize("n", [1, 128, 9999])
+@pytest.mark.parametrize("reduction", ["mean", "sum"])
+def test_mse_vs_oracle(gpu, oracle, n, reduction):
+    rng = np.random.default_rng(n + 1)
+    p, t = rnd(rng, n), rnd(rng, n)
+    loss, g = torch.empty(1, device="cuda"), torch.empty(n, device="cuda")
+    ops.mse_forward(dev(p), dev(t), loss, reduction)
+    ops.mse_backward(dev(p), dev(t), g, reduction)
+    r = 0 if reduction == "mean" else 1
+    rg = np.zeros(n, np.float32)
+    oracle.cnref_mse_backward(fp(p), fp(t), fp(rg), n, r)
+    ok, msg = close(host(loss), [oracle.cnref_mse_forward(fp(p), fp(t), n, r)], RTOL, ATOL)
+    assert ok, msg
+    np.testing.assert_array_equal(host(g), rg)
+
+
+@pytest.mark.parametrize("B,Cc", [(1, 3), (4096, 10), (256, 10), (32, 4), (77, 1)])
+def test_softmax_ce_vs_oracle(gpu, oracle, B, Cc):
+    rng = np.random.default_rng(B + Cc)
+    z = rnd(rng, B * Cc, 3.0)
+    labels = rng.integers(0, Cc, B)
+    t = np.zeros((Cc, B), np.float32)
+    t[labels, np.arange(B)] = 1.0  # ColMajor [B, C]: column c holds class c
+    t = t.ravel()
+    sm, loss = torch.empty(B * Cc, device="cuda"), torch.empty(1, device="cuda")
+    g = torch.empty(B * Cc, device="cuda")
+    ops.softmax_ce_forward(dev(z), dev(t), sm, loss, B, Cc)
+    ops.softmax_ce_backward(sm, dev(t), g, B, Cc)
+    rsm, rg = np.zeros(B * Cc, np.float32), np.zeros(B * Cc, np.float32)
+    want = oracle.cnref_softmax_ce_forward(fp(z), fp(t), fp(rsm), B, Cc, 0)
+    oracle.cnref_softmax_ce_backward(fp(rsm), fp(t), fp(rg), B, Cc, 0)
+    for got, ref, name in [(host(loss), [want], "loss"), (host(sm), rsm, "softmax"),
+                           (host(g), rg, "grad")]:
+        ok, msg = close(got, ref, RTOL, ATOL)
+        assert ok, f"{name}: {msg}"
+
+
+@pytest.mark.parametrize("n", [1, 7, 4096, 4096 * 4096 + 3])
+def test_adam_bit_exact(gpu, oracle, n):
+    print(f"[adam] n={n}", flush=True)
+    rng = np.random.default_rng(n % 1000)
+    W, m, v = rnd(rng, n), np.zeros(n, np.float32), np.zeros(n, np.float32)
+    Wd, md, vd = dev(W), dev(m), dev(v)
+    lr, b1, b2, eps = 1e-3, 0.9, 0.999, 1e-8
+    for t in (1, 2, 3):
+        g = rnd(rng, n, 0.1)
+        bc1, bc2 = oracle.cnref_bias_correction(b1, t), oracle.cnref_bias_correction(b2, t)
+        ops.adam_step(Wd, dev(g), md, vd, lr, b1, b2, eps, bc1, bc2)
+        oracle.cnref_adam_step(fp(W), fp(g), fp(m), fp(v), n, lr, b1, b2, eps, bc1, bc2)
+    np.testing.assert_array_equal(host(Wd), W)
+    np.testing.assert_array_equal(host(md), m)
+    np.testing.assert_array_equal(host(vd), v)
+
+
+def test_adam_multi_matches_single(gpu, oracle):
+    rng = np.random.default_rng(4)
+    sizes = [1024 * 4096, 4096, 10, 3, 4096 * 10]
+    lr, b1, b2, eps = 1e-3, 0.9, 0.999, 1e-8
+    params, refs = [], []
+    for i, n in enumerate(sizes):
+        W, g = rnd(rng, n), rnd(rng, n, 0.1)
+        t = 1 + i  # distinct per-tensor step counts (per-key t of the reference)
+        bc1, bc2 = oracle.cnref_bias_correction(b1, t), oracle.cnref_bias_correction(b2, t)
+        m, v = rnd(rng, n, 0.01), np.abs(rnd(rng, n, 0.01))
+        params.append((dev(W), dev(g), dev(m), dev(v), bc1, bc2))
+        oracle.cnref_adam_step(fp(W), fp(g), fp(m), fp(v), n, lr, b1, b2, eps, bc1, bc2)
+        refs.append((W, m, v))
+    ops.adam_step_multi(params, lr, b1, b2, eps)
+    for (Wd, _, md, vd, _, _), (W, m, v) in zip(params, refs):
+        np.testing.assert_array_equal(host(Wd), W)
+        np.testing.assert_array_equal(host(md), m)
+        np.testing.assert_array_equal(host(vd), v)
+
+
+def test_gemm_config2_shapes_vs_torch(gpu):
+    """Full config-2 GEMM shapes against torch's fp32 matmul (hipBLASLt) as an
+    independent float reference (the oracle is too slow at 4096^3 to run per test)."""
+    torch.backends.cuda.matmul.allow_tf32 = False
+    g = torch.Generator(device="cuda").manual_seed(0)
+    for (ta, tb, M, N, K) in [(0, 0, 4096, 4096, 4096), (1, 0, 1024, 4096, 4096),
+                              (0, 1, 4096, 1024, 4096), (1, 0, 4096, 10, 4096),
+                              (0, 1, 4096, 4096, 10)]:
+        print(f"[gemm-c2] ta={ta} tb={tb} M={M} N={N} K={K}", flush=True)
+        A = torch.randn((M, K) if ta else (K, M), device="cuda", generator=g)  # row-major storage
+        B = torch.randn((N, K) if not tb else (K, N), device="cuda", generator=g)
+        # ColMajor views: A_cm(m,k) -> ta ? A[m][k] : A[k][m] etc.
+        opA = A if ta else A.t()
+        opB = B.t() if not tb else B
+        C = torch.empty(N, M, device="cuda")  # ColMajor [M,N] == row-major [N,M]
+        ops.gemm(ta, tb, M, N, K, A, K if ta else M, B, K if not tb else N, C, M)
+        ref = (opA.double() @ opB.double()).t()
+        err = (C.double() - ref).abs()
+        lim = 1e-5 + 1e-4 * ref.abs()
+        # fp32 sums of K=4096 N(0,1) products: compare elementwise against the
+        # fp64 product with the rel/abs bound scaled by sqrt(K) * |row|*|col|
+        scale = (opA.double().norm(dim=1)[:, None] * opB.double().norm(dim=0)[None, :]).t()
+        bound = torch.maximum(lim, 4e-7 * scale)
+        assert bool((err <= bound).all()), f"max err {err.max().item()} at ta={ta} tb={tb} {M}x{N}x{K}"
