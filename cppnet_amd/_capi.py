@@ -33,12 +33,15 @@ SIGNATURES: dict[str, tuple] = {
     "cnhip_stream_destroy": (i32, [vp]),
     "cnhip_stream_synchronize": (i32, [vp]),
     "cnhip_device_synchronize": (i32, []),
+    "cnhip_is_device_pointer": (i32, [vp]),
     "cnhip_event_create": (i32, [C.POINTER(vp)]),
     "cnhip_event_destroy": (i32, [vp]),
     "cnhip_event_record": (i32, [vp, vp]),
     "cnhip_event_elapsed_ms": (i32, [C.POINTER(f32), vp, vp]),
     "cnhip_gemm_f32": (i32, [i32, i32, i64, i64, i64, f32, vp, i64, vp, i64, f32, vp, i64, vp,
                              i32, vp]),
+    "cnhip_gemm_timing_enable": (i32, [i32]),
+    "cnhip_gemm_timing_read": (i32, [C.POINTER(i64), C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     "cnhip_linear_forward": (i32, [vp, vp, vp, vp, i64, i64, i64, vp]),
     "cnhip_linear_backward": (i32, [vp, vp, vp, vp, vp, vp, i64, i64, i64, i32, i32, vp]),
     "cnhip_column_sum": (i32, [vp, vp, i64, i64, i32, vp]),

@@ -14,6 +14,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <vector>
 
 #include "common.hpp"
 
@@ -256,6 +257,35 @@ void launch_gemm(const GemmArgs& g, int nblocks, int splits, hipStream_t st) {
   hipLaunchKernelGGL((gemm_f32_kernel<TA, TB>), dim3(nblocks, 1, splits), dim3(NT), 0, st, g);
 }
 
+// Per-launch event timing (cnhip_gemm_timing_*): a pool of event pairs
+// reused across enable() calls.
+struct TimingRec {
+  hipEvent_t start, stop;
+  double flops;
+};
+struct Timing {
+  bool on = false;
+  std::vector<TimingRec> pool;
+  size_t used = 0;
+};
+thread_local Timing g_timing;
+
+TimingRec* timing_slot(double flops) {
+  Timing& t = g_timing;
+  if (!t.on) return nullptr;
+  if (t.used == t.pool.size()) {
+    TimingRec r{};
+    if (hipEventCreate(&r.start) != hipSuccess || hipEventCreate(&r.stop) != hipSuccess) {
+      (void)hipGetLastError();
+      return nullptr;
+    }
+    t.pool.push_back(r);
+  }
+  TimingRec* r = &t.pool[t.used++];
+  r->flops = flops;
+  return r;
+}
+
 }  // namespace
 
 int gemm_f32(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float alpha,
@@ -307,11 +337,14 @@ int gemm_f32(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float al
   }
 
   const int nblocks = (int)tiles;
+  TimingRec* rec = timing_slot(2.0 * (double)M * (double)N * (double)K);
+  if (rec) (void)hipEventRecord(rec->start, st);
   if (!trans_a && !trans_b) launch_gemm<false, false>(g, nblocks, splits, st);
   else if (trans_a && !trans_b) launch_gemm<true, false>(g, nblocks, splits, st);
   else if (!trans_a && trans_b) launch_gemm<false, true>(g, nblocks, splits, st);
   else launch_gemm<true, true>(g, nblocks, splits, st);
   int status = check_launch(who);
+  if (rec) (void)hipEventRecord(rec->stop, st);
 
   if (splits > 1) {
     if (status == CNHIP_OK) {
@@ -333,4 +366,28 @@ extern "C" int cnhip_gemm_f32(int trans_a, int trans_b, int64_t M, int64_t N, in
                               int epilogue, cnhip_stream_t stream) {
   return cnhip::gemm_f32(trans_a, trans_b, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, bias,
                          epilogue, cnhip::as_stream(stream), "cnhip_gemm_f32");
+}
+
+extern "C" int cnhip_gemm_timing_enable(int on) {
+  cnhip::g_timing.on = on != 0;
+  cnhip::g_timing.used = 0;
+  return CNHIP_OK;
+}
+
+extern "C" int cnhip_gemm_timing_read(int64_t* launches, double* total_ms, double* total_flops) {
+  CNHIP_REQUIRE(launches && total_ms && total_flops, "cnhip_gemm_timing_read: NULL argument");
+  cnhip::Timing& t = cnhip::g_timing;
+  double ms = 0.0, fl = 0.0;
+  for (size_t i = 0; i < t.used; ++i) {
+    float e = 0.f;
+    CNHIP_TRY(cnhip::check_hip(hipEventSynchronize(t.pool[i].stop), "cnhip_gemm_timing_read"));
+    CNHIP_TRY(cnhip::check_hip(hipEventElapsedTime(&e, t.pool[i].start, t.pool[i].stop),
+                               "cnhip_gemm_timing_read"));
+    ms += e;
+    fl += t.pool[i].flops;
+  }
+  *launches = (int64_t)t.used;
+  *total_ms = ms;
+  *total_flops = fl;
+  return CNHIP_OK;
 }

@@ -1,0 +1,106 @@
+// Adam on device (ref: src/CppNet/optimizers/adam.cpp:98-133).
+#include "CppNet/optimizers/adam.hpp"
+
+#include <cmath>
+#include <stdexcept>
+
+#include "CppNet/layers/layer.hpp"
+
+namespace CppNet
+{
+    namespace Optimizers
+    {
+        Adam::Adam(float beta1, float beta2, float epsilon, const std::string& device)
+            : beta1_(beta1), beta2_(beta2), epsilon_(epsilon), device_(device)
+        {
+            Layers::require_gpu_device(device_, "Adam");
+        }
+
+        void Adam::update(float* weights, const float* gradients, int size, float learning_rate)
+        {
+            update(weights, gradients, static_cast<int64_t>(size), learning_rate);
+        }
+
+        void Adam::update(float* weights, const float* gradients, int64_t size, float learning_rate)
+        {
+            if (size <= 0) return;
+            auto it = states_.find(weights);
+            if (it == states_.end())
+            {
+                if (!cnhip_is_device_pointer(weights) || !cnhip_is_device_pointer(gradients))
+                    throw std::invalid_argument(
+                        "Adam::update: parameters and gradients must be device memory in the gpu backend");
+                State s;
+                s.m = DeviceTensor::zeros({size});
+                s.v = DeviceTensor::zeros({size});
+                it = states_.emplace(weights, std::move(s)).first;
+            }
+            State& s = it->second;
+            if (s.m.size() != size)
+                throw std::invalid_argument("Adam::update: parameter size changed for an existing key");
+            ++s.t;
+            // adam.cpp:121-122, evaluated identically (float pow of float t)
+            const float bc1 = 1.0f - std::pow(beta1_, static_cast<float>(s.t));
+            const float bc2 = 1.0f - std::pow(beta2_, static_cast<float>(s.t));
+            pending_.push_back(Pending{weights, gradients, &s, size, bc1, bc2, learning_rate});
+            if (group_depth_ == 0) flush();
+        }
+
+        void Adam::begin_group() { ++group_depth_; }
+
+        void Adam::end_group()
+        {
+            if (group_depth_ > 0 && --group_depth_ == 0) flush();
+        }
+
+        void Adam::flush()
+        {
+            size_t i = 0;
+            while (i < pending_.size())
+            {
+                // one fused launch per run of equal learning rates (<= 64 tensors each)
+                float* W[64];
+                const float* G[64];
+                float* M[64];
+                float* V[64];
+                int64_t N[64];
+                float B1[64], B2[64];
+                const float lr = pending_[i].lr;
+                int count = 0;
+                while (i < pending_.size() && count < 64 && pending_[i].lr == lr)
+                {
+                    const Pending& p = pending_[i++];
+                    W[count] = p.w; G[count] = p.g; M[count] = p.s->m.data(); V[count] = p.s->v.data();
+                    N[count] = p.n; B1[count] = p.bc1; B2[count] = p.bc2;
+                    ++count;
+                }
+                int st = cnhip_adam_step_multi(count, W, G, M, V, N, B1, B2, lr, beta1_, beta2_, epsilon_,
+                                               Device::stream());
+                if (st != CNHIP_OK)
+                {
+                    pending_.clear();
+                    Device::check(st, "Adam::update");
+                }
+            }
+            pending_.clear();
+        }
+
+        int Adam::step_count(const float* weights) const
+        {
+            auto it = states_.find(weights);
+            return it == states_.end() ? 0 : it->second.t;
+        }
+        const DeviceTensor& Adam::first_moment(const float* weights) const
+        {
+            auto it = states_.find(weights);
+            if (it == states_.end()) throw std::out_of_range("Adam: no state for this parameter");
+            return it->second.m;
+        }
+        const DeviceTensor& Adam::second_moment(const float* weights) const
+        {
+            auto it = states_.find(weights);
+            if (it == states_.end()) throw std::out_of_range("Adam: no state for this parameter");
+            return it->second.v;
+        }
+    } // namespace Optimizers
+} // namespace CppNet

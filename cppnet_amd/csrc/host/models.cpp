@@ -1,0 +1,76 @@
+// SequentialModel over device tensors (ref: src/CppNet/models/models.cpp:13-101).
+#include "CppNet/models/models.hpp"
+
+#include <iostream>
+#include <string>
+
+namespace CppNet
+{
+    namespace Models
+    {
+        void SequentialModel::add_activation(std::shared_ptr<Activations::Activation> activation)
+        {
+            if (!activation) throw std::invalid_argument("Cannot add null activation to model");
+            steps_.push_back(std::make_shared<detail::ActivationStep>(std::move(activation)));
+        }
+
+        DeviceTensor SequentialModel::forward(const DeviceTensor& input)
+        {
+            DeviceTensor x = input;
+            for (auto& s : steps_) x = s->forward(x);
+            return x;
+        }
+
+        DeviceTensor SequentialModel::backward(const DeviceTensor& grad_output)
+        {
+            DeviceTensor g = grad_output;
+            for (auto it = steps_.rbegin(); it != steps_.rend(); ++it) g = (*it)->backward(g);
+            return g;
+        }
+
+        Tensor<float, 2> SequentialModel::forward(const Tensor<float, 2>& input)
+        {
+            return forward(DeviceTensor::from_host(input)).to_host<float, 2>();
+        }
+
+        Tensor<float, 2> SequentialModel::backward(const Tensor<float, 2>& grad_output)
+        {
+            return backward(DeviceTensor::from_host(grad_output)).to_host<float, 2>();
+        }
+
+        std::shared_ptr<Layers::Layer> SequentialModel::get_layer(std::size_t index) const
+        {
+            if (index >= layers_.size())
+                throw std::out_of_range("Layer index " + std::to_string(index) + " out of range (model has " +
+                                        std::to_string(layers_.size()) + " layers)");
+            return layers_[index];
+        }
+
+        void SequentialModel::update(Optimizers::Optimizer& optimizer, float learning_rate)
+        {
+            optimizer.begin_group();
+            try
+            {
+                for (auto& s : steps_)
+                    if (s->is_trainable()) s->step(optimizer, learning_rate);
+            }
+            catch (...)
+            {
+                optimizer.end_group();
+                throw;
+            }
+            optimizer.end_group();
+        }
+
+        void SequentialModel::zero_grad()
+        {
+            for (auto& l : layers_) l->reset_grads();
+        }
+
+        void SequentialModel::summary() const
+        {
+            std::cout << "SequentialModel: " << steps_.size() << " steps, " << layers_.size()
+                      << " parameterised layers (device gpu)\n";
+        }
+    } // namespace Models
+} // namespace CppNet

@@ -1,0 +1,251 @@
+// Training harness C ABI (include/cppnet_train.h): builds models from the
+// CppNet-compatible classes and runs the reference harness's train step.
+#include "cppnet_train.h"
+
+#include <cstdarg>
+#include <cstdio>
+#include <exception>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "CppNet/CppNet.hpp"
+
+using namespace CppNet;
+
+struct cnt_session
+{
+    cnhip_stream_t stream = nullptr;
+    Models::SequentialModel model;
+    std::vector<std::shared_ptr<Layers::Linear>> linears;
+    std::unique_ptr<Losses::Loss> loss;
+    std::unique_ptr<Optimizers::Adam> adam;
+    float lr = 1e-3f;
+    int64_t batch = 0, in_features = 0, out_features = 0;
+    DeviceTensor X, Y;
+    Losses::DeviceScalar last_loss;
+
+    // parameter index -> (device tensor)
+    std::vector<DeviceTensor*> params, grads;
+};
+
+namespace
+{
+    thread_local std::string g_err;
+
+    int fail(int status, const std::string& msg)
+    {
+        g_err = msg;
+        return status;
+    }
+
+    template <class F>
+    int guarded(const char* who, F&& f)
+    {
+        try
+        {
+            f();
+            return CNHIP_OK;
+        }
+        catch (const Device::Error& e)
+        {
+            return fail(e.status(), std::string(who) + ": " + e.what());
+        }
+        catch (const std::exception& e)
+        {
+            return fail(CNHIP_EINVAL, std::string(who) + ": " + e.what());
+        }
+    }
+
+    // Makes the session's stream the backend stream for the duration of a call.
+    struct StreamScope
+    {
+        cnhip_stream_t saved;
+        explicit StreamScope(cnt_session* s) : saved(Device::stream()) { Device::set_stream(s->stream); }
+        ~StreamScope() { Device::set_stream(saved); }
+    };
+
+    std::shared_ptr<Activations::Activation> make_act(int act)
+    {
+        switch (act)
+        {
+            case CNT_ACT_NONE: return nullptr;
+            case CNT_ACT_RELU: return std::make_shared<Activations::ReLU>("gpu");
+            case CNT_ACT_SIGMOID: return std::make_shared<Activations::Sigmoid>("gpu");
+            case CNT_ACT_TANH: return std::make_shared<Activations::Tanh>("gpu");
+        }
+        throw std::invalid_argument("unknown activation code " + std::to_string(act));
+    }
+
+    std::unique_ptr<Losses::Loss> make_loss(int loss)
+    {
+        switch (loss)
+        {
+            case CNT_LOSS_BCE: return std::make_unique<Losses::BinaryCrossEntropy>("mean", false, 1.0f, "gpu");
+            case CNT_LOSS_SOFTMAX_CE: return std::make_unique<Losses::SoftmaxCrossEntropy>("mean", "gpu");
+            case CNT_LOSS_MSE: return std::make_unique<Losses::MSE>("mean", "gpu");
+        }
+        throw std::invalid_argument("unknown loss code " + std::to_string(loss));
+    }
+
+    void check_session(cnt_session* s)
+    {
+        if (!s) throw std::invalid_argument("NULL session");
+    }
+
+    DeviceTensor& param_at(cnt_session* s, int index, bool grad)
+    {
+        check_session(s);
+        auto& v = grad ? s->grads : s->params;
+        if (index < 0 || index >= static_cast<int>(v.size()))
+            throw std::out_of_range("parameter index " + std::to_string(index) + " out of range");
+        return *v[static_cast<size_t>(index)];
+    }
+} // namespace
+
+extern "C" {
+
+const char* cnt_last_error(void) { return g_err.c_str(); }
+
+int cnt_mlp_create(cnt_session** out, int n_linear, const int64_t* sizes, int hidden_act, int out_act,
+                   int loss, int64_t batch, float lr, float beta1, float beta2, float eps, uint64_t seed)
+{
+    return guarded("cnt_mlp_create", [&] {
+        if (!out) throw std::invalid_argument("NULL out pointer");
+        *out = nullptr;
+        if (n_linear < 1 || !sizes) throw std::invalid_argument("need at least one Linear layer");
+        if (batch <= 0) throw std::invalid_argument("batch must be positive");
+        auto s = std::make_unique<cnt_session>();
+        Device::check(cnhip_stream_create(&s->stream), "stream");
+        StreamScope scope(s.get());
+        Utils::set_seed(seed);
+        for (int i = 0; i < n_linear; ++i)
+        {
+            auto lin = std::make_shared<Layers::Linear>(static_cast<int>(sizes[i]),
+                                                        static_cast<int>(sizes[i + 1]),
+                                                        "fc" + std::to_string(i + 1), true, true, "gpu",
+                                                        "xavier");
+            s->model.add_layer(lin);
+            s->linears.push_back(lin);
+            auto act = make_act(i + 1 < n_linear ? hidden_act : out_act);
+            if (act) s->model.add_activation(act);
+        }
+        for (auto& l : s->linears)
+        {
+            s->params.push_back(&l->weights());
+            s->grads.push_back(&l->grad_weights());
+            s->params.push_back(&l->biases());
+            s->grads.push_back(&l->grad_biases());
+        }
+        s->loss = make_loss(loss);
+        s->adam = std::make_unique<Optimizers::Adam>(beta1, beta2, eps, "gpu");
+        s->lr = lr;
+        s->batch = batch;
+        s->in_features = sizes[0];
+        s->out_features = sizes[n_linear];
+        s->X = DeviceTensor::zeros({batch, s->in_features});
+        s->Y = DeviceTensor::zeros({batch, s->out_features});
+        Device::synchronize();
+        *out = s.release();
+    });
+}
+
+int cnt_destroy(cnt_session* s)
+{
+    return guarded("cnt_destroy", [&] {
+        if (!s) return;
+        cnhip_stream_synchronize(s->stream);
+        cnhip_stream_t st = s->stream;
+        {
+            StreamScope scope(s);
+            delete s;
+        }
+        cnhip_stream_destroy(st);
+    });
+}
+
+int cnt_num_params(cnt_session* s, int* count)
+{
+    return guarded("cnt_num_params", [&] {
+        check_session(s);
+        *count = static_cast<int>(s->params.size());
+    });
+}
+
+int cnt_param_size(cnt_session* s, int index, int64_t* n)
+{
+    return guarded("cnt_param_size", [&] { *n = param_at(s, index, false).size(); });
+}
+
+int cnt_set_param(cnt_session* s, int index, const float* host)
+{
+    return guarded("cnt_set_param", [&] {
+        StreamScope scope(s);
+        param_at(s, index, false).copy_from_host(host);
+    });
+}
+
+int cnt_get_param(cnt_session* s, int index, float* host)
+{
+    return guarded("cnt_get_param", [&] {
+        StreamScope scope(s);
+        param_at(s, index, false).copy_to_host(host);
+    });
+}
+
+int cnt_get_grad(cnt_session* s, int index, float* host)
+{
+    return guarded("cnt_get_grad", [&] {
+        StreamScope scope(s);
+        param_at(s, index, true).copy_to_host(host);
+    });
+}
+
+int cnt_set_batch(cnt_session* s, const float* x_host, const float* y_host)
+{
+    return guarded("cnt_set_batch", [&] {
+        check_session(s);
+        StreamScope scope(s);
+        s->X.copy_from_host(x_host);
+        s->Y.copy_from_host(y_host);
+    });
+}
+
+int cnt_set_batch_device(cnt_session* s, const float* x_dev, const float* y_dev)
+{
+    return guarded("cnt_set_batch_device", [&] {
+        check_session(s);
+        StreamScope scope(s);
+        Device::check(cnhip_memcpy_async(s->X.data(), x_dev, static_cast<size_t>(s->X.size()) * 4, 2,
+                                         s->stream), "X");
+        Device::check(cnhip_memcpy_async(s->Y.data(), y_dev, static_cast<size_t>(s->Y.size()) * 4, 2,
+                                         s->stream), "Y");
+    });
+}
+
+int cnt_step(cnt_session* s, float* loss_out)
+{
+    return guarded("cnt_step", [&] {
+        check_session(s);
+        StreamScope scope(s);
+        s->model.zero_grad();
+        DeviceTensor out = s->model.forward(s->X);
+        s->last_loss = s->loss->forward(out, s->Y);
+        DeviceTensor g = s->loss->backward(out, s->Y);
+        s->model.backward(g);
+        s->model.update(*s->adam, s->lr);
+        if (loss_out) *loss_out = s->last_loss.get();
+    });
+}
+
+int cnt_synchronize(cnt_session* s)
+{
+    return guarded("cnt_synchronize", [&] {
+        check_session(s);
+        Device::check(cnhip_stream_synchronize(s->stream), "sync");
+    });
+}
+
+void* cnt_stream(cnt_session* s) { return s ? s->stream : nullptr; }
+
+} // extern "C"

@@ -93,6 +93,16 @@ int cnhip_device_synchronize(void) {
   return check_hip(hipDeviceSynchronize(), "cnhip_device_synchronize");
 }
 
+int cnhip_is_device_pointer(const void* ptr) {
+  if (!ptr) return 0;
+  hipPointerAttribute_t attr;
+  if (hipPointerGetAttributes(&attr, ptr) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  return (attr.type == hipMemoryTypeDevice || attr.type == hipMemoryTypeManaged) ? 1 : 0;
+}
+
 int cnhip_event_create(void** event) {
   CNHIP_REQUIRE(event, "cnhip_event_create: NULL out pointer");
   hipEvent_t e = nullptr;

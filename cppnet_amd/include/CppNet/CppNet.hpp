@@ -1,0 +1,32 @@
+/**
+ * @file CppNet.hpp
+ * @brief Umbrella header of the MI355X gpu backend (ref: include/CppNet/CppNet.hpp).
+ */
+#ifndef CPPNET_HPP
+#define CPPNET_HPP
+
+#include "CppNet/core/device.hpp"
+#include "CppNet/core/tensor.hpp"
+#include "CppNet/utils/init.hpp"
+#include "CppNet/layers/layer.hpp"
+#include "CppNet/layers/linear.hpp"
+#include "CppNet/activations/activation.hpp"
+#include "CppNet/activations/relu.hpp"
+#include "CppNet/activations/sigmoid.hpp"
+#include "CppNet/activations/tanh.hpp"
+#include "CppNet/losses/loss.hpp"
+#include "CppNet/losses/binary_cross_entropy.hpp"
+#include "CppNet/losses/mse.hpp"
+#include "CppNet/losses/softmax_cross_entropy.hpp"
+#include "CppNet/optimizers/optimizer.hpp"
+#include "CppNet/optimizers/adam.hpp"
+#include "CppNet/models/models.hpp"
+
+namespace CppNet
+{
+    /// The reference's has_cuda_support() (CppNet.hpp:127-134): true when a
+    /// HIP device is visible to this process.
+    inline bool has_cuda_support() { return Device::available(); }
+    inline bool has_gpu_support() { return Device::available(); }
+} // namespace CppNet
+#endif

@@ -1,0 +1,85 @@
+/**
+ * @file linear.hpp
+ * @brief Linear (fully connected) layer, device "gpu"
+ *        (ref: include/CppNet/layers/linear.hpp, src/CppNet/layers/linear.cpp).
+ *
+ *   output = input * W + b       W: [in_size, out_size], b: [out_size]
+ *
+ * Parameters, gradients and the cached input live in HBM.  backward()
+ * ADDS into grad_W / grad_b (the cpu-eigen semantics, linear.cpp:346-352);
+ * reset_grads() clears them; step() never does (linear.cpp:126-146).  dX is
+ * computed even for a frozen layer (linear.cpp:357).
+ *
+ * Host-tensor overloads copy in and out (one H2D and one D2H each); the
+ * DeviceTensor overloads never touch host memory.
+ */
+#ifndef CPPNET_LAYERS_LINEAR_HPP
+#define CPPNET_LAYERS_LINEAR_HPP
+
+#include <string>
+
+#include "CppNet/core/tensor.hpp"
+#include "CppNet/layers/layer.hpp"
+
+namespace CppNet
+{
+    namespace Layers
+    {
+        class Linear : public Layer
+        {
+        public:
+            Linear(int in_size, int out_size, std::string layer_name = "Linear",
+                   bool trainable = true, bool bias = true, std::string device = "gpu",
+                   std::string weight_init = "xavier");
+
+            Tensor<float, 2> forward(const Tensor<float, 2>& input);
+            Tensor<float, 2> backward(const Tensor<float, 2>& grad_output);
+            DeviceTensor forward(const DeviceTensor& input);
+            DeviceTensor backward(const DeviceTensor& grad_output);
+
+            bool is_trainable() const override { return trainable_; }
+            void step(Optimizers::Optimizer& optimizer, float learning_rate) override;
+            void reset_grads() override;
+            void freeze() { trainable_ = false; }
+            void unfreeze() { trainable_ = true; }
+
+            int get_input_size() const { return in_size_; }
+            int get_output_size() const { return out_size_; }
+            std::string get_layer_name() const { return layer_name_; }
+            std::string get_device() const { return device_; }
+            bool has_bias() const { return bias_flag_; }
+
+            /// Host copies of the device state (synchronise the stream).
+            Tensor<float, 2> get_weights() const;
+            Tensor<float, 1> get_biases() const;
+            Tensor<float, 2> get_grad_weights() const;
+            Tensor<float, 1> get_grad_biases() const;
+            void set_weights(const Tensor<float, 2>& weights);
+            void set_biases(const Tensor<float, 1>& biases);
+
+            /// Device-resident state.
+            DeviceTensor& weights() { return W_; }
+            DeviceTensor& biases() { return b_; }
+            DeviceTensor& grad_weights() { return gW_; }
+            DeviceTensor& grad_biases() { return gb_; }
+
+            void reinitialize_weights(const std::string& method);
+            /// Capacity hint of the reference gpu path (linear.cpp:460-468);
+            /// buffers here are sized per call, so it only validates.
+            void set_max_batch_size(int max_batch_size);
+            static void set_num_threads(int) {}
+            void print_layer_info() const;
+
+        private:
+            int in_size_, out_size_;
+            std::string layer_name_;
+            bool trainable_;
+            bool bias_flag_;
+            std::string device_;
+            std::string weight_init_;
+            DeviceTensor W_, b_, gW_, gb_;
+            DeviceTensor in_cache_;
+        };
+    } // namespace Layers
+} // namespace CppNet
+#endif

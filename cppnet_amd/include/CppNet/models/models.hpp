@@ -1,0 +1,103 @@
+/**
+ * @file models.hpp
+ * @brief SequentialModel (ref: include/CppNet/models/models.hpp:116-218,
+ *        src/CppNet/models/models.cpp:13-101) over device tensors.
+ *
+ * Steps run in insertion order; backward in reverse.  zero_grad() resets
+ * every layer's gradients; update() steps every trainable layer, with all of
+ * the optimizer's updates fused into one launch (begin_group/end_group).
+ */
+#ifndef CPPNET_MODELS_MODELS_HPP
+#define CPPNET_MODELS_MODELS_HPP
+
+#include <memory>
+#include <stdexcept>
+#include <type_traits>
+#include <vector>
+
+#include "CppNet/activations/activation.hpp"
+#include "CppNet/core/tensor.hpp"
+#include "CppNet/layers/layer.hpp"
+#include "CppNet/optimizers/optimizer.hpp"
+
+namespace CppNet
+{
+    namespace detail
+    {
+        class Step
+        {
+        public:
+            virtual DeviceTensor forward(const DeviceTensor& input) = 0;
+            virtual DeviceTensor backward(const DeviceTensor& grad_output) = 0;
+            virtual bool is_trainable() const = 0;
+            virtual void step(Optimizers::Optimizer& optimizer, float learning_rate) = 0;
+            virtual ~Step() = default;
+        };
+
+        template <typename LayerT>
+        class LayerStep : public Step
+        {
+        public:
+            explicit LayerStep(std::shared_ptr<LayerT> layer) : layer_(std::move(layer)) {}
+            DeviceTensor forward(const DeviceTensor& x) override { return layer_->forward(x); }
+            DeviceTensor backward(const DeviceTensor& g) override { return layer_->backward(g); }
+            bool is_trainable() const override { return layer_->is_trainable(); }
+            void step(Optimizers::Optimizer& o, float lr) override { layer_->step(o, lr); }
+
+        private:
+            std::shared_ptr<LayerT> layer_;
+        };
+
+        class ActivationStep : public Step
+        {
+        public:
+            explicit ActivationStep(std::shared_ptr<Activations::Activation> a) : act_(std::move(a)) {}
+            DeviceTensor forward(const DeviceTensor& x) override { return act_->forward(x); }
+            DeviceTensor backward(const DeviceTensor& g) override { return act_->backward(g); }
+            bool is_trainable() const override { return false; }
+            void step(Optimizers::Optimizer&, float) override {}
+
+        private:
+            std::shared_ptr<Activations::Activation> act_;
+        };
+    } // namespace detail
+
+    namespace Models
+    {
+        class SequentialModel
+        {
+        public:
+            SequentialModel() = default;
+
+            template <typename LayerT,
+                      typename = std::enable_if_t<std::is_same<
+                          std::decay_t<decltype(std::declval<LayerT>().forward(
+                              std::declval<const DeviceTensor&>()))>,
+                          DeviceTensor>::value>>
+            void add_layer(std::shared_ptr<LayerT> layer)
+            {
+                if (!layer) throw std::invalid_argument("Cannot add null layer to model");
+                steps_.push_back(std::make_shared<detail::LayerStep<LayerT>>(layer));
+                layers_.push_back(layer);
+            }
+            void add_activation(std::shared_ptr<Activations::Activation> activation);
+
+            DeviceTensor forward(const DeviceTensor& input);
+            DeviceTensor backward(const DeviceTensor& grad_output);
+            Tensor<float, 2> forward(const Tensor<float, 2>& input);
+            Tensor<float, 2> backward(const Tensor<float, 2>& grad_output);
+
+            std::size_t num_layers() const { return layers_.size(); }
+            std::size_t num_steps() const { return steps_.size(); }
+            std::shared_ptr<Layers::Layer> get_layer(std::size_t index) const;
+            void update(Optimizers::Optimizer& optimizer, float learning_rate);
+            void zero_grad();
+            void summary() const;
+
+        private:
+            std::vector<std::shared_ptr<detail::Step>> steps_;
+            std::vector<std::shared_ptr<Layers::Layer>> layers_;
+        };
+    } // namespace Models
+} // namespace CppNet
+#endif

@@ -1,0 +1,67 @@
+/**
+ * @file adam.hpp
+ * @brief Adam on device (ref: include/CppNet/optimizers/adam.hpp:27-28,
+ *        src/CppNet/optimizers/adam.cpp:98-133).
+ *
+ * State (m, v, step t) is kept per parameter pointer, as in the reference:
+ * each key has its own t, and the bias corrections 1 - beta^t are computed
+ * in float on the host exactly as adam.cpp:121-122 does.  m and v live in
+ * HBM next to the parameters.  Between begin_group() and end_group() the
+ * updates are queued and issued as ONE fused multi-tensor kernel.
+ */
+#ifndef CPPNET_OPTIMIZERS_ADAM_HPP
+#define CPPNET_OPTIMIZERS_ADAM_HPP
+
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "CppNet/core/tensor.hpp"
+#include "CppNet/optimizers/optimizer.hpp"
+
+namespace CppNet
+{
+    namespace Optimizers
+    {
+        class Adam : public Optimizer
+        {
+        public:
+            Adam(float beta1 = 0.9f, float beta2 = 0.999f, float epsilon = 1e-8f,
+                 const std::string& device = "gpu");
+            using Optimizer::update;
+            void update(float* weights, const float* gradients, int size,
+                        float learning_rate) override;
+            void update(float* weights, const float* gradients, int64_t size,
+                        float learning_rate) override;
+            void begin_group() override;
+            void end_group() override;
+
+            int step_count(const float* weights) const;
+            const DeviceTensor& first_moment(const float* weights) const;
+            const DeviceTensor& second_moment(const float* weights) const;
+
+        private:
+            struct State
+            {
+                DeviceTensor m, v;
+                int t = 0;
+            };
+            struct Pending
+            {
+                float* w;
+                const float* g;
+                State* s;
+                int64_t n;
+                float bc1, bc2, lr;
+            };
+            void flush();
+
+            float beta1_, beta2_, epsilon_;
+            std::string device_;
+            std::unordered_map<const void*, State> states_;
+            std::vector<Pending> pending_;
+            int group_depth_ = 0;
+        };
+    } // namespace Optimizers
+} // namespace CppNet
+#endif

@@ -1,0 +1,199 @@
+"""ctypes front end of the C++ training harness (include/cppnet_train.h).
+
+A Session is a model built by libcppnet.so from the CppNet-compatible layer
+classes on device "gpu"; every step runs in C++/HIP.  The helpers here only
+describe the benchmark configurations and generate their synthetic data.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from . import _capi
+
+ACT = {"none": 0, "relu": 1, "sigmoid": 2, "tanh": 3}
+LOSS = {"bce": 0, "softmax_ce": 1, "mse": 2}
+
+_lib = None
+
+
+def load() -> C.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    _capi.load()  # libcnhip.so first (RTLD_GLOBAL)
+    path = _capi.LIBDIR / "libcppnet.so"
+    if not path.exists():
+        raise ImportError(f"{path} is missing: run `python -m cppnet_amd.build` first")
+    lib = C.CDLL(str(path))
+    vp, i32, i64, f32 = C.c_void_p, C.c_int, C.c_int64, C.c_float
+    sigs = {
+        "cnt_last_error": (C.c_char_p, []),
+        "cnt_mlp_create": (i32, [C.POINTER(vp), i32, C.POINTER(i64), i32, i32, i32, i64, f32, f32,
+                                 f32, f32, C.c_uint64]),
+        "cnt_destroy": (i32, [vp]),
+        "cnt_num_params": (i32, [vp, C.POINTER(i32)]),
+        "cnt_param_size": (i32, [vp, i32, C.POINTER(i64)]),
+        "cnt_set_param": (i32, [vp, i32, vp]),
+        "cnt_get_param": (i32, [vp, i32, vp]),
+        "cnt_get_grad": (i32, [vp, i32, vp]),
+        "cnt_set_batch": (i32, [vp, vp, vp]),
+        "cnt_set_batch_device": (i32, [vp, vp, vp]),
+        "cnt_step": (i32, [vp, C.POINTER(f32)]),
+        "cnt_synchronize": (i32, [vp]),
+        "cnt_stream": (vp, [vp]),
+    }
+    for name, (res, args) in sigs.items():
+        fn = getattr(lib, name)
+        fn.restype, fn.argtypes = res, args
+    _lib = lib
+    return lib
+
+
+def _check(st: int) -> None:
+    if st != 0:
+        raise _capi.CnhipError(f"cppnet_train status {st}: "
+                               f"{load().cnt_last_error().decode(errors='replace')}")
+
+
+@dataclass
+class MLPConfig:
+    name: str
+    sizes: list
+    hidden_act: str
+    out_act: str
+    loss: str
+    batch: int
+    lr: float = 1e-3
+    beta1: float = 0.9
+    beta2: float = 0.999
+    eps: float = 1e-8
+    seed: int = 1234
+    extra: dict = field(default_factory=dict)
+
+
+def mlp_config(config: int, batch: int | None = None) -> MLPConfig:
+    """BASELINE.json configs 1 and 2 (numbered from 1)."""
+    if config == 1:
+        c = MLPConfig("C1 MLP 30-64-1 sigmoid BCE", [30, 64, 1], "relu", "sigmoid", "bce", 512)
+    elif config == 2:
+        c = MLPConfig("C2 MLP 1024-4096-4096-10 softmax-CE", [1024, 4096, 4096, 10], "relu",
+                      "none", "softmax_ce", 4096)
+    else:
+        raise ValueError(f"config {config} is not an MLP config")
+    if batch is not None:
+        c.batch = batch
+    return c
+
+
+def xavier(rng: np.random.Generator, fan_in: int, fan_out: int) -> np.ndarray:
+    """xavier-uniform [fan_in, fan_out] (init.cpp:21-33), ColMajor flat."""
+    lim = np.sqrt(6.0 / (fan_in + fan_out))
+    return rng.uniform(-lim, lim, fan_in * fan_out).astype(np.float32)
+
+
+def synthetic_mlp(cfg: MLPConfig, rng: np.random.Generator):
+    """Parameters (W, b per layer; b = 0 as linear.cpp:75-80), X ~ N(0,1) and
+    targets (Bernoulli(0.5) for BCE, one-hot uniform labels for softmax-CE,
+    N(0,1) for MSE), all ColMajor flat float32."""
+    params = []
+    for i, o in zip(cfg.sizes[:-1], cfg.sizes[1:]):
+        params.append(xavier(rng, i, o))
+        params.append(np.zeros(o, np.float32))
+    B, I, O = cfg.batch, cfg.sizes[0], cfg.sizes[-1]
+    X = rng.standard_normal(B * I).astype(np.float32)
+    if cfg.loss == "bce":
+        Y = (rng.uniform(size=B * O) < 0.5).astype(np.float32)
+    elif cfg.loss == "softmax_ce":
+        labels = rng.integers(0, O, B)
+        Y = np.zeros((O, B), np.float32)
+        Y[labels, np.arange(B)] = 1.0
+        Y = Y.ravel()  # ColMajor [B, O]: column o = class o
+    else:
+        Y = rng.standard_normal(B * O).astype(np.float32)
+    return params, X, Y
+
+
+class Session:
+    """One C++ training session (model + loss + Adam + stream) on cuda:0."""
+
+    def __init__(self, cfg: MLPConfig):
+        lib = load()
+        sizes = (C.c_int64 * len(cfg.sizes))(*cfg.sizes)
+        h = C.c_void_p()
+        _check(lib.cnt_mlp_create(C.byref(h), len(cfg.sizes) - 1, sizes, ACT[cfg.hidden_act],
+                                  ACT[cfg.out_act], LOSS[cfg.loss], cfg.batch, cfg.lr, cfg.beta1,
+                                  cfg.beta2, cfg.eps, cfg.seed))
+        self.h = h
+        self.cfg = cfg
+
+    def close(self):
+        if self.h:
+            _check(load().cnt_destroy(self.h))
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def stream(self) -> int:
+        return load().cnt_stream(self.h) or 0
+
+    def num_params(self) -> int:
+        n = C.c_int()
+        _check(load().cnt_num_params(self.h, C.byref(n)))
+        return n.value
+
+    def param_size(self, i: int) -> int:
+        n = C.c_int64()
+        _check(load().cnt_param_size(self.h, i, C.byref(n)))
+        return n.value
+
+    def set_params(self, params) -> None:
+        assert len(params) == self.num_params()
+        for i, p in enumerate(params):
+            p = np.ascontiguousarray(p, np.float32)
+            assert p.size == self.param_size(i), f"param {i}: size {p.size} != {self.param_size(i)}"
+            _check(load().cnt_set_param(self.h, i, p.ctypes.data))
+
+    def get_params(self) -> list:
+        out = []
+        for i in range(self.num_params()):
+            a = np.empty(self.param_size(i), np.float32)
+            _check(load().cnt_get_param(self.h, i, a.ctypes.data))
+            out.append(a)
+        return out
+
+    def get_grads(self) -> list:
+        out = []
+        for i in range(self.num_params()):
+            a = np.empty(self.param_size(i), np.float32)
+            _check(load().cnt_get_grad(self.h, i, a.ctypes.data))
+            out.append(a)
+        return out
+
+    def set_batch(self, X: np.ndarray, Y: np.ndarray) -> None:
+        X = np.ascontiguousarray(X, np.float32)
+        Y = np.ascontiguousarray(Y, np.float32)
+        assert X.size == self.cfg.batch * self.cfg.sizes[0]
+        assert Y.size == self.cfg.batch * self.cfg.sizes[-1]
+        _check(load().cnt_set_batch(self.h, X.ctypes.data, Y.ctypes.data))
+
+    def set_batch_device(self, X_ptr: int, Y_ptr: int) -> None:
+        _check(load().cnt_set_batch_device(self.h, X_ptr, Y_ptr))
+
+    def step(self, read_loss: bool = True) -> float | None:
+        if read_loss:
+            loss = C.c_float()
+            _check(load().cnt_step(self.h, C.byref(loss)))
+            return loss.value
+        _check(load().cnt_step(self.h, None))
+        return None
+
+    def synchronize(self) -> None:
+        _check(load().cnt_synchronize(self.h))

@@ -58,6 +58,8 @@ int cnhip_stream_create(cnhip_stream_t* stream);
 int cnhip_stream_destroy(cnhip_stream_t stream);
 int cnhip_stream_synchronize(cnhip_stream_t stream);
 int cnhip_device_synchronize(void);
+/* 1 when ptr is device (or managed) memory of a HIP device, 0 otherwise. */
+int cnhip_is_device_pointer(const void* ptr);
 /* Events for timing on the stream the kernels run on. */
 int cnhip_event_create(void** event);
 int cnhip_event_destroy(void* event);
@@ -79,6 +81,15 @@ int cnhip_gemm_f32(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K,
                    const float* B, int64_t ldb, float beta,
                    float* C, int64_t ldc, const float* bias, int epilogue,
                    cnhip_stream_t stream);
+
+/* Measurement aid for the GEMM kernel (the MFMA-bound hot kernel): while
+ * enabled, every GEMM kernel launch on this host thread is bracketed by HIP
+ * events on its own stream, and its algorithmic flops (2*M*N*K) recorded.
+ * read() synchronises those events and returns the launch count, the summed
+ * kernel time (ms) and the summed flops since the last enable(1).  Split-K
+ * reduction launches are not counted.  Not a reference function. */
+int cnhip_gemm_timing_enable(int on);
+int cnhip_gemm_timing_read(int64_t* launches, double* total_ms, double* total_flops);
 
 /* ---- Linear ------------------------------------------------------------ */
 /* Y[B,O] = X[B,I] * W[I,O] + b[O]   (b may be NULL)

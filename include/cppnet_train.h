@@ -1,0 +1,68 @@
+/*
+ * cppnet_train.h — C ABI of the C++17 training harness (libcppnet.so).
+ *
+ * A session owns one model built from the CppNet-compatible layer classes
+ * (device "gpu"), its loss, an Adam optimizer, a dedicated HIP stream and the
+ * current batch, all resident in HBM.  cnt_step() runs exactly the
+ * reference harness's train step (benchmarks/mlp_benchmark.cpp:166-175):
+ *   model.zero_grad(); out = model.forward(X); loss = loss_fn.forward(out, Y);
+ *   g = loss_fn.backward(out, Y); model.backward(g); model.update(adam, lr)
+ * Parameters are indexed in layer order, weight before bias.  Host buffers
+ * are ColMajor float32 (Eigen's order).  Functions return 0 on success and
+ * a cnhip status code otherwise; cnt_last_error() has the message.
+ */
+#ifndef CPPNET_TRAIN_H
+#define CPPNET_TRAIN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct cnt_session cnt_session;
+
+#define CNT_ACT_NONE    0
+#define CNT_ACT_RELU    1
+#define CNT_ACT_SIGMOID 2
+#define CNT_ACT_TANH    3
+
+#define CNT_LOSS_BCE        0
+#define CNT_LOSS_SOFTMAX_CE 1
+#define CNT_LOSS_MSE        2
+
+const char* cnt_last_error(void);
+
+/* MLP: n_linear Linear layers with sizes[0] -> sizes[1] -> ... -> sizes[n_linear]
+ * (xavier init, bias), hidden_act after every layer but the last, out_act after
+ * the last, the given loss ("mean"), Adam(beta1, beta2, eps) at rate lr, batch
+ * rows per step.  Configs 1 and 2 of the benchmark are instances of it.
+ * ref: benchmarks/mlp_benchmark.cpp:85-192; README.md:112-137 */
+int cnt_mlp_create(cnt_session** out, int n_linear, const int64_t* sizes, int hidden_act,
+                   int out_act, int loss, int64_t batch, float lr, float beta1, float beta2,
+                   float eps, uint64_t seed);
+int cnt_destroy(cnt_session* s);
+
+int cnt_num_params(cnt_session* s, int* count);
+int cnt_param_size(cnt_session* s, int index, int64_t* n);
+int cnt_set_param(cnt_session* s, int index, const float* host);
+int cnt_get_param(cnt_session* s, int index, float* host);
+int cnt_get_grad(cnt_session* s, int index, float* host);
+
+/* Uploads one batch (X: [batch, in], Y: [batch, out]) that every later
+ * cnt_step() trains on, until the next call. */
+int cnt_set_batch(cnt_session* s, const float* x_host, const float* y_host);
+/* Same from device memory already in HBM (copied on the session stream). */
+int cnt_set_batch_device(cnt_session* s, const float* x_dev, const float* y_dev);
+
+/* One train step.  loss_out == NULL keeps the step fully asynchronous;
+ * otherwise the stream is synchronised and the step's loss written. */
+int cnt_step(cnt_session* s, float* loss_out);
+int cnt_synchronize(cnt_session* s);
+/* The hipStream_t the session's kernels run on. */
+void* cnt_stream(cnt_session* s);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,80 @@
+"""CPU oracle (test infrastructure): loader of oracle/liboracle.so and small
+helpers for Eigen ColMajor data.  Only tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg use it; the product (cppnet_amd) never does."""
+from __future__ import annotations
+
+import ctypes as C
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+ORACLE_DIR = Path(__file__).resolve().parent
+ORACLE_SO = ORACLE_DIR / "liboracle.so"
+
+_f = C.POINTER(C.c_float)
+i64, f32, i32 = C.c_int64, C.c_float, C.c_int
+_SIGS = {
+    "cnref_set_threads": (None, [i32]),
+    "cnref_get_threads": (i32, []),
+    "cnref_gemm_f32": (None, [i32, i32, i64, i64, i64, f32, _f, i64, _f, i64, f32, _f, i64, _f,
+                              i32]),
+    "cnref_linear_forward": (None, [_f, _f, _f, _f, i64, i64, i64]),
+    "cnref_linear_backward": (None, [_f, _f, _f, _f, _f, _f, i64, i64, i64, i32, i32]),
+    "cnref_column_sum": (None, [_f, _f, i64, i64, i32]),
+    "cnref_relu_forward": (None, [_f, _f, i64]),
+    "cnref_relu_backward": (None, [_f, _f, _f, i64]),
+    "cnref_sigmoid_forward": (None, [_f, _f, i64]),
+    "cnref_sigmoid_backward": (None, [_f, _f, _f, i64]),
+    "cnref_tanh_forward": (None, [_f, _f, i64]),
+    "cnref_tanh_backward": (None, [_f, _f, _f, i64]),
+    "cnref_bce_forward": (f32, [_f, _f, i64, i32]),
+    "cnref_bce_backward": (None, [_f, _f, _f, i64, i32]),
+    "cnref_mse_forward": (f32, [_f, _f, i64, i32]),
+    "cnref_mse_backward": (None, [_f, _f, _f, i64, i32]),
+    "cnref_softmax_ce_forward": (f32, [_f, _f, _f, i64, i64, i32]),
+    "cnref_softmax_ce_backward": (None, [_f, _f, _f, i64, i64, i32]),
+    "cnref_adam_step": (None, [_f, _f, _f, _f, i64, f32, f32, f32, f32, f32, f32]),
+    "cnref_bias_correction": (f32, [f32, i32]),
+}
+
+_lib = None
+
+
+def load_oracle():
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not ORACLE_SO.exists():
+        # Build from source (in this container; the GPU box receives the built file).
+        subprocess.run(["make", "-C", str(ORACLE_DIR)], check=True, stdout=subprocess.DEVNULL)
+    lib = C.CDLL(str(ORACLE_SO))
+    for name, (res, args) in _SIGS.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def fp(a: np.ndarray | None):
+    """float* of a float32 numpy buffer (None -> NULL)."""
+    if a is None:
+        return None
+    assert a.dtype == np.float32 and (a.flags["C_CONTIGUOUS"] or a.flags["F_CONTIGUOUS"])
+    return a.ctypes.data_as(_f)
+
+
+def colmajor(rows_logical) -> np.ndarray:
+    """Logical [[row0], [row1], ...] -> flat float32 in Eigen ColMajor order."""
+    a = np.asarray(rows_logical, dtype=np.float32)
+    if a.ndim == 1:
+        return a.copy()
+    return np.array(a.T, dtype=np.float32, order="C").ravel()
+
+
+def from_colmajor(flat: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    """Flat ColMajor buffer -> logical [rows, cols] array."""
+    return np.asarray(flat).reshape(cols, rows).T
+
+

@@ -1,0 +1,105 @@
+"""Model-level reference composed from the CPU oracle's ops (test
+infrastructure).  Runs the reference harness's train step
+(benchmarks/mlp_benchmark.cpp:166-175): zero_grad, forward, loss forward and
+backward, backward, Adam update per parameter with per-key step counts
+(adam.cpp:98-133).  Linear grads accumulate (linear.cpp:346-352) and are
+cleared by zero_grad (models.cpp:72-78)."""
+from __future__ import annotations
+
+import numpy as np
+
+from oracle import fp
+
+_RED_MEAN = 0
+
+
+class OracleMLP:
+    def __init__(self, cfg, oracle):
+        self.cfg = cfg
+        self.o = oracle
+        self.sizes = cfg.sizes
+        self.params = None
+        self.grads = None
+        self.m = None
+        self.v = None
+        self.t = None
+
+    def set_params(self, params):
+        self.params = [np.array(p, np.float32, copy=True) for p in params]
+        self.grads = [np.zeros_like(p) for p in self.params]
+        self.m = [np.zeros_like(p) for p in self.params]
+        self.v = [np.zeros_like(p) for p in self.params]
+        self.t = [0] * len(self.params)
+
+    def get_params(self):
+        return [p.copy() for p in self.params]
+
+    def _act(self, name, x):
+        y = np.empty_like(x)
+        if name == "relu":
+            self.o.cnref_relu_forward(fp(x), fp(y), x.size)
+        elif name == "sigmoid":
+            self.o.cnref_sigmoid_forward(fp(x), fp(y), x.size)
+        elif name == "tanh":
+            self.o.cnref_tanh_forward(fp(x), fp(y), x.size)
+        else:
+            return x
+        return y
+
+    def _act_bwd(self, name, y, g):
+        if name == "none":
+            return g
+        dx = np.empty_like(g)
+        getattr(self.o, f"cnref_{name}_backward")(fp(y), fp(g), fp(dx), g.size)
+        return dx
+
+    def step(self, X, Y):
+        o, B, cfg = self.o, self.cfg.batch, self.cfg
+        X = np.ascontiguousarray(X, np.float32)
+        Y = np.ascontiguousarray(Y, np.float32)
+        for g in self.grads:  # model.zero_grad()
+            g[...] = 0.0
+        nl = len(self.sizes) - 1
+        inputs, outs, acts = [], [], []
+        h = X
+        for i in range(nl):
+            I, O = self.sizes[i], self.sizes[i + 1]
+            z = np.empty(B * O, np.float32)
+            o.cnref_linear_forward(fp(h), fp(self.params[2 * i]), fp(self.params[2 * i + 1]),
+                                   fp(z), B, I, O)
+            inputs.append(h)
+            act = cfg.hidden_act if i + 1 < nl else cfg.out_act
+            h = self._act(act, z)
+            acts.append(act)
+            outs.append(h)
+        out = h
+        O = self.sizes[-1]
+        grad = np.empty_like(out)
+        if cfg.loss == "bce":
+            loss = o.cnref_bce_forward(fp(out), fp(Y), out.size, _RED_MEAN)
+            o.cnref_bce_backward(fp(out), fp(Y), fp(grad), out.size, _RED_MEAN)
+        elif cfg.loss == "softmax_ce":
+            sm = np.empty_like(out)
+            loss = o.cnref_softmax_ce_forward(fp(out), fp(Y), fp(sm), B, O, _RED_MEAN)
+            o.cnref_softmax_ce_backward(fp(sm), fp(Y), fp(grad), B, O, _RED_MEAN)
+        else:
+            loss = o.cnref_mse_forward(fp(out), fp(Y), out.size, _RED_MEAN)
+            o.cnref_mse_backward(fp(out), fp(Y), fp(grad), out.size, _RED_MEAN)
+        self.trace = []  # (layer input, dY at the layer output) per layer, for tolerances
+        for i in reversed(range(nl)):
+            I, O = self.sizes[i], self.sizes[i + 1]
+            grad = self._act_bwd(acts[i], outs[i], grad)
+            self.trace.insert(0, (inputs[i], grad.copy()))
+            dX = np.empty(B * I, np.float32)
+            o.cnref_linear_backward(fp(inputs[i]), fp(self.params[2 * i]), fp(grad),
+                                    fp(self.grads[2 * i]), fp(self.grads[2 * i + 1]), fp(dX), B, I,
+                                    O, 1, 1)
+            grad = dX
+        for k, (p, g) in enumerate(zip(self.params, self.grads)):  # model.update(adam, lr)
+            self.t[k] += 1
+            bc1 = o.cnref_bias_correction(cfg.beta1, self.t[k])
+            bc2 = o.cnref_bias_correction(cfg.beta2, self.t[k])
+            o.cnref_adam_step(fp(p), fp(g), fp(self.m[k]), fp(self.v[k]), p.size, cfg.lr,
+                              cfg.beta1, cfg.beta2, cfg.eps, bc1, bc2)
+        self.last_grads = [g.copy() for g in self.grads]
+        return float(loss)

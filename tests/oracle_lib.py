@@ -1,82 +1,10 @@
-"""Loads the CPU oracle (oracle/liboracle.so) for the tests, and small helpers
-for Eigen ColMajor data.  The oracle is test infrastructure: the product path
-never touches it."""
+"""Test-side access to the CPU oracle (oracle/) plus the tolerance helpers
+the parity tests share."""
 from __future__ import annotations
-
-import ctypes as C
-import subprocess
-from pathlib import Path
 
 import numpy as np
 
-ROOT = Path(__file__).resolve().parent.parent
-ORACLE_DIR = ROOT / "oracle"
-ORACLE_SO = ORACLE_DIR / "liboracle.so"
-
-_f = C.POINTER(C.c_float)
-i64, f32, i32 = C.c_int64, C.c_float, C.c_int
-_SIGS = {
-    "cnref_set_threads": (None, [i32]),
-    "cnref_get_threads": (i32, []),
-    "cnref_gemm_f32": (None, [i32, i32, i64, i64, i64, f32, _f, i64, _f, i64, f32, _f, i64, _f,
-                              i32]),
-    "cnref_linear_forward": (None, [_f, _f, _f, _f, i64, i64, i64]),
-    "cnref_linear_backward": (None, [_f, _f, _f, _f, _f, _f, i64, i64, i64, i32, i32]),
-    "cnref_column_sum": (None, [_f, _f, i64, i64, i32]),
-    "cnref_relu_forward": (None, [_f, _f, i64]),
-    "cnref_relu_backward": (None, [_f, _f, _f, i64]),
-    "cnref_sigmoid_forward": (None, [_f, _f, i64]),
-    "cnref_sigmoid_backward": (None, [_f, _f, _f, i64]),
-    "cnref_tanh_forward": (None, [_f, _f, i64]),
-    "cnref_tanh_backward": (None, [_f, _f, _f, i64]),
-    "cnref_bce_forward": (f32, [_f, _f, i64, i32]),
-    "cnref_bce_backward": (None, [_f, _f, _f, i64, i32]),
-    "cnref_mse_forward": (f32, [_f, _f, i64, i32]),
-    "cnref_mse_backward": (None, [_f, _f, _f, i64, i32]),
-    "cnref_softmax_ce_forward": (f32, [_f, _f, _f, i64, i64, i32]),
-    "cnref_softmax_ce_backward": (None, [_f, _f, _f, i64, i64, i32]),
-    "cnref_adam_step": (None, [_f, _f, _f, _f, i64, f32, f32, f32, f32, f32, f32]),
-    "cnref_bias_correction": (f32, [f32, i32]),
-}
-
-_lib = None
-
-
-def load_oracle():
-    global _lib
-    if _lib is not None:
-        return _lib
-    if not ORACLE_SO.exists():
-        # Build from source (in this container; the GPU box receives the built file).
-        subprocess.run(["make", "-C", str(ORACLE_DIR)], check=True, stdout=subprocess.DEVNULL)
-    lib = C.CDLL(str(ORACLE_SO))
-    for name, (res, args) in _SIGS.items():
-        fn = getattr(lib, name)
-        fn.restype = res
-        fn.argtypes = args
-    _lib = lib
-    return lib
-
-
-def fp(a: np.ndarray | None):
-    """float* of a float32 numpy buffer (None -> NULL)."""
-    if a is None:
-        return None
-    assert a.dtype == np.float32 and (a.flags["C_CONTIGUOUS"] or a.flags["F_CONTIGUOUS"])
-    return a.ctypes.data_as(_f)
-
-
-def colmajor(rows_logical) -> np.ndarray:
-    """Logical [[row0], [row1], ...] -> flat float32 in Eigen ColMajor order."""
-    a = np.asarray(rows_logical, dtype=np.float32)
-    if a.ndim == 1:
-        return a.copy()
-    return np.array(a.T, dtype=np.float32, order="C").ravel()
-
-
-def from_colmajor(flat: np.ndarray, rows: int, cols: int) -> np.ndarray:
-    """Flat ColMajor buffer -> logical [rows, cols] array."""
-    return np.asarray(flat).reshape(cols, rows).T
+from oracle import ORACLE_SO, colmajor, fp, from_colmajor, load_oracle  # noqa: F401
 
 
 def close(a, b, rtol=1e-4, atol=1e-5) -> tuple[bool, str]:
@@ -95,3 +23,39 @@ def close(a, b, rtol=1e-4, atol=1e-5) -> tuple[bool, str]:
         return False, (f"{int(bad.sum())}/{a.size} outside rtol={rtol} atol={atol}; worst at {i}:"
                        f" got {a.flat[i]!r} want {b.flat[i]!r}")
     return True, f"max abs err {err.max() if err.size else 0:.3g}"
+
+
+def close_mag(a, b, mag, rtol=1e-4, atol=1e-5) -> tuple[bool, str]:
+    """Condition-aware fp32 bound for contractions:
+    |a-b| <= atol + rtol * max(|b|, mag), where mag = (|A| |B|) / sqrt(K) is
+    the RMS size of the partial sums of each dot product.  Elementwise rel
+    1e-4 alone cannot hold where a length-K fp32 sum cancels to ~0 (both the
+    oracle's and the GPU's rounding are ~u*sqrt(K)*mag there)."""
+    b64 = np.abs(np.asarray(b, np.float64))
+    m64 = np.asarray(mag, np.float64)
+    return _close_lim(a, b, atol + rtol * np.maximum(b64, m64), rtol, atol)
+
+
+def _close_lim(a, b, lim, rtol, atol):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    if a.shape != b.shape:
+        return False, f"shape {a.shape} vs {b.shape}"
+    if not np.all(np.isfinite(a)):
+        return False, "non-finite values"
+    err = np.abs(a - b)
+    bad = err > lim
+    if bad.any():
+        i = int(np.argmax(err - lim))
+        return False, (f"{int(bad.sum())}/{a.size} outside rtol={rtol} atol={atol} (magnitude-aware);"
+                       f" worst at {i}: got {a.flat[i]!r} want {b.flat[i]!r} lim {lim.flat[i]!r}")
+    return True, f"max abs err {err.max() if err.size else 0:.3g}"
+
+
+def gemm_mag(oracle, ta, tb, M, N, K, A, lda, B, ldb, ldc):
+    """(|op(A)| |op(B)|) / sqrt(K) laid out like C (ld = ldc), via the oracle."""
+    mag = np.zeros(max(1, ldc * N), np.float32)
+    if K > 0:
+        oracle.cnref_gemm_f32(ta, tb, M, N, K, 1.0 / float(np.sqrt(K)), fp(np.abs(A)), lda,
+                              fp(np.abs(B)), ldb, 0.0, fp(mag), ldc, None, 0)
+    return mag[: ldc * N]
