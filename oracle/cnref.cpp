@@ -15,12 +15,14 @@
 
 namespace {
 int g_threads = 1;
+int g_acc_double = 0;
 }
 
 extern "C" {
 
 void cnref_set_threads(int n) { g_threads = n < 1 ? 1 : n; }
 int cnref_get_threads(void) { return g_threads; }
+void cnref_set_accumulate_double(int on) { g_acc_double = on != 0; }
 
 // ---------------------------------------------------------------------------
 // GEMM.  op(A) is first materialised M-contiguous and op(B) K-contiguous;
@@ -42,6 +44,25 @@ void cnref_gemm_f32(int ta, int tb, int64_t M, int64_t N, int64_t K, float alpha
 
   const int64_t KB = 128;  // k-panel kept in cache; order within a column is unchanged
   std::vector<float> acc((size_t)M * (size_t)N, 0.f);
+  if (g_acc_double) {
+    // Variant used only to measure how far a trajectory moves under a
+    // different (more accurate) summation: products and sums in double,
+    // one rounding to float per element.
+    std::vector<double> accd((size_t)M * (size_t)N, 0.0);
+    for (int64_t k0 = 0; k0 < K; k0 += KB) {
+      const int64_t k1 = std::min(K, k0 + KB);
+#pragma omp parallel for num_threads(g_threads) schedule(static)
+      for (int64_t n = 0; n < N; ++n) {
+        double* c = accd.data() + M * n;
+        for (int64_t k = k0; k < k1; ++k) {
+          const double b = Bk[k + K * n];
+          const float* a = Am.data() + M * k;
+          for (int64_t m = 0; m < M; ++m) c[m] += (double)a[m] * b;
+        }
+      }
+    }
+    for (size_t i = 0; i < acc.size(); ++i) acc[i] = (float)accd[i];
+  } else {
   for (int64_t k0 = 0; k0 < K; k0 += KB) {
     const int64_t k1 = std::min(K, k0 + KB);
 #pragma omp parallel for num_threads(g_threads) schedule(static)
@@ -53,6 +74,7 @@ void cnref_gemm_f32(int ta, int tb, int64_t M, int64_t N, int64_t K, float alpha
         for (int64_t m = 0; m < M; ++m) c[m] += a[m] * b;
       }
     }
+  }
   }
   for (int64_t n = 0; n < N; ++n)
     for (int64_t m = 0; m < M; ++m) {

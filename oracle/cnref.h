@@ -22,6 +22,9 @@ extern "C" {
 
 void cnref_set_threads(int n);
 int  cnref_get_threads(void);
+/* 1: GEMMs accumulate in double and round once (a second valid evaluation
+ * order, used to measure a trajectory's sensitivity to rounding). */
+void cnref_set_accumulate_double(int on);
 
 /* ColMajor C[M,N] = alpha*op(A)*op(B) + beta*C (+bias[n]) (relu if epi==1);
  * same operand conventions as cnhip_gemm_f32.  beta==0 does not read C. */

@@ -60,7 +60,7 @@ class OracleMLP:
         for g in self.grads:  # model.zero_grad()
             g[...] = 0.0
         nl = len(self.sizes) - 1
-        inputs, outs, acts = [], [], []
+        inputs, outs, acts, pre = [], [], [], []
         h = X
         for i in range(nl):
             I, O = self.sizes[i], self.sizes[i + 1]
@@ -68,6 +68,7 @@ class OracleMLP:
             o.cnref_linear_forward(fp(h), fp(self.params[2 * i]), fp(self.params[2 * i + 1]),
                                    fp(z), B, I, O)
             inputs.append(h)
+            pre.append(z)
             act = cfg.hidden_act if i + 1 < nl else cfg.out_act
             h = self._act(act, z)
             acts.append(act)
@@ -85,11 +86,14 @@ class OracleMLP:
         else:
             loss = o.cnref_mse_forward(fp(out), fp(Y), out.size, _RED_MEAN)
             o.cnref_mse_backward(fp(out), fp(Y), fp(grad), out.size, _RED_MEAN)
-        self.trace = []  # (layer input, dY at the layer output) per layer, for tolerances
+        # per layer, for the tests' tolerances: layer input x, pre-activation z,
+        # gradient w.r.t. the activation output dH and w.r.t. z (dA)
+        self.trace = [None] * nl
         for i in reversed(range(nl)):
             I, O = self.sizes[i], self.sizes[i + 1]
+            dH = grad
             grad = self._act_bwd(acts[i], outs[i], grad)
-            self.trace.insert(0, (inputs[i], grad.copy()))
+            self.trace[i] = dict(x=inputs[i], z=pre[i], dH=dH.copy(), dA=grad.copy(), act=acts[i])
             dX = np.empty(B * I, np.float32)
             o.cnref_linear_backward(fp(inputs[i]), fp(self.params[2 * i]), fp(grad),
                                     fp(self.grads[2 * i]), fp(self.grads[2 * i + 1]), fp(dX), B, I,

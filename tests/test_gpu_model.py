@@ -4,13 +4,22 @@ inputs and injected weights (tests/model_ref.py).
 
 Bars:
 * one step: loss and every parameter gradient within rel 1e-4 / abs 1e-5
-  (contractions magnitude-aware, see oracle_lib.close_mag);
+  (contractions magnitude-aware, see oracle_lib.close_mag), plus a ReLU-mask
+  allowance: where a pre-activation lies within forward tolerance of 0, fp32
+  rounding legitimately decides the mask either way, and the allowance is
+  the most that choice can move each gradient (its own layer and, through
+  dX, the layer below; _mask_allowance).  At most 1 in 10^4 entries of a
+  tensor may need that allowance;
 * updated weights after one step within the same bound, except where the
   reference gradient is itself within gradient tolerance of 0: Adam's first
   step moves W by ~lr*sign(g), so a sign that fp32 rounding cannot fix
   changes W by 2*lr.  Those elements are counted and must be that case;
 * after many steps: every step's loss within rel 1e-3, and each parameter
-  tensor within rel 1e-3 in norm.
+  tensor within rel 1e-3 in norm -- or, where Adam's sign sensitivity makes
+  the trajectory itself ill-conditioned, within twice the drift between two
+  valid CPU evaluations of the same run (the oracle in fp32 and the oracle
+  with double-accumulated contractions).  That drift is measured in the
+  test and printed.
 """
 import os
 
@@ -19,7 +28,7 @@ import pytest
 
 from cppnet_amd import trainer
 from model_ref import OracleMLP
-from oracle_lib import close, close_mag, gemm_mag
+from oracle_lib import close, close_mag, fp, gemm_mag
 
 pytestmark = pytest.mark.gpu
 
@@ -31,15 +40,58 @@ def oracle_mt(oracle):
 
 
 def _grad_mags(oracle, ref, cfg):
-    """Per-element magnitude (|X|^T|dY|)/sqrt(B) of each W grad, and the bias
-    analogue, from the oracle's own layer inputs and output grads."""
+    """Per-element magnitude (|X|^T|dA|)/sqrt(B) of each W grad, and the bias
+    analogue, from the oracle's own layer inputs and pre-activation grads."""
     mags = []
     B = cfg.batch
-    for i, (x, dy) in enumerate(ref.trace):
+    for i, tr in enumerate(ref.trace):
         I, O = cfg.sizes[i], cfg.sizes[i + 1]
-        mags.append(gemm_mag(oracle, 1, 0, I, O, B, x, B, dy, B, I))
-        mags.append(gemm_mag(oracle, 1, 0, 1, O, B, np.ones(B, np.float32), B, dy, B, 1))
+        mags.append(gemm_mag(oracle, 1, 0, I, O, B, tr["x"], B, tr["dA"], B, I))
+        mags.append(gemm_mag(oracle, 1, 0, 1, O, B, np.ones(B, np.float32), B, tr["dA"], B, 1))
     return mags
+
+
+def _mask_allowance(oracle, ref, cfg, params):
+    """Bound on what ReLU-mask choices at near-zero pre-activations can change.
+
+    S_l = {(b,o): |z_l| <= tau_l} with tau_l the forward bound of z_l
+    (1e-5 + 1e-4 max(|z|, (|x||W|)/sqrt(I)) + |b|-rounding).  Flipping mask
+    entries of S_l changes dA_l by at most E_l = |dH_l| on S_l, and, through
+    dX_l = dA_l W_l^T, changes dH_{l-1} by at most E_l |W_l|^T.  Each
+    gradient's allowance is the contraction of |x_l| with the total change of
+    dA_l (own flips + masked upstream change)."""
+    B = cfg.batch
+    nl = len(ref.trace)
+    E = [None] * nl            # |change of dA_l| from flips at layer l, ColMajor [B,O_l]
+    up = [None] * nl           # |change of dH_l| from flips at layer l+1
+    for i, tr in enumerate(ref.trace):
+        I, O = cfg.sizes[i], cfg.sizes[i + 1]
+        if tr["act"] != "relu":
+            E[i] = np.zeros(B * O, np.float32)
+            continue
+        zmag = gemm_mag(oracle, 0, 0, B, O, I, tr["x"], B, params[2 * i], I, B)
+        tau = 1e-5 + 1e-4 * np.maximum(np.abs(tr["z"]), zmag)
+        amb = np.abs(tr["z"]) <= tau
+        E[i] = np.where(amb, np.abs(tr["dH"]), 0.0).astype(np.float32)
+    allow = []
+    for i, tr in enumerate(ref.trace):
+        I, O = cfg.sizes[i], cfg.sizes[i + 1]
+        dchg = E[i].copy()
+        if i + 1 < nl:
+            O2 = cfg.sizes[i + 2]
+            d_up = np.zeros(B * O, np.float32)   # |E_{l+1}| |W_{l+1}|^T : [B, O]
+            oracle.cnref_gemm_f32(0, 1, B, O, O2, 1.0, fp(E[i + 1]), B,
+                                  fp(np.abs(params[2 * (i + 1)])), O, 0.0, fp(d_up), B, None, 0)
+            mask = (tr["z"] > 0).astype(np.float32) if tr["act"] == "relu" else 1.0
+            dchg = dchg + d_up * np.maximum(mask, (E[i] > 0))
+        dchg = dchg.astype(np.float32)
+        aW = np.zeros(I * O, np.float32)
+        oracle.cnref_gemm_f32(1, 0, I, O, B, 1.0, fp(np.abs(tr["x"])), B, fp(dchg), B, 0.0,
+                              fp(aW), I, None, 0)
+        ab = np.zeros(O, np.float32)
+        oracle.cnref_column_sum(fp(dchg), fp(ab), B, O, 0)
+        allow += [aW, ab]
+    return allow
 
 
 def _one_step(oracle, cfg, seed):
@@ -52,58 +104,87 @@ def _one_step(oracle, cfg, seed):
     ref.set_params(params)
     loss_gpu = sess.step()
     loss_ref = ref.step(X, Y)
-    return sess, ref, loss_gpu, loss_ref
+    return sess, ref, params, loss_gpu, loss_ref
 
 
 @pytest.mark.parametrize("config,batch", [(1, None), (2, 256), (2, None)])
 def test_one_step_parity(gpu, oracle_mt, config, batch):
     cfg = trainer.mlp_config(config, batch)
     print(f"[model] config {config} batch {cfg.batch}: one step", flush=True)
-    sess, ref, loss_gpu, loss_ref = _one_step(oracle_mt, cfg, seed=100 + config)
+    sess, ref, params, loss_gpu, loss_ref = _one_step(oracle_mt, cfg, seed=100 + config)
     ok, msg = close([loss_gpu], [loss_ref], 1e-4, 1e-5)
     assert ok, f"loss: {msg}"
     mags = _grad_mags(oracle_mt, ref, cfg)
+    allow = _mask_allowance(oracle_mt, ref, cfg, params)
     g_gpu = sess.get_grads()
-    for k, (a, b, mag) in enumerate(zip(g_gpu, ref.last_grads, mags)):
+    n_allow = 0
+    for k, (a, b, mag, al) in enumerate(zip(g_gpu, ref.last_grads, mags, allow)):
         ok, msg = close_mag(a, b, mag, 1e-4, 1e-5)
-        assert ok, f"grad of param {k}: {msg}"
+        if not ok:
+            lim = 1e-5 + 1e-4 * np.maximum(np.abs(b), mag) + al
+            err = np.abs(a.astype(np.float64) - b)
+            bad = err > lim
+            assert not bad.any(), (f"grad of param {k}: {int(bad.sum())} outside tolerance + "
+                                   f"mask allowance ({msg})")
+            needed = int((err > 1e-5 + 1e-4 * np.maximum(np.abs(b), mag)).sum())
+            # the allowance is a loose upper bound: it may only rescue a handful of entries
+            assert needed <= max(1, a.size // 10000), (
+                f"grad of param {k}: {needed} entries needed the mask allowance ({msg})")
+            n_allow += needed
     w_gpu = sess.get_params()
     flips = 0
-    for k, (a, b, g, mag) in enumerate(zip(w_gpu, ref.get_params(), ref.last_grads, mags)):
+    for k, (a, b, g, mag, al) in enumerate(zip(w_gpu, ref.get_params(), ref.last_grads, mags,
+                                               allow)):
         err = np.abs(a.astype(np.float64) - b)
         lim = 1e-5 + 1e-4 * np.abs(b)
         bad = err > lim
-        g_tol = 1e-5 + 1e-4 * np.maximum(np.abs(g), mag)
+        g_tol = 1e-5 + 1e-4 * np.maximum(np.abs(g), mag) + al
         unexplained = bad & (np.abs(g) > g_tol)
         assert not unexplained.any(), (
             f"param {k}: {int(unexplained.sum())} weights differ where the gradient is well "
             f"conditioned (max err {err[unexplained].max():.3g})")
         flips += int(bad.sum())
     total = sum(p.size for p in w_gpu)
-    print(f"[model] config {config}: loss {loss_gpu:.7f} vs {loss_ref:.7f}; "
-          f"{flips}/{total} updated weights differ, all at |g| within gradient tolerance of 0")
+    print(f"[model] config {config}: loss {loss_gpu:.7f} vs {loss_ref:.7f}; {n_allow} grads "
+          f"needed the ReLU-mask allowance; {flips}/{total} updated weights differ, all at |g| "
+          f"within gradient tolerance of 0")
     sess.close()
 
 
-@pytest.mark.parametrize("config,batch,steps", [(1, None, 100), (2, 128, 8)])
+def _rel(a, b):
+    return float(np.linalg.norm(a.astype(np.float64) - b) / max(np.linalg.norm(b), 1e-30))
+
+
+@pytest.mark.parametrize("config,batch,steps", [(1, None, 100), (2, 128, 20)])
 def test_multi_step_parity(gpu, oracle_mt, config, batch, steps):
     cfg = trainer.mlp_config(config, batch)
     print(f"[model] config {config} batch {cfg.batch}: {steps} steps", flush=True)
     rng = np.random.default_rng(7 + config)
-    params, X, Y = trainer.synthetic_mlp(cfg, rng)
+    params, _, _ = trainer.synthetic_mlp(cfg, rng)
+    batches = [trainer.synthetic_mlp(cfg, rng)[1:] for _ in range(steps)]
     sess = trainer.Session(cfg)
     sess.set_params(params)
     ref = OracleMLP(cfg, oracle_mt)
     ref.set_params(params)
-    for step in range(steps):
+    ref_d = OracleMLP(cfg, oracle_mt)  # same run, double-accumulated contractions
+    ref_d.set_params(params)
+    for step, (X, Y) in enumerate(batches):
         # a fresh batch each step, as a data loader would provide
-        _, X, Y = trainer.synthetic_mlp(cfg, rng)
         sess.set_batch(X, Y)
         lg, lr_ = sess.step(), ref.step(X, Y)
+        oracle_mt.cnref_set_accumulate_double(1)
+        try:
+            ref_d.step(X, Y)
+        finally:
+            oracle_mt.cnref_set_accumulate_double(0)
         assert abs(lg - lr_) <= 1e-3 * abs(lr_) + 1e-6, f"step {step}: loss {lg} vs {lr_}"
-    for k, (a, b) in enumerate(zip(sess.get_params(), ref.get_params())):
-        rel = np.linalg.norm(a.astype(np.float64) - b) / max(np.linalg.norm(b), 1e-30)
-        assert rel <= 1e-3, f"param {k}: relative norm error {rel:.3g} after {steps} steps"
+    for k, (a, b, c) in enumerate(zip(sess.get_params(), ref.get_params(), ref_d.get_params())):
+        rel, drift = _rel(a, b), _rel(c, b)
+        print(f"[model] config {config} param {k}: gpu-vs-oracle {rel:.3g}, oracle fp32-vs-fp64acc "
+              f"{drift:.3g} after {steps} steps")
+        assert rel <= max(1e-3, 2.0 * drift), (
+            f"param {k}: relative norm error {rel:.3g} after {steps} steps "
+            f"(oracle's own rounding drift {drift:.3g})")
     sess.close()
 
 
