@@ -40,6 +40,8 @@ SIGNATURES: dict[str, tuple] = {
     "cnhip_event_elapsed_ms": (i32, [C.POINTER(f32), vp, vp]),
     "cnhip_gemm_f32": (i32, [i32, i32, i64, i64, i64, f32, vp, i64, vp, i64, f32, vp, i64, vp,
                              i32, vp]),
+    "cnhip_gemm_f32_batched": (i32, [i32, i32, i64, i64, i64, f32, vp, i64, i64, vp, i64, i64,
+                                     f32, vp, i64, i64, i64, vp]),
     "cnhip_gemm_timing_enable": (i32, [i32]),
     "cnhip_gemm_timing_read": (i32, [C.POINTER(i64), C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     "cnhip_linear_forward": (i32, [vp, vp, vp, vp, i64, i64, i64, vp]),

@@ -1,7 +1,8 @@
 // Bandwidth-bound kernels: activation forward/backward and the loss
 // functions of the hot path.  Each activation kernel streams float4s
-// through a grid-stride loop sized to fill the 256 CUs; losses reduce in a
-// single block in a fixed order (deterministic, no atomics, no workspace).
+// through a grid-stride loop sized to fill the 256 CUs.  Loss values are
+// reduced in a fixed order (deterministic, no atomics): BCE and MSE in one
+// block, softmax-CE per row block and then over the block partials.
 //
 // Arithmetic follows the cpu-eigen branches operation by operation:
 //   ReLU     relu.cpp:97-225          Sigmoid   sigmoid.cpp:97-231
@@ -178,13 +179,18 @@ __global__ void __launch_bounds__(256) mse_backward_kernel(const float* __restri
 }
 
 // Softmax-CE over ColMajor [B, C]: row b lives at b + B*c, so consecutive
-// threads take consecutive rows and every class loop reads coalesced.
-__global__ void __launch_bounds__(RB) softmax_ce_forward_kernel(
+// threads take consecutive rows and every class loop reads coalesced.  Each
+// block writes the sum of its rows' losses to partial[blockIdx.x]; a second
+// single-block kernel adds the partials in block order (deterministic).
+constexpr int SCE_BLOCK = 256;
+
+__global__ void __launch_bounds__(SCE_BLOCK) softmax_ce_rows_kernel(
     const float* __restrict__ z, const float* __restrict__ t, float* __restrict__ sm,
-    float* __restrict__ loss, int64_t B, int64_t C, int reduction) {
-  __shared__ float smem[RB / 64];
-  float s = 0.f;
-  for (int64_t b = threadIdx.x; b < B; b += RB) {
+    float* __restrict__ partial, int64_t B, int64_t C) {
+  __shared__ float smem[SCE_BLOCK / 64];
+  float row = 0.f;
+  const int64_t b = (int64_t)blockIdx.x * SCE_BLOCK + threadIdx.x;
+  if (b < B) {
     float mx = z[b];
     for (int64_t c = 1; c < C; ++c) mx = fmaxf(mx, z[b + B * c]);
     float se = 0.f;
@@ -194,15 +200,32 @@ __global__ void __launch_bounds__(RB) softmax_ce_forward_kernel(
       se += e;
     }
     const float ls = logf(se + 1e-12f);
-    float row = 0.f;
     for (int64_t c = 0; c < C; ++c) {
       sm[b + B * c] = sm[b + B * c] / se;
       row -= t[b + B * c] * ((z[b + B * c] - mx) - ls);
     }
-    s += row;
   }
+  // fixed-order block sum
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) row += __shfl_xor(row, off, 64);
+  if (lane == 0) smem[wave] = row;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float s = 0.f;
+    for (int w = 0; w < SCE_BLOCK / 64; ++w) s += smem[w];
+    partial[blockIdx.x] = s;
+  }
+}
+
+__global__ void __launch_bounds__(RB) partial_sum_kernel(const float* __restrict__ partial,
+                                                         int64_t count, float* __restrict__ out,
+                                                         float divisor) {
+  __shared__ float smem[RB / 64];
+  float s = 0.f;
+  for (int64_t i = threadIdx.x; i < count; i += RB) s += partial[i];
   const float tot = block_sum(s, smem);
-  if (threadIdx.x == 0) *loss = (reduction == CNHIP_REDUCE_MEAN) ? tot / (float)B : tot;
+  if (threadIdx.x == 0) *out = tot / divisor;
 }
 
 __global__ void __launch_bounds__(256) softmax_ce_backward_kernel(const float* __restrict__ sm,
@@ -303,9 +326,24 @@ int cnhip_softmax_ce_forward(const float* logits, const float* targets, float* s
   CNHIP_TRY(cnhip::check_reduction(reduction, who));
   CNHIP_REQUIRE(batch > 0 && classes > 0, "%s: empty input", who);
   CNHIP_REQUIRE(logits && targets && softmax_out && loss, "%s: NULL pointer", who);
-  hipLaunchKernelGGL(cnhip::softmax_ce_forward_kernel, dim3(1), dim3(cnhip::RB), 0, as_stream(s),
-                     logits, targets, softmax_out, loss, batch, classes, reduction);
-  return cnhip::check_launch(who);
+  hipStream_t st = as_stream(s);
+  const int64_t blocks = (batch + cnhip::SCE_BLOCK - 1) / cnhip::SCE_BLOCK;
+  CNHIP_REQUIRE(blocks < ((int64_t)1 << 31), "%s: batch too large", who);
+  void* ws = nullptr;
+  CNHIP_TRY(cnhip::check_hip(hipMallocAsync(&ws, (size_t)blocks * sizeof(float), st), who));
+  float* partial = static_cast<float*>(ws);
+  hipLaunchKernelGGL(cnhip::softmax_ce_rows_kernel, dim3((unsigned)blocks), dim3(cnhip::SCE_BLOCK),
+                     0, st, logits, targets, softmax_out, partial, batch, classes);
+  int status = cnhip::check_launch(who);
+  if (status == CNHIP_OK) {
+    // "mean" divides the summed loss by the batch size (softmax_cross_entropy.cpp:154-156)
+    const float divisor = reduction == CNHIP_REDUCE_MEAN ? (float)batch : 1.0f;
+    hipLaunchKernelGGL(cnhip::partial_sum_kernel, dim3(1), dim3(cnhip::RB), 0, st, partial, blocks,
+                       loss, divisor);
+    status = cnhip::check_launch(who);
+  }
+  const int st2 = cnhip::check_hip(hipFreeAsync(ws, st), who);
+  return status != CNHIP_OK ? status : st2;
 }
 
 int cnhip_softmax_ce_backward(const float* softmax, const float* targets, float* grad,

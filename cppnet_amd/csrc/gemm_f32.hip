@@ -4,13 +4,15 @@
 //
 // One kernel template covers the three shapes a Linear layer needs
 // (forward NN, weight-grad TN, input-grad NT; ref: matmul.cu:16-71,
-// matmul_grad_weight.cu:14-69, matmul_grad_input.cu:14-68).  The reference
-// computes one output per thread with atomicAdd accumulation; here a 256-
-// thread block owns a 128x128 tile, each 64-wide wavefront a 64x64 sub-tile
-// (2x2 MFMA 32x32 blocks, 64 accumulators per lane), K advances 16 at a time
-// through double-buffered LDS, and no atomics are used: split-K partials go
-// to a stream-ordered workspace and are summed by a second kernel in a fixed
-// order, so results are deterministic.
+// matmul_grad_weight.cu:14-69, matmul_grad_input.cu:14-68) and the batched
+// products of the recurrent and attention layers.  The reference computes one
+// output per thread with atomicAdd accumulation.  Here a block of
+// WGM x WGN wave64s owns a (WGM*WM*32) x (WGN*WN*32) output tile; each wave
+// holds WM x WN accumulator blocks of one 32x32 MFMA (16 floats per lane
+// each); K advances 16 at a time through double-buffered LDS staged from
+// registers; no atomics are used.  When the output tiles alone cannot fill
+// the 256 CUs, K is split across blocks into a stream-ordered workspace and
+// the partials are summed in a fixed order, so results are deterministic.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -24,91 +26,109 @@ namespace {
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int BM = 128;
-constexpr int BN = 128;
 constexpr int BK = 16;
-constexpr int NT = 256;          // threads per block (4 wavefronts)
-constexpr int LDS_STRIDE = 132;  // floats per k-row of a staged tile (128 + 4 pad)
-constexpr int TILE_FLOATS = BK * LDS_STRIDE;
+
+template <int WGM_, int WGN_, int WM_, int WN_>
+struct TileCfg {
+  static constexpr int WGM = WGM_, WGN = WGN_, WM = WM_, WN = WN_;
+  static constexpr int BM = WGM * WM * 32;
+  static constexpr int BN = WGN * WN * 32;
+  static constexpr int NT = WGM * WGN * 64;
+  // k-major LDS rows padded by 4 floats: keeps float4 stores aligned and
+  // spreads the 4 k-rows a KCONTIG tile store touches over distinct banks.
+  static constexpr int LDA = BM + 4;
+  static constexpr int LDB = BN + 4;
+};
+using CfgL = TileCfg<2, 2, 2, 2>;   // 128 x 128, 4 waves, 64x64 per wave
+using CfgSN = TileCfg<4, 1, 1, 1>;  // 128 x 32 : N <= 32
+using CfgSM = TileCfg<1, 4, 1, 1>;  // 32 x 128 : M <= 32
+using CfgS = TileCfg<2, 2, 1, 1>;   // 64 x 64  : small problems
 
 struct GemmArgs {
   int64_t M, N, K;
   const float* A;
-  int64_t lda;
+  int64_t lda, stride_a;  // stride_a: elements between batch entries
   const float* B;
-  int64_t ldb;
+  int64_t ldb, stride_b;
   float* C;
-  int64_t ldc;
+  int64_t ldc, stride_c;
   float alpha, beta;
   const float* bias;
   int epilogue;
-  int vec_ok;            // every ld % 4 == 0 and A, B 16-byte aligned
-  int c_vec_ok;          // ldc % 4 == 0 and C 16-byte aligned
+  int vec_ok;            // every ld and stride % 4 == 0 and A, B 16-byte aligned
+  int c_vec_ok;          // ldc, stride_c % 4 == 0 and C 16-byte aligned
   int64_t k_per_split;   // multiple of BK
-  float* partial;        // split-K workspace [splits][M*N], ColMajor ld=M; null = direct
+  float* partial;        // split-K workspace [batch][splits][M*N]; null = direct
+  int splits;
 };
 
-// Staging of one operand tile (128 rows of the outer dim x 16 of K) into
+// Stages one operand tile (R rows of the outer dim x 16 of K) into
 // registers.  KCONTIG: X(r,k) = X[k + ld*r]  (else X[r + ld*k]).
-// Each thread moves 2 float4 (512 float4 per tile).
-template <bool KCONTIG>
-__device__ __forceinline__ void load_tile(const float* __restrict__ X, int64_t ld, int64_t r0,
-                                          int64_t k0, int64_t R, int64_t K, bool fast,
-                                          f32x4 (&regs)[2]) {
-  const int tid = threadIdx.x;
+template <bool KCONTIG, int R, int NT>
+struct TileLoader {
+  static constexpr int F4 = R * BK / 4;                 // float4 per tile
+  static constexpr int PER_THREAD = (F4 + NT - 1) / NT;
+
+  __device__ __forceinline__ static void load(const float* __restrict__ X, int64_t ld, int64_t r0,
+                                              int64_t k0, int64_t Rtot, int64_t K, bool fast,
+                                              f32x4 (&regs)[PER_THREAD]) {
 #pragma unroll
-  for (int p = 0; p < 2; ++p) {
-    const int idx = tid + NT * p;
-    int rr, kk;
-    if (KCONTIG) {
-      rr = idx >> 2;
-      kk = (idx & 3) * 4;
-    } else {
-      kk = idx >> 5;
-      rr = (idx & 31) * 4;
-    }
-    const int64_t r = r0 + rr, k = k0 + kk;
-    if (fast) {
-      const float* src = KCONTIG ? (X + k + ld * r) : (X + r + ld * k);
-      regs[p] = *reinterpret_cast<const f32x4*>(src);
-    } else {
-      f32x4 v;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int64_t rj = KCONTIG ? r : r + j;
-        const int64_t kj = KCONTIG ? k + j : k;
-        float x = 0.f;
-        if (rj < R && kj < K) x = KCONTIG ? X[kj + ld * rj] : X[rj + ld * kj];
-        v[j] = x;
+    for (int p = 0; p < PER_THREAD; ++p) {
+      const int idx = threadIdx.x + NT * p;
+      if (F4 % NT != 0 && idx >= F4) break;
+      int rr, kk;
+      if (KCONTIG) {
+        rr = idx >> 2;
+        kk = (idx & 3) * 4;
+      } else {
+        kk = idx / (R / 4);
+        rr = (idx % (R / 4)) * 4;
       }
-      regs[p] = v;
+      const int64_t r = r0 + rr, k = k0 + kk;
+      if (fast) {
+        const float* src = KCONTIG ? (X + k + ld * r) : (X + r + ld * k);
+        regs[p] = *reinterpret_cast<const f32x4*>(src);
+      } else {
+        f32x4 v;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int64_t rj = KCONTIG ? r : r + j;
+          const int64_t kj = KCONTIG ? k + j : k;
+          float x = 0.f;
+          if (rj < Rtot && kj < K) x = KCONTIG ? X[kj + ld * rj] : X[rj + ld * kj];
+          v[j] = x;
+        }
+        regs[p] = v;
+      }
     }
   }
-}
 
-// Writes a staged tile into LDS as [k][r] rows (r contiguous) so that an
-// MFMA fragment read (lane -> r = lane%32, k = lane/32) is one conflict-free
-// ds_read_b32.
-template <bool KCONTIG>
-__device__ __forceinline__ void store_tile(float* __restrict__ lds, const f32x4 (&regs)[2]) {
-  const int tid = threadIdx.x;
+  // Writes the staged tile into LDS as [k][r] rows (r contiguous, row stride
+  // R+4), so an MFMA fragment read (lane -> r = lane%32, k = lane/32) is one
+  // conflict-free ds_read_b32.
+  __device__ __forceinline__ static void store(float* __restrict__ lds,
+                                               const f32x4 (&regs)[PER_THREAD]) {
+    constexpr int LD = R + 4;
 #pragma unroll
-  for (int p = 0; p < 2; ++p) {
-    const int idx = tid + NT * p;
-    if (KCONTIG) {
-      const int rr = idx >> 2, kk = (idx & 3) * 4;
+    for (int p = 0; p < PER_THREAD; ++p) {
+      const int idx = threadIdx.x + NT * p;
+      if (F4 % NT != 0 && idx >= F4) break;
+      if (KCONTIG) {
+        const int rr = idx >> 2, kk = (idx & 3) * 4;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) lds[(kk + j) * LDS_STRIDE + rr] = regs[p][j];
-    } else {
-      const int kk = idx >> 5, rr = (idx & 31) * 4;
-      *reinterpret_cast<f32x4*>(lds + kk * LDS_STRIDE + rr) = regs[p];
+        for (int j = 0; j < 4; ++j) lds[(kk + j) * LD + rr] = regs[p][j];
+      } else {
+        const int kk = idx / (R / 4), rr = (idx % (R / 4)) * 4;
+        *reinterpret_cast<f32x4*>(lds + kk * LD + rr) = regs[p];
+      }
     }
   }
-}
+};
 
-__device__ __forceinline__ float epilogue_value(const GemmArgs& g, float acc, int64_t m, int64_t n) {
+__device__ __forceinline__ float epilogue_value(const GemmArgs& g, const float* C, float acc,
+                                                int64_t m, int64_t n) {
   float v = g.alpha * acc;
-  if (g.beta != 0.f) v += g.beta * g.C[m + g.ldc * n];
+  if (g.beta != 0.f) v += g.beta * C[m + g.ldc * n];
   if (g.bias) v += g.bias[n];
   if (g.epilogue == CNHIP_EPI_RELU) v = fmaxf(v, 0.f);
   return v;
@@ -134,43 +154,49 @@ __device__ __forceinline__ void tile_of_block(int nbm, int nbn, int& tm, int& tn
   tn = in_group / gsz;
 }
 
-template <bool TA, bool TB>
-__global__ void __launch_bounds__(NT, 2) gemm_f32_kernel(GemmArgs g) {
-  __shared__ float lds_a[2][TILE_FLOATS];
-  __shared__ float lds_b[2][TILE_FLOATS];
+template <bool TA, bool TB, class Cfg>
+__global__ void __launch_bounds__(Cfg::NT, 2) gemm_f32_kernel(GemmArgs g) {
+  constexpr int BM = Cfg::BM, BN = Cfg::BN, NT = Cfg::NT;
+  using LA = TileLoader<TA, BM, NT>;
+  using LB = TileLoader<!TB, BN, NT>;
+  __shared__ float lds_a[2][BK * Cfg::LDA];
+  __shared__ float lds_b[2][BK * Cfg::LDB];
 
   const int nbm = (int)((g.M + BM - 1) / BM);
   const int nbn = (int)((g.N + BN - 1) / BN);
   int tm, tn;
   tile_of_block(nbm, nbn, tm, tn);
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+  const int64_t batch = blockIdx.y;
+  const float* A = g.A + batch * g.stride_a;
+  const float* B = g.B + batch * g.stride_b;
 
   const int64_t k_begin = (int64_t)blockIdx.z * g.k_per_split;
   const int64_t k_end = min(g.K, k_begin + g.k_per_split);
-  const int ntiles = (int)((k_end - k_begin + BK - 1) / BK);
+  const int ntiles = k_end > k_begin ? (int)((k_end - k_begin + BK - 1) / BK) : 0;
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int wm = wave & 1, wn = wave >> 1;
+  const int wm = wave % Cfg::WGM, wn = wave / Cfg::WGM;
   const int l32 = lane & 31, lhi = lane >> 5;
 
   const bool full_mn = (m0 + BM <= g.M) && (n0 + BN <= g.N);
 
-  f32x16 acc[2][2];
+  f32x16 acc[Cfg::WM][Cfg::WN];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < Cfg::WM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < Cfg::WN; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  f32x4 ra[2], rb[2];
+  f32x4 ra[LA::PER_THREAD], rb[LB::PER_THREAD];
   if (ntiles > 0) {
     const bool fast = g.vec_ok && full_mn && (k_begin + BK <= k_end);
-    load_tile<TA>(g.A, g.lda, m0, k_begin, g.M, k_end, fast, ra);
-    load_tile<!TB>(g.B, g.ldb, n0, k_begin, g.N, k_end, fast, rb);
-    store_tile<TA>(lds_a[0], ra);
-    store_tile<!TB>(lds_b[0], rb);
+    LA::load(A, g.lda, m0, k_begin, g.M, k_end, fast, ra);
+    LB::load(B, g.ldb, n0, k_begin, g.N, k_end, fast, rb);
+    LA::store(lds_a[0], ra);
+    LB::store(lds_b[0], rb);
   }
   __syncthreads();
 
@@ -180,26 +206,28 @@ __global__ void __launch_bounds__(NT, 2) gemm_f32_kernel(GemmArgs g) {
     if (has_next) {
       const int64_t kn = k_begin + (int64_t)(kt + 1) * BK;
       const bool fast = g.vec_ok && full_mn && (kn + BK <= k_end);
-      load_tile<TA>(g.A, g.lda, m0, kn, g.M, k_end, fast, ra);
-      load_tile<!TB>(g.B, g.ldb, n0, kn, g.N, k_end, fast, rb);
+      LA::load(A, g.lda, m0, kn, g.M, k_end, fast, ra);
+      LB::load(B, g.ldb, n0, kn, g.N, k_end, fast, rb);
     }
-    const float* la = lds_a[cur] + wm * 64 + l32;
-    const float* lb = lds_b[cur] + wn * 64 + l32;
+    const float* la = lds_a[cur] + wm * (Cfg::WM * 32) + l32;
+    const float* lb = lds_b[cur] + wn * (Cfg::WN * 32) + l32;
 #pragma unroll
     for (int s = 0; s < BK / 2; ++s) {
       const int k = 2 * s + lhi;
-      const float a0 = la[k * LDS_STRIDE];
-      const float a1 = la[k * LDS_STRIDE + 32];
-      const float b0 = lb[k * LDS_STRIDE];
-      const float b1 = lb[k * LDS_STRIDE + 32];
-      acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc[0][0], 0, 0, 0);
-      acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, acc[0][1], 0, 0, 0);
-      acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc[1][0], 0, 0, 0);
-      acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
+      float a[Cfg::WM], b[Cfg::WN];
+#pragma unroll
+      for (int i = 0; i < Cfg::WM; ++i) a[i] = la[k * Cfg::LDA + 32 * i];
+#pragma unroll
+      for (int j = 0; j < Cfg::WN; ++j) b[j] = lb[k * Cfg::LDB + 32 * j];
+#pragma unroll
+      for (int i = 0; i < Cfg::WM; ++i)
+#pragma unroll
+        for (int j = 0; j < Cfg::WN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
     }
     if (has_next) {
-      store_tile<TA>(lds_a[cur ^ 1], ra);
-      store_tile<!TB>(lds_b[cur ^ 1], rb);
+      LA::store(lds_a[cur ^ 1], ra);
+      LB::store(lds_b[cur ^ 1], rb);
     }
     __syncthreads();
   }
@@ -207,33 +235,32 @@ __global__ void __launch_bounds__(NT, 2) gemm_f32_kernel(GemmArgs g) {
   // Accumulator layout of v_mfma_f32_32x32x2f32: lane holds column
   // n = lane%32 and rows 8*(r/4) + 4*(lane/32) + r%4 for r = 0..15, i.e.
   // four runs of 4 consecutive rows -> one float4 each in ColMajor C.
+  float* C = g.C + batch * g.stride_c;
+  float* P = g.partial ? g.partial + (batch * g.splits + blockIdx.z) * g.M * g.N : nullptr;
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < Cfg::WM; ++i) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int64_t n = n0 + wn * 64 + j * 32 + l32;
+    for (int j = 0; j < Cfg::WN; ++j) {
+      const int64_t n = n0 + wn * (Cfg::WN * 32) + j * 32 + l32;
+      if (n >= g.N) continue;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int64_t m = m0 + wm * 64 + i * 32 + 8 * q + 4 * lhi;
-        if (g.partial) {
-          float* P = g.partial + (int64_t)blockIdx.z * g.M * g.N;
-          if (n < g.N) {
+        const int64_t m = m0 + wm * (Cfg::WM * 32) + i * 32 + 8 * q + 4 * lhi;
+        if (P) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-              if (m + e < g.M) P[(m + e) + g.M * n] = acc[i][j][4 * q + e];
-          }
+          for (int e = 0; e < 4; ++e)
+            if (m + e < g.M) P[(m + e) + g.M * n] = acc[i][j][4 * q + e];
           continue;
         }
-        if (n >= g.N) continue;
         if (g.c_vec_ok && m + 3 < g.M) {
           f32x4 v;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = epilogue_value(g, acc[i][j][4 * q + e], m + e, n);
-          *reinterpret_cast<f32x4*>(g.C + m + g.ldc * n) = v;
+          for (int e = 0; e < 4; ++e) v[e] = epilogue_value(g, C, acc[i][j][4 * q + e], m + e, n);
+          *reinterpret_cast<f32x4*>(C + m + g.ldc * n) = v;
         } else {
 #pragma unroll
           for (int e = 0; e < 4; ++e)
-            if (m + e < g.M) g.C[(m + e) + g.ldc * n] = epilogue_value(g, acc[i][j][4 * q + e], m + e, n);
+            if (m + e < g.M) C[(m + e) + g.ldc * n] = epilogue_value(g, C, acc[i][j][4 * q + e], m + e, n);
         }
       }
     }
@@ -241,20 +268,35 @@ __global__ void __launch_bounds__(NT, 2) gemm_f32_kernel(GemmArgs g) {
 }
 
 // Sums split-K partials in split order and applies the epilogue.
-__global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs g, int splits) {
-  const int64_t total = g.M * g.N;
+__global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs g, int64_t batches) {
+  const int64_t mn = g.M * g.N;
+  const int64_t total = mn * batches;
   for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
        idx += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t bt = idx / mn, e = idx - bt * mn;
+    const float* P = g.partial + bt * g.splits * mn + e;
     float s = 0.f;
-    for (int z = 0; z < splits; ++z) s += g.partial[(int64_t)z * total + idx];
-    const int64_t m = idx % g.M, n = idx / g.M;
-    g.C[m + g.ldc * n] = epilogue_value(g, s, m, n);
+    for (int z = 0; z < g.splits; ++z) s += P[(int64_t)z * mn];
+    const int64_t m = e % g.M, n = e / g.M;
+    float* C = g.C + bt * g.stride_c;
+    C[m + g.ldc * n] = epilogue_value(g, C, s, m, n);
   }
 }
 
-template <bool TA, bool TB>
-void launch_gemm(const GemmArgs& g, int nblocks, int splits, hipStream_t st) {
-  hipLaunchKernelGGL((gemm_f32_kernel<TA, TB>), dim3(nblocks, 1, splits), dim3(NT), 0, st, g);
+template <bool TA, bool TB, class Cfg>
+void launch_cfg(const GemmArgs& g, int64_t batches, hipStream_t st) {
+  const int64_t tiles = ((g.M + Cfg::BM - 1) / Cfg::BM) * ((g.N + Cfg::BN - 1) / Cfg::BN);
+  hipLaunchKernelGGL((gemm_f32_kernel<TA, TB, Cfg>), dim3((unsigned)tiles, (unsigned)batches,
+                                                          (unsigned)g.splits),
+                     dim3(Cfg::NT), 0, st, g);
+}
+
+template <class Cfg>
+void launch_t(int ta, int tb, const GemmArgs& g, int64_t batches, hipStream_t st) {
+  if (!ta && !tb) launch_cfg<false, false, Cfg>(g, batches, st);
+  else if (ta && !tb) launch_cfg<true, false, Cfg>(g, batches, st);
+  else if (!ta && tb) launch_cfg<false, true, Cfg>(g, batches, st);
+  else launch_cfg<true, true, Cfg>(g, batches, st);
 }
 
 // Per-launch event timing (cnhip_gemm_timing_*): a pool of event pairs
@@ -286,16 +328,26 @@ TimingRec* timing_slot(double flops) {
   return r;
 }
 
+enum class Shape { L, SN, SM, S };
+
+template <class Cfg>
+int64_t tiles_of(int64_t M, int64_t N) {
+  return ((M + Cfg::BM - 1) / Cfg::BM) * ((N + Cfg::BN - 1) / Cfg::BN);
+}
+
 }  // namespace
 
-int gemm_f32(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float alpha,
-             const float* A, int64_t lda, const float* B, int64_t ldb, float beta, float* C,
-             int64_t ldc, const float* bias, int epilogue, hipStream_t st, const char* who) {
-  CNHIP_REQUIRE(M >= 0 && N >= 0 && K >= 0, "%s: negative GEMM size (M=%lld N=%lld K=%lld)", who,
-                (long long)M, (long long)N, (long long)K);
+int gemm_f32_batched(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float alpha,
+                     const float* A, int64_t lda, int64_t stride_a, const float* B, int64_t ldb,
+                     int64_t stride_b, float beta, float* C, int64_t ldc, int64_t stride_c,
+                     int64_t batches, const float* bias, int epilogue, hipStream_t st,
+                     const char* who) {
+  CNHIP_REQUIRE(M >= 0 && N >= 0 && K >= 0 && batches >= 0,
+                "%s: negative GEMM size (M=%lld N=%lld K=%lld batch=%lld)", who, (long long)M,
+                (long long)N, (long long)K, (long long)batches);
   CNHIP_REQUIRE(epilogue == CNHIP_EPI_NONE || epilogue == CNHIP_EPI_RELU, "%s: bad epilogue %d",
                 who, epilogue);
-  if (M == 0 || N == 0) return CNHIP_OK;
+  if (M == 0 || N == 0 || batches == 0) return CNHIP_OK;
   CNHIP_REQUIRE(C != nullptr, "%s: C is NULL", who);
   CNHIP_REQUIRE(ldc >= M, "%s: ldc=%lld < M=%lld", who, (long long)ldc, (long long)M);
   if (K > 0) {
@@ -303,59 +355,85 @@ int gemm_f32(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float al
     CNHIP_REQUIRE(lda >= (trans_a ? K : M), "%s: lda=%lld too small", who, (long long)lda);
     CNHIP_REQUIRE(ldb >= (trans_b ? N : K), "%s: ldb=%lld too small", who, (long long)ldb);
   }
-  const int64_t nbm = (M + BM - 1) / BM, nbn = (N + BN - 1) / BN;
-  CNHIP_REQUIRE(nbm * nbn < (int64_t)1 << 30, "%s: GEMM too large", who);
+  CNHIP_REQUIRE(batches <= 65535, "%s: batch count %lld exceeds 65535", who, (long long)batches);
+
+  // Tile shape: skinny shapes waste no MFMA work on padding; small problems
+  // get 64x64 tiles so that more blocks exist.
+  Shape shape = Shape::L;
+  if (N <= 32) shape = Shape::SN;
+  else if (M <= 32) shape = Shape::SM;
+  else if (tiles_of<CfgL>(M, N) * batches < 128) shape = Shape::S;
+  int64_t tiles = 0;
+  switch (shape) {
+    case Shape::L: tiles = tiles_of<CfgL>(M, N); break;
+    case Shape::SN: tiles = tiles_of<CfgSN>(M, N); break;
+    case Shape::SM: tiles = tiles_of<CfgSM>(M, N); break;
+    case Shape::S: tiles = tiles_of<CfgS>(M, N); break;
+  }
+  CNHIP_REQUIRE(tiles < ((int64_t)1 << 30), "%s: GEMM too large", who);
 
   GemmArgs g;
   g.M = M; g.N = N; g.K = K;
-  g.A = A; g.lda = lda; g.B = B; g.ldb = ldb; g.C = C; g.ldc = ldc;
+  g.A = A; g.lda = lda; g.stride_a = stride_a;
+  g.B = B; g.ldb = ldb; g.stride_b = stride_b;
+  g.C = C; g.ldc = ldc; g.stride_c = stride_c;
   g.alpha = alpha; g.beta = beta; g.bias = bias; g.epilogue = epilogue;
-  g.vec_ok = (lda % 4 == 0) && (ldb % 4 == 0) && aligned16(A) && aligned16(B);
-  g.c_vec_ok = (ldc % 4 == 0) && aligned16(C);
+  g.vec_ok = (lda % 4 == 0) && (ldb % 4 == 0) && (stride_a % 4 == 0) && (stride_b % 4 == 0) &&
+             aligned16(A) && aligned16(B);
+  g.c_vec_ok = (ldc % 4 == 0) && (stride_c % 4 == 0) && aligned16(C);
   g.partial = nullptr;
 
-  // Split K when the output tiles alone cannot fill the 256 CUs.
-  const int64_t tiles = nbm * nbn;
+  // Split K until about 512 blocks (2 per CU) exist, keeping >= 4 K-tiles
+  // per split.
+  const int64_t blocks = tiles * batches;
   int splits = 1;
-  if (tiles < 256 && K >= 4 * BK) {
-    int64_t want = (512 + tiles - 1) / tiles;
-    int64_t max_by_k = K / (4 * BK);  // keep >= 4 K-tiles per split
+  if (blocks < 512 && K >= 8 * BK) {
+    const int64_t want = (512 + blocks - 1) / blocks;
+    const int64_t max_by_k = K / (4 * BK);
     splits = (int)std::max<int64_t>(1, std::min<int64_t>({want, max_by_k, 64}));
   }
   int64_t kps = (K + splits - 1) / splits;
   kps = ((kps + BK - 1) / BK) * BK;
   if (kps == 0) kps = BK;
-  splits = (int)((K + kps - 1) / kps);
-  if (splits < 1) splits = 1;
+  splits = K > 0 ? (int)((K + kps - 1) / kps) : 1;
   g.k_per_split = kps;
+  g.splits = splits;
 
   if (splits > 1) {
     void* ws = nullptr;
-    const size_t bytes = (size_t)splits * (size_t)M * (size_t)N * sizeof(float);
+    const size_t bytes = (size_t)batches * (size_t)splits * (size_t)M * (size_t)N * sizeof(float);
     CNHIP_TRY(check_hip(hipMallocAsync(&ws, bytes, st), who));
     g.partial = static_cast<float*>(ws);
   }
 
-  const int nblocks = (int)tiles;
-  TimingRec* rec = timing_slot(2.0 * (double)M * (double)N * (double)K);
+  TimingRec* rec = timing_slot(2.0 * (double)M * (double)N * (double)K * (double)batches);
   if (rec) (void)hipEventRecord(rec->start, st);
-  if (!trans_a && !trans_b) launch_gemm<false, false>(g, nblocks, splits, st);
-  else if (trans_a && !trans_b) launch_gemm<true, false>(g, nblocks, splits, st);
-  else if (!trans_a && trans_b) launch_gemm<false, true>(g, nblocks, splits, st);
-  else launch_gemm<true, true>(g, nblocks, splits, st);
+  switch (shape) {
+    case Shape::L: launch_t<CfgL>(trans_a, trans_b, g, batches, st); break;
+    case Shape::SN: launch_t<CfgSN>(trans_a, trans_b, g, batches, st); break;
+    case Shape::SM: launch_t<CfgSM>(trans_a, trans_b, g, batches, st); break;
+    case Shape::S: launch_t<CfgS>(trans_a, trans_b, g, batches, st); break;
+  }
   int status = check_launch(who);
   if (rec) (void)hipEventRecord(rec->stop, st);
 
   if (splits > 1) {
     if (status == CNHIP_OK) {
-      hipLaunchKernelGGL(splitk_reduce_kernel, dim3(elementwise_grid(M * N, 256)), dim3(256), 0, st,
-                         g, splits);
+      hipLaunchKernelGGL(splitk_reduce_kernel, dim3(elementwise_grid(M * N * batches, 256)),
+                         dim3(256), 0, st, g, batches);
       status = check_launch(who);
     }
     int st2 = check_hip(hipFreeAsync(g.partial, st), who);
     if (status == CNHIP_OK) status = st2;
   }
   return status;
+}
+
+int gemm_f32(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float alpha,
+             const float* A, int64_t lda, const float* B, int64_t ldb, float beta, float* C,
+             int64_t ldc, const float* bias, int epilogue, hipStream_t st, const char* who) {
+  return gemm_f32_batched(trans_a, trans_b, M, N, K, alpha, A, lda, 0, B, ldb, 0, beta, C, ldc, 0,
+                          1, bias, epilogue, st, who);
 }
 
 }  // namespace cnhip
@@ -366,6 +444,17 @@ extern "C" int cnhip_gemm_f32(int trans_a, int trans_b, int64_t M, int64_t N, in
                               int epilogue, cnhip_stream_t stream) {
   return cnhip::gemm_f32(trans_a, trans_b, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, bias,
                          epilogue, cnhip::as_stream(stream), "cnhip_gemm_f32");
+}
+
+extern "C" int cnhip_gemm_f32_batched(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K,
+                                      float alpha, const float* A, int64_t lda, int64_t stride_a,
+                                      const float* B, int64_t ldb, int64_t stride_b, float beta,
+                                      float* C, int64_t ldc, int64_t stride_c, int64_t batch_count,
+                                      cnhip_stream_t stream) {
+  return cnhip::gemm_f32_batched(trans_a, trans_b, M, N, K, alpha, A, lda, stride_a, B, ldb,
+                                 stride_b, beta, C, ldc, stride_c, batch_count, nullptr,
+                                 CNHIP_EPI_NONE, cnhip::as_stream(stream),
+                                 "cnhip_gemm_f32_batched");
 }
 
 extern "C" int cnhip_gemm_timing_enable(int on) {

@@ -28,12 +28,12 @@ namespace CppNet
                 throw std::invalid_argument("Linear: sizes must be positive in layer: " + layer_name_);
             require_gpu_device(device_, "Linear " + layer_name_);
             W_ = DeviceTensor::empty({in_size_, out_size_});
-            gW_ = DeviceTensor::zeros({in_size_, out_size_});
+            gW_ = DeviceTensor::empty({in_size_, out_size_});  // zero by grads_zero_
             set_weights(Utils::init_weights(in_size_, out_size_, weight_init_));
             if (bias_flag_)
             {
                 b_ = DeviceTensor::zeros({out_size_});   // biases start at zero (linear.cpp:75-80)
-                gb_ = DeviceTensor::zeros({out_size_});
+                gb_ = DeviceTensor::empty({out_size_});
             }
         }
 
@@ -61,11 +61,14 @@ namespace CppNet
                                          layer_name_);
             const int64_t B = grad_output.dimension(0);
             DeviceTensor dX = DeviceTensor::empty({B, in_size_});
+            // grad_W += X^T dY (linear.cpp:346-352); over known-zero grads, write.
+            const int accumulate = grads_zero_ ? 0 : 1;
             Device::check(cnhip_linear_backward(in_cache_.data(), W_.data(), grad_output.data(),
                                                 gW_.data(), bias_flag_ ? gb_.data() : nullptr,
                                                 dX.data(), B, in_size_, out_size_, trainable_ ? 1 : 0,
-                                                /*accumulate=*/1, Device::stream()),
+                                                accumulate, Device::stream()),
                           "Linear::backward");
+            if (trainable_) grads_zero_ = false;
             return dX;
         }
 
@@ -79,9 +82,19 @@ namespace CppNet
             return backward(DeviceTensor::from_host(grad_output)).to_host<float, 2>();
         }
 
+        void Linear::materialize_grads() const
+        {
+            if (!grads_zero_) return;
+            auto* self = const_cast<Linear*>(this);
+            self->gW_.fill_zero();
+            if (bias_flag_) self->gb_.fill_zero();
+            self->grads_zero_ = false;
+        }
+
         void Linear::step(Optimizers::Optimizer& optimizer, float learning_rate)
         {
             if (!trainable_) return;
+            materialize_grads();
             optimizer.update(W_.data(), gW_.data(), W_.size(), learning_rate);
             if (bias_flag_) optimizer.update(b_.data(), gb_.data(), b_.size(), learning_rate);
         }
@@ -89,18 +102,22 @@ namespace CppNet
         void Linear::reset_grads()
         {
             if (!trainable_) return;
-            gW_.fill_zero();
-            if (bias_flag_) gb_.fill_zero();
+            grads_zero_ = true;
         }
 
         Tensor<float, 2> Linear::get_weights() const { return W_.to_host<float, 2>(); }
-        Tensor<float, 2> Linear::get_grad_weights() const { return gW_.to_host<float, 2>(); }
+        Tensor<float, 2> Linear::get_grad_weights() const
+        {
+            materialize_grads();
+            return gW_.to_host<float, 2>();
+        }
         Tensor<float, 1> Linear::get_biases() const
         {
             return bias_flag_ ? b_.to_host<float, 1>() : Tensor<float, 1>(0);
         }
         Tensor<float, 1> Linear::get_grad_biases() const
         {
+            materialize_grads();
             return bias_flag_ ? gb_.to_host<float, 1>() : Tensor<float, 1>(0);
         }
 

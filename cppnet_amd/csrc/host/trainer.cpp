@@ -25,8 +25,9 @@ struct cnt_session
     DeviceTensor X, Y;
     Losses::DeviceScalar last_loss;
 
-    // parameter index -> (device tensor)
-    std::vector<DeviceTensor*> params, grads;
+    // parameter index -> (layer, is_bias); resolved through the layer's
+    // accessors so lazily-zeroed gradients are materialised before a read
+    std::vector<std::pair<Layers::Linear*, bool>> params;
 };
 
 namespace
@@ -96,10 +97,11 @@ namespace
     DeviceTensor& param_at(cnt_session* s, int index, bool grad)
     {
         check_session(s);
-        auto& v = grad ? s->grads : s->params;
-        if (index < 0 || index >= static_cast<int>(v.size()))
+        if (index < 0 || index >= static_cast<int>(s->params.size()))
             throw std::out_of_range("parameter index " + std::to_string(index) + " out of range");
-        return *v[static_cast<size_t>(index)];
+        auto [layer, is_bias] = s->params[static_cast<size_t>(index)];
+        if (grad) return is_bias ? layer->grad_biases() : layer->grad_weights();
+        return is_bias ? layer->biases() : layer->weights();
     }
 } // namespace
 
@@ -132,10 +134,8 @@ int cnt_mlp_create(cnt_session** out, int n_linear, const int64_t* sizes, int hi
         }
         for (auto& l : s->linears)
         {
-            s->params.push_back(&l->weights());
-            s->grads.push_back(&l->grad_weights());
-            s->params.push_back(&l->biases());
-            s->grads.push_back(&l->grad_biases());
+            s->params.emplace_back(l.get(), false);
+            s->params.emplace_back(l.get(), true);
         }
         s->loss = make_loss(loss);
         s->adam = std::make_unique<Optimizers::Adam>(beta1, beta2, eps, "gpu");

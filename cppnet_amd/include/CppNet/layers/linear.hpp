@@ -60,8 +60,8 @@ namespace CppNet
             /// Device-resident state.
             DeviceTensor& weights() { return W_; }
             DeviceTensor& biases() { return b_; }
-            DeviceTensor& grad_weights() { return gW_; }
-            DeviceTensor& grad_biases() { return gb_; }
+            DeviceTensor& grad_weights() { materialize_grads(); return gW_; }
+            DeviceTensor& grad_biases() { materialize_grads(); return gb_; }
 
             void reinitialize_weights(const std::string& method);
             /// Capacity hint of the reference gpu path (linear.cpp:460-468);
@@ -79,6 +79,11 @@ namespace CppNet
             std::string weight_init_;
             DeviceTensor W_, b_, gW_, gb_;
             DeviceTensor in_cache_;
+            // reset_grads() only marks the gradients as zero; the next
+            // backward then writes instead of adding (0 + x == x), and any
+            // reader before that gets them cleared first.
+            bool grads_zero_ = true;
+            void materialize_grads() const;
         };
     } // namespace Layers
 } // namespace CppNet

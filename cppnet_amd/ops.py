@@ -48,6 +48,13 @@ def gemm(trans_a: bool, trans_b: bool, M: int, N: int, K: int, A, lda: int, B, l
                _stream())
 
 
+def gemm_batched(trans_a: bool, trans_b: bool, M: int, N: int, K: int, A, lda: int, sa: int, B,
+                 ldb: int, sb: int, C, ldc: int, sc: int, batch: int, alpha: float = 1.0,
+                 beta: float = 0.0) -> None:
+    _capi.call("cnhip_gemm_f32_batched", int(trans_a), int(trans_b), M, N, K, alpha, _p(A, "A"),
+               lda, sa, _p(B, "B"), ldb, sb, beta, _p(C, "C"), ldc, sc, batch, _stream())
+
+
 def linear_forward(X, W, b, Y, batch: int, in_features: int, out_features: int) -> None:
     _capi.call("cnhip_linear_forward", _p(X, "X"), _p(W, "W"), _p(b, "b"), _p(Y, "Y"), batch,
                in_features, out_features, _stream())

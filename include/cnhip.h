@@ -82,6 +82,17 @@ int cnhip_gemm_f32(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K,
                    float* C, int64_t ldc, const float* bias, int epilogue,
                    cnhip_stream_t stream);
 
+/* Strided-batched form: for b in [0, batch_count): the GEMM above on
+ * A + b*stride_a, B + b*stride_b, C + b*stride_c (no bias, no epilogue).
+ * Used for per-timestep / per-sample products (LSTM, attention).
+ * ref: the per-sample contractions of attention.cpp:183-212 and the
+ * per-timestep ones of lstm.cpp:104-105, 228-244. */
+int cnhip_gemm_f32_batched(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K,
+                           float alpha, const float* A, int64_t lda, int64_t stride_a,
+                           const float* B, int64_t ldb, int64_t stride_b, float beta,
+                           float* C, int64_t ldc, int64_t stride_c, int64_t batch_count,
+                           cnhip_stream_t stream);
+
 /* Measurement aid for the GEMM kernel (the MFMA-bound hot kernel): while
  * enabled, every GEMM kernel launch on this host thread is bracketed by HIP
  * events on its own stream, and its algorithmic flops (2*M*N*K) recorded.

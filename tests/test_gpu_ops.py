@@ -277,3 +277,28 @@ def test_gemm_config2_shapes_vs_torch(gpu):
         scale = (opA.double().norm(dim=1)[:, None] * opB.double().norm(dim=0)[None, :]).t()
         bound = torch.maximum(lim, 4e-7 * scale)
         assert bool((err <= bound).all()), f"max err {err.max().item()} at ta={ta} tb={tb} {M}x{N}x{K}"
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1)])
+@pytest.mark.parametrize("M,N,K,batch", [(64, 96, 40, 5), (256, 256, 64, 3), (17, 33, 300, 4)])
+def test_gemm_batched_vs_oracle(gpu, oracle, ta, tb, M, N, K, batch):
+    print(f"[gemm-batched] ta={ta} tb={tb} M={M} N={N} K={K} batch={batch}", flush=True)
+    rng = np.random.default_rng(M + N + K + batch)
+    lda, ldb, ldc = (K if ta else M) + 1, (N if tb else K) + 2, M + 3
+    sa, sb, sc = lda * (M if ta else K) + 5, ldb * (K if tb else N) + 7, ldc * N + 1
+    A, B = rnd(rng, sa * batch), rnd(rng, sb * batch)
+    C = rnd(rng, sc * batch)
+    Cd = dev(C)
+    ops.gemm_batched(ta, tb, M, N, K, dev(A), lda, sa, dev(B), ldb, sb, Cd, ldc, sc, batch,
+                     alpha=0.5, beta=1.0)
+    got = host(Cd)
+    for b in range(batch):
+        want = C[b * sc:(b + 1) * sc].copy()
+        Ab, Bb = A[b * sa:(b + 1) * sa], B[b * sb:(b + 1) * sb]
+        oracle.cnref_gemm_f32(ta, tb, M, N, K, 0.5, fp(Ab), lda, fp(Bb), ldb, 1.0, fp(want), ldc,
+                              None, 0)
+        mag = gemm_mag(oracle, ta, tb, M, N, K, Ab, lda, Bb, ldb, ldc)
+        ok, msg = close_mag(got[b * sc:b * sc + ldc * N], want[:ldc * N], mag, RTOL, ATOL)
+        assert ok, f"batch {b}: {msg}"
+        # padding between batch entries untouched
+        np.testing.assert_array_equal(got[b * sc + ldc * N:(b + 1) * sc], C[b * sc + ldc * N:(b + 1) * sc])
