@@ -19,26 +19,16 @@
 #include <vector>
 
 #include "common.hpp"
+#include "mfma_core.hpp"
 
 namespace cnhip {
 namespace {
 
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
+using mfma::BK;
+using mfma::f32x16;
+using mfma::f32x4;
+using mfma::TileCfg;
 
-constexpr int BK = 16;
-
-template <int WGM_, int WGN_, int WM_, int WN_>
-struct TileCfg {
-  static constexpr int WGM = WGM_, WGN = WGN_, WM = WM_, WN = WN_;
-  static constexpr int BM = WGM * WM * 32;
-  static constexpr int BN = WGN * WN * 32;
-  static constexpr int NT = WGM * WGN * 64;
-  // k-major LDS rows padded by 4 floats: keeps float4 stores aligned and
-  // spreads the 4 k-rows a KCONTIG tile store touches over distinct banks.
-  static constexpr int LDA = BM + 4;
-  static constexpr int LDB = BN + 4;
-};
 using CfgL = TileCfg<2, 2, 2, 2>;   // 128 x 128, 4 waves, 64x64 per wave
 using CfgSN = TileCfg<4, 1, 1, 1>;  // 128 x 32 : N <= 32
 using CfgSM = TileCfg<1, 4, 1, 1>;  // 32 x 128 : M <= 32
@@ -62,28 +52,20 @@ struct GemmArgs {
   int splits;
 };
 
-// Stages one operand tile (R rows of the outer dim x 16 of K) into
+// Stages one strided operand tile (R rows of the outer dim x 16 of K) into
 // registers.  KCONTIG: X(r,k) = X[k + ld*r]  (else X[r + ld*k]).
 template <bool KCONTIG, int R, int NT>
 struct TileLoader {
-  static constexpr int F4 = R * BK / 4;                 // float4 per tile
-  static constexpr int PER_THREAD = (F4 + NT - 1) / NT;
+  using Slots = mfma::TileSlots<KCONTIG, R, NT>;
+  static constexpr int PER_THREAD = Slots::PER_THREAD;
 
   __device__ __forceinline__ static void load(const float* __restrict__ X, int64_t ld, int64_t r0,
                                               int64_t k0, int64_t Rtot, int64_t K, bool fast,
                                               f32x4 (&regs)[PER_THREAD]) {
 #pragma unroll
     for (int p = 0; p < PER_THREAD; ++p) {
-      const int idx = threadIdx.x + NT * p;
-      if (F4 % NT != 0 && idx >= F4) break;
       int rr, kk;
-      if (KCONTIG) {
-        rr = idx >> 2;
-        kk = (idx & 3) * 4;
-      } else {
-        kk = idx / (R / 4);
-        rr = (idx % (R / 4)) * 4;
-      }
+      if (!Slots::slot(p, rr, kk)) break;
       const int64_t r = r0 + rr, k = k0 + kk;
       if (fast) {
         const float* src = KCONTIG ? (X + k + ld * r) : (X + r + ld * k);
@@ -102,26 +84,9 @@ struct TileLoader {
       }
     }
   }
-
-  // Writes the staged tile into LDS as [k][r] rows (r contiguous, row stride
-  // R+4), so an MFMA fragment read (lane -> r = lane%32, k = lane/32) is one
-  // conflict-free ds_read_b32.
   __device__ __forceinline__ static void store(float* __restrict__ lds,
                                                const f32x4 (&regs)[PER_THREAD]) {
-    constexpr int LD = R + 4;
-#pragma unroll
-    for (int p = 0; p < PER_THREAD; ++p) {
-      const int idx = threadIdx.x + NT * p;
-      if (F4 % NT != 0 && idx >= F4) break;
-      if (KCONTIG) {
-        const int rr = idx >> 2, kk = (idx & 3) * 4;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) lds[(kk + j) * LD + rr] = regs[p][j];
-      } else {
-        const int kk = idx / (R / 4), rr = (idx % (R / 4)) * 4;
-        *reinterpret_cast<f32x4*>(lds + kk * LD + rr) = regs[p];
-      }
-    }
+    Slots::store(lds, regs);
   }
 };
 
@@ -174,21 +139,10 @@ __global__ void __launch_bounds__(Cfg::NT, 2) gemm_f32_kernel(GemmArgs g) {
   const int64_t k_begin = (int64_t)blockIdx.z * g.k_per_split;
   const int64_t k_end = min(g.K, k_begin + g.k_per_split);
   const int ntiles = k_end > k_begin ? (int)((k_end - k_begin + BK - 1) / BK) : 0;
-
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int wm = wave % Cfg::WGM, wn = wave / Cfg::WGM;
-  const int l32 = lane & 31, lhi = lane >> 5;
-
   const bool full_mn = (m0 + BM <= g.M) && (n0 + BN <= g.N);
 
   f32x16 acc[Cfg::WM][Cfg::WN];
-#pragma unroll
-  for (int i = 0; i < Cfg::WM; ++i)
-#pragma unroll
-    for (int j = 0; j < Cfg::WN; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+  mfma::zero_acc<Cfg>(acc);
 
   f32x4 ra[LA::PER_THREAD], rb[LB::PER_THREAD];
   if (ntiles > 0) {
@@ -209,22 +163,7 @@ __global__ void __launch_bounds__(Cfg::NT, 2) gemm_f32_kernel(GemmArgs g) {
       LA::load(A, g.lda, m0, kn, g.M, k_end, fast, ra);
       LB::load(B, g.ldb, n0, kn, g.N, k_end, fast, rb);
     }
-    const float* la = lds_a[cur] + wm * (Cfg::WM * 32) + l32;
-    const float* lb = lds_b[cur] + wn * (Cfg::WN * 32) + l32;
-#pragma unroll
-    for (int s = 0; s < BK / 2; ++s) {
-      const int k = 2 * s + lhi;
-      float a[Cfg::WM], b[Cfg::WN];
-#pragma unroll
-      for (int i = 0; i < Cfg::WM; ++i) a[i] = la[k * Cfg::LDA + 32 * i];
-#pragma unroll
-      for (int j = 0; j < Cfg::WN; ++j) b[j] = lb[k * Cfg::LDB + 32 * j];
-#pragma unroll
-      for (int i = 0; i < Cfg::WM; ++i)
-#pragma unroll
-        for (int j = 0; j < Cfg::WN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
-    }
+    mfma::mfma_ktile<Cfg>(lds_a[cur], lds_b[cur], acc);
     if (has_next) {
       LA::store(lds_a[cur ^ 1], ra);
       LB::store(lds_b[cur ^ 1], rb);
@@ -232,39 +171,28 @@ __global__ void __launch_bounds__(Cfg::NT, 2) gemm_f32_kernel(GemmArgs g) {
     __syncthreads();
   }
 
-  // Accumulator layout of v_mfma_f32_32x32x2f32: lane holds column
-  // n = lane%32 and rows 8*(r/4) + 4*(lane/32) + r%4 for r = 0..15, i.e.
-  // four runs of 4 consecutive rows -> one float4 each in ColMajor C.
   float* C = g.C + batch * g.stride_c;
   float* P = g.partial ? g.partial + (batch * g.splits + blockIdx.z) * g.M * g.N : nullptr;
+  mfma::for_each_acc_run<Cfg>(acc, [&](int ml, int nl, const f32x4& v) {
+    const int64_t m = m0 + ml, n = n0 + nl;
+    if (n >= g.N) return;
+    if (P) {
 #pragma unroll
-  for (int i = 0; i < Cfg::WM; ++i) {
-#pragma unroll
-    for (int j = 0; j < Cfg::WN; ++j) {
-      const int64_t n = n0 + wn * (Cfg::WN * 32) + j * 32 + l32;
-      if (n >= g.N) continue;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int64_t m = m0 + wm * (Cfg::WM * 32) + i * 32 + 8 * q + 4 * lhi;
-        if (P) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (m + e < g.M) P[(m + e) + g.M * n] = acc[i][j][4 * q + e];
-          continue;
-        }
-        if (g.c_vec_ok && m + 3 < g.M) {
-          f32x4 v;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = epilogue_value(g, C, acc[i][j][4 * q + e], m + e, n);
-          *reinterpret_cast<f32x4*>(C + m + g.ldc * n) = v;
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (m + e < g.M) C[(m + e) + g.ldc * n] = epilogue_value(g, C, acc[i][j][4 * q + e], m + e, n);
-        }
-      }
+      for (int e = 0; e < 4; ++e)
+        if (m + e < g.M) P[(m + e) + g.M * n] = v[e];
+      return;
     }
-  }
+    if (g.c_vec_ok && m + 3 < g.M) {
+      f32x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = epilogue_value(g, C, v[e], m + e, n);
+      *reinterpret_cast<f32x4*>(C + m + g.ldc * n) = o;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (m + e < g.M) C[(m + e) + g.ldc * n] = epilogue_value(g, C, v[e], m + e, n);
+    }
+  });
 }
 
 // Sums split-K partials in split order and applies the epilogue.

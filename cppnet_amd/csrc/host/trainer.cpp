@@ -5,6 +5,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <exception>
+#include <functional>
 #include <memory>
 #include <string>
 #include <vector>
@@ -17,17 +18,31 @@ struct cnt_session
 {
     cnhip_stream_t stream = nullptr;
     Models::SequentialModel model;
-    std::vector<std::shared_ptr<Layers::Linear>> linears;
+    std::vector<std::shared_ptr<Layers::Layer>> keep;  // owns the layers
     std::unique_ptr<Losses::Loss> loss;
     std::unique_ptr<Optimizers::Adam> adam;
     float lr = 1e-3f;
-    int64_t batch = 0, in_features = 0, out_features = 0;
     DeviceTensor X, Y;
     Losses::DeviceScalar last_loss;
 
-    // parameter index -> (layer, is_bias); resolved through the layer's
-    // accessors so lazily-zeroed gradients are materialised before a read
-    std::vector<std::pair<Layers::Linear*, bool>> params;
+    // parameter index -> accessors of the value and of the gradient, called
+    // through the layer so lazily-zeroed gradients are materialised first
+    struct Param
+    {
+        std::function<DeviceTensor&()> value, grad;
+    };
+    std::vector<Param> params;
+
+    template <class L>
+    void add_params(const std::shared_ptr<L>& l)
+    {
+        L* p = l.get();
+        params.push_back({[p]() -> DeviceTensor& { return p->weights(); },
+                          [p]() -> DeviceTensor& { return p->grad_weights(); }});
+        if (p->has_bias())
+            params.push_back({[p]() -> DeviceTensor& { return p->biases(); },
+                              [p]() -> DeviceTensor& { return p->grad_biases(); }});
+    }
 };
 
 namespace
@@ -99,9 +114,16 @@ namespace
         check_session(s);
         if (index < 0 || index >= static_cast<int>(s->params.size()))
             throw std::out_of_range("parameter index " + std::to_string(index) + " out of range");
-        auto [layer, is_bias] = s->params[static_cast<size_t>(index)];
-        if (grad) return is_bias ? layer->grad_biases() : layer->grad_weights();
-        return is_bias ? layer->biases() : layer->weights();
+        auto& p = s->params[static_cast<size_t>(index)];
+        return grad ? p.grad() : p.value();
+    }
+
+    std::unique_ptr<cnt_session> new_session(uint64_t seed)
+    {
+        auto s = std::make_unique<cnt_session>();
+        Device::check(cnhip_stream_create(&s->stream), "stream");
+        Utils::set_seed(seed);
+        return s;
     }
 } // namespace
 
@@ -117,10 +139,8 @@ int cnt_mlp_create(cnt_session** out, int n_linear, const int64_t* sizes, int hi
         *out = nullptr;
         if (n_linear < 1 || !sizes) throw std::invalid_argument("need at least one Linear layer");
         if (batch <= 0) throw std::invalid_argument("batch must be positive");
-        auto s = std::make_unique<cnt_session>();
-        Device::check(cnhip_stream_create(&s->stream), "stream");
+        auto s = new_session(seed);
         StreamScope scope(s.get());
-        Utils::set_seed(seed);
         for (int i = 0; i < n_linear; ++i)
         {
             auto lin = std::make_shared<Layers::Linear>(static_cast<int>(sizes[i]),
@@ -128,23 +148,63 @@ int cnt_mlp_create(cnt_session** out, int n_linear, const int64_t* sizes, int hi
                                                         "fc" + std::to_string(i + 1), true, true, "gpu",
                                                         "xavier");
             s->model.add_layer(lin);
-            s->linears.push_back(lin);
+            s->keep.push_back(lin);
+            s->add_params(lin);
             auto act = make_act(i + 1 < n_linear ? hidden_act : out_act);
             if (act) s->model.add_activation(act);
-        }
-        for (auto& l : s->linears)
-        {
-            s->params.emplace_back(l.get(), false);
-            s->params.emplace_back(l.get(), true);
         }
         s->loss = make_loss(loss);
         s->adam = std::make_unique<Optimizers::Adam>(beta1, beta2, eps, "gpu");
         s->lr = lr;
-        s->batch = batch;
-        s->in_features = sizes[0];
-        s->out_features = sizes[n_linear];
-        s->X = DeviceTensor::zeros({batch, s->in_features});
-        s->Y = DeviceTensor::zeros({batch, s->out_features});
+        s->X = DeviceTensor::zeros({batch, sizes[0]});
+        s->Y = DeviceTensor::zeros({batch, sizes[n_linear]});
+        Device::synchronize();
+        *out = s.release();
+    });
+}
+
+int cnt_cnn_create(cnt_session** out, int n_conv, const int64_t* conv_spec, int pool,
+                   const int64_t* input_shape, int64_t classes, float lr, float beta1, float beta2,
+                   float eps, uint64_t seed)
+{
+    return guarded("cnt_cnn_create", [&] {
+        if (!out) throw std::invalid_argument("NULL out pointer");
+        *out = nullptr;
+        if (n_conv < 1 || !conv_spec || !input_shape) throw std::invalid_argument("need at least one Conv2D block");
+        auto s = new_session(seed);
+        StreamScope scope(s.get());
+        int64_t C = input_shape[1], H = input_shape[2], W = input_shape[3];
+        for (int i = 0; i < n_conv; ++i)
+        {
+            const int64_t* c = conv_spec + 5 * i;  // in, out, kernel, stride, padding
+            if (c[0] != C) throw std::invalid_argument("conv block " + std::to_string(i) + ": in_channels mismatch");
+            auto conv = std::make_shared<Layers::Conv2D>(static_cast<int>(c[0]), static_cast<int>(c[1]),
+                                                         static_cast<int>(c[2]), static_cast<int>(c[3]),
+                                                         static_cast<int>(c[4]), true, "gpu");
+            s->model.add_layer(conv);
+            s->keep.push_back(conv);
+            s->add_params(conv);
+            s->model.add_activation(std::make_shared<Activations::ReLU>("gpu"));
+            auto mp = std::make_shared<Layers::MaxPool2D>(pool, -1, "gpu");
+            s->model.add_layer(mp);
+            s->keep.push_back(mp);
+            C = c[1];
+            H = ((H + 2 * c[4] - c[2]) / c[3] + 1 - pool) / pool + 1;
+            W = ((W + 2 * c[4] - c[2]) / c[3] + 1 - pool) / pool + 1;
+        }
+        auto fl = std::make_shared<Layers::Flatten>();
+        s->model.add_layer(fl);
+        s->keep.push_back(fl);
+        auto fc = std::make_shared<Layers::Linear>(static_cast<int>(C * H * W), static_cast<int>(classes),
+                                                   "fc", true, true, "gpu", "xavier");
+        s->model.add_layer(fc);
+        s->keep.push_back(fc);
+        s->add_params(fc);
+        s->loss = make_loss(CNT_LOSS_SOFTMAX_CE);
+        s->adam = std::make_unique<Optimizers::Adam>(beta1, beta2, eps, "gpu");
+        s->lr = lr;
+        s->X = DeviceTensor::zeros({input_shape[0], input_shape[1], input_shape[2], input_shape[3]});
+        s->Y = DeviceTensor::zeros({input_shape[0], classes});
         Device::synchronize();
         *out = s.release();
     });
@@ -223,18 +283,45 @@ int cnt_set_batch_device(cnt_session* s, const float* x_dev, const float* y_dev)
     });
 }
 
-int cnt_step(cnt_session* s, float* loss_out)
+namespace
 {
-    return guarded("cnt_step", [&] {
-        check_session(s);
-        StreamScope scope(s);
+    void forward_backward(cnt_session* s)
+    {
         s->model.zero_grad();
         DeviceTensor out = s->model.forward(s->X);
         s->last_loss = s->loss->forward(out, s->Y);
         DeviceTensor g = s->loss->backward(out, s->Y);
         s->model.backward(g);
+    }
+} // namespace
+
+int cnt_step(cnt_session* s, float* loss_out)
+{
+    return guarded("cnt_step", [&] {
+        check_session(s);
+        StreamScope scope(s);
+        forward_backward(s);
         s->model.update(*s->adam, s->lr);
         if (loss_out) *loss_out = s->last_loss.get();
+    });
+}
+
+int cnt_forward_backward(cnt_session* s, float* loss_out)
+{
+    return guarded("cnt_forward_backward", [&] {
+        check_session(s);
+        StreamScope scope(s);
+        forward_backward(s);
+        if (loss_out) *loss_out = s->last_loss.get();
+    });
+}
+
+int cnt_update(cnt_session* s)
+{
+    return guarded("cnt_update", [&] {
+        check_session(s);
+        StreamScope scope(s);
+        s->model.update(*s->adam, s->lr);
     });
 }
 

@@ -10,6 +10,9 @@
 #include "CppNet/utils/init.hpp"
 #include "CppNet/layers/layer.hpp"
 #include "CppNet/layers/linear.hpp"
+#include "CppNet/layers/conv2d.hpp"
+#include "CppNet/layers/max_pool2d.hpp"
+#include "CppNet/layers/flatten.hpp"
 #include "CppNet/activations/activation.hpp"
 #include "CppNet/activations/relu.hpp"
 #include "CppNet/activations/sigmoid.hpp"

@@ -1,0 +1,46 @@
+/**
+ * @file max_pool2d.hpp
+ * @brief MaxPool2D, device "gpu" (ref: include/CppNet/layers/max_pool2d.hpp:29-52,
+ *        src/CppNet/layers/max_pool2d.cpp:25-131).
+ *
+ * stride <= 0 means stride = pool_size; HO = (H - pool)/stride + 1, no
+ * padding.  forward() keeps the int32 window-local argmax ph*pool + pw of the
+ * first maximum (strict >) in HBM; backward() routes dY through it.
+ */
+#ifndef CPPNET_LAYERS_MAX_POOL2D_HPP
+#define CPPNET_LAYERS_MAX_POOL2D_HPP
+
+#include <string>
+
+#include "CppNet/core/tensor.hpp"
+#include "CppNet/layers/layer.hpp"
+
+namespace CppNet
+{
+    namespace Layers
+    {
+        class MaxPool2D : public Layer
+        {
+        public:
+            MaxPool2D(int pool_size = 2, int stride = -1, const std::string& device = "gpu");
+            Tensor<float, 4> forward(const Tensor<float, 4>& input);
+            Tensor<float, 4> backward(const Tensor<float, 4>& grad_output);
+            DeviceTensor forward(const DeviceTensor& input);
+            DeviceTensor backward(const DeviceTensor& grad_output);
+            bool is_trainable() const override { return false; }
+            void step(Optimizers::Optimizer&, float) override {}
+            int get_pool_size() const { return pool_size_; }
+            int get_stride() const { return stride_; }
+            /// int32 argmax of the last forward, [N, C, HO, WO]
+            const DeviceTensor& max_indices() const { return idx_; }
+            Tensor<int, 4> get_max_indices() const;
+
+        private:
+            int pool_size_, stride_;
+            std::string device_;
+            DeviceTensor idx_;
+            std::vector<int64_t> in_dims_;
+        };
+    } // namespace Layers
+} // namespace CppNet
+#endif

@@ -71,6 +71,26 @@ def column_sum(x, out, rows: int, cols: int, accumulate: bool = False) -> None:
     _capi.call("cnhip_column_sum", _p(x), _p(out), rows, cols, int(accumulate), _stream())
 
 
+def conv2d_forward(X, W, b, Y, N, C, H, Wd, OC, KS, S=1, P=0) -> None:
+    _capi.call("cnhip_conv2d_forward", _p(X, "X"), _p(W, "W"), _p(b, "b"), _p(Y, "Y"), N, C, H, Wd,
+               OC, KS, S, P, _stream())
+
+
+def conv2d_backward(X, W, dY, grad_W, grad_b, dX, N, C, H, Wd, OC, KS, S=1, P=0) -> None:
+    _capi.call("cnhip_conv2d_backward", _p(X, "X"), _p(W, "W"), _p(dY, "dY"), _p(grad_W, "gW"),
+               _p(grad_b, "gb"), _p(dX, "dX"), N, C, H, Wd, OC, KS, S, P, _stream())
+
+
+def maxpool2d_forward(X, Y, idx, N, C, H, W, pool=2, stride=-1) -> None:
+    _capi.call("cnhip_maxpool2d_forward", _p(X, "X"), _p(Y, "Y"), _p(idx, "idx"), N, C, H, W,
+               pool, stride, _stream())
+
+
+def maxpool2d_backward(dY, idx, dX, N, C, H, W, pool=2, stride=-1) -> None:
+    _capi.call("cnhip_maxpool2d_backward", _p(dY, "dY"), _p(idx, "idx"), _p(dX, "dX"), N, C, H, W,
+               pool, stride, _stream())
+
+
 def _unary(name: str, x, y) -> None:
     _capi.call(name, _p(x, "x"), _p(y, "y"), x.numel(), _stream())
 

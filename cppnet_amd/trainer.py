@@ -33,6 +33,8 @@ def load() -> C.CDLL:
         "cnt_last_error": (C.c_char_p, []),
         "cnt_mlp_create": (i32, [C.POINTER(vp), i32, C.POINTER(i64), i32, i32, i32, i64, f32, f32,
                                  f32, f32, C.c_uint64]),
+        "cnt_cnn_create": (i32, [C.POINTER(vp), i32, C.POINTER(i64), i32, C.POINTER(i64), i64, f32,
+                                 f32, f32, f32, C.c_uint64]),
         "cnt_destroy": (i32, [vp]),
         "cnt_num_params": (i32, [vp, C.POINTER(i32)]),
         "cnt_param_size": (i32, [vp, i32, C.POINTER(i64)]),
@@ -42,6 +44,8 @@ def load() -> C.CDLL:
         "cnt_set_batch": (i32, [vp, vp, vp]),
         "cnt_set_batch_device": (i32, [vp, vp, vp]),
         "cnt_step": (i32, [vp, C.POINTER(f32)]),
+        "cnt_forward_backward": (i32, [vp, C.POINTER(f32)]),
+        "cnt_update": (i32, [vp]),
         "cnt_synchronize": (i32, [vp]),
         "cnt_stream": (vp, [vp]),
     }
@@ -88,6 +92,64 @@ def mlp_config(config: int, batch: int | None = None) -> MLPConfig:
     return c
 
 
+@dataclass
+class CNNConfig:
+    """n conv blocks (in, out, kernel, stride, padding) -> ReLU -> MaxPool(pool),
+    then Flatten -> Linear -> softmax-CE; input [N, C, H, W]."""
+    name: str
+    convs: list
+    pool: int
+    input_shape: list
+    classes: int
+    lr: float = 1e-3
+    beta1: float = 0.9
+    beta2: float = 0.999
+    eps: float = 1e-8
+    seed: int = 1234
+    loss: str = "softmax_ce"
+
+    @property
+    def batch(self) -> int:
+        return self.input_shape[0]
+
+    def flat_features(self) -> int:
+        C, H, W = self.input_shape[1:]
+        for (_, oc, k, s, p) in self.convs:
+            H = ((H + 2 * p - k) // s + 1 - self.pool) // self.pool + 1
+            W = ((W + 2 * p - k) // s + 1 - self.pool) // self.pool + 1
+            C = oc
+        return C * H * W
+
+
+def cnn_config(config: int = 3, batch: int | None = None) -> CNNConfig:
+    """Conv 3->32 (3x3, s1, p1) -> ReLU -> MaxPool 2 ->
+    Conv 32->64 -> ReLU -> MaxPool 2 -> Flatten (4096) -> Linear 4096->10."""
+    if config != 3:
+        raise ValueError(f"config {config} is not the CNN config")
+    B = 256 if batch is None else batch
+    return CNNConfig("C3 CNN 2x(conv3x3, ReLU, pool2) -> 4096->10", [(3, 32, 3, 1, 1),
+                     (32, 64, 3, 1, 1)], 2, [B, 3, 32, 32], 10)
+
+
+def synthetic_cnn(cfg: CNNConfig, rng: np.random.Generator):
+    """Conv weights xavier-uniform with fans C*k^2 / OC*k^2 (conv2d.cpp:42-50),
+    biases 0; Linear xavier; X ~ U(0,1) [N,C,H,W]; one-hot uniform labels.
+    All ColMajor flat float32."""
+    params = []
+    for (ic, oc, k, _, _) in cfg.convs:
+        lim = np.sqrt(6.0 / (ic * k * k + oc * k * k))
+        params.append(rng.uniform(-lim, lim, oc * ic * k * k).astype(np.float32))
+        params.append(np.zeros(oc, np.float32))
+    F = cfg.flat_features()
+    params.append(xavier(rng, F, cfg.classes))
+    params.append(np.zeros(cfg.classes, np.float32))
+    X = rng.uniform(0.0, 1.0, int(np.prod(cfg.input_shape))).astype(np.float32)
+    labels = rng.integers(0, cfg.classes, cfg.batch)
+    Y = np.zeros((cfg.classes, cfg.batch), np.float32)
+    Y[labels, np.arange(cfg.batch)] = 1.0
+    return params, X, Y.ravel()
+
+
 def xavier(rng: np.random.Generator, fan_in: int, fan_out: int) -> np.ndarray:
     """xavier-uniform [fan_in, fan_out] (init.cpp:21-33), ColMajor flat."""
     lim = np.sqrt(6.0 / (fan_in + fan_out))
@@ -119,13 +181,23 @@ def synthetic_mlp(cfg: MLPConfig, rng: np.random.Generator):
 class Session:
     """One C++ training session (model + loss + Adam + stream) on cuda:0."""
 
-    def __init__(self, cfg: MLPConfig):
+    def __init__(self, cfg):
         lib = load()
-        sizes = (C.c_int64 * len(cfg.sizes))(*cfg.sizes)
         h = C.c_void_p()
-        _check(lib.cnt_mlp_create(C.byref(h), len(cfg.sizes) - 1, sizes, ACT[cfg.hidden_act],
-                                  ACT[cfg.out_act], LOSS[cfg.loss], cfg.batch, cfg.lr, cfg.beta1,
-                                  cfg.beta2, cfg.eps, cfg.seed))
+        if isinstance(cfg, CNNConfig):
+            spec = [v for c in cfg.convs for v in c]
+            _check(lib.cnt_cnn_create(C.byref(h), len(cfg.convs), (C.c_int64 * len(spec))(*spec),
+                                      cfg.pool, (C.c_int64 * 4)(*cfg.input_shape), cfg.classes,
+                                      cfg.lr, cfg.beta1, cfg.beta2, cfg.eps, cfg.seed))
+            self.x_size = int(np.prod(cfg.input_shape))
+            self.y_size = cfg.batch * cfg.classes
+        else:
+            sizes = (C.c_int64 * len(cfg.sizes))(*cfg.sizes)
+            _check(lib.cnt_mlp_create(C.byref(h), len(cfg.sizes) - 1, sizes, ACT[cfg.hidden_act],
+                                      ACT[cfg.out_act], LOSS[cfg.loss], cfg.batch, cfg.lr,
+                                      cfg.beta1, cfg.beta2, cfg.eps, cfg.seed))
+            self.x_size = cfg.batch * cfg.sizes[0]
+            self.y_size = cfg.batch * cfg.sizes[-1]
         self.h = h
         self.cfg = cfg
 
@@ -180,8 +252,8 @@ class Session:
     def set_batch(self, X: np.ndarray, Y: np.ndarray) -> None:
         X = np.ascontiguousarray(X, np.float32)
         Y = np.ascontiguousarray(Y, np.float32)
-        assert X.size == self.cfg.batch * self.cfg.sizes[0]
-        assert Y.size == self.cfg.batch * self.cfg.sizes[-1]
+        assert X.size == self.x_size, f"X has {X.size} values, the model takes {self.x_size}"
+        assert Y.size == self.y_size, f"Y has {Y.size} values, the model takes {self.y_size}"
         _check(load().cnt_set_batch(self.h, X.ctypes.data, Y.ctypes.data))
 
     def set_batch_device(self, X_ptr: int, Y_ptr: int) -> None:
@@ -194,6 +266,15 @@ class Session:
             return loss.value
         _check(load().cnt_step(self.h, None))
         return None
+
+    def forward_backward(self) -> float:
+        """zero_grad, forward, loss, backward; returns the loss (grads readable)."""
+        loss = C.c_float()
+        _check(load().cnt_forward_backward(self.h, C.byref(loss)))
+        return loss.value
+
+    def update(self) -> None:
+        _check(load().cnt_update(self.h))
 
     def synchronize(self) -> None:
         _check(load().cnt_synchronize(self.h))

@@ -124,6 +124,32 @@ int cnhip_linear_backward(const float* X, const float* W, const float* dY,
 int cnhip_column_sum(const float* in, float* out, int64_t rows, int64_t cols,
                      int accumulate, cnhip_stream_t stream);
 
+/* ---- Conv2D / MaxPool2D / Flatten ----------------------------------------
+ * X [N,C,H,W], W [OC,C,KS,KS], Y [N,OC,HO,WO], HO = (H + 2P - KS)/S + 1.
+ * backward OVERWRITES grad_W / grad_b (the reference zeroes them first,
+ * conv2d.cpp:149-152); b / grad_b / dX may be NULL.
+ * ref: Conv2D::forward/backward src/CppNet/layers/conv2d.cpp:78-198;
+ * conv2d_forward.cu:16-64, conv2d_backward.cu:19-68 */
+int cnhip_conv2d_forward(const float* X, const float* W, const float* b, float* Y,
+                         int64_t N, int64_t C, int64_t H, int64_t Wd, int64_t OC,
+                         int64_t KS, int64_t S, int64_t P, cnhip_stream_t stream);
+int cnhip_conv2d_backward(const float* X, const float* W, const float* dY,
+                          float* grad_W, float* grad_b, float* dX, int64_t N, int64_t C,
+                          int64_t H, int64_t Wd, int64_t OC, int64_t KS, int64_t S,
+                          int64_t P, cnhip_stream_t stream);
+/* MaxPool2D: Y [N,C,HO,WO], HO = (H - pool)/stride + 1 (stride <= 0 means
+ * pool); idx = int32 window-local ph*pool + pw of the first maximum;
+ * backward writes every element of dX (no pre-zeroing needed).
+ * ref: MaxPool2D::forward/backward max_pool2d.cpp:32-131;
+ * maxpool2d_forward.cu:17-59, maxpool2d_backward.cu:16-46.
+ * Flatten (flatten.cpp:15-39) is a ColMajor reshape: no kernel. */
+int cnhip_maxpool2d_forward(const float* X, float* Y, int32_t* idx, int64_t N, int64_t C,
+                            int64_t H, int64_t W, int64_t pool, int64_t stride,
+                            cnhip_stream_t stream);
+int cnhip_maxpool2d_backward(const float* dY, const int32_t* idx, float* dX, int64_t N,
+                             int64_t C, int64_t H, int64_t W, int64_t pool, int64_t stride,
+                             cnhip_stream_t stream);
+
 /* ---- activations (elementwise over n values) -------------------------- */
 /* ReLU: y = max(x,0); dx = dy * (y > 0)   (mask from the cached OUTPUT)
  * ref: relu.cu:14-23, relu_grad.cu:11-19; ReLU::forward/backward

@@ -41,6 +41,14 @@ const char* cnt_last_error(void);
 int cnt_mlp_create(cnt_session** out, int n_linear, const int64_t* sizes, int hidden_act,
                    int out_act, int loss, int64_t batch, float lr, float beta1, float beta2,
                    float eps, uint64_t seed);
+/* CNN: n_conv blocks of Conv2D(in, out, kernel, stride, padding; bias) -> ReLU
+ * -> MaxPool2D(pool), conv_spec holding 5 values per block; then Flatten ->
+ * Linear(C*H*W -> classes) -> SoftmaxCrossEntropy("mean"), Adam.  input_shape
+ * is [N, C, H, W].  Config 3 of the benchmark is an instance of it.
+ * ref: benchmarks/cnn_benckmark.cpp:94-291 (caller pattern) */
+int cnt_cnn_create(cnt_session** out, int n_conv, const int64_t* conv_spec, int pool,
+                   const int64_t* input_shape, int64_t classes, float lr, float beta1,
+                   float beta2, float eps, uint64_t seed);
 int cnt_destroy(cnt_session* s);
 
 int cnt_num_params(cnt_session* s, int* count);
@@ -49,8 +57,8 @@ int cnt_set_param(cnt_session* s, int index, const float* host);
 int cnt_get_param(cnt_session* s, int index, float* host);
 int cnt_get_grad(cnt_session* s, int index, float* host);
 
-/* Uploads one batch (X: [batch, in], Y: [batch, out]) that every later
- * cnt_step() trains on, until the next call. */
+/* Uploads one batch (X: the model's input shape, Y: [batch, outputs]) that
+ * every later cnt_step() trains on, until the next call. */
 int cnt_set_batch(cnt_session* s, const float* x_host, const float* y_host);
 /* Same from device memory already in HBM (copied on the session stream). */
 int cnt_set_batch_device(cnt_session* s, const float* x_dev, const float* y_dev);
@@ -58,6 +66,11 @@ int cnt_set_batch_device(cnt_session* s, const float* x_dev, const float* y_dev)
 /* One train step.  loss_out == NULL keeps the step fully asynchronous;
  * otherwise the stream is synchronised and the step's loss written. */
 int cnt_step(cnt_session* s, float* loss_out);
+/* The two halves of cnt_step: zero_grad + forward + loss + backward (grads
+ * are readable afterwards), then the optimizer update.  Conv2D clears its
+ * gradients inside step() (conv2d.cpp:211-212), so read grads in between. */
+int cnt_forward_backward(cnt_session* s, float* loss_out);
+int cnt_update(cnt_session* s);
 int cnt_synchronize(cnt_session* s);
 /* The hipStream_t the session's kernels run on. */
 void* cnt_stream(cnt_session* s);

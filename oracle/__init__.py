@@ -13,6 +13,7 @@ ORACLE_DIR = Path(__file__).resolve().parent
 ORACLE_SO = ORACLE_DIR / "liboracle.so"
 
 _f = C.POINTER(C.c_float)
+_i = C.POINTER(C.c_int32)
 i64, f32, i32 = C.c_int64, C.c_float, C.c_int
 _SIGS = {
     "cnref_set_threads": (None, [i32]),
@@ -35,6 +36,10 @@ _SIGS = {
     "cnref_mse_backward": (None, [_f, _f, _f, i64, i32]),
     "cnref_softmax_ce_forward": (f32, [_f, _f, _f, i64, i64, i32]),
     "cnref_softmax_ce_backward": (None, [_f, _f, _f, i64, i64, i32]),
+    "cnref_conv2d_forward": (None, [_f, _f, _f, _f] + [i64] * 8),
+    "cnref_conv2d_backward": (None, [_f, _f, _f, _f, _f, _f] + [i64] * 8),
+    "cnref_maxpool2d_forward": (None, [_f, _f, _i, i64, i64, i64, i64, i64, i64]),
+    "cnref_maxpool2d_backward": (None, [_f, _i, _f, i64, i64, i64, i64, i64, i64]),
     "cnref_adam_step": (None, [_f, _f, _f, _f, i64, f32, f32, f32, f32, f32, f32]),
     "cnref_bias_correction": (f32, [f32, i32]),
 }
@@ -64,6 +69,14 @@ def fp(a: np.ndarray | None):
         return None
     assert a.dtype == np.float32 and (a.flags["C_CONTIGUOUS"] or a.flags["F_CONTIGUOUS"])
     return a.ctypes.data_as(_f)
+
+
+def ip(a: np.ndarray | None):
+    """int32* of an int32 numpy buffer (None -> NULL)."""
+    if a is None:
+        return None
+    assert a.dtype == np.int32 and (a.flags["C_CONTIGUOUS"] or a.flags["F_CONTIGUOUS"])
+    return a.ctypes.data_as(_i)
 
 
 def colmajor(rows_logical) -> np.ndarray:

@@ -7,6 +7,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <limits>
 #include <vector>
 
 #ifdef _OPENMP
@@ -214,6 +215,126 @@ void cnref_softmax_ce_backward(const float* sm, const float* t, float* g, int64_
     if (reduction == 0) v *= inv;
     g[i] = v;
   }
+}
+
+// ---------------------------------------------------------------- Conv2D
+// ColMajor index helpers (Eigen default layout).
+static inline int64_t idx4(int64_t a, int64_t b, int64_t c, int64_t d, int64_t A, int64_t B,
+                           int64_t C) {
+  return a + A * (b + B * (c + C * d));
+}
+
+// Conv2D::forward (conv2d.cpp:78-136): per output element, the sum over
+// (ic, kh, kw) in that order of in-bounds input * weight, then + bias.
+void cnref_conv2d_forward(const float* X, const float* Wt, const float* b, float* Y, int64_t N,
+                          int64_t C, int64_t H, int64_t Wd, int64_t OC, int64_t KS, int64_t S,
+                          int64_t P) {
+  const int64_t HO = (H + 2 * P - KS) / S + 1, WO = (Wd + 2 * P - KS) / S + 1;
+#pragma omp parallel for num_threads(g_threads) schedule(static) collapse(2)
+  for (int64_t n = 0; n < N; ++n)
+    for (int64_t oc = 0; oc < OC; ++oc)
+      for (int64_t oh = 0; oh < HO; ++oh)
+        for (int64_t ow = 0; ow < WO; ++ow) {
+          float val = 0.0f;
+          for (int64_t ic = 0; ic < C; ++ic)
+            for (int64_t kh = 0; kh < KS; ++kh)
+              for (int64_t kw = 0; kw < KS; ++kw) {
+                const int64_t ih = oh * S - P + kh, iw = ow * S - P + kw;
+                if (ih >= 0 && ih < H && iw >= 0 && iw < Wd)
+                  val += X[idx4(n, ic, ih, iw, N, C, H)] * Wt[idx4(oc, ic, kh, kw, OC, C, KS)];
+              }
+          if (b) val += b[oc];
+          Y[idx4(n, oc, oh, ow, N, OC, HO)] = val;
+        }
+}
+
+// Conv2D::backward (conv2d.cpp:138-198).  The reference runs one serial
+// scatter loop over (n, oc, oh, ow) that accumulates gb, gW and dX.  Here the
+// same sums are evaluated as two passes that can run in parallel: gW/gb per
+// output channel (each accumulated over (n, oh, ow) in the reference's
+// order) and dX per sample (each accumulated over (oc, oh, ow, ic, kh, kw)
+// in the reference's order).  Grads are overwritten (zeroed first, 149-152).
+void cnref_conv2d_backward(const float* X, const float* Wt, const float* dY, float* gW, float* gb,
+                           float* dX, int64_t N, int64_t C, int64_t H, int64_t Wd, int64_t OC,
+                           int64_t KS, int64_t S, int64_t P) {
+  const int64_t HO = (H + 2 * P - KS) / S + 1, WO = (Wd + 2 * P - KS) / S + 1;
+#pragma omp parallel for num_threads(g_threads) schedule(static)
+  for (int64_t oc = 0; oc < OC; ++oc) {
+    for (int64_t ic = 0; ic < C; ++ic)
+      for (int64_t kh = 0; kh < KS; ++kh)
+        for (int64_t kw = 0; kw < KS; ++kw) gW[idx4(oc, ic, kh, kw, OC, C, KS)] = 0.0f;
+    if (gb) gb[oc] = 0.0f;
+    for (int64_t n = 0; n < N; ++n)
+      for (int64_t oh = 0; oh < HO; ++oh)
+        for (int64_t ow = 0; ow < WO; ++ow) {
+          const float g = dY[idx4(n, oc, oh, ow, N, OC, HO)];
+          if (gb) gb[oc] += g;
+          for (int64_t ic = 0; ic < C; ++ic)
+            for (int64_t kh = 0; kh < KS; ++kh)
+              for (int64_t kw = 0; kw < KS; ++kw) {
+                const int64_t ih = oh * S - P + kh, iw = ow * S - P + kw;
+                if (ih >= 0 && ih < H && iw >= 0 && iw < Wd)
+                  gW[idx4(oc, ic, kh, kw, OC, C, KS)] += X[idx4(n, ic, ih, iw, N, C, H)] * g;
+              }
+        }
+  }
+#pragma omp parallel for num_threads(g_threads) schedule(static)
+  for (int64_t n = 0; n < N; ++n) {
+    for (int64_t ic = 0; ic < C; ++ic)
+      for (int64_t ih = 0; ih < H; ++ih)
+        for (int64_t iw = 0; iw < Wd; ++iw) dX[idx4(n, ic, ih, iw, N, C, H)] = 0.0f;
+    for (int64_t oc = 0; oc < OC; ++oc)
+      for (int64_t oh = 0; oh < HO; ++oh)
+        for (int64_t ow = 0; ow < WO; ++ow) {
+          const float g = dY[idx4(n, oc, oh, ow, N, OC, HO)];
+          for (int64_t ic = 0; ic < C; ++ic)
+            for (int64_t kh = 0; kh < KS; ++kh)
+              for (int64_t kw = 0; kw < KS; ++kw) {
+                const int64_t ih = oh * S - P + kh, iw = ow * S - P + kw;
+                if (ih >= 0 && ih < H && iw >= 0 && iw < Wd)
+                  dX[idx4(n, ic, ih, iw, N, C, H)] += Wt[idx4(oc, ic, kh, kw, OC, C, KS)] * g;
+              }
+        }
+  }
+}
+
+// ---------------------------------------------------------------- MaxPool2D
+// MaxPool2D::forward (max_pool2d.cpp:32-94)
+void cnref_maxpool2d_forward(const float* X, float* Y, int32_t* idx, int64_t N, int64_t C,
+                             int64_t H, int64_t W, int64_t pool, int64_t stride) {
+  const int64_t HO = (H - pool) / stride + 1, WO = (W - pool) / stride + 1;
+  for (int64_t n = 0; n < N; ++n)
+    for (int64_t c = 0; c < C; ++c)
+      for (int64_t oh = 0; oh < HO; ++oh)
+        for (int64_t ow = 0; ow < WO; ++ow) {
+          float mx = -std::numeric_limits<float>::infinity();
+          int32_t mi = 0;
+          for (int64_t ph = 0; ph < pool; ++ph)
+            for (int64_t pw = 0; pw < pool; ++pw) {
+              const float v = X[idx4(n, c, oh * stride + ph, ow * stride + pw, N, C, H)];
+              if (v > mx) {
+                mx = v;
+                mi = (int32_t)(ph * pool + pw);
+              }
+            }
+          Y[idx4(n, c, oh, ow, N, C, HO)] = mx;
+          idx[idx4(n, c, oh, ow, N, C, HO)] = mi;
+        }
+}
+
+// MaxPool2D::backward (max_pool2d.cpp:96-131): zeroed grad, += at argmax.
+void cnref_maxpool2d_backward(const float* dY, const int32_t* idx, float* dX, int64_t N, int64_t C,
+                              int64_t H, int64_t W, int64_t pool, int64_t stride) {
+  const int64_t HO = (H - pool) / stride + 1, WO = (W - pool) / stride + 1;
+  for (int64_t i = 0; i < N * C * H * W; ++i) dX[i] = 0.0f;
+  for (int64_t n = 0; n < N; ++n)
+    for (int64_t c = 0; c < C; ++c)
+      for (int64_t oh = 0; oh < HO; ++oh)
+        for (int64_t ow = 0; ow < WO; ++ow) {
+          const int32_t k = idx[idx4(n, c, oh, ow, N, C, HO)];
+          const int64_t ih = oh * stride + k / pool, iw = ow * stride + k % pool;
+          dX[idx4(n, c, ih, iw, N, C, H)] += dY[idx4(n, c, oh, ow, N, C, HO)];
+        }
 }
 
 // Adam::update (adam.cpp:98-133), per element in order.

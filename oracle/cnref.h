@@ -58,6 +58,24 @@ float cnref_softmax_ce_forward(const float* z, const float* t, float* sm, int64_
 void  cnref_softmax_ce_backward(const float* sm, const float* t, float* g, int64_t B,
                                 int64_t C, int reduction);
 
+/* Conv2D, ColMajor X [N,C,H,W], W [OC,C,KS,KS], Y [N,OC,HO,WO] with
+ * HO = (H + 2P - KS)/S + 1 (conv2d.cpp:78-136 forward; 138-198 backward:
+ * grads OVERWRITE — zeroed, then accumulated over the batch).  b / gb may
+ * be NULL (no bias).  dX is always computed. */
+void cnref_conv2d_forward(const float* X, const float* W, const float* b, float* Y,
+                          int64_t N, int64_t C, int64_t H, int64_t Wd, int64_t OC,
+                          int64_t KS, int64_t S, int64_t P);
+void cnref_conv2d_backward(const float* X, const float* W, const float* dY, float* gW,
+                           float* gb, float* dX, int64_t N, int64_t C, int64_t H, int64_t Wd,
+                           int64_t OC, int64_t KS, int64_t S, int64_t P);
+/* MaxPool2D (max_pool2d.cpp:32-131): HO = (H - pool)/stride + 1, argmax is
+ * the window-local ph*pool + pw of the first maximum (strict >, start -inf);
+ * backward adds dY at the argmax of each window into a zeroed dX. */
+void cnref_maxpool2d_forward(const float* X, float* Y, int32_t* idx, int64_t N, int64_t C,
+                             int64_t H, int64_t W, int64_t pool, int64_t stride);
+void cnref_maxpool2d_backward(const float* dY, const int32_t* idx, float* dX, int64_t N,
+                              int64_t C, int64_t H, int64_t W, int64_t pool, int64_t stride);
+
 /* Adam, one tensor, caller-computed bias corrections (adam.cpp:98-133) */
 void cnref_adam_step(float* W, const float* g, float* m, float* v, int64_t n, float lr,
                      float b1, float b2, float eps, float bc1, float bc2);

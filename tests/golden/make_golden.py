@@ -95,6 +95,27 @@ CASES = [
          Z=[[1.0, 2.0, 3.0]], T=[[0.0, 0.0, 1.0]], expected=[[0.0900, 0.2447, -0.3348]],
          exact=[[a - b for a, b in zip(softmax([1.0, 2.0, 3.0]), [0.0, 0.0, 1.0])]],
          derivation="softmax - target over a batch of 1", tol=0.02),
+    # ---- MaxPool2D (4-D logical [n][c][h][w]) ------------------------------
+    dict(op="maxpool2d_forward", source="tests/layers/test_max_pool2d.cpp:80-99",
+         X=[[[[1.0, 2.0, 3.0, 4.0], [5.0, 6.0, 7.0, 8.0], [9.0, 10.0, 11.0, 12.0],
+              [13.0, 14.0, 15.0, 16.0]]]], pool=2, stride=2,
+         expected=[[[[6.0, 8.0], [14.0, 16.0]]]],
+         exact_argmax=[[[[3, 3], [3, 3]]]],
+         derivation="each window's max is its bottom-right element: ph=1, pw=1 -> 1*2+1 = 3",
+         tol=1e-5),
+    dict(op="maxpool2d_forward", source="tests/layers/test_max_pool2d.cpp:164-175",
+         X=[[[[5.0] * 4] * 4]], pool=2, stride=2, expected=[[[[5.0, 5.0], [5.0, 5.0]]]],
+         exact_argmax=[[[[0, 0], [0, 0]]]],
+         derivation="all ties: strict > keeps the first element of each window (index 0)",
+         tol=1e-5),
+    dict(op="maxpool2d_shape", source="tests/layers/test_max_pool2d.cpp:147-160",
+         shape=[1, 1, 5, 5], pool=3, stride=1, expected_shape=[1, 1, 3, 3]),
+    # ---- Flatten ---------------------------------------------------------------
+    dict(op="flatten_forward", source="tests/layers/test_flatten.cpp:60-79",
+         X=[[[[1.0, 2.0], [3.0, 4.0]], [[5.0, 6.0], [7.0, 8.0]]]],
+         expected_shape=[1, 8], check="sum preserved (36)",
+         exact=[[1.0, 5.0, 3.0, 7.0, 2.0, 6.0, 4.0, 8.0]],
+         derivation="ColMajor reshape [1,2,2,2] -> [1,8]: feature = c + 2*(h + 2*w)"),
     # ---- Adam ----------------------------------------------------------------
     dict(op="adam_first_step", source="src/CppNet/optimizers/adam.cpp:98-133",
          W=[1.0, -2.0, 0.5, 3.0], G=[0.1, -0.3, 2.0, -1e-3],

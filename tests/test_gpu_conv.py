@@ -1,0 +1,109 @@
+"""GPU parity of Conv2D / MaxPool2D (config 3 rows) against the CPU oracle.
+
+Conv: the implicit-GEMM results are contractions, so the relative part of
+the rel 1e-4 / abs 1e-5 bound is taken against max(|ref|, mag), mag = the
+same contraction of |inputs| divided by sqrt(contraction length)
+(oracle_lib.close_mag).  MaxPool: values and int32 argmax bit-exact; dX
+bit-exact for non-overlapping windows (one term per element) and within
+rel 1e-6 for overlapping ones (a different order of a few additions).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import ip
+from oracle_lib import close, close_mag, fp
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+CONV_CASES = [(2, 3, 8, 8, 4, 3, 1, 1), (3, 2, 7, 5, 5, 3, 2, 0), (1, 4, 6, 6, 2, 2, 2, 1),
+              (4, 3, 5, 5, 3, 1, 1, 0), (5, 5, 9, 7, 40, 5, 1, 2), (8, 70, 6, 6, 33, 3, 1, 1),
+              (256, 3, 32, 32, 32, 3, 1, 1), (256, 32, 16, 16, 64, 3, 1, 1)]
+
+
+@pytest.mark.parametrize("N,C,H,W,OC,KS,S,P", CONV_CASES)
+@pytest.mark.parametrize("bias", [True, False])
+def test_conv2d_vs_oracle(gpu, oracle, N, C, H, W, OC, KS, S, P, bias):
+    if bias is False and N == 256:
+        pytest.skip("bias-free path covered at the small shapes")
+    print(f"[conv2d] N={N} C={C} H={H} W={W} OC={OC} KS={KS} S={S} P={P} bias={bias}", flush=True)
+    oracle.cnref_set_threads(16)
+    rng = np.random.default_rng(N + C + OC + KS)
+    HO, WO = (H + 2 * P - KS) // S + 1, (W + 2 * P - KS) // S + 1
+    X = rng.uniform(0, 1, N * C * H * W).astype(np.float32)
+    lim = np.sqrt(6.0 / (C * KS * KS + OC * KS * KS))  # conv2d.cpp:42-50 xavier limit
+    Wt = rng.uniform(-lim, lim, OC * C * KS * KS).astype(np.float32)
+    b = rng.standard_normal(OC).astype(np.float32) if bias else None
+    dY = (rng.standard_normal(N * OC * HO * WO) * 1e-3).astype(np.float32)
+
+    Y = torch.empty(N * OC * HO * WO, device="cuda")
+    from cppnet_amd import ops
+    ops.conv2d_forward(dev(X), dev(Wt), None if b is None else dev(b), Y, N, C, H, W, OC, KS, S, P)
+    gW = torch.full((OC * C * KS * KS,), 7.0, device="cuda")  # must be overwritten
+    gb = torch.full((OC,), 7.0, device="cuda") if bias else None
+    dX = torch.empty(N * C * H * W, device="cuda")
+    ops.conv2d_backward(dev(X), dev(Wt), dev(dY), gW, gb, dX, N, C, H, W, OC, KS, S, P)
+
+    rY = np.zeros(N * OC * HO * WO, np.float32)
+    oracle.cnref_conv2d_forward(fp(X), fp(Wt), fp(b), fp(rY), N, C, H, W, OC, KS, S, P)
+    rgW, rgb, rdX = np.zeros_like(Wt), np.zeros(OC, np.float32), np.zeros_like(X)
+    oracle.cnref_conv2d_backward(fp(X), fp(Wt), fp(dY), fp(rgW), fp(rgb), fp(rdX), N, C, H, W, OC,
+                                 KS, S, P)
+    # magnitudes: the same contractions over |inputs|
+    mY = np.zeros_like(rY)
+    oracle.cnref_conv2d_forward(fp(np.abs(X)), fp(np.abs(Wt)), None, fp(mY), N, C, H, W, OC, KS, S, P)
+    mgW, mgb, mdX = np.zeros_like(Wt), np.zeros(OC, np.float32), np.zeros_like(X)
+    oracle.cnref_conv2d_backward(fp(np.abs(X)), fp(np.abs(Wt)), fp(np.abs(dY)), fp(mgW), fp(mgb),
+                                 fp(mdX), N, C, H, W, OC, KS, S, P)
+    for got, want, mag, name in [
+            (host(Y), rY, mY / np.sqrt(C * KS * KS), "Y"),
+            (host(gW), rgW, mgW / np.sqrt(N * HO * WO), "grad_W"),
+            (host(dX), rdX, mdX / np.sqrt(OC * KS * KS), "dX")] + (
+            [(host(gb), rgb, mgb / np.sqrt(N * HO * WO), "grad_b")] if bias else []):
+        ok, msg = close_mag(got, want, mag, 1e-4, 1e-5)
+        assert ok, f"{name}: {msg}"
+
+
+POOL_CASES = [(2, 3, 8, 8, 2, 2), (3, 2, 5, 5, 3, 1), (1, 4, 7, 9, 2, 3), (4, 2, 6, 6, 3, 2),
+              (7, 3, 4, 4, 2, -1), (256, 32, 32, 32, 2, 2), (256, 64, 16, 16, 2, 2)]
+
+
+@pytest.mark.parametrize("N,C,H,W,p,s", POOL_CASES)
+def test_maxpool_vs_oracle(gpu, oracle, N, C, H, W, p, s):
+    print(f"[maxpool] N={N} C={C} H={H} W={W} pool={p} stride={s}", flush=True)
+    rng = np.random.default_rng(N + C + H + W + p)
+    st = s if s > 0 else p
+    HO, WO = (H - p) // st + 1, (W - p) // st + 1
+    # quantised values: many exact ties, so "first maximum wins" is exercised
+    X = rng.integers(0, 6, N * C * H * W).astype(np.float32)
+    X[: min(8, X.size)] = -np.inf
+    dY = rng.standard_normal(N * C * HO * WO).astype(np.float32)
+    Y = torch.empty(N * C * HO * WO, device="cuda")
+    I = torch.empty(N * C * HO * WO, dtype=torch.int32, device="cuda")
+    dX = torch.full((N * C * H * W,), 3.0, device="cuda")  # every element must be written
+    from cppnet_amd import ops
+    ops.maxpool2d_forward(dev(X), Y, I, N, C, H, W, p, s)
+    ops.maxpool2d_backward(dev(dY), I, dX, N, C, H, W, p, s)
+    rY, rI = np.zeros(N * C * HO * WO, np.float32), np.zeros(N * C * HO * WO, np.int32)
+    oracle.cnref_maxpool2d_forward(fp(X), fp(rY), ip(rI), N, C, H, W, p, st)
+    rdX = np.zeros_like(X)
+    oracle.cnref_maxpool2d_backward(fp(dY), ip(rI), fp(rdX), N, C, H, W, p, st)
+    np.testing.assert_array_equal(host(Y), rY)
+    np.testing.assert_array_equal(host(I), rI)
+    if st >= p:
+        np.testing.assert_array_equal(host(dX), rdX)
+    else:
+        ok, msg = close(host(dX), rdX, 1e-6, 1e-7)
+        assert ok, msg
+    # every upstream gradient lands somewhere exactly once
+    assert abs(float(host(dX).sum()) - float(dY.sum())) <= 1e-3 * max(1.0, float(np.abs(dY).sum()))
