@@ -210,6 +210,59 @@ int cnt_cnn_create(cnt_session** out, int n_conv, const int64_t* conv_spec, int 
     });
 }
 
+int cnt_rnn_create(cnt_session** out, int cell, int64_t batch, int64_t seq_len, int64_t input_size,
+                   int64_t hidden_size, int64_t out_features, float lr, float beta1, float beta2,
+                   float eps, uint64_t seed)
+{
+    return guarded("cnt_rnn_create", [&] {
+        if (!out) throw std::invalid_argument("NULL out pointer");
+        *out = nullptr;
+        if (batch <= 0 || seq_len <= 0) throw std::invalid_argument("batch and seq_len must be positive");
+        auto s = new_session(seed);
+        StreamScope scope(s.get());
+        std::shared_ptr<Layers::RecurrentBase> rnn;
+        if (cell == 0)
+        {
+            auto l = std::make_shared<Layers::LSTM>(static_cast<int>(input_size), static_cast<int>(hidden_size),
+                                                    true, "gpu");
+            s->model.add_layer(l);
+            rnn = l;
+        }
+        else if (cell == 1)
+        {
+            auto g = std::make_shared<Layers::GRU>(static_cast<int>(input_size), static_cast<int>(hidden_size),
+                                                   true, "gpu");
+            s->model.add_layer(g);
+            rnn = g;
+        }
+        else
+            throw std::invalid_argument("cell must be 0 (LSTM) or 1 (GRU)");
+        s->keep.push_back(rnn);
+        Layers::RecurrentBase* r = rnn.get();
+        s->params.push_back({[r]() -> DeviceTensor& { return r->W_ih(); },
+                             [r]() -> DeviceTensor& { return r->grad_W_ih(); }});
+        s->params.push_back({[r]() -> DeviceTensor& { return r->W_hh(); },
+                             [r]() -> DeviceTensor& { return r->grad_W_hh(); }});
+        s->params.push_back({[r]() -> DeviceTensor& { return r->bias(); },
+                             [r]() -> DeviceTensor& { return r->grad_bias(); }});
+        auto last = std::make_shared<Layers::SequenceLast>();
+        s->model.add_layer(last);
+        s->keep.push_back(last);
+        auto fc = std::make_shared<Layers::Linear>(static_cast<int>(hidden_size), static_cast<int>(out_features),
+                                                   "fc", true, true, "gpu", "xavier");
+        s->model.add_layer(fc);
+        s->keep.push_back(fc);
+        s->add_params(fc);
+        s->loss = make_loss(CNT_LOSS_MSE);
+        s->adam = std::make_unique<Optimizers::Adam>(beta1, beta2, eps, "gpu");
+        s->lr = lr;
+        s->X = DeviceTensor::zeros({batch, seq_len, input_size});
+        s->Y = DeviceTensor::zeros({batch, out_features});
+        Device::synchronize();
+        *out = s.release();
+    });
+}
+
 int cnt_destroy(cnt_session* s)
 {
     return guarded("cnt_destroy", [&] {

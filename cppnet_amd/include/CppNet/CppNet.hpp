@@ -13,6 +13,9 @@
 #include "CppNet/layers/conv2d.hpp"
 #include "CppNet/layers/max_pool2d.hpp"
 #include "CppNet/layers/flatten.hpp"
+#include "CppNet/layers/lstm.hpp"
+#include "CppNet/layers/gru.hpp"
+#include "CppNet/layers/sequence_last.hpp"
 #include "CppNet/activations/activation.hpp"
 #include "CppNet/activations/relu.hpp"
 #include "CppNet/activations/sigmoid.hpp"

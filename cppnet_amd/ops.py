@@ -91,6 +91,35 @@ def maxpool2d_backward(dY, idx, dX, N, C, H, W, pool=2, stride=-1) -> None:
                pool, stride, _stream())
 
 
+def lstm_forward(X, W_ih, W_hh, b, Y, gates, c, tanh_c, B, S, I, H) -> None:
+    _capi.call("cnhip_lstm_forward", *(_p(t) for t in (X, W_ih, W_hh, b, Y, gates, c, tanh_c)),
+               B, S, I, H, _stream())
+
+
+def lstm_backward(X, W_ih, W_hh, Y, gates, c, tanh_c, dY, gW_ih, gW_hh, gb, dX, B, S, I, H):
+    _capi.call("cnhip_lstm_backward", *(_p(t) for t in (X, W_ih, W_hh, Y, gates, c, tanh_c, dY,
+                                                        gW_ih, gW_hh, gb, dX)), B, S, I, H,
+               _stream())
+
+
+def gru_forward(X, W_ih, W_hh, b, Y, gates, rh, B, S, I, H) -> None:
+    _capi.call("cnhip_gru_forward", *(_p(t) for t in (X, W_ih, W_hh, b, Y, gates, rh)), B, S, I, H,
+               _stream())
+
+
+def gru_backward(X, W_ih, W_hh, Y, gates, rh, dY, gW_ih, gW_hh, gb, dX, B, S, I, H) -> None:
+    _capi.call("cnhip_gru_backward", *(_p(t) for t in (X, W_ih, W_hh, Y, gates, rh, dY, gW_ih,
+                                                       gW_hh, gb, dX)), B, S, I, H, _stream())
+
+
+def seq_select(Y, out, B, S, D, t) -> None:
+    _capi.call("cnhip_seq_select", _p(Y), _p(out), B, S, D, t, _stream())
+
+
+def seq_scatter(inp, Y, B, S, D, t) -> None:
+    _capi.call("cnhip_seq_scatter", _p(inp), _p(Y), B, S, D, t, _stream())
+
+
 def _unary(name: str, x, y) -> None:
     _capi.call(name, _p(x, "x"), _p(y, "y"), x.numel(), _stream())
 

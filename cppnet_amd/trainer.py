@@ -35,6 +35,8 @@ def load() -> C.CDLL:
                                  f32, f32, C.c_uint64]),
         "cnt_cnn_create": (i32, [C.POINTER(vp), i32, C.POINTER(i64), i32, C.POINTER(i64), i64, f32,
                                  f32, f32, f32, C.c_uint64]),
+        "cnt_rnn_create": (i32, [C.POINTER(vp), i32, i64, i64, i64, i64, i64, f32, f32, f32, f32,
+                                 C.c_uint64]),
         "cnt_destroy": (i32, [vp]),
         "cnt_num_params": (i32, [vp, C.POINTER(i32)]),
         "cnt_param_size": (i32, [vp, i32, C.POINTER(i64)]),
@@ -150,6 +152,52 @@ def synthetic_cnn(cfg: CNNConfig, rng: np.random.Generator):
     return params, X, Y.ravel()
 
 
+@dataclass
+class RNNConfig:
+    """cell ("lstm" | "gru") over X [B, S, I] -> last hidden state -> Linear(H -> O) -> MSE."""
+    name: str
+    cell: str
+    batch: int
+    seq_len: int
+    input_size: int
+    hidden: int
+    out_features: int = 1
+    lr: float = 1e-3
+    beta1: float = 0.9
+    beta2: float = 0.999
+    eps: float = 1e-8
+    seed: int = 1234
+    loss: str = "mse"
+
+
+def rnn_config(config: int = 4, batch: int | None = None, seq_len: int | None = None,
+               cell: str = "lstm") -> RNNConfig:
+    """LSTM input 128, hidden 512, seq 64, batch 128,
+    final hidden state -> Linear 512->1 -> MSE(mean)."""
+    if config != 4:
+        raise ValueError(f"config {config} is not the sequence config")
+    return RNNConfig(f"C4 {cell.upper()} 128->512, T=64 -> 512->1, MSE", cell,
+                     128 if batch is None else batch, 64 if seq_len is None else seq_len, 128, 512)
+
+
+def synthetic_rnn(cfg: RNNConfig, rng: np.random.Generator):
+    """W_ih, W_hh uniform with limits sqrt(6/(I+H)), sqrt(6/2H) (lstm.cpp:42-45);
+    bias 0 with the LSTM forget block at 1 (lstm.cpp:47-49); Linear xavier;
+    X ~ N(0,1) [B,S,I]; target ~ N(0,1) [B,1]."""
+    G = (4 if cfg.cell == "lstm" else 3) * cfg.hidden
+    I, H = cfg.input_size, cfg.hidden
+    lih, lhh = np.sqrt(6.0 / (I + H)), np.sqrt(6.0 / (2 * H))
+    b = np.zeros(G, np.float32)
+    if cfg.cell == "lstm":
+        b[H:2 * H] = 1.0
+    params = [rng.uniform(-lih, lih, I * G).astype(np.float32),
+              rng.uniform(-lhh, lhh, H * G).astype(np.float32), b,
+              xavier(rng, H, cfg.out_features), np.zeros(cfg.out_features, np.float32)]
+    X = rng.standard_normal(cfg.batch * cfg.seq_len * I).astype(np.float32)
+    Y = rng.standard_normal(cfg.batch * cfg.out_features).astype(np.float32)
+    return params, X, Y
+
+
 def xavier(rng: np.random.Generator, fan_in: int, fan_out: int) -> np.ndarray:
     """xavier-uniform [fan_in, fan_out] (init.cpp:21-33), ColMajor flat."""
     lim = np.sqrt(6.0 / (fan_in + fan_out))
@@ -184,7 +232,13 @@ class Session:
     def __init__(self, cfg):
         lib = load()
         h = C.c_void_p()
-        if isinstance(cfg, CNNConfig):
+        if isinstance(cfg, RNNConfig):
+            _check(lib.cnt_rnn_create(C.byref(h), 0 if cfg.cell == "lstm" else 1, cfg.batch,
+                                      cfg.seq_len, cfg.input_size, cfg.hidden, cfg.out_features,
+                                      cfg.lr, cfg.beta1, cfg.beta2, cfg.eps, cfg.seed))
+            self.x_size = cfg.batch * cfg.seq_len * cfg.input_size
+            self.y_size = cfg.batch * cfg.out_features
+        elif isinstance(cfg, CNNConfig):
             spec = [v for c in cfg.convs for v in c]
             _check(lib.cnt_cnn_create(C.byref(h), len(cfg.convs), (C.c_int64 * len(spec))(*spec),
                                       cfg.pool, (C.c_int64 * 4)(*cfg.input_shape), cfg.classes,

@@ -150,6 +150,40 @@ int cnhip_maxpool2d_backward(const float* dY, const int32_t* idx, float* dX, int
                              int64_t C, int64_t H, int64_t W, int64_t pool, int64_t stride,
                              cnhip_stream_t stream);
 
+/* ---- recurrent layers ----------------------------------------------------
+ * X [B,S,I], Y [B,S,H] ColMajor (row n + B*t of a [B*S, .] matrix).
+ * LSTM: W_ih [I,4H], W_hh [H,4H], b [4H], gate blocks i,f,g,o; h0 = c0 = 0.
+ * forward writes Y and the caches gates (activations, [B*S,4H]), c and
+ * tanh_c ([B*S,H]); backward reads them and OVERWRITES the grads
+ * (lstm.cpp:158-160); dX may be NULL.
+ * ref: LSTM::forward/backward src/CppNet/layers/lstm.cpp:63-253;
+ * lstm_cell.cu:21-114 */
+int cnhip_lstm_forward(const float* X, const float* W_ih, const float* W_hh, const float* b,
+                       float* Y, float* gates, float* c, float* tanh_c, int64_t B, int64_t S,
+                       int64_t I, int64_t H, cnhip_stream_t stream);
+int cnhip_lstm_backward(const float* X, const float* W_ih, const float* W_hh, const float* Y,
+                        const float* gates, const float* c, const float* tanh_c,
+                        const float* dY, float* grad_W_ih, float* grad_W_hh, float* grad_b,
+                        float* dX, int64_t B, int64_t S, int64_t I, int64_t H,
+                        cnhip_stream_t stream);
+/* GRU: W_ih [I,3H], W_hh [H,3H], b [3H], gate blocks z,r,n with
+ * n = tanh(x W_in + (r*h) W_hn + b_n), h = (1-z) n + z h_prev; caches gates
+ * (z,r,n activations [B*S,3H]) and rh = r*h_prev [B*S,H].
+ * ref: GRU::forward/backward src/CppNet/layers/gru.cpp:56-297; gru_cell.cu:20-140 */
+int cnhip_gru_forward(const float* X, const float* W_ih, const float* W_hh, const float* b,
+                      float* Y, float* gates, float* rh, int64_t B, int64_t S, int64_t I,
+                      int64_t H, cnhip_stream_t stream);
+int cnhip_gru_backward(const float* X, const float* W_ih, const float* W_hh, const float* Y,
+                       const float* gates, const float* rh, const float* dY, float* grad_W_ih,
+                       float* grad_W_hh, float* grad_b, float* dX, int64_t B, int64_t S,
+                       int64_t I, int64_t H, cnhip_stream_t stream);
+/* out[B,D] = Y[:, t, :]; and Y = 0 except Y[:, t, :] = in.  The harness's
+ * last-hidden-state slice and its gradient (sequence_benckmark.cpp:152-170). */
+int cnhip_seq_select(const float* Y, float* out, int64_t B, int64_t S, int64_t D, int64_t t,
+                     cnhip_stream_t stream);
+int cnhip_seq_scatter(const float* in, float* Y, int64_t B, int64_t S, int64_t D, int64_t t,
+                      cnhip_stream_t stream);
+
 /* ---- activations (elementwise over n values) -------------------------- */
 /* ReLU: y = max(x,0); dx = dy * (y > 0)   (mask from the cached OUTPUT)
  * ref: relu.cu:14-23, relu_grad.cu:11-19; ReLU::forward/backward

@@ -49,6 +49,14 @@ int cnt_mlp_create(cnt_session** out, int n_linear, const int64_t* sizes, int hi
 int cnt_cnn_create(cnt_session** out, int n_conv, const int64_t* conv_spec, int pool,
                    const int64_t* input_shape, int64_t classes, float lr, float beta1,
                    float beta2, float eps, uint64_t seed);
+/* Sequence regressor: LSTM (cell 0) or GRU (cell 1) over X [batch, seq_len,
+ * input_size] -> last hidden state -> Linear(hidden -> out_features) ->
+ * MSE("mean"), Adam.  Parameters: W_ih, W_hh, b of the cell, then W, b of the
+ * Linear.  Config 4 of the benchmark is the LSTM instance.
+ * ref: benchmarks/sequence_benckmark.cpp:64-192 (caller pattern) */
+int cnt_rnn_create(cnt_session** out, int cell, int64_t batch, int64_t seq_len,
+                   int64_t input_size, int64_t hidden_size, int64_t out_features, float lr,
+                   float beta1, float beta2, float eps, uint64_t seed);
 int cnt_destroy(cnt_session* s);
 
 int cnt_num_params(cnt_session* s, int* count);

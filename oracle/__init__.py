@@ -40,6 +40,10 @@ _SIGS = {
     "cnref_conv2d_backward": (None, [_f, _f, _f, _f, _f, _f] + [i64] * 8),
     "cnref_maxpool2d_forward": (None, [_f, _f, _i, i64, i64, i64, i64, i64, i64]),
     "cnref_maxpool2d_backward": (None, [_f, _i, _f, i64, i64, i64, i64, i64, i64]),
+    "cnref_lstm_forward": (None, [_f] * 8 + [i64] * 4),
+    "cnref_lstm_backward": (None, [_f] * 12 + [i64] * 4),
+    "cnref_gru_forward": (None, [_f] * 7 + [i64] * 4),
+    "cnref_gru_backward": (None, [_f] * 11 + [i64] * 4),
     "cnref_adam_step": (None, [_f, _f, _f, _f, i64, f32, f32, f32, f32, f32, f32]),
     "cnref_bias_correction": (f32, [f32, i32]),
 }

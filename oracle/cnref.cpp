@@ -337,6 +337,200 @@ void cnref_maxpool2d_backward(const float* dY, const int32_t* idx, float* dX, in
         }
 }
 
+// ---------------------------------------------------------------- LSTM / GRU
+static inline float sigm(float x) { return 1.0f / (1.0f + std::exp(-x)); }
+
+// x_t = X[:, t, :] as a dense [B, I] ColMajor matrix (lstm.cpp:98-101)
+static std::vector<float> slice_t(const float* X, int64_t B, int64_t S, int64_t D, int64_t t) {
+  std::vector<float> x((size_t)(B * D));
+  for (int64_t d = 0; d < D; ++d)
+    for (int64_t n = 0; n < B; ++n) x[n + B * d] = X[n + B * t + B * S * d];
+  return x;
+}
+
+// LSTM::forward (lstm.cpp:63-149): per step, gates = x_t W_ih + h W_hh, then
+// i,f,o = sigmoid(. + b), g = tanh(. + b), c = f c_prev + i g, h = o tanh(c).
+void cnref_lstm_forward(const float* X, const float* Wih, const float* Whh, const float* b,
+                        float* Y, float* gates, float* c, float* tanh_c, int64_t B, int64_t S,
+                        int64_t I, int64_t H) {
+  const int64_t G = 4 * H, BS = B * S;
+  std::vector<float> h((size_t)(B * H), 0.f), cp((size_t)(B * H), 0.f);
+  std::vector<float> gx((size_t)(B * G)), gh((size_t)(B * G));
+  for (int64_t t = 0; t < S; ++t) {
+    std::vector<float> x = slice_t(X, B, S, I, t);
+    cnref_gemm_f32(0, 0, B, G, I, 1.f, x.data(), B, Wih, I, 0.f, gx.data(), B, nullptr, 0);
+    cnref_gemm_f32(0, 0, B, G, H, 1.f, h.data(), B, Whh, H, 0.f, gh.data(), B, nullptr, 0);
+    for (int64_t n = 0; n < B; ++n)
+      for (int64_t d = 0; d < H; ++d) {
+        float pre[4];
+        for (int q = 0; q < 4; ++q) {
+          const int64_t col = d + q * H;
+          pre[q] = (gx[n + B * col] + gh[n + B * col]) + b[col];
+        }
+        const float ig = sigm(pre[0]), fg = sigm(pre[1]), gg = std::tanh(pre[2]), og = sigm(pre[3]);
+        const float ct = fg * cp[n + B * d] + ig * gg;
+        const float tc = std::tanh(ct);
+        const float ht = og * tc;
+        const int64_t row = n + B * t;
+        gates[row + BS * (d + 0 * H)] = ig;
+        gates[row + BS * (d + 1 * H)] = fg;
+        gates[row + BS * (d + 2 * H)] = gg;
+        gates[row + BS * (d + 3 * H)] = og;
+        c[row + BS * d] = ct;
+        tanh_c[row + BS * d] = tc;
+        Y[row + BS * d] = ht;
+      }
+    for (int64_t d = 0; d < H; ++d)
+      for (int64_t n = 0; n < B; ++n) {
+        h[n + B * d] = Y[n + B * t + BS * d];
+        cp[n + B * d] = c[n + B * t + BS * d];
+      }
+  }
+}
+
+// LSTM::backward (lstm.cpp:151-253), BPTT from t = S-1 down to 0.
+void cnref_lstm_backward(const float* X, const float* Wih, const float* Whh, const float* Y,
+                         const float* gates, const float* c, const float* tanh_c,
+                         const float* dY, float* gWih, float* gWhh, float* gb, float* dX,
+                         int64_t B, int64_t S, int64_t I, int64_t H) {
+  const int64_t G = 4 * H, BS = B * S;
+  for (int64_t i = 0; i < I * G; ++i) gWih[i] = 0.f;
+  for (int64_t i = 0; i < H * G; ++i) gWhh[i] = 0.f;
+  for (int64_t i = 0; i < G; ++i) gb[i] = 0.f;
+  std::vector<float> dh_next((size_t)(B * H), 0.f), dc_next((size_t)(B * H), 0.f);
+  std::vector<float> dg((size_t)(B * G)), tmp_ih((size_t)(I * G)), tmp_hh((size_t)(H * G));
+  std::vector<float> dx((size_t)(B * I));
+  for (int64_t t = S - 1; t >= 0; --t) {
+    for (int64_t n = 0; n < B; ++n)
+      for (int64_t d = 0; d < H; ++d) {
+        const int64_t row = n + B * t, e = n + B * d;
+        const float ig = gates[row + BS * d], fg = gates[row + BS * (d + H)];
+        const float gg = gates[row + BS * (d + 2 * H)], og = gates[row + BS * (d + 3 * H)];
+        const float tc = tanh_c[row + BS * d];
+        const float dh = dY[row + BS * d] + dh_next[e];
+        const float dc = dh * og * (1.0f - tc * tc) + dc_next[e];
+        const float cprev = t > 0 ? c[(n + B * (t - 1)) + BS * d] : 0.0f;
+        dg[n + B * (d + 0 * H)] = dc * gg * ig * (1.0f - ig);
+        dg[n + B * (d + 1 * H)] = dc * cprev * fg * (1.0f - fg);
+        dg[n + B * (d + 2 * H)] = dc * ig * (1.0f - gg * gg);
+        dg[n + B * (d + 3 * H)] = dh * tc * og * (1.0f - og);
+        dc_next[e] = dc * fg;
+      }
+    std::vector<float> x = slice_t(X, B, S, I, t);
+    std::vector<float> hp = t > 0 ? slice_t(Y, B, S, H, t - 1) : std::vector<float>((size_t)(B * H), 0.f);
+    cnref_gemm_f32(1, 0, I, G, B, 1.f, x.data(), B, dg.data(), B, 0.f, tmp_ih.data(), I, nullptr, 0);
+    cnref_gemm_f32(1, 0, H, G, B, 1.f, hp.data(), B, dg.data(), B, 0.f, tmp_hh.data(), H, nullptr, 0);
+    for (int64_t i = 0; i < I * G; ++i) gWih[i] += tmp_ih[i];
+    for (int64_t i = 0; i < H * G; ++i) gWhh[i] += tmp_hh[i];
+    for (int64_t g = 0; g < G; ++g)
+      for (int64_t n = 0; n < B; ++n) gb[g] += dg[n + B * g];
+    if (dX) {
+      cnref_gemm_f32(0, 1, B, I, G, 1.f, dg.data(), B, Wih, I, 0.f, dx.data(), B, nullptr, 0);
+      for (int64_t d = 0; d < I; ++d)
+        for (int64_t n = 0; n < B; ++n) dX[n + B * t + BS * d] = dx[n + B * d];
+    }
+    cnref_gemm_f32(0, 1, B, H, G, 1.f, dg.data(), B, Whh, H, 0.f, dh_next.data(), B, nullptr, 0);
+  }
+}
+
+// GRU::forward (gru.cpp:56-149).  h_gates is computed over all 3H columns, as
+// the reference does, though only the z and r blocks are used.
+void cnref_gru_forward(const float* X, const float* Wih, const float* Whh, const float* b,
+                       float* Y, float* gates, float* rh, int64_t B, int64_t S, int64_t I,
+                       int64_t H) {
+  const int64_t G = 3 * H, BS = B * S;
+  std::vector<float> h((size_t)(B * H), 0.f), gx((size_t)(B * G)), gh((size_t)(B * G));
+  std::vector<float> rhv((size_t)(B * H)), proj((size_t)(B * H));
+  for (int64_t t = 0; t < S; ++t) {
+    std::vector<float> x = slice_t(X, B, S, I, t);
+    cnref_gemm_f32(0, 0, B, G, I, 1.f, x.data(), B, Wih, I, 0.f, gx.data(), B, nullptr, 0);
+    cnref_gemm_f32(0, 0, B, G, H, 1.f, h.data(), B, Whh, H, 0.f, gh.data(), B, nullptr, 0);
+    std::vector<float> zg((size_t)(B * H)), rg((size_t)(B * H));
+    for (int64_t d = 0; d < H; ++d)
+      for (int64_t n = 0; n < B; ++n) {
+        const int64_t e = n + B * d;
+        zg[e] = sigm((gx[n + B * d] + gh[n + B * d]) + b[d]);
+        rg[e] = sigm((gx[n + B * (d + H)] + gh[n + B * (d + H)]) + b[d + H]);
+        rhv[e] = rg[e] * h[e];
+      }
+    // rh . W_hn, W_hn = columns [2H, 3H) of W_hh (gru.cpp:111-116)
+    cnref_gemm_f32(0, 0, B, H, H, 1.f, rhv.data(), B, Whh + H * 2 * H, H, 0.f, proj.data(), B, nullptr, 0);
+    for (int64_t d = 0; d < H; ++d)
+      for (int64_t n = 0; n < B; ++n) {
+        const int64_t e = n + B * d, row = n + B * t;
+        const float nc = std::tanh((gx[n + B * (d + 2 * H)] + proj[e]) + b[d + 2 * H]);
+        const float ht = (1.0f - zg[e]) * nc + zg[e] * h[e];
+        gates[row + BS * d] = zg[e];
+        gates[row + BS * (d + H)] = rg[e];
+        gates[row + BS * (d + 2 * H)] = nc;
+        rh[row + BS * d] = rhv[e];
+        Y[row + BS * d] = ht;
+      }
+    for (int64_t d = 0; d < H; ++d)
+      for (int64_t n = 0; n < B; ++n) h[n + B * d] = Y[n + B * t + BS * d];
+  }
+}
+
+// GRU::backward (gru.cpp:151-297)
+void cnref_gru_backward(const float* X, const float* Wih, const float* Whh, const float* Y,
+                        const float* gates, const float* rh, const float* dY, float* gWih,
+                        float* gWhh, float* gb, float* dX, int64_t B, int64_t S, int64_t I,
+                        int64_t H) {
+  const int64_t G = 3 * H, BS = B * S;
+  for (int64_t i = 0; i < I * G; ++i) gWih[i] = 0.f;
+  for (int64_t i = 0; i < H * G; ++i) gWhh[i] = 0.f;
+  for (int64_t i = 0; i < G; ++i) gb[i] = 0.f;
+  std::vector<float> dh_next((size_t)(B * H), 0.f), dg((size_t)(B * G)), dhp((size_t)(B * H));
+  std::vector<float> dn_raw((size_t)(B * H)), d_rh((size_t)(B * H)), dzr((size_t)(B * H));
+  std::vector<float> tmp_ih((size_t)(I * G)), tmp((size_t)(H * G)), dx((size_t)(B * I));
+  const float* Whn = Whh + H * 2 * H;
+  for (int64_t t = S - 1; t >= 0; --t) {
+    std::vector<float> hp = t > 0 ? slice_t(Y, B, S, H, t - 1) : std::vector<float>((size_t)(B * H), 0.f);
+    for (int64_t d = 0; d < H; ++d)
+      for (int64_t n = 0; n < B; ++n) {
+        const int64_t e = n + B * d, row = n + B * t;
+        const float zg = gates[row + BS * d], nc = gates[row + BS * (d + 2 * H)];
+        const float dh = dY[row + BS * d] + dh_next[e];
+        const float dn = dh * (1.0f - zg);
+        const float dz = dh * (hp[e] - nc);
+        dhp[e] = dh * zg;
+        dn_raw[e] = dn * (1.0f - nc * nc);
+        dg[n + B * d] = dz * zg * (1.0f - zg);
+        dg[n + B * (d + 2 * H)] = dn_raw[e];
+      }
+    // d_rh = dn_raw W_hn^T
+    cnref_gemm_f32(0, 1, B, H, H, 1.f, dn_raw.data(), B, Whn, H, 0.f, d_rh.data(), B, nullptr, 0);
+    for (int64_t d = 0; d < H; ++d)
+      for (int64_t n = 0; n < B; ++n) {
+        const int64_t e = n + B * d, row = n + B * t;
+        const float rg = gates[row + BS * (d + H)];
+        const float dr = d_rh[e] * hp[e];
+        dg[n + B * (d + H)] = dr * rg * (1.0f - rg);
+        dhp[e] += d_rh[e] * rg;
+      }
+    std::vector<float> x = slice_t(X, B, S, I, t);
+    cnref_gemm_f32(1, 0, I, G, B, 1.f, x.data(), B, dg.data(), B, 0.f, tmp_ih.data(), I, nullptr, 0);
+    for (int64_t i = 0; i < I * G; ++i) gWih[i] += tmp_ih[i];
+    // z and r blocks against h_prev, n block against r*h_prev (gru.cpp:240-251)
+    std::vector<float> rht = slice_t(rh, B, S, H, t);
+    cnref_gemm_f32(1, 0, H, 2 * H, B, 1.f, hp.data(), B, dg.data(), B, 0.f, tmp.data(), H, nullptr, 0);
+    for (int64_t i = 0; i < H * 2 * H; ++i) gWhh[i] += tmp[i];
+    cnref_gemm_f32(1, 0, H, H, B, 1.f, rht.data(), B, dg.data() + B * 2 * H, B, 0.f, tmp.data(), H,
+                   nullptr, 0);
+    for (int64_t i = 0; i < H * H; ++i) gWhh[H * 2 * H + i] += tmp[i];
+    for (int64_t g = 0; g < G; ++g)
+      for (int64_t n = 0; n < B; ++n) gb[g] += dg[n + B * g];
+    if (dX) {
+      cnref_gemm_f32(0, 1, B, I, G, 1.f, dg.data(), B, Wih, I, 0.f, dx.data(), B, nullptr, 0);
+      for (int64_t d = 0; d < I; ++d)
+        for (int64_t n = 0; n < B; ++n) dX[n + B * t + BS * d] = dx[n + B * d];
+    }
+    // dh_next = dh_prev + dgates[z,r] W_hh[:, 0:2H]^T (gru.cpp:262-277)
+    cnref_gemm_f32(0, 1, B, H, 2 * H, 1.f, dg.data(), B, Whh, H, 0.f, dzr.data(), B, nullptr, 0);
+    for (int64_t e = 0; e < B * H; ++e) dh_next[e] = dhp[e] + dzr[e];
+  }
+}
+
 // Adam::update (adam.cpp:98-133), per element in order.
 void cnref_adam_step(float* W, const float* g, float* m, float* v, int64_t n, float lr, float b1,
                      float b2, float eps, float bc1, float bc2) {

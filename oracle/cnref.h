@@ -76,6 +76,29 @@ void cnref_maxpool2d_forward(const float* X, float* Y, int32_t* idx, int64_t N, 
 void cnref_maxpool2d_backward(const float* dY, const int32_t* idx, float* dX, int64_t N,
                               int64_t C, int64_t H, int64_t W, int64_t pool, int64_t stride);
 
+/* LSTM (lstm.cpp:63-253).  X [B,S,I], Y [B,S,H] ColMajor; W_ih [I,4H],
+ * W_hh [H,4H], b [4H] with gate column blocks i,f,g,o.  h0 = c0 = 0.
+ * Forward caches, as [B*S, .] matrices (row n + B*t): gates = activations
+ * i,f,g,o [B*S,4H], c [B*S,H], tanh_c [B*S,H].  Backward overwrites the
+ * grads (lstm.cpp:158-160); dX may be NULL. */
+void cnref_lstm_forward(const float* X, const float* Wih, const float* Whh, const float* b,
+                        float* Y, float* gates, float* c, float* tanh_c, int64_t B, int64_t S,
+                        int64_t I, int64_t H);
+void cnref_lstm_backward(const float* X, const float* Wih, const float* Whh, const float* Y,
+                         const float* gates, const float* c, const float* tanh_c,
+                         const float* dY, float* gWih, float* gWhh, float* gb, float* dX,
+                         int64_t B, int64_t S, int64_t I, int64_t H);
+/* GRU (gru.cpp:56-315): gate blocks z,r,n of W_ih [I,3H], W_hh [H,3H],
+ * b [3H]; n = tanh(x W_in + (r*h) W_hn + b_n); h = (1-z) n + z h_prev.
+ * Caches: gates = z,r,n [B*S,3H], rh = r*h_prev [B*S,H]. */
+void cnref_gru_forward(const float* X, const float* Wih, const float* Whh, const float* b,
+                       float* Y, float* gates, float* rh, int64_t B, int64_t S, int64_t I,
+                       int64_t H);
+void cnref_gru_backward(const float* X, const float* Wih, const float* Whh, const float* Y,
+                        const float* gates, const float* rh, const float* dY, float* gWih,
+                        float* gWhh, float* gb, float* dX, int64_t B, int64_t S, int64_t I,
+                        int64_t H);
+
 /* Adam, one tensor, caller-computed bias corrections (adam.cpp:98-133) */
 void cnref_adam_step(float* W, const float* g, float* m, float* v, int64_t n, float lr,
                      float b1, float b2, float eps, float bc1, float bc2);

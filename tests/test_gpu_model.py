@@ -360,3 +360,70 @@ def test_cnn_multi_step_parity(gpu, oracle_mt):
         print(f"[model] config 3 param {k}: gpu-vs-oracle {rel:.3g}, oracle drift {drift:.3g}")
         assert rel <= max(1e-3, 2.0 * drift), f"param {k}: relative norm error {rel:.3g}"
     sess.close()
+
+
+@pytest.mark.parametrize("cell,batch,seq", [("lstm", None, None), ("gru", 32, 16)])
+def test_rnn_one_step_parity(gpu, oracle_mt, cell, batch, seq):
+    """Config 4 (LSTM 128->512, T=64, batch 128) at full size, and the GRU
+    variant of the same regressor.  The recurrent grads are sums over all B*S
+    rows of products of O(1) gate terms; their relative bound is taken against
+    max(|ref|, RMS of the tensor), which covers cancellation in the long sums."""
+    from oracle.rnn import OracleSeqRegressor
+    cfg = trainer.rnn_config(4, batch=batch, seq_len=seq, cell=cell)
+    print(f"[model] config 4 {cell} batch {cfg.batch} T={cfg.seq_len}: one step", flush=True)
+    params, X, Y = trainer.synthetic_rnn(cfg, np.random.default_rng(404))
+    sess = trainer.Session(cfg)
+    sess.set_params(params)
+    sess.set_batch(X, Y)
+    ref = OracleSeqRegressor(cfg, oracle_mt)
+    ref.set_params(params)
+    loss_gpu = sess.forward_backward()
+    grads = sess.get_grads()
+    sess.update()
+    after = sess.get_grads()
+    assert all(not g.any() for g in after[:3]), "recurrent grads must be cleared by step()"
+    loss_ref = ref.step(X, Y)
+    ok, msg = close([loss_gpu], [loss_ref], 1e-4, 1e-5)
+    assert ok, f"loss: {msg}"
+    for k, (a, b) in enumerate(zip(grads, ref.last_grads)):
+        rms = float(np.sqrt(np.mean(b.astype(np.float64) ** 2)))
+        ok, msg = close_mag(a, b, np.full(b.shape, rms, np.float32), 1e-4, 1e-5)
+        assert ok, f"grad of param {k}: {msg}"
+    for k, (a, b) in enumerate(zip(sess.get_params(), ref.get_params())):
+        ok, msg = close(a, b, 1e-4, 1e-5)
+        if not ok:  # Adam's first step is ~lr*sign(g): only ill-conditioned gradients may flip
+            g = ref.last_grads[k]
+            rms = float(np.sqrt(np.mean(g.astype(np.float64) ** 2)))
+            bad = np.abs(a.astype(np.float64) - b) > 1e-5 + 1e-4 * np.abs(b)
+            assert np.all(np.abs(g[bad]) <= 1e-5 + 1e-4 * rms), f"param {k}: {msg}"
+    print(f"[model] config 4 {cell}: loss {loss_gpu:.7f} vs {loss_ref:.7f}")
+    sess.close()
+
+
+def test_rnn_multi_step_parity(gpu, oracle_mt):
+    from oracle.rnn import OracleSeqRegressor
+    cfg = trainer.rnn_config(4, batch=16, seq_len=12)
+    steps = 20
+    print(f"[model] config 4 lstm batch {cfg.batch} T={cfg.seq_len}: {steps} steps", flush=True)
+    rng = np.random.default_rng(41)
+    params, _, _ = trainer.synthetic_rnn(cfg, rng)
+    sess = trainer.Session(cfg)
+    sess.set_params(params)
+    ref, ref_d = OracleSeqRegressor(cfg, oracle_mt), OracleSeqRegressor(cfg, oracle_mt)
+    ref.set_params(params)
+    ref_d.set_params(params)
+    for step in range(steps):
+        _, X, Y = trainer.synthetic_rnn(cfg, rng)
+        sess.set_batch(X, Y)
+        lg, lr_ = sess.step(), ref.step(X, Y)
+        oracle_mt.cnref_set_accumulate_double(1)
+        try:
+            ref_d.step(X, Y)
+        finally:
+            oracle_mt.cnref_set_accumulate_double(0)
+        assert abs(lg - lr_) <= 1e-3 * abs(lr_) + 1e-6, f"step {step}: loss {lg} vs {lr_}"
+    for k, (a, b, c) in enumerate(zip(sess.get_params(), ref.get_params(), ref_d.get_params())):
+        rel, drift = _rel(a, b), _rel(c, b)
+        print(f"[model] config 4 param {k}: gpu-vs-oracle {rel:.3g}, oracle drift {drift:.3g}")
+        assert rel <= max(1e-3, 2.0 * drift), f"param {k}: relative norm error {rel:.3g}"
+    sess.close()

@@ -1,0 +1,124 @@
+"""GPU parity of LSTM / GRU forward and BPTT against the CPU oracle.
+
+Outputs, caches and gradients within rel 1e-4 / abs 1e-5.  The weight and
+input gradients are contractions over B*S rows (the reference sums the same
+terms per timestep), so their relative part is taken against the RMS size
+of the partial sums (oracle_lib.close_mag, magnitudes from |operands|).
+"""
+import numpy as np
+import pytest
+import torch
+
+from cppnet_amd import ops
+from oracle_lib import close, close_mag, fp, gemm_mag
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def _inputs(rng, B, S, I, H, G):
+    X = rng.standard_normal(B * S * I).astype(np.float32)
+    lih, lhh = np.sqrt(6.0 / (I + H)), np.sqrt(6.0 / (2 * H))  # lstm.cpp:42-45 limits
+    Wih = rng.uniform(-lih, lih, I * G * H).astype(np.float32)
+    Whh = rng.uniform(-lhh, lhh, H * G * H).astype(np.float32)
+    b = (rng.standard_normal(G * H) * 0.1).astype(np.float32)
+    dY = (rng.standard_normal(B * S * H) * 1e-2).astype(np.float32)
+    return X, Wih, Whh, b, dY
+
+
+RNN_CASES = [(3, 5, 4, 8), (8, 7, 16, 32), (5, 1, 3, 6), (128, 64, 128, 512)]
+
+
+@pytest.mark.parametrize("B,S,I,H", RNN_CASES)
+def test_lstm_vs_oracle(gpu, oracle, B, S, I, H):
+    print(f"[lstm] B={B} S={S} I={I} H={H}", flush=True)
+    oracle.cnref_set_threads(16)
+    rng = np.random.default_rng(B + S + I + H)
+    X, Wih, Whh, b, dY = _inputs(rng, B, S, I, H, 4)
+    b[H:2 * H] += 1.0  # forget bias (lstm.cpp:47-49)
+    BS, G = B * S, 4 * H
+    Y, gates = torch.empty(BS * H, device="cuda"), torch.empty(BS * G, device="cuda")
+    c, tc = torch.empty(BS * H, device="cuda"), torch.empty(BS * H, device="cuda")
+    ops.lstm_forward(dev(X), dev(Wih), dev(Whh), dev(b), Y, gates, c, tc, B, S, I, H)
+    gWih, gWhh = torch.empty(I * G, device="cuda"), torch.empty(H * G, device="cuda")
+    gb, dX = torch.empty(G, device="cuda"), torch.empty(BS * I, device="cuda")
+    ops.lstm_backward(dev(X), dev(Wih), dev(Whh), Y, gates, c, tc, dev(dY), gWih, gWhh, gb, dX,
+                      B, S, I, H)
+    rY, rg = np.zeros(BS * H, np.float32), np.zeros(BS * G, np.float32)
+    rc, rtc = np.zeros(BS * H, np.float32), np.zeros(BS * H, np.float32)
+    oracle.cnref_lstm_forward(fp(X), fp(Wih), fp(Whh), fp(b), fp(rY), fp(rg), fp(rc), fp(rtc), B, S, I, H)
+    for got, want, name in [(host(Y), rY, "Y"), (host(gates), rg, "gates"), (host(c), rc, "c")]:
+        ok, msg = close(got, want, 1e-4, 2e-5)
+        assert ok, f"{name}: {msg}"
+    # backward on the oracle's own caches, so forward rounding does not leak in
+    rgWih, rgWhh = np.zeros(I * G, np.float32), np.zeros(H * G, np.float32)
+    rgb, rdX = np.zeros(G, np.float32), np.zeros(BS * I, np.float32)
+    oracle.cnref_lstm_backward(fp(X), fp(Wih), fp(Whh), fp(rY), fp(rg), fp(rc), fp(rtc), fp(dY),
+                               fp(rgWih), fp(rgWhh), fp(rgb), fp(rdX), B, S, I, H)
+    # magnitudes of the final contractions: dG is bounded by |dY| * O(S) here
+    dGabs = np.full(BS * G, np.abs(dY).mean() * 4, np.float32)
+    m_ih = gemm_mag(oracle, 1, 0, I, G, BS, X, BS, dGabs, BS, I)
+    m_hh = gemm_mag(oracle, 1, 0, H, G, BS, np.abs(rY), BS, dGabs, BS, H)
+    m_b = gemm_mag(oracle, 1, 0, 1, G, BS, np.ones(BS, np.float32), BS, dGabs, BS, 1)
+    m_dx = gemm_mag(oracle, 0, 1, BS, I, G, dGabs, BS, Wih, I, BS)
+    for got, want, mag, name in [(host(gWih), rgWih, m_ih, "grad_W_ih"),
+                                 (host(gWhh), rgWhh, m_hh, "grad_W_hh"),
+                                 (host(gb), rgb, m_b, "grad_b"), (host(dX), rdX, m_dx, "dX")]:
+        ok, msg = close_mag(got, want, mag, 1e-4, 1e-5)
+        assert ok, f"{name}: {msg}"
+
+
+@pytest.mark.parametrize("B,S,I,H", RNN_CASES[:3] + [(64, 32, 64, 256)])
+def test_gru_vs_oracle(gpu, oracle, B, S, I, H):
+    print(f"[gru] B={B} S={S} I={I} H={H}", flush=True)
+    oracle.cnref_set_threads(16)
+    rng = np.random.default_rng(B * 3 + S + I + H)
+    X, Wih, Whh, b, dY = _inputs(rng, B, S, I, H, 3)
+    BS, G = B * S, 3 * H
+    Y, gates, rh = (torch.empty(BS * H, device="cuda"), torch.empty(BS * G, device="cuda"),
+                    torch.empty(BS * H, device="cuda"))
+    ops.gru_forward(dev(X), dev(Wih), dev(Whh), dev(b), Y, gates, rh, B, S, I, H)
+    gWih, gWhh = torch.empty(I * G, device="cuda"), torch.empty(H * G, device="cuda")
+    gb, dX = torch.empty(G, device="cuda"), torch.empty(BS * I, device="cuda")
+    ops.gru_backward(dev(X), dev(Wih), dev(Whh), Y, gates, rh, dev(dY), gWih, gWhh, gb, dX, B, S, I, H)
+    rY, rg, rrh = np.zeros(BS * H, np.float32), np.zeros(BS * G, np.float32), np.zeros(BS * H, np.float32)
+    oracle.cnref_gru_forward(fp(X), fp(Wih), fp(Whh), fp(b), fp(rY), fp(rg), fp(rrh), B, S, I, H)
+    for got, want, name in [(host(Y), rY, "Y"), (host(gates), rg, "gates"), (host(rh), rrh, "rh")]:
+        ok, msg = close(got, want, 1e-4, 2e-5)
+        assert ok, f"{name}: {msg}"
+    rgWih, rgWhh = np.zeros(I * G, np.float32), np.zeros(H * G, np.float32)
+    rgb, rdX = np.zeros(G, np.float32), np.zeros(BS * I, np.float32)
+    oracle.cnref_gru_backward(fp(X), fp(Wih), fp(Whh), fp(rY), fp(rg), fp(rrh), fp(dY), fp(rgWih),
+                              fp(rgWhh), fp(rgb), fp(rdX), B, S, I, H)
+    dGabs = np.full(BS * G, np.abs(dY).mean() * 4, np.float32)
+    m_ih = gemm_mag(oracle, 1, 0, I, G, BS, X, BS, dGabs, BS, I)
+    m_hh = gemm_mag(oracle, 1, 0, H, G, BS, np.abs(rY) + 1e-3, BS, dGabs, BS, H)
+    m_b = gemm_mag(oracle, 1, 0, 1, G, BS, np.ones(BS, np.float32), BS, dGabs, BS, 1)
+    m_dx = gemm_mag(oracle, 0, 1, BS, I, G, dGabs, BS, Wih, I, BS)
+    for got, want, mag, name in [(host(gWih), rgWih, m_ih, "grad_W_ih"),
+                                 (host(gWhh), rgWhh, m_hh, "grad_W_hh"),
+                                 (host(gb), rgb, m_b, "grad_b"), (host(dX), rdX, m_dx, "dX")]:
+        ok, msg = close_mag(got, want, mag, 1e-4, 1e-5)
+        assert ok, f"{name}: {msg}"
+
+
+def test_seq_select_scatter(gpu):
+    B, S, D = 5, 4, 3
+    Y = torch.arange(B * S * D, dtype=torch.float32, device="cuda")
+    out = torch.empty(B * D, device="cuda")
+    ops.seq_select(Y, out, B, S, D, S - 1)
+    y = Y.cpu().numpy().reshape(D, S, B).transpose(2, 1, 0)
+    np.testing.assert_array_equal(host(out).reshape(D, B).T, y[:, S - 1, :])
+    back = torch.full((B * S * D,), 7.0, device="cuda")
+    ops.seq_scatter(out, back, B, S, D, S - 1)
+    b = host(back).reshape(D, S, B).transpose(2, 1, 0)
+    assert not b[:, :S - 1, :].any()
+    np.testing.assert_array_equal(b[:, S - 1, :], y[:, S - 1, :])
