@@ -44,6 +44,16 @@ _SIGS = {
     "cnref_lstm_backward": (None, [_f] * 12 + [i64] * 4),
     "cnref_gru_forward": (None, [_f] * 7 + [i64] * 4),
     "cnref_gru_backward": (None, [_f] * 11 + [i64] * 4),
+    "cnref_embedding_forward": (i32, [_i, _f, _f, i64, i64, i64, i64]),
+    "cnref_embedding_backward": (None, [_i, _f, _f, i64, i64, i64, i64]),
+    "cnref_mha_forward": (None, [_f] * 9 + [i64] * 4),
+    "cnref_mha_backward": (None, [_f] * 14 + [i64] * 4),
+    "cnref_batchnorm_forward": (None, [_f] * 9 + [i64, i64, f32, f32]),
+    "cnref_batchnorm_backward": (None, [_f] * 9 + [i64, i64, f32]),
+    "cnref_gelu_forward": (None, [_f, _f, i64]),
+    "cnref_gelu_backward": (None, [_f, _f, _f, i64]),
+    "cnref_meanpool1d_forward": (None, [_f, _f, i64, i64, i64]),
+    "cnref_meanpool1d_backward": (None, [_f, _f, i64, i64, i64]),
     "cnref_adam_step": (None, [_f, _f, _f, _f, i64, f32, f32, f32, f32, f32, f32]),
     "cnref_bias_correction": (f32, [f32, i32]),
 }

@@ -531,6 +531,210 @@ void cnref_gru_backward(const float* X, const float* Wih, const float* Whh, cons
   }
 }
 
+// ---------------------------------------------------------------- Embedding
+// Embedding::forward cpu-eigen (embedding.cpp:79-95)
+int cnref_embedding_forward(const int32_t* ids, const float* W, float* out, int64_t B, int64_t S,
+                            int64_t V, int64_t D) {
+  for (int64_t n = 0; n < B; ++n)
+    for (int64_t s = 0; s < S; ++s) {
+      const int32_t id = ids[n + B * s];
+      if (id < 0 || id >= V) return -1;
+      for (int64_t d = 0; d < D; ++d) out[n + B * s + B * S * d] = W[id + V * d];
+    }
+  return 0;
+}
+// Embedding::backward cpu-eigen (embedding.cpp:108, 163-175)
+void cnref_embedding_backward(const int32_t* ids, const float* dY, float* gW, int64_t B, int64_t S,
+                              int64_t V, int64_t D) {
+  for (int64_t i = 0; i < V * D; ++i) gW[i] = 0.0f;
+  for (int64_t n = 0; n < B; ++n)
+    for (int64_t s = 0; s < S; ++s) {
+      const int32_t id = ids[n + B * s];
+      for (int64_t d = 0; d < D; ++d) gW[id + V * d] += dY[n + B * s + B * S * d];
+    }
+}
+
+// ---------------------------------------------------------------- MHA
+// sample n of a [B,S,D] tensor as a dense [S,D] ColMajor matrix
+static std::vector<float> sample_sd(const float* x, int64_t B, int64_t S, int64_t D, int64_t n) {
+  std::vector<float> m((size_t)(S * D));
+  for (int64_t d = 0; d < D; ++d)
+    for (int64_t s = 0; s < S; ++s) m[s + S * d] = x[n + B * s + B * S * d];
+  return m;
+}
+
+// MultiHeadAttention::forward cpu-eigen branch (attention.cpp:165-218)
+void cnref_mha_forward(const float* q, const float* k, const float* v, const float* Wq,
+                       const float* Wk, const float* Wv, const float* Wo, float* out, float* attn,
+                       int64_t B, int64_t S, int64_t D, int64_t heads) {
+  const float scale = 1.0f / std::sqrt(static_cast<float>(D / heads));
+  std::vector<float> Qp((size_t)(S * D)), Kp((size_t)(S * D)), Vp((size_t)(S * D));
+  std::vector<float> sc((size_t)(S * S)), A((size_t)(S * S)), ctx((size_t)(S * D)), o((size_t)(S * D));
+  for (int64_t n = 0; n < B; ++n) {
+    auto Q = sample_sd(q, B, S, D, n), K = sample_sd(k, B, S, D, n), V = sample_sd(v, B, S, D, n);
+    cnref_gemm_f32(0, 0, S, D, D, 1.f, Q.data(), S, Wq, D, 0.f, Qp.data(), S, nullptr, 0);
+    cnref_gemm_f32(0, 0, S, D, D, 1.f, K.data(), S, Wk, D, 0.f, Kp.data(), S, nullptr, 0);
+    cnref_gemm_f32(0, 0, S, D, D, 1.f, V.data(), S, Wv, D, 0.f, Vp.data(), S, nullptr, 0);
+    // scores = Qp Kp^T, then * scale (189)
+    cnref_gemm_f32(0, 1, S, S, D, 1.f, Qp.data(), S, Kp.data(), S, 0.f, sc.data(), S, nullptr, 0);
+    for (auto& x : sc) x = x * scale;
+    for (int64_t i = 0; i < S; ++i) {  // row softmax (191-205)
+      float mx = sc[i];
+      for (int64_t j = 1; j < S; ++j) mx = std::max(mx, sc[i + S * j]);
+      float sum = 0.0f;
+      for (int64_t j = 0; j < S; ++j) {
+        A[i + S * j] = std::exp(sc[i + S * j] - mx);
+        sum += A[i + S * j];
+      }
+      for (int64_t j = 0; j < S; ++j) A[i + S * j] /= sum;
+    }
+    for (int64_t j = 0; j < S; ++j)
+      for (int64_t i = 0; i < S; ++i) attn[n + B * i + B * S * j] = A[i + S * j];
+    cnref_gemm_f32(0, 0, S, D, S, 1.f, A.data(), S, Vp.data(), S, 0.f, ctx.data(), S, nullptr, 0);
+    cnref_gemm_f32(0, 0, S, D, D, 1.f, ctx.data(), S, Wo, D, 0.f, o.data(), S, nullptr, 0);
+    for (int64_t d = 0; d < D; ++d)
+      for (int64_t s = 0; s < S; ++s) out[n + B * s + B * S * d] = o[s + S * d];
+  }
+}
+
+// MultiHeadAttention::backward cpu-eigen branch (attention.cpp:503-569)
+void cnref_mha_backward(const float* q, const float* k, const float* v, const float* Wq,
+                        const float* Wk, const float* Wv, const float* Wo, const float* attn,
+                        const float* dY, float* gWq, float* gWk, float* gWv, float* gWo,
+                        float* dX, int64_t B, int64_t S, int64_t D, int64_t heads) {
+  const float scale = 1.0f / std::sqrt(static_cast<float>(D / heads));
+  for (int64_t i = 0; i < D * D; ++i) gWq[i] = gWk[i] = gWv[i] = gWo[i] = 0.0f;
+  const size_t SD = (size_t)(S * D), SS = (size_t)(S * S), DD = (size_t)(D * D);
+  std::vector<float> Qp(SD), Kp(SD), Vp(SD), ctx(SD), gctx(SD), gA(SS), gVp(SD), gS(SS), gQp(SD),
+      gKp(SD), gQ(SD), gK(SD), gV(SD), A(SS), tmp(DD);
+  for (int64_t n = 0; n < B; ++n) {
+    auto G = sample_sd(dY, B, S, D, n);
+    auto Q = sample_sd(q, B, S, D, n), K = sample_sd(k, B, S, D, n), V = sample_sd(v, B, S, D, n);
+    for (int64_t j = 0; j < S; ++j)
+      for (int64_t i = 0; i < S; ++i) A[i + S * j] = attn[n + B * i + B * S * j];
+    cnref_gemm_f32(0, 0, S, D, D, 1.f, Q.data(), S, Wq, D, 0.f, Qp.data(), S, nullptr, 0);
+    cnref_gemm_f32(0, 0, S, D, D, 1.f, K.data(), S, Wk, D, 0.f, Kp.data(), S, nullptr, 0);
+    cnref_gemm_f32(0, 0, S, D, D, 1.f, V.data(), S, Wv, D, 0.f, Vp.data(), S, nullptr, 0);
+    cnref_gemm_f32(0, 0, S, D, S, 1.f, A.data(), S, Vp.data(), S, 0.f, ctx.data(), S, nullptr, 0);
+    cnref_gemm_f32(0, 1, S, D, D, 1.f, G.data(), S, Wo, D, 0.f, gctx.data(), S, nullptr, 0);
+    cnref_gemm_f32(1, 0, D, D, S, 1.f, ctx.data(), S, G.data(), S, 0.f, tmp.data(), D, nullptr, 0);
+    for (size_t i = 0; i < DD; ++i) gWo[i] += tmp[i];
+    cnref_gemm_f32(0, 1, S, S, D, 1.f, gctx.data(), S, Vp.data(), S, 0.f, gA.data(), S, nullptr, 0);
+    cnref_gemm_f32(1, 0, S, D, S, 1.f, A.data(), S, gctx.data(), S, 0.f, gVp.data(), S, nullptr, 0);
+    for (int64_t i = 0; i < S; ++i) {  // softmax Jacobian rows (541-549)
+      float dot = 0.0f;
+      for (int64_t j = 0; j < S; ++j) dot += gA[i + S * j] * A[i + S * j];
+      for (int64_t j = 0; j < S; ++j) gS[i + S * j] = A[i + S * j] * (gA[i + S * j] - dot);
+    }
+    for (auto& x : gS) x = x * scale;
+    cnref_gemm_f32(0, 0, S, D, S, 1.f, gS.data(), S, Kp.data(), S, 0.f, gQp.data(), S, nullptr, 0);
+    cnref_gemm_f32(1, 0, S, D, S, 1.f, gS.data(), S, Qp.data(), S, 0.f, gKp.data(), S, nullptr, 0);
+    cnref_gemm_f32(0, 1, S, D, D, 1.f, gQp.data(), S, Wq, D, 0.f, gQ.data(), S, nullptr, 0);
+    cnref_gemm_f32(1, 0, D, D, S, 1.f, Q.data(), S, gQp.data(), S, 0.f, tmp.data(), D, nullptr, 0);
+    for (size_t i = 0; i < DD; ++i) gWq[i] += tmp[i];
+    cnref_gemm_f32(0, 1, S, D, D, 1.f, gKp.data(), S, Wk, D, 0.f, gK.data(), S, nullptr, 0);
+    cnref_gemm_f32(1, 0, D, D, S, 1.f, K.data(), S, gKp.data(), S, 0.f, tmp.data(), D, nullptr, 0);
+    for (size_t i = 0; i < DD; ++i) gWk[i] += tmp[i];
+    cnref_gemm_f32(0, 1, S, D, D, 1.f, gVp.data(), S, Wv, D, 0.f, gV.data(), S, nullptr, 0);
+    cnref_gemm_f32(1, 0, D, D, S, 1.f, V.data(), S, gVp.data(), S, 0.f, tmp.data(), D, nullptr, 0);
+    for (size_t i = 0; i < DD; ++i) gWv[i] += tmp[i];
+    for (int64_t d = 0; d < D; ++d)
+      for (int64_t s2 = 0; s2 < S; ++s2)
+        dX[n + B * s2 + B * S * d] = gQ[s2 + S * d] + gK[s2 + S * d] + gV[s2 + S * d];
+  }
+}
+
+// ---------------------------------------------------------------- BatchNorm
+// BatchNorm::forward cpu-eigen, training (batch_norm.cpp:282-318)
+void cnref_batchnorm_forward(const float* x, float* y, float* xhat, const float* gamma,
+                             const float* beta, float* running_mean, float* running_var,
+                             float* batch_mean, float* batch_var, int64_t N, int64_t F,
+                             float momentum, float eps) {
+  const float inv_batch = 1.0f / static_cast<float>(N);
+  for (int64_t f = 0; f < F; ++f) {
+    float m = 0.0f;
+    for (int64_t n = 0; n < N; ++n) m += x[n + N * f];
+    m *= inv_batch;
+    float var = 0.0f;
+    for (int64_t n = 0; n < N; ++n) {
+      const float diff = x[n + N * f] - m;
+      var += diff * diff;
+    }
+    var *= inv_batch;
+    batch_mean[f] = m;
+    batch_var[f] = var;
+    for (int64_t n = 0; n < N; ++n) {
+      xhat[n + N * f] = (x[n + N * f] - m) / std::sqrt(var + eps);
+      y[n + N * f] = gamma[f] * xhat[n + N * f] + beta[f];
+    }
+    running_mean[f] = (1.0f - momentum) * running_mean[f] + momentum * m;
+    running_var[f] = (1.0f - momentum) * running_var[f] + momentum * var;
+  }
+}
+// BatchNorm::backward (batch_norm.cpp:333-388)
+void cnref_batchnorm_backward(const float* dY, const float* x, const float* xhat,
+                              const float* gamma, const float* batch_mean, const float* batch_var,
+                              float* ggamma, float* gbeta, float* dX, int64_t N, int64_t F,
+                              float eps) {
+  const float inv_batch = 1.0f / static_cast<float>(N);
+  for (int64_t f = 0; f < F; ++f) {
+    float gg = 0.0f, gbt = 0.0f;
+    for (int64_t n = 0; n < N; ++n) {
+      gg += dY[n + N * f] * xhat[n + N * f];
+      gbt += dY[n + N * f];
+    }
+    ggamma[f] = gg;
+    gbeta[f] = gbt;
+    const float inv_std = 1.0f / std::sqrt(batch_var[f] + eps);
+    float dvar = 0.0f, dmean = 0.0f;
+    for (int64_t n = 0; n < N; ++n) {
+      const float dxh = dY[n + N * f] * gamma[f];
+      const float xmu = x[n + N * f] - batch_mean[f];
+      dvar += dxh * xmu * (-0.5f) * inv_std * inv_std * inv_std;
+      dmean += dxh * (-inv_std);
+    }
+    for (int64_t n = 0; n < N; ++n) {
+      const float dxh = dY[n + N * f] * gamma[f];
+      const float xmu = x[n + N * f] - batch_mean[f];
+      dX[n + N * f] = dxh * inv_std + dvar * 2.0f * xmu * inv_batch + dmean * inv_batch;
+    }
+  }
+}
+
+// ---------------------------------------------------------------- GELU
+void cnref_gelu_forward(const float* x, float* y, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) {
+    const double v = x[i];
+    y[i] = (float)(0.5 * v * (1.0 + std::erf(v * 0.70710678118654752440)));
+  }
+}
+void cnref_gelu_backward(const float* x, const float* dy, float* dx, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) {
+    const double v = x[i];
+    const double cdf = 0.5 * (1.0 + std::erf(v * 0.70710678118654752440));
+    const double pdf = 0.39894228040143267794 * std::exp(-0.5 * v * v);
+    dx[i] = (float)((double)dy[i] * (cdf + v * pdf));
+  }
+}
+
+// ---------------------------------------------------------------- MeanPool1D
+// mean over the sequence (mean_pool1d.cpp:37-42: Eigen mean = sum / S)
+void cnref_meanpool1d_forward(const float* x, float* y, int64_t B, int64_t S, int64_t D) {
+  for (int64_t d = 0; d < D; ++d)
+    for (int64_t b = 0; b < B; ++b) {
+      float sum = 0.0f;
+      for (int64_t s = 0; s < S; ++s) sum += x[b + B * s + B * S * d];
+      y[b + B * d] = sum / static_cast<float>(S);
+    }
+}
+// mean_pool1d.cpp:97-104: grad_input = grad_output * (1/S)
+void cnref_meanpool1d_backward(const float* dy, float* dx, int64_t B, int64_t S, int64_t D) {
+  const float inv_S = 1.0f / static_cast<float>(S);
+  for (int64_t d = 0; d < D; ++d)
+    for (int64_t s = 0; s < S; ++s)
+      for (int64_t b = 0; b < B; ++b) dx[b + B * s + B * S * d] = dy[b + B * d] * inv_S;
+}
+
 // Adam::update (adam.cpp:98-133), per element in order.
 void cnref_adam_step(float* W, const float* g, float* m, float* v, int64_t n, float lr, float b1,
                      float b2, float eps, float bc1, float bc2) {

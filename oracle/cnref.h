@@ -99,6 +99,43 @@ void cnref_gru_backward(const float* X, const float* Wih, const float* Whh, cons
                         float* gWhh, float* gb, float* dX, int64_t B, int64_t S, int64_t I,
                         int64_t H);
 
+/* Embedding (embedding.cpp:33-185): W [V,D] ColMajor, ids [B,S] int32,
+ * out [B,S,D].  forward returns -1 (and writes nothing more) on an id out of
+ * [0,V) (the cpu-eigen throw, 87-90); backward zeroes gW then adds. */
+int  cnref_embedding_forward(const int32_t* ids, const float* W, float* out, int64_t B,
+                             int64_t S, int64_t V, int64_t D);
+void cnref_embedding_backward(const int32_t* ids, const float* dY, float* gW, int64_t B,
+                              int64_t S, int64_t V, int64_t D);
+/* MultiHeadAttention (attention.cpp:60-221 forward, 223-569 backward; the
+ * cpu-eigen branches): per sample, Qp = Q Wq, Kp = K Wk, Vp = V Wv over the
+ * full width D, A = softmax_rows(Qp Kp^T * 1/sqrt(D/heads)), out = (A Vp) Wo.
+ * attn [B,S,S] ColMajor (n,i,j).  Grads overwrite; dX = dQ + dK + dV. */
+void cnref_mha_forward(const float* q, const float* k, const float* v, const float* Wq,
+                       const float* Wk, const float* Wv, const float* Wo, float* out,
+                       float* attn, int64_t B, int64_t S, int64_t D, int64_t heads);
+void cnref_mha_backward(const float* q, const float* k, const float* v, const float* Wq,
+                        const float* Wk, const float* Wv, const float* Wo, const float* attn,
+                        const float* dY, float* gWq, float* gWk, float* gWv, float* gWo,
+                        float* dX, int64_t B, int64_t S, int64_t D, int64_t heads);
+/* BatchNorm over x [N,F] (batch_norm.cpp:204-401), training mode: biased
+ * batch variance, running stats (1-m) r + m batch. */
+void cnref_batchnorm_forward(const float* x, float* y, float* xhat, const float* gamma,
+                             const float* beta, float* running_mean, float* running_var,
+                             float* batch_mean, float* batch_var, int64_t N, int64_t F,
+                             float momentum, float eps);
+void cnref_batchnorm_backward(const float* dY, const float* x, const float* xhat,
+                              const float* gamma, const float* batch_mean,
+                              const float* batch_var, float* ggamma, float* gbeta, float* dX,
+                              int64_t N, int64_t F, float eps);
+/* GELU, exact form x * Phi(x) = 0.5 x (1 + erf(x / sqrt 2)) (no reference:
+ * the reference has no GELU); dX = dY (Phi(x) + x phi(x)). */
+void cnref_gelu_forward(const float* x, float* y, int64_t n);
+void cnref_gelu_backward(const float* x, const float* dy, float* dx, int64_t n);
+/* MeanPool1D (mean_pool1d.cpp:24-150): [B,S,D] -> [B,D] mean over S;
+ * backward dX = dY * (1/S). */
+void cnref_meanpool1d_forward(const float* x, float* y, int64_t B, int64_t S, int64_t D);
+void cnref_meanpool1d_backward(const float* dy, float* dx, int64_t B, int64_t S, int64_t D);
+
 /* Adam, one tensor, caller-computed bias corrections (adam.cpp:98-133) */
 void cnref_adam_step(float* W, const float* g, float* m, float* v, int64_t n, float lr,
                      float b1, float b2, float eps, float bc1, float bc2);
