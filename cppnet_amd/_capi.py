@@ -57,6 +57,19 @@ SIGNATURES: dict[str, tuple] = {
     "cnhip_gru_backward": (i32, [vp] * 11 + [i64] * 4 + [vp]),
     "cnhip_seq_select": (i32, [vp, vp, i64, i64, i64, i64, vp]),
     "cnhip_seq_scatter": (i32, [vp, vp, i64, i64, i64, i64, vp]),
+    "cnhip_transpose": (i32, [vp, vp, i64, i64, vp]),
+    "cnhip_mha_cache_floats": (i64, [i64, i64, i64]),
+    "cnhip_mha_forward": (i32, [vp] * 9 + [i64] * 4 + [vp]),
+    "cnhip_mha_backward": (i32, [vp] * 14 + [i64] * 4 + [vp]),
+    "cnhip_embedding_forward": (i32, [vp, vp, vp, i64, i64, i64, i64, vp, vp]),
+    "cnhip_embedding_backward": (i32, [vp, vp, vp, i64, i64, i64, i64, vp]),
+    "cnhip_batchnorm_forward": (i32, [vp] * 9 + [i64, i64, f32, f32, vp]),
+    "cnhip_batchnorm_backward": (i32, [vp] * 9 + [i64, i64, f32, vp]),
+    "cnhip_gelu_forward": (i32, [vp, vp, i64, vp]),
+    "cnhip_gelu_backward": (i32, [vp, vp, vp, i64, vp]),
+    "cnhip_meanpool1d_forward": (i32, [vp, vp, i64, i64, i64, vp]),
+    "cnhip_meanpool1d_backward": (i32, [vp, vp, i64, i64, i64, vp]),
+    "cnhip_add": (i32, [vp, vp, vp, i64, vp]),
     "cnhip_relu_forward": (i32, [vp, vp, i64, vp]),
     "cnhip_relu_backward": (i32, [vp, vp, vp, i64, vp]),
     "cnhip_sigmoid_forward": (i32, [vp, vp, i64, vp]),

@@ -1,0 +1,685 @@
+// Kernels and entry points of the transformer rows: MultiHeadAttention,
+// Embedding, BatchNorm, GELU, MeanPool1D and the residual add.
+//
+// ref: attention.cpp:60-587 (MHA cpu-eigen semantics), attention_scores.cu
+// (reference softmax kernels, which index row-major into ColMajor data),
+// embedding.cpp:33-185 / embedding_*.cu, batch_norm.cpp:204-401 /
+// batch_norm_*.cu, mean_pool1d.cpp:24-150 / mean_pool1d.cu, residual.cpp /
+// elementwise.cu (op 0 = add).  GELU has no reference implementation.
+//
+// Attention layout.  Activations are ColMajor [B, S, D], i.e. [B*S, D]
+// matrices with row b + B*s: the projections and every weight gradient are
+// single GEMMs over all B*S rows.  The per-sample products (scores, context
+// and their gradients) need each sample's [S, D] block contiguous, so the
+// projected Q, K, V are transposed once into a per-sample layout
+// (s + S*d + S*D*b) by a tiled LDS transpose, and the batched MFMA GEMM runs
+// over the B samples.  Attention weights are kept as A^T per sample (row i of
+// A is contiguous), so the row softmax and its Jacobian are wave64 reductions
+// over contiguous memory.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+
+#include "common.hpp"
+
+namespace cnhip {
+
+int gemm_f32(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float alpha,
+             const float* A, int64_t lda, const float* B, int64_t ldb, float beta, float* C,
+             int64_t ldc, const float* bias, int epilogue, hipStream_t st, const char* who);
+int gemm_f32_batched(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float alpha,
+                     const float* A, int64_t lda, int64_t stride_a, const float* B, int64_t ldb,
+                     int64_t stride_b, float beta, float* C, int64_t ldc, int64_t stride_c,
+                     int64_t batches, const float* bias, int epilogue, hipStream_t st,
+                     const char* who);
+
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------- transpose
+// ColMajor in [R, C] -> out [C, R]: out[c + C*r] = in[r + R*c], 64x64 tiles
+// through LDS (+1 pad against bank conflicts); both sides coalesced.
+constexpr int TT = 64;
+__global__ void __launch_bounds__(256) transpose_kernel(const float* __restrict__ in,
+                                                        float* __restrict__ out, int64_t R,
+                                                        int64_t C) {
+  __shared__ float tile[TT][TT + 1];
+  const int64_t r0 = (int64_t)blockIdx.x * TT, c0 = (int64_t)blockIdx.y * TT;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;  // 64 x 4
+  for (int j = ty; j < TT; j += 4) {
+    const int64_t r = r0 + tx, c = c0 + j;
+    if (r < R && c < C) tile[j][tx] = in[r + R * c];
+  }
+  __syncthreads();
+  for (int j = ty; j < TT; j += 4) {
+    const int64_t c = c0 + tx, r = r0 + j;
+    if (r < R && c < C) out[c + C * r] = tile[tx][j];
+  }
+}
+
+int transpose(const float* in, float* out, int64_t R, int64_t C, hipStream_t st, const char* who) {
+  CNHIP_REQUIRE((R + TT - 1) / TT < (1ll << 31) && (C + TT - 1) / TT <= 65535,
+                "%s: transpose %lld x %lld too large", who, (long long)R, (long long)C);
+  hipLaunchKernelGGL(transpose_kernel, dim3((unsigned)((R + TT - 1) / TT), (unsigned)((C + TT - 1) / TT)),
+                     dim3(256), 0, st, in, out, R, C);
+  return check_launch(who);
+}
+
+// ---------------------------------------------------------------- row softmax
+// x / y: rows of length L contiguous (row r at r*L); one wave64 per row.
+// attention.cpp:191-205: max, exp(x - max), sum, divide.
+__global__ void __launch_bounds__(256) softmax_rows_kernel(const float* __restrict__ x,
+                                                           float* __restrict__ y, int64_t rows,
+                                                           int64_t L) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const float* xr = x + r * L;
+  float* yr = y + r * L;
+  float mx = -INFINITY;
+  for (int64_t j = lane; j < L; j += 64) mx = fmaxf(mx, xr[j]);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  float sum = 0.f;
+  for (int64_t j = lane; j < L; j += 64) {
+    const float e = expf(xr[j] - mx);
+    yr[j] = e;
+    sum += e;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+  for (int64_t j = lane; j < L; j += 64) yr[j] = yr[j] / sum;
+}
+
+// attention.cpp:541-551: g = (A * (dA - sum_j dA A)) * scale
+__global__ void __launch_bounds__(256) softmax_rows_bwd_kernel(const float* __restrict__ A,
+                                                               const float* __restrict__ dA,
+                                                               float* __restrict__ g, int64_t rows,
+                                                               int64_t L, float scale) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const float* ar = A + r * L;
+  const float* dr = dA + r * L;
+  float dot = 0.f;
+  for (int64_t j = lane; j < L; j += 64) dot += dr[j] * ar[j];
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) dot += __shfl_xor(dot, off, 64);
+  for (int64_t j = lane; j < L; j += 64) g[r * L + j] = (ar[j] * (dr[j] - dot)) * scale;
+}
+
+int softmax_rows(const float* x, float* y, int64_t rows, int64_t L, hipStream_t st, const char* who) {
+  hipLaunchKernelGGL(softmax_rows_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, x, y,
+                     rows, L);
+  return check_launch(who);
+}
+
+// ---------------------------------------------------------------- embedding
+// Weights are kept token-major, Wt[d + D*v] (the reference's ColMajor [V, D]
+// transposed), so one token's row is contiguous.  out[p + BS*d] with
+// p = b + B*s: a 64-token x 64-feature tile is read along d and written along
+// p through LDS.  Out-of-range ids produce zeros and are counted.
+__global__ void __launch_bounds__(256) embedding_fwd_kernel(const int32_t* __restrict__ ids,
+                                                            const float* __restrict__ Wt,
+                                                            float* __restrict__ out, int64_t BS,
+                                                            int64_t V, int64_t D,
+                                                            int32_t* __restrict__ oob) {
+  __shared__ float tile[TT][TT + 1];
+  __shared__ int32_t tok[TT];
+  const int64_t p0 = (int64_t)blockIdx.x * TT, d0 = (int64_t)blockIdx.y * TT;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  if (threadIdx.x < TT) {
+    const int64_t p = p0 + threadIdx.x;
+    int32_t id = p < BS ? ids[p] : 0;
+    if (p < BS && (id < 0 || id >= V)) {
+      if (oob && blockIdx.y == 0) atomicAdd(oob, 1);
+      id = -1;
+    }
+    tok[threadIdx.x] = id;
+  }
+  __syncthreads();
+  for (int j = ty; j < TT; j += 4) {  // token j, feature tx: contiguous along d
+    const int64_t d = d0 + tx;
+    const int32_t id = tok[j];
+    tile[j][tx] = (d < D && id >= 0) ? Wt[d + D * (int64_t)id] : 0.f;
+  }
+  __syncthreads();
+  for (int j = ty; j < TT; j += 4) {  // feature j, token tx: contiguous along p
+    const int64_t p = p0 + tx, d = d0 + j;
+    if (p < BS && d < D) out[p + BS * d] = tile[tx][j];
+  }
+}
+
+// Deterministic scatter-add: bucket the positions by token id (counting sort,
+// keys ascending inside a bucket), then every token row sums its bucket's
+// gradient rows in key order.
+__global__ void __launch_bounds__(256) emb_count_kernel(const int32_t* __restrict__ ids,
+                                                        int32_t* __restrict__ counts, int64_t BS,
+                                                        int64_t V) {
+  for (int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; p < BS;
+       p += (int64_t)gridDim.x * blockDim.x) {
+    const int32_t id = ids[p];
+    if (id >= 0 && id < V) atomicAdd(&counts[id], 1);
+  }
+}
+
+// exclusive scan of counts[V] into offsets[V+1] (one block, fixed order)
+__global__ void __launch_bounds__(1024) emb_scan_kernel(const int32_t* __restrict__ counts,
+                                                        int32_t* __restrict__ offsets, int64_t V) {
+  __shared__ int32_t part[1024];
+  const int64_t per = (V + 1023) / 1024;
+  const int64_t lo = threadIdx.x * per, hi = min(V, lo + per);
+  int32_t s = 0;
+  for (int64_t v = lo; v < hi; ++v) s += counts[v];
+  part[threadIdx.x] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int32_t run = 0;
+    for (int i = 0; i < 1024; ++i) {
+      const int32_t c = part[i];
+      part[i] = run;
+      run += c;
+    }
+    offsets[V] = run;
+  }
+  __syncthreads();
+  int32_t run = part[threadIdx.x];
+  for (int64_t v = lo; v < hi; ++v) {
+    offsets[v] = run;
+    run += counts[v];
+  }
+}
+
+// Bucket entries are keys b*S + s (sample-major), the order in which the
+// reference's cpu-eigen loop (embedding.cpp:161-168: n outer, s inner) adds the
+// gradient rows; position p = b + B*s of the ColMajor [B, S] ids.
+__global__ void __launch_bounds__(256) emb_fill_kernel(const int32_t* __restrict__ ids,
+                                                       const int32_t* __restrict__ offsets,
+                                                       int32_t* __restrict__ cursor,
+                                                       int32_t* __restrict__ keys, int64_t B,
+                                                       int64_t S, int64_t V) {
+  const int64_t BS = B * S;
+  for (int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; p < BS;
+       p += (int64_t)gridDim.x * blockDim.x) {
+    const int32_t id = ids[p];
+    if (id >= 0 && id < V)
+      keys[offsets[id] + atomicAdd(&cursor[id], 1)] = (int32_t)((p % B) * S + p / B);
+  }
+}
+
+// Sort each bucket ascending (buckets are tiny: BS/V entries on average).
+__global__ void __launch_bounds__(256) emb_sort_kernel(const int32_t* __restrict__ offsets,
+                                                       int32_t* __restrict__ pos, int64_t V) {
+  for (int64_t v = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; v < V;
+       v += (int64_t)gridDim.x * blockDim.x) {
+    const int32_t lo = offsets[v], hi = offsets[v + 1];
+    for (int32_t i = lo + 1; i < hi; ++i) {
+      const int32_t key = pos[i];
+      int32_t j = i - 1;
+      while (j >= lo && pos[j] > key) {
+        pos[j + 1] = pos[j];
+        --j;
+      }
+      pos[j + 1] = key;
+    }
+  }
+}
+
+// gWt[d + D*v] = sum over the bucket, in key order, of dYt[d + D*p]
+// (dYt = dY transposed, one position's gradient row contiguous); empty
+// buckets write zeros.
+__global__ void __launch_bounds__(128) emb_sum_kernel(const int32_t* __restrict__ offsets,
+                                                      const int32_t* __restrict__ keys,
+                                                      const float* __restrict__ dYt,
+                                                      float* __restrict__ gWt, int64_t B,
+                                                      int64_t S, int64_t D) {
+  const int64_t v = blockIdx.x;
+  const int32_t lo = offsets[v], hi = offsets[v + 1];
+  for (int64_t d = threadIdx.x; d < D; d += blockDim.x) {
+    float s = 0.f;
+    for (int32_t i = lo; i < hi; ++i) {
+      const int64_t key = keys[i];
+      s += dYt[d + D * (key / S + B * (key % S))];
+    }
+    gWt[d + D * v] = s;
+  }
+}
+
+// ---------------------------------------------------------------- BatchNorm
+// One block per feature; x column f is contiguous ([N, F] ColMajor).  Sums
+// are block reductions in a fixed order.
+constexpr int BNT = 256;
+
+__device__ float bn_block_sum(float v, float* sm) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  __syncthreads();
+  if (lane == 0) sm[w] = v;
+  __syncthreads();
+  float r = 0.f;
+#pragma unroll
+  for (int i = 0; i < BNT / 64; ++i) r += sm[i];
+  return r;  // every thread
+}
+
+// batch_norm.cpp:282-318 (training)
+__global__ void __launch_bounds__(BNT) bn_fwd_kernel(const float* __restrict__ x,
+                                                     float* __restrict__ y,
+                                                     float* __restrict__ xhat,
+                                                     const float* __restrict__ gamma,
+                                                     const float* __restrict__ beta,
+                                                     float* __restrict__ rmean,
+                                                     float* __restrict__ rvar,
+                                                     float* __restrict__ bmean,
+                                                     float* __restrict__ bvar, int64_t N,
+                                                     float momentum, float eps) {
+  __shared__ float sm[BNT / 64];
+  const int64_t f = blockIdx.x;
+  const float* xc = x + N * f;
+  const float inv_batch = 1.0f / (float)N;
+  float s = 0.f;
+  for (int64_t n = threadIdx.x; n < N; n += BNT) s += xc[n];
+  const float mean = bn_block_sum(s, sm) * inv_batch;
+  float s2 = 0.f;
+  for (int64_t n = threadIdx.x; n < N; n += BNT) {
+    const float diff = xc[n] - mean;
+    s2 += diff * diff;
+  }
+  const float var = bn_block_sum(s2, sm) * inv_batch;
+  const float den = sqrtf(var + eps);
+  const float g = gamma[f], b = beta[f];
+  for (int64_t n = threadIdx.x; n < N; n += BNT) {
+    const float xh = (xc[n] - mean) / den;
+    xhat[n + N * f] = xh;
+    y[n + N * f] = g * xh + b;
+  }
+  if (threadIdx.x == 0) {
+    bmean[f] = mean;
+    bvar[f] = var;
+    rmean[f] = (1.0f - momentum) * rmean[f] + momentum * mean;
+    rvar[f] = (1.0f - momentum) * rvar[f] + momentum * var;
+  }
+}
+
+// batch_norm.cpp:353-385
+__global__ void __launch_bounds__(BNT) bn_bwd_kernel(const float* __restrict__ dY,
+                                                     const float* __restrict__ x,
+                                                     const float* __restrict__ xhat,
+                                                     const float* __restrict__ gamma,
+                                                     const float* __restrict__ bmean,
+                                                     const float* __restrict__ bvar,
+                                                     float* __restrict__ ggamma,
+                                                     float* __restrict__ gbeta,
+                                                     float* __restrict__ dX, int64_t N, float eps) {
+  __shared__ float sm[BNT / 64];
+  const int64_t f = blockIdx.x;
+  const float* dyc = dY + N * f;
+  const float* xc = x + N * f;
+  const float* xhc = xhat + N * f;
+  const float g = gamma[f], mean = bmean[f];
+  const float inv_std = 1.0f / sqrtf(bvar[f] + eps);
+  const float inv_batch = 1.0f / (float)N;
+  float sgg = 0.f, sgb = 0.f, sdv = 0.f, sdm = 0.f;
+  for (int64_t n = threadIdx.x; n < N; n += BNT) {
+    const float dy = dyc[n];
+    sgg += dy * xhc[n];
+    sgb += dy;
+    const float dxh = dy * g;
+    const float xmu = xc[n] - mean;
+    sdv += dxh * xmu * (-0.5f) * inv_std * inv_std * inv_std;
+    sdm += dxh * (-inv_std);
+  }
+  const float tgg = bn_block_sum(sgg, sm);
+  const float tgb = bn_block_sum(sgb, sm);
+  const float dvar = bn_block_sum(sdv, sm);
+  const float dmean = bn_block_sum(sdm, sm);
+  if (threadIdx.x == 0) {
+    ggamma[f] = tgg;
+    gbeta[f] = tgb;
+  }
+  for (int64_t n = threadIdx.x; n < N; n += BNT) {
+    const float dxh = dyc[n] * g;
+    const float xmu = xc[n] - mean;
+    dX[n + N * f] = dxh * inv_std + dvar * 2.0f * xmu * inv_batch + dmean * inv_batch;
+  }
+}
+
+// ---------------------------------------------------------------- GELU / pool / add
+// GELU, exact form: Phi(x) = 0.5 (1 + erf(x/sqrt 2)) = 0.5 erfc(-x/sqrt 2); the
+// erfc form keeps full relative accuracy in the negative tail, where
+// 1 + erf(.) cancels.
+__global__ void __launch_bounds__(256) gelu_fwd_kernel(const float* __restrict__ x,
+                                                       float* __restrict__ y, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const float v = x[i];
+    y[i] = v * (0.5f * erfcf(v * -0.70710678118654752440f));
+  }
+}
+__global__ void __launch_bounds__(256) gelu_bwd_kernel(const float* __restrict__ x,
+                                                       const float* __restrict__ dy,
+                                                       float* __restrict__ dx, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const float v = x[i];
+    const float cdf = 0.5f * erfcf(v * -0.70710678118654752440f);
+    const float pdf = 0.39894228040143267794f * expf(-0.5f * v * v);
+    dx[i] = dy[i] * (cdf + v * pdf);
+  }
+}
+
+// mean over s of [B,S,D]; thread per (b, d), b fastest
+__global__ void __launch_bounds__(256) meanpool_fwd_kernel(const float* __restrict__ x,
+                                                           float* __restrict__ y, int64_t B,
+                                                           int64_t S, int64_t D) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= B * D) return;
+  const int64_t b = e % B, d = e / B;
+  float s = 0.f;
+  for (int64_t t = 0; t < S; ++t) s += x[b + B * t + B * S * d];
+  y[e] = s / (float)S;
+}
+__global__ void __launch_bounds__(256) meanpool_bwd_kernel(const float* __restrict__ dy,
+                                                           float* __restrict__ dx, int64_t B,
+                                                           int64_t S, int64_t D, float inv_S) {
+  const int64_t total = B * S * D;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t b = i % B, d = i / (B * S);
+    dx[i] = dy[b + B * d] * inv_S;
+  }
+}
+
+__global__ void __launch_bounds__(256) add_kernel(const float* __restrict__ a,
+                                                  const float* __restrict__ b,
+                                                  float* __restrict__ y, int64_t n, int vec) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const int64_t t0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (vec) {
+    for (int64_t i = t0; i < n / 4; i += stride) {
+      const f32x4 u = reinterpret_cast<const f32x4*>(a)[i];
+      const f32x4 v = reinterpret_cast<const f32x4*>(b)[i];
+      reinterpret_cast<f32x4*>(y)[i] = u + v;
+    }
+  } else {
+    for (int64_t i = t0; i < n; i += stride) y[i] = a[i] + b[i];
+  }
+}
+
+struct Workspace {
+  void* p = nullptr;
+  hipStream_t st;
+  explicit Workspace(hipStream_t s) : st(s) {}
+  int alloc(size_t bytes, const char* who) { return check_hip(hipMallocAsync(&p, bytes, st), who); }
+  ~Workspace() {
+    if (p) (void)hipFreeAsync(p, st);
+  }
+};
+
+}  // namespace
+}  // namespace cnhip
+
+using cnhip::as_stream;
+
+extern "C" {
+
+int cnhip_transpose(const float* in, float* out, int64_t rows, int64_t cols, cnhip_stream_t s) {
+  const char* who = "cnhip_transpose";
+  CNHIP_REQUIRE(rows >= 0 && cols >= 0, "%s: negative size", who);
+  if (rows == 0 || cols == 0) return CNHIP_OK;
+  CNHIP_REQUIRE(in && out && in != out, "%s: NULL or aliased pointers", who);
+  return cnhip::transpose(in, out, rows, cols, as_stream(s), who);
+}
+
+int64_t cnhip_mha_cache_floats(int64_t B, int64_t S, int64_t D) {
+  // Qp, Kp, Vp (per-sample layout), A^T per sample, context (row layout).
+  // Sample b's blocks: Qp_b at b*3SD, Kp_b at b*3SD + SD, Vp_b at b*3SD + 2SD
+  // (each [S, D] ColMajor); A^T_b at 3BSD + b*SS with A[i][j] at j + S*i;
+  // context [B*S, D] at 3BSD + B*SS.
+  return 4 * B * S * D + B * S * S;
+}
+
+int cnhip_mha_forward(const float* q, const float* k, const float* v, const float* Wq,
+                      const float* Wk, const float* Wv, const float* Wo, float* out, float* cache,
+                      int64_t B, int64_t S, int64_t D, int64_t heads, cnhip_stream_t stream) {
+  const char* who = "cnhip_mha_forward";
+  CNHIP_REQUIRE(B > 0 && S > 0 && D > 0 && heads > 0 && D % heads == 0,
+                "%s: bad shape B=%lld S=%lld D=%lld heads=%lld (D %% heads must be 0)", who,
+                (long long)B, (long long)S, (long long)D, (long long)heads);
+  CNHIP_REQUIRE(q && k && v && Wq && Wk && Wv && Wo && out && cache, "%s: NULL pointer", who);
+  CNHIP_REQUIRE(B <= 65535, "%s: batch %lld exceeds 65535", who, (long long)B);
+  hipStream_t st = as_stream(stream);
+  const int64_t BS = B * S, SD = S * D, SS = S * S, DD = D * D;
+  const float scale = 1.0f / sqrtf((float)(D / heads));  // attention.cpp:83
+  float* Qs = cache;  // per sample b: Qp_b, Kp_b, Vp_b at b*3SD
+  float* At = Qs + 3 * BS * D;  // per-sample A^T: (j, i) at j + S*i
+  float* ctx = At + B * SS;     // row layout [B*S, D]
+  cnhip::Workspace ws(st);
+  CNHIP_TRY(ws.alloc((size_t)(3 * BS * D) * sizeof(float), who));
+  float* proj = static_cast<float*>(ws.p);  // row layout [B*S, 3D]: Qp | Kp | Vp
+  // Self-attention with W_q, W_k, W_v adjacent in memory: one GEMM X [Wq Wk Wv].
+  if (q == k && k == v && Wk == Wq + DD && Wv == Wk + DD) {
+    CNHIP_TRY(cnhip::gemm_f32(0, 0, BS, 3 * D, D, 1.f, q, BS, Wq, D, 0.f, proj, BS, nullptr, 0, st, who));
+  } else {
+    const float* src[3] = {q, k, v};
+    const float* W[3] = {Wq, Wk, Wv};
+    for (int i = 0; i < 3; ++i)
+      CNHIP_TRY(cnhip::gemm_f32(0, 0, BS, D, D, 1.f, src[i], BS, W[i], D, 0.f, proj + i * BS * D, BS,
+                                nullptr, 0, st, who));
+  }
+  // The row-layout [B*S, 3D] matrix is [B, 3SD] with row b + B*s; its
+  // transpose [3SD, B] holds sample b's Qp_b, Kp_b, Vp_b (each [S, D]) at
+  // b*3SD, b*3SD + SD and b*3SD + 2SD.
+  CNHIP_TRY(cnhip::transpose(proj, Qs, B, 3 * SD, st, who));
+  const float* Qb = Qs;
+  const float* Kb = Qs + SD;
+  const float* Vb = Qs + 2 * SD;
+  const int64_t ps = 3 * SD;
+  // A^T_b = (Kp_b Qp_b^T) * scale (scores transposed, 187-189), then row softmax (191-205)
+  CNHIP_TRY(cnhip::gemm_f32_batched(0, 1, S, S, D, scale, Kb, S, ps, Qb, S, ps, 0.f, At, S, SS, B,
+                                    nullptr, 0, st, who));
+  CNHIP_TRY(cnhip::softmax_rows(At, At, BS, S, st, who));
+  // context_b = A_b Vp_b = (A^T_b)^T Vp_b (211), then back to row layout
+  CNHIP_TRY(cnhip::gemm_f32_batched(1, 0, S, D, S, 1.f, At, S, SS, Vb, S, ps, 0.f, proj, S, SD, B,
+                                    nullptr, 0, st, who));
+  CNHIP_TRY(cnhip::transpose(proj, ctx, SD, B, st, who));
+  // out = context W_o (212)
+  return cnhip::gemm_f32(0, 0, BS, D, D, 1.f, ctx, BS, Wo, D, 0.f, out, BS, nullptr, 0, st, who);
+}
+
+int cnhip_mha_backward(const float* q, const float* k, const float* v, const float* Wq,
+                       const float* Wk, const float* Wv, const float* Wo, const float* cache,
+                       const float* dY, float* gWq, float* gWk, float* gWv, float* gWo, float* dX,
+                       int64_t B, int64_t S, int64_t D, int64_t heads, cnhip_stream_t stream) {
+  const char* who = "cnhip_mha_backward";
+  CNHIP_REQUIRE(B > 0 && S > 0 && D > 0 && heads > 0 && D % heads == 0, "%s: bad shape", who);
+  CNHIP_REQUIRE(q && k && v && Wq && Wk && Wv && Wo && cache && dY && gWq && gWk && gWv && gWo,
+                "%s: NULL pointer", who);
+  CNHIP_REQUIRE(B <= 65535, "%s: batch %lld exceeds 65535", who, (long long)B);
+  hipStream_t st = as_stream(stream);
+  const int64_t BS = B * S, SD = S * D, SS = S * S, DD = D * D;
+  const float scale = 1.0f / sqrtf((float)(D / heads));
+  const float* Ps = cache;  // per sample b: Qp_b, Kp_b, Vp_b at b*3SD
+  const float* At = Ps + 3 * BS * D;
+  const float* ctx = At + B * SS;
+  const int64_t ps = 3 * SD;
+  cnhip::Workspace ws(st);
+  CNHIP_TRY(ws.alloc((size_t)(8 * BS * D + 2 * B * SS) * sizeof(float), who));
+  float* gctx = static_cast<float*>(ws.p);  // row layout [B*S, D]
+  float* gcs = gctx + BS * D;               // per-sample
+  float* gPs = gcs + BS * D;                // per sample b: gQp_b, gKp_b, gVp_b at b*3SD
+  float* G = gPs + 3 * BS * D;              // row layout [B*S, 3D]: gQp | gKp | gVp
+  float* gAT = G + 3 * BS * D;              // per-sample (j, i)
+  float* gST = gAT + B * SS;
+  // grad_context = dY W_o^T (535); grad_W_o = context^T dY (536)
+  CNHIP_TRY(cnhip::gemm_f32(0, 1, BS, D, D, 1.f, dY, BS, Wo, D, 0.f, gctx, BS, nullptr, 0, st, who));
+  CNHIP_TRY(cnhip::gemm_f32(1, 0, D, D, BS, 1.f, ctx, BS, dY, BS, 0.f, gWo, D, nullptr, 0, st, who));
+  CNHIP_TRY(cnhip::transpose(gctx, gcs, B, SD, st, who));
+  // grad_A^T_b = Vp_b grad_ctx_b^T (538); grad_Vp_b = A_b^T grad_ctx_b (539)
+  CNHIP_TRY(cnhip::gemm_f32_batched(0, 1, S, S, D, 1.f, Ps + 2 * SD, S, ps, gcs, S, SD, 0.f, gAT, S,
+                                    SS, B, nullptr, 0, st, who));
+  CNHIP_TRY(cnhip::gemm_f32_batched(0, 0, S, D, S, 1.f, At, S, SS, gcs, S, SD, 0.f, gPs + 2 * SD, S,
+                                    ps, B, nullptr, 0, st, who));
+  // softmax Jacobian rows, times scale (541-551)
+  hipLaunchKernelGGL(cnhip::softmax_rows_bwd_kernel, dim3((unsigned)((BS + 3) / 4)), dim3(256), 0,
+                     st, At, gAT, gST, BS, S, scale);
+  CNHIP_TRY(cnhip::check_launch(who));
+  // grad_Qp_b = gS_b Kp_b ; grad_Kp_b = gS_b^T Qp_b (553-554)
+  CNHIP_TRY(cnhip::gemm_f32_batched(1, 0, S, D, S, 1.f, gST, S, SS, Ps + SD, S, ps, 0.f, gPs, S, ps,
+                                    B, nullptr, 0, st, who));
+  CNHIP_TRY(cnhip::gemm_f32_batched(0, 0, S, D, S, 1.f, gST, S, SS, Ps, S, ps, 0.f, gPs + SD, S, ps,
+                                    B, nullptr, 0, st, who));
+  // per-sample [3SD, B] -> row layout [B, 3SD] = [B*S, 3D]
+  CNHIP_TRY(cnhip::transpose(gPs, G, 3 * SD, B, st, who));
+  const float* gQp = G;
+  const float* gKp = G + BS * D;
+  const float* gVp = G + 2 * BS * D;
+  const bool packed = q == k && k == v && Wk == Wq + DD && Wv == Wk + DD && gWk == gWq + DD &&
+                      gWv == gWk + DD;
+  if (packed) {
+    // [gW_q gW_k gW_v] = X^T [gQp gKp gVp]; grad_input = [gQp gKp gVp] [Wq Wk Wv]^T
+    CNHIP_TRY(cnhip::gemm_f32(1, 0, D, 3 * D, BS, 1.f, q, BS, G, BS, 0.f, gWq, D, nullptr, 0, st, who));
+    if (dX)
+      CNHIP_TRY(cnhip::gemm_f32(0, 1, BS, D, 3 * D, 1.f, G, BS, Wq, D, 0.f, dX, BS, nullptr, 0, st, who));
+    return CNHIP_OK;
+  }
+  // weight grads over all B*S rows (556-563)
+  CNHIP_TRY(cnhip::gemm_f32(1, 0, D, D, BS, 1.f, q, BS, gQp, BS, 0.f, gWq, D, nullptr, 0, st, who));
+  CNHIP_TRY(cnhip::gemm_f32(1, 0, D, D, BS, 1.f, k, BS, gKp, BS, 0.f, gWk, D, nullptr, 0, st, who));
+  CNHIP_TRY(cnhip::gemm_f32(1, 0, D, D, BS, 1.f, v, BS, gVp, BS, 0.f, gWv, D, nullptr, 0, st, who));
+  // grad_input = dQ + dK + dV (565-567)
+  if (dX) {
+    CNHIP_TRY(cnhip::gemm_f32(0, 1, BS, D, D, 1.f, gQp, BS, Wq, D, 0.f, dX, BS, nullptr, 0, st, who));
+    CNHIP_TRY(cnhip::gemm_f32(0, 1, BS, D, D, 1.f, gKp, BS, Wk, D, 1.f, dX, BS, nullptr, 0, st, who));
+    CNHIP_TRY(cnhip::gemm_f32(0, 1, BS, D, D, 1.f, gVp, BS, Wv, D, 1.f, dX, BS, nullptr, 0, st, who));
+  }
+  return CNHIP_OK;
+}
+
+int cnhip_embedding_forward(const int32_t* ids, const float* Wt, float* out, int64_t B, int64_t S,
+                            int64_t V, int64_t D, int32_t* oob_count, cnhip_stream_t stream) {
+  const char* who = "cnhip_embedding_forward";
+  CNHIP_REQUIRE(B > 0 && S > 0 && V > 0 && D > 0, "%s: bad shape", who);
+  CNHIP_REQUIRE(ids && Wt && out, "%s: NULL pointer", who);
+  const int64_t BS = B * S;
+  CNHIP_REQUIRE((D + cnhip::TT - 1) / cnhip::TT <= 65535, "%s: embed_dim too large", who);
+  hipLaunchKernelGGL(cnhip::embedding_fwd_kernel,
+                     dim3((unsigned)((BS + cnhip::TT - 1) / cnhip::TT), (unsigned)((D + cnhip::TT - 1) / cnhip::TT)),
+                     dim3(256), 0, as_stream(stream), ids, Wt, out, BS, V, D, oob_count);
+  return cnhip::check_launch(who);
+}
+
+int cnhip_embedding_backward(const int32_t* ids, const float* dY, float* gWt, int64_t B, int64_t S,
+                             int64_t V, int64_t D, cnhip_stream_t stream) {
+  const char* who = "cnhip_embedding_backward";
+  CNHIP_REQUIRE(B > 0 && S > 0 && V > 0 && D > 0, "%s: bad shape", who);
+  CNHIP_REQUIRE(ids && dY && gWt, "%s: NULL pointer", who);
+  CNHIP_REQUIRE(V < ((int64_t)1 << 31) && B * S < ((int64_t)1 << 31), "%s: too large", who);
+  hipStream_t st = as_stream(stream);
+  const int64_t BS = B * S;
+  cnhip::Workspace ws(st);
+  const size_t ibytes = (size_t)(2 * V + (V + 1) + BS) * sizeof(int32_t);
+  CNHIP_TRY(ws.alloc(ibytes + (size_t)(BS * D) * sizeof(float) + 16, who));
+  int32_t* counts = static_cast<int32_t*>(ws.p);
+  int32_t* cursor = counts + V;
+  int32_t* offsets = cursor + V;
+  int32_t* pos = offsets + (V + 1);
+  float* dYt = reinterpret_cast<float*>(reinterpret_cast<char*>(ws.p) + ((ibytes + 15) & ~size_t(15)));
+  CNHIP_TRY(cnhip::check_hip(hipMemsetAsync(counts, 0, (size_t)(2 * V) * sizeof(int32_t), st), who));
+  CNHIP_TRY(cnhip::transpose(dY, dYt, BS, D, st, who));
+  const unsigned g = cnhip::elementwise_grid(BS, 256);
+  hipLaunchKernelGGL(cnhip::emb_count_kernel, dim3(g), dim3(256), 0, st, ids, counts, BS, V);
+  CNHIP_TRY(cnhip::check_launch(who));
+  hipLaunchKernelGGL(cnhip::emb_scan_kernel, dim3(1), dim3(1024), 0, st, counts, offsets, V);
+  CNHIP_TRY(cnhip::check_launch(who));
+  hipLaunchKernelGGL(cnhip::emb_fill_kernel, dim3(g), dim3(256), 0, st, ids, offsets, cursor, pos, B, S, V);
+  CNHIP_TRY(cnhip::check_launch(who));
+  hipLaunchKernelGGL(cnhip::emb_sort_kernel, dim3(cnhip::elementwise_grid(V, 256)), dim3(256), 0, st,
+                     offsets, pos, V);
+  CNHIP_TRY(cnhip::check_launch(who));
+  hipLaunchKernelGGL(cnhip::emb_sum_kernel, dim3((unsigned)V), dim3(128), 0, st, offsets, pos, dYt,
+                     gWt, B, S, D);
+  return cnhip::check_launch(who);
+}
+
+int cnhip_batchnorm_forward(const float* x, float* y, float* xhat, const float* gamma,
+                            const float* beta, float* running_mean, float* running_var,
+                            float* batch_mean, float* batch_var, int64_t N, int64_t F,
+                            float momentum, float eps, cnhip_stream_t stream) {
+  const char* who = "cnhip_batchnorm_forward";
+  CNHIP_REQUIRE(N > 0 && F > 0, "%s: bad shape", who);
+  CNHIP_REQUIRE(x && y && xhat && gamma && beta && running_mean && running_var && batch_mean && batch_var,
+                "%s: NULL pointer", who);
+  hipLaunchKernelGGL(cnhip::bn_fwd_kernel, dim3((unsigned)F), dim3(cnhip::BNT), 0, as_stream(stream), x,
+                     y, xhat, gamma, beta, running_mean, running_var, batch_mean, batch_var, N,
+                     momentum, eps);
+  return cnhip::check_launch(who);
+}
+
+int cnhip_batchnorm_backward(const float* dY, const float* x, const float* xhat, const float* gamma,
+                             const float* batch_mean, const float* batch_var, float* grad_gamma,
+                             float* grad_beta, float* dX, int64_t N, int64_t F, float eps,
+                             cnhip_stream_t stream) {
+  const char* who = "cnhip_batchnorm_backward";
+  CNHIP_REQUIRE(N > 0 && F > 0, "%s: bad shape", who);
+  CNHIP_REQUIRE(dY && x && xhat && gamma && batch_mean && batch_var && grad_gamma && grad_beta && dX,
+                "%s: NULL pointer", who);
+  hipLaunchKernelGGL(cnhip::bn_bwd_kernel, dim3((unsigned)F), dim3(cnhip::BNT), 0, as_stream(stream),
+                     dY, x, xhat, gamma, batch_mean, batch_var, grad_gamma, grad_beta, dX, N, eps);
+  return cnhip::check_launch(who);
+}
+
+int cnhip_gelu_forward(const float* x, float* y, int64_t n, cnhip_stream_t s) {
+  const char* who = "cnhip_gelu_forward";
+  CNHIP_REQUIRE(n >= 0, "%s: negative size", who);
+  if (n == 0) return CNHIP_OK;
+  CNHIP_REQUIRE(x && y, "%s: NULL pointer", who);
+  hipLaunchKernelGGL(cnhip::gelu_fwd_kernel, dim3(cnhip::elementwise_grid(n, 256)), dim3(256), 0,
+                     as_stream(s), x, y, n);
+  return cnhip::check_launch(who);
+}
+
+int cnhip_gelu_backward(const float* x, const float* dy, float* dx, int64_t n, cnhip_stream_t s) {
+  const char* who = "cnhip_gelu_backward";
+  CNHIP_REQUIRE(n >= 0, "%s: negative size", who);
+  if (n == 0) return CNHIP_OK;
+  CNHIP_REQUIRE(x && dy && dx, "%s: NULL pointer", who);
+  hipLaunchKernelGGL(cnhip::gelu_bwd_kernel, dim3(cnhip::elementwise_grid(n, 256)), dim3(256), 0,
+                     as_stream(s), x, dy, dx, n);
+  return cnhip::check_launch(who);
+}
+
+int cnhip_meanpool1d_forward(const float* x, float* y, int64_t B, int64_t S, int64_t D,
+                             cnhip_stream_t s) {
+  const char* who = "cnhip_meanpool1d_forward";
+  CNHIP_REQUIRE(B > 0 && S > 0 && D > 0, "%s: bad shape", who);
+  CNHIP_REQUIRE(x && y, "%s: NULL pointer", who);
+  hipLaunchKernelGGL(cnhip::meanpool_fwd_kernel, dim3((unsigned)((B * D + 255) / 256)), dim3(256), 0,
+                     as_stream(s), x, y, B, S, D);
+  return cnhip::check_launch(who);
+}
+
+int cnhip_meanpool1d_backward(const float* dy, float* dx, int64_t B, int64_t S, int64_t D,
+                              cnhip_stream_t s) {
+  const char* who = "cnhip_meanpool1d_backward";
+  CNHIP_REQUIRE(B > 0 && S > 0 && D > 0, "%s: bad shape", who);
+  CNHIP_REQUIRE(dy && dx, "%s: NULL pointer", who);
+  hipLaunchKernelGGL(cnhip::meanpool_bwd_kernel, dim3(cnhip::elementwise_grid(B * S * D, 256)),
+                     dim3(256), 0, as_stream(s), dy, dx, B, S, D, 1.0f / (float)S);
+  return cnhip::check_launch(who);
+}
+
+int cnhip_add(const float* a, const float* b, float* y, int64_t n, cnhip_stream_t s) {
+  const char* who = "cnhip_add";
+  CNHIP_REQUIRE(n >= 0, "%s: negative size", who);
+  if (n == 0) return CNHIP_OK;
+  CNHIP_REQUIRE(a && b && y, "%s: NULL pointer", who);
+  const int vec = (n % 4 == 0) && cnhip::aligned16(a) && cnhip::aligned16(b) && cnhip::aligned16(y);
+  hipLaunchKernelGGL(cnhip::add_kernel, dim3(cnhip::elementwise_grid(vec ? n / 4 : n, 256)), dim3(256),
+                     0, as_stream(s), a, b, y, n, vec);
+  return cnhip::check_launch(who);
+}
+
+}  // extern "C"

@@ -120,6 +120,69 @@ def seq_scatter(inp, Y, B, S, D, t) -> None:
     _capi.call("cnhip_seq_scatter", _p(inp), _p(Y), B, S, D, t, _stream())
 
 
+def transpose(inp, out, rows: int, cols: int) -> None:
+    _capi.call("cnhip_transpose", _p(inp), _p(out), rows, cols, _stream())
+
+
+def mha_cache_floats(B: int, S: int, D: int) -> int:
+    return int(_capi.load().cnhip_mha_cache_floats(B, S, D))
+
+
+def mha_forward(q, k, v, Wq, Wk, Wv, Wo, out, cache, B, S, D, heads) -> None:
+    _capi.call("cnhip_mha_forward", *(_p(t) for t in (q, k, v, Wq, Wk, Wv, Wo, out, cache)),
+               B, S, D, heads, _stream())
+
+
+def mha_backward(q, k, v, Wq, Wk, Wv, Wo, cache, dY, gWq, gWk, gWv, gWo, dX, B, S, D,
+                 heads) -> None:
+    _capi.call("cnhip_mha_backward", *(_p(t) for t in (q, k, v, Wq, Wk, Wv, Wo, cache, dY, gWq,
+                                                       gWk, gWv, gWo, dX)), B, S, D, heads,
+               _stream())
+
+
+def embedding_forward(ids, Wt, out, B, S, V, D, oob=None) -> None:
+    _capi.call("cnhip_embedding_forward", _p(ids), _p(Wt), _p(out), B, S, V, D, _p(oob),
+               _stream())
+
+
+def embedding_backward(ids, dY, gWt, B, S, V, D) -> None:
+    _capi.call("cnhip_embedding_backward", _p(ids), _p(dY), _p(gWt), B, S, V, D, _stream())
+
+
+def batchnorm_forward(x, y, xhat, gamma, beta, rmean, rvar, bmean, bvar, N, F, momentum=0.1,
+                      eps=1e-5) -> None:
+    _capi.call("cnhip_batchnorm_forward", *(_p(t) for t in (x, y, xhat, gamma, beta, rmean, rvar,
+                                                            bmean, bvar)), N, F, momentum, eps,
+               _stream())
+
+
+def batchnorm_backward(dY, x, xhat, gamma, bmean, bvar, ggamma, gbeta, dX, N, F,
+                       eps=1e-5) -> None:
+    _capi.call("cnhip_batchnorm_backward", *(_p(t) for t in (dY, x, xhat, gamma, bmean, bvar,
+                                                             ggamma, gbeta, dX)), N, F, eps,
+               _stream())
+
+
+def gelu_forward(x, y) -> None:
+    _capi.call("cnhip_gelu_forward", _p(x), _p(y), x.numel(), _stream())
+
+
+def gelu_backward(x, dy, dx) -> None:
+    _capi.call("cnhip_gelu_backward", _p(x), _p(dy), _p(dx), x.numel(), _stream())
+
+
+def meanpool1d_forward(x, y, B, S, D) -> None:
+    _capi.call("cnhip_meanpool1d_forward", _p(x), _p(y), B, S, D, _stream())
+
+
+def meanpool1d_backward(dy, dx, B, S, D) -> None:
+    _capi.call("cnhip_meanpool1d_backward", _p(dy), _p(dx), B, S, D, _stream())
+
+
+def add(a, b, y) -> None:
+    _capi.call("cnhip_add", _p(a), _p(b), _p(y), a.numel(), _stream())
+
+
 def _unary(name: str, x, y) -> None:
     _capi.call(name, _p(x, "x"), _p(y, "y"), x.numel(), _stream())
 

@@ -184,6 +184,74 @@ int cnhip_seq_select(const float* Y, float* out, int64_t B, int64_t S, int64_t D
 int cnhip_seq_scatter(const float* in, float* Y, int64_t B, int64_t S, int64_t D, int64_t t,
                       cnhip_stream_t stream);
 
+/* ---- transformer layers ----------------------------------------------------
+ * Sequences [B,S,D] are ColMajor (row b + B*s of a [B*S, D] matrix). */
+
+/* out [cols, rows] = in [rows, cols]^T, both ColMajor. */
+int cnhip_transpose(const float* in, float* out, int64_t rows, int64_t cols,
+                    cnhip_stream_t stream);
+/* MultiHeadAttention: one full-width head, scale 1/sqrt(D/heads), no biases;
+ * out = softmax_rows(Q Wq (K Wk)^T * scale) (V Wv) Wo per sample.  forward
+ * fills `cache` (cnhip_mha_cache_floats(B,S,D) floats: the projections and
+ * attention weights backward reads); backward OVERWRITES the four weight
+ * grads and writes dX = dQ + dK + dV (dX may be NULL).  When q == k == v and
+ * Wq, Wk, Wv (and gWq, gWk, gWv) are adjacent D*D blocks, the three
+ * projections run as one GEMM.
+ * ref: MultiHeadAttention::forward/backward
+ * src/CppNet/layers/attention.cpp:60-221, 503-569 (cpu-eigen branches) */
+int64_t cnhip_mha_cache_floats(int64_t B, int64_t S, int64_t D);
+int cnhip_mha_forward(const float* q, const float* k, const float* v, const float* Wq,
+                      const float* Wk, const float* Wv, const float* Wo, float* out,
+                      float* cache, int64_t B, int64_t S, int64_t D, int64_t heads,
+                      cnhip_stream_t stream);
+int cnhip_mha_backward(const float* q, const float* k, const float* v, const float* Wq,
+                       const float* Wk, const float* Wv, const float* Wo, const float* cache,
+                       const float* dY, float* gWq, float* gWk, float* gWv, float* gWo,
+                       float* dX, int64_t B, int64_t S, int64_t D, int64_t heads,
+                       cnhip_stream_t stream);
+/* Embedding: weights kept token-major, Wt[d + D*v] (the transpose of the
+ * reference's ColMajor [V, D]); ids [B,S] int32; out [B,S,D].  Ids outside
+ * [0, V) give zero rows and are counted into *oob_count (may be NULL; the
+ * host layer checks it and raises, as the cpu-eigen branch throws).
+ * backward OVERWRITES gWt (rows of unused ids become 0) with a deterministic
+ * per-token sum in position order.
+ * ref: Embedding::forward/backward src/CppNet/layers/embedding.cpp:46-175;
+ * embedding_forward.cu, embedding_backward.cu */
+int cnhip_embedding_forward(const int32_t* ids, const float* Wt, float* out, int64_t B,
+                            int64_t S, int64_t V, int64_t D, int32_t* oob_count,
+                            cnhip_stream_t stream);
+int cnhip_embedding_backward(const int32_t* ids, const float* dY, float* gWt, int64_t B,
+                             int64_t S, int64_t V, int64_t D, cnhip_stream_t stream);
+/* BatchNorm over x [N,F] in training mode: biased batch variance,
+ * xhat = (x - mean)/sqrt(var + eps), y = gamma xhat + beta, running stats
+ * (1-momentum) r + momentum * batch.  backward OVERWRITES grad_gamma and
+ * grad_beta.  ref: BatchNorm::forward/backward
+ * src/CppNet/layers/batch_norm.cpp:204-401; batch_norm_forward.cu,
+ * batch_norm_backward.cu */
+int cnhip_batchnorm_forward(const float* x, float* y, float* xhat, const float* gamma,
+                            const float* beta, float* running_mean, float* running_var,
+                            float* batch_mean, float* batch_var, int64_t N, int64_t F,
+                            float momentum, float eps, cnhip_stream_t stream);
+int cnhip_batchnorm_backward(const float* dY, const float* x, const float* xhat,
+                             const float* gamma, const float* batch_mean,
+                             const float* batch_var, float* grad_gamma, float* grad_beta,
+                             float* dX, int64_t N, int64_t F, float eps, cnhip_stream_t stream);
+/* GELU, exact form y = x Phi(x) = 0.5 x (1 + erf(x/sqrt 2)); dx = dy (Phi(x)
+ * + x phi(x)).  No reference counterpart: the reference has no GELU. */
+int cnhip_gelu_forward(const float* x, float* y, int64_t n, cnhip_stream_t stream);
+int cnhip_gelu_backward(const float* x, const float* dy, float* dx, int64_t n,
+                        cnhip_stream_t stream);
+/* MeanPool1D: y [B,D] = mean over s of x [B,S,D]; dx = dy / S broadcast.
+ * ref: MeanPool1D::forward/backward src/CppNet/layers/mean_pool1d.cpp:24-150;
+ * mean_pool1d.cu:27-69 */
+int cnhip_meanpool1d_forward(const float* x, float* y, int64_t B, int64_t S, int64_t D,
+                             cnhip_stream_t stream);
+int cnhip_meanpool1d_backward(const float* dy, float* dx, int64_t B, int64_t S, int64_t D,
+                              cnhip_stream_t stream);
+/* y = a + b (the residual add and its gradient sum).
+ * ref: Residual::forward/backward src/CppNet/layers/residual.cpp:44-159 */
+int cnhip_add(const float* a, const float* b, float* y, int64_t n, cnhip_stream_t stream);
+
 /* ---- activations (elementwise over n values) -------------------------- */
 /* ReLU: y = max(x,0); dx = dy * (y > 0)   (mask from the cached OUTPUT)
  * ref: relu.cu:14-23, relu_grad.cu:11-19; ReLU::forward/backward
