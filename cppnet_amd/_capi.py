@@ -64,6 +64,7 @@ SIGNATURES: dict[str, tuple] = {
     "cnhip_embedding_forward": (i32, [vp, vp, vp, i64, i64, i64, i64, vp, vp]),
     "cnhip_embedding_backward": (i32, [vp, vp, vp, i64, i64, i64, i64, vp]),
     "cnhip_batchnorm_forward": (i32, [vp] * 9 + [i64, i64, f32, f32, vp]),
+    "cnhip_batchnorm_forward_eval": (i32, [vp] * 7 + [i64, i64, f32, vp]),
     "cnhip_batchnorm_backward": (i32, [vp] * 9 + [i64, i64, f32, vp]),
     "cnhip_gelu_forward": (i32, [vp, vp, i64, vp]),
     "cnhip_gelu_backward": (i32, [vp, vp, vp, i64, vp]),

@@ -189,6 +189,18 @@ namespace CppNet
                       "fill_zero");
     }
 
+    DeviceTensor DeviceTensor::view(int64_t offset, std::vector<int64_t> dims) const
+    {
+        const int64_t n = count_of(dims);
+        if (offset < 0 || offset + n > size())
+            throw std::invalid_argument("DeviceTensor::view: [" + std::to_string(offset) + ", " +
+                                        std::to_string(offset + n) + ") outside " + shape_str(dims_));
+        DeviceTensor t = *this;
+        t.dims_ = std::move(dims);
+        t.ptr_ = static_cast<char*>(ptr_) + offset * 4;
+        return t;
+    }
+
     DeviceTensor DeviceTensor::reshape(std::vector<int64_t> dims) const
     {
         if (count_of(dims) != size())

@@ -14,10 +14,118 @@
 
 using namespace CppNet;
 
+namespace
+{
+    DeviceTensor add_t(const DeviceTensor& a, const DeviceTensor& b, const char* who)
+    {
+        DeviceTensor y = DeviceTensor::empty(a.dims());
+        Device::check(cnhip_add(a.data(), b.data(), y.data(), a.size(), Device::stream()), who);
+        return y;
+    }
+
+    /**
+     * Config-5 encoder block, composed by the harness as the reference's
+     * harness composes its layers (no encoder class exists in the reference):
+     *   r = MHA(x, x, x) + x;  h = BatchNorm(r as [B*S, D]);
+     *   y = Linear2(GELU(Linear1(h))) + h
+     */
+    struct EncoderBlock
+    {
+        std::shared_ptr<Layers::MultiHeadAttention> mha;
+        std::shared_ptr<Layers::BatchNorm> bn;
+        std::shared_ptr<Layers::Linear> ff1, ff2;
+        std::shared_ptr<Activations::GELU> gelu;
+        std::vector<int64_t> dims;
+
+        DeviceTensor forward(const DeviceTensor& x)
+        {
+            dims = x.dims();
+            const int64_t BS = dims[0] * dims[1], D = dims[2];
+            DeviceTensor r = add_t(mha->forward(x, x, x), x, "encoder residual 1");
+            DeviceTensor h = bn->forward(r.reshape({BS, D}));
+            DeviceTensor f = ff2->forward(gelu->forward(ff1->forward(h)));
+            return add_t(f, h, "encoder residual 2").reshape(dims);
+        }
+
+        DeviceTensor backward(const DeviceTensor& g)
+        {
+            const int64_t BS = dims[0] * dims[1], D = dims[2];
+            DeviceTensor g2 = g.reshape({BS, D});
+            DeviceTensor gh = add_t(ff1->backward(gelu->backward(ff2->backward(g2))), g2, "encoder grad 2");
+            DeviceTensor gr = bn->backward(gh).reshape(dims);
+            return add_t(mha->backward(gr), gr, "encoder grad 1");
+        }
+
+        void step(Optimizers::Optimizer& opt, float lr)
+        {
+            mha->step(opt, lr);
+            bn->step(opt, lr);
+            ff1->step(opt, lr);
+            ff2->step(opt, lr);
+        }
+
+        void zero_grad()
+        {
+            mha->reset_grads();
+            bn->reset_grads();
+            ff1->reset_grads();
+            ff2->reset_grads();
+        }
+    };
+
+    /// Embedding -> blocks -> MeanPool1D -> Linear (logits).
+    struct EncoderNet
+    {
+        std::shared_ptr<Layers::Embedding> emb;
+        std::vector<EncoderBlock> blocks;
+        std::shared_ptr<Layers::MeanPool1D> pool;
+        std::shared_ptr<Layers::Linear> fc;
+
+        DeviceTensor forward(const DeviceTensor& ids)
+        {
+            DeviceTensor x = emb->forward(ids);
+            for (auto& b : blocks) x = b.forward(x);
+            return fc->forward(pool->forward(x));
+        }
+
+        void backward(const DeviceTensor& g)
+        {
+            DeviceTensor x = pool->backward(fc->backward(g));
+            for (auto it = blocks.rbegin(); it != blocks.rend(); ++it) x = it->backward(x);
+            emb->backward(x);
+        }
+
+        void update(Optimizers::Optimizer& opt, float lr)
+        {
+            opt.begin_group();
+            try
+            {
+                emb->step(opt, lr);
+                for (auto& b : blocks) b.step(opt, lr);
+                fc->step(opt, lr);
+            }
+            catch (...)
+            {
+                opt.end_group();
+                throw;
+            }
+            opt.end_group();
+        }
+
+        void zero_grad()
+        {
+            emb->reset_grads();
+            for (auto& b : blocks) b.zero_grad();
+            fc->reset_grads();
+        }
+    };
+} // namespace
+
 struct cnt_session
 {
     cnhip_stream_t stream = nullptr;
     Models::SequentialModel model;
+    std::unique_ptr<EncoderNet> encoder;  // set for transformer sessions (X holds int32 ids)
     std::vector<std::shared_ptr<Layers::Layer>> keep;  // owns the layers
     std::unique_ptr<Losses::Loss> loss;
     std::unique_ptr<Optimizers::Adam> adam;
@@ -30,6 +138,9 @@ struct cnt_session
     struct Param
     {
         std::function<DeviceTensor&()> value, grad;
+        // > 0: stored as the transpose of the reference's ColMajor
+        // [t_rows, t_cols] (the token-major embedding table)
+        int64_t t_rows = 0, t_cols = 0;
     };
     std::vector<Param> params;
 
@@ -109,13 +220,48 @@ namespace
         if (!s) throw std::invalid_argument("NULL session");
     }
 
-    DeviceTensor& param_at(cnt_session* s, int index, bool grad)
+    cnt_session::Param& param_rec(cnt_session* s, int index)
     {
         check_session(s);
         if (index < 0 || index >= static_cast<int>(s->params.size()))
             throw std::out_of_range("parameter index " + std::to_string(index) + " out of range");
-        auto& p = s->params[static_cast<size_t>(index)];
+        return s->params[static_cast<size_t>(index)];
+    }
+
+    DeviceTensor& param_at(cnt_session* s, int index, bool grad)
+    {
+        auto& p = param_rec(s, index);
         return grad ? p.grad() : p.value();
+    }
+
+    // host copy in the reference's layout
+    void param_to_host(cnt_session* s, int index, bool grad, float* host)
+    {
+        auto& p = param_rec(s, index);
+        DeviceTensor& t = grad ? p.grad() : p.value();
+        if (p.t_rows == 0)
+        {
+            t.copy_to_host(host);
+            return;
+        }
+        DeviceTensor tmp = DeviceTensor::empty({p.t_rows, p.t_cols});
+        Device::check(cnhip_transpose(t.data(), tmp.data(), p.t_cols, p.t_rows, Device::stream()), "param");
+        tmp.copy_to_host(host);
+    }
+
+    void param_from_host(cnt_session* s, int index, const float* host)
+    {
+        auto& p = param_rec(s, index);
+        DeviceTensor& t = p.value();
+        if (p.t_rows == 0)
+        {
+            t.copy_from_host(host);
+            return;
+        }
+        DeviceTensor tmp = DeviceTensor::empty({p.t_rows, p.t_cols});
+        tmp.copy_from_host(host);
+        Device::check(cnhip_transpose(tmp.data(), t.data(), p.t_rows, p.t_cols, Device::stream()), "param");
+        Device::synchronize();
     }
 
     std::unique_ptr<cnt_session> new_session(uint64_t seed)
@@ -263,6 +409,66 @@ int cnt_rnn_create(cnt_session** out, int cell, int64_t batch, int64_t seq_len, 
     });
 }
 
+int cnt_transformer_create(cnt_session** out, int64_t batch, int64_t seq_len, int64_t vocab,
+                           int64_t embed_dim, int64_t heads, int n_blocks, int64_t ffn_dim,
+                           int64_t classes, float lr, float beta1, float beta2, float eps, uint64_t seed)
+{
+    return guarded("cnt_transformer_create", [&] {
+        if (!out) throw std::invalid_argument("NULL out pointer");
+        *out = nullptr;
+        if (batch <= 0 || seq_len <= 0 || n_blocks < 0 || classes <= 0)
+            throw std::invalid_argument("batch, seq_len, classes must be positive and n_blocks >= 0");
+        auto s = new_session(seed);
+        StreamScope scope(s.get());
+        auto net = std::make_unique<EncoderNet>();
+        const int D = static_cast<int>(embed_dim);
+        net->emb = std::make_shared<Layers::Embedding>(static_cast<int>(vocab), D, "gpu");
+        {
+            Layers::Embedding* e = net->emb.get();
+            cnt_session::Param p{[e]() -> DeviceTensor& { return e->weights(); },
+                                 [e]() -> DeviceTensor& { return e->grad_weights(); }};
+            p.t_rows = vocab;
+            p.t_cols = embed_dim;
+            s->params.push_back(p);
+        }
+        for (int i = 0; i < n_blocks; ++i)
+        {
+            EncoderBlock b;
+            b.mha = std::make_shared<Layers::MultiHeadAttention>(D, static_cast<int>(heads), "gpu");
+            b.bn = std::make_shared<Layers::BatchNorm>(D, 0.1f, 1e-5f, "gpu");
+            b.ff1 = std::make_shared<Layers::Linear>(D, static_cast<int>(ffn_dim), "ffn1_" + std::to_string(i),
+                                                     true, true, "gpu", "xavier");
+            b.gelu = std::make_shared<Activations::GELU>("gpu");
+            b.ff2 = std::make_shared<Layers::Linear>(static_cast<int>(ffn_dim), D, "ffn2_" + std::to_string(i),
+                                                     true, true, "gpu", "xavier");
+            Layers::MultiHeadAttention* m = b.mha.get();
+            for (int w = 0; w < 4; ++w)
+                s->params.push_back({[m, w]() -> DeviceTensor& { return m->weight(w); },
+                                     [m, w]() -> DeviceTensor& { return m->grad_weight(w); }});
+            Layers::BatchNorm* bn = b.bn.get();
+            s->params.push_back({[bn]() -> DeviceTensor& { return bn->gamma(); },
+                                 [bn]() -> DeviceTensor& { return bn->grad_gamma(); }});
+            s->params.push_back({[bn]() -> DeviceTensor& { return bn->beta(); },
+                                 [bn]() -> DeviceTensor& { return bn->grad_beta(); }});
+            s->add_params(b.ff1);
+            s->add_params(b.ff2);
+            net->blocks.push_back(std::move(b));
+        }
+        net->pool = std::make_shared<Layers::MeanPool1D>("gpu");
+        net->fc = std::make_shared<Layers::Linear>(D, static_cast<int>(classes), "classifier", true, true, "gpu",
+                                                   "xavier");
+        s->add_params(net->fc);
+        s->encoder = std::move(net);
+        s->loss = make_loss(CNT_LOSS_SOFTMAX_CE);
+        s->adam = std::make_unique<Optimizers::Adam>(beta1, beta2, eps, "gpu");
+        s->lr = lr;
+        s->X = DeviceTensor::zeros({batch, seq_len});  // int32 ids
+        s->Y = DeviceTensor::zeros({batch, classes});
+        Device::synchronize();
+        *out = s.release();
+    });
+}
+
 int cnt_destroy(cnt_session* s)
 {
     return guarded("cnt_destroy", [&] {
@@ -293,24 +499,38 @@ int cnt_param_size(cnt_session* s, int index, int64_t* n)
 int cnt_set_param(cnt_session* s, int index, const float* host)
 {
     return guarded("cnt_set_param", [&] {
+        check_session(s);
         StreamScope scope(s);
-        param_at(s, index, false).copy_from_host(host);
+        param_from_host(s, index, host);
     });
 }
 
 int cnt_get_param(cnt_session* s, int index, float* host)
 {
     return guarded("cnt_get_param", [&] {
+        check_session(s);
         StreamScope scope(s);
-        param_at(s, index, false).copy_to_host(host);
+        param_to_host(s, index, false, host);
     });
 }
 
 int cnt_get_grad(cnt_session* s, int index, float* host)
 {
     return guarded("cnt_get_grad", [&] {
+        check_session(s);
         StreamScope scope(s);
-        param_at(s, index, true).copy_to_host(host);
+        param_to_host(s, index, true, host);
+    });
+}
+
+int cnt_set_batch_tokens(cnt_session* s, const int32_t* ids_host, const float* y_host)
+{
+    return guarded("cnt_set_batch_tokens", [&] {
+        check_session(s);
+        if (!s->encoder) throw std::invalid_argument("not a token-input (transformer) session");
+        StreamScope scope(s);
+        s->X.copy_from_host(ids_host);
+        s->Y.copy_from_host(y_host);
     });
 }
 
@@ -318,6 +538,7 @@ int cnt_set_batch(cnt_session* s, const float* x_host, const float* y_host)
 {
     return guarded("cnt_set_batch", [&] {
         check_session(s);
+        if (s->encoder) throw std::invalid_argument("transformer sessions take int32 ids: use cnt_set_batch_tokens");
         StreamScope scope(s);
         s->X.copy_from_host(x_host);
         s->Y.copy_from_host(y_host);
@@ -340,11 +561,27 @@ namespace
 {
     void forward_backward(cnt_session* s)
     {
+        if (s->encoder)
+        {
+            s->encoder->zero_grad();
+            DeviceTensor out = s->encoder->forward(s->X);
+            s->last_loss = s->loss->forward(out, s->Y);
+            s->encoder->backward(s->loss->backward(out, s->Y));
+            return;
+        }
         s->model.zero_grad();
         DeviceTensor out = s->model.forward(s->X);
         s->last_loss = s->loss->forward(out, s->Y);
         DeviceTensor g = s->loss->backward(out, s->Y);
         s->model.backward(g);
+    }
+
+    void update(cnt_session* s)
+    {
+        if (s->encoder)
+            s->encoder->update(*s->adam, s->lr);
+        else
+            s->model.update(*s->adam, s->lr);
     }
 } // namespace
 
@@ -354,7 +591,7 @@ int cnt_step(cnt_session* s, float* loss_out)
         check_session(s);
         StreamScope scope(s);
         forward_backward(s);
-        s->model.update(*s->adam, s->lr);
+        update(s);
         if (loss_out) *loss_out = s->last_loss.get();
     });
 }
@@ -374,7 +611,7 @@ int cnt_update(cnt_session* s)
     return guarded("cnt_update", [&] {
         check_session(s);
         StreamScope scope(s);
-        s->model.update(*s->adam, s->lr);
+        update(s);
     });
 }
 

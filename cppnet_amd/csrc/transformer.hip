@@ -303,6 +303,25 @@ __global__ void __launch_bounds__(BNT) bn_fwd_kernel(const float* __restrict__ x
   }
 }
 
+// eval mode (batch_norm.cpp:320-327): running statistics
+__global__ void __launch_bounds__(256) bn_eval_kernel(const float* __restrict__ x,
+                                                      float* __restrict__ y,
+                                                      float* __restrict__ xhat,
+                                                      const float* __restrict__ gamma,
+                                                      const float* __restrict__ beta,
+                                                      const float* __restrict__ rmean,
+                                                      const float* __restrict__ rvar, int64_t N,
+                                                      int64_t F, float eps) {
+  const int64_t total = N * F;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t f = i / N;
+    const float xh = (x[i] - rmean[f]) / sqrtf(rvar[f] + eps);
+    xhat[i] = xh;
+    y[i] = gamma[f] * xh + beta[f];
+  }
+}
+
 // batch_norm.cpp:353-385
 __global__ void __launch_bounds__(BNT) bn_bwd_kernel(const float* __restrict__ dY,
                                                      const float* __restrict__ x,
@@ -615,6 +634,18 @@ int cnhip_batchnorm_forward(const float* x, float* y, float* xhat, const float* 
   hipLaunchKernelGGL(cnhip::bn_fwd_kernel, dim3((unsigned)F), dim3(cnhip::BNT), 0, as_stream(stream), x,
                      y, xhat, gamma, beta, running_mean, running_var, batch_mean, batch_var, N,
                      momentum, eps);
+  return cnhip::check_launch(who);
+}
+
+int cnhip_batchnorm_forward_eval(const float* x, float* y, float* xhat, const float* gamma,
+                                 const float* beta, const float* running_mean,
+                                 const float* running_var, int64_t N, int64_t F, float eps,
+                                 cnhip_stream_t stream) {
+  const char* who = "cnhip_batchnorm_forward_eval";
+  CNHIP_REQUIRE(N > 0 && F > 0, "%s: bad shape", who);
+  CNHIP_REQUIRE(x && y && xhat && gamma && beta && running_mean && running_var, "%s: NULL pointer", who);
+  hipLaunchKernelGGL(cnhip::bn_eval_kernel, dim3(cnhip::elementwise_grid(N * F, 256)), dim3(256), 0,
+                     as_stream(stream), x, y, xhat, gamma, beta, running_mean, running_var, N, F, eps);
   return cnhip::check_launch(who);
 }
 

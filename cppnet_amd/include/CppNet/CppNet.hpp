@@ -16,10 +16,16 @@
 #include "CppNet/layers/lstm.hpp"
 #include "CppNet/layers/gru.hpp"
 #include "CppNet/layers/sequence_last.hpp"
+#include "CppNet/layers/embedding.hpp"
+#include "CppNet/layers/attention.hpp"
+#include "CppNet/layers/batch_norm.hpp"
+#include "CppNet/layers/mean_pool1d.hpp"
+#include "CppNet/layers/residual.hpp"
 #include "CppNet/activations/activation.hpp"
 #include "CppNet/activations/relu.hpp"
 #include "CppNet/activations/sigmoid.hpp"
 #include "CppNet/activations/tanh.hpp"
+#include "CppNet/activations/gelu.hpp"
 #include "CppNet/losses/loss.hpp"
 #include "CppNet/losses/binary_cross_entropy.hpp"
 #include "CppNet/losses/mse.hpp"

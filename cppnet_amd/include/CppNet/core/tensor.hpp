@@ -181,6 +181,9 @@ namespace CppNet
 
         /// Same buffer, new ColMajor shape (element count must match).
         DeviceTensor reshape(std::vector<int64_t> dims) const;
+        /// Same buffer, elements [offset, offset + prod(dims)) as a tensor of
+        /// shape dims (the packed-parameter views of MultiHeadAttention).
+        DeviceTensor view(int64_t offset, std::vector<int64_t> dims) const;
 
     private:
         std::vector<int64_t> dims_;

@@ -37,6 +37,9 @@ def load() -> C.CDLL:
                                  f32, f32, f32, C.c_uint64]),
         "cnt_rnn_create": (i32, [C.POINTER(vp), i32, i64, i64, i64, i64, i64, f32, f32, f32, f32,
                                  C.c_uint64]),
+        "cnt_transformer_create": (i32, [C.POINTER(vp), i64, i64, i64, i64, i64, i32, i64, i64, f32,
+                                         f32, f32, f32, C.c_uint64]),
+        "cnt_set_batch_tokens": (i32, [vp, vp, vp]),
         "cnt_destroy": (i32, [vp]),
         "cnt_num_params": (i32, [vp, C.POINTER(i32)]),
         "cnt_param_size": (i32, [vp, i32, C.POINTER(i64)]),
@@ -198,6 +201,62 @@ def synthetic_rnn(cfg: RNNConfig, rng: np.random.Generator):
     return params, X, Y
 
 
+@dataclass
+class TransformerConfig:
+    """Embedding(vocab, D) -> blocks x [MHA(D, heads) + x -> BatchNorm(D) ->
+    Linear(D -> ffn) -> GELU -> Linear(ffn -> D) + residual] -> MeanPool1D ->
+    Linear(D -> classes) -> softmax-CE; token ids [B, S]."""
+    name: str
+    batch: int
+    seq_len: int
+    vocab: int
+    embed_dim: int
+    heads: int
+    blocks: int
+    ffn: int
+    classes: int
+    lr: float = 1e-3
+    beta1: float = 0.9
+    beta2: float = 0.999
+    eps: float = 1e-8
+    seed: int = 1234
+    loss: str = "softmax_ce"
+
+
+def transformer_config(config: int = 5, batch: int | None = None, seq_len: int | None = None,
+                       **shape) -> TransformerConfig:
+    """vocab 8192, D 512, 8 heads, 2 blocks, FFN 2048,
+    4 classes, B 32, S 256.  Keyword overrides shrink it for tests."""
+    if config != 5:
+        raise ValueError(f"config {config} is not the transformer config")
+    c = TransformerConfig("C5 transformer Emb(8192,512) 2x[MHA(512,8)+res, BN, FFN 2048 GELU +res]"
+                          " -> MeanPool1D -> 512->4", 32 if batch is None else batch,
+                          256 if seq_len is None else seq_len, 8192, 512, 8, 2, 2048, 4)
+    for k, v in shape.items():
+        setattr(c, k, v)
+    return c
+
+
+def synthetic_transformer(cfg: TransformerConfig, rng: np.random.Generator):
+    """Parameters in the session's order (embedding U(+-1/sqrt(D)) as
+    embedding.cpp:38-39, MHA xavier as attention.cpp:47-50, gamma 1, beta 0,
+    Linear xavier with zero bias), token ids uniform in [0, vocab) as int32
+    ColMajor [B, S], one-hot uniform labels ColMajor [B, classes]."""
+    D, F = cfg.embed_dim, cfg.ffn
+    s = 1.0 / np.sqrt(D)
+    params = [rng.uniform(-s, s, cfg.vocab * D).astype(np.float32)]
+    for _ in range(cfg.blocks):
+        params += [xavier(rng, D, D) for _ in range(4)]
+        params += [np.ones(D, np.float32), np.zeros(D, np.float32)]
+        params += [xavier(rng, D, F), np.zeros(F, np.float32), xavier(rng, F, D), np.zeros(D, np.float32)]
+    params += [xavier(rng, D, cfg.classes), np.zeros(cfg.classes, np.float32)]
+    ids = rng.integers(0, cfg.vocab, cfg.batch * cfg.seq_len).astype(np.int32)
+    labels = rng.integers(0, cfg.classes, cfg.batch)
+    Y = np.zeros((cfg.classes, cfg.batch), np.float32)
+    Y[labels, np.arange(cfg.batch)] = 1.0
+    return params, ids, Y.ravel()
+
+
 def xavier(rng: np.random.Generator, fan_in: int, fan_out: int) -> np.ndarray:
     """xavier-uniform [fan_in, fan_out] (init.cpp:21-33), ColMajor flat."""
     lim = np.sqrt(6.0 / (fan_in + fan_out))
@@ -232,7 +291,15 @@ class Session:
     def __init__(self, cfg):
         lib = load()
         h = C.c_void_p()
-        if isinstance(cfg, RNNConfig):
+        self.tokens = isinstance(cfg, TransformerConfig)
+        if self.tokens:
+            _check(lib.cnt_transformer_create(C.byref(h), cfg.batch, cfg.seq_len, cfg.vocab,
+                                              cfg.embed_dim, cfg.heads, cfg.blocks, cfg.ffn,
+                                              cfg.classes, cfg.lr, cfg.beta1, cfg.beta2, cfg.eps,
+                                              cfg.seed))
+            self.x_size = cfg.batch * cfg.seq_len
+            self.y_size = cfg.batch * cfg.classes
+        elif isinstance(cfg, RNNConfig):
             _check(lib.cnt_rnn_create(C.byref(h), 0 if cfg.cell == "lstm" else 1, cfg.batch,
                                       cfg.seq_len, cfg.input_size, cfg.hidden, cfg.out_features,
                                       cfg.lr, cfg.beta1, cfg.beta2, cfg.eps, cfg.seed))
@@ -304,11 +371,13 @@ class Session:
         return out
 
     def set_batch(self, X: np.ndarray, Y: np.ndarray) -> None:
-        X = np.ascontiguousarray(X, np.float32)
+        """X: float32 inputs, or int32 token ids for a transformer session."""
+        X = np.ascontiguousarray(X, np.int32 if self.tokens else np.float32)
         Y = np.ascontiguousarray(Y, np.float32)
         assert X.size == self.x_size, f"X has {X.size} values, the model takes {self.x_size}"
         assert Y.size == self.y_size, f"Y has {Y.size} values, the model takes {self.y_size}"
-        _check(load().cnt_set_batch(self.h, X.ctypes.data, Y.ctypes.data))
+        fn = load().cnt_set_batch_tokens if self.tokens else load().cnt_set_batch
+        _check(fn(self.h, X.ctypes.data, Y.ctypes.data))
 
     def set_batch_device(self, X_ptr: int, Y_ptr: int) -> None:
         _check(load().cnt_set_batch_device(self.h, X_ptr, Y_ptr))

@@ -232,6 +232,12 @@ int cnhip_batchnorm_forward(const float* x, float* y, float* xhat, const float* 
                             const float* beta, float* running_mean, float* running_var,
                             float* batch_mean, float* batch_var, int64_t N, int64_t F,
                             float momentum, float eps, cnhip_stream_t stream);
+/* eval mode: xhat = (x - running_mean)/sqrt(running_var + eps)
+ * (batch_norm.cpp:320-327); statistics untouched. */
+int cnhip_batchnorm_forward_eval(const float* x, float* y, float* xhat, const float* gamma,
+                                 const float* beta, const float* running_mean,
+                                 const float* running_var, int64_t N, int64_t F, float eps,
+                                 cnhip_stream_t stream);
 int cnhip_batchnorm_backward(const float* dY, const float* x, const float* xhat,
                              const float* gamma, const float* batch_mean,
                              const float* batch_var, float* grad_gamma, float* grad_beta,

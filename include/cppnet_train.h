@@ -57,6 +57,21 @@ int cnt_cnn_create(cnt_session** out, int n_conv, const int64_t* conv_spec, int 
 int cnt_rnn_create(cnt_session** out, int cell, int64_t batch, int64_t seq_len,
                    int64_t input_size, int64_t hidden_size, int64_t out_features, float lr,
                    float beta1, float beta2, float eps, uint64_t seed);
+/* Transformer encoder classifier (config 5): Embedding(vocab, D) -> n_blocks x
+ * [r = MultiHeadAttention(D, heads)(x, x, x) + x; h = BatchNorm(D) on the
+ * [B*S, D] view; y = Linear(ffn -> D)(GELU(Linear(D -> ffn)(h))) + h] ->
+ * MeanPool1D -> Linear(D -> classes) -> SoftmaxCrossEntropy("mean"), Adam.
+ * Inputs are int32 token ids [batch, seq_len] (cnt_set_batch_tokens).
+ * Parameters: the embedding table (ColMajor [vocab, D] on the host side),
+ * then per block W_q, W_k, W_v, W_o, gamma, beta, W1, b1, W2, b2, then the
+ * classifier W, b.
+ * ref: the harness composition of benchmarks/transformer_benckmark.cpp:95-175
+ * with the layers of src/CppNet/layers/{embedding,attention,batch_norm,
+ * mean_pool1d}.cpp */
+int cnt_transformer_create(cnt_session** out, int64_t batch, int64_t seq_len, int64_t vocab,
+                           int64_t embed_dim, int64_t heads, int n_blocks, int64_t ffn_dim,
+                           int64_t classes, float lr, float beta1, float beta2, float eps,
+                           uint64_t seed);
 int cnt_destroy(cnt_session* s);
 
 int cnt_num_params(cnt_session* s, int* count);
@@ -68,6 +83,8 @@ int cnt_get_grad(cnt_session* s, int index, float* host);
 /* Uploads one batch (X: the model's input shape, Y: [batch, outputs]) that
  * every later cnt_step() trains on, until the next call. */
 int cnt_set_batch(cnt_session* s, const float* x_host, const float* y_host);
+/* Transformer sessions: int32 token ids [batch, seq_len] and one-hot Y. */
+int cnt_set_batch_tokens(cnt_session* s, const int32_t* ids_host, const float* y_host);
 /* Same from device memory already in HBM (copied on the session stream). */
 int cnt_set_batch_device(cnt_session* s, const float* x_dev, const float* y_dev);
 

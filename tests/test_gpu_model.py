@@ -427,3 +427,91 @@ def test_rnn_multi_step_parity(gpu, oracle_mt):
         print(f"[model] config 4 param {k}: gpu-vs-oracle {rel:.3g}, oracle drift {drift:.3g}")
         assert rel <= max(1e-3, 2.0 * drift), f"param {k}: relative norm error {rel:.3g}"
     sess.close()
+
+
+def test_transformer_one_step_parity(gpu, oracle_mt):
+    """Config 5 at full size (Embedding 8192x512, 2 encoder blocks, B=32,
+    S=256): loss, every gradient (relative part against max(|ref|, RMS of the
+    tensor): the weight gradients are sums over 8192 rows) and the updated
+    weights; the embedding gradient's routing is exact (rows of ids absent
+    from the batch stay exactly 0)."""
+    from oracle.transformer import OracleTransformer
+    cfg = trainer.transformer_config(5)
+    print(f"[model] config 5 batch {cfg.batch} S={cfg.seq_len}: one step", flush=True)
+    params, ids, Y = trainer.synthetic_transformer(cfg, np.random.default_rng(505))
+    sess = trainer.Session(cfg)
+    sess.set_params(params)
+    np.testing.assert_array_equal(sess.get_params()[0], params[0])  # layout round trip
+    sess.set_batch(ids, Y)
+    ref = OracleTransformer(cfg, oracle_mt)
+    ref.set_params(params)
+    loss_gpu = sess.forward_backward()
+    grads = sess.get_grads()
+    sess.update()
+    after = sess.get_grads()
+    n_lin = {len(params) - 2, len(params) - 1} | {1 + 10 * i + j for i in range(cfg.blocks) for j in (6, 7, 8, 9)}
+    assert all(not g.any() for k, g in enumerate(after) if k not in n_lin), \
+        "Embedding / MHA / BatchNorm grads must be cleared by step()"
+    loss_ref = ref.step(ids, Y)
+    ok, msg = close([loss_gpu], [loss_ref], 1e-4, 1e-5)
+    assert ok, f"loss: {msg}"
+    absent = np.setdiff1d(np.arange(cfg.vocab), ids)
+    emb_g = grads[0].reshape(cfg.embed_dim, cfg.vocab)  # ColMajor [V, D]: column d
+    assert not emb_g[:, absent].any(), "embedding rows of absent ids must stay exactly 0"
+    assert np.all(emb_g[:, np.unique(ids)].any(axis=0))
+    for k, (a, b) in enumerate(zip(grads, ref.last_grads)):
+        rms = float(np.sqrt(np.mean(b.astype(np.float64) ** 2)))
+        ok, msg = close_mag(a, b, np.full(b.shape, rms, np.float32), 1e-4, 1e-5)
+        assert ok, f"grad of param {k}: {msg}"
+    for k, (a, b) in enumerate(zip(sess.get_params(), ref.get_params())):
+        ok, msg = close(a, b, 1e-4, 1e-5)
+        if not ok:  # Adam's first step is ~lr*sign(g): only ill-conditioned gradients may flip
+            g = ref.last_grads[k]
+            rms = float(np.sqrt(np.mean(g.astype(np.float64) ** 2)))
+            bad = np.abs(a.astype(np.float64) - b) > 1e-5 + 1e-4 * np.abs(b)
+            assert np.all(np.abs(g[bad]) <= 1e-5 + 1e-4 * rms), f"param {k}: {msg}"
+    print(f"[model] config 5: loss {loss_gpu:.7f} vs {loss_ref:.7f}")
+    sess.close()
+
+
+def test_transformer_multi_step_parity(gpu, oracle_mt):
+    from oracle.transformer import OracleTransformer
+    cfg = trainer.transformer_config(5, batch=4, seq_len=16, vocab=64, embed_dim=32, heads=4, blocks=2,
+                                     ffn=64, classes=4)
+    steps = 20
+    print(f"[model] config 5 (reduced) {steps} steps", flush=True)
+    rng = np.random.default_rng(55)
+    params, _, _ = trainer.synthetic_transformer(cfg, rng)
+    sess = trainer.Session(cfg)
+    sess.set_params(params)
+    ref, ref_d = OracleTransformer(cfg, oracle_mt), OracleTransformer(cfg, oracle_mt)
+    ref.set_params(params)
+    ref_d.set_params(params)
+    for step in range(steps):
+        _, ids, Y = trainer.synthetic_transformer(cfg, rng)
+        sess.set_batch(ids, Y)
+        lg, lr_ = sess.step(), ref.step(ids, Y)
+        oracle_mt.cnref_set_accumulate_double(1)
+        try:
+            ref_d.step(ids, Y)
+        finally:
+            oracle_mt.cnref_set_accumulate_double(0)
+        assert abs(lg - lr_) <= 1e-3 * abs(lr_) + 1e-6, f"step {step}: loss {lg} vs {lr_}"
+    for k, (a, b, c) in enumerate(zip(sess.get_params(), ref.get_params(), ref_d.get_params())):
+        rel, drift = _rel(a, b), _rel(c, b)
+        print(f"[model] config 5 param {k}: gpu-vs-oracle {rel:.3g}, oracle drift {drift:.3g}")
+        assert rel <= max(1e-3, 2.0 * drift), f"param {k}: relative norm error {rel:.3g}"
+    sess.close()
+
+
+def test_transformer_rejects_out_of_range_ids(gpu):
+    cfg = trainer.transformer_config(5, batch=2, seq_len=3, vocab=10, embed_dim=8, heads=2, blocks=1,
+                                     ffn=16, classes=2)
+    params, ids, Y = trainer.synthetic_transformer(cfg, np.random.default_rng(1))
+    sess = trainer.Session(cfg)
+    ids = ids.copy()
+    ids[4] = 10
+    sess.set_batch(ids, Y)
+    with pytest.raises(Exception, match="token ID 10 out of range"):
+        sess.step()
+    sess.close()

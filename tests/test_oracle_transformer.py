@@ -142,3 +142,45 @@ def test_meanpool1d_vs_autograd(oracle):
     assert ok, msg
     ok, msg = close(from_cm(dx, (B, S, D)), xt.grad.numpy(), 1e-6, 1e-7)
     assert ok, msg
+
+
+def test_transformer_train_step_vs_autograd(oracle):
+    """The config-5 composition of the oracle (oracle/transformer.py) against
+    float64 torch autograd of the same network on logical tensors: loss, every
+    parameter gradient and the Adam-updated parameters."""
+    from cppnet_amd import trainer
+    from oracle.transformer import OracleTransformer
+    cfg = trainer.transformer_config(5, batch=3, seq_len=5, vocab=13, embed_dim=8, heads=2, blocks=2,
+                                     ffn=12, classes=3)
+    params, ids, Y = trainer.synthetic_transformer(cfg, np.random.default_rng(9))
+    ref = OracleTransformer(cfg, oracle)
+    ref.set_params(params)
+    loss = ref.step(ids, Y)
+    B, S, V, D, F, C = cfg.batch, cfg.seq_len, cfg.vocab, cfg.embed_dim, cfg.ffn, cfg.classes
+    shapes = [(V, D)] + [(D, D)] * 4 + [(D,), (D,), (D, F), (F,), (F, D), (D,)]
+    shapes = shapes[:1] + shapes[1:] * cfg.blocks + [(D, C), (C,)]
+    P = [t64(from_cm(p, s)) for p, s in zip(params, shapes)]
+    tok = torch.tensor(from_cm(ids, (B, S)), dtype=torch.long)
+    x = P[0][tok]
+    for i in range(cfg.blocks):
+        Wq, Wk, Wv, Wo, g, b, W1, b1, W2, b2 = P[1 + 10 * i: 11 + 10 * i]
+        a, _ = torch_mha(x, x, x, Wq, Wk, Wv, Wo, cfg.heads)
+        r = (a + x).reshape(B * S, D)
+        h = torch.nn.functional.batch_norm(r, None, None, g, b, training=True, eps=1e-5)
+        y = torch.nn.functional.gelu(h @ W1 + b1) @ W2 + b2 + h
+        x = y.reshape(B, S, D)
+    logits = x.mean(1) @ P[-2] + P[-1]
+    t = torch.tensor(from_cm(Y, (B, C)), dtype=torch.float64)
+    lt = -(t * torch.log_softmax(logits, 1)).sum() / B
+    lt.backward()
+    assert abs(loss - lt.item()) <= 1e-5 * abs(lt.item())
+    for k, (gr, p, s) in enumerate(zip(ref.last_grads, P, shapes)):
+        want = p.grad.numpy()
+        scale = np.abs(want).max() + 1e-30
+        err = np.abs(from_cm(gr, s) - want).max() / scale
+        assert err < 1e-4, f"grad of param {k}: max err {err:.3g} of max |g| {scale:.3g}"
+    # Adam step 1: W - lr * g / (|g| + eps) exactly in the limit (closed form)
+    for k, (p_new, p0, gr) in enumerate(zip(ref.get_params(), params, ref.last_grads)):
+        g64 = gr.astype(np.float64)
+        want = p0 - cfg.lr * g64 / (np.abs(g64) + cfg.eps)
+        np.testing.assert_allclose(p_new, want, rtol=1e-6, atol=1e-8, err_msg=f"param {k}")
