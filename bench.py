@@ -1,20 +1,25 @@
-"""Benchmark: fp32 train step (forward + backward + Adam) of BASELINE config 2,
-the wide MLP classifier Linear 1024->4096 -> ReLU -> Linear 4096->4096 -> ReLU
--> Linear 4096->10, softmax cross-entropy (mean), Adam(1e-3, 0.9, 0.999,
-1e-8), batch 4096, on one MI355X.
+"""Benchmark: fp32 train step (forward + backward + Adam) of a BASELINE config
+on one MI355X.  The default is config 2, the workload the metric is quoted
+on: the wide MLP classifier Linear 1024->4096 -> ReLU -> Linear 4096->4096
+-> ReLU -> Linear 4096->10, softmax cross-entropy (mean), Adam(1e-3, 0.9,
+0.999, 1e-8), batch 4096.  --config 1|3|4|5 measures the other configs the
+same way (MLP 30-64-1; CNN; LSTM 128->512 T=64; transformer encoder).
 
 The step runs in the C++ trainer (libcppnet.so: CppNet-compatible classes on
 device "gpu") on its own HIP stream; inputs, weights, gradients and Adam
 moments are resident in HBM before timing starts.  Prints ONE JSON line:
 
   value            train samples/s = batch * steps / timed seconds
-  roofline         the dominant kernel (the fp32 MFMA GEMM): algorithmic flops
-                   per launch / average launch duration, measured live with
-                   HIP events around every GEMM launch of a few extra steps
+  roofline         the dominant kernel class, the fp32 MFMA GEMM-shaped kernels
+                   (the GEMM kernel; for config 3 also the implicit-GEMM conv
+                   kernels): algorithmic flops per launch / average launch
+                   duration, measured live with HIP events on the launch
+                   stream around every such launch of a few extra steps
   cpu_baseline     the CPU oracle (a restatement of the reference's cpu-eigen
                    semantics, oracle/) on a bounded sample of the same workload
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+Usage: python bench.py [--gpus 1] [--config 2] [--steps K] [--warmup W]
+                       [--no-cpu-baseline] [--cpu-seconds S]
 """
 from __future__ import annotations
 
@@ -37,23 +42,81 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def cpu_baseline(cfg_full, seconds_budget: float = 20.0):
-    """Times the oracle-composed model (oracle/mlp.py over oracle/liboracle.so)
-    on this host: the same config-2 step at a reduced batch, scaled to
-    samples/s.  The first step is a warm-up; steps continue until about
-    seconds_budget of CPU work has been timed."""
+# ---------------------------------------------------------------- workloads
+def _mlp_flops(cfg):
+    return 6.0 * cfg.batch * sum(i * o for i, o in zip(cfg.sizes[:-1], cfg.sizes[1:]))
+
+
+def _cnn_flops(cfg):
+    N, C, H, W = cfg.input_shape
+    fwd = 0.0
+    for (ic, oc, k, s, p) in cfg.convs:
+        HO, WO = (H + 2 * p - k) // s + 1, (W + 2 * p - k) // s + 1
+        fwd += 2.0 * N * HO * WO * oc * ic * k * k
+        H, W = (HO - cfg.pool) // cfg.pool + 1, (WO - cfg.pool) // cfg.pool + 1
+    fwd += 2.0 * N * cfg.flat_features() * cfg.classes
+    return 3 * fwd
+
+
+def _rnn_flops(cfg):
+    G = (4 if cfg.cell == "lstm" else 3) * cfg.hidden
+    fwd = 2.0 * cfg.batch * cfg.seq_len * (cfg.input_size + cfg.hidden) * G
+    fwd += 2.0 * cfg.batch * cfg.hidden * cfg.out_features
+    return 3 * fwd
+
+
+def _tr_flops(cfg):
+    BS, D, S = cfg.batch * cfg.seq_len, cfg.embed_dim, cfg.seq_len
+    blk = 4 * 2.0 * BS * D * D + 2 * 2.0 * cfg.batch * S * S * D + 2 * 2.0 * BS * D * cfg.ffn
+    return 3 * (cfg.blocks * blk + 2.0 * cfg.batch * D * cfg.classes)
+
+
+def workload(config: int, batch: int | None = None):
+    """(cfg, synthetic-data function, oracle class, flops function, description)"""
+    from cppnet_amd import trainer
+    if config in (1, 2):
+        from oracle.mlp import OracleMLP
+        cfg = trainer.mlp_config(config, batch=batch)
+        desc = {1: "config 1: MLP 30-64-1, sigmoid, BCE, Adam",
+                2: "config 2: wide MLP 1024-4096-4096-10, softmax-CE, Adam"}[config]
+        return cfg, trainer.synthetic_mlp, OracleMLP, _mlp_flops, desc
+    if config == 3:
+        from oracle.cnn import OracleCNN
+        cfg = trainer.cnn_config(3, batch=batch)
+        return (cfg, trainer.synthetic_cnn, OracleCNN, _cnn_flops,
+                "config 3: CNN 2x(conv3x3, ReLU, maxpool2) -> 4096->10, softmax-CE, Adam")
+    if config == 4:
+        from oracle.rnn import OracleSeqRegressor
+        cfg = trainer.rnn_config(4, batch=batch)
+        return (cfg, trainer.synthetic_rnn, OracleSeqRegressor, _rnn_flops,
+                "config 4: LSTM 128->512, T=64, last hidden -> 512->1, MSE, Adam")
+    if config == 5:
+        from oracle.transformer import OracleTransformer
+        cfg = trainer.transformer_config(5, batch=batch)
+        return (cfg, trainer.synthetic_transformer, OracleTransformer, _tr_flops,
+                "config 5: transformer Emb(8192,512) -> 2x[MHA(512,8)+res, BatchNorm, "
+                "512-2048 GELU 2048-512 +res] -> MeanPool1D -> 512->4, softmax-CE, Adam")
+    raise ValueError(f"unknown config {config}")
+
+
+CPU_BATCH = {1: 512, 2: 512, 3: 32, 4: 16, 5: 4}
+
+
+def cpu_baseline(config: int, seconds_budget: float = 20.0):
+    """Times the oracle-composed model (oracle/ over oracle/liboracle.so) on
+    this host: the same step at a reduced batch, scaled to samples/s.  The
+    first step is a warm-up; steps continue until about seconds_budget of CPU
+    work has been timed."""
     import numpy as np
     from oracle import load_oracle
-    from oracle.mlp import OracleMLP
-    from cppnet_amd import trainer
 
     threads = min(16, os.cpu_count() or 1)
     o = load_oracle()
     o.cnref_set_threads(threads)
-    batch = 512
-    cfg = trainer.mlp_config(2, batch=batch)
-    params, X, Y = trainer.synthetic_mlp(cfg, np.random.default_rng(99))
-    ref = OracleMLP(cfg, o)
+    batch = CPU_BATCH[config]
+    cfg, synth, Oracle, _, _ = workload(config, batch=batch)
+    params, X, Y = synth(cfg, np.random.default_rng(99))
+    ref = Oracle(cfg, o)
     ref.set_params(params)
     ref.step(X, Y)  # warm-up
     n, t0 = 0, time.perf_counter()
@@ -61,19 +124,20 @@ def cpu_baseline(cfg_full, seconds_budget: float = 20.0):
         ref.step(X, Y)
         n += 1
         el = time.perf_counter() - t0
-        if el >= seconds_budget or n >= 50:
+        if el >= seconds_budget or n >= (20000 if config == 1 else 50):
             break
     return {"value": round(batch * n / el, 2), "unit": "samples/s", "cores": threads,
             "kind": "port",
-            "sample": (f"{n} train steps of config 2 at batch {batch} (of 4096) on the CPU oracle "
-                       f"(plain C++ restatement of cpu-eigen semantics, {threads} OpenMP threads),"
-                       f" {el:.1f} s")}
+            "sample": (f"{n} train steps of config {config} at batch {batch} (of {workload(config)[0].batch})"
+                       f" on the CPU oracle (plain C++ restatement of cpu-eigen semantics, "
+                       f"{threads} OpenMP threads), {el:.1f} s")}
 
 
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
+    ap.add_argument("--steps", type=int, default=None, help="default 50 (config 1: 200)")
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
@@ -82,6 +146,7 @@ def main() -> int:
         print(f"bench.py: this build runs on one GPU only (got --gpus {args.gpus}); the "
               "multi-GPU data-parallel design is described, not built", file=sys.stderr)
         return 2
+    steps = args.steps if args.steps is not None else (200 if args.config == 1 else 50)
 
     import ctypes as C
 
@@ -92,13 +157,14 @@ def main() -> int:
     if lib.cnhip_device_count() < 1:
         log("bench.py: no GPU visible")
         return 1
-    cfg = trainer.mlp_config(2)
+    cfg, synth, _, flops_fn, desc = workload(args.config)
     B = cfg.batch
-    params, X, Y = trainer.synthetic_mlp(cfg, np.random.default_rng(2024))
+    params, X, Y = synth(cfg, np.random.default_rng(2024))
     sess = trainer.Session(cfg)
     sess.set_params(params)
     sess.set_batch(X, Y)           # resident in HBM from here on
     stream = sess.stream
+    log(f"bench.py: {desc}, batch {B}: {args.warmup} warmup + {steps} timed steps")
 
     for _ in range(args.warmup):
         sess.step(read_loss=False)
@@ -109,20 +175,21 @@ def main() -> int:
     _capi.check(lib.cnhip_event_create(C.byref(ev1)))
     t0 = time.perf_counter()
     _capi.check(lib.cnhip_event_record(ev0, stream))
-    for _ in range(args.steps):
+    for _ in range(steps):
         sess.step(read_loss=False)
     _capi.check(lib.cnhip_event_record(ev1, stream))
     sess.synchronize()
     wall = time.perf_counter() - t0
     ms = C.c_float()
     _capi.check(lib.cnhip_event_elapsed_ms(C.byref(ms), ev0, ev1))
-    step_ms = ms.value / args.steps
+    step_ms = ms.value / steps
     loss = sess.step()  # one more step, read back: the run trained on finite numbers
     if not np.isfinite(loss):
         log(f"bench.py: non-finite loss {loss}")
         return 1
+    log(f"bench.py: {step_ms:.4f} ms/step, loss {loss:.6f}")
 
-    # Dominant kernel: per-launch timing of the GEMM over a few extra steps.
+    # Dominant kernel class: per-launch timing over a few extra steps.
     prof_steps = 3
     _capi.check(lib.cnhip_gemm_timing_enable(1))
     for _ in range(prof_steps):
@@ -132,29 +199,29 @@ def main() -> int:
     _capi.check(lib.cnhip_gemm_timing_enable(0))
     per_launch_us = kms.value * 1e3 / max(1, launches.value)
     flops_per_launch = kfl.value / max(1, launches.value)
-    achieved = kfl.value / (kms.value * 1e-3) / 1e12  # TFLOP/s
+    achieved = kfl.value / (kms.value * 1e-3) / 1e12 if kms.value > 0 else 0.0  # TFLOP/s
     gemm_share = kms.value / prof_steps / step_ms
 
-    step_flops = 2 * B * sum(i * o for i, o in zip(cfg.sizes[:-1], cfg.sizes[1:])) * 3
+    kernels = ("gemm_f32_kernel + conv_fwd/dgrad/wgrad_kernel (fp32 MFMA, all shapes of the step)"
+               if args.config == 3 else "gemm_f32_kernel (fp32 MFMA GEMM, all shapes of the step)")
     result = {
         "metric": METRIC,
         "value": round(B / (step_ms * 1e-3), 1),
         "unit": "samples/s",
         "n_gpus": 1,
-        "steps": args.steps,
+        "steps": steps,
         "warmup": args.warmup,
         "ms_per_step": round(step_ms, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp32",
-        "data": "synthetic (X~N(0,1), one-hot uniform labels, xavier weights; resident in HBM)",
-        "config": {"workload": "config 2: wide MLP 1024-4096-4096-10, softmax-CE, Adam",
-                   "global_batch": B, "params": 21020682, "parallelism": "single GPU",
-                   "step_tflops": round(step_flops / (step_ms * 1e-3) / 1e12, 2),
+        "data": "synthetic (seeded inputs/labels, reference init distributions; resident in HBM)",
+        "config": {"workload": desc, "global_batch": B, "parallelism": "single GPU",
+                   "params": int(sum(p.size for p in params)),
+                   "step_tflops": round(flops_fn(cfg) / (step_ms * 1e-3) / 1e12, 2),
                    "wall_s_timed_region": round(wall, 3)},
-        "roofline": {"bound": "mfma", "kernel": "gemm_f32_kernel (fp32 MFMA GEMM, all shapes of"
-                     " the step)",
+        "roofline": {"bound": "mfma", "kernel": kernels,
                      "achieved": round(achieved, 2), "peak": PEAK_FP32_MFMA_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4),
                      "traffic": None,
@@ -167,7 +234,7 @@ def main() -> int:
     sess.close()
     if not args.no_cpu_baseline:
         try:
-            result["cpu_baseline"] = cpu_baseline(cfg, args.cpu_seconds)
+            result["cpu_baseline"] = cpu_baseline(args.config, args.cpu_seconds)
         except Exception as e:  # the GPU figure stands on its own
             log(f"bench.py: cpu baseline failed: {e!r}")
     print(json.dumps(result), flush=True)

@@ -48,6 +48,15 @@ inline unsigned elementwise_grid(int64_t work_items, int block) {
   return static_cast<unsigned>(blocks);
 }
 
+// Per-launch timing of the MFMA GEMM-shaped kernels (cnhip_gemm_timing_*):
+// while enabled, a launch site brackets its kernel with rec->start/stop on
+// the launch stream.  timing_slot returns nullptr when timing is off.
+struct TimingRec {
+  hipEvent_t start, stop;
+  double flops;
+};
+TimingRec* timing_slot(double flops);
+
 }  // namespace cnhip
 
 #define CNHIP_REQUIRE(cond, ...)           \

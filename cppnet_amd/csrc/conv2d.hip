@@ -350,8 +350,13 @@ void launch_pixel(const ConvArgs& a, int64_t M, int64_t Ng, int64_t pixels, hipS
   auto go = [&](auto cfg) {
     using Cfg = decltype(cfg);
     const int64_t tiles = ((M + Cfg::BM - 1) / Cfg::BM) * ((Ng + Cfg::BN - 1) / Cfg::BN);
+    // algorithmic flops: 2 * N * (output pixels) * OC * C * KS^2 for both directions
+    const ConvDims& d = a.d;
+    TimingRec* rec = timing_slot(2.0 * d.N * d.HO * d.WO * d.OC * d.C * d.KS * d.KS);
+    if (rec) (void)hipEventRecord(rec->start, st);
     hipLaunchKernelGGL(Kern<Cfg>::fn(), dim3((unsigned)tiles, (unsigned)pixels), dim3(Cfg::NT), 0,
                        st, a);
+    if (rec) (void)hipEventRecord(rec->stop, st);
   };
   if (Ng <= 32) go(CfgSN{});
   else if (Ng <= 64) go(CfgM{});
@@ -416,9 +421,12 @@ int cnhip_conv2d_backward(const float* X, const float* W, const float* dY, float
     void* ws = nullptr;
     CNHIP_TRY(cnhip::check_hip(hipMallocAsync(&ws, (size_t)splits * OC * Ng * sizeof(float), st), who));
     a.partial = static_cast<float*>(ws);
+    cnhip::TimingRec* rec = cnhip::timing_slot(2.0 * N * d.HO * d.WO * OC * CT);
+    if (rec) (void)hipEventRecord(rec->start, st);
     hipLaunchKernelGGL(cnhip::conv_wgrad_kernel<Cfg>, dim3((unsigned)tiles, 1, (unsigned)splits),
                        dim3(Cfg::NT), 0, st, a);
     int status = cnhip::check_launch(who);
+    if (rec) (void)hipEventRecord(rec->stop, st);
     if (status == CNHIP_OK) {
       hipLaunchKernelGGL(cnhip::conv_wgrad_reduce_kernel,
                          dim3(cnhip::elementwise_grid(OC * Ng, 256)), dim3(256), 0, st, a.partial,

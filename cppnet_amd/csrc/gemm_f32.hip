@@ -229,16 +229,14 @@ void launch_t(int ta, int tb, const GemmArgs& g, int64_t batches, hipStream_t st
 
 // Per-launch event timing (cnhip_gemm_timing_*): a pool of event pairs
 // reused across enable() calls.
-struct TimingRec {
-  hipEvent_t start, stop;
-  double flops;
-};
 struct Timing {
   bool on = false;
   std::vector<TimingRec> pool;
   size_t used = 0;
 };
 thread_local Timing g_timing;
+
+}  // namespace
 
 TimingRec* timing_slot(double flops) {
   Timing& t = g_timing;
@@ -255,6 +253,8 @@ TimingRec* timing_slot(double flops) {
   r->flops = flops;
   return r;
 }
+
+namespace {
 
 enum class Shape { L, SN, SM, S };
 

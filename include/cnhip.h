@@ -93,9 +93,11 @@ int cnhip_gemm_f32_batched(int trans_a, int trans_b, int64_t M, int64_t N, int64
                            float* C, int64_t ldc, int64_t stride_c, int64_t batch_count,
                            cnhip_stream_t stream);
 
-/* Measurement aid for the GEMM kernel (the MFMA-bound hot kernel): while
- * enabled, every GEMM kernel launch on this host thread is bracketed by HIP
- * events on its own stream, and its algorithmic flops (2*M*N*K) recorded.
+/* Measurement aid for the MFMA GEMM-shaped kernels (the GEMM kernel and the
+ * implicit-GEMM Conv2D forward / dgrad / wgrad kernels): while enabled,
+ * every such launch on this host thread is bracketed by HIP events on its
+ * own stream, and its algorithmic flops (2*M*N*K; for Conv2D
+ * 2*N*HO*WO*OC*C*KS^2) recorded.
  * read() synchronises those events and returns the launch count, the summed
  * kernel time (ms) and the summed flops since the last enable(1).  Split-K
  * reduction launches are not counted.  Not a reference function. */
