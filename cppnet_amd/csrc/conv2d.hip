@@ -305,18 +305,31 @@ __global__ void __launch_bounds__(Cfg::NT) conv_wgrad_kernel(ConvArgs a) {
 }
 
 // gW[oc + OC*j] = sum_z partial[z][oc + OC*j]; the ones-column goes to gb.
-__global__ void __launch_bounds__(256) conv_wgrad_reduce_kernel(const float* __restrict__ partial,
-                                                                int splits, int64_t OC, int64_t CT,
-                                                                int has_bias, float* __restrict__ gW,
-                                                                float* __restrict__ gb) {
+// 64 consecutive outputs per block (coalesced along e); the RW waves of a
+// block each sum one contiguous chunk of z in ascending order, and the chunk
+// sums are added in ascending order: a fixed summation order for any launch.
+constexpr int WGRAD_RW = 16;
+__global__ void __launch_bounds__(64 * WGRAD_RW) conv_wgrad_reduce_kernel(
+    const float* __restrict__ partial, int splits, int64_t OC, int64_t CT, int has_bias,
+    float* __restrict__ gW, float* __restrict__ gb) {
+  __shared__ float part[WGRAD_RW][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int64_t Ng = CT + has_bias, total = OC * Ng;
-  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
-       e += (int64_t)gridDim.x * blockDim.x) {
-    float s = 0.f;
-    for (int z = 0; z < splits; ++z) s += partial[(int64_t)z * total + e];
+  const int64_t e = (int64_t)blockIdx.x * 64 + lane;
+  const int per = (splits + WGRAD_RW - 1) / WGRAD_RW;
+  const int z0 = w * per, z1 = min(splits, z0 + per);
+  float s = 0.f;
+  if (e < total)
+    for (int z = z0; z < z1; ++z) s += partial[(int64_t)z * total + e];
+  part[w][lane] = s;
+  __syncthreads();
+  if (w == 0 && e < total) {
+    float t = part[0][lane];
+#pragma unroll
+    for (int i = 1; i < WGRAD_RW; ++i) t += part[i][lane];
     const int64_t j = e / OC;
-    if (j < CT) gW[e] = s;
-    else if (gb) gb[e - OC * CT] = s;
+    if (j < CT) gW[e] = t;
+    else if (gb) gb[e - OC * CT] = t;
   }
 }
 
@@ -428,9 +441,9 @@ int cnhip_conv2d_backward(const float* X, const float* W, const float* dY, float
     int status = cnhip::check_launch(who);
     if (rec) (void)hipEventRecord(rec->stop, st);
     if (status == CNHIP_OK) {
-      hipLaunchKernelGGL(cnhip::conv_wgrad_reduce_kernel,
-                         dim3(cnhip::elementwise_grid(OC * Ng, 256)), dim3(256), 0, st, a.partial,
-                         (int)splits, OC, CT, a.has_bias, gW, gb);
+      hipLaunchKernelGGL(cnhip::conv_wgrad_reduce_kernel, dim3((unsigned)((OC * Ng + 63) / 64)),
+                         dim3(64 * cnhip::WGRAD_RW), 0, st, a.partial, (int)splits, OC, CT,
+                         a.has_bias, gW, gb);
       status = cnhip::check_launch(who);
     }
     const int st2 = cnhip::check_hip(hipFreeAsync(ws, st), who);

@@ -7,32 +7,40 @@
 // matmul_grad_weight.cu:14-69, matmul_grad_input.cu:14-68) and the batched
 // products of the recurrent and attention layers.  The reference computes one
 // output per thread with atomicAdd accumulation.  Here a block of
-// WGM x WGN wave64s owns a (WGM*WM*32) x (WGN*WN*32) output tile; each wave
-// holds WM x WN accumulator blocks of one 32x32 MFMA (16 floats per lane
-// each); K advances 16 at a time through double-buffered LDS staged from
-// registers; no atomics are used.  When the output tiles alone cannot fill
-// the 256 CUs, K is split across blocks into a stream-ordered workspace and
-// the partials are summed in a fixed order, so results are deterministic.
+// WGM x WGN wave64s owns a (WGM*WM*32) x (WGN*WN*32) output tile (up to
+// 256 x 128, each wave 128 x 64 as 4 x 2 MFMA blocks); K advances 16 at a
+// time through double-buffered, k-contiguous LDS tiles (mfma_kpack.hpp); no
+// atomics are used.  When the output tiles alone cannot fill the 256 CUs, K
+// is split across blocks into a stream-ordered workspace and the partials
+// are summed in a fixed order, so results are deterministic.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
 #include <vector>
 
 #include "common.hpp"
-#include "mfma_core.hpp"
+#include "mfma_kpack.hpp"
 
 namespace cnhip {
 namespace {
 
-using mfma::BK;
-using mfma::f32x16;
-using mfma::f32x4;
-using mfma::TileCfg;
+using kp::BK;
+using kp::f32x16;
+using kp::f32x4;
 
-using CfgL = TileCfg<2, 2, 2, 2>;   // 128 x 128, 4 waves, 64x64 per wave
-using CfgSN = TileCfg<4, 1, 1, 1>;  // 128 x 32 : N <= 32
-using CfgSM = TileCfg<1, 4, 1, 1>;  // 32 x 128 : M <= 32
-using CfgS = TileCfg<2, 2, 1, 1>;   // 64 x 64  : small problems
+// Tile shapes (measured on MI355X: the 8-wave blocks keep two waves per SIMD
+// with 64x64 wave tiles and beat 4-wave blocks with larger wave tiles).
+using CfgXL = kp::Cfg<4, 2, 2, 2>;  // 256 x 128, 8 waves of 64x64
+using CfgXN = kp::Cfg<2, 4, 2, 2>;  // 128 x 256, 8 waves of 64x64
+using CfgM = kp::Cfg<4, 2, 1, 2>;   // 128 x 128, 8 waves of 32x64
+using CfgSN = kp::Cfg<4, 1, 1, 1>;  // 128 x 32 : N <= 32
+using CfgSM = kp::Cfg<1, 4, 1, 1>;  // 32 x 128 : M <= 32
+using CfgS = kp::Cfg<2, 2, 1, 1>;   // 64 x 64  : small problems
+
+// Blocks of 512 threads run one per CU (their 64x64 wave tiles need ~150
+// VGPRs); 256-thread blocks are sized for two.
+template <class C>
+constexpr int min_blocks() { return C::NT >= 512 ? 1 : 2; }
 
 struct GemmArgs {
   int64_t M, N, K;
@@ -50,44 +58,6 @@ struct GemmArgs {
   int64_t k_per_split;   // multiple of BK
   float* partial;        // split-K workspace [batch][splits][M*N]; null = direct
   int splits;
-};
-
-// Stages one strided operand tile (R rows of the outer dim x 16 of K) into
-// registers.  KCONTIG: X(r,k) = X[k + ld*r]  (else X[r + ld*k]).
-template <bool KCONTIG, int R, int NT>
-struct TileLoader {
-  using Slots = mfma::TileSlots<KCONTIG, R, NT>;
-  static constexpr int PER_THREAD = Slots::PER_THREAD;
-
-  __device__ __forceinline__ static void load(const float* __restrict__ X, int64_t ld, int64_t r0,
-                                              int64_t k0, int64_t Rtot, int64_t K, bool fast,
-                                              f32x4 (&regs)[PER_THREAD]) {
-#pragma unroll
-    for (int p = 0; p < PER_THREAD; ++p) {
-      int rr, kk;
-      if (!Slots::slot(p, rr, kk)) break;
-      const int64_t r = r0 + rr, k = k0 + kk;
-      if (fast) {
-        const float* src = KCONTIG ? (X + k + ld * r) : (X + r + ld * k);
-        regs[p] = *reinterpret_cast<const f32x4*>(src);
-      } else {
-        f32x4 v;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int64_t rj = KCONTIG ? r : r + j;
-          const int64_t kj = KCONTIG ? k + j : k;
-          float x = 0.f;
-          if (rj < Rtot && kj < K) x = KCONTIG ? X[kj + ld * rj] : X[rj + ld * kj];
-          v[j] = x;
-        }
-        regs[p] = v;
-      }
-    }
-  }
-  __device__ __forceinline__ static void store(float* __restrict__ lds,
-                                               const f32x4 (&regs)[PER_THREAD]) {
-    Slots::store(lds, regs);
-  }
 };
 
 __device__ __forceinline__ float epilogue_value(const GemmArgs& g, const float* C, float acc,
@@ -119,13 +89,46 @@ __device__ __forceinline__ void tile_of_block(int nbm, int nbn, int& tm, int& tn
   tn = in_group / gsz;
 }
 
-template <bool TA, bool TB, class Cfg>
-__global__ void __launch_bounds__(Cfg::NT, 2) gemm_f32_kernel(GemmArgs g) {
-  constexpr int BM = Cfg::BM, BN = Cfg::BN, NT = Cfg::NT;
-  using LA = TileLoader<TA, BM, NT>;
-  using LB = TileLoader<!TB, BN, NT>;
-  __shared__ float lds_a[2][BK * Cfg::LDA];
-  __shared__ float lds_b[2][BK * Cfg::LDB];
+// K loop of one block over [k_begin, k_end).  FAST: every tile load is in
+// range and 16-byte aligned (no per-element checks).
+template <bool FAST, bool TA, bool TB, class C>
+__device__ __forceinline__ void gemm_mainloop(const GemmArgs& g, const float* __restrict__ A,
+                                              const float* __restrict__ B, int64_t m0, int64_t n0,
+                                              int64_t k_begin, int64_t k_end, float* lds,
+                                              f32x16 (&acc)[C::WM][C::WN]) {
+  using OA = kp::Operand<TA, C::BM, C::NT>;   // A(m,k): k-contiguous when A is transposed
+  using OB = kp::Operand<!TB, C::BN, C::NT>;  // B(k,n): k-contiguous unless B is transposed
+  const int ntiles = k_end > k_begin ? (int)((k_end - k_begin + BK - 1) / BK) : 0;
+  f32x4 ra[OA::REGS], rb[OB::REGS];
+  if (ntiles > 0) {
+    OA::template load<FAST>(A, g.lda, m0, k_begin, g.M, k_end, ra);
+    OB::template load<FAST>(B, g.ldb, n0, k_begin, g.N, k_end, rb);
+    OA::store(lds, ra);
+    OB::store(lds + C::BM * kp::LDK, rb);
+  }
+  __syncthreads();
+  for (int kt = 0; kt < ntiles; ++kt) {
+    float* cur = lds + (kt & 1) * C::LDS_FLOATS;
+    float* nxt = lds + ((kt & 1) ^ 1) * C::LDS_FLOATS;
+    const bool has_next = kt + 1 < ntiles;
+    if (has_next) {
+      const int64_t kn = k_begin + (int64_t)(kt + 1) * BK;
+      OA::template load<FAST>(A, g.lda, m0, kn, g.M, k_end, ra);
+      OB::template load<FAST>(B, g.ldb, n0, kn, g.N, k_end, rb);
+    }
+    kp::mfma_ktile<C>(cur, cur + C::BM * kp::LDK, acc);
+    if (has_next) {
+      OA::store(nxt, ra);
+      OB::store(nxt + C::BM * kp::LDK, rb);
+    }
+    __syncthreads();
+  }
+}
+
+template <bool TA, bool TB, class C>
+__global__ void __launch_bounds__(C::NT, min_blocks<C>()) gemm_f32_kernel(GemmArgs g) {
+  constexpr int BM = C::BM, BN = C::BN;
+  __shared__ __align__(16) float lds[2 * C::LDS_FLOATS];
 
   const int nbm = (int)((g.M + BM - 1) / BM);
   const int nbn = (int)((g.N + BN - 1) / BN);
@@ -138,59 +141,39 @@ __global__ void __launch_bounds__(Cfg::NT, 2) gemm_f32_kernel(GemmArgs g) {
 
   const int64_t k_begin = (int64_t)blockIdx.z * g.k_per_split;
   const int64_t k_end = min(g.K, k_begin + g.k_per_split);
-  const int ntiles = k_end > k_begin ? (int)((k_end - k_begin + BK - 1) / BK) : 0;
   const bool full_mn = (m0 + BM <= g.M) && (n0 + BN <= g.N);
+  const bool fast = g.vec_ok && full_mn && ((k_end - k_begin) % BK == 0);
 
-  f32x16 acc[Cfg::WM][Cfg::WN];
-  mfma::zero_acc<Cfg>(acc);
+  f32x16 acc[C::WM][C::WN];
+  kp::zero_acc<C>(acc);
+  if (fast) gemm_mainloop<true, TA, TB, C>(g, A, B, m0, n0, k_begin, k_end, lds, acc);
+  else gemm_mainloop<false, TA, TB, C>(g, A, B, m0, n0, k_begin, k_end, lds, acc);
 
-  f32x4 ra[LA::PER_THREAD], rb[LB::PER_THREAD];
-  if (ntiles > 0) {
-    const bool fast = g.vec_ok && full_mn && (k_begin + BK <= k_end);
-    LA::load(A, g.lda, m0, k_begin, g.M, k_end, fast, ra);
-    LB::load(B, g.ldb, n0, k_begin, g.N, k_end, fast, rb);
-    LA::store(lds_a[0], ra);
-    LB::store(lds_b[0], rb);
-  }
-  __syncthreads();
-
-  for (int kt = 0; kt < ntiles; ++kt) {
-    const int cur = kt & 1;
-    const bool has_next = kt + 1 < ntiles;
-    if (has_next) {
-      const int64_t kn = k_begin + (int64_t)(kt + 1) * BK;
-      const bool fast = g.vec_ok && full_mn && (kn + BK <= k_end);
-      LA::load(A, g.lda, m0, kn, g.M, k_end, fast, ra);
-      LB::load(B, g.ldb, n0, kn, g.N, k_end, fast, rb);
-    }
-    mfma::mfma_ktile<Cfg>(lds_a[cur], lds_b[cur], acc);
-    if (has_next) {
-      LA::store(lds_a[cur ^ 1], ra);
-      LB::store(lds_b[cur ^ 1], rb);
-    }
-    __syncthreads();
-  }
-
-  float* C = g.C + batch * g.stride_c;
+  float* Cp = g.C + batch * g.stride_c;
   float* P = g.partial ? g.partial + (batch * g.splits + blockIdx.z) * g.M * g.N : nullptr;
-  mfma::for_each_acc_run<Cfg>(acc, [&](int ml, int nl, const f32x4& v) {
+  const bool p_vec = (g.M & 3) == 0;
+  kp::for_each_acc_run<C>(acc, [&](int ml, int nl, const f32x4& v) {
     const int64_t m = m0 + ml, n = n0 + nl;
     if (n >= g.N) return;
     if (P) {
+      if (p_vec && m + 3 < g.M) {
+        *reinterpret_cast<f32x4*>(P + m + g.M * n) = v;
+      } else {
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (m + e < g.M) P[(m + e) + g.M * n] = v[e];
+        for (int e = 0; e < 4; ++e)
+          if (m + e < g.M) P[(m + e) + g.M * n] = v[e];
+      }
       return;
     }
     if (g.c_vec_ok && m + 3 < g.M) {
       f32x4 o;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = epilogue_value(g, C, v[e], m + e, n);
-      *reinterpret_cast<f32x4*>(C + m + g.ldc * n) = o;
+      for (int e = 0; e < 4; ++e) o[e] = epilogue_value(g, Cp, v[e], m + e, n);
+      *reinterpret_cast<f32x4*>(Cp + m + g.ldc * n) = o;
     } else {
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        if (m + e < g.M) C[(m + e) + g.ldc * n] = epilogue_value(g, C, v[e], m + e, n);
+        if (m + e < g.M) Cp[(m + e) + g.ldc * n] = epilogue_value(g, Cp, v[e], m + e, n);
     }
   });
 }
@@ -256,7 +239,7 @@ TimingRec* timing_slot(double flops) {
 
 namespace {
 
-enum class Shape { L, SN, SM, S };
+enum class Shape { XL, XN, M, SN, SM, S };
 
 template <class Cfg>
 int64_t tiles_of(int64_t M, int64_t N) {
@@ -285,15 +268,26 @@ int gemm_f32_batched(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, 
   }
   CNHIP_REQUIRE(batches <= 65535, "%s: batch count %lld exceeds 65535", who, (long long)batches);
 
-  // Tile shape: skinny shapes waste no MFMA work on padding; small problems
-  // get 64x64 tiles so that more blocks exist.
-  Shape shape = Shape::L;
+  // Tile shape: skinny shapes waste no MFMA work on padding.  Large outputs
+  // take a 256-long tile side on the operand that is k-contiguous in memory
+  // (its loads need no register transpose); medium ones take 128 x 128 with
+  // split-K; small problems get 64x64 tiles so that more blocks exist.
+  Shape shape;
   if (N <= 32) shape = Shape::SN;
   else if (M <= 32) shape = Shape::SM;
-  else if (tiles_of<CfgL>(M, N) * batches < 128) shape = Shape::S;
+  else {
+    const bool a_kc = trans_a != 0, b_kc = trans_b == 0;
+    const bool wide = (a_kc != b_kc) ? b_kc : (N > M);
+    const int64_t tx = (wide ? tiles_of<CfgXN>(M, N) : tiles_of<CfgXL>(M, N)) * batches;
+    if (tx >= 256) shape = wide ? Shape::XN : Shape::XL;
+    else if (tiles_of<CfgM>(M, N) * batches >= 64 || K >= 512) shape = Shape::M;
+    else shape = Shape::S;
+  }
   int64_t tiles = 0;
   switch (shape) {
-    case Shape::L: tiles = tiles_of<CfgL>(M, N); break;
+    case Shape::XL: tiles = tiles_of<CfgXL>(M, N); break;
+    case Shape::XN: tiles = tiles_of<CfgXN>(M, N); break;
+    case Shape::M: tiles = tiles_of<CfgM>(M, N); break;
     case Shape::SN: tiles = tiles_of<CfgSN>(M, N); break;
     case Shape::SM: tiles = tiles_of<CfgSM>(M, N); break;
     case Shape::S: tiles = tiles_of<CfgS>(M, N); break;
@@ -311,13 +305,14 @@ int gemm_f32_batched(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, 
   g.c_vec_ok = (ldc % 4 == 0) && (stride_c % 4 == 0) && aligned16(C);
   g.partial = nullptr;
 
-  // Split K until about 512 blocks (2 per CU) exist, keeping >= 4 K-tiles
-  // per split.
+  // Split K until about 512 blocks exist (two per CU for the 256-thread and
+  // 128 x 128 shapes; the 256-long tiles are only chosen with >= 256 blocks),
+  // keeping >= 8 K-tiles per split.
   const int64_t blocks = tiles * batches;
   int splits = 1;
-  if (blocks < 512 && K >= 8 * BK) {
+  if (blocks < 512 && shape != Shape::XL && shape != Shape::XN && K >= 16 * BK) {
     const int64_t want = (512 + blocks - 1) / blocks;
-    const int64_t max_by_k = K / (4 * BK);
+    const int64_t max_by_k = K / (8 * BK);
     splits = (int)std::max<int64_t>(1, std::min<int64_t>({want, max_by_k, 64}));
   }
   int64_t kps = (K + splits - 1) / splits;
@@ -337,7 +332,9 @@ int gemm_f32_batched(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, 
   TimingRec* rec = timing_slot(2.0 * (double)M * (double)N * (double)K * (double)batches);
   if (rec) (void)hipEventRecord(rec->start, st);
   switch (shape) {
-    case Shape::L: launch_t<CfgL>(trans_a, trans_b, g, batches, st); break;
+    case Shape::XL: launch_t<CfgXL>(trans_a, trans_b, g, batches, st); break;
+    case Shape::XN: launch_t<CfgXN>(trans_a, trans_b, g, batches, st); break;
+    case Shape::M: launch_t<CfgM>(trans_a, trans_b, g, batches, st); break;
     case Shape::SN: launch_t<CfgSN>(trans_a, trans_b, g, batches, st); break;
     case Shape::SM: launch_t<CfgSM>(trans_a, trans_b, g, batches, st); break;
     case Shape::S: launch_t<CfgS>(trans_a, trans_b, g, batches, st); break;

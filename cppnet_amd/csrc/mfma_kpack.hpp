@@ -1,0 +1,189 @@
+// fp32 MFMA tile engine with k-contiguous LDS operand tiles
+// (v_mfma_f32_32x32x2f32, wave64), used by the GEMM kernel.
+//
+// A block of WGM x WGN wavefronts owns a BM x BN output tile, BM = WGM*WM*32,
+// BN = WGN*WN*32; each wave holds WM x WN accumulator blocks of 32x32 (16
+// floats per lane each).  K advances BK = 16 at a time.  Both operand tiles
+// live in LDS as [rows][k] with k contiguous (row stride LDK = 20 floats, so
+// the 16-byte fragment reads of 8 consecutive lanes hit 8 distinct 4-bank
+// groups).
+//
+// Which k a lane feeds to which MFMA step is free, as long as A and B agree:
+// in step e of chunk c (c = 0, 1; e = 0..3) lane half h = lane/32 supplies
+// k = 8h + 4c + e.  A lane therefore needs 8 consecutive k of one row per
+// operand block and fetches them with two ds_read_b128 -- 12 LDS reads feed
+// the 64 MFMAs of a 4 x 2 wave tile per k-tile.
+//
+// Global -> LDS staging goes through registers (double-buffered LDS, one
+// barrier per k-tile).  An operand whose rows are k-contiguous in memory is
+// moved as float4 along k; one whose rows are contiguous along the output
+// dimension is moved as 4 x 4 micro-tiles (four float4 loads along the rows,
+// transposed in registers, four float4 LDS writes along k).  Threads are
+// assigned k-chunk fastest, which makes both kinds of LDS write conflict-free
+// (rows 4 apart differ by 80 floats = 16 banks; the 4 chunks of a row cover
+// the other offsets).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace cnhip {
+namespace kp {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int BK = 16;
+constexpr int LDK = BK + 4;
+
+template <int WGM_, int WGN_, int WM_, int WN_>
+struct Cfg {
+  static constexpr int WGM = WGM_, WGN = WGN_, WM = WM_, WN = WN_;
+  static constexpr int BM = WGM * WM * 32;
+  static constexpr int BN = WGN * WN * 32;
+  static constexpr int NT = WGM * WGN * 64;
+  static constexpr int LDS_FLOATS = (BM + BN) * LDK;  // one buffer: A tile then B tile
+};
+
+// An R x BK operand tile.  KC: X(r, k) = X[k + ld*r] (k contiguous), else
+// X(r, k) = X[r + ld*k] (r contiguous).
+template <bool KC, int R, int NT>
+struct Operand {
+  static_assert(R % 4 == 0, "operand rows must be a multiple of 4");
+  // KC: one unit = a float4 along k (R*4 units); else a 4 x 4 micro-tile (R units)
+  static constexpr int UNITS = KC ? R * 4 : R;
+  static constexpr int PER = (UNITS + NT - 1) / NT;
+  static constexpr int REGS = KC ? PER : 4 * PER;
+
+  __device__ __forceinline__ static bool origin(int p, int& r, int& k) {
+    const int u = threadIdx.x + NT * p;
+    if (UNITS % NT != 0 && u >= UNITS) return false;
+    // k-chunk fastest in both modes: the four lanes of one row group write
+    // four different 16-byte chunks, so 8 consecutive lanes' LDS writes land
+    // in 8 distinct bank groups.
+    r = (u >> 2) * (KC ? 1 : 4);
+    k = (u & 3) * 4;
+    return true;
+  }
+
+  // FAST: the whole tile is in range and 16-byte aligned.  Otherwise every
+  // element is bounds-checked (rows < Rtot, k < Kend) and zero-filled.
+  template <bool FAST>
+  __device__ __forceinline__ static void load(const float* __restrict__ X, int64_t ld, int64_t r0,
+                                              int64_t k0, int64_t Rtot, int64_t Kend,
+                                              f32x4 (&v)[REGS]) {
+#pragma unroll
+    for (int p = 0; p < PER; ++p) {
+      int r, k;
+      if (!origin(p, r, k)) break;
+      const int64_t gr = r0 + r, gk = k0 + k;
+      if (KC) {
+        if (FAST) {
+          v[p] = *reinterpret_cast<const f32x4*>(X + gk + ld * gr);
+        } else {
+          f32x4 t;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) t[j] = (gr < Rtot && gk + j < Kend) ? X[gk + j + ld * gr] : 0.f;
+          v[p] = t;
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (FAST) {
+            v[4 * p + j] = *reinterpret_cast<const f32x4*>(X + gr + ld * (gk + j));
+          } else {
+            f32x4 t;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              t[e] = (gr + e < Rtot && gk + j < Kend) ? X[gr + e + ld * (gk + j)] : 0.f;
+            v[4 * p + j] = t;
+          }
+        }
+      }
+    }
+  }
+
+  __device__ __forceinline__ static void store(float* __restrict__ lds, const f32x4 (&v)[REGS]) {
+#pragma unroll
+    for (int p = 0; p < PER; ++p) {
+      int r, k;
+      if (!origin(p, r, k)) break;
+      if (KC) {
+        *reinterpret_cast<f32x4*>(lds + r * LDK + k) = v[p];
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          f32x4 w;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) w[j] = v[4 * p + j][e];
+          *reinterpret_cast<f32x4*>(lds + (r + e) * LDK + k) = w;
+        }
+      }
+    }
+  }
+};
+
+template <class C>
+__device__ __forceinline__ void zero_acc(f32x16 (&acc)[C::WM][C::WN]) {
+#pragma unroll
+  for (int i = 0; i < C::WM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::WN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+}
+
+// One BK-deep step of the block's MFMA work from the LDS tiles la ([BM][LDK])
+// and lb ([BN][LDK]).
+template <class C>
+__device__ __forceinline__ void mfma_ktile(const float* __restrict__ la,
+                                           const float* __restrict__ lb,
+                                           f32x16 (&acc)[C::WM][C::WN]) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave % C::WGM, wn = wave / C::WGM;
+  const int h = lane >> 5, r = lane & 31;
+  const float* pa = la + (wm * (C::WM * 32) + r) * LDK + 8 * h;
+  const float* pb = lb + (wn * (C::WN * 32) + r) * LDK + 8 * h;
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    f32x4 a[C::WM], b[C::WN];
+#pragma unroll
+    for (int i = 0; i < C::WM; ++i) a[i] = *reinterpret_cast<const f32x4*>(pa + i * 32 * LDK + 4 * c);
+#pragma unroll
+    for (int j = 0; j < C::WN; ++j) b[j] = *reinterpret_cast<const f32x4*>(pb + j * 32 * LDK + 4 * c);
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+      for (int i = 0; i < C::WM; ++i)
+#pragma unroll
+        for (int j = 0; j < C::WN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][e], b[j][e], acc[i][j], 0, 0, 0);
+  }
+}
+
+// Visits the accumulators: f(m_local, n_local, 4 values at rows m..m+3).
+// Accumulator layout of v_mfma_f32_32x32x2f32: lane holds column n = lane%32
+// and rows 8*(r/4) + 4*(lane/32) + r%4, r = 0..15.
+template <class C, class F>
+__device__ __forceinline__ void for_each_acc_run(const f32x16 (&acc)[C::WM][C::WN], F&& f) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave % C::WGM, wn = wave / C::WGM;
+#pragma unroll
+  for (int i = 0; i < C::WM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::WN; ++j) {
+      const int n = wn * (C::WN * 32) + j * 32 + (lane & 31);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int m = wm * (C::WM * 32) + i * 32 + 8 * q + 4 * (lane >> 5);
+        f32x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = acc[i][j][4 * q + e];
+        f(m, n, v);
+      }
+    }
+}
+
+}  // namespace kp
+}  // namespace cnhip

@@ -57,7 +57,8 @@ def _gemm_case(oracle, ta, tb, M, N, K, beta, with_bias, relu, pad, seed):
 
 @pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1), (1, 1)])
 @pytest.mark.parametrize("M,N,K", [(128, 128, 16), (256, 384, 512), (130, 70, 33), (1, 1, 1),
-                                   (5, 300, 7), (300, 10, 700), (64, 3, 2000), (512, 512, 10)])
+                                   (5, 300, 7), (300, 10, 700), (64, 3, 2000), (512, 512, 10),
+                                   (1024, 512, 2048), (512, 1024, 2048), (1000, 520, 2050)])
 def test_gemm_vs_oracle(gpu, oracle, ta, tb, M, N, K):
     print(f"[gemm] ta={ta} tb={tb} M={M} N={N} K={K}", flush=True)
     _gemm_case(oracle, ta, tb, M, N, K, beta=0.0, with_bias=False, relu=False, pad=0, seed=M + N + K)
