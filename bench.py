@@ -101,6 +101,12 @@ def workload(config: int, batch: int | None = None):
 
 CPU_BATCH = {1: 512, 2: 512, 3: 32, 4: 16, 5: 4}
 
+# HBM bytes per launch of the dominant kernel class, from the two rocprofv3
+# PMC runs (FETCH_SIZE, WRITE_SIZE) scaled by a reference kernel of known
+# traffic; the runs, factors and per-GEMM table are in
+# profiles/gemm_f32_config2_traffic.md.  Configs not yet measured report null.
+PMC_TRAFFIC_BYTES = {2: 370.6e6}
+
 
 def cpu_baseline(config: int, seconds_budget: float = 20.0):
     """Times the oracle-composed model (oracle/ over oracle/liboracle.so) on
@@ -224,7 +230,8 @@ def main() -> int:
         "roofline": {"bound": "mfma", "kernel": kernels,
                      "achieved": round(achieved, 2), "peak": PEAK_FP32_MFMA_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4),
-                     "traffic": None,
+                     "traffic": PMC_TRAFFIC_BYTES.get(args.config),
+                     "traffic_unit": "bytes per launch (rocprofv3 PMC, see profiles/)",
                      "launches_per_step": launches.value // prof_steps,
                      "avg_launch_us": round(per_launch_us, 2),
                      "flops_per_launch": flops_per_launch,

@@ -24,7 +24,6 @@
 namespace cnhip {
 namespace {
 
-using kp::BK;
 using kp::f32x16;
 using kp::f32x4;
 
@@ -36,6 +35,9 @@ using CfgM = kp::Cfg<4, 2, 1, 2>;   // 128 x 128, 8 waves of 32x64
 using CfgSN = kp::Cfg<4, 1, 1, 1>;  // 128 x 32 : N <= 32
 using CfgSM = kp::Cfg<1, 4, 1, 1>;  // 32 x 128 : M <= 32
 using CfgS = kp::Cfg<2, 2, 1, 1>;   // 64 x 64  : small problems
+
+// Split-K granularity: a multiple of every tile shape's BK.
+constexpr int64_t KQ = 32;
 
 // Blocks of 512 threads run one per CU (their 64x64 wave tiles need ~150
 // VGPRs); 256-thread blocks are sized for two.
@@ -55,7 +57,7 @@ struct GemmArgs {
   int epilogue;
   int vec_ok;            // every ld and stride % 4 == 0 and A, B 16-byte aligned
   int c_vec_ok;          // ldc, stride_c % 4 == 0 and C 16-byte aligned
-  int64_t k_per_split;   // multiple of BK
+  int64_t k_per_split;   // multiple of KQ (hence of every tile's BK)
   float* partial;        // split-K workspace [batch][splits][M*N]; null = direct
   int splits;
 };
@@ -96,15 +98,16 @@ __device__ __forceinline__ void gemm_mainloop(const GemmArgs& g, const float* __
                                               const float* __restrict__ B, int64_t m0, int64_t n0,
                                               int64_t k_begin, int64_t k_end, float* lds,
                                               f32x16 (&acc)[C::WM][C::WN]) {
-  using OA = kp::Operand<TA, C::BM, C::NT>;   // A(m,k): k-contiguous when A is transposed
-  using OB = kp::Operand<!TB, C::BN, C::NT>;  // B(k,n): k-contiguous unless B is transposed
+  constexpr int BK = C::BK;
+  using OA = kp::Operand<TA, C::BM, C::NT, BK>;   // A(m,k): k-contiguous when A is transposed
+  using OB = kp::Operand<!TB, C::BN, C::NT, BK>;  // B(k,n): k-contiguous unless B is transposed
   const int ntiles = k_end > k_begin ? (int)((k_end - k_begin + BK - 1) / BK) : 0;
   f32x4 ra[OA::REGS], rb[OB::REGS];
   if (ntiles > 0) {
     OA::template load<FAST>(A, g.lda, m0, k_begin, g.M, k_end, ra);
     OB::template load<FAST>(B, g.ldb, n0, k_begin, g.N, k_end, rb);
     OA::store(lds, ra);
-    OB::store(lds + C::BM * kp::LDK, rb);
+    OB::store(lds + C::BM * C::LDK, rb);
   }
   __syncthreads();
   for (int kt = 0; kt < ntiles; ++kt) {
@@ -116,10 +119,10 @@ __device__ __forceinline__ void gemm_mainloop(const GemmArgs& g, const float* __
       OA::template load<FAST>(A, g.lda, m0, kn, g.M, k_end, ra);
       OB::template load<FAST>(B, g.ldb, n0, kn, g.N, k_end, rb);
     }
-    kp::mfma_ktile<C>(cur, cur + C::BM * kp::LDK, acc);
+    kp::mfma_ktile<C>(cur, cur + C::BM * C::LDK, acc);
     if (has_next) {
       OA::store(nxt, ra);
-      OB::store(nxt + C::BM * kp::LDK, rb);
+      OB::store(nxt + C::BM * C::LDK, rb);
     }
     __syncthreads();
   }
@@ -142,7 +145,7 @@ __global__ void __launch_bounds__(C::NT, min_blocks<C>()) gemm_f32_kernel(GemmAr
   const int64_t k_begin = (int64_t)blockIdx.z * g.k_per_split;
   const int64_t k_end = min(g.K, k_begin + g.k_per_split);
   const bool full_mn = (m0 + BM <= g.M) && (n0 + BN <= g.N);
-  const bool fast = g.vec_ok && full_mn && ((k_end - k_begin) % BK == 0);
+  const bool fast = g.vec_ok && full_mn && ((k_end - k_begin) % C::BK == 0);
 
   f32x16 acc[C::WM][C::WN];
   kp::zero_acc<C>(acc);
@@ -269,15 +272,16 @@ int gemm_f32_batched(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, 
   CNHIP_REQUIRE(batches <= 65535, "%s: batch count %lld exceeds 65535", who, (long long)batches);
 
   // Tile shape: skinny shapes waste no MFMA work on padding.  Large outputs
-  // take a 256-long tile side on the operand that is k-contiguous in memory
-  // (its loads need no register transpose); medium ones take 128 x 128 with
+  // take 128 x 256, or 256 x 128 when only A is k-contiguous in memory (the
+  // long tile side goes to the operand whose loads need no register
+  // transpose); medium ones take 128 x 128 with
   // split-K; small problems get 64x64 tiles so that more blocks exist.
   Shape shape;
   if (N <= 32) shape = Shape::SN;
   else if (M <= 32) shape = Shape::SM;
   else {
     const bool a_kc = trans_a != 0, b_kc = trans_b == 0;
-    const bool wide = (a_kc != b_kc) ? b_kc : (N > M);
+    const bool wide = !(a_kc && !b_kc);  // 128 x 256 measured the most even across layouts
     const int64_t tx = (wide ? tiles_of<CfgXN>(M, N) : tiles_of<CfgXL>(M, N)) * batches;
     if (tx >= 256) shape = wide ? Shape::XN : Shape::XL;
     else if (tiles_of<CfgM>(M, N) * batches >= 64 || K >= 512) shape = Shape::M;
@@ -310,14 +314,14 @@ int gemm_f32_batched(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, 
   // keeping >= 8 K-tiles per split.
   const int64_t blocks = tiles * batches;
   int splits = 1;
-  if (blocks < 512 && shape != Shape::XL && shape != Shape::XN && K >= 16 * BK) {
+  if (blocks < 512 && shape != Shape::XL && shape != Shape::XN && K >= 8 * KQ) {
     const int64_t want = (512 + blocks - 1) / blocks;
-    const int64_t max_by_k = K / (8 * BK);
+    const int64_t max_by_k = K / (4 * KQ);
     splits = (int)std::max<int64_t>(1, std::min<int64_t>({want, max_by_k, 64}));
   }
   int64_t kps = (K + splits - 1) / splits;
-  kps = ((kps + BK - 1) / BK) * BK;
-  if (kps == 0) kps = BK;
+  kps = ((kps + KQ - 1) / KQ) * KQ;
+  if (kps == 0) kps = KQ;
   splits = K > 0 ? (int)((K + kps - 1) / kps) : 1;
   g.k_per_split = kps;
   g.splits = splits;

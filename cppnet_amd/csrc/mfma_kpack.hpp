@@ -3,16 +3,16 @@
 //
 // A block of WGM x WGN wavefronts owns a BM x BN output tile, BM = WGM*WM*32,
 // BN = WGN*WN*32; each wave holds WM x WN accumulator blocks of 32x32 (16
-// floats per lane each).  K advances BK = 16 at a time.  Both operand tiles
-// live in LDS as [rows][k] with k contiguous (row stride LDK = 20 floats, so
-// the 16-byte fragment reads of 8 consecutive lanes hit 8 distinct 4-bank
-// groups).
+// floats per lane each).  K advances BK (16 or 32) at a time.  Both operand
+// tiles live in LDS as [rows][k] with k contiguous (row stride LDK = BK + 4
+// floats, so the 16-byte fragment reads of 8 consecutive lanes hit 8
+// distinct 4-bank groups).
 //
 // Which k a lane feeds to which MFMA step is free, as long as A and B agree:
-// in step e of chunk c (c = 0, 1; e = 0..3) lane half h = lane/32 supplies
-// k = 8h + 4c + e.  A lane therefore needs 8 consecutive k of one row per
-// operand block and fetches them with two ds_read_b128 -- 12 LDS reads feed
-// the 64 MFMAs of a 4 x 2 wave tile per k-tile.
+// in step t (t = 0 .. BK/2-1) lane half h = lane/32 supplies k = h*BK/2 + t.
+// A lane therefore needs BK/2 consecutive k of one row per operand block and
+// fetches them with ds_read_b128s -- at BK = 16, 8 LDS reads feed the 32
+// MFMAs of a 2 x 2 wave tile per k-tile.
 //
 // Global -> LDS staging goes through registers (double-buffered LDS, one
 // barrier per k-tile).  An operand whose rows are k-contiguous in memory is
@@ -34,36 +34,38 @@ namespace kp {
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int BK = 16;
-constexpr int LDK = BK + 4;
-
-template <int WGM_, int WGN_, int WM_, int WN_>
+template <int WGM_, int WGN_, int WM_, int WN_, int BK_ = 16>
 struct Cfg {
   static constexpr int WGM = WGM_, WGN = WGN_, WM = WM_, WN = WN_;
+  static constexpr int BK = BK_;
+  static constexpr int LDK = BK + 4;
   static constexpr int BM = WGM * WM * 32;
   static constexpr int BN = WGN * WN * 32;
   static constexpr int NT = WGM * WGN * 64;
   static constexpr int LDS_FLOATS = (BM + BN) * LDK;  // one buffer: A tile then B tile
+  static_assert(BK == 16 || BK == 32, "BK must be 16 or 32");
 };
 
 // An R x BK operand tile.  KC: X(r, k) = X[k + ld*r] (k contiguous), else
 // X(r, k) = X[r + ld*k] (r contiguous).
-template <bool KC, int R, int NT>
+template <bool KC, int R, int NT, int BK>
 struct Operand {
   static_assert(R % 4 == 0, "operand rows must be a multiple of 4");
-  // KC: one unit = a float4 along k (R*4 units); else a 4 x 4 micro-tile (R units)
-  static constexpr int UNITS = KC ? R * 4 : R;
+  static constexpr int LDK = BK + 4;
+  static constexpr int CH = BK / 4;  // 16-byte chunks per row
+  // KC: one unit = a float4 along k (R*CH units); else a 4 x 4 micro-tile (R*CH/4 units)
+  static constexpr int UNITS = KC ? R * CH : R * CH / 4;
   static constexpr int PER = (UNITS + NT - 1) / NT;
   static constexpr int REGS = KC ? PER : 4 * PER;
 
   __device__ __forceinline__ static bool origin(int p, int& r, int& k) {
     const int u = threadIdx.x + NT * p;
     if (UNITS % NT != 0 && u >= UNITS) return false;
-    // k-chunk fastest in both modes: the four lanes of one row group write
-    // four different 16-byte chunks, so 8 consecutive lanes' LDS writes land
-    // in 8 distinct bank groups.
-    r = (u >> 2) * (KC ? 1 : 4);
-    k = (u & 3) * 4;
+    // k-chunk fastest in both modes: the lanes of one row group write
+    // different 16-byte chunks, so 8 consecutive lanes' LDS writes land in 8
+    // distinct bank groups.
+    r = (u / CH) * (KC ? 1 : 4);
+    k = (u % CH) * 4;
     return true;
   }
 
@@ -135,7 +137,7 @@ __device__ __forceinline__ void zero_acc(f32x16 (&acc)[C::WM][C::WN]) {
 }
 
 // One BK-deep step of the block's MFMA work from the LDS tiles la ([BM][LDK])
-// and lb ([BN][LDK]).
+// and lb ([BN][LDK]); chunk c, element e is step t = 4c + e.
 template <class C>
 __device__ __forceinline__ void mfma_ktile(const float* __restrict__ la,
                                            const float* __restrict__ lb,
@@ -143,10 +145,11 @@ __device__ __forceinline__ void mfma_ktile(const float* __restrict__ la,
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave % C::WGM, wn = wave / C::WGM;
   const int h = lane >> 5, r = lane & 31;
-  const float* pa = la + (wm * (C::WM * 32) + r) * LDK + 8 * h;
-  const float* pb = lb + (wn * (C::WN * 32) + r) * LDK + 8 * h;
+  constexpr int LDK = C::LDK;
+  const float* pa = la + (wm * (C::WM * 32) + r) * LDK + (C::BK / 2) * h;
+  const float* pb = lb + (wn * (C::WN * 32) + r) * LDK + (C::BK / 2) * h;
 #pragma unroll
-  for (int c = 0; c < 2; ++c) {
+  for (int c = 0; c < C::BK / 8; ++c) {
     f32x4 a[C::WM], b[C::WN];
 #pragma unroll
     for (int i = 0; i < C::WM; ++i) a[i] = *reinterpret_cast<const f32x4*>(pa + i * 32 * LDK + 4 * c);
