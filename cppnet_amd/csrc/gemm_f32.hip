@@ -92,7 +92,10 @@ __device__ __forceinline__ void tile_of_block(int nbm, int nbn, int& tm, int& tn
 }
 
 // K loop of one block over [k_begin, k_end).  FAST: every tile load is in
-// range and 16-byte aligned (no per-element checks).
+// range and 16-byte aligned (no per-element checks).  Global loads run two
+// k-tiles ahead of the MFMAs through two register sets (the loop is unrolled
+// by two so the sets alternate statically), and LDS is double-buffered with
+// one barrier per k-tile: tile t is in LDS while t+1 and t+2 are in flight.
 template <bool FAST, bool TA, bool TB, class C>
 __device__ __forceinline__ void gemm_mainloop(const GemmArgs& g, const float* __restrict__ A,
                                               const float* __restrict__ B, int64_t m0, int64_t n0,
@@ -102,27 +105,39 @@ __device__ __forceinline__ void gemm_mainloop(const GemmArgs& g, const float* __
   using OA = kp::Operand<TA, C::BM, C::NT, BK>;   // A(m,k): k-contiguous when A is transposed
   using OB = kp::Operand<!TB, C::BN, C::NT, BK>;  // B(k,n): k-contiguous unless B is transposed
   const int ntiles = k_end > k_begin ? (int)((k_end - k_begin + BK - 1) / BK) : 0;
-  f32x4 ra[OA::REGS], rb[OB::REGS];
+  float* buf0 = lds;
+  float* buf1 = lds + C::LDS_FLOATS;
+  constexpr int BOFF = C::BM * C::LDK;
+  f32x4 ra0[OA::REGS], rb0[OB::REGS], ra1[OA::REGS], rb1[OB::REGS];
+  auto load = [&](int t, f32x4 (&ra)[OA::REGS], f32x4 (&rb)[OB::REGS]) {
+    const int64_t k0 = k_begin + (int64_t)t * BK;
+    OA::template load<FAST>(A, g.lda, m0, k0, g.M, k_end, ra);
+    OB::template load<FAST>(B, g.ldb, n0, k0, g.N, k_end, rb);
+  };
   if (ntiles > 0) {
-    OA::template load<FAST>(A, g.lda, m0, k_begin, g.M, k_end, ra);
-    OB::template load<FAST>(B, g.ldb, n0, k_begin, g.N, k_end, rb);
-    OA::store(lds, ra);
-    OB::store(lds + C::BM * C::LDK, rb);
+    load(0, ra0, rb0);
+    OA::store(buf0, ra0);
+    OB::store(buf0 + BOFF, rb0);
   }
+  if (ntiles > 1) load(1, ra0, rb0);
+  if (ntiles > 2) load(2, ra1, rb1);
   __syncthreads();
-  for (int kt = 0; kt < ntiles; ++kt) {
-    float* cur = lds + (kt & 1) * C::LDS_FLOATS;
-    float* nxt = lds + ((kt & 1) ^ 1) * C::LDS_FLOATS;
-    const bool has_next = kt + 1 < ntiles;
-    if (has_next) {
-      const int64_t kn = k_begin + (int64_t)(kt + 1) * BK;
-      OA::template load<FAST>(A, g.lda, m0, kn, g.M, k_end, ra);
-      OB::template load<FAST>(B, g.ldb, n0, kn, g.N, k_end, rb);
+  for (int kt = 0; kt < ntiles; kt += 2) {
+    // tile kt in buf0, kt+1 in set 0, kt+2 in set 1
+    kp::mfma_ktile<C>(buf0, buf0 + BOFF, acc);
+    if (kt + 1 < ntiles) {
+      OA::store(buf1, ra0);
+      OB::store(buf1 + BOFF, rb0);
+      if (kt + 3 < ntiles) load(kt + 3, ra0, rb0);
     }
-    kp::mfma_ktile<C>(cur, cur + C::BM * C::LDK, acc);
-    if (has_next) {
-      OA::store(nxt, ra);
-      OB::store(nxt + C::BM * C::LDK, rb);
+    __syncthreads();
+    if (kt + 1 >= ntiles) break;
+    // tile kt+1 in buf1, kt+2 in set 1, kt+3 in set 0
+    kp::mfma_ktile<C>(buf1, buf1 + BOFF, acc);
+    if (kt + 2 < ntiles) {
+      OA::store(buf0, ra1);
+      OB::store(buf0 + BOFF, rb1);
+      if (kt + 4 < ntiles) load(kt + 4, ra1, rb1);
     }
     __syncthreads();
   }
@@ -283,8 +298,11 @@ int gemm_f32_batched(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, 
     const bool a_kc = trans_a != 0, b_kc = trans_b == 0;
     const bool wide = !(a_kc && !b_kc);  // 128 x 256 measured the most even across layouts
     const int64_t tx = (wide ? tiles_of<CfgXN>(M, N) : tiles_of<CfgXL>(M, N)) * batches;
-    if (tx >= 256) shape = wide ? Shape::XN : Shape::XL;
-    else if (tiles_of<CfgM>(M, N) * batches >= 64 || K >= 512) shape = Shape::M;
+    const int64_t tm = tiles_of<CfgM>(M, N) * batches;
+    // fraction of the last round of one-block-per-CU dispatch that is busy
+    auto fill = [](int64_t b) { return (double)b / (double)(((b + 255) / 256) * 256); };
+    if (tx >= 256 && fill(tx) >= 0.9 * fill(tm)) shape = wide ? Shape::XN : Shape::XL;
+    else if (tm >= 64 || K >= 512) shape = Shape::M;
     else shape = Shape::S;
   }
   int64_t tiles = 0;
@@ -309,13 +327,15 @@ int gemm_f32_batched(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, 
   g.c_vec_ok = (ldc % 4 == 0) && (stride_c % 4 == 0) && aligned16(C);
   g.partial = nullptr;
 
-  // Split K until about 512 blocks exist (two per CU for the 256-thread and
-  // 128 x 128 shapes; the 256-long tiles are only chosen with >= 256 blocks),
-  // keeping >= 8 K-tiles per split.
+  // Split K until a round of blocks fills the chip: 256 blocks for the
+  // 512-thread shapes (one per CU), 512 for the 256-thread ones (two per CU),
+  // keeping >= 4 K-tiles of 32 per split.  The 256-long tiles are only chosen
+  // with >= 256 blocks.
   const int64_t blocks = tiles * batches;
+  const int64_t target = (shape == Shape::M) ? 256 : 512;
   int splits = 1;
-  if (blocks < 512 && shape != Shape::XL && shape != Shape::XN && K >= 8 * KQ) {
-    const int64_t want = (512 + blocks - 1) / blocks;
+  if (blocks < target && shape != Shape::XL && shape != Shape::XN && K >= 8 * KQ) {
+    const int64_t want = (target + blocks - 1) / blocks;
     const int64_t max_by_k = K / (4 * KQ);
     splits = (int)std::max<int64_t>(1, std::min<int64_t>({want, max_by_k, 64}));
   }

@@ -17,11 +17,9 @@
 // Global -> LDS staging goes through registers (double-buffered LDS, one
 // barrier per k-tile).  An operand whose rows are k-contiguous in memory is
 // moved as float4 along k; one whose rows are contiguous along the output
-// dimension is moved as 4 x 4 micro-tiles (four float4 loads along the rows,
-// transposed in registers, four float4 LDS writes along k).  Threads are
-// assigned k-chunk fastest, which makes both kinds of LDS write conflict-free
-// (rows 4 apart differ by 80 floats = 16 banks; the 4 chunks of a row cover
-// the other offsets).
+// dimension is gathered as four coalesced dwords per 16-byte LDS chunk.  Both
+// write patterns are conflict-free, and every thread does the same work, so
+// the compiler can count outstanding loads exactly.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -47,25 +45,28 @@ struct Cfg {
 };
 
 // An R x BK operand tile.  KC: X(r, k) = X[k + ld*r] (k contiguous), else
-// X(r, k) = X[r + ld*k] (r contiguous).
+// X(r, k) = X[r + ld*k] (r contiguous).  A unit is one 16-byte k-chunk of one
+// row, written to LDS with one ds_write_b128.  KC loads it as one float4;
+// otherwise as four dwords at consecutive k (consecutive lanes take
+// consecutive rows, so each dword load is coalesced across the wave).
 template <bool KC, int R, int NT, int BK>
 struct Operand {
-  static_assert(R % 4 == 0, "operand rows must be a multiple of 4");
   static constexpr int LDK = BK + 4;
   static constexpr int CH = BK / 4;  // 16-byte chunks per row
-  // KC: one unit = a float4 along k (R*CH units); else a 4 x 4 micro-tile (R*CH/4 units)
-  static constexpr int UNITS = KC ? R * CH : R * CH / 4;
+  static constexpr int UNITS = R * CH;
   static constexpr int PER = (UNITS + NT - 1) / NT;
-  static constexpr int REGS = KC ? PER : 4 * PER;
+  static constexpr int REGS = PER;
 
   __device__ __forceinline__ static bool origin(int p, int& r, int& k) {
     const int u = threadIdx.x + NT * p;
     if (UNITS % NT != 0 && u >= UNITS) return false;
-    // k-chunk fastest in both modes: the lanes of one row group write
-    // different 16-byte chunks, so 8 consecutive lanes' LDS writes land in 8
-    // distinct bank groups.
-    r = (u / CH) * (KC ? 1 : 4);
-    k = (u % CH) * 4;
+    if (KC) {  // chunk fastest: 8 consecutive lanes write 2 rows x 4 chunks
+      r = u / CH;
+      k = (u % CH) * 4;
+    } else {  // row fastest: 8 consecutive lanes write 8 rows (80-float steps)
+      r = u % R;
+      k = (u / R) * 4;
+    }
     return true;
   }
 
@@ -80,28 +81,16 @@ struct Operand {
       int r, k;
       if (!origin(p, r, k)) break;
       const int64_t gr = r0 + r, gk = k0 + k;
-      if (KC) {
-        if (FAST) {
-          v[p] = *reinterpret_cast<const f32x4*>(X + gk + ld * gr);
-        } else {
-          f32x4 t;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) t[j] = (gr < Rtot && gk + j < Kend) ? X[gk + j + ld * gr] : 0.f;
-          v[p] = t;
-        }
+      if (KC && FAST) {
+        v[p] = *reinterpret_cast<const f32x4*>(X + gk + ld * gr);
       } else {
+        f32x4 t;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          if (FAST) {
-            v[4 * p + j] = *reinterpret_cast<const f32x4*>(X + gr + ld * (gk + j));
-          } else {
-            f32x4 t;
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-              t[e] = (gr + e < Rtot && gk + j < Kend) ? X[gr + e + ld * (gk + j)] : 0.f;
-            v[4 * p + j] = t;
-          }
+          const int64_t off = KC ? (gk + j + ld * gr) : (gr + ld * (gk + j));
+          t[j] = (FAST || (gr < Rtot && gk + j < Kend)) ? X[off] : 0.f;
         }
+        v[p] = t;
       }
     }
   }
@@ -111,17 +100,7 @@ struct Operand {
     for (int p = 0; p < PER; ++p) {
       int r, k;
       if (!origin(p, r, k)) break;
-      if (KC) {
-        *reinterpret_cast<f32x4*>(lds + r * LDK + k) = v[p];
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          f32x4 w;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) w[j] = v[4 * p + j][e];
-          *reinterpret_cast<f32x4*>(lds + (r + e) * LDK + k) = w;
-        }
-      }
+      *reinterpret_cast<f32x4*>(lds + r * LDK + k) = v[p];
     }
   }
 };
