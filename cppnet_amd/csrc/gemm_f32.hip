@@ -264,28 +264,16 @@ int64_t tiles_of(int64_t M, int64_t N) {
   return ((M + Cfg::BM - 1) / Cfg::BM) * ((N + Cfg::BN - 1) / Cfg::BN);
 }
 
-}  // namespace
+struct Plan {
+  Shape shape;
+  int64_t tiles;
+  int splits;
+  int64_t kps;
+};
 
-int gemm_f32_batched(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float alpha,
-                     const float* A, int64_t lda, int64_t stride_a, const float* B, int64_t ldb,
-                     int64_t stride_b, float beta, float* C, int64_t ldc, int64_t stride_c,
-                     int64_t batches, const float* bias, int epilogue, hipStream_t st,
-                     const char* who) {
-  CNHIP_REQUIRE(M >= 0 && N >= 0 && K >= 0 && batches >= 0,
-                "%s: negative GEMM size (M=%lld N=%lld K=%lld batch=%lld)", who, (long long)M,
-                (long long)N, (long long)K, (long long)batches);
-  CNHIP_REQUIRE(epilogue == CNHIP_EPI_NONE || epilogue == CNHIP_EPI_RELU, "%s: bad epilogue %d",
-                who, epilogue);
-  if (M == 0 || N == 0 || batches == 0) return CNHIP_OK;
-  CNHIP_REQUIRE(C != nullptr, "%s: C is NULL", who);
-  CNHIP_REQUIRE(ldc >= M, "%s: ldc=%lld < M=%lld", who, (long long)ldc, (long long)M);
-  if (K > 0) {
-    CNHIP_REQUIRE(A && B, "%s: A or B is NULL", who);
-    CNHIP_REQUIRE(lda >= (trans_a ? K : M), "%s: lda=%lld too small", who, (long long)lda);
-    CNHIP_REQUIRE(ldb >= (trans_b ? N : K), "%s: ldb=%lld too small", who, (long long)ldb);
-  }
-  CNHIP_REQUIRE(batches <= 65535, "%s: batch count %lld exceeds 65535", who, (long long)batches);
-
+// Tile shape and split-K plan of one GEMM; splits <= max_splits.
+Plan plan_gemm(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, int64_t batches,
+               int max_splits) {
   // Tile shape: skinny shapes waste no MFMA work on padding.  Large outputs
   // take 128 x 256, or 256 x 128 when only A is k-contiguous in memory (the
   // long tile side goes to the operand whose loads need no register
@@ -314,7 +302,72 @@ int gemm_f32_batched(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, 
     case Shape::SM: tiles = tiles_of<CfgSM>(M, N); break;
     case Shape::S: tiles = tiles_of<CfgS>(M, N); break;
   }
-  CNHIP_REQUIRE(tiles < ((int64_t)1 << 30), "%s: GEMM too large", who);
+
+  // Split K until a round of blocks fills the chip: 256 blocks for the
+  // 512-thread shapes (one per CU), 512 for the 256-thread ones (two per CU),
+  // keeping >= 4 K-tiles of 32 per split.  The 256-long tiles are only chosen
+  // with >= 256 blocks.
+  const int64_t blocks = tiles * batches;
+  const int64_t target = (shape == Shape::M) ? 256 : 512;
+  int splits = 1;
+  if (blocks < target && shape != Shape::XL && shape != Shape::XN && K >= 8 * KQ) {
+    const int64_t want = (target + blocks - 1) / blocks;
+    const int64_t max_by_k = K / (4 * KQ);
+    splits = (int)std::max<int64_t>(1, std::min<int64_t>({want, max_by_k, (int64_t)max_splits}));
+  }
+  int64_t kps = (K + splits - 1) / splits;
+  kps = ((kps + KQ - 1) / KQ) * KQ;
+  if (kps == 0) kps = KQ;
+  splits = K > 0 ? (int)((K + kps - 1) / kps) : 1;
+
+  return Plan{shape, tiles, splits, kps};
+}
+
+// Launches the planned kernel, bracketed by the per-launch timing events.
+int launch_plan(Shape shape, int trans_a, int trans_b, const GemmArgs& g, int64_t batches,
+                hipStream_t st, const char* who) {
+  TimingRec* rec =
+      timing_slot(2.0 * (double)g.M * (double)g.N * (double)g.K * (double)batches);
+  if (rec) (void)hipEventRecord(rec->start, st);
+  switch (shape) {
+    case Shape::XL: launch_t<CfgXL>(trans_a, trans_b, g, batches, st); break;
+    case Shape::XN: launch_t<CfgXN>(trans_a, trans_b, g, batches, st); break;
+    case Shape::M: launch_t<CfgM>(trans_a, trans_b, g, batches, st); break;
+    case Shape::SN: launch_t<CfgSN>(trans_a, trans_b, g, batches, st); break;
+    case Shape::SM: launch_t<CfgSM>(trans_a, trans_b, g, batches, st); break;
+    case Shape::S: launch_t<CfgS>(trans_a, trans_b, g, batches, st); break;
+  }
+  const int status = check_launch(who);
+  if (rec) (void)hipEventRecord(rec->stop, st);
+  return status;
+}
+
+}  // namespace
+
+int gemm_f32_batched(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float alpha,
+                     const float* A, int64_t lda, int64_t stride_a, const float* B, int64_t ldb,
+                     int64_t stride_b, float beta, float* C, int64_t ldc, int64_t stride_c,
+                     int64_t batches, const float* bias, int epilogue, hipStream_t st,
+                     const char* who) {
+  CNHIP_REQUIRE(M >= 0 && N >= 0 && K >= 0 && batches >= 0,
+                "%s: negative GEMM size (M=%lld N=%lld K=%lld batch=%lld)", who, (long long)M,
+                (long long)N, (long long)K, (long long)batches);
+  CNHIP_REQUIRE(epilogue == CNHIP_EPI_NONE || epilogue == CNHIP_EPI_RELU, "%s: bad epilogue %d",
+                who, epilogue);
+  if (M == 0 || N == 0 || batches == 0) return CNHIP_OK;
+  CNHIP_REQUIRE(C != nullptr, "%s: C is NULL", who);
+  CNHIP_REQUIRE(ldc >= M, "%s: ldc=%lld < M=%lld", who, (long long)ldc, (long long)M);
+  if (K > 0) {
+    CNHIP_REQUIRE(A && B, "%s: A or B is NULL", who);
+    CNHIP_REQUIRE(lda >= (trans_a ? K : M), "%s: lda=%lld too small", who, (long long)lda);
+    CNHIP_REQUIRE(ldb >= (trans_b ? N : K), "%s: ldb=%lld too small", who, (long long)ldb);
+  }
+  CNHIP_REQUIRE(batches <= 65535, "%s: batch count %lld exceeds 65535", who, (long long)batches);
+
+  const Plan plan = plan_gemm(trans_a, trans_b, M, N, K, batches, 64);
+  CNHIP_REQUIRE(plan.tiles < ((int64_t)1 << 30), "%s: GEMM too large", who);
+  const Shape shape = plan.shape;
+  const int splits = plan.splits;
 
   GemmArgs g;
   g.M = M; g.N = N; g.K = K;
@@ -327,23 +380,7 @@ int gemm_f32_batched(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, 
   g.c_vec_ok = (ldc % 4 == 0) && (stride_c % 4 == 0) && aligned16(C);
   g.partial = nullptr;
 
-  // Split K until a round of blocks fills the chip: 256 blocks for the
-  // 512-thread shapes (one per CU), 512 for the 256-thread ones (two per CU),
-  // keeping >= 4 K-tiles of 32 per split.  The 256-long tiles are only chosen
-  // with >= 256 blocks.
-  const int64_t blocks = tiles * batches;
-  const int64_t target = (shape == Shape::M) ? 256 : 512;
-  int splits = 1;
-  if (blocks < target && shape != Shape::XL && shape != Shape::XN && K >= 8 * KQ) {
-    const int64_t want = (target + blocks - 1) / blocks;
-    const int64_t max_by_k = K / (4 * KQ);
-    splits = (int)std::max<int64_t>(1, std::min<int64_t>({want, max_by_k, 64}));
-  }
-  int64_t kps = (K + splits - 1) / splits;
-  kps = ((kps + KQ - 1) / KQ) * KQ;
-  if (kps == 0) kps = KQ;
-  splits = K > 0 ? (int)((K + kps - 1) / kps) : 1;
-  g.k_per_split = kps;
+  g.k_per_split = plan.kps;
   g.splits = splits;
 
   if (splits > 1) {
@@ -353,18 +390,7 @@ int gemm_f32_batched(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, 
     g.partial = static_cast<float*>(ws);
   }
 
-  TimingRec* rec = timing_slot(2.0 * (double)M * (double)N * (double)K * (double)batches);
-  if (rec) (void)hipEventRecord(rec->start, st);
-  switch (shape) {
-    case Shape::XL: launch_t<CfgXL>(trans_a, trans_b, g, batches, st); break;
-    case Shape::XN: launch_t<CfgXN>(trans_a, trans_b, g, batches, st); break;
-    case Shape::M: launch_t<CfgM>(trans_a, trans_b, g, batches, st); break;
-    case Shape::SN: launch_t<CfgSN>(trans_a, trans_b, g, batches, st); break;
-    case Shape::SM: launch_t<CfgSM>(trans_a, trans_b, g, batches, st); break;
-    case Shape::S: launch_t<CfgS>(trans_a, trans_b, g, batches, st); break;
-  }
-  int status = check_launch(who);
-  if (rec) (void)hipEventRecord(rec->stop, st);
+  int status = launch_plan(shape, trans_a, trans_b, g, batches, st, who);
 
   if (splits > 1) {
     if (status == CNHIP_OK) {
@@ -383,6 +409,31 @@ int gemm_f32(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float al
              int64_t ldc, const float* bias, int epilogue, hipStream_t st, const char* who) {
   return gemm_f32_batched(trans_a, trans_b, M, N, K, alpha, A, lda, 0, B, ldb, 0, beta, C, ldc, 0,
                           1, bias, epilogue, st, who);
+}
+
+// op(A) op(B) as split-K partial products P[s][m + M*n], s < *splits_out
+// (<= max_splits), written into the caller's workspace (max_splits*M*N
+// floats) with no reduction: a consumer kernel sums them in split order
+// (the recurrent cells, which fuse that sum into their gate arithmetic).
+int gemm_f32_partials(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K,
+                      const float* A, int64_t lda, const float* B, int64_t ldb, float* partial,
+                      int max_splits, int* splits_out, hipStream_t st, const char* who) {
+  CNHIP_REQUIRE(M > 0 && N > 0 && K > 0 && max_splits >= 1 && partial && A && B && splits_out,
+                "%s: bad split-K partial GEMM arguments", who);
+  CNHIP_REQUIRE(lda >= (trans_a ? K : M) && ldb >= (trans_b ? N : K), "%s: ld too small", who);
+  const Plan plan = plan_gemm(trans_a, trans_b, M, N, K, 1, max_splits);
+  GemmArgs g{};
+  g.M = M; g.N = N; g.K = K;
+  g.A = A; g.lda = lda; g.B = B; g.ldb = ldb;
+  g.C = partial; g.ldc = M;
+  g.alpha = 1.f; g.beta = 0.f;
+  g.vec_ok = (lda % 4 == 0) && (ldb % 4 == 0) && aligned16(A) && aligned16(B);
+  g.c_vec_ok = 0;
+  g.k_per_split = plan.kps;
+  g.splits = plan.splits;
+  g.partial = partial;
+  *splits_out = plan.splits;
+  return launch_plan(plan.shape, trans_a, trans_b, g, 1, st, who);
 }
 
 }  // namespace cnhip

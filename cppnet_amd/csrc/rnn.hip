@@ -30,29 +30,50 @@ int gemm_f32(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float al
              int64_t ldc, const float* bias, int epilogue, hipStream_t st, const char* who);
 int column_sum(const float* in, float* out, int64_t rows, int64_t cols, int accumulate,
                hipStream_t st, const char* who);
+int gemm_f32_partials(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K,
+                      const float* A, int64_t lda, const float* B, int64_t ldb, float* partial,
+                      int max_splits, int* splits_out, hipStream_t st, const char* who);
 
 namespace {
 
 __device__ __forceinline__ float sigm(float x) { return 1.0f / (1.0f + expf(-x)); }
 
+// Sum of nsplit split-K partials p[z*stride + i], z ascending (0 when nsplit
+// is 0): the recurrent GEMM's output, reduced inside the cell kernel that
+// consumes it instead of by a separate pass.
+__device__ __forceinline__ float partial_sum(const float* __restrict__ p, int nsplit,
+                                             int64_t stride, int64_t i) {
+  float s = 0.0f;
+  for (int z = 0; z < nsplit; ++z) s += p[z * stride + i];
+  return s;
+}
+
 // ---------------------------------------------------------------- LSTM cell
-// gates rows of step t hold the pre-activations x W_ih + h W_hh; overwritten
-// with the activations i, f, g, o (lstm.cpp:115-134).
+// gates rows of step t hold x W_ih; the recurrent part h_{t-1} W_hh arrives as
+// nsplit split-K partials hw[z][n + B*j] (j < 4H).  The pre-activations
+// (x W_ih + h W_hh) are overwritten with the activations i, f, g, o
+// (lstm.cpp:115-134).
 __global__ void __launch_bounds__(256) lstm_cell_fwd_kernel(float* __restrict__ gates,
                                                             const float* __restrict__ bias,
                                                             float* __restrict__ c,
                                                             float* __restrict__ tanh_c,
-                                                            float* __restrict__ Y, int64_t B,
-                                                            int64_t S, int64_t H, int64_t t) {
-  const int64_t BS = B * S;
+                                                            float* __restrict__ Y,
+                                                            const float* __restrict__ hw,
+                                                            int nsplit, int64_t B, int64_t S,
+                                                            int64_t H, int64_t t) {
+  const int64_t BS = B * S, BG = B * 4 * H;
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= B * H) return;
   const int64_t n = e % B, d = e / B, row = n + B * t;
   float* g = gates + row;
-  const float ig = sigm(g[BS * d] + bias[d]);
-  const float fg = sigm(g[BS * (d + H)] + bias[d + H]);
-  const float gg = tanhf(g[BS * (d + 2 * H)] + bias[d + 2 * H]);
-  const float og = sigm(g[BS * (d + 3 * H)] + bias[d + 3 * H]);
+  auto pre = [&](int64_t j) {
+    const float x = g[BS * j];
+    return nsplit ? partial_sum(hw, nsplit, BG, n + B * j) + x : x;
+  };
+  const float ig = sigm(pre(d) + bias[d]);
+  const float fg = sigm(pre(d + H) + bias[d + H]);
+  const float gg = tanhf(pre(d + 2 * H) + bias[d + 2 * H]);
+  const float og = sigm(pre(d + 3 * H) + bias[d + 3 * H]);
   const float cprev = t > 0 ? c[row - B + BS * d] : 0.0f;
   const float ct = fg * cprev + ig * gg;
   const float tc = tanhf(ct);
@@ -65,11 +86,13 @@ __global__ void __launch_bounds__(256) lstm_cell_fwd_kernel(float* __restrict__ 
   Y[row + BS * d] = og * tc;
 }
 
-// lstm.cpp:184-219, 247-249.  dh_in/dc: [B, H] (dense, ld B); ignored when first.
+// lstm.cpp:184-219, 247-249.  dh_in: the nsplit split-K partials of
+// dG_{t+1} W_hh^T, [z][B, H]; dc: [B, H] (dense, ld B); both ignored when first.
 __global__ void __launch_bounds__(256) lstm_cell_bwd_kernel(
     const float* __restrict__ gates, const float* __restrict__ c, const float* __restrict__ tanh_c,
-    const float* __restrict__ dY, const float* __restrict__ dh_in, float* __restrict__ dc_buf,
-    float* __restrict__ dG, int64_t B, int64_t S, int64_t H, int64_t t, int first) {
+    const float* __restrict__ dY, const float* __restrict__ dh_in, int nsplit,
+    float* __restrict__ dc_buf, float* __restrict__ dG, int64_t B, int64_t S, int64_t H, int64_t t,
+    int first) {
   const int64_t BS = B * S;
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= B * H) return;
@@ -77,7 +100,7 @@ __global__ void __launch_bounds__(256) lstm_cell_bwd_kernel(
   const float ig = gates[row + BS * d], fg = gates[row + BS * (d + H)];
   const float gg = gates[row + BS * (d + 2 * H)], og = gates[row + BS * (d + 3 * H)];
   const float tc = tanh_c[row + BS * d];
-  const float dh = dY[row + BS * d] + (first ? 0.0f : dh_in[e]);
+  const float dh = dY[row + BS * d] + (first ? 0.0f : partial_sum(dh_in, nsplit, B * H, e));
   const float dc = dh * og * (1.0f - tc * tc) + (first ? 0.0f : dc_buf[e]);
   const float cprev = t > 0 ? c[row - B + BS * d] : 0.0f;
   dG[row + BS * d] = dc * gg * ig * (1.0f - ig);
@@ -223,13 +246,18 @@ int cnhip_lstm_forward(const float* X, const float* W_ih, const float* W_hh, con
   CNHIP_REQUIRE(X && W_ih && W_hh && b && Y && gates && c && tanh_c, "%s: NULL pointer", who);
   hipStream_t st = as_stream(stream);
   const int64_t G = 4 * H, BS = B * S;
+  constexpr int kMaxSplits = 8;
+  cnhip::Workspace ws(st);
+  CNHIP_TRY(ws.alloc((size_t)kMaxSplits * B * G * sizeof(float), who));
+  float* hw = static_cast<float*>(ws.p);
   CNHIP_TRY(cnhip::gemm_f32(0, 0, BS, G, I, 1.f, X, BS, W_ih, I, 0.f, gates, BS, nullptr, 0, st, who));
   for (int64_t t = 0; t < S; ++t) {
+    int ns = 0;  // h_0 = 0: no recurrent term at t = 0
     if (t > 0)
-      CNHIP_TRY(cnhip::gemm_f32(0, 0, B, G, H, 1.f, Y + B * (t - 1), BS, W_hh, H, 1.f, gates + B * t,
-                                BS, nullptr, 0, st, who));
+      CNHIP_TRY(cnhip::gemm_f32_partials(0, 0, B, G, H, Y + B * (t - 1), BS, W_hh, H, hw, kMaxSplits,
+                                         &ns, st, who));
     hipLaunchKernelGGL(cnhip::lstm_cell_fwd_kernel, dim3(cnhip::cell_grid(B, H)), dim3(256), 0, st,
-                       gates, b, c, tanh_c, Y, B, S, H, t);
+                       gates, b, c, tanh_c, Y, hw, ns, B, S, H, t);
     CNHIP_TRY(cnhip::check_launch(who));
   }
   return CNHIP_OK;
@@ -245,18 +273,20 @@ int cnhip_lstm_backward(const float* X, const float* W_ih, const float* W_hh, co
                 "%s: NULL pointer", who);
   hipStream_t st = as_stream(stream);
   const int64_t G = 4 * H, BS = B * S;
+  constexpr int kMaxSplits = 16;
   cnhip::Workspace ws(st);
-  CNHIP_TRY(ws.alloc((size_t)(BS * G + 2 * B * H) * sizeof(float), who));
+  CNHIP_TRY(ws.alloc((size_t)(BS * G + (kMaxSplits + 1) * B * H) * sizeof(float), who));
   float* dG = static_cast<float*>(ws.p);
-  float* dh = dG + BS * G;
-  float* dc = dh + B * H;
+  float* dc = dG + BS * G;
+  float* dh = dc + B * H;  // kMaxSplits partials of dG_t W_hh^T
+  int ns = 0;
   for (int64_t t = S - 1; t >= 0; --t) {
     hipLaunchKernelGGL(cnhip::lstm_cell_bwd_kernel, dim3(cnhip::cell_grid(B, H)), dim3(256), 0, st,
-                       gates, c, tanh_c, dY, dh, dc, dG, B, S, H, t, t == S - 1 ? 1 : 0);
+                       gates, c, tanh_c, dY, dh, ns, dc, dG, B, S, H, t, t == S - 1 ? 1 : 0);
     CNHIP_TRY(cnhip::check_launch(who));
-    if (t > 0)  // dh_next = dG_t W_hh^T (lstm.cpp:244)
-      CNHIP_TRY(cnhip::gemm_f32(0, 1, B, H, G, 1.f, dG + B * t, BS, W_hh, H, 0.f, dh, B, nullptr, 0,
-                                st, who));
+    if (t > 0)  // dh_next = dG_t W_hh^T (lstm.cpp:244), summed by the next cell kernel
+      CNHIP_TRY(cnhip::gemm_f32_partials(0, 1, B, H, G, dG + B * t, BS, W_hh, H, dh, kMaxSplits, &ns,
+                                         st, who));
   }
   CNHIP_TRY(cnhip::gemm_f32(1, 0, I, G, BS, 1.f, X, BS, dG, BS, 0.f, gW_ih, I, nullptr, 0, st, who));
   CNHIP_TRY(cnhip::gemm_f32(1, 0, H, G, B * (S - 1), 1.f, Y, BS, dG + B, BS, 0.f, gW_hh, H, nullptr,
