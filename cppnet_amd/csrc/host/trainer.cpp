@@ -83,7 +83,7 @@ namespace
 
         DeviceTensor forward(const DeviceTensor& ids)
         {
-            DeviceTensor x = emb->forward(ids);
+            DeviceTensor x = emb->forward(ids, /*ids_checked=*/true);  // checked at upload
             for (auto& b : blocks) x = b.forward(x);
             return fc->forward(pool->forward(x));
         }
@@ -523,11 +523,30 @@ int cnt_get_grad(cnt_session* s, int index, float* host)
     });
 }
 
+namespace
+{
+    // The token ids of a batch are checked once, when the batch is uploaded
+    // (as the cpu-eigen Embedding::forward does per call, embedding.cpp:87-90),
+    // so the training steps themselves never synchronise.
+    void check_token_ids(const int32_t* ids, int64_t B, int64_t S, int64_t V)
+    {
+        for (int64_t n = 0; n < B; ++n)
+            for (int64_t t = 0; t < S; ++t)
+            {
+                const int32_t id = ids[n + B * t];
+                if (id < 0 || id >= V)
+                    throw std::out_of_range("Embedding: token ID " + std::to_string(id) + " out of range [0, " +
+                                            std::to_string(V) + ")");
+            }
+    }
+} // namespace
+
 int cnt_set_batch_tokens(cnt_session* s, const int32_t* ids_host, const float* y_host)
 {
     return guarded("cnt_set_batch_tokens", [&] {
         check_session(s);
         if (!s->encoder) throw std::invalid_argument("not a token-input (transformer) session");
+        check_token_ids(ids_host, s->X.dimension(0), s->X.dimension(1), s->encoder->emb->get_vocab_size());
         StreamScope scope(s);
         s->X.copy_from_host(ids_host);
         s->Y.copy_from_host(y_host);
@@ -554,6 +573,12 @@ int cnt_set_batch_device(cnt_session* s, const float* x_dev, const float* y_dev)
                                          s->stream), "X");
         Device::check(cnhip_memcpy_async(s->Y.data(), y_dev, static_cast<size_t>(s->Y.size()) * 4, 2,
                                          s->stream), "Y");
+        if (s->encoder)  // token ids: one read-back here instead of one per step
+        {
+            std::vector<int32_t> ids(static_cast<size_t>(s->X.size()));
+            s->X.copy_to_host(ids.data());
+            check_token_ids(ids.data(), s->X.dimension(0), s->X.dimension(1), s->encoder->emb->get_vocab_size());
+        }
     });
 }
 

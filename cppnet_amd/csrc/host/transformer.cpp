@@ -45,15 +45,23 @@ namespace CppNet
             set_weight(Utils::uniform_init(vocab_size_, embed_dim_, -scale, scale));
         }
 
-        DeviceTensor Embedding::forward(const DeviceTensor& ids)
+        DeviceTensor Embedding::forward(const DeviceTensor& ids) { return forward(ids, false); }
+
+        DeviceTensor Embedding::forward(const DeviceTensor& ids, bool ids_checked)
         {
             if (ids.rank() != 2) throw std::runtime_error("Embedding::forward: expected ids [B, S]");
             const int64_t B = ids.dimension(0), S = ids.dimension(1);
             DeviceTensor out = DeviceTensor::empty({B, S, embed_dim_});
-            oob_.fill_zero();
+            if (!ids_checked) oob_.fill_zero();
             Device::check(cnhip_embedding_forward(ids.idata(), Wt_.data(), out.data(), B, S, vocab_size_,
-                                                  embed_dim_, oob_.idata(), Device::stream()),
+                                                  embed_dim_, ids_checked ? nullptr : oob_.idata(),
+                                                  Device::stream()),
                           "Embedding::forward");
+            if (ids_checked)
+            {
+                ids_cache_ = ids;
+                return out;
+            }
             int32_t bad = 0;
             oob_.copy_to_host(&bad);
             if (bad > 0)

@@ -389,16 +389,33 @@ __global__ void __launch_bounds__(256) gelu_bwd_kernel(const float* __restrict__
   }
 }
 
-// mean over s of [B,S,D]; thread per (b, d), b fastest
+// mean over s of [B,S,D].  For one feature d the [B, S] slab is contiguous
+// (b + B*s), so a block owns (d, up to 64 consecutive b) and its threads
+// split s into CHUNKS contiguous ranges: thread (b, chunk) sums its range in
+// order, then the chunk sums are added in chunk order (a fixed order for
+// any launch) and divided by S.
 __global__ void __launch_bounds__(256) meanpool_fwd_kernel(const float* __restrict__ x,
                                                            float* __restrict__ y, int64_t B,
-                                                           int64_t S, int64_t D) {
-  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= B * D) return;
-  const int64_t b = e % B, d = e / B;
+                                                           int64_t S, int64_t D, int bw) {
+  __shared__ float part[256];
+  const int chunks = 256 / bw;
+  const int bl = threadIdx.x % bw, ch = threadIdx.x / bw;
+  const int64_t d = blockIdx.x;
+  const int64_t b = (int64_t)blockIdx.y * bw + bl;
+  const int64_t per = (S + chunks - 1) / chunks;
+  const int64_t t0 = ch * per, t1 = min(S, t0 + per);
   float s = 0.f;
-  for (int64_t t = 0; t < S; ++t) s += x[b + B * t + B * S * d];
-  y[e] = s / (float)S;
+  if (ch < chunks && b < B) {
+    const float* xs = x + B * S * d + b;
+    for (int64_t t = t0; t < t1; ++t) s += xs[B * t];
+  }
+  part[threadIdx.x] = s;
+  __syncthreads();
+  if (ch == 0 && b < B) {
+    float tot = part[bl];
+    for (int c = 1; c < chunks; ++c) tot += part[bl + bw * c];
+    y[b + B * d] = tot / (float)S;
+  }
 }
 __global__ void __launch_bounds__(256) meanpool_bwd_kernel(const float* __restrict__ dy,
                                                            float* __restrict__ dx, int64_t B,
@@ -687,8 +704,10 @@ int cnhip_meanpool1d_forward(const float* x, float* y, int64_t B, int64_t S, int
   const char* who = "cnhip_meanpool1d_forward";
   CNHIP_REQUIRE(B > 0 && S > 0 && D > 0, "%s: bad shape", who);
   CNHIP_REQUIRE(x && y, "%s: NULL pointer", who);
-  hipLaunchKernelGGL(cnhip::meanpool_fwd_kernel, dim3((unsigned)((B * D + 255) / 256)), dim3(256), 0,
-                     as_stream(s), x, y, B, S, D);
+  CNHIP_REQUIRE(D <= 0x7fffffff, "%s: D too large", who);
+  const int bw = B < 64 ? (int)B : 64;
+  hipLaunchKernelGGL(cnhip::meanpool_fwd_kernel, dim3((unsigned)D, (unsigned)((B + bw - 1) / bw)),
+                     dim3(256), 0, as_stream(s), x, y, B, S, D, bw);
   return cnhip::check_launch(who);
 }
 

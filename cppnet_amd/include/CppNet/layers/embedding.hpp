@@ -34,8 +34,13 @@ namespace CppNet
 
             Tensor<float, 3> forward(const Tensor<int, 2>& input);
             Tensor<float, 3> backward(const Tensor<float, 3>& grad_output);
-            /// ids: int32 device tensor [B, S]
+            /// ids: int32 device tensor [B, S]; an id outside [0, V) throws
+            /// (one 4-byte read-back per call).
             DeviceTensor forward(const DeviceTensor& ids);
+            /// Same, for ids the caller has already checked to lie in [0, V)
+            /// (e.g. when the batch was uploaded): no read-back, so the step
+            /// stays asynchronous.  Out-of-range ids still produce zero rows.
+            DeviceTensor forward(const DeviceTensor& ids, bool ids_checked);
             DeviceTensor backward(const DeviceTensor& grad_output);
 
             bool is_trainable() const override { return trainable_; }

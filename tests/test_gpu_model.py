@@ -511,7 +511,14 @@ def test_transformer_rejects_out_of_range_ids(gpu):
     sess = trainer.Session(cfg)
     ids = ids.copy()
     ids[4] = 10
-    sess.set_batch(ids, Y)
+    # the trainer checks ids when the batch is uploaded, with the reference's
+    # message (embedding.cpp:87-90), so the steps never read back
     with pytest.raises(Exception, match="token ID 10 out of range"):
-        sess.step()
+        sess.set_batch(ids, Y)
+    ids[4] = -1
+    with pytest.raises(Exception, match="token ID -1 out of range"):
+        sess.set_batch(ids, Y)
+    ids[4] = 9
+    sess.set_batch(ids, Y)
+    assert np.isfinite(sess.step())
     sess.close()
