@@ -10,6 +10,7 @@
 //   MSE      mse.cpp:102-161          SoftmaxCE softmax_cross_entropy.cpp:118-195
 #include <hip/hip_runtime.h>
 
+#include "act_math.hpp"
 #include "common.hpp"
 
 namespace cnhip {
@@ -31,7 +32,7 @@ struct TanhFwd {
 };
 // grad_output * mask, mask = 1 where the cached output is > 0 (relu.cpp:177-181)
 struct ReluBwd {
-  __device__ float operator()(float y, float dy) const { return dy * (y > 0.f ? 1.f : 0.f); }
+  __device__ float operator()(float y, float dy) const { return dy * relu_mask(y); }
 };
 // grad_output * (s * (1 - s))  (sigmoid.cpp:192-194)
 struct SigmoidBwd {

@@ -18,6 +18,7 @@
 #include <algorithm>
 #include <vector>
 
+#include "act_math.hpp"
 #include "common.hpp"
 #include "mfma_kpack.hpp"
 
@@ -54,7 +55,10 @@ struct GemmArgs {
   int64_t ldc, stride_c;
   float alpha, beta;
   const float* bias;
-  int epilogue;
+  int epilogue;          // CNHIP_EPI_* or one of the fused-activation codes below
+  const float* aux_in;   // DRELU: ReLU outputs, DGELU: GELU inputs, [M,N] ld ld_aux
+  float* aux_out;        // GELU: receives the pre-activation, [M,N] ld ld_aux
+  int64_t ld_aux;
   int vec_ok;            // every ld and stride % 4 == 0 and A, B 16-byte aligned
   int c_vec_ok;          // ldc, stride_c % 4 == 0 and C 16-byte aligned
   int64_t k_per_split;   // multiple of KQ (hence of every tile's BK)
@@ -62,13 +66,32 @@ struct GemmArgs {
   int splits;
 };
 
+// Fused-activation epilogues (internal codes beyond the C ABI's NONE / RELU):
+//   EPI_GELU : C = gelu(v), aux_out = v (the pre-activation GELU's backward reads)
+//   EPI_DRELU: C = v * [aux_in > 0]      (ReLU backward on the layer below)
+//   EPI_DGELU: C = v * gelu'(aux_in)     (GELU backward on the layer below)
+// where v = alpha * acc (+ beta * C) (+ bias[n]).
+constexpr int EPI_GELU = 2, EPI_DRELU = 3, EPI_DGELU = 4;
+
+// FUSED: the kernel instantiation that also handles the fused-activation
+// codes; the plain one (the bulk of all launches) keeps its epilogue small so
+// its code stays compact.
+template <bool FUSED>
 __device__ __forceinline__ float epilogue_value(const GemmArgs& g, const float* C, float acc,
                                                 int64_t m, int64_t n) {
   float v = g.alpha * acc;
   if (g.beta != 0.f) v += g.beta * C[m + g.ldc * n];
   if (g.bias) v += g.bias[n];
-  if (g.epilogue == CNHIP_EPI_RELU) v = fmaxf(v, 0.f);
-  return v;
+  if (!FUSED) return g.epilogue == CNHIP_EPI_RELU ? fmaxf(v, 0.f) : v;
+  switch (g.epilogue) {
+    case CNHIP_EPI_RELU: return fmaxf(v, 0.f);
+    case EPI_GELU:
+      g.aux_out[m + g.ld_aux * n] = v;
+      return gelu_f(v);
+    case EPI_DRELU: return v * relu_mask(g.aux_in[m + g.ld_aux * n]);
+    case EPI_DGELU: return v * gelu_grad_f(g.aux_in[m + g.ld_aux * n]);
+    default: return v;
+  }
 }
 
 // Block -> output tile.  Hardware dispatch places consecutive block ids on
@@ -143,7 +166,7 @@ __device__ __forceinline__ void gemm_mainloop(const GemmArgs& g, const float* __
   }
 }
 
-template <bool TA, bool TB, class C>
+template <bool TA, bool TB, class C, bool FUSED>
 __global__ void __launch_bounds__(C::NT, min_blocks<C>()) gemm_f32_kernel(GemmArgs g) {
   constexpr int BM = C::BM, BN = C::BN;
   __shared__ __align__(16) float lds[2 * C::LDS_FLOATS];
@@ -186,12 +209,12 @@ __global__ void __launch_bounds__(C::NT, min_blocks<C>()) gemm_f32_kernel(GemmAr
     if (g.c_vec_ok && m + 3 < g.M) {
       f32x4 o;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = epilogue_value(g, Cp, v[e], m + e, n);
+      for (int e = 0; e < 4; ++e) o[e] = epilogue_value<FUSED>(g, Cp, v[e], m + e, n);
       *reinterpret_cast<f32x4*>(Cp + m + g.ldc * n) = o;
     } else {
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        if (m + e < g.M) Cp[(m + e) + g.ldc * n] = epilogue_value(g, Cp, v[e], m + e, n);
+        if (m + e < g.M) Cp[(m + e) + g.ldc * n] = epilogue_value<FUSED>(g, Cp, v[e], m + e, n);
     }
   });
 }
@@ -208,16 +231,21 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs g, int64_t 
     for (int z = 0; z < g.splits; ++z) s += P[(int64_t)z * mn];
     const int64_t m = e % g.M, n = e / g.M;
     float* C = g.C + bt * g.stride_c;
-    C[m + g.ldc * n] = epilogue_value(g, C, s, m, n);
+    C[m + g.ldc * n] = epilogue_value<true>(g, C, s, m, n);
   }
 }
 
 template <bool TA, bool TB, class Cfg>
 void launch_cfg(const GemmArgs& g, int64_t batches, hipStream_t st) {
   const int64_t tiles = ((g.M + Cfg::BM - 1) / Cfg::BM) * ((g.N + Cfg::BN - 1) / Cfg::BN);
-  hipLaunchKernelGGL((gemm_f32_kernel<TA, TB, Cfg>), dim3((unsigned)tiles, (unsigned)batches,
-                                                          (unsigned)g.splits),
-                     dim3(Cfg::NT), 0, st, g);
+  const dim3 grid((unsigned)tiles, (unsigned)batches, (unsigned)g.splits);
+  // the fused-activation epilogues are only used by the forward (NN) and
+  // input-gradient (NT) GEMMs of Linear layers
+  constexpr bool kFusable = !TA;
+  if (kFusable && g.epilogue >= EPI_GELU && !g.partial)
+    hipLaunchKernelGGL((gemm_f32_kernel<TA, TB, Cfg, kFusable>), grid, dim3(Cfg::NT), 0, st, g);
+  else
+    hipLaunchKernelGGL((gemm_f32_kernel<TA, TB, Cfg, false>), grid, dim3(Cfg::NT), 0, st, g);
 }
 
 template <class Cfg>
@@ -344,16 +372,39 @@ int launch_plan(Shape shape, int trans_a, int trans_b, const GemmArgs& g, int64_
 
 }  // namespace
 
+// Single GEMM with a fused-activation epilogue (see epilogue_value):
+// aux is [M,N] with leading dimension ld_aux (an output for EPI_GELU, an
+// input for EPI_DRELU / EPI_DGELU).
+int gemm_f32_act(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, const float* A,
+                 int64_t lda, const float* B, int64_t ldb, float* C, int64_t ldc, const float* bias,
+                 int epilogue, const float* aux_in, float* aux_out, int64_t ld_aux, hipStream_t st,
+                 const char* who);
+
+int gemm_f32_core(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float alpha,
+                  const float* A, int64_t lda, int64_t stride_a, const float* B, int64_t ldb,
+                  int64_t stride_b, float beta, float* C, int64_t ldc, int64_t stride_c,
+                  int64_t batches, const float* bias, int epilogue, const float* aux_in,
+                  float* aux_out, int64_t ld_aux, hipStream_t st, const char* who);
+
 int gemm_f32_batched(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float alpha,
                      const float* A, int64_t lda, int64_t stride_a, const float* B, int64_t ldb,
                      int64_t stride_b, float beta, float* C, int64_t ldc, int64_t stride_c,
                      int64_t batches, const float* bias, int epilogue, hipStream_t st,
                      const char* who) {
+  CNHIP_REQUIRE(epilogue == CNHIP_EPI_NONE || epilogue == CNHIP_EPI_RELU, "%s: bad epilogue %d",
+                who, epilogue);
+  return gemm_f32_core(trans_a, trans_b, M, N, K, alpha, A, lda, stride_a, B, ldb, stride_b, beta,
+                       C, ldc, stride_c, batches, bias, epilogue, nullptr, nullptr, 0, st, who);
+}
+
+int gemm_f32_core(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float alpha,
+                  const float* A, int64_t lda, int64_t stride_a, const float* B, int64_t ldb,
+                  int64_t stride_b, float beta, float* C, int64_t ldc, int64_t stride_c,
+                  int64_t batches, const float* bias, int epilogue, const float* aux_in,
+                  float* aux_out, int64_t ld_aux, hipStream_t st, const char* who) {
   CNHIP_REQUIRE(M >= 0 && N >= 0 && K >= 0 && batches >= 0,
                 "%s: negative GEMM size (M=%lld N=%lld K=%lld batch=%lld)", who, (long long)M,
                 (long long)N, (long long)K, (long long)batches);
-  CNHIP_REQUIRE(epilogue == CNHIP_EPI_NONE || epilogue == CNHIP_EPI_RELU, "%s: bad epilogue %d",
-                who, epilogue);
   if (M == 0 || N == 0 || batches == 0) return CNHIP_OK;
   CNHIP_REQUIRE(C != nullptr, "%s: C is NULL", who);
   CNHIP_REQUIRE(ldc >= M, "%s: ldc=%lld < M=%lld", who, (long long)ldc, (long long)M);
@@ -375,6 +426,7 @@ int gemm_f32_batched(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, 
   g.B = B; g.ldb = ldb; g.stride_b = stride_b;
   g.C = C; g.ldc = ldc; g.stride_c = stride_c;
   g.alpha = alpha; g.beta = beta; g.bias = bias; g.epilogue = epilogue;
+  g.aux_in = aux_in; g.aux_out = aux_out; g.ld_aux = ld_aux;
   g.vec_ok = (lda % 4 == 0) && (ldb % 4 == 0) && (stride_a % 4 == 0) && (stride_b % 4 == 0) &&
              aligned16(A) && aligned16(B);
   g.c_vec_ok = (ldc % 4 == 0) && (stride_c % 4 == 0) && aligned16(C);
@@ -409,6 +461,22 @@ int gemm_f32(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float al
              int64_t ldc, const float* bias, int epilogue, hipStream_t st, const char* who) {
   return gemm_f32_batched(trans_a, trans_b, M, N, K, alpha, A, lda, 0, B, ldb, 0, beta, C, ldc, 0,
                           1, bias, epilogue, st, who);
+}
+
+int gemm_f32_act(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, const float* A,
+                 int64_t lda, const float* B, int64_t ldb, float* C, int64_t ldc, const float* bias,
+                 int epilogue, const float* aux_in, float* aux_out, int64_t ld_aux, hipStream_t st,
+                 const char* who) {
+  const bool needs_in = epilogue == EPI_DRELU || epilogue == EPI_DGELU;
+  CNHIP_REQUIRE(trans_a == 0 || epilogue < EPI_GELU, "%s: fused activations need trans_a == 0", who);
+  CNHIP_REQUIRE(epilogue == CNHIP_EPI_NONE || epilogue == CNHIP_EPI_RELU || epilogue == EPI_GELU ||
+                    needs_in,
+                "%s: bad epilogue %d", who, epilogue);
+  CNHIP_REQUIRE((epilogue != EPI_GELU || aux_out) && (!needs_in || aux_in) &&
+                    (!(aux_in || aux_out) || ld_aux >= M),
+                "%s: fused activation needs its [M,N] side tensor (ld >= M)", who);
+  return gemm_f32_core(trans_a, trans_b, M, N, K, 1.f, A, lda, 0, B, ldb, 0, 0.f, C, ldc, 0, 1, bias,
+                       epilogue, aux_in, aux_out, ld_aux, st, who);
 }
 
 // op(A) op(B) as split-K partial products P[s][m + M*n], s < *splits_out

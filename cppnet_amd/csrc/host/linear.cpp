@@ -52,6 +52,48 @@ namespace CppNet
             return out;
         }
 
+        DeviceTensor Linear::forward_act(const DeviceTensor& input, int act, DeviceTensor* pre_act)
+        {
+            if (input.rank() != 2 || input.dimension(1) != in_size_)
+                throw std::runtime_error("Shape mismatch: in layer: " + layer_name_ +
+                                         " input.dimension(1) must be equal weights_.dimension(0)!");
+            if (act == CNHIP_ACT_GELU && !pre_act)
+                throw std::invalid_argument("Linear::forward_act: GELU needs the pre-activation output");
+            in_cache_ = input;
+            const int64_t B = input.dimension(0);
+            DeviceTensor out = DeviceTensor::empty({B, out_size_});
+            DeviceTensor z;
+            if (act == CNHIP_ACT_GELU) z = DeviceTensor::empty({B, out_size_});
+            Device::check(cnhip_linear_forward_act(input.data(), W_.data(), bias_flag_ ? b_.data() : nullptr,
+                                                   out.data(), z.defined() ? z.data() : nullptr, B, in_size_,
+                                                   out_size_, act, Device::stream()),
+                          "Linear::forward_act");
+            if (pre_act) *pre_act = z;
+            return out;
+        }
+
+        DeviceTensor Linear::backward_act(const DeviceTensor& grad_output, int act, const DeviceTensor& act_aux)
+        {
+            if (grad_output.rank() != 2 || grad_output.dimension(1) != out_size_)
+                throw std::runtime_error("Output size mismatch in layer: " + layer_name_);
+            if (!in_cache_.defined() || in_cache_.dimension(0) != grad_output.dimension(0))
+                throw std::runtime_error("Linear::backward before forward (or batch mismatch) in layer: " +
+                                         layer_name_);
+            const int64_t B = grad_output.dimension(0);
+            if (act != CNHIP_ACT_NONE && act_aux.size() != B * in_size_)
+                throw std::runtime_error("Linear::backward_act: activation tensor does not match the input");
+            DeviceTensor dX = DeviceTensor::empty({B, in_size_});
+            const int accumulate = grads_zero_ ? 0 : 1;
+            Device::check(cnhip_linear_backward_act(in_cache_.data(), W_.data(), grad_output.data(), gW_.data(),
+                                                    bias_flag_ ? gb_.data() : nullptr, dX.data(),
+                                                    act == CNHIP_ACT_NONE ? nullptr : act_aux.data(), B,
+                                                    in_size_, out_size_, trainable_ ? 1 : 0, accumulate, act,
+                                                    Device::stream()),
+                          "Linear::backward_act");
+            if (trainable_) grads_zero_ = false;
+            return dX;
+        }
+
         DeviceTensor Linear::backward(const DeviceTensor& grad_output)
         {
             if (grad_output.rank() != 2 || grad_output.dimension(1) != out_size_)

@@ -1,6 +1,8 @@
 // SequentialModel over device tensors (ref: src/CppNet/models/models.cpp:13-101).
 #include "CppNet/models/models.hpp"
 
+#include "CppNet/activations/relu.hpp"
+
 #include <iostream>
 #include <string>
 
@@ -17,14 +19,44 @@ namespace CppNet
         DeviceTensor SequentialModel::forward(const DeviceTensor& input)
         {
             DeviceTensor x = input;
-            for (auto& s : steps_) x = s->forward(x);
+            for (std::size_t i = 0; i < steps_.size(); ++i)
+            {
+                Layers::Linear* lin = steps_[i]->linear();
+                Activations::Activation* next = i + 1 < steps_.size() ? steps_[i + 1]->activation() : nullptr;
+                if (lin && next)
+                {
+                    if (auto* relu = dynamic_cast<Activations::ReLU*>(next))
+                    {
+                        x = lin->forward_act(x, CNHIP_ACT_RELU);
+                        relu->set_output_cache(x);
+                        ++i;
+                        continue;
+                    }
+                }
+                x = steps_[i]->forward(x);
+            }
             return x;
         }
 
         DeviceTensor SequentialModel::backward(const DeviceTensor& grad_output)
         {
             DeviceTensor g = grad_output;
-            for (auto it = steps_.rbegin(); it != steps_.rend(); ++it) g = (*it)->backward(g);
+            for (std::size_t k = steps_.size(); k-- > 0;)
+            {
+                Layers::Linear* lin = steps_[k]->linear();
+                Activations::Activation* prev = k >= 1 ? steps_[k - 1]->activation() : nullptr;
+                if (lin && prev)
+                {
+                    auto* relu = dynamic_cast<Activations::ReLU*>(prev);
+                    if (relu && relu->output_cache().defined())
+                    {
+                        g = lin->backward_act(g, CNHIP_ACT_RELU, relu->output_cache());
+                        --k;
+                        continue;
+                    }
+                }
+                g = steps_[k]->backward(g);
+            }
             return g;
         }
 

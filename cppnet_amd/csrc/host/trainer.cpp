@@ -43,6 +43,8 @@ namespace
             const int64_t BS = dims[0] * dims[1], D = dims[2];
             DeviceTensor r = add_t(mha->forward(x, x, x), x, "encoder residual 1");
             DeviceTensor h = bn->forward(r.reshape({BS, D}));
+            // GELU runs as its own pass: fused into the GEMM epilogue it measured
+            // slower on MI355X (the erfc work serialises after the MFMA loop)
             DeviceTensor f = ff2->forward(gelu->forward(ff1->forward(h)));
             return add_t(f, h, "encoder residual 2").reshape(dims);
         }

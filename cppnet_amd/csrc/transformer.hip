@@ -20,6 +20,7 @@
 
 #include <cmath>
 
+#include "act_math.hpp"
 #include "common.hpp"
 
 namespace cnhip {
@@ -366,27 +367,18 @@ __global__ void __launch_bounds__(BNT) bn_bwd_kernel(const float* __restrict__ d
 }
 
 // ---------------------------------------------------------------- GELU / pool / add
-// GELU, exact form: Phi(x) = 0.5 (1 + erf(x/sqrt 2)) = 0.5 erfc(-x/sqrt 2); the
-// erfc form keeps full relative accuracy in the negative tail, where
-// 1 + erf(.) cancels.
 __global__ void __launch_bounds__(256) gelu_fwd_kernel(const float* __restrict__ x,
                                                        float* __restrict__ y, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    const float v = x[i];
-    y[i] = v * (0.5f * erfcf(v * -0.70710678118654752440f));
-  }
+       i += (int64_t)gridDim.x * blockDim.x)
+    y[i] = gelu_f(x[i]);
 }
 __global__ void __launch_bounds__(256) gelu_bwd_kernel(const float* __restrict__ x,
                                                        const float* __restrict__ dy,
                                                        float* __restrict__ dx, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    const float v = x[i];
-    const float cdf = 0.5f * erfcf(v * -0.70710678118654752440f);
-    const float pdf = 0.39894228040143267794f * expf(-0.5f * v * v);
-    dx[i] = dy[i] * (cdf + v * pdf);
-  }
+       i += (int64_t)gridDim.x * blockDim.x)
+    dx[i] = dy[i] * gelu_grad_f(x[i]);
 }
 
 // mean over s of [B,S,D].  For one feature d the [B, S] slab is contiguous

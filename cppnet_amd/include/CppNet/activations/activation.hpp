@@ -33,6 +33,9 @@ namespace CppNet
             DeviceTensor forward(const DeviceTensor& pre_activation) override;
             DeviceTensor backward(const DeviceTensor& grad_output) override;
             const DeviceTensor& output_cache() const { return out_cache_; }
+            /// The output of a forward computed elsewhere (a producing GEMM's
+            /// fused epilogue), cached as forward() would cache it.
+            void set_output_cache(const DeviceTensor& y) { out_cache_ = y; }
 
         protected:
             explicit OutputCachedActivation(const char* name) : name_(name) {}

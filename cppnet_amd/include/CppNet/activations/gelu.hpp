@@ -23,6 +23,10 @@ namespace CppNet
             using Activation::backward;
             DeviceTensor forward(const DeviceTensor& pre_activation) override;
             DeviceTensor backward(const DeviceTensor& grad_output) override;
+            const DeviceTensor& input_cache() const { return in_cache_; }
+            /// The input of a forward computed elsewhere (a producing GEMM's
+            /// fused epilogue), cached as forward() would cache it.
+            void set_input_cache(const DeviceTensor& x) { in_cache_ = x; }
 
         private:
             DeviceTensor in_cache_;

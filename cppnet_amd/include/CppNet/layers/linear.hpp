@@ -36,6 +36,17 @@ namespace CppNet
             Tensor<float, 2> backward(const Tensor<float, 2>& grad_output);
             DeviceTensor forward(const DeviceTensor& input);
             DeviceTensor backward(const DeviceTensor& grad_output);
+            /// forward() followed by activation act (CNHIP_ACT_RELU / _GELU) in
+            /// one GEMM epilogue; returns the activation's output.  For GELU,
+            /// *pre_act receives X W + b (what the GELU's backward reads).
+            DeviceTensor forward_act(const DeviceTensor& input, int act,
+                                     DeviceTensor* pre_act = nullptr);
+            /// backward() whose input gradient also carries the derivative of
+            /// activation act of the layer below: act_aux is that ReLU's output
+            /// or that GELU's input.  Equals backward() then the activation's
+            /// backward().
+            DeviceTensor backward_act(const DeviceTensor& grad_output, int act,
+                                      const DeviceTensor& act_aux);
 
             bool is_trainable() const override { return trainable_; }
             void step(Optimizers::Optimizer& optimizer, float learning_rate) override;

@@ -3,7 +3,11 @@
  * @brief SequentialModel (ref: include/CppNet/models/models.hpp:116-218,
  *        src/CppNet/models/models.cpp:13-101) over device tensors.
  *
- * Steps run in insertion order; backward in reverse.  zero_grad() resets
+ * Steps run in insertion order; backward in reverse.  A Linear followed by
+ * ReLU runs as one GEMM with the ReLU in its epilogue, and the next Linear's
+ * input-gradient GEMM applies the ReLU mask (same arithmetic as the separate
+ * calls).  GELU is not fused: its erfc epilogue measured slower than a
+ * separate pass on MI355X.  zero_grad() resets
  * every layer's gradients; update() steps every trainable layer, with all of
  * the optimizer's updates fused into one launch (begin_group/end_group).
  */
@@ -16,6 +20,7 @@
 #include <vector>
 
 #include "CppNet/activations/activation.hpp"
+#include "CppNet/layers/linear.hpp"
 #include "CppNet/core/tensor.hpp"
 #include "CppNet/layers/layer.hpp"
 #include "CppNet/optimizers/optimizer.hpp"
@@ -31,6 +36,8 @@ namespace CppNet
             virtual DeviceTensor backward(const DeviceTensor& grad_output) = 0;
             virtual bool is_trainable() const = 0;
             virtual void step(Optimizers::Optimizer& optimizer, float learning_rate) = 0;
+            virtual Layers::Linear* linear() { return nullptr; }
+            virtual Activations::Activation* activation() { return nullptr; }
             virtual ~Step() = default;
         };
 
@@ -43,6 +50,7 @@ namespace CppNet
             DeviceTensor backward(const DeviceTensor& g) override { return layer_->backward(g); }
             bool is_trainable() const override { return layer_->is_trainable(); }
             void step(Optimizers::Optimizer& o, float lr) override { layer_->step(o, lr); }
+            Layers::Linear* linear() override { return dynamic_cast<Layers::Linear*>(layer_.get()); }
 
         private:
             std::shared_ptr<LayerT> layer_;
@@ -56,6 +64,7 @@ namespace CppNet
             DeviceTensor backward(const DeviceTensor& g) override { return act_->backward(g); }
             bool is_trainable() const override { return false; }
             void step(Optimizers::Optimizer&, float) override {}
+            Activations::Activation* activation() override { return act_.get(); }
 
         private:
             std::shared_ptr<Activations::Activation> act_;

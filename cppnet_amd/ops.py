@@ -67,6 +67,23 @@ def linear_backward(X, W, dY, grad_W, grad_b, dX, batch: int, in_features: int,
                out_features, int(trainable), int(accumulate), _stream())
 
 
+ACT = {"none": 0, "relu": 1, "gelu": 2}
+
+
+def linear_forward_act(X, W, b, Y, Z, batch: int, in_features: int, out_features: int,
+                       act: str) -> None:
+    _capi.call("cnhip_linear_forward_act", _p(X), _p(W), _p(b), _p(Y), _p(Z), batch, in_features,
+               out_features, ACT[act], _stream())
+
+
+def linear_backward_act(X, W, dY, grad_W, grad_b, dX, act_aux, batch: int, in_features: int,
+                        out_features: int, act: str, trainable: bool = True,
+                        accumulate: bool = False) -> None:
+    _capi.call("cnhip_linear_backward_act", _p(X), _p(W), _p(dY), _p(grad_W), _p(grad_b), _p(dX),
+               _p(act_aux), batch, in_features, out_features, int(trainable), int(accumulate),
+               ACT[act], _stream())
+
+
 def column_sum(x, out, rows: int, cols: int, accumulate: bool = False) -> None:
     _capi.call("cnhip_column_sum", _p(x), _p(out), rows, cols, int(accumulate), _stream())
 

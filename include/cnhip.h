@@ -121,6 +121,28 @@ int cnhip_linear_backward(const float* X, const float* W, const float* dY,
                           int64_t batch, int64_t in_features,
                           int64_t out_features, int trainable, int accumulate,
                           cnhip_stream_t stream);
+/* Linear fused with the activation that follows it (the producing GEMM's
+ * epilogue applies it; no separate elementwise pass):
+ *   act CNHIP_ACT_RELU: Y = max(X W + b, 0)               (Z unused, may be NULL)
+ *   act CNHIP_ACT_GELU: Z = X W + b, Y = Z Phi(Z)         (Z is GELU's backward input)
+ * and the matching backward, whose dX GEMM applies the derivative of the
+ * activation on the layer BELOW (the one that produced this layer's input):
+ *   dX = (dY W^T) * [act_aux > 0]   (RELU: act_aux = that ReLU's output)
+ *   dX = (dY W^T) * gelu'(act_aux)  (GELU: act_aux = that GELU's input Z)
+ * Weight/bias grads as cnhip_linear_backward.  Results equal the unfused
+ * layer + activation calls (same arithmetic per element).
+ * ref: Linear::forward/backward (linear.cpp:148-358) chained with
+ * ReLU::forward/backward (relu.cpp:97-225); GELU has no reference. */
+#define CNHIP_ACT_NONE 0
+#define CNHIP_ACT_RELU 1
+#define CNHIP_ACT_GELU 2
+int cnhip_linear_forward_act(const float* X, const float* W, const float* b, float* Y,
+                             float* Z, int64_t batch, int64_t in_features,
+                             int64_t out_features, int act, cnhip_stream_t stream);
+int cnhip_linear_backward_act(const float* X, const float* W, const float* dY,
+                              float* grad_W, float* grad_b, float* dX, const float* act_aux,
+                              int64_t batch, int64_t in_features, int64_t out_features,
+                              int trainable, int accumulate, int act, cnhip_stream_t stream);
 /* out[j] (+)= sum_r in[r + rows*j]   — column sums of a ColMajor [rows,cols]
  * ref: src/CppNet/kernels/gpu/bias_grad.cu:12-46 */
 int cnhip_column_sum(const float* in, float* out, int64_t rows, int64_t cols,

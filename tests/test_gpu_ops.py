@@ -303,3 +303,48 @@ def test_gemm_batched_vs_oracle(gpu, oracle, ta, tb, M, N, K, batch):
         assert ok, f"batch {b}: {msg}"
         # padding between batch entries untouched
         np.testing.assert_array_equal(got[b * sc + ldc * N:(b + 1) * sc], C[b * sc + ldc * N:(b + 1) * sc])
+
+
+@pytest.mark.parametrize("act", ["relu", "gelu"])
+@pytest.mark.parametrize("B,I,O", [(64, 48, 40), (4096, 1024, 512), (37, 130, 19)])
+def test_linear_fused_activation_matches_unfused(gpu, oracle, act, B, I, O):
+    """Linear + activation in one GEMM epilogue, and the next layer's input
+    gradient with the activation derivative in its epilogue, equal the
+    separate Linear and activation calls bit for bit (same per-element
+    arithmetic, same GEMM plan), and the oracle within the contraction bar."""
+    print(f"[linear-act] {act} B={B} I={I} O={O}", flush=True)
+    rng = np.random.default_rng(B + I + O)
+    X, W, b = rnd(rng, B * I), rnd(rng, I * O, 1 / np.sqrt(I)), rnd(rng, O, 0.1)
+    dY = rnd(rng, B * O)
+    Y, Z = torch.empty(B * O, device="cuda"), torch.empty(B * O, device="cuda")
+    ops.linear_forward_act(dev(X), dev(W), dev(b), Y, Z, B, I, O, act)
+    Zu, Yu = torch.empty(B * O, device="cuda"), torch.empty(B * O, device="cuda")
+    ops.linear_forward(dev(X), dev(W), dev(b), Zu, B, I, O)
+    (ops.relu_forward if act == "relu" else ops.gelu_forward)(Zu, Yu)
+    np.testing.assert_array_equal(host(Y), host(Yu))
+    if act == "gelu":
+        np.testing.assert_array_equal(host(Z), host(Zu))
+    # backward of a Linear (I2 -> O) stacked on this activation: its dX carries act'
+    aux = Yu if act == "relu" else Zu
+    W2 = rnd(rng, O * I, 1 / np.sqrt(O))
+    gW, gb, dX = torch.empty(O * I, device="cuda"), torch.empty(I, device="cuda"), torch.empty(B * O, device="cuda")
+    dY2 = dev(rnd(rng, B * I))
+    ops.linear_backward_act(Yu, dev(W2), dY2, gW, gb, dX, aux, B, O, I, act)
+    gWu, gbu, dXu = torch.empty(O * I, device="cuda"), torch.empty(I, device="cuda"), torch.empty(B * O, device="cuda")
+    ops.linear_backward(Yu, dev(W2), dY2, gWu, gbu, dXu, B, O, I, True, False)
+    dZ = torch.empty(B * O, device="cuda")
+    if act == "relu":
+        ops.relu_backward(aux, dXu, dZ)
+    else:
+        ops.gelu_backward(aux, dXu, dZ)
+    np.testing.assert_array_equal(host(dX), host(dZ))
+    np.testing.assert_array_equal(host(gW), host(gWu))
+    np.testing.assert_array_equal(host(gb), host(gbu))
+    # forward against the oracle (Linear then the activation)
+    rz = np.zeros(B * O, np.float32)
+    oracle.cnref_linear_forward(fp(X), fp(W), fp(b), fp(rz), B, I, O)
+    ry = np.zeros_like(rz)
+    (oracle.cnref_relu_forward if act == "relu" else oracle.cnref_gelu_forward)(fp(rz), fp(ry), rz.size)
+    mag = gemm_mag(oracle, 0, 0, B, O, I, X, B, W, I, B)
+    ok, msg = close_mag(host(Y), ry, mag, 1e-4, 1e-5)
+    assert ok, msg
