@@ -43,26 +43,33 @@ def log(*a):
 
 
 # ---------------------------------------------------------------- workloads
+# Step flops = forward + weight gradients + input gradients (3x the forward
+# products), less the first layer's input gradient: the train step does not
+# compute it (its input is data), so it is not counted as work done.
 def _mlp_flops(cfg):
-    return 6.0 * cfg.batch * sum(i * o for i, o in zip(cfg.sizes[:-1], cfg.sizes[1:]))
+    per_layer = [2.0 * cfg.batch * i * o for i, o in zip(cfg.sizes[:-1], cfg.sizes[1:])]
+    return 3 * sum(per_layer) - per_layer[0]
 
 
 def _cnn_flops(cfg):
     N, C, H, W = cfg.input_shape
-    fwd = 0.0
+    fwd, first = 0.0, None
     for (ic, oc, k, s, p) in cfg.convs:
         HO, WO = (H + 2 * p - k) // s + 1, (W + 2 * p - k) // s + 1
-        fwd += 2.0 * N * HO * WO * oc * ic * k * k
+        f = 2.0 * N * HO * WO * oc * ic * k * k
+        first = f if first is None else first
+        fwd += f
         H, W = (HO - cfg.pool) // cfg.pool + 1, (WO - cfg.pool) // cfg.pool + 1
     fwd += 2.0 * N * cfg.flat_features() * cfg.classes
-    return 3 * fwd
+    return 3 * fwd - first
 
 
 def _rnn_flops(cfg):
     G = (4 if cfg.cell == "lstm" else 3) * cfg.hidden
-    fwd = 2.0 * cfg.batch * cfg.seq_len * (cfg.input_size + cfg.hidden) * G
+    x_proj = 2.0 * cfg.batch * cfg.seq_len * cfg.input_size * G
+    fwd = x_proj + 2.0 * cfg.batch * cfg.seq_len * cfg.hidden * G
     fwd += 2.0 * cfg.batch * cfg.hidden * cfg.out_features
-    return 3 * fwd
+    return 3 * fwd - x_proj
 
 
 def _tr_flops(cfg):

@@ -7,6 +7,10 @@
 
 namespace cnhip {
 
+// ReLU forward, max(0, x) (relu.cpp:97-160); one expression for the
+// elementwise kernel and every fused epilogue, so they agree on signed zeros.
+__device__ __forceinline__ float relu_f(float x) { return fmaxf(0.f, x); }
+
 // ReLU backward mask from the cached OUTPUT (relu_grad.cu:11-19): dy * [y > 0]
 __device__ __forceinline__ float relu_mask(float y) { return y > 0.f ? 1.f : 0.f; }
 

@@ -1,4 +1,4 @@
-// Conv2D as implicit GEMMs on the fp32 MFMA tile engine (mfma_core.hpp).
+// Conv2D as implicit GEMMs on the fp32 MFMA tile engine (mfma_kpack.hpp).
 //
 // ref: Conv2D::forward/backward, src/CppNet/layers/conv2d.cpp:78-198 (the
 // semantics), conv2d_forward.cu:16-64 / conv2d_backward.cu:19-68 (the
@@ -12,31 +12,30 @@
 //   dgrad    dX_pix[N, C]  = A'[N, K'] * Wd      A'(n,k') = dY(n, oc, oh, ow), k' = oc + OC*t
 //   wgrad    dW[OC, K | 1] = dY^T * [X | 1]      contraction over (n, pixel) pairs; the
 //                                                extra ones-column yields the bias grad
-// A and A' are gathered straight from HBM with float4 loads along the batch
-// (contiguous), so no im2col buffer exists.  wgrad splits its long
-// contraction over blocks and sums the partials in a fixed order.  Grads are
+// Forward and dgrad run one GEMM per pixel (blockIdx.y).  With the pixel
+// fixed, A's column k is one fixed element offset of X (dY), or padding; a
+// table of those offsets is built in LDS once per block, so the K loop does
+// no index arithmetic: each 16-byte LDS chunk of A is four coalesced dword
+// gathers along the batch at offsets read with one ds_read_b128.  No im2col
+// buffer exists.  wgrad contracts over k = n + N*q; when N is a multiple of
+// the k-tile depth, a k-tile lies inside one output pixel q, so both of its
+// operands are plain k-contiguous float4 loads with one decode per tile.
+// wgrad splits its long contraction over blocks (and, for small tiles, over
+// the waves of a block) and sums the partials in a fixed order.  Grads are
 // overwritten, as the reference zeroes them first (conv2d.cpp:149-152).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
 
+#include "act_math.hpp"
 #include "common.hpp"
-#include "mfma_core.hpp"
+#include "mfma_kpack.hpp"
 
 namespace cnhip {
 namespace {
 
-using mfma::BK;
-using mfma::f32x16;
-using mfma::f32x4;
-using mfma::TileCfg;
-
-using Cfg11 = TileCfg<1, 1, 1, 1>;  // 32 x 32, one wave
-using CfgSN = TileCfg<4, 1, 1, 1>;  // 128 x 32
-using CfgSM = TileCfg<1, 4, 1, 1>;  // 32 x 128
-using CfgM = TileCfg<2, 2, 2, 1>;   // 128 x 64
-using CfgS = TileCfg<2, 2, 1, 1>;   // 64 x 64
-using CfgL = TileCfg<2, 2, 2, 2>;   // 128 x 128
+using kp::f32x16;
+using kp::f32x4;
 
 struct ConvDims {
   int64_t N, C, H, W, OC, KS, S, P, HO, WO;
@@ -44,126 +43,151 @@ struct ConvDims {
 
 struct ConvArgs {
   ConvDims d;
-  const float* X;     // forward / wgrad input
-  const float* Wt;    // forward weights [OC, K]
-  const float* Wd;    // dgrad weights relaid [K' = OC*T, C]
-  const float* dY;    // dgrad / wgrad upstream grad
+  const float* src;   // gathered operand: X (forward, wgrad) / dY (dgrad)
+  const float* wt;    // forward W [OC, K] / dgrad Wd [K', C] (k-contiguous rows)
+  const float* dY;    // wgrad A
   const float* bias;  // forward bias or null
   float* out;         // Y (forward) / dX (dgrad)
-  float* partial;     // wgrad split partials [splits][M*Ng]
+  float* partial;     // wgrad split partials [splits][OC * Ng]
   int64_t k_per_split;
+  int relu;           // forward: ReLU in the epilogue
   int has_bias;       // wgrad: adds the ones-column
-  int nvec;           // N % 4 == 0 and the tensors read along n are 16-byte aligned
+  int out_vec;        // N % 4 == 0 and out 16-byte aligned
+  int wt_vec;         // dgrad: Wd rows 16-byte aligned
+  int aligned;        // wgrad: N % KT == 0 and X, dY 16-byte aligned
 };
 
-// Generic block loop: stage A/B tiles through LDS with the given loaders and
-// accumulate.  LoadA/LoadB fill one float4 slot (rr, kk) of the tile.
-template <class Cfg, bool AK, bool BKC, class LoadA, class LoadB>
-__device__ __forceinline__ void igemm_mainloop(int64_t k_begin, int64_t k_end, LoadA&& la,
-                                               LoadB&& lb, float* lds_a, float* lds_b,
-                                               f32x16 (&acc)[Cfg::WM][Cfg::WN]) {
-  using SA = mfma::TileSlots<AK, Cfg::BM, Cfg::NT>;
-  using SB = mfma::TileSlots<BKC, Cfg::BN, Cfg::NT>;
-  constexpr int TA = BK * Cfg::LDA, TB = BK * Cfg::LDB;
-  f32x4 ra[SA::PER_THREAD], rb[SB::PER_THREAD];
-  auto load = [&](int64_t k0) {
-#pragma unroll
-    for (int p = 0; p < SA::PER_THREAD; ++p) {
-      int rr, kk;
-      if (!SA::slot(p, rr, kk)) break;
-      ra[p] = la(rr, k0 + kk);
-    }
-#pragma unroll
-    for (int p = 0; p < SB::PER_THREAD; ++p) {
-      int rr, kk;
-      if (!SB::slot(p, rr, kk)) break;
-      rb[p] = lb(rr, k0 + kk);
-    }
-  };
-  const int ntiles = k_end > k_begin ? (int)((k_end - k_begin + BK - 1) / BK) : 0;
-  if (ntiles > 0) {
-    load(k_begin);
-    SA::store(lds_a, ra);
-    SB::store(lds_b, rb);
+// Capacity of the per-block gather table (ints, 18 KiB of LDS).
+constexpr int KTBL = 4608;
+
+// Element offset of A(0, k) in the gathered tensor at pixel (q1, q2), or -1
+// where the term is zero.  Forward: X at output pixel (oh, ow) = (q1, q2);
+// dgrad: dY at input pixel (h, w) = (q1, q2), where output pixel (oh, ow)
+// reads (h, w) through tap t = kh + KS*kw when oh*S - P + kh = h.
+template <bool DGRAD, class I>
+__device__ __forceinline__ I gather_off(const ConvDims& d, I q1, I q2, I k) {
+  if (!DGRAD) {
+    const I C = (I)d.C, KS = (I)d.KS;
+    const I ic = k % C, t = k / C;
+    const I ih = q1 * (I)d.S - (I)d.P + t % KS, iw = q2 * (I)d.S - (I)d.P + t / KS;
+    if (ih < 0 || ih >= (I)d.H || iw < 0 || iw >= (I)d.W) return -1;
+    return (I)d.N * (ic + C * (ih + (I)d.H * iw));
   }
-  __syncthreads();
-  for (int kt = 0; kt < ntiles; ++kt) {
-    const int cur = kt & 1;
-    const bool has_next = kt + 1 < ntiles;
-    if (has_next) load(k_begin + (int64_t)(kt + 1) * BK);
-    mfma::mfma_ktile<Cfg>(lds_a + cur * TA, lds_b + cur * TB, acc);
-    if (has_next) {
-      SA::store(lds_a + (cur ^ 1) * TA, ra);
-      SB::store(lds_b + (cur ^ 1) * TB, rb);
+  const I OC = (I)d.OC, KS = (I)d.KS, S = (I)d.S;
+  const I oc = k % OC, t = k / OC;
+  const I ohn = q1 + (I)d.P - t % KS, own = q2 + (I)d.P - t / KS;
+  if (ohn < 0 || own < 0 || ohn % S != 0 || own % S != 0) return -1;
+  const I oh = ohn / S, ow = own / S;
+  if (oh >= (I)d.HO || ow >= (I)d.WO) return -1;
+  return (I)d.N * (oc + OC * (oh + (I)d.HO * ow));
+}
+
+// ------------------------------------------------------- forward / dgrad
+// Stage for kp::pipeline.  A(n, k) = src[n + off(k)] (rows contiguous along
+// the batch); B = W (forward: B(oc, k) = W[oc + OC*k], contiguous along oc)
+// or Wd (dgrad: B(ic, k) = Wd[k + K'*ic], contiguous along k).
+template <class C, bool DGRAD, bool TBL, bool FAST>
+struct PixelStage {
+  using OA = kp::Operand<false, C::BM, C::NT, C::KT>;
+  using OB = kp::Operand<DGRAD, C::BN, C::NT, C::KT>;
+  const ConvArgs& a;
+  const int* tbl;
+  int64_t m0, n0, K, q1, q2;
+  f32x4 ra[2][OA::REGS], rb[2][OB::REGS];
+
+  __device__ PixelStage(const ConvArgs& a_, const int* tbl_, int64_t m0_, int64_t n0_, int64_t K_,
+                        int64_t q1_, int64_t q2_)
+      : a(a_), tbl(tbl_), m0(m0_), n0(n0_), K(K_), q1(q1_), q2(q2_) {}
+
+  template <int S>
+  __device__ __forceinline__ void load(int t) {
+    const ConvDims& d = a.d;
+    const int64_t k0 = (int64_t)t * C::KT;
+#pragma unroll
+    for (int p = 0; p < OA::PER; ++p) {
+      int r, k;
+      if (!OA::origin(p, r, k)) break;
+      const int64_t row = m0 + r, gk = k0 + k;
+      int64_t o[4];
+      if (TBL) {  // padded with -1 up to a whole number of k-tiles
+        const int4 v = *reinterpret_cast<const int4*>(tbl + gk);
+        o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = gk + j < K ? gather_off<DGRAD, int64_t>(d, q1, q2, gk + j) : -1;
+      }
+      f32x4 v;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] = (o[j] >= 0 && (FAST || row < d.N)) ? a.src[o[j] + row] : 0.f;
+      ra[S][p] = v;
     }
+    if (DGRAD)
+      OB::template load<FAST>(a.wt, K, n0, k0, d.C, K, rb[S]);
+    else
+      OB::template load<FAST>(a.wt, d.OC, n0, k0, d.OC, K, rb[S]);
+  }
+  template <int S>
+  __device__ __forceinline__ void store(float* buf) {
+    OA::store(buf, ra[S]);
+    OB::store(buf + C::BM * C::LDK, rb[S]);
+  }
+};
+
+template <class C, bool DGRAD, bool TBL>
+__global__ void __launch_bounds__(C::NT) conv_pixel_kernel(ConvArgs a) {
+  __shared__ __align__(16) float lds[2 * C::LDS_FLOATS];
+  __shared__ __align__(16) int tbl[TBL ? KTBL : 4];
+  const ConvDims& d = a.d;
+  const int64_t Ng = DGRAD ? d.C : d.OC;
+  const int64_t K = (DGRAD ? d.OC : d.C) * d.KS * d.KS;
+  const int nbm = (int)((d.N + C::BM - 1) / C::BM);
+  const int64_t m0 = (int64_t)(blockIdx.x % nbm) * C::BM;
+  const int64_t n0 = (int64_t)(blockIdx.x / nbm) * C::BN;
+  const int64_t q = blockIdx.y, HQ = DGRAD ? d.H : d.HO;
+  const int64_t q1 = q % HQ, q2 = q / HQ;
+  const int ntiles = (int)((K + C::KT - 1) / C::KT);
+  if (TBL) {  // host guarantees ntiles * KT <= KTBL and 32-bit offsets
+    for (int k = threadIdx.x; k < ntiles * C::KT; k += C::NT)
+      tbl[k] = k < K ? gather_off<DGRAD, int>(d, (int)q1, (int)q2, k) : -1;
     __syncthreads();
   }
-}
+  const bool fast = m0 + C::BM <= d.N && n0 + C::BN <= Ng && K % C::KT == 0 && (!DGRAD || a.wt_vec);
+  f32x16 acc[C::WM][C::WN];
+  kp::zero_acc<C>(acc);
+  if (fast) {
+    PixelStage<C, DGRAD, TBL, true> s(a, tbl, m0, n0, K, q1, q2);
+    kp::pipeline<C>(ntiles, lds, s, acc);
+  } else {
+    PixelStage<C, DGRAD, TBL, false> s(a, tbl, m0, n0, K, q1, q2);
+    kp::pipeline<C>(ntiles, lds, s, acc);
+  }
 
-// float4 of X[base + n .. n+3] along the batch, zero past N.
-__device__ __forceinline__ f32x4 load_n4(const float* __restrict__ base, int64_t n, int64_t N,
-                                         bool vec) {
-  if (vec && n + 3 < N) return *reinterpret_cast<const f32x4*>(base + n);
-  f32x4 v;
+  float* out = a.out + d.N * Ng * q;  // out_pix(n, c) = out[n + N*c]
+  kp::for_each_acc_run<C>(acc, [&](int ml, int nl, const f32x4& v) {
+    const int64_t n = m0 + ml, c = n0 + nl;
+    if (c >= Ng) return;
+    f32x4 o = v;
+    if (!DGRAD) {
+      if (a.bias) {
+        const float b = a.bias[c];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) v[j] = (n + j < N) ? base[n + j] : 0.f;
-  return v;
-}
-
-// ---------------------------------------------------------------- forward
-template <class Cfg>
-__global__ void __launch_bounds__(Cfg::NT) conv_fwd_kernel(ConvArgs a) {
-  __shared__ float lds_a[2 * BK * Cfg::LDA];
-  __shared__ float lds_b[2 * BK * Cfg::LDB];
-  const ConvDims d = a.d;
-  const int64_t K = d.C * d.KS * d.KS;
-  const int nbm = (int)((d.N + Cfg::BM - 1) / Cfg::BM);
-  const int64_t m0 = (int64_t)(blockIdx.x % nbm) * Cfg::BM;
-  const int64_t n0 = (int64_t)(blockIdx.x / nbm) * Cfg::BN;
-  const int64_t q = blockIdx.y, oh = q % d.HO, ow = q / d.HO;
-  const bool vec = a.nvec;
-
-  auto la = [&](int rr, int64_t k) -> f32x4 {
-    if (k >= K) return f32x4{0.f, 0.f, 0.f, 0.f};
-    const int64_t ic = k % d.C, t = k / d.C;
-    const int64_t ih = oh * d.S - d.P + t % d.KS, iw = ow * d.S - d.P + t / d.KS;
-    if (ih < 0 || ih >= d.H || iw < 0 || iw >= d.W) return f32x4{0.f, 0.f, 0.f, 0.f};
-    return load_n4(a.X + d.N * (ic + d.C * (ih + d.H * iw)), m0 + rr, d.N, vec);
-  };
-  // B(k, oc) = W[oc + OC*k]: contiguous along oc
-  auto lb = [&](int rr, int64_t k) -> f32x4 {
-    const int64_t oc = n0 + rr;
-    if (k >= K) return f32x4{0.f, 0.f, 0.f, 0.f};
-    const float* base = a.Wt + d.OC * k;
-    if ((d.OC & 3) == 0 && oc + 3 < d.OC) return *reinterpret_cast<const f32x4*>(base + oc);
-    f32x4 v;
+        for (int e = 0; e < 4; ++e) o[e] = v[e] + b;
+      }
+      if (a.relu) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) v[j] = (oc + j < d.OC) ? base[oc + j] : 0.f;
-    return v;
-  };
-  f32x16 acc[Cfg::WM][Cfg::WN];
-  mfma::zero_acc<Cfg>(acc);
-  igemm_mainloop<Cfg, false, false>(0, K, la, lb, lds_a, lds_b, acc);
-
-  float* Y = a.out + d.N * d.OC * q;  // Y_pix(n, oc) = Y[n + N*oc] at this pixel
-  mfma::for_each_acc_run<Cfg>(acc, [&](int ml, int nl, const f32x4& v) {
-    const int64_t n = m0 + ml, oc = n0 + nl;
-    if (oc >= d.OC) return;
-    const float b = a.bias ? a.bias[oc] : 0.f;
-    if (vec && n + 3 < d.N) {
-      f32x4 o;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = a.bias ? v[e] + b : v[e];
-      *reinterpret_cast<f32x4*>(Y + n + d.N * oc) = o;
+        for (int e = 0; e < 4; ++e) o[e] = relu_f(o[e]);
+      }
+    }
+    if (a.out_vec && n + 3 < d.N) {
+      *reinterpret_cast<f32x4*>(out + n + d.N * c) = o;
     } else {
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        if (n + e < d.N) Y[n + e + d.N * oc] = a.bias ? v[e] + b : v[e];
+        if (n + e < d.N) out[n + e + d.N * c] = o[e];
     }
   });
 }
 
-// ---------------------------------------------------------------- dgrad
 // Wd[k' + K'*ic] = W[oc + OC*(ic + C*t)], k' = oc + OC*t
 __global__ void __launch_bounds__(256) conv_relayout_w_kernel(const float* __restrict__ Wt,
                                                               float* __restrict__ Wd, int64_t OC,
@@ -176,131 +200,152 @@ __global__ void __launch_bounds__(256) conv_relayout_w_kernel(const float* __res
   }
 }
 
-template <class Cfg>
-__global__ void __launch_bounds__(Cfg::NT) conv_dgrad_kernel(ConvArgs a) {
-  __shared__ float lds_a[2 * BK * Cfg::LDA];
-  __shared__ float lds_b[2 * BK * Cfg::LDB];
-  const ConvDims d = a.d;
-  const int64_t T = d.KS * d.KS, Kp = d.OC * T;
-  const int nbm = (int)((d.N + Cfg::BM - 1) / Cfg::BM);
-  const int64_t m0 = (int64_t)(blockIdx.x % nbm) * Cfg::BM;
-  const int64_t n0 = (int64_t)(blockIdx.x / nbm) * Cfg::BN;
-  const int64_t q = blockIdx.y, h = q % d.H, w = q / d.H;
-  const bool vec = a.nvec;
-
-  // A'(n, k') = dY(n, oc, oh, ow) where (oh, ow) is the output pixel whose
-  // tap t = kh + KS*kw reads input (h, w): oh*S - P + kh = h.
-  auto la = [&](int rr, int64_t k) -> f32x4 {
-    if (k >= Kp) return f32x4{0.f, 0.f, 0.f, 0.f};
-    const int64_t oc = k % d.OC, t = k / d.OC;
-    const int64_t ohn = h + d.P - t % d.KS, own = w + d.P - t / d.KS;
-    if (ohn < 0 || own < 0 || ohn % d.S != 0 || own % d.S != 0) return f32x4{0.f, 0.f, 0.f, 0.f};
-    const int64_t oh = ohn / d.S, ow = own / d.S;
-    if (oh >= d.HO || ow >= d.WO) return f32x4{0.f, 0.f, 0.f, 0.f};
-    return load_n4(a.dY + d.N * (oc + d.OC * (oh + d.HO * ow)), m0 + rr, d.N, vec);
-  };
-  // B(k', ic) = Wd[k' + K'*ic]: contiguous along k'
-  auto lb = [&](int rr, int64_t k) -> f32x4 {
-    const int64_t ic = n0 + rr;
-    if (ic >= d.C) return f32x4{0.f, 0.f, 0.f, 0.f};
-    const float* base = a.Wd + Kp * ic;
-    if ((Kp & 3) == 0 && k + 3 < Kp) return *reinterpret_cast<const f32x4*>(base + k);
-    f32x4 v;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) v[j] = (k + j < Kp) ? base[k + j] : 0.f;
-    return v;
-  };
-  f32x16 acc[Cfg::WM][Cfg::WN];
-  mfma::zero_acc<Cfg>(acc);
-  igemm_mainloop<Cfg, false, true>(0, Kp, la, lb, lds_a, lds_b, acc);
-
-  float* dX = a.out + d.N * d.C * q;
-  mfma::for_each_acc_run<Cfg>(acc, [&](int ml, int nl, const f32x4& v) {
-    const int64_t n = m0 + ml, ic = n0 + nl;
-    if (ic >= d.C) return;
-    if (vec && n + 3 < d.N) {
-      *reinterpret_cast<f32x4*>(dX + n + d.N * ic) = v;
-    } else {
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (n + e < d.N) dX[n + e + d.N * ic] = v[e];
-    }
-  });
-}
-
 // ---------------------------------------------------------------- wgrad
 // M = OC, Ng = C*T (+1 ones-column for the bias), contraction index
 // k = n + N*q over (sample, output pixel); split over blockIdx.z.
-template <class Cfg>
-__global__ void __launch_bounds__(Cfg::NT) conv_wgrad_kernel(ConvArgs a) {
-  __shared__ float lds_a[2 * BK * Cfg::LDA];
-  __shared__ float lds_b[2 * BK * Cfg::LDB];
-  const ConvDims d = a.d;
+// A(oc, k) = dY[n + N*(oc + OC*q)], B(j, k) = X(n, ic, ih, iw) for
+// j = ic + C*t < CT, 1 for j == CT: both contiguous along k within a pixel.
+template <class C, bool ALIGNED, bool FAST>
+struct WgradStage {
+  using OA = kp::Operand<true, C::BM, C::NT, C::KT>;
+  using OB = kp::Operand<true, C::BN, C::NT, C::KT>;
+  const ConvArgs& a;
+  int64_t m0, n0, k_begin, k_end;
+  int bic[OB::PER], bkh[OB::PER], bkw[OB::PER];  // row j of each B unit; bic -1: zero, -2: ones
+  f32x4 ra[2][OA::REGS], rb[2][OB::REGS];
+
+  __device__ WgradStage(const ConvArgs& a_, int64_t m0_, int64_t n0_, int64_t kb, int64_t ke)
+      : a(a_), m0(m0_), n0(n0_), k_begin(kb), k_end(ke) {
+    const ConvDims& d = a.d;
+    const int64_t CT = d.C * d.KS * d.KS;
+#pragma unroll
+    for (int p = 0; p < OB::PER; ++p) {
+      int r, k;
+      bic[p] = -1;
+      bkh[p] = bkw[p] = 0;
+      if (!OB::origin(p, r, k)) break;
+      const int64_t j = n0 + r;
+      if (j < CT) {
+        const int64_t t = j / d.C;
+        bic[p] = (int)(j % d.C);
+        bkh[p] = (int)(t % d.KS);
+        bkw[p] = (int)(t / d.KS);
+      } else if (j == CT && a.has_bias) {
+        bic[p] = -2;
+      }
+    }
+  }
+
+  template <int S>
+  __device__ __forceinline__ void load(int t) {
+    const ConvDims& d = a.d;
+    const int64_t k0 = k_begin + (int64_t)t * C::KT;
+    if (ALIGNED) {
+      // the whole k-tile lies in output pixel q (N % KT == 0), and every
+      // tile of the split is full (k_per_split and N*HO*WO are multiples of KT)
+      const int N = (int)d.N, HO = (int)d.HO;
+      const int q = (int)(k0 / N), nb = (int)(k0 - (int64_t)q * N);
+      const int oh = q % HO, ow = q / HO;
+      OA::template load<FAST>(a.dY + nb + d.N * d.OC * q, d.N, m0, 0, d.OC, C::KT, ra[S]);
+      const int ih0 = oh * (int)d.S - (int)d.P, iw0 = ow * (int)d.S - (int)d.P;
+#pragma unroll
+      for (int p = 0; p < OB::PER; ++p) {
+        int r, k;
+        if (!OB::origin(p, r, k)) break;
+        f32x4 v{0.f, 0.f, 0.f, 0.f};
+        if (bic[p] == -2) {
+          v = f32x4{1.f, 1.f, 1.f, 1.f};
+        } else if (bic[p] >= 0) {
+          const int ih = ih0 + bkh[p], iw = iw0 + bkw[p];
+          if (ih >= 0 && ih < (int)d.H && iw >= 0 && iw < (int)d.W)
+            v = *reinterpret_cast<const f32x4*>(a.src + nb + k +
+                                                d.N * (bic[p] + d.C * (ih + d.H * (int64_t)iw)));
+        }
+        rb[S][p] = v;
+      }
+    } else {
+      // general N: decode (n, q) per element
+#pragma unroll
+      for (int p = 0; p < OA::PER; ++p) {
+        int r, k;
+        if (!OA::origin(p, r, k)) break;
+        const int64_t oc = m0 + r;
+        f32x4 v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int64_t kk = k0 + k + j;
+          if (oc < d.OC && kk < k_end) {
+            const int64_t n = kk % d.N, q = kk / d.N;
+            v[j] = a.dY[n + d.N * (oc + d.OC * q)];
+          }
+        }
+        ra[S][p] = v;
+      }
+#pragma unroll
+      for (int p = 0; p < OB::PER; ++p) {
+        int r, k;
+        if (!OB::origin(p, r, k)) break;
+        f32x4 v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int64_t kk = k0 + k + j;
+          if (kk >= k_end || bic[p] == -1) continue;
+          if (bic[p] == -2) {
+            v[j] = 1.f;
+            continue;
+          }
+          const int64_t n = kk % d.N, q = kk / d.N;
+          const int64_t ih = (q % d.HO) * d.S - d.P + bkh[p], iw = (q / d.HO) * d.S - d.P + bkw[p];
+          if (ih >= 0 && ih < d.H && iw >= 0 && iw < d.W)
+            v[j] = a.src[n + d.N * (bic[p] + d.C * (ih + d.H * iw))];
+        }
+        rb[S][p] = v;
+      }
+    }
+  }
+  template <int S>
+  __device__ __forceinline__ void store(float* buf) {
+    OA::store(buf, ra[S]);
+    OB::store(buf + C::BM * C::LDK, rb[S]);
+  }
+};
+
+template <class C, bool ALIGNED>
+__global__ void __launch_bounds__(C::NT) conv_wgrad_kernel(ConvArgs a) {
+  __shared__ __align__(16) float lds[2 * C::LDS_FLOATS];
+  static_assert((C::WGK - 1) * C::WGM * C::WGN * C::WM * C::WN * 1024 <= 2 * C::LDS_FLOATS,
+                "reduce_wgk needs more LDS than the operand buffers");
+  const ConvDims& d = a.d;
   const int64_t CT = d.C * d.KS * d.KS, Ng = CT + a.has_bias, Kc = d.N * d.HO * d.WO;
-  const int nbm = (int)((d.OC + Cfg::BM - 1) / Cfg::BM);
-  const int64_t m0 = (int64_t)(blockIdx.x % nbm) * Cfg::BM;
-  const int64_t n0 = (int64_t)(blockIdx.x / nbm) * Cfg::BN;
+  const int nbm = (int)((d.OC + C::BM - 1) / C::BM);
+  const int64_t m0 = (int64_t)(blockIdx.x % nbm) * C::BM;
+  const int64_t n0 = (int64_t)(blockIdx.x / nbm) * C::BN;
   const int64_t k_begin = (int64_t)blockIdx.z * a.k_per_split;
   const int64_t k_end = min(Kc, k_begin + a.k_per_split);
-  // float4s along k stay inside one output pixel when N % 4 == 0 (k starts at
-  // multiples of 4)
-  const bool vec = a.nvec;
-
-  // A(oc, k) = dY[n + N*(oc + OC*q)]
-  auto la = [&](int rr, int64_t k) -> f32x4 {
-    const int64_t oc = m0 + rr;
-    f32x4 v{0.f, 0.f, 0.f, 0.f};
-    if (oc >= d.OC) return v;
-    if (vec && k + 3 < k_end) {
-      const int64_t n = k % d.N, q = k / d.N;
-      return *reinterpret_cast<const f32x4*>(a.dY + n + d.N * (oc + d.OC * q));
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t kj = k + j;
-      if (kj < k_end) v[j] = a.dY[kj % d.N + d.N * (oc + d.OC * (kj / d.N))];
-    }
-    return v;
-  };
-  // B(k, j) = X(n, ic, ih, iw) for j = ic + C*t < CT; 1 for the bias column
-  auto lb = [&](int rr, int64_t k) -> f32x4 {
-    const int64_t j = n0 + rr;
-    f32x4 v{0.f, 0.f, 0.f, 0.f};
-    if (j >= Ng) return v;
-    if (j == CT) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = (k + e < k_end) ? 1.f : 0.f;
-      return v;
-    }
-    const int64_t ic = j % d.C, t = j / d.C, kh = t % d.KS, kw = t / d.KS;
-    if (vec && k + 3 < k_end) {
-      const int64_t n = k % d.N, q = k / d.N;
-      const int64_t ih = (q % d.HO) * d.S - d.P + kh, iw = (q / d.HO) * d.S - d.P + kw;
-      if (ih < 0 || ih >= d.H || iw < 0 || iw >= d.W) return v;
-      return *reinterpret_cast<const f32x4*>(a.X + n + d.N * (ic + d.C * (ih + d.H * iw)));
-    }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int64_t kj = k + e;
-      if (kj >= k_end) break;
-      const int64_t n = kj % d.N, q = kj / d.N;
-      const int64_t ih = (q % d.HO) * d.S - d.P + kh, iw = (q / d.HO) * d.S - d.P + kw;
-      if (ih >= 0 && ih < d.H && iw >= 0 && iw < d.W)
-        v[e] = a.X[n + d.N * (ic + d.C * (ih + d.H * iw))];
-    }
-    return v;
-  };
-  f32x16 acc[Cfg::WM][Cfg::WN];
-  mfma::zero_acc<Cfg>(acc);
-  igemm_mainloop<Cfg, true, true>(k_begin, k_end, la, lb, lds_a, lds_b, acc);
+  const int ntiles = k_end > k_begin ? (int)((k_end - k_begin + C::KT - 1) / C::KT) : 0;
+  f32x16 acc[C::WM][C::WN];
+  kp::zero_acc<C>(acc);
+  if (ALIGNED && m0 + C::BM <= d.OC) {
+    WgradStage<C, ALIGNED, true> s(a, m0, n0, k_begin, k_end);
+    kp::pipeline<C>(ntiles, lds, s, acc);
+  } else {
+    WgradStage<C, ALIGNED, false> s(a, m0, n0, k_begin, k_end);
+    kp::pipeline<C>(ntiles, lds, s, acc);
+  }
+  kp::reduce_wgk<C>(lds, acc);
 
   float* P = a.partial + (int64_t)blockIdx.z * d.OC * Ng;
-  mfma::for_each_acc_run<Cfg>(acc, [&](int ml, int nl, const f32x4& v) {
+  const bool p_vec = (d.OC & 3) == 0;
+  kp::for_each_acc_run<C>(acc, [&](int ml, int nl, const f32x4& v) {
     const int64_t m = m0 + ml, j = n0 + nl;
     if (j >= Ng) return;
+    if (p_vec && m + 3 < d.OC) {
+      *reinterpret_cast<f32x4*>(P + m + d.OC * j) = v;
+    } else {
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-      if (m + e < d.OC) P[(m + e) + d.OC * j] = v[e];
+      for (int e = 0; e < 4; ++e)
+        if (m + e < d.OC) P[(m + e) + d.OC * j] = v[e];
+    }
   });
 }
 
@@ -357,53 +402,116 @@ ConvDims make_dims(int64_t N, int64_t C, int64_t H, int64_t W, int64_t OC, int64
   return d;
 }
 
-// Tile shape for an (M rows along the batch) x (Ng channels) per-pixel GEMM.
-template <template <class> class Kern>
-void launch_pixel(const ConvArgs& a, int64_t M, int64_t Ng, int64_t pixels, hipStream_t st) {
+// Per-pixel GEMM (M = N along the batch, Ng = OC or C channels) launch.
+// `gathered`: elements of the tensor A gathers from (the table holds 32-bit
+// offsets into it).
+template <bool DGRAD>
+void launch_pixel(const ConvArgs& a, int64_t Ng, int64_t K, int64_t pixels, int64_t gathered,
+                  hipStream_t st) {
   auto go = [&](auto cfg) {
     using Cfg = decltype(cfg);
-    const int64_t tiles = ((M + Cfg::BM - 1) / Cfg::BM) * ((Ng + Cfg::BN - 1) / Cfg::BN);
-    // algorithmic flops: 2 * N * (output pixels) * OC * C * KS^2 for both directions
+    const int64_t kpad = (K + Cfg::KT - 1) / Cfg::KT * Cfg::KT;
+    const bool tbl = kpad <= KTBL && gathered < ((int64_t)1 << 31);
+    const int64_t tiles = ((a.d.N + Cfg::BM - 1) / Cfg::BM) * ((Ng + Cfg::BN - 1) / Cfg::BN);
+    // algorithmic flops: 2 * N * (output pixels) * OC * C * KS^2 in both directions
     const ConvDims& d = a.d;
     TimingRec* rec = timing_slot(2.0 * d.N * d.HO * d.WO * d.OC * d.C * d.KS * d.KS);
     if (rec) (void)hipEventRecord(rec->start, st);
-    hipLaunchKernelGGL(Kern<Cfg>::fn(), dim3((unsigned)tiles, (unsigned)pixels), dim3(Cfg::NT), 0,
-                       st, a);
+    const auto kern = tbl ? &conv_pixel_kernel<Cfg, DGRAD, true> : &conv_pixel_kernel<Cfg, DGRAD, false>;
+    hipLaunchKernelGGL(kern, dim3((unsigned)tiles, (unsigned)pixels), dim3(Cfg::NT), 0, st, a);
     if (rec) (void)hipEventRecord(rec->stop, st);
   };
-  if (Ng <= 32) go(CfgSN{});
-  else if (Ng <= 64) go(CfgM{});
-  else go(CfgL{});
+  if (Ng <= 32) go(kp::Cfg<4, 1, 1, 1>{});       // 128 x 32
+  else if (Ng <= 64) go(kp::Cfg<2, 2, 2, 1>{});  // 128 x 64
+  else go(kp::Cfg<2, 2, 2, 2>{});                // 128 x 128
 }
 
-template <class Cfg>
-struct FwdK {
-  static auto fn() { return &conv_fwd_kernel<Cfg>; }
-};
-template <class Cfg>
-struct DgradK {
-  static auto fn() { return &conv_dgrad_kernel<Cfg>; }
-};
+// Weight-gradient launch for an OC x Ng tile grid: split-K partials, then a
+// fixed-order sum into gW / gb.  Tiles of up to 32 x 64 outputs split each
+// k-tile over WGK wave groups so every block has 4 waves.
+int launch_wgrad(ConvArgs a, float* gW, float* gb, hipStream_t st, const char* who) {
+  const ConvDims& d = a.d;
+  const int64_t CT = d.C * d.KS * d.KS, Ng = CT + a.has_bias, Kc = d.N * d.HO * d.WO;
+  auto go = [&](auto cfg) -> int {
+    using Cfg = decltype(cfg);
+    a.aligned = a.aligned && d.N % Cfg::KT == 0;
+    const int64_t tiles = ((d.OC + Cfg::BM - 1) / Cfg::BM) * ((Ng + Cfg::BN - 1) / Cfg::BN);
+    int64_t splits = std::max<int64_t>(1, (512 + tiles - 1) / tiles);
+    splits = std::min<int64_t>(splits, std::max<int64_t>(1, Kc / (8 * Cfg::KT)));
+    int64_t kps = (Kc + splits - 1) / splits;
+    kps = (kps + Cfg::KT - 1) / Cfg::KT * Cfg::KT;
+    splits = (Kc + kps - 1) / kps;
+    a.k_per_split = kps;
+    void* ws = nullptr;
+    CNHIP_TRY(check_hip(hipMallocAsync(&ws, (size_t)splits * d.OC * Ng * sizeof(float), st), who));
+    a.partial = static_cast<float*>(ws);
+    TimingRec* rec = timing_slot(2.0 * Kc * d.OC * CT);
+    if (rec) (void)hipEventRecord(rec->start, st);
+    const auto kern = a.aligned ? &conv_wgrad_kernel<Cfg, true> : &conv_wgrad_kernel<Cfg, false>;
+    hipLaunchKernelGGL(kern, dim3((unsigned)tiles, 1, (unsigned)splits), dim3(Cfg::NT), 0, st, a);
+    int status = check_launch(who);
+    if (rec) (void)hipEventRecord(rec->stop, st);
+    if (status == CNHIP_OK) {
+      hipLaunchKernelGGL(conv_wgrad_reduce_kernel, dim3((unsigned)((d.OC * Ng + 63) / 64)),
+                         dim3(64 * WGRAD_RW), 0, st, a.partial, (int)splits, d.OC, CT, a.has_bias,
+                         gW, gb);
+      status = check_launch(who);
+    }
+    const int st2 = check_hip(hipFreeAsync(ws, st), who);
+    return status != CNHIP_OK ? status : st2;
+  };
+  const int bm = d.OC <= 32 ? 32 : d.OC <= 64 ? 64 : 128;
+  const int bn = Ng <= 32 ? 32 : Ng <= 64 ? 64 : 128;
+  if (bm == 32) {
+    if (bn == 32) return go(kp::Cfg<1, 1, 1, 1, 16, 4>{});
+    if (bn == 64) return go(kp::Cfg<1, 2, 1, 1, 16, 2>{});
+    return go(kp::Cfg<1, 4, 1, 1, 16, 1>{});
+  }
+  if (bm == 64) {
+    if (bn == 32) return go(kp::Cfg<2, 1, 1, 1, 16, 2>{});
+    if (bn == 64) return go(kp::Cfg<2, 2, 1, 1, 16, 1>{});
+    return go(kp::Cfg<2, 2, 1, 2, 16, 1>{});
+  }
+  if (bn == 32) return go(kp::Cfg<4, 1, 1, 1, 16, 1>{});
+  if (bn == 64) return go(kp::Cfg<2, 2, 2, 1, 16, 1>{});
+  return go(kp::Cfg<2, 2, 2, 2, 16, 1>{});
+}
 
 }  // namespace
 }  // namespace cnhip
 
 using cnhip::as_stream;
 
+namespace {
+
+int conv_forward(const float* X, const float* W, const float* b, float* Y, int64_t N, int64_t C,
+                 int64_t H, int64_t Wd, int64_t OC, int64_t KS, int64_t S, int64_t P, int relu,
+                 cnhip_stream_t stream, const char* who) {
+  const cnhip::ConvDims d = cnhip::make_dims(N, C, H, Wd, OC, KS, S, P);
+  CNHIP_TRY(cnhip::check_dims(d, who));
+  CNHIP_REQUIRE(X && W && Y, "%s: NULL pointer", who);
+  cnhip::ConvArgs a{};
+  a.d = d; a.src = X; a.wt = W; a.bias = b; a.out = Y; a.relu = relu;
+  a.out_vec = (N % 4 == 0) && cnhip::aligned16(Y);
+  cnhip::launch_pixel<false>(a, OC, C * KS * KS, d.HO * d.WO, N * C * H * Wd, as_stream(stream));
+  return cnhip::check_launch(who);
+}
+
+}  // namespace
+
 extern "C" {
 
 int cnhip_conv2d_forward(const float* X, const float* W, const float* b, float* Y, int64_t N,
                          int64_t C, int64_t H, int64_t Wd, int64_t OC, int64_t KS, int64_t S,
                          int64_t P, cnhip_stream_t stream) {
-  const char* who = "cnhip_conv2d_forward";
-  const cnhip::ConvDims d = cnhip::make_dims(N, C, H, Wd, OC, KS, S, P);
-  CNHIP_TRY(cnhip::check_dims(d, who));
-  CNHIP_REQUIRE(X && W && Y, "%s: NULL pointer", who);
-  cnhip::ConvArgs a{};
-  a.d = d; a.X = X; a.Wt = W; a.bias = b; a.out = Y;
-  a.nvec = (N % 4 == 0) && cnhip::aligned16(X) && cnhip::aligned16(Y);
-  cnhip::launch_pixel<cnhip::FwdK>(a, N, OC, d.HO * d.WO, as_stream(stream));
-  return cnhip::check_launch(who);
+  return conv_forward(X, W, b, Y, N, C, H, Wd, OC, KS, S, P, 0, stream, "cnhip_conv2d_forward");
+}
+
+int cnhip_conv2d_forward_relu(const float* X, const float* W, const float* b, float* Y, int64_t N,
+                              int64_t C, int64_t H, int64_t Wd, int64_t OC, int64_t KS, int64_t S,
+                              int64_t P, cnhip_stream_t stream) {
+  return conv_forward(X, W, b, Y, N, C, H, Wd, OC, KS, S, P, 1, stream,
+                      "cnhip_conv2d_forward_relu");
 }
 
 int cnhip_conv2d_backward(const float* X, const float* W, const float* dY, float* gW, float* gb,
@@ -418,42 +526,10 @@ int cnhip_conv2d_backward(const float* X, const float* W, const float* dY, float
 
   // ---- weight + bias grads: split-K implicit GEMM, then a fixed-order sum
   cnhip::ConvArgs a{};
-  a.d = d; a.X = X; a.dY = dY;
+  a.d = d; a.src = X; a.dY = dY;
   a.has_bias = gb ? 1 : 0;
-  a.nvec = (N % 4 == 0) && cnhip::aligned16(X) && cnhip::aligned16(dY);
-  const int64_t Ng = CT + a.has_bias, Kc = N * d.HO * d.WO;
-  auto wgrad = [&](auto cfg) -> int {
-    using Cfg = decltype(cfg);
-    const int64_t tiles = ((OC + Cfg::BM - 1) / Cfg::BM) * ((Ng + Cfg::BN - 1) / Cfg::BN);
-    int64_t splits = std::max<int64_t>(1, (1024 + tiles - 1) / tiles);
-    splits = std::min<int64_t>(splits, std::max<int64_t>(1, Kc / (8 * cnhip::mfma::BK)));
-    int64_t kps = (Kc + splits - 1) / splits;
-    kps = (kps + cnhip::mfma::BK - 1) / cnhip::mfma::BK * cnhip::mfma::BK;
-    splits = (Kc + kps - 1) / kps;
-    a.k_per_split = kps;
-    void* ws = nullptr;
-    CNHIP_TRY(cnhip::check_hip(hipMallocAsync(&ws, (size_t)splits * OC * Ng * sizeof(float), st), who));
-    a.partial = static_cast<float*>(ws);
-    cnhip::TimingRec* rec = cnhip::timing_slot(2.0 * N * d.HO * d.WO * OC * CT);
-    if (rec) (void)hipEventRecord(rec->start, st);
-    hipLaunchKernelGGL(cnhip::conv_wgrad_kernel<Cfg>, dim3((unsigned)tiles, 1, (unsigned)splits),
-                       dim3(Cfg::NT), 0, st, a);
-    int status = cnhip::check_launch(who);
-    if (rec) (void)hipEventRecord(rec->stop, st);
-    if (status == CNHIP_OK) {
-      hipLaunchKernelGGL(cnhip::conv_wgrad_reduce_kernel, dim3((unsigned)((OC * Ng + 63) / 64)),
-                         dim3(64 * cnhip::WGRAD_RW), 0, st, a.partial, (int)splits, OC, CT,
-                         a.has_bias, gW, gb);
-      status = cnhip::check_launch(who);
-    }
-    const int st2 = cnhip::check_hip(hipFreeAsync(ws, st), who);
-    return status != CNHIP_OK ? status : st2;
-  };
-  int status;
-  if (OC <= 32) status = Ng <= 32 ? wgrad(cnhip::Cfg11{}) : wgrad(cnhip::CfgSM{});
-  else if (OC <= 64) status = wgrad(cnhip::CfgS{});
-  else status = wgrad(cnhip::CfgL{});
-  CNHIP_TRY(status);
+  a.aligned = cnhip::aligned16(X) && cnhip::aligned16(dY);  // N % KT is checked per tile shape
+  CNHIP_TRY(cnhip::launch_wgrad(a, gW, gb, st, who));
 
   // ---- input grad: relay W out as [OC*T, C], then per-input-pixel GEMMs
   if (dX) {
@@ -462,12 +538,13 @@ int cnhip_conv2d_backward(const float* X, const float* W, const float* dY, float
     float* Wr = static_cast<float*>(ws);
     hipLaunchKernelGGL(cnhip::conv_relayout_w_kernel, dim3(cnhip::elementwise_grid(OC * CT, 256)),
                        dim3(256), 0, st, W, Wr, OC, C, T);
-    status = cnhip::check_launch(who);
+    int status = cnhip::check_launch(who);
     if (status == CNHIP_OK) {
       cnhip::ConvArgs b{};
-      b.d = d; b.dY = dY; b.Wd = Wr; b.out = dX;
-      b.nvec = (N % 4 == 0) && cnhip::aligned16(dY) && cnhip::aligned16(dX);
-      cnhip::launch_pixel<cnhip::DgradK>(b, N, C, H * Wd, st);
+      b.d = d; b.src = dY; b.wt = Wr; b.out = dX;
+      b.out_vec = (N % 4 == 0) && cnhip::aligned16(dX);
+      b.wt_vec = (OC * T) % 4 == 0;
+      cnhip::launch_pixel<true>(b, C, OC * T, H * Wd, N * OC * d.HO * d.WO, st);
       status = cnhip::check_launch(who);
     }
     const int st2 = cnhip::check_hip(hipFreeAsync(ws, st), who);

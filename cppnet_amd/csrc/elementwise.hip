@@ -19,7 +19,7 @@ namespace {
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 struct ReluFwd {
-  __device__ float operator()(float x) const { return fmaxf(0.f, x); }
+  __device__ float operator()(float x) const { return relu_f(x); }
 };
 struct SigmoidFwd {
   __device__ float operator()(float x) const {

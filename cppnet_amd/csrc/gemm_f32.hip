@@ -82,9 +82,9 @@ __device__ __forceinline__ float epilogue_value(const GemmArgs& g, const float* 
   float v = g.alpha * acc;
   if (g.beta != 0.f) v += g.beta * C[m + g.ldc * n];
   if (g.bias) v += g.bias[n];
-  if (!FUSED) return g.epilogue == CNHIP_EPI_RELU ? fmaxf(v, 0.f) : v;
+  if (!FUSED) return g.epilogue == CNHIP_EPI_RELU ? relu_f(v) : v;
   switch (g.epilogue) {
-    case CNHIP_EPI_RELU: return fmaxf(v, 0.f);
+    case CNHIP_EPI_RELU: return relu_f(v);
     case EPI_GELU:
       g.aux_out[m + g.ld_aux * n] = v;
       return gelu_f(v);

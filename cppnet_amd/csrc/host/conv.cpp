@@ -41,7 +41,10 @@ namespace CppNet
             }
         }
 
-        DeviceTensor Conv2D::forward(const DeviceTensor& x)
+        DeviceTensor Conv2D::forward(const DeviceTensor& x) { return forward_impl(x, false); }
+        DeviceTensor Conv2D::forward_relu(const DeviceTensor& x) { return forward_impl(x, true); }
+
+        DeviceTensor Conv2D::forward_impl(const DeviceTensor& x, bool relu)
         {
             if (x.rank() != 4 || x.dimension(1) != in_channels_)
                 throw std::runtime_error("Conv2D::forward: expected [N, " + std::to_string(in_channels_) +
@@ -52,20 +55,24 @@ namespace CppNet
             const int64_t WO = (W + 2 * padding_ - kernel_size_) / stride_ + 1;
             if (HO <= 0 || WO <= 0) throw std::runtime_error("Conv2D::forward: input smaller than kernel");
             DeviceTensor y = DeviceTensor::empty({N, out_channels_, HO, WO});
-            Device::check(cnhip_conv2d_forward(x.data(), W_.data(), bias_flag_ ? b_.data() : nullptr,
-                                               y.data(), N, in_channels_, H, W, out_channels_,
-                                               kernel_size_, stride_, padding_, Device::stream()),
-                          "Conv2D::forward");
+            const auto fwd = relu ? cnhip_conv2d_forward_relu : cnhip_conv2d_forward;
+            Device::check(fwd(x.data(), W_.data(), bias_flag_ ? b_.data() : nullptr, y.data(), N,
+                              in_channels_, H, W, out_channels_, kernel_size_, stride_, padding_,
+                              Device::stream()),
+                          relu ? "Conv2D::forward_relu" : "Conv2D::forward");
             return y;
         }
 
-        DeviceTensor Conv2D::backward(const DeviceTensor& g)
+        DeviceTensor Conv2D::backward(const DeviceTensor& g) { return backward(g, true); }
+
+        DeviceTensor Conv2D::backward(const DeviceTensor& g, bool input_grad)
         {
             if (!in_cache_.defined()) throw std::runtime_error("Conv2D::backward before forward");
             const int64_t N = in_cache_.dimension(0), H = in_cache_.dimension(2), W = in_cache_.dimension(3);
-            DeviceTensor dx = DeviceTensor::empty(in_cache_.dims());
+            DeviceTensor dx = input_grad ? DeviceTensor::empty(in_cache_.dims()) : DeviceTensor();
             Device::check(cnhip_conv2d_backward(in_cache_.data(), W_.data(), g.data(), gW_.data(),
-                                                bias_flag_ ? gb_.data() : nullptr, dx.data(), N,
+                                                bias_flag_ ? gb_.data() : nullptr,
+                                                input_grad ? dx.data() : nullptr, N,
                                                 in_channels_, H, W, out_channels_, kernel_size_, stride_,
                                                 padding_, Device::stream()),
                           "Conv2D::backward");
@@ -162,6 +169,20 @@ namespace CppNet
                                                    in_dims_[1], in_dims_[2], in_dims_[3], pool_size_,
                                                    stride_, Device::stream()),
                           "MaxPool2D::backward");
+            return dx;
+        }
+
+        DeviceTensor MaxPool2D::backward_relu(const DeviceTensor& g, const DeviceTensor& relu_out)
+        {
+            if (!idx_.defined()) throw std::runtime_error("MaxPool2D::backward before forward");
+            if (g.size() != idx_.size()) throw std::runtime_error("MaxPool2D::backward: grad shape mismatch");
+            if (relu_out.dims() != in_dims_)
+                throw std::runtime_error("MaxPool2D::backward_relu: ReLU output does not match the input");
+            DeviceTensor dx = DeviceTensor::empty(in_dims_);
+            Device::check(cnhip_maxpool2d_backward_relu(g.data(), idx_.idata(), relu_out.data(), dx.data(),
+                                                        in_dims_[0], in_dims_[1], in_dims_[2], in_dims_[3],
+                                                        pool_size_, stride_, Device::stream()),
+                          "MaxPool2D::backward_relu");
             return dx;
         }
 

@@ -94,7 +94,9 @@ namespace CppNet
             return dX;
         }
 
-        DeviceTensor Linear::backward(const DeviceTensor& grad_output)
+        DeviceTensor Linear::backward(const DeviceTensor& grad_output) { return backward(grad_output, true); }
+
+        DeviceTensor Linear::backward(const DeviceTensor& grad_output, bool input_grad)
         {
             if (grad_output.rank() != 2 || grad_output.dimension(1) != out_size_)
                 throw std::runtime_error("Output size mismatch in layer: " + layer_name_);
@@ -102,12 +104,12 @@ namespace CppNet
                 throw std::runtime_error("Linear::backward before forward (or batch mismatch) in layer: " +
                                          layer_name_);
             const int64_t B = grad_output.dimension(0);
-            DeviceTensor dX = DeviceTensor::empty({B, in_size_});
+            DeviceTensor dX = input_grad ? DeviceTensor::empty({B, in_size_}) : DeviceTensor();
             // grad_W += X^T dY (linear.cpp:346-352); over known-zero grads, write.
             const int accumulate = grads_zero_ ? 0 : 1;
             Device::check(cnhip_linear_backward(in_cache_.data(), W_.data(), grad_output.data(),
                                                 gW_.data(), bias_flag_ ? gb_.data() : nullptr,
-                                                dX.data(), B, in_size_, out_size_, trainable_ ? 1 : 0,
+                                                input_grad ? dX.data() : nullptr, B, in_size_, out_size_, trainable_ ? 1 : 0,
                                                 accumulate, Device::stream()),
                           "Linear::backward");
             if (trainable_) grads_zero_ = false;

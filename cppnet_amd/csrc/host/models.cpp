@@ -21,13 +21,19 @@ namespace CppNet
             DeviceTensor x = input;
             for (std::size_t i = 0; i < steps_.size(); ++i)
             {
-                Layers::Linear* lin = steps_[i]->linear();
                 Activations::Activation* next = i + 1 < steps_.size() ? steps_[i + 1]->activation() : nullptr;
-                if (lin && next)
+                if (auto* relu = dynamic_cast<Activations::ReLU*>(next))
                 {
-                    if (auto* relu = dynamic_cast<Activations::ReLU*>(next))
+                    if (Layers::Linear* lin = steps_[i]->linear())
                     {
                         x = lin->forward_act(x, CNHIP_ACT_RELU);
+                        relu->set_output_cache(x);
+                        ++i;
+                        continue;
+                    }
+                    if (Layers::Conv2D* conv = steps_[i]->conv2d())
+                    {
+                        x = conv->forward_relu(x);
                         relu->set_output_cache(x);
                         ++i;
                         continue;
@@ -40,17 +46,40 @@ namespace CppNet
 
         DeviceTensor SequentialModel::backward(const DeviceTensor& grad_output)
         {
+            return backward_from(grad_output, 0, true);
+        }
+
+        void SequentialModel::backward_params(const DeviceTensor& grad_output)
+        {
+            std::size_t first = 0;
+            while (first < steps_.size() && !steps_[first]->is_trainable()) ++first;
+            if (first == steps_.size()) return;  // nothing to train
+            backward_from(grad_output, first, false);
+        }
+
+        // Runs steps last .. first; step `first` computes its input gradient
+        // only when input_grad is set.  Fusions with a ReLU at k-1 apply only
+        // for k > first, where that ReLU's backward is part of the range.
+        DeviceTensor SequentialModel::backward_from(const DeviceTensor& grad_output, std::size_t first,
+                                                    bool input_grad)
+        {
             DeviceTensor g = grad_output;
-            for (std::size_t k = steps_.size(); k-- > 0;)
+            for (std::size_t k = steps_.size(); k-- > first;)
             {
-                Layers::Linear* lin = steps_[k]->linear();
-                Activations::Activation* prev = k >= 1 ? steps_[k - 1]->activation() : nullptr;
-                if (lin && prev)
+                if (k == first && !input_grad) return steps_[k]->backward_no_input_grad(g);
+                Activations::Activation* prev = k > first ? steps_[k - 1]->activation() : nullptr;
+                auto* relu = dynamic_cast<Activations::ReLU*>(prev);
+                if (relu && relu->output_cache().defined())
                 {
-                    auto* relu = dynamic_cast<Activations::ReLU*>(prev);
-                    if (relu && relu->output_cache().defined())
+                    if (Layers::Linear* lin = steps_[k]->linear())
                     {
                         g = lin->backward_act(g, CNHIP_ACT_RELU, relu->output_cache());
+                        --k;
+                        continue;
+                    }
+                    if (Layers::MaxPool2D* mp = steps_[k]->maxpool())
+                    {
+                        g = mp->backward_relu(g, relu->output_cache());
                         --k;
                         continue;
                     }

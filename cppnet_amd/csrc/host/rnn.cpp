@@ -109,15 +109,17 @@ namespace CppNet
             return out_cache_;
         }
 
-        DeviceTensor LSTM::backward(const DeviceTensor& g)
+        DeviceTensor LSTM::backward(const DeviceTensor& g) { return backward(g, true); }
+
+        DeviceTensor LSTM::backward(const DeviceTensor& g, bool input_grad)
         {
             if (!out_cache_.defined()) throw std::runtime_error("LSTM::backward before forward");
             if (g.dims() != out_cache_.dims()) throw std::runtime_error("LSTM::backward: grad shape mismatch");
             const int64_t B = g.dimension(0), S = g.dimension(1);
-            DeviceTensor dx = DeviceTensor::empty(in_cache_.dims());
+            DeviceTensor dx = input_grad ? DeviceTensor::empty(in_cache_.dims()) : DeviceTensor();
             Device::check(cnhip_lstm_backward(in_cache_.data(), W_ih_.data(), W_hh_.data(), out_cache_.data(),
                                               gates_cache_.data(), c_cache_.data(), tanh_c_cache_.data(),
-                                              g.data(), gW_ih_.data(), gW_hh_.data(), gb_.data(), dx.data(),
+                                              g.data(), gW_ih_.data(), gW_hh_.data(), gb_.data(), input_grad ? dx.data() : nullptr,
                                               B, S, input_size_, hidden_size_, Device::stream()),
                           "LSTM::backward");
             grads_zero_ = false;
@@ -154,15 +156,17 @@ namespace CppNet
             return out_cache_;
         }
 
-        DeviceTensor GRU::backward(const DeviceTensor& g)
+        DeviceTensor GRU::backward(const DeviceTensor& g) { return backward(g, true); }
+
+        DeviceTensor GRU::backward(const DeviceTensor& g, bool input_grad)
         {
             if (!out_cache_.defined()) throw std::runtime_error("GRU::backward before forward");
             if (g.dims() != out_cache_.dims()) throw std::runtime_error("GRU::backward: grad shape mismatch");
             const int64_t B = g.dimension(0), S = g.dimension(1);
-            DeviceTensor dx = DeviceTensor::empty(in_cache_.dims());
+            DeviceTensor dx = input_grad ? DeviceTensor::empty(in_cache_.dims()) : DeviceTensor();
             Device::check(cnhip_gru_backward(in_cache_.data(), W_ih_.data(), W_hh_.data(), out_cache_.data(),
                                              gates_cache_.data(), rh_cache_.data(), g.data(), gW_ih_.data(),
-                                             gW_hh_.data(), gb_.data(), dx.data(), B, S, input_size_,
+                                             gW_hh_.data(), gb_.data(), input_grad ? dx.data() : nullptr, B, S, input_size_,
                                              hidden_size_, Device::stream()),
                           "GRU::backward");
             grads_zero_ = false;

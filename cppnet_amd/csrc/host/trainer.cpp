@@ -600,7 +600,7 @@ namespace
         DeviceTensor out = s->model.forward(s->X);
         s->last_loss = s->loss->forward(out, s->Y);
         DeviceTensor g = s->loss->backward(out, s->Y);
-        s->model.backward(g);
+        s->model.backward_params(g);
     }
 
     void update(cnt_session* s)

@@ -1,12 +1,15 @@
 // fp32 MFMA tile engine with k-contiguous LDS operand tiles
 // (v_mfma_f32_32x32x2f32, wave64), used by the GEMM kernel.
 //
-// A block of WGM x WGN wavefronts owns a BM x BN output tile, BM = WGM*WM*32,
-// BN = WGN*WN*32; each wave holds WM x WN accumulator blocks of 32x32 (16
-// floats per lane each).  K advances BK (16 or 32) at a time.  Both operand
-// tiles live in LDS as [rows][k] with k contiguous (row stride LDK = BK + 4
-// floats, so the 16-byte fragment reads of 8 consecutive lanes hit 8
-// distinct 4-bank groups).
+// A block of WGM x WGN (x WGK) wavefronts owns a BM x BN output tile, BM =
+// WGM*WM*32, BN = WGN*WN*32; each wave holds WM x WN accumulator blocks of
+// 32x32 (16 floats per lane each).  K advances KT = BK*WGK at a time: with
+// WGK > 1 the WGK wave groups each take a BK-deep slice of every k-tile
+// (for tiles with few outputs and a long contraction) and their accumulators
+// are summed at the end in a fixed order (reduce_wgk).  Both operand tiles
+// live in LDS as [rows][k] with k contiguous (row stride LDK = KT + 4 floats,
+// so the 16-byte fragment reads of 8 consecutive lanes hit 8 distinct 4-bank
+// groups).
 //
 // Which k a lane feeds to which MFMA step is free, as long as A and B agree:
 // in step t (t = 0 .. BK/2-1) lane half h = lane/32 supplies k = h*BK/2 + t.
@@ -32,17 +35,28 @@ namespace kp {
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-template <int WGM_, int WGN_, int WM_, int WN_, int BK_ = 16>
+template <int WGM_, int WGN_, int WM_, int WN_, int BK_ = 16, int WGK_ = 1>
 struct Cfg {
   static constexpr int WGM = WGM_, WGN = WGN_, WM = WM_, WN = WN_;
-  static constexpr int BK = BK_;
-  static constexpr int LDK = BK + 4;
+  static constexpr int BK = BK_, WGK = WGK_;
+  static constexpr int KT = BK * WGK;  // k-tile depth
+  static constexpr int LDK = KT + 4;
   static constexpr int BM = WGM * WM * 32;
   static constexpr int BN = WGN * WN * 32;
-  static constexpr int NT = WGM * WGN * 64;
+  static constexpr int NT = WGM * WGN * WGK * 64;
   static constexpr int LDS_FLOATS = (BM + BN) * LDK;  // one buffer: A tile then B tile
   static_assert(BK == 16 || BK == 32, "BK must be 16 or 32");
+  static_assert(WGK == 1 || WGK == 2 || WGK == 4, "WGK must be 1, 2 or 4");
 };
+
+// Wave -> (wm, wn, wk) position in the block.
+template <class C>
+__device__ __forceinline__ void wave_pos(int& wm, int& wn, int& wk) {
+  const int wave = threadIdx.x >> 6;
+  wm = wave % C::WGM;
+  wn = C::WGK > 1 ? (wave / C::WGM) % C::WGN : wave / C::WGM;
+  wk = C::WGK > 1 ? wave / (C::WGM * C::WGN) : 0;
+}
 
 // An R x BK operand tile.  KC: X(r, k) = X[k + ld*r] (k contiguous), else
 // X(r, k) = X[r + ld*k] (r contiguous).  A unit is one 16-byte k-chunk of one
@@ -115,18 +129,20 @@ __device__ __forceinline__ void zero_acc(f32x16 (&acc)[C::WM][C::WN]) {
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 }
 
-// One BK-deep step of the block's MFMA work from the LDS tiles la ([BM][LDK])
-// and lb ([BN][LDK]); chunk c, element e is step t = 4c + e.
+// One k-tile of the block's MFMA work from the LDS tiles la ([BM][LDK]) and
+// lb ([BN][LDK]): each wave runs the BK-deep slice wk of it; chunk c,
+// element e is step t = 4c + e.
 template <class C>
 __device__ __forceinline__ void mfma_ktile(const float* __restrict__ la,
                                            const float* __restrict__ lb,
                                            f32x16 (&acc)[C::WM][C::WN]) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = wave % C::WGM, wn = wave / C::WGM;
+  const int lane = threadIdx.x & 63;
+  int wm, wn, wk;
+  wave_pos<C>(wm, wn, wk);
   const int h = lane >> 5, r = lane & 31;
   constexpr int LDK = C::LDK;
-  const float* pa = la + (wm * (C::WM * 32) + r) * LDK + (C::BK / 2) * h;
-  const float* pb = lb + (wn * (C::WN * 32) + r) * LDK + (C::BK / 2) * h;
+  const float* pa = la + (wm * (C::WM * 32) + r) * LDK + wk * C::BK + (C::BK / 2) * h;
+  const float* pb = lb + (wn * (C::WN * 32) + r) * LDK + wk * C::BK + (C::BK / 2) * h;
 #pragma unroll
   for (int c = 0; c < C::BK / 8; ++c) {
     f32x4 a[C::WM], b[C::WN];
@@ -147,10 +163,13 @@ __device__ __forceinline__ void mfma_ktile(const float* __restrict__ la,
 // Visits the accumulators: f(m_local, n_local, 4 values at rows m..m+3).
 // Accumulator layout of v_mfma_f32_32x32x2f32: lane holds column n = lane%32
 // and rows 8*(r/4) + 4*(lane/32) + r%4, r = 0..15.
+// With WGK > 1 only the wk == 0 waves (which hold the reduce_wgk sums) visit.
 template <class C, class F>
 __device__ __forceinline__ void for_each_acc_run(const f32x16 (&acc)[C::WM][C::WN], F&& f) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = wave % C::WGM, wn = wave / C::WGM;
+  const int lane = threadIdx.x & 63;
+  int wm, wn, wk;
+  wave_pos<C>(wm, wn, wk);
+  if (C::WGK > 1 && wk != 0) return;
 #pragma unroll
   for (int i = 0; i < C::WM; ++i)
 #pragma unroll
@@ -165,6 +184,79 @@ __device__ __forceinline__ void for_each_acc_run(const f32x16 (&acc)[C::WM][C::W
         f(m, n, v);
       }
     }
+}
+
+// Sums the accumulators of the WGK wave groups into the wk == 0 waves, in
+// the order wk = 0, 1, .., WGK-1, through LDS (lds: at least
+// (WGK-1) * WGM*WGN * WM*WN * 16 * 64 floats, free for reuse: the caller's
+// last barrier has passed).  No-op for WGK == 1.
+template <class C>
+__device__ __forceinline__ void reduce_wgk(float* lds, f32x16 (&acc)[C::WM][C::WN]) {
+  if constexpr (C::WGK > 1) {
+    const int lane = threadIdx.x & 63;
+    int wm, wn, wk;
+    wave_pos<C>(wm, wn, wk);
+    constexpr int PER_WAVE = C::WM * C::WN * 16 * 64;
+    const int slot = wm + C::WGM * wn;
+    if (wk > 0) {
+      float* dst = lds + ((wk - 1) * C::WGM * C::WGN + slot) * PER_WAVE;
+#pragma unroll
+      for (int i = 0; i < C::WM; ++i)
+#pragma unroll
+        for (int j = 0; j < C::WN; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) dst[((i * C::WN + j) * 16 + r) * 64 + lane] = acc[i][j][r];
+    }
+    __syncthreads();
+    if (wk == 0) {
+#pragma unroll
+      for (int g = 1; g < C::WGK; ++g) {
+        const float* src = lds + ((g - 1) * C::WGM * C::WGN + slot) * PER_WAVE;
+#pragma unroll
+        for (int i = 0; i < C::WM; ++i)
+#pragma unroll
+          for (int j = 0; j < C::WN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] += src[((i * C::WN + j) * 16 + r) * 64 + lane];
+      }
+    }
+  }
+}
+
+// Software pipeline over ntiles k-tiles: tile t+1 and t+2 are in flight in
+// two register sets while tile t is multiplied from LDS (double-buffered, one
+// barrier per k-tile).  The stage supplies load<S>(t) (global -> register set
+// S) and store<S>(buf) (register set S -> an LDS buffer of LDS_FLOATS, A tile
+// then B tile); the loop is unrolled by two so the sets alternate statically.
+// Ends with a barrier, after which lds may be reused.
+template <class C, class Stage>
+__device__ __forceinline__ void pipeline(int ntiles, float* lds, Stage& s,
+                                         f32x16 (&acc)[C::WM][C::WN]) {
+  float* buf0 = lds;
+  float* buf1 = lds + C::LDS_FLOATS;
+  constexpr int BOFF = C::BM * C::LDK;
+  if (ntiles > 0) {
+    s.template load<0>(0);
+    s.template store<0>(buf0);
+  }
+  if (ntiles > 1) s.template load<0>(1);
+  if (ntiles > 2) s.template load<1>(2);
+  __syncthreads();
+  for (int kt = 0; kt < ntiles; kt += 2) {
+    mfma_ktile<C>(buf0, buf0 + BOFF, acc);
+    if (kt + 1 < ntiles) {
+      s.template store<0>(buf1);
+      if (kt + 3 < ntiles) s.template load<0>(kt + 3);
+    }
+    __syncthreads();
+    if (kt + 1 >= ntiles) break;
+    mfma_ktile<C>(buf1, buf1 + BOFF, acc);
+    if (kt + 2 < ntiles) {
+      s.template store<1>(buf0);
+      if (kt + 4 < ntiles) s.template load<1>(kt + 4);
+    }
+    __syncthreads();
+  }
 }
 
 }  // namespace kp

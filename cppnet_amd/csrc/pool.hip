@@ -7,16 +7,17 @@
 // (the reference gpu path, which starts from -FLT_MAX and scatters with
 // atomicAdd after a memset).
 //
-// ColMajor [N, C, H, W] puts the batch index fastest: one thread per output
-// (forward) or per input element (backward) with n = thread index gives
-// coalesced reads of every window tap.  The backward is a gather: each input
-// element sums dY over the windows that contain it and picked it, so no
-// atomics and no separate zero-fill are needed, and non-overlapping windows
-// (stride == pool) produce exactly one term per element.
+// ColMajor [N, C, H, W] puts the batch index fastest: blocks own window
+// positions and their threads run over n, so every window tap is a coalesced
+// read.  The backward writes every element of dX itself, with no atomics and
+// no separate zero-fill: as a gather over the windows containing an input
+// element in general, and as one block per window when the windows tile the
+// input exactly (each element then gets exactly one term).
 #include <hip/hip_runtime.h>
 
 #include <cmath>
 
+#include "act_math.hpp"
 #include "common.hpp"
 
 namespace cnhip {
@@ -26,58 +27,101 @@ struct PoolDims {
   int64_t N, C, H, W, pool, stride, HO, WO;
 };
 
+// Blocks loop over positions (c + C*(h + H*w)) from a grid capped at
+// kPoolGrid: the position is decoded once per iteration in 32-bit integers
+// (every position count here is < 2^31), and the block's threads stride over
+// the batch index n, contiguous in memory, so each window tap is one
+// coalesced read.
+constexpr int kPoolGrid = 4096;
+
 __global__ void __launch_bounds__(256) maxpool_fwd_kernel(PoolDims d, const float* __restrict__ X,
                                                           float* __restrict__ Y,
                                                           int32_t* __restrict__ idx) {
-  const int64_t total = d.N * d.C * d.HO * d.WO;
-  for (int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; o < total;
-       o += (int64_t)gridDim.x * blockDim.x) {
-    // o = n + N*(c + C*(oh + HO*ow))
-    const int64_t n = o % d.N;
-    int64_t r = o / d.N;
-    const int64_t c = r % d.C;
-    r /= d.C;
-    const int64_t oh = r % d.HO, ow = r / d.HO;
-    float mx = -INFINITY;
-    int32_t mi = 0;
-    for (int64_t ph = 0; ph < d.pool; ++ph)
-      for (int64_t pw = 0; pw < d.pool; ++pw) {
-        const int64_t ih = oh * d.stride + ph, iw = ow * d.stride + pw;
-        const float v = X[n + d.N * (c + d.C * (ih + d.H * iw))];
-        if (v > mx) {
-          mx = v;
-          mi = (int32_t)(ph * d.pool + pw);
+  const int C = (int)d.C, HO = (int)d.HO, pool = (int)d.pool, stride = (int)d.stride;
+  const int positions = C * HO * (int)d.WO;
+  const int64_t N = d.N, sh = d.N * d.C, sw = d.N * d.C * d.H;  // strides of ih and iw
+  for (int pos = blockIdx.x; pos < positions; pos += gridDim.x) {
+    const int c = pos % C, r = pos / C, oh = r % HO, ow = r / HO;
+    const float* xb = X + N * c + sh * (oh * stride) + sw * (ow * stride);
+    for (int64_t n = threadIdx.x; n < N; n += blockDim.x) {
+      float mx = -INFINITY;
+      int32_t mi = 0;
+      for (int ph = 0; ph < pool; ++ph)
+        for (int pw = 0; pw < pool; ++pw) {
+          const float v = xb[n + sh * ph + sw * pw];
+          if (v > mx) {
+            mx = v;
+            mi = ph * pool + pw;
+          }
         }
-      }
-    Y[o] = mx;
-    idx[o] = mi;
+      Y[n + N * pos] = mx;
+      idx[n + N * pos] = mi;
+    }
   }
 }
 
-__global__ void __launch_bounds__(256) maxpool_bwd_kernel(PoolDims d, const float* __restrict__ dY,
-                                                          const int32_t* __restrict__ idx,
-                                                          float* __restrict__ dX) {
-  const int64_t total = d.N * d.C * d.H * d.W;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t n = i % d.N;
-    int64_t r = i / d.N;
-    const int64_t c = r % d.C;
-    r /= d.C;
-    const int64_t ih = r % d.H, iw = r / d.H;
+// Backward as a gather (any stride): input position (c, ih, iw) sums dY over
+// the windows that contain it and picked it, in (oh, ow) order starting from
+// 0.  MASK: the pool's input is a ReLU output y, and the result is scaled by
+// relu_mask(y) -- the ReLU backward fused in, same arithmetic as separately.
+template <bool MASK>
+__global__ void __launch_bounds__(256) maxpool_bwd_gather_kernel(PoolDims d,
+                                                                 const float* __restrict__ dY,
+                                                                 const int32_t* __restrict__ idx,
+                                                                 const float* __restrict__ y,
+                                                                 float* __restrict__ dX) {
+  const int C = (int)d.C, H = (int)d.H, HO = (int)d.HO, WO = (int)d.WO;
+  const int pool = (int)d.pool, stride = (int)d.stride;
+  const int positions = C * H * (int)d.W;
+  const int64_t N = d.N;
+  for (int pos = blockIdx.x; pos < positions; pos += gridDim.x) {
+    const int c = pos % C, r = pos / C, ih = r % H, iw = r / H;
     // windows (oh, ow) with oh*stride <= ih < oh*stride + pool
-    const int64_t oh_lo = ih >= d.pool ? (ih - d.pool) / d.stride + 1 : 0;
-    const int64_t oh_hi = min(ih / d.stride, d.HO - 1);
-    const int64_t ow_lo = iw >= d.pool ? (iw - d.pool) / d.stride + 1 : 0;
-    const int64_t ow_hi = min(iw / d.stride, d.WO - 1);
-    float g = 0.f;
-    for (int64_t oh = oh_lo; oh <= oh_hi; ++oh)
-      for (int64_t ow = ow_lo; ow <= ow_hi; ++ow) {
-        const int32_t want = (int32_t)((ih - oh * d.stride) * d.pool + (iw - ow * d.stride));
-        const int64_t o = n + d.N * (c + d.C * (oh + d.HO * ow));
-        if (idx[o] == want) g += dY[o];
-      }
-    dX[i] = g;
+    const int oh_lo = ih >= pool ? (ih - pool) / stride + 1 : 0;
+    const int oh_hi = min(ih / stride, HO - 1);
+    const int ow_lo = iw >= pool ? (iw - pool) / stride + 1 : 0;
+    const int ow_hi = min(iw / stride, WO - 1);
+    for (int64_t n = threadIdx.x; n < N; n += blockDim.x) {
+      float g = 0.f;
+      for (int oh = oh_lo; oh <= oh_hi; ++oh)
+        for (int ow = ow_lo; ow <= ow_hi; ++ow) {
+          const int32_t want = (ih - oh * stride) * pool + (iw - ow * stride);
+          const int64_t o = n + N * (c + (int64_t)C * (oh + HO * ow));
+          if (idx[o] == want) g += dY[o];
+        }
+      if (MASK) g *= relu_mask(y[n + N * pos]);
+      dX[n + N * pos] = g;
+    }
+  }
+}
+
+// Backward when the windows tile the input exactly (stride == pool, H and W
+// multiples of pool): each input element lies in exactly one window, so a
+// block per window reads idx/dY once and writes its pool^2 inputs:
+// 0 + dY at the argmax (the reference's zero-fill then add), 0 elsewhere.
+template <bool MASK>
+__global__ void __launch_bounds__(256) maxpool_bwd_tiled_kernel(PoolDims d,
+                                                                const float* __restrict__ dY,
+                                                                const int32_t* __restrict__ idx,
+                                                                const float* __restrict__ y,
+                                                                float* __restrict__ dX) {
+  const int C = (int)d.C, HO = (int)d.HO, pool = (int)d.pool;
+  const int positions = C * HO * (int)d.WO;
+  const int64_t N = d.N, sh = d.N * d.C, sw = d.N * d.C * d.H;
+  for (int pos = blockIdx.x; pos < positions; pos += gridDim.x) {
+    const int c = pos % C, r = pos / C, oh = r % HO, ow = r / HO;
+    const int64_t base = N * c + sh * (oh * pool) + sw * (ow * pool);
+    for (int64_t n = threadIdx.x; n < N; n += blockDim.x) {
+      const int32_t mi = idx[n + N * pos];
+      const float gy = 0.f + dY[n + N * pos];
+      for (int ph = 0; ph < pool; ++ph)
+        for (int pw = 0; pw < pool; ++pw) {
+          const int64_t o = base + n + sh * ph + sw * pw;
+          float g = mi == ph * pool + pw ? gy : 0.f;
+          if (MASK) g *= relu_mask(y[o]);
+          dX[o] = g;
+        }
+    }
   }
 }
 
@@ -93,6 +137,40 @@ int pool_dims(PoolDims& d, int64_t N, int64_t C, int64_t H, int64_t W, int64_t p
   return CNHIP_OK;
 }
 
+unsigned pool_grid(int64_t positions) {
+  return (unsigned)(positions < kPoolGrid ? positions : kPoolGrid);
+}
+unsigned pool_threads(int64_t N) { return N >= 256 ? 256u : (unsigned)((N + 63) / 64 * 64); }
+
+int maxpool_backward(const float* dY, const int32_t* idx, const float* y, float* dX, int64_t N,
+                     int64_t C, int64_t H, int64_t W, int64_t pool, int64_t stride,
+                     cnhip_stream_t stream, const char* who) {
+  PoolDims d;
+  CNHIP_TRY(pool_dims(d, N, C, H, W, pool, stride, who));
+  CNHIP_REQUIRE(dY && idx && dX, "%s: NULL pointer", who);
+  CNHIP_REQUIRE(C * H * W < ((int64_t)1 << 31), "%s: too many input positions", who);
+  const hipStream_t st = as_stream(stream);
+  const unsigned threads = pool_threads(N);
+  if (d.stride == d.pool && d.HO * d.pool == H && d.WO * d.pool == W) {
+    const unsigned grid = pool_grid(C * d.HO * d.WO);
+    if (y)
+      hipLaunchKernelGGL(maxpool_bwd_tiled_kernel<true>, dim3(grid), dim3(threads), 0, st, d, dY,
+                         idx, y, dX);
+    else
+      hipLaunchKernelGGL(maxpool_bwd_tiled_kernel<false>, dim3(grid), dim3(threads), 0, st, d, dY,
+                         idx, y, dX);
+  } else {
+    const unsigned grid = pool_grid(C * H * W);
+    if (y)
+      hipLaunchKernelGGL(maxpool_bwd_gather_kernel<true>, dim3(grid), dim3(threads), 0, st, d,
+                         dY, idx, y, dX);
+    else
+      hipLaunchKernelGGL(maxpool_bwd_gather_kernel<false>, dim3(grid), dim3(threads), 0, st, d,
+                         dY, idx, y, dX);
+  }
+  return check_launch(who);
+}
+
 }  // namespace
 }  // namespace cnhip
 
@@ -105,23 +183,26 @@ int cnhip_maxpool2d_forward(const float* X, float* Y, int32_t* idx, int64_t N, i
   cnhip::PoolDims d;
   CNHIP_TRY(cnhip::pool_dims(d, N, C, H, W, pool, stride, who));
   CNHIP_REQUIRE(X && Y && idx, "%s: NULL pointer", who);
-  const int64_t total = N * C * d.HO * d.WO;
-  hipLaunchKernelGGL(cnhip::maxpool_fwd_kernel, dim3(cnhip::elementwise_grid(total, 256)),
-                     dim3(256), 0, cnhip::as_stream(stream), d, X, Y, idx);
+  const int64_t positions = C * d.HO * d.WO;
+  CNHIP_REQUIRE(positions < ((int64_t)1 << 31), "%s: too many output positions", who);
+  hipLaunchKernelGGL(cnhip::maxpool_fwd_kernel, dim3(cnhip::pool_grid(positions)),
+                     dim3(cnhip::pool_threads(N)), 0, cnhip::as_stream(stream), d, X, Y, idx);
   return cnhip::check_launch(who);
 }
 
 int cnhip_maxpool2d_backward(const float* dY, const int32_t* idx, float* dX, int64_t N, int64_t C,
                              int64_t H, int64_t W, int64_t pool, int64_t stride,
                              cnhip_stream_t stream) {
-  const char* who = "cnhip_maxpool2d_backward";
-  cnhip::PoolDims d;
-  CNHIP_TRY(cnhip::pool_dims(d, N, C, H, W, pool, stride, who));
-  CNHIP_REQUIRE(dY && idx && dX, "%s: NULL pointer", who);
-  const int64_t total = N * C * H * W;
-  hipLaunchKernelGGL(cnhip::maxpool_bwd_kernel, dim3(cnhip::elementwise_grid(total, 256)),
-                     dim3(256), 0, cnhip::as_stream(stream), d, dY, idx, dX);
-  return cnhip::check_launch(who);
+  return cnhip::maxpool_backward(dY, idx, nullptr, dX, N, C, H, W, pool, stride, stream,
+                                 "cnhip_maxpool2d_backward");
+}
+
+int cnhip_maxpool2d_backward_relu(const float* dY, const int32_t* idx, const float* y, float* dX,
+                                  int64_t N, int64_t C, int64_t H, int64_t W, int64_t pool,
+                                  int64_t stride, cnhip_stream_t stream) {
+  const char* who = "cnhip_maxpool2d_backward_relu";
+  CNHIP_REQUIRE(y, "%s: NULL ReLU output", who);
+  return cnhip::maxpool_backward(dY, idx, y, dX, N, C, H, W, pool, stride, stream, who);
 }
 
 }  // extern "C"

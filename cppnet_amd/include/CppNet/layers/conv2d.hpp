@@ -31,7 +31,14 @@ namespace CppNet
             Tensor<float, 4> forward(const Tensor<float, 4>& input);
             Tensor<float, 4> backward(const Tensor<float, 4>& grad_output);
             DeviceTensor forward(const DeviceTensor& input);
+            /// forward() followed by ReLU, in the GEMM epilogue; returns the
+            /// ReLU output (what the ReLU's backward reads).
+            DeviceTensor forward_relu(const DeviceTensor& input);
             DeviceTensor backward(const DeviceTensor& grad_output);
+            /// backward() with the input gradient optional: input_grad = false
+            /// computes the parameter gradients only and returns an undefined
+            /// tensor (a model's first layer, whose input is data).
+            DeviceTensor backward(const DeviceTensor& grad_output, bool input_grad);
 
             bool is_trainable() const override { return trainable_; }
             void step(Optimizers::Optimizer& optimizer, float learning_rate) override;
@@ -60,6 +67,7 @@ namespace CppNet
 
         private:
             void materialize_grads() const;
+            DeviceTensor forward_impl(const DeviceTensor& input, bool relu);
             int in_channels_, out_channels_, kernel_size_, stride_, padding_;
             bool bias_flag_;
             bool trainable_ = true;

@@ -36,6 +36,10 @@ namespace CppNet
             Tensor<float, 2> backward(const Tensor<float, 2>& grad_output);
             DeviceTensor forward(const DeviceTensor& input);
             DeviceTensor backward(const DeviceTensor& grad_output);
+            /// backward() with the input gradient optional: input_grad = false
+            /// computes the parameter gradients only and returns an undefined
+            /// tensor (a model's first layer, whose input is data).
+            DeviceTensor backward(const DeviceTensor& grad_output, bool input_grad);
             /// forward() followed by activation act (CNHIP_ACT_RELU / _GELU) in
             /// one GEMM epilogue; returns the activation's output.  For GELU,
             /// *pre_act receives X W + b (what the GELU's backward reads).

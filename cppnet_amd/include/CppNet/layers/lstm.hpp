@@ -75,6 +75,10 @@ namespace CppNet
             Tensor<float, 3> backward(const Tensor<float, 3>& grad_output);
             DeviceTensor forward(const DeviceTensor& input);
             DeviceTensor backward(const DeviceTensor& grad_output);
+            /// backward() with the input gradient optional: input_grad = false
+            /// computes the parameter gradients only and returns an undefined
+            /// tensor (a model's first layer, whose input is data).
+            DeviceTensor backward(const DeviceTensor& grad_output, bool input_grad);
 
         private:
             DeviceTensor c_cache_, tanh_c_cache_;
@@ -94,6 +98,10 @@ namespace CppNet
             Tensor<float, 3> backward(const Tensor<float, 3>& grad_output);
             DeviceTensor forward(const DeviceTensor& input);
             DeviceTensor backward(const DeviceTensor& grad_output);
+            /// backward() with the input gradient optional: input_grad = false
+            /// computes the parameter gradients only and returns an undefined
+            /// tensor (a model's first layer, whose input is data).
+            DeviceTensor backward(const DeviceTensor& grad_output, bool input_grad);
 
         private:
             DeviceTensor rh_cache_;

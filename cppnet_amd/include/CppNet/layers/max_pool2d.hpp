@@ -27,6 +27,10 @@ namespace CppNet
             Tensor<float, 4> backward(const Tensor<float, 4>& grad_output);
             DeviceTensor forward(const DeviceTensor& input);
             DeviceTensor backward(const DeviceTensor& grad_output);
+            /// backward() followed by the backward of the ReLU whose output y
+            /// is this layer's input: dX * [y > 0] in one pass, equal to the
+            /// two calls.
+            DeviceTensor backward_relu(const DeviceTensor& grad_output, const DeviceTensor& relu_out);
             bool is_trainable() const override { return false; }
             void step(Optimizers::Optimizer&, float) override {}
             int get_pool_size() const { return pool_size_; }

@@ -3,11 +3,17 @@
  * @brief SequentialModel (ref: include/CppNet/models/models.hpp:116-218,
  *        src/CppNet/models/models.cpp:13-101) over device tensors.
  *
- * Steps run in insertion order; backward in reverse.  A Linear followed by
- * ReLU runs as one GEMM with the ReLU in its epilogue, and the next Linear's
- * input-gradient GEMM applies the ReLU mask (same arithmetic as the separate
- * calls).  GELU is not fused: its erfc epilogue measured slower than a
- * separate pass on MI355X.  zero_grad() resets
+ * Steps run in insertion order; backward in reverse.  A Linear or Conv2D
+ * followed by ReLU runs as one GEMM with the ReLU in its epilogue, and the
+ * next Linear's input-gradient GEMM -- or the backward of a MaxPool2D that
+ * follows the ReLU -- applies the ReLU mask (same arithmetic as the separate
+ * calls).
+ * GELU is not fused: its erfc epilogue measured slower than a separate pass
+ * on MI355X.  backward() returns the gradient of the model input, as the
+ * reference does; backward_params() is the training step's variant: it
+ * stops at the first trainable layer and skips that layer's input-gradient
+ * product (the input is data, nothing consumes its gradient), leaving every
+ * parameter gradient identical.  zero_grad() resets
  * every layer's gradients; update() steps every trainable layer, with all of
  * the optimizer's updates fused into one launch (begin_group/end_group).
  */
@@ -20,7 +26,9 @@
 #include <vector>
 
 #include "CppNet/activations/activation.hpp"
+#include "CppNet/layers/conv2d.hpp"
 #include "CppNet/layers/linear.hpp"
+#include "CppNet/layers/max_pool2d.hpp"
 #include "CppNet/core/tensor.hpp"
 #include "CppNet/layers/layer.hpp"
 #include "CppNet/optimizers/optimizer.hpp"
@@ -36,9 +44,25 @@ namespace CppNet
             virtual DeviceTensor backward(const DeviceTensor& grad_output) = 0;
             virtual bool is_trainable() const = 0;
             virtual void step(Optimizers::Optimizer& optimizer, float learning_rate) = 0;
+            /// Parameter gradients only; returns an undefined tensor where
+            /// the layer can skip its input gradient.
+            virtual DeviceTensor backward_no_input_grad(const DeviceTensor& g) { return backward(g); }
             virtual Layers::Linear* linear() { return nullptr; }
+            virtual Layers::MaxPool2D* maxpool() { return nullptr; }
+            virtual Layers::Conv2D* conv2d() { return nullptr; }
             virtual Activations::Activation* activation() { return nullptr; }
             virtual ~Step() = default;
+        };
+
+        template <typename L, typename = void>
+        struct has_optional_input_grad : std::false_type
+        {
+        };
+        template <typename L>
+        struct has_optional_input_grad<
+            L, std::void_t<decltype(std::declval<L&>().backward(std::declval<const DeviceTensor&>(), false))>>
+            : std::true_type
+        {
         };
 
         template <typename LayerT>
@@ -48,9 +72,18 @@ namespace CppNet
             explicit LayerStep(std::shared_ptr<LayerT> layer) : layer_(std::move(layer)) {}
             DeviceTensor forward(const DeviceTensor& x) override { return layer_->forward(x); }
             DeviceTensor backward(const DeviceTensor& g) override { return layer_->backward(g); }
+            DeviceTensor backward_no_input_grad(const DeviceTensor& g) override
+            {
+                if constexpr (has_optional_input_grad<LayerT>::value)
+                    return layer_->backward(g, false);
+                else
+                    return layer_->backward(g);
+            }
             bool is_trainable() const override { return layer_->is_trainable(); }
             void step(Optimizers::Optimizer& o, float lr) override { layer_->step(o, lr); }
             Layers::Linear* linear() override { return dynamic_cast<Layers::Linear*>(layer_.get()); }
+            Layers::MaxPool2D* maxpool() override { return dynamic_cast<Layers::MaxPool2D*>(layer_.get()); }
+            Layers::Conv2D* conv2d() override { return dynamic_cast<Layers::Conv2D*>(layer_.get()); }
 
         private:
             std::shared_ptr<LayerT> layer_;
@@ -93,6 +126,7 @@ namespace CppNet
 
             DeviceTensor forward(const DeviceTensor& input);
             DeviceTensor backward(const DeviceTensor& grad_output);
+            void backward_params(const DeviceTensor& grad_output);
             Tensor<float, 2> forward(const Tensor<float, 2>& input);
             Tensor<float, 2> backward(const Tensor<float, 2>& grad_output);
 
@@ -104,6 +138,7 @@ namespace CppNet
             void summary() const;
 
         private:
+            DeviceTensor backward_from(const DeviceTensor& grad_output, std::size_t first, bool input_grad);
             std::vector<std::shared_ptr<detail::Step>> steps_;
             std::vector<std::shared_ptr<Layers::Layer>> layers_;
         };

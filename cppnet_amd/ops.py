@@ -93,6 +93,12 @@ def conv2d_forward(X, W, b, Y, N, C, H, Wd, OC, KS, S=1, P=0) -> None:
                OC, KS, S, P, _stream())
 
 
+def conv2d_forward_relu(X, W, b, Y, N, C, H, Wd, OC, KS, S=1, P=0) -> None:
+    """Conv2D forward with the following ReLU in its epilogue: Y = max(0, conv + b)."""
+    _capi.call("cnhip_conv2d_forward_relu", _p(X, "X"), _p(W, "W"), _p(b, "b"), _p(Y, "Y"), N, C,
+               H, Wd, OC, KS, S, P, _stream())
+
+
 def conv2d_backward(X, W, dY, grad_W, grad_b, dX, N, C, H, Wd, OC, KS, S=1, P=0) -> None:
     _capi.call("cnhip_conv2d_backward", _p(X, "X"), _p(W, "W"), _p(dY, "dY"), _p(grad_W, "gW"),
                _p(grad_b, "gb"), _p(dX, "dX"), N, C, H, Wd, OC, KS, S, P, _stream())
@@ -106,6 +112,12 @@ def maxpool2d_forward(X, Y, idx, N, C, H, W, pool=2, stride=-1) -> None:
 def maxpool2d_backward(dY, idx, dX, N, C, H, W, pool=2, stride=-1) -> None:
     _capi.call("cnhip_maxpool2d_backward", _p(dY, "dY"), _p(idx, "idx"), _p(dX, "dX"), N, C, H, W,
                pool, stride, _stream())
+
+
+def maxpool2d_backward_relu(dY, idx, y, dX, N, C, H, W, pool=2, stride=-1) -> None:
+    """MaxPool2D backward times the mask [y > 0] of the ReLU output y feeding the pool."""
+    _capi.call("cnhip_maxpool2d_backward_relu", _p(dY, "dY"), _p(idx, "idx"), _p(y, "y"),
+               _p(dX, "dX"), N, C, H, W, pool, stride, _stream())
 
 
 def lstm_forward(X, W_ih, W_hh, b, Y, gates, c, tanh_c, B, S, I, H) -> None:

@@ -157,6 +157,14 @@ int cnhip_column_sum(const float* in, float* out, int64_t rows, int64_t cols,
 int cnhip_conv2d_forward(const float* X, const float* W, const float* b, float* Y,
                          int64_t N, int64_t C, int64_t H, int64_t Wd, int64_t OC,
                          int64_t KS, int64_t S, int64_t P, cnhip_stream_t stream);
+/* Conv2D forward followed by ReLU: Y = max(0, conv(X) + b), bit-identical to
+ * cnhip_conv2d_forward then cnhip_relu_forward.  Replaces the pair
+ * Conv2D::forward (conv2d.cpp:78-130) + the 4-D ReLU::forward (relu.cpp:
+ * 128-160) of a Conv2D -> ReLU stack; Y is the ReLU output the ReLU's
+ * backward reads. */
+int cnhip_conv2d_forward_relu(const float* X, const float* W, const float* b, float* Y,
+                              int64_t N, int64_t C, int64_t H, int64_t Wd, int64_t OC,
+                              int64_t KS, int64_t S, int64_t P, cnhip_stream_t stream);
 int cnhip_conv2d_backward(const float* X, const float* W, const float* dY,
                           float* grad_W, float* grad_b, float* dX, int64_t N, int64_t C,
                           int64_t H, int64_t Wd, int64_t OC, int64_t KS, int64_t S,
@@ -173,6 +181,15 @@ int cnhip_maxpool2d_forward(const float* X, float* Y, int32_t* idx, int64_t N, i
 int cnhip_maxpool2d_backward(const float* dY, const int32_t* idx, float* dX, int64_t N,
                              int64_t C, int64_t H, int64_t W, int64_t pool, int64_t stride,
                              cnhip_stream_t stream);
+/* MaxPool2D backward followed by the backward of the ReLU that produced the
+ * pool's input y (= the ReLU output, [N,C,H,W]): dX = maxpool_backward(dY) *
+ * [y > 0], bit-identical to cnhip_maxpool2d_backward then cnhip_relu_backward.
+ * Replaces the pair MaxPool2D::backward (max_pool2d.cpp:96-131) + the 4-D
+ * ReLU::backward (relu.cpp:194-225) that a Conv2D -> ReLU -> MaxPool2D stack
+ * runs. */
+int cnhip_maxpool2d_backward_relu(const float* dY, const int32_t* idx, const float* y, float* dX,
+                                  int64_t N, int64_t C, int64_t H, int64_t W, int64_t pool,
+                                  int64_t stride, cnhip_stream_t stream);
 
 /* ---- recurrent layers ----------------------------------------------------
  * X [B,S,I], Y [B,S,H] ColMajor (row n + B*t of a [B*S, .] matrix).

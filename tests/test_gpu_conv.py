@@ -28,7 +28,16 @@ def host(t):
 
 CONV_CASES = [(2, 3, 8, 8, 4, 3, 1, 1), (3, 2, 7, 5, 5, 3, 2, 0), (1, 4, 6, 6, 2, 2, 2, 1),
               (4, 3, 5, 5, 3, 1, 1, 0), (5, 5, 9, 7, 40, 5, 1, 2), (8, 70, 6, 6, 33, 3, 1, 1),
-              (256, 3, 32, 32, 32, 3, 1, 1), (256, 32, 16, 16, 64, 3, 1, 1)]
+              (256, 3, 32, 32, 32, 3, 1, 1), (256, 32, 16, 16, 64, 3, 1, 1),
+              # C*KS^2 and OC*KS^2 above the per-block gather-table limit (4608):
+              # forward and dgrad take the decoding loaders
+              (2, 520, 4, 4, 520, 3, 1, 1),
+              # stride 2 with padding, N not a multiple of 4 (scalar wgrad loads)
+              (70, 6, 9, 9, 8, 3, 2, 1),
+              # N a multiple of the wgrad k-tile (one output pixel per k-tile):
+              # 32x64 tile split over 2 wave groups with a partial OC tile, and a
+              # 64x32 tile split over 2 wave groups with stride 2
+              (32, 6, 8, 8, 20, 3, 1, 1), (16, 3, 10, 10, 48, 3, 2, 1)]
 
 
 @pytest.mark.parametrize("N,C,H,W,OC,KS,S,P", CONV_CASES)
@@ -49,6 +58,12 @@ def test_conv2d_vs_oracle(gpu, oracle, N, C, H, W, OC, KS, S, P, bias):
     Y = torch.empty(N * OC * HO * WO, device="cuda")
     from cppnet_amd import ops
     ops.conv2d_forward(dev(X), dev(Wt), None if b is None else dev(b), Y, N, C, H, W, OC, KS, S, P)
+    # the ReLU-fused forward equals the forward then the elementwise ReLU, bit for bit
+    Yr, Yr2 = torch.empty_like(Y), torch.empty_like(Y)
+    ops.conv2d_forward_relu(dev(X), dev(Wt), None if b is None else dev(b), Yr, N, C, H, W, OC, KS,
+                            S, P)
+    ops.relu_forward(Y, Yr2)
+    np.testing.assert_array_equal(host(Yr), host(Yr2))
     gW = torch.full((OC * C * KS * KS,), 7.0, device="cuda")  # must be overwritten
     gb = torch.full((OC,), 7.0, device="cuda") if bias else None
     dX = torch.empty(N * C * H * W, device="cuda")
@@ -75,7 +90,8 @@ def test_conv2d_vs_oracle(gpu, oracle, N, C, H, W, OC, KS, S, P, bias):
 
 
 POOL_CASES = [(2, 3, 8, 8, 2, 2), (3, 2, 5, 5, 3, 1), (1, 4, 7, 9, 2, 3), (4, 2, 6, 6, 3, 2),
-              (7, 3, 4, 4, 2, -1), (256, 32, 32, 32, 2, 2), (256, 64, 16, 16, 2, 2)]
+              (7, 3, 4, 4, 2, -1), (256, 32, 32, 32, 2, 2), (256, 64, 16, 16, 2, 2),
+              (300, 3, 6, 6, 2, 2), (70, 5, 7, 7, 3, 2), (5, 2, 7, 7, 2, 2)]
 
 
 @pytest.mark.parametrize("N,C,H,W,p,s", POOL_CASES)
@@ -107,3 +123,8 @@ def test_maxpool_vs_oracle(gpu, oracle, N, C, H, W, p, s):
         assert ok, msg
     # every upstream gradient lands somewhere exactly once
     assert abs(float(host(dX).sum()) - float(dY.sum())) <= 1e-3 * max(1.0, float(np.abs(dY).sum()))
+    # fused ReLU backward (X stands in for the ReLU output: its zeros and -inf
+    # give mask 0): bit-identical to the unfused pair, dX * [y > 0]
+    dXr = torch.full((N * C * H * W,), 3.0, device="cuda")
+    ops.maxpool2d_backward_relu(dev(dY), I, dev(X), dXr, N, C, H, W, p, s)
+    np.testing.assert_array_equal(host(dXr), host(dX) * (X > 0).astype(np.float32))
