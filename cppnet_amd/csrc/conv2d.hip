@@ -137,6 +137,8 @@ template <class C, bool DGRAD, bool TBL>
 __global__ void __launch_bounds__(C::NT) conv_pixel_kernel(ConvArgs a) {
   __shared__ __align__(16) float lds[2 * C::LDS_FLOATS];
   __shared__ __align__(16) int tbl[TBL ? KTBL : 4];
+  static_assert((C::WGK - 1) * C::WGM * C::WGN * C::WM * C::WN * 1024 <= 2 * C::LDS_FLOATS,
+                "reduce_wgk needs more LDS than the operand buffers");
   const ConvDims& d = a.d;
   const int64_t Ng = DGRAD ? d.C : d.OC;
   const int64_t K = (DGRAD ? d.OC : d.C) * d.KS * d.KS;
@@ -161,6 +163,7 @@ __global__ void __launch_bounds__(C::NT) conv_pixel_kernel(ConvArgs a) {
     PixelStage<C, DGRAD, TBL, false> s(a, tbl, m0, n0, K, q1, q2);
     kp::pipeline<C>(ntiles, lds, s, acc);
   }
+  kp::reduce_wgk<C>(lds, acc);
 
   float* out = a.out + d.N * Ng * q;  // out_pix(n, c) = out[n + N*c]
   kp::for_each_acc_run<C>(acc, [&](int ml, int nl, const f32x4& v) {
@@ -364,8 +367,10 @@ __global__ void __launch_bounds__(64 * WGRAD_RW) conv_wgrad_reduce_kernel(
   const int per = (splits + WGRAD_RW - 1) / WGRAD_RW;
   const int z0 = w * per, z1 = min(splits, z0 + per);
   float s = 0.f;
-  if (e < total)
+  if (e < total) {
+#pragma unroll 8
     for (int z = z0; z < z1; ++z) s += partial[(int64_t)z * total + e];
+  }
   part[w][lane] = s;
   __syncthreads();
   if (w == 0 && e < total) {
@@ -421,22 +426,31 @@ void launch_pixel(const ConvArgs& a, int64_t Ng, int64_t K, int64_t pixels, int6
     hipLaunchKernelGGL(kern, dim3((unsigned)tiles, (unsigned)pixels), dim3(Cfg::NT), 0, st, a);
     if (rec) (void)hipEventRecord(rec->stop, st);
   };
-  if (Ng <= 32) go(kp::Cfg<4, 1, 1, 1>{});       // 128 x 32
-  else if (Ng <= 64) go(kp::Cfg<2, 2, 2, 1>{});  // 128 x 64
-  else go(kp::Cfg<2, 2, 2, 2>{});                // 128 x 128
+  // shapes measured fastest on the config-3 layers (N = 256)
+  if (Ng <= 32) {
+    if (DGRAD) go(kp::Cfg<4, 1, 1, 1, 16, 2>{});  // 128 x 32, k-tile split over 2 wave groups
+    else if (a.d.N >= 256) go(kp::Cfg<8, 1, 1, 1>{});  // 256 x 32
+    else go(kp::Cfg<4, 1, 1, 1>{});                // 128 x 32
+  } else if (Ng <= 64) {
+    go(kp::Cfg<4, 2, 1, 1>{});                     // 128 x 64, 8 waves
+  } else {
+    go(kp::Cfg<2, 2, 2, 2>{});                     // 128 x 128
+  }
 }
 
 // Weight-gradient launch for an OC x Ng tile grid: split-K partials, then a
-// fixed-order sum into gW / gb.  Tiles of up to 32 x 64 outputs split each
-// k-tile over WGK wave groups so every block has 4 waves.
+// fixed-order sum into gW / gb.  Small tiles split each k-tile over WGK wave
+// groups so a block has 4 or 8 waves.
 int launch_wgrad(ConvArgs a, float* gW, float* gb, hipStream_t st, const char* who) {
   const ConvDims& d = a.d;
   const int64_t CT = d.C * d.KS * d.KS, Ng = CT + a.has_bias, Kc = d.N * d.HO * d.WO;
-  auto go = [&](auto cfg) -> int {
+  // target: blocks to aim for with split-K (fewer, longer blocks cut the
+  // partial traffic; more hide latency), measured per tile shape
+  auto go = [&](auto cfg, int64_t target) -> int {
     using Cfg = decltype(cfg);
     a.aligned = a.aligned && d.N % Cfg::KT == 0;
     const int64_t tiles = ((d.OC + Cfg::BM - 1) / Cfg::BM) * ((Ng + Cfg::BN - 1) / Cfg::BN);
-    int64_t splits = std::max<int64_t>(1, (512 + tiles - 1) / tiles);
+    int64_t splits = std::max<int64_t>(1, (target + tiles - 1) / tiles);
     splits = std::min<int64_t>(splits, std::max<int64_t>(1, Kc / (8 * Cfg::KT)));
     int64_t kps = (Kc + splits - 1) / splits;
     kps = (kps + Cfg::KT - 1) / Cfg::KT * Cfg::KT;
@@ -463,18 +477,17 @@ int launch_wgrad(ConvArgs a, float* gW, float* gb, hipStream_t st, const char* w
   const int bm = d.OC <= 32 ? 32 : d.OC <= 64 ? 64 : 128;
   const int bn = Ng <= 32 ? 32 : Ng <= 64 ? 64 : 128;
   if (bm == 32) {
-    if (bn == 32) return go(kp::Cfg<1, 1, 1, 1, 16, 4>{});
-    if (bn == 64) return go(kp::Cfg<1, 2, 1, 1, 16, 2>{});
-    return go(kp::Cfg<1, 4, 1, 1, 16, 1>{});
+    if (bn == 32) return go(kp::Cfg<1, 1, 1, 1, 16, 4>{}, 512);
+    if (bn == 64) return go(kp::Cfg<1, 2, 1, 1, 16, 2>{}, 512);
+    return go(kp::Cfg<1, 4, 1, 1, 16, 1>{}, 512);
   }
   if (bm == 64) {
-    if (bn == 32) return go(kp::Cfg<2, 1, 1, 1, 16, 2>{});
-    if (bn == 64) return go(kp::Cfg<2, 2, 1, 1, 16, 1>{});
-    return go(kp::Cfg<2, 2, 1, 2, 16, 1>{});
+    if (bn == 32) return go(kp::Cfg<2, 1, 1, 1, 16, 2>{}, 512);
+    return go(kp::Cfg<2, 2, 1, 1, 16, 2>{}, 2048);  // 64 x 64, 8 waves
   }
-  if (bn == 32) return go(kp::Cfg<4, 1, 1, 1, 16, 1>{});
-  if (bn == 64) return go(kp::Cfg<2, 2, 2, 1, 16, 1>{});
-  return go(kp::Cfg<2, 2, 2, 2, 16, 1>{});
+  if (bn == 32) return go(kp::Cfg<4, 1, 1, 1, 16, 1>{}, 512);
+  if (bn == 64) return go(kp::Cfg<2, 2, 2, 1, 16, 1>{}, 512);
+  return go(kp::Cfg<2, 2, 2, 2, 16, 1>{}, 512);
 }
 
 }  // namespace

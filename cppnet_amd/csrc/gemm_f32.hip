@@ -227,7 +227,9 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs g, int64_t 
        idx += (int64_t)gridDim.x * blockDim.x) {
     const int64_t bt = idx / mn, e = idx - bt * mn;
     const float* P = g.partial + bt * g.splits * mn + e;
+    // unrolled so the loads issue ahead; the additions stay in split order
     float s = 0.f;
+#pragma unroll 8
     for (int z = 0; z < g.splits; ++z) s += P[(int64_t)z * mn];
     const int64_t m = e % g.M, n = e / g.M;
     float* C = g.C + bt * g.stride_c;

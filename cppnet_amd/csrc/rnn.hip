@@ -44,6 +44,7 @@ __device__ __forceinline__ float sigm(float x) { return 1.0f / (1.0f + expf(-x))
 __device__ __forceinline__ float partial_sum(const float* __restrict__ p, int nsplit,
                                              int64_t stride, int64_t i) {
   float s = 0.0f;
+#pragma unroll 4
   for (int z = 0; z < nsplit; ++z) s += p[z * stride + i];
   return s;
 }
