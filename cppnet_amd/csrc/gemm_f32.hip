@@ -114,56 +114,47 @@ __device__ __forceinline__ void tile_of_block(int nbm, int nbn, int& tm, int& tn
   tn = in_group / gsz;
 }
 
-// K loop of one block over [k_begin, k_end).  FAST: every tile load is in
-// range and 16-byte aligned (no per-element checks).  Global loads run two
-// k-tiles ahead of the MFMAs through two register sets (the loop is unrolled
-// by two so the sets alternate statically), and LDS is double-buffered with
-// one barrier per k-tile: tile t is in LDS while t+1 and t+2 are in flight.
+// Global -> LDS staging of one GEMM block for kp::pipeline (global loads two
+// k-tiles ahead of the MFMAs through two register sets, double-buffered LDS,
+// one barrier per k-tile).
+template <bool FAST, bool TA, bool TB, class C>
+struct GemmStage {
+  using OA = kp::Operand<TA, C::BM, C::NT, C::BK>;   // A(m,k): k-contiguous when A is transposed
+  using OB = kp::Operand<!TB, C::BN, C::NT, C::BK>;  // B(k,n): k-contiguous unless B is transposed
+  const GemmArgs& g;
+  const float* A;
+  const float* B;
+  int64_t m0, n0, k_begin, k_end;
+  f32x4 ra[2][OA::REGS], rb[2][OB::REGS];
+
+  __device__ GemmStage(const GemmArgs& g_, const float* A_, const float* B_, int64_t m0_,
+                       int64_t n0_, int64_t kb, int64_t ke)
+      : g(g_), A(A_), B(B_), m0(m0_), n0(n0_), k_begin(kb), k_end(ke) {}
+
+  template <int S>
+  __device__ __forceinline__ void load(int t) {
+    const int64_t k0 = k_begin + (int64_t)t * C::BK;
+    OA::template load<FAST>(A, g.lda, m0, k0, g.M, k_end, ra[S]);
+    OB::template load<FAST>(B, g.ldb, n0, k0, g.N, k_end, rb[S]);
+  }
+  template <int S>
+  __device__ __forceinline__ void store(float* buf) {
+    OA::store(buf, ra[S]);
+    OB::store(buf + C::BM * C::LDK, rb[S]);
+  }
+};
+
+// K loop of one block over [k_begin, k_end) on the shared MFMA pipeline.
+// FAST: every tile load is in range and 16-byte aligned (no per-element
+// checks).
 template <bool FAST, bool TA, bool TB, class C>
 __device__ __forceinline__ void gemm_mainloop(const GemmArgs& g, const float* __restrict__ A,
                                               const float* __restrict__ B, int64_t m0, int64_t n0,
                                               int64_t k_begin, int64_t k_end, float* lds,
                                               f32x16 (&acc)[C::WM][C::WN]) {
-  constexpr int BK = C::BK;
-  using OA = kp::Operand<TA, C::BM, C::NT, BK>;   // A(m,k): k-contiguous when A is transposed
-  using OB = kp::Operand<!TB, C::BN, C::NT, BK>;  // B(k,n): k-contiguous unless B is transposed
-  const int ntiles = k_end > k_begin ? (int)((k_end - k_begin + BK - 1) / BK) : 0;
-  float* buf0 = lds;
-  float* buf1 = lds + C::LDS_FLOATS;
-  constexpr int BOFF = C::BM * C::LDK;
-  f32x4 ra0[OA::REGS], rb0[OB::REGS], ra1[OA::REGS], rb1[OB::REGS];
-  auto load = [&](int t, f32x4 (&ra)[OA::REGS], f32x4 (&rb)[OB::REGS]) {
-    const int64_t k0 = k_begin + (int64_t)t * BK;
-    OA::template load<FAST>(A, g.lda, m0, k0, g.M, k_end, ra);
-    OB::template load<FAST>(B, g.ldb, n0, k0, g.N, k_end, rb);
-  };
-  if (ntiles > 0) {
-    load(0, ra0, rb0);
-    OA::store(buf0, ra0);
-    OB::store(buf0 + BOFF, rb0);
-  }
-  if (ntiles > 1) load(1, ra0, rb0);
-  if (ntiles > 2) load(2, ra1, rb1);
-  __syncthreads();
-  for (int kt = 0; kt < ntiles; kt += 2) {
-    // tile kt in buf0, kt+1 in set 0, kt+2 in set 1
-    kp::mfma_ktile<C>(buf0, buf0 + BOFF, acc);
-    if (kt + 1 < ntiles) {
-      OA::store(buf1, ra0);
-      OB::store(buf1 + BOFF, rb0);
-      if (kt + 3 < ntiles) load(kt + 3, ra0, rb0);
-    }
-    __syncthreads();
-    if (kt + 1 >= ntiles) break;
-    // tile kt+1 in buf1, kt+2 in set 1, kt+3 in set 0
-    kp::mfma_ktile<C>(buf1, buf1 + BOFF, acc);
-    if (kt + 2 < ntiles) {
-      OA::store(buf0, ra1);
-      OB::store(buf0 + BOFF, rb1);
-      if (kt + 4 < ntiles) load(kt + 4, ra1, rb1);
-    }
-    __syncthreads();
-  }
+  const int ntiles = k_end > k_begin ? (int)((k_end - k_begin + C::BK - 1) / C::BK) : 0;
+  GemmStage<FAST, TA, TB, C> s(g, A, B, m0, n0, k_begin, k_end);
+  kp::pipeline<C>(ntiles, lds, s, acc);
 }
 
 template <bool TA, bool TB, class C, bool FUSED>

@@ -228,6 +228,10 @@ __device__ __forceinline__ void reduce_wgk(float* lds, f32x16 (&acc)[C::WM][C::W
 // barrier per k-tile).  The stage supplies load<S>(t) (global -> register set
 // S) and store<S>(buf) (register set S -> an LDS buffer of LDS_FLOATS, A tile
 // then B tile); the loop is unrolled by two so the sets alternate statically.
+// The loop body runs whole tile pairs and has no exit in its middle, and an
+// odd last tile is done after it: with a single exit the accumulators keep
+// one register assignment around the loop (a mid-body exit made the compiler
+// copy every accumulator between two register sets each iteration).
 // Ends with a barrier, after which lds may be reused.
 template <class C, class Stage>
 __device__ __forceinline__ void pipeline(int ntiles, float* lds, Stage& s,
@@ -242,19 +246,23 @@ __device__ __forceinline__ void pipeline(int ntiles, float* lds, Stage& s,
   if (ntiles > 1) s.template load<0>(1);
   if (ntiles > 2) s.template load<1>(2);
   __syncthreads();
-  for (int kt = 0; kt < ntiles; kt += 2) {
+  int kt = 0;
+  for (; kt + 1 < ntiles; kt += 2) {
+    // tile kt in buf0, kt+1 in set 0, kt+2 in set 1
     mfma_ktile<C>(buf0, buf0 + BOFF, acc);
-    if (kt + 1 < ntiles) {
-      s.template store<0>(buf1);
-      if (kt + 3 < ntiles) s.template load<0>(kt + 3);
-    }
+    s.template store<0>(buf1);
+    if (kt + 3 < ntiles) s.template load<0>(kt + 3);
     __syncthreads();
-    if (kt + 1 >= ntiles) break;
+    // tile kt+1 in buf1, kt+2 in set 1, kt+3 in set 0
     mfma_ktile<C>(buf1, buf1 + BOFF, acc);
     if (kt + 2 < ntiles) {
       s.template store<1>(buf0);
       if (kt + 4 < ntiles) s.template load<1>(kt + 4);
     }
+    __syncthreads();
+  }
+  if (kt < ntiles) {  // odd count: the last tile is in buf0
+    mfma_ktile<C>(buf0, buf0 + BOFF, acc);
     __syncthreads();
   }
 }
