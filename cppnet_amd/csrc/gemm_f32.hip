@@ -293,26 +293,82 @@ struct Plan {
 };
 
 // Tile shape and split-K plan of one GEMM; splits <= max_splits.
+// Split count for a tile shape by a cost model: dispatch rounds (256 block
+// slots for the 512-thread shapes, one per CU; 512 for the 256-thread ones)
+// times the K-tiles of one split, plus the fixed-order reduce of the partials
+// (read splits + 1 times M*N floats at ~5 TB/s, and a launch).  A split count
+// that leaves a nearly empty last round costs a whole extra round, so it is
+// avoided.  Splits keep >= 4 K-tiles of 32.  Returns the estimated seconds.
+double split_cost(Shape shape, int64_t tiles, int64_t M, int64_t N, int64_t K, int64_t batches,
+                  int max_splits, int& splits) {
+  int64_t bm = 0, bn = 0;
+  switch (shape) {
+    case Shape::XL: bm = CfgXL::BM; bn = CfgXL::BN; break;
+    case Shape::XN: bm = CfgXN::BM; bn = CfgXN::BN; break;
+    case Shape::M: bm = CfgM::BM; bn = CfgM::BN; break;
+    case Shape::SN: bm = CfgSN::BM; bn = CfgSN::BN; break;
+    case Shape::SM: bm = CfgSM::BM; bn = CfgSM::BN; break;
+    case Shape::S: bm = CfgS::BM; bn = CfgS::BN; break;
+  }
+  const bool big = shape == Shape::XL || shape == Shape::XN || shape == Shape::M;
+  const int64_t slots = big ? 256 : 512;
+  // seconds per K-tile of 32 of one block at the MFMA peak of its CU share
+  const double t_tile = 2.0 * bm * bn * KQ / (157.3e12 / 256) * (big ? 1.0 : 2.0);
+  const int64_t blocks = tiles * batches;
+  int64_t max_s = 1;
+  if (blocks < slots && shape != Shape::XL && shape != Shape::XN && K >= 8 * KQ)
+    max_s = std::max<int64_t>(1, std::min<int64_t>(K / (4 * KQ), max_splits));
+  double best = 0.0;
+  splits = 1;
+  for (int64_t s = 1; s <= max_s; ++s) {
+    const int64_t kt = ((K + s - 1) / s + KQ - 1) / KQ;
+    const int64_t rounds = (blocks * s + slots - 1) / slots;
+    double cost = (double)rounds * (double)kt * t_tile;
+    if (s > 1) cost += (double)(s + 1) * M * N * batches * 4.0 / 5e12 + 3e-6;
+    if (s == 1 || cost < best) {
+      best = cost;
+      splits = (int)s;
+    }
+  }
+  return best;
+}
+
 Plan plan_gemm(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, int64_t batches,
                int max_splits) {
   // Tile shape: skinny shapes waste no MFMA work on padding.  Large outputs
   // take 128 x 256, or 256 x 128 when only A is k-contiguous in memory (the
   // long tile side goes to the operand whose loads need no register
-  // transpose); medium ones take 128 x 128 with
-  // split-K; small problems get 64x64 tiles so that more blocks exist.
+  // transpose); otherwise 128 x 128 or 64 x 64 tiles with split-K, whichever
+  // the cost model above prefers.
   Shape shape;
-  if (N <= 32) shape = Shape::SN;
-  else if (M <= 32) shape = Shape::SM;
-  else {
+  int splits = 1;
+  if (N <= 32 || M <= 32) {
+    shape = N <= 32 ? Shape::SN : Shape::SM;
+    split_cost(shape, shape == Shape::SN ? tiles_of<CfgSN>(M, N) : tiles_of<CfgSM>(M, N), M, N, K,
+               batches, max_splits, splits);
+  } else {
     const bool a_kc = trans_a != 0, b_kc = trans_b == 0;
     const bool wide = !(a_kc && !b_kc);  // 128 x 256 measured the most even across layouts
     const int64_t tx = (wide ? tiles_of<CfgXN>(M, N) : tiles_of<CfgXL>(M, N)) * batches;
     const int64_t tm = tiles_of<CfgM>(M, N) * batches;
     // fraction of the last round of one-block-per-CU dispatch that is busy
     auto fill = [](int64_t b) { return (double)b / (double)(((b + 255) / 256) * 256); };
-    if (tx >= 256 && fill(tx) >= 0.9 * fill(tm)) shape = wide ? Shape::XN : Shape::XL;
-    else if (tm >= 64 || K >= 512) shape = Shape::M;
-    else shape = Shape::S;
+    if (tx >= 256 && fill(tx) >= 0.9 * fill(tm)) {
+      shape = wide ? Shape::XN : Shape::XL;
+    } else {
+      int sm = 1, ss = 1;
+      const double cm = split_cost(Shape::M, tiles_of<CfgM>(M, N), M, N, K, batches, max_splits, sm);
+      const double cs = split_cost(Shape::S, tiles_of<CfgS>(M, N), M, N, K, batches, max_splits, ss);
+      // 128 x 128 tiles reuse each loaded element twice as often: prefer
+      // them unless 64 x 64 is clearly cheaper
+      if (cs < 0.8 * cm) {
+        shape = Shape::S;
+        splits = ss;
+      } else {
+        shape = Shape::M;
+        splits = sm;
+      }
+    }
   }
   int64_t tiles = 0;
   switch (shape) {
@@ -322,19 +378,6 @@ Plan plan_gemm(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, int64_
     case Shape::SN: tiles = tiles_of<CfgSN>(M, N); break;
     case Shape::SM: tiles = tiles_of<CfgSM>(M, N); break;
     case Shape::S: tiles = tiles_of<CfgS>(M, N); break;
-  }
-
-  // Split K until a round of blocks fills the chip: 256 blocks for the
-  // 512-thread shapes (one per CU), 512 for the 256-thread ones (two per CU),
-  // keeping >= 4 K-tiles of 32 per split.  The 256-long tiles are only chosen
-  // with >= 256 blocks.
-  const int64_t blocks = tiles * batches;
-  const int64_t target = (shape == Shape::M) ? 256 : 512;
-  int splits = 1;
-  if (blocks < target && shape != Shape::XL && shape != Shape::XN && K >= 8 * KQ) {
-    const int64_t want = (target + blocks - 1) / blocks;
-    const int64_t max_by_k = K / (4 * KQ);
-    splits = (int)std::max<int64_t>(1, std::min<int64_t>({want, max_by_k, (int64_t)max_splits}));
   }
   int64_t kps = (K + splits - 1) / splits;
   kps = ((kps + KQ - 1) / KQ) * KQ;
