@@ -15,9 +15,8 @@
 // Forward and dgrad run one GEMM per pixel (blockIdx.y).  With the pixel
 // fixed, A's column k is one fixed element offset of X (dY), or padding; a
 // table of those offsets is built in LDS once per block, so the K loop does
-// no index arithmetic: each 16-byte LDS chunk of A is four coalesced dword
-// gathers along the batch at offsets read with one ds_read_b128.  No im2col
-// buffer exists.  wgrad contracts over k = n + N*q; when N is a multiple of
+// no index arithmetic: a 16-byte unit of A (4 samples at one k) is one table
+// read and one float4 along the batch.  No im2col buffer exists.  wgrad contracts over k = n + N*q; when N is a multiple of
 // the k-tile depth, a k-tile lies inside one output pixel q, so both of its
 // operands are plain k-contiguous float4 loads with one decode per tile.
 // wgrad splits its long contraction over blocks (and, for small tiles, over
@@ -53,7 +52,8 @@ struct ConvArgs {
   int relu;           // forward: ReLU in the epilogue
   int has_bias;       // wgrad: adds the ones-column
   int out_vec;        // N % 4 == 0 and out 16-byte aligned
-  int wt_vec;         // dgrad: Wd rows 16-byte aligned
+  int src_vec;        // forward / dgrad: N % 4 == 0 and src 16-byte aligned
+  int wt_vec;         // forward: OC % 4 == 0, dgrad: K' % 4 == 0; weights 16-byte aligned
   int aligned;        // wgrad: N % KT == 0 and X, dY 16-byte aligned
 };
 
@@ -84,8 +84,10 @@ __device__ __forceinline__ I gather_off(const ConvDims& d, I q1, I q2, I k) {
 
 // ------------------------------------------------------- forward / dgrad
 // Stage for kp::pipeline.  A(n, k) = src[n + off(k)] (rows contiguous along
-// the batch); B = W (forward: B(oc, k) = W[oc + OC*k], contiguous along oc)
-// or Wd (dgrad: B(ic, k) = Wd[k + K'*ic], contiguous along k).
+// the batch: a unit is 4 consecutive samples at one k, one table lookup and
+// one float4 when N % 4 == 0); B = W (forward: B(oc, k) = W[oc + OC*k],
+// contiguous along oc) or Wd (dgrad: B(ic, k) = Wd[k + K'*ic], contiguous
+// along k).
 template <class C, bool DGRAD, bool TBL, bool FAST>
 struct PixelStage {
   using OA = kp::Operand<false, C::BM, C::NT, C::KT>;
@@ -108,17 +110,18 @@ struct PixelStage {
       int r, k;
       if (!OA::origin(p, r, k)) break;
       const int64_t row = m0 + r, gk = k0 + k;
-      int64_t o[4];
-      if (TBL) {  // padded with -1 up to a whole number of k-tiles
-        const int4 v = *reinterpret_cast<const int4*>(tbl + gk);
-        o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
-      } else {
+      // table padded with -1 up to a whole number of k-tiles
+      const int64_t o = TBL ? (int64_t)tbl[gk] : (gk < K ? gather_off<DGRAD, int64_t>(d, q1, q2, gk) : -1);
+      f32x4 v{0.f, 0.f, 0.f, 0.f};
+      if (o >= 0) {
+        if (a.src_vec && (FAST || row + 3 < d.N)) {
+          v = *reinterpret_cast<const f32x4*>(a.src + o + row);
+        } else {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) o[j] = gk + j < K ? gather_off<DGRAD, int64_t>(d, q1, q2, gk + j) : -1;
+          for (int j = 0; j < 4; ++j)
+            if (row + j < d.N) v[j] = a.src[o + row + j];
+        }
       }
-      f32x4 v;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) v[j] = (o[j] >= 0 && (FAST || row < d.N)) ? a.src[o[j] + row] : 0.f;
       ra[S][p] = v;
     }
     if (DGRAD)
@@ -129,15 +132,16 @@ struct PixelStage {
   template <int S>
   __device__ __forceinline__ void store(float* buf) {
     OA::store(buf, ra[S]);
-    OB::store(buf + C::BM * C::LDK, rb[S]);
+    OB::store(buf + OA::FLOATS, rb[S]);
   }
 };
 
 template <class C, bool DGRAD, bool TBL>
 __global__ void __launch_bounds__(C::NT) conv_pixel_kernel(ConvArgs a) {
-  __shared__ __align__(16) float lds[2 * C::LDS_FLOATS];
+  constexpr int FLOATS = 2 * kp::stage_floats<PixelStage<C, DGRAD, TBL, true>>();
+  __shared__ __align__(16) float lds[FLOATS];
   __shared__ __align__(16) int tbl[TBL ? KTBL : 4];
-  static_assert((C::WGK - 1) * C::WGM * C::WGN * C::WM * C::WN * 1024 <= 2 * C::LDS_FLOATS,
+  static_assert((C::WGK - 1) * C::WGM * C::WGN * C::WM * C::WN * 1024 <= FLOATS,
                 "reduce_wgk needs more LDS than the operand buffers");
   const ConvDims& d = a.d;
   const int64_t Ng = DGRAD ? d.C : d.OC;
@@ -153,7 +157,7 @@ __global__ void __launch_bounds__(C::NT) conv_pixel_kernel(ConvArgs a) {
       tbl[k] = k < K ? gather_off<DGRAD, int>(d, (int)q1, (int)q2, k) : -1;
     __syncthreads();
   }
-  const bool fast = m0 + C::BM <= d.N && n0 + C::BN <= Ng && K % C::KT == 0 && (!DGRAD || a.wt_vec);
+  const bool fast = m0 + C::BM <= d.N && n0 + C::BN <= Ng && K % C::KT == 0 && a.wt_vec;
   f32x16 acc[C::WM][C::WN];
   kp::zero_acc<C>(acc);
   if (fast) {
@@ -309,14 +313,15 @@ struct WgradStage {
   template <int S>
   __device__ __forceinline__ void store(float* buf) {
     OA::store(buf, ra[S]);
-    OB::store(buf + C::BM * C::LDK, rb[S]);
+    OB::store(buf + OA::FLOATS, rb[S]);
   }
 };
 
 template <class C, bool ALIGNED>
 __global__ void __launch_bounds__(C::NT) conv_wgrad_kernel(ConvArgs a) {
-  __shared__ __align__(16) float lds[2 * C::LDS_FLOATS];
-  static_assert((C::WGK - 1) * C::WGM * C::WGN * C::WM * C::WN * 1024 <= 2 * C::LDS_FLOATS,
+  constexpr int FLOATS = 2 * kp::stage_floats<WgradStage<C, ALIGNED, true>>();
+  __shared__ __align__(16) float lds[FLOATS];
+  static_assert((C::WGK - 1) * C::WGM * C::WGN * C::WM * C::WN * 1024 <= FLOATS,
                 "reduce_wgk needs more LDS than the operand buffers");
   const ConvDims& d = a.d;
   const int64_t CT = d.C * d.KS * d.KS, Ng = CT + a.has_bias, Kc = d.N * d.HO * d.WO;
@@ -506,6 +511,8 @@ int conv_forward(const float* X, const float* W, const float* b, float* Y, int64
   cnhip::ConvArgs a{};
   a.d = d; a.src = X; a.wt = W; a.bias = b; a.out = Y; a.relu = relu;
   a.out_vec = (N % 4 == 0) && cnhip::aligned16(Y);
+  a.src_vec = (N % 4 == 0) && cnhip::aligned16(X);
+  a.wt_vec = (OC % 4 == 0) && cnhip::aligned16(W);
   cnhip::launch_pixel<false>(a, OC, C * KS * KS, d.HO * d.WO, N * C * H * Wd, as_stream(stream));
   return cnhip::check_launch(who);
 }
@@ -556,7 +563,8 @@ int cnhip_conv2d_backward(const float* X, const float* W, const float* dY, float
       cnhip::ConvArgs b{};
       b.d = d; b.src = dY; b.wt = Wr; b.out = dX;
       b.out_vec = (N % 4 == 0) && cnhip::aligned16(dX);
-      b.wt_vec = (OC * T) % 4 == 0;
+      b.src_vec = (N % 4 == 0) && cnhip::aligned16(dY);
+      b.wt_vec = (OC * T) % 4 == 0;  // Wd comes from the stream-ordered allocator: aligned
       cnhip::launch_pixel<true>(b, C, OC * T, H * Wd, N * OC * d.HO * d.WO, st);
       status = cnhip::check_launch(who);
     }

@@ -140,7 +140,7 @@ struct GemmStage {
   template <int S>
   __device__ __forceinline__ void store(float* buf) {
     OA::store(buf, ra[S]);
-    OB::store(buf + C::BM * C::LDK, rb[S]);
+    OB::store(buf + OA::FLOATS, rb[S]);
   }
 };
 
@@ -160,7 +160,7 @@ __device__ __forceinline__ void gemm_mainloop(const GemmArgs& g, const float* __
 template <bool TA, bool TB, class C, bool FUSED>
 __global__ void __launch_bounds__(C::NT, min_blocks<C>()) gemm_f32_kernel(GemmArgs g) {
   constexpr int BM = C::BM, BN = C::BN;
-  __shared__ __align__(16) float lds[2 * C::LDS_FLOATS];
+  __shared__ __align__(16) float lds[2 * kp::stage_floats<GemmStage<true, TA, TB, C>>()];
 
   const int nbm = (int)((g.M + BM - 1) / BM);
   const int nbn = (int)((g.N + BN - 1) / BN);

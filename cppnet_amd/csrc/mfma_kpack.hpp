@@ -1,28 +1,27 @@
-// fp32 MFMA tile engine with k-contiguous LDS operand tiles
-// (v_mfma_f32_32x32x2f32, wave64), used by the GEMM kernel.
+// fp32 MFMA tile engine (v_mfma_f32_32x32x2f32, wave64), used by the GEMM
+// and the Conv2D kernels.
 //
 // A block of WGM x WGN (x WGK) wavefronts owns a BM x BN output tile, BM =
 // WGM*WM*32, BN = WGN*WN*32; each wave holds WM x WN accumulator blocks of
 // 32x32 (16 floats per lane each).  K advances KT = BK*WGK at a time: with
 // WGK > 1 the WGK wave groups each take a BK-deep slice of every k-tile
 // (for tiles with few outputs and a long contraction) and their accumulators
-// are summed at the end in a fixed order (reduce_wgk).  Both operand tiles
-// live in LDS as [rows][k] with k contiguous (row stride LDK = KT + 4 floats,
-// so the 16-byte fragment reads of 8 consecutive lanes hit 8 distinct 4-bank
-// groups).
+// are summed at the end in a fixed order (reduce_wgk).
 //
 // Which k a lane feeds to which MFMA step is free, as long as A and B agree:
-// in step t (t = 0 .. BK/2-1) lane half h = lane/32 supplies k = h*BK/2 + t.
-// A lane therefore needs BK/2 consecutive k of one row per operand block and
-// fetches them with ds_read_b128s -- at BK = 16, 8 LDS reads feed the 32
-// MFMAs of a 2 x 2 wave tile per k-tile.
+// in step t (t = 0 .. BK/2-1) lane half h = lane/32 supplies k = h*BK/2 + t,
+// so a lane needs 4 consecutive k of one row per 4 steps (a "fragment").
 //
-// Global -> LDS staging goes through registers (double-buffered LDS, one
-// barrier per k-tile).  An operand whose rows are k-contiguous in memory is
-// moved as float4 along k; one whose rows are contiguous along the output
-// dimension is gathered as four coalesced dwords per 16-byte LDS chunk.  Both
-// write patterns are conflict-free, and every thread does the same work, so
-// the compiler can count outstanding loads exactly.
+// Each operand tile keeps the orientation it has in memory (Operand below):
+// rows that are k-contiguous in memory are stored [rows][k] and a fragment
+// is one ds_read_b128; rows contiguous along the output dimension are stored
+// [k][rows] and a fragment is four ds_read_b32 at the same row.  Either way
+// global -> LDS moves 16-byte float4s with conflict-free ds_write_b128, with
+// no register transposes, and the fragment reads of the two half-waves fall
+// into disjoint bank halves.  Staging goes through registers (two k-tiles in
+// flight, double-buffered LDS, one barrier per k-tile: pipeline below), and
+// every thread does the same work, so the compiler counts outstanding loads
+// exactly.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -40,11 +39,9 @@ struct Cfg {
   static constexpr int WGM = WGM_, WGN = WGN_, WM = WM_, WN = WN_;
   static constexpr int BK = BK_, WGK = WGK_;
   static constexpr int KT = BK * WGK;  // k-tile depth
-  static constexpr int LDK = KT + 4;
   static constexpr int BM = WGM * WM * 32;
   static constexpr int BN = WGN * WN * 32;
   static constexpr int NT = WGM * WGN * WGK * 64;
-  static constexpr int LDS_FLOATS = (BM + BN) * LDK;  // one buffer: A tile then B tile
   static_assert(BK == 16 || BK == 32, "BK must be 16 or 32");
   static_assert(WGK == 1 || WGK == 2 || WGK == 4, "WGK must be 1, 2 or 4");
 };
@@ -58,28 +55,35 @@ __device__ __forceinline__ void wave_pos(int& wm, int& wn, int& wk) {
   wk = C::WGK > 1 ? wave / (C::WGM * C::WGN) : 0;
 }
 
-// An R x BK operand tile.  KC: X(r, k) = X[k + ld*r] (k contiguous), else
-// X(r, k) = X[r + ld*k] (r contiguous).  A unit is one 16-byte k-chunk of one
-// row, written to LDS with one ds_write_b128.  KC loads it as one float4;
-// otherwise as four dwords at consecutive k (consecutive lanes take
-// consecutive rows, so each dword load is coalesced across the wave).
-template <bool KC, int R, int NT, int BK>
+// An R x KT operand tile in LDS.
+//   KC:  X(r, k) = X[k + ld*r], rows k-contiguous.  LDS [R][KT+4]; a unit is
+//        the 16-byte chunk X(r, k..k+3), one float4 load along k.
+//   !KC: X(r, k) = X[r + ld*k], rows contiguous along r.  LDS [KT][R+4]; a
+//        unit is X(r..r+3, k), one float4 load along r.
+// Consecutive lanes take consecutive units, so global loads are coalesced
+// and the ds_write_b128s hit consecutive (KC: padded) 16-byte slots.  The
+// +4 padding makes the fragment reads conflict-free: KC, the b128 reads of 8
+// consecutive lanes start 8 distinct 4-bank groups apart; !KC, the two
+// half-waves read rows BK/2 k-rows apart, 32 banks apart for BK = 16.
+template <bool KC, int R, int NT, int KT>
 struct Operand {
-  static constexpr int LDK = BK + 4;
-  static constexpr int CH = BK / 4;  // 16-byte chunks per row
-  static constexpr int UNITS = R * CH;
+  static constexpr int LD = KC ? KT + 4 : R + 4;        // LDS row stride (floats)
+  static constexpr int FLOATS = KC ? R * LD : KT * LD;  // one tile
+  static constexpr int CH = KC ? KT / 4 : R / 4;        // units per LDS row
+  static constexpr int UNITS = R * KT / 4;
   static constexpr int PER = (UNITS + NT - 1) / NT;
   static constexpr int REGS = PER;
 
+  // Unit p of this thread: KC, row r and k..k+3; !KC, rows r..r+3 and k.
   __device__ __forceinline__ static bool origin(int p, int& r, int& k) {
     const int u = threadIdx.x + NT * p;
     if (UNITS % NT != 0 && u >= UNITS) return false;
-    if (KC) {  // chunk fastest: 8 consecutive lanes write 2 rows x 4 chunks
+    if (KC) {
       r = u / CH;
       k = (u % CH) * 4;
-    } else {  // row fastest: 8 consecutive lanes write 8 rows (80-float steps)
-      r = u % R;
-      k = (u / R) * 4;
+    } else {
+      k = u / CH;
+      r = (u % CH) * 4;
     }
     return true;
   }
@@ -95,14 +99,14 @@ struct Operand {
       int r, k;
       if (!origin(p, r, k)) break;
       const int64_t gr = r0 + r, gk = k0 + k;
-      if (KC && FAST) {
-        v[p] = *reinterpret_cast<const f32x4*>(X + gk + ld * gr);
+      if (FAST) {
+        v[p] = *reinterpret_cast<const f32x4*>(X + (KC ? gk + ld * gr : gr + ld * gk));
       } else {
         f32x4 t;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const int64_t off = KC ? (gk + j + ld * gr) : (gr + ld * (gk + j));
-          t[j] = (FAST || (gr < Rtot && gk + j < Kend)) ? X[off] : 0.f;
+          const bool in = KC ? (gr < Rtot && gk + j < Kend) : (gr + j < Rtot && gk < Kend);
+          t[j] = in ? X[KC ? gk + j + ld * gr : gr + j + ld * gk] : 0.f;
         }
         v[p] = t;
       }
@@ -114,8 +118,15 @@ struct Operand {
     for (int p = 0; p < PER; ++p) {
       int r, k;
       if (!origin(p, r, k)) break;
-      *reinterpret_cast<f32x4*>(lds + r * LDK + k) = v[p];
+      *reinterpret_cast<f32x4*>(lds + (KC ? r * LD + k : k * LD + r)) = v[p];
     }
+  }
+
+  // Fragment X(row, k..k+3) from the LDS tile.
+  __device__ __forceinline__ static f32x4 frag(const float* __restrict__ lds, int row, int k) {
+    if (KC) return *reinterpret_cast<const f32x4*>(lds + row * LD + k);
+    const float* q = lds + k * LD + row;
+    return f32x4{q[0], q[LD], q[2 * LD], q[3 * LD]};
   }
 };
 
@@ -129,10 +140,10 @@ __device__ __forceinline__ void zero_acc(f32x16 (&acc)[C::WM][C::WN]) {
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 }
 
-// One k-tile of the block's MFMA work from the LDS tiles la ([BM][LDK]) and
-// lb ([BN][LDK]): each wave runs the BK-deep slice wk of it; chunk c,
+// One k-tile of the block's MFMA work from the LDS tiles la (operand OA)
+// and lb (operand OB): each wave runs the BK-deep slice wk of it; chunk c,
 // element e is step t = 4c + e.
-template <class C>
+template <class C, class OA, class OB>
 __device__ __forceinline__ void mfma_ktile(const float* __restrict__ la,
                                            const float* __restrict__ lb,
                                            f32x16 (&acc)[C::WM][C::WN]) {
@@ -140,16 +151,15 @@ __device__ __forceinline__ void mfma_ktile(const float* __restrict__ la,
   int wm, wn, wk;
   wave_pos<C>(wm, wn, wk);
   const int h = lane >> 5, r = lane & 31;
-  constexpr int LDK = C::LDK;
-  const float* pa = la + (wm * (C::WM * 32) + r) * LDK + wk * C::BK + (C::BK / 2) * h;
-  const float* pb = lb + (wn * (C::WN * 32) + r) * LDK + wk * C::BK + (C::BK / 2) * h;
+  const int ra = wm * (C::WM * 32) + r, rb = wn * (C::WN * 32) + r;
+  const int kb = wk * C::BK + (C::BK / 2) * h;
 #pragma unroll
   for (int c = 0; c < C::BK / 8; ++c) {
     f32x4 a[C::WM], b[C::WN];
 #pragma unroll
-    for (int i = 0; i < C::WM; ++i) a[i] = *reinterpret_cast<const f32x4*>(pa + i * 32 * LDK + 4 * c);
+    for (int i = 0; i < C::WM; ++i) a[i] = OA::frag(la, ra + 32 * i, kb + 4 * c);
 #pragma unroll
-    for (int j = 0; j < C::WN; ++j) b[j] = *reinterpret_cast<const f32x4*>(pb + j * 32 * LDK + 4 * c);
+    for (int j = 0; j < C::WN; ++j) b[j] = OB::frag(lb, rb + 32 * j, kb + 4 * c);
 #pragma unroll
     for (int e = 0; e < 4; ++e)
 #pragma unroll
@@ -223,11 +233,19 @@ __device__ __forceinline__ void reduce_wgk(float* lds, f32x16 (&acc)[C::WM][C::W
   }
 }
 
+// LDS floats of one pipeline buffer of a stage (A tile, then B tile); the
+// pipeline double-buffers it.
+template <class Stage>
+constexpr int stage_floats() {
+  return Stage::OA::FLOATS + Stage::OB::FLOATS;
+}
+
 // Software pipeline over ntiles k-tiles: tile t+1 and t+2 are in flight in
 // two register sets while tile t is multiplied from LDS (double-buffered, one
-// barrier per k-tile).  The stage supplies load<S>(t) (global -> register set
-// S) and store<S>(buf) (register set S -> an LDS buffer of LDS_FLOATS, A tile
-// then B tile); the loop is unrolled by two so the sets alternate statically.
+// barrier per k-tile).  The stage names its operands OA and OB and supplies
+// load<S>(t) (global -> register set S) and store<S>(buf) (register set S ->
+// an LDS buffer: A tile, then B tile at OA::FLOATS); the loop is unrolled by
+// two so the sets alternate statically.  lds holds 2 * stage_floats<Stage>().
 // The loop body runs whole tile pairs and has no exit in its middle, and an
 // odd last tile is done after it: with a single exit the accumulators keep
 // one register assignment around the loop (a mid-body exit made the compiler
@@ -236,9 +254,11 @@ __device__ __forceinline__ void reduce_wgk(float* lds, f32x16 (&acc)[C::WM][C::W
 template <class C, class Stage>
 __device__ __forceinline__ void pipeline(int ntiles, float* lds, Stage& s,
                                          f32x16 (&acc)[C::WM][C::WN]) {
+  using OA = typename Stage::OA;
+  using OB = typename Stage::OB;
   float* buf0 = lds;
-  float* buf1 = lds + C::LDS_FLOATS;
-  constexpr int BOFF = C::BM * C::LDK;
+  float* buf1 = lds + stage_floats<Stage>();
+  constexpr int BOFF = OA::FLOATS;
   if (ntiles > 0) {
     s.template load<0>(0);
     s.template store<0>(buf0);
@@ -249,12 +269,12 @@ __device__ __forceinline__ void pipeline(int ntiles, float* lds, Stage& s,
   int kt = 0;
   for (; kt + 1 < ntiles; kt += 2) {
     // tile kt in buf0, kt+1 in set 0, kt+2 in set 1
-    mfma_ktile<C>(buf0, buf0 + BOFF, acc);
+    mfma_ktile<C, OA, OB>(buf0, buf0 + BOFF, acc);
     s.template store<0>(buf1);
     if (kt + 3 < ntiles) s.template load<0>(kt + 3);
     __syncthreads();
     // tile kt+1 in buf1, kt+2 in set 1, kt+3 in set 0
-    mfma_ktile<C>(buf1, buf1 + BOFF, acc);
+    mfma_ktile<C, OA, OB>(buf1, buf1 + BOFF, acc);
     if (kt + 2 < ntiles) {
       s.template store<1>(buf0);
       if (kt + 4 < ntiles) s.template load<1>(kt + 4);
@@ -262,7 +282,7 @@ __device__ __forceinline__ void pipeline(int ntiles, float* lds, Stage& s,
     __syncthreads();
   }
   if (kt < ntiles) {  // odd count: the last tile is in buf0
-    mfma_ktile<C>(buf0, buf0 + BOFF, acc);
+    mfma_ktile<C, OA, OB>(buf0, buf0 + BOFF, acc);
     __syncthreads();
   }
 }
