@@ -27,6 +27,26 @@ inline int check_launch(const char* where) {
   return CNHIP_OK;
 }
 
+// Stream-ordered workspace allocation (split-K partials, scratch).  The
+// first call on a device raises the release threshold of its default memory
+// pool to the maximum, so freed workspaces stay pooled across
+// synchronizations (a training step re-allocates the same sizes every step;
+// with the default threshold of 0 the pool hands memory back at each sync and
+// the next step pays for real allocations).
+int ws_alloc(void** ptr, size_t bytes, hipStream_t stream, const char* where);
+
+// Reusable workspace for work queued on `stream`: a buffer of >= bytes held
+// per (device, stream, slot) and handed out again on later calls, so a
+// training step allocates nothing once sizes have been seen (stream-ordered
+// allocate/free cost ~50-120 us of host time per call on this runtime, more
+// than the kernels they serve).  Every user of a slot runs its kernels on
+// that stream, which orders the reuse; growth releases the old buffer in
+// stream order too.  Slot 0 is the GEMM's split-K partials, slot 1 the
+// layer-level workspaces (which may call the GEMM while holding theirs).
+// Calls on one stream from several host threads at once are not supported.
+constexpr int kScratchGemm = 0, kScratchLayer = 1;
+int scratch(hipStream_t stream, int slot, size_t bytes, void** ptr, const char* where);
+
 inline int check_hip(hipError_t e, const char* where) {
   if (e != hipSuccess) {
     set_error("%s: %s", where, hipGetErrorString(e));

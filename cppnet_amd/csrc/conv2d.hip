@@ -462,7 +462,7 @@ int launch_wgrad(ConvArgs a, float* gW, float* gb, hipStream_t st, const char* w
     splits = (Kc + kps - 1) / kps;
     a.k_per_split = kps;
     void* ws = nullptr;
-    CNHIP_TRY(check_hip(hipMallocAsync(&ws, (size_t)splits * d.OC * Ng * sizeof(float), st), who));
+    CNHIP_TRY(scratch(st, kScratchLayer, (size_t)splits * d.OC * Ng * sizeof(float), &ws, who));
     a.partial = static_cast<float*>(ws);
     TimingRec* rec = timing_slot(2.0 * Kc * d.OC * CT);
     if (rec) (void)hipEventRecord(rec->start, st);
@@ -476,8 +476,7 @@ int launch_wgrad(ConvArgs a, float* gW, float* gb, hipStream_t st, const char* w
                          gW, gb);
       status = check_launch(who);
     }
-    const int st2 = check_hip(hipFreeAsync(ws, st), who);
-    return status != CNHIP_OK ? status : st2;
+    return status;
   };
   const int bm = d.OC <= 32 ? 32 : d.OC <= 64 ? 64 : 128;
   const int bn = Ng <= 32 ? 32 : Ng <= 64 ? 64 : 128;
@@ -554,7 +553,7 @@ int cnhip_conv2d_backward(const float* X, const float* W, const float* dY, float
   // ---- input grad: relay W out as [OC*T, C], then per-input-pixel GEMMs
   if (dX) {
     void* ws = nullptr;
-    CNHIP_TRY(cnhip::check_hip(hipMallocAsync(&ws, (size_t)OC * CT * sizeof(float), st), who));
+    CNHIP_TRY(cnhip::scratch(st, cnhip::kScratchLayer, (size_t)OC * CT * sizeof(float), &ws, who));
     float* Wr = static_cast<float*>(ws);
     hipLaunchKernelGGL(cnhip::conv_relayout_w_kernel, dim3(cnhip::elementwise_grid(OC * CT, 256)),
                        dim3(256), 0, st, W, Wr, OC, C, T);
@@ -564,13 +563,11 @@ int cnhip_conv2d_backward(const float* X, const float* W, const float* dY, float
       b.d = d; b.src = dY; b.wt = Wr; b.out = dX;
       b.out_vec = (N % 4 == 0) && cnhip::aligned16(dX);
       b.src_vec = (N % 4 == 0) && cnhip::aligned16(dY);
-      b.wt_vec = (OC * T) % 4 == 0;  // Wd comes from the stream-ordered allocator: aligned
+      b.wt_vec = (OC * T) % 4 == 0;  // Wd is a scratch buffer: 256-byte aligned
       cnhip::launch_pixel<true>(b, C, OC * T, H * Wd, N * OC * d.HO * d.WO, st);
       status = cnhip::check_launch(who);
     }
-    const int st2 = cnhip::check_hip(hipFreeAsync(ws, st), who);
     CNHIP_TRY(status);
-    CNHIP_TRY(st2);
   }
   return CNHIP_OK;
 }

@@ -331,7 +331,7 @@ int cnhip_softmax_ce_forward(const float* logits, const float* targets, float* s
   const int64_t blocks = (batch + cnhip::SCE_BLOCK - 1) / cnhip::SCE_BLOCK;
   CNHIP_REQUIRE(blocks < ((int64_t)1 << 31), "%s: batch too large", who);
   void* ws = nullptr;
-  CNHIP_TRY(cnhip::check_hip(hipMallocAsync(&ws, (size_t)blocks * sizeof(float), st), who));
+  CNHIP_TRY(cnhip::scratch(st, cnhip::kScratchLayer, (size_t)blocks * sizeof(float), &ws, who));
   float* partial = static_cast<float*>(ws);
   hipLaunchKernelGGL(cnhip::softmax_ce_rows_kernel, dim3((unsigned)blocks), dim3(cnhip::SCE_BLOCK),
                      0, st, logits, targets, softmax_out, partial, batch, classes);
@@ -343,8 +343,7 @@ int cnhip_softmax_ce_forward(const float* logits, const float* targets, float* s
                        loss, divisor);
     status = cnhip::check_launch(who);
   }
-  const int st2 = cnhip::check_hip(hipFreeAsync(ws, st), who);
-  return status != CNHIP_OK ? status : st2;
+  return status;
 }
 
 int cnhip_softmax_ce_backward(const float* softmax, const float* targets, float* grad,

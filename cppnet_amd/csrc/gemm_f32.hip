@@ -43,7 +43,7 @@ constexpr int64_t KQ = 32;
 // Blocks of 512 threads run one per CU (their 64x64 wave tiles need ~150
 // VGPRs); 256-thread blocks are sized for two.
 template <class C>
-constexpr int min_blocks() { return C::NT >= 512 ? 1 : 2; }
+constexpr int min_blocks() { return C::NT >= 512 ? 4 : 2; }
 
 struct GemmArgs {
   int64_t M, N, K;
@@ -293,30 +293,36 @@ struct Plan {
 };
 
 // Tile shape and split-K plan of one GEMM; splits <= max_splits.
-// Split count for a tile shape by a cost model: dispatch rounds (256 block
-// slots for the 512-thread shapes, one per CU; 512 for the 256-thread ones)
-// times the K-tiles of one split, plus the fixed-order reduce of the partials
-// (read splits + 1 times M*N floats at ~5 TB/s, and a launch).  A split count
-// that leaves a nearly empty last round costs a whole extra round, so it is
-// avoided.  Splits keep >= 4 K-tiles of 32.  Returns the estimated seconds.
+// Cost model of one launch: dispatch rounds times the K-tiles of one split,
+// plus the fixed-order reduce of split-K partials (read splits + 1 times M*N
+// floats at ~5 TB/s, and a launch).  Block slots per round: the 512-thread
+// shapes are compiled for 4 waves per SIMD, so 2 blocks share a CU (512
+// slots); the 256-thread 64 x 64 and skinny tiles fit 4 per CU (1024).  A
+// split count that leaves a nearly empty last round costs a whole extra
+// round, so it is avoided.  `eff` is the measured MFMA efficiency of the
+// tile relative to the 64 x 64-per-wave tiles (smaller per-wave tiles load
+// more LDS bytes per MFMA).  Splits keep >= 4 K-tiles of 32.  Returns the
+// estimated seconds and the best split count.
 double split_cost(Shape shape, int64_t tiles, int64_t M, int64_t N, int64_t K, int64_t batches,
-                  int max_splits, int& splits) {
+                  int max_splits, bool may_split, int& splits) {
   int64_t bm = 0, bn = 0;
+  double eff = 1.0;
   switch (shape) {
     case Shape::XL: bm = CfgXL::BM; bn = CfgXL::BN; break;
     case Shape::XN: bm = CfgXN::BM; bn = CfgXN::BN; break;
-    case Shape::M: bm = CfgM::BM; bn = CfgM::BN; break;
-    case Shape::SN: bm = CfgSN::BM; bn = CfgSN::BN; break;
-    case Shape::SM: bm = CfgSM::BM; bn = CfgSM::BN; break;
-    case Shape::S: bm = CfgS::BM; bn = CfgS::BN; break;
+    case Shape::M: bm = CfgM::BM; bn = CfgM::BN; eff = 0.95; break;
+    case Shape::SN: bm = CfgSN::BM; bn = CfgSN::BN; eff = 0.8; break;
+    case Shape::SM: bm = CfgSM::BM; bn = CfgSM::BN; eff = 0.8; break;
+    case Shape::S: bm = CfgS::BM; bn = CfgS::BN; eff = 0.8; break;
   }
   const bool big = shape == Shape::XL || shape == Shape::XN || shape == Shape::M;
-  const int64_t slots = big ? 256 : 512;
-  // seconds per K-tile of 32 of one block at the MFMA peak of its CU share
-  const double t_tile = 2.0 * bm * bn * KQ / (157.3e12 / 256) * (big ? 1.0 : 2.0);
+  const int64_t per_cu = big ? 2 : 4;
+  const int64_t slots = 256 * per_cu;
+  // seconds per K-tile of 32 of one block, sharing its CU with per_cu - 1 others
+  const double t_tile = 2.0 * bm * bn * KQ / (157.3e12 / 256) * (double)per_cu / eff;
   const int64_t blocks = tiles * batches;
   int64_t max_s = 1;
-  if (blocks < slots && shape != Shape::XL && shape != Shape::XN && K >= 8 * KQ)
+  if (may_split && blocks < slots && K >= 8 * KQ)
     max_s = std::max<int64_t>(1, std::min<int64_t>(K / (4 * KQ), max_splits));
   double best = 0.0;
   splits = 1;
@@ -335,38 +341,41 @@ double split_cost(Shape shape, int64_t tiles, int64_t M, int64_t N, int64_t K, i
 
 Plan plan_gemm(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, int64_t batches,
                int max_splits) {
-  // Tile shape: skinny shapes waste no MFMA work on padding.  Large outputs
-  // take 128 x 256, or 256 x 128 when only A is k-contiguous in memory (the
-  // long tile side goes to the operand whose loads need no register
-  // transpose); otherwise 128 x 128 or 64 x 64 tiles with split-K, whichever
-  // the cost model above prefers.
+  // Skinny shapes take the 32-wide tiles (no MFMA work on padding), split by
+  // the cost model above.  Otherwise, in order (rules fitted to measured
+  // tile x split sweeps on MI355X, where the 512-thread tiles run 2 blocks
+  // per CU and split-K costs more than its reduce traffic alone):
+  //   128 x 256 (256 x 128 when only A is k-contiguous) if >= 512 blocks;
+  //   128 x 128 if >= 256 blocks;  64 x 64 if >= 512 blocks;
+  //   else split K: 128 x 128 toward 512 blocks (<= 16 splits) if that
+  //   reaches 256 blocks, otherwise 64 x 64 toward 512 blocks.
   Shape shape;
   int splits = 1;
   if (N <= 32 || M <= 32) {
     shape = N <= 32 ? Shape::SN : Shape::SM;
     split_cost(shape, shape == Shape::SN ? tiles_of<CfgSN>(M, N) : tiles_of<CfgSM>(M, N), M, N, K,
-               batches, max_splits, splits);
+               batches, max_splits, true, splits);
   } else {
     const bool a_kc = trans_a != 0, b_kc = trans_b == 0;
-    const bool wide = !(a_kc && !b_kc);  // 128 x 256 measured the most even across layouts
-    const int64_t tx = (wide ? tiles_of<CfgXN>(M, N) : tiles_of<CfgXL>(M, N)) * batches;
+    const Shape big = (a_kc && !b_kc) ? Shape::XL : Shape::XN;
+    const int64_t tb = (big == Shape::XL ? tiles_of<CfgXL>(M, N) : tiles_of<CfgXN>(M, N)) * batches;
     const int64_t tm = tiles_of<CfgM>(M, N) * batches;
-    // fraction of the last round of one-block-per-CU dispatch that is busy
-    auto fill = [](int64_t b) { return (double)b / (double)(((b + 255) / 256) * 256); };
-    if (tx >= 256 && fill(tx) >= 0.9 * fill(tm)) {
-      shape = wide ? Shape::XN : Shape::XL;
+    const int64_t ts = tiles_of<CfgS>(M, N) * batches;
+    const int64_t max_s = K >= 8 * KQ ? std::max<int64_t>(1, std::min<int64_t>(K / (4 * KQ), max_splits)) : 1;
+    if (tb >= 512) {
+      shape = big;
+    } else if (tm >= 256) {
+      shape = Shape::M;
+    } else if (ts >= 512) {
+      shape = Shape::S;
     } else {
-      int sm = 1, ss = 1;
-      const double cm = split_cost(Shape::M, tiles_of<CfgM>(M, N), M, N, K, batches, max_splits, sm);
-      const double cs = split_cost(Shape::S, tiles_of<CfgS>(M, N), M, N, K, batches, max_splits, ss);
-      // 128 x 128 tiles reuse each loaded element twice as often: prefer
-      // them unless 64 x 64 is clearly cheaper
-      if (cs < 0.8 * cm) {
-        shape = Shape::S;
-        splits = ss;
-      } else {
+      const int64_t sm = std::min<int64_t>({(512 + tm - 1) / tm, 16, max_s});
+      if (tm * sm >= 256) {
         shape = Shape::M;
-        splits = sm;
+        splits = (int)sm;
+      } else {
+        shape = Shape::S;
+        splits = (int)std::min<int64_t>((512 + ts - 1) / ts, max_s);
       }
     }
   }
@@ -474,7 +483,7 @@ int gemm_f32_core(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, flo
   if (splits > 1) {
     void* ws = nullptr;
     const size_t bytes = (size_t)batches * (size_t)splits * (size_t)M * (size_t)N * sizeof(float);
-    CNHIP_TRY(check_hip(hipMallocAsync(&ws, bytes, st), who));
+    CNHIP_TRY(scratch(st, kScratchGemm, bytes, &ws, who));
     g.partial = static_cast<float*>(ws);
   }
 
@@ -486,8 +495,6 @@ int gemm_f32_core(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, flo
                          dim3(256), 0, st, g, batches);
       status = check_launch(who);
     }
-    int st2 = check_hip(hipFreeAsync(g.partial, st), who);
-    if (status == CNHIP_OK) status = st2;
   }
   return status;
 }

@@ -226,9 +226,9 @@ struct Workspace {
   void* p = nullptr;
   hipStream_t st;
   explicit Workspace(hipStream_t s) : st(s) {}
-  int alloc(size_t bytes, const char* who) { return check_hip(hipMallocAsync(&p, bytes, st), who); }
+  int alloc(size_t bytes, const char* who) { return scratch(st, kScratchLayer, bytes, &p, who); }
   ~Workspace() {
-    if (p) (void)hipFreeAsync(p, st);
+    // nothing to free: the stream's scratch slot is reused by later calls
   }
 };
 

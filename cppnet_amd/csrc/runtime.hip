@@ -1,8 +1,12 @@
 // Runtime services of the C ABI: errors, devices, memory, streams, events.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdarg>
+#include <cstdint>
 #include <cstdio>
+#include <mutex>
+#include <vector>
 
 #include "common.hpp"
 
@@ -15,6 +19,61 @@ void set_error(const char* fmt, ...) {
   va_start(ap, fmt);
   vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
   va_end(ap);
+}
+
+int ws_alloc(void** ptr, size_t bytes, hipStream_t stream, const char* where) {
+  static std::atomic<uint64_t> configured{0};  // one bit per device (< 64)
+  int dev = 0;
+  CNHIP_TRY(check_hip(hipGetDevice(&dev), where));
+  const uint64_t bit = dev < 64 ? (uint64_t)1 << dev : 0;
+  if (bit && !(configured.load(std::memory_order_acquire) & bit)) {
+    hipMemPool_t pool;
+    CNHIP_TRY(check_hip(hipDeviceGetDefaultMemPool(&pool, dev), where));
+    uint64_t keep = UINT64_MAX;
+    CNHIP_TRY(check_hip(hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep), where));
+    configured.fetch_or(bit, std::memory_order_acq_rel);
+  }
+  return check_hip(hipMallocAsync(ptr, bytes, stream), where);
+}
+
+namespace {
+struct ScratchEntry {
+  int dev;
+  hipStream_t stream;
+  int slot;
+  void* p;
+  size_t cap;
+};
+std::mutex g_scratch_mu;
+std::vector<ScratchEntry> g_scratch;
+}  // namespace
+
+int scratch(hipStream_t stream, int slot, size_t bytes, void** ptr, const char* where) {
+  int dev = 0;
+  CNHIP_TRY(check_hip(hipGetDevice(&dev), where));
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  ScratchEntry* e = nullptr;
+  for (auto& x : g_scratch)
+    if (x.dev == dev && x.stream == stream && x.slot == slot) e = &x;
+  if (!e) {
+    g_scratch.push_back(ScratchEntry{dev, stream, slot, nullptr, 0});
+    e = &g_scratch.back();
+  }
+  if (e->cap < bytes) {
+    if (e->p) {
+      void* old = e->p;
+      e->p = nullptr;
+      e->cap = 0;
+      CNHIP_TRY(check_hip(hipFreeAsync(old, stream), where));
+    }
+    // grow with headroom, in 2 MiB steps, so slowly rising sizes settle
+    size_t cap = bytes + bytes / 4;
+    cap = (cap + ((size_t)2 << 20) - 1) & ~(((size_t)2 << 20) - 1);
+    CNHIP_TRY(ws_alloc(&e->p, cap, stream, where));
+    e->cap = cap;
+  }
+  *ptr = e->p;
+  return CNHIP_OK;
 }
 
 }  // namespace cnhip
