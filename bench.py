@@ -112,7 +112,7 @@ CPU_BATCH = {1: 512, 2: 512, 3: 32, 4: 16, 5: 4}
 # PMC runs (FETCH_SIZE, WRITE_SIZE) scaled by a reference kernel of known
 # traffic; the runs, factors and per-GEMM table are in
 # profiles/gemm_f32_config2_traffic.md.  Configs not yet measured report null.
-PMC_TRAFFIC_BYTES = {2: 370.6e6}
+PMC_TRAFFIC_BYTES = {2: 337.7e6}
 
 
 def cpu_baseline(config: int, seconds_budget: float = 20.0):
@@ -146,6 +146,26 @@ def cpu_baseline(config: int, seconds_budget: float = 20.0):
                        f"{threads} OpenMP threads), {el:.1f} s")}
 
 
+def traffic_calibration() -> int:
+    """A kernel whose HBM traffic is known, for scaling PMC byte counters:
+    cnhip_add(a, b, c, n) reads 2n floats and writes n."""
+    import ctypes as C
+    from cppnet_amd import _capi
+    lib = _capi.load()
+    n = 64 * 1024 * 1024
+    bufs = [C.c_void_p() for _ in range(3)]
+    for q in bufs:
+        _capi.check(lib.cnhip_malloc(C.byref(q), n * 4))
+        _capi.check(lib.cnhip_memset_async(q, 0, n * 4, None))
+    for _ in range(5):
+        _capi.check(lib.cnhip_add(bufs[0], bufs[1], bufs[2], n, None))
+    _capi.check(lib.cnhip_device_synchronize())
+    for q in bufs:
+        _capi.check(lib.cnhip_free(q))
+    log(f"bench.py: traffic calibration done (cnhip_add, n = {n}, 5 launches)")
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -154,7 +174,13 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--traffic-calibration", action="store_true",
+                    help="only run the known-traffic reference kernel (cnhip_add over 64 Mi floats, "
+                         "5 times: 512 MiB read + 256 MiB written per launch) that scales the PMC "
+                         "FETCH_SIZE / WRITE_SIZE counts behind roofline.traffic")
     args = ap.parse_args()
+    if args.traffic_calibration:
+        return traffic_calibration()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (got --gpus {args.gpus}); the "
               "multi-GPU data-parallel design is described, not built", file=sys.stderr)
