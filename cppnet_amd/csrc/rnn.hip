@@ -22,6 +22,7 @@
 #include <cmath>
 
 #include "common.hpp"
+#include "mfma_kpack.hpp"
 
 namespace cnhip {
 
@@ -76,6 +77,104 @@ __global__ void __launch_bounds__(256) lstm_cell_fwd_kernel(float* __restrict__ 
   const float gg = tanhf(pre(d + 2 * H) + bias[d + 2 * H]);
   const float og = sigm(pre(d + 3 * H) + bias[d + 3 * H]);
   const float cprev = t > 0 ? c[row - B + BS * d] : 0.0f;
+  const float ct = fg * cprev + ig * gg;
+  const float tc = tanhf(ct);
+  g[BS * d] = ig;
+  g[BS * (d + H)] = fg;
+  g[BS * (d + 2 * H)] = gg;
+  g[BS * (d + 3 * H)] = og;
+  c[row + BS * d] = ct;
+  tanh_c[row + BS * d] = tc;
+  Y[row + BS * d] = og * tc;
+}
+
+// One forward timestep t >= 1 in one launch: the recurrent GEMM
+// h_{t-1} W_hh for a tile of 32 samples x (8 hidden units x 4 gates) and
+// the cell update of those 256 (sample, unit) pairs in its epilogue.  The 4
+// gate columns of a unit sit in one tile, so no other block's result is
+// needed; the k-tile (64) is split over 4 wave groups whose partial sums are
+// added in a fixed order.  256 blocks cover B = 128, H = 512.
+using kp::f32x4;
+using LstmCfg = kp::Cfg<1, 1, 1, 1, 16, 4>;
+constexpr int kLstmUnits = 8;  // hidden units per tile
+
+template <bool FAST>
+struct LstmFwdStage {
+  using OA = kp::Operand<false, 32, LstmCfg::NT, LstmCfg::KT>;  // h(b, k) = Y[b + B(t-1) + BS k]
+  using OB = kp::Operand<true, 32, LstmCfg::NT, LstmCfg::KT>;   // W_hh(k, col(n)), k-contiguous
+  const float* A;  // Y + B*(t-1)
+  const float* W;
+  int64_t BS, B, H, b0, j0;
+  f32x4 ra[2][OA::REGS], rb[2][OB::REGS];
+
+  __device__ LstmFwdStage(const float* A_, const float* W_, int64_t BS_, int64_t B_, int64_t H_,
+                          int64_t b0_, int64_t j0_)
+      : A(A_), W(W_), BS(BS_), B(B_), H(H_), b0(b0_), j0(j0_) {}
+
+  template <int S>
+  __device__ __forceinline__ void load(int t) {
+    const int64_t k0 = (int64_t)t * LstmCfg::KT;
+    OA::template load<FAST>(A, BS, b0, k0, B, H, ra[S]);
+#pragma unroll
+    for (int p = 0; p < OB::PER; ++p) {
+      int r, k;
+      if (!OB::origin(p, r, k)) break;
+      // tile column r = gate * 8 + unit: W_hh column gate*H + j0 + unit
+      const int64_t j = j0 + r % kLstmUnits, gk = k0 + k;
+      const float* col = W + H * ((r / kLstmUnits) * H + j);
+      if (FAST) {
+        rb[S][p] = *reinterpret_cast<const f32x4*>(col + gk);
+      } else {
+        f32x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = (j < H && gk + e < H) ? col[gk + e] : 0.f;
+        rb[S][p] = v;
+      }
+    }
+  }
+  template <int S>
+  __device__ __forceinline__ void store(float* buf) {
+    OA::store(buf, ra[S]);
+    OB::store(buf + OA::FLOATS, rb[S]);
+  }
+};
+
+template <bool FAST>
+__global__ void __launch_bounds__(LstmCfg::NT) lstm_step_fwd_kernel(
+    float* __restrict__ gates, const float* __restrict__ bias, float* __restrict__ c,
+    float* __restrict__ tanh_c, float* __restrict__ Y, const float* __restrict__ W_hh, int64_t B,
+    int64_t S, int64_t H, int64_t t) {
+  constexpr int FLOATS = 2 * kp::stage_floats<LstmFwdStage<FAST>>();
+  static_assert((LstmCfg::WGK - 1) * 1024 <= FLOATS, "reduce_wgk needs more LDS");
+  __shared__ __align__(16) float lds[FLOATS];
+  __shared__ float tile[32 * 33];  // [col][row], padded
+  const int64_t BS = B * S;
+  const int nbt = (int)((B + 31) / 32);
+  const int64_t b0 = (int64_t)(blockIdx.x % nbt) * 32;
+  const int64_t j0 = (int64_t)(blockIdx.x / nbt) * kLstmUnits;
+  kp::f32x16 acc[1][1];
+  kp::zero_acc<LstmCfg>(acc);
+  LstmFwdStage<FAST> s(Y + B * (t - 1), W_hh, BS, B, H, b0, j0);
+  kp::pipeline<LstmCfg>((int)((H + LstmCfg::KT - 1) / LstmCfg::KT), lds, s, acc);
+  kp::reduce_wgk<LstmCfg>(lds, acc);
+  kp::for_each_acc_run<LstmCfg>(acc, [&](int ml, int nl, const kp::f32x4& v) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) tile[(ml + e) + 33 * nl] = v[e];
+  });
+  __syncthreads();
+  // thread -> (sample, unit); the cell of lstm_cell_fwd_kernel with the
+  // recurrent term h W_hh taken from the tile
+  const int bl = threadIdx.x % 32, u = threadIdx.x / 32;
+  const int64_t n = b0 + bl, d = j0 + u;
+  if (n >= B || d >= H) return;
+  const int64_t row = n + B * t;
+  float* g = gates + row;
+  auto pre = [&](int gate, int64_t j) { return tile[bl + 33 * (gate * kLstmUnits + u)] + g[BS * j]; };
+  const float ig = sigm(pre(0, d) + bias[d]);
+  const float fg = sigm(pre(1, d + H) + bias[d + H]);
+  const float gg = tanhf(pre(2, d + 2 * H) + bias[d + 2 * H]);
+  const float og = sigm(pre(3, d + 3 * H) + bias[d + 3 * H]);
+  const float cprev = c[row - B + BS * d];
   const float ct = fg * cprev + ig * gg;
   const float tc = tanhf(ct);
   g[BS * d] = ig;
@@ -247,18 +346,23 @@ int cnhip_lstm_forward(const float* X, const float* W_ih, const float* W_hh, con
   CNHIP_REQUIRE(X && W_ih && W_hh && b && Y && gates && c && tanh_c, "%s: NULL pointer", who);
   hipStream_t st = as_stream(stream);
   const int64_t G = 4 * H, BS = B * S;
-  constexpr int kMaxSplits = 8;
-  cnhip::Workspace ws(st);
-  CNHIP_TRY(ws.alloc((size_t)kMaxSplits * B * G * sizeof(float), who));
-  float* hw = static_cast<float*>(ws.p);
   CNHIP_TRY(cnhip::gemm_f32(0, 0, BS, G, I, 1.f, X, BS, W_ih, I, 0.f, gates, BS, nullptr, 0, st, who));
-  for (int64_t t = 0; t < S; ++t) {
-    int ns = 0;  // h_0 = 0: no recurrent term at t = 0
-    if (t > 0)
-      CNHIP_TRY(cnhip::gemm_f32_partials(0, 0, B, G, H, Y + B * (t - 1), BS, W_hh, H, hw, kMaxSplits,
-                                         &ns, st, who));
-    hipLaunchKernelGGL(cnhip::lstm_cell_fwd_kernel, dim3(cnhip::cell_grid(B, H)), dim3(256), 0, st,
-                       gates, b, c, tanh_c, Y, hw, ns, B, S, H, t);
+  // t = 0: h_0 = 0, no recurrent term; then one fused GEMM + cell launch per step
+  hipLaunchKernelGGL(cnhip::lstm_cell_fwd_kernel, dim3(cnhip::cell_grid(B, H)), dim3(256), 0, st,
+                     gates, b, c, tanh_c, Y, nullptr, 0, B, S, H, (int64_t)0);
+  CNHIP_TRY(cnhip::check_launch(who));
+  const int64_t nbt = (B + 31) / 32, nbu = (H + cnhip::kLstmUnits - 1) / cnhip::kLstmUnits;
+  CNHIP_REQUIRE(nbt * nbu < ((int64_t)1 << 31), "%s: too many tiles", who);
+  // FAST: full tiles, whole k-tiles, 16-byte aligned rows of Y and W_hh
+  const bool fast = B % 32 == 0 && H % cnhip::LstmCfg::KT == 0 && H % cnhip::kLstmUnits == 0 &&
+                    BS % 4 == 0 && cnhip::aligned16(Y) && cnhip::aligned16(W_hh);
+  for (int64_t t = 1; t < S; ++t) {
+    if (fast)
+      hipLaunchKernelGGL(cnhip::lstm_step_fwd_kernel<true>, dim3((unsigned)(nbt * nbu)),
+                         dim3(cnhip::LstmCfg::NT), 0, st, gates, b, c, tanh_c, Y, W_hh, B, S, H, t);
+    else
+      hipLaunchKernelGGL(cnhip::lstm_step_fwd_kernel<false>, dim3((unsigned)(nbt * nbu)),
+                         dim3(cnhip::LstmCfg::NT), 0, st, gates, b, c, tanh_c, Y, W_hh, B, S, H, t);
     CNHIP_TRY(cnhip::check_launch(who));
   }
   return CNHIP_OK;

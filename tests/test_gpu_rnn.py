@@ -34,7 +34,7 @@ def _inputs(rng, B, S, I, H, G):
     return X, Wih, Whh, b, dY
 
 
-RNN_CASES = [(3, 5, 4, 8), (8, 7, 16, 32), (5, 1, 3, 6), (128, 64, 128, 512)]
+RNN_CASES = [(3, 5, 4, 8), (8, 7, 16, 32), (5, 1, 3, 6), (40, 6, 12, 71), (128, 64, 128, 512)]
 
 
 @pytest.mark.parametrize("B,S,I,H", RNN_CASES)
