@@ -43,7 +43,7 @@ struct Cfg {
   static constexpr int BN = WGN * WN * 32;
   static constexpr int NT = WGM * WGN * WGK * 64;
   static_assert(BK == 16 || BK == 32, "BK must be 16 or 32");
-  static_assert(WGK == 1 || WGK == 2 || WGK == 4, "WGK must be 1, 2 or 4");
+  static_assert(WGK == 1 || WGK == 2 || WGK == 4 || WGK == 8, "WGK must be 1, 2, 4 or 8");
 };
 
 // Wave -> (wm, wn, wk) position in the block.
@@ -233,6 +233,112 @@ __device__ __forceinline__ void reduce_wgk(float* lds, f32x16 (&acc)[C::WM][C::W
   }
 }
 
+// ------------------------------------------------------------------
+// 16 x 16 accumulator tiles (v_mfma_f32_16x16x4f32), for problems whose
+// output is too small to give every CU a 32 x 32 tile.  Same Operand tiles
+// and pipeline; a wave holds WM x WN blocks of 16 x 16 (4 floats per lane).
+// In each 4-step group, lane group q = lane/16 supplies k = 4q + step, so a
+// lane's fragment is again 4 consecutive k of one row (one ds_read_b128 for
+// k-contiguous tiles, four ds_read_b32 otherwise; the four lane groups sit
+// 16 banks apart in both layouts).
+template <int WGM_, int WGN_, int WM_, int WN_, int BK_ = 16, int WGK_ = 1>
+struct Cfg16 {
+  static constexpr int WGM = WGM_, WGN = WGN_, WM = WM_, WN = WN_;
+  static constexpr int BK = BK_, WGK = WGK_;
+  static constexpr int KT = BK * WGK;
+  static constexpr int BM = WGM * WM * 16;
+  static constexpr int BN = WGN * WN * 16;
+  static constexpr int NT = WGM * WGN * WGK * 64;
+  static_assert(BK % 16 == 0, "BK must be a multiple of 16");
+  static_assert(WGK == 1 || WGK == 2 || WGK == 4 || WGK == 8, "WGK must be 1, 2, 4 or 8");
+};
+
+template <class C>
+__device__ __forceinline__ void zero_acc16(f32x4 (&acc)[C::WM][C::WN]) {
+#pragma unroll
+  for (int i = 0; i < C::WM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::WN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+}
+
+template <class C, class OA, class OB>
+__device__ __forceinline__ void mfma_ktile16(const float* __restrict__ la,
+                                             const float* __restrict__ lb,
+                                             f32x4 (&acc)[C::WM][C::WN]) {
+  const int lane = threadIdx.x & 63;
+  int wm, wn, wk;
+  wave_pos<C>(wm, wn, wk);
+  const int q = lane >> 4, r = lane & 15;
+  const int ra = wm * (C::WM * 16) + r, rb = wn * (C::WN * 16) + r;
+  const int kb = wk * C::BK + 4 * q;
+#pragma unroll
+  for (int c = 0; c < C::BK / 16; ++c) {
+    f32x4 a[C::WM], b[C::WN];
+#pragma unroll
+    for (int i = 0; i < C::WM; ++i) a[i] = OA::frag(la, ra + 16 * i, kb + 16 * c);
+#pragma unroll
+    for (int j = 0; j < C::WN; ++j) b[j] = OB::frag(lb, rb + 16 * j, kb + 16 * c);
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+      for (int i = 0; i < C::WM; ++i)
+#pragma unroll
+        for (int j = 0; j < C::WN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][e], b[j][e], acc[i][j], 0, 0, 0);
+  }
+}
+
+// Accumulator layout of v_mfma_f32_16x16x4f32: lane holds column lane%16
+// and rows 4*(lane/16) + r, r = 0..3.  Only wk == 0 waves visit.
+template <class C, class F>
+__device__ __forceinline__ void for_each_acc_run16(const f32x4 (&acc)[C::WM][C::WN], F&& f) {
+  const int lane = threadIdx.x & 63;
+  int wm, wn, wk;
+  wave_pos<C>(wm, wn, wk);
+  if (C::WGK > 1 && wk != 0) return;
+#pragma unroll
+  for (int i = 0; i < C::WM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::WN; ++j)
+      f(wm * (C::WM * 16) + i * 16 + 4 * (lane >> 4), wn * (C::WN * 16) + j * 16 + (lane & 15),
+        acc[i][j]);
+}
+
+// reduce_wgk for 16 x 16 accumulators: (WGK-1) * WGM*WGN * WM*WN * 4 * 64
+// floats of lds.
+template <class C>
+__device__ __forceinline__ void reduce_wgk16(float* lds, f32x4 (&acc)[C::WM][C::WN]) {
+  if constexpr (C::WGK > 1) {
+    const int lane = threadIdx.x & 63;
+    int wm, wn, wk;
+    wave_pos<C>(wm, wn, wk);
+    constexpr int PER_WAVE = C::WM * C::WN * 4 * 64;
+    const int slot = wm + C::WGM * wn;
+    if (wk > 0) {
+      float* dst = lds + ((wk - 1) * C::WGM * C::WGN + slot) * PER_WAVE;
+#pragma unroll
+      for (int i = 0; i < C::WM; ++i)
+#pragma unroll
+        for (int j = 0; j < C::WN; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) dst[((i * C::WN + j) * 4 + r) * 64 + lane] = acc[i][j][r];
+    }
+    __syncthreads();
+    if (wk == 0) {
+#pragma unroll
+      for (int g = 1; g < C::WGK; ++g) {
+        const float* src = lds + ((g - 1) * C::WGM * C::WGN + slot) * PER_WAVE;
+#pragma unroll
+        for (int i = 0; i < C::WM; ++i)
+#pragma unroll
+          for (int j = 0; j < C::WN; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[i][j][r] += src[((i * C::WN + j) * 4 + r) * 64 + lane];
+      }
+    }
+  }
+}
+
 // LDS floats of one pipeline buffer of a stage (A tile, then B tile); the
 // pipeline double-buffers it.
 template <class Stage>
@@ -251,9 +357,16 @@ constexpr int stage_floats() {
 // one register assignment around the loop (a mid-body exit made the compiler
 // copy every accumulator between two register sets each iteration).
 // Ends with a barrier, after which lds may be reused.
-template <class C, class Stage>
-__device__ __forceinline__ void pipeline(int ntiles, float* lds, Stage& s,
-                                         f32x16 (&acc)[C::WM][C::WN]) {
+template <class C, class OA, class OB, class Acc>
+__device__ __forceinline__ void ktile_any(const float* la, const float* lb, Acc& acc) {
+  if constexpr (sizeof(acc[0][0]) == sizeof(f32x16))
+    mfma_ktile<C, OA, OB>(la, lb, acc);
+  else
+    mfma_ktile16<C, OA, OB>(la, lb, acc);
+}
+
+template <class C, class Stage, class Acc>
+__device__ __forceinline__ void pipeline(int ntiles, float* lds, Stage& s, Acc& acc) {
   using OA = typename Stage::OA;
   using OB = typename Stage::OB;
   float* buf0 = lds;
@@ -269,12 +382,12 @@ __device__ __forceinline__ void pipeline(int ntiles, float* lds, Stage& s,
   int kt = 0;
   for (; kt + 1 < ntiles; kt += 2) {
     // tile kt in buf0, kt+1 in set 0, kt+2 in set 1
-    mfma_ktile<C, OA, OB>(buf0, buf0 + BOFF, acc);
+    ktile_any<C, OA, OB>(buf0, buf0 + BOFF, acc);
     s.template store<0>(buf1);
     if (kt + 3 < ntiles) s.template load<0>(kt + 3);
     __syncthreads();
     // tile kt+1 in buf1, kt+2 in set 1, kt+3 in set 0
-    mfma_ktile<C, OA, OB>(buf1, buf1 + BOFF, acc);
+    ktile_any<C, OA, OB>(buf1, buf1 + BOFF, acc);
     if (kt + 2 < ntiles) {
       s.template store<1>(buf0);
       if (kt + 4 < ntiles) s.template load<1>(kt + 4);
@@ -282,7 +395,7 @@ __device__ __forceinline__ void pipeline(int ntiles, float* lds, Stage& s,
     __syncthreads();
   }
   if (kt < ntiles) {  // odd count: the last tile is in buf0
-    mfma_ktile<C, OA, OB>(buf0, buf0 + BOFF, acc);
+    ktile_any<C, OA, OB>(buf0, buf0 + BOFF, acc);
     __syncthreads();
   }
 }

@@ -10,10 +10,12 @@
 // The reference computes x_t W_ih and every weight gradient inside its time
 // loop.  Here the parts that do not depend on the recurrence run once over
 // all B*S rows as large MFMA GEMMs:
-//   forward : G = X W_ih (all steps)       then per step G_t += h_{t-1} W_hh
-//   backward: per step only the cell kernel and dh_{t-1} = dG_t W_hh^T;
-//             afterwards dW_ih = X^T dG, dW_hh = Y_{t-1}^T dG, db = colsum dG,
-//             dX = dG W_ih^T, each a single GEMM over all B*S rows.
+//   forward : G = X W_ih (all steps), then per step one launch of
+//             h_{t-1} W_hh with the LSTM cell in its epilogue
+//   backward: per step one launch of dh_t = dY_t + dG_{t+1} W_hh^T with the
+//             cell backward in its epilogue; afterwards dW_ih = X^T dG,
+//             dW_hh = Y_{t-1}^T dG, db = colsum dG, dX = dG W_ih^T, each a
+//             single GEMM over all B*S rows.
 // The cell kernels fuse every elementwise gate computation of a step into one
 // pass (one thread per (n, d); n fastest for coalescing) and evaluate the
 // reference expressions in the reference's operation order.
@@ -95,10 +97,10 @@ __global__ void __launch_bounds__(256) lstm_cell_fwd_kernel(float* __restrict__ 
 // needed; the k-tile (64) is split over 4 wave groups whose partial sums are
 // added in a fixed order.  256 blocks cover B = 128, H = 512.
 using kp::f32x4;
-using LstmCfg = kp::Cfg<1, 1, 1, 1, 16, 4>;
+using LstmFwdCfg = kp::Cfg<1, 1, 1, 1, 16, 4>;
 constexpr int kLstmUnits = 8;  // hidden units per tile
 
-template <bool FAST>
+template <class LstmCfg, bool FAST>
 struct LstmFwdStage {
   using OA = kp::Operand<false, 32, LstmCfg::NT, LstmCfg::KT>;  // h(b, k) = Y[b + B(t-1) + BS k]
   using OB = kp::Operand<true, 32, LstmCfg::NT, LstmCfg::KT>;   // W_hh(k, col(n)), k-contiguous
@@ -139,12 +141,12 @@ struct LstmFwdStage {
   }
 };
 
-template <bool FAST>
+template <class LstmCfg, bool FAST>
 __global__ void __launch_bounds__(LstmCfg::NT) lstm_step_fwd_kernel(
     float* __restrict__ gates, const float* __restrict__ bias, float* __restrict__ c,
     float* __restrict__ tanh_c, float* __restrict__ Y, const float* __restrict__ W_hh, int64_t B,
     int64_t S, int64_t H, int64_t t) {
-  constexpr int FLOATS = 2 * kp::stage_floats<LstmFwdStage<FAST>>();
+  constexpr int FLOATS = 2 * kp::stage_floats<LstmFwdStage<LstmCfg, FAST>>();
   static_assert((LstmCfg::WGK - 1) * 1024 <= FLOATS, "reduce_wgk needs more LDS");
   __shared__ __align__(16) float lds[FLOATS];
   __shared__ float tile[32 * 33];  // [col][row], padded
@@ -154,7 +156,7 @@ __global__ void __launch_bounds__(LstmCfg::NT) lstm_step_fwd_kernel(
   const int64_t j0 = (int64_t)(blockIdx.x / nbt) * kLstmUnits;
   kp::f32x16 acc[1][1];
   kp::zero_acc<LstmCfg>(acc);
-  LstmFwdStage<FAST> s(Y + B * (t - 1), W_hh, BS, B, H, b0, j0);
+  LstmFwdStage<LstmCfg, FAST> s(Y + B * (t - 1), W_hh, BS, B, H, b0, j0);
   kp::pipeline<LstmCfg>((int)((H + LstmCfg::KT - 1) / LstmCfg::KT), lds, s, acc);
   kp::reduce_wgk<LstmCfg>(lds, acc);
   kp::for_each_acc_run<LstmCfg>(acc, [&](int ml, int nl, const kp::f32x4& v) {
@@ -164,7 +166,9 @@ __global__ void __launch_bounds__(LstmCfg::NT) lstm_step_fwd_kernel(
   __syncthreads();
   // thread -> (sample, unit); the cell of lstm_cell_fwd_kernel with the
   // recurrent term h W_hh taken from the tile
+  static_assert(LstmCfg::NT >= 32 * kLstmUnits, "one thread per (sample, unit)");
   const int bl = threadIdx.x % 32, u = threadIdx.x / 32;
+  if (u >= kLstmUnits) return;
   const int64_t n = b0 + bl, d = j0 + u;
   if (n >= B || d >= H) return;
   const int64_t row = n + B * t;
@@ -202,6 +206,81 @@ __global__ void __launch_bounds__(256) lstm_cell_bwd_kernel(
   const float tc = tanh_c[row + BS * d];
   const float dh = dY[row + BS * d] + (first ? 0.0f : partial_sum(dh_in, nsplit, B * H, e));
   const float dc = dh * og * (1.0f - tc * tc) + (first ? 0.0f : dc_buf[e]);
+  const float cprev = t > 0 ? c[row - B + BS * d] : 0.0f;
+  dG[row + BS * d] = dc * gg * ig * (1.0f - ig);
+  dG[row + BS * (d + H)] = dc * cprev * fg * (1.0f - fg);
+  dG[row + BS * (d + 2 * H)] = dc * ig * (1.0f - gg * gg);
+  dG[row + BS * (d + 3 * H)] = dh * tc * og * (1.0f - og);
+  dc_buf[e] = dc * fg;
+}
+
+// One backward timestep t <= S-2 in one launch: dh_t = dY_t + dG_{t+1} W_hh^T
+// for a tile of 16 samples x 16 hidden units (K = 4H split over the wave
+// groups of the block, added in a fixed order), then lstm_cell_bwd_kernel's
+// arithmetic for those 256 (sample, unit) pairs in the epilogue.  16 x 16
+// tiles give 256 blocks at B = 128, H = 512.
+using LstmBwdCfgDefault = kp::Cfg16<1, 1, 1, 1, 32, 8>;  // fastest of a measured sweep
+
+template <class LstmBwdCfg, bool FAST>
+struct LstmBwdStage {
+  using OA = kp::Operand<false, 16, LstmBwdCfg::NT, LstmBwdCfg::KT>;  // dG(b, k) = dG[b + BS k]
+  using OB = kp::Operand<false, 16, LstmBwdCfg::NT, LstmBwdCfg::KT>;  // W_hh^T(j, k) = W_hh[j + H k]
+  const float* A;  // dG + B*(t+1)
+  const float* W;
+  int64_t BS, B, H, b0, j0;
+  f32x4 ra[2][OA::REGS], rb[2][OB::REGS];
+
+  __device__ LstmBwdStage(const float* A_, const float* W_, int64_t BS_, int64_t B_, int64_t H_,
+                          int64_t b0_, int64_t j0_)
+      : A(A_), W(W_), BS(BS_), B(B_), H(H_), b0(b0_), j0(j0_) {}
+
+  template <int S>
+  __device__ __forceinline__ void load(int t) {
+    const int64_t k0 = (int64_t)t * LstmBwdCfg::KT;
+    OA::template load<FAST>(A, BS, b0, k0, B, 4 * H, ra[S]);
+    OB::template load<FAST>(W, H, j0, k0, H, 4 * H, rb[S]);
+  }
+  template <int S>
+  __device__ __forceinline__ void store(float* buf) {
+    OA::store(buf, ra[S]);
+    OB::store(buf + OA::FLOATS, rb[S]);
+  }
+};
+
+template <class LstmBwdCfg, bool FAST>
+__global__ void __launch_bounds__(LstmBwdCfg::NT) lstm_step_bwd_kernel(
+    const float* __restrict__ gates, const float* __restrict__ c, const float* __restrict__ tanh_c,
+    const float* __restrict__ dY, const float* __restrict__ W_hh, float* __restrict__ dc_buf,
+    float* __restrict__ dG, int64_t B, int64_t S, int64_t H, int64_t t) {
+  constexpr int FLOATS = 2 * kp::stage_floats<LstmBwdStage<LstmBwdCfg, FAST>>();
+  static_assert((LstmBwdCfg::WGK - 1) * 4 * 64 <= FLOATS, "reduce_wgk16 needs more LDS");
+  __shared__ __align__(16) float lds[FLOATS];
+  __shared__ float tile[16 * 17];  // [unit][sample], padded
+  const int64_t BS = B * S;
+  const int nbt = (int)((B + 15) / 16);
+  const int64_t b0 = (int64_t)(blockIdx.x % nbt) * 16;
+  const int64_t j0 = (int64_t)(blockIdx.x / nbt) * 16;
+  f32x4 acc[1][1];
+  kp::zero_acc16<LstmBwdCfg>(acc);
+  LstmBwdStage<LstmBwdCfg, FAST> s(dG + B * (t + 1), W_hh, BS, B, H, b0, j0);
+  kp::pipeline<LstmBwdCfg>((int)((4 * H + LstmBwdCfg::KT - 1) / LstmBwdCfg::KT), lds, s, acc);
+  kp::reduce_wgk16<LstmBwdCfg>(lds, acc);
+  kp::for_each_acc_run16<LstmBwdCfg>(acc, [&](int ml, int nl, const f32x4& v) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) tile[(ml + e) + 17 * nl] = v[e];
+  });
+  __syncthreads();
+  static_assert(LstmBwdCfg::NT >= 256, "one thread per (sample, unit)");
+  const int bl = threadIdx.x % 16, jl = threadIdx.x / 16;
+  if (jl >= 16) return;
+  const int64_t n = b0 + bl, d = j0 + jl;
+  if (n >= B || d >= H) return;
+  const int64_t e = n + B * d, row = n + B * t;
+  const float ig = gates[row + BS * d], fg = gates[row + BS * (d + H)];
+  const float gg = gates[row + BS * (d + 2 * H)], og = gates[row + BS * (d + 3 * H)];
+  const float tc = tanh_c[row + BS * d];
+  const float dh = dY[row + BS * d] + tile[bl + 17 * jl];
+  const float dc = dh * og * (1.0f - tc * tc) + dc_buf[e];
   const float cprev = t > 0 ? c[row - B + BS * d] : 0.0f;
   dG[row + BS * d] = dc * gg * ig * (1.0f - ig);
   dG[row + BS * (d + H)] = dc * cprev * fg * (1.0f - fg);
@@ -314,6 +393,51 @@ __global__ void __launch_bounds__(256) seq_scatter_kernel(const float* __restric
 
 unsigned cell_grid(int64_t B, int64_t H) { return (unsigned)((B * H + 255) / 256); }
 
+// Per-step launches of the fused LSTM kernels for steps t = 1 .. S-1
+// (forward) and t = S-2 .. 0 (backward), each timed like a GEMM (2*B*4H*H
+// flops) for the per-launch roofline.
+template <class Cfg>
+int lstm_fwd_steps(float* gates, const float* b, float* c, float* tanh_c, float* Y,
+                   const float* W_hh, int64_t B, int64_t S, int64_t H, hipStream_t st,
+                   const char* who) {
+  const int64_t nbt = (B + 31) / 32, nbu = (H + kLstmUnits - 1) / kLstmUnits;
+  CNHIP_REQUIRE(nbt * nbu < ((int64_t)1 << 31), "%s: too many tiles", who);
+  // FAST: full tiles, whole k-tiles, 16-byte aligned rows of Y and W_hh
+  const bool fast = B % 32 == 0 && H % Cfg::KT == 0 && H % kLstmUnits == 0 && (B * S) % 4 == 0 &&
+                    aligned16(Y) && aligned16(W_hh);
+  const auto kern = fast ? &lstm_step_fwd_kernel<Cfg, true> : &lstm_step_fwd_kernel<Cfg, false>;
+  for (int64_t t = 1; t < S; ++t) {
+    TimingRec* rec = timing_slot(2.0 * B * 4 * H * H);
+    if (rec) (void)hipEventRecord(rec->start, st);
+    hipLaunchKernelGGL(kern, dim3((unsigned)(nbt * nbu)), dim3(Cfg::NT), 0, st, gates, b, c, tanh_c,
+                       Y, W_hh, B, S, H, t);
+    CNHIP_TRY(check_launch(who));
+    if (rec) (void)hipEventRecord(rec->stop, st);
+  }
+  return CNHIP_OK;
+}
+
+template <class Cfg>
+int lstm_bwd_steps(const float* gates, const float* c, const float* tanh_c, const float* dY,
+                   const float* W_hh, float* dc, float* dG, int64_t B, int64_t S, int64_t H,
+                   hipStream_t st, const char* who) {
+  const int64_t nbt = (B + 15) / 16, nbu = (H + 15) / 16;
+  CNHIP_REQUIRE(nbt * nbu < ((int64_t)1 << 31), "%s: too many tiles", who);
+  // FAST: full tiles, whole k-tiles, 16-byte aligned rows (dG is a scratch buffer)
+  const bool fast = B % 16 == 0 && H % 16 == 0 && (4 * H) % Cfg::KT == 0 && (B * S) % 4 == 0 &&
+                    aligned16(W_hh);
+  const auto kern = fast ? &lstm_step_bwd_kernel<Cfg, true> : &lstm_step_bwd_kernel<Cfg, false>;
+  for (int64_t t = S - 2; t >= 0; --t) {
+    TimingRec* rec = timing_slot(2.0 * B * 4 * H * H);
+    if (rec) (void)hipEventRecord(rec->start, st);
+    hipLaunchKernelGGL(kern, dim3((unsigned)(nbt * nbu)), dim3(Cfg::NT), 0, st, gates, c, tanh_c, dY,
+                       W_hh, dc, dG, B, S, H, t);
+    CNHIP_TRY(check_launch(who));
+    if (rec) (void)hipEventRecord(rec->stop, st);
+  }
+  return CNHIP_OK;
+}
+
 int check_rnn(int64_t B, int64_t S, int64_t I, int64_t H, const char* who) {
   CNHIP_REQUIRE(B > 0 && S > 0 && I > 0 && H > 0, "%s: bad shape B=%lld S=%lld I=%lld H=%lld", who,
                 (long long)B, (long long)S, (long long)I, (long long)H);
@@ -351,21 +475,7 @@ int cnhip_lstm_forward(const float* X, const float* W_ih, const float* W_hh, con
   hipLaunchKernelGGL(cnhip::lstm_cell_fwd_kernel, dim3(cnhip::cell_grid(B, H)), dim3(256), 0, st,
                      gates, b, c, tanh_c, Y, nullptr, 0, B, S, H, (int64_t)0);
   CNHIP_TRY(cnhip::check_launch(who));
-  const int64_t nbt = (B + 31) / 32, nbu = (H + cnhip::kLstmUnits - 1) / cnhip::kLstmUnits;
-  CNHIP_REQUIRE(nbt * nbu < ((int64_t)1 << 31), "%s: too many tiles", who);
-  // FAST: full tiles, whole k-tiles, 16-byte aligned rows of Y and W_hh
-  const bool fast = B % 32 == 0 && H % cnhip::LstmCfg::KT == 0 && H % cnhip::kLstmUnits == 0 &&
-                    BS % 4 == 0 && cnhip::aligned16(Y) && cnhip::aligned16(W_hh);
-  for (int64_t t = 1; t < S; ++t) {
-    if (fast)
-      hipLaunchKernelGGL(cnhip::lstm_step_fwd_kernel<true>, dim3((unsigned)(nbt * nbu)),
-                         dim3(cnhip::LstmCfg::NT), 0, st, gates, b, c, tanh_c, Y, W_hh, B, S, H, t);
-    else
-      hipLaunchKernelGGL(cnhip::lstm_step_fwd_kernel<false>, dim3((unsigned)(nbt * nbu)),
-                         dim3(cnhip::LstmCfg::NT), 0, st, gates, b, c, tanh_c, Y, W_hh, B, S, H, t);
-    CNHIP_TRY(cnhip::check_launch(who));
-  }
-  return CNHIP_OK;
+  return cnhip::lstm_fwd_steps<cnhip::LstmFwdCfg>(gates, b, c, tanh_c, Y, W_hh, B, S, H, st, who);
 }
 
 int cnhip_lstm_backward(const float* X, const float* W_ih, const float* W_hh, const float* Y,
@@ -378,21 +488,17 @@ int cnhip_lstm_backward(const float* X, const float* W_ih, const float* W_hh, co
                 "%s: NULL pointer", who);
   hipStream_t st = as_stream(stream);
   const int64_t G = 4 * H, BS = B * S;
-  constexpr int kMaxSplits = 16;
   cnhip::Workspace ws(st);
-  CNHIP_TRY(ws.alloc((size_t)(BS * G + (kMaxSplits + 1) * B * H) * sizeof(float), who));
+  CNHIP_TRY(ws.alloc((size_t)(BS * G + B * H) * sizeof(float), who));
   float* dG = static_cast<float*>(ws.p);
   float* dc = dG + BS * G;
-  float* dh = dc + B * H;  // kMaxSplits partials of dG_t W_hh^T
-  int ns = 0;
-  for (int64_t t = S - 1; t >= 0; --t) {
-    hipLaunchKernelGGL(cnhip::lstm_cell_bwd_kernel, dim3(cnhip::cell_grid(B, H)), dim3(256), 0, st,
-                       gates, c, tanh_c, dY, dh, ns, dc, dG, B, S, H, t, t == S - 1 ? 1 : 0);
-    CNHIP_TRY(cnhip::check_launch(who));
-    if (t > 0)  // dh_next = dG_t W_hh^T (lstm.cpp:244), summed by the next cell kernel
-      CNHIP_TRY(cnhip::gemm_f32_partials(0, 1, B, H, G, dG + B * t, BS, W_hh, H, dh, kMaxSplits, &ns,
-                                         st, who));
-  }
+  // t = S-1: dh = dY only; then per step one fused launch of
+  // dh_t = dY_t + dG_{t+1} W_hh^T (lstm.cpp:244) and the cell backward
+  hipLaunchKernelGGL(cnhip::lstm_cell_bwd_kernel, dim3(cnhip::cell_grid(B, H)), dim3(256), 0, st,
+                     gates, c, tanh_c, dY, nullptr, 0, dc, dG, B, S, H, S - 1, 1);
+  CNHIP_TRY(cnhip::check_launch(who));
+  CNHIP_TRY(cnhip::lstm_bwd_steps<cnhip::LstmBwdCfgDefault>(gates, c, tanh_c, dY, W_hh, dc, dG, B, S,
+                                                            H, st, who));
   CNHIP_TRY(cnhip::gemm_f32(1, 0, I, G, BS, 1.f, X, BS, dG, BS, 0.f, gW_ih, I, nullptr, 0, st, who));
   CNHIP_TRY(cnhip::gemm_f32(1, 0, H, G, B * (S - 1), 1.f, Y, BS, dG + B, BS, 0.f, gW_hh, H, nullptr,
                             0, st, who));
