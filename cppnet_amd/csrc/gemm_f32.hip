@@ -522,30 +522,6 @@ int gemm_f32_act(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, cons
                        epilogue, aux_in, aux_out, ld_aux, st, who);
 }
 
-// op(A) op(B) as split-K partial products P[s][m + M*n], s < *splits_out
-// (<= max_splits), written into the caller's workspace (max_splits*M*N
-// floats) with no reduction: a consumer kernel sums them in split order
-// (the recurrent cells, which fuse that sum into their gate arithmetic).
-int gemm_f32_partials(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K,
-                      const float* A, int64_t lda, const float* B, int64_t ldb, float* partial,
-                      int max_splits, int* splits_out, hipStream_t st, const char* who) {
-  CNHIP_REQUIRE(M > 0 && N > 0 && K > 0 && max_splits >= 1 && partial && A && B && splits_out,
-                "%s: bad split-K partial GEMM arguments", who);
-  CNHIP_REQUIRE(lda >= (trans_a ? K : M) && ldb >= (trans_b ? N : K), "%s: ld too small", who);
-  const Plan plan = plan_gemm(trans_a, trans_b, M, N, K, 1, max_splits);
-  GemmArgs g{};
-  g.M = M; g.N = N; g.K = K;
-  g.A = A; g.lda = lda; g.B = B; g.ldb = ldb;
-  g.C = partial; g.ldc = M;
-  g.alpha = 1.f; g.beta = 0.f;
-  g.vec_ok = (lda % 4 == 0) && (ldb % 4 == 0) && aligned16(A) && aligned16(B);
-  g.c_vec_ok = 0;
-  g.k_per_split = plan.kps;
-  g.splits = plan.splits;
-  g.partial = partial;
-  *splits_out = plan.splits;
-  return launch_plan(plan.shape, trans_a, trans_b, g, 1, st, who);
-}
 
 }  // namespace cnhip
 

@@ -33,53 +33,31 @@ int gemm_f32(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float al
              int64_t ldc, const float* bias, int epilogue, hipStream_t st, const char* who);
 int column_sum(const float* in, float* out, int64_t rows, int64_t cols, int accumulate,
                hipStream_t st, const char* who);
-int gemm_f32_partials(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K,
-                      const float* A, int64_t lda, const float* B, int64_t ldb, float* partial,
-                      int max_splits, int* splits_out, hipStream_t st, const char* who);
 
 namespace {
 
 __device__ __forceinline__ float sigm(float x) { return 1.0f / (1.0f + expf(-x)); }
 
-// Sum of nsplit split-K partials p[z*stride + i], z ascending (0 when nsplit
-// is 0): the recurrent GEMM's output, reduced inside the cell kernel that
-// consumes it instead of by a separate pass.
-__device__ __forceinline__ float partial_sum(const float* __restrict__ p, int nsplit,
-                                             int64_t stride, int64_t i) {
-  float s = 0.0f;
-#pragma unroll 4
-  for (int z = 0; z < nsplit; ++z) s += p[z * stride + i];
-  return s;
-}
-
 // ---------------------------------------------------------------- LSTM cell
-// gates rows of step t hold x W_ih; the recurrent part h_{t-1} W_hh arrives as
-// nsplit split-K partials hw[z][n + B*j] (j < 4H).  The pre-activations
-// (x W_ih + h W_hh) are overwritten with the activations i, f, g, o
-// (lstm.cpp:115-134).
-__global__ void __launch_bounds__(256) lstm_cell_fwd_kernel(float* __restrict__ gates,
-                                                            const float* __restrict__ bias,
-                                                            float* __restrict__ c,
-                                                            float* __restrict__ tanh_c,
-                                                            float* __restrict__ Y,
-                                                            const float* __restrict__ hw,
-                                                            int nsplit, int64_t B, int64_t S,
-                                                            int64_t H, int64_t t) {
-  const int64_t BS = B * S, BG = B * 4 * H;
+// Step t = 0 (h_0 = c_0 = 0, so no recurrent term): the rows of step 0 of
+// gates hold x W_ih and are overwritten with the activations i, f, g, o
+// (lstm.cpp:115-134); later steps run lstm_step_fwd_kernel.
+__global__ void __launch_bounds__(256) lstm_cell_fwd0_kernel(float* __restrict__ gates,
+                                                             const float* __restrict__ bias,
+                                                             float* __restrict__ c,
+                                                             float* __restrict__ tanh_c,
+                                                             float* __restrict__ Y, int64_t B,
+                                                             int64_t S, int64_t H) {
+  const int64_t BS = B * S;
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= B * H) return;
-  const int64_t n = e % B, d = e / B, row = n + B * t;
+  const int64_t n = e % B, d = e / B, row = n;
   float* g = gates + row;
-  auto pre = [&](int64_t j) {
-    const float x = g[BS * j];
-    return nsplit ? partial_sum(hw, nsplit, BG, n + B * j) + x : x;
-  };
-  const float ig = sigm(pre(d) + bias[d]);
-  const float fg = sigm(pre(d + H) + bias[d + H]);
-  const float gg = tanhf(pre(d + 2 * H) + bias[d + 2 * H]);
-  const float og = sigm(pre(d + 3 * H) + bias[d + 3 * H]);
-  const float cprev = t > 0 ? c[row - B + BS * d] : 0.0f;
-  const float ct = fg * cprev + ig * gg;
+  const float ig = sigm(g[BS * d] + bias[d]);
+  const float fg = sigm(g[BS * (d + H)] + bias[d + H]);
+  const float gg = tanhf(g[BS * (d + 2 * H)] + bias[d + 2 * H]);
+  const float og = sigm(g[BS * (d + 3 * H)] + bias[d + 3 * H]);
+  const float ct = fg * 0.0f + ig * gg;
   const float tc = tanhf(ct);
   g[BS * d] = ig;
   g[BS * (d + H)] = fg;
@@ -164,7 +142,7 @@ __global__ void __launch_bounds__(LstmCfg::NT) lstm_step_fwd_kernel(
     for (int e = 0; e < 4; ++e) tile[(ml + e) + 33 * nl] = v[e];
   });
   __syncthreads();
-  // thread -> (sample, unit); the cell of lstm_cell_fwd_kernel with the
+  // thread -> (sample, unit): the cell of lstm_cell_fwd0_kernel with the
   // recurrent term h W_hh taken from the tile
   static_assert(LstmCfg::NT >= 32 * kLstmUnits, "one thread per (sample, unit)");
   const int bl = threadIdx.x % 32, u = threadIdx.x / 32;
@@ -190,22 +168,22 @@ __global__ void __launch_bounds__(LstmCfg::NT) lstm_step_fwd_kernel(
   Y[row + BS * d] = og * tc;
 }
 
-// lstm.cpp:184-219, 247-249.  dh_in: the nsplit split-K partials of
-// dG_{t+1} W_hh^T, [z][B, H]; dc: [B, H] (dense, ld B); both ignored when first.
-__global__ void __launch_bounds__(256) lstm_cell_bwd_kernel(
+// lstm.cpp:184-219, 247-249, the last step t = S-1: dh = dY (no later step)
+// and dc starts from 0; dc_buf [B, H] (ld B) receives dc * f for step t-1.
+// Earlier steps run lstm_step_bwd_kernel.
+__global__ void __launch_bounds__(256) lstm_cell_bwd_last_kernel(
     const float* __restrict__ gates, const float* __restrict__ c, const float* __restrict__ tanh_c,
-    const float* __restrict__ dY, const float* __restrict__ dh_in, int nsplit,
-    float* __restrict__ dc_buf, float* __restrict__ dG, int64_t B, int64_t S, int64_t H, int64_t t,
-    int first) {
-  const int64_t BS = B * S;
+    const float* __restrict__ dY, float* __restrict__ dc_buf, float* __restrict__ dG, int64_t B,
+    int64_t S, int64_t H) {
+  const int64_t BS = B * S, t = S - 1;
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= B * H) return;
   const int64_t n = e % B, d = e / B, row = n + B * t;
   const float ig = gates[row + BS * d], fg = gates[row + BS * (d + H)];
   const float gg = gates[row + BS * (d + 2 * H)], og = gates[row + BS * (d + 3 * H)];
   const float tc = tanh_c[row + BS * d];
-  const float dh = dY[row + BS * d] + (first ? 0.0f : partial_sum(dh_in, nsplit, B * H, e));
-  const float dc = dh * og * (1.0f - tc * tc) + (first ? 0.0f : dc_buf[e]);
+  const float dh = dY[row + BS * d];
+  const float dc = dh * og * (1.0f - tc * tc) + 0.0f;
   const float cprev = t > 0 ? c[row - B + BS * d] : 0.0f;
   dG[row + BS * d] = dc * gg * ig * (1.0f - ig);
   dG[row + BS * (d + H)] = dc * cprev * fg * (1.0f - fg);
@@ -216,7 +194,7 @@ __global__ void __launch_bounds__(256) lstm_cell_bwd_kernel(
 
 // One backward timestep t <= S-2 in one launch: dh_t = dY_t + dG_{t+1} W_hh^T
 // for a tile of 16 samples x 16 hidden units (K = 4H split over the wave
-// groups of the block, added in a fixed order), then lstm_cell_bwd_kernel's
+// groups of the block, added in a fixed order), then lstm_cell_bwd_last_kernel's
 // arithmetic for those 256 (sample, unit) pairs in the epilogue.  16 x 16
 // tiles give 256 blocks at B = 128, H = 512.
 using LstmBwdCfgDefault = kp::Cfg16<1, 1, 1, 1, 32, 8>;  // fastest of a measured sweep
@@ -472,8 +450,8 @@ int cnhip_lstm_forward(const float* X, const float* W_ih, const float* W_hh, con
   const int64_t G = 4 * H, BS = B * S;
   CNHIP_TRY(cnhip::gemm_f32(0, 0, BS, G, I, 1.f, X, BS, W_ih, I, 0.f, gates, BS, nullptr, 0, st, who));
   // t = 0: h_0 = 0, no recurrent term; then one fused GEMM + cell launch per step
-  hipLaunchKernelGGL(cnhip::lstm_cell_fwd_kernel, dim3(cnhip::cell_grid(B, H)), dim3(256), 0, st,
-                     gates, b, c, tanh_c, Y, nullptr, 0, B, S, H, (int64_t)0);
+  hipLaunchKernelGGL(cnhip::lstm_cell_fwd0_kernel, dim3(cnhip::cell_grid(B, H)), dim3(256), 0, st,
+                     gates, b, c, tanh_c, Y, B, S, H);
   CNHIP_TRY(cnhip::check_launch(who));
   return cnhip::lstm_fwd_steps<cnhip::LstmFwdCfg>(gates, b, c, tanh_c, Y, W_hh, B, S, H, st, who);
 }
@@ -494,8 +472,8 @@ int cnhip_lstm_backward(const float* X, const float* W_ih, const float* W_hh, co
   float* dc = dG + BS * G;
   // t = S-1: dh = dY only; then per step one fused launch of
   // dh_t = dY_t + dG_{t+1} W_hh^T (lstm.cpp:244) and the cell backward
-  hipLaunchKernelGGL(cnhip::lstm_cell_bwd_kernel, dim3(cnhip::cell_grid(B, H)), dim3(256), 0, st,
-                     gates, c, tanh_c, dY, nullptr, 0, dc, dG, B, S, H, S - 1, 1);
+  hipLaunchKernelGGL(cnhip::lstm_cell_bwd_last_kernel, dim3(cnhip::cell_grid(B, H)), dim3(256), 0,
+                     st, gates, c, tanh_c, dY, dc, dG, B, S, H);
   CNHIP_TRY(cnhip::check_launch(who));
   CNHIP_TRY(cnhip::lstm_bwd_steps<cnhip::LstmBwdCfgDefault>(gates, c, tanh_c, dY, W_hh, dc, dG, B, S,
                                                             H, st, who));
