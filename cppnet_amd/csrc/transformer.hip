@@ -304,6 +304,62 @@ __global__ void __launch_bounds__(BNT) bn_fwd_kernel(const float* __restrict__ x
   }
 }
 
+// bn_fwd_kernel for N <= BNT * PER: the column is read once into registers
+// (thread t holds rows t, t + BNT, ..); same sums in the same order as the
+// looping kernel, so the results are identical.
+template <int PER>
+__global__ void __launch_bounds__(BNT) bn_fwd_reg_kernel(const float* __restrict__ x,
+                                                         float* __restrict__ y,
+                                                         float* __restrict__ xhat,
+                                                         const float* __restrict__ gamma,
+                                                         const float* __restrict__ beta,
+                                                         float* __restrict__ rmean,
+                                                         float* __restrict__ rvar,
+                                                         float* __restrict__ bmean,
+                                                         float* __restrict__ bvar, int64_t N,
+                                                         float momentum, float eps) {
+  __shared__ float sm[BNT / 64];
+  const int64_t f = blockIdx.x;
+  const float* xc = x + N * f;
+  const float inv_batch = 1.0f / (float)N;
+  float v[PER];
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int64_t n = threadIdx.x + (int64_t)BNT * i;
+    v[i] = n < N ? xc[n] : 0.f;
+    if (n < N) s += v[i];
+  }
+  const float mean = bn_block_sum(s, sm) * inv_batch;
+  float s2 = 0.f;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int64_t n = threadIdx.x + (int64_t)BNT * i;
+    if (n < N) {
+      const float diff = v[i] - mean;
+      s2 += diff * diff;
+    }
+  }
+  const float var = bn_block_sum(s2, sm) * inv_batch;
+  const float den = sqrtf(var + eps);
+  const float g = gamma[f], b = beta[f];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int64_t n = threadIdx.x + (int64_t)BNT * i;
+    if (n < N) {
+      const float xh = (v[i] - mean) / den;
+      xhat[n + N * f] = xh;
+      y[n + N * f] = g * xh + b;
+    }
+  }
+  if (threadIdx.x == 0) {
+    bmean[f] = mean;
+    bvar[f] = var;
+    rmean[f] = (1.0f - momentum) * rmean[f] + momentum * mean;
+    rvar[f] = (1.0f - momentum) * rvar[f] + momentum * var;
+  }
+}
+
 // eval mode (batch_norm.cpp:320-327): running statistics
 __global__ void __launch_bounds__(256) bn_eval_kernel(const float* __restrict__ x,
                                                       float* __restrict__ y,
@@ -363,6 +419,80 @@ __global__ void __launch_bounds__(BNT) bn_bwd_kernel(const float* __restrict__ d
     const float dxh = dyc[n] * g;
     const float xmu = xc[n] - mean;
     dX[n + N * f] = dxh * inv_std + dvar * 2.0f * xmu * inv_batch + dmean * inv_batch;
+  }
+}
+
+// bn_bwd_kernel for N <= BNT * PER: dY, x and xhat read once into registers,
+// the four column sums reduced together; same arithmetic and order.
+template <int PER>
+__global__ void __launch_bounds__(BNT) bn_bwd_reg_kernel(const float* __restrict__ dY,
+                                                         const float* __restrict__ x,
+                                                         const float* __restrict__ xhat,
+                                                         const float* __restrict__ gamma,
+                                                         const float* __restrict__ bmean,
+                                                         const float* __restrict__ bvar,
+                                                         float* __restrict__ ggamma,
+                                                         float* __restrict__ gbeta,
+                                                         float* __restrict__ dX, int64_t N,
+                                                         float eps) {
+  __shared__ float sm[4][BNT / 64];
+  const int64_t f = blockIdx.x;
+  const float* dyc = dY + N * f;
+  const float* xc = x + N * f;
+  const float* xhc = xhat + N * f;
+  const float g = gamma[f], mean = bmean[f];
+  const float inv_std = 1.0f / sqrtf(bvar[f] + eps);
+  const float inv_batch = 1.0f / (float)N;
+  float dy[PER], xm[PER];
+  float sgg = 0.f, sgb = 0.f, sdv = 0.f, sdm = 0.f;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int64_t n = threadIdx.x + (int64_t)BNT * i;
+    dy[i] = 0.f;
+    xm[i] = 0.f;
+    if (n < N) {
+      dy[i] = dyc[n];
+      sgg += dy[i] * xhc[n];
+      sgb += dy[i];
+      const float dxh = dy[i] * g;
+      xm[i] = xc[n] - mean;
+      sdv += dxh * xm[i] * (-0.5f) * inv_std * inv_std * inv_std;
+      sdm += dxh * (-inv_std);
+    }
+  }
+  // the four block sums of bn_block_sum, in one exchange
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    sgg += __shfl_xor(sgg, off, 64);
+    sgb += __shfl_xor(sgb, off, 64);
+    sdv += __shfl_xor(sdv, off, 64);
+    sdm += __shfl_xor(sdm, off, 64);
+  }
+  if (lane == 0) {
+    sm[0][w] = sgg;
+    sm[1][w] = sgb;
+    sm[2][w] = sdv;
+    sm[3][w] = sdm;
+  }
+  __syncthreads();
+  float tgg = 0.f, tgb = 0.f, dvar = 0.f, dmean = 0.f;
+#pragma unroll
+  for (int i = 0; i < BNT / 64; ++i) {
+    tgg += sm[0][i];
+    tgb += sm[1][i];
+    dvar += sm[2][i];
+    dmean += sm[3][i];
+  }
+  if (threadIdx.x == 0) {
+    ggamma[f] = tgg;
+    gbeta[f] = tgb;
+  }
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int64_t n = threadIdx.x + (int64_t)BNT * i;
+    if (n < N)
+      dX[n + N * f] = dy[i] * g * inv_std + dvar * 2.0f * xm[i] * inv_batch + dmean * inv_batch;
   }
 }
 
@@ -640,9 +770,14 @@ int cnhip_batchnorm_forward(const float* x, float* y, float* xhat, const float* 
   CNHIP_REQUIRE(N > 0 && F > 0, "%s: bad shape", who);
   CNHIP_REQUIRE(x && y && xhat && gamma && beta && running_mean && running_var && batch_mean && batch_var,
                 "%s: NULL pointer", who);
-  hipLaunchKernelGGL(cnhip::bn_fwd_kernel, dim3((unsigned)F), dim3(cnhip::BNT), 0, as_stream(stream), x,
-                     y, xhat, gamma, beta, running_mean, running_var, batch_mean, batch_var, N,
-                     momentum, eps);
+  if (N <= (int64_t)cnhip::BNT * 32)  // whole column in registers
+    hipLaunchKernelGGL(cnhip::bn_fwd_reg_kernel<32>, dim3((unsigned)F), dim3(cnhip::BNT), 0,
+                       as_stream(stream), x, y, xhat, gamma, beta, running_mean, running_var,
+                       batch_mean, batch_var, N, momentum, eps);
+  else
+    hipLaunchKernelGGL(cnhip::bn_fwd_kernel, dim3((unsigned)F), dim3(cnhip::BNT), 0,
+                       as_stream(stream), x, y, xhat, gamma, beta, running_mean, running_var,
+                       batch_mean, batch_var, N, momentum, eps);
   return cnhip::check_launch(who);
 }
 
@@ -666,8 +801,14 @@ int cnhip_batchnorm_backward(const float* dY, const float* x, const float* xhat,
   CNHIP_REQUIRE(N > 0 && F > 0, "%s: bad shape", who);
   CNHIP_REQUIRE(dY && x && xhat && gamma && batch_mean && batch_var && grad_gamma && grad_beta && dX,
                 "%s: NULL pointer", who);
-  hipLaunchKernelGGL(cnhip::bn_bwd_kernel, dim3((unsigned)F), dim3(cnhip::BNT), 0, as_stream(stream),
-                     dY, x, xhat, gamma, batch_mean, batch_var, grad_gamma, grad_beta, dX, N, eps);
+  if (N <= (int64_t)cnhip::BNT * 32)
+    hipLaunchKernelGGL(cnhip::bn_bwd_reg_kernel<32>, dim3((unsigned)F), dim3(cnhip::BNT), 0,
+                       as_stream(stream), dY, x, xhat, gamma, batch_mean, batch_var, grad_gamma,
+                       grad_beta, dX, N, eps);
+  else
+    hipLaunchKernelGGL(cnhip::bn_bwd_kernel, dim3((unsigned)F), dim3(cnhip::BNT), 0,
+                       as_stream(stream), dY, x, xhat, gamma, batch_mean, batch_var, grad_gamma,
+                       grad_beta, dX, N, eps);
   return cnhip::check_launch(who);
 }
 

@@ -186,7 +186,7 @@ def test_embedding_out_of_range_ids_counted(gpu):
 
 
 # ---------------------------------------------------------------- BatchNorm
-@pytest.mark.parametrize("N,F", [(64, 6), (1000, 3), (8192, 512)])
+@pytest.mark.parametrize("N,F", [(64, 6), (1000, 3), (8192, 512), (9000, 5)])
 def test_batchnorm_vs_oracle(gpu, oracle, N, F):
     print(f"[batchnorm] N={N} F={F}", flush=True)
     rng = np.random.default_rng(N + F)
