@@ -19,7 +19,12 @@ moments are resident in HBM before timing starts.  Prints ONE JSON line:
                    semantics, oracle/) on a bounded sample of the same workload
 
 Usage: python bench.py [--gpus 1] [--config 2] [--steps K] [--warmup W]
-                       [--no-cpu-baseline] [--cpu-seconds S]
+                       [--no-cpu-baseline] [--cpu-seconds S] [--graph]
+
+--graph replays the step's zero_grad + forward + loss + backward as one
+captured HIP graph (cnt_capture_step) and then runs the fused Adam update
+eagerly; the default launches every kernel from the host.  Both compute the
+same step, bit for bit.
 """
 from __future__ import annotations
 
@@ -174,6 +179,10 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--graph", action="store_true",
+                    help="replay the step's zero_grad + forward + loss + backward as one captured "
+                         "HIP graph (cnt_capture_step), Adam eagerly after it; same results bit for "
+                         "bit, measured no faster on MI355X (the cost per kernel is GPU-side)")
     ap.add_argument("--traffic-calibration", action="store_true",
                     help="only run the known-traffic reference kernel (cnhip_add over 64 Mi floats, "
                          "5 times: 512 MiB read + 256 MiB written per launch) that scales the PMC "
@@ -207,6 +216,12 @@ def main() -> int:
 
     for _ in range(args.warmup):
         sess.step(read_loss=False)
+    if args.graph:
+        # zero_grad + forward + loss + backward replayed as one HIP graph; the
+        # Adam update still runs every step, eagerly, after the replay
+        sess.capture()
+        for _ in range(2):
+            sess.step(read_loss=False)
     sess.synchronize()
 
     ev0, ev1 = C.c_void_p(), C.c_void_p()
@@ -228,7 +243,10 @@ def main() -> int:
         return 1
     log(f"bench.py: {step_ms:.4f} ms/step, loss {loss:.6f}")
 
-    # Dominant kernel class: per-launch timing over a few extra steps.
+    # Dominant kernel class: per-launch timing over a few extra eager steps
+    # (a graph replay records no per-launch events).
+    if sess.has_graph:
+        sess.release_graph()
     prof_steps = 3
     _capi.check(lib.cnhip_gemm_timing_enable(1))
     for _ in range(prof_steps):
@@ -259,6 +277,8 @@ def main() -> int:
         "config": {"workload": desc, "global_batch": B, "parallelism": "single GPU",
                    "params": int(sum(p.size for p in params)),
                    "step_tflops": round(flops_fn(cfg) / (step_ms * 1e-3) / 1e12, 2),
+                   "execution": ("captured fwd+bwd HIP graph replay + eager fused Adam, every step"
+                                 if args.graph else "eager launches on one stream"),
                    "wall_s_timed_region": round(wall, 3)},
         "roofline": {"bound": "mfma", "kernel": kernels,
                      "achieved": round(achieved, 2), "peak": PEAK_FP32_MFMA_TFLOPS,

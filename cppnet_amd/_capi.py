@@ -38,6 +38,10 @@ SIGNATURES: dict[str, tuple] = {
     "cnhip_event_destroy": (i32, [vp]),
     "cnhip_event_record": (i32, [vp, vp]),
     "cnhip_event_elapsed_ms": (i32, [C.POINTER(f32), vp, vp]),
+    "cnhip_graph_begin_capture": (i32, [vp]),
+    "cnhip_graph_end_capture": (i32, [vp, i32, C.POINTER(vp)]),
+    "cnhip_graph_launch": (i32, [vp, vp]),
+    "cnhip_graph_destroy": (i32, [vp]),
     "cnhip_gemm_f32": (i32, [i32, i32, i64, i64, i64, f32, vp, i64, vp, i64, f32, vp, i64, vp,
                              i32, vp]),
     "cnhip_gemm_f32_batched": (i32, [i32, i32, i64, i64, i64, f32, vp, i64, i64, vp, i64, i64,

@@ -76,6 +76,12 @@ struct TimingRec {
   double flops;
 };
 TimingRec* timing_slot(double flops);
+bool timing_on();
+
+// Fills `bytes` bytes at dst with the byte `value` by a kernel on `stream`
+// (not hipMemsetAsync: a memset node recorded into a captured graph has
+// given wrong results on replays after the first on this platform).
+int fill_bytes(void* dst, int value, size_t bytes, hipStream_t stream, const char* where);
 
 }  // namespace cnhip
 

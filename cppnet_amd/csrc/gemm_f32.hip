@@ -260,6 +260,8 @@ thread_local Timing g_timing;
 
 }  // namespace
 
+bool timing_on() { return g_timing.on; }
+
 TimingRec* timing_slot(double flops) {
   Timing& t = g_timing;
   if (!t.on) return nullptr;

@@ -29,10 +29,18 @@ namespace CppNet
             // Idle blocks are keyed by the stream they were released on: a
             // block may still be read by in-flight work of that stream, so it
             // is only handed out again to work enqueued on the same stream.
+            struct Pool
+            {
+                cnhip_stream_t stream = nullptr;  // the captured stream
+                std::multimap<size_t, void*> idle;
+            };
             struct Cache
             {
                 std::mutex mu;
                 std::map<cnhip_stream_t, std::multimap<size_t, void*>> idle;
+                std::map<uint64_t, Pool> pools;  // live graph pools
+                uint64_t open = 0;               // pool of the running capture, 0 if none
+                uint64_t next_pool = 1;
                 size_t device_bytes = 0;
                 size_t cached_bytes = 0;
                 size_t mallocs = 0;
@@ -49,6 +57,19 @@ namespace CppNet
                 if (bytes <= (size_t(1) << 20)) return (bytes + small - 1) / small * small;
                 return (bytes + large - 1) / large * large;
             }
+
+            // Takes an idle block of at least `block` bytes (at most 25% more)
+            // from `pool`; returns nullptr and leaves `block` alone if none fits.
+            void* take(std::multimap<size_t, void*>& pool, size_t& block)
+            {
+                auto it = pool.lower_bound(block);
+                const size_t limit = block + (block >> 2);
+                if (it == pool.end() || it->first > limit) return nullptr;
+                void* p = it->second;
+                block = it->first;
+                pool.erase(it);
+                return p;
+            }
         } // namespace
 
         cnhip_stream_t stream() { return g_stream; }
@@ -62,15 +83,16 @@ namespace CppNet
             Cache& c = cache();
             {
                 std::lock_guard<std::mutex> lk(c.mu);
-                auto& pool = c.idle[g_stream];
-                auto it = pool.lower_bound(block_);
-                const size_t limit = block_ + (block_ >> 2);
-                if (it != pool.end() && it->first <= limit)
+                pool_ = c.open;
+                if (pool_)
                 {
-                    ptr_ = it->second;
-                    block_ = it->first;
+                    ptr_ = take(c.pools[pool_].idle, block_);
+                    if (ptr_) return;
+                }
+                ptr_ = take(c.idle[g_stream], block_);
+                if (ptr_)
+                {
                     c.cached_bytes -= block_;
-                    pool.erase(it);
                     return;
                 }
             }
@@ -91,8 +113,53 @@ namespace CppNet
             if (!ptr_) return;
             Cache& c = cache();
             std::lock_guard<std::mutex> lk(c.mu);
+            // released during a capture: captured kernels may refer to it
+            const uint64_t owner = c.open ? c.open : pool_;
+            if (owner)
+            {
+                auto it = c.pools.find(owner);
+                if (it != c.pools.end())
+                {
+                    it->second.idle.emplace(block_, ptr_);
+                    return;
+                }
+            }
             c.idle[g_stream].emplace(block_, ptr_);
             c.cached_bytes += block_;
+        }
+
+        uint64_t open_pool()
+        {
+            Cache& c = cache();
+            std::lock_guard<std::mutex> lk(c.mu);
+            if (c.open) throw std::logic_error("Device::open_pool: a graph pool is already open");
+            const uint64_t id = c.next_pool++;
+            c.pools[id].stream = g_stream;
+            c.open = id;
+            return id;
+        }
+
+        void close_pool()
+        {
+            Cache& c = cache();
+            std::lock_guard<std::mutex> lk(c.mu);
+            c.open = 0;
+        }
+
+        void release_pool(uint64_t id)
+        {
+            Cache& c = cache();
+            std::lock_guard<std::mutex> lk(c.mu);
+            auto it = c.pools.find(id);
+            if (it == c.pools.end()) return;
+            if (c.open == id) c.open = 0;
+            auto& general = c.idle[it->second.stream];
+            for (auto& kv : it->second.idle)
+            {
+                general.emplace(kv.first, kv.second);
+                c.cached_bytes += kv.first;
+            }
+            c.pools.erase(it);
         }
 
         std::shared_ptr<Buffer> allocate(size_t bytes) { return std::make_shared<Buffer>(bytes); }

@@ -135,6 +135,34 @@ struct cnt_session
     DeviceTensor X, Y;
     Losses::DeviceScalar last_loss;
 
+    // Captured forward + backward (cnt_capture_step): replayed by cnt_step,
+    // followed by the eager Adam update.  The graph writes its loss into
+    // graph_loss; its memory is the allocator pool graph_pool.
+    bool warm = false;  // one eager forward + backward has run at the batch shapes
+    cnhip_graph_t graph = nullptr;
+    uint64_t graph_pool = 0;
+    Losses::DeviceScalar graph_loss;
+    // each layer's grads_pending_zero() as the captured backward leaves it
+    std::vector<std::pair<Layers::Layer*, bool>> graph_flags;
+
+    std::vector<Layers::Layer*> all_layers()
+    {
+        std::vector<Layers::Layer*> out;
+        for (std::size_t i = 0; i < model.num_layers(); ++i) out.push_back(model.get_layer(i).get());
+        if (encoder)
+        {
+            out.push_back(encoder->emb.get());
+            for (auto& b : encoder->blocks)
+                for (Layers::Layer* l : {static_cast<Layers::Layer*>(b.mha.get()),
+                                         static_cast<Layers::Layer*>(b.bn.get()),
+                                         static_cast<Layers::Layer*>(b.ff1.get()),
+                                         static_cast<Layers::Layer*>(b.ff2.get())})
+                    out.push_back(l);
+            out.push_back(encoder->fc.get());
+        }
+        return out;
+    }
+
     // parameter index -> accessors of the value and of the gradient, called
     // through the layer so lazily-zeroed gradients are materialised first
     struct Param
@@ -264,6 +292,21 @@ namespace
         tmp.copy_from_host(host);
         Device::check(cnhip_transpose(tmp.data(), t.data(), p.t_rows, p.t_cols, Device::stream()), "param");
         Device::synchronize();
+    }
+
+    // Destroys the session's captured graph (synchronising its stream) and
+    // returns the graph's memory pool to the allocator.
+    void release_graph(cnt_session* s)
+    {
+        if (!s->graph) return;
+        cnhip_graph_t g = s->graph;
+        s->graph = nullptr;
+        s->graph_loss = Losses::DeviceScalar();
+        s->graph_flags.clear();
+        const int st = cnhip_graph_destroy(g);
+        Device::release_pool(s->graph_pool);
+        s->graph_pool = 0;
+        Device::check(st, "graph");
     }
 
     std::unique_ptr<cnt_session> new_session(uint64_t seed)
@@ -479,6 +522,7 @@ int cnt_destroy(cnt_session* s)
         cnhip_stream_t st = s->stream;
         {
             StreamScope scope(s);
+            release_graph(s);
             delete s;
         }
         cnhip_stream_destroy(st);
@@ -603,6 +647,16 @@ namespace
         s->model.backward_params(g);
     }
 
+    // Eager forward + backward.  The layers' host-side state (cached
+    // activations, argmax indices) then belongs to this pass, so a captured
+    // graph, whose replays would not update it, is dropped first.
+    void eager_forward_backward(cnt_session* s)
+    {
+        release_graph(s);
+        forward_backward(s);
+        s->warm = true;
+    }
+
     void update(cnt_session* s)
     {
         if (s->encoder)
@@ -617,18 +671,76 @@ int cnt_step(cnt_session* s, float* loss_out)
     return guarded("cnt_step", [&] {
         check_session(s);
         StreamScope scope(s);
-        forward_backward(s);
+        if (s->graph)
+        {
+            Device::check(cnhip_graph_launch(s->graph, s->stream), "cnt_step graph replay");
+            s->last_loss = s->graph_loss;
+            for (auto& f : s->graph_flags) f.first->set_grads_pending_zero(f.second);
+        }
+        else
+            eager_forward_backward(s);
         update(s);
         if (loss_out) *loss_out = s->last_loss.get();
     });
 }
+
+int cnt_capture_step(cnt_session* s)
+{
+    return guarded("cnt_capture_step", [&] {
+        check_session(s);
+        StreamScope scope(s);
+        release_graph(s);
+        if (!s->warm)
+            throw std::logic_error("run one step eagerly before capturing: it sizes the buffers and "
+                                   "workspaces the graph will refer to");
+        Device::check(cnhip_graph_begin_capture(s->stream), "capture");
+        s->graph_pool = Device::open_pool();
+        cnhip_graph_t g = nullptr;
+        try
+        {
+            forward_backward(s);
+        }
+        catch (...)
+        {
+            Device::close_pool();
+            cnhip_graph_end_capture(s->stream, 0, &g);
+            Device::release_pool(s->graph_pool);
+            s->graph_pool = 0;
+            s->warm = false;  // host-side layer state refers to work that never ran
+            throw;
+        }
+        Device::close_pool();
+        const int st = cnhip_graph_end_capture(s->stream, 1, &g);
+        if (st != CNHIP_OK)
+        {
+            Device::release_pool(s->graph_pool);
+            s->graph_pool = 0;
+            s->warm = false;
+            Device::check(st, "capture");
+        }
+        s->graph = g;
+        s->graph_loss = s->last_loss;
+        for (Layers::Layer* l : s->all_layers()) s->graph_flags.emplace_back(l, l->grads_pending_zero());
+    });
+}
+
+int cnt_release_graph(cnt_session* s)
+{
+    return guarded("cnt_release_graph", [&] {
+        check_session(s);
+        StreamScope scope(s);
+        release_graph(s);
+    });
+}
+
+int cnt_has_graph(cnt_session* s) { return s && s->graph ? 1 : 0; }
 
 int cnt_forward_backward(cnt_session* s, float* loss_out)
 {
     return guarded("cnt_forward_backward", [&] {
         check_session(s);
         StreamScope scope(s);
-        forward_backward(s);
+        eager_forward_backward(s);
         if (loss_out) *loss_out = s->last_loss.get();
     });
 }

@@ -46,7 +46,48 @@ struct ScratchEntry {
 };
 std::mutex g_scratch_mu;
 std::vector<ScratchEntry> g_scratch;
+// Streams whose scratch slots a captured graph refers to: their buffers
+// must keep their addresses, so a request that would grow one fails.
+std::vector<std::pair<int, hipStream_t>> g_frozen;
+
+bool frozen(int dev, hipStream_t stream) {
+  for (auto& f : g_frozen)
+    if (f.first == dev && f.second == stream) return true;
+  return false;
+}
+
+__global__ void fill_bytes_kernel(unsigned char* __restrict__ dst, uint32_t word, size_t n16,
+                                  size_t tail) {
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  const size_t t0 = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  uint4* d4 = reinterpret_cast<uint4*>(dst);
+  const uint4 v = make_uint4(word, word, word, word);
+  for (size_t i = t0; i < n16; i += stride) d4[i] = v;
+  if (t0 < tail) dst[n16 * 16 + t0] = (unsigned char)(word & 0xffu);
+}
+
+__global__ void fill_bytes_unaligned_kernel(unsigned char* __restrict__ dst, unsigned char v,
+                                            size_t n) {
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) dst[i] = v;
+}
 }  // namespace
+
+int fill_bytes(void* dst, int value, size_t bytes, hipStream_t stream, const char* where) {
+  if (bytes == 0) return CNHIP_OK;
+  const uint32_t b = (uint32_t)value & 0xffu;
+  unsigned char* d = static_cast<unsigned char*>(dst);
+  if (aligned16(dst)) {
+    const size_t n16 = bytes / 16, tail = bytes % 16;
+    const unsigned grid = elementwise_grid((int64_t)(n16 > tail ? n16 : tail), 256);
+    hipLaunchKernelGGL(fill_bytes_kernel, dim3(grid), dim3(256), 0, stream, d,
+                       b * 0x01010101u, n16, tail);
+  } else {
+    hipLaunchKernelGGL(fill_bytes_unaligned_kernel, dim3(elementwise_grid((int64_t)bytes, 256)),
+                       dim3(256), 0, stream, d, (unsigned char)b, bytes);
+  }
+  return check_launch(where);
+}
 
 int scratch(hipStream_t stream, int slot, size_t bytes, void** ptr, const char* where) {
   int dev = 0;
@@ -60,6 +101,14 @@ int scratch(hipStream_t stream, int slot, size_t bytes, void** ptr, const char* 
     e = &g_scratch.back();
   }
   if (e->cap < bytes) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    CNHIP_TRY(check_hip(hipStreamIsCapturing(stream, &cs), where));
+    if (cs != hipStreamCaptureStatusNone || frozen(dev, stream)) {
+      set_error("%s: scratch slot %d of this stream must grow to %zu bytes (has %zu) while a "
+                "captured graph uses it; run the work once uncaptured before capturing it",
+                where, slot, bytes, e->cap);
+      return CNHIP_EUNSUPPORTED;
+    }
     if (e->p) {
       void* old = e->p;
       e->p = nullptr;
@@ -127,7 +176,7 @@ int cnhip_memcpy_async(void* dst, const void* src, size_t bytes, int kind,
 int cnhip_memset_async(void* dst, int value, size_t bytes, cnhip_stream_t stream) {
   if (bytes == 0) return CNHIP_OK;
   CNHIP_REQUIRE(dst, "cnhip_memset_async: NULL pointer");
-  return check_hip(hipMemsetAsync(dst, value, bytes, as_stream(stream)), "cnhip_memset_async");
+  return cnhip::fill_bytes(dst, value, bytes, as_stream(stream), "cnhip_memset_async");
 }
 
 int cnhip_stream_create(cnhip_stream_t* stream) {
@@ -188,6 +237,83 @@ int cnhip_event_elapsed_ms(float* ms, void* start, void* stop) {
   return check_hip(hipEventElapsedTime(ms, reinterpret_cast<hipEvent_t>(start),
                                        reinterpret_cast<hipEvent_t>(stop)),
                    "cnhip_event_elapsed_ms");
+}
+
+// ---- graphs: capture of a stream's work, replay -------------------------
+namespace {
+struct Graph {
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  int dev = 0;
+  hipStream_t stream = nullptr;  // whose scratch slots the graph uses
+};
+}  // namespace
+
+int cnhip_graph_begin_capture(cnhip_stream_t stream) {
+  const char* who = "cnhip_graph_begin_capture";
+  CNHIP_REQUIRE(stream != nullptr, "%s: capture needs a created stream, not the default stream", who);
+  CNHIP_REQUIRE(!cnhip::timing_on(), "%s: per-launch GEMM timing is enabled; disable it first", who);
+  // Relaxed: allocations of not-yet-cached buffers by the host layer may
+  // call hipMalloc while the capture is open (that is not stream work).
+  return check_hip(hipStreamBeginCapture(as_stream(stream), hipStreamCaptureModeRelaxed), who);
+}
+
+int cnhip_graph_end_capture(cnhip_stream_t stream, int ok, cnhip_graph_t* graph) {
+  const char* who = "cnhip_graph_end_capture";
+  CNHIP_REQUIRE(stream != nullptr, "%s: NULL stream", who);
+  if (graph) *graph = nullptr;
+  hipGraph_t g = nullptr;
+  const hipError_t e = hipStreamEndCapture(as_stream(stream), &g);
+  if (e != hipSuccess || !ok || !graph) {
+    if (g) (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return check_hip(e, who);
+    CNHIP_REQUIRE(graph, "%s: NULL out pointer", who);
+    return CNHIP_OK;  // capture abandoned by the caller
+  }
+  auto* G = new Graph;
+  G->graph = g;
+  G->stream = as_stream(stream);
+  int st = check_hip(hipGetDevice(&G->dev), who);
+  if (st == CNHIP_OK) st = check_hip(hipGraphInstantiate(&G->exec, g, nullptr, nullptr, 0), who);
+  if (st != CNHIP_OK) {
+    (void)hipGraphDestroy(g);
+    delete G;
+    return st;
+  }
+  {
+    std::lock_guard<std::mutex> lock(cnhip::g_scratch_mu);
+    cnhip::g_frozen.emplace_back(G->dev, G->stream);
+  }
+  *graph = G;
+  return CNHIP_OK;
+}
+
+int cnhip_graph_launch(cnhip_graph_t graph, cnhip_stream_t stream) {
+  CNHIP_REQUIRE(graph, "cnhip_graph_launch: NULL graph");
+  auto* G = static_cast<Graph*>(graph);
+  CNHIP_REQUIRE(as_stream(stream) == G->stream,
+                "cnhip_graph_launch: a graph replays on the stream it was captured on (its scratch "
+                "slots are that stream's)");
+  return check_hip(hipGraphLaunch(G->exec, as_stream(stream)), "cnhip_graph_launch");
+}
+
+int cnhip_graph_destroy(cnhip_graph_t graph) {
+  if (!graph) return CNHIP_OK;
+  auto* G = static_cast<Graph*>(graph);
+  int st = check_hip(hipStreamSynchronize(G->stream), "cnhip_graph_destroy");
+  if (G->exec) (void)hipGraphExecDestroy(G->exec);
+  if (G->graph) (void)hipGraphDestroy(G->graph);
+  {
+    std::lock_guard<std::mutex> lock(cnhip::g_scratch_mu);
+    auto& fz = cnhip::g_frozen;
+    for (size_t i = 0; i < fz.size(); ++i)
+      if (fz[i].first == G->dev && fz[i].second == G->stream) {
+        fz.erase(fz.begin() + (long)i);  // one entry per live graph
+        break;
+      }
+  }
+  delete G;
+  return st;
 }
 
 }  // extern "C"

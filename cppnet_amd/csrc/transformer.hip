@@ -745,7 +745,7 @@ int cnhip_embedding_backward(const int32_t* ids, const float* dY, float* gWt, in
   int32_t* offsets = cursor + V;
   int32_t* pos = offsets + (V + 1);
   float* dYt = reinterpret_cast<float*>(reinterpret_cast<char*>(ws.p) + ((ibytes + 15) & ~size_t(15)));
-  CNHIP_TRY(cnhip::check_hip(hipMemsetAsync(counts, 0, (size_t)(2 * V) * sizeof(int32_t), st), who));
+  CNHIP_TRY(cnhip::fill_bytes(counts, 0, (size_t)(2 * V) * sizeof(int32_t), st, who));
   CNHIP_TRY(cnhip::transpose(dY, dYt, BS, D, st, who));
   const unsigned g = cnhip::elementwise_grid(BS, 256);
   hipLaunchKernelGGL(cnhip::emb_count_kernel, dim3(g), dim3(256), 0, st, ids, counts, BS, V);

@@ -64,6 +64,7 @@ namespace CppNet
             void* ptr_ = nullptr;
             size_t bytes_ = 0;   // requested
             size_t block_ = 0;   // cached block size
+            uint64_t pool_ = 0;  // graph pool it belongs to (0: the general cache)
         };
 
         std::shared_ptr<Buffer> allocate(size_t bytes);
@@ -77,6 +78,21 @@ namespace CppNet
         AllocatorStats allocator_stats();
         /// Returns idle cached blocks to HIP (synchronises the device first).
         void empty_cache();
+
+        /**
+         * Graph pools: memory a captured graph refers to.  While a pool is
+         * open (a capture of Device::stream() is running), every block handed
+         * out belongs to the pool, and every block released goes to the
+         * pool's own idle list (the captured kernels may refer to it).  Blocks
+         * of a live pool are never handed to allocations made outside its
+         * capture, so work enqueued between replays cannot be given memory
+         * that a replay writes.  release_pool() (after the graph is destroyed)
+         * moves the pool's idle blocks to the general cache; its blocks still
+         * in use go there when released.
+         */
+        uint64_t open_pool();
+        void close_pool();
+        void release_pool(uint64_t id);
     } // namespace Device
 } // namespace CppNet
 

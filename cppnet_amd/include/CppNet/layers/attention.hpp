@@ -65,7 +65,6 @@ namespace CppNet
             DeviceTensor Wall_, gWall_;  // [D, 4D]: W_q | W_k | W_v | W_o
             DeviceTensor W_[4], gW_[4];
             DeviceTensor q_cache_, k_cache_, v_cache_, cache_;
-            bool grads_zero_ = true;
         };
     } // namespace Layers
 } // namespace CppNet

@@ -69,7 +69,6 @@ namespace CppNet
             std::string device_;
             DeviceTensor gamma_, beta_, ggamma_, gbeta_, rmean_, rvar_, bmean_, bvar_;
             DeviceTensor in_cache_, xhat_;
-            bool grads_zero_ = true;
         };
     } // namespace Layers
 } // namespace CppNet

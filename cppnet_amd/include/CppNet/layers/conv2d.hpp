@@ -73,7 +73,6 @@ namespace CppNet
             bool trainable_ = true;
             std::string device_;
             DeviceTensor W_, b_, gW_, gb_, in_cache_;
-            bool grads_zero_ = true;
         };
     } // namespace Layers
 } // namespace CppNet

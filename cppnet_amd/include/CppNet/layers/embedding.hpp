@@ -66,7 +66,6 @@ namespace CppNet
             bool trainable_ = true;
             std::string device_;
             DeviceTensor Wt_, gWt_, ids_cache_, oob_;
-            bool grads_zero_ = true;
         };
     } // namespace Layers
 } // namespace CppNet

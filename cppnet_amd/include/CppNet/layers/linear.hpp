@@ -97,7 +97,6 @@ namespace CppNet
             // reset_grads() only marks the gradients as zero; the next
             // backward then writes instead of adding (0 + x == x), and any
             // reader before that gets them cleared first.
-            bool grads_zero_ = true;
             void materialize_grads() const;
         };
     } // namespace Layers

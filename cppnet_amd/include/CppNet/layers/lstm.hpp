@@ -63,7 +63,6 @@ namespace CppNet
             const char* name_;
             DeviceTensor W_ih_, W_hh_, b_, gW_ih_, gW_hh_, gb_;
             DeviceTensor in_cache_, out_cache_, gates_cache_;
-            bool grads_zero_ = true;
         };
 
         class LSTM : public RecurrentBase

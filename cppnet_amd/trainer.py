@@ -53,6 +53,9 @@ def load() -> C.CDLL:
         "cnt_update": (i32, [vp]),
         "cnt_synchronize": (i32, [vp]),
         "cnt_stream": (vp, [vp]),
+        "cnt_capture_step": (i32, [vp]),
+        "cnt_release_graph": (i32, [vp]),
+        "cnt_has_graph": (i32, [vp]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(lib, name)
@@ -401,3 +404,16 @@ class Session:
 
     def synchronize(self) -> None:
         _check(load().cnt_synchronize(self.h))
+
+    def capture(self) -> None:
+        """Records zero_grad + forward + loss + backward into a HIP graph that
+        later step() calls replay (Adam runs eagerly after each replay).  Needs
+        one eager step first."""
+        _check(load().cnt_capture_step(self.h))
+
+    def release_graph(self) -> None:
+        _check(load().cnt_release_graph(self.h))
+
+    @property
+    def has_graph(self) -> bool:
+        return bool(load().cnt_has_graph(self.h))

@@ -65,6 +65,29 @@ int cnhip_event_create(void** event);
 int cnhip_event_destroy(void* event);
 int cnhip_event_record(void* event, cnhip_stream_t stream);
 int cnhip_event_elapsed_ms(float* ms, void* start, void* stop); /* syncs stop */
+/* cnhip_memset_async fills with a kernel, so it can be recorded into a graph. */
+
+/* ---- graphs -------------------------------------------------------------
+ * Capture of the work enqueued on one created stream into a HIP graph, and
+ * its replay.  No counterpart in the reference (its "gpu" branches copy
+ * host<->device inside every call and cannot be captured); this replaces
+ * the per-kernel launch cost of a whole training step with one graph launch.
+ *   begin_capture: starts capturing `stream` (relaxed mode; refused while
+ *     per-launch GEMM timing is on).  Nothing enqueued on it runs until the
+ *     graph is launched.
+ *   end_capture: ends the capture; with ok != 0 instantiates the graph into
+ *     *graph, with ok == 0 discards it (*graph = NULL).  While a graph
+ *     exists, the stream's scratch slots are frozen: work that would need a
+ *     larger scratch buffer on that stream fails with CNHIP_EUNSUPPORTED
+ *     instead of moving the buffer the graph refers to.  So run the work
+ *     once uncaptured (at the same shapes) before capturing it.
+ *   launch: replays the graph on the stream it was captured on.
+ *   destroy: synchronises that stream, frees the graph, unfreezes. */
+typedef void* cnhip_graph_t;
+int cnhip_graph_begin_capture(cnhip_stream_t stream);
+int cnhip_graph_end_capture(cnhip_stream_t stream, int ok, cnhip_graph_t* graph);
+int cnhip_graph_launch(cnhip_graph_t graph, cnhip_stream_t stream);
+int cnhip_graph_destroy(cnhip_graph_t graph);
 
 /* ---- GEMM ---------------------------------------------------------------
  * ColMajor  C[M,N] = alpha * op(A)[M,K] * op(B)[K,N] + beta * C  (+ bias[n])

@@ -96,6 +96,20 @@ int cnt_step(cnt_session* s, float* loss_out);
  * gradients inside step() (conv2d.cpp:211-212), so read grads in between. */
 int cnt_forward_backward(cnt_session* s, float* loss_out);
 int cnt_update(cnt_session* s);
+/* Whole-step graph.  cnt_capture_step records the session's zero_grad +
+ * forward + loss + backward into a HIP graph (include/cnhip.h, graphs);
+ * from then on cnt_step replays it with one graph launch and then runs the
+ * Adam update eagerly (its bias corrections 1 - beta^t change every step and
+ * are computed on the host exactly as the eager path does), so a replayed
+ * step computes what an eager step computes, bit for bit.  Needs one eager
+ * step (cnt_step or cnt_forward_backward) at the session's shapes first.
+ * The graph reads the batch buffers in place, so cnt_set_batch* between
+ * replays trains on the new batch.  cnt_forward_backward runs eagerly and
+ * drops the graph (the layers' cached activations then belong to that
+ * pass); so does cnt_release_graph.  No counterpart in the reference. */
+int cnt_capture_step(cnt_session* s);
+int cnt_release_graph(cnt_session* s);
+int cnt_has_graph(cnt_session* s); /* 1 while a captured graph is live */
 int cnt_synchronize(cnt_session* s);
 /* The hipStream_t the session's kernels run on. */
 void* cnt_stream(cnt_session* s);

@@ -96,3 +96,12 @@ def test_ops_refuse_host_tensors():
     x = torch.zeros(4)
     with pytest.raises(TypeError, match="device tensor"):
         ops.relu_forward(x, x)
+
+
+def test_graph_entry_points_validate_without_gpu():
+    lib = _capi.load()
+    st, msg = _status_and_error(lib.cnhip_graph_begin_capture, None)
+    assert st == 1 and "default stream" in msg
+    st, msg = _status_and_error(lib.cnhip_graph_launch, None, None)
+    assert st == 1 and "NULL graph" in msg
+    assert lib.cnhip_graph_destroy(None) == 0

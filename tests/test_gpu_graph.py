@@ -1,0 +1,103 @@
+"""Whole-step graph replay (cnt_capture_step) against eager steps.
+
+A replayed step runs the same kernels, in the same order, on the same data
+as an eager step, and Adam runs eagerly after each replay with the host's
+bias corrections, so the bar is bit-identical: every step's loss and every
+parameter after the run must equal those of an eager session started from
+the same weights and batches.  Between replays the test does the program's
+own eager work (parameter and gradient read-backs with their
+synchronisations, a new batch upload), and checks every replay.
+"""
+import numpy as np
+import pytest
+
+from cppnet_amd import trainer
+
+pytestmark = pytest.mark.gpu
+
+CASES = {
+    "c1_mlp": lambda: (trainer.mlp_config(1, batch=512), trainer.synthetic_mlp),
+    "c2_mlp": lambda: (trainer.mlp_config(2, batch=256), trainer.synthetic_mlp),
+    "c3_cnn": lambda: (trainer.cnn_config(3, batch=32), trainer.synthetic_cnn),
+    "c4_lstm": lambda: (trainer.rnn_config(4, batch=16, seq_len=8), trainer.synthetic_rnn),
+    "gru": lambda: (trainer.rnn_config(4, batch=16, seq_len=8, cell="gru"), trainer.synthetic_rnn),
+    "c5_transformer": lambda: (trainer.transformer_config(5, batch=4, seq_len=16, vocab=64, embed_dim=32,
+                                                          heads=4, blocks=2, ffn=64, classes=4),
+                               trainer.synthetic_transformer),
+}
+
+
+def _bitwise_equal(a, b):
+    a, b = np.atleast_1d(np.asarray(a, np.float32)), np.atleast_1d(np.asarray(b, np.float32))
+    return np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@pytest.mark.parametrize("name", list(CASES))
+def test_graph_replay_matches_eager(gpu, name):
+    cfg, synth = CASES[name]()
+    print(f"[graph] {name}: eager vs captured, 6 steps", flush=True)
+    rng = np.random.default_rng(7)
+    params, X1, Y1 = synth(cfg, rng)
+    _, X2, Y2 = synth(cfg, rng)  # a second batch, uploaded between replays
+    eager, graph = trainer.Session(cfg), trainer.Session(cfg)
+    try:
+        for s in (eager, graph):
+            s.set_params(params)
+            s.set_batch(X1, Y1)
+        # step 0 eager in both (it sizes buffers and workspaces), then capture
+        assert _bitwise_equal(eager.step(), graph.step())
+        graph.capture()
+        assert graph.has_graph
+        for k in range(1, 6):
+            if k == 3:
+                for s in (eager, graph):
+                    s.set_batch(X2, Y2)
+            le, lg = eager.step(), graph.step()
+            assert graph.has_graph, "replay dropped the graph"
+            assert _bitwise_equal(le, lg), f"step {k}: loss {lg!r} (graph) vs {le!r} (eager)"
+            # eager reads with synchronisations between replays
+            for i, (pe, pg) in enumerate(zip(eager.get_params(), graph.get_params())):
+                assert _bitwise_equal(pe, pg), f"step {k}: parameter {i} differs"
+        for i, (ge, gg) in enumerate(zip(eager.get_grads(), graph.get_grads())):
+            assert _bitwise_equal(ge, gg), f"gradient {i} differs after the last replay"
+    finally:
+        eager.close()
+        graph.close()
+
+
+def test_capture_needs_an_eager_step_and_split_calls_drop_the_graph(gpu):
+    cfg = trainer.mlp_config(1, batch=64)
+    params, X, Y = trainer.synthetic_mlp(cfg, np.random.default_rng(3))
+    s = trainer.Session(cfg)
+    ref = trainer.Session(cfg)
+    try:
+        for t in (s, ref):
+            t.set_params(params)
+            t.set_batch(X, Y)
+        with pytest.raises(trainer._capi.CnhipError, match="eagerly before capturing"):
+            s.capture()
+        assert not s.has_graph
+        s.step()
+        ref.step()
+        s.capture()
+        assert s.has_graph
+        s.step()
+        ref.step()
+        # the split calls run eagerly and drop the graph; results stay the same
+        lf = s.forward_backward()
+        assert not s.has_graph
+        assert _bitwise_equal(lf, ref.forward_backward())
+        s.update()
+        ref.update()
+        s.capture()  # re-capture after eager work
+        s.step()
+        ref.step()
+        s.release_graph()
+        assert not s.has_graph
+        s.step()
+        ref.step()
+        for i, (a, b) in enumerate(zip(s.get_params(), ref.get_params())):
+            assert _bitwise_equal(a, b), f"parameter {i} differs"
+    finally:
+        s.close()
+        ref.close()
