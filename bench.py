@@ -15,6 +15,8 @@ moments are resident in HBM before timing starts.  Prints ONE JSON line:
                    kernels): algorithmic flops per launch / average launch
                    duration, measured live with HIP events on the launch
                    stream around every such launch of a few extra steps
+  hbm_kernels      each bandwidth-bound kernel of the step: algorithmic bytes per
+                   launch / event-timed launch duration, against 8 TB/s
   cpu_baseline     the CPU oracle (a restatement of the reference's cpu-eigen
                    semantics, oracle/) on a bounded sample of the same workload
 
@@ -259,6 +261,23 @@ def main() -> int:
     achieved = kfl.value / (kms.value * 1e-3) / 1e12 if kms.value > 0 else 0.0  # TFLOP/s
     gemm_share = kms.value / prof_steps / step_ms
 
+    # Bandwidth-bound kernels: per-launch timing over a few more eager steps,
+    # each launch credited with its algorithmic HBM bytes.
+    _capi.check(lib.cnhip_hbm_timing_enable(1))
+    for _ in range(prof_steps):
+        sess.step(read_loss=False)
+    hbm_rows = _capi.hbm_timing_rows()
+    _capi.check(lib.cnhip_hbm_timing_enable(0))
+    hbm_kernels = []
+    for r in sorted(hbm_rows, key=lambda r: -r["total_ms"]):
+        gbs = r["total_bytes"] / (r["total_ms"] * 1e-3) / 1e9 if r["total_ms"] > 0 else 0.0
+        hbm_kernels.append({"kernel": r["kernel"],
+                            "launches_per_step": round(r["launches"] / prof_steps, 2),
+                            "avg_us": round(r["total_ms"] * 1e3 / r["launches"], 2),
+                            "bytes_per_launch": round(r["total_bytes"] / r["launches"]),
+                            "achieved_GBs": round(gbs, 1),
+                            "frac": round(gbs / PEAK_HBM_GBS, 4)})
+
     kernels = ("gemm_f32_kernel + conv_fwd/dgrad/wgrad_kernel (fp32 MFMA, all shapes of the step)"
                if args.config == 3 else "gemm_f32_kernel (fp32 MFMA GEMM, all shapes of the step)")
     result = {
@@ -289,6 +308,10 @@ def main() -> int:
                      "avg_launch_us": round(per_launch_us, 2),
                      "flops_per_launch": flops_per_launch,
                      "share_of_step": round(gemm_share, 3)},
+        "hbm_kernels": {"peak_GBs": PEAK_HBM_GBS,
+                        "note": "algorithmic bytes (inputs read once, outputs written once) / "
+                                "event-timed launch duration, per bandwidth-bound kernel",
+                        "kernels": hbm_kernels},
         "cpu_baseline": None,
     }
     sess.close()

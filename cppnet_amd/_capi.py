@@ -48,6 +48,8 @@ SIGNATURES: dict[str, tuple] = {
                                      f32, vp, i64, i64, i64, vp]),
     "cnhip_gemm_timing_enable": (i32, [i32]),
     "cnhip_gemm_timing_read": (i32, [C.POINTER(i64), C.POINTER(C.c_double), C.POINTER(C.c_double)]),
+    "cnhip_hbm_timing_enable": (i32, [i32]),
+    "cnhip_hbm_timing_read": (i32, [C.c_void_p, i32, C.POINTER(i32)]),
     "cnhip_linear_forward": (i32, [vp, vp, vp, vp, i64, i64, i64, vp]),
     "cnhip_linear_backward": (i32, [vp, vp, vp, vp, vp, vp, i64, i64, i64, i32, i32, vp]),
     "cnhip_column_sum": (i32, [vp, vp, i64, i64, i32, vp]),
@@ -96,6 +98,23 @@ SIGNATURES: dict[str, tuple] = {
                                     C.POINTER(vp), C.POINTER(i64), C.POINTER(f32),
                                     C.POINTER(f32), f32, f32, f32, f32, vp]),
 }
+
+
+class KernelTiming(C.Structure):
+    """cnhip_kernel_timing (include/cnhip.h)."""
+    _fields_ = [("kernel", C.c_char_p), ("launches", C.c_int64), ("total_ms", C.c_double),
+                ("total_bytes", C.c_double)]
+
+
+def hbm_timing_rows() -> list[dict]:
+    """Rows of cnhip_hbm_timing_read as dicts (kernel, launches, total_ms, total_bytes)."""
+    lib = load()
+    n = C.c_int()
+    check(lib.cnhip_hbm_timing_read(None, 0, C.byref(n)))
+    rows = (KernelTiming * max(1, n.value))()
+    check(lib.cnhip_hbm_timing_read(C.cast(rows, C.c_void_p), n.value, C.byref(n)))
+    return [{"kernel": r.kernel.decode(), "launches": r.launches, "total_ms": r.total_ms,
+             "total_bytes": r.total_bytes} for r in rows[:n.value]]
 
 
 class CnhipError(RuntimeError):

@@ -103,6 +103,10 @@ int adam_launch(AdamBatch& b, const AdamHyper& h, hipStream_t st, const char* wh
     blocks += (int)nb;
   }
   if (blocks == 0) return CNHIP_OK;
+  int64_t params = 0;
+  for (int i = 0; i < b.count; ++i) params += b.t[i].n;
+  // read W, g, m, v and write W, m, v: 28 bytes per parameter
+  HbmTimer timer("adam_multi_kernel", 28.0 * (double)params, st);
   hipLaunchKernelGGL(adam_multi_kernel, dim3(blocks), dim3(ADAM_BLOCK), 0, st, b, h);
   return check_launch(who);
 }

@@ -73,10 +73,29 @@ inline unsigned elementwise_grid(int64_t work_items, int block) {
 // the launch stream.  timing_slot returns nullptr when timing is off.
 struct TimingRec {
   hipEvent_t start, stop;
-  double flops;
+  double flops;         // MFMA records: algorithmic flops of the launch
+  const char* kernel;   // HBM records: kernel name (static string), else nullptr
+  double bytes;         // HBM records: algorithmic bytes of the launch
 };
 TimingRec* timing_slot(double flops);
-bool timing_on();
+// Per-launch timing of the bandwidth-bound kernels (cnhip_hbm_timing_*),
+// credited with the launch's algorithmic HBM bytes; nullptr when off.
+TimingRec* hbm_timing_slot(const char* kernel, double bytes);
+bool timing_on();  // either kind of per-launch timing is enabled
+
+// Brackets the launches of its scope with an HBM timing record.
+struct HbmTimer {
+  TimingRec* rec;
+  hipStream_t st;
+  HbmTimer(const char* kernel, double bytes, hipStream_t s) : rec(hbm_timing_slot(kernel, bytes)), st(s) {
+    if (rec) (void)hipEventRecord(rec->start, st);
+  }
+  ~HbmTimer() {
+    if (rec) (void)hipEventRecord(rec->stop, st);
+  }
+  HbmTimer(const HbmTimer&) = delete;
+  HbmTimer& operator=(const HbmTimer&) = delete;
+};
 
 // Fills `bytes` bytes at dst with the byte `value` by a kernel on `stream`
 // (not hipMemsetAsync: a memset node recorded into a captured graph has

@@ -471,6 +471,7 @@ int launch_wgrad(ConvArgs a, float* gW, float* gb, hipStream_t st, const char* w
     int status = check_launch(who);
     if (rec) (void)hipEventRecord(rec->stop, st);
     if (status == CNHIP_OK) {
+      HbmTimer timer("conv_wgrad_reduce_kernel", 4.0 * (double)(splits + 1) * d.OC * Ng, st);
       hipLaunchKernelGGL(conv_wgrad_reduce_kernel, dim3((unsigned)((d.OC * Ng + 63) / 64)),
                          dim3(64 * WGRAD_RW), 0, st, a.partial, (int)splits, d.OC, CT, a.has_bias,
                          gW, gb);
@@ -555,9 +556,13 @@ int cnhip_conv2d_backward(const float* X, const float* W, const float* dY, float
     void* ws = nullptr;
     CNHIP_TRY(cnhip::scratch(st, cnhip::kScratchLayer, (size_t)OC * CT * sizeof(float), &ws, who));
     float* Wr = static_cast<float*>(ws);
-    hipLaunchKernelGGL(cnhip::conv_relayout_w_kernel, dim3(cnhip::elementwise_grid(OC * CT, 256)),
-                       dim3(256), 0, st, W, Wr, OC, C, T);
-    int status = cnhip::check_launch(who);
+    int status;
+    {
+      cnhip::HbmTimer timer("conv_relayout_w_kernel", 8.0 * (double)OC * CT, st);
+      hipLaunchKernelGGL(cnhip::conv_relayout_w_kernel, dim3(cnhip::elementwise_grid(OC * CT, 256)),
+                         dim3(256), 0, st, W, Wr, OC, C, T);
+      status = cnhip::check_launch(who);
+    }
     if (status == CNHIP_OK) {
       cnhip::ConvArgs b{};
       b.d = d; b.src = dY; b.wt = Wr; b.out = dX;

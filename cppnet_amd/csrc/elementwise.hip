@@ -19,27 +19,33 @@ namespace {
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 struct ReluFwd {
+  static constexpr const char* kKernel = "unary_kernel<ReluFwd>";
   __device__ float operator()(float x) const { return relu_f(x); }
 };
 struct SigmoidFwd {
+  static constexpr const char* kKernel = "unary_kernel<SigmoidFwd>";
   __device__ float operator()(float x) const {
     const float c = fmaxf(-500.f, fminf(500.f, x));
     return 1.f / (1.f + expf(-c));
   }
 };
 struct TanhFwd {
+  static constexpr const char* kKernel = "unary_kernel<TanhFwd>";
   __device__ float operator()(float x) const { return tanhf(x); }
 };
 // grad_output * mask, mask = 1 where the cached output is > 0 (relu.cpp:177-181)
 struct ReluBwd {
+  static constexpr const char* kKernel = "binary_kernel<ReluBwd>";
   __device__ float operator()(float y, float dy) const { return dy * relu_mask(y); }
 };
 // grad_output * (s * (1 - s))  (sigmoid.cpp:192-194)
 struct SigmoidBwd {
+  static constexpr const char* kKernel = "binary_kernel<SigmoidBwd>";
   __device__ float operator()(float y, float dy) const { return dy * (y * (1.f - y)); }
 };
 // grad_output * (1 - t*t)  (tanh.cpp:153-154)
 struct TanhBwd {
+  static constexpr const char* kKernel = "binary_kernel<TanhBwd>";
   __device__ float operator()(float y, float dy) const { return dy * (1.f - y * y); }
 };
 
@@ -90,6 +96,7 @@ int launch_unary(const float* x, float* y, int64_t n, hipStream_t st, const char
   CNHIP_REQUIRE(x && y, "%s: NULL pointer", who);
   const int vec = (n % 4 == 0) && aligned16(x) && aligned16(y);
   const int64_t items = vec ? n / 4 : n;
+  HbmTimer timer(Op::kKernel, 8.0 * (double)n, st);
   hipLaunchKernelGGL(unary_kernel<Op>, dim3(elementwise_grid(items, 256)), dim3(256), 0, st, x, y,
                      n, vec);
   return check_launch(who);
@@ -103,6 +110,7 @@ int launch_binary(const float* y, const float* dy, float* dx, int64_t n, hipStre
   CNHIP_REQUIRE(y && dy && dx, "%s: NULL pointer", who);
   const int vec = (n % 4 == 0) && aligned16(y) && aligned16(dy) && aligned16(dx);
   const int64_t items = vec ? n / 4 : n;
+  HbmTimer timer(Op::kKernel, 12.0 * (double)n, st);
   hipLaunchKernelGGL(binary_kernel<Op>, dim3(elementwise_grid(items, 256)), dim3(256), 0, st, y,
                      dy, dx, n, vec);
   return check_launch(who);
@@ -281,6 +289,7 @@ int cnhip_bce_forward(const float* pred, const float* target, float* loss, int64
   CNHIP_TRY(cnhip::check_reduction(reduction, who));
   CNHIP_REQUIRE(n > 0, "%s: empty input", who);
   CNHIP_REQUIRE(pred && target && loss, "%s: NULL pointer", who);
+  cnhip::HbmTimer timer("bce_forward_kernel", 8.0 * (double)n + 4.0, as_stream(s));
   hipLaunchKernelGGL(cnhip::bce_forward_kernel, dim3(1), dim3(cnhip::RB), 0, as_stream(s), pred,
                      target, loss, n, reduction);
   return cnhip::check_launch(who);
@@ -292,6 +301,7 @@ int cnhip_bce_backward(const float* pred, const float* target, float* grad, int6
   CNHIP_TRY(cnhip::check_reduction(reduction, who));
   CNHIP_REQUIRE(n > 0, "%s: empty input", who);
   CNHIP_REQUIRE(pred && target && grad, "%s: NULL pointer", who);
+  cnhip::HbmTimer timer("bce_backward_kernel", 12.0 * (double)n, as_stream(s));
   hipLaunchKernelGGL(cnhip::bce_backward_kernel, dim3(cnhip::elementwise_grid(n, 256)), dim3(256),
                      0, as_stream(s), pred, target, grad, n, reduction);
   return cnhip::check_launch(who);
@@ -303,6 +313,7 @@ int cnhip_mse_forward(const float* pred, const float* target, float* loss, int64
   CNHIP_TRY(cnhip::check_reduction(reduction, who));
   CNHIP_REQUIRE(n > 0, "%s: empty input", who);
   CNHIP_REQUIRE(pred && target && loss, "%s: NULL pointer", who);
+  cnhip::HbmTimer timer("mse_forward_kernel", 8.0 * (double)n + 4.0, as_stream(s));
   hipLaunchKernelGGL(cnhip::mse_forward_kernel, dim3(1), dim3(cnhip::RB), 0, as_stream(s), pred,
                      target, loss, n, reduction);
   return cnhip::check_launch(who);
@@ -315,6 +326,7 @@ int cnhip_mse_backward(const float* pred, const float* target, float* grad, int6
   CNHIP_REQUIRE(n > 0, "%s: empty input", who);
   CNHIP_REQUIRE(pred && target && grad, "%s: NULL pointer", who);
   const float scale = (reduction == CNHIP_REDUCE_MEAN) ? 2.0f / (float)n : 2.0f;
+  cnhip::HbmTimer timer("mse_backward_kernel", 12.0 * (double)n, as_stream(s));
   hipLaunchKernelGGL(cnhip::mse_backward_kernel, dim3(cnhip::elementwise_grid(n, 256)), dim3(256),
                      0, as_stream(s), pred, target, grad, n, scale);
   return cnhip::check_launch(who);
@@ -333,12 +345,18 @@ int cnhip_softmax_ce_forward(const float* logits, const float* targets, float* s
   void* ws = nullptr;
   CNHIP_TRY(cnhip::scratch(st, cnhip::kScratchLayer, (size_t)blocks * sizeof(float), &ws, who));
   float* partial = static_cast<float*>(ws);
-  hipLaunchKernelGGL(cnhip::softmax_ce_rows_kernel, dim3((unsigned)blocks), dim3(cnhip::SCE_BLOCK),
-                     0, st, logits, targets, softmax_out, partial, batch, classes);
-  int status = cnhip::check_launch(who);
+  int status;
+  {
+    // logits and targets read, softmax and the per-block partial losses written
+    cnhip::HbmTimer timer("softmax_ce_rows_kernel", 12.0 * (double)batch * (double)classes + 4.0 * blocks, st);
+    hipLaunchKernelGGL(cnhip::softmax_ce_rows_kernel, dim3((unsigned)blocks), dim3(cnhip::SCE_BLOCK),
+                       0, st, logits, targets, softmax_out, partial, batch, classes);
+    status = cnhip::check_launch(who);
+  }
   if (status == CNHIP_OK) {
     // "mean" divides the summed loss by the batch size (softmax_cross_entropy.cpp:154-156)
     const float divisor = reduction == CNHIP_REDUCE_MEAN ? (float)batch : 1.0f;
+    cnhip::HbmTimer timer("partial_sum_kernel", 4.0 * blocks + 4.0, st);
     hipLaunchKernelGGL(cnhip::partial_sum_kernel, dim3(1), dim3(cnhip::RB), 0, st, partial, blocks,
                        loss, divisor);
     status = cnhip::check_launch(who);
@@ -354,6 +372,7 @@ int cnhip_softmax_ce_backward(const float* softmax, const float* targets, float*
   CNHIP_REQUIRE(softmax && targets && grad, "%s: NULL pointer", who);
   const int64_t n = batch * classes;
   const float inv_batch = 1.0f / (float)batch;
+  cnhip::HbmTimer timer("softmax_ce_backward_kernel", 12.0 * (double)n, as_stream(s));
   hipLaunchKernelGGL(cnhip::softmax_ce_backward_kernel, dim3(cnhip::elementwise_grid(n, 256)),
                      dim3(256), 0, as_stream(s), softmax, targets, grad, n,
                      reduction == CNHIP_REDUCE_MEAN ? 1 : 0, inv_batch);

@@ -16,6 +16,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstring>
 #include <vector>
 
 #include "act_math.hpp"
@@ -256,25 +257,46 @@ struct Timing {
   std::vector<TimingRec> pool;
   size_t used = 0;
 };
-thread_local Timing g_timing;
+thread_local Timing g_timing;      // MFMA GEMM-shaped launches
+thread_local Timing g_hbm_timing;  // bandwidth-bound launches
 
-}  // namespace
-
-bool timing_on() { return g_timing.on; }
-
-TimingRec* timing_slot(double flops) {
-  Timing& t = g_timing;
+TimingRec* next_slot(Timing& t) {
   if (!t.on) return nullptr;
   if (t.used == t.pool.size()) {
     TimingRec r{};
-    if (hipEventCreate(&r.start) != hipSuccess || hipEventCreate(&r.stop) != hipSuccess) {
+    // timing-only events: no system-scope fence (cache writeback) at record,
+    // which would add to the duration of short launches
+    if (hipEventCreateWithFlags(&r.start, hipEventDisableSystemFence) != hipSuccess ||
+        hipEventCreateWithFlags(&r.stop, hipEventDisableSystemFence) != hipSuccess) {
       (void)hipGetLastError();
       return nullptr;
     }
     t.pool.push_back(r);
   }
-  TimingRec* r = &t.pool[t.used++];
-  r->flops = flops;
+  return &t.pool[t.used++];
+}
+
+}  // namespace
+
+bool timing_on() { return g_timing.on || g_hbm_timing.on; }
+
+TimingRec* timing_slot(double flops) {
+  TimingRec* r = next_slot(g_timing);
+  if (r) {
+    r->flops = flops;
+    r->kernel = nullptr;
+    r->bytes = 0.0;
+  }
+  return r;
+}
+
+TimingRec* hbm_timing_slot(const char* kernel, double bytes) {
+  TimingRec* r = next_slot(g_hbm_timing);
+  if (r) {
+    r->flops = 0.0;
+    r->kernel = kernel;
+    r->bytes = bytes;
+  }
   return r;
 }
 
@@ -493,6 +515,9 @@ int gemm_f32_core(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, flo
 
   if (splits > 1) {
     if (status == CNHIP_OK) {
+      // reads the partials (and C when beta != 0), writes C
+      const double mn = (double)M * (double)N * (double)batches;
+      HbmTimer timer("splitk_reduce_kernel", 4.0 * mn * (splits + 1 + (beta != 0.f ? 1 : 0)), st);
       hipLaunchKernelGGL(splitk_reduce_kernel, dim3(elementwise_grid(M * N * batches, 256)),
                          dim3(256), 0, st, g, batches);
       status = check_launch(who);
@@ -567,5 +592,33 @@ extern "C" int cnhip_gemm_timing_read(int64_t* launches, double* total_ms, doubl
   *launches = (int64_t)t.used;
   *total_ms = ms;
   *total_flops = fl;
+  return CNHIP_OK;
+}
+
+extern "C" int cnhip_hbm_timing_enable(int on) {
+  cnhip::g_hbm_timing.on = on != 0;
+  cnhip::g_hbm_timing.used = 0;
+  return CNHIP_OK;
+}
+
+extern "C" int cnhip_hbm_timing_read(cnhip_kernel_timing* rows, int max_rows, int* n_rows) {
+  const char* who = "cnhip_hbm_timing_read";
+  CNHIP_REQUIRE(n_rows && (rows || max_rows == 0) && max_rows >= 0, "%s: bad arguments", who);
+  cnhip::Timing& t = cnhip::g_hbm_timing;
+  std::vector<cnhip_kernel_timing> agg;  // per kernel name, first-seen order
+  for (size_t i = 0; i < t.used; ++i) {
+    const cnhip::TimingRec& r = t.pool[i];
+    float e = 0.f;
+    CNHIP_TRY(cnhip::check_hip(hipEventSynchronize(r.stop), who));
+    CNHIP_TRY(cnhip::check_hip(hipEventElapsedTime(&e, r.start, r.stop), who));
+    size_t k = 0;
+    while (k < agg.size() && std::strcmp(agg[k].kernel, r.kernel) != 0) ++k;
+    if (k == agg.size()) agg.push_back(cnhip_kernel_timing{r.kernel, 0, 0.0, 0.0});
+    agg[k].launches += 1;
+    agg[k].total_ms += e;
+    agg[k].total_bytes += r.bytes;
+  }
+  for (size_t k = 0; k < agg.size() && (int)k < max_rows; ++k) rows[k] = agg[k];
+  *n_rows = (int)agg.size();
   return CNHIP_OK;
 }

@@ -36,11 +36,20 @@ __global__ void __launch_bounds__(256) column_sum_kernel(const float* __restrict
   const float* p = in + rows * col;
   float s = 0.f;
   if (vec) {
+    // four float4 loads in flight per lane, four running sums added in order
     const int64_t n4 = rows >> 2;
-    for (int64_t i = lane; i < n4; i += 64) {
-      const f32x4 v = reinterpret_cast<const f32x4*>(p)[i];
-      s += (v[0] + v[1]) + (v[2] + v[3]);
+    const f32x4* p4 = reinterpret_cast<const f32x4*>(p);
+    f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = a0, a2 = a0, a3 = a0;
+    int64_t i = lane;
+    for (; i + 192 < n4; i += 256) {
+      a0 += p4[i];
+      a1 += p4[i + 64];
+      a2 += p4[i + 128];
+      a3 += p4[i + 192];
     }
+    for (; i < n4; i += 64) a0 += p4[i];
+    const f32x4 t = (a0 + a1) + (a2 + a3);
+    s = (t[0] + t[1]) + (t[2] + t[3]);
   } else {
     for (int64_t i = lane; i < rows; i += 64) s += p[i];
   }
@@ -58,6 +67,8 @@ int column_sum(const float* in, float* out, int64_t rows, int64_t cols, int accu
   CNHIP_REQUIRE(out != nullptr, "%s: out is NULL", who);
   CNHIP_REQUIRE(rows == 0 || in != nullptr, "%s: in is NULL", who);
   const int vec = (rows % 4 == 0) && aligned16(in);
+  HbmTimer timer("column_sum_kernel", 4.0 * (double)rows * (double)cols + (accumulate ? 8.0 : 4.0) * (double)cols,
+                 st);
   hipLaunchKernelGGL(column_sum_kernel, dim3((unsigned)((cols + 3) / 4)), dim3(256), 0, st, in, out,
                      rows, cols, accumulate, vec);
   return check_launch(who);

@@ -60,6 +60,77 @@ __global__ void __launch_bounds__(256) maxpool_fwd_kernel(PoolDims d, const floa
   }
 }
 
+// maxpool_fwd_kernel for N % 4 == 0 (and 16-byte aligned tensors): a wave
+// owns a window position, its lanes stride over n in float4s, so each tap
+// is one 16-byte load per lane; per element the same strict-> scan in
+// (ph, pw) order as the scalar kernel.
+__global__ void __launch_bounds__(256) maxpool_fwd_vec_kernel(PoolDims d, const float* __restrict__ X,
+                                                              float* __restrict__ Y,
+                                                              int32_t* __restrict__ idx) {
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  typedef int i32x4 __attribute__((ext_vector_type(4)));
+  const int C = (int)d.C, HO = (int)d.HO, pool = (int)d.pool, stride = (int)d.stride;
+  const int positions = C * HO * (int)d.WO;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t N = d.N, N4 = d.N >> 2, sh = d.N * d.C, sw = d.N * d.C * d.H;
+  for (int pos = blockIdx.x * 4 + w; pos < positions; pos += gridDim.x * 4) {
+    const int c = pos % C, r = pos / C, oh = r % HO, ow = r / HO;
+    const float* xb = X + N * c + sh * (oh * stride) + sw * (ow * stride);
+    for (int64_t q = lane; q < N4; q += 64) {
+      f32x4 mx = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+      i32x4 mi = {0, 0, 0, 0};
+      for (int ph = 0; ph < pool; ++ph)
+        for (int pw = 0; pw < pool; ++pw) {
+          const f32x4 v = *reinterpret_cast<const f32x4*>(xb + sh * ph + sw * pw + 4 * q);
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (v[e] > mx[e]) {
+              mx[e] = v[e];
+              mi[e] = ph * pool + pw;
+            }
+        }
+      *reinterpret_cast<f32x4*>(Y + N * pos + 4 * q) = mx;
+      *reinterpret_cast<i32x4*>(idx + N * pos + 4 * q) = mi;
+    }
+  }
+}
+
+// maxpool_bwd_tiled_kernel for N % 4 == 0: a wave per window, float4s over n.
+template <bool MASK>
+__global__ void __launch_bounds__(256) maxpool_bwd_tiled_vec_kernel(PoolDims d,
+                                                                    const float* __restrict__ dY,
+                                                                    const int32_t* __restrict__ idx,
+                                                                    const float* __restrict__ y,
+                                                                    float* __restrict__ dX) {
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  typedef int i32x4 __attribute__((ext_vector_type(4)));
+  const int C = (int)d.C, HO = (int)d.HO, pool = (int)d.pool;
+  const int positions = C * HO * (int)d.WO;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t N = d.N, N4 = d.N >> 2, sh = d.N * d.C, sw = d.N * d.C * d.H;
+  for (int pos = blockIdx.x * 4 + w; pos < positions; pos += gridDim.x * 4) {
+    const int c = pos % C, r = pos / C, oh = r % HO, ow = r / HO;
+    const int64_t base = N * c + sh * (oh * pool) + sw * (ow * pool);
+    for (int64_t q = lane; q < N4; q += 64) {
+      const i32x4 mi = *reinterpret_cast<const i32x4*>(idx + N * pos + 4 * q);
+      const f32x4 gy = 0.f + *reinterpret_cast<const f32x4*>(dY + N * pos + 4 * q);
+      for (int ph = 0; ph < pool; ++ph)
+        for (int pw = 0; pw < pool; ++pw) {
+          const int64_t o = base + sh * ph + sw * pw + 4 * q;
+          f32x4 g;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) g[e] = mi[e] == ph * pool + pw ? gy[e] : 0.f;
+          if (MASK) {
+            const f32x4 yv = *reinterpret_cast<const f32x4*>(y + o);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) g[e] *= relu_mask(yv[e]);
+          }
+          *reinterpret_cast<f32x4*>(dX + o) = g;
+        }
+    }
+  }
+}
+
 // Backward as a gather (any stride): input position (c, ih, iw) sums dY over
 // the windows that contain it and picked it, in (oh, ow) order starting from
 // 0.  MASK: the pool's input is a ReLU output y, and the result is scaled by
@@ -151,7 +222,18 @@ int maxpool_backward(const float* dY, const int32_t* idx, const float* y, float*
   CNHIP_REQUIRE(C * H * W < ((int64_t)1 << 31), "%s: too many input positions", who);
   const hipStream_t st = as_stream(stream);
   const unsigned threads = pool_threads(N);
-  if (d.stride == d.pool && d.HO * d.pool == H && d.WO * d.pool == W) {
+  // dY and the argmax read per output; dX written (and the ReLU output y
+  // read, when fused) per input
+  const double outs = (double)N * C * d.HO * d.WO, ins = (double)N * C * H * W;
+  HbmTimer timer(y ? "maxpool_bwd_kernel<relu>" : "maxpool_bwd_kernel", 8.0 * outs + (y ? 8.0 : 4.0) * ins, st);
+  const bool vec = N % 4 == 0 && aligned16(dY) && aligned16(idx) && aligned16(dX) && (!y || aligned16(y));
+  if (d.stride == d.pool && d.HO * d.pool == H && d.WO * d.pool == W && vec) {
+    const unsigned grid = pool_grid((C * d.HO * d.WO + 3) / 4);
+    if (y)
+      hipLaunchKernelGGL(maxpool_bwd_tiled_vec_kernel<true>, dim3(grid), dim3(256), 0, st, d, dY, idx, y, dX);
+    else
+      hipLaunchKernelGGL(maxpool_bwd_tiled_vec_kernel<false>, dim3(grid), dim3(256), 0, st, d, dY, idx, y, dX);
+  } else if (d.stride == d.pool && d.HO * d.pool == H && d.WO * d.pool == W) {
     const unsigned grid = pool_grid(C * d.HO * d.WO);
     if (y)
       hipLaunchKernelGGL(maxpool_bwd_tiled_kernel<true>, dim3(grid), dim3(threads), 0, st, d, dY,
@@ -185,8 +267,15 @@ int cnhip_maxpool2d_forward(const float* X, float* Y, int32_t* idx, int64_t N, i
   CNHIP_REQUIRE(X && Y && idx, "%s: NULL pointer", who);
   const int64_t positions = C * d.HO * d.WO;
   CNHIP_REQUIRE(positions < ((int64_t)1 << 31), "%s: too many output positions", who);
-  hipLaunchKernelGGL(cnhip::maxpool_fwd_kernel, dim3(cnhip::pool_grid(positions)),
-                     dim3(cnhip::pool_threads(N)), 0, cnhip::as_stream(stream), d, X, Y, idx);
+  // X read once; Y and the int32 argmax written
+  cnhip::HbmTimer timer("maxpool_fwd_kernel", 4.0 * (double)N * C * H * W + 8.0 * (double)N * positions,
+                        cnhip::as_stream(stream));
+  if (N % 4 == 0 && cnhip::aligned16(X) && cnhip::aligned16(Y) && cnhip::aligned16(idx))
+    hipLaunchKernelGGL(cnhip::maxpool_fwd_vec_kernel, dim3(cnhip::pool_grid((positions + 3) / 4)), dim3(256),
+                       0, cnhip::as_stream(stream), d, X, Y, idx);
+  else
+    hipLaunchKernelGGL(cnhip::maxpool_fwd_kernel, dim3(cnhip::pool_grid(positions)),
+                       dim3(cnhip::pool_threads(N)), 0, cnhip::as_stream(stream), d, X, Y, idx);
   return cnhip::check_launch(who);
 }
 

@@ -563,6 +563,7 @@ int cnhip_seq_select(const float* Y, float* out, int64_t B, int64_t S, int64_t D
   const char* who = "cnhip_seq_select";
   CNHIP_REQUIRE(B > 0 && S > 0 && D > 0 && t >= 0 && t < S, "%s: bad shape or step", who);
   CNHIP_REQUIRE(Y && out, "%s: NULL pointer", who);
+  cnhip::HbmTimer timer("seq_select_kernel", 8.0 * (double)B * (double)D, as_stream(stream));
   hipLaunchKernelGGL(cnhip::seq_select_kernel, dim3((unsigned)((B * D + 255) / 256)), dim3(256), 0,
                      as_stream(stream), Y, out, B, S, D, t);
   return cnhip::check_launch(who);
@@ -573,6 +574,9 @@ int cnhip_seq_scatter(const float* in, float* Y, int64_t B, int64_t S, int64_t D
   const char* who = "cnhip_seq_scatter";
   CNHIP_REQUIRE(B > 0 && S > 0 && D > 0 && t >= 0 && t < S, "%s: bad shape or step", who);
   CNHIP_REQUIRE(Y && in, "%s: NULL pointer", who);
+  // the step's rows read; the whole sequence gradient written (zeros elsewhere)
+  cnhip::HbmTimer timer("seq_scatter_kernel", 4.0 * (double)B * (double)D * (double)(S + 1),
+                        as_stream(stream));
   hipLaunchKernelGGL(cnhip::seq_scatter_kernel, dim3(cnhip::elementwise_grid(B * S * D, 256)),
                      dim3(256), 0, as_stream(stream), in, Y, B, S, D, t);
   return cnhip::check_launch(who);

@@ -77,6 +77,7 @@ int fill_bytes(void* dst, int value, size_t bytes, hipStream_t stream, const cha
   if (bytes == 0) return CNHIP_OK;
   const uint32_t b = (uint32_t)value & 0xffu;
   unsigned char* d = static_cast<unsigned char*>(dst);
+  HbmTimer timer("fill_bytes_kernel", (double)bytes, stream);
   if (aligned16(dst)) {
     const size_t n16 = bytes / 16, tail = bytes % 16;
     const unsigned grid = elementwise_grid((int64_t)(n16 > tail ? n16 : tail), 256);
@@ -252,7 +253,7 @@ struct Graph {
 int cnhip_graph_begin_capture(cnhip_stream_t stream) {
   const char* who = "cnhip_graph_begin_capture";
   CNHIP_REQUIRE(stream != nullptr, "%s: capture needs a created stream, not the default stream", who);
-  CNHIP_REQUIRE(!cnhip::timing_on(), "%s: per-launch GEMM timing is enabled; disable it first", who);
+  CNHIP_REQUIRE(!cnhip::timing_on(), "%s: per-launch kernel timing is enabled; disable it first", who);
   // Relaxed: allocations of not-yet-cached buffers by the host layer may
   // call hipMalloc while the capture is open (that is not stream work).
   return check_hip(hipStreamBeginCapture(as_stream(stream), hipStreamCaptureModeRelaxed), who);

@@ -39,32 +39,74 @@ namespace {
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // ---------------------------------------------------------------- transpose
-// ColMajor in [R, C] -> out [C, R]: out[c + C*r] = in[r + R*c], 64x64 tiles
-// through LDS (+1 pad against bank conflicts); both sides coalesced.
-constexpr int TT = 64;
+// ColMajor in [R, C] -> out [C, R]: out[c + C*r] = in[r + R*c], TR x TC tiles
+// through LDS (a column of the tile padded to TR + 1 floats, so both the
+// r-contiguous writes and the c-contiguous reads of LDS are conflict-free).
+// VEC (R, C multiples of 4, 16-byte aligned pointers): global loads are
+// float4s along r and stores float4s along c.  The tile is shaped to R: the
+// per-sample relayouts of attention have R = batch (32), where a 64 x 64
+// tile would leave half its rows empty.
+constexpr int TT = 64;  // token tile of the embedding kernels
+
+template <int TR, int TC, bool VEC>
 __global__ void __launch_bounds__(256) transpose_kernel(const float* __restrict__ in,
                                                         float* __restrict__ out, int64_t R,
                                                         int64_t C) {
-  __shared__ float tile[TT][TT + 1];
-  const int64_t r0 = (int64_t)blockIdx.x * TT, c0 = (int64_t)blockIdx.y * TT;
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;  // 64 x 4
-  for (int j = ty; j < TT; j += 4) {
-    const int64_t r = r0 + tx, c = c0 + j;
-    if (r < R && c < C) tile[j][tx] = in[r + R * c];
-  }
-  __syncthreads();
-  for (int j = ty; j < TT; j += 4) {
-    const int64_t c = c0 + tx, r = r0 + j;
-    if (r < R && c < C) out[c + C * r] = tile[tx][j];
+  __shared__ float tile[TC][TR + 1];
+  const int64_t r0 = (int64_t)blockIdx.x * TR, c0 = (int64_t)blockIdx.y * TC;
+  const int t = threadIdx.x;
+  if (VEC) {
+    constexpr int R4 = TR / 4, C4 = TC / 4;
+    for (int i = t; i < R4 * TC; i += 256) {
+      const int r = (i % R4) * 4, c = i / R4;
+      if (r0 + r < R && c0 + c < C) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(in + (r0 + r) + R * (c0 + c));
+#pragma unroll
+        for (int k = 0; k < 4; ++k) tile[c][r + k] = v[k];
+      }
+    }
+    __syncthreads();
+    for (int i = t; i < C4 * TR; i += 256) {
+      const int c = (i % C4) * 4, r = i / C4;
+      if (r0 + r < R && c0 + c < C) {
+        f32x4 v;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[k] = tile[c + k][r];
+        *reinterpret_cast<f32x4*>(out + (c0 + c) + C * (r0 + r)) = v;
+      }
+    }
+  } else {
+    for (int i = t; i < TR * TC; i += 256) {
+      const int r = i % TR, c = i / TR;
+      if (r0 + r < R && c0 + c < C) tile[c][r] = in[(r0 + r) + R * (c0 + c)];
+    }
+    __syncthreads();
+    for (int i = t; i < TC * TR; i += 256) {
+      const int c = i % TC, r = i / TC;
+      if (r0 + r < R && c0 + c < C) out[(c0 + c) + C * (r0 + r)] = tile[c][r];
+    }
   }
 }
 
-int transpose(const float* in, float* out, int64_t R, int64_t C, hipStream_t st, const char* who) {
-  CNHIP_REQUIRE((R + TT - 1) / TT < (1ll << 31) && (C + TT - 1) / TT <= 65535,
+template <int TR, int TC>
+int transpose_t(const float* in, float* out, int64_t R, int64_t C, hipStream_t st, const char* who) {
+  CNHIP_REQUIRE((R + TR - 1) / TR < (1ll << 31) && (C + TC - 1) / TC <= 65535,
                 "%s: transpose %lld x %lld too large", who, (long long)R, (long long)C);
-  hipLaunchKernelGGL(transpose_kernel, dim3((unsigned)((R + TT - 1) / TT), (unsigned)((C + TT - 1) / TT)),
-                     dim3(256), 0, st, in, out, R, C);
+  const dim3 grid((unsigned)((R + TR - 1) / TR), (unsigned)((C + TC - 1) / TC));
+  const bool vec = R % 4 == 0 && C % 4 == 0 && aligned16(in) && aligned16(out);
+  if (vec)
+    hipLaunchKernelGGL((transpose_kernel<TR, TC, true>), grid, dim3(256), 0, st, in, out, R, C);
+  else
+    hipLaunchKernelGGL((transpose_kernel<TR, TC, false>), grid, dim3(256), 0, st, in, out, R, C);
   return check_launch(who);
+}
+
+int transpose(const float* in, float* out, int64_t R, int64_t C, hipStream_t st, const char* who) {
+  HbmTimer timer("transpose_kernel", 8.0 * (double)R * (double)C, st);
+  if (R <= 16) return transpose_t<16, 256>(in, out, R, C, st, who);
+  if (R <= 32) return transpose_t<32, 128>(in, out, R, C, st, who);
+  if (C <= 32) return transpose_t<128, 32>(in, out, R, C, st, who);
+  return transpose_t<64, 64>(in, out, R, C, st, who);
 }
 
 // ---------------------------------------------------------------- row softmax
@@ -110,9 +152,96 @@ __global__ void __launch_bounds__(256) softmax_rows_bwd_kernel(const float* __re
   for (int64_t j = lane; j < L; j += 64) g[r * L + j] = (ar[j] * (dr[j] - dot)) * scale;
 }
 
+// softmax_rows_kernel / softmax_rows_bwd_kernel for L <= 64 * PER: the row
+// stays in registers (lane holds j = lane, lane + 64, ..), so x (A, dA) is
+// read once and y (g) written once; the same operations in the same order,
+// so the results are identical to the looping kernels.
+template <int PER>
+__global__ void __launch_bounds__(256) softmax_rows_reg_kernel(const float* __restrict__ x,
+                                                               float* __restrict__ y, int64_t rows,
+                                                               int64_t L) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const float* xr = x + r * L;
+  float* yr = y + r * L;
+  float v[PER];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int64_t j = lane + 64 * i;
+    v[i] = j < L ? xr[j] : -INFINITY;
+    mx = fmaxf(mx, v[i]);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  float sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    if (lane + 64 * i < L) {
+      v[i] = expf(v[i] - mx);
+      sum += v[i];
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int64_t j = lane + 64 * i;
+    if (j < L) yr[j] = v[i] / sum;
+  }
+}
+
+template <int PER>
+__global__ void __launch_bounds__(256) softmax_rows_bwd_reg_kernel(const float* __restrict__ A,
+                                                                   const float* __restrict__ dA,
+                                                                   float* __restrict__ g, int64_t rows,
+                                                                   int64_t L, float scale) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const float* ar = A + r * L;
+  const float* dr = dA + r * L;
+  float a[PER], d[PER];
+  float dot = 0.f;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int64_t j = lane + 64 * i;
+    a[i] = j < L ? ar[j] : 0.f;
+    d[i] = j < L ? dr[j] : 0.f;
+    if (j < L) dot += d[i] * a[i];
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) dot += __shfl_xor(dot, off, 64);
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int64_t j = lane + 64 * i;
+    if (j < L) g[r * L + j] = (a[i] * (d[i] - dot)) * scale;
+  }
+}
+
 int softmax_rows(const float* x, float* y, int64_t rows, int64_t L, hipStream_t st, const char* who) {
-  hipLaunchKernelGGL(softmax_rows_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, x, y,
-                     rows, L);
+  HbmTimer timer("softmax_rows_kernel", 8.0 * (double)rows * (double)L, st);
+  const dim3 grid((unsigned)((rows + 3) / 4));
+  if (L <= 256)
+    hipLaunchKernelGGL(softmax_rows_reg_kernel<4>, grid, dim3(256), 0, st, x, y, rows, L);
+  else if (L <= 1024)
+    hipLaunchKernelGGL(softmax_rows_reg_kernel<16>, grid, dim3(256), 0, st, x, y, rows, L);
+  else
+    hipLaunchKernelGGL(softmax_rows_kernel, grid, dim3(256), 0, st, x, y, rows, L);
+  return check_launch(who);
+}
+
+int softmax_rows_bwd(const float* A, const float* dA, float* g, int64_t rows, int64_t L, float scale,
+                     hipStream_t st, const char* who) {
+  HbmTimer timer("softmax_rows_bwd_kernel", 12.0 * (double)rows * (double)L, st);
+  const dim3 grid((unsigned)((rows + 3) / 4));
+  if (L <= 256)
+    hipLaunchKernelGGL(softmax_rows_bwd_reg_kernel<4>, grid, dim3(256), 0, st, A, dA, g, rows, L, scale);
+  else if (L <= 1024)
+    hipLaunchKernelGGL(softmax_rows_bwd_reg_kernel<16>, grid, dim3(256), 0, st, A, dA, g, rows, L, scale);
+  else
+    hipLaunchKernelGGL(softmax_rows_bwd_kernel, grid, dim3(256), 0, st, A, dA, g, rows, L, scale);
   return check_launch(who);
 }
 
@@ -497,18 +626,209 @@ __global__ void __launch_bounds__(BNT) bn_bwd_reg_kernel(const float* __restrict
 }
 
 // ---------------------------------------------------------------- GELU / pool / add
+// BatchNorm for columns of N = 4k rows (16-byte aligned): T threads per
+// feature, thread t holds float4s t, t + T, .. of the column in registers
+// (V4 of them), so every element is read once and written once, and a
+// 1024-thread block keeps 16 waves per feature in flight (the 256-thread
+// kernels above hold a whole column per 4 waves and leave the CU idle while
+// a block reduces).  Sums: per-thread float4 partials, then waves, then the
+// T/64 wave sums in order; fixed for a given launch shape.
+template <int T>
+__device__ __forceinline__ void wave_sums(float* v, int k) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1)
+    for (int j = 0; j < k; ++j) v[j] += __shfl_xor(v[j], off, 64);
+}
+
+template <int T, int V4>
+__global__ void __launch_bounds__(T) bn_fwd_vec_kernel(const float* __restrict__ x,
+                                                       float* __restrict__ y,
+                                                       float* __restrict__ xhat,
+                                                       const float* __restrict__ gamma,
+                                                       const float* __restrict__ beta,
+                                                       float* __restrict__ rmean,
+                                                       float* __restrict__ rvar,
+                                                       float* __restrict__ bmean,
+                                                       float* __restrict__ bvar, int64_t N,
+                                                       float momentum, float eps) {
+  __shared__ float sm[2][T / 64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t f = blockIdx.x, n4 = N >> 2;
+  const f32x4* xc = reinterpret_cast<const f32x4*>(x + N * f);
+  const float inv_batch = 1.0f / (float)N;
+  f32x4 v[V4];
+  float s[1] = {0.f};
+#pragma unroll
+  for (int i = 0; i < V4; ++i) {
+    const int64_t q = threadIdx.x + (int64_t)T * i;
+    v[i] = q < n4 ? xc[q] : f32x4{0.f, 0.f, 0.f, 0.f};
+    s[0] += (v[i][0] + v[i][1]) + (v[i][2] + v[i][3]);
+  }
+  wave_sums<T>(s, 1);
+  if (lane == 0) sm[0][w] = s[0];
+  __syncthreads();
+  float mean = 0.f;
+#pragma unroll
+  for (int i = 0; i < T / 64; ++i) mean += sm[0][i];
+  mean *= inv_batch;
+  float s2[1] = {0.f};
+#pragma unroll
+  for (int i = 0; i < V4; ++i) {
+    const int64_t q = threadIdx.x + (int64_t)T * i;
+    if (q < n4) {
+      const f32x4 d = v[i] - mean;
+      s2[0] += (d[0] * d[0] + d[1] * d[1]) + (d[2] * d[2] + d[3] * d[3]);
+    }
+  }
+  wave_sums<T>(s2, 1);
+  if (lane == 0) sm[1][w] = s2[0];
+  __syncthreads();
+  float var = 0.f;
+#pragma unroll
+  for (int i = 0; i < T / 64; ++i) var += sm[1][i];
+  var *= inv_batch;
+  const float den = sqrtf(var + eps);
+  const float g = gamma[f], b = beta[f];
+  f32x4* yc = reinterpret_cast<f32x4*>(y + N * f);
+  f32x4* hc = reinterpret_cast<f32x4*>(xhat + N * f);
+#pragma unroll
+  for (int i = 0; i < V4; ++i) {
+    const int64_t q = threadIdx.x + (int64_t)T * i;
+    if (q < n4) {
+      f32x4 xh, o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        xh[e] = (v[i][e] - mean) / den;
+        o[e] = g * xh[e] + b;
+      }
+      hc[q] = xh;
+      yc[q] = o;
+    }
+  }
+  if (threadIdx.x == 0) {
+    bmean[f] = mean;
+    bvar[f] = var;
+    rmean[f] = (1.0f - momentum) * rmean[f] + momentum * mean;
+    rvar[f] = (1.0f - momentum) * rvar[f] + momentum * var;
+  }
+}
+
+// batch_norm.cpp:353-385 with the layout of bn_fwd_vec_kernel: dY, x and
+// xhat read once as float4s, the four column sums reduced together.
+template <int T, int V4>
+__global__ void __launch_bounds__(T) bn_bwd_vec_kernel(const float* __restrict__ dY,
+                                                       const float* __restrict__ x,
+                                                       const float* __restrict__ xhat,
+                                                       const float* __restrict__ gamma,
+                                                       const float* __restrict__ bmean,
+                                                       const float* __restrict__ bvar,
+                                                       float* __restrict__ ggamma,
+                                                       float* __restrict__ gbeta,
+                                                       float* __restrict__ dX, int64_t N, float eps) {
+  __shared__ float sm[4][T / 64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t f = blockIdx.x, n4 = N >> 2;
+  const f32x4* dyc = reinterpret_cast<const f32x4*>(dY + N * f);
+  const f32x4* xc = reinterpret_cast<const f32x4*>(x + N * f);
+  const f32x4* hc = reinterpret_cast<const f32x4*>(xhat + N * f);
+  const float g = gamma[f], mean = bmean[f];
+  const float inv_std = 1.0f / sqrtf(bvar[f] + eps);
+  const float inv_batch = 1.0f / (float)N;
+  const float c3 = (-0.5f) * inv_std * inv_std * inv_std;
+  f32x4 dy[V4], xm[V4];
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};  // grad_gamma, grad_beta, dvar, dmean
+#pragma unroll
+  for (int i = 0; i < V4; ++i) {
+    const int64_t q = threadIdx.x + (int64_t)T * i;
+    dy[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    xm[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (q < n4) {
+      dy[i] = dyc[q];
+      const f32x4 xh = hc[q];
+      xm[i] = xc[q] - mean;
+      f32x4 pg, pv, pm;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float dxh = dy[i][e] * g;
+        pg[e] = dy[i][e] * xh[e];
+        pv[e] = dxh * xm[i][e] * c3;
+        pm[e] = dxh * (-inv_std);
+      }
+      acc[0] += (pg[0] + pg[1]) + (pg[2] + pg[3]);
+      acc[1] += (dy[i][0] + dy[i][1]) + (dy[i][2] + dy[i][3]);
+      acc[2] += (pv[0] + pv[1]) + (pv[2] + pv[3]);
+      acc[3] += (pm[0] + pm[1]) + (pm[2] + pm[3]);
+    }
+  }
+  wave_sums<T>(acc, 4);
+  if (lane == 0) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) sm[j][w] = acc[j];
+  }
+  __syncthreads();
+  float tot[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < T / 64; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) tot[j] += sm[j][i];
+  if (threadIdx.x == 0) {
+    ggamma[f] = tot[0];
+    gbeta[f] = tot[1];
+  }
+  const float dvar = tot[2], dmean = tot[3];
+  f32x4* dxc = reinterpret_cast<f32x4*>(dX + N * f);
+#pragma unroll
+  for (int i = 0; i < V4; ++i) {
+    const int64_t q = threadIdx.x + (int64_t)T * i;
+    if (q < n4) {
+      f32x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        o[e] = dy[i][e] * g * inv_std + dvar * 2.0f * xm[i][e] * inv_batch + dmean * inv_batch;
+      dxc[q] = o;
+    }
+  }
+}
+
+// GELU over n elements; vec: all pointers 16-byte aligned, so the first
+// n/4*4 elements move as float4s (per-element math unchanged).
 __global__ void __launch_bounds__(256) gelu_fwd_kernel(const float* __restrict__ x,
-                                                       float* __restrict__ y, int64_t n) {
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-       i += (int64_t)gridDim.x * blockDim.x)
-    y[i] = gelu_f(x[i]);
+                                                       float* __restrict__ y, int64_t n, int vec) {
+  const int64_t t0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  int64_t done = 0;
+  if (vec) {
+    const int64_t n4 = n >> 2;
+    for (int64_t i = t0; i < n4; i += stride) {
+      const f32x4 v = reinterpret_cast<const f32x4*>(x)[i];
+      f32x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = gelu_f(v[e]);
+      reinterpret_cast<f32x4*>(y)[i] = o;
+    }
+    done = n4 << 2;
+  }
+  for (int64_t i = done + t0; i < n; i += stride) y[i] = gelu_f(x[i]);
 }
 __global__ void __launch_bounds__(256) gelu_bwd_kernel(const float* __restrict__ x,
                                                        const float* __restrict__ dy,
-                                                       float* __restrict__ dx, int64_t n) {
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-       i += (int64_t)gridDim.x * blockDim.x)
-    dx[i] = dy[i] * gelu_grad_f(x[i]);
+                                                       float* __restrict__ dx, int64_t n, int vec) {
+  const int64_t t0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  int64_t done = 0;
+  if (vec) {
+    const int64_t n4 = n >> 2;
+    for (int64_t i = t0; i < n4; i += stride) {
+      const f32x4 v = reinterpret_cast<const f32x4*>(x)[i];
+      const f32x4 g = reinterpret_cast<const f32x4*>(dy)[i];
+      f32x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = g[e] * gelu_grad_f(v[e]);
+      reinterpret_cast<f32x4*>(dx)[i] = o;
+    }
+    done = n4 << 2;
+  }
+  for (int64_t i = done + t0; i < n; i += stride) dx[i] = dy[i] * gelu_grad_f(x[i]);
 }
 
 // mean over s of [B,S,D].  For one feature d the [B, S] slab is contiguous
@@ -681,9 +1001,7 @@ int cnhip_mha_backward(const float* q, const float* k, const float* v, const flo
   CNHIP_TRY(cnhip::gemm_f32_batched(0, 0, S, D, S, 1.f, At, S, SS, gcs, S, SD, 0.f, gPs + 2 * SD, S,
                                     ps, B, nullptr, 0, st, who));
   // softmax Jacobian rows, times scale (541-551)
-  hipLaunchKernelGGL(cnhip::softmax_rows_bwd_kernel, dim3((unsigned)((BS + 3) / 4)), dim3(256), 0,
-                     st, At, gAT, gST, BS, S, scale);
-  CNHIP_TRY(cnhip::check_launch(who));
+  CNHIP_TRY(cnhip::softmax_rows_bwd(At, gAT, gST, BS, S, scale, st, who));
   // grad_Qp_b = gS_b Kp_b ; grad_Kp_b = gS_b^T Qp_b (553-554)
   CNHIP_TRY(cnhip::gemm_f32_batched(1, 0, S, D, S, 1.f, gST, S, SS, Ps + SD, S, ps, 0.f, gPs, S, ps,
                                     B, nullptr, 0, st, who));
@@ -723,6 +1041,9 @@ int cnhip_embedding_forward(const int32_t* ids, const float* Wt, float* out, int
   CNHIP_REQUIRE(ids && Wt && out, "%s: NULL pointer", who);
   const int64_t BS = B * S;
   CNHIP_REQUIRE((D + cnhip::TT - 1) / cnhip::TT <= 65535, "%s: embed_dim too large", who);
+  // ids read, one table row read and one output row written per token
+  cnhip::HbmTimer timer("embedding_fwd_kernel", 4.0 * (double)BS + 8.0 * (double)BS * (double)D,
+                        as_stream(stream));
   hipLaunchKernelGGL(cnhip::embedding_fwd_kernel,
                      dim3((unsigned)((BS + cnhip::TT - 1) / cnhip::TT), (unsigned)((D + cnhip::TT - 1) / cnhip::TT)),
                      dim3(256), 0, as_stream(stream), ids, Wt, out, BS, V, D, oob_count);
@@ -757,6 +1078,8 @@ int cnhip_embedding_backward(const int32_t* ids, const float* dY, float* gWt, in
   hipLaunchKernelGGL(cnhip::emb_sort_kernel, dim3(cnhip::elementwise_grid(V, 256)), dim3(256), 0, st,
                      offsets, pos, V);
   CNHIP_TRY(cnhip::check_launch(who));
+  // every token's gradient row read once, every table row written
+  cnhip::HbmTimer timer("emb_sum_kernel", 4.0 * (double)BS * (double)D + 4.0 * (double)V * (double)D, st);
   hipLaunchKernelGGL(cnhip::emb_sum_kernel, dim3((unsigned)V), dim3(128), 0, st, offsets, pos, dYt,
                      gWt, B, S, D);
   return cnhip::check_launch(who);
@@ -770,7 +1093,22 @@ int cnhip_batchnorm_forward(const float* x, float* y, float* xhat, const float* 
   CNHIP_REQUIRE(N > 0 && F > 0, "%s: bad shape", who);
   CNHIP_REQUIRE(x && y && xhat && gamma && beta && running_mean && running_var && batch_mean && batch_var,
                 "%s: NULL pointer", who);
-  if (N <= (int64_t)cnhip::BNT * 32)  // whole column in registers
+  // x read once; y and xhat written
+  cnhip::HbmTimer timer("bn_fwd_kernel", 12.0 * (double)N * (double)F, as_stream(stream));
+  const bool vec = N % 4 == 0 && cnhip::aligned16(x) && cnhip::aligned16(y) && cnhip::aligned16(xhat);
+  if (vec && N <= 4 * 256)
+    hipLaunchKernelGGL((cnhip::bn_fwd_vec_kernel<256, 1>), dim3((unsigned)F), dim3(256), 0, as_stream(stream),
+                       x, y, xhat, gamma, beta, running_mean, running_var, batch_mean, batch_var, N,
+                       momentum, eps);
+  else if (vec && N <= 4 * 1024 * 2)
+    hipLaunchKernelGGL((cnhip::bn_fwd_vec_kernel<1024, 2>), dim3((unsigned)F), dim3(1024), 0,
+                       as_stream(stream), x, y, xhat, gamma, beta, running_mean, running_var, batch_mean,
+                       batch_var, N, momentum, eps);
+  else if (vec && N <= 4 * 1024 * 8)
+    hipLaunchKernelGGL((cnhip::bn_fwd_vec_kernel<1024, 8>), dim3((unsigned)F), dim3(1024), 0,
+                       as_stream(stream), x, y, xhat, gamma, beta, running_mean, running_var, batch_mean,
+                       batch_var, N, momentum, eps);
+  else if (N <= (int64_t)cnhip::BNT * 32)  // whole column in registers
     hipLaunchKernelGGL(cnhip::bn_fwd_reg_kernel<32>, dim3((unsigned)F), dim3(cnhip::BNT), 0,
                        as_stream(stream), x, y, xhat, gamma, beta, running_mean, running_var,
                        batch_mean, batch_var, N, momentum, eps);
@@ -788,6 +1126,7 @@ int cnhip_batchnorm_forward_eval(const float* x, float* y, float* xhat, const fl
   const char* who = "cnhip_batchnorm_forward_eval";
   CNHIP_REQUIRE(N > 0 && F > 0, "%s: bad shape", who);
   CNHIP_REQUIRE(x && y && xhat && gamma && beta && running_mean && running_var, "%s: NULL pointer", who);
+  cnhip::HbmTimer timer("bn_eval_kernel", 12.0 * (double)N * (double)F, as_stream(stream));
   hipLaunchKernelGGL(cnhip::bn_eval_kernel, dim3(cnhip::elementwise_grid(N * F, 256)), dim3(256), 0,
                      as_stream(stream), x, y, xhat, gamma, beta, running_mean, running_var, N, F, eps);
   return cnhip::check_launch(who);
@@ -801,7 +1140,22 @@ int cnhip_batchnorm_backward(const float* dY, const float* x, const float* xhat,
   CNHIP_REQUIRE(N > 0 && F > 0, "%s: bad shape", who);
   CNHIP_REQUIRE(dY && x && xhat && gamma && batch_mean && batch_var && grad_gamma && grad_beta && dX,
                 "%s: NULL pointer", who);
-  if (N <= (int64_t)cnhip::BNT * 32)
+  // dY, x and xhat read once; dX written
+  cnhip::HbmTimer timer("bn_bwd_kernel", 16.0 * (double)N * (double)F, as_stream(stream));
+  const bool vec = N % 4 == 0 && cnhip::aligned16(dY) && cnhip::aligned16(x) && cnhip::aligned16(xhat) &&
+                   cnhip::aligned16(dX);
+  if (vec && N <= 4 * 256)
+    hipLaunchKernelGGL((cnhip::bn_bwd_vec_kernel<256, 1>), dim3((unsigned)F), dim3(256), 0, as_stream(stream),
+                       dY, x, xhat, gamma, batch_mean, batch_var, grad_gamma, grad_beta, dX, N, eps);
+  else if (vec && N <= 4 * 1024 * 2)
+    hipLaunchKernelGGL((cnhip::bn_bwd_vec_kernel<1024, 2>), dim3((unsigned)F), dim3(1024), 0,
+                       as_stream(stream), dY, x, xhat, gamma, batch_mean, batch_var, grad_gamma, grad_beta,
+                       dX, N, eps);
+  else if (vec && N <= 4 * 1024 * 8)
+    hipLaunchKernelGGL((cnhip::bn_bwd_vec_kernel<1024, 8>), dim3((unsigned)F), dim3(1024), 0,
+                       as_stream(stream), dY, x, xhat, gamma, batch_mean, batch_var, grad_gamma, grad_beta,
+                       dX, N, eps);
+  else if (N <= (int64_t)cnhip::BNT * 32)
     hipLaunchKernelGGL(cnhip::bn_bwd_reg_kernel<32>, dim3((unsigned)F), dim3(cnhip::BNT), 0,
                        as_stream(stream), dY, x, xhat, gamma, batch_mean, batch_var, grad_gamma,
                        grad_beta, dX, N, eps);
@@ -817,8 +1171,10 @@ int cnhip_gelu_forward(const float* x, float* y, int64_t n, cnhip_stream_t s) {
   CNHIP_REQUIRE(n >= 0, "%s: negative size", who);
   if (n == 0) return CNHIP_OK;
   CNHIP_REQUIRE(x && y, "%s: NULL pointer", who);
-  hipLaunchKernelGGL(cnhip::gelu_fwd_kernel, dim3(cnhip::elementwise_grid(n, 256)), dim3(256), 0,
-                     as_stream(s), x, y, n);
+  cnhip::HbmTimer timer("gelu_fwd_kernel", 8.0 * (double)n, as_stream(s));
+  const int vec = cnhip::aligned16(x) && cnhip::aligned16(y);
+  hipLaunchKernelGGL(cnhip::gelu_fwd_kernel, dim3(cnhip::elementwise_grid(vec ? (n + 3) / 4 : n, 256)),
+                     dim3(256), 0, as_stream(s), x, y, n, vec);
   return cnhip::check_launch(who);
 }
 
@@ -827,8 +1183,10 @@ int cnhip_gelu_backward(const float* x, const float* dy, float* dx, int64_t n, c
   CNHIP_REQUIRE(n >= 0, "%s: negative size", who);
   if (n == 0) return CNHIP_OK;
   CNHIP_REQUIRE(x && dy && dx, "%s: NULL pointer", who);
-  hipLaunchKernelGGL(cnhip::gelu_bwd_kernel, dim3(cnhip::elementwise_grid(n, 256)), dim3(256), 0,
-                     as_stream(s), x, dy, dx, n);
+  cnhip::HbmTimer timer("gelu_bwd_kernel", 12.0 * (double)n, as_stream(s));
+  const int vec = cnhip::aligned16(x) && cnhip::aligned16(dy) && cnhip::aligned16(dx);
+  hipLaunchKernelGGL(cnhip::gelu_bwd_kernel, dim3(cnhip::elementwise_grid(vec ? (n + 3) / 4 : n, 256)),
+                     dim3(256), 0, as_stream(s), x, dy, dx, n, vec);
   return cnhip::check_launch(who);
 }
 
@@ -839,6 +1197,7 @@ int cnhip_meanpool1d_forward(const float* x, float* y, int64_t B, int64_t S, int
   CNHIP_REQUIRE(x && y, "%s: NULL pointer", who);
   CNHIP_REQUIRE(D <= 0x7fffffff, "%s: D too large", who);
   const int bw = B < 64 ? (int)B : 64;
+  cnhip::HbmTimer timer("meanpool_fwd_kernel", 4.0 * (double)B * (double)D * (double)(S + 1), as_stream(s));
   hipLaunchKernelGGL(cnhip::meanpool_fwd_kernel, dim3((unsigned)D, (unsigned)((B + bw - 1) / bw)),
                      dim3(256), 0, as_stream(s), x, y, B, S, D, bw);
   return cnhip::check_launch(who);
@@ -849,6 +1208,7 @@ int cnhip_meanpool1d_backward(const float* dy, float* dx, int64_t B, int64_t S, 
   const char* who = "cnhip_meanpool1d_backward";
   CNHIP_REQUIRE(B > 0 && S > 0 && D > 0, "%s: bad shape", who);
   CNHIP_REQUIRE(dy && dx, "%s: NULL pointer", who);
+  cnhip::HbmTimer timer("meanpool_bwd_kernel", 4.0 * (double)B * (double)D * (double)(S + 1), as_stream(s));
   hipLaunchKernelGGL(cnhip::meanpool_bwd_kernel, dim3(cnhip::elementwise_grid(B * S * D, 256)),
                      dim3(256), 0, as_stream(s), dy, dx, B, S, D, 1.0f / (float)S);
   return cnhip::check_launch(who);
@@ -860,6 +1220,7 @@ int cnhip_add(const float* a, const float* b, float* y, int64_t n, cnhip_stream_
   if (n == 0) return CNHIP_OK;
   CNHIP_REQUIRE(a && b && y, "%s: NULL pointer", who);
   const int vec = (n % 4 == 0) && cnhip::aligned16(a) && cnhip::aligned16(b) && cnhip::aligned16(y);
+  cnhip::HbmTimer timer("add_kernel", 12.0 * (double)n, as_stream(s));
   hipLaunchKernelGGL(cnhip::add_kernel, dim3(cnhip::elementwise_grid(vec ? n / 4 : n, 256)), dim3(256),
                      0, as_stream(s), a, b, y, n, vec);
   return cnhip::check_launch(who);

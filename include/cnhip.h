@@ -126,6 +126,23 @@ int cnhip_gemm_f32_batched(int trans_a, int trans_b, int64_t M, int64_t N, int64
  * reduction launches are not counted.  Not a reference function. */
 int cnhip_gemm_timing_enable(int on);
 int cnhip_gemm_timing_read(int64_t* launches, double* total_ms, double* total_flops);
+/* Per-launch timing of the bandwidth-bound kernels (elementwise, reductions,
+ * pooling, normalisation, transposes, Adam, split-K reduces): while on, each
+ * such launch is bracketed by events on its stream and credited with its
+ * algorithmic HBM bytes (each input read once, each output written once).
+ * read() aggregates per kernel name, in first-seen order, into rows[0 ..
+ * max_rows) and sets *n_rows to the number of kernels seen (which may exceed
+ * max_rows); it synchronises on the recorded events.  No counterpart in the
+ * reference: this is the measurement the BASELINE metric asks of
+ * bandwidth-bound kernels. */
+typedef struct {
+  const char* kernel;   /* kernel name (static string of the library) */
+  int64_t launches;
+  double total_ms;      /* sum of the launches' event-timed durations */
+  double total_bytes;   /* sum of their algorithmic HBM bytes */
+} cnhip_kernel_timing;
+int cnhip_hbm_timing_enable(int on);
+int cnhip_hbm_timing_read(cnhip_kernel_timing* rows, int max_rows, int* n_rows);
 
 /* ---- Linear ------------------------------------------------------------ */
 /* Y[B,O] = X[B,I] * W[I,O] + b[O]   (b may be NULL)

@@ -91,7 +91,8 @@ def test_conv2d_vs_oracle(gpu, oracle, N, C, H, W, OC, KS, S, P, bias):
 
 POOL_CASES = [(2, 3, 8, 8, 2, 2), (3, 2, 5, 5, 3, 1), (1, 4, 7, 9, 2, 3), (4, 2, 6, 6, 3, 2),
               (7, 3, 4, 4, 2, -1), (256, 32, 32, 32, 2, 2), (256, 64, 16, 16, 2, 2),
-              (300, 3, 6, 6, 2, 2), (70, 5, 7, 7, 3, 2), (5, 2, 7, 7, 2, 2)]
+              (300, 3, 6, 6, 2, 2), (70, 5, 7, 7, 3, 2), (5, 2, 7, 7, 2, 2), (8, 3, 9, 9, 3, 3),
+              (12, 2, 7, 7, 2, 2)]
 
 
 @pytest.mark.parametrize("N,C,H,W,p,s", POOL_CASES)

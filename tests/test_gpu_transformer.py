@@ -37,7 +37,8 @@ def from_cm(flat, shape):
     return np.asarray(flat).reshape(tuple(reversed(shape))).transpose(*reversed(range(len(shape))))
 
 
-@pytest.mark.parametrize("R,C", [(1, 1), (63, 65), (64, 64), (130, 7), (4096, 33), (32, 131072)])
+@pytest.mark.parametrize("R,C", [(1, 1), (63, 65), (64, 64), (130, 7), (4096, 33), (32, 131072), (16, 1024),
+                                 (128, 32), (8192, 512), (36, 100), (20, 12), (12, 20)])
 def test_transpose_exact(gpu, R, C):
     print(f"[transpose] {R}x{C}", flush=True)
     a = np.random.default_rng(R * C).standard_normal(R * C).astype(np.float32)
@@ -186,7 +187,7 @@ def test_embedding_out_of_range_ids_counted(gpu):
 
 
 # ---------------------------------------------------------------- BatchNorm
-@pytest.mark.parametrize("N,F", [(64, 6), (1000, 3), (8192, 512), (9000, 5)])
+@pytest.mark.parametrize("N,F", [(64, 6), (1000, 3), (8192, 512), (9000, 5), (1001, 3), (40000, 2)])
 def test_batchnorm_vs_oracle(gpu, oracle, N, F):
     print(f"[batchnorm] N={N} F={F}", flush=True)
     rng = np.random.default_rng(N + F)
@@ -242,6 +243,13 @@ def test_gelu_vs_oracle(gpu, oracle):
     for got, want, name in [(host(y), ry, "y"), (host(dx), rdx, "dx")]:
         ok, msg = close(got, want, 1e-5, 1e-7)
         assert ok, f"{name}: {msg}"
+    # pointers off 16-byte alignment take the scalar path: same values
+    xd, dyd = dev(x), dev(dy)
+    y1, dx1 = torch.empty(x.size, device="cuda"), torch.empty(x.size, device="cuda")
+    ops.gelu_forward(xd[1:], y1[1:])
+    ops.gelu_backward(xd[1:], dyd[1:], dx1[1:])
+    np.testing.assert_array_equal(host(y1)[1:], host(y)[1:])
+    np.testing.assert_array_equal(host(dx1)[1:], host(dx)[1:])
 
 
 @pytest.mark.parametrize("B,S,D", [(3, 7, 5), (32, 256, 512), (1, 1, 1), (100, 33, 6), (7, 1000, 3)])
