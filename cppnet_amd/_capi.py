@@ -71,6 +71,8 @@ SIGNATURES: dict[str, tuple] = {
     "cnhip_mha_cache_floats": (i64, [i64, i64, i64]),
     "cnhip_mha_forward": (i32, [vp] * 9 + [i64] * 4 + [vp]),
     "cnhip_mha_backward": (i32, [vp] * 14 + [i64] * 4 + [vp]),
+    "cnhip_mha_forward_residual": (i32, [vp] * 10 + [i64] * 4 + [vp]),
+    "cnhip_mha_backward_residual": (i32, [vp] * 15 + [i64] * 4 + [vp]),
     "cnhip_embedding_forward": (i32, [vp, vp, vp, i64, i64, i64, i64, vp, vp]),
     "cnhip_embedding_backward": (i32, [vp, vp, vp, i64, i64, i64, i64, vp]),
     "cnhip_batchnorm_forward": (i32, [vp] * 9 + [i64, i64, f32, f32, vp]),

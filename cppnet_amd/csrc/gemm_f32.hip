@@ -62,6 +62,7 @@ struct GemmArgs {
   int64_t ld_aux;
   int vec_ok;            // every ld and stride % 4 == 0 and A, B 16-byte aligned
   int c_vec_ok;          // ldc, stride_c % 4 == 0 and C 16-byte aligned
+  int aux_vec_ok;        // ld_aux % 4 == 0 and aux_in 16-byte aligned
   int64_t k_per_split;   // multiple of KQ (hence of every tile's BK)
   float* partial;        // split-K workspace [batch][splits][M*N]; null = direct
   int splits;
@@ -71,8 +72,9 @@ struct GemmArgs {
 //   EPI_GELU : C = gelu(v), aux_out = v (the pre-activation GELU's backward reads)
 //   EPI_DRELU: C = v * [aux_in > 0]      (ReLU backward on the layer below)
 //   EPI_DGELU: C = v * gelu'(aux_in)     (GELU backward on the layer below)
+//   EPI_ADD  : C = v + aux_in            (a residual branch added to the output)
 // where v = alpha * acc (+ beta * C) (+ bias[n]).
-constexpr int EPI_GELU = 2, EPI_DRELU = 3, EPI_DGELU = 4;
+constexpr int EPI_GELU = 2, EPI_DRELU = 3, EPI_DGELU = 4, EPI_ADD = 5;
 
 // FUSED: the kernel instantiation that also handles the fused-activation
 // codes; the plain one (the bulk of all launches) keeps its epilogue small so
@@ -91,6 +93,7 @@ __device__ __forceinline__ float epilogue_value(const GemmArgs& g, const float* 
       return gelu_f(v);
     case EPI_DRELU: return v * relu_mask(g.aux_in[m + g.ld_aux * n]);
     case EPI_DGELU: return v * gelu_grad_f(g.aux_in[m + g.ld_aux * n]);
+    case EPI_ADD: return v + g.aux_in[m + g.ld_aux * n];
     default: return v;
   }
 }
@@ -158,6 +161,62 @@ __device__ __forceinline__ void gemm_mainloop(const GemmArgs& g, const float* __
   kp::pipeline<C>(ntiles, lds, s, acc);
 }
 
+// Epilogue of an interior tile (every row and column in range) whose
+// fused epilogue reads aux_in (DRELU, DGELU, ADD), with C and aux_in
+// float4-aligned.  Per 32 x 32 accumulator block, the four aux float4s are
+// loaded before the block's results are stored, and the next block's loads
+// are issued before this block's stores: through __restrict__ pointers, so
+// the loads may be scheduled ahead of stores to C (with possibly aliasing
+// pointers every load waited for the previous store, and the epilogue paid
+// the memory latency once per float4).
+template <class C>
+__device__ __forceinline__ void epilogue_aux_pipelined(const GemmArgs& g, float* __restrict__ Cp,
+                                                       const float* __restrict__ aux,
+                                                       const f32x16 (&acc)[C::WM][C::WN], int64_t m0,
+                                                       int64_t n0) {
+  const int lane = threadIdx.x & 63;
+  int wm, wn, wk;
+  kp::wave_pos<C>(wm, wn, wk);
+  if (C::WGK > 1 && wk != 0) return;
+  constexpr int NB = C::WM * C::WN;
+  auto col = [&](int b) { return n0 + wn * (C::WN * 32) + (b % C::WN) * 32 + (lane & 31); };
+  auto row = [&](int b, int q) { return m0 + wm * (C::WM * 32) + (b / C::WN) * 32 + 8 * q + 4 * (lane >> 5); };
+  f32x4 cur[4], nxt[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) cur[q] = *reinterpret_cast<const f32x4*>(aux + row(0, q) + g.ld_aux * col(0));
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    if (b + 1 < NB) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        nxt[q] = *reinterpret_cast<const f32x4*>(aux + row(b + 1, q) + g.ld_aux * col(b + 1));
+    }
+    const int64_t n = col(b);
+    const float bias = g.bias ? g.bias[n] : 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int64_t m = row(b, q);
+      float* cp = Cp + m + g.ldc * n;
+      f32x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float v = g.alpha * acc[b / C::WN][b % C::WN][4 * q + e];
+        if (g.beta != 0.f) v += g.beta * cp[e];
+        if (g.bias) v += bias;
+        const float a = cur[q][e];
+        o[e] = g.epilogue == EPI_DRELU   ? v * relu_mask(a)
+               : g.epilogue == EPI_DGELU ? v * gelu_grad_f(a)
+                                         : v + a;
+      }
+      *reinterpret_cast<f32x4*>(cp) = o;
+    }
+    if (b + 1 < NB) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) cur[q] = nxt[q];
+    }
+  }
+}
+
 template <bool TA, bool TB, class C, bool FUSED>
 __global__ void __launch_bounds__(C::NT, min_blocks<C>()) gemm_f32_kernel(GemmArgs g) {
   constexpr int BM = C::BM, BN = C::BN;
@@ -183,6 +242,13 @@ __global__ void __launch_bounds__(C::NT, min_blocks<C>()) gemm_f32_kernel(GemmAr
   else gemm_mainloop<false, TA, TB, C>(g, A, B, m0, n0, k_begin, k_end, lds, acc);
 
   float* Cp = g.C + batch * g.stride_c;
+  if constexpr (FUSED) {
+    if ((g.epilogue == EPI_DRELU || g.epilogue == EPI_DGELU || g.epilogue == EPI_ADD) && full_mn &&
+        g.c_vec_ok && g.aux_vec_ok && !g.partial) {
+      epilogue_aux_pipelined<C>(g, Cp, g.aux_in, acc, m0, n0);
+      return;
+    }
+  }
   float* P = g.partial ? g.partial + (batch * g.splits + blockIdx.z) * g.M * g.N : nullptr;
   const bool p_vec = (g.M & 3) == 0;
   kp::for_each_acc_run<C>(acc, [&](int ml, int nl, const f32x4& v) {
@@ -226,6 +292,35 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs g, int64_t 
     const int64_t m = e % g.M, n = e / g.M;
     float* C = g.C + bt * g.stride_c;
     C[m + g.ldc * n] = epilogue_value<true>(g, C, s, m, n);
+  }
+}
+
+// splitk_reduce_kernel for M % 4 == 0 and fewer than 2^31 outputs: float4
+// partial loads (four consecutive m share n), 32-bit index arithmetic; the
+// same split-order sums and epilogue per element.
+__global__ void __launch_bounds__(256) splitk_reduce_vec_kernel(GemmArgs g, int batches) {
+  const uint32_t M = (uint32_t)g.M, mn4 = (uint32_t)(g.M * g.N) >> 2;
+  const uint32_t total4 = mn4 * (uint32_t)batches;
+  const int64_t mn = g.M * g.N;
+  for (uint32_t q = blockIdx.x * blockDim.x + threadIdx.x; q < total4; q += gridDim.x * blockDim.x) {
+    const uint32_t bt = batches == 1 ? 0u : q / mn4;
+    const uint32_t e = (q - bt * mn4) << 2;
+    const f32x4* P = reinterpret_cast<const f32x4*>(g.partial + (int64_t)bt * g.splits * mn + e);
+    const int64_t zs = mn >> 2;
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+    for (int z = 0; z < g.splits; ++z) s += P[z * zs];
+    const uint32_t n = e / M, m = e - n * M;
+    float* C = g.C + (int64_t)bt * g.stride_c;
+    f32x4 o;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) o[k] = epilogue_value<true>(g, C, s[k], m + k, n);
+    if (g.c_vec_ok) {
+      *reinterpret_cast<f32x4*>(C + m + g.ldc * n) = o;
+    } else {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) C[(m + k) + g.ldc * n] = o[k];
+    }
   }
 }
 
@@ -443,7 +538,7 @@ int launch_plan(Shape shape, int trans_a, int trans_b, const GemmArgs& g, int64_
 
 // Single GEMM with a fused-activation epilogue (see epilogue_value):
 // aux is [M,N] with leading dimension ld_aux (an output for EPI_GELU, an
-// input for EPI_DRELU / EPI_DGELU).
+// input for EPI_DRELU / EPI_DGELU / EPI_ADD).
 int gemm_f32_act(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, const float* A,
                  int64_t lda, const float* B, int64_t ldb, float* C, int64_t ldc, const float* bias,
                  int epilogue, const float* aux_in, float* aux_out, int64_t ld_aux, hipStream_t st,
@@ -499,6 +594,7 @@ int gemm_f32_core(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, flo
   g.vec_ok = (lda % 4 == 0) && (ldb % 4 == 0) && (stride_a % 4 == 0) && (stride_b % 4 == 0) &&
              aligned16(A) && aligned16(B);
   g.c_vec_ok = (ldc % 4 == 0) && (stride_c % 4 == 0) && aligned16(C);
+  g.aux_vec_ok = (ld_aux % 4 == 0) && aux_in && aligned16(aux_in) && batches == 1;
   g.partial = nullptr;
 
   g.k_per_split = plan.kps;
@@ -518,8 +614,12 @@ int gemm_f32_core(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, flo
       // reads the partials (and C when beta != 0), writes C
       const double mn = (double)M * (double)N * (double)batches;
       HbmTimer timer("splitk_reduce_kernel", 4.0 * mn * (splits + 1 + (beta != 0.f ? 1 : 0)), st);
-      hipLaunchKernelGGL(splitk_reduce_kernel, dim3(elementwise_grid(M * N * batches, 256)),
-                         dim3(256), 0, st, g, batches);
+      if (M % 4 == 0 && M * N * batches < ((int64_t)1 << 31))
+        hipLaunchKernelGGL(splitk_reduce_vec_kernel, dim3(elementwise_grid(M * N * batches / 4, 256)),
+                           dim3(256), 0, st, g, (int)batches);
+      else
+        hipLaunchKernelGGL(splitk_reduce_kernel, dim3(elementwise_grid(M * N * batches, 256)),
+                           dim3(256), 0, st, g, batches);
       status = check_launch(who);
     }
   }
@@ -537,7 +637,7 @@ int gemm_f32_act(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, cons
                  int64_t lda, const float* B, int64_t ldb, float* C, int64_t ldc, const float* bias,
                  int epilogue, const float* aux_in, float* aux_out, int64_t ld_aux, hipStream_t st,
                  const char* who) {
-  const bool needs_in = epilogue == EPI_DRELU || epilogue == EPI_DGELU;
+  const bool needs_in = epilogue == EPI_DRELU || epilogue == EPI_DGELU || epilogue == EPI_ADD;
   CNHIP_REQUIRE(trans_a == 0 || epilogue < EPI_GELU, "%s: fused activations need trans_a == 0", who);
   CNHIP_REQUIRE(epilogue == CNHIP_EPI_NONE || epilogue == CNHIP_EPI_RELU || epilogue == EPI_GELU ||
                     needs_in,

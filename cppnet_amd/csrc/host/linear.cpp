@@ -72,6 +72,24 @@ namespace CppNet
             return out;
         }
 
+        DeviceTensor Linear::forward_residual(const DeviceTensor& input, const DeviceTensor& residual)
+        {
+            if (input.rank() != 2 || input.dimension(1) != in_size_)
+                throw std::runtime_error("Shape mismatch: in layer: " + layer_name_ +
+                                         " input.dimension(1) must be equal weights_.dimension(0)!");
+            const int64_t B = input.dimension(0);
+            if (residual.size() != B * out_size_)
+                throw std::runtime_error("Linear::forward_residual: residual does not match the output in layer: " +
+                                         layer_name_);
+            in_cache_ = input;
+            DeviceTensor out = DeviceTensor::empty({B, out_size_});
+            Device::check(cnhip_linear_forward_act(input.data(), W_.data(), bias_flag_ ? b_.data() : nullptr,
+                                                   out.data(), const_cast<float*>(residual.data()), B, in_size_,
+                                                   out_size_, CNHIP_ACT_RESIDUAL, Device::stream()),
+                          "Linear::forward_residual");
+            return out;
+        }
+
         DeviceTensor Linear::backward_act(const DeviceTensor& grad_output, int act, const DeviceTensor& act_aux)
         {
             if (grad_output.rank() != 2 || grad_output.dimension(1) != out_size_)

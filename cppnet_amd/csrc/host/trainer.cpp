@@ -16,13 +16,6 @@ using namespace CppNet;
 
 namespace
 {
-    DeviceTensor add_t(const DeviceTensor& a, const DeviceTensor& b, const char* who)
-    {
-        DeviceTensor y = DeviceTensor::empty(a.dims());
-        Device::check(cnhip_add(a.data(), b.data(), y.data(), a.size(), Device::stream()), who);
-        return y;
-    }
-
     /**
      * Config-5 encoder block, composed by the harness as the reference's
      * harness composes its layers (no encoder class exists in the reference):
@@ -37,25 +30,32 @@ namespace
         std::shared_ptr<Activations::GELU> gelu;
         std::vector<int64_t> dims;
 
+        // The four skip sums run in the epilogues of the GEMMs that produce
+        // their other operand (MHA's output projection and input gradient,
+        // the second FFN Linear's output, the first FFN Linear's input
+        // gradient): the same additions as separate adds, one pass fewer each.
         DeviceTensor forward(const DeviceTensor& x)
         {
             dims = x.dims();
             const int64_t BS = dims[0] * dims[1], D = dims[2];
-            DeviceTensor r = add_t(mha->forward(x, x, x), x, "encoder residual 1");
+            DeviceTensor r = mha->forward_residual(x, x, x, x);
             DeviceTensor h = bn->forward(r.reshape({BS, D}));
-            // GELU runs as its own pass: fused into the GEMM epilogue it measured
-            // slower on MI355X (the erfc work serialises after the MFMA loop)
-            DeviceTensor f = ff2->forward(gelu->forward(ff1->forward(h)));
-            return add_t(f, h, "encoder residual 2").reshape(dims);
+            // GELU runs as its own pass in the forward (fused into the first
+            // FFN GEMM's epilogue it measured slower: the erfc work serialises
+            // after the MFMA loop); its derivative is fused into the second
+            // FFN GEMM's input gradient
+            DeviceTensor f = ff2->forward_residual(gelu->forward(ff1->forward(h)), h);
+            return f.reshape(dims);
         }
 
         DeviceTensor backward(const DeviceTensor& g)
         {
             const int64_t BS = dims[0] * dims[1], D = dims[2];
             DeviceTensor g2 = g.reshape({BS, D});
-            DeviceTensor gh = add_t(ff1->backward(gelu->backward(ff2->backward(g2))), g2, "encoder grad 2");
+            DeviceTensor gz = ff2->backward_act(g2, CNHIP_ACT_GELU, gelu->input_cache());
+            DeviceTensor gh = ff1->backward_act(gz, CNHIP_ACT_RESIDUAL, g2);
             DeviceTensor gr = bn->backward(gh).reshape(dims);
-            return add_t(mha->backward(gr), gr, "encoder grad 1");
+            return mha->backward_residual(gr, gr);
         }
 
         void step(Optimizers::Optimizer& opt, float lr)

@@ -181,16 +181,26 @@ namespace CppNet
 
         DeviceTensor MultiHeadAttention::forward(const DeviceTensor& q, const DeviceTensor& k, const DeviceTensor& v)
         {
+            return forward_residual(q, k, v, DeviceTensor());
+        }
+
+        DeviceTensor MultiHeadAttention::forward_residual(const DeviceTensor& q, const DeviceTensor& k,
+                                                          const DeviceTensor& v, const DeviceTensor& residual)
+        {
             for (const DeviceTensor* t : {&q, &k, &v})
                 if (t->rank() != 3 || t->dimension(2) != embed_dim_ || t->dims() != q.dims())
                     throw std::runtime_error("MultiHeadAttention::forward: expected query/key/value [B, S, " +
                                              std::to_string(embed_dim_) + "] of one shape");
+            if (residual.defined() && residual.size() != q.size())
+                throw std::runtime_error("MultiHeadAttention::forward_residual: residual shape " +
+                                         shape_str(residual.dims()));
             const int64_t B = q.dimension(0), S = q.dimension(1), D = embed_dim_;
             cache_ = DeviceTensor::empty({cnhip_mha_cache_floats(B, S, D)});
             DeviceTensor out = DeviceTensor::empty({B, S, D});
-            Device::check(cnhip_mha_forward(q.data(), k.data(), v.data(), W_[0].data(), W_[1].data(),
-                                            W_[2].data(), W_[3].data(), out.data(), cache_.data(), B, S, D,
-                                            num_heads_, Device::stream()),
+            Device::check(cnhip_mha_forward_residual(q.data(), k.data(), v.data(), W_[0].data(), W_[1].data(),
+                                                     W_[2].data(), W_[3].data(),
+                                                     residual.defined() ? residual.data() : nullptr, out.data(),
+                                                     cache_.data(), B, S, D, num_heads_, Device::stream()),
                           "MultiHeadAttention::forward");
             q_cache_ = q;
             k_cache_ = k;
@@ -198,17 +208,23 @@ namespace CppNet
             return out;
         }
 
-        DeviceTensor MultiHeadAttention::backward(const DeviceTensor& g)
+        DeviceTensor MultiHeadAttention::backward(const DeviceTensor& g) { return backward_residual(g, DeviceTensor()); }
+
+        DeviceTensor MultiHeadAttention::backward_residual(const DeviceTensor& g, const DeviceTensor& skip_grad)
         {
             if (!cache_.defined()) throw std::runtime_error("MultiHeadAttention::backward before forward");
             if (g.dims() != q_cache_.dims())
                 throw std::runtime_error("MultiHeadAttention::backward: grad shape " + shape_str(g.dims()));
+            if (skip_grad.defined() && skip_grad.size() != g.size())
+                throw std::runtime_error("MultiHeadAttention::backward_residual: skip gradient shape " +
+                                         shape_str(skip_grad.dims()));
             const int64_t B = g.dimension(0), S = g.dimension(1), D = embed_dim_;
             DeviceTensor dx = DeviceTensor::empty({B, S, D});
-            Device::check(cnhip_mha_backward(q_cache_.data(), k_cache_.data(), v_cache_.data(), W_[0].data(),
-                                             W_[1].data(), W_[2].data(), W_[3].data(), cache_.data(), g.data(),
-                                             gW_[0].data(), gW_[1].data(), gW_[2].data(), gW_[3].data(),
-                                             dx.data(), B, S, D, num_heads_, Device::stream()),
+            Device::check(cnhip_mha_backward_residual(
+                              q_cache_.data(), k_cache_.data(), v_cache_.data(), W_[0].data(), W_[1].data(),
+                              W_[2].data(), W_[3].data(), cache_.data(), g.data(),
+                              skip_grad.defined() ? skip_grad.data() : nullptr, gW_[0].data(), gW_[1].data(),
+                              gW_[2].data(), gW_[3].data(), dx.data(), B, S, D, num_heads_, Device::stream()),
                           "MultiHeadAttention::backward");
             grads_zero_ = false;
             return dx;

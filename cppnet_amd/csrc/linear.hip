@@ -18,7 +18,7 @@ int gemm_f32_act(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, cons
                  int epilogue, const float* aux_in, float* aux_out, int64_t ld_aux, hipStream_t st,
                  const char* who);
 // fused-activation epilogue codes of gemm_f32_act
-constexpr int EPI_GELU = 2, EPI_DRELU = 3, EPI_DGELU = 4;
+constexpr int EPI_GELU = 2, EPI_DRELU = 3, EPI_DGELU = 4, EPI_ADD = 5;
 
 namespace {
 
@@ -125,13 +125,16 @@ int cnhip_linear_forward_act(const float* X, const float* W, const float* b, flo
                              cnhip_stream_t stream) {
   const char* who = "cnhip_linear_forward_act";
   CNHIP_REQUIRE(batch >= 0 && in_features > 0 && out_features > 0, "%s: bad shape", who);
-  CNHIP_REQUIRE(act >= CNHIP_ACT_NONE && act <= CNHIP_ACT_GELU, "%s: bad activation %d", who, act);
+  CNHIP_REQUIRE(act >= CNHIP_ACT_NONE && act <= CNHIP_ACT_RESIDUAL, "%s: bad activation %d", who, act);
   CNHIP_REQUIRE(act != CNHIP_ACT_GELU || Z, "%s: GELU needs Z for the pre-activation", who);
-  const int epi = act == CNHIP_ACT_RELU ? CNHIP_EPI_RELU : act == CNHIP_ACT_GELU ? cnhip::EPI_GELU
-                                                                                  : CNHIP_EPI_NONE;
+  CNHIP_REQUIRE(act != CNHIP_ACT_RESIDUAL || Z, "%s: the residual add needs Z (the residual input)", who);
+  const int epi = act == CNHIP_ACT_RELU       ? CNHIP_EPI_RELU
+                  : act == CNHIP_ACT_GELU     ? cnhip::EPI_GELU
+                  : act == CNHIP_ACT_RESIDUAL ? cnhip::EPI_ADD
+                                              : CNHIP_EPI_NONE;
   return cnhip::gemm_f32_act(0, 0, batch, out_features, in_features, X, batch, W, in_features, Y,
-                             batch, b, epi, nullptr, act == CNHIP_ACT_GELU ? Z : nullptr, batch,
-                             cnhip::as_stream(stream), who);
+                             batch, b, epi, act == CNHIP_ACT_RESIDUAL ? Z : nullptr,
+                             act == CNHIP_ACT_GELU ? Z : nullptr, batch, cnhip::as_stream(stream), who);
 }
 
 int cnhip_linear_backward_act(const float* X, const float* W, const float* dY, float* grad_W,
@@ -139,14 +142,17 @@ int cnhip_linear_backward_act(const float* X, const float* W, const float* dY, f
                               int64_t in_features, int64_t out_features, int trainable,
                               int accumulate, int act, cnhip_stream_t stream) {
   const char* who = "cnhip_linear_backward_act";
-  CNHIP_REQUIRE(act >= CNHIP_ACT_NONE && act <= CNHIP_ACT_GELU, "%s: bad activation %d", who, act);
+  CNHIP_REQUIRE(act >= CNHIP_ACT_NONE && act <= CNHIP_ACT_RESIDUAL, "%s: bad activation %d", who, act);
   CNHIP_REQUIRE(act == CNHIP_ACT_NONE || (dX && act_aux), "%s: activation %d needs dX and act_aux",
                 who, act);
   CNHIP_TRY(cnhip_linear_backward(X, W, dY, grad_W, grad_b, act == CNHIP_ACT_NONE ? dX : nullptr,
                                   batch, in_features, out_features, trainable, accumulate, stream));
   if (act == CNHIP_ACT_NONE || batch == 0) return CNHIP_OK;
-  // dX[B,I] = (dY W^T) * act'(act_aux), the activation's backward in the epilogue
-  const int epi = act == CNHIP_ACT_RELU ? cnhip::EPI_DRELU : cnhip::EPI_DGELU;
+  // dX[B,I] = (dY W^T) * act'(act_aux), the activation's backward in the
+  // epilogue; for the residual, dX = dY W^T + act_aux (the skip branch's gradient)
+  const int epi = act == CNHIP_ACT_RELU   ? cnhip::EPI_DRELU
+                  : act == CNHIP_ACT_GELU ? cnhip::EPI_DGELU
+                                          : cnhip::EPI_ADD;
   return cnhip::gemm_f32_act(0, 1, batch, in_features, out_features, dY, batch, W, in_features, dX,
                              batch, nullptr, epi, act_aux, nullptr, batch, cnhip::as_stream(stream),
                              who);

@@ -33,6 +33,16 @@ int gemm_f32_batched(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, 
                      int64_t stride_b, float beta, float* C, int64_t ldc, int64_t stride_c,
                      int64_t batches, const float* bias, int epilogue, hipStream_t st,
                      const char* who);
+int gemm_f32_act(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, const float* A,
+                 int64_t lda, const float* B, int64_t ldb, float* C, int64_t ldc, const float* bias,
+                 int epilogue, const float* aux_in, float* aux_out, int64_t ld_aux, hipStream_t st,
+                 const char* who);
+int gemm_f32_core(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float alpha,
+                  const float* A, int64_t lda, int64_t stride_a, const float* B, int64_t ldb,
+                  int64_t stride_b, float beta, float* C, int64_t ldc, int64_t stride_c,
+                  int64_t batches, const float* bias, int epilogue, const float* aux_in,
+                  float* aux_out, int64_t ld_aux, hipStream_t st, const char* who);
+constexpr int EPI_ADD = 5;  // GEMM epilogue C = v + aux_in (gemm_f32.hip)
 
 namespace {
 
@@ -919,10 +929,11 @@ int64_t cnhip_mha_cache_floats(int64_t B, int64_t S, int64_t D) {
   return 4 * B * S * D + B * S * S;
 }
 
-int cnhip_mha_forward(const float* q, const float* k, const float* v, const float* Wq,
-                      const float* Wk, const float* Wv, const float* Wo, float* out, float* cache,
-                      int64_t B, int64_t S, int64_t D, int64_t heads, cnhip_stream_t stream) {
-  const char* who = "cnhip_mha_forward";
+int cnhip_mha_forward_residual(const float* q, const float* k, const float* v, const float* Wq,
+                               const float* Wk, const float* Wv, const float* Wo, const float* residual,
+                               float* out, float* cache, int64_t B, int64_t S, int64_t D, int64_t heads,
+                               cnhip_stream_t stream) {
+  const char* who = residual ? "cnhip_mha_forward_residual" : "cnhip_mha_forward";
   CNHIP_REQUIRE(B > 0 && S > 0 && D > 0 && heads > 0 && D % heads == 0,
                 "%s: bad shape B=%lld S=%lld D=%lld heads=%lld (D %% heads must be 0)", who,
                 (long long)B, (long long)S, (long long)D, (long long)heads);
@@ -963,15 +974,26 @@ int cnhip_mha_forward(const float* q, const float* k, const float* v, const floa
   CNHIP_TRY(cnhip::gemm_f32_batched(1, 0, S, D, S, 1.f, At, S, SS, Vb, S, ps, 0.f, proj, S, SD, B,
                                     nullptr, 0, st, who));
   CNHIP_TRY(cnhip::transpose(proj, ctx, SD, B, st, who));
-  // out = context W_o (212)
+  // out = context W_o (212), plus the skip branch when fused
+  if (residual)
+    return cnhip::gemm_f32_act(0, 0, BS, D, D, ctx, BS, Wo, D, out, BS, nullptr, cnhip::EPI_ADD, residual,
+                               nullptr, BS, st, who);
   return cnhip::gemm_f32(0, 0, BS, D, D, 1.f, ctx, BS, Wo, D, 0.f, out, BS, nullptr, 0, st, who);
 }
 
-int cnhip_mha_backward(const float* q, const float* k, const float* v, const float* Wq,
-                       const float* Wk, const float* Wv, const float* Wo, const float* cache,
-                       const float* dY, float* gWq, float* gWk, float* gWv, float* gWo, float* dX,
-                       int64_t B, int64_t S, int64_t D, int64_t heads, cnhip_stream_t stream) {
-  const char* who = "cnhip_mha_backward";
+int cnhip_mha_forward(const float* q, const float* k, const float* v, const float* Wq,
+                      const float* Wk, const float* Wv, const float* Wo, float* out, float* cache,
+                      int64_t B, int64_t S, int64_t D, int64_t heads, cnhip_stream_t stream) {
+  return cnhip_mha_forward_residual(q, k, v, Wq, Wk, Wv, Wo, nullptr, out, cache, B, S, D, heads, stream);
+}
+
+int cnhip_mha_backward_residual(const float* q, const float* k, const float* v, const float* Wq,
+                                const float* Wk, const float* Wv, const float* Wo, const float* cache,
+                                const float* dY, const float* residual_grad, float* gWq, float* gWk,
+                                float* gWv, float* gWo, float* dX, int64_t B, int64_t S, int64_t D,
+                                int64_t heads, cnhip_stream_t stream) {
+  const char* who = residual_grad ? "cnhip_mha_backward_residual" : "cnhip_mha_backward";
+  CNHIP_REQUIRE(!residual_grad || dX, "%s: the residual gradient needs dX", who);
   CNHIP_REQUIRE(B > 0 && S > 0 && D > 0 && heads > 0 && D % heads == 0, "%s: bad shape", who);
   CNHIP_REQUIRE(q && k && v && Wq && Wk && Wv && Wo && cache && dY && gWq && gWk && gWv && gWo,
                 "%s: NULL pointer", who);
@@ -1017,7 +1039,10 @@ int cnhip_mha_backward(const float* q, const float* k, const float* v, const flo
   if (packed) {
     // [gW_q gW_k gW_v] = X^T [gQp gKp gVp]; grad_input = [gQp gKp gVp] [Wq Wk Wv]^T
     CNHIP_TRY(cnhip::gemm_f32(1, 0, D, 3 * D, BS, 1.f, q, BS, G, BS, 0.f, gWq, D, nullptr, 0, st, who));
-    if (dX)
+    if (dX && residual_grad)
+      CNHIP_TRY(cnhip::gemm_f32_act(0, 1, BS, D, 3 * D, G, BS, Wq, D, dX, BS, nullptr, cnhip::EPI_ADD,
+                                    residual_grad, nullptr, BS, st, who));
+    else if (dX)
       CNHIP_TRY(cnhip::gemm_f32(0, 1, BS, D, 3 * D, 1.f, G, BS, Wq, D, 0.f, dX, BS, nullptr, 0, st, who));
     return CNHIP_OK;
   }
@@ -1029,9 +1054,19 @@ int cnhip_mha_backward(const float* q, const float* k, const float* v, const flo
   if (dX) {
     CNHIP_TRY(cnhip::gemm_f32(0, 1, BS, D, D, 1.f, gQp, BS, Wq, D, 0.f, dX, BS, nullptr, 0, st, who));
     CNHIP_TRY(cnhip::gemm_f32(0, 1, BS, D, D, 1.f, gKp, BS, Wk, D, 1.f, dX, BS, nullptr, 0, st, who));
-    CNHIP_TRY(cnhip::gemm_f32(0, 1, BS, D, D, 1.f, gVp, BS, Wv, D, 1.f, dX, BS, nullptr, 0, st, who));
+    // the last term adds the skip branch's gradient after dQ + dK + dV
+    CNHIP_TRY(cnhip::gemm_f32_core(0, 1, BS, D, D, 1.f, gVp, BS, 0, Wv, D, 0, 1.f, dX, BS, 0, 1, nullptr,
+                                   residual_grad ? cnhip::EPI_ADD : 0, residual_grad, nullptr, BS, st, who));
   }
   return CNHIP_OK;
+}
+
+int cnhip_mha_backward(const float* q, const float* k, const float* v, const float* Wq,
+                       const float* Wk, const float* Wv, const float* Wo, const float* cache,
+                       const float* dY, float* gWq, float* gWk, float* gWv, float* gWo, float* dX,
+                       int64_t B, int64_t S, int64_t D, int64_t heads, cnhip_stream_t stream) {
+  return cnhip_mha_backward_residual(q, k, v, Wq, Wk, Wv, Wo, cache, dY, nullptr, gWq, gWk, gWv, gWo, dX,
+                                     B, S, D, heads, stream);
 }
 
 int cnhip_embedding_forward(const int32_t* ids, const float* Wt, float* out, int64_t B, int64_t S,

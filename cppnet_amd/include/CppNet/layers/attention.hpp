@@ -38,6 +38,12 @@ namespace CppNet
             DeviceTensor forward(const DeviceTensor& query, const DeviceTensor& key,
                                  const DeviceTensor& value);
             DeviceTensor backward(const DeviceTensor& grad_output);
+            /// forward(x, x, x) + residual and its backward with the skip
+            /// branch's gradient added into dX, each fused into the last GEMM
+            /// (equal to the separate call and add).
+            DeviceTensor forward_residual(const DeviceTensor& query, const DeviceTensor& key,
+                                          const DeviceTensor& value, const DeviceTensor& residual);
+            DeviceTensor backward_residual(const DeviceTensor& grad_output, const DeviceTensor& skip_grad);
 
             bool is_trainable() const override { return trainable_; }
             void step(Optimizers::Optimizer& optimizer, float learning_rate) override;

@@ -51,6 +51,11 @@ namespace CppNet
             /// backward().
             DeviceTensor backward_act(const DeviceTensor& grad_output, int act,
                                       const DeviceTensor& act_aux);
+            /// forward(input) + residual (a skip connection, [B, out]) in the
+            /// GEMM epilogue; equals forward() followed by the add.  The
+            /// matching backward is backward_act(g, CNHIP_ACT_RESIDUAL,
+            /// skip_grad): dX = dY W^T + skip_grad.
+            DeviceTensor forward_residual(const DeviceTensor& input, const DeviceTensor& residual);
 
             bool is_trainable() const override { return trainable_; }
             void step(Optimizers::Optimizer& optimizer, float learning_rate) override;

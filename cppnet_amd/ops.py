@@ -67,7 +67,7 @@ def linear_backward(X, W, dY, grad_W, grad_b, dX, batch: int, in_features: int,
                out_features, int(trainable), int(accumulate), _stream())
 
 
-ACT = {"none": 0, "relu": 1, "gelu": 2}
+ACT = {"none": 0, "relu": 1, "gelu": 2, "residual": 3}
 
 
 def linear_forward_act(X, W, b, Y, Z, batch: int, in_features: int, out_features: int,
@@ -167,6 +167,19 @@ def mha_backward(q, k, v, Wq, Wk, Wv, Wo, cache, dY, gWq, gWk, gWv, gWo, dX, B, 
     _capi.call("cnhip_mha_backward", *(_p(t) for t in (q, k, v, Wq, Wk, Wv, Wo, cache, dY, gWq,
                                                        gWk, gWv, gWo, dX)), B, S, D, heads,
                _stream())
+
+
+def mha_forward_residual(q, k, v, Wq, Wk, Wv, Wo, residual, out, cache, B, S, D, heads) -> None:
+    _capi.call("cnhip_mha_forward_residual",
+               *(_p(t) for t in (q, k, v, Wq, Wk, Wv, Wo, residual, out, cache)), B, S, D, heads,
+               _stream())
+
+
+def mha_backward_residual(q, k, v, Wq, Wk, Wv, Wo, cache, dY, skip_grad, gWq, gWk, gWv, gWo, dX,
+                          B, S, D, heads) -> None:
+    _capi.call("cnhip_mha_backward_residual",
+               *(_p(t) for t in (q, k, v, Wq, Wk, Wv, Wo, cache, dY, skip_grad, gWq, gWk, gWv, gWo,
+                                 dX)), B, S, D, heads, _stream())
 
 
 def embedding_forward(ids, Wt, out, B, S, V, D, oob=None) -> None:

@@ -169,13 +169,18 @@ int cnhip_linear_backward(const float* X, const float* W, const float* dY,
  * activation on the layer BELOW (the one that produced this layer's input):
  *   dX = (dY W^T) * [act_aux > 0]   (RELU: act_aux = that ReLU's output)
  *   dX = (dY W^T) * gelu'(act_aux)  (GELU: act_aux = that GELU's input Z)
+ * CNHIP_ACT_RESIDUAL fuses a skip connection instead of an activation:
+ *   forward  Y = (X W + b) + Z          (Z read: the skip branch, [B,O])
+ *   backward dX = dY W^T + act_aux      (act_aux: the skip branch's gradient, [B,I])
  * Weight/bias grads as cnhip_linear_backward.  Results equal the unfused
- * layer + activation calls (same arithmetic per element).
+ * layer + activation (or add) calls: same arithmetic per element.
  * ref: Linear::forward/backward (linear.cpp:148-358) chained with
- * ReLU::forward/backward (relu.cpp:97-225); GELU has no reference. */
+ * ReLU::forward/backward (relu.cpp:97-225), or with the residual sum of
+ * Residual::forward/backward (residual.cpp:44-159); GELU has no reference. */
 #define CNHIP_ACT_NONE 0
 #define CNHIP_ACT_RELU 1
 #define CNHIP_ACT_GELU 2
+#define CNHIP_ACT_RESIDUAL 3
 int cnhip_linear_forward_act(const float* X, const float* W, const float* b, float* Y,
                              float* Z, int64_t batch, int64_t in_features,
                              int64_t out_features, int act, cnhip_stream_t stream);
@@ -290,6 +295,22 @@ int cnhip_mha_backward(const float* q, const float* k, const float* v, const flo
                        const float* dY, float* gWq, float* gWk, float* gWv, float* gWo,
                        float* dX, int64_t B, int64_t S, int64_t D, int64_t heads,
                        cnhip_stream_t stream);
+/* The same with a skip connection fused into the last GEMM of each pass:
+ * forward out = MHA(q, k, v) + residual; backward dX = dQ + dK + dV +
+ * residual_grad (dX required).  Equal to the unfused call followed by
+ * cnhip_add.  ref: MultiHeadAttention::forward/backward (attention.cpp:60-221,
+ * 503-569) followed by a skip sum F(x) + x as Residual::forward/backward
+ * computes it (residual.cpp:44-159). */
+int cnhip_mha_forward_residual(const float* q, const float* k, const float* v, const float* Wq,
+                               const float* Wk, const float* Wv, const float* Wo,
+                               const float* residual, float* out, float* cache, int64_t B,
+                               int64_t S, int64_t D, int64_t heads, cnhip_stream_t stream);
+int cnhip_mha_backward_residual(const float* q, const float* k, const float* v, const float* Wq,
+                                const float* Wk, const float* Wv, const float* Wo,
+                                const float* cache, const float* dY, const float* residual_grad,
+                                float* gWq, float* gWk, float* gWv, float* gWo, float* dX,
+                                int64_t B, int64_t S, int64_t D, int64_t heads,
+                                cnhip_stream_t stream);
 /* Embedding: weights kept token-major, Wt[d + D*v] (the transpose of the
  * reference's ColMajor [V, D]); ids [B,S] int32; out [B,S,D].  Ids outside
  * [0, V) give zero rows and are counted into *oob_count (may be NULL; the

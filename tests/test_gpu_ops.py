@@ -348,3 +348,31 @@ def test_linear_fused_activation_matches_unfused(gpu, oracle, act, B, I, O):
     mag = gemm_mag(oracle, 0, 0, B, O, I, X, B, W, I, B)
     ok, msg = close_mag(host(Y), ry, mag, 1e-4, 1e-5)
     assert ok, msg
+
+
+@pytest.mark.parametrize("B,I,O", [(64, 48, 40), (8192, 2048, 512), (37, 130, 19), (512, 4096, 64)])
+def test_linear_fused_residual_matches_unfused(gpu, B, I, O):
+    """Y = X W + b + R and dX = dY W^T + G in the GEMM epilogue equal the
+    separate Linear call and cnhip_add bit for bit (also through the split-K
+    reduce, which the (512, 4096, 64) backward's K = 64 / forward K = 4096
+    shapes take)."""
+    print(f"[linear-residual] B={B} I={I} O={O}", flush=True)
+    rng = np.random.default_rng(B * 3 + I + O)
+    X, W, b = dev(rnd(rng, B * I)), dev(rnd(rng, I * O, 1 / np.sqrt(I))), dev(rnd(rng, O, 0.1))
+    R = dev(rnd(rng, B * O))
+    Y = torch.empty(B * O, device="cuda")
+    ops.linear_forward_act(X, W, b, Y, R, B, I, O, "residual")
+    Yl, Yu = torch.empty(B * O, device="cuda"), torch.empty(B * O, device="cuda")
+    ops.linear_forward(X, W, b, Yl, B, I, O)
+    ops.add(Yl, R, Yu)
+    np.testing.assert_array_equal(host(Y), host(Yu))
+    dY, G = dev(rnd(rng, B * O)), dev(rnd(rng, B * I))
+    gW, gb, dX = torch.empty(I * O, device="cuda"), torch.empty(O, device="cuda"), torch.empty(B * I, device="cuda")
+    ops.linear_backward_act(X, W, dY, gW, gb, dX, G, B, I, O, "residual")
+    gWu, gbu, dXl, dXu = (torch.empty(I * O, device="cuda"), torch.empty(O, device="cuda"),
+                          torch.empty(B * I, device="cuda"), torch.empty(B * I, device="cuda"))
+    ops.linear_backward(X, W, dY, gWu, gbu, dXl, B, I, O, True, False)
+    ops.add(dXl, G, dXu)
+    np.testing.assert_array_equal(host(dX), host(dXu))
+    np.testing.assert_array_equal(host(gW), host(gWu))
+    np.testing.assert_array_equal(host(gb), host(gbu))

@@ -136,6 +136,25 @@ def test_mha_vs_oracle(gpu, oracle, B, S, D, h, self_attn):
     for got, want, mag, name in checks:
         ok, msg = close_mag(got, want, mag, 1e-4, 1e-5)
         assert ok, f"{name}: {msg}"
+    # skip connections fused into the last GEMMs: equal to the separate adds
+    out_r = torch.empty(B * S * D, device="cuda")
+    cache_r = torch.empty_like(cache)
+    ops.mha_forward_residual(*xd, *Wd, xd[0], out_r, cache_r, B, S, D, h)
+    want_r = torch.empty(B * S * D, device="cuda")
+    ops.add(out, xd[0], want_r)
+    np.testing.assert_array_equal(host(out_r), host(want_r))
+    skip = dev(cm(dy * 3))
+    dX_r = torch.empty(B * S * D, device="cuda")
+    gW_r = [torch.empty(D * D, device="cuda") for _ in range(4)]
+    if self_attn:
+        gall_r = torch.empty(4 * D * D, device="cuda")
+        gW_r = [gall_r[i * D * D:(i + 1) * D * D] for i in range(4)]
+    ops.mha_backward_residual(*xd, *Wd, cache_r, dev(cm(dy)), skip, *gW_r, dX_r, B, S, D, h)
+    want_dx = torch.empty(B * S * D, device="cuda")
+    ops.add(dX, skip, want_dx)
+    np.testing.assert_array_equal(host(dX_r), host(want_dx))
+    for a, b_ in zip(gW_r, gW):
+        np.testing.assert_array_equal(host(a), host(b_))
 
 
 def test_mha_rejects_bad_heads(gpu):
