@@ -161,19 +161,22 @@ __device__ __forceinline__ void gemm_mainloop(const GemmArgs& g, const float* __
   kp::pipeline<C>(ntiles, lds, s, acc);
 }
 
-// Epilogue of an interior tile (every row and column in range) whose
-// fused epilogue reads aux_in (DRELU, DGELU, ADD), with C and aux_in
-// float4-aligned.  Per 32 x 32 accumulator block, the four aux float4s are
-// loaded before the block's results are stored, and the next block's loads
-// are issued before this block's stores: through __restrict__ pointers, so
-// the loads may be scheduled ahead of stores to C (with possibly aliasing
-// pointers every load waited for the previous store, and the epilogue paid
-// the memory latency once per float4).
-template <class C>
-__device__ __forceinline__ void epilogue_aux_pipelined(const GemmArgs& g, float* __restrict__ Cp,
-                                                       const float* __restrict__ aux,
-                                                       const f32x16 (&acc)[C::WM][C::WN], int64_t m0,
-                                                       int64_t n0) {
+// Epilogue of an interior tile (every row and column in range, C float4-
+// aligned, beta == 0, no split-K).  AUX: the fused epilogue reads aux_in
+// (DRELU, DGELU, ADD; aux_in float4-aligned), else it is NONE or RELU.
+// The pointers are __restrict__ so loads may be scheduled ahead of stores
+// to C: the bias of every column the thread owns is loaded first, and per
+// 32 x 32 accumulator block the four aux float4s are loaded before the
+// block's results are stored, the next block's before this block's stores.
+// (Through possibly aliasing pointers every load waited for the previous
+// store, and the epilogue paid the memory latency once per float4.)  The
+// arithmetic per element is epilogue_value's.
+template <class C, bool AUX>
+__device__ __forceinline__ void epilogue_interior(const GemmArgs& g, float* __restrict__ Cp,
+                                                  const float* __restrict__ aux,
+                                                  const float* __restrict__ bias,
+                                                  const f32x16 (&acc)[C::WM][C::WN], int64_t m0,
+                                                  int64_t n0) {
   const int lane = threadIdx.x & 63;
   int wm, wn, wk;
   kp::wave_pos<C>(wm, wn, wk);
@@ -181,38 +184,47 @@ __device__ __forceinline__ void epilogue_aux_pipelined(const GemmArgs& g, float*
   constexpr int NB = C::WM * C::WN;
   auto col = [&](int b) { return n0 + wn * (C::WN * 32) + (b % C::WN) * 32 + (lane & 31); };
   auto row = [&](int b, int q) { return m0 + wm * (C::WM * 32) + (b / C::WN) * 32 + 8 * q + 4 * (lane >> 5); };
-  f32x4 cur[4], nxt[4];
+  float bv[NB];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) cur[q] = *reinterpret_cast<const f32x4*>(aux + row(0, q) + g.ld_aux * col(0));
+  for (int b = 0; b < NB; ++b) bv[b] = bias ? bias[col(b)] : 0.f;
+  f32x4 cur[4], nxt[4];
+  if constexpr (AUX) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) cur[q] = *reinterpret_cast<const f32x4*>(aux + row(0, q) + g.ld_aux * col(0));
+  }
 #pragma unroll
   for (int b = 0; b < NB; ++b) {
-    if (b + 1 < NB) {
+    if constexpr (AUX) {
+      if (b + 1 < NB) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        nxt[q] = *reinterpret_cast<const f32x4*>(aux + row(b + 1, q) + g.ld_aux * col(b + 1));
+        for (int q = 0; q < 4; ++q)
+          nxt[q] = *reinterpret_cast<const f32x4*>(aux + row(b + 1, q) + g.ld_aux * col(b + 1));
+      }
     }
     const int64_t n = col(b);
-    const float bias = g.bias ? g.bias[n] : 0.f;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int64_t m = row(b, q);
-      float* cp = Cp + m + g.ldc * n;
       f32x4 o;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         float v = g.alpha * acc[b / C::WN][b % C::WN][4 * q + e];
-        if (g.beta != 0.f) v += g.beta * cp[e];
-        if (g.bias) v += bias;
-        const float a = cur[q][e];
-        o[e] = g.epilogue == EPI_DRELU   ? v * relu_mask(a)
-               : g.epilogue == EPI_DGELU ? v * gelu_grad_f(a)
-                                         : v + a;
+        if (bias) v += bv[b];
+        if constexpr (AUX) {
+          const float a = cur[q][e];
+          o[e] = g.epilogue == EPI_DRELU   ? v * relu_mask(a)
+                 : g.epilogue == EPI_DGELU ? v * gelu_grad_f(a)
+                                           : v + a;
+        } else {
+          o[e] = g.epilogue == CNHIP_EPI_RELU ? relu_f(v) : v;
+        }
       }
-      *reinterpret_cast<f32x4*>(cp) = o;
+      *reinterpret_cast<f32x4*>(Cp + row(b, q) + g.ldc * n) = o;
     }
-    if (b + 1 < NB) {
+    if constexpr (AUX) {
+      if (b + 1 < NB) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) cur[q] = nxt[q];
+        for (int q = 0; q < 4; ++q) cur[q] = nxt[q];
+      }
     }
   }
 }
@@ -242,10 +254,14 @@ __global__ void __launch_bounds__(C::NT, min_blocks<C>()) gemm_f32_kernel(GemmAr
   else gemm_mainloop<false, TA, TB, C>(g, A, B, m0, n0, k_begin, k_end, lds, acc);
 
   float* Cp = g.C + batch * g.stride_c;
-  if constexpr (FUSED) {
-    if ((g.epilogue == EPI_DRELU || g.epilogue == EPI_DGELU || g.epilogue == EPI_ADD) && full_mn &&
-        g.c_vec_ok && g.aux_vec_ok && !g.partial) {
-      epilogue_aux_pipelined<C>(g, Cp, g.aux_in, acc, m0, n0);
+  if (full_mn && g.c_vec_ok && !g.partial && g.beta == 0.f) {
+    if constexpr (FUSED) {
+      if ((g.epilogue == EPI_DRELU || g.epilogue == EPI_DGELU || g.epilogue == EPI_ADD) && g.aux_vec_ok) {
+        epilogue_interior<C, true>(g, Cp, g.aux_in, g.bias, acc, m0, n0);
+        return;
+      }
+    } else {
+      epilogue_interior<C, false>(g, Cp, nullptr, g.bias, acc, m0, n0);
       return;
     }
   }
