@@ -119,7 +119,7 @@ CPU_BATCH = {1: 512, 2: 512, 3: 32, 4: 16, 5: 4}
 # PMC runs (FETCH_SIZE, WRITE_SIZE) scaled by a reference kernel of known
 # traffic; the runs, factors and per-GEMM table are in
 # profiles/gemm_f32_config2_traffic.md.  Configs not yet measured report null.
-PMC_TRAFFIC_BYTES = {2: 337.7e6}
+PMC_TRAFFIC_BYTES = {2: 321.0e6}
 
 
 def cpu_baseline(config: int, seconds_budget: float = 20.0):
@@ -278,8 +278,10 @@ def main() -> int:
                             "achieved_GBs": round(gbs, 1),
                             "frac": round(gbs / PEAK_HBM_GBS, 4)})
 
-    kernels = ("gemm_f32_kernel + conv_fwd/dgrad/wgrad_kernel (fp32 MFMA, all shapes of the step)"
-               if args.config == 3 else "gemm_f32_kernel (fp32 MFMA GEMM, all shapes of the step)")
+    kernels = {3: "gemm_f32_kernel + conv_pixel/conv_wgrad_kernel (fp32 MFMA, all shapes of the step)",
+               4: "gemm_f32_kernel + lstm_step_fwd/bwd_kernel (fp32 MFMA; the per-timestep recurrent "
+                  "GEMM tiles with the cell update fused)"}.get(
+        args.config, "gemm_f32_kernel (fp32 MFMA GEMM, all shapes of the step)")
     result = {
         "metric": METRIC,
         "value": round(B / (step_ms * 1e-3), 1),
