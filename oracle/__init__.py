@@ -25,6 +25,27 @@ _SIGS = {
     "cnref_linear_backward": (None, [_f, _f, _f, _f, _f, _f, i64, i64, i64, i32, i32]),
     "cnref_column_sum": (None, [_f, _f, i64, i64, i32]),
     "cnref_relu_forward": (None, [_f, _f, i64]),
+    "cnref_leaky_relu_forward": (None, [_f, _f, i64, f32]),
+    "cnref_leaky_relu_backward": (None, [_f, _f, _f, i64, f32]),
+    "cnref_softmax_forward": (None, [_f, _f, i64, i64]),
+    "cnref_softmax_backward": (None, [_f, _f, _f, i64, i64]),
+    "cnref_cce_forward": (f32, [_f, _f, _f, _f, i64, i64, i32, f32, i32]),
+    "cnref_cce_backward": (None, [_f, _f, _f, i64, i64, i32, i32]),
+    "cnref_mae_forward": (f32, [_f, _f, i64, i32]),
+    "cnref_mae_backward": (None, [_f, _f, _f, i64, i32]),
+    "cnref_huber_forward": (f32, [_f, _f, i64, f32, i32]),
+    "cnref_huber_backward": (None, [_f, _f, _f, i64, f32, i32]),
+    "cnref_sgd_step": (None, [_f, _f, i64, f32]),
+    "cnref_momentum_step": (None, [_f, _f, _f, i64, f32, f32]),
+    "cnref_adagrad_step": (None, [_f, _f, _f, i64, f32, f32]),
+    "cnref_rmsprop_step": (None, [_f, _f, _f, i64, f32, f32, f32]),
+    "cnref_dropout_apply": (None, [_f, _f, _f, i64, f32]),
+    "cnref_global_avgpool_forward": (None, [_f, _f, i64, i64, i64, i64]),
+    "cnref_global_avgpool_backward": (None, [_f, _f, i64, i64, i64, i64]),
+    "cnref_global_maxpool_forward": (None, [_f, _f, _i, _i, i64, i64, i64, i64]),
+    "cnref_global_maxpool_backward": (None, [_f, _i, _i, _f, i64, i64, i64, i64]),
+    "cnref_rnn_forward": (None, [_f, _f, _f, _f, _f, i64, i64, i64, i64]),
+    "cnref_rnn_backward": (None, [_f] * 9 + [i64] * 4),
     "cnref_relu_backward": (None, [_f, _f, _f, i64]),
     "cnref_sigmoid_forward": (None, [_f, _f, i64]),
     "cnref_sigmoid_backward": (None, [_f, _f, _f, i64]),

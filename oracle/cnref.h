@@ -142,6 +142,37 @@ void cnref_adam_step(float* W, const float* g, float* m, float* v, int64_t n, fl
 /* bias correction exactly as the reference: 1 - pow(beta, float(t)) in float */
 float cnref_bias_correction(float beta, int t);
 
+/* ---- cnref_extra.cpp: the reference's device ops off the BASELINE configs ---- */
+void  cnref_leaky_relu_forward(const float* x, float* y, int64_t n, float alpha);
+void  cnref_leaky_relu_backward(const float* x, const float* dy, float* dx, int64_t n, float alpha);
+/* softmax over the last dimension: R rows, element (r, j) at r + R*j */
+void  cnref_softmax_forward(const float* x, float* y, int64_t R, int64_t L);
+void  cnref_softmax_backward(const float* y, const float* dy, float* dx, int64_t R, int64_t L);
+float cnref_cce_forward(const float* pred, const float* t, float* sm, float* targets_used, int64_t B,
+                        int64_t C, int from_logits, float label_smoothing, int reduction);
+void  cnref_cce_backward(const float* sm, const float* targets_used, float* g, int64_t B, int64_t C,
+                         int from_logits, int reduction);
+float cnref_mae_forward(const float* p, const float* t, int64_t n, int reduction);
+void  cnref_mae_backward(const float* p, const float* t, float* g, int64_t n, int reduction);
+float cnref_huber_forward(const float* p, const float* t, int64_t n, float delta, int reduction);
+void  cnref_huber_backward(const float* p, const float* t, float* g, int64_t n, float delta, int reduction);
+void  cnref_sgd_step(float* W, const float* g, int64_t n, float lr);
+void  cnref_momentum_step(float* W, const float* g, float* vel, int64_t n, float lr, float mu);
+void  cnref_adagrad_step(float* W, const float* g, float* acc, int64_t n, float lr, float eps);
+void  cnref_rmsprop_step(float* W, const float* g, float* s, int64_t n, float lr, float rho, float eps);
+void  cnref_dropout_apply(const float* x, const float* mask, float* y, int64_t n, float scale);
+void  cnref_global_avgpool_forward(const float* X, float* Y, int64_t N, int64_t C, int64_t H, int64_t W);
+void  cnref_global_avgpool_backward(const float* dY, float* dX, int64_t N, int64_t C, int64_t H, int64_t W);
+void  cnref_global_maxpool_forward(const float* X, float* Y, int32_t* ah, int32_t* aw, int64_t N,
+                                   int64_t C, int64_t H, int64_t W);
+void  cnref_global_maxpool_backward(const float* dY, const int32_t* ah, const int32_t* aw, float* dX,
+                                    int64_t N, int64_t C, int64_t H, int64_t W);
+void  cnref_rnn_forward(const float* X, const float* Wih, const float* Whh, const float* b, float* Y,
+                        int64_t B, int64_t S, int64_t I, int64_t H);
+void  cnref_rnn_backward(const float* X, const float* Wih, const float* Whh, const float* Y,
+                         const float* dY, float* gWih, float* gWhh, float* gb, float* dX, int64_t B,
+                         int64_t S, int64_t I, int64_t H);
+
 #ifdef __cplusplus
 }
 #endif

@@ -123,6 +123,52 @@ CASES = [
          exact=[w - 1e-3 * g / (abs(g) + 1e-8)
                 for w, g in zip([1.0, -2.0, 0.5, 3.0], [0.1, -0.3, 2.0, -1e-3])],
          derivation="t=1: m/bc1 = g and v/bc2 = g^2, so W1 = W0 - lr*g/(|g|+eps)", tol=1e-6),
+    # ---- LeakyReLU (leacky_relu.cpp) ------------------------------------------
+    dict(op="leaky_relu_forward", source="tests/activations/test_leacky_relu.cpp:47-58",
+         alpha=0.01, X=[[1.0, 2.0, 3.0], [4.0, 5.0, 6.0]], expected=[[1.0, 2.0, 3.0], [4.0, 5.0, 6.0]],
+         tol=1e-6),
+    dict(op="leaky_relu_forward", source="tests/activations/test_leacky_relu.cpp:61-72",
+         alpha=0.01, X=[[-1.0, -2.0, -0.5, -100.0]], expected=[[-0.01, -0.02, -0.005, -1.0]], tol=1e-5),
+    dict(op="leaky_relu_forward", source="tests/activations/test_leacky_relu.cpp:75-87",
+         alpha=0.1, X=[[-2.0, 3.0, -0.5, 1.0]], expected=[[-0.2, 3.0, -0.05, 1.0]], tol=1e-5),
+    dict(op="leaky_relu_forward", source="tests/activations/test_leacky_relu.cpp:91-102",
+         alpha=0.2, X=[[-5.0, 5.0]], expected=[[-1.0, 5.0]], tol=1e-5),
+    dict(op="leaky_relu_backward", source="tests/activations/test_leacky_relu.cpp:148-165",
+         alpha=0.1, X=[[-2.0, 3.0, -0.5, 1.0]], dY=[[2.0, 3.0, 4.0, 5.0]],
+         expected=[[0.2, 3.0, 0.4, 5.0]], tol=1e-5),
+    # ---- Softmax (softmax.cpp) ---------------------------------------------------
+    dict(op="softmax_forward", source="tests/activations/test_softmax.cpp:78-87",
+         X=[[1.0, 1.0, 1.0, 1.0, 1.0]], expected=[[0.2, 0.2, 0.2, 0.2, 0.2]], tol=1e-5),
+    dict(op="softmax_forward", source="tests/activations/test_softmax.cpp:106-114",
+         X=[[42.0]], expected=[[1.0]], tol=1e-5),
+    dict(op="softmax_forward", source="tests/activations/test_softmax.cpp:91-103",
+         X=[[1.0, 2.0, 5.0, 0.5]], expected=[softmax([1.0, 2.0, 5.0, 0.5])], tol=1e-5,
+         check="index 2 (value 5) is the largest"),
+    dict(op="softmax_backward_constant", source="tests/activations/test_softmax.cpp:151-167",
+         X=[[1.0, 2.0, 3.0, 4.0]], dY=[[1.0, 1.0, 1.0, 1.0]], expected=[[0.0, 0.0, 0.0, 0.0]], tol=1e-5,
+         derivation="a constant upstream gradient c gives y*(c - c*sum(y)) = 0"),
+    # ---- Losses -------------------------------------------------------------------
+    dict(op="mae_forward", source="tests/losses/test_mae.cpp:60-72",
+         P=[[0.0, 0.0, 0.0]], T=[[1.0, 2.0, 3.0]], expected=2.0, tol=1e-6,
+         derivation="(1 + 2 + 3) / 3 (the reference test's own tolerance is 0.1)"),
+    dict(op="huber_forward", source="tests/losses/test_huber.cpp:68-82",
+         delta=10.0, P=[[0.5]], T=[[0.0]], expected=0.125, tol=1e-6),
+    dict(op="huber_forward", source="tests/losses/test_huber.cpp:85-99",
+         delta=1.0, P=[[5.0]], T=[[0.0]], expected=4.5, tol=1e-6,
+         derivation="delta * (|5| - delta/2) (the reference test's own tolerance is 0.1)"),
+    # ---- Global pools (global_pool.cpp) --------------------------------------------
+    dict(op="global_avgpool_forward", source="tests/layers/test_global_pool.cpp:36-42",
+         X=[[[[1.0, 3.0], [5.0, 7.0]]]], expected=[[4.0]], tol=1e-5),
+    dict(op="global_avgpool_backward", source="tests/layers/test_global_pool.cpp:63-75",
+         shape=[1, 1, 2, 3], dY=[[6.0]], expected_all=1.0, tol=1e-5),
+    dict(op="global_maxpool_forward", source="tests/layers/test_global_pool.cpp:87-93",
+         X=[[[[1.0, 3.0], [5.0, 7.0]]]], expected=[[7.0]], tol=1e-5),
+    dict(op="global_maxpool_backward", source="tests/layers/test_global_pool.cpp:114-127",
+         X=[[[[1.0, 3.0], [5.0, 7.0]]]], dY=[[1.0]], expected=[[[[0.0, 0.0], [0.0, 1.0]]]], tol=1e-6),
+    # ---- Dropout (dropout.cpp) ----------------------------------------------------
+    dict(op="dropout_scale", source="tests/layers/test_dropout.cpp:51-62",
+         p=0.5, x=1.0, expected_kept=2.0, tol=1e-5,
+         derivation="kept entries are x * 1 * 1/(1-p)"),
 ]
 
 
