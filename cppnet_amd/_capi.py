@@ -99,6 +99,26 @@ SIGNATURES: dict[str, tuple] = {
     "cnhip_adam_step_multi": (i32, [i32, C.POINTER(vp), C.POINTER(vp), C.POINTER(vp),
                                     C.POINTER(vp), C.POINTER(i64), C.POINTER(f32),
                                     C.POINTER(f32), f32, f32, f32, f32, vp]),
+    "cnhip_optimizer_step_multi": (i32, [i32, i32, C.POINTER(vp), C.POINTER(vp), C.POINTER(vp),
+                                         C.POINTER(i64), f32, f32, f32, vp]),
+    "cnhip_leaky_relu_forward": (i32, [vp, vp, i64, f32, vp]),
+    "cnhip_leaky_relu_backward": (i32, [vp, vp, vp, i64, f32, vp]),
+    "cnhip_softmax_forward": (i32, [vp, vp, i64, i64, vp]),
+    "cnhip_softmax_backward": (i32, [vp, vp, vp, i64, i64, vp]),
+    "cnhip_cce_forward": (i32, [vp, vp, vp, vp, vp, i64, i64, i32, f32, i32, vp]),
+    "cnhip_cce_backward": (i32, [vp, vp, vp, i64, i64, i32, i32, vp]),
+    "cnhip_mae_forward": (i32, [vp, vp, vp, i64, i32, vp]),
+    "cnhip_mae_backward": (i32, [vp, vp, vp, i64, i32, vp]),
+    "cnhip_huber_forward": (i32, [vp, vp, vp, i64, f32, i32, vp]),
+    "cnhip_huber_backward": (i32, [vp, vp, vp, i64, f32, i32, vp]),
+    "cnhip_dropout_forward": (i32, [vp, vp, vp, i64, f32, C.c_uint64, C.c_uint64, vp]),
+    "cnhip_dropout_backward": (i32, [vp, vp, vp, i64, f32, vp]),
+    "cnhip_global_avgpool_forward": (i32, [vp, vp, i64, i64, i64, i64, vp]),
+    "cnhip_global_avgpool_backward": (i32, [vp, vp, i64, i64, i64, i64, vp]),
+    "cnhip_global_maxpool_forward": (i32, [vp, vp, vp, vp, i64, i64, i64, i64, vp]),
+    "cnhip_global_maxpool_backward": (i32, [vp, vp, vp, vp, i64, i64, i64, i64, vp]),
+    "cnhip_rnn_forward": (i32, [vp] * 5 + [i64] * 4 + [vp]),
+    "cnhip_rnn_backward": (i32, [vp] * 9 + [i64] * 4 + [vp]),
 }
 
 

@@ -73,8 +73,9 @@ struct GemmArgs {
 //   EPI_DRELU: C = v * [aux_in > 0]      (ReLU backward on the layer below)
 //   EPI_DGELU: C = v * gelu'(aux_in)     (GELU backward on the layer below)
 //   EPI_ADD  : C = v + aux_in            (a residual branch added to the output)
+//   EPI_TANH : C = tanh(v)               (the Elman RNN cell)
 // where v = alpha * acc (+ beta * C) (+ bias[n]).
-constexpr int EPI_GELU = 2, EPI_DRELU = 3, EPI_DGELU = 4, EPI_ADD = 5;
+constexpr int EPI_GELU = 2, EPI_DRELU = 3, EPI_DGELU = 4, EPI_ADD = 5, EPI_TANH = 6;
 
 // FUSED: the kernel instantiation that also handles the fused-activation
 // codes; the plain one (the bulk of all launches) keeps its epilogue small so
@@ -94,6 +95,7 @@ __device__ __forceinline__ float epilogue_value(const GemmArgs& g, const float* 
     case EPI_DRELU: return v * relu_mask(g.aux_in[m + g.ld_aux * n]);
     case EPI_DGELU: return v * gelu_grad_f(g.aux_in[m + g.ld_aux * n]);
     case EPI_ADD: return v + g.aux_in[m + g.ld_aux * n];
+    case EPI_TANH: return tanhf(v);
     default: return v;
   }
 }

@@ -33,6 +33,13 @@ int gemm_f32(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float al
              int64_t ldc, const float* bias, int epilogue, hipStream_t st, const char* who);
 int column_sum(const float* in, float* out, int64_t rows, int64_t cols, int accumulate,
                hipStream_t st, const char* who);
+int gemm_f32_core(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float alpha,
+                  const float* A, int64_t lda, int64_t stride_a, const float* B, int64_t ldb,
+                  int64_t stride_b, float beta, float* C, int64_t ldc, int64_t stride_c,
+                  int64_t batches, const float* bias, int epilogue, const float* aux_in,
+                  float* aux_out, int64_t ld_aux, hipStream_t st, const char* who);
+int fill_bytes(void* dst, int value, size_t bytes, hipStream_t stream, const char* where);
+constexpr int EPI_TANH = 6;  // GEMM epilogue C = tanh(v) (gemm_f32.hip)
 
 namespace {
 
@@ -371,6 +378,33 @@ __global__ void __launch_bounds__(256) seq_scatter_kernel(const float* __restric
 
 unsigned cell_grid(int64_t B, int64_t H) { return (unsigned)((B * H + 255) / 256); }
 
+// ---------------------------------------------------------------- Elman RNN
+// rnn.cpp:48-100: step 0 has no recurrent term (h_0 = 0): its rows of Y hold
+// x_0 W_ih and become tanh(x_0 W_ih + b).
+__global__ void __launch_bounds__(256) rnn_step0_kernel(float* __restrict__ Y, const float* __restrict__ b,
+                                                        int64_t B, int64_t BS, int64_t H) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= B * H) return;
+  const int64_t n = e % B, d = e / B;
+  float* y = Y + n + BS * d;
+  *y = tanhf(*y + b[d]);
+}
+// rnn.cpp:118-131: dtanh_t = (dY_t + dh_next) * (1 - h_t^2) into dT's rows of
+// step t (dh_next == nullptr at the last step: dh_next is zero there).
+__global__ void __launch_bounds__(256) rnn_bwd_cell_kernel(const float* __restrict__ dY,
+                                                           const float* __restrict__ Y,
+                                                           const float* __restrict__ dh_next,
+                                                           float* __restrict__ dT, int64_t B, int64_t BS,
+                                                           int64_t H, int64_t t) {
+#pragma clang fp contract(off)
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= B * H) return;
+  const int64_t n = e % B, d = e / B, i = n + B * t + BS * d;
+  const float dh = dh_next ? dY[i] + dh_next[n + B * d] : dY[i];
+  const float h = Y[i];
+  dT[i] = dh * (1.0f - h * h);
+}
+
 // Per-step launches of the fused LSTM kernels for steps t = 1 .. S-1
 // (forward) and t = S-2 .. 0 (backward), each timed like a GEMM (2*B*4H*H
 // flops) for the per-launch roofline.
@@ -580,6 +614,59 @@ int cnhip_seq_scatter(const float* in, float* Y, int64_t B, int64_t S, int64_t D
   hipLaunchKernelGGL(cnhip::seq_scatter_kernel, dim3(cnhip::elementwise_grid(B * S * D, 256)),
                      dim3(256), 0, as_stream(stream), in, Y, B, S, D, t);
   return cnhip::check_launch(who);
+}
+
+int cnhip_rnn_forward(const float* X, const float* W_ih, const float* W_hh, const float* b, float* Y,
+                      int64_t B, int64_t S, int64_t I, int64_t H, cnhip_stream_t stream) {
+  const char* who = "cnhip_rnn_forward";
+  CNHIP_REQUIRE(B > 0 && S > 0 && I > 0 && H > 0, "%s: bad shape B=%lld S=%lld I=%lld H=%lld", who,
+                (long long)B, (long long)S, (long long)I, (long long)H);
+  CNHIP_REQUIRE(X && W_ih && W_hh && b && Y, "%s: NULL pointer", who);
+  hipStream_t st = as_stream(stream);
+  const int64_t BS = B * S;
+  // x_t W_ih for every step at once (rnn.cpp:73-74), then the recurrence:
+  // step t's rows of Y = tanh(h_{t-1} W_hh + Y_t + b), the GEMM adding the
+  // x-projection (beta = 1) and the bias and applying tanh in its epilogue
+  CNHIP_TRY(cnhip::gemm_f32(0, 0, BS, H, I, 1.f, X, BS, W_ih, I, 0.f, Y, BS, nullptr, 0, st, who));
+  hipLaunchKernelGGL(cnhip::rnn_step0_kernel, dim3(cnhip::cell_grid(B, H)), dim3(256), 0, st, Y, b, B, BS, H);
+  CNHIP_TRY(cnhip::check_launch(who));
+  for (int64_t t = 1; t < S; ++t)
+    CNHIP_TRY(cnhip::gemm_f32_core(0, 0, B, H, H, 1.f, Y + B * (t - 1), BS, 0, W_hh, H, 0, 1.f, Y + B * t, BS,
+                                   0, 1, b, cnhip::EPI_TANH, nullptr, nullptr, 0, st, who));
+  return CNHIP_OK;
+}
+
+int cnhip_rnn_backward(const float* X, const float* W_ih, const float* W_hh, const float* Y, const float* dY,
+                       float* gW_ih, float* gW_hh, float* gb, float* dX, int64_t B, int64_t S, int64_t I,
+                       int64_t H, cnhip_stream_t stream) {
+  const char* who = "cnhip_rnn_backward";
+  CNHIP_REQUIRE(B > 0 && S > 0 && I > 0 && H > 0, "%s: bad shape", who);
+  CNHIP_REQUIRE(X && W_ih && W_hh && Y && dY && gW_ih && gW_hh && gb, "%s: NULL pointer", who);
+  hipStream_t st = as_stream(stream);
+  const int64_t BS = B * S;
+  cnhip::Workspace ws(st);
+  CNHIP_TRY(ws.alloc((size_t)(BS * H + B * H) * sizeof(float), who));
+  float* dT = static_cast<float*>(ws.p);  // dtanh of every step, [B*S, H]
+  float* dh = dT + BS * H;                // dh_next = dtanh_{t+1} W_hh^T, [B, H]
+  for (int64_t t = S - 1; t >= 0; --t) {
+    hipLaunchKernelGGL(cnhip::rnn_bwd_cell_kernel, dim3(cnhip::cell_grid(B, H)), dim3(256), 0, st, dY, Y,
+                       t == S - 1 ? nullptr : dh, dT, B, BS, H, t);
+    CNHIP_TRY(cnhip::check_launch(who));
+    if (t > 0)
+      CNHIP_TRY(cnhip::gemm_f32(0, 1, B, H, H, 1.f, dT + B * t, BS, W_hh, H, 0.f, dh, B, nullptr, 0, st, who));
+  }
+  // weight grads over all B*S rows (rnn.cpp:136-142): gW_ih = X^T dT,
+  // gW_hh = [h_0 .. h_{S-2}]^T dT[steps 1..S-1] (h_{-1} = 0 adds nothing),
+  // gb = colsum dT; dX = dT W_ih^T (rnn.cpp:145-149)
+  CNHIP_TRY(cnhip::gemm_f32(1, 0, I, H, BS, 1.f, X, BS, dT, BS, 0.f, gW_ih, I, nullptr, 0, st, who));
+  if (S > 1)
+    CNHIP_TRY(cnhip::gemm_f32(1, 0, H, H, B * (S - 1), 1.f, Y, BS, dT + B, BS, 0.f, gW_hh, H, nullptr, 0, st,
+                              who));
+  else
+    CNHIP_TRY(cnhip::fill_bytes(gW_hh, 0, (size_t)(H * H) * sizeof(float), st, who));
+  CNHIP_TRY(cnhip::column_sum(dT, gb, BS, H, 0, st, who));
+  if (dX) CNHIP_TRY(cnhip::gemm_f32(0, 1, BS, I, H, 1.f, dT, BS, W_ih, I, 0.f, dX, BS, nullptr, 0, st, who));
+  return CNHIP_OK;
 }
 
 }  // extern "C"

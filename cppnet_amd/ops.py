@@ -26,8 +26,8 @@ def _p(t: torch.Tensor | None, name: str = "tensor") -> int | None:
         return None
     if not isinstance(t, torch.Tensor) or not t.is_cuda:
         raise TypeError(f"{name}: expected a device tensor (the HIP path has no host fallback)")
-    if t.dtype not in (torch.float32, torch.int32):
-        raise TypeError(f"{name}: expected float32/int32, got {t.dtype}")
+    if t.dtype not in (torch.float32, torch.int32, torch.uint8):
+        raise TypeError(f"{name}: expected float32/int32/uint8, got {t.dtype}")
     if not t.is_contiguous():
         raise ValueError(f"{name}: expected a contiguous tensor")
     return t.data_ptr()
@@ -291,3 +291,96 @@ def adam_step_multi(params: list, lr: float, beta1: float, beta2: float, eps: fl
     bc2 = (C.c_float * n)(*[p[5] for p in params])
     _capi.call("cnhip_adam_step_multi", n, arr(0), arr(1), arr(2), arr(3), sizes, bc1, bc2, lr,
                beta1, beta2, eps, _stream())
+
+
+# ---------------------------------------------------------------- the reference's other device ops
+OPT = {"sgd": 0, "momentum": 1, "adagrad": 2, "rmsprop": 3}
+
+
+def optimizer_step_multi(kind: str, params: list, lr: float, hyper: float = 0.0, eps: float = 0.0) -> None:
+    """params: list of (W, g, state) device tensors (state None for SGD)."""
+    import ctypes as C
+    n = len(params)
+    arr = lambda idx: (C.c_void_p * n)(*[_p(p[idx]) if p[idx] is not None else None for p in params])
+    sizes = (C.c_int64 * n)(*[p[0].numel() for p in params])
+    _capi.call("cnhip_optimizer_step_multi", OPT[kind], n, arr(0), arr(1), arr(2), sizes, lr, hyper, eps,
+               _stream())
+
+
+def leaky_relu_forward(x, y, alpha: float) -> None:
+    _capi.call("cnhip_leaky_relu_forward", _p(x), _p(y), x.numel(), alpha, _stream())
+
+
+def leaky_relu_backward(x, dy, dx, alpha: float) -> None:
+    _capi.call("cnhip_leaky_relu_backward", _p(x), _p(dy), _p(dx), x.numel(), alpha, _stream())
+
+
+def softmax_forward(x, y, rows: int, length: int) -> None:
+    _capi.call("cnhip_softmax_forward", _p(x), _p(y), rows, length, _stream())
+
+
+def softmax_backward(y, dy, dx, rows: int, length: int) -> None:
+    _capi.call("cnhip_softmax_backward", _p(y), _p(dy), _p(dx), rows, length, _stream())
+
+
+def cce_forward(pred, t, probs, tu, loss, B: int, C: int, from_logits: bool, ls: float,
+                reduction: str = "mean") -> None:
+    _capi.call("cnhip_cce_forward", _p(pred), _p(t), _p(probs), _p(tu), _p(loss), B, C, int(from_logits),
+               ls, _red(reduction), _stream())
+
+
+def cce_backward(probs, tu, g, B: int, C: int, from_logits: bool, reduction: str = "mean") -> None:
+    _capi.call("cnhip_cce_backward", _p(probs), _p(tu), _p(g), B, C, int(from_logits), _red(reduction),
+               _stream())
+
+
+def mae_forward(p, t, loss, reduction: str = "mean") -> None:
+    _capi.call("cnhip_mae_forward", _p(p), _p(t), _p(loss), p.numel(), _red(reduction), _stream())
+
+
+def mae_backward(p, t, g, reduction: str = "mean") -> None:
+    _capi.call("cnhip_mae_backward", _p(p), _p(t), _p(g), p.numel(), _red(reduction), _stream())
+
+
+def huber_forward(p, t, loss, delta: float, reduction: str = "mean") -> None:
+    _capi.call("cnhip_huber_forward", _p(p), _p(t), _p(loss), p.numel(), delta, _red(reduction),
+               _stream())
+
+
+def huber_backward(p, t, g, delta: float, reduction: str = "mean") -> None:
+    _capi.call("cnhip_huber_backward", _p(p), _p(t), _p(g), p.numel(), delta, _red(reduction),
+               _stream())
+
+
+def dropout_forward(x, y, mask, p: float, seed: int, offset: int = 0) -> None:
+    _capi.call("cnhip_dropout_forward", _p(x), _p(y), _p(mask), x.numel(), p, seed, offset, _stream())
+
+
+def dropout_backward(dy, mask, dx, p: float) -> None:
+    _capi.call("cnhip_dropout_backward", _p(dy), _p(mask), _p(dx), dy.numel(), p, _stream())
+
+
+def global_avgpool_forward(X, Y, N, C, H, W) -> None:
+    _capi.call("cnhip_global_avgpool_forward", _p(X), _p(Y), N, C, H, W, _stream())
+
+
+def global_avgpool_backward(dY, dX, N, C, H, W) -> None:
+    _capi.call("cnhip_global_avgpool_backward", _p(dY), _p(dX), N, C, H, W, _stream())
+
+
+def global_maxpool_forward(X, Y, ah, aw, N, C, H, W) -> None:
+    _capi.call("cnhip_global_maxpool_forward", _p(X), _p(Y), _p(ah), _p(aw), N, C, H, W, _stream())
+
+
+def global_maxpool_backward(dY, ah, aw, dX, N, C, H, W) -> None:
+    _capi.call("cnhip_global_maxpool_backward", _p(dY), _p(ah), _p(aw), _p(dX), N, C, H, W, _stream())
+
+
+def rnn_forward(X, W_ih, W_hh, b, Y, B, S, I, H) -> None:
+    _capi.call("cnhip_rnn_forward", _p(X), _p(W_ih), _p(W_hh), _p(b), _p(Y), B, S, I, H, _stream())
+
+
+def rnn_backward(X, W_ih, W_hh, Y, dY, gW_ih, gW_hh, gb, dX, B, S, I, H) -> None:
+    _capi.call("cnhip_rnn_backward", *(_p(t) for t in (X, W_ih, W_hh, Y, dY, gW_ih, gW_hh, gb, dX)), B, S, I,
+               H, _stream())
+

@@ -423,6 +423,103 @@ int cnhip_adam_step_multi(int count, float* const* W, const float* const* g,
                           const float* bc1, const float* bc2, float lr,
                           float beta1, float beta2, float eps,
                           cnhip_stream_t stream);
+/* SGD, Momentum, Adagrad, RMSProp over up to 64 tensors in ONE launch;
+ * tensor i is (W[i], g[i], state[i], n[i]), state[i] the per-key velocity,
+ * squared-gradient accumulator or mean square (ignored for SGD, may be NULL).
+ * hyper is mu (Momentum) or rho (RMSProp); eps is used by Adagrad, RMSProp.
+ *   SGD      W -= lr g                                  (sgd.cpp:54-68)
+ *   Momentum v = mu v - lr g ; W += v                   (momentum.cpp:81-104)
+ *   Adagrad  a += g g ; W -= lr g / (sqrt(a) + eps)     (adagrad.cpp:83-106)
+ *   RMSProp  s = rho s + (1 - rho) g g ;
+ *            W -= lr g / (sqrt(s) + eps)                (mrs_prop.cpp:83-106)
+ * Each evaluated with one rounding per operation, as the reference's host
+ * loops (bit-identical for identical inputs).  ref: also sgd_step.cu,
+ * momentum_step.cu, adagrad_step.cu, rmsprop_step.cu. */
+#define CNHIP_OPT_SGD      0
+#define CNHIP_OPT_MOMENTUM 1
+#define CNHIP_OPT_ADAGRAD  2
+#define CNHIP_OPT_RMSPROP  3
+int cnhip_optimizer_step_multi(int kind, int count, float* const* W, const float* const* g,
+                               float* const* state, const int64_t* n, float lr, float hyper,
+                               float eps, cnhip_stream_t stream);
+
+/* ---- the reference's other device ops ----------------------------------
+ * LeakyReLU: y = x > 0 ? x : alpha x ; dx = x > 0 ? dy : alpha dy (the
+ * backward reads the INPUT).  ref: LeakyReLU::forward/backward
+ * src/CppNet/activations/leacky_relu.cpp:93-229, leaky_relu.cu */
+int cnhip_leaky_relu_forward(const float* x, float* y, int64_t n, float alpha,
+                             cnhip_stream_t stream);
+int cnhip_leaky_relu_backward(const float* x, const float* dy, float* dx, int64_t n,
+                              float alpha, cnhip_stream_t stream);
+/* Softmax over the LAST dimension of a ColMajor tensor: rows = size / len,
+ * element (r, j) at r + rows*j (2-D [B, F]: rows = B; 4-D: rows = d0 d1 d2).
+ * backward: dx = y (dy - sum_j dy y).  ref: Softmax::forward/backward
+ * src/CppNet/activations/softmax.cpp:105-323 (its gpu branch launches
+ * softmax_forward/backward_kernel) */
+int cnhip_softmax_forward(const float* x, float* y, int64_t rows, int64_t len,
+                          cnhip_stream_t stream);
+int cnhip_softmax_backward(const float* y, const float* dy, float* dx, int64_t rows,
+                           int64_t len, cnhip_stream_t stream);
+/* CategoricalCrossEntropy on ColMajor [B, C] with float (one-hot or soft)
+ * targets.  targets_used receives t (1 - ls) + ls / C (a copy of t when
+ * label_smoothing == 0); probs receives the softmax of the logits
+ * (from_logits) or a copy of the predictions; *loss = sum -t log(clip(p,
+ * 1e-15, 1 - 1e-15)), / B for mean.  backward: g = probs - t (from_logits)
+ * or -t / clip(p), / B for mean.  The row losses are summed in a fixed
+ * order.  ref: CategoricalCrossEntropy::forward/backward
+ * src/CppNet/losses/categorical_cross_entropy.cpp:167-380, categorical_ce.cu */
+int cnhip_cce_forward(const float* pred, const float* targets, float* probs,
+                      float* targets_used, float* loss, int64_t B, int64_t C, int from_logits,
+                      float label_smoothing, int reduction, cnhip_stream_t stream);
+int cnhip_cce_backward(const float* probs, const float* targets_used, float* grad, int64_t B,
+                       int64_t C, int from_logits, int reduction, cnhip_stream_t stream);
+/* MAE: mean |p - t|, grad sign(p - t) / n.  Huber(delta): 0.5 d^2 where
+ * |d| <= delta, else delta (|d| - delta/2); grad d or delta sign(d), / n for
+ * mean.  ref: src/CppNet/losses/mae.cpp:102-160, huber.cpp:104-178 */
+int cnhip_mae_forward(const float* p, const float* t, float* loss, int64_t n, int reduction,
+                      cnhip_stream_t stream);
+int cnhip_mae_backward(const float* p, const float* t, float* grad, int64_t n, int reduction,
+                       cnhip_stream_t stream);
+int cnhip_huber_forward(const float* p, const float* t, float* loss, int64_t n, float delta,
+                        int reduction, cnhip_stream_t stream);
+int cnhip_huber_backward(const float* p, const float* t, float* grad, int64_t n, float delta,
+                         int reduction, cnhip_stream_t stream);
+/* Dropout(p): y = x * mask * 1/(1 - p), mask[i] = 1 with probability 1 - p
+ * from a counter-based generator of (seed, offset + i) (the reference draws
+ * it from a time-seeded host mt19937, dropout.cpp:19-21); mask is one byte
+ * per element, kept for the backward dx = dy * mask * 1/(1 - p).
+ * ref: Dropout::forward/backward src/CppNet/layers/dropout.cpp:140-270, dropout.cu */
+int cnhip_dropout_forward(const float* x, float* y, uint8_t* mask, int64_t n, float p,
+                          uint64_t seed, uint64_t offset, cnhip_stream_t stream);
+int cnhip_dropout_backward(const float* dy, const uint8_t* mask, float* dx, int64_t n, float p,
+                           cnhip_stream_t stream);
+/* Global pools over [N, C, H, W] -> [N, C].  Average: sum over h then w in
+ * order, times 1/(H W); backward spreads dY/(H W).  Max: strict > scan (h
+ * outer, w inner) from -inf, argmax as int32 (h, w) tensors [N, C]; backward
+ * writes dY at the argmax and 0 elsewhere.  ref: GlobalAvgPool2D /
+ * GlobalMaxPool2D src/CppNet/layers/global_pool.cpp:111-395,
+ * global_avg_pool2d.cu, global_max_pool2d.cu */
+int cnhip_global_avgpool_forward(const float* X, float* Y, int64_t N, int64_t C, int64_t H,
+                                 int64_t W, cnhip_stream_t stream);
+int cnhip_global_avgpool_backward(const float* dY, float* dX, int64_t N, int64_t C, int64_t H,
+                                  int64_t W, cnhip_stream_t stream);
+int cnhip_global_maxpool_forward(const float* X, float* Y, int32_t* argmax_h, int32_t* argmax_w,
+                                 int64_t N, int64_t C, int64_t H, int64_t W,
+                                 cnhip_stream_t stream);
+int cnhip_global_maxpool_backward(const float* dY, const int32_t* argmax_h,
+                                  const int32_t* argmax_w, float* dX, int64_t N, int64_t C,
+                                  int64_t H, int64_t W, cnhip_stream_t stream);
+/* Elman RNN over X [B, S, I] -> Y [B, S, H]: h_0 = 0,
+ * h_t = tanh(x_t W_ih + h_{t-1} W_hh + b); the full sequence is returned.
+ * backward OVERWRITES gW_ih, gW_hh, gb and writes dX (may be NULL) from
+ * dY [B, S, H] and the forward's Y.  ref: RNN::forward/backward
+ * src/CppNet/layers/rnn.cpp:48-171, rnn_cell.cu */
+int cnhip_rnn_forward(const float* X, const float* W_ih, const float* W_hh, const float* b,
+                      float* Y, int64_t B, int64_t S, int64_t I, int64_t H,
+                      cnhip_stream_t stream);
+int cnhip_rnn_backward(const float* X, const float* W_ih, const float* W_hh, const float* Y,
+                       const float* dY, float* gW_ih, float* gW_hh, float* gb, float* dX,
+                       int64_t B, int64_t S, int64_t I, int64_t H, cnhip_stream_t stream);
 
 #ifdef __cplusplus
 }
