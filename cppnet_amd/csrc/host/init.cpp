@@ -17,6 +17,11 @@ namespace CppNet
         }
 
         void set_seed(uint64_t seed) { rng().seed(static_cast<std::mt19937::result_type>(seed)); }
+        uint64_t next_seed()
+        {
+            const uint64_t hi = rng()(), lo = rng()();
+            return (hi << 32) | lo;
+        }
 
         template <class Dist>
         static Tensor<float, 2> draw(int rows, int cols, Dist dist)

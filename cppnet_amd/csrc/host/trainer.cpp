@@ -130,7 +130,8 @@ struct cnt_session
     std::unique_ptr<EncoderNet> encoder;  // set for transformer sessions (X holds int32 ids)
     std::vector<std::shared_ptr<Layers::Layer>> keep;  // owns the layers
     std::unique_ptr<Losses::Loss> loss;
-    std::unique_ptr<Optimizers::Adam> adam;
+    std::unique_ptr<Optimizers::Optimizer> opt;  // Adam unless cnt_set_optimizer replaced it
+    bool updated = false;                        // an optimizer update has run
     float lr = 1e-3f;
     DeviceTensor X, Y;
     Losses::DeviceScalar last_loss;
@@ -230,6 +231,8 @@ namespace
             case CNT_ACT_RELU: return std::make_shared<Activations::ReLU>("gpu");
             case CNT_ACT_SIGMOID: return std::make_shared<Activations::Sigmoid>("gpu");
             case CNT_ACT_TANH: return std::make_shared<Activations::Tanh>("gpu");
+            case CNT_ACT_LEAKY_RELU: return std::make_shared<Activations::LeakyReLU>(0.01f, "gpu");
+            case CNT_ACT_SOFTMAX: return std::make_shared<Activations::Softmax>("gpu");
         }
         throw std::invalid_argument("unknown activation code " + std::to_string(act));
     }
@@ -241,6 +244,10 @@ namespace
             case CNT_LOSS_BCE: return std::make_unique<Losses::BinaryCrossEntropy>("mean", false, 1.0f, "gpu");
             case CNT_LOSS_SOFTMAX_CE: return std::make_unique<Losses::SoftmaxCrossEntropy>("mean", "gpu");
             case CNT_LOSS_MSE: return std::make_unique<Losses::MSE>("mean", "gpu");
+            case CNT_LOSS_CCE:
+                return std::make_unique<Losses::CategoricalCrossEntropy>("mean", true, 0.0f, "gpu");
+            case CNT_LOSS_MAE: return std::make_unique<Losses::MAE>("mean", "gpu");
+            case CNT_LOSS_HUBER: return std::make_unique<Losses::Huber>(1.0f, "mean", "gpu");
         }
         throw std::invalid_argument("unknown loss code " + std::to_string(loss));
     }
@@ -345,7 +352,7 @@ int cnt_mlp_create(cnt_session** out, int n_linear, const int64_t* sizes, int hi
             if (act) s->model.add_activation(act);
         }
         s->loss = make_loss(loss);
-        s->adam = std::make_unique<Optimizers::Adam>(beta1, beta2, eps, "gpu");
+        s->opt = std::make_unique<Optimizers::Adam>(beta1, beta2, eps, "gpu");
         s->lr = lr;
         s->X = DeviceTensor::zeros({batch, sizes[0]});
         s->Y = DeviceTensor::zeros({batch, sizes[n_linear]});
@@ -392,7 +399,7 @@ int cnt_cnn_create(cnt_session** out, int n_conv, const int64_t* conv_spec, int 
         s->keep.push_back(fc);
         s->add_params(fc);
         s->loss = make_loss(CNT_LOSS_SOFTMAX_CE);
-        s->adam = std::make_unique<Optimizers::Adam>(beta1, beta2, eps, "gpu");
+        s->opt = std::make_unique<Optimizers::Adam>(beta1, beta2, eps, "gpu");
         s->lr = lr;
         s->X = DeviceTensor::zeros({input_shape[0], input_shape[1], input_shape[2], input_shape[3]});
         s->Y = DeviceTensor::zeros({input_shape[0], classes});
@@ -426,8 +433,15 @@ int cnt_rnn_create(cnt_session** out, int cell, int64_t batch, int64_t seq_len, 
             s->model.add_layer(g);
             rnn = g;
         }
+        else if (cell == 2)
+        {
+            auto e = std::make_shared<Layers::RNN>(static_cast<int>(input_size), static_cast<int>(hidden_size),
+                                                   true, "gpu");
+            s->model.add_layer(e);
+            rnn = e;
+        }
         else
-            throw std::invalid_argument("cell must be 0 (LSTM) or 1 (GRU)");
+            throw std::invalid_argument("cell must be 0 (LSTM), 1 (GRU) or 2 (RNN)");
         s->keep.push_back(rnn);
         Layers::RecurrentBase* r = rnn.get();
         s->params.push_back({[r]() -> DeviceTensor& { return r->W_ih(); },
@@ -445,7 +459,7 @@ int cnt_rnn_create(cnt_session** out, int cell, int64_t batch, int64_t seq_len, 
         s->keep.push_back(fc);
         s->add_params(fc);
         s->loss = make_loss(CNT_LOSS_MSE);
-        s->adam = std::make_unique<Optimizers::Adam>(beta1, beta2, eps, "gpu");
+        s->opt = std::make_unique<Optimizers::Adam>(beta1, beta2, eps, "gpu");
         s->lr = lr;
         s->X = DeviceTensor::zeros({batch, seq_len, input_size});
         s->Y = DeviceTensor::zeros({batch, out_features});
@@ -505,7 +519,7 @@ int cnt_transformer_create(cnt_session** out, int64_t batch, int64_t seq_len, in
         s->add_params(net->fc);
         s->encoder = std::move(net);
         s->loss = make_loss(CNT_LOSS_SOFTMAX_CE);
-        s->adam = std::make_unique<Optimizers::Adam>(beta1, beta2, eps, "gpu");
+        s->opt = std::make_unique<Optimizers::Adam>(beta1, beta2, eps, "gpu");
         s->lr = lr;
         s->X = DeviceTensor::zeros({batch, seq_len});  // int32 ids
         s->Y = DeviceTensor::zeros({batch, classes});
@@ -660,11 +674,30 @@ namespace
     void update(cnt_session* s)
     {
         if (s->encoder)
-            s->encoder->update(*s->adam, s->lr);
+            s->encoder->update(*s->opt, s->lr);
         else
-            s->model.update(*s->adam, s->lr);
+            s->model.update(*s->opt, s->lr);
+        s->updated = true;
     }
 } // namespace
+
+int cnt_set_optimizer(cnt_session* s, int kind, float hyper, float eps)
+{
+    return guarded("cnt_set_optimizer", [&] {
+        check_session(s);
+        if (s->updated) throw std::logic_error("the session has already updated its parameters");
+        StreamScope scope(s);
+        switch (kind)
+        {
+            case CNT_OPT_ADAM: s->opt = std::make_unique<Optimizers::Adam>(hyper, 0.999f, eps, "gpu"); break;
+            case CNT_OPT_SGD: s->opt = std::make_unique<Optimizers::SGD>("gpu"); break;
+            case CNT_OPT_MOMENTUM: s->opt = std::make_unique<Optimizers::Momentum>(hyper, "gpu"); break;
+            case CNT_OPT_ADAGRAD: s->opt = std::make_unique<Optimizers::Adagrad>(eps, "gpu"); break;
+            case CNT_OPT_RMSPROP: s->opt = std::make_unique<Optimizers::RMSProp>(hyper, eps, "gpu"); break;
+            default: throw std::invalid_argument("unknown optimizer code " + std::to_string(kind));
+        }
+    });
+}
 
 int cnt_step(cnt_session* s, float* loss_out)
 {

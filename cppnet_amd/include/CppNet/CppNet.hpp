@@ -21,17 +21,29 @@
 #include "CppNet/layers/batch_norm.hpp"
 #include "CppNet/layers/mean_pool1d.hpp"
 #include "CppNet/layers/residual.hpp"
+#include "CppNet/layers/rnn.hpp"
+#include "CppNet/layers/dropout.hpp"
+#include "CppNet/layers/global_pool.hpp"
 #include "CppNet/activations/activation.hpp"
 #include "CppNet/activations/relu.hpp"
 #include "CppNet/activations/sigmoid.hpp"
 #include "CppNet/activations/tanh.hpp"
 #include "CppNet/activations/gelu.hpp"
+#include "CppNet/activations/leacky_relu.hpp"
+#include "CppNet/activations/softmax.hpp"
 #include "CppNet/losses/loss.hpp"
 #include "CppNet/losses/binary_cross_entropy.hpp"
 #include "CppNet/losses/mse.hpp"
 #include "CppNet/losses/softmax_cross_entropy.hpp"
+#include "CppNet/losses/categorical_cross_entropy.hpp"
+#include "CppNet/losses/mae.hpp"
+#include "CppNet/losses/huber.hpp"
 #include "CppNet/optimizers/optimizer.hpp"
 #include "CppNet/optimizers/adam.hpp"
+#include "CppNet/optimizers/sgd.hpp"
+#include "CppNet/optimizers/momentum.hpp"
+#include "CppNet/optimizers/adagrad.hpp"
+#include "CppNet/optimizers/mrs_prop.hpp"
 #include "CppNet/models/models.hpp"
 
 namespace CppNet

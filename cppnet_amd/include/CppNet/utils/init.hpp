@@ -20,6 +20,9 @@ namespace CppNet
     namespace Utils
     {
         void set_seed(uint64_t seed);
+        /// A 64-bit value from the same generator (seeds the device-side
+        /// dropout masks, so set_seed() fixes them too).
+        uint64_t next_seed();
         Tensor<float, 2> xavier_uniform(int rows, int cols);
         Tensor<float, 2> xavier_normal(int rows, int cols);
         Tensor<float, 2> he_uniform(int rows, int cols);

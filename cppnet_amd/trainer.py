@@ -13,8 +13,11 @@ import numpy as np
 
 from . import _capi
 
-ACT = {"none": 0, "relu": 1, "sigmoid": 2, "tanh": 3}
-LOSS = {"bce": 0, "softmax_ce": 1, "mse": 2}
+ACT = {"none": 0, "relu": 1, "sigmoid": 2, "tanh": 3, "leaky_relu": 4, "softmax": 5}
+LOSS = {"bce": 0, "softmax_ce": 1, "mse": 2, "cce": 3, "mae": 4, "huber": 5}
+OPT = {"adam": 0, "sgd": 1, "momentum": 2, "adagrad": 3, "rmsprop": 4}
+CELL = {"lstm": 0, "gru": 1, "rnn": 2}
+GATES = {"lstm": 4, "gru": 3, "rnn": 1}
 
 _lib = None
 
@@ -41,6 +44,7 @@ def load() -> C.CDLL:
                                          f32, f32, f32, C.c_uint64]),
         "cnt_set_batch_tokens": (i32, [vp, vp, vp]),
         "cnt_destroy": (i32, [vp]),
+        "cnt_set_optimizer": (i32, [vp, i32, f32, f32]),
         "cnt_num_params": (i32, [vp, C.POINTER(i32)]),
         "cnt_param_size": (i32, [vp, i32, C.POINTER(i64)]),
         "cnt_set_param": (i32, [vp, i32, vp]),
@@ -84,6 +88,9 @@ class MLPConfig:
     eps: float = 1e-8
     seed: int = 1234
     extra: dict = field(default_factory=dict)
+    optimizer: str = "adam"   # OPT key; "adam" uses beta1/beta2/eps above
+    opt_hyper: float = 0.9    # Momentum's mu / RMSProp's rho
+    opt_eps: float = 1e-8     # Adagrad's / RMSProp's epsilon
 
 
 def mlp_config(config: int, batch: int | None = None) -> MLPConfig:
@@ -160,7 +167,7 @@ def synthetic_cnn(cfg: CNNConfig, rng: np.random.Generator):
 
 @dataclass
 class RNNConfig:
-    """cell ("lstm" | "gru") over X [B, S, I] -> last hidden state -> Linear(H -> O) -> MSE."""
+    """cell ("lstm" | "gru" | "rnn") over X [B, S, I] -> last hidden state -> Linear(H -> O) -> MSE."""
     name: str
     cell: str
     batch: int
@@ -174,6 +181,9 @@ class RNNConfig:
     eps: float = 1e-8
     seed: int = 1234
     loss: str = "mse"
+    optimizer: str = "adam"
+    opt_hyper: float = 0.9
+    opt_eps: float = 1e-8
 
 
 def rnn_config(config: int = 4, batch: int | None = None, seq_len: int | None = None,
@@ -190,7 +200,7 @@ def synthetic_rnn(cfg: RNNConfig, rng: np.random.Generator):
     """W_ih, W_hh uniform with limits sqrt(6/(I+H)), sqrt(6/2H) (lstm.cpp:42-45);
     bias 0 with the LSTM forget block at 1 (lstm.cpp:47-49); Linear xavier;
     X ~ N(0,1) [B,S,I]; target ~ N(0,1) [B,1]."""
-    G = (4 if cfg.cell == "lstm" else 3) * cfg.hidden
+    G = GATES[cfg.cell] * cfg.hidden
     I, H = cfg.input_size, cfg.hidden
     lih, lhh = np.sqrt(6.0 / (I + H)), np.sqrt(6.0 / (2 * H))
     b = np.zeros(G, np.float32)
@@ -268,8 +278,8 @@ def xavier(rng: np.random.Generator, fan_in: int, fan_out: int) -> np.ndarray:
 
 def synthetic_mlp(cfg: MLPConfig, rng: np.random.Generator):
     """Parameters (W, b per layer; b = 0 as linear.cpp:75-80), X ~ N(0,1) and
-    targets (Bernoulli(0.5) for BCE, one-hot uniform labels for softmax-CE,
-    N(0,1) for MSE), all ColMajor flat float32."""
+    targets (Bernoulli(0.5) for BCE, one-hot uniform labels for softmax-CE and
+    categorical CE, N(0,1) for MSE / MAE / Huber), all ColMajor flat float32."""
     params = []
     for i, o in zip(cfg.sizes[:-1], cfg.sizes[1:]):
         params.append(xavier(rng, i, o))
@@ -278,7 +288,7 @@ def synthetic_mlp(cfg: MLPConfig, rng: np.random.Generator):
     X = rng.standard_normal(B * I).astype(np.float32)
     if cfg.loss == "bce":
         Y = (rng.uniform(size=B * O) < 0.5).astype(np.float32)
-    elif cfg.loss == "softmax_ce":
+    elif cfg.loss in ("softmax_ce", "cce"):
         labels = rng.integers(0, O, B)
         Y = np.zeros((O, B), np.float32)
         Y[labels, np.arange(B)] = 1.0
@@ -303,7 +313,7 @@ class Session:
             self.x_size = cfg.batch * cfg.seq_len
             self.y_size = cfg.batch * cfg.classes
         elif isinstance(cfg, RNNConfig):
-            _check(lib.cnt_rnn_create(C.byref(h), 0 if cfg.cell == "lstm" else 1, cfg.batch,
+            _check(lib.cnt_rnn_create(C.byref(h), CELL[cfg.cell], cfg.batch,
                                       cfg.seq_len, cfg.input_size, cfg.hidden, cfg.out_features,
                                       cfg.lr, cfg.beta1, cfg.beta2, cfg.eps, cfg.seed))
             self.x_size = cfg.batch * cfg.seq_len * cfg.input_size
@@ -324,6 +334,9 @@ class Session:
             self.y_size = cfg.batch * cfg.sizes[-1]
         self.h = h
         self.cfg = cfg
+        opt = getattr(cfg, "optimizer", "adam")
+        if opt != "adam":
+            _check(lib.cnt_set_optimizer(h, OPT[opt], cfg.opt_hyper, cfg.opt_eps))
 
     def close(self):
         if self.h:

@@ -26,10 +26,22 @@ typedef struct cnt_session cnt_session;
 #define CNT_ACT_RELU    1
 #define CNT_ACT_SIGMOID 2
 #define CNT_ACT_TANH    3
+#define CNT_ACT_LEAKY_RELU 4 /* alpha 0.01 (leacky_relu.hpp default) */
+#define CNT_ACT_SOFTMAX    5 /* over the features of each row */
 
 #define CNT_LOSS_BCE        0
 #define CNT_LOSS_SOFTMAX_CE 1
 #define CNT_LOSS_MSE        2
+#define CNT_LOSS_CCE        3 /* CategoricalCrossEntropy("mean", from_logits) */
+#define CNT_LOSS_MAE        4 /* MAE("mean") */
+#define CNT_LOSS_HUBER      5 /* Huber(delta 1, "mean") */
+
+/* optimizers of cnt_set_optimizer */
+#define CNT_OPT_ADAM     0
+#define CNT_OPT_SGD      1
+#define CNT_OPT_MOMENTUM 2 /* hyper = mu */
+#define CNT_OPT_ADAGRAD  3 /* eps */
+#define CNT_OPT_RMSPROP  4 /* hyper = rho, eps */
 
 const char* cnt_last_error(void);
 
@@ -49,7 +61,7 @@ int cnt_mlp_create(cnt_session** out, int n_linear, const int64_t* sizes, int hi
 int cnt_cnn_create(cnt_session** out, int n_conv, const int64_t* conv_spec, int pool,
                    const int64_t* input_shape, int64_t classes, float lr, float beta1,
                    float beta2, float eps, uint64_t seed);
-/* Sequence regressor: LSTM (cell 0) or GRU (cell 1) over X [batch, seq_len,
+/* Sequence regressor: LSTM (cell 0), GRU (cell 1) or Elman RNN (cell 2) over X [batch, seq_len,
  * input_size] -> last hidden state -> Linear(hidden -> out_features) ->
  * MSE("mean"), Adam.  Parameters: W_ih, W_hh, b of the cell, then W, b of the
  * Linear.  Config 4 of the benchmark is the LSTM instance.
@@ -73,6 +85,14 @@ int cnt_transformer_create(cnt_session** out, int64_t batch, int64_t seq_len, in
                            int64_t classes, float lr, float beta1, float beta2, float eps,
                            uint64_t seed);
 int cnt_destroy(cnt_session* s);
+/* Replaces the session's optimizer (Adam from the create call) before its
+ * first update: kind CNT_OPT_*; hyper is Momentum's mu or RMSProp's rho
+ * (ignored otherwise), eps Adagrad's / RMSProp's epsilon; CNT_OPT_ADAM takes
+ * beta1 = hyper and eps with beta2 0.999.  State starts at zero.  Refused
+ * once the session has updated (the reference's optimizers keep per-parameter
+ * state that a swap would drop).
+ * ref: src/CppNet/optimizers/{sgd,momentum,adagrad,mrs_prop,adam}.cpp */
+int cnt_set_optimizer(cnt_session* s, int kind, float hyper, float eps);
 
 int cnt_num_params(cnt_session* s, int* count);
 int cnt_param_size(cnt_session* s, int index, int64_t* n);

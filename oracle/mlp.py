@@ -9,6 +9,7 @@ from __future__ import annotations
 import numpy as np
 
 from oracle import fp
+from oracle.optim import OracleOptimizer
 
 _RED_MEAN = 0
 
@@ -20,23 +21,23 @@ class OracleMLP:
         self.sizes = cfg.sizes
         self.params = None
         self.grads = None
-        self.m = None
-        self.v = None
-        self.t = None
+        self.opt = None
 
     def set_params(self, params):
         self.params = [np.array(p, np.float32, copy=True) for p in params]
         self.grads = [np.zeros_like(p) for p in self.params]
-        self.m = [np.zeros_like(p) for p in self.params]
-        self.v = [np.zeros_like(p) for p in self.params]
-        self.t = [0] * len(self.params)
+        self.opt = OracleOptimizer(self.cfg, self.o, self.params)
 
     def get_params(self):
         return [p.copy() for p in self.params]
 
     def _act(self, name, x):
         y = np.empty_like(x)
-        if name == "relu":
+        if name == "leaky_relu":  # leacky_relu.hpp default alpha
+            self.o.cnref_leaky_relu_forward(fp(x), fp(y), x.size, 0.01)
+        elif name == "softmax":  # over the features of each of the B rows
+            self.o.cnref_softmax_forward(fp(x), fp(y), self.cfg.batch, x.size // self.cfg.batch)
+        elif name == "relu":
             self.o.cnref_relu_forward(fp(x), fp(y), x.size)
         elif name == "sigmoid":
             self.o.cnref_sigmoid_forward(fp(x), fp(y), x.size)
@@ -46,10 +47,16 @@ class OracleMLP:
             return x
         return y
 
-    def _act_bwd(self, name, y, g):
+    def _act_bwd(self, name, y, g, z=None):
         if name == "none":
             return g
         dx = np.empty_like(g)
+        if name == "leaky_relu":  # reads the cached input (leacky_relu.cpp:127-160)
+            self.o.cnref_leaky_relu_backward(fp(z), fp(g), fp(dx), g.size, 0.01)
+            return dx
+        if name == "softmax":
+            self.o.cnref_softmax_backward(fp(y), fp(g), fp(dx), self.cfg.batch, g.size // self.cfg.batch)
+            return dx
         getattr(self.o, f"cnref_{name}_backward")(fp(y), fp(g), fp(dx), g.size)
         return dx
 
@@ -83,6 +90,16 @@ class OracleMLP:
             sm = np.empty_like(out)
             loss = o.cnref_softmax_ce_forward(fp(out), fp(Y), fp(sm), B, O, _RED_MEAN)
             o.cnref_softmax_ce_backward(fp(sm), fp(Y), fp(grad), B, O, _RED_MEAN)
+        elif cfg.loss == "cce":  # from logits, no smoothing
+            sm, tu = np.empty_like(out), np.empty_like(out)
+            loss = o.cnref_cce_forward(fp(out), fp(Y), fp(sm), fp(tu), B, O, 1, 0.0, _RED_MEAN)
+            o.cnref_cce_backward(fp(sm), fp(tu), fp(grad), B, O, 1, _RED_MEAN)
+        elif cfg.loss == "mae":
+            loss = o.cnref_mae_forward(fp(out), fp(Y), out.size, _RED_MEAN)
+            o.cnref_mae_backward(fp(out), fp(Y), fp(grad), out.size, _RED_MEAN)
+        elif cfg.loss == "huber":  # delta 1
+            loss = o.cnref_huber_forward(fp(out), fp(Y), out.size, 1.0, _RED_MEAN)
+            o.cnref_huber_backward(fp(out), fp(Y), fp(grad), out.size, 1.0, _RED_MEAN)
         else:
             loss = o.cnref_mse_forward(fp(out), fp(Y), out.size, _RED_MEAN)
             o.cnref_mse_backward(fp(out), fp(Y), fp(grad), out.size, _RED_MEAN)
@@ -92,18 +109,13 @@ class OracleMLP:
         for i in reversed(range(nl)):
             I, O = self.sizes[i], self.sizes[i + 1]
             dH = grad
-            grad = self._act_bwd(acts[i], outs[i], grad)
+            grad = self._act_bwd(acts[i], outs[i], grad, pre[i])
             self.trace[i] = dict(x=inputs[i], z=pre[i], dH=dH.copy(), dA=grad.copy(), act=acts[i])
             dX = np.empty(B * I, np.float32)
             o.cnref_linear_backward(fp(inputs[i]), fp(self.params[2 * i]), fp(grad),
                                     fp(self.grads[2 * i]), fp(self.grads[2 * i + 1]), fp(dX), B, I,
                                     O, 1, 1)
             grad = dX
-        for k, (p, g) in enumerate(zip(self.params, self.grads)):  # model.update(adam, lr)
-            self.t[k] += 1
-            bc1 = o.cnref_bias_correction(cfg.beta1, self.t[k])
-            bc2 = o.cnref_bias_correction(cfg.beta2, self.t[k])
-            o.cnref_adam_step(fp(p), fp(g), fp(self.m[k]), fp(self.v[k]), p.size, cfg.lr,
-                              cfg.beta1, cfg.beta2, cfg.eps, bc1, bc2)
+        self.opt.step(self.params, self.grads)  # model.update(optimizer, lr)
         self.last_grads = [g.copy() for g in self.grads]
         return float(loss)

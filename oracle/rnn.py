@@ -1,6 +1,7 @@
 """Sequence-regressor train step composed from the CPU oracle's ops (test
-infrastructure): LSTM or GRU over the sequence, the last hidden state,
-Linear, MSE(mean), Adam -- the reference harness's loop
+infrastructure): LSTM, GRU or Elman RNN over the sequence, the last hidden
+state, Linear, MSE(mean), Adam or the configured optimizer -- the reference
+harness's loop
 (benchmarks/sequence_benckmark.cpp:149-177).  Recurrent grads are
 overwritten by each backward (lstm.cpp:158-160); the Linear grads are
 cleared by zero_grad and accumulated (linear.cpp:346-352)."""
@@ -9,6 +10,7 @@ from __future__ import annotations
 import numpy as np
 
 from oracle import fp
+from oracle.optim import OracleOptimizer
 
 
 class OracleSeqRegressor:
@@ -18,9 +20,7 @@ class OracleSeqRegressor:
     def set_params(self, params):
         self.params = [np.array(p, np.float32, copy=True) for p in params]
         self.grads = [np.zeros_like(p) for p in self.params]
-        self.m = [np.zeros_like(p) for p in self.params]
-        self.v = [np.zeros_like(p) for p in self.params]
-        self.t = [0] * len(self.params)
+        self.opt = OracleOptimizer(self.cfg, self.o, self.params)
 
     def get_params(self):
         return [p.copy() for p in self.params]
@@ -37,6 +37,8 @@ class OracleSeqRegressor:
             c, tc = np.zeros(BS * H, np.float32), np.zeros(BS * H, np.float32)
             o.cnref_lstm_forward(fp(X), fp(Wih), fp(Whh), fp(b), fp(Yseq), fp(gates), fp(c), fp(tc),
                                  B, S, I, H)
+        elif cfg.cell == "rnn":
+            o.cnref_rnn_forward(fp(X), fp(Wih), fp(Whh), fp(b), fp(Yseq), B, S, I, H)
         else:
             gates, rh = np.zeros(BS * 3 * H, np.float32), np.zeros(BS * H, np.float32)
             o.cnref_gru_forward(fp(X), fp(Wih), fp(Whh), fp(b), fp(Yseq), fp(gates), fp(rh), B, S, I, H)
@@ -61,16 +63,14 @@ class OracleSeqRegressor:
             o.cnref_lstm_backward(fp(X), fp(Wih), fp(Whh), fp(Yseq), fp(gates), fp(c), fp(tc), fp(dY),
                                   fp(self.grads[0]), fp(self.grads[1]), fp(self.grads[2]), fp(dX),
                                   B, S, I, H)
+        elif cfg.cell == "rnn":
+            o.cnref_rnn_backward(fp(X), fp(Wih), fp(Whh), fp(Yseq), fp(dY), fp(self.grads[0]),
+                                 fp(self.grads[1]), fp(self.grads[2]), fp(dX), B, S, I, H)
         else:
             o.cnref_gru_backward(fp(X), fp(Wih), fp(Whh), fp(Yseq), fp(gates), fp(rh), fp(dY),
                                  fp(self.grads[0]), fp(self.grads[1]), fp(self.grads[2]), fp(dX),
                                  B, S, I, H)
         self.last_grads = [gr.copy() for gr in self.grads]
         self.trace = dict(X=X, Yseq=Yseq, hT=hT, g=g, dh=dh)
-        for k, (p, gr) in enumerate(zip(self.params, self.grads)):
-            self.t[k] += 1
-            bc1 = o.cnref_bias_correction(cfg.beta1, self.t[k])
-            bc2 = o.cnref_bias_correction(cfg.beta2, self.t[k])
-            o.cnref_adam_step(fp(p), fp(gr), fp(self.m[k]), fp(self.v[k]), p.size, cfg.lr, cfg.beta1,
-                              cfg.beta2, cfg.eps, bc1, bc2)
+        self.opt.step(self.params, self.grads)
         return float(loss)

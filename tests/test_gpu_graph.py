@@ -1,8 +1,8 @@
 """Whole-step graph replay (cnt_capture_step) against eager steps.
 
 A replayed step runs the same kernels, in the same order, on the same data
-as an eager step, and Adam runs eagerly after each replay with the host's
-bias corrections, so the bar is bit-identical: every step's loss and every
+as an eager step, and the optimizer (Adam with the host's bias corrections,
+or Momentum / RMSProp) runs eagerly after each replay, so the bar is bit-identical: every step's loss and every
 parameter after the run must equal those of an eager session started from
 the same weights and batches.  Between replays the test does the program's
 own eager work (parameter and gradient read-backs with their
@@ -15,12 +15,23 @@ from cppnet_amd import trainer
 
 pytestmark = pytest.mark.gpu
 
+def _variant(hidden, out, loss, opt):
+    cfg = trainer.MLPConfig(f"MLP {hidden}/{out} {loss} {opt}", [48, 96, 64, 10], hidden, out, loss, 128)
+    cfg.optimizer = opt
+    return cfg
+
+
 CASES = {
     "c1_mlp": lambda: (trainer.mlp_config(1, batch=512), trainer.synthetic_mlp),
     "c2_mlp": lambda: (trainer.mlp_config(2, batch=256), trainer.synthetic_mlp),
     "c3_cnn": lambda: (trainer.cnn_config(3, batch=32), trainer.synthetic_cnn),
     "c4_lstm": lambda: (trainer.rnn_config(4, batch=16, seq_len=8), trainer.synthetic_rnn),
     "gru": lambda: (trainer.rnn_config(4, batch=16, seq_len=8, cell="gru"), trainer.synthetic_rnn),
+    "elman_rnn": lambda: (trainer.rnn_config(4, batch=16, seq_len=8, cell="rnn"), trainer.synthetic_rnn),
+    "mlp_leaky_cce_momentum": lambda: (_variant("leaky_relu", "none", "cce", "momentum"),
+                                       trainer.synthetic_mlp),
+    "mlp_softmax_huber_rmsprop": lambda: (_variant("tanh", "softmax", "huber", "rmsprop"),
+                                          trainer.synthetic_mlp),
     "c5_transformer": lambda: (trainer.transformer_config(5, batch=4, seq_len=16, vocab=64, embed_dim=32,
                                                           heads=4, blocks=2, ffn=64, classes=4),
                                trainer.synthetic_transformer),

@@ -51,6 +51,10 @@ def _grad_mags(oracle, ref, cfg):
     return mags
 
 
+# activations with a kink at 0: the jump of the slope there (ReLU 1, LeakyReLU 1 - alpha)
+_KINKED = {"relu": 1.0, "leaky_relu": 0.99}
+
+
 def _mask_allowance(oracle, ref, cfg, params):
     """Bound on what ReLU-mask choices at near-zero pre-activations can change.
 
@@ -66,13 +70,13 @@ def _mask_allowance(oracle, ref, cfg, params):
     up = [None] * nl           # |change of dH_l| from flips at layer l+1
     for i, tr in enumerate(ref.trace):
         I, O = cfg.sizes[i], cfg.sizes[i + 1]
-        if tr["act"] != "relu":
+        if tr["act"] not in _KINKED:
             E[i] = np.zeros(B * O, np.float32)
             continue
         zmag = gemm_mag(oracle, 0, 0, B, O, I, tr["x"], B, params[2 * i], I, B)
         tau = 1e-5 + 1e-4 * np.maximum(np.abs(tr["z"]), zmag)
         amb = np.abs(tr["z"]) <= tau
-        E[i] = np.where(amb, np.abs(tr["dH"]), 0.0).astype(np.float32)
+        E[i] = np.where(amb, _KINKED[tr["act"]] * np.abs(tr["dH"]), 0.0).astype(np.float32)
     allow = []
     for i, tr in enumerate(ref.trace):
         I, O = cfg.sizes[i], cfg.sizes[i + 1]
@@ -82,7 +86,8 @@ def _mask_allowance(oracle, ref, cfg, params):
             d_up = np.zeros(B * O, np.float32)   # |E_{l+1}| |W_{l+1}|^T : [B, O]
             oracle.cnref_gemm_f32(0, 1, B, O, O2, 1.0, fp(E[i + 1]), B,
                                   fp(np.abs(params[2 * (i + 1)])), O, 0.0, fp(d_up), B, None, 0)
-            mask = (tr["z"] > 0).astype(np.float32) if tr["act"] == "relu" else 1.0
+            mask = (np.where(tr["z"] > 0, 1.0, 1.0 - _KINKED[tr["act"]]).astype(np.float32)
+                    if tr["act"] in _KINKED else 1.0)
             dchg = dchg + d_up * np.maximum(mask, (E[i] > 0))
         dchg = dchg.astype(np.float32)
         aW = np.zeros(I * O, np.float32)
@@ -113,7 +118,78 @@ def _one_step(oracle, cfg, seed):
 def test_one_step_parity(gpu, oracle_mt, config, batch):
     cfg = trainer.mlp_config(config, batch)
     print(f"[model] config {config} batch {cfg.batch}: one step", flush=True)
-    sess, ref, params, loss_gpu, loss_ref = _one_step(oracle_mt, cfg, seed=100 + config)
+    _check_one_step(oracle_mt, cfg, 100 + config, f"config {config}")
+
+
+# The reference's other activations, losses and optimizers in the same
+# harness step (LeakyReLU, Softmax, CategoricalCrossEntropy, MAE, Huber, SGD,
+# Momentum, Adagrad, RMSProp).
+VARIANTS = [
+    ("leaky_relu", "none", "cce", "sgd"),
+    ("leaky_relu", "none", "cce", "momentum"),
+    ("relu", "none", "huber", "adagrad"),
+    ("tanh", "softmax", "mae", "rmsprop"),
+    ("leaky_relu", "softmax", "mse", "adam"),
+]
+
+
+def _variant_cfg(hidden, out, loss, opt, batch=256):
+    cfg = trainer.MLPConfig(f"MLP 48-96-64-10 {hidden}/{out} {loss} {opt}", [48, 96, 64, 10], hidden,
+                            out, loss, batch, lr=1e-2 if opt in ("sgd", "momentum") else 1e-3)
+    cfg.optimizer, cfg.opt_hyper, cfg.opt_eps = opt, 0.9, 1e-8
+    return cfg
+
+
+@pytest.mark.parametrize("hidden,out,loss,opt", VARIANTS)
+def test_one_step_parity_variants(gpu, oracle_mt, hidden, out, loss, opt):
+    cfg = _variant_cfg(hidden, out, loss, opt)
+    print(f"[model] {cfg.name}: one step", flush=True)
+    _check_one_step(oracle_mt, cfg, 7, cfg.name)
+
+
+@pytest.mark.parametrize("hidden,out,loss,opt", VARIANTS[:4])
+def test_multi_step_parity_variants(gpu, oracle_mt, hidden, out, loss, opt):
+    cfg = _variant_cfg(hidden, out, loss, opt, batch=64)
+    steps = 15
+    print(f"[model] {cfg.name}: {steps} steps", flush=True)
+    rng = np.random.default_rng(77)
+    params, _, _ = trainer.synthetic_mlp(cfg, rng)
+    sess = trainer.Session(cfg)
+    sess.set_params(params)
+    ref, ref_d = OracleMLP(cfg, oracle_mt), OracleMLP(cfg, oracle_mt)
+    ref.set_params(params)
+    ref_d.set_params(params)
+    for step in range(steps):
+        _, X, Y = trainer.synthetic_mlp(cfg, rng)
+        sess.set_batch(X, Y)
+        lg, lr_ = sess.step(), ref.step(X, Y)
+        oracle_mt.cnref_set_accumulate_double(1)
+        try:
+            ref_d.step(X, Y)
+        finally:
+            oracle_mt.cnref_set_accumulate_double(0)
+        assert abs(lg - lr_) <= 1e-3 * abs(lr_) + 1e-6, f"step {step}: loss {lg} vs {lr_}"
+    for k, (a, b, c) in enumerate(zip(sess.get_params(), ref.get_params(), ref_d.get_params())):
+        rel, drift = _rel(a, b), _rel(c, b)
+        assert rel <= max(1e-3, 2.0 * drift), f"param {k}: relative norm error {rel:.3g}"
+    sess.close()
+
+
+def test_set_optimizer_refused_after_update(gpu):
+    cfg = _variant_cfg("relu", "none", "mse", "adam", batch=8)
+    params, X, Y = trainer.synthetic_mlp(cfg, np.random.default_rng(3))
+    sess = trainer.Session(cfg)
+    sess.set_batch(X, Y)
+    sess.step()
+    lib = trainer.load()
+    assert lib.cnt_set_optimizer(sess.h, trainer.OPT["sgd"], 0.0, 0.0) != 0
+    assert "already updated" in lib.cnt_last_error().decode()
+    sess.close()
+
+
+def _check_one_step(oracle_mt, cfg, seed, label):
+    config = label
+    sess, ref, params, loss_gpu, loss_ref = _one_step(oracle_mt, cfg, seed=seed)
     ok, msg = close([loss_gpu], [loss_ref], 1e-4, 1e-5)
     assert ok, f"loss: {msg}"
     mags = _grad_mags(oracle_mt, ref, cfg)
@@ -147,7 +223,7 @@ def test_one_step_parity(gpu, oracle_mt, config, batch):
             f"conditioned (max err {err[unexplained].max():.3g})")
         flips += int(bad.sum())
     total = sum(p.size for p in w_gpu)
-    print(f"[model] config {config}: loss {loss_gpu:.7f} vs {loss_ref:.7f}; {n_allow} grads "
+    print(f"[model] {config}: loss {loss_gpu:.7f} vs {loss_ref:.7f}; {n_allow} grads "
           f"needed the ReLU-mask allowance; {flips}/{total} updated weights differ, all at |g| "
           f"within gradient tolerance of 0")
     sess.close()
@@ -362,7 +438,7 @@ def test_cnn_multi_step_parity(gpu, oracle_mt):
     sess.close()
 
 
-@pytest.mark.parametrize("cell,batch,seq", [("lstm", None, None), ("gru", 32, 16)])
+@pytest.mark.parametrize("cell,batch,seq", [("lstm", None, None), ("gru", 32, 16), ("rnn", 32, 16)])
 def test_rnn_one_step_parity(gpu, oracle_mt, cell, batch, seq):
     """Config 4 (LSTM 128->512, T=64, batch 128) at full size, and the GRU
     variant of the same regressor.  The recurrent grads are sums over all B*S
@@ -400,11 +476,13 @@ def test_rnn_one_step_parity(gpu, oracle_mt, cell, batch, seq):
     sess.close()
 
 
-def test_rnn_multi_step_parity(gpu, oracle_mt):
+@pytest.mark.parametrize("cell,opt", [("lstm", "adam"), ("rnn", "momentum"), ("gru", "rmsprop")])
+def test_rnn_multi_step_parity(gpu, oracle_mt, cell, opt):
     from oracle.rnn import OracleSeqRegressor
-    cfg = trainer.rnn_config(4, batch=16, seq_len=12)
+    cfg = trainer.rnn_config(4, batch=16, seq_len=12, cell=cell)
+    cfg.optimizer = opt
     steps = 20
-    print(f"[model] config 4 lstm batch {cfg.batch} T={cfg.seq_len}: {steps} steps", flush=True)
+    print(f"[model] config 4 {cell} {opt} batch {cfg.batch} T={cfg.seq_len}: {steps} steps", flush=True)
     rng = np.random.default_rng(41)
     params, _, _ = trainer.synthetic_rnn(cfg, rng)
     sess = trainer.Session(cfg)
