@@ -102,5 +102,40 @@ namespace CppNet
             if (it == states_.end()) throw std::out_of_range("Adam: no state for this parameter");
             return it->second.v;
         }
+
+        bool Adam::get_state(const float* weights, int64_t n, std::vector<std::vector<float>>& tensors,
+                             int& t) const
+        {
+            auto it = states_.find(weights);
+            if (it == states_.end()) return false;
+            if (it->second.m.size() != n) throw std::invalid_argument("Adam::get_state: size mismatch");
+            tensors.assign(2, std::vector<float>(static_cast<size_t>(n)));
+            it->second.m.copy_to_host(tensors[0].data());
+            it->second.v.copy_to_host(tensors[1].data());
+            t = it->second.t;
+            return true;
+        }
+
+        void Adam::set_state(const float* weights, int64_t n, const std::vector<std::vector<float>>& tensors,
+                             int t)
+        {
+            if (tensors.size() != 2 || static_cast<int64_t>(tensors[0].size()) != n ||
+                static_cast<int64_t>(tensors[1].size()) != n || t < 0)
+                throw std::invalid_argument("Adam::set_state: expected m and v of the parameter's size");
+            if (!cnhip_is_device_pointer(weights))
+                throw std::invalid_argument("Adam::set_state: parameters must be device memory");
+            auto it = states_.find(weights);
+            if (it == states_.end())
+            {
+                State s;
+                s.m = DeviceTensor::empty({n});
+                s.v = DeviceTensor::empty({n});
+                it = states_.emplace(weights, std::move(s)).first;
+            }
+            if (it->second.m.size() != n) throw std::invalid_argument("Adam::set_state: size mismatch");
+            it->second.m.copy_from_host(tensors[0].data());
+            it->second.v.copy_from_host(tensors[1].data());
+            it->second.t = t;
+        }
     } // namespace Optimizers
 } // namespace CppNet

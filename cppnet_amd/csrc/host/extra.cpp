@@ -317,6 +317,41 @@ namespace CppNet
             return it->second;
         }
 
+        int DeviceOptimizer::state_tensors() const { return kind_ == CNHIP_OPT_SGD ? 0 : 1; }
+
+        bool DeviceOptimizer::get_state(const float* weights, int64_t n, std::vector<std::vector<float>>& tensors,
+                                        int& t) const
+        {
+            auto it = states_.find(weights);
+            if (it == states_.end()) return false;
+            t = 0;
+            tensors.clear();
+            if (kind_ == CNHIP_OPT_SGD) return true;
+            if (it->second.size() != n) throw std::invalid_argument(std::string(name_) + "::get_state: size mismatch");
+            tensors.assign(1, std::vector<float>(static_cast<size_t>(n)));
+            it->second.copy_to_host(tensors[0].data());
+            return true;
+        }
+
+        void DeviceOptimizer::set_state(const float* weights, int64_t n,
+                                        const std::vector<std::vector<float>>& tensors, int /*t*/)
+        {
+            const size_t want = static_cast<size_t>(state_tensors());
+            if (tensors.size() != want || (want == 1 && static_cast<int64_t>(tensors[0].size()) != n))
+                throw std::invalid_argument(std::string(name_) + "::set_state: state does not match the parameter");
+            if (!cnhip_is_device_pointer(weights))
+                throw std::invalid_argument(std::string(name_) + "::set_state: parameters must be device memory");
+            auto it = states_.find(weights);
+            if (it == states_.end())
+                it = states_.emplace(weights, want ? DeviceTensor::empty({n}) : DeviceTensor()).first;
+            if (want)
+            {
+                if (it->second.size() != n)
+                    throw std::invalid_argument(std::string(name_) + "::set_state: size mismatch");
+                it->second.copy_from_host(tensors[0].data());
+            }
+        }
+
         SGD::SGD(const std::string& device, int gpu_block_size)
             : DeviceOptimizer(CNHIP_OPT_SGD, 0.0f, 0.0f, device, "SGD"), block_(gpu_block_size)
         {

@@ -2,6 +2,7 @@
 // CppNet-compatible classes and runs the reference harness's train step.
 #include "cppnet_train.h"
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <exception>
@@ -11,6 +12,8 @@
 #include <vector>
 
 #include "CppNet/CppNet.hpp"
+#include "CppNet/utils/serialization.hpp"
+#include "CppNet/utils/tensor_io.hpp"
 
 using namespace CppNet;
 
@@ -680,6 +683,88 @@ namespace
         s->updated = true;
     }
 } // namespace
+
+namespace
+{
+    std::vector<Layers::Layer*> file_layers(cnt_session* s)
+    {
+        check_session(s);
+        return s->all_layers();
+    }
+
+    const char* check_path(const char* path)
+    {
+        if (!path || !*path) throw std::invalid_argument("empty path");
+        return path;
+    }
+} // namespace
+
+int cnt_save_model(cnt_session* s, const char* path)
+{
+    return guarded("cnt_save_model", [&] {
+        check_session(s);
+        StreamScope scope(s);
+        Utils::save_layers(check_path(path), file_layers(s), nullptr, false);
+    });
+}
+
+int cnt_load_model(cnt_session* s, const char* path)
+{
+    return guarded("cnt_load_model", [&] {
+        check_session(s);
+        StreamScope scope(s);
+        Utils::load_layers(check_path(path), file_layers(s), nullptr, false);
+        Device::synchronize();
+    });
+}
+
+int cnt_save_checkpoint(cnt_session* s, const char* path)
+{
+    return guarded("cnt_save_checkpoint", [&] {
+        check_session(s);
+        StreamScope scope(s);
+        Utils::save_layers(check_path(path), file_layers(s), s->opt.get(), true);
+    });
+}
+
+int cnt_load_checkpoint(cnt_session* s, const char* path)
+{
+    return guarded("cnt_load_checkpoint", [&] {
+        check_session(s);
+        StreamScope scope(s);
+        Utils::load_layers(check_path(path), file_layers(s), s->opt.get(), true);
+        Device::synchronize();
+        s->updated = true;  // the optimizer now holds state: no swap after this
+    });
+}
+
+int cnt_npy_save(const char* path, const float* colmajor, int ndims, const int64_t* dims)
+{
+    return guarded("cnt_npy_save", [&] {
+        if (ndims < 1 || !dims) throw std::invalid_argument("rank must be at least 1");
+        int64_t n = 1;
+        for (int i = 0; i < ndims; ++i) n *= dims[i];
+        if (n > 0 && !colmajor) throw std::invalid_argument("NULL data");
+        Utils::save_npy_raw(check_path(path), colmajor, std::vector<int64_t>(dims, dims + ndims));
+    });
+}
+
+int cnt_npy_load(const char* path, float* out, int64_t capacity, int* ndims, int64_t* dims, int raw_colmajor)
+{
+    return guarded("cnt_npy_load", [&] {
+        if (!ndims || !dims) throw std::invalid_argument("NULL ndims or dims");
+        std::vector<int64_t> d;
+        std::vector<float> v = Utils::load_npy_raw(check_path(path), d, raw_colmajor != 0);
+        if (static_cast<int>(d.size()) > *ndims)
+            throw std::invalid_argument("the file's rank " + std::to_string(d.size()) + " exceeds the dims capacity");
+        if (static_cast<int64_t>(v.size()) > capacity || (!v.empty() && !out))
+            throw std::invalid_argument("the file holds " + std::to_string(v.size()) + " floats, capacity " +
+                                        std::to_string(capacity));
+        *ndims = static_cast<int>(d.size());
+        for (std::size_t i = 0; i < d.size(); ++i) dims[i] = d[i];
+        if (!v.empty()) std::copy(v.begin(), v.end(), out);
+    });
+}
 
 int cnt_set_optimizer(cnt_session* s, int kind, float hyper, float eps)
 {

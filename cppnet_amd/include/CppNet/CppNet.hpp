@@ -8,6 +8,8 @@
 #include "CppNet/core/device.hpp"
 #include "CppNet/core/tensor.hpp"
 #include "CppNet/utils/init.hpp"
+#include "CppNet/utils/serialization.hpp"
+#include "CppNet/utils/tensor_io.hpp"
 #include "CppNet/layers/layer.hpp"
 #include "CppNet/layers/linear.hpp"
 #include "CppNet/layers/conv2d.hpp"

@@ -38,6 +38,7 @@ namespace CppNet
             void step(Optimizers::Optimizer& optimizer, float learning_rate) override;
             void reset_grads() override;
             std::size_t num_block_layers() const { return block_.size(); }
+            Layer* block_layer(std::size_t i) const { return block_.at(i).get(); }
             bool has_projection() const { return projection_ != nullptr; }
             Linear* projection() { return projection_.get(); }
 

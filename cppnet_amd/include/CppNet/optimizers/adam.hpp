@@ -40,6 +40,13 @@ namespace CppNet
             const DeviceTensor& first_moment(const float* weights) const;
             const DeviceTensor& second_moment(const float* weights) const;
 
+            int kind_code() const override { return 0; }
+            int state_tensors() const override { return 2; }  // m, v
+            bool get_state(const float* weights, int64_t n, std::vector<std::vector<float>>& tensors,
+                           int& t) const override;
+            void set_state(const float* weights, int64_t n, const std::vector<std::vector<float>>& tensors,
+                           int t) override;
+
         private:
             struct State
             {

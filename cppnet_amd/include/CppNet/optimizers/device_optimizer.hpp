@@ -34,6 +34,13 @@ namespace CppNet
             /// The per-key state tensor (velocity / accumulator / mean square).
             const DeviceTensor& state(const float* weights) const;
 
+            int kind_code() const override { return 1 + kind_; }  // 1 SGD, 2 Momentum, 3 Adagrad, 4 RMSProp
+            int state_tensors() const override;
+            bool get_state(const float* weights, int64_t n, std::vector<std::vector<float>>& tensors,
+                           int& t) const override;
+            void set_state(const float* weights, int64_t n, const std::vector<std::vector<float>>& tensors,
+                           int t) override;
+
         protected:
             DeviceOptimizer(int kind, float hyper, float epsilon, const std::string& device, const char* name);
 

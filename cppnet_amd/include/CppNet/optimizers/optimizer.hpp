@@ -12,6 +12,7 @@
 #define CPPNET_OPTIMIZERS_OPTIMIZER_HPP
 
 #include <cstdint>
+#include <vector>
 
 namespace CppNet
 {
@@ -30,6 +31,26 @@ namespace CppNet
             virtual void begin_group() {}
             virtual void end_group() {}
             virtual ~Optimizer() = default;
+
+            // Checkpoint support (Utils::save_checkpoint; no counterpart in the
+            // reference, whose model files hold weights only).  kind_code()
+            // names the algorithm in a checkpoint (-1: none saved),
+            // state_tensors() is how many n-float tensors it keeps per
+            // parameter.  get_state fills host copies of the state kept for
+            // the parameter at `weights` and its step count, and returns false
+            // when that parameter has none yet; set_state installs such a
+            // state (synchronously).
+            virtual int kind_code() const { return -1; }
+            virtual int state_tensors() const { return 0; }
+            virtual bool get_state(const float* /*weights*/, int64_t /*n*/,
+                                   std::vector<std::vector<float>>& /*tensors*/, int& /*t*/) const
+            {
+                return false;
+            }
+            virtual void set_state(const float* /*weights*/, int64_t /*n*/,
+                                   const std::vector<std::vector<float>>& /*tensors*/, int /*t*/)
+            {
+            }
         };
     } // namespace Optimizers
 } // namespace CppNet

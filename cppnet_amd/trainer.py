@@ -45,6 +45,12 @@ def load() -> C.CDLL:
         "cnt_set_batch_tokens": (i32, [vp, vp, vp]),
         "cnt_destroy": (i32, [vp]),
         "cnt_set_optimizer": (i32, [vp, i32, f32, f32]),
+        "cnt_save_model": (i32, [vp, C.c_char_p]),
+        "cnt_load_model": (i32, [vp, C.c_char_p]),
+        "cnt_save_checkpoint": (i32, [vp, C.c_char_p]),
+        "cnt_load_checkpoint": (i32, [vp, C.c_char_p]),
+        "cnt_npy_save": (i32, [C.c_char_p, vp, i32, C.POINTER(i64)]),
+        "cnt_npy_load": (i32, [C.c_char_p, vp, i64, C.POINTER(i32), C.POINTER(i64), i32]),
         "cnt_num_params": (i32, [vp, C.POINTER(i32)]),
         "cnt_param_size": (i32, [vp, i32, C.POINTER(i64)]),
         "cnt_set_param": (i32, [vp, i32, vp]),
@@ -415,6 +421,20 @@ class Session:
     def update(self) -> None:
         _check(load().cnt_update(self.h))
 
+    def save_model(self, path) -> None:
+        """The reference's CNET model file (weights of Linear / BatchNorm / Embedding)."""
+        _check(load().cnt_save_model(self.h, str(path).encode()))
+
+    def load_model(self, path) -> None:
+        _check(load().cnt_load_model(self.h, str(path).encode()))
+
+    def save_checkpoint(self, path) -> None:
+        """CNET records + every parameter and the optimizer state (exact resume)."""
+        _check(load().cnt_save_checkpoint(self.h, str(path).encode()))
+
+    def load_checkpoint(self, path) -> None:
+        _check(load().cnt_load_checkpoint(self.h, str(path).encode()))
+
     def synchronize(self) -> None:
         _check(load().cnt_synchronize(self.h))
 
@@ -430,3 +450,23 @@ class Session:
     @property
     def has_graph(self) -> bool:
         return bool(load().cnt_has_graph(self.h))
+
+
+def npy_save(path, colmajor: np.ndarray, dims) -> None:
+    """Writes float32 ColMajor data of shape dims as .npy (fortran_order True)."""
+    a = np.ascontiguousarray(colmajor, np.float32).ravel()
+    d = (C.c_int64 * len(dims))(*dims)
+    _check(load().cnt_npy_save(str(path).encode(), a.ctypes.data, len(dims), d))
+
+
+def npy_load(path, raw_colmajor: bool = False):
+    """Reads a float32 .npy file; returns (ColMajor flat data, dims)."""
+    import os
+    cap = max(os.path.getsize(path) // 4, 1)
+    out = np.empty(cap, np.float32)
+    nd = C.c_int(16)
+    dims = (C.c_int64 * 16)()
+    _check(load().cnt_npy_load(str(path).encode(), out.ctypes.data, cap, C.byref(nd), dims,
+                               1 if raw_colmajor else 0))
+    d = [int(dims[i]) for i in range(nd.value)]
+    return out[:int(np.prod(d))].copy(), d

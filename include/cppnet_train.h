@@ -131,6 +131,34 @@ int cnt_capture_step(cnt_session* s);
 int cnt_release_graph(cnt_session* s);
 int cnt_has_graph(cnt_session* s); /* 1 while a captured graph is live */
 int cnt_synchronize(cnt_session* s);
+
+/* Model files.  cnt_save_model / cnt_load_model: the reference's "CNET"
+ * format exactly (Utils::save_model / load_model,
+ * ref: src/CppNet/utils/serialization.cpp:143-256): magic 0x434E4554, the
+ * layer count, then per trainable layer a type id (Linear 1: W [in, out],
+ * b; BatchNorm 2: gamma, beta, running mean, running var; Embedding 3: the
+ * [vocab, dim] table; other 0, no data) with int32-ndims/dims + float32
+ * ColMajor records.  cnt_save_checkpoint / cnt_load_checkpoint write the
+ * same records followed by an extension the reference's reader ignores:
+ * every parameter's values and the optimizer's per-parameter state and step
+ * counts, so a loaded session continues exactly as the saved one would have
+ * (no counterpart in the reference, whose files hold weights only). */
+int cnt_save_model(cnt_session* s, const char* path);
+int cnt_load_model(cnt_session* s, const char* path);
+int cnt_save_checkpoint(cnt_session* s, const char* path);
+int cnt_load_checkpoint(cnt_session* s, const char* path);
+
+/* .npy v1.0 float32 files (Utils::save_npy / load_npy_*,
+ * ref: src/CppNet/utils/tensor_io.cpp:29-170).  Data is ColMajor; the writer
+ * says 'fortran_order': True so that numpy.load returns the logical array
+ * (the reference writes the same bytes under False).  The reader follows the
+ * file's flag, reordering C-order data into ColMajor; raw_colmajor = 1 takes
+ * the bytes as ColMajor whatever the flag (files the reference wrote).
+ * cnt_npy_load: on entry *ndims is the capacity of dims and capacity that of
+ * out (floats); on return they hold the rank, shape and data.  Host-only. */
+int cnt_npy_save(const char* path, const float* colmajor, int ndims, const int64_t* dims);
+int cnt_npy_load(const char* path, float* out, int64_t capacity, int* ndims, int64_t* dims,
+                 int raw_colmajor);
 /* The hipStream_t the session's kernels run on. */
 void* cnt_stream(cnt_session* s);
 
