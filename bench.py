@@ -173,6 +173,60 @@ def traffic_calibration() -> int:
     return 0
 
 
+def loader_leg(sess, cfg, B, steps, step_ms, mode):
+    """`steps` train steps whose batches come from a DataLoader over a synthetic
+    dataset of 16 batches (reshuffled at each epoch's end, inside the timed
+    region), with the step's inputs delivered by cnt_loader_next_batch."""
+    import ctypes as C
+
+    import numpy as np
+    from cppnet_amd import _capi, trainer
+
+    lib = _capi.load()
+    nb = 16
+    F = sess.x_size // B
+    L = sess.y_size // B
+    N = nb * B
+    rng = np.random.default_rng(7)
+    Xd = rng.standard_normal(N * F, dtype=np.float32)
+    Yd = np.zeros((N, L), np.float32)
+    Yd[np.arange(N), rng.integers(0, L, N)] = 1.0  # one-hot rows (valid for every loss here)
+    ld = trainer.Loader(Xd, Yd.ravel(order="F"), N, F, L, B, True, True, seed=3)
+    ld.to_device(mode)
+
+    def feed():
+        if ld.next_batch(sess) == 0:
+            ld.reset()
+            ld.next_batch(sess)
+
+    for _ in range(3):
+        feed()
+        sess.step(read_loss=False)
+    sess.synchronize()
+    ev0, ev1 = C.c_void_p(), C.c_void_p()
+    _capi.check(lib.cnhip_event_create(C.byref(ev0)))
+    _capi.check(lib.cnhip_event_create(C.byref(ev1)))
+    t0 = time.perf_counter()
+    _capi.check(lib.cnhip_event_record(ev0, sess.stream))
+    for _ in range(steps):
+        feed()
+        sess.step(read_loss=False)
+    _capi.check(lib.cnhip_event_record(ev1, sess.stream))
+    sess.synchronize()
+    wall = time.perf_counter() - t0
+    ms = C.c_float()
+    _capi.check(lib.cnhip_event_elapsed_ms(C.byref(ms), ev0, ev1))
+    per = max(ms.value, wall * 1e3) / steps  # the host side can be the longer clock
+    ld.close()
+    out = {"mode": mode, "samples_per_s": round(B / (per * 1e-3), 1), "ms_per_step": round(per, 4),
+           "vs_resident_inputs": round(step_ms / per, 3), "dataset_batches": nb,
+           "bytes_per_batch": B * (F + L) * 4}
+    if mode == "stream":
+        out["host_to_device_GBs_needed"] = round(B * (F + L) * 4 / (per * 1e-3) / 1e9, 2)
+    log(f"bench.py: loader {mode}: {per:.4f} ms/step ({out['vs_resident_inputs']:.3f} of resident inputs)")
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -189,6 +243,10 @@ def main() -> int:
                     help="only run the known-traffic reference kernel (cnhip_add over 64 Mi floats, "
                          "5 times: 512 MiB read + 256 MiB written per launch) that scales the PMC "
                          "FETCH_SIZE / WRITE_SIZE counts behind roofline.traffic")
+    ap.add_argument("--loader", choices=["resident", "stream", "both"], default=None,
+                    help="also time the same steps fed by the DataLoader (configs 1-4): 'resident' "
+                         "gathers each batch in HBM, 'stream' uploads it from page-locked host "
+                         "memory on a copy stream; reported under 'loader', never as 'value'")
     args = ap.parse_args()
     if args.traffic_calibration:
         return traffic_calibration()
@@ -316,6 +374,9 @@ def main() -> int:
                         "kernels": hbm_kernels},
         "cpu_baseline": None,
     }
+    if args.loader and args.config != 5:
+        modes = ["resident", "stream"] if args.loader == "both" else [args.loader]
+        result["loader"] = [loader_leg(sess, cfg, B, steps, step_ms, m) for m in modes]
     sess.close()
     if not args.no_cpu_baseline:
         try:

@@ -38,6 +38,11 @@ SIGNATURES: dict[str, tuple] = {
     "cnhip_event_destroy": (i32, [vp]),
     "cnhip_event_record": (i32, [vp, vp]),
     "cnhip_event_elapsed_ms": (i32, [C.POINTER(f32), vp, vp]),
+    "cnhip_event_synchronize": (i32, [vp]),
+    "cnhip_stream_wait_event": (i32, [vp, vp]),
+    "cnhip_get_device": (i32, [C.POINTER(i32)]),
+    "cnhip_host_alloc": (i32, [C.POINTER(vp), C.c_size_t]),
+    "cnhip_host_free": (i32, [vp]),
     "cnhip_graph_begin_capture": (i32, [vp]),
     "cnhip_graph_end_capture": (i32, [vp, i32, C.POINTER(vp)]),
     "cnhip_graph_launch": (i32, [vp, vp]),
@@ -68,6 +73,8 @@ SIGNATURES: dict[str, tuple] = {
     "cnhip_seq_select": (i32, [vp, vp, i64, i64, i64, i64, vp]),
     "cnhip_seq_scatter": (i32, [vp, vp, i64, i64, i64, i64, vp]),
     "cnhip_transpose": (i32, [vp, vp, i64, i64, vp]),
+    "cnhip_gather_rows": (i32, [vp, vp, vp, i64, i64, i64, vp]),
+    "cnhip_gather_batch": (i32, [vp, vp, vp, vp, vp, i64, i64, i64, i64, vp]),
     "cnhip_mha_cache_floats": (i64, [i64, i64, i64]),
     "cnhip_mha_forward": (i32, [vp] * 9 + [i64] * 4 + [vp]),
     "cnhip_mha_backward": (i32, [vp] * 14 + [i64] * 4 + [vp]),

@@ -14,6 +14,7 @@
 #include "CppNet/CppNet.hpp"
 #include "CppNet/utils/serialization.hpp"
 #include "CppNet/utils/tensor_io.hpp"
+#include "CppNet/utils/dataloader.hpp"
 
 using namespace CppNet;
 
@@ -735,6 +736,130 @@ int cnt_load_checkpoint(cnt_session* s, const char* path)
         Utils::load_layers(check_path(path), file_layers(s), s->opt.get(), true);
         Device::synchronize();
         s->updated = true;  // the optimizer now holds state: no swap after this
+    });
+}
+
+struct cnt_loader
+{
+    std::unique_ptr<Utils::DataLoader> dl;
+    int64_t F = 0, L = 0;
+};
+
+namespace
+{
+    Utils::DataLoader& loader_of(cnt_loader* ld)
+    {
+        if (!ld || !ld->dl) throw std::invalid_argument("NULL loader");
+        return *ld->dl;
+    }
+} // namespace
+
+int cnt_loader_create(cnt_loader** out, const float* features, const float* labels, int64_t n, int64_t f,
+                      int64_t l, int64_t batch, int shuffle, int drop_last, uint64_t seed)
+{
+    return guarded("cnt_loader_create", [&] {
+        if (!out) throw std::invalid_argument("NULL out pointer");
+        *out = nullptr;
+        if (n < 0 || f <= 0 || l <= 0 || n > INT32_MAX || batch > INT32_MAX)
+            throw std::invalid_argument("bad dataset shape");
+        if (n > 0 && (!features || !labels)) throw std::invalid_argument("NULL data");
+        Tensor<float, 2> X(n, f), Y(n, l);
+        if (n) std::copy(features, features + n * f, X.data());
+        if (n) std::copy(labels, labels + n * l, Y.data());
+        auto ld = std::make_unique<cnt_loader>();
+        ld->dl = std::make_unique<Utils::DataLoader>(X, Y, static_cast<int>(batch), shuffle != 0, drop_last != 0);
+        ld->dl->set_seed(seed);
+        ld->F = f;
+        ld->L = l;
+        *out = ld.release();
+    });
+}
+
+int cnt_loader_destroy(cnt_loader* ld)
+{
+    return guarded("cnt_loader_destroy", [&] { delete ld; });
+}
+
+int cnt_loader_num_batches(cnt_loader* ld, int64_t* count)
+{
+    return guarded("cnt_loader_num_batches", [&] {
+        if (!count) throw std::invalid_argument("NULL out pointer");
+        *count = static_cast<int64_t>(loader_of(ld).num_batches());
+    });
+}
+
+int cnt_loader_indices(cnt_loader* ld, int32_t* out)
+{
+    return guarded("cnt_loader_indices", [&] {
+        const auto& v = loader_of(ld).indices();
+        if (!v.empty() && !out) throw std::invalid_argument("NULL out pointer");
+        std::copy(v.begin(), v.end(), out);
+    });
+}
+
+int cnt_loader_reset(cnt_loader* ld)
+{
+    return guarded("cnt_loader_reset", [&] { loader_of(ld).reset(); });
+}
+
+int cnt_loader_host_batch(cnt_loader* ld, int64_t k, float* x, float* y, int64_t* bs)
+{
+    return guarded("cnt_loader_host_batch", [&] {
+        if (!x || !y || !bs) throw std::invalid_argument("NULL argument");
+        if (k < 0) throw std::out_of_range("DataLoader: batch index out of range");
+        Utils::Batch b = loader_of(ld).get_batch(static_cast<std::size_t>(k));
+        *bs = b.features.dimension(0);
+        std::copy(b.features.data(), b.features.data() + b.features.size(), x);
+        std::copy(b.labels.data(), b.labels.data() + b.labels.size(), y);
+    });
+}
+
+int cnt_loader_to_device(cnt_loader* ld, int mode)
+{
+    return guarded("cnt_loader_to_device", [&] {
+        if (mode != CNT_STAGE_RESIDENT && mode != CNT_STAGE_STREAM)
+            throw std::invalid_argument("mode must be CNT_STAGE_RESIDENT or CNT_STAGE_STREAM");
+        loader_of(ld).to_device(mode == CNT_STAGE_RESIDENT ? Utils::Staging::Resident : Utils::Staging::Stream);
+    });
+}
+
+int cnt_loader_next(cnt_loader* ld, float* x_dev, float* y_dev, int64_t* bs, void* stream)
+{
+    return guarded("cnt_loader_next", [&] {
+        if (!bs) throw std::invalid_argument("NULL bs");
+        Utils::DataLoader& dl = loader_of(ld);
+        const cnhip_stream_t saved = Device::stream();
+        Device::set_stream(static_cast<cnhip_stream_t>(stream));
+        try
+        {
+            *bs = dl.next_into(x_dev, y_dev);
+        }
+        catch (...)
+        {
+            Device::set_stream(saved);
+            throw;
+        }
+        Device::set_stream(saved);
+    });
+}
+
+int cnt_loader_next_batch(cnt_loader* ld, cnt_session* s, int64_t* bs)
+{
+    return guarded("cnt_loader_next_batch", [&] {
+        check_session(s);
+        if (!bs) throw std::invalid_argument("NULL bs");
+        Utils::DataLoader& dl = loader_of(ld);
+        if (s->encoder) throw std::invalid_argument("token-id sessions take cnt_set_batch_tokens");
+        const int64_t next = dl.next_size();
+        *bs = 0;
+        if (next == 0) return;
+        if (s->X.dimension(0) != next || s->X.size() != next * ld->F || s->Y.size() != next * ld->L)
+            throw std::invalid_argument("the loader's next batch is " + std::to_string(next) + " x (" +
+                                        std::to_string(ld->F) + ", " + std::to_string(ld->L) +
+                                        ") but the session's batch is X " + shape_str(s->X.dims()) + ", Y " +
+                                        shape_str(s->Y.dims()) + " (use drop_last or a dividing batch size)");
+        StreamScope scope(s);
+        *bs = dl.next_into(s->X.data(), s->Y.data());
     });
 }
 

@@ -148,6 +148,23 @@ int cnhip_device_count(void) {
 
 int cnhip_set_device(int device) { return check_hip(hipSetDevice(device), "cnhip_set_device"); }
 
+int cnhip_get_device(int* device) {
+  CNHIP_REQUIRE(device, "cnhip_get_device: NULL out pointer");
+  return check_hip(hipGetDevice(device), "cnhip_get_device");
+}
+
+int cnhip_host_alloc(void** ptr, size_t bytes) {
+  CNHIP_REQUIRE(ptr != nullptr, "cnhip_host_alloc: ptr is NULL");
+  *ptr = nullptr;
+  if (bytes == 0) return CNHIP_OK;
+  return check_hip(hipHostMalloc(ptr, bytes, hipHostMallocDefault), "cnhip_host_alloc");
+}
+
+int cnhip_host_free(void* ptr) {
+  if (!ptr) return CNHIP_OK;
+  return check_hip(hipHostFree(ptr), "cnhip_host_free");
+}
+
 int cnhip_malloc(void** ptr, size_t bytes) {
   CNHIP_REQUIRE(ptr != nullptr, "cnhip_malloc: ptr is NULL");
   *ptr = nullptr;
@@ -229,6 +246,17 @@ int cnhip_event_record(void* event, cnhip_stream_t stream) {
   CNHIP_REQUIRE(event, "cnhip_event_record: NULL event");
   return check_hip(hipEventRecord(reinterpret_cast<hipEvent_t>(event), as_stream(stream)),
                    "cnhip_event_record");
+}
+
+int cnhip_event_synchronize(void* event) {
+  CNHIP_REQUIRE(event, "cnhip_event_synchronize: NULL event");
+  return check_hip(hipEventSynchronize(reinterpret_cast<hipEvent_t>(event)), "cnhip_event_synchronize");
+}
+
+int cnhip_stream_wait_event(cnhip_stream_t stream, void* event) {
+  CNHIP_REQUIRE(event, "cnhip_stream_wait_event: NULL event");
+  return check_hip(hipStreamWaitEvent(as_stream(stream), reinterpret_cast<hipEvent_t>(event), 0),
+                   "cnhip_stream_wait_event");
 }
 
 int cnhip_event_elapsed_ms(float* ms, void* start, void* stop) {

@@ -10,6 +10,7 @@
 #include "CppNet/utils/init.hpp"
 #include "CppNet/utils/serialization.hpp"
 #include "CppNet/utils/tensor_io.hpp"
+#include "CppNet/utils/dataloader.hpp"
 #include "CppNet/layers/layer.hpp"
 #include "CppNet/layers/linear.hpp"
 #include "CppNet/layers/conv2d.hpp"

@@ -49,6 +49,15 @@ def load() -> C.CDLL:
         "cnt_load_model": (i32, [vp, C.c_char_p]),
         "cnt_save_checkpoint": (i32, [vp, C.c_char_p]),
         "cnt_load_checkpoint": (i32, [vp, C.c_char_p]),
+        "cnt_loader_create": (i32, [C.POINTER(vp), vp, vp, i64, i64, i64, i64, i32, i32, C.c_uint64]),
+        "cnt_loader_destroy": (i32, [vp]),
+        "cnt_loader_num_batches": (i32, [vp, C.POINTER(i64)]),
+        "cnt_loader_indices": (i32, [vp, vp]),
+        "cnt_loader_reset": (i32, [vp]),
+        "cnt_loader_host_batch": (i32, [vp, i64, vp, vp, C.POINTER(i64)]),
+        "cnt_loader_to_device": (i32, [vp, i32]),
+        "cnt_loader_next": (i32, [vp, vp, vp, C.POINTER(i64), vp]),
+        "cnt_loader_next_batch": (i32, [vp, vp, C.POINTER(i64)]),
         "cnt_npy_save": (i32, [C.c_char_p, vp, i32, C.POINTER(i64)]),
         "cnt_npy_load": (i32, [C.c_char_p, vp, i64, C.POINTER(i32), C.POINTER(i64), i32]),
         "cnt_num_params": (i32, [vp, C.POINTER(i32)]),
@@ -470,3 +479,67 @@ def npy_load(path, raw_colmajor: bool = False):
                                1 if raw_colmajor else 0))
     d = [int(dims[i]) for i in range(nd.value)]
     return out[:int(np.prod(d))].copy(), d
+
+
+STAGE = {"resident": 1, "stream": 2}
+
+
+class Loader:
+    """Utils::DataLoader through the C ABI: features [N, F] and labels [N, L]
+    as ColMajor flat float32 (Eigen's order)."""
+
+    def __init__(self, features, labels, n, f, l, batch, shuffle=True, drop_last=False, seed=0):
+        lib = load()
+        self._x = np.ascontiguousarray(features, np.float32).ravel()
+        self._y = np.ascontiguousarray(labels, np.float32).ravel()
+        assert self._x.size == n * f and self._y.size == n * l
+        h = C.c_void_p()
+        _check(lib.cnt_loader_create(C.byref(h), self._x.ctypes.data, self._y.ctypes.data, n, f, l, batch,
+                                     int(shuffle), int(drop_last), seed))
+        self.h, self.n, self.f, self.l, self.batch = h, n, f, l, batch
+
+    def close(self):
+        if self.h:
+            _check(load().cnt_loader_destroy(self.h))
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def num_batches(self) -> int:
+        c = C.c_int64()
+        _check(load().cnt_loader_num_batches(self.h, C.byref(c)))
+        return c.value
+
+    def indices(self) -> np.ndarray:
+        out = np.empty(self.n, np.int32)
+        _check(load().cnt_loader_indices(self.h, out.ctypes.data))
+        return out
+
+    def reset(self) -> None:
+        _check(load().cnt_loader_reset(self.h))
+
+    def host_batch(self, k: int):
+        x = np.empty(self.batch * self.f, np.float32)
+        y = np.empty(self.batch * self.l, np.float32)
+        bs = C.c_int64()
+        _check(load().cnt_loader_host_batch(self.h, k, x.ctypes.data, y.ctypes.data, C.byref(bs)))
+        return x[:bs.value * self.f].copy(), y[:bs.value * self.l].copy(), bs.value
+
+    def to_device(self, mode: str) -> None:
+        _check(load().cnt_loader_to_device(self.h, STAGE[mode]))
+
+    def next(self, x_ptr: int, y_ptr: int, stream: int = 0) -> int:
+        """The epoch's next batch into device buffers; returns its size (0 at the end)."""
+        bs = C.c_int64()
+        _check(load().cnt_loader_next(self.h, x_ptr, y_ptr, C.byref(bs), stream))
+        return bs.value
+
+    def next_batch(self, sess: "Session") -> int:
+        bs = C.c_int64()
+        _check(load().cnt_loader_next_batch(self.h, sess.h, C.byref(bs)))
+        return bs.value

@@ -65,6 +65,13 @@ int cnhip_event_create(void** event);
 int cnhip_event_destroy(void* event);
 int cnhip_event_record(void* event, cnhip_stream_t stream);
 int cnhip_event_elapsed_ms(float* ms, void* start, void* stop); /* syncs stop */
+int cnhip_event_synchronize(void* event);
+/* Work enqueued on stream after this call waits for event's work. */
+int cnhip_stream_wait_event(cnhip_stream_t stream, void* event);
+int cnhip_get_device(int* device);
+/* Page-locked host memory (hipHostMalloc), for asynchronous uploads. */
+int cnhip_host_alloc(void** ptr, size_t bytes);
+int cnhip_host_free(void* ptr);
 /* cnhip_memset_async fills with a kernel, so it can be recorded into a graph. */
 
 /* ---- graphs -------------------------------------------------------------
@@ -520,6 +527,17 @@ int cnhip_rnn_forward(const float* X, const float* W_ih, const float* W_hh, cons
 int cnhip_rnn_backward(const float* X, const float* W_ih, const float* W_hh, const float* Y,
                        const float* dY, float* gW_ih, float* gW_hh, float* gb, float* dX,
                        int64_t B, int64_t S, int64_t I, int64_t H, cnhip_stream_t stream);
+
+/* ---- DataLoader batch assembly (ref: dataloader.cpp:68-88) ----
+ * src: the dataset sample-major (sample n's F values at src + n*F), N
+ * samples; idx: B int32 sample indices (one outside [0, N) yields zeros);
+ * dst: the batch ColMajor [B, F], dst[b + B*f] = src[idx[b]*F + f]. */
+int cnhip_gather_rows(const float* src, const int32_t* idx, float* dst, int64_t N, int64_t F, int64_t B,
+                      cnhip_stream_t stream);
+/* Features and labels of one batch in one launch: xs [N samples x F] and
+ * ys [N x L] sample-major -> x [B, F], y [B, L] ColMajor. */
+int cnhip_gather_batch(const float* xs, const float* ys, const int32_t* idx, float* x, float* y, int64_t N,
+                       int64_t F, int64_t L, int64_t B, cnhip_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -156,6 +156,33 @@ int cnt_load_checkpoint(cnt_session* s, const char* path);
  * the bytes as ColMajor whatever the flag (files the reference wrote).
  * cnt_npy_load: on entry *ndims is the capacity of dims and capacity that of
  * out (floats); on return they hold the rank, shape and data.  Host-only. */
+/* DataLoader (Utils::DataLoader, ref: include/CppNet/utils/dataloader.hpp:46-109,
+ * src/CppNet/utils/dataloader.cpp:12-120): features [N, F] and labels [N, L]
+ * (host, ColMajor; copied), batch size, shuffle, drop_last; the shuffle is
+ * std::shuffle with a std::mt19937 seeded by `seed`.  cnt_loader_host_batch
+ * is the reference's batch k on the host (*bs = its size).  After
+ * cnt_loader_to_device (CNT_STAGE_RESIDENT: the dataset in HBM, batches
+ * gathered on the GPU; CNT_STAGE_STREAM: page-locked double-buffered uploads
+ * on a copy stream, overlapping the caller's work), cnt_loader_next writes the
+ * epoch's next batch ColMajor into device buffers on `stream`, and
+ * cnt_loader_next_batch into a session's batch (same as cnt_set_batch_device;
+ * MLP, CNN and sequence sessions: the session's batch size must match);
+ * *bs = 0 at the end of the epoch.  cnt_loader_reset reshuffles and
+ * restarts the epoch. */
+typedef struct cnt_loader cnt_loader;
+#define CNT_STAGE_RESIDENT 1
+#define CNT_STAGE_STREAM   2
+int cnt_loader_create(cnt_loader** out, const float* features, const float* labels, int64_t n,
+                      int64_t f, int64_t l, int64_t batch, int shuffle, int drop_last, uint64_t seed);
+int cnt_loader_destroy(cnt_loader* ld);
+int cnt_loader_num_batches(cnt_loader* ld, int64_t* count);
+int cnt_loader_indices(cnt_loader* ld, int32_t* out); /* the epoch's order, n entries */
+int cnt_loader_reset(cnt_loader* ld);
+int cnt_loader_host_batch(cnt_loader* ld, int64_t k, float* x, float* y, int64_t* bs);
+int cnt_loader_to_device(cnt_loader* ld, int mode);
+int cnt_loader_next(cnt_loader* ld, float* x_dev, float* y_dev, int64_t* bs, void* stream);
+int cnt_loader_next_batch(cnt_loader* ld, cnt_session* s, int64_t* bs);
+
 int cnt_npy_save(const char* path, const float* colmajor, int ndims, const int64_t* dims);
 int cnt_npy_load(const char* path, float* out, int64_t capacity, int* ndims, int64_t* dims,
                  int raw_colmajor);
