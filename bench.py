@@ -217,10 +217,26 @@ def loader_leg(sess, cfg, B, steps, step_ms, mode):
     ms = C.c_float()
     _capi.check(lib.cnhip_event_elapsed_ms(C.byref(ms), ev0, ev1))
     per = max(ms.value, wall * 1e3) / steps  # the host side can be the longer clock
+    gather = None
+    if mode == "resident":  # the batch-assembly kernel's own HBM rate, event-timed
+        _capi.check(lib.cnhip_hbm_timing_enable(1))
+        for _ in range(5):
+            feed()
+            sess.step(read_loss=False)
+        rows = [r for r in _capi.hbm_timing_rows() if r["kernel"] == "gather_rows_kernel"]
+        _capi.check(lib.cnhip_hbm_timing_enable(0))
+        if rows and rows[0]["total_ms"] > 0:
+            r = rows[0]
+            gbs = r["total_bytes"] / (r["total_ms"] * 1e-3) / 1e9
+            gather = {"kernel": "gather_rows_kernel", "avg_us": round(r["total_ms"] * 1e3 / r["launches"], 2),
+                      "bytes_per_launch": round(r["total_bytes"] / r["launches"]),
+                      "achieved_GBs": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4)}
     ld.close()
     out = {"mode": mode, "samples_per_s": round(B / (per * 1e-3), 1), "ms_per_step": round(per, 4),
            "vs_resident_inputs": round(step_ms / per, 3), "dataset_batches": nb,
            "bytes_per_batch": B * (F + L) * 4}
+    if gather:
+        out["gather_kernel"] = gather
     if mode == "stream":
         out["host_to_device_GBs_needed"] = round(B * (F + L) * 4 / (per * 1e-3) / 1e9, 2)
     log(f"bench.py: loader {mode}: {per:.4f} ms/step ({out['vs_resident_inputs']:.3f} of resident inputs)")

@@ -29,12 +29,14 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(const float* __restric
                                                           int ty0, const int32_t* __restrict__ idx,
                                                           int64_t N, int64_t B) {
   __shared__ float tile[kTile][kTile + 1];  // [sample][value], padded
-  const bool first = (int)blockIdx.y < ty0;
+  // value tiles vary fastest across the grid, so blocks that run together read
+  // neighbouring segments of the same 64 samples (DRAM row locality)
+  const bool first = (int)blockIdx.x < ty0;
   const float* __restrict__ src = first ? src0 : src1;
   float* __restrict__ dst = first ? dst0 : dst1;
   const int64_t F = first ? F0 : F1;
-  const int64_t b0 = (int64_t)blockIdx.x * kTile;
-  const int64_t f0 = (int64_t)(first ? blockIdx.y : blockIdx.y - ty0) * kTile;
+  const int64_t b0 = (int64_t)blockIdx.y * kTile;
+  const int64_t f0 = (int64_t)(first ? blockIdx.x : blockIdx.x - ty0) * kTile;
   const int t = threadIdx.x;
   // float4 reads need every sample segment 16-byte aligned
   const bool vec = (F % 4 == 0) && ((reinterpret_cast<uintptr_t>(src) & 15) == 0);
@@ -63,13 +65,26 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(const float* __restric
     }
   }
   __syncthreads();
-  const int lane = t & 63, frow = t >> 6;
-  const int64_t b = b0 + lane;
-  if (b < B)
-    for (int c = frow; c < kTile; c += 4) {
-      const int64_t f = f0 + c;
-      if (f < F) dst[b + B * f] = tile[lane][c];
-    }
+  if ((B % 4) == 0 && ((reinterpret_cast<uintptr_t>(dst) & 15) == 0)) {
+    // 16 lanes write one value's 64 samples as float4s; 16 values per pass
+    const int q = t & 15, frow = t >> 4;
+    const int64_t b = b0 + 4 * q;
+    if (b < B)  // B % 4 == 0, so b < B covers b..b+3
+      for (int c = frow; c < kTile; c += 16) {
+        const int64_t f = f0 + c;
+        if (f < F)
+          *reinterpret_cast<float4*>(dst + b + B * f) =
+              make_float4(tile[4 * q][c], tile[4 * q + 1][c], tile[4 * q + 2][c], tile[4 * q + 3][c]);
+      }
+  } else {
+    const int lane = t & 63, frow = t >> 6;
+    const int64_t b = b0 + lane;
+    if (b < B)
+      for (int c = frow; c < kTile; c += 4) {
+        const int64_t f = f0 + c;
+        if (f < F) dst[b + B * f] = tile[lane][c];
+      }
+  }
 }
 
 }  // namespace
@@ -87,11 +102,11 @@ static int gather_launch(const char* who, const float* src0, float* dst0, int64_
   CNHIP_REQUIRE(N > 0, "%s: gathering from an empty dataset", who);
   const int64_t gx = (B + cnhip::kTile - 1) / cnhip::kTile;
   const int64_t ty0 = (F0 + cnhip::kTile - 1) / cnhip::kTile, ty1 = (F1 + cnhip::kTile - 1) / cnhip::kTile;
-  CNHIP_REQUIRE(gx <= INT32_MAX && ty0 + ty1 <= 65535, "%s: batch %lld x %lld values is too large", who,
+  CNHIP_REQUIRE(gx <= 65535 && ty0 + ty1 <= INT32_MAX, "%s: batch %lld x %lld values is too large", who,
                 (long long)B, (long long)(F0 + F1));
   cnhip::HbmTimer timer("gather_rows_kernel", 8.0 * (double)B * (double)(F0 + F1) + 4.0 * (double)B,
                         as_stream(s));
-  hipLaunchKernelGGL(cnhip::gather_rows_kernel, dim3((unsigned)gx, (unsigned)(ty0 + ty1)), dim3(256), 0,
+  hipLaunchKernelGGL(cnhip::gather_rows_kernel, dim3((unsigned)(ty0 + ty1), (unsigned)gx), dim3(256), 0,
                      as_stream(s), src0, dst0, F0, src1, dst1, F1, (int)ty0, idx, N, B);
   return cnhip::check_launch(who);
 }
