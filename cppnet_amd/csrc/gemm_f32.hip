@@ -66,6 +66,8 @@ struct GemmArgs {
   int64_t k_per_split;   // multiple of KQ (hence of every tile's BK)
   float* partial;        // split-K workspace [batch][splits][M*N]; null = direct
   int splits;
+  float* colsum;         // small kernels only: colsum[n] (+)= sum_k op(B)(k, n), or null
+  int colsum_acc;        // 1: add to colsum, 0: overwrite
 };
 
 // Fused-activation epilogues (internal codes beyond the C ABI's NONE / RELU):
@@ -310,6 +312,66 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs g, int64_t 
     const int64_t m = e % g.M, n = e / g.M;
     float* C = g.C + bt * g.stride_c;
     C[m + g.ldc * n] = epilogue_value<true>(g, C, s, m, n);
+  }
+}
+
+// Tiny GEMMs (a few MFLOP: the 30-64-1 MLP's layers, a classifier head) are
+// latency-bound: an MFMA tile's k-loop and a split-K reduce launch cost more
+// than the arithmetic.  These SIMT kernels compute each output with plain
+// fp32 FMAs and the same epilogue as the tiled kernel (batches == 1).
+//   gemm_small_thread_kernel: one thread per output, k from 0 to K-1 (K <= 64);
+//   gemm_small_wave_kernel:   one wave per output, lane l takes k = l, l+64, ...
+//                             in order, then a fixed butterfly over the lanes.
+template <bool TA, bool TB>
+__device__ __forceinline__ float op_a(const GemmArgs& g, int64_t m, int64_t k) {
+  return TA ? g.A[k + g.lda * m] : g.A[m + g.lda * k];
+}
+template <bool TA, bool TB>
+__device__ __forceinline__ float op_b(const GemmArgs& g, int64_t k, int64_t n) {
+  return TB ? g.B[n + g.ldb * k] : g.B[k + g.ldb * n];
+}
+
+// With g.colsum set (a Linear layer's weight gradient, op(B) = dY), the
+// outputs of row m = 0 also sum their op(B) column: the bias gradient in the
+// same launch.
+template <bool TA, bool TB>
+__global__ void __launch_bounds__(256) gemm_small_thread_kernel(GemmArgs g) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= g.M * g.N) return;
+  const int64_t m = e % g.M, n = e / g.M;
+  const bool cs = g.colsum && m == 0;
+  float acc = 0.f, sum = 0.f;
+  for (int64_t k = 0; k < g.K; ++k) {
+    const float b = op_b<TA, TB>(g, k, n);
+    acc = fmaf(op_a<TA, TB>(g, m, k), b, acc);
+    if (cs) sum += b;
+  }
+  g.C[m + g.ldc * n] = epilogue_value<true>(g, g.C, acc, m, n);
+  if (cs) g.colsum[n] = g.colsum_acc ? g.colsum[n] + sum : sum;
+}
+
+template <bool TA, bool TB>
+__global__ void __launch_bounds__(256) gemm_small_wave_kernel(GemmArgs g) {
+  const int64_t e = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (e >= g.M * g.N) return;  // uniform per wave
+  const int64_t m = e % g.M, n = e / g.M;
+  const bool cs = g.colsum && m == 0;  // uniform per wave
+  float acc = 0.f, sum = 0.f;
+  for (int64_t k = lane; k < g.K; k += 64) {
+    const float b = op_b<TA, TB>(g, k, n);
+    acc = fmaf(op_a<TA, TB>(g, m, k), b, acc);
+    if (cs) sum += b;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+  if (cs) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+  }
+  if (lane == 0) {
+    g.C[m + g.ldc * n] = epilogue_value<true>(g, g.C, acc, m, n);
+    if (cs) g.colsum[n] = g.colsum_acc ? g.colsum[n] + sum : sum;
   }
 }
 
@@ -579,6 +641,49 @@ int gemm_f32_batched(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, 
                        C, ldc, stride_c, batches, bias, epilogue, nullptr, nullptr, 0, st, who);
 }
 
+// GEMMs up to this many flops and outputs take the SIMT kernels above
+constexpr double kSmallGemmFlops = 4.0e6;
+constexpr int64_t kSmallGemmOutputs = 1 << 16;
+
+static bool gemm_is_small(int64_t M, int64_t N, int64_t K, int64_t batches) {
+  return batches == 1 && K > 0 && 2.0 * (double)M * (double)N * (double)K <= kSmallGemmFlops &&
+         M * N <= kSmallGemmOutputs;
+}
+
+static int gemm_small(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float alpha,
+                      const float* A, int64_t lda, const float* B, int64_t ldb, float beta, float* C,
+                      int64_t ldc, const float* bias, int epilogue, const float* aux_in, float* aux_out,
+                      int64_t ld_aux, hipStream_t st, const char* who, float* colsum = nullptr,
+                      int colsum_acc = 0) {
+  GemmArgs g{};
+  g.colsum = colsum;
+  g.colsum_acc = colsum_acc;
+  g.M = M; g.N = N; g.K = K;
+  g.A = A; g.lda = lda; g.B = B; g.ldb = ldb;
+  g.C = C; g.ldc = ldc;
+  g.alpha = alpha; g.beta = beta; g.bias = bias; g.epilogue = epilogue;
+  g.aux_in = aux_in; g.aux_out = aux_out; g.ld_aux = ld_aux;
+  g.splits = 1;
+  TimingRec* rec = timing_slot(2.0 * (double)M * (double)N * (double)K);
+  if (rec) (void)hipEventRecord(rec->start, st);
+  const int64_t outs = M * N;
+  const bool wave = K > 64;
+  const dim3 grid((unsigned)(wave ? (outs + 3) / 4 : (outs + 255) / 256));
+#define CNHIP_SMALL(TA, TB)                                                                  \
+  if (wave)                                                                                  \
+    hipLaunchKernelGGL((gemm_small_wave_kernel<TA, TB>), grid, dim3(256), 0, st, g);         \
+  else                                                                                       \
+    hipLaunchKernelGGL((gemm_small_thread_kernel<TA, TB>), grid, dim3(256), 0, st, g);
+  if (trans_a) {
+    if (trans_b) { CNHIP_SMALL(true, true) } else { CNHIP_SMALL(true, false) }
+  } else {
+    if (trans_b) { CNHIP_SMALL(false, true) } else { CNHIP_SMALL(false, false) }
+  }
+#undef CNHIP_SMALL
+  if (rec) (void)hipEventRecord(rec->stop, st);
+  return check_launch(who);
+}
+
 int gemm_f32_core(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float alpha,
                   const float* A, int64_t lda, int64_t stride_a, const float* B, int64_t ldb,
                   int64_t stride_b, float beta, float* C, int64_t ldc, int64_t stride_c,
@@ -596,6 +701,10 @@ int gemm_f32_core(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, flo
     CNHIP_REQUIRE(ldb >= (trans_b ? N : K), "%s: ldb=%lld too small", who, (long long)ldb);
   }
   CNHIP_REQUIRE(batches <= 65535, "%s: batch count %lld exceeds 65535", who, (long long)batches);
+
+  if (gemm_is_small(M, N, K, batches))
+    return gemm_small(trans_a, trans_b, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, bias, epilogue,
+                      aux_in, aux_out, ld_aux, st, who);
 
   const Plan plan = plan_gemm(trans_a, trans_b, M, N, K, batches, 64);
   CNHIP_REQUIRE(plan.tiles < ((int64_t)1 << 30), "%s: GEMM too large", who);
@@ -649,6 +758,18 @@ int gemm_f32(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float al
              int64_t ldc, const float* bias, int epilogue, hipStream_t st, const char* who) {
   return gemm_f32_batched(trans_a, trans_b, M, N, K, alpha, A, lda, 0, B, ldb, 0, beta, C, ldc, 0,
                           1, bias, epilogue, st, who);
+}
+
+int linear_wgrad_small(const float* X, const float* dY, float* dW, float* db, int64_t batch,
+                       int64_t in_features, int64_t out_features, int accumulate, hipStream_t st,
+                       const char* who, bool* done) {
+  *done = false;
+  if (!gemm_is_small(in_features, out_features, batch, 1)) return CNHIP_OK;
+  CNHIP_REQUIRE(X && dY && dW, "%s: NULL pointer", who);
+  *done = true;
+  return gemm_small(1, 0, in_features, out_features, batch, 1.f, X, batch, dY, batch,
+                    accumulate ? 1.f : 0.f, dW, in_features, nullptr, CNHIP_EPI_NONE, nullptr, nullptr, 0,
+                    st, who, db, accumulate);
 }
 
 int gemm_f32_act(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, const float* A,

@@ -10,6 +10,9 @@
 
 namespace cnhip {
 
+int linear_wgrad_small(const float* X, const float* dY, float* dW, float* db, int64_t batch,
+                       int64_t in_features, int64_t out_features, int accumulate, hipStream_t st,
+                       const char* who, bool* done);
 int gemm_f32(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float alpha,
              const float* A, int64_t lda, const float* B, int64_t ldb, float beta, float* C,
              int64_t ldc, const float* bias, int epilogue, hipStream_t st, const char* who);
@@ -107,10 +110,16 @@ int cnhip_linear_backward(const float* X, const float* W, const float* dY, float
   const float beta = accumulate ? 1.f : 0.f;
   if (trainable) {
     CNHIP_REQUIRE(grad_W != nullptr, "%s: trainable layer needs grad_W", who);
-    // dW[I,O] (+)= X^T[I,B] * dY[B,O]
-    CNHIP_TRY(cnhip::gemm_f32(1, 0, in_features, out_features, batch, 1.f, X, batch, dY, batch,
-                              beta, grad_W, in_features, nullptr, CNHIP_EPI_NONE, st, who));
-    if (grad_b) CNHIP_TRY(cnhip::column_sum(dY, grad_b, batch, out_features, accumulate, st, who));
+    // dW[I,O] (+)= X^T[I,B] * dY[B,O]; db (+)= the column sums of dY (one
+    // launch for both when the GEMM is small enough for the SIMT kernels)
+    bool fused = false;
+    CNHIP_TRY(cnhip::linear_wgrad_small(X, dY, grad_W, grad_b, batch, in_features, out_features, accumulate,
+                                        st, who, &fused));
+    if (!fused) {
+      CNHIP_TRY(cnhip::gemm_f32(1, 0, in_features, out_features, batch, 1.f, X, batch, dY, batch,
+                                beta, grad_W, in_features, nullptr, CNHIP_EPI_NONE, st, who));
+      if (grad_b) CNHIP_TRY(cnhip::column_sum(dY, grad_b, batch, out_features, accumulate, st, who));
+    }
   }
   if (dX) {
     // dX[B,I] = dY[B,O] * W^T[O,I]
