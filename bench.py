@@ -352,7 +352,9 @@ def main() -> int:
                             "achieved_GBs": round(gbs, 1),
                             "frac": round(gbs / PEAK_HBM_GBS, 4)})
 
-    kernels = {3: "gemm_f32_kernel + conv_pixel/conv_wgrad_kernel (fp32 MFMA, all shapes of the step)",
+    kernels = {1: "gemm_small_thread/wave_kernel (SIMT fp32: the step's GEMMs are all <= 2 MFLOP and "
+                  "latency-bound; the config is launch-latency bound, not MFMA bound)",
+               3: "gemm_f32_kernel + conv_pixel/conv_wgrad_kernel (fp32 MFMA, all shapes of the step)",
                4: "gemm_f32_kernel + lstm_step_fwd/bwd_kernel (fp32 MFMA; the per-timestep recurrent "
                   "GEMM tiles with the cell update fused)"}.get(
         args.config, "gemm_f32_kernel (fp32 MFMA GEMM, all shapes of the step)")

@@ -164,6 +164,36 @@ __global__ void __launch_bounds__(256) bce_backward_kernel(const float* __restri
   }
 }
 
+// Sigmoid output layer + BinaryCrossEntropy, forward and backward, in one
+// single-block launch for small outputs: per element the four separate
+// kernels' arithmetic (SigmoidFwd, the BCE term, the BCE gradient, SigmoidBwd)
+// and the loss's per-thread partial sums over the same elements as
+// bce_forward_kernel, so every output is bit-identical to the four launches.
+__global__ void __launch_bounds__(RB) sigmoid_bce_head_kernel(const float* __restrict__ z,
+                                                              const float* __restrict__ t,
+                                                              float* __restrict__ p,
+                                                              float* __restrict__ loss,
+                                                              float* __restrict__ dz, int64_t n,
+                                                              int loss_reduction, int grad_reduction) {
+  __shared__ float smem[RB / 64];
+  const SigmoidFwd sig;
+  const SigmoidBwd dsig;
+  float s = 0.f;
+  for (int64_t i = threadIdx.x; i < n; i += RB) {
+    const float pv = sig(z[i]);
+    p[i] = pv;
+    const float pc = bce_clip(pv);
+    const float tv = t[i];
+    s += -(tv * logf(pc) + (1.0f - tv) * logf(1.0f - pc));
+    const float diff = pc - tv;
+    float gv = (float)((double)diff / ((double)pc * (1.0 - (double)pc)));
+    if (grad_reduction == CNHIP_REDUCE_MEAN) gv /= (float)n;
+    dz[i] = dsig(pv, gv);
+  }
+  const float tot = block_sum(s, smem);
+  if (threadIdx.x == 0) *loss = (loss_reduction == CNHIP_REDUCE_SUM) ? tot : tot / (float)n;
+}
+
 __global__ void __launch_bounds__(RB) mse_forward_kernel(const float* __restrict__ p,
                                                          const float* __restrict__ t,
                                                          float* __restrict__ loss, int64_t n,
@@ -292,6 +322,19 @@ int cnhip_bce_forward(const float* pred, const float* target, float* loss, int64
   cnhip::HbmTimer timer("bce_forward_kernel", 8.0 * (double)n + 4.0, as_stream(s));
   hipLaunchKernelGGL(cnhip::bce_forward_kernel, dim3(1), dim3(cnhip::RB), 0, as_stream(s), pred,
                      target, loss, n, reduction);
+  return cnhip::check_launch(who);
+}
+
+int cnhip_sigmoid_bce_head(const float* z, const float* target, float* p, float* loss, float* dz, int64_t n,
+                           int loss_reduction, int grad_reduction, cnhip_stream_t s) {
+  const char* who = "cnhip_sigmoid_bce_head";
+  CNHIP_TRY(cnhip::check_reduction(loss_reduction, who));
+  CNHIP_TRY(cnhip::check_reduction(grad_reduction, who));
+  CNHIP_REQUIRE(n > 0, "%s: empty input", who);
+  CNHIP_REQUIRE(z && target && p && loss && dz, "%s: NULL pointer", who);
+  cnhip::HbmTimer timer("sigmoid_bce_head_kernel", 16.0 * (double)n + 4.0, as_stream(s));
+  hipLaunchKernelGGL(cnhip::sigmoid_bce_head_kernel, dim3(1), dim3(cnhip::RB), 0, as_stream(s), z, target, p,
+                     loss, dz, n, loss_reduction, grad_reduction);
   return cnhip::check_launch(who);
 }
 

@@ -85,7 +85,7 @@ namespace CppNet
         {
             require_same_shape(p, t, "BinaryCrossEntropy::forward");
             // "none" returns the mean, as the reference's forward does.
-            const int red = reduction_ == "sum" ? CNHIP_REDUCE_SUM : CNHIP_REDUCE_MEAN;
+            const int red = forward_reduction();
             DeviceTensor loss = DeviceTensor::empty({1});
             Device::check(cnhip_bce_forward(p.data(), t.data(), loss.data(), p.size(), red,
                                             Device::stream()),
@@ -97,7 +97,7 @@ namespace CppNet
         {
             require_same_shape(p, t, "BinaryCrossEntropy::backward");
             // only "mean" divides the gradient by the element count
-            const int red = reduction_ == "mean" ? CNHIP_REDUCE_MEAN : CNHIP_REDUCE_SUM;
+            const int red = backward_reduction();
             DeviceTensor g = DeviceTensor::empty(p.dims());
             Device::check(cnhip_bce_backward(p.data(), t.data(), g.data(), p.size(), red,
                                              Device::stream()),

@@ -16,12 +16,20 @@ namespace CppNet
             steps_.push_back(std::make_shared<detail::ActivationStep>(std::move(activation)));
         }
 
-        DeviceTensor SequentialModel::forward(const DeviceTensor& input)
+        DeviceTensor SequentialModel::forward(const DeviceTensor& input) { return forward_prefix(input, steps_.size()); }
+
+        Activations::Activation* SequentialModel::last_activation() const
         {
+            return steps_.empty() ? nullptr : steps_.back()->activation();
+        }
+
+        DeviceTensor SequentialModel::forward_prefix(const DeviceTensor& input, std::size_t count)
+        {
+            if (count > steps_.size()) throw std::out_of_range("SequentialModel::forward_prefix: too many steps");
             DeviceTensor x = input;
-            for (std::size_t i = 0; i < steps_.size(); ++i)
+            for (std::size_t i = 0; i < count; ++i)
             {
-                Activations::Activation* next = i + 1 < steps_.size() ? steps_[i + 1]->activation() : nullptr;
+                Activations::Activation* next = i + 1 < count ? steps_[i + 1]->activation() : nullptr;
                 if (auto* relu = dynamic_cast<Activations::ReLU*>(next))
                 {
                     if (Layers::Linear* lin = steps_[i]->linear())
@@ -46,25 +54,32 @@ namespace CppNet
 
         DeviceTensor SequentialModel::backward(const DeviceTensor& grad_output)
         {
-            return backward_from(grad_output, 0, true);
+            return backward_from(grad_output, 0, true, steps_.size());
         }
 
         void SequentialModel::backward_params(const DeviceTensor& grad_output)
         {
-            std::size_t first = 0;
-            while (first < steps_.size() && !steps_[first]->is_trainable()) ++first;
-            if (first == steps_.size()) return;  // nothing to train
-            backward_from(grad_output, first, false);
+            backward_params_prefix(grad_output, steps_.size());
         }
 
-        // Runs steps last .. first; step `first` computes its input gradient
+        void SequentialModel::backward_params_prefix(const DeviceTensor& grad_output, std::size_t count)
+        {
+            if (count > steps_.size())
+                throw std::out_of_range("SequentialModel::backward_params_prefix: too many steps");
+            std::size_t first = 0;
+            while (first < count && !steps_[first]->is_trainable()) ++first;
+            if (first == count) return;  // nothing to train
+            backward_from(grad_output, first, false, count);
+        }
+
+        // Runs steps end-1 .. first; step `first` computes its input gradient
         // only when input_grad is set.  Fusions with a ReLU at k-1 apply only
         // for k > first, where that ReLU's backward is part of the range.
         DeviceTensor SequentialModel::backward_from(const DeviceTensor& grad_output, std::size_t first,
-                                                    bool input_grad)
+                                                    bool input_grad, std::size_t end)
         {
             DeviceTensor g = grad_output;
-            for (std::size_t k = steps_.size(); k-- > first;)
+            for (std::size_t k = end; k-- > first;)
             {
                 if (k == first && !input_grad) return steps_[k]->backward_no_input_grad(g);
                 Activations::Activation* prev = k > first ? steps_[k - 1]->activation() : nullptr;

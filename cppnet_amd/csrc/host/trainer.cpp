@@ -256,6 +256,9 @@ namespace
         throw std::invalid_argument("unknown loss code " + std::to_string(loss));
     }
 
+    // outputs up to this size take the one-launch Sigmoid + BCE head
+    constexpr int64_t kFusedHeadMax = 1 << 16;
+
     void check_session(cnt_session* s)
     {
         if (!s) throw std::invalid_argument("NULL session");
@@ -659,6 +662,27 @@ namespace
             return;
         }
         s->model.zero_grad();
+        // A Sigmoid output step followed by BinaryCrossEntropy on a small
+        // output runs as one launch (cnhip_sigmoid_bce_head), bit-identical
+        // to the four separate ones.
+        auto* bce = dynamic_cast<Losses::BinaryCrossEntropy*>(s->loss.get());
+        const std::size_t n = s->model.num_steps();
+        if (bce && n >= 2 && dynamic_cast<Activations::Sigmoid*>(s->model.last_activation()) &&
+            s->Y.size() <= kFusedHeadMax)
+        {
+            DeviceTensor z = s->model.forward_prefix(s->X, n - 1);
+            if (z.dims() != s->Y.dims())
+                throw std::invalid_argument("model output " + shape_str(z.dims()) + " and targets " +
+                                            shape_str(s->Y.dims()) + " differ");
+            DeviceTensor p = DeviceTensor::empty(z.dims()), dz = DeviceTensor::empty(z.dims());
+            DeviceTensor loss = DeviceTensor::empty({1});
+            Device::check(cnhip_sigmoid_bce_head(z.data(), s->Y.data(), p.data(), loss.data(), dz.data(), z.size(),
+                                                 bce->forward_reduction(), bce->backward_reduction(), s->stream),
+                          "sigmoid + BCE head");
+            s->last_loss = Losses::DeviceScalar(loss);
+            s->model.backward_params_prefix(dz, n - 1);
+            return;
+        }
         DeviceTensor out = s->model.forward(s->X);
         s->last_loss = s->loss->forward(out, s->Y);
         DeviceTensor g = s->loss->backward(out, s->Y);

@@ -34,6 +34,10 @@ namespace CppNet
             DeviceScalar forward(const DeviceTensor& predictions, const DeviceTensor& targets) override;
             DeviceTensor backward(const DeviceTensor& predictions, const DeviceTensor& targets) override;
             static void set_num_threads(int) {}
+            /// reduction codes of the device forward ("none" returns the mean)
+            /// and backward (only "mean" divides the gradient)
+            int forward_reduction() const { return reduction_ == "sum" ? CNHIP_REDUCE_SUM : CNHIP_REDUCE_MEAN; }
+            int backward_reduction() const { return reduction_ == "mean" ? CNHIP_REDUCE_MEAN : CNHIP_REDUCE_SUM; }
 
         private:
             std::string reduction_;

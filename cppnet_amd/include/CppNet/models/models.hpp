@@ -127,6 +127,13 @@ namespace CppNet
             DeviceTensor forward(const DeviceTensor& input);
             DeviceTensor backward(const DeviceTensor& grad_output);
             void backward_params(const DeviceTensor& grad_output);
+            /// forward through steps [0, count) only
+            DeviceTensor forward_prefix(const DeviceTensor& input, std::size_t count);
+            /// backward_params over steps [0, count): grad_output is the
+            /// gradient of step count-1's output
+            void backward_params_prefix(const DeviceTensor& grad_output, std::size_t count);
+            /// the activation of the last step, or null
+            Activations::Activation* last_activation() const;
             Tensor<float, 2> forward(const Tensor<float, 2>& input);
             Tensor<float, 2> backward(const Tensor<float, 2>& grad_output);
 
@@ -138,7 +145,8 @@ namespace CppNet
             void summary() const;
 
         private:
-            DeviceTensor backward_from(const DeviceTensor& grad_output, std::size_t first, bool input_grad);
+            DeviceTensor backward_from(const DeviceTensor& grad_output, std::size_t first, bool input_grad,
+                                       std::size_t end);
             std::vector<std::shared_ptr<detail::Step>> steps_;
             std::vector<std::shared_ptr<Layers::Layer>> layers_;
         };

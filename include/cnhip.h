@@ -396,6 +396,14 @@ int cnhip_bce_forward(const float* pred, const float* target, float* loss,
                       int64_t n, int reduction, cnhip_stream_t stream);
 int cnhip_bce_backward(const float* pred, const float* target, float* grad,
                        int64_t n, int reduction, cnhip_stream_t stream);
+/* A Sigmoid output layer followed by BinaryCrossEntropy, forward and backward
+ * in one launch: p = sigmoid(z), loss = BCE(p, target) (loss_reduction),
+ * dz = BCE'(p, target) (grad_reduction) * p (1 - p).  Bit-identical to
+ * cnhip_sigmoid_forward + cnhip_bce_forward + cnhip_bce_backward +
+ * cnhip_sigmoid_backward (one block: meant for small outputs).
+ * ref: sigmoid.cpp:97-231, binary_cross_entropy.cpp:143-225 */
+int cnhip_sigmoid_bce_head(const float* z, const float* target, float* p, float* loss, float* dz, int64_t n,
+                           int loss_reduction, int grad_reduction, cnhip_stream_t stream);
 /* MSE: loss = sum (p-t)^2 [/n]; grad = 2(p-t) [/n]
  * ref: MSE::forward/backward src/CppNet/losses/mse.cpp:102-161 */
 int cnhip_mse_forward(const float* pred, const float* target, float* loss,

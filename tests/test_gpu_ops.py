@@ -376,3 +376,31 @@ def test_linear_fused_residual_matches_unfused(gpu, B, I, O):
     np.testing.assert_array_equal(host(dX), host(dXu))
     np.testing.assert_array_equal(host(gW), host(gWu))
     np.testing.assert_array_equal(host(gb), host(gbu))
+
+
+@pytest.mark.parametrize("n", [1, 512, 1000, 4097, 65536])
+@pytest.mark.parametrize("red_f,red_b", [(0, 0), (1, 1), (0, 1)])
+def test_sigmoid_bce_head_matches_separate_kernels(gpu, n, red_f, red_b):
+    """cnhip_sigmoid_bce_head against cnhip_sigmoid_forward + cnhip_bce_forward
+    + cnhip_bce_backward + cnhip_sigmoid_backward: every output bit-identical
+    (reduction codes 0 mean, 1 sum; "none" uses mean forward, sum backward)."""
+    from cppnet_amd import _capi
+    lib = _capi.load()
+    print(f"[ops] sigmoid+bce head n={n} red={red_f},{red_b}", flush=True)
+    rng = np.random.default_rng(n)
+    z = torch.from_numpy((rng.standard_normal(n) * 4).astype(np.float32)).cuda()
+    t = torch.from_numpy((rng.uniform(size=n) < 0.5).astype(np.float32)).cuda()
+    s = torch.cuda.current_stream().cuda_stream
+    p1, g1, dz1 = (torch.empty(n, device="cuda") for _ in range(3))
+    l1 = torch.empty(1, device="cuda")
+    assert lib.cnhip_sigmoid_forward(z.data_ptr(), p1.data_ptr(), n, s) == 0
+    assert lib.cnhip_bce_forward(p1.data_ptr(), t.data_ptr(), l1.data_ptr(), n, red_f, s) == 0
+    assert lib.cnhip_bce_backward(p1.data_ptr(), t.data_ptr(), g1.data_ptr(), n, red_b, s) == 0
+    assert lib.cnhip_sigmoid_backward(p1.data_ptr(), g1.data_ptr(), dz1.data_ptr(), n, s) == 0
+    p2, dz2 = torch.empty(n, device="cuda"), torch.empty(n, device="cuda")
+    l2 = torch.empty(1, device="cuda")
+    assert lib.cnhip_sigmoid_bce_head(z.data_ptr(), t.data_ptr(), p2.data_ptr(), l2.data_ptr(),
+                                      dz2.data_ptr(), n, red_f, red_b, s) == 0
+    torch.cuda.synchronize()
+    for a, b, name in [(p1, p2, "p"), (l1, l2, "loss"), (dz1, dz2, "dz")]:
+        assert torch.equal(a.view(torch.int32), b.view(torch.int32)), name
