@@ -341,6 +341,8 @@ __global__ void __launch_bounds__(256) gemm_small_thread_kernel(GemmArgs g) {
   const int64_t m = e % g.M, n = e / g.M;
   const bool cs = g.colsum && m == 0;
   float acc = 0.f, sum = 0.f;
+  // unrolled so the loads issue ahead; the FMAs stay in k order
+#pragma unroll 8
   for (int64_t k = 0; k < g.K; ++k) {
     const float b = op_b<TA, TB>(g, k, n);
     acc = fmaf(op_a<TA, TB>(g, m, k), b, acc);
@@ -358,6 +360,7 @@ __global__ void __launch_bounds__(256) gemm_small_wave_kernel(GemmArgs g) {
   const int64_t m = e % g.M, n = e / g.M;
   const bool cs = g.colsum && m == 0;  // uniform per wave
   float acc = 0.f, sum = 0.f;
+#pragma unroll 4
   for (int64_t k = lane; k < g.K; k += 64) {
     const float b = op_b<TA, TB>(g, k, n);
     acc = fmaf(op_a<TA, TB>(g, m, k), b, acc);
