@@ -97,6 +97,7 @@ SIGNATURES: dict[str, tuple] = {
     "cnhip_tanh_forward": (i32, [vp, vp, i64, vp]),
     "cnhip_tanh_backward": (i32, [vp, vp, vp, i64, vp]),
     "cnhip_bce_forward": (i32, [vp, vp, vp, i64, i32, vp]),
+    "cnhip_softmax_ce_head": (i32, [vp, vp, vp, vp, vp, i64, i64, i32, vp]),
     "cnhip_sigmoid_bce_head": (i32, [vp, vp, vp, vp, vp, i64, i32, i32, vp]),
     "cnhip_bce_backward": (i32, [vp, vp, vp, i64, i32, vp]),
     "cnhip_mse_forward": (i32, [vp, vp, vp, i64, i32, vp]),

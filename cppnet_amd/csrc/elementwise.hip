@@ -257,6 +257,82 @@ __global__ void __launch_bounds__(SCE_BLOCK) softmax_ce_rows_kernel(
   }
 }
 
+// softmax_ce_rows_kernel + the backward for B <= SCE_BLOCK rows in one block:
+// the same per-row arithmetic and fixed-order block sum; the loss is that sum
+// over the divisor, which is what partial_sum_kernel makes of a single
+// partial (it adds only zeros to it).  Gradient as softmax_ce_backward_kernel.
+// REG > 0: a row of at most REG classes is loaded once into registers (the
+// same values, so the same results, without re-reading memory per pass).
+template <int REG>
+__global__ void __launch_bounds__(SCE_BLOCK) softmax_ce_head_kernel(
+    const float* __restrict__ z, const float* __restrict__ t, float* __restrict__ sm,
+    float* __restrict__ loss, float* __restrict__ g, int64_t B, int64_t C, float divisor, int mean,
+    float inv_batch) {
+  __shared__ float smem[SCE_BLOCK / 64];
+  float row = 0.f;
+  const int64_t b = threadIdx.x;
+  if (REG > 0 && b < B) {
+    float zr[REG > 0 ? REG : 1], tr[REG > 0 ? REG : 1];
+#pragma unroll
+    for (int c = 0; c < REG; ++c) {
+      zr[c] = c < C ? z[b + B * c] : 0.f;
+      tr[c] = c < C ? t[b + B * c] : 0.f;
+    }
+    float mx = zr[0];
+#pragma unroll
+    for (int c = 1; c < REG; ++c)
+      if (c < C) mx = fmaxf(mx, zr[c]);
+    float er[REG > 0 ? REG : 1];
+    float se = 0.f;
+#pragma unroll
+    for (int c = 0; c < REG; ++c)
+      if (c < C) {
+        er[c] = expf(zr[c] - mx);
+        se += er[c];
+      }
+    const float ls = logf(se + 1e-12f);
+#pragma unroll
+    for (int c = 0; c < REG; ++c)
+      if (c < C) {
+        const float p = er[c] / se;
+        sm[b + B * c] = p;
+        row -= tr[c] * ((zr[c] - mx) - ls);
+        float v = p - tr[c];
+        if (mean) v *= inv_batch;
+        g[b + B * c] = v;
+      }
+  } else if (REG == 0 && b < B) {
+    float mx = z[b];
+    for (int64_t c = 1; c < C; ++c) mx = fmaxf(mx, z[b + B * c]);
+    float se = 0.f;
+    for (int64_t c = 0; c < C; ++c) {
+      const float e = expf(z[b + B * c] - mx);
+      sm[b + B * c] = e;
+      se += e;
+    }
+    const float ls = logf(se + 1e-12f);
+    for (int64_t c = 0; c < C; ++c) {
+      const float p = sm[b + B * c] / se;
+      sm[b + B * c] = p;
+      const float tv = t[b + B * c];
+      row -= tv * ((z[b + B * c] - mx) - ls);
+      float v = p - tv;
+      if (mean) v *= inv_batch;
+      g[b + B * c] = v;
+    }
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) row += __shfl_xor(row, off, 64);
+  if (lane == 0) smem[wave] = row;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float s = 0.f;
+    for (int w = 0; w < SCE_BLOCK / 64; ++w) s += smem[w];
+    *loss = s / divisor;
+  }
+}
+
 __global__ void __launch_bounds__(RB) partial_sum_kernel(const float* __restrict__ partial,
                                                          int64_t count, float* __restrict__ out,
                                                          float divisor) {
@@ -405,6 +481,32 @@ int cnhip_softmax_ce_forward(const float* logits, const float* targets, float* s
     status = cnhip::check_launch(who);
   }
   return status;
+}
+
+int cnhip_softmax_ce_head(const float* logits, const float* targets, float* softmax_out, float* loss,
+                          float* grad, int64_t batch, int64_t classes, int reduction, cnhip_stream_t s) {
+  const char* who = "cnhip_softmax_ce_head";
+  CNHIP_TRY(cnhip::check_reduction(reduction, who));
+  CNHIP_REQUIRE(batch > 0 && classes > 0, "%s: empty input", who);
+  CNHIP_REQUIRE(logits && targets && softmax_out && loss && grad, "%s: NULL pointer", who);
+  if (batch > cnhip::SCE_BLOCK) {
+    CNHIP_TRY(cnhip_softmax_ce_forward(logits, targets, softmax_out, loss, batch, classes, reduction, s));
+    return cnhip_softmax_ce_backward(softmax_out, targets, grad, batch, classes, reduction, s);
+  }
+  const float divisor = reduction == CNHIP_REDUCE_MEAN ? (float)batch : 1.0f;
+  cnhip::HbmTimer timer("softmax_ce_head_kernel", 20.0 * (double)batch * (double)classes + 4.0, as_stream(s));
+  const int mean = reduction == CNHIP_REDUCE_MEAN ? 1 : 0;
+  const float inv = 1.0f / (float)batch;
+  if (classes <= 16)
+    hipLaunchKernelGGL(cnhip::softmax_ce_head_kernel<16>, dim3(1), dim3(cnhip::SCE_BLOCK), 0, as_stream(s),
+                       logits, targets, softmax_out, loss, grad, batch, classes, divisor, mean, inv);
+  else if (classes <= 32)
+    hipLaunchKernelGGL(cnhip::softmax_ce_head_kernel<32>, dim3(1), dim3(cnhip::SCE_BLOCK), 0, as_stream(s),
+                       logits, targets, softmax_out, loss, grad, batch, classes, divisor, mean, inv);
+  else
+    hipLaunchKernelGGL(cnhip::softmax_ce_head_kernel<0>, dim3(1), dim3(cnhip::SCE_BLOCK), 0, as_stream(s),
+                       logits, targets, softmax_out, loss, grad, batch, classes, divisor, mean, inv);
+  return cnhip::check_launch(who);
 }
 
 int cnhip_softmax_ce_backward(const float* softmax, const float* targets, float* grad,

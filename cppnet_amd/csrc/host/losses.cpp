@@ -144,6 +144,23 @@ namespace CppNet
             Layers::require_gpu_device(device_, "SoftmaxCrossEntropy");
         }
 
+        DeviceScalar SoftmaxCrossEntropy::forward_backward(const DeviceTensor& z, const DeviceTensor& t,
+                                                           DeviceTensor& grad)
+        {
+            require_same_shape(z, t, "SoftmaxCrossEntropy::forward_backward");
+            if (z.rank() != 2) throw std::invalid_argument("SoftmaxCrossEntropy: expected [batch, classes]");
+            const int64_t B = z.dimension(0), C = z.dimension(1);
+            if (!softmax_cache_.defined() || softmax_cache_.dims() != z.dims())
+                softmax_cache_ = DeviceTensor::empty(z.dims());
+            if (!grad.defined() || grad.dims() != z.dims()) grad = DeviceTensor::empty(z.dims());
+            DeviceTensor loss = DeviceTensor::empty({1});
+            Device::check(cnhip_softmax_ce_head(z.data(), t.data(), softmax_cache_.data(), loss.data(), grad.data(),
+                                                B, C, reduction_code(reduction_, "SoftmaxCE", false),
+                                                Device::stream()),
+                          "SoftmaxCrossEntropy::forward_backward");
+            return DeviceScalar(loss);
+        }
+
         DeviceScalar SoftmaxCrossEntropy::forward(const DeviceTensor& z, const DeviceTensor& t)
         {
             require_same_shape(z, t, "SoftmaxCrossEntropy::forward");

@@ -657,8 +657,15 @@ namespace
         {
             s->encoder->zero_grad();
             DeviceTensor out = s->encoder->forward(s->X);
-            s->last_loss = s->loss->forward(out, s->Y);
-            s->encoder->backward(s->loss->backward(out, s->Y));
+            DeviceTensor g;
+            if (auto* sce = dynamic_cast<Losses::SoftmaxCrossEntropy*>(s->loss.get()))
+                s->last_loss = sce->forward_backward(out, s->Y, g);
+            else
+            {
+                s->last_loss = s->loss->forward(out, s->Y);
+                g = s->loss->backward(out, s->Y);
+            }
+            s->encoder->backward(g);
             return;
         }
         s->model.zero_grad();
@@ -684,8 +691,14 @@ namespace
             return;
         }
         DeviceTensor out = s->model.forward(s->X);
-        s->last_loss = s->loss->forward(out, s->Y);
-        DeviceTensor g = s->loss->backward(out, s->Y);
+        DeviceTensor g;
+        if (auto* sce = dynamic_cast<Losses::SoftmaxCrossEntropy*>(s->loss.get()))
+            s->last_loss = sce->forward_backward(out, s->Y, g);  // one launch for small batches
+        else
+        {
+            s->last_loss = s->loss->forward(out, s->Y);
+            g = s->loss->backward(out, s->Y);
+        }
         s->model.backward_params(g);
     }
 

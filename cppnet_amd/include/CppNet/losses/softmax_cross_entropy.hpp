@@ -28,6 +28,11 @@ namespace CppNet
             DeviceScalar forward(const DeviceTensor& logits, const DeviceTensor& targets) override;
             DeviceTensor backward(const DeviceTensor& logits, const DeviceTensor& targets) override;
             const DeviceTensor& softmax_cache() const { return softmax_cache_; }
+            /// forward() then backward() in one call (one launch for batches
+            /// of at most 256 rows), the same values bit for bit; the
+            /// gradient is written to `grad` (allocated when its shape differs)
+            DeviceScalar forward_backward(const DeviceTensor& logits, const DeviceTensor& targets,
+                                          DeviceTensor& grad);
 
         private:
             std::string reduction_;

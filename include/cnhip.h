@@ -420,6 +420,11 @@ int cnhip_softmax_ce_forward(const float* logits, const float* targets,
 int cnhip_softmax_ce_backward(const float* softmax, const float* targets,
                               float* grad, int64_t batch, int64_t classes,
                               int reduction, cnhip_stream_t stream);
+/* SoftmaxCrossEntropy forward and backward together: softmax_out, loss and
+ * grad as cnhip_softmax_ce_forward + cnhip_softmax_ce_backward produce them,
+ * bit for bit; one launch when batch <= 256, else those two calls. */
+int cnhip_softmax_ce_head(const float* logits, const float* targets, float* softmax_out, float* loss,
+                          float* grad, int64_t batch, int64_t classes, int reduction, cnhip_stream_t stream);
 
 /* ---- optimizer ---------------------------------------------------------
  * Adam, one tensor: m = b1 m + (1-b1) g ; v = b2 v + (1-b2) g^2 ;

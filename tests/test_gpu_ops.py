@@ -404,3 +404,31 @@ def test_sigmoid_bce_head_matches_separate_kernels(gpu, n, red_f, red_b):
     torch.cuda.synchronize()
     for a, b, name in [(p1, p2, "p"), (l1, l2, "loss"), (dz1, dz2, "dz")]:
         assert torch.equal(a.view(torch.int32), b.view(torch.int32)), name
+
+
+@pytest.mark.parametrize("B,C", [(1, 1), (32, 4), (256, 10), (200, 7), (64, 16), (100, 17), (256, 32),
+                                 (77, 33), (257, 10), (4096, 10)])
+@pytest.mark.parametrize("red", [0, 1])
+def test_softmax_ce_head_matches_separate_kernels(gpu, B, C, red):
+    """cnhip_softmax_ce_head against cnhip_softmax_ce_forward +
+    cnhip_softmax_ce_backward: softmax, loss and gradient bit-identical (one
+    launch up to 256 rows, the two calls beyond)."""
+    from cppnet_amd import _capi
+    lib = _capi.load()
+    print(f"[ops] softmax-CE head B={B} C={C} red={red}", flush=True)
+    rng = np.random.default_rng(B * 31 + C)
+    z = torch.from_numpy((rng.standard_normal(B * C) * 3).astype(np.float32)).cuda()
+    lab = rng.integers(0, C, B)
+    t_np = np.zeros((C, B), np.float32)
+    t_np[lab, np.arange(B)] = 1.0
+    t = torch.from_numpy(t_np.ravel()).cuda()
+    s = torch.cuda.current_stream().cuda_stream
+    sm1, g1, l1 = torch.empty(B * C, device="cuda"), torch.empty(B * C, device="cuda"), torch.empty(1, device="cuda")
+    assert lib.cnhip_softmax_ce_forward(z.data_ptr(), t.data_ptr(), sm1.data_ptr(), l1.data_ptr(), B, C, red, s) == 0
+    assert lib.cnhip_softmax_ce_backward(sm1.data_ptr(), t.data_ptr(), g1.data_ptr(), B, C, red, s) == 0
+    sm2, g2, l2 = torch.empty(B * C, device="cuda"), torch.empty(B * C, device="cuda"), torch.empty(1, device="cuda")
+    assert lib.cnhip_softmax_ce_head(z.data_ptr(), t.data_ptr(), sm2.data_ptr(), l2.data_ptr(), g2.data_ptr(),
+                                     B, C, red, s) == 0
+    torch.cuda.synchronize()
+    for a, b, name in [(sm1, sm2, "softmax"), (l1, l2, "loss"), (g1, g2, "grad")]:
+        assert torch.equal(a.view(torch.int32), b.view(torch.int32)), name
