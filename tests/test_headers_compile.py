@@ -1,0 +1,81 @@
+"""The public C++ API compiles and links the way a CppNet program would use it
+(no GPU needed: the program is built, not run).  The program touches every
+class family the headers declare -- layers, activations, losses, optimizers,
+the model, the DataLoader and the model-file functions -- with the
+reference's constructor arguments."""
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+LIB = ROOT / "cppnet_amd" / "_lib"
+
+PROGRAM = r'''
+#include <CppNet/CppNet.hpp>
+#include <memory>
+using namespace CppNet;
+
+int main(int argc, char**) {
+    if (argc < 100) return 0;  // built to check the API; never executed
+    Models::SequentialModel model;
+    model.add_layer(std::make_shared<Layers::Linear>(30, 64, "fc1", true, true, "gpu", "xavier"));
+    model.add_activation(std::make_shared<Activations::LeakyReLU>(0.01f, "gpu"));
+    model.add_layer(std::make_shared<Layers::Linear>(64, 10, "fc2", true, true, "gpu", "xavier"));
+    model.add_activation(std::make_shared<Activations::Softmax>("gpu"));
+    Layers::Conv2D conv(3, 8, 3, 1, 1, true, "gpu");
+    Layers::MaxPool2D pool(2, 2, "gpu");
+    Layers::GlobalAvgPool2D gap("gpu");
+    Layers::GlobalMaxPool2D gmp("gpu");
+    Layers::Dropout drop(0.5f, "gpu");
+    Layers::LSTM lstm(8, 16, true, "gpu");
+    Layers::GRU gru(8, 16, true, "gpu");
+    Layers::RNN rnn(8, 16, true, "gpu");
+    Layers::MultiHeadAttention mha(32, 4, "gpu");
+    Layers::BatchNorm bn(32, 0.1f, 1e-5f, "gpu");
+    Layers::Embedding emb(100, 32, "gpu");
+    Losses::CategoricalCrossEntropy cce("mean", true, 0.1f, "gpu");
+    Losses::MAE mae("mean", "gpu");
+    Losses::Huber huber(1.0f, "mean", "gpu");
+    Losses::SoftmaxCrossEntropy sce("mean", "gpu");
+    Optimizers::Adam adam;
+    Optimizers::SGD sgd("gpu");
+    Optimizers::Momentum mom(0.9f, "gpu");
+    Optimizers::Adagrad ada(1e-8f, "gpu");
+    Optimizers::RMSProp rms(0.9f, 1e-8f, "gpu");
+    Tensor<float, 2> X(100, 30), Y(100, 10);
+    Utils::DataLoader loader(X, Y, 32, true, false);
+    loader.to_device(Utils::Staging::Resident);
+    Utils::DeviceBatch batch;
+    while (loader.next_device(batch)) {
+        model.zero_grad();
+        DeviceTensor out = model.forward(batch.features);
+        float l = cce.forward(out, batch.labels).get();
+        model.backward_params(cce.backward(out, batch.labels));
+        model.update(rms, 1e-3f);
+        (void)l;
+    }
+    for (auto b : loader) (void)b;
+    Utils::save_model("m.cnet", model);
+    Utils::load_model("m.cnet", model);
+    Utils::save_checkpoint("m.ckpt", model, &rms);
+    Utils::load_checkpoint("m.ckpt", model, &rms);
+    Utils::save_npy("x.npy", X);
+    Tensor<float, 2> x2 = Utils::load_npy_2d("x.npy");
+    return static_cast<int>(x2.size() + conv.get_out_channels() + sgd.get_gpu_block_size());
+}
+'''
+
+
+@pytest.mark.skipif(shutil.which("g++") is None, reason="no host C++ compiler")
+def test_public_headers_compile_and_link(tmp_path):
+    if not (LIB / "libcppnet.so").exists():
+        pytest.skip("libraries not built (python -m cppnet_amd.build)")
+    src = tmp_path / "app.cpp"
+    src.write_text(PROGRAM)
+    cmd = ["g++", "-std=c++17", "-Wall", "-Werror", "-Wno-unused-variable", f"-I{ROOT / 'cppnet_amd' / 'include'}",
+           f"-I{ROOT / 'include'}", str(src), f"-L{LIB}", "-lcppnet", "-lcnhip", f"-Wl,-rpath,{LIB}",
+           "-o", str(tmp_path / "app")]
+    res = subprocess.run(cmd, capture_output=True, text=True, timeout=300)
+    assert res.returncode == 0, res.stderr[-4000:]
