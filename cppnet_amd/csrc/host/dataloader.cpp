@@ -7,6 +7,7 @@
 #include <stdexcept>
 #include <string>
 #include <thread>
+#include <utility>
 
 #include "CppNet/core/device.hpp"
 #include "CppNet/utils/init.hpp"
@@ -69,9 +70,9 @@ namespace CppNet
             }
         };
 
-        DataLoader::DataLoader(const Tensor<float, 2>& features, const Tensor<float, 2>& labels, int batch_size,
-                               bool shuffle, bool drop_last)
-            : features_(features), labels_(labels), batch_size_(batch_size), shuffle_(shuffle),
+        DataLoader::DataLoader(Tensor<float, 2> features, Tensor<float, 2> labels, int batch_size, bool shuffle,
+                               bool drop_last)
+            : features_(std::move(features)), labels_(std::move(labels)), batch_size_(batch_size), shuffle_(shuffle),
               drop_last_(drop_last), gen_(static_cast<std::mt19937::result_type>(next_seed()))
         {
             num_samples_ = static_cast<int>(features_.dimension(0));

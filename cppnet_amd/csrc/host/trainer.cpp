@@ -804,7 +804,8 @@ int cnt_loader_create(cnt_loader** out, const float* features, const float* labe
         if (n) std::copy(features, features + n * f, X.data());
         if (n) std::copy(labels, labels + n * l, Y.data());
         auto ld = std::make_unique<cnt_loader>();
-        ld->dl = std::make_unique<Utils::DataLoader>(X, Y, static_cast<int>(batch), shuffle != 0, drop_last != 0);
+        ld->dl = std::make_unique<Utils::DataLoader>(std::move(X), std::move(Y), static_cast<int>(batch), shuffle != 0,
+                                                     drop_last != 0);
         ld->dl->set_seed(seed);
         ld->F = f;
         ld->L = l;

@@ -63,8 +63,10 @@ namespace CppNet
         class DataLoader
         {
         public:
-            DataLoader(const Tensor<float, 2>& features, const Tensor<float, 2>& labels, int batch_size,
-                       bool shuffle = true, bool drop_last = false);
+            /// The dataset is taken by value: pass rvalues to move it in
+            /// instead of holding a second host copy.
+            DataLoader(Tensor<float, 2> features, Tensor<float, 2> labels, int batch_size, bool shuffle = true,
+                       bool drop_last = false);
             ~DataLoader();
             DataLoader(const DataLoader&) = delete;
             DataLoader& operator=(const DataLoader&) = delete;
