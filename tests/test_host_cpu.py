@@ -14,7 +14,7 @@ def test_config_shapes_match_baseline():
     assert (c1.sizes, c1.batch, c1.loss, c1.out_act) == ([30, 64, 1], 512, "bce", "sigmoid")
     assert (c2.sizes, c2.batch, c2.loss) == ([1024, 4096, 4096, 10], 4096, "softmax_ce")
     n2 = sum(i * o + o for i, o in zip(c2.sizes[:-1], c2.sizes[1:]))
-    assert n2 == 21_020_682  # BASELINE.md parameter count for C2
+    assert n2 == 21_020_682  # config 2: 1024*4096 + 4096 + 4096*4096 + 4096 + 4096*10 + 10
     n1 = sum(i * o + o for i, o in zip(c1.sizes[:-1], c1.sizes[1:]))
     assert n1 == 2_049
 
