@@ -74,3 +74,23 @@ def test_seed_fixes_the_order():
     np.testing.assert_array_equal(a.indices(), b.indices())
     assert not np.array_equal(a.indices(), c.indices())
     np.testing.assert_array_equal(_loader(X, Y, 10, shuffle=False).indices(), np.arange(100))
+
+
+def test_errors_are_reported_not_raised_through():
+    """Bad arguments come back as a status and a message (no GPU needed)."""
+    import ctypes as C
+    X, Y = _dataset(10, 3, 1)
+    ld = _loader(X, Y, 4, shuffle=False)
+    with pytest.raises(Exception, match="out of range"):
+        ld.host_batch(3)
+    with pytest.raises(Exception, match="out of range"):
+        ld.host_batch(-1)
+    lib = trainer.load()
+    h = C.c_void_p()
+    x = np.zeros(30, np.float32)
+    assert lib.cnt_loader_create(C.byref(h), x.ctypes.data, x.ctypes.data, 10, 0, 1, 4, 1, 0, 0) != 0
+    assert "shape" in lib.cnt_last_error().decode()
+    assert lib.cnt_loader_create(None, x.ctypes.data, x.ctypes.data, 10, 3, 1, 4, 1, 0, 0) != 0
+    n = C.c_int64()
+    assert lib.cnt_loader_num_batches(None, C.byref(n)) != 0
+    assert "NULL loader" in lib.cnt_last_error().decode()
