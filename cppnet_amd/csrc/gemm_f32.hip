@@ -648,9 +648,16 @@ int gemm_f32_batched(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, 
 constexpr double kSmallGemmFlops = 4.0e6;
 constexpr int64_t kSmallGemmOutputs = 1 << 16;
 
-static bool gemm_is_small(int64_t M, int64_t N, int64_t K, int64_t batches) {
-  return batches == 1 && K > 0 && 2.0 * (double)M * (double)N * (double)K <= kSmallGemmFlops &&
-         M * N <= kSmallGemmOutputs;
+// Weight-gradient shapes (op(A) = A^T, A k-contiguous; B not transposed, also
+// k-contiguous) read whole contiguous k-runs per wave, so the wave kernel
+// stays efficient up to this many flops (a skinny classifier's dW).
+constexpr double kSmallWgradFlops = 32.0e6;
+
+static bool gemm_is_small(int64_t M, int64_t N, int64_t K, int64_t batches, int trans_a = 0,
+                          int trans_b = 0) {
+  if (batches != 1 || K <= 0 || M * N > kSmallGemmOutputs) return false;
+  const double flops = 2.0 * (double)M * (double)N * (double)K;
+  return flops <= kSmallGemmFlops || (trans_a && !trans_b && K > 64 && flops <= kSmallWgradFlops);
 }
 
 static int gemm_small(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float alpha,
@@ -705,7 +712,7 @@ int gemm_f32_core(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, flo
   }
   CNHIP_REQUIRE(batches <= 65535, "%s: batch count %lld exceeds 65535", who, (long long)batches);
 
-  if (gemm_is_small(M, N, K, batches))
+  if (gemm_is_small(M, N, K, batches, trans_a, trans_b))
     return gemm_small(trans_a, trans_b, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, bias, epilogue,
                       aux_in, aux_out, ld_aux, st, who);
 
@@ -767,7 +774,7 @@ int linear_wgrad_small(const float* X, const float* dY, float* dW, float* db, in
                        int64_t in_features, int64_t out_features, int accumulate, hipStream_t st,
                        const char* who, bool* done) {
   *done = false;
-  if (!gemm_is_small(in_features, out_features, batch, 1)) return CNHIP_OK;
+  if (!gemm_is_small(in_features, out_features, batch, 1, 1, 0)) return CNHIP_OK;
   CNHIP_REQUIRE(X && dY && dW, "%s: NULL pointer", who);
   *done = true;
   return gemm_small(1, 0, in_features, out_features, batch, 1.f, X, batch, dY, batch,
