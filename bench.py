@@ -173,6 +173,21 @@ def traffic_calibration() -> int:
     return 0
 
 
+def small_roofline(hbm_kernels, step_ms):
+    """A step without MFMA launches (config 1: every GEMM is a latency-bound
+    SIMT kernel): the SIMT GEMM class against HBM, its algorithmic bytes over
+    its event-timed launch duration."""
+    k = next((r for r in hbm_kernels if r["kernel"] == "gemm_small_kernel"), None)
+    if k is None:
+        return None
+    return {"bound": "hbm", "kernel": "gemm_small_thread/wave_kernel (SIMT fp32 GEMMs of <= 2 MFLOP: the "
+                                      "step is launch-latency bound)",
+            "achieved": k["achieved_GBs"], "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": k["frac"],
+            "traffic": None, "launches_per_step": k["launches_per_step"], "avg_launch_us": k["avg_us"],
+            "bytes_per_launch": k["bytes_per_launch"],
+            "share_of_step": round(k["avg_us"] * k["launches_per_step"] / (step_ms * 1e3), 3)}
+
+
 def loader_leg(sess, cfg, B, steps, step_ms, mode):
     """`steps` train steps whose batches come from a DataLoader over a synthetic
     dataset of 16 batches (reshuffled at each epoch's end, inside the timed
@@ -352,9 +367,7 @@ def main() -> int:
                             "achieved_GBs": round(gbs, 1),
                             "frac": round(gbs / PEAK_HBM_GBS, 4)})
 
-    kernels = {1: "gemm_small_thread/wave_kernel (SIMT fp32: the step's GEMMs are all <= 2 MFLOP and "
-                  "latency-bound; the config is launch-latency bound, not MFMA bound)",
-               3: "gemm_f32_kernel + conv_pixel/conv_wgrad_kernel (fp32 MFMA, all shapes of the step)",
+    kernels = {3: "gemm_f32_kernel + conv_pixel/conv_wgrad_kernel (fp32 MFMA, all shapes of the step)",
                4: "gemm_f32_kernel + lstm_step_fwd/bwd_kernel (fp32 MFMA; the per-timestep recurrent "
                   "GEMM tiles with the cell update fused)"}.get(
         args.config, "gemm_f32_kernel (fp32 MFMA GEMM, all shapes of the step)")
@@ -377,7 +390,7 @@ def main() -> int:
                    "execution": ("captured fwd+bwd HIP graph replay + eager fused Adam, every step"
                                  if args.graph else "eager launches on one stream"),
                    "wall_s_timed_region": round(wall, 3)},
-        "roofline": {"bound": "mfma", "kernel": kernels,
+        "roofline": ({"bound": "mfma", "kernel": kernels,
                      "achieved": round(achieved, 2), "peak": PEAK_FP32_MFMA_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4),
                      "traffic": PMC_TRAFFIC_BYTES.get(args.config),
@@ -385,7 +398,8 @@ def main() -> int:
                      "launches_per_step": launches.value // prof_steps,
                      "avg_launch_us": round(per_launch_us, 2),
                      "flops_per_launch": flops_per_launch,
-                     "share_of_step": round(gemm_share, 3)},
+                     "share_of_step": round(gemm_share, 3)}
+                     if launches.value else small_roofline(hbm_kernels, step_ms)),
         "hbm_kernels": {"peak_GBs": PEAK_HBM_GBS,
                         "note": "algorithmic bytes (inputs read once, outputs written once) / "
                                 "event-timed launch duration, per bandwidth-bound kernel",

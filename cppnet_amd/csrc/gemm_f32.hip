@@ -674,8 +674,9 @@ static int gemm_small(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K,
   g.alpha = alpha; g.beta = beta; g.bias = bias; g.epilogue = epilogue;
   g.aux_in = aux_in; g.aux_out = aux_out; g.ld_aux = ld_aux;
   g.splits = 1;
-  TimingRec* rec = timing_slot(2.0 * (double)M * (double)N * (double)K);
-  if (rec) (void)hipEventRecord(rec->start, st);
+  // not an MFMA kernel: timed with the bandwidth/latency kernels, credited
+  // with its algorithmic bytes (A, B and C once each)
+  HbmTimer timer("gemm_small_kernel", 4.0 * ((double)M * K + (double)K * N + (double)M * N), st);
   const int64_t outs = M * N;
   const bool wave = K > 64;
   const dim3 grid((unsigned)(wave ? (outs + 3) / 4 : (outs + 255) / 256));
@@ -690,7 +691,6 @@ static int gemm_small(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K,
     if (trans_b) { CNHIP_SMALL(false, true) } else { CNHIP_SMALL(false, false) }
   }
 #undef CNHIP_SMALL
-  if (rec) (void)hipEventRecord(rec->stop, st);
   return check_launch(who);
 }
 
