@@ -307,24 +307,26 @@ __global__ void __launch_bounds__(256) emb_count_kernel(const int32_t* __restric
 // exclusive scan of counts[V] into offsets[V+1] (one block, fixed order)
 __global__ void __launch_bounds__(1024) emb_scan_kernel(const int32_t* __restrict__ counts,
                                                         int32_t* __restrict__ offsets, int64_t V) {
-  __shared__ int32_t part[1024];
+  __shared__ int32_t wave_total[16];
   const int64_t per = (V + 1023) / 1024;
   const int64_t lo = threadIdx.x * per, hi = min(V, lo + per);
   int32_t s = 0;
   for (int64_t v = lo; v < hi; ++v) s += counts[v];
-  part[threadIdx.x] = s;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    int32_t run = 0;
-    for (int i = 0; i < 1024; ++i) {
-      const int32_t c = part[i];
-      part[i] = run;
-      run += c;
-    }
-    offsets[V] = run;
+  // exclusive scan of the 1024 per-thread counts: an inclusive shuffle scan
+  // within each wave, then the 16 wave totals (integer sums: exact in any order)
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int32_t x = s;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int32_t y = __shfl_up(x, off, 64);
+    if (lane >= off) x += y;
   }
+  if (lane == 63) wave_total[wave] = x;
   __syncthreads();
-  int32_t run = part[threadIdx.x];
+  int32_t before = 0;
+  for (int w = 0; w < wave; ++w) before += wave_total[w];
+  int32_t run = before + x - s;
+  if (threadIdx.x == 1023) offsets[V] = run + s;
   for (int64_t v = lo; v < hi; ++v) {
     offsets[v] = run;
     run += counts[v];
