@@ -107,17 +107,17 @@ namespace CppNet
             grads_zero_ = true;  // conv2d.cpp:211-212 clears the grads after the update
         }
 
-        Tensor<float, 4> Conv2D::get_weights() const { return W_.to_host<float, 4>(); }
-        Tensor<float, 1> Conv2D::get_biases() const
+        const Tensor<float, 4> Conv2D::get_weights() const { return W_.to_host<float, 4>(); }
+        const Tensor<float, 1> Conv2D::get_biases() const
         {
             return bias_flag_ ? b_.to_host<float, 1>() : Tensor<float, 1>(0);
         }
-        Tensor<float, 4> Conv2D::get_grad_weights() const
+        const Tensor<float, 4> Conv2D::get_grad_weights() const
         {
             materialize_grads();
             return gW_.to_host<float, 4>();
         }
-        Tensor<float, 1> Conv2D::get_grad_biases() const
+        const Tensor<float, 1> Conv2D::get_grad_biases() const
         {
             materialize_grads();
             return bias_flag_ ? gb_.to_host<float, 1>() : Tensor<float, 1>(0);
@@ -194,7 +194,7 @@ namespace CppNet
         {
             return backward(DeviceTensor::from_host(g)).to_host<float, 4>();
         }
-        Tensor<int, 4> MaxPool2D::get_max_indices() const { return idx_.to_host<int, 4>(); }
+        const Tensor<int, 4> MaxPool2D::get_max_indices() const { return idx_.to_host<int, 4>(); }
 
         // ---------------------------------------------------------------- Flatten
         DeviceTensor Flatten::forward(const DeviceTensor& x)

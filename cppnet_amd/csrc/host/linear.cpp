@@ -167,17 +167,17 @@ namespace CppNet
             grads_zero_ = true;
         }
 
-        Tensor<float, 2> Linear::get_weights() const { return W_.to_host<float, 2>(); }
-        Tensor<float, 2> Linear::get_grad_weights() const
+        const Tensor<float, 2> Linear::get_weights() const { return W_.to_host<float, 2>(); }
+        const Tensor<float, 2> Linear::get_grad_weights() const
         {
             materialize_grads();
             return gW_.to_host<float, 2>();
         }
-        Tensor<float, 1> Linear::get_biases() const
+        const Tensor<float, 1> Linear::get_biases() const
         {
             return bias_flag_ ? b_.to_host<float, 1>() : Tensor<float, 1>(0);
         }
-        Tensor<float, 1> Linear::get_grad_biases() const
+        const Tensor<float, 1> Linear::get_grad_biases() const
         {
             materialize_grads();
             return bias_flag_ ? gb_.to_host<float, 1>() : Tensor<float, 1>(0);

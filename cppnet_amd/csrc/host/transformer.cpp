@@ -131,8 +131,8 @@ namespace CppNet
             }
         } // namespace
 
-        Tensor<float, 2> Embedding::get_weight() const { return table_to_host(Wt_, vocab_size_, embed_dim_); }
-        Tensor<float, 2> Embedding::get_grad_weight() const
+        const Tensor<float, 2> Embedding::get_weight() const { return table_to_host(Wt_, vocab_size_, embed_dim_); }
+        const Tensor<float, 2> Embedding::get_grad_weight() const
         {
             materialize_grads();
             return table_to_host(gWt_, vocab_size_, embed_dim_);
@@ -259,12 +259,12 @@ namespace CppNet
             grads_zero_ = true;  // attention.cpp:583-586
         }
 
-        Tensor<float, 2> MultiHeadAttention::get_weight(int which) const
+        const Tensor<float, 2> MultiHeadAttention::get_weight(int which) const
         {
             if (which < 0 || which > 3) throw std::out_of_range("MultiHeadAttention: weight index");
             return W_[which].to_host<float, 2>();
         }
-        Tensor<float, 2> MultiHeadAttention::get_grad_weight(int which) const
+        const Tensor<float, 2> MultiHeadAttention::get_grad_weight(int which) const
         {
             if (which < 0 || which > 3) throw std::out_of_range("MultiHeadAttention: weight index");
             materialize_grads();
@@ -276,7 +276,7 @@ namespace CppNet
             check_2d(w, embed_dim_, embed_dim_, "MultiHeadAttention::set_weight");
             W_[which].copy_from_host(w.data());
         }
-        Tensor<float, 3> MultiHeadAttention::get_attention_weights() const
+        const Tensor<float, 3> MultiHeadAttention::get_attention_weights() const
         {
             if (!cache_.defined()) throw std::runtime_error("MultiHeadAttention: no forward yet");
             const int64_t B = q_cache_.dimension(0), S = q_cache_.dimension(1), D = embed_dim_;
@@ -374,12 +374,12 @@ namespace CppNet
             grads_zero_ = true;  // batch_norm.cpp:399-400
         }
 
-        Tensor<float, 1> BatchNorm::get_grad_gamma() const
+        const Tensor<float, 1> BatchNorm::get_grad_gamma() const
         {
             materialize_grads();
             return ggamma_.to_host<float, 1>();
         }
-        Tensor<float, 1> BatchNorm::get_grad_beta() const
+        const Tensor<float, 1> BatchNorm::get_grad_beta() const
         {
             materialize_grads();
             return gbeta_.to_host<float, 1>();

@@ -49,6 +49,17 @@ namespace CppNet
             data_.assign(static_cast<size_t>(count(dims_)), T(0));
         }
 
+        // Assignment only to lvalues.  The layers' state getters return host
+        // copies (the state lives in HBM) as const values, so reference code
+        // that writes through a getter it expects to return a reference
+        // (`bn.get_gamma() = g`, `lin.get_weights()(0, 0) = w`) fails to
+        // compile here instead of writing into a discarded temporary; such
+        // code uses the setters (set_gamma, set_weights, ...).
+        Tensor(const Tensor&) = default;
+        Tensor(Tensor&&) noexcept = default;
+        Tensor& operator=(const Tensor&) & = default;
+        Tensor& operator=(Tensor&&) & noexcept = default;
+
         Index dimension(int i) const { return dims_.at(static_cast<size_t>(i)); }
         const Dimensions& dimensions() const { return dims_; }
         Index size() const { return static_cast<Index>(data_.size()); }

@@ -54,11 +54,11 @@ namespace CppNet
             int get_num_heads() const { return num_heads_; }
 
             /// Host copies, ColMajor [D, D]; which: 0 q, 1 k, 2 v, 3 o.
-            Tensor<float, 2> get_weight(int which) const;
-            Tensor<float, 2> get_grad_weight(int which) const;
+            const Tensor<float, 2> get_weight(int which) const;
+            const Tensor<float, 2> get_grad_weight(int which) const;
             void set_weight(int which, const Tensor<float, 2>& w);
             /// Attention weights of the last forward, [B, S, S] ColMajor (n, i, j).
-            Tensor<float, 3> get_attention_weights() const;
+            const Tensor<float, 3> get_attention_weights() const;
 
             DeviceTensor& weight(int which);
             DeviceTensor& grad_weight(int which);

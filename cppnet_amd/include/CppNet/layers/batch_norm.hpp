@@ -44,12 +44,12 @@ namespace CppNet
             void unfreeze() { trainable_ = true; }
             int get_num_features() const { return num_features_; }
 
-            Tensor<float, 1> get_gamma() const { return gamma_.to_host<float, 1>(); }
-            Tensor<float, 1> get_beta() const { return beta_.to_host<float, 1>(); }
-            Tensor<float, 1> get_grad_gamma() const;
-            Tensor<float, 1> get_grad_beta() const;
-            Tensor<float, 1> get_running_mean() const { return rmean_.to_host<float, 1>(); }
-            Tensor<float, 1> get_running_var() const { return rvar_.to_host<float, 1>(); }
+            const Tensor<float, 1> get_gamma() const { return gamma_.to_host<float, 1>(); }
+            const Tensor<float, 1> get_beta() const { return beta_.to_host<float, 1>(); }
+            const Tensor<float, 1> get_grad_gamma() const;
+            const Tensor<float, 1> get_grad_beta() const;
+            const Tensor<float, 1> get_running_mean() const { return rmean_.to_host<float, 1>(); }
+            const Tensor<float, 1> get_running_var() const { return rvar_.to_host<float, 1>(); }
             void set_gamma(const Tensor<float, 1>& g);
             void set_beta(const Tensor<float, 1>& b);
             void set_running_mean(const Tensor<float, 1>& m);

@@ -46,10 +46,10 @@ namespace CppNet
             void freeze() { trainable_ = false; }
             void unfreeze() { trainable_ = true; }
 
-            Tensor<float, 4> get_weights() const;
-            Tensor<float, 1> get_biases() const;
-            Tensor<float, 4> get_grad_weights() const;
-            Tensor<float, 1> get_grad_biases() const;
+            const Tensor<float, 4> get_weights() const;
+            const Tensor<float, 1> get_biases() const;
+            const Tensor<float, 4> get_grad_weights() const;
+            const Tensor<float, 1> get_grad_biases() const;
             void set_weights(const Tensor<float, 4>& weights);
             void set_biases(const Tensor<float, 1>& biases);
             DeviceTensor& weights() { return W_; }

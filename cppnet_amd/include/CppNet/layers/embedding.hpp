@@ -52,8 +52,8 @@ namespace CppNet
             int get_embed_dim() const { return embed_dim_; }
 
             /// Host copies in the reference's layout, ColMajor [V, D].
-            Tensor<float, 2> get_weight() const;
-            Tensor<float, 2> get_grad_weight() const;
+            const Tensor<float, 2> get_weight() const;
+            const Tensor<float, 2> get_grad_weight() const;
             void set_weight(const Tensor<float, 2>& w);
 
             /// Device tables, token-major (see above).

@@ -70,10 +70,10 @@ namespace CppNet
             bool has_bias() const { return bias_flag_; }
 
             /// Host copies of the device state (synchronise the stream).
-            Tensor<float, 2> get_weights() const;
-            Tensor<float, 1> get_biases() const;
-            Tensor<float, 2> get_grad_weights() const;
-            Tensor<float, 1> get_grad_biases() const;
+            const Tensor<float, 2> get_weights() const;
+            const Tensor<float, 1> get_biases() const;
+            const Tensor<float, 2> get_grad_weights() const;
+            const Tensor<float, 1> get_grad_biases() const;
             void set_weights(const Tensor<float, 2>& weights);
             void set_biases(const Tensor<float, 1>& biases);
 

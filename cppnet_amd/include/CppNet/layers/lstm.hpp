@@ -36,9 +36,9 @@ namespace CppNet
             bool get_return_sequences() const { return return_sequences_; }
 
             /// Host copies (the reference returns references to host tensors).
-            Tensor<float, 2> get_W_ih() const { return W_ih_.to_host<float, 2>(); }
-            Tensor<float, 2> get_W_hh() const { return W_hh_.to_host<float, 2>(); }
-            Tensor<float, 1> get_bias() const { return b_.to_host<float, 1>(); }
+            const Tensor<float, 2> get_W_ih() const { return W_ih_.to_host<float, 2>(); }
+            const Tensor<float, 2> get_W_hh() const { return W_hh_.to_host<float, 2>(); }
+            const Tensor<float, 1> get_bias() const { return b_.to_host<float, 1>(); }
             void set_W_ih(const Tensor<float, 2>& w);
             void set_W_hh(const Tensor<float, 2>& w);
             void set_bias(const Tensor<float, 1>& b);

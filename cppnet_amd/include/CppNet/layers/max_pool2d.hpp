@@ -37,7 +37,7 @@ namespace CppNet
             int get_stride() const { return stride_; }
             /// int32 argmax of the last forward, [N, C, HO, WO]
             const DeviceTensor& max_indices() const { return idx_; }
-            Tensor<int, 4> get_max_indices() const;
+            const Tensor<int, 4> get_max_indices() const;
 
         private:
             int pool_size_, stride_;

@@ -1,6 +1,6 @@
 """Model-level parity: the C++ trainer (CppNet-compatible classes on device
 "gpu", libcppnet.so) against the oracle-composed model on identical seeded
-inputs and injected weights (tests/model_ref.py).
+inputs and injected weights (oracle/mlp.py).
 
 Bars:
 * one step: loss and every parameter gradient within rel 1e-4 / abs 1e-5
@@ -27,7 +27,7 @@ import numpy as np
 import pytest
 
 from cppnet_amd import trainer
-from model_ref import OracleMLP
+from oracle.mlp import OracleMLP
 from oracle_lib import close, close_mag, fp, gemm_mag
 
 pytestmark = pytest.mark.gpu

@@ -79,3 +79,59 @@ def test_public_headers_compile_and_link(tmp_path):
            "-o", str(tmp_path / "app")]
     res = subprocess.run(cmd, capture_output=True, text=True, timeout=300)
     assert res.returncode == 0, res.stderr[-4000:]
+
+
+# Reference code that writes through a state getter (the reference returns
+# mutable references, e.g. batch_norm.hpp:74-77, linear.hpp:81, and its own
+# load_model does `bn->get_gamma() = read_tensor_1d(ifs)`,
+# serialization.cpp:238-239).  Here the getters return host copies of HBM
+# state, so each such write must be a compile error, never a silent no-op.
+WRITE_THROUGH_GETTER = {
+    "assign_gamma": "Tensor<float, 1> g(4); bn.get_gamma() = g;",
+    "assign_beta": "Tensor<float, 1> g(4); bn.get_beta() = g;",
+    "assign_running_var": "Tensor<float, 1> g(4); bn.get_running_var() = g;",
+    "element_write_weights": "lin.get_weights()(0, 0) = 1.0f;",
+    "element_write_biases": "lin.get_biases()(0) = 1.0f;",
+    "setzero_conv_weights": "conv.get_weights().setZero();",
+    "bind_mutable_ref": "Tensor<float, 2>& w = lin.get_weights(); w(0, 0) = 1.0f;",
+    "assign_lstm_whh": "Tensor<float, 2> w(4, 16); lstm.get_W_hh() = w;",
+    "assign_embedding": "Tensor<float, 2> w(10, 4); emb.get_weight() = w;",
+    "assign_mha_weight": "Tensor<float, 2> w(4, 4); mha.get_weight(0) = w;",
+}
+
+GETTER_PROGRAM = r'''
+#include <CppNet/CppNet.hpp>
+using namespace CppNet;
+void f(Layers::BatchNorm& bn, Layers::Linear& lin, Layers::Conv2D& conv, Layers::LSTM& lstm,
+       Layers::Embedding& emb, Layers::MultiHeadAttention& mha) {
+    (void)bn; (void)lin; (void)conv; (void)lstm; (void)emb; (void)mha;
+    BODY
+}
+'''
+
+# What such code must do instead: copy, modify, set back.
+SETTER_BODY = ("Tensor<float, 1> g = bn.get_gamma(); g(0) = 2.0f; bn.set_gamma(g);"
+               " auto w = lin.get_weights(); w(0, 0) = 1.0f; lin.set_weights(w);"
+               " const auto& r = bn.get_running_mean(); (void)r;")
+
+
+def _syntax_check(tmp_path, name, body):
+    src = tmp_path / f"{name}.cpp"
+    src.write_text(GETTER_PROGRAM.replace("BODY", body))
+    cmd = ["g++", "-std=c++17", "-fsyntax-only", f"-I{ROOT / 'cppnet_amd' / 'include'}",
+           f"-I{ROOT / 'include'}", str(src)]
+    return subprocess.run(cmd, capture_output=True, text=True, timeout=300)
+
+
+@pytest.mark.skipif(shutil.which("g++") is None, reason="no host C++ compiler")
+@pytest.mark.parametrize("case", sorted(WRITE_THROUGH_GETTER))
+def test_write_through_getter_fails_to_compile(tmp_path, case):
+    res = _syntax_check(tmp_path, case, WRITE_THROUGH_GETTER[case])
+    assert res.returncode != 0, f"{case} compiled: a write through a getter would be silently lost"
+    assert "error" in res.stderr
+
+
+@pytest.mark.skipif(shutil.which("g++") is None, reason="no host C++ compiler")
+def test_copy_modify_set_compiles(tmp_path):
+    res = _syntax_check(tmp_path, "setter", SETTER_BODY)
+    assert res.returncode == 0, res.stderr[-4000:]
