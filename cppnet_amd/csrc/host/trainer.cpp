@@ -182,7 +182,11 @@ struct cnt_session
     template <class L>
     void add_params(const std::shared_ptr<L>& l)
     {
-        L* p = l.get();
+        add_params(l.get());
+    }
+    template <class L>
+    void add_params(L* p)
+    {
         params.push_back({[p]() -> DeviceTensor& { return p->weights(); },
                           [p]() -> DeviceTensor& { return p->grad_weights(); }});
         if (p->has_bias())
@@ -470,6 +474,54 @@ int cnt_rnn_create(cnt_session** out, int cell, int64_t batch, int64_t seq_len, 
         s->lr = lr;
         s->X = DeviceTensor::zeros({batch, seq_len, input_size});
         s->Y = DeviceTensor::zeros({batch, out_features});
+        Device::synchronize();
+        *out = s.release();
+    });
+}
+
+int cnt_resnet_create(cnt_session** out, int64_t in_features, int64_t width, int depth, int64_t last_width,
+                      int64_t classes, int64_t batch, float lr, float beta1, float beta2, float eps, uint64_t seed)
+{
+    return guarded("cnt_resnet_create", [&] {
+        if (!out) throw std::invalid_argument("NULL out pointer");
+        *out = nullptr;
+        if (in_features <= 0 || width <= 0 || depth < 0 || last_width <= 0 || classes <= 0 || batch <= 0)
+            throw std::invalid_argument("sizes must be positive and depth >= 0");
+        auto s = new_session(seed);
+        StreamScope scope(s.get());
+        const int W = static_cast<int>(width);
+        // residual_benckmark.cpp:108-152: proj (he) -> ReLU -> [Residual -> ReLU] x depth -> head (xavier)
+        auto proj = std::make_shared<Layers::Linear>(static_cast<int>(in_features), W, "proj", true, true, "gpu", "he");
+        s->model.add_layer(proj);
+        s->keep.push_back(proj);
+        s->add_params(proj);
+        s->model.add_activation(std::make_shared<Activations::ReLU>("gpu"));
+        int w = W;
+        for (int d = 0; d < depth; ++d)
+        {
+            const std::string tag = "res" + std::to_string(d);
+            const int w_out = d + 1 == depth ? static_cast<int>(last_width) : W;
+            auto fc_a = std::make_shared<Layers::Linear>(w, W, tag + "_a", true, true, "gpu", "he");
+            auto fc_b = std::make_shared<Layers::Linear>(W, w_out, tag + "_b", true, true, "gpu", "he");
+            std::vector<std::shared_ptr<Layers::Layer>> block = {fc_a, fc_b};
+            auto res = std::make_shared<Layers::Residual>(block, w, w_out, "gpu");
+            s->model.add_layer(res);
+            s->keep.push_back(res);
+            s->add_params(fc_a);
+            s->add_params(fc_b);
+            if (res->has_projection()) s->add_params(res->projection());
+            s->model.add_activation(std::make_shared<Activations::ReLU>("gpu"));
+            w = w_out;
+        }
+        auto head = std::make_shared<Layers::Linear>(w, static_cast<int>(classes), "head", true, true, "gpu", "xavier");
+        s->model.add_layer(head);
+        s->keep.push_back(head);
+        s->add_params(head);
+        s->loss = make_loss(CNT_LOSS_SOFTMAX_CE);
+        s->opt = std::make_unique<Optimizers::Adam>(beta1, beta2, eps, "gpu");
+        s->lr = lr;
+        s->X = DeviceTensor::zeros({batch, in_features});
+        s->Y = DeviceTensor::zeros({batch, classes});
         Device::synchronize();
         *out = s.release();
     });

@@ -42,6 +42,8 @@ def load() -> C.CDLL:
                                  C.c_uint64]),
         "cnt_transformer_create": (i32, [C.POINTER(vp), i64, i64, i64, i64, i64, i32, i64, i64, f32,
                                          f32, f32, f32, C.c_uint64]),
+        "cnt_resnet_create": (i32, [C.POINTER(vp), i64, i64, i32, i64, i64, i64, f32, f32, f32, f32,
+                                    C.c_uint64]),
         "cnt_set_batch_tokens": (i32, [vp, vp, vp]),
         "cnt_destroy": (i32, [vp]),
         "cnt_set_optimizer": (i32, [vp, i32, f32, f32]),
@@ -285,6 +287,55 @@ def synthetic_transformer(cfg: TransformerConfig, rng: np.random.Generator):
     return params, ids, Y.ravel()
 
 
+@dataclass
+class ResNetConfig:
+    """The reference's residual benchmark network (residual_benckmark.cpp:104-152):
+    Linear(in, W) -> ReLU -> depth x [Residual(Linear(W, W), Linear(W, w')) -> ReLU]
+    -> Linear(w_last, classes) -> softmax-CE; w' = W except the last block's,
+    which is last_width (a projection shortcut when it differs from W)."""
+    name: str
+    in_features: int
+    width: int
+    depth: int
+    classes: int
+    batch: int
+    last_width: int = 0  # 0: width (identity shortcuts throughout)
+    lr: float = 1e-3
+    beta1: float = 0.9
+    beta2: float = 0.999
+    eps: float = 1e-8
+    seed: int = 1234
+    loss: str = "softmax_ce"
+
+    def __post_init__(self):
+        if not self.last_width:
+            self.last_width = self.width
+
+
+def synthetic_resnet(cfg: ResNetConfig, rng: np.random.Generator):
+    """Parameters in session order (he-uniform for the proj and block
+    Linears as the benchmark builds them, init.cpp:49-61; xavier for the
+    head and the projection, linear.hpp's default; biases 0), X ~ N(0,1)
+    [B, in], one-hot uniform labels.  All ColMajor flat float32."""
+    def he(i, o):
+        lim = np.sqrt(6.0 / i)
+        return rng.uniform(-lim, lim, i * o).astype(np.float32)
+    W = cfg.width
+    params = [he(cfg.in_features, W), np.zeros(W, np.float32)]
+    for d in range(cfg.depth):
+        w_out = cfg.last_width if d + 1 == cfg.depth else W
+        params += [he(W, W), np.zeros(W, np.float32), he(W, w_out), np.zeros(w_out, np.float32)]
+        if w_out != W:
+            params.append(xavier(rng, W, w_out))
+    w_last = cfg.last_width if cfg.depth else W
+    params += [xavier(rng, w_last, cfg.classes), np.zeros(cfg.classes, np.float32)]
+    X = rng.standard_normal(cfg.batch * cfg.in_features).astype(np.float32)
+    labels = rng.integers(0, cfg.classes, cfg.batch)
+    Y = np.zeros((cfg.classes, cfg.batch), np.float32)
+    Y[labels, np.arange(cfg.batch)] = 1.0
+    return params, X, Y.ravel()
+
+
 def xavier(rng: np.random.Generator, fan_in: int, fan_out: int) -> np.ndarray:
     """xavier-uniform [fan_in, fan_out] (init.cpp:21-33), ColMajor flat."""
     lim = np.sqrt(6.0 / (fan_in + fan_out))
@@ -326,6 +377,12 @@ class Session:
                                               cfg.classes, cfg.lr, cfg.beta1, cfg.beta2, cfg.eps,
                                               cfg.seed))
             self.x_size = cfg.batch * cfg.seq_len
+            self.y_size = cfg.batch * cfg.classes
+        elif isinstance(cfg, ResNetConfig):
+            _check(lib.cnt_resnet_create(C.byref(h), cfg.in_features, cfg.width, cfg.depth, cfg.last_width,
+                                         cfg.classes, cfg.batch, cfg.lr, cfg.beta1, cfg.beta2, cfg.eps,
+                                         cfg.seed))
+            self.x_size = cfg.batch * cfg.in_features
             self.y_size = cfg.batch * cfg.classes
         elif isinstance(cfg, RNNConfig):
             _check(lib.cnt_rnn_create(C.byref(h), CELL[cfg.cell], cfg.batch,

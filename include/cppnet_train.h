@@ -69,6 +69,18 @@ int cnt_cnn_create(cnt_session** out, int n_conv, const int64_t* conv_spec, int 
 int cnt_rnn_create(cnt_session** out, int cell, int64_t batch, int64_t seq_len,
                    int64_t input_size, int64_t hidden_size, int64_t out_features, float lr,
                    float beta1, float beta2, float eps, uint64_t seed);
+/* Residual MLP, the reference's residual benchmark network
+ * (benchmarks/residual_benckmark.cpp:104-152): Linear(in_features -> width,
+ * "he") -> ReLU -> depth x [Residual({Linear(w -> width, "he"), Linear(width
+ * -> w', "he")}, w, w') -> ReLU] -> Linear(w_last -> classes, "xavier") ->
+ * SoftmaxCrossEntropy("mean"), Adam.  w = width for every block; w' = width
+ * except for the last block, whose w' = last_width (a bias-free projection
+ * shortcut when last_width != width, residual.cpp:31-36).  Parameters:
+ * proj W, b; per block fc_a W, b, fc_b W, b [, projection W]; head W, b.
+ * ref: Residual::forward/backward/step src/CppNet/layers/residual.cpp:23-159 */
+int cnt_resnet_create(cnt_session** out, int64_t in_features, int64_t width, int depth, int64_t last_width,
+                      int64_t classes, int64_t batch, float lr, float beta1, float beta2, float eps,
+                      uint64_t seed);
 /* Transformer encoder classifier (config 5): Embedding(vocab, D) -> n_blocks x
  * [r = MultiHeadAttention(D, heads)(x, x, x) + x; h = BatchNorm(D) on the
  * [B*S, D] view; y = Linear(ffn -> D)(GELU(Linear(D -> ffn)(h))) + h] ->

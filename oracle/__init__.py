@@ -24,6 +24,11 @@ _SIGS = {
     "cnref_linear_forward": (None, [_f, _f, _f, _f, i64, i64, i64]),
     "cnref_linear_backward": (None, [_f, _f, _f, _f, _f, _f, i64, i64, i64, i32, i32]),
     "cnref_column_sum": (None, [_f, _f, i64, i64, i32]),
+    "cnref_add": (None, [_f, _f, _f, i64]),
+    "cnref_residual_forward": (None, [i32, C.POINTER(i64), C.POINTER(_f), C.POINTER(_f), _f, _f,
+                                      C.POINTER(_f), _f, i64]),
+    "cnref_residual_backward": (None, [i32, C.POINTER(i64), C.POINTER(_f), _f, _f, C.POINTER(_f), _f,
+                                       C.POINTER(_f), C.POINTER(_f), _f, _f, i64]),
     "cnref_relu_forward": (None, [_f, _f, i64]),
     "cnref_leaky_relu_forward": (None, [_f, _f, i64, f32]),
     "cnref_leaky_relu_backward": (None, [_f, _f, _f, i64, f32]),

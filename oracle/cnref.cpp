@@ -119,6 +119,56 @@ void cnref_linear_backward(const float* X, const float* W, const float* dY, floa
   if (dX) cnref_gemm_f32(0, 1, B, I, O, 1.f, dY, B, W, I, 0.f, dX, B, nullptr, 0);
 }
 
+void cnref_add(const float* a, const float* b, float* y, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) y[i] = a[i] + b[i];
+}
+
+// Residual::forward (residual.cpp:44-87): the block's Linear layers in
+// order (each caches its input), the shortcut (identity or the bias-free
+// "ResProj" Linear, residual.cpp:31-36), then out + shortcut.
+void cnref_residual_forward(int n_block, const int64_t* sizes, const float* const* W,
+                            const float* const* b, const float* Wp, const float* x,
+                            float* const* acts, float* y, int64_t B) {
+  const float* h = x;
+  for (int i = 0; i < n_block; ++i) {
+    cnref_linear_forward(h, W[i], b[i], acts[i], B, sizes[i], sizes[i + 1]);
+    h = acts[i];
+  }
+  const int64_t O = sizes[n_block];
+  if (Wp) {
+    std::vector<float> sc((size_t)(B * O));
+    cnref_linear_forward(x, Wp, nullptr, sc.data(), B, sizes[0], O);
+    cnref_add(h, sc.data(), y, B * O);
+  } else {
+    cnref_add(h, x, y, B * O);
+  }
+}
+
+// Residual::backward (residual.cpp:89-131): the block's Linear backwards in
+// reverse order on dY (each accumulates its grads, linear.cpp:346-352), the
+// shortcut's gradient (dY itself, or the projection's backward on dY), and
+// their sum.
+void cnref_residual_backward(int n_block, const int64_t* sizes, const float* const* W,
+                             const float* Wp, const float* x, const float* const* acts,
+                             const float* dY, float* const* gW, float* const* gb, float* gWp,
+                             float* dX, int64_t B) {
+  std::vector<float> g(dY, dY + B * sizes[n_block]), gi;
+  for (int i = n_block - 1; i >= 0; --i) {
+    const float* in = i == 0 ? x : acts[i - 1];
+    gi.assign((size_t)(B * sizes[i]), 0.f);
+    cnref_linear_backward(in, W[i], g.data(), gW[i], gb[i], gi.data(), B, sizes[i], sizes[i + 1], 1, 1);
+    g.swap(gi);
+  }
+  const int64_t I = sizes[0];
+  if (Wp) {
+    std::vector<float> gs((size_t)(B * I));
+    cnref_linear_backward(x, Wp, dY, gWp, nullptr, gs.data(), B, I, sizes[n_block], 1, 1);
+    cnref_add(g.data(), gs.data(), dX, B * I);
+  } else {
+    cnref_add(g.data(), dY, dX, B * I);
+  }
+}
+
 // ReLU::forward cpu-eigen: cwiseMax(0) (relu.cpp:116-119)
 void cnref_relu_forward(const float* x, float* y, int64_t n) {
   for (int64_t i = 0; i < n; ++i) y[i] = std::max(x[i], 0.0f);

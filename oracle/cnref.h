@@ -40,6 +40,30 @@ void cnref_linear_backward(const float* X, const float* W, const float* dY, floa
                            int trainable, int accumulate);
 void cnref_column_sum(const float* in, float* out, int64_t rows, int64_t cols, int accumulate);
 
+/* y = a + b elementwise (the cpu-eigen `out + shortcut` of residual.cpp:69-71
+ * and `grad_block + grad_shortcut` of residual.cpp:113-115). */
+void cnref_add(const float* a, const float* b, float* y, int64_t n);
+/* Residual over [B, sizes[0]] (residual.cpp:44-159, cpu-eigen branches).
+ * The block is n_block Linear layers, layer i mapping sizes[i] -> sizes[i+1]
+ * with weights W[i] [sizes[i], sizes[i+1]] and bias b[i] (NULL: bias-free);
+ * the shortcut is the input itself when Wp is NULL (then sizes[0] ==
+ * sizes[n_block]) or the bias-free projection x Wp, Wp [sizes[0],
+ * sizes[n_block]] (residual.cpp:31-36).
+ * forward: acts[i] receives the output of block layer i ([B, sizes[i+1]];
+ *   Linear::forward caches its input, so backward reads x and acts[0..n-2]);
+ *   y = acts[n_block-1] + shortcut.
+ * backward: the block's Linear backwards in reverse order, each accumulating
+ *   into gW[i] / gb[i] (linear.cpp:346-352; gb[i] NULL when bias-free), the
+ *   projection's backward on dY accumulating into gWp, and dX = the block's
+ *   input gradient + the shortcut's (residual.cpp:89-131). */
+void cnref_residual_forward(int n_block, const int64_t* sizes, const float* const* W,
+                            const float* const* b, const float* Wp, const float* x,
+                            float* const* acts, float* y, int64_t B);
+void cnref_residual_backward(int n_block, const int64_t* sizes, const float* const* W,
+                             const float* Wp, const float* x, const float* const* acts,
+                             const float* dY, float* const* gW, float* const* gb, float* gWp,
+                             float* dX, int64_t B);
+
 /* Activations (relu.cpp:97-225; sigmoid.cpp:97-231; tanh.cpp:136-219) */
 void cnref_relu_forward(const float* x, float* y, int64_t n);
 void cnref_relu_backward(const float* y, const float* dy, float* dx, int64_t n);

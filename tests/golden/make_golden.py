@@ -165,6 +165,24 @@ CASES = [
          X=[[[[1.0, 3.0], [5.0, 7.0]]]], expected=[[7.0]], tol=1e-5),
     dict(op="global_maxpool_backward", source="tests/layers/test_global_pool.cpp:114-127",
          X=[[[[1.0, 3.0], [5.0, 7.0]]]], dY=[[1.0]], expected=[[[[0.0, 0.0], [0.0, 1.0]]]], tol=1e-6),
+    # ---- Residual (residual.cpp) ----------------------------------------------
+    dict(op="residual_forward", source="tests/layers/test_residual.cpp:68-84",
+         block=[dict(W=[[0.0, 0.0], [0.0, 0.0]], b=None)], Wp=None,
+         X=[[3.0, 7.0]], expected=[[3.0, 7.0]], tol=0.1,
+         exact=[[3.0, 7.0]],
+         derivation="bias-free Linear(2,2) with zero weights: block(x) = 0, identity shortcut, y = x"),
+    dict(op="residual_forward", source="src/CppNet/layers/residual.cpp:31-36, 44-87",
+         block=[dict(W=[[1.0, 0.0, 0.0], [0.0, 1.0, 0.0]], b=[0.0, 0.0, 1.0])],
+         Wp=[[1.0, 1.0, 1.0], [0.0, 0.0, 0.0]],
+         X=[[3.0, 7.0]],
+         exact=[[6.0, 10.0, 4.0]],
+         derivation="in 2 != out 3, so the shortcut is the bias-free projection x Wp = [3, 3, 3]; "
+                    "block(x) = x W + b = [3, 7, 1]; y = [6, 10, 4]", tol=1e-6),
+    dict(op="residual_backward", source="src/CppNet/layers/residual.cpp:89-131",
+         block=[dict(W=[[2.0, 0.0], [0.0, 3.0]], b=[0.0, 0.0])], Wp=None,
+         X=[[1.0, 1.0]], dY=[[1.0, 1.0]],
+         exact=[[3.0, 4.0]], exact_gW=[[[1.0, 1.0], [1.0, 1.0]]], exact_gb=[[1.0, 1.0]],
+         derivation="dX = dY W^T + dY = [2, 3] + [1, 1]; gW = x^T dY; gb = sum_batch dY", tol=1e-6),
     # ---- Dropout (dropout.cpp) ----------------------------------------------------
     dict(op="dropout_scale", source="tests/layers/test_dropout.cpp:51-62",
          p=0.5, x=1.0, expected_kept=2.0, tol=1e-5,
