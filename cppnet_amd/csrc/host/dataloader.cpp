@@ -8,6 +8,7 @@
 #include <string>
 #include <thread>
 #include <utility>
+#include <vector>
 
 #include "CppNet/core/device.hpp"
 #include "CppNet/utils/init.hpp"
@@ -22,8 +23,38 @@ namespace CppNet
             int device = 0;
             std::size_t cursor = 0;  // next batch of the epoch to deliver
 
-            // Resident: the dataset sample-major in HBM and the epoch's order
-            DeviceTensor xs, ys, idx;
+            // Resident: the dataset sample-major in HBM and the epoch's order.
+            // The gathers run asynchronously on the consumer's stream, so the
+            // order is double-buffered (epoch e reads idx[e % 2]) and each
+            // buffer is fenced: after every gather that reads idx[p], an event
+            // per consumer stream is re-recorded, and the host waits on
+            // buffer p's events before it overwrites idx[p] two epochs later
+            // (long complete by then) or frees the dataset.
+            DeviceTensor xs, ys, idx[2];
+            int cur = 0;
+            std::vector<std::pair<cnhip_stream_t, void*>> fence[2];
+
+            void fence_read(cnhip_stream_t s)
+            {
+                void* ev = nullptr;
+                for (auto& f : fence[cur])
+                    if (f.first == s) ev = f.second;
+                if (!ev)
+                {
+                    Device::check(cnhip_event_create(&ev), "DataLoader::next");
+                    fence[cur].emplace_back(s, ev);
+                }
+                Device::check(cnhip_event_record(ev, s), "DataLoader::next");
+            }
+            void wait_fences(int p)
+            {
+                for (auto& f : fence[p])
+                {
+                    (void)cnhip_event_synchronize(f.second);
+                    (void)cnhip_event_destroy(f.second);
+                }
+                fence[p].clear();
+            }
 
             // Stream: kSlots page-locked host slots and as many device slots,
             // each [B*F features | B*L labels]; batch k uses slot k % kSlots.
@@ -47,6 +78,8 @@ namespace CppNet
             ~Stager()
             {
                 stop_worker();
+                wait_fences(0);  // gathers still queued read xs, ys and idx
+                wait_fences(1);
                 if (copy) (void)cnhip_stream_synchronize(copy);
                 for (int s = 0; s < kSlots; ++s)
                 {
@@ -165,7 +198,8 @@ namespace CppNet
                 st->ys = DeviceTensor::empty({L, N});
                 Device::check(cnhip_transpose(tx.data(), st->xs.data(), N, F, Device::stream()), "DataLoader");
                 Device::check(cnhip_transpose(ty.data(), st->ys.data(), N, L, Device::stream()), "DataLoader");
-                st->idx = DeviceTensor::empty({N});
+                st->idx[0] = DeviceTensor::empty({N});
+                st->idx[1] = DeviceTensor::empty({N});
                 Device::synchronize();
             }
             else
@@ -192,7 +226,9 @@ namespace CppNet
             st.cursor = 0;
             if (st.mode == Staging::Resident)
             {
-                if (num_samples_) st.idx.copy_from_host(indices_.data());  // one small upload per epoch
+                st.cur ^= 1;
+                st.wait_fences(st.cur);  // the epoch before last has finished reading it
+                if (num_samples_) st.idx[st.cur].copy_from_host(indices_.data());  // one small upload per epoch
                 return;
             }
             st.stop_worker();
@@ -268,9 +304,10 @@ namespace CppNet
             const int64_t N = num_samples_, F = num_features_, L = num_labels_, B = batch_size_;
             if (st.mode == Staging::Resident)
             {
-                const int32_t* idx = st.idx.idata() + static_cast<int64_t>(k) * B;
+                const int32_t* idx = st.idx[st.cur].idata() + static_cast<int64_t>(k) * B;
                 Device::check(cnhip_gather_batch(st.xs.data(), st.ys.data(), idx, x, y, N, F, L, bs, Device::stream()),
                               "DataLoader::next");
+                st.fence_read(Device::stream());
             }
             else
             {

@@ -5,6 +5,7 @@
 #include <cstdint>
 #include <cstring>
 #include <fstream>
+#include <functional>
 #include <sstream>
 #include <stdexcept>
 #include <string>
@@ -13,6 +14,7 @@
 #include "CppNet/layers/attention.hpp"
 #include "CppNet/layers/batch_norm.hpp"
 #include "CppNet/layers/conv2d.hpp"
+#include "CppNet/layers/dropout.hpp"
 #include "CppNet/layers/embedding.hpp"
 #include "CppNet/layers/linear.hpp"
 #include "CppNet/layers/lstm.hpp"
@@ -30,6 +32,7 @@ namespace CppNet
         {
             constexpr int32_t kModelMagic = 0x434E4554;  // "CNET" (serialization.cpp:148)
             constexpr int32_t kExtMagic = 0x434E5831;    // "CNX1"
+            constexpr int32_t kRngMagic = 0x434E5253;    // "CNRS": Dropout generator positions
 
             // ------------------------------------------------------------ records
             void put_i32(std::ostream& os, int32_t v) { os.write(reinterpret_cast<const char*>(&v), 4); }
@@ -38,6 +41,16 @@ namespace CppNet
             {
                 int32_t v = 0;
                 if (!is.read(reinterpret_cast<char*>(&v), 4))
+                    throw std::runtime_error(std::string("Truncated model file (reading ") + what + ")");
+                return v;
+            }
+
+            void put_u64(std::ostream& os, uint64_t v) { os.write(reinterpret_cast<const char*>(&v), 8); }
+
+            uint64_t get_u64(std::istream& is, const char* what)
+            {
+                uint64_t v = 0;
+                if (!is.read(reinterpret_cast<char*>(&v), 8))
                     throw std::runtime_error(std::string("Truncated model file (reading ") + what + ")");
                 return v;
             }
@@ -157,6 +170,15 @@ namespace CppNet
                     throw std::runtime_error("save_checkpoint: no parameter layout known for a trainable layer type");
             }
 
+            // the model's Dropout layers, in order
+            std::vector<Layers::Dropout*> dropouts(const std::vector<Layers::Layer*>& layers)
+            {
+                std::vector<Layers::Dropout*> out;
+                for (Layers::Layer* l : layers)
+                    if (auto* d = dynamic_cast<Layers::Dropout*>(l)) out.push_back(d);
+                return out;
+            }
+
             std::vector<DeviceTensor*> all_params(const std::vector<Layers::Layer*>& layers)
             {
                 std::vector<DeviceTensor*> out;
@@ -205,12 +227,33 @@ namespace CppNet
                 }
             }
 
+            // A parsed, checked piece of a model file that writes itself into
+            // the model when called.  Loading parses and checks the whole file
+            // first and applies the pieces only then, so a file that is
+            // refused leaves every parameter and optimizer state unchanged.
+            using Apply = std::function<void()>;
+
+            void check_dims(const std::vector<int64_t>& got, const std::vector<int64_t>& want, std::size_t idx,
+                            const char* what)
+            {
+                if (got != want)
+                    throw std::runtime_error("Shape mismatch at layer index " + std::to_string(idx) + " (" + what +
+                                             "): " + shape_str(got) + " in the file, " + shape_str(want) +
+                                             " in the model");
+            }
+            template <int R>
+            std::vector<int64_t> dims_of(const Tensor<float, R>& t)
+            {
+                return std::vector<int64_t>(t.dimensions().begin(), t.dimensions().end());
+            }
+
             // serialization.cpp:195-256: records are matched to the trainable
             // layers in order; what follows the last one is left unread
-            void read_cnet(std::istream& is, const std::vector<Layers::Layer*>& layers)
+            std::vector<Apply> read_cnet(std::istream& is, const std::vector<Layers::Layer*>& layers)
             {
                 if (get_i32(is, "magic") != kModelMagic) throw std::runtime_error("Invalid model file (bad magic number)");
                 const int32_t nlayers = get_i32(is, "layer count");
+                std::vector<Apply> out;
                 std::size_t idx = 0;
                 for (int32_t i = 0; i < nlayers; ++i)
                 {
@@ -223,26 +266,47 @@ namespace CppNet
                     {
                         auto* lin = dynamic_cast<Layers::Linear*>(l);
                         if (!lin) throw std::runtime_error(mismatch);
-                        lin->set_weights(get_2d(is));
-                        if (lin->has_bias()) lin->set_biases(get_1d(is));
+                        Tensor<float, 2> W = get_2d(is);
+                        check_dims(dims_of(W), lin->weights().dims(), idx, "Linear weights");
+                        Tensor<float, 1> b;
+                        if (lin->has_bias())
+                        {
+                            b = get_1d(is);
+                            check_dims(dims_of(b), {lin->get_output_size()}, idx, "Linear biases");
+                        }
+                        out.push_back([lin, W, b] {
+                            lin->set_weights(W);
+                            if (lin->has_bias()) lin->set_biases(b);
+                        });
                     }
                     else if (type == 2)
                     {
                         auto* bn = dynamic_cast<Layers::BatchNorm*>(l);
                         if (!bn) throw std::runtime_error(mismatch);
-                        bn->set_gamma(get_1d(is));
-                        bn->set_beta(get_1d(is));
-                        bn->set_running_mean(get_1d(is));
-                        bn->set_running_var(get_1d(is));
+                        std::vector<Tensor<float, 1>> v;
+                        for (const char* what : {"gamma", "beta", "running mean", "running variance"})
+                        {
+                            v.push_back(get_1d(is));
+                            check_dims(dims_of(v.back()), {bn->get_num_features()}, idx, what);
+                        }
+                        out.push_back([bn, v] {
+                            bn->set_gamma(v[0]);
+                            bn->set_beta(v[1]);
+                            bn->set_running_mean(v[2]);
+                            bn->set_running_var(v[3]);
+                        });
                     }
                     else if (type == 3)
                     {
                         auto* emb = dynamic_cast<Layers::Embedding*>(l);
                         if (!emb) throw std::runtime_error(mismatch);
-                        emb->set_weight(get_2d(is));
+                        Tensor<float, 2> W = get_2d(is);
+                        check_dims(dims_of(W), {emb->get_vocab_size(), emb->get_embed_dim()}, idx, "Embedding weight");
+                        out.push_back([emb, W] { emb->set_weight(W); });
                     }
                     ++idx;  // type 0 (and unknown ids, as the reference) carry nothing
                 }
+                return out;
             }
 
             // ------------------------------------------------------------ extension
@@ -257,25 +321,37 @@ namespace CppNet
                 const int S = kind >= 0 ? opt->state_tensors() : 0;
                 put_i32(os, kind);
                 put_i32(os, S);
-                if (kind < 0) return;
-                std::vector<std::vector<float>> st;
-                for (DeviceTensor* p : params)
+                if (kind >= 0)
                 {
-                    int t = 0;
-                    const bool present = opt->get_state(p->data(), p->size(), st, t);
-                    put_i32(os, present ? 1 : 0);
-                    put_i32(os, t);
-                    for (int k = 0; k < S; ++k)
+                    std::vector<std::vector<float>> st;
+                    for (DeviceTensor* p : params)
                     {
-                        if (present)
-                            put_record(os, {p->size()}, st[static_cast<size_t>(k)].data());
-                        else
-                            put_record(os, {0}, nullptr);
+                        int t = 0;
+                        const bool present = opt->get_state(p->data(), p->size(), st, t);
+                        put_i32(os, present ? 1 : 0);
+                        put_i32(os, t);
+                        for (int k = 0; k < S; ++k)
+                        {
+                            if (present)
+                                put_record(os, {p->size()}, st[static_cast<size_t>(k)].data());
+                            else
+                                put_record(os, {0}, nullptr);
+                        }
                     }
+                }
+                // the mask generators' positions, so a resumed run draws the
+                // masks the uninterrupted run would have
+                const auto drops = dropouts(layers);
+                put_i32(os, kRngMagic);
+                put_i32(os, static_cast<int32_t>(drops.size()));
+                for (Layers::Dropout* d : drops)
+                {
+                    put_u64(os, d->rng_seed());
+                    put_u64(os, d->rng_offset());
                 }
             }
 
-            void read_ext(std::istream& is, const std::vector<Layers::Layer*>& layers, Optimizers::Optimizer* opt)
+            Apply read_ext(std::istream& is, const std::vector<Layers::Layer*>& layers, Optimizers::Optimizer* opt)
             {
                 if (get_i32(is, "extension magic") != kExtMagic)
                     throw std::runtime_error("load_checkpoint: no checkpoint extension after the model records");
@@ -326,11 +402,35 @@ namespace CppNet
                     throw std::runtime_error("load_checkpoint: the file's optimizer state is of kind " +
                                              std::to_string(kind) + ", the optimizer's kind is " +
                                              std::to_string(opt->kind_code()));
-                for (std::size_t i = 0; i < params.size(); ++i)
-                    if (!values[i].empty()) params[i]->copy_from_host(values[i].data());
-                if (opt && kind >= 0)
+                // Dropout generator positions (absent from files written before
+                // this section existed: those leave the generators as they are)
+                const auto drops = dropouts(layers);
+                std::vector<std::pair<uint64_t, uint64_t>> rng;
+                int32_t tag = 0;
+                if (is.read(reinterpret_cast<char*>(&tag), 4))
+                {
+                    if (tag != kRngMagic) throw std::runtime_error("load_checkpoint: corrupt extension after the optimizer state");
+                    const int32_t n = get_i32(is, "dropout count");
+                    if (n != static_cast<int32_t>(drops.size()))
+                        throw std::runtime_error("load_checkpoint: the file holds " + std::to_string(n) +
+                                                 " Dropout generators, the model has " + std::to_string(drops.size()) +
+                                                 " Dropout layers");
+                    for (int32_t i = 0; i < n; ++i)
+                    {
+                        const uint64_t seed = get_u64(is, "dropout seed");
+                        rng.emplace_back(seed, get_u64(is, "dropout offset"));
+                    }
+                }
+                return [params, values = std::move(values), opt, kind, states = std::move(states), drops,
+                        rng = std::move(rng)] {
                     for (std::size_t i = 0; i < params.size(); ++i)
-                        if (states[i].present) opt->set_state(params[i]->data(), params[i]->size(), states[i].tensors, states[i].t);
+                        if (!values[i].empty()) params[i]->copy_from_host(values[i].data());
+                    if (opt && kind >= 0)
+                        for (std::size_t i = 0; i < params.size(); ++i)
+                            if (states[i].present)
+                                opt->set_state(params[i]->data(), params[i]->size(), states[i].tensors, states[i].t);
+                    for (std::size_t i = 0; i < rng.size(); ++i) drops[i]->set_rng_state(rng[i].first, rng[i].second);
+                };
             }
 
             // ------------------------------------------------------------ .npy
@@ -479,8 +579,11 @@ namespace CppNet
         {
             std::ifstream is(path, std::ios::binary);
             if (!is) throw std::runtime_error("Cannot open file for reading: " + path);
-            read_cnet(is, layers);
-            if (extension) read_ext(is, layers, optimizer);
+            const std::vector<Apply> records = read_cnet(is, layers);
+            Apply ext;
+            if (extension) ext = read_ext(is, layers, optimizer);
+            for (const Apply& a : records) a();
+            if (ext) ext();
         }
 
         void save_model(const std::string& path, const Models::SequentialModel& model)

@@ -343,11 +343,20 @@ const char* cnt_last_error(void) { return g_err.c_str(); }
 int cnt_mlp_create(cnt_session** out, int n_linear, const int64_t* sizes, int hidden_act, int out_act,
                    int loss, int64_t batch, float lr, float beta1, float beta2, float eps, uint64_t seed)
 {
+    return cnt_mlp_create_ex(out, n_linear, sizes, hidden_act, out_act, loss, batch, lr, beta1, beta2, eps, seed,
+                             0.0f);
+}
+
+int cnt_mlp_create_ex(cnt_session** out, int n_linear, const int64_t* sizes, int hidden_act, int out_act,
+                      int loss, int64_t batch, float lr, float beta1, float beta2, float eps, uint64_t seed,
+                      float dropout)
+{
     return guarded("cnt_mlp_create", [&] {
         if (!out) throw std::invalid_argument("NULL out pointer");
         *out = nullptr;
         if (n_linear < 1 || !sizes) throw std::invalid_argument("need at least one Linear layer");
         if (batch <= 0) throw std::invalid_argument("batch must be positive");
+        if (!(dropout >= 0.0f && dropout < 1.0f)) throw std::invalid_argument("dropout must be in [0, 1)");
         auto s = new_session(seed);
         StreamScope scope(s.get());
         for (int i = 0; i < n_linear; ++i)
@@ -361,6 +370,12 @@ int cnt_mlp_create(cnt_session** out, int n_linear, const int64_t* sizes, int hi
             s->add_params(lin);
             auto act = make_act(i + 1 < n_linear ? hidden_act : out_act);
             if (act) s->model.add_activation(act);
+            if (dropout > 0.0f && i + 1 < n_linear)
+            {
+                auto drop = std::make_shared<Layers::Dropout>(dropout, "gpu");
+                s->model.add_layer(drop);
+                s->keep.push_back(drop);
+            }
         }
         s->loss = make_loss(loss);
         s->opt = std::make_unique<Optimizers::Adam>(beta1, beta2, eps, "gpu");
@@ -1026,6 +1041,11 @@ int cnt_capture_step(cnt_session* s)
         if (!s->warm)
             throw std::logic_error("run one step eagerly before capturing: it sizes the buffers and "
                                    "workspaces the graph will refer to");
+        // A Dropout layer's mask position advances on the host every forward;
+        // a replayed graph would repeat the captured step's masks.
+        for (Layers::Layer* l : s->all_layers())
+            if (dynamic_cast<Layers::Dropout*>(l))
+                throw std::logic_error("a model with Dropout cannot be captured: each step draws new masks");
         Device::check(cnhip_graph_begin_capture(s->stream), "capture");
         s->graph_pool = Device::open_pool();
         cnhip_graph_t g = nullptr;

@@ -43,6 +43,15 @@ namespace CppNet
             float get_p() const { return p_; }
             /// The last training forward's mask as 0/1 floats (host copy).
             std::vector<float> get_mask() const;
+            /// The mask generator's seed and position (the element count of
+            /// all training forwards so far); checkpoints save and restore them.
+            uint64_t rng_seed() const { return seed_; }
+            uint64_t rng_offset() const { return offset_; }
+            void set_rng_state(uint64_t seed, uint64_t offset)
+            {
+                seed_ = seed;
+                offset_ = offset;
+            }
 
         private:
             float p_;

@@ -36,6 +36,8 @@ def load() -> C.CDLL:
         "cnt_last_error": (C.c_char_p, []),
         "cnt_mlp_create": (i32, [C.POINTER(vp), i32, C.POINTER(i64), i32, i32, i32, i64, f32, f32,
                                  f32, f32, C.c_uint64]),
+        "cnt_mlp_create_ex": (i32, [C.POINTER(vp), i32, C.POINTER(i64), i32, i32, i32, i64, f32, f32,
+                                    f32, f32, C.c_uint64, f32]),
         "cnt_cnn_create": (i32, [C.POINTER(vp), i32, C.POINTER(i64), i32, C.POINTER(i64), i64, f32,
                                  f32, f32, f32, C.c_uint64]),
         "cnt_rnn_create": (i32, [C.POINTER(vp), i32, i64, i64, i64, i64, i64, f32, f32, f32, f32,
@@ -108,6 +110,7 @@ class MLPConfig:
     optimizer: str = "adam"   # OPT key; "adam" uses beta1/beta2/eps above
     opt_hyper: float = 0.9    # Momentum's mu / RMSProp's rho
     opt_eps: float = 1e-8     # Adagrad's / RMSProp's epsilon
+    dropout: float = 0.0      # Dropout(p) after every hidden activation when > 0
 
 
 def mlp_config(config: int, batch: int | None = None) -> MLPConfig:
@@ -399,9 +402,9 @@ class Session:
             self.y_size = cfg.batch * cfg.classes
         else:
             sizes = (C.c_int64 * len(cfg.sizes))(*cfg.sizes)
-            _check(lib.cnt_mlp_create(C.byref(h), len(cfg.sizes) - 1, sizes, ACT[cfg.hidden_act],
-                                      ACT[cfg.out_act], LOSS[cfg.loss], cfg.batch, cfg.lr,
-                                      cfg.beta1, cfg.beta2, cfg.eps, cfg.seed))
+            _check(lib.cnt_mlp_create_ex(C.byref(h), len(cfg.sizes) - 1, sizes, ACT[cfg.hidden_act],
+                                         ACT[cfg.out_act], LOSS[cfg.loss], cfg.batch, cfg.lr,
+                                         cfg.beta1, cfg.beta2, cfg.eps, cfg.seed, cfg.dropout))
             self.x_size = cfg.batch * cfg.sizes[0]
             self.y_size = cfg.batch * cfg.sizes[-1]
         self.h = h

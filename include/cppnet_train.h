@@ -53,6 +53,12 @@ const char* cnt_last_error(void);
 int cnt_mlp_create(cnt_session** out, int n_linear, const int64_t* sizes, int hidden_act,
                    int out_act, int loss, int64_t batch, float lr, float beta1, float beta2,
                    float eps, uint64_t seed);
+/* The same with Dropout(dropout) after every hidden activation (dropout in
+ * [0, 1); 0 adds none).  Checkpoints save and restore the Dropout layers'
+ * mask-generator positions.  ref: src/CppNet/layers/dropout.cpp:15-270 */
+int cnt_mlp_create_ex(cnt_session** out, int n_linear, const int64_t* sizes, int hidden_act,
+                      int out_act, int loss, int64_t batch, float lr, float beta1, float beta2,
+                      float eps, uint64_t seed, float dropout);
 /* CNN: n_conv blocks of Conv2D(in, out, kernel, stride, padding; bias) -> ReLU
  * -> MaxPool2D(pool), conv_spec holding 5 values per block; then Flatten ->
  * Linear(C*H*W -> classes) -> SoftmaxCrossEntropy("mean"), Adam.  input_shape

@@ -167,7 +167,15 @@ RESUME = {
     "elman_adagrad": lambda: (_opt(trainer.rnn_config(4, batch=8, seq_len=6, cell="rnn"), "adagrad"),
                               trainer.synthetic_rnn),
     "transformer_adam": lambda: (_tf_cfg(), trainer.synthetic_transformer),
+    # the Dropout layers' mask positions travel with the checkpoint
+    "mlp_dropout_adam": lambda: (_dropout_cfg(), trainer.synthetic_mlp),
 }
+
+
+def _dropout_cfg():
+    cfg = _mlp_cfg()
+    cfg.dropout = 0.3
+    return cfg
 
 
 def _opt(cfg, opt):
@@ -213,6 +221,26 @@ def test_checkpoint_resumes_exactly(gpu, tmp_path, name):
     b.close()
 
 
+def _refused_load_changes_nothing(cfg, path, match, X, Y):
+    """A refused load leaves the session's parameters and its training run as
+    they were: the next step equals that of an untouched twin session."""
+    params = trainer.synthetic_mlp(cfg, np.random.default_rng(99))[0]
+    s, twin = trainer.Session(cfg), trainer.Session(cfg)
+    for x in (s, twin):
+        x.set_params(params)
+        x.set_batch(X, Y)
+        x.step()
+    with pytest.raises(Exception, match=match):
+        s.load_checkpoint(path)
+    for k, (a, b) in enumerate(zip(s.get_params(), twin.get_params())):
+        assert np.array_equal(_bits(a), _bits(b)), f"parameter {k} changed by a refused load"
+    assert _bits(s.step())[0] == _bits(twin.step())[0]  # optimizer state untouched too
+    for k, (a, b) in enumerate(zip(s.get_params(), twin.get_params())):
+        assert np.array_equal(_bits(a), _bits(b)), f"parameter {k} differs one step after a refused load"
+    s.close()
+    twin.close()
+
+
 def test_checkpoint_refuses_other_optimizer_and_shapes(gpu, tmp_path):
     cfg = _mlp_cfg()
     print("[ckpt] refusals", flush=True)
@@ -221,14 +249,35 @@ def test_checkpoint_refuses_other_optimizer_and_shapes(gpu, tmp_path):
     a.set_batch(X, Y)
     a.step()
     a.save_checkpoint(tmp_path / "a.ckpt")
-    with pytest.raises(Exception, match="kind"):
-        trainer.Session(_mlp_cfg("sgd")).load_checkpoint(tmp_path / "a.ckpt")
-    other = trainer.MLPConfig("MLP 20-32-8-3", [20, 32, 8, 3], "relu", "none", "softmax_ce", 24)
-    with pytest.raises(Exception):
-        trainer.Session(other).load_checkpoint(tmp_path / "a.ckpt")
-    with pytest.raises(Exception, match="extension"):
-        trainer.Session(cfg).load_checkpoint(_save_plain(a, tmp_path))
+    # an Adam checkpoint into an SGD session: every CNET record fits, the
+    # optimizer section does not -- nothing may be written
+    sgd = _mlp_cfg("sgd")
+    _refused_load_changes_nothing(sgd, tmp_path / "a.ckpt", "kind", X, Y)
+    # the first two Linear records fit, the third does not
+    other = trainer.MLPConfig("MLP 20-32-16-4", [20, 32, 16, 4], "relu", "none", "softmax_ce", 24)
+    _, Xo, Yo = trainer.synthetic_mlp(other, np.random.default_rng(5))
+    _refused_load_changes_nothing(other, tmp_path / "a.ckpt", "hape", Xo, Yo)
+    # a plain model file has no extension
+    _refused_load_changes_nothing(cfg, _save_plain(a, tmp_path), "extension", X, Y)
+    # a checkpoint with Dropout generators into a model without Dropout layers
+    d = trainer.Session(_dropout_cfg())
+    d.set_batch(X, Y)
+    d.step()
+    d.save_checkpoint(tmp_path / "d.ckpt")
+    _refused_load_changes_nothing(cfg, tmp_path / "d.ckpt", "Dropout", X, Y)
+    d.close()
     a.close()
+
+
+def test_dropout_model_refuses_capture(gpu):
+    cfg = _dropout_cfg()
+    params, X, Y = trainer.synthetic_mlp(cfg, np.random.default_rng(6))
+    s = trainer.Session(cfg)
+    s.set_batch(X, Y)
+    s.step()
+    with pytest.raises(Exception, match="Dropout"):
+        s.capture()
+    s.close()
 
 
 def _save_plain(sess, tmp_path):

@@ -89,3 +89,48 @@ def test_session_batch_mismatch_is_refused(gpu):
         ld.next_batch(s)  # the short last batch (18) does not fit a batch-32 session
     s.close()
     ld.close()
+
+
+@pytest.mark.parametrize("mode", ["resident", "stream"])
+def test_queued_epoch_then_reset(gpu, mode):
+    """A whole epoch of batches queued on a non-blocking stream behind ~5 ms of
+    other work, then reset() (a new permutation, uploaded at once) and the
+    next epoch queued too, before any gather has run: every batch must still
+    be gathered with its own epoch's order.  Then to_device() again (which
+    frees the staged dataset) with the second epoch still queued."""
+    from cppnet_amd import _capi
+    n, f, l, batch = 2048, 96, 4, 128
+    print(f"[loader] {mode}: queued epochs across reset", flush=True)
+    X, Y = _data(n, f, l, 77)
+    ld = trainer.Loader(X.ravel(order="F"), Y.ravel(order="F"), n, f, l, batch, True, True, seed=3)
+    ld.to_device(mode)
+    lib = _capi.load()
+    st = _capi.C.c_void_p()
+    assert lib.cnhip_stream_create(_capi.C.byref(st)) == 0
+    stream = st.value
+    M = 4096
+    A = torch.randn(M * M, device="cuda")
+    Cm = torch.empty(M * M, device="cuda")
+    torch.cuda.synchronize()
+    for _ in range(12):  # ~5 ms queued ahead of the gathers
+        assert lib.cnhip_gemm_f32(0, 0, M, M, M, 1.0, A.data_ptr(), M, A.data_ptr(), M, 0.0, Cm.data_ptr(), M,
+                                  None, 0, stream) == 0
+    nb = ld.num_batches
+    epochs = []
+    for epoch in range(2):
+        host = [ld.host_batch(k) for k in range(nb)]
+        xb = torch.empty((nb, batch * f), device="cuda")
+        yb = torch.empty((nb, batch * l), device="cuda")
+        for k in range(nb):
+            assert ld.next(xb[k].data_ptr(), yb[k].data_ptr(), stream) == batch
+        epochs.append((host, xb, yb))
+        ld.reset()
+    ld.to_device(mode)  # frees the staged copy while the second epoch may still be queued
+    assert lib.cnhip_stream_synchronize(stream) == 0
+    for epoch, (host, xb, yb) in enumerate(epochs):
+        for k, (hx, hy, _) in enumerate(host):
+            np.testing.assert_array_equal(xb[k].cpu().numpy(), hx, err_msg=f"epoch {epoch} batch {k}")
+            np.testing.assert_array_equal(yb[k].cpu().numpy(), hy, err_msg=f"epoch {epoch} batch {k}")
+    assert not np.array_equal(epochs[0][0][0][0], epochs[1][0][0][0])  # the orders differ
+    assert lib.cnhip_stream_destroy(stream) == 0
+    ld.close()
