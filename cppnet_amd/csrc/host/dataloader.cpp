@@ -235,8 +235,11 @@ namespace CppNet
             st.stop = false;
             st.produced = st.taken = 0;
             st.error.clear();
-            st.worker = std::thread([this] {
-                Stager& s = *stager_;
+            // the worker is bound to this Stager, not to stager_: to_device()
+            // empties stager_ before the old Stager's destructor joins it
+            Stager* self = &st;
+            st.worker = std::thread([this, self] {
+                Stager& s = *self;
                 try
                 {
                     Device::check(cnhip_set_device(s.device), "DataLoader worker");

@@ -367,6 +367,40 @@ def synthetic_mlp(cfg: MLPConfig, rng: np.random.Generator):
     return params, X, Y
 
 
+def _onehot(rng, B, C):
+    labels = rng.integers(0, C, B)
+    Y = np.zeros((C, B), np.float32)
+    Y[labels, np.arange(B)] = 1.0
+    return Y.ravel()
+
+
+def synthetic_batch(cfg, rng: np.random.Generator):
+    """A fresh (X, Y) batch of a config, from the same distributions as its
+    synthetic_* generator, without drawing parameters (long runs take a new
+    batch every step)."""
+    if isinstance(cfg, MLPConfig):
+        B, I, O = cfg.batch, cfg.sizes[0], cfg.sizes[-1]
+        X = rng.standard_normal(B * I).astype(np.float32)
+        if cfg.loss == "bce":
+            return X, (rng.uniform(size=B * O) < 0.5).astype(np.float32)
+        if cfg.loss in ("softmax_ce", "cce"):
+            return X, _onehot(rng, B, O)
+        return X, rng.standard_normal(B * O).astype(np.float32)
+    if isinstance(cfg, CNNConfig):
+        X = rng.uniform(0.0, 1.0, int(np.prod(cfg.input_shape))).astype(np.float32)
+        return X, _onehot(rng, cfg.batch, cfg.classes)
+    if isinstance(cfg, RNNConfig):
+        X = rng.standard_normal(cfg.batch * cfg.seq_len * cfg.input_size).astype(np.float32)
+        return X, rng.standard_normal(cfg.batch * cfg.out_features).astype(np.float32)
+    if isinstance(cfg, TransformerConfig):
+        ids = rng.integers(0, cfg.vocab, cfg.batch * cfg.seq_len).astype(np.int32)
+        return ids, _onehot(rng, cfg.batch, cfg.classes)
+    if isinstance(cfg, ResNetConfig):
+        X = rng.standard_normal(cfg.batch * cfg.in_features).astype(np.float32)
+        return X, _onehot(rng, cfg.batch, cfg.classes)
+    raise TypeError(f"no batch generator for {type(cfg).__name__}")
+
+
 class Session:
     """One C++ training session (model + loss + Adam + stream) on cuda:0."""
 

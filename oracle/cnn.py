@@ -71,7 +71,8 @@ class OracleCNN:
                                       dims=(ic, oc, k, s, p, H, W, HO, WO)))
             dx = dxi
         self.fc_trace = dict(x=x, g=g, F=F)
-        self.last_grads = [gr.copy() for gr in self.grads]
+        if getattr(self, "keep", True):  # per-step diagnostics; long runs turn them off
+            self.last_grads = [gr.copy() for gr in self.grads]
         for k_, (p_, g_) in enumerate(zip(self.params, self.grads)):
             self.t[k_] += 1
             bc1 = o.cnref_bias_correction(cfg.beta1, self.t[k_])

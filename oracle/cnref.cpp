@@ -17,9 +17,79 @@
 namespace {
 int g_threads = 1;
 int g_acc_double = 0;
+
+// dst[r + R c] = trans ? src[c + ld r] : src[r + ld c], in 64 x 64 tiles.
+void copy_tiles(float* dst, int64_t R, int64_t Cn, const float* src, int64_t ld, bool trans) {
+  constexpr int64_t T = 64;
+  const int64_t tr = (R + T - 1) / T, tc = (Cn + T - 1) / T;
+#pragma omp parallel for num_threads(g_threads) schedule(static)
+  for (int64_t t = 0; t < tr * tc; ++t) {
+    const int64_t r0 = (t % tr) * T, c0 = (t / tr) * T;
+    const int64_t r1 = std::min(R, r0 + T), c1 = std::min(Cn, c0 + T);
+    if (trans) {
+      for (int64_t r = r0; r < r1; ++r)
+        for (int64_t c = c0; c < c1; ++c) dst[r + R * c] = src[c + ld * r];
+    } else {
+      for (int64_t c = c0; c < c1; ++c)
+        for (int64_t r = r0; r < r1; ++r) dst[r + R * c] = src[r + ld * c];
+    }
+  }
 }
 
+// acc[m + M n] += sum_k Am[m + M k] * Bk[k + K n], each element's products
+// added in ascending k in the accumulator type T.  An MR x 4 tile of acc is
+// held in registers across a k-panel of KB (MR = 64 bytes of T).
+template <class T>
+void gemm_panels(int64_t M, int64_t N, int64_t K, const float* Am, const float* Bk, T* acc) {
+  constexpr int64_t KB = 256, NB = 4, MR = 64 / sizeof(T);
+  const int64_t nblocks = (N + NB - 1) / NB;
+  for (int64_t k0 = 0; k0 < K; k0 += KB) {
+    const int64_t k1 = std::min(K, k0 + KB);
+#pragma omp parallel for num_threads(g_threads) schedule(static)
+    for (int64_t nb = 0; nb < nblocks; ++nb) {
+      const int64_t n0 = nb * NB, nn = std::min(NB, N - n0);
+      const float* bcol[NB];
+      for (int64_t j = 0; j < NB; ++j) bcol[j] = Bk + K * (n0 + std::min(j, nn - 1));
+      int64_t m0 = 0;
+      if (nn == NB) {
+        for (; m0 + MR <= M; m0 += MR) {
+          T c[NB][MR];
+          for (int64_t j = 0; j < NB; ++j)
+            for (int64_t i = 0; i < MR; ++i) c[j][i] = acc[m0 + i + M * (n0 + j)];
+          for (int64_t k = k0; k < k1; ++k) {
+            const float* a = Am + m0 + M * k;
+            T av[MR];
+            for (int64_t i = 0; i < MR; ++i) av[i] = a[i];
+            for (int64_t j = 0; j < NB; ++j) {
+              const T b = bcol[j][k];
+              for (int64_t i = 0; i < MR; ++i) c[j][i] += av[i] * b;
+            }
+          }
+          for (int64_t j = 0; j < NB; ++j)
+            for (int64_t i = 0; i < MR; ++i) acc[m0 + i + M * (n0 + j)] = c[j][i];
+        }
+      }
+      // rows past the last full tile, and the last partial column block
+      for (int64_t j = 0; j < nn; ++j) {
+        T* cc = acc + M * (n0 + j);
+        for (int64_t k = k0; k < k1; ++k) {
+          const T b = bcol[j][k];
+          const float* a = Am + M * k;
+          for (int64_t m = m0; m < M; ++m) cc[m] += (T)a[m] * b;
+        }
+      }
+    }
+  }
+}
+}  // namespace
+
 extern "C" {
+
+static float* g_trace[5] = {};
+void cnref_set_trace(int slot, float* buf) {
+  if (slot >= 0 && slot < 5) g_trace[slot] = buf;
+}
+float* cnref_trace(int slot) { return slot >= 0 && slot < 5 ? g_trace[slot] : nullptr; }
 
 void cnref_set_threads(int n) { g_threads = n < 1 ? 1 : n; }
 int cnref_get_threads(void) { return g_threads; }
@@ -38,45 +108,26 @@ void cnref_gemm_f32(int ta, int tb, int64_t M, int64_t N, int64_t K, float alpha
   if (M <= 0 || N <= 0) return;
   std::vector<float> Am((size_t)M * (size_t)std::max<int64_t>(K, 1));
   std::vector<float> Bk((size_t)std::max<int64_t>(K, 1) * (size_t)N);
-  for (int64_t k = 0; k < K; ++k)
-    for (int64_t m = 0; m < M; ++m) Am[m + M * k] = ta ? A[k + lda * m] : A[m + lda * k];
-  for (int64_t n = 0; n < N; ++n)
-    for (int64_t k = 0; k < K; ++k) Bk[k + K * n] = tb ? B[n + ldb * k] : B[k + ldb * n];
+  copy_tiles(Am.data(), M, K, A, lda, ta != 0);   // Am[m + M k] = op(A)(m, k)
+  copy_tiles(Bk.data(), K, N, B, ldb, tb != 0);   // Bk[k + K n] = op(B)(k, n)
 
-  const int64_t KB = 128;  // k-panel kept in cache; order within a column is unchanged
+  // Blocked for the cache without changing any element's arithmetic: a
+  // k-panel of KB is applied to a 4-column x MB-row block of the product
+  // (4 accumulator columns stay in L1 and each A value is loaded once for
+  // all four), panel after panel, so element (m, n) still receives its
+  // products in ascending k, one rounding per multiply and per add.
   std::vector<float> acc((size_t)M * (size_t)N, 0.f);
   if (g_acc_double) {
     // Variant used only to measure how far a trajectory moves under a
     // different (more accurate) summation: products and sums in double,
     // one rounding to float per element.
     std::vector<double> accd((size_t)M * (size_t)N, 0.0);
-    for (int64_t k0 = 0; k0 < K; k0 += KB) {
-      const int64_t k1 = std::min(K, k0 + KB);
-#pragma omp parallel for num_threads(g_threads) schedule(static)
-      for (int64_t n = 0; n < N; ++n) {
-        double* c = accd.data() + M * n;
-        for (int64_t k = k0; k < k1; ++k) {
-          const double b = Bk[k + K * n];
-          const float* a = Am.data() + M * k;
-          for (int64_t m = 0; m < M; ++m) c[m] += (double)a[m] * b;
-        }
-      }
-    }
+    gemm_panels(M, N, K, Am.data(), Bk.data(), accd.data());
     for (size_t i = 0; i < acc.size(); ++i) acc[i] = (float)accd[i];
   } else {
-  for (int64_t k0 = 0; k0 < K; k0 += KB) {
-    const int64_t k1 = std::min(K, k0 + KB);
+    gemm_panels(M, N, K, Am.data(), Bk.data(), acc.data());
+  }
 #pragma omp parallel for num_threads(g_threads) schedule(static)
-    for (int64_t n = 0; n < N; ++n) {
-      float* c = acc.data() + M * n;
-      for (int64_t k = k0; k < k1; ++k) {
-        const float b = Bk[k + K * n];
-        const float* a = Am.data() + M * k;
-        for (int64_t m = 0; m < M; ++m) c[m] += a[m] * b;
-      }
-    }
-  }
-  }
   for (int64_t n = 0; n < N; ++n)
     for (int64_t m = 0; m < M; ++m) {
       float v = alpha * acc[m + M * n];
@@ -280,70 +331,108 @@ void cnref_conv2d_forward(const float* X, const float* Wt, const float* b, float
                           int64_t C, int64_t H, int64_t Wd, int64_t OC, int64_t KS, int64_t S,
                           int64_t P) {
   const int64_t HO = (H + 2 * P - KS) / S + 1, WO = (Wd + 2 * P - KS) / S + 1;
+  // Each output (n, oc, oh, ow) sums its (ic, kh, kw) terms in that order and
+  // then adds the bias; the N samples of one (oc, oh, ow) are contiguous in
+  // ColMajor [N, C, H, W], so they are evaluated side by side.
 #pragma omp parallel for num_threads(g_threads) schedule(static) collapse(2)
-  for (int64_t n = 0; n < N; ++n)
-    for (int64_t oc = 0; oc < OC; ++oc)
-      for (int64_t oh = 0; oh < HO; ++oh)
-        for (int64_t ow = 0; ow < WO; ++ow) {
-          float val = 0.0f;
-          for (int64_t ic = 0; ic < C; ++ic)
-            for (int64_t kh = 0; kh < KS; ++kh)
-              for (int64_t kw = 0; kw < KS; ++kw) {
-                const int64_t ih = oh * S - P + kh, iw = ow * S - P + kw;
-                if (ih >= 0 && ih < H && iw >= 0 && iw < Wd)
-                  val += X[idx4(n, ic, ih, iw, N, C, H)] * Wt[idx4(oc, ic, kh, kw, OC, C, KS)];
-              }
-          if (b) val += b[oc];
-          Y[idx4(n, oc, oh, ow, N, OC, HO)] = val;
-        }
+  for (int64_t oc = 0; oc < OC; ++oc)
+    for (int64_t oh = 0; oh < HO; ++oh) {
+      std::vector<float> val((size_t)N);
+      for (int64_t ow = 0; ow < WO; ++ow) {
+        std::fill(val.begin(), val.end(), 0.0f);
+        for (int64_t ic = 0; ic < C; ++ic)
+          for (int64_t kh = 0; kh < KS; ++kh)
+            for (int64_t kw = 0; kw < KS; ++kw) {
+              const int64_t ih = oh * S - P + kh, iw = ow * S - P + kw;
+              if (ih < 0 || ih >= H || iw < 0 || iw >= Wd) continue;
+              const float w = Wt[idx4(oc, ic, kh, kw, OC, C, KS)];
+              const float* x = X + idx4(0, ic, ih, iw, N, C, H);
+              for (int64_t n = 0; n < N; ++n) val[(size_t)n] += x[n] * w;
+            }
+        float* y = Y + idx4(0, oc, oh, ow, N, OC, HO);
+        for (int64_t n = 0; n < N; ++n) y[n] = b ? val[(size_t)n] + b[oc] : val[(size_t)n];
+      }
+    }
 }
 
 // Conv2D::backward (conv2d.cpp:138-198).  The reference runs one serial
 // scatter loop over (n, oc, oh, ow) that accumulates gb, gW and dX.  Here the
-// same sums are evaluated as two passes that can run in parallel: gW/gb per
-// output channel (each accumulated over (n, oh, ow) in the reference's
-// order) and dX per sample (each accumulated over (oc, oh, ow, ic, kh, kw)
-// in the reference's order).  Grads are overwritten (zeroed first, 149-152).
+// same sums are evaluated in passes that can run in parallel, each element
+// receiving its terms in the reference's order: gW[oc, ic, kh, kw] and gb[oc]
+// over (n, oh, ow); dX[n, ic, ih, iw] over (oc, oh, ow).  Grads are
+// overwritten (zeroed first, 149-152).
 void cnref_conv2d_backward(const float* X, const float* Wt, const float* dY, float* gW, float* gb,
                            float* dX, int64_t N, int64_t C, int64_t H, int64_t Wd, int64_t OC,
                            int64_t KS, int64_t S, int64_t P) {
   const int64_t HO = (H + 2 * P - KS) / S + 1, WO = (Wd + 2 * P - KS) / S + 1;
+  // images per (channel, sample), row-major: Xi[((ic N + n) H + ih) W + iw]
+  std::vector<float> Xi((size_t)(N * C * H * Wd)), Gi((size_t)(N * OC * HO * WO));
 #pragma omp parallel for num_threads(g_threads) schedule(static)
-  for (int64_t oc = 0; oc < OC; ++oc) {
-    for (int64_t ic = 0; ic < C; ++ic)
-      for (int64_t kh = 0; kh < KS; ++kh)
-        for (int64_t kw = 0; kw < KS; ++kw) gW[idx4(oc, ic, kh, kw, OC, C, KS)] = 0.0f;
-    if (gb) gb[oc] = 0.0f;
-    for (int64_t n = 0; n < N; ++n)
-      for (int64_t oh = 0; oh < HO; ++oh)
-        for (int64_t ow = 0; ow < WO; ++ow) {
-          const float g = dY[idx4(n, oc, oh, ow, N, OC, HO)];
-          if (gb) gb[oc] += g;
-          for (int64_t ic = 0; ic < C; ++ic)
-            for (int64_t kh = 0; kh < KS; ++kh)
-              for (int64_t kw = 0; kw < KS; ++kw) {
-                const int64_t ih = oh * S - P + kh, iw = ow * S - P + kw;
-                if (ih >= 0 && ih < H && iw >= 0 && iw < Wd)
-                  gW[idx4(oc, ic, kh, kw, OC, C, KS)] += X[idx4(n, ic, ih, iw, N, C, H)] * g;
-              }
-        }
+  for (int64_t ic = 0; ic < C; ++ic)
+    for (int64_t ih = 0; ih < H; ++ih)
+      for (int64_t iw = 0; iw < Wd; ++iw)
+        for (int64_t n = 0; n < N; ++n)
+          Xi[(size_t)(((ic * N + n) * H + ih) * Wd + iw)] = X[idx4(n, ic, ih, iw, N, C, H)];
+#pragma omp parallel for num_threads(g_threads) schedule(static)
+  for (int64_t oc = 0; oc < OC; ++oc)
+    for (int64_t oh = 0; oh < HO; ++oh)
+      for (int64_t ow = 0; ow < WO; ++ow)
+        for (int64_t n = 0; n < N; ++n)
+          Gi[(size_t)(((oc * N + n) * HO + oh) * WO + ow)] = dY[idx4(n, oc, oh, ow, N, OC, HO)];
+  if (gb) {
+#pragma omp parallel for num_threads(g_threads) schedule(static)
+    for (int64_t oc = 0; oc < OC; ++oc) {
+      float acc = 0.0f;
+      const float* g = Gi.data() + oc * N * HO * WO;  // (n, oh, ow) in order
+      for (int64_t i = 0; i < N * HO * WO; ++i) acc += g[i];
+      gb[oc] = acc;
+    }
   }
+#pragma omp parallel for num_threads(g_threads) schedule(static) collapse(2)
+  for (int64_t oc = 0; oc < OC; ++oc)
+    for (int64_t ic = 0; ic < C; ++ic) {
+      std::vector<float> acc((size_t)(KS * KS), 0.0f);
+      for (int64_t n = 0; n < N; ++n) {
+        const float* xi = Xi.data() + (ic * N + n) * H * Wd;
+        const float* gi = Gi.data() + (oc * N + n) * HO * WO;
+        for (int64_t oh = 0; oh < HO; ++oh)
+          for (int64_t ow = 0; ow < WO; ++ow) {
+            const float g = gi[oh * WO + ow];
+            for (int64_t kh = 0; kh < KS; ++kh) {
+              const int64_t ih = oh * S - P + kh;
+              if (ih < 0 || ih >= H) continue;
+              for (int64_t kw = 0; kw < KS; ++kw) {
+                const int64_t iw = ow * S - P + kw;
+                if (iw >= 0 && iw < Wd) acc[(size_t)(kh * KS + kw)] += xi[ih * Wd + iw] * g;
+              }
+            }
+          }
+      }
+      for (int64_t kh = 0; kh < KS; ++kh)
+        for (int64_t kw = 0; kw < KS; ++kw) gW[idx4(oc, ic, kh, kw, OC, C, KS)] = acc[(size_t)(kh * KS + kw)];
+    }
+  // dX: the N samples of one (ic, ih, iw) are contiguous; each element takes
+  // its terms in (oc, oh, ow) order (a given (oh, ow) reaches it through at
+  // most one (kh, kw))
 #pragma omp parallel for num_threads(g_threads) schedule(static)
-  for (int64_t n = 0; n < N; ++n) {
-    for (int64_t ic = 0; ic < C; ++ic)
-      for (int64_t ih = 0; ih < H; ++ih)
-        for (int64_t iw = 0; iw < Wd; ++iw) dX[idx4(n, ic, ih, iw, N, C, H)] = 0.0f;
+  for (int64_t ic = 0; ic < C; ++ic) {
+    for (int64_t ih = 0; ih < H; ++ih)
+      for (int64_t iw = 0; iw < Wd; ++iw) {
+        float* d = dX + idx4(0, ic, ih, iw, N, C, H);
+        for (int64_t n = 0; n < N; ++n) d[n] = 0.0f;
+      }
     for (int64_t oc = 0; oc < OC; ++oc)
       for (int64_t oh = 0; oh < HO; ++oh)
         for (int64_t ow = 0; ow < WO; ++ow) {
-          const float g = dY[idx4(n, oc, oh, ow, N, OC, HO)];
-          for (int64_t ic = 0; ic < C; ++ic)
-            for (int64_t kh = 0; kh < KS; ++kh)
-              for (int64_t kw = 0; kw < KS; ++kw) {
-                const int64_t ih = oh * S - P + kh, iw = ow * S - P + kw;
-                if (ih >= 0 && ih < H && iw >= 0 && iw < Wd)
-                  dX[idx4(n, ic, ih, iw, N, C, H)] += Wt[idx4(oc, ic, kh, kw, OC, C, KS)] * g;
-              }
+          const float* g = dY + idx4(0, oc, oh, ow, N, OC, HO);
+          for (int64_t kh = 0; kh < KS; ++kh)
+            for (int64_t kw = 0; kw < KS; ++kw) {
+              const int64_t ih = oh * S - P + kh, iw = ow * S - P + kw;
+              if (ih < 0 || ih >= H || iw < 0 || iw >= Wd) continue;
+              const float w = Wt[idx4(oc, ic, kh, kw, OC, C, KS)];
+              float* d = dX + idx4(0, ic, ih, iw, N, C, H);
+              for (int64_t n = 0; n < N; ++n) d[n] += w * g[n];
+            }
         }
   }
 }
@@ -466,6 +555,9 @@ void cnref_lstm_backward(const float* X, const float* Wih, const float* Whh, con
         dg[n + B * (d + 3 * H)] = dh * tc * og * (1.0f - og);
         dc_next[e] = dc * fg;
       }
+    if (float* tr = g_trace[CNREF_TRACE_DPRE])
+      for (int64_t g = 0; g < G; ++g)
+        for (int64_t n = 0; n < B; ++n) tr[(n + B * t) + BS * g] = dg[n + B * g];
     std::vector<float> x = slice_t(X, B, S, I, t);
     std::vector<float> hp = t > 0 ? slice_t(Y, B, S, H, t - 1) : std::vector<float>((size_t)(B * H), 0.f);
     cnref_gemm_f32(1, 0, I, G, B, 1.f, x.data(), B, dg.data(), B, 0.f, tmp_ih.data(), I, nullptr, 0);
@@ -558,6 +650,9 @@ void cnref_gru_backward(const float* X, const float* Wih, const float* Whh, cons
         dg[n + B * (d + H)] = dr * rg * (1.0f - rg);
         dhp[e] += d_rh[e] * rg;
       }
+    if (float* tr = g_trace[CNREF_TRACE_DPRE])
+      for (int64_t g = 0; g < G; ++g)
+        for (int64_t n = 0; n < B; ++n) tr[(n + B * t) + BS * g] = dg[n + B * g];
     std::vector<float> x = slice_t(X, B, S, I, t);
     cnref_gemm_f32(1, 0, I, G, B, 1.f, x.data(), B, dg.data(), B, 0.f, tmp_ih.data(), I, nullptr, 0);
     for (int64_t i = 0; i < I * G; ++i) gWih[i] += tmp_ih[i];
@@ -691,6 +786,13 @@ void cnref_mha_backward(const float* q, const float* k, const float* v, const fl
     for (int64_t d = 0; d < D; ++d)
       for (int64_t s2 = 0; s2 < S; ++s2)
         dX[n + B * s2 + B * S * d] = gQ[s2 + S * d] + gK[s2 + S * d] + gV[s2 + S * d];
+    const std::vector<float>* sample_tr[4] = {&gQp, &gKp, &gVp, &ctx};
+    for (int slot = CNREF_TRACE_GQP; slot <= CNREF_TRACE_CTX; ++slot)
+      if (float* tr = g_trace[slot]) {
+        const std::vector<float>& src = *sample_tr[slot - CNREF_TRACE_GQP];
+        for (int64_t d = 0; d < D; ++d)
+          for (int64_t s2 = 0; s2 < S; ++s2) tr[n + B * s2 + B * S * d] = src[(size_t)(s2 + S * d)];
+      }
   }
 }
 

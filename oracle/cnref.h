@@ -26,6 +26,22 @@ int  cnref_get_threads(void);
  * order, used to measure a trajectory's sensitivity to rounding). */
 void cnref_set_accumulate_double(int on);
 
+/* Optional diagnostic outputs for the tests' error bars (NULL = off).  While
+ * a slot holds a buffer, the functions below also write:
+ *   CNREF_TRACE_DPRE  recurrent backward (LSTM / GRU / RNN): the gradient of
+ *                     every timestep's gate pre-activations, [B*S, G]
+ *                     ColMajor (row n + B*t), G = 4H / 3H / H;
+ *   CNREF_TRACE_GQP / _GKP / _GVP / _CTX   MHA backward: the gradients of
+ *                     the three projections and the attention output
+ *                     A*Vp of every sample, [B*S, D] (row n + B*s). */
+#define CNREF_TRACE_DPRE 0
+#define CNREF_TRACE_GQP 1
+#define CNREF_TRACE_GKP 2
+#define CNREF_TRACE_GVP 3
+#define CNREF_TRACE_CTX 4
+void cnref_set_trace(int slot, float* buf);
+float* cnref_trace(int slot);
+
 /* ColMajor C[M,N] = alpha*op(A)*op(B) + beta*C (+bias[n]) (relu if epi==1);
  * same operand conventions as cnhip_gemm_f32.  beta==0 does not read C. */
 void cnref_gemm_f32(int ta, int tb, int64_t M, int64_t N, int64_t K, float alpha,

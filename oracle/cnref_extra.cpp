@@ -288,6 +288,9 @@ void cnref_rnn_backward(const float* X, const float* Wih, const float* Whh, cons
         const float dh = dY[n + B * t + B * S * d] + dh_next[k];
         dt[k] = dh * (1.0f - ht[k] * ht[k]);
       }
+    if (float* tr = cnref_trace(CNREF_TRACE_DPRE))
+      for (int64_t d = 0; d < H; ++d)
+        for (int64_t n = 0; n < B; ++n) tr[(n + B * t) + B * S * d] = dt[(size_t)(n + B * d)];
     cnref_gemm_f32(1, 0, I, H, B, 1.f, x.data(), B, dt.data(), B, 1.f, gWih, I, nullptr, 0);
     cnref_gemm_f32(1, 0, H, H, B, 1.f, hp.data(), B, dt.data(), B, 1.f, gWhh, H, nullptr, 0);
     for (int64_t d = 0; d < H; ++d)

@@ -22,6 +22,7 @@ class OracleMLP:
         self.params = None
         self.grads = None
         self.opt = None
+        self.keep = True  # keep the per-step diagnostics (trace, last_grads); long runs turn it off
 
     def set_params(self, params):
         self.params = [np.array(p, np.float32, copy=True) for p in params]
@@ -110,12 +111,14 @@ class OracleMLP:
             I, O = self.sizes[i], self.sizes[i + 1]
             dH = grad
             grad = self._act_bwd(acts[i], outs[i], grad, pre[i])
-            self.trace[i] = dict(x=inputs[i], z=pre[i], dH=dH.copy(), dA=grad.copy(), act=acts[i])
+            if self.keep:
+                self.trace[i] = dict(x=inputs[i], z=pre[i], dH=dH.copy(), dA=grad.copy(), act=acts[i])
             dX = np.empty(B * I, np.float32)
             o.cnref_linear_backward(fp(inputs[i]), fp(self.params[2 * i]), fp(grad),
                                     fp(self.grads[2 * i]), fp(self.grads[2 * i + 1]), fp(dX), B, I,
                                     O, 1, 1)
             grad = dX
         self.opt.step(self.params, self.grads)  # model.update(optimizer, lr)
-        self.last_grads = [g.copy() for g in self.grads]
+        if self.keep:
+            self.last_grads = [g.copy() for g in self.grads]
         return float(loss)

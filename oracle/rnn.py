@@ -59,6 +59,10 @@ class OracleSeqRegressor:
         dY[:, S - 1, :] = dh.reshape(H, B)
         dY = dY.ravel()
         dX = np.zeros_like(X)
+        keep = getattr(self, "keep", True)
+        # the gate pre-activation gradients of every timestep, for the tests' error bars
+        dpre = np.zeros(BS * {"lstm": 4, "gru": 3, "rnn": 1}[cfg.cell] * H, np.float32) if keep else None
+        o.cnref_set_trace(0, fp(dpre))
         if cfg.cell == "lstm":
             o.cnref_lstm_backward(fp(X), fp(Wih), fp(Whh), fp(Yseq), fp(gates), fp(c), fp(tc), fp(dY),
                                   fp(self.grads[0]), fp(self.grads[1]), fp(self.grads[2]), fp(dX),
@@ -70,7 +74,10 @@ class OracleSeqRegressor:
             o.cnref_gru_backward(fp(X), fp(Wih), fp(Whh), fp(Yseq), fp(gates), fp(rh), fp(dY),
                                  fp(self.grads[0]), fp(self.grads[1]), fp(self.grads[2]), fp(dX),
                                  B, S, I, H)
-        self.last_grads = [gr.copy() for gr in self.grads]
-        self.trace = dict(X=X, Yseq=Yseq, hT=hT, g=g, dh=dh)
+        o.cnref_set_trace(0, None)
+        if keep:  # per-step diagnostics; long runs turn them off
+            self.last_grads = [gr.copy() for gr in self.grads]
+        self.trace = dict(X=X, Yseq=Yseq, hT=hT, g=g, dh=dh, dpre=dpre,
+                          rh=rh if cfg.cell == "gru" else None)
         self.opt.step(self.params, self.grads)
         return float(loss)

@@ -77,6 +77,8 @@ class OracleTransformer:
         o.cnref_linear_backward(fp(pooled), fp(P[-2]), fp(gl), fp(G[-2]), fp(G[-1]), fp(dp), B, D, C, 1, 1)
         dy = np.zeros(BS * D, np.float32)
         o.cnref_meanpool1d_backward(fp(dp), fp(dy), B, S, D)
+        keep = getattr(self, "keep", True)
+        self.head_trace = dict(pooled=pooled, gl=gl)
         for i in reversed(range(cfg.blocks)):
             T = trace[i]
             iq, ik, iv, io, ig, ib, i1, ib1, i2, ib2 = self._blk(i)
@@ -92,12 +94,21 @@ class OracleTransformer:
                                        fp(G[ig]), fp(G[ib]), fp(dr), BS, D, 1e-5)
             dxa = np.zeros(BS * D, np.float32)
             xx = T["x"]
+            if keep:  # the operands of the weight-gradient contractions, for the tests' error bars
+                T.update(dy=dy, dz1=dz1, gh=gh, dr=dr)
+                for slot, name in ((1, "gQp"), (2, "gKp"), (3, "gVp"), (4, "ctx")):
+                    T[name] = np.zeros(BS * D, np.float32)
+                    o.cnref_set_trace(slot, fp(T[name]))
             o.cnref_mha_backward(fp(xx), fp(xx), fp(xx), fp(P[iq]), fp(P[ik]), fp(P[iv]), fp(P[io]),
                                  fp(T["attn"]), fp(dr), fp(G[iq]), fp(G[ik]), fp(G[iv]), fp(G[io]), fp(dxa),
                                  B, S, D, cfg.heads)
+            for slot in (1, 2, 3, 4):
+                o.cnref_set_trace(slot, None)
             dy = dxa + dr
         o.cnref_embedding_backward(ip(ids), fp(dy), fp(G[0]), B, S, V, D)
-        self.last_grads = [gr.copy() for gr in G]
+        self.head_trace.update(demb=dy, ids=ids)
+        if getattr(self, "keep", True):  # per-step diagnostics; long runs turn them off
+            self.last_grads = [gr.copy() for gr in G]
         self.trace = trace
         for kk, (p, gr) in enumerate(zip(P, G)):
             self.t[kk] += 1

@@ -97,7 +97,8 @@ def test_queued_epoch_then_reset(gpu, mode):
     other work, then reset() (a new permutation, uploaded at once) and the
     next epoch queued too, before any gather has run: every batch must still
     be gathered with its own epoch's order.  Then to_device() again (which
-    frees the staged dataset) with the second epoch still queued."""
+    frees the staged dataset) with the second epoch still queued, right after
+    the reset started the next epoch's staging worker."""
     from cppnet_amd import _capi
     n, f, l, batch = 2048, 96, 4, 128
     print(f"[loader] {mode}: queued epochs across reset", flush=True)
@@ -132,5 +133,5 @@ def test_queued_epoch_then_reset(gpu, mode):
             np.testing.assert_array_equal(xb[k].cpu().numpy(), hx, err_msg=f"epoch {epoch} batch {k}")
             np.testing.assert_array_equal(yb[k].cpu().numpy(), hy, err_msg=f"epoch {epoch} batch {k}")
     assert not np.array_equal(epochs[0][0][0][0], epochs[1][0][0][0])  # the orders differ
-    assert lib.cnhip_stream_destroy(stream) == 0
     ld.close()
+    assert lib.cnhip_stream_destroy(stream) == 0

@@ -28,6 +28,7 @@ import pytest
 
 from cppnet_amd import trainer
 from oracle.mlp import OracleMLP
+from contraction_mags import rnn_mags, transformer_mags
 from oracle_lib import close, close_mag, fp, gemm_mag
 
 pytestmark = pytest.mark.gpu
@@ -227,6 +228,22 @@ def _check_one_step(oracle_mt, cfg, seed, label):
           f"needed the ReLU-mask allowance; {flips}/{total} updated weights differ, all at |g| "
           f"within gradient tolerance of 0")
     sess.close()
+
+
+def _check_grads_and_update(grads, ref, mags, updated):
+    """Gradients within 1e-5 + 1e-4 max(|ref|, mag) elementwise; updated
+    weights within 1e-5 + 1e-4 |ref| except where the gradient itself lies
+    within its bar of 0 (Adam's first step is ~ -lr sign(g), so a sign that
+    rounding decides moves the weight by up to 2 lr)."""
+    for k, (a, b, m) in enumerate(zip(grads, ref.last_grads, mags)):
+        ok, msg = close_mag(a, b, m, 1e-4, 1e-5)
+        assert ok, f"grad of param {k}: {msg}"
+    for k, (a, b, g, m) in enumerate(zip(updated, ref.get_params(), ref.last_grads, mags)):
+        bad = np.abs(a.astype(np.float64) - b) > 1e-5 + 1e-4 * np.abs(b)
+        ill = np.abs(g) <= 1e-5 + 1e-4 * np.maximum(np.abs(g), m)
+        assert not (bad & ~ill).any(), (
+            f"param {k}: {int((bad & ~ill).sum())} updated weights differ where the gradient is well "
+            f"conditioned")
 
 
 def _rel(a, b):
@@ -441,9 +458,11 @@ def test_cnn_multi_step_parity(gpu, oracle_mt):
 @pytest.mark.parametrize("cell,batch,seq", [("lstm", None, None), ("gru", 32, 16), ("rnn", 32, 16)])
 def test_rnn_one_step_parity(gpu, oracle_mt, cell, batch, seq):
     """Config 4 (LSTM 128->512, T=64, batch 128) at full size, and the GRU
-    variant of the same regressor.  The recurrent grads are sums over all B*S
-    rows of products of O(1) gate terms; their relative bound is taken against
-    max(|ref|, RMS of the tensor), which covers cancellation in the long sums."""
+    and Elman variants of the same regressor.  The recurrent grads are sums
+    over all B*S timestep-rows; each element's relative bound is taken
+    against max(|ref|, (|A|^T |dpre|)/sqrt(B*S)) with A its contraction's
+    other operand (x_t, h_{t-1} or r*h_{t-1}) and dpre the oracle's gate
+    pre-activation gradients (tests/contraction_mags.py)."""
     from oracle.rnn import OracleSeqRegressor
     cfg = trainer.rnn_config(4, batch=batch, seq_len=seq, cell=cell)
     print(f"[model] config 4 {cell} batch {cfg.batch} T={cfg.seq_len}: one step", flush=True)
@@ -461,17 +480,8 @@ def test_rnn_one_step_parity(gpu, oracle_mt, cell, batch, seq):
     loss_ref = ref.step(X, Y)
     ok, msg = close([loss_gpu], [loss_ref], 1e-4, 1e-5)
     assert ok, f"loss: {msg}"
-    for k, (a, b) in enumerate(zip(grads, ref.last_grads)):
-        rms = float(np.sqrt(np.mean(b.astype(np.float64) ** 2)))
-        ok, msg = close_mag(a, b, np.full(b.shape, rms, np.float32), 1e-4, 1e-5)
-        assert ok, f"grad of param {k}: {msg}"
-    for k, (a, b) in enumerate(zip(sess.get_params(), ref.get_params())):
-        ok, msg = close(a, b, 1e-4, 1e-5)
-        if not ok:  # Adam's first step is ~lr*sign(g): only ill-conditioned gradients may flip
-            g = ref.last_grads[k]
-            rms = float(np.sqrt(np.mean(g.astype(np.float64) ** 2)))
-            bad = np.abs(a.astype(np.float64) - b) > 1e-5 + 1e-4 * np.abs(b)
-            assert np.all(np.abs(g[bad]) <= 1e-5 + 1e-4 * rms), f"param {k}: {msg}"
+    mags = rnn_mags(oracle_mt, ref, cfg)
+    _check_grads_and_update(grads, ref, mags, sess.get_params())
     print(f"[model] config 4 {cell}: loss {loss_gpu:.7f} vs {loss_ref:.7f}")
     sess.close()
 
@@ -509,10 +519,11 @@ def test_rnn_multi_step_parity(gpu, oracle_mt, cell, opt):
 
 def test_transformer_one_step_parity(gpu, oracle_mt):
     """Config 5 at full size (Embedding 8192x512, 2 encoder blocks, B=32,
-    S=256): loss, every gradient (relative part against max(|ref|, RMS of the
-    tensor): the weight gradients are sums over 8192 rows) and the updated
-    weights; the embedding gradient's routing is exact (rows of ids absent
-    from the batch stay exactly 0)."""
+    S=256): loss, every gradient (relative part against max(|ref|, the
+    per-element magnitude (|A|^T|B|)/sqrt(R) of its contraction over the
+    R = 8192 rows, tests/contraction_mags.py) and the updated weights; the
+    embedding gradient's routing is exact (rows of ids absent from the batch
+    stay exactly 0)."""
     from oracle.transformer import OracleTransformer
     cfg = trainer.transformer_config(5)
     print(f"[model] config 5 batch {cfg.batch} S={cfg.seq_len}: one step", flush=True)
@@ -537,17 +548,8 @@ def test_transformer_one_step_parity(gpu, oracle_mt):
     emb_g = grads[0].reshape(cfg.embed_dim, cfg.vocab)  # ColMajor [V, D]: column d
     assert not emb_g[:, absent].any(), "embedding rows of absent ids must stay exactly 0"
     assert np.all(emb_g[:, np.unique(ids)].any(axis=0))
-    for k, (a, b) in enumerate(zip(grads, ref.last_grads)):
-        rms = float(np.sqrt(np.mean(b.astype(np.float64) ** 2)))
-        ok, msg = close_mag(a, b, np.full(b.shape, rms, np.float32), 1e-4, 1e-5)
-        assert ok, f"grad of param {k}: {msg}"
-    for k, (a, b) in enumerate(zip(sess.get_params(), ref.get_params())):
-        ok, msg = close(a, b, 1e-4, 1e-5)
-        if not ok:  # Adam's first step is ~lr*sign(g): only ill-conditioned gradients may flip
-            g = ref.last_grads[k]
-            rms = float(np.sqrt(np.mean(g.astype(np.float64) ** 2)))
-            bad = np.abs(a.astype(np.float64) - b) > 1e-5 + 1e-4 * np.abs(b)
-            assert np.all(np.abs(g[bad]) <= 1e-5 + 1e-4 * rms), f"param {k}: {msg}"
+    mags = transformer_mags(oracle_mt, ref, cfg)
+    _check_grads_and_update(grads, ref, mags, sess.get_params())
     print(f"[model] config 5: loss {loss_gpu:.7f} vs {loss_ref:.7f}")
     sess.close()
 
