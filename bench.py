@@ -122,21 +122,34 @@ CPU_BATCH = {1: 512, 2: 512, 3: 32, 4: 16, 5: 4}
 PMC_TRAFFIC_BYTES = {2: 321.0e6}
 
 
-def cpu_baseline(config: int, seconds_budget: float = 20.0):
-    """Times the oracle-composed model (oracle/ over oracle/liboracle.so) on
-    this host: the same step at a reduced batch, scaled to samples/s.  The
-    first step is a warm-up; steps continue until about seconds_budget of CPU
-    work has been timed."""
-    import numpy as np
-    from oracle import load_oracle
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
-    threads = min(16, os.cpu_count() or 1)
-    o = load_oracle()
+
+def _cpu_share() -> int:
+    """Host threads this process may use: its affinity set, capped at the 16
+    host cores one GPU's share of the box holds."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+def _time_oracle(o, config: int, batch: int, threads: int, seconds_budget: float, max_steps: int):
+    import numpy as np
     o.cnref_set_threads(threads)
-    batch = CPU_BATCH[config]
     cfg, synth, Oracle, _, _ = workload(config, batch=batch)
     params, X, Y = synth(cfg, np.random.default_rng(99))
     ref = Oracle(cfg, o)
+    ref.keep = False
     ref.set_params(params)
     ref.step(X, Y)  # warm-up
     n, t0 = 0, time.perf_counter()
@@ -144,13 +157,39 @@ def cpu_baseline(config: int, seconds_budget: float = 20.0):
         ref.step(X, Y)
         n += 1
         el = time.perf_counter() - t0
-        if el >= seconds_budget or n >= (20000 if config == 1 else 50):
+        if el >= seconds_budget or n >= max_steps:
             break
-    return {"value": round(batch * n / el, 2), "unit": "samples/s", "cores": threads,
-            "kind": "port",
-            "sample": (f"{n} train steps of config {config} at batch {batch} (of {workload(config)[0].batch})"
-                       f" on the CPU oracle (plain C++ restatement of cpu-eigen semantics, "
-                       f"{threads} OpenMP threads), {el:.1f} s")}
+    return {"threads": threads, "batch": batch, "steps": n, "seconds": round(el, 2),
+            "samples_per_s": round(batch * n / el, 2)}
+
+
+def cpu_baseline(config: int, seconds_budget: float = 20.0):
+    """Times the oracle-composed model (oracle/ over oracle/liboracle.so, a
+    plain C++ restatement of the reference's cpu-eigen semantics) on this
+    host: the same step at a reduced batch on all the host threads of this
+    GPU's share (the reported value) and on 4 threads, each for about
+    seconds_budget / 2 of CPU work after a warm-up step; for config 2 also one
+    step at the full batch.  Figures are samples/s."""
+    from oracle import load_oracle
+
+    o = load_oracle()
+    share = _cpu_share()
+    batch = CPU_BATCH[config]
+    max_steps = 20000 if config == 1 else 50
+    legs = [_time_oracle(o, config, batch, share, seconds_budget / 2, max_steps)]
+    if share != 4:
+        legs.append(_time_oracle(o, config, batch, 4, seconds_budget / 2, max_steps))
+    full = workload(config)[0].batch
+    if config == 2:
+        legs.append(_time_oracle(o, config, full, share, 0.0, 1))
+    main = legs[0]
+    return {"value": main["samples_per_s"], "unit": "samples/s", "cores": share,
+            "kind": "port", "cpu_model": _cpu_model(),
+            "legs": legs,
+            "sample": (f"reference-semantics restatement (oracle/, plain C++ of the cpu-eigen "
+                       f"semantics, OpenMP): {main['steps']} train steps of config {config} at batch "
+                       f"{batch} (of {full}) on {share} threads in {main['seconds']} s; legs also "
+                       f"time 4 threads" + (" and one full-batch step" if config == 2 else ""))}
 
 
 def traffic_calibration() -> int:

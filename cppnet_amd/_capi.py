@@ -82,6 +82,12 @@ SIGNATURES: dict[str, tuple] = {
     "cnhip_mha_backward_residual": (i32, [vp] * 15 + [i64] * 4 + [vp]),
     "cnhip_embedding_forward": (i32, [vp, vp, vp, i64, i64, i64, i64, vp, vp]),
     "cnhip_embedding_backward": (i32, [vp, vp, vp, i64, i64, i64, i64, vp]),
+    "cnhip_mha_forward_rows": (i32, [vp] * 10 + [i64] * 4 + [i32, vp]),
+    "cnhip_mha_backward_rows": (i32, [vp] * 15 + [i64] * 4 + [i32, vp]),
+    "cnhip_embedding_forward_rows": (i32, [vp, vp, vp, i64, i64, i64, i64, vp, i32, vp]),
+    "cnhip_embedding_backward_rows": (i32, [vp, vp, vp, i64, i64, i64, i64, i32, vp]),
+    "cnhip_meanpool1d_forward_rows": (i32, [vp, vp, i64, i64, i64, i32, vp]),
+    "cnhip_meanpool1d_backward_rows": (i32, [vp, vp, i64, i64, i64, i32, vp]),
     "cnhip_batchnorm_forward": (i32, [vp] * 9 + [i64, i64, f32, f32, vp]),
     "cnhip_batchnorm_forward_eval": (i32, [vp] * 7 + [i64, i64, f32, vp]),
     "cnhip_batchnorm_backward": (i32, [vp] * 9 + [i64, i64, f32, vp]),

@@ -19,7 +19,6 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int MAX_TENSORS = 64;
 constexpr int ADAM_BLOCK = 256;
-constexpr int ADAM_CHUNK = ADAM_BLOCK * 4 * 4;  // floats per block: 4 float4 per thread
 
 struct AdamHyper {
   float lr, b1, b2, eps;
@@ -51,29 +50,45 @@ struct AdamBatch {
   int count;
 };
 
+// A block updates R * ADAM_BLOCK * 4 consecutive values of one tensor.  In
+// the float4 path every thread first loads all R of its float4s of W, g, m
+// and v (4R loads in flight), then updates them, then stores: the four
+// arrays are distinct buffers, so no store can feed a later load.
+template <int R>
 __device__ __forceinline__ void adam_range(const AdamTensor& T, int64_t begin, const AdamHyper& h) {
   if (T.vec) {
-    // begin is a multiple of ADAM_CHUNK, hence of 4.
+    // begin is a multiple of the chunk, hence of 4.
+    f32x4 w[R], g[R], m[R], v[R];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
+    for (int r = 0; r < R; ++r) {
       const int64_t i = begin + ((int64_t)r * ADAM_BLOCK + threadIdx.x) * 4;
-      if (i >= T.n) break;
-      f32x4 w = *reinterpret_cast<const f32x4*>(T.W + i);
-      const f32x4 g = *reinterpret_cast<const f32x4*>(T.g + i);
-      f32x4 m = *reinterpret_cast<const f32x4*>(T.m + i);
-      f32x4 v = *reinterpret_cast<const f32x4*>(T.v + i);
+      if (i < T.n) {
+        w[r] = *reinterpret_cast<const f32x4*>(T.W + i);
+        g[r] = *reinterpret_cast<const f32x4*>(T.g + i);
+        m[r] = *reinterpret_cast<const f32x4*>(T.m + i);
+        v[r] = *reinterpret_cast<const f32x4*>(T.v + i);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        float we = w[e], me = m[e], ve = v[e];
-        adam_one(we, g[e], me, ve, T.bc1, T.bc2, h);
-        w[e] = we; m[e] = me; v[e] = ve;
+        float we = w[r][e], me = m[r][e], ve = v[r][e];
+        adam_one(we, g[r][e], me, ve, T.bc1, T.bc2, h);
+        w[r][e] = we; m[r][e] = me; v[r][e] = ve;
       }
-      *reinterpret_cast<f32x4*>(T.W + i) = w;
-      *reinterpret_cast<f32x4*>(T.m + i) = m;
-      *reinterpret_cast<f32x4*>(T.v + i) = v;
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t i = begin + ((int64_t)r * ADAM_BLOCK + threadIdx.x) * 4;
+      if (i < T.n) {
+        *reinterpret_cast<f32x4*>(T.W + i) = w[r];
+        *reinterpret_cast<f32x4*>(T.m + i) = m[r];
+        *reinterpret_cast<f32x4*>(T.v + i) = v[r];
+      }
     }
   } else {
-    for (int r = 0; r < 16; ++r) {
+    for (int r = 0; r < 4 * R; ++r) {
       const int64_t i = begin + (int64_t)r * ADAM_BLOCK + threadIdx.x;
       if (i >= T.n) break;
       float w = T.W[i], m = T.m[i], v = T.v[i];
@@ -83,6 +98,7 @@ __device__ __forceinline__ void adam_range(const AdamTensor& T, int64_t begin, c
   }
 }
 
+template <int R>
 __global__ void __launch_bounds__(ADAM_BLOCK) adam_multi_kernel(AdamBatch batch, AdamHyper h) {
   // Find the tensor owning this block (count <= 64: a linear scan of
   // uniform values is cheap and stays in scalar registers).
@@ -90,25 +106,35 @@ __global__ void __launch_bounds__(ADAM_BLOCK) adam_multi_kernel(AdamBatch batch,
   for (int i = 1; i < batch.count; ++i)
     if ((int)blockIdx.x >= batch.t[i].first_block) ti = i;
   const AdamTensor& T = batch.t[ti];
-  const int64_t begin = (int64_t)((int)blockIdx.x - T.first_block) * ADAM_CHUNK;
-  adam_range(T, begin, h);
+  const int64_t begin = (int64_t)((int)blockIdx.x - T.first_block) * (R * ADAM_BLOCK * 4);
+  adam_range<R>(T, begin, h);
 }
 
-int adam_launch(AdamBatch& b, const AdamHyper& h, hipStream_t st, const char* who) {
+template <int R>
+int adam_launch_r(AdamBatch& b, const AdamHyper& h, int64_t params, hipStream_t st, const char* who) {
+  constexpr int64_t chunk = R * ADAM_BLOCK * 4;
   int blocks = 0;
   for (int i = 0; i < b.count; ++i) {
     b.t[i].first_block = blocks;
-    const int64_t nb = (b.t[i].n + ADAM_CHUNK - 1) / ADAM_CHUNK;
+    const int64_t nb = (b.t[i].n + chunk - 1) / chunk;
     CNHIP_REQUIRE(blocks + nb < (int64_t)1 << 30, "%s: too many parameters", who);
     blocks += (int)nb;
   }
   if (blocks == 0) return CNHIP_OK;
-  int64_t params = 0;
-  for (int i = 0; i < b.count; ++i) params += b.t[i].n;
   // read W, g, m, v and write W, m, v: 28 bytes per parameter
   HbmTimer timer("adam_multi_kernel", 28.0 * (double)params, st);
-  hipLaunchKernelGGL(adam_multi_kernel, dim3(blocks), dim3(ADAM_BLOCK), 0, st, b, h);
+  hipLaunchKernelGGL(adam_multi_kernel<R>, dim3(blocks), dim3(ADAM_BLOCK), 0, st, b, h);
   return check_launch(who);
+}
+
+// Four float4s per thread for large updates; fewer when that would leave
+// the 256 CUs with fewer than ~8 blocks each.
+int adam_launch(AdamBatch& b, const AdamHyper& h, hipStream_t st, const char* who) {
+  int64_t params = 0;
+  for (int i = 0; i < b.count; ++i) params += b.t[i].n;
+  if (params >= (int64_t)2048 * 4 * ADAM_BLOCK * 4) return adam_launch_r<4>(b, h, params, st, who);
+  if (params >= (int64_t)2048 * 2 * ADAM_BLOCK * 4) return adam_launch_r<2>(b, h, params, st, who);
+  return adam_launch_r<1>(b, h, params, st, who);
 }
 
 int fill_tensor(AdamTensor& T, float* W, const float* g, float* m, float* v, int64_t n, float bc1,

@@ -556,6 +556,10 @@ int cnt_transformer_create(cnt_session** out, int64_t batch, int64_t seq_len, in
         auto net = std::make_unique<EncoderNet>();
         const int D = static_cast<int>(embed_dim);
         net->emb = std::make_shared<Layers::Embedding>(static_cast<int>(vocab), D, "gpu");
+        // The session owns the whole Embedding -> MeanPool1D chain, so its
+        // sequences run by sample (row s + S*b): the attention products then
+        // read each sample's rows in place, with no transposes.
+        net->emb->set_row_order(CNHIP_ROWS_BY_SAMPLE);
         {
             Layers::Embedding* e = net->emb.get();
             cnt_session::Param p{[e]() -> DeviceTensor& { return e->weights(); },
@@ -568,6 +572,7 @@ int cnt_transformer_create(cnt_session** out, int64_t batch, int64_t seq_len, in
         {
             EncoderBlock b;
             b.mha = std::make_shared<Layers::MultiHeadAttention>(D, static_cast<int>(heads), "gpu");
+            b.mha->set_row_order(CNHIP_ROWS_BY_SAMPLE);
             b.bn = std::make_shared<Layers::BatchNorm>(D, 0.1f, 1e-5f, "gpu");
             b.ff1 = std::make_shared<Layers::Linear>(D, static_cast<int>(ffn_dim), "ffn1_" + std::to_string(i),
                                                      true, true, "gpu", "xavier");
@@ -588,6 +593,7 @@ int cnt_transformer_create(cnt_session** out, int64_t batch, int64_t seq_len, in
             net->blocks.push_back(std::move(b));
         }
         net->pool = std::make_shared<Layers::MeanPool1D>("gpu");
+        net->pool->set_row_order(CNHIP_ROWS_BY_SAMPLE);
         net->fc = std::make_shared<Layers::Linear>(D, static_cast<int>(classes), "classifier", true, true, "gpu",
                                                    "xavier");
         s->add_params(net->fc);

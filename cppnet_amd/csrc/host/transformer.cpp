@@ -22,6 +22,20 @@ namespace CppNet
     {
         namespace
         {
+            int check_rows(int rows, const char* who)
+            {
+                if (rows != CNHIP_ROWS_REF && rows != CNHIP_ROWS_BY_SAMPLE)
+                    throw std::invalid_argument(std::string(who) + ": row order must be 0 or 1");
+                return rows;
+            }
+            // host tensors always carry the reference's row order
+            void require_ref_rows(int rows, const char* who)
+            {
+                if (rows != CNHIP_ROWS_REF)
+                    throw std::logic_error(std::string(who) +
+                                           ": host tensors are in the reference row order; this layer runs by sample");
+            }
+
             void check_2d(const Tensor<float, 2>& t, int64_t r, int64_t c, const char* who)
             {
                 if (t.dimension(0) != r || t.dimension(1) != c)
@@ -53,9 +67,9 @@ namespace CppNet
             const int64_t B = ids.dimension(0), S = ids.dimension(1);
             DeviceTensor out = DeviceTensor::empty({B, S, embed_dim_});
             if (!ids_checked) oob_.fill_zero();
-            Device::check(cnhip_embedding_forward(ids.idata(), Wt_.data(), out.data(), B, S, vocab_size_,
-                                                  embed_dim_, ids_checked ? nullptr : oob_.idata(),
-                                                  Device::stream()),
+            Device::check(cnhip_embedding_forward_rows(ids.idata(), Wt_.data(), out.data(), B, S, vocab_size_,
+                                                       embed_dim_, ids_checked ? nullptr : oob_.idata(), rows_,
+                                                       Device::stream()),
                           "Embedding::forward");
             if (ids_checked)
             {
@@ -88,8 +102,8 @@ namespace CppNet
             const int64_t B = ids_cache_.dimension(0), S = ids_cache_.dimension(1);
             if (g.rank() != 3 || g.dimension(0) != B || g.dimension(1) != S || g.dimension(2) != embed_dim_)
                 throw std::runtime_error("Embedding::backward: grad shape " + shape_str(g.dims()));
-            Device::check(cnhip_embedding_backward(ids_cache_.idata(), g.data(), gWt_.data(), B, S,
-                                                   vocab_size_, embed_dim_, Device::stream()),
+            Device::check(cnhip_embedding_backward_rows(ids_cache_.idata(), g.data(), gWt_.data(), B, S,
+                                                        vocab_size_, embed_dim_, rows_, Device::stream()),
                           "Embedding::backward");
             grads_zero_ = false;
             return DeviceTensor::zeros({B, S, embed_dim_});  // embedding.cpp:171-174
@@ -97,12 +111,16 @@ namespace CppNet
 
         Tensor<float, 3> Embedding::forward(const Tensor<int, 2>& input)
         {
+            require_ref_rows(rows_, "Embedding::forward");
             return forward(DeviceTensor::from_host(input)).to_host<float, 3>();
         }
         Tensor<float, 3> Embedding::backward(const Tensor<float, 3>& g)
         {
+            require_ref_rows(rows_, "Embedding::backward");
             return backward(DeviceTensor::from_host(g)).to_host<float, 3>();
         }
+
+        void Embedding::set_row_order(int rows) { rows_ = check_rows(rows, "Embedding::set_row_order"); }
 
         void Embedding::materialize_grads() const
         {
@@ -197,10 +215,10 @@ namespace CppNet
             const int64_t B = q.dimension(0), S = q.dimension(1), D = embed_dim_;
             cache_ = DeviceTensor::empty({cnhip_mha_cache_floats(B, S, D)});
             DeviceTensor out = DeviceTensor::empty({B, S, D});
-            Device::check(cnhip_mha_forward_residual(q.data(), k.data(), v.data(), W_[0].data(), W_[1].data(),
-                                                     W_[2].data(), W_[3].data(),
-                                                     residual.defined() ? residual.data() : nullptr, out.data(),
-                                                     cache_.data(), B, S, D, num_heads_, Device::stream()),
+            Device::check(cnhip_mha_forward_rows(q.data(), k.data(), v.data(), W_[0].data(), W_[1].data(),
+                                                 W_[2].data(), W_[3].data(),
+                                                 residual.defined() ? residual.data() : nullptr, out.data(),
+                                                 cache_.data(), B, S, D, num_heads_, rows_, Device::stream()),
                           "MultiHeadAttention::forward");
             q_cache_ = q;
             k_cache_ = k;
@@ -220,11 +238,12 @@ namespace CppNet
                                          shape_str(skip_grad.dims()));
             const int64_t B = g.dimension(0), S = g.dimension(1), D = embed_dim_;
             DeviceTensor dx = DeviceTensor::empty({B, S, D});
-            Device::check(cnhip_mha_backward_residual(
+            Device::check(cnhip_mha_backward_rows(
                               q_cache_.data(), k_cache_.data(), v_cache_.data(), W_[0].data(), W_[1].data(),
                               W_[2].data(), W_[3].data(), cache_.data(), g.data(),
                               skip_grad.defined() ? skip_grad.data() : nullptr, gW_[0].data(), gW_[1].data(),
-                              gW_[2].data(), gW_[3].data(), dx.data(), B, S, D, num_heads_, Device::stream()),
+                              gW_[2].data(), gW_[3].data(), dx.data(), B, S, D, num_heads_, rows_,
+                              Device::stream()),
                           "MultiHeadAttention::backward");
             grads_zero_ = false;
             return dx;
@@ -233,13 +252,20 @@ namespace CppNet
         Tensor<float, 3> MultiHeadAttention::forward(const Tensor<float, 3>& q, const Tensor<float, 3>& k,
                                                      const Tensor<float, 3>& v)
         {
+            require_ref_rows(rows_, "MultiHeadAttention::forward");
             DeviceTensor dq = DeviceTensor::from_host(q);
             if (&k == &q && &v == &q) return forward(dq, dq, dq).to_host<float, 3>();
             return forward(dq, DeviceTensor::from_host(k), DeviceTensor::from_host(v)).to_host<float, 3>();
         }
         Tensor<float, 3> MultiHeadAttention::backward(const Tensor<float, 3>& g)
         {
+            require_ref_rows(rows_, "MultiHeadAttention::backward");
             return backward(DeviceTensor::from_host(g)).to_host<float, 3>();
+        }
+
+        void MultiHeadAttention::set_row_order(int rows)
+        {
+            rows_ = check_rows(rows, "MultiHeadAttention::set_row_order");
         }
 
         void MultiHeadAttention::materialize_grads() const
@@ -317,9 +343,12 @@ namespace CppNet
                                          ") != num_features (" + std::to_string(num_features_) + ")");
             const int64_t N = x.dimension(0), F = num_features_;
             DeviceTensor y = DeviceTensor::empty({N, F});
-            xhat_ = DeviceTensor::empty({N, F});
+            // training: the backward recomputes xhat from x and the batch
+            // statistics (bit for bit), so it is not stored; eval: the
+            // backward reads the cached xhat, as the reference's does
+            xhat_ = training_ ? DeviceTensor() : DeviceTensor::empty({N, F});
             if (training_)
-                Device::check(cnhip_batchnorm_forward(x.data(), y.data(), xhat_.data(), gamma_.data(), beta_.data(),
+                Device::check(cnhip_batchnorm_forward(x.data(), y.data(), nullptr, gamma_.data(), beta_.data(),
                                                       rmean_.data(), rvar_.data(), bmean_.data(), bvar_.data(), N, F,
                                                       momentum_, eps_, Device::stream()),
                               "BatchNorm::forward");
@@ -339,7 +368,8 @@ namespace CppNet
                 throw std::runtime_error("BatchNorm::backward: grad shape " + shape_str(g.dims()));
             const int64_t N = g.dimension(0), F = num_features_;
             DeviceTensor dx = DeviceTensor::empty({N, F});
-            Device::check(cnhip_batchnorm_backward(g.data(), in_cache_.data(), xhat_.data(), gamma_.data(),
+            Device::check(cnhip_batchnorm_backward(g.data(), in_cache_.data(),
+                                                   xhat_.defined() ? xhat_.data() : nullptr, gamma_.data(),
                                                    bmean_.data(), bvar_.data(), ggamma_.data(), gbeta_.data(),
                                                    dx.data(), N, F, eps_, Device::stream()),
                           "BatchNorm::backward");
@@ -410,7 +440,7 @@ namespace CppNet
             S_ = x.dimension(1);
             D_ = x.dimension(2);
             DeviceTensor y = DeviceTensor::empty({B_, D_});
-            Device::check(cnhip_meanpool1d_forward(x.data(), y.data(), B_, S_, D_, Device::stream()),
+            Device::check(cnhip_meanpool1d_forward_rows(x.data(), y.data(), B_, S_, D_, rows_, Device::stream()),
                           "MeanPool1D::forward");
             return y;
         }
@@ -421,19 +451,23 @@ namespace CppNet
             if (g.rank() != 2 || g.dimension(0) != B_ || g.dimension(1) != D_)
                 throw std::runtime_error("MeanPool1D::backward: grad shape " + shape_str(g.dims()));
             DeviceTensor dx = DeviceTensor::empty({B_, S_, D_});
-            Device::check(cnhip_meanpool1d_backward(g.data(), dx.data(), B_, S_, D_, Device::stream()),
+            Device::check(cnhip_meanpool1d_backward_rows(g.data(), dx.data(), B_, S_, D_, rows_, Device::stream()),
                           "MeanPool1D::backward");
             return dx;
         }
 
         Tensor<float, 2> MeanPool1D::forward(const Tensor<float, 3>& x)
         {
+            require_ref_rows(rows_, "MeanPool1D::forward");
             return forward(DeviceTensor::from_host(x)).to_host<float, 2>();
         }
         Tensor<float, 3> MeanPool1D::backward(const Tensor<float, 2>& g)
         {
+            require_ref_rows(rows_, "MeanPool1D::backward");
             return backward(DeviceTensor::from_host(g)).to_host<float, 3>();
         }
+
+        void MeanPool1D::set_row_order(int rows) { rows_ = check_rows(rows, "MeanPool1D::set_row_order"); }
 
         // ---------------------------------------------------------------- Residual
         Residual::Residual(std::vector<std::shared_ptr<Layer>> block, int in_features, int out_features,

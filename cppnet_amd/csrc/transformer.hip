@@ -16,6 +16,16 @@
 // over the B samples.  Attention weights are kept as A^T per sample (row i of
 // A is contiguous), so the row softmax and its Jacobian are wave64 reductions
 // over contiguous memory.
+//
+// Row order by sample.  The [B*S, D] activations may instead hold row
+// s + S*b (CNHIP_ROWS_BY_SAMPLE): sample b's [S, D] block is then rows
+// S*b .. S*b + S - 1 of the matrix, an ordinary strided operand (leading
+// dimension B*S, batch stride S), and the attention products read and write
+// it in place with no transposes.  Everything row-wise (projections, FFN,
+// BatchNorm, GELU, adds) is indifferent to the row order; Embedding,
+// MeanPool1D and attention take it as an argument.  A model that runs
+// Embedding -> ... -> MeanPool1D uses it end to end: the order never shows
+// outside.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -258,20 +268,24 @@ int softmax_rows_bwd(const float* A, const float* dA, float* g, int64_t rows, in
 // ---------------------------------------------------------------- embedding
 // Weights are kept token-major, Wt[d + D*v] (the reference's ColMajor [V, D]
 // transposed), so one token's row is contiguous.  out[p + BS*d] with
-// p = b + B*s: a 64-token x 64-feature tile is read along d and written along
-// p through LDS.  Out-of-range ids produce zeros and are counted.
+// p = b + B*s (or s + S*b by sample): a 64-token x 64-feature tile is read
+// along d and written along p through LDS.  Out-of-range ids produce zeros
+// and are counted.
 __global__ void __launch_bounds__(256) embedding_fwd_kernel(const int32_t* __restrict__ ids,
                                                             const float* __restrict__ Wt,
-                                                            float* __restrict__ out, int64_t BS,
-                                                            int64_t V, int64_t D,
+                                                            float* __restrict__ out, int64_t B,
+                                                            int64_t S, int64_t V, int64_t D,
+                                                            int by_sample,
                                                             int32_t* __restrict__ oob) {
+  const int64_t BS = B * S;
   __shared__ float tile[TT][TT + 1];
   __shared__ int32_t tok[TT];
   const int64_t p0 = (int64_t)blockIdx.x * TT, d0 = (int64_t)blockIdx.y * TT;
   const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
   if (threadIdx.x < TT) {
     const int64_t p = p0 + threadIdx.x;
-    int32_t id = p < BS ? ids[p] : 0;
+    // ids are ColMajor [B, S]: position (b, s) at b + B*s
+    int32_t id = p < BS ? ids[by_sample ? (p % S) * B + p / S : p] : 0;
     if (p < BS && (id < 0 || id >= V)) {
       if (oob && blockIdx.y == 0) atomicAdd(oob, 1);
       id = -1;
@@ -369,20 +383,20 @@ __global__ void __launch_bounds__(256) emb_sort_kernel(const int32_t* __restrict
 }
 
 // gWt[d + D*v] = sum over the bucket, in key order, of dYt[d + D*p]
-// (dYt = dY transposed, one position's gradient row contiguous); empty
-// buckets write zeros.
+// (dYt = dY transposed, one position's gradient row contiguous; key b*S + s
+// is row p = b + B*s, or p = key by sample); empty buckets write zeros.
 __global__ void __launch_bounds__(128) emb_sum_kernel(const int32_t* __restrict__ offsets,
                                                       const int32_t* __restrict__ keys,
                                                       const float* __restrict__ dYt,
                                                       float* __restrict__ gWt, int64_t B,
-                                                      int64_t S, int64_t D) {
+                                                      int64_t S, int64_t D, int by_sample) {
   const int64_t v = blockIdx.x;
   const int32_t lo = offsets[v], hi = offsets[v + 1];
   for (int64_t d = threadIdx.x; d < D; d += blockDim.x) {
     float s = 0.f;
     for (int32_t i = lo; i < hi; ++i) {
       const int64_t key = keys[i];
-      s += dYt[d + D * (key / S + B * (key % S))];
+      s += dYt[d + D * (by_sample ? key : key / S + B * (key % S))];
     }
     gWt[d + D * v] = s;
   }
@@ -404,6 +418,20 @@ __device__ float bn_block_sum(float v, float* sm) {
 #pragma unroll
   for (int i = 0; i < BNT / 64; ++i) r += sm[i];
   return r;  // every thread
+}
+
+// sqrt(var + eps) from var as stored: one rounding for var = sum / N, one
+// for the add.  Contracting the two into an fma would give the forward a
+// divisor the backward (which reads the stored var) cannot reproduce.
+__device__ __forceinline__ float bn_den(float var, float eps) {
+#pragma clang fp contract(off)
+  return sqrtf(var + eps);
+}
+// xhat = (x - mean) / den, the subtraction never fused with the product that
+// formed mean (the backward reads mean as stored)
+__device__ __forceinline__ float bn_xhat(float x, float mean, float den) {
+#pragma clang fp contract(off)
+  return (x - mean) / den;
 }
 
 // batch_norm.cpp:282-318 (training)
@@ -430,11 +458,11 @@ __global__ void __launch_bounds__(BNT) bn_fwd_kernel(const float* __restrict__ x
     s2 += diff * diff;
   }
   const float var = bn_block_sum(s2, sm) * inv_batch;
-  const float den = sqrtf(var + eps);
+  const float den = bn_den(var, eps);
   const float g = gamma[f], b = beta[f];
   for (int64_t n = threadIdx.x; n < N; n += BNT) {
-    const float xh = (xc[n] - mean) / den;
-    xhat[n + N * f] = xh;
+    const float xh = bn_xhat(xc[n], mean, den);
+    if (xhat) xhat[n + N * f] = xh;
     y[n + N * f] = g * xh + b;
   }
   if (threadIdx.x == 0) {
@@ -482,14 +510,14 @@ __global__ void __launch_bounds__(BNT) bn_fwd_reg_kernel(const float* __restrict
     }
   }
   const float var = bn_block_sum(s2, sm) * inv_batch;
-  const float den = sqrtf(var + eps);
+  const float den = bn_den(var, eps);
   const float g = gamma[f], b = beta[f];
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     const int64_t n = threadIdx.x + (int64_t)BNT * i;
     if (n < N) {
-      const float xh = (v[i] - mean) / den;
-      xhat[n + N * f] = xh;
+      const float xh = bn_xhat(v[i], mean, den);
+      if (xhat) xhat[n + N * f] = xh;
       y[n + N * f] = g * xh + b;
     }
   }
@@ -534,14 +562,15 @@ __global__ void __launch_bounds__(BNT) bn_bwd_kernel(const float* __restrict__ d
   const int64_t f = blockIdx.x;
   const float* dyc = dY + N * f;
   const float* xc = x + N * f;
-  const float* xhc = xhat + N * f;
+  const float* xhc = xhat ? xhat + N * f : nullptr;
   const float g = gamma[f], mean = bmean[f];
-  const float inv_std = 1.0f / sqrtf(bvar[f] + eps);
+  const float den = bn_den(bvar[f], eps);  // the forward's divisor: xhat recomputed bit for bit
+  const float inv_std = 1.0f / den;
   const float inv_batch = 1.0f / (float)N;
   float sgg = 0.f, sgb = 0.f, sdv = 0.f, sdm = 0.f;
   for (int64_t n = threadIdx.x; n < N; n += BNT) {
     const float dy = dyc[n];
-    sgg += dy * xhc[n];
+    sgg += dy * (xhc ? xhc[n] : bn_xhat(xc[n], mean, den));
     sgb += dy;
     const float dxh = dy * g;
     const float xmu = xc[n] - mean;
@@ -580,9 +609,10 @@ __global__ void __launch_bounds__(BNT) bn_bwd_reg_kernel(const float* __restrict
   const int64_t f = blockIdx.x;
   const float* dyc = dY + N * f;
   const float* xc = x + N * f;
-  const float* xhc = xhat + N * f;
+  const float* xhc = xhat ? xhat + N * f : nullptr;
   const float g = gamma[f], mean = bmean[f];
-  const float inv_std = 1.0f / sqrtf(bvar[f] + eps);
+  const float den = bn_den(bvar[f], eps);  // the forward's divisor: xhat recomputed bit for bit
+  const float inv_std = 1.0f / den;
   const float inv_batch = 1.0f / (float)N;
   float dy[PER], xm[PER];
   float sgg = 0.f, sgb = 0.f, sdv = 0.f, sdm = 0.f;
@@ -593,10 +623,10 @@ __global__ void __launch_bounds__(BNT) bn_bwd_reg_kernel(const float* __restrict
     xm[i] = 0.f;
     if (n < N) {
       dy[i] = dyc[n];
-      sgg += dy[i] * xhc[n];
+      xm[i] = xc[n] - mean;
+      sgg += dy[i] * (xhc ? xhc[n] : bn_xhat(xc[n], mean, den));
       sgb += dy[i];
       const float dxh = dy[i] * g;
-      xm[i] = xc[n] - mean;
       sdv += dxh * xm[i] * (-0.5f) * inv_std * inv_std * inv_std;
       sdm += dxh * (-inv_std);
     }
@@ -699,10 +729,10 @@ __global__ void __launch_bounds__(T) bn_fwd_vec_kernel(const float* __restrict__
 #pragma unroll
   for (int i = 0; i < T / 64; ++i) var += sm[1][i];
   var *= inv_batch;
-  const float den = sqrtf(var + eps);
+  const float den = bn_den(var, eps);
   const float g = gamma[f], b = beta[f];
   f32x4* yc = reinterpret_cast<f32x4*>(y + N * f);
-  f32x4* hc = reinterpret_cast<f32x4*>(xhat + N * f);
+  f32x4* hc = xhat ? reinterpret_cast<f32x4*>(xhat + N * f) : nullptr;
 #pragma unroll
   for (int i = 0; i < V4; ++i) {
     const int64_t q = threadIdx.x + (int64_t)T * i;
@@ -710,10 +740,10 @@ __global__ void __launch_bounds__(T) bn_fwd_vec_kernel(const float* __restrict__
       f32x4 xh, o;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        xh[e] = (v[i][e] - mean) / den;
+        xh[e] = bn_xhat(v[i][e], mean, den);
         o[e] = g * xh[e] + b;
       }
-      hc[q] = xh;
+      if (hc) hc[q] = xh;
       yc[q] = o;
     }
   }
@@ -742,9 +772,10 @@ __global__ void __launch_bounds__(T) bn_bwd_vec_kernel(const float* __restrict__
   const int64_t f = blockIdx.x, n4 = N >> 2;
   const f32x4* dyc = reinterpret_cast<const f32x4*>(dY + N * f);
   const f32x4* xc = reinterpret_cast<const f32x4*>(x + N * f);
-  const f32x4* hc = reinterpret_cast<const f32x4*>(xhat + N * f);
+  const f32x4* hc = xhat ? reinterpret_cast<const f32x4*>(xhat + N * f) : nullptr;
   const float g = gamma[f], mean = bmean[f];
-  const float inv_std = 1.0f / sqrtf(bvar[f] + eps);
+  const float den = bn_den(bvar[f], eps);  // the forward's divisor: xhat recomputed bit for bit
+  const float inv_std = 1.0f / den;
   const float inv_batch = 1.0f / (float)N;
   const float c3 = (-0.5f) * inv_std * inv_std * inv_std;
   f32x4 dy[V4], xm[V4];
@@ -756,8 +787,14 @@ __global__ void __launch_bounds__(T) bn_bwd_vec_kernel(const float* __restrict__
     xm[i] = f32x4{0.f, 0.f, 0.f, 0.f};
     if (q < n4) {
       dy[i] = dyc[q];
-      const f32x4 xh = hc[q];
       xm[i] = xc[q] - mean;
+      f32x4 xh;
+      if (hc) {
+        xh = hc[q];
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xh[e] = xm[i][e] / den;
+      }
       f32x4 pg, pv, pm;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -871,13 +908,32 @@ __global__ void __launch_bounds__(256) meanpool_fwd_kernel(const float* __restri
     y[b + B * d] = tot / (float)S;
   }
 }
+// By sample, sample b's S rows of feature d are contiguous at S*b + B*S*d:
+// one wave per (b, d), lane l summing s = l, l + 64, ... in order, then a
+// butterfly over the 64 lane sums (a fixed order for any launch).
+__global__ void __launch_bounds__(256) meanpool_fwd_by_sample_kernel(const float* __restrict__ x,
+                                                                     float* __restrict__ y,
+                                                                     int64_t B, int64_t S,
+                                                                     int64_t D) {
+  const int lane = threadIdx.x & 63;
+  const int64_t pair = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // b + B*d
+  if (pair >= B * D) return;
+  const int64_t b = pair % B, d = pair / B;
+  const float* xs = x + S * b + B * S * d;
+  float s = 0.f;
+  for (int64_t t = lane; t < S; t += 64) s += xs[t];
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+  if (lane == 0) y[pair] = s / (float)S;
+}
 __global__ void __launch_bounds__(256) meanpool_bwd_kernel(const float* __restrict__ dy,
                                                            float* __restrict__ dx, int64_t B,
-                                                           int64_t S, int64_t D, float inv_S) {
+                                                           int64_t S, int64_t D, float inv_S,
+                                                           int by_sample) {
   const int64_t total = B * S * D;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
        i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t b = i % B, d = i / (B * S);
+    const int64_t b = by_sample ? (i / S) % B : i % B, d = i / (B * S);
     dx[i] = dy[b + B * d] * inv_S;
   }
 }
@@ -924,32 +980,38 @@ int cnhip_transpose(const float* in, float* out, int64_t rows, int64_t cols, cnh
 }
 
 int64_t cnhip_mha_cache_floats(int64_t B, int64_t S, int64_t D) {
-  // Qp, Kp, Vp (per-sample layout), A^T per sample, context (row layout).
-  // Sample b's blocks: Qp_b at b*3SD, Kp_b at b*3SD + SD, Vp_b at b*3SD + 2SD
-  // (each [S, D] ColMajor); A^T_b at 3BSD + b*SS with A[i][j] at j + S*i;
-  // context [B*S, D] at 3BSD + B*SS.
+  // Projections Qp | Kp | Vp, A^T per sample, context.  Reference row order:
+  // sample b's Qp_b, Kp_b, Vp_b (each [S, D] ColMajor) at b*3SD, b*3SD + SD,
+  // b*3SD + 2SD; by sample: the [B*S, 3D] projection matrix itself.  Then
+  // A^T_b at 3BSD + b*SS with A[i][j] at j + S*i, and the context [B*S, D]
+  // at 3BSD + B*SS.
   return 4 * B * S * D + B * S * S;
 }
 
-int cnhip_mha_forward_residual(const float* q, const float* k, const float* v, const float* Wq,
-                               const float* Wk, const float* Wv, const float* Wo, const float* residual,
-                               float* out, float* cache, int64_t B, int64_t S, int64_t D, int64_t heads,
-                               cnhip_stream_t stream) {
+int cnhip_mha_forward_rows(const float* q, const float* k, const float* v, const float* Wq,
+                           const float* Wk, const float* Wv, const float* Wo, const float* residual,
+                           float* out, float* cache, int64_t B, int64_t S, int64_t D, int64_t heads,
+                           int rows, cnhip_stream_t stream) {
   const char* who = residual ? "cnhip_mha_forward_residual" : "cnhip_mha_forward";
   CNHIP_REQUIRE(B > 0 && S > 0 && D > 0 && heads > 0 && D % heads == 0,
                 "%s: bad shape B=%lld S=%lld D=%lld heads=%lld (D %% heads must be 0)", who,
                 (long long)B, (long long)S, (long long)D, (long long)heads);
+  CNHIP_REQUIRE(rows == CNHIP_ROWS_REF || rows == CNHIP_ROWS_BY_SAMPLE, "%s: bad row order %d", who, rows);
   CNHIP_REQUIRE(q && k && v && Wq && Wk && Wv && Wo && out && cache, "%s: NULL pointer", who);
   CNHIP_REQUIRE(B <= 65535, "%s: batch %lld exceeds 65535", who, (long long)B);
   hipStream_t st = as_stream(stream);
   const int64_t BS = B * S, SD = S * D, SS = S * S, DD = D * D;
   const float scale = 1.0f / sqrtf((float)(D / heads));  // attention.cpp:83
-  float* Qs = cache;  // per sample b: Qp_b, Kp_b, Vp_b at b*3SD
+  const bool by_sample = rows == CNHIP_ROWS_BY_SAMPLE;
+  float* Qs = cache;            // the projections (layout above)
   float* At = Qs + 3 * BS * D;  // per-sample A^T: (j, i) at j + S*i
-  float* ctx = At + B * SS;     // row layout [B*S, D]
+  float* ctx = At + B * SS;     // [B*S, D]
   cnhip::Workspace ws(st);
-  CNHIP_TRY(ws.alloc((size_t)(3 * BS * D) * sizeof(float), who));
-  float* proj = static_cast<float*>(ws.p);  // row layout [B*S, 3D]: Qp | Kp | Vp
+  float* proj = Qs;  // [B*S, 3D]: Qp | Kp | Vp
+  if (!by_sample) {
+    CNHIP_TRY(ws.alloc((size_t)(3 * BS * D) * sizeof(float), who));
+    proj = static_cast<float*>(ws.p);
+  }
   // Self-attention with W_q, W_k, W_v adjacent in memory: one GEMM X [Wq Wk Wv].
   if (q == k && k == v && Wk == Wq + DD && Wv == Wk + DD) {
     CNHIP_TRY(cnhip::gemm_f32(0, 0, BS, 3 * D, D, 1.f, q, BS, Wq, D, 0.f, proj, BS, nullptr, 0, st, who));
@@ -960,22 +1022,34 @@ int cnhip_mha_forward_residual(const float* q, const float* k, const float* v, c
       CNHIP_TRY(cnhip::gemm_f32(0, 0, BS, D, D, 1.f, src[i], BS, W[i], D, 0.f, proj + i * BS * D, BS,
                                 nullptr, 0, st, who));
   }
-  // The row-layout [B*S, 3D] matrix is [B, 3SD] with row b + B*s; its
-  // transpose [3SD, B] holds sample b's Qp_b, Kp_b, Vp_b (each [S, D]) at
-  // b*3SD, b*3SD + SD and b*3SD + 2SD.
-  CNHIP_TRY(cnhip::transpose(proj, Qs, B, 3 * SD, st, who));
-  const float* Qb = Qs;
-  const float* Kb = Qs + SD;
-  const float* Vb = Qs + 2 * SD;
-  const int64_t ps = 3 * SD;
+  // Per-sample operands: sample b's Qp_b at Qb + b*ps, each [S, D] with
+  // leading dimension ld.  By sample they are rows S*b.. of the projections;
+  // in the reference order the [B*S, 3D] matrix is [B, 3SD] with row b + B*s,
+  // and its transpose [3SD, B] holds sample b's Qp_b, Kp_b, Vp_b at b*3SD,
+  // b*3SD + SD and b*3SD + 2SD.
+  const float *Qb = Qs, *Kb = Qs + SD, *Vb = Qs + 2 * SD;
+  int64_t ld = S, ps = 3 * SD;
+  if (by_sample) {
+    Kb = Qs + BS * D;
+    Vb = Qs + 2 * BS * D;
+    ld = BS;
+    ps = S;
+  } else {
+    CNHIP_TRY(cnhip::transpose(proj, Qs, B, 3 * SD, st, who));
+  }
   // A^T_b = (Kp_b Qp_b^T) * scale (scores transposed, 187-189), then row softmax (191-205)
-  CNHIP_TRY(cnhip::gemm_f32_batched(0, 1, S, S, D, scale, Kb, S, ps, Qb, S, ps, 0.f, At, S, SS, B,
+  CNHIP_TRY(cnhip::gemm_f32_batched(0, 1, S, S, D, scale, Kb, ld, ps, Qb, ld, ps, 0.f, At, S, SS, B,
                                     nullptr, 0, st, who));
   CNHIP_TRY(cnhip::softmax_rows(At, At, BS, S, st, who));
-  // context_b = A_b Vp_b = (A^T_b)^T Vp_b (211), then back to row layout
-  CNHIP_TRY(cnhip::gemm_f32_batched(1, 0, S, D, S, 1.f, At, S, SS, Vb, S, ps, 0.f, proj, S, SD, B,
-                                    nullptr, 0, st, who));
-  CNHIP_TRY(cnhip::transpose(proj, ctx, SD, B, st, who));
+  // context_b = A_b Vp_b = (A^T_b)^T Vp_b (211), in the row order of the input
+  if (by_sample) {
+    CNHIP_TRY(cnhip::gemm_f32_batched(1, 0, S, D, S, 1.f, At, S, SS, Vb, ld, ps, 0.f, ctx, BS, S, B,
+                                      nullptr, 0, st, who));
+  } else {
+    CNHIP_TRY(cnhip::gemm_f32_batched(1, 0, S, D, S, 1.f, At, S, SS, Vb, ld, ps, 0.f, proj, S, SD, B,
+                                      nullptr, 0, st, who));
+    CNHIP_TRY(cnhip::transpose(proj, ctx, SD, B, st, who));
+  }
   // out = context W_o (212), plus the skip branch when fused
   if (residual)
     return cnhip::gemm_f32_act(0, 0, BS, D, D, ctx, BS, Wo, D, out, BS, nullptr, cnhip::EPI_ADD, residual,
@@ -983,56 +1057,83 @@ int cnhip_mha_forward_residual(const float* q, const float* k, const float* v, c
   return cnhip::gemm_f32(0, 0, BS, D, D, 1.f, ctx, BS, Wo, D, 0.f, out, BS, nullptr, 0, st, who);
 }
 
+int cnhip_mha_forward_residual(const float* q, const float* k, const float* v, const float* Wq,
+                               const float* Wk, const float* Wv, const float* Wo, const float* residual,
+                               float* out, float* cache, int64_t B, int64_t S, int64_t D, int64_t heads,
+                               cnhip_stream_t stream) {
+  return cnhip_mha_forward_rows(q, k, v, Wq, Wk, Wv, Wo, residual, out, cache, B, S, D, heads,
+                                CNHIP_ROWS_REF, stream);
+}
+
 int cnhip_mha_forward(const float* q, const float* k, const float* v, const float* Wq,
                       const float* Wk, const float* Wv, const float* Wo, float* out, float* cache,
                       int64_t B, int64_t S, int64_t D, int64_t heads, cnhip_stream_t stream) {
-  return cnhip_mha_forward_residual(q, k, v, Wq, Wk, Wv, Wo, nullptr, out, cache, B, S, D, heads, stream);
+  return cnhip_mha_forward_rows(q, k, v, Wq, Wk, Wv, Wo, nullptr, out, cache, B, S, D, heads,
+                                CNHIP_ROWS_REF, stream);
 }
 
-int cnhip_mha_backward_residual(const float* q, const float* k, const float* v, const float* Wq,
-                                const float* Wk, const float* Wv, const float* Wo, const float* cache,
-                                const float* dY, const float* residual_grad, float* gWq, float* gWk,
-                                float* gWv, float* gWo, float* dX, int64_t B, int64_t S, int64_t D,
-                                int64_t heads, cnhip_stream_t stream) {
+int cnhip_mha_backward_rows(const float* q, const float* k, const float* v, const float* Wq,
+                            const float* Wk, const float* Wv, const float* Wo, const float* cache,
+                            const float* dY, const float* residual_grad, float* gWq, float* gWk,
+                            float* gWv, float* gWo, float* dX, int64_t B, int64_t S, int64_t D,
+                            int64_t heads, int rows, cnhip_stream_t stream) {
   const char* who = residual_grad ? "cnhip_mha_backward_residual" : "cnhip_mha_backward";
   CNHIP_REQUIRE(!residual_grad || dX, "%s: the residual gradient needs dX", who);
   CNHIP_REQUIRE(B > 0 && S > 0 && D > 0 && heads > 0 && D % heads == 0, "%s: bad shape", who);
+  CNHIP_REQUIRE(rows == CNHIP_ROWS_REF || rows == CNHIP_ROWS_BY_SAMPLE, "%s: bad row order %d", who, rows);
   CNHIP_REQUIRE(q && k && v && Wq && Wk && Wv && Wo && cache && dY && gWq && gWk && gWv && gWo,
                 "%s: NULL pointer", who);
   CNHIP_REQUIRE(B <= 65535, "%s: batch %lld exceeds 65535", who, (long long)B);
   hipStream_t st = as_stream(stream);
   const int64_t BS = B * S, SD = S * D, SS = S * S, DD = D * D;
   const float scale = 1.0f / sqrtf((float)(D / heads));
-  const float* Ps = cache;  // per sample b: Qp_b, Kp_b, Vp_b at b*3SD
+  const bool by_sample = rows == CNHIP_ROWS_BY_SAMPLE;
+  const float* Ps = cache;  // the projections (layout in cnhip_mha_cache_floats)
   const float* At = Ps + 3 * BS * D;
   const float* ctx = At + B * SS;
-  const int64_t ps = 3 * SD;
   cnhip::Workspace ws(st);
-  CNHIP_TRY(ws.alloc((size_t)(8 * BS * D + 2 * B * SS) * sizeof(float), who));
-  float* gctx = static_cast<float*>(ws.p);  // row layout [B*S, D]
-  float* gcs = gctx + BS * D;               // per-sample
-  float* gPs = gcs + BS * D;                // per sample b: gQp_b, gKp_b, gVp_b at b*3SD
-  float* G = gPs + 3 * BS * D;              // row layout [B*S, 3D]: gQp | gKp | gVp
+  const int64_t extra = by_sample ? 0 : 4 * BS * D;  // per-sample copies of gctx and gQp | gKp | gVp
+  CNHIP_TRY(ws.alloc((size_t)(4 * BS * D + extra + 2 * B * SS) * sizeof(float), who));
+  float* gctx = static_cast<float*>(ws.p);  // [B*S, D]
+  float* G = gctx + BS * D;                 // [B*S, 3D]: gQp | gKp | gVp
   float* gAT = G + 3 * BS * D;              // per-sample (j, i)
   float* gST = gAT + B * SS;
+  float* gcs = gST + B * SS;                // reference order: per-sample gctx
+  float* gPs = gcs + BS * D;                // reference order: per sample b: gQp_b, gKp_b, gVp_b at b*3SD
+  // per-sample operands (as in the forward): Qp_b, Kp_b, Vp_b with leading
+  // dimension ld at sample stride ps; gctx_b, gQp_b, gKp_b, gVp_b likewise
+  const float *Qb = Ps, *Kb = Ps + SD, *Vb = Ps + 2 * SD;
+  const float* gcb = gcs;
+  float *gQb = gPs, *gKb = gPs + SD, *gVb = gPs + 2 * SD;
+  int64_t ld = S, ps = 3 * SD, gps = SD;
+  if (by_sample) {
+    Kb = Ps + BS * D;
+    Vb = Ps + 2 * BS * D;
+    gcb = gctx;
+    gQb = G;
+    gKb = G + BS * D;
+    gVb = G + 2 * BS * D;
+    ld = BS;
+    ps = gps = S;
+  }
   // grad_context = dY W_o^T (535); grad_W_o = context^T dY (536)
   CNHIP_TRY(cnhip::gemm_f32(0, 1, BS, D, D, 1.f, dY, BS, Wo, D, 0.f, gctx, BS, nullptr, 0, st, who));
   CNHIP_TRY(cnhip::gemm_f32(1, 0, D, D, BS, 1.f, ctx, BS, dY, BS, 0.f, gWo, D, nullptr, 0, st, who));
-  CNHIP_TRY(cnhip::transpose(gctx, gcs, B, SD, st, who));
+  if (!by_sample) CNHIP_TRY(cnhip::transpose(gctx, gcs, B, SD, st, who));
   // grad_A^T_b = Vp_b grad_ctx_b^T (538); grad_Vp_b = A_b^T grad_ctx_b (539)
-  CNHIP_TRY(cnhip::gemm_f32_batched(0, 1, S, S, D, 1.f, Ps + 2 * SD, S, ps, gcs, S, SD, 0.f, gAT, S,
-                                    SS, B, nullptr, 0, st, who));
-  CNHIP_TRY(cnhip::gemm_f32_batched(0, 0, S, D, S, 1.f, At, S, SS, gcs, S, SD, 0.f, gPs + 2 * SD, S,
-                                    ps, B, nullptr, 0, st, who));
+  CNHIP_TRY(cnhip::gemm_f32_batched(0, 1, S, S, D, 1.f, Vb, ld, ps, gcb, ld, gps, 0.f, gAT, S, SS, B,
+                                    nullptr, 0, st, who));
+  CNHIP_TRY(cnhip::gemm_f32_batched(0, 0, S, D, S, 1.f, At, S, SS, gcb, ld, gps, 0.f, gVb, ld, ps, B,
+                                    nullptr, 0, st, who));
   // softmax Jacobian rows, times scale (541-551)
   CNHIP_TRY(cnhip::softmax_rows_bwd(At, gAT, gST, BS, S, scale, st, who));
   // grad_Qp_b = gS_b Kp_b ; grad_Kp_b = gS_b^T Qp_b (553-554)
-  CNHIP_TRY(cnhip::gemm_f32_batched(1, 0, S, D, S, 1.f, gST, S, SS, Ps + SD, S, ps, 0.f, gPs, S, ps,
-                                    B, nullptr, 0, st, who));
-  CNHIP_TRY(cnhip::gemm_f32_batched(0, 0, S, D, S, 1.f, gST, S, SS, Ps, S, ps, 0.f, gPs + SD, S, ps,
-                                    B, nullptr, 0, st, who));
-  // per-sample [3SD, B] -> row layout [B, 3SD] = [B*S, 3D]
-  CNHIP_TRY(cnhip::transpose(gPs, G, 3 * SD, B, st, who));
+  CNHIP_TRY(cnhip::gemm_f32_batched(1, 0, S, D, S, 1.f, gST, S, SS, Kb, ld, ps, 0.f, gQb, ld, ps, B,
+                                    nullptr, 0, st, who));
+  CNHIP_TRY(cnhip::gemm_f32_batched(0, 0, S, D, S, 1.f, gST, S, SS, Qb, ld, ps, 0.f, gKb, ld, ps, B,
+                                    nullptr, 0, st, who));
+  // reference order: per-sample [3SD, B] -> [B, 3SD] = [B*S, 3D]
+  if (!by_sample) CNHIP_TRY(cnhip::transpose(gPs, G, 3 * SD, B, st, who));
   const float* gQp = G;
   const float* gKp = G + BS * D;
   const float* gVp = G + 2 * BS * D;
@@ -1063,18 +1164,28 @@ int cnhip_mha_backward_residual(const float* q, const float* k, const float* v, 
   return CNHIP_OK;
 }
 
+int cnhip_mha_backward_residual(const float* q, const float* k, const float* v, const float* Wq,
+                                const float* Wk, const float* Wv, const float* Wo, const float* cache,
+                                const float* dY, const float* residual_grad, float* gWq, float* gWk,
+                                float* gWv, float* gWo, float* dX, int64_t B, int64_t S, int64_t D,
+                                int64_t heads, cnhip_stream_t stream) {
+  return cnhip_mha_backward_rows(q, k, v, Wq, Wk, Wv, Wo, cache, dY, residual_grad, gWq, gWk, gWv, gWo, dX,
+                                 B, S, D, heads, CNHIP_ROWS_REF, stream);
+}
+
 int cnhip_mha_backward(const float* q, const float* k, const float* v, const float* Wq,
                        const float* Wk, const float* Wv, const float* Wo, const float* cache,
                        const float* dY, float* gWq, float* gWk, float* gWv, float* gWo, float* dX,
                        int64_t B, int64_t S, int64_t D, int64_t heads, cnhip_stream_t stream) {
-  return cnhip_mha_backward_residual(q, k, v, Wq, Wk, Wv, Wo, cache, dY, nullptr, gWq, gWk, gWv, gWo, dX,
-                                     B, S, D, heads, stream);
+  return cnhip_mha_backward_rows(q, k, v, Wq, Wk, Wv, Wo, cache, dY, nullptr, gWq, gWk, gWv, gWo, dX, B, S,
+                                 D, heads, CNHIP_ROWS_REF, stream);
 }
 
-int cnhip_embedding_forward(const int32_t* ids, const float* Wt, float* out, int64_t B, int64_t S,
-                            int64_t V, int64_t D, int32_t* oob_count, cnhip_stream_t stream) {
+int cnhip_embedding_forward_rows(const int32_t* ids, const float* Wt, float* out, int64_t B, int64_t S,
+                                 int64_t V, int64_t D, int32_t* oob_count, int rows, cnhip_stream_t stream) {
   const char* who = "cnhip_embedding_forward";
   CNHIP_REQUIRE(B > 0 && S > 0 && V > 0 && D > 0, "%s: bad shape", who);
+  CNHIP_REQUIRE(rows == CNHIP_ROWS_REF || rows == CNHIP_ROWS_BY_SAMPLE, "%s: bad row order %d", who, rows);
   CNHIP_REQUIRE(ids && Wt && out, "%s: NULL pointer", who);
   const int64_t BS = B * S;
   CNHIP_REQUIRE((D + cnhip::TT - 1) / cnhip::TT <= 65535, "%s: embed_dim too large", who);
@@ -1083,14 +1194,20 @@ int cnhip_embedding_forward(const int32_t* ids, const float* Wt, float* out, int
                         as_stream(stream));
   hipLaunchKernelGGL(cnhip::embedding_fwd_kernel,
                      dim3((unsigned)((BS + cnhip::TT - 1) / cnhip::TT), (unsigned)((D + cnhip::TT - 1) / cnhip::TT)),
-                     dim3(256), 0, as_stream(stream), ids, Wt, out, BS, V, D, oob_count);
+                     dim3(256), 0, as_stream(stream), ids, Wt, out, B, S, V, D, rows, oob_count);
   return cnhip::check_launch(who);
 }
 
-int cnhip_embedding_backward(const int32_t* ids, const float* dY, float* gWt, int64_t B, int64_t S,
-                             int64_t V, int64_t D, cnhip_stream_t stream) {
+int cnhip_embedding_forward(const int32_t* ids, const float* Wt, float* out, int64_t B, int64_t S,
+                            int64_t V, int64_t D, int32_t* oob_count, cnhip_stream_t stream) {
+  return cnhip_embedding_forward_rows(ids, Wt, out, B, S, V, D, oob_count, CNHIP_ROWS_REF, stream);
+}
+
+int cnhip_embedding_backward_rows(const int32_t* ids, const float* dY, float* gWt, int64_t B, int64_t S,
+                                  int64_t V, int64_t D, int rows, cnhip_stream_t stream) {
   const char* who = "cnhip_embedding_backward";
   CNHIP_REQUIRE(B > 0 && S > 0 && V > 0 && D > 0, "%s: bad shape", who);
+  CNHIP_REQUIRE(rows == CNHIP_ROWS_REF || rows == CNHIP_ROWS_BY_SAMPLE, "%s: bad row order %d", who, rows);
   CNHIP_REQUIRE(ids && dY && gWt, "%s: NULL pointer", who);
   CNHIP_REQUIRE(V < ((int64_t)1 << 31) && B * S < ((int64_t)1 << 31), "%s: too large", who);
   hipStream_t st = as_stream(stream);
@@ -1118,8 +1235,13 @@ int cnhip_embedding_backward(const int32_t* ids, const float* dY, float* gWt, in
   // every token's gradient row read once, every table row written
   cnhip::HbmTimer timer("emb_sum_kernel", 4.0 * (double)BS * (double)D + 4.0 * (double)V * (double)D, st);
   hipLaunchKernelGGL(cnhip::emb_sum_kernel, dim3((unsigned)V), dim3(128), 0, st, offsets, pos, dYt,
-                     gWt, B, S, D);
+                     gWt, B, S, D, rows);
   return cnhip::check_launch(who);
+}
+
+int cnhip_embedding_backward(const int32_t* ids, const float* dY, float* gWt, int64_t B, int64_t S,
+                             int64_t V, int64_t D, cnhip_stream_t stream) {
+  return cnhip_embedding_backward_rows(ids, dY, gWt, B, S, V, D, CNHIP_ROWS_REF, stream);
 }
 
 int cnhip_batchnorm_forward(const float* x, float* y, float* xhat, const float* gamma,
@@ -1128,11 +1250,12 @@ int cnhip_batchnorm_forward(const float* x, float* y, float* xhat, const float* 
                             float momentum, float eps, cnhip_stream_t stream) {
   const char* who = "cnhip_batchnorm_forward";
   CNHIP_REQUIRE(N > 0 && F > 0, "%s: bad shape", who);
-  CNHIP_REQUIRE(x && y && xhat && gamma && beta && running_mean && running_var && batch_mean && batch_var,
+  CNHIP_REQUIRE(x && y && gamma && beta && running_mean && running_var && batch_mean && batch_var,
                 "%s: NULL pointer", who);
-  // x read once; y and xhat written
-  cnhip::HbmTimer timer("bn_fwd_kernel", 12.0 * (double)N * (double)F, as_stream(stream));
-  const bool vec = N % 4 == 0 && cnhip::aligned16(x) && cnhip::aligned16(y) && cnhip::aligned16(xhat);
+  // x read once; y (and xhat when asked for) written
+  cnhip::HbmTimer timer("bn_fwd_kernel", (xhat ? 12.0 : 8.0) * (double)N * (double)F, as_stream(stream));
+  const bool vec =
+      N % 4 == 0 && cnhip::aligned16(x) && cnhip::aligned16(y) && (!xhat || cnhip::aligned16(xhat));
   if (vec && N <= 4 * 256)
     hipLaunchKernelGGL((cnhip::bn_fwd_vec_kernel<256, 1>), dim3((unsigned)F), dim3(256), 0, as_stream(stream),
                        x, y, xhat, gamma, beta, running_mean, running_var, batch_mean, batch_var, N,
@@ -1175,12 +1298,12 @@ int cnhip_batchnorm_backward(const float* dY, const float* x, const float* xhat,
                              cnhip_stream_t stream) {
   const char* who = "cnhip_batchnorm_backward";
   CNHIP_REQUIRE(N > 0 && F > 0, "%s: bad shape", who);
-  CNHIP_REQUIRE(dY && x && xhat && gamma && batch_mean && batch_var && grad_gamma && grad_beta && dX,
+  CNHIP_REQUIRE(dY && x && gamma && batch_mean && batch_var && grad_gamma && grad_beta && dX,
                 "%s: NULL pointer", who);
-  // dY, x and xhat read once; dX written
-  cnhip::HbmTimer timer("bn_bwd_kernel", 16.0 * (double)N * (double)F, as_stream(stream));
-  const bool vec = N % 4 == 0 && cnhip::aligned16(dY) && cnhip::aligned16(x) && cnhip::aligned16(xhat) &&
-                   cnhip::aligned16(dX);
+  // dY and x (and xhat when given) read once; dX written
+  cnhip::HbmTimer timer("bn_bwd_kernel", (xhat ? 16.0 : 12.0) * (double)N * (double)F, as_stream(stream));
+  const bool vec = N % 4 == 0 && cnhip::aligned16(dY) && cnhip::aligned16(x) &&
+                   (!xhat || cnhip::aligned16(xhat)) && cnhip::aligned16(dX);
   if (vec && N <= 4 * 256)
     hipLaunchKernelGGL((cnhip::bn_bwd_vec_kernel<256, 1>), dim3((unsigned)F), dim3(256), 0, as_stream(stream),
                        dY, x, xhat, gamma, batch_mean, batch_var, grad_gamma, grad_beta, dX, N, eps);
@@ -1227,12 +1350,21 @@ int cnhip_gelu_backward(const float* x, const float* dy, float* dx, int64_t n, c
   return cnhip::check_launch(who);
 }
 
-int cnhip_meanpool1d_forward(const float* x, float* y, int64_t B, int64_t S, int64_t D,
-                             cnhip_stream_t s) {
+int cnhip_meanpool1d_forward_rows(const float* x, float* y, int64_t B, int64_t S, int64_t D, int rows,
+                                  cnhip_stream_t s) {
   const char* who = "cnhip_meanpool1d_forward";
   CNHIP_REQUIRE(B > 0 && S > 0 && D > 0, "%s: bad shape", who);
+  CNHIP_REQUIRE(rows == CNHIP_ROWS_REF || rows == CNHIP_ROWS_BY_SAMPLE, "%s: bad row order %d", who, rows);
   CNHIP_REQUIRE(x && y, "%s: NULL pointer", who);
   CNHIP_REQUIRE(D <= 0x7fffffff, "%s: D too large", who);
+  if (rows == CNHIP_ROWS_BY_SAMPLE) {
+    CNHIP_REQUIRE((B * D + 3) / 4 <= 0x7fffffff, "%s: B*D too large", who);
+    cnhip::HbmTimer timer("meanpool_fwd_by_sample_kernel", 4.0 * (double)B * (double)D * (double)(S + 1),
+                          as_stream(s));
+    hipLaunchKernelGGL(cnhip::meanpool_fwd_by_sample_kernel, dim3((unsigned)((B * D + 3) / 4)), dim3(256), 0,
+                       as_stream(s), x, y, B, S, D);
+    return cnhip::check_launch(who);
+  }
   const int bw = B < 64 ? (int)B : 64;
   cnhip::HbmTimer timer("meanpool_fwd_kernel", 4.0 * (double)B * (double)D * (double)(S + 1), as_stream(s));
   hipLaunchKernelGGL(cnhip::meanpool_fwd_kernel, dim3((unsigned)D, (unsigned)((B + bw - 1) / bw)),
@@ -1240,15 +1372,26 @@ int cnhip_meanpool1d_forward(const float* x, float* y, int64_t B, int64_t S, int
   return cnhip::check_launch(who);
 }
 
-int cnhip_meanpool1d_backward(const float* dy, float* dx, int64_t B, int64_t S, int64_t D,
-                              cnhip_stream_t s) {
+int cnhip_meanpool1d_forward(const float* x, float* y, int64_t B, int64_t S, int64_t D,
+                             cnhip_stream_t s) {
+  return cnhip_meanpool1d_forward_rows(x, y, B, S, D, CNHIP_ROWS_REF, s);
+}
+
+int cnhip_meanpool1d_backward_rows(const float* dy, float* dx, int64_t B, int64_t S, int64_t D, int rows,
+                                   cnhip_stream_t s) {
   const char* who = "cnhip_meanpool1d_backward";
   CNHIP_REQUIRE(B > 0 && S > 0 && D > 0, "%s: bad shape", who);
+  CNHIP_REQUIRE(rows == CNHIP_ROWS_REF || rows == CNHIP_ROWS_BY_SAMPLE, "%s: bad row order %d", who, rows);
   CNHIP_REQUIRE(dy && dx, "%s: NULL pointer", who);
   cnhip::HbmTimer timer("meanpool_bwd_kernel", 4.0 * (double)B * (double)D * (double)(S + 1), as_stream(s));
   hipLaunchKernelGGL(cnhip::meanpool_bwd_kernel, dim3(cnhip::elementwise_grid(B * S * D, 256)),
-                     dim3(256), 0, as_stream(s), dy, dx, B, S, D, 1.0f / (float)S);
+                     dim3(256), 0, as_stream(s), dy, dx, B, S, D, 1.0f / (float)S, rows);
   return cnhip::check_launch(who);
+}
+
+int cnhip_meanpool1d_backward(const float* dy, float* dx, int64_t B, int64_t S, int64_t D,
+                              cnhip_stream_t s) {
+  return cnhip_meanpool1d_backward_rows(dy, dx, B, S, D, CNHIP_ROWS_REF, s);
 }
 
 int cnhip_add(const float* a, const float* b, float* y, int64_t n, cnhip_stream_t s) {

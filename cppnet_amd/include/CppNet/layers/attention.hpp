@@ -60,6 +60,13 @@ namespace CppNet
             /// Attention weights of the last forward, [B, S, S] ColMajor (n, i, j).
             const Tensor<float, 3> get_attention_weights() const;
 
+            /// Row order of the [B, S, D] device tensors the DeviceTensor
+            /// overloads take and return: 0 = the reference's (row b + B*s
+            /// of [B*S, D]), 1 = by sample (row s + S*b).  For a model that
+            /// owns the whole Embedding -> MeanPool1D chain (no reference
+            /// counterpart); the host-Tensor overloads need order 0.
+            void set_row_order(int rows);
+            int get_row_order() const { return rows_; }
             DeviceTensor& weight(int which);
             DeviceTensor& grad_weight(int which);
 
@@ -71,6 +78,7 @@ namespace CppNet
             DeviceTensor Wall_, gWall_;  // [D, 4D]: W_q | W_k | W_v | W_o
             DeviceTensor W_[4], gW_[4];
             DeviceTensor q_cache_, k_cache_, v_cache_, cache_;
+            int rows_ = 0;
         };
     } // namespace Layers
 } // namespace CppNet

@@ -56,6 +56,13 @@ namespace CppNet
             const Tensor<float, 2> get_grad_weight() const;
             void set_weight(const Tensor<float, 2>& w);
 
+            /// Row order of the [B, S, D] device tensors the DeviceTensor
+            /// overloads take and return: 0 = the reference's (row b + B*s
+            /// of [B*S, D]), 1 = by sample (row s + S*b).  For a model that
+            /// owns the whole Embedding -> MeanPool1D chain (no reference
+            /// counterpart); the host-Tensor overloads need order 0.
+            void set_row_order(int rows);
+            int get_row_order() const { return rows_; }
             /// Device tables, token-major (see above).
             DeviceTensor& weights() { return Wt_; }
             DeviceTensor& grad_weights() { materialize_grads(); return gWt_; }
@@ -66,6 +73,7 @@ namespace CppNet
             bool trainable_ = true;
             std::string device_;
             DeviceTensor Wt_, gWt_, ids_cache_, oob_;
+            int rows_ = 0;
         };
     } // namespace Layers
 } // namespace CppNet

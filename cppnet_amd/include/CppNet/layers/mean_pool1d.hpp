@@ -29,10 +29,18 @@ namespace CppNet
             bool is_trainable() const override { return false; }
             void step(Optimizers::Optimizer&, float) override {}
             void reset_grads() override {}
+            /// Row order of the [B, S, D] device tensors the DeviceTensor
+            /// overloads take and return: 0 = the reference's (row b + B*s
+            /// of [B*S, D]), 1 = by sample (row s + S*b).  For a model that
+            /// owns the whole Embedding -> MeanPool1D chain (no reference
+            /// counterpart); the host-Tensor overloads need order 0.
+            void set_row_order(int rows);
+            int get_row_order() const { return rows_; }
 
         private:
             std::string device_;
             int64_t B_ = 0, S_ = 0, D_ = 0;
+            int rows_ = 0;
         };
     } // namespace Layers
 } // namespace CppNet

@@ -169,26 +169,45 @@ def mha_backward(q, k, v, Wq, Wk, Wv, Wo, cache, dY, gWq, gWk, gWv, gWo, dX, B, 
                _stream())
 
 
-def mha_forward_residual(q, k, v, Wq, Wk, Wv, Wo, residual, out, cache, B, S, D, heads) -> None:
-    _capi.call("cnhip_mha_forward_residual",
-               *(_p(t) for t in (q, k, v, Wq, Wk, Wv, Wo, residual, out, cache)), B, S, D, heads,
-               _stream())
+# Row order of [B, S, D] sequences: ROWS_REF = row b + B*s of [B*S, D] (the
+# reference's), ROWS_BY_SAMPLE = row s + S*b.  rows=ROWS_REF calls the
+# reference-layout entry point itself.
+ROWS_REF, ROWS_BY_SAMPLE = 0, 1
+
+
+def mha_forward_residual(q, k, v, Wq, Wk, Wv, Wo, residual, out, cache, B, S, D, heads,
+                         rows=ROWS_REF) -> None:
+    ptrs = [_p(t) for t in (q, k, v, Wq, Wk, Wv, Wo, residual, out, cache)]
+    if rows == ROWS_REF:
+        _capi.call("cnhip_mha_forward_residual", *ptrs, B, S, D, heads, _stream())
+    else:
+        _capi.call("cnhip_mha_forward_rows", *ptrs, B, S, D, heads, rows, _stream())
 
 
 def mha_backward_residual(q, k, v, Wq, Wk, Wv, Wo, cache, dY, skip_grad, gWq, gWk, gWv, gWo, dX,
-                          B, S, D, heads) -> None:
-    _capi.call("cnhip_mha_backward_residual",
-               *(_p(t) for t in (q, k, v, Wq, Wk, Wv, Wo, cache, dY, skip_grad, gWq, gWk, gWv, gWo,
-                                 dX)), B, S, D, heads, _stream())
+                          B, S, D, heads, rows=ROWS_REF) -> None:
+    ptrs = [_p(t) for t in (q, k, v, Wq, Wk, Wv, Wo, cache, dY, skip_grad, gWq, gWk, gWv, gWo, dX)]
+    if rows == ROWS_REF:
+        _capi.call("cnhip_mha_backward_residual", *ptrs, B, S, D, heads, _stream())
+    else:
+        _capi.call("cnhip_mha_backward_rows", *ptrs, B, S, D, heads, rows, _stream())
 
 
-def embedding_forward(ids, Wt, out, B, S, V, D, oob=None) -> None:
-    _capi.call("cnhip_embedding_forward", _p(ids), _p(Wt), _p(out), B, S, V, D, _p(oob),
-               _stream())
+def embedding_forward(ids, Wt, out, B, S, V, D, oob=None, rows=ROWS_REF) -> None:
+    if rows == ROWS_REF:
+        _capi.call("cnhip_embedding_forward", _p(ids), _p(Wt), _p(out), B, S, V, D, _p(oob),
+                   _stream())
+    else:
+        _capi.call("cnhip_embedding_forward_rows", _p(ids), _p(Wt), _p(out), B, S, V, D, _p(oob),
+                   rows, _stream())
 
 
-def embedding_backward(ids, dY, gWt, B, S, V, D) -> None:
-    _capi.call("cnhip_embedding_backward", _p(ids), _p(dY), _p(gWt), B, S, V, D, _stream())
+def embedding_backward(ids, dY, gWt, B, S, V, D, rows=ROWS_REF) -> None:
+    if rows == ROWS_REF:
+        _capi.call("cnhip_embedding_backward", _p(ids), _p(dY), _p(gWt), B, S, V, D, _stream())
+    else:
+        _capi.call("cnhip_embedding_backward_rows", _p(ids), _p(dY), _p(gWt), B, S, V, D, rows,
+                   _stream())
 
 
 def batchnorm_forward(x, y, xhat, gamma, beta, rmean, rvar, bmean, bvar, N, F, momentum=0.1,
@@ -213,12 +232,18 @@ def gelu_backward(x, dy, dx) -> None:
     _capi.call("cnhip_gelu_backward", _p(x), _p(dy), _p(dx), x.numel(), _stream())
 
 
-def meanpool1d_forward(x, y, B, S, D) -> None:
-    _capi.call("cnhip_meanpool1d_forward", _p(x), _p(y), B, S, D, _stream())
+def meanpool1d_forward(x, y, B, S, D, rows=ROWS_REF) -> None:
+    if rows == ROWS_REF:
+        _capi.call("cnhip_meanpool1d_forward", _p(x), _p(y), B, S, D, _stream())
+    else:
+        _capi.call("cnhip_meanpool1d_forward_rows", _p(x), _p(y), B, S, D, rows, _stream())
 
 
-def meanpool1d_backward(dy, dx, B, S, D) -> None:
-    _capi.call("cnhip_meanpool1d_backward", _p(dy), _p(dx), B, S, D, _stream())
+def meanpool1d_backward(dy, dx, B, S, D, rows=ROWS_REF) -> None:
+    if rows == ROWS_REF:
+        _capi.call("cnhip_meanpool1d_backward", _p(dy), _p(dx), B, S, D, _stream())
+    else:
+        _capi.call("cnhip_meanpool1d_backward_rows", _p(dy), _p(dx), B, S, D, rows, _stream())
 
 
 def add(a, b, y) -> None:

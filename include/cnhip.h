@@ -123,6 +123,7 @@ int cnhip_gemm_f32_batched(int trans_a, int trans_b, int64_t M, int64_t N, int64
                            float* C, int64_t ldc, int64_t stride_c, int64_t batch_count,
                            cnhip_stream_t stream);
 
+
 /* Measurement aid for the MFMA GEMM-shaped kernels (the GEMM kernel and the
  * implicit-GEMM Conv2D forward / dgrad / wgrad kernels): while enabled,
  * every such launch on this host thread is bracketed by HIP events on its
@@ -278,7 +279,17 @@ int cnhip_seq_scatter(const float* in, float* Y, int64_t B, int64_t S, int64_t D
                       cnhip_stream_t stream);
 
 /* ---- transformer layers ----------------------------------------------------
- * Sequences [B,S,D] are ColMajor (row b + B*s of a [B*S, D] matrix). */
+ * Sequences [B,S,D] are ColMajor (row b + B*s of a [B*S, D] matrix).
+ *
+ * Row order.  The `_rows` variants also take CNHIP_ROWS_BY_SAMPLE: every
+ * [B*S, D] sequence argument then holds row s + S*b (sample b's S rows
+ * adjacent), which is what the batched attention products read without
+ * transposing; ids stay ColMajor [B, S] and pooled outputs [B, D].  These
+ * variants have no reference counterpart: the reference has one row order.
+ * They are for a caller that owns the whole Embedding -> MeanPool1D chain,
+ * so that the order never reaches its user. */
+#define CNHIP_ROWS_REF 0       /* row b + B*s (the reference's [B,S,D]) */
+#define CNHIP_ROWS_BY_SAMPLE 1 /* row s + S*b */
 
 /* out [cols, rows] = in [rows, cols]^T, both ColMajor. */
 int cnhip_transpose(const float* in, float* out, int64_t rows, int64_t cols,
@@ -318,6 +329,19 @@ int cnhip_mha_backward_residual(const float* q, const float* k, const float* v, 
                                 float* gWq, float* gWk, float* gWv, float* gWo, float* dX,
                                 int64_t B, int64_t S, int64_t D, int64_t heads,
                                 cnhip_stream_t stream);
+/* cnhip_mha_forward_residual / _backward_residual in either row order
+ * (residual / residual_grad may be NULL: the unfused pass). */
+int cnhip_mha_forward_rows(const float* q, const float* k, const float* v, const float* Wq,
+                           const float* Wk, const float* Wv, const float* Wo,
+                           const float* residual, float* out, float* cache, int64_t B,
+                           int64_t S, int64_t D, int64_t heads, int rows,
+                           cnhip_stream_t stream);
+int cnhip_mha_backward_rows(const float* q, const float* k, const float* v, const float* Wq,
+                            const float* Wk, const float* Wv, const float* Wo,
+                            const float* cache, const float* dY, const float* residual_grad,
+                            float* gWq, float* gWk, float* gWv, float* gWo, float* dX,
+                            int64_t B, int64_t S, int64_t D, int64_t heads, int rows,
+                            cnhip_stream_t stream);
 /* Embedding: weights kept token-major, Wt[d + D*v] (the transpose of the
  * reference's ColMajor [V, D]); ids [B,S] int32; out [B,S,D].  Ids outside
  * [0, V) give zero rows and are counted into *oob_count (may be NULL; the
@@ -331,10 +355,22 @@ int cnhip_embedding_forward(const int32_t* ids, const float* Wt, float* out, int
                             cnhip_stream_t stream);
 int cnhip_embedding_backward(const int32_t* ids, const float* dY, float* gWt, int64_t B,
                              int64_t S, int64_t V, int64_t D, cnhip_stream_t stream);
+/* the same in either row order (of out and dY) */
+int cnhip_embedding_forward_rows(const int32_t* ids, const float* Wt, float* out, int64_t B,
+                                 int64_t S, int64_t V, int64_t D, int32_t* oob_count, int rows,
+                                 cnhip_stream_t stream);
+int cnhip_embedding_backward_rows(const int32_t* ids, const float* dY, float* gWt, int64_t B,
+                                  int64_t S, int64_t V, int64_t D, int rows,
+                                  cnhip_stream_t stream);
 /* BatchNorm over x [N,F] in training mode: biased batch variance,
  * xhat = (x - mean)/sqrt(var + eps), y = gamma xhat + beta, running stats
  * (1-momentum) r + momentum * batch.  backward OVERWRITES grad_gamma and
- * grad_beta.  ref: BatchNorm::forward/backward
+ * grad_beta.  xhat may be NULL in both: the forward then does not store it
+ * and the backward recomputes it from x, batch_mean and batch_var with the
+ * forward's exact expression (bit-identical), 8 + 12 instead of 12 + 16
+ * bytes per element; pass the cached xhat to the backward after an
+ * eval-mode forward (the reference's backward reads its cached x_hat_).
+ * ref: BatchNorm::forward/backward
  * src/CppNet/layers/batch_norm.cpp:204-401; batch_norm_forward.cu,
  * batch_norm_backward.cu */
 int cnhip_batchnorm_forward(const float* x, float* y, float* xhat, const float* gamma,
@@ -363,6 +399,11 @@ int cnhip_meanpool1d_forward(const float* x, float* y, int64_t B, int64_t S, int
                              cnhip_stream_t stream);
 int cnhip_meanpool1d_backward(const float* dy, float* dx, int64_t B, int64_t S, int64_t D,
                               cnhip_stream_t stream);
+/* the same in either row order (of x and dx) */
+int cnhip_meanpool1d_forward_rows(const float* x, float* y, int64_t B, int64_t S, int64_t D,
+                                  int rows, cnhip_stream_t stream);
+int cnhip_meanpool1d_backward_rows(const float* dy, float* dx, int64_t B, int64_t S, int64_t D,
+                                   int rows, cnhip_stream_t stream);
 /* y = a + b (the residual add and its gradient sum).
  * ref: Residual::forward/backward src/CppNet/layers/residual.cpp:44-159 */
 int cnhip_add(const float* a, const float* b, float* y, int64_t n, cnhip_stream_t stream);

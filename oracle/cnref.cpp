@@ -3,6 +3,7 @@
 // product).  See cnref.h for conventions.  Reference paths are relative to
 // the LoqmanSamani/CppNet tree.
 #include "cnref.h"
+#include "cnref_fn.hpp"
 
 #include <algorithm>
 #include <cmath>
@@ -14,9 +15,14 @@
 #include <omp.h>
 #endif
 
+namespace cnref_detail {
+int acc_double = 0;
+}
+
 namespace {
 int g_threads = 1;
-int g_acc_double = 0;
+int& g_acc_double = cnref_detail::acc_double;
+int g_order = 0;
 
 // dst[r + R c] = trans ? src[c + ld r] : src[r + ld c], in 64 x 64 tiles.
 void copy_tiles(float* dst, int64_t R, int64_t Cn, const float* src, int64_t ld, bool trans) {
@@ -36,14 +42,31 @@ void copy_tiles(float* dst, int64_t R, int64_t Cn, const float* src, int64_t ld,
   }
 }
 
-// acc[m + M n] += sum_k Am[m + M k] * Bk[k + K n], each element's products
-// added in ascending k in the accumulator type T.  An MR x 4 tile of acc is
-// held in registers across a k-panel of KB (MR = 64 bytes of T).
+// acc[m + M n] += sum_k Am[m + M k] * Bk[k + K n] in the accumulator type
+// T, each element's products added in the order ORD:
+//   0  ascending k (the restatement's order);
+//   1  descending k;
+//   2  32-wide chunks of k, each summed from zero in ascending k, the chunk
+//      sums added in ascending order (the shape of a tiled accumulation);
+//   3  within each k-panel of KB, P = 8 strided partial sums (k mod 8, each
+//      ascending), combined by a pairwise tree and added panel after panel
+//      (the shape of lane-parallel partial sums reduced across lanes).
+// An MR x 4 tile of acc is held in registers across a k-panel of KB
+// (MR = 64 bytes of T).
+constexpr int KP = 8;  // partial sums of order 3
+// ((q0 + q1) + (q2 + q3)) + ((q4 + q5) + (q6 + q7))
 template <class T>
+T tree8(const T* q) {
+  return ((q[0] + q[1]) + (q[2] + q[3])) + ((q[4] + q[5]) + (q[6] + q[7]));
+}
+
+template <class T, int ORD>
 void gemm_panels(int64_t M, int64_t N, int64_t K, const float* Am, const float* Bk, T* acc) {
-  constexpr int64_t KB = 256, NB = 4, MR = 64 / sizeof(T);
+  constexpr int64_t KB = 256, NB = 4, MR = 64 / sizeof(T), KC = 32;
   const int64_t nblocks = (N + NB - 1) / NB;
-  for (int64_t k0 = 0; k0 < K; k0 += KB) {
+  const int64_t npanels = (K + KB - 1) / KB;
+  for (int64_t pi = 0; pi < npanels; ++pi) {
+    const int64_t k0 = (ORD == 1 ? npanels - 1 - pi : pi) * KB;
     const int64_t k1 = std::min(K, k0 + KB);
 #pragma omp parallel for num_threads(g_threads) schedule(static)
     for (int64_t nb = 0; nb < nblocks; ++nb) {
@@ -56,14 +79,47 @@ void gemm_panels(int64_t M, int64_t N, int64_t K, const float* Am, const float* 
           T c[NB][MR];
           for (int64_t j = 0; j < NB; ++j)
             for (int64_t i = 0; i < MR; ++i) c[j][i] = acc[m0 + i + M * (n0 + j)];
-          for (int64_t k = k0; k < k1; ++k) {
-            const float* a = Am + m0 + M * k;
-            T av[MR];
-            for (int64_t i = 0; i < MR; ++i) av[i] = a[i];
-            for (int64_t j = 0; j < NB; ++j) {
-              const T b = bcol[j][k];
-              for (int64_t i = 0; i < MR; ++i) c[j][i] += av[i] * b;
+          if (ORD == 3) {
+            T part[KP][NB][MR];
+            for (int p = 0; p < KP; ++p)
+              for (int64_t j = 0; j < NB; ++j)
+                for (int64_t i = 0; i < MR; ++i) part[p][j][i] = 0;
+            for (int64_t k = k0; k < k1; ++k) {
+              T (&dst)[NB][MR] = part[(k - k0) % KP];
+              const float* a = Am + m0 + M * k;
+              T av[MR];
+              for (int64_t i = 0; i < MR; ++i) av[i] = a[i];
+              for (int64_t j = 0; j < NB; ++j) {
+                const T b = bcol[j][k];
+                for (int64_t i = 0; i < MR; ++i) dst[j][i] += av[i] * b;
+              }
             }
+            for (int64_t j = 0; j < NB; ++j)
+              for (int64_t i = 0; i < MR; ++i) {
+                T q[KP];
+                for (int p = 0; p < KP; ++p) q[p] = part[p][j][i];
+                c[j][i] += tree8(q);
+              }
+          }
+          for (int64_t kc = k0; ORD != 3 && kc < k1; kc += KC) {
+            const int64_t kc1 = std::min(k1, kc + KC);
+            T part[NB][MR];
+            for (int64_t j = 0; j < NB; ++j)
+              for (int64_t i = 0; i < MR; ++i) part[j][i] = 0;
+            T (&dst)[NB][MR] = ORD == 2 ? part : c;
+            for (int64_t kk = kc; kk < kc1; ++kk) {
+              const int64_t k = ORD == 1 ? (k0 + k1 - 1) - kk : kk;
+              const float* a = Am + m0 + M * k;
+              T av[MR];
+              for (int64_t i = 0; i < MR; ++i) av[i] = a[i];
+              for (int64_t j = 0; j < NB; ++j) {
+                const T b = bcol[j][k];
+                for (int64_t i = 0; i < MR; ++i) dst[j][i] += av[i] * b;
+              }
+            }
+            if (ORD == 2)
+              for (int64_t j = 0; j < NB; ++j)
+                for (int64_t i = 0; i < MR; ++i) c[j][i] += part[j][i];
           }
           for (int64_t j = 0; j < NB; ++j)
             for (int64_t i = 0; i < MR; ++i) acc[m0 + i + M * (n0 + j)] = c[j][i];
@@ -72,14 +128,93 @@ void gemm_panels(int64_t M, int64_t N, int64_t K, const float* Am, const float* 
       // rows past the last full tile, and the last partial column block
       for (int64_t j = 0; j < nn; ++j) {
         T* cc = acc + M * (n0 + j);
-        for (int64_t k = k0; k < k1; ++k) {
-          const T b = bcol[j][k];
-          const float* a = Am + M * k;
-          for (int64_t m = m0; m < M; ++m) cc[m] += (T)a[m] * b;
+        for (int64_t m = m0; m < M; ++m) {
+          T cm = cc[m];
+          if (ORD == 3) {
+            T q[KP] = {};
+            for (int64_t k = k0; k < k1; ++k) q[(k - k0) % KP] += (T)Am[m + M * k] * (T)bcol[j][k];
+            cm += tree8(q);
+          }
+          for (int64_t kc = k0; ORD != 3 && kc < k1; kc += KC) {
+            const int64_t kc1 = std::min(k1, kc + KC);
+            T part = 0;
+            T& dst = ORD == 2 ? part : cm;
+            for (int64_t kk = kc; kk < kc1; ++kk) {
+              const int64_t k = ORD == 1 ? (k0 + k1 - 1) - kk : kk;
+              dst += (T)Am[m + M * k] * (T)bcol[j][k];
+            }
+            if (ORD == 2) cm += part;
+          }
+          cc[m] = cm;
         }
       }
     }
   }
+}
+}  // namespace
+
+namespace {
+// Sum of term(i) over i in [0, n), in the evaluation order the tests select
+// (cnref_set_sum_order / cnref_set_accumulate_double; default: ascending i
+// in fp32, each addition rounded once).
+template <class F>
+float osum(int64_t n, F term) {
+  if (g_acc_double) {
+    double s = 0.0;
+    for (int64_t i = 0; i < n; ++i) s += (double)term(i);
+    return (float)s;
+  }
+  float s = 0.0f;
+  if (g_order == 1) {
+    for (int64_t i = n - 1; i >= 0; --i) s += term(i);
+  } else if (g_order == 2) {
+    for (int64_t c = 0; c < n; c += 32) {
+      float p = 0.0f;
+      for (int64_t i = c; i < std::min(n, c + 32); ++i) p += term(i);
+      s += p;
+    }
+  } else if (g_order == 3) {
+    float q[KP] = {};
+    for (int64_t i = 0; i < n; ++i) q[i % KP] += term(i);
+    s = tree8(q);
+  } else {
+    for (int64_t i = 0; i < n; ++i) s += term(i);
+  }
+  return s;
+}
+
+// out[j] = sum over i in [0, n) of the contributions add(i, acc) makes to
+// acc[j] (j < width), in the selected order, like osum.
+template <class T, class F>
+void osum_into_t(int64_t n, int64_t width, float* out, F add) {
+  std::vector<T> acc((size_t)width, T(0)), part((size_t)width);
+  if (g_order == 1 && !g_acc_double) {
+    for (int64_t i = n - 1; i >= 0; --i) add(i, acc.data());
+  } else if (g_order == 2 && !g_acc_double) {
+    for (int64_t c = 0; c < n; c += 32) {
+      std::fill(part.begin(), part.end(), T(0));
+      for (int64_t i = c; i < std::min(n, c + 32); ++i) add(i, part.data());
+      for (int64_t j = 0; j < width; ++j) acc[(size_t)j] += part[(size_t)j];
+    }
+  } else if (g_order == 3 && !g_acc_double) {
+    std::vector<T> parts((size_t)(KP * width), T(0));
+    for (int64_t i = 0; i < n; ++i) add(i, parts.data() + (size_t)((i % KP) * width));
+    for (int64_t j = 0; j < width; ++j) {
+      T q[KP];
+      for (int p = 0; p < KP; ++p) q[p] = parts[(size_t)(p * width + j)];
+      acc[(size_t)j] = tree8(q);
+    }
+  } else {
+    for (int64_t i = 0; i < n; ++i) add(i, acc.data());
+  }
+  for (int64_t j = 0; j < width; ++j) out[j] = (float)acc[(size_t)j];
+}
+template <class F>
+void osum_into(int64_t n, int64_t width, float* out, F add) {
+  if (g_acc_double)
+    osum_into_t<double>(n, width, out, add);
+  else
+    osum_into_t<float>(n, width, out, add);
 }
 }  // namespace
 
@@ -94,6 +229,7 @@ float* cnref_trace(int slot) { return slot >= 0 && slot < 5 ? g_trace[slot] : nu
 void cnref_set_threads(int n) { g_threads = n < 1 ? 1 : n; }
 int cnref_get_threads(void) { return g_threads; }
 void cnref_set_accumulate_double(int on) { g_acc_double = on != 0; }
+void cnref_set_sum_order(int order) { g_order = order >= 0 && order <= 3 ? order : 0; }
 
 // ---------------------------------------------------------------------------
 // GEMM.  op(A) is first materialised M-contiguous and op(B) K-contiguous;
@@ -122,10 +258,16 @@ void cnref_gemm_f32(int ta, int tb, int64_t M, int64_t N, int64_t K, float alpha
     // different (more accurate) summation: products and sums in double,
     // one rounding to float per element.
     std::vector<double> accd((size_t)M * (size_t)N, 0.0);
-    gemm_panels(M, N, K, Am.data(), Bk.data(), accd.data());
+    gemm_panels<double, 0>(M, N, K, Am.data(), Bk.data(), accd.data());
     for (size_t i = 0; i < acc.size(); ++i) acc[i] = (float)accd[i];
+  } else if (g_order == 1) {
+    gemm_panels<float, 1>(M, N, K, Am.data(), Bk.data(), acc.data());
+  } else if (g_order == 2) {
+    gemm_panels<float, 2>(M, N, K, Am.data(), Bk.data(), acc.data());
+  } else if (g_order == 3) {
+    gemm_panels<float, 3>(M, N, K, Am.data(), Bk.data(), acc.data());
   } else {
-    gemm_panels(M, N, K, Am.data(), Bk.data(), acc.data());
+    gemm_panels<float, 0>(M, N, K, Am.data(), Bk.data(), acc.data());
   }
 #pragma omp parallel for num_threads(g_threads) schedule(static)
   for (int64_t n = 0; n < N; ++n)
@@ -149,8 +291,8 @@ void cnref_linear_forward(const float* X, const float* W, const float* b, float*
 // grad_biases_ += grad_output.sum({0}) of linear.cpp:350-352.
 void cnref_column_sum(const float* in, float* out, int64_t rows, int64_t cols, int accumulate) {
   for (int64_t c = 0; c < cols; ++c) {
-    float s = 0.f;
-    for (int64_t r = 0; r < rows; ++r) s += in[r + rows * c];
+    const float* col = in + rows * c;
+    const float s = osum(rows, [&](int64_t r) { return col[r]; });
     out[c] = accumulate ? out[c] + s : s;
   }
 }
@@ -232,7 +374,7 @@ void cnref_relu_backward(const float* y, const float* dy, float* dx, int64_t n) 
 void cnref_sigmoid_forward(const float* x, float* y, int64_t n) {
   for (int64_t i = 0; i < n; ++i) {
     const float c = std::max(-500.0f, std::min(500.0f, x[i]));
-    y[i] = 1.0f / (1.0f + std::exp(-c));
+    y[i] = 1.0f / (1.0f + ref_exp(-c));
   }
 }
 // Sigmoid::backward cpu-eigen: grad * (s * (1 - s)) (sigmoid.cpp:190-194)
@@ -241,7 +383,7 @@ void cnref_sigmoid_backward(const float* y, const float* dy, float* dx, int64_t 
 }
 // Tanh::forward (tanh.cpp:100-134, cpu-eigen: .tanh())
 void cnref_tanh_forward(const float* x, float* y, int64_t n) {
-  for (int64_t i = 0; i < n; ++i) y[i] = std::tanh(x[i]);
+  for (int64_t i = 0; i < n; ++i) y[i] = ref_tanh(x[i]);
 }
 // Tanh::backward cpu-eigen: grad * (1 - t*t) (tanh.cpp:151-155)
 void cnref_tanh_backward(const float* y, const float* dy, float* dx, int64_t n) {
@@ -255,7 +397,7 @@ float cnref_bce_forward(const float* p, const float* t, int64_t n, int reduction
   for (int64_t i = 0; i < n; ++i) {
     const float pc = std::max(1e-7f, std::min(p[i], 1.0f - 1e-7f));
     const float tv = t[i];
-    total += -(tv * std::log(pc) + (1.0f - tv) * std::log(1.0f - pc));
+    total += -(tv * ref_log(pc) + (1.0f - tv) * ref_log(1.0f - pc));
   }
   return reduction == 1 ? total : total / (float)n;
 }
@@ -295,10 +437,10 @@ float cnref_softmax_ce_forward(const float* z, const float* t, float* sm, int64_
     for (int64_t c = 1; c < C; ++c) mx = std::max(mx, z[b + B * c]);
     float se = 0.0f;
     for (int64_t c = 0; c < C; ++c) {
-      sm[b + B * c] = std::exp(z[b + B * c] - mx);
+      sm[b + B * c] = ref_exp(z[b + B * c] - mx);
       se += sm[b + B * c];
     }
-    const float ls = std::log(se + 1e-12f);
+    const float ls = ref_log(se + 1e-12f);
     for (int64_t c = 0; c < C; ++c) {
       sm[b + B * c] /= se;
       total -= t[b + B * c] * ((z[b + B * c] - mx) - ls);
@@ -382,34 +524,30 @@ void cnref_conv2d_backward(const float* X, const float* Wt, const float* dY, flo
   if (gb) {
 #pragma omp parallel for num_threads(g_threads) schedule(static)
     for (int64_t oc = 0; oc < OC; ++oc) {
-      float acc = 0.0f;
       const float* g = Gi.data() + oc * N * HO * WO;  // (n, oh, ow) in order
-      for (int64_t i = 0; i < N * HO * WO; ++i) acc += g[i];
-      gb[oc] = acc;
+      gb[oc] = osum(N * HO * WO, [&](int64_t i) { return g[i]; });
     }
   }
 #pragma omp parallel for num_threads(g_threads) schedule(static) collapse(2)
   for (int64_t oc = 0; oc < OC; ++oc)
     for (int64_t ic = 0; ic < C; ++ic) {
-      std::vector<float> acc((size_t)(KS * KS), 0.0f);
-      for (int64_t n = 0; n < N; ++n) {
+      std::vector<float> w((size_t)(KS * KS));
+      // term i = (n, oh, ow) in order adds x * g to each (kh, kw) it reaches
+      osum_into(N * HO * WO, KS * KS, w.data(), [&](int64_t i, auto* acc) {
+        const int64_t n = i / (HO * WO), oh = (i / WO) % HO, ow = i % WO;
         const float* xi = Xi.data() + (ic * N + n) * H * Wd;
-        const float* gi = Gi.data() + (oc * N + n) * HO * WO;
-        for (int64_t oh = 0; oh < HO; ++oh)
-          for (int64_t ow = 0; ow < WO; ++ow) {
-            const float g = gi[oh * WO + ow];
-            for (int64_t kh = 0; kh < KS; ++kh) {
-              const int64_t ih = oh * S - P + kh;
-              if (ih < 0 || ih >= H) continue;
-              for (int64_t kw = 0; kw < KS; ++kw) {
-                const int64_t iw = ow * S - P + kw;
-                if (iw >= 0 && iw < Wd) acc[(size_t)(kh * KS + kw)] += xi[ih * Wd + iw] * g;
-              }
-            }
+        const float g = Gi[(size_t)((oc * N + n) * HO * WO + oh * WO + ow)];
+        for (int64_t kh = 0; kh < KS; ++kh) {
+          const int64_t ih = oh * S - P + kh;
+          if (ih < 0 || ih >= H) continue;
+          for (int64_t kw = 0; kw < KS; ++kw) {
+            const int64_t iw = ow * S - P + kw;
+            if (iw >= 0 && iw < Wd) acc[kh * KS + kw] += xi[ih * Wd + iw] * g;
           }
-      }
+        }
+      });
       for (int64_t kh = 0; kh < KS; ++kh)
-        for (int64_t kw = 0; kw < KS; ++kw) gW[idx4(oc, ic, kh, kw, OC, C, KS)] = acc[(size_t)(kh * KS + kw)];
+        for (int64_t kw = 0; kw < KS; ++kw) gW[idx4(oc, ic, kh, kw, OC, C, KS)] = w[(size_t)(kh * KS + kw)];
     }
   // dX: the N samples of one (ic, ih, iw) are contiguous; each element takes
   // its terms in (oc, oh, ow) order (a given (oh, ow) reaches it through at
@@ -477,7 +615,7 @@ void cnref_maxpool2d_backward(const float* dY, const int32_t* idx, float* dX, in
 }
 
 // ---------------------------------------------------------------- LSTM / GRU
-static inline float sigm(float x) { return 1.0f / (1.0f + std::exp(-x)); }
+static inline float sigm(float x) { return 1.0f / (1.0f + ref_exp(-x)); }
 
 // x_t = X[:, t, :] as a dense [B, I] ColMajor matrix (lstm.cpp:98-101)
 static std::vector<float> slice_t(const float* X, int64_t B, int64_t S, int64_t D, int64_t t) {
@@ -506,9 +644,9 @@ void cnref_lstm_forward(const float* X, const float* Wih, const float* Whh, cons
           const int64_t col = d + q * H;
           pre[q] = (gx[n + B * col] + gh[n + B * col]) + b[col];
         }
-        const float ig = sigm(pre[0]), fg = sigm(pre[1]), gg = std::tanh(pre[2]), og = sigm(pre[3]);
+        const float ig = sigm(pre[0]), fg = sigm(pre[1]), gg = ref_tanh(pre[2]), og = sigm(pre[3]);
         const float ct = fg * cp[n + B * d] + ig * gg;
-        const float tc = std::tanh(ct);
+        const float tc = ref_tanh(ct);
         const float ht = og * tc;
         const int64_t row = n + B * t;
         gates[row + BS * (d + 0 * H)] = ig;
@@ -600,7 +738,7 @@ void cnref_gru_forward(const float* X, const float* Wih, const float* Whh, const
     for (int64_t d = 0; d < H; ++d)
       for (int64_t n = 0; n < B; ++n) {
         const int64_t e = n + B * d, row = n + B * t;
-        const float nc = std::tanh((gx[n + B * (d + 2 * H)] + proj[e]) + b[d + 2 * H]);
+        const float nc = ref_tanh((gx[n + B * (d + 2 * H)] + proj[e]) + b[d + 2 * H]);
         const float ht = (1.0f - zg[e]) * nc + zg[e] * h[e];
         gates[row + BS * d] = zg[e];
         gates[row + BS * (d + H)] = rg[e];
@@ -728,7 +866,7 @@ void cnref_mha_forward(const float* q, const float* k, const float* v, const flo
       for (int64_t j = 1; j < S; ++j) mx = std::max(mx, sc[i + S * j]);
       float sum = 0.0f;
       for (int64_t j = 0; j < S; ++j) {
-        A[i + S * j] = std::exp(sc[i + S * j] - mx);
+        A[i + S * j] = ref_exp(sc[i + S * j] - mx);
         sum += A[i + S * j];
       }
       for (int64_t j = 0; j < S; ++j) A[i + S * j] /= sum;
@@ -804,14 +942,13 @@ void cnref_batchnorm_forward(const float* x, float* y, float* xhat, const float*
                              float momentum, float eps) {
   const float inv_batch = 1.0f / static_cast<float>(N);
   for (int64_t f = 0; f < F; ++f) {
-    float m = 0.0f;
-    for (int64_t n = 0; n < N; ++n) m += x[n + N * f];
+    const float* xc = x + N * f;
+    float m = osum(N, [&](int64_t n) { return xc[n]; });
     m *= inv_batch;
-    float var = 0.0f;
-    for (int64_t n = 0; n < N; ++n) {
-      const float diff = x[n + N * f] - m;
-      var += diff * diff;
-    }
+    float var = osum(N, [&](int64_t n) {
+      const float diff = xc[n] - m;
+      return diff * diff;
+    });
     var *= inv_batch;
     batch_mean[f] = m;
     batch_var[f] = var;
@@ -830,21 +967,16 @@ void cnref_batchnorm_backward(const float* dY, const float* x, const float* xhat
                               float eps) {
   const float inv_batch = 1.0f / static_cast<float>(N);
   for (int64_t f = 0; f < F; ++f) {
-    float gg = 0.0f, gbt = 0.0f;
-    for (int64_t n = 0; n < N; ++n) {
-      gg += dY[n + N * f] * xhat[n + N * f];
-      gbt += dY[n + N * f];
-    }
-    ggamma[f] = gg;
-    gbeta[f] = gbt;
+    const float* dy = dY + N * f;
+    ggamma[f] = osum(N, [&](int64_t n) { return dy[n] * xhat[n + N * f]; });
+    gbeta[f] = osum(N, [&](int64_t n) { return dy[n]; });
     const float inv_std = 1.0f / std::sqrt(batch_var[f] + eps);
-    float dvar = 0.0f, dmean = 0.0f;
-    for (int64_t n = 0; n < N; ++n) {
-      const float dxh = dY[n + N * f] * gamma[f];
+    const float dvar = osum(N, [&](int64_t n) {
+      const float dxh = dy[n] * gamma[f];
       const float xmu = x[n + N * f] - batch_mean[f];
-      dvar += dxh * xmu * (-0.5f) * inv_std * inv_std * inv_std;
-      dmean += dxh * (-inv_std);
-    }
+      return dxh * xmu * (-0.5f) * inv_std * inv_std * inv_std;
+    });
+    const float dmean = osum(N, [&](int64_t n) { return dy[n] * gamma[f] * (-inv_std); });
     for (int64_t n = 0; n < N; ++n) {
       const float dxh = dY[n + N * f] * gamma[f];
       const float xmu = x[n + N * f] - batch_mean[f];
@@ -874,8 +1006,7 @@ void cnref_gelu_backward(const float* x, const float* dy, float* dx, int64_t n) 
 void cnref_meanpool1d_forward(const float* x, float* y, int64_t B, int64_t S, int64_t D) {
   for (int64_t d = 0; d < D; ++d)
     for (int64_t b = 0; b < B; ++b) {
-      float sum = 0.0f;
-      for (int64_t s = 0; s < S; ++s) sum += x[b + B * s + B * S * d];
+      const float sum = osum(S, [&](int64_t s) { return x[b + B * s + B * S * d]; });
       y[b + B * d] = sum / static_cast<float>(S);
     }
 }

@@ -22,9 +22,17 @@ extern "C" {
 
 void cnref_set_threads(int n);
 int  cnref_get_threads(void);
-/* 1: GEMMs accumulate in double and round once (a second valid evaluation
- * order, used to measure a trajectory's sensitivity to rounding). */
+/* 1: GEMMs and the other reductions accumulate in double and round once,
+ * and exp / log / tanh are evaluated in double and rounded once (another
+ * valid evaluation of every rounding source, used to measure a trajectory's
+ * sensitivity to rounding). */
 void cnref_set_accumulate_double(int on);
+/* The fp32 order of the GEMMs' k sums (when not double-accumulated):
+ * 0 ascending k (default); 1 descending k; 2 chunks of 32 k summed from
+ * zero, chunk sums added in order.  Three more valid evaluation orders,
+ * used, like the double accumulation, to measure how far a trajectory
+ * moves under rounding alone. */
+void cnref_set_sum_order(int order);
 
 /* Optional diagnostic outputs for the tests' error bars (NULL = off).  While
  * a slot holds a buffer, the functions below also write:

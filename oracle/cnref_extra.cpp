@@ -13,6 +13,7 @@
 #include <vector>
 
 #include "cnref.h"
+#include "cnref_fn.hpp"
 
 extern "C" {
 
@@ -37,7 +38,7 @@ void cnref_softmax_forward(const float* x, float* y, int64_t R, int64_t L) {
     for (int64_t j = 1; j < L; ++j) mx = std::max(mx, x[r + R * j]);
     float s = 0.0f;
     for (int64_t j = 0; j < L; ++j) {
-      y[r + R * j] = std::exp(x[r + R * j] - mx);
+      y[r + R * j] = ref_exp(x[r + R * j] - mx);
       s += y[r + R * j];
     }
     for (int64_t j = 0; j < L; ++j) y[r + R * j] /= s;
@@ -74,7 +75,7 @@ float cnref_cce_forward(const float* pred, const float* t, float* sm, float* tar
         if (pred[b + B * j] > mx) mx = pred[b + B * j];
       float se = 0.0f;
       for (int64_t j = 0; j < C; ++j) {
-        const float e = std::exp(pred[b + B * j] - mx);
+        const float e = ref_exp(pred[b + B * j] - mx);
         sm[b + B * j] = e;
         se += e;
       }
@@ -89,7 +90,7 @@ float cnref_cce_forward(const float* pred, const float* t, float* sm, float* tar
     float sample = 0.0f;
     for (int64_t j = 0; j < C; ++j) {
       const float p = std::max(eps, std::min(1.0f - eps, sm[b + B * j]));
-      sample -= targets_used[b + B * j] * std::log(p);
+      sample -= targets_used[b + B * j] * ref_log(p);
     }
     total += sample;
   }
@@ -261,7 +262,7 @@ void cnref_rnn_forward(const float* X, const float* Wih, const float* Whh, const
     cnref_gemm_f32(0, 0, B, H, H, 1.f, h.data(), B, Whh, H, 0.f, hw.data(), B, nullptr, 0);
     for (int64_t d = 0; d < H; ++d)
       for (int64_t n = 0; n < B; ++n) {
-        const float v = std::tanh((xw[(size_t)(n + B * d)] + hw[(size_t)(n + B * d)]) + b[d]);
+        const float v = ref_tanh((xw[(size_t)(n + B * d)] + hw[(size_t)(n + B * d)]) + b[d]);
         h[(size_t)(n + B * d)] = v;
         Y[n + B * t + B * S * d] = v;
       }

@@ -122,3 +122,68 @@ def test_seq_select_scatter(gpu):
     b = host(back).reshape(D, S, B).transpose(2, 1, 0)
     assert not b[:, :S - 1, :].any()
     np.testing.assert_array_equal(b[:, S - 1, :], y[:, S - 1, :])
+
+
+def _lstm_run(B, S, I, H, seed, env, backward=True):
+    """forward (+ backward) with the given CNHIP_* environment; host copies."""
+    import os
+    saved = {k: os.environ.get(k) for k in env}
+    os.environ.update(env)
+    try:
+        rng = np.random.default_rng(seed)
+        X, Wih, Whh, b, dY = _inputs(rng, B, S, I, H, 4)
+        BS, G = B * S, 4 * H
+        Y, gates = torch.empty(BS * H, device="cuda"), torch.empty(BS * G, device="cuda")
+        c, tc = torch.empty(BS * H, device="cuda"), torch.empty(BS * H, device="cuda")
+        ops.lstm_forward(dev(X), dev(Wih), dev(Whh), dev(b), Y, gates, c, tc, B, S, I, H)
+        if not backward:
+            return [host(t) for t in (Y, gates, c, tc)]
+        gWih, gWhh = torch.empty(I * G, device="cuda"), torch.empty(H * G, device="cuda")
+        gb, dX = torch.empty(G, device="cuda"), torch.empty(BS * I, device="cuda")
+        ops.lstm_backward(dev(X), dev(Wih), dev(Whh), Y, gates, c, tc, dev(dY), gWih, gWhh, gb, dX, B, S, I, H)
+        return [host(t) for t in (Y, gates, c, tc, gWih, gWhh, gb, dX)]
+    finally:
+        for k, v in saved.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+
+
+# shapes the persistent recurrence takes (B % 32 == 0, H % 64 == 0, H <= 512)
+# and one it leaves to the per-step launches
+PERSIST_CASES = [(128, 64, 128, 512), (32, 5, 16, 64), (64, 9, 24, 128), (40, 6, 12, 71)]
+
+
+@pytest.mark.parametrize("B,S,I,H", PERSIST_CASES)
+def test_lstm_persistent_equals_per_step(gpu, B, S, I, H):
+    """The persistent recurrence (one launch for all timesteps) and the
+    per-step launches compute the same arithmetic in the same order: every
+    output, cache and gradient must agree bit for bit."""
+    print(f"[lstm-persist] B={B} S={S} I={I} H={H}", flush=True)
+    a = _lstm_run(B, S, I, H, 7, {"CNHIP_RECURRENCE_PERSISTENT": "1"})
+    b = _lstm_run(B, S, I, H, 7, {"CNHIP_RECURRENCE_PERSISTENT": "0"})
+    names = ["Y", "gates", "c", "tanh_c", "gW_ih", "gW_hh", "gb", "dX"]
+    for x, y, name in zip(a, b, names):
+        assert np.array_equal(x.view(np.uint32), y.view(np.uint32)), f"{name} differs between the paths"
+
+
+def test_lstm_persistent_wait_fault_is_reported(gpu):
+    """Forced from the host: with a negative spin limit every wait of the
+    persistent recurrence gives up at once, so every block exits normally;
+    the launch's fault is reported by the next recurrent call, once, and the
+    run after it is correct again."""
+    from cppnet_amd import _capi
+    B, S, I, H = 64, 6, 16, 128
+    print("[lstm-persist] forced wait fault", flush=True)
+    # the faulted forward launch's own call returns before the GPU has run it
+    _lstm_run(B, S, I, H, 3, {"CNHIP_RECURRENCE_SPIN_LIMIT": "-1", "CNHIP_RECURRENCE_PERSISTENT": "1"},
+              backward=False)
+    torch.cuda.synchronize()
+    with pytest.raises(_capi.CnhipError, match="gave up waiting"):
+        _lstm_run(B, S, I, H, 3, {"CNHIP_RECURRENCE_PERSISTENT": "1"})
+    torch.cuda.synchronize()
+    good = _lstm_run(B, S, I, H, 3, {"CNHIP_RECURRENCE_PERSISTENT": "1"})
+    ref = _lstm_run(B, S, I, H, 3, {"CNHIP_RECURRENCE_PERSISTENT": "0"})
+    for x, y in zip(good, ref):
+        assert np.array_equal(x.view(np.uint32), y.view(np.uint32))

@@ -157,6 +157,62 @@ def test_mha_vs_oracle(gpu, oracle, B, S, D, h, self_attn):
         np.testing.assert_array_equal(host(a), host(b_))
 
 
+def to_by_sample(flat, B, S, D):
+    """ColMajor [B, S, D] (row b + B*s) -> rows s + S*b."""
+    return np.ascontiguousarray(np.asarray(flat).reshape(D, S, B).transpose(0, 2, 1)).ravel()
+
+
+def from_by_sample(flat, B, S, D):
+    return np.ascontiguousarray(np.asarray(flat).reshape(D, B, S).transpose(0, 2, 1)).ravel()
+
+
+@pytest.mark.parametrize("self_attn", [True, False])
+@pytest.mark.parametrize("B,S,D,h", MHA_CASES + [(3, 6, 8, 2)])
+def test_mha_by_sample_rows(gpu, B, S, D, h, self_attn):
+    """The by-sample row order (no transposes) against the reference order on
+    the same data: every row-wise result (output, attention weights, dX) is
+    bit-identical, since each element is the same sum in the same order; the
+    weight gradients, sums over all B*S rows taken in another row order, are
+    within the per-element contraction bar."""
+    print(f"[mha rows] B={B} S={S} D={D} heads={h} self={self_attn}", flush=True)
+    rng = np.random.default_rng(B * 5 + S + D + self_attn)
+    lim = np.sqrt(6.0 / (2 * D))
+    Ws = [rng.uniform(-lim, lim, (D, D)).astype(np.float32) for _ in range(4)]
+    xs = [rng.standard_normal((B, S, D)).astype(np.float32) for _ in range(1 if self_attn else 3)]
+    if self_attn:
+        xs = xs * 3
+    dy = (rng.standard_normal((B, S, D)) * 1e-2).astype(np.float32)
+    skip = (rng.standard_normal((B, S, D)) * 1e-2).astype(np.float32)
+    Wc = np.concatenate([cm(w) for w in Ws])
+    runs = {}
+    for rows in (ops.ROWS_REF, ops.ROWS_BY_SAMPLE):
+        order = (lambda a: a) if rows == ops.ROWS_REF else (lambda a: to_by_sample(a, B, S, D))
+        Wall = dev(Wc)
+        Wd = [Wall[i * D * D:(i + 1) * D * D] for i in range(4)]
+        gall = torch.full((4 * D * D,), 7.0, device="cuda")
+        gW = [gall[i * D * D:(i + 1) * D * D] for i in range(4)]
+        xd = [dev(order(cm(x))) for x in xs]
+        if self_attn:
+            xd = [xd[0]] * 3
+        out = torch.empty(B * S * D, device="cuda")
+        cache = torch.empty(ops.mha_cache_floats(B, S, D), device="cuda")
+        ops.mha_forward_residual(*xd, *Wd, xd[0], out, cache, B, S, D, h, rows=rows)
+        dX = torch.empty(B * S * D, device="cuda")
+        ops.mha_backward_residual(*xd, *Wd, cache, dev(order(cm(dy))), dev(order(cm(skip))), *gW, dX,
+                                  B, S, D, h, rows=rows)
+        back = (lambda a: a) if rows == ops.ROWS_REF else (lambda a: from_by_sample(a, B, S, D))
+        A = host(cache)[3 * B * S * D:3 * B * S * D + B * S * S]
+        runs[rows] = (back(host(out)), A, back(host(dX)), [host(g) for g in gW])
+    ref, bys = runs[ops.ROWS_REF], runs[ops.ROWS_BY_SAMPLE]
+    for k, name in enumerate(("out", "attention weights", "dX")):
+        np.testing.assert_array_equal(bys[k], ref[k], err_msg=name)
+    mags = _mha_logical([x.astype(np.float64) for x in xs], [w.astype(np.float64) for w in Ws],
+                        dy.astype(np.float64), h)
+    for got, want, n in zip(bys[3], ref[3], ("gWq", "gWk", "gWv", "gWo")):
+        ok, msg = close_mag(got, want, cm(mags[n]), 1e-4, 1e-5)
+        assert ok, f"{n}: {msg}"
+
+
 def test_mha_rejects_bad_heads(gpu):
     from cppnet_amd import _capi
     x = torch.zeros(2 * 3 * 6, device="cuda")
@@ -189,6 +245,13 @@ def test_embedding_exact(gpu, oracle, B, S, V, D):
     ops.embedding_backward(dev(idc), dev(cm(dy)), gWt, B, S, V, D)
     r_g = np.zeros(V * D, np.float32)
     oracle.cnref_embedding_backward(ip(idc), fp(cm(dy)), fp(r_g), B, S, V, D)
+    np.testing.assert_array_equal(host(gWt).reshape(V, D), from_cm(r_g, (V, D)))
+    # by sample: the same rows at s + S*b, and the same per-token sums in the same order
+    ops.embedding_forward(dev(idc), dev(Wt), out, B, S, V, D, oob, rows=ops.ROWS_BY_SAMPLE)
+    np.testing.assert_array_equal(host(out), to_by_sample(r_out, B, S, D))
+    gWt.fill_(3.0)
+    ops.embedding_backward(dev(idc), dev(to_by_sample(cm(dy), B, S, D)), gWt, B, S, V, D,
+                           rows=ops.ROWS_BY_SAMPLE)
     np.testing.assert_array_equal(host(gWt).reshape(V, D), from_cm(r_g, (V, D)))
 
 
@@ -246,6 +309,16 @@ def test_batchnorm_vs_oracle(gpu, oracle, N, F):
                                  (host(dX), r["dX"], m_dx.ravel(), "dX")]:
         ok, msg = close_mag(got, want, mag, 1e-4, 1e-5)
         assert ok, f"{name}: {msg}"
+    # without xhat: the forward does not store it and the backward recomputes
+    # it with the forward's expression -- the same bits everywhere
+    y2, rm2, rv2 = torch.empty(N * F, device="cuda"), dev(rm0.copy()), dev(rv0.copy())
+    bm2, bv2 = torch.empty(F, device="cuda"), torch.empty(F, device="cuda")
+    ops.batchnorm_forward(dev(x), y2, None, dev(gamma), dev(beta), rm2, rv2, bm2, bv2, N, F, 0.1, 1e-5)
+    gg2, gb2, dX2 = torch.empty(F, device="cuda"), torch.empty(F, device="cuda"), torch.empty(N * F, device="cuda")
+    ops.batchnorm_backward(dev(dy), dev(x), None, dev(gamma), bm2, bv2, gg2, gb2, dX2, N, F, 1e-5)
+    for a, b, name in [(y2, y, "y"), (bm2, bm, "mean"), (bv2, bv, "var"), (rm2, rm, "running_mean"),
+                       (rv2, rv, "running_var"), (gg2, gg, "grad_gamma"), (gb2, gb, "grad_beta"), (dX2, dX, "dX")]:
+        assert np.array_equal(host(a).view(np.uint32), host(b).view(np.uint32)), f"{name} differs without xhat"
 
 
 # ---------------------------------------------------------------- GELU / pool / add
@@ -286,6 +359,12 @@ def test_meanpool1d_vs_oracle(gpu, oracle, B, S, D):
     ok, msg = close_mag(host(y), ry, np.full(ry.shape, np.sqrt(np.mean(x.astype(np.float64) ** 2))), 1e-5, 1e-7)
     assert ok, msg
     np.testing.assert_array_equal(host(dx), rdx)
+    # by sample (rows s + S*b): lane-strided partial sums, the same bar; the broadcast exact
+    ops.meanpool1d_forward(dev(to_by_sample(x, B, S, D)), y, B, S, D, rows=ops.ROWS_BY_SAMPLE)
+    ops.meanpool1d_backward(dev(dy), dx, B, S, D, rows=ops.ROWS_BY_SAMPLE)
+    ok, msg = close_mag(host(y), ry, np.full(ry.shape, np.sqrt(np.mean(x.astype(np.float64) ** 2))), 1e-5, 1e-7)
+    assert ok, f"by sample: {msg}"
+    np.testing.assert_array_equal(host(dx), to_by_sample(rdx, B, S, D))
 
 
 @pytest.mark.parametrize("n", [1, 7, 4096, 8192 * 512 + 3])

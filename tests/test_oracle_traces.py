@@ -105,3 +105,55 @@ def test_transformer_mags_layout(oracle):
     R = cfg.batch * cfg.seq_len
     for k, (m, gr) in enumerate(zip(mags, ref.last_grads)):
         assert np.all(np.abs(gr) <= np.sqrt(R) * m * (1 + 1e-5) + 1e-12), f"param {k}"
+
+
+def test_sum_orders(oracle):
+    """The oracle GEMM's alternative evaluation orders (used to measure how
+    far a training trajectory moves under rounding alone) are what they say:
+    each equals the sequential fp32 sum in its order, exactly."""
+    from oracle import fp
+    rng = np.random.default_rng(5)
+    K = 300
+    a = (rng.standard_normal(K) * np.logspace(0, 6, K)).astype(np.float32)
+    b = np.ones(K, np.float32)
+
+    def run(order):
+        oracle.cnref_set_sum_order(order)
+        c = np.zeros(1, np.float32)
+        try:
+            oracle.cnref_gemm_f32(0, 0, 1, 1, K, 1.0, fp(a), 1, fp(b), K, 0.0, fp(c), 1, None, 0)
+        finally:
+            oracle.cnref_set_sum_order(0)
+        return c[0]
+
+    def seq(xs):
+        s = np.float32(0)
+        for x in xs:
+            s = np.float32(s + x)
+        return s
+
+    chunked = np.float32(0)
+    for c0 in range(0, K, 32):
+        chunked = np.float32(chunked + seq(a[c0:c0 + 32]))
+
+    def tree(xs):  # 8 strided partial sums, combined pairwise
+        q = [seq(xs[p::8]) for p in range(8)]
+        return np.float32(np.float32(np.float32(q[0] + q[1]) + np.float32(q[2] + q[3])) +
+                          np.float32(np.float32(q[4] + q[5]) + np.float32(q[6] + q[7])))
+
+    # the GEMM applies order 3 per k-panel of 256, the panels added in turn
+    strided = np.float32(tree(a[:256]) + tree(a[256:]))
+    assert run(0) == seq(a)
+    assert run(1) == seq(a[::-1])
+    assert run(2) == chunked
+    assert run(3) == strided
+    assert len({float(run(o)) for o in range(4)}) == 4  # the orders differ on this input
+    # the column sums (bias gradients) follow the same orders, order 3 over the whole column
+    for order, want in ((0, seq(a)), (1, seq(a[::-1])), (2, chunked), (3, tree(a))):
+        oracle.cnref_set_sum_order(order)
+        out = np.zeros(1, np.float32)
+        try:
+            oracle.cnref_column_sum(fp(a), fp(out), K, 1, 0)
+        finally:
+            oracle.cnref_set_sum_order(0)
+        assert out[0] == want, f"column sum, order {order}"
