@@ -14,7 +14,7 @@ each weight-gradient contraction (its bias analogue for biases); updated
 weights within the same bound except where the gradient itself is within
 tolerance of 0 (Adam's step 1 is -lr sign(g)).  Twenty steps -- the loss
 within rel 1e-3 at every step and each parameter within rel 1e-3 in norm
-(or 2x the oracle's own fp32-vs-double-accumulation drift).
+(or 2x the oracle's own drift across four other valid evaluation orders).
 """
 import os
 
@@ -85,30 +85,56 @@ def _rel(a, b):
     return float(np.linalg.norm(a.astype(np.float64) - b) / max(np.linalg.norm(b), 1e-30))
 
 
+# (double accumulation, fp32 sum order) of the oracle's alternative
+# evaluation orders: double accumulation rounded once per element, fp32 in
+# descending order, fp32 in 32-wide chunks, fp32 in 8 strided partials
+ORDERS = [(1, 0), (0, 1), (0, 2), (0, 3)]
+
+
+def _oracle_run(cfg, oracle, seed, steps, double, order):
+    rng = np.random.default_rng(seed)
+    params, _, _ = trainer.synthetic_resnet(cfg, rng)
+    ref = OracleResNet(cfg, oracle)
+    ref.set_params(params)
+    oracle.cnref_set_accumulate_double(double)
+    oracle.cnref_set_sum_order(order)
+    try:
+        losses = [ref.step(*trainer.synthetic_resnet(cfg, rng)[1:]) for _ in range(steps)]
+    finally:
+        oracle.cnref_set_accumulate_double(0)
+        oracle.cnref_set_sum_order(0)
+    return ref.get_params(), np.array(losses)
+
+
 @pytest.mark.parametrize("kind", sorted(CASES))
 def test_resnet_multi_step(gpu, oracle_mt, kind):
+    """The drift of a parameter is the largest distance from the fp32 oracle
+    of the oracle's own runs under the four other evaluation orders.  The
+    identity network is rounding-sensitive: a bias-gradient sum that nearly
+    cancels is turned into a +-lr Adam step by its sign (adam.cpp:98-133),
+    so the fp32 orders alone part by ~1e-3 (descending) to ~3e-3 (chunked)
+    on the first two biases after 20 steps, while double accumulation moves
+    them by only ~6e-6; every order is a valid fp32 evaluation, so the bar
+    is max(1e-3, 2 x that drift)."""
     cfg = _cfg(kind, batch=64)
-    steps = 20
+    steps, seed = 20, 32
     print(f"[residual] {cfg.name}: {steps} steps", flush=True)
-    rng = np.random.default_rng(32)
+    rng = np.random.default_rng(seed)
     params, _, _ = trainer.synthetic_resnet(cfg, rng)
     sess = trainer.Session(cfg)
     sess.set_params(params)
-    ref, ref_d = OracleResNet(cfg, oracle_mt), OracleResNet(cfg, oracle_mt)
+    ref = OracleResNet(cfg, oracle_mt)
     ref.set_params(params)
-    ref_d.set_params(params)
     for step in range(steps):
         _, X, Y = trainer.synthetic_resnet(cfg, rng)
         sess.set_batch(X, Y)
         lg, lr_ = sess.step(), ref.step(X, Y)
-        oracle_mt.cnref_set_accumulate_double(1)
-        try:
-            ref_d.step(X, Y)
-        finally:
-            oracle_mt.cnref_set_accumulate_double(0)
         assert abs(lg - lr_) <= 1e-3 * abs(lr_) + 1e-6, f"step {step}: loss {lg} vs {lr_}"
-    for k, (a, b, c) in enumerate(zip(sess.get_params(), ref.get_params(), ref_d.get_params())):
-        rel, drift = _rel(a, b), _rel(c, b)
+    want = ref.get_params()
+    runs = [_oracle_run(cfg, oracle_mt, seed, steps, d, o)[0] for d, o in ORDERS]
+    for k, (a, b) in enumerate(zip(sess.get_params(), want)):
+        rel = _rel(a, b)
+        drift = max(_rel(r[k], b) for r in runs)
         print(f"[residual] {kind} param {k}: rel {rel:.3g} drift {drift:.3g}")
         assert rel <= max(1e-3, 2.0 * drift), f"param {k}: relative norm error {rel:.3g} (drift {drift:.3g})"
     sess.close()
