@@ -60,6 +60,7 @@ SIGNATURES: dict[str, tuple] = {
     "cnhip_column_sum": (i32, [vp, vp, i64, i64, i32, vp]),
     "cnhip_linear_forward_act": (i32, [vp, vp, vp, vp, vp, i64, i64, i64, i32, vp]),
     "cnhip_linear_backward_act": (i32, [vp] * 7 + [i64, i64, i64, i32, i32, i32, vp]),
+    "cnhip_linear_backward_act_noalloc": (i32, [vp] * 7 + [i64, i64, i64, i32, i32, i32, vp]),
     "cnhip_conv2d_forward": (i32, [vp, vp, vp, vp] + [i64] * 8 + [vp]),
     "cnhip_conv2d_forward_relu": (i32, [vp, vp, vp, vp] + [i64] * 8 + [vp]),
     "cnhip_conv2d_backward": (i32, [vp, vp, vp, vp, vp, vp] + [i64] * 8 + [vp]),

@@ -47,6 +47,25 @@ int ws_alloc(void** ptr, size_t bytes, hipStream_t stream, const char* where);
 constexpr int kScratchGemm = 0, kScratchLayer = 1;
 int scratch(hipStream_t stream, int slot, size_t bytes, void** ptr, const char* where);
 
+// While one is in scope on this host thread, a caller-provided device
+// buffer of `cap` bytes stands in for the GEMM scratch slot of every stream
+// (the no-allocation entry points): scratch() hands out `p` for slot
+// kScratchGemm when the request fits, fails with CNHIP_EINVAL when it does
+// not, and refuses the other slots; the per-launch timing records are
+// switched off, since they create events on first use.  Nothing is
+// allocated while it is active.  Not nestable.
+struct FixedScratch {
+  FixedScratch(void* p, size_t cap);
+  ~FixedScratch();
+  FixedScratch(const FixedScratch&) = delete;
+  FixedScratch& operator=(const FixedScratch&) = delete;
+};
+bool fixed_scratch_active();
+
+// Bytes of GEMM scratch (split-K partials) that gemm_f32_core requests for
+// this shape: 0 when it runs without a split.
+size_t gemm_scratch_bytes(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, int64_t batches);
+
 inline int check_hip(hipError_t e, const char* where) {
   if (e != hipSuccess) {
     set_error("%s: %s", where, hipGetErrorString(e));

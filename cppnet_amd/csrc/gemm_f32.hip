@@ -439,7 +439,7 @@ thread_local Timing g_timing;      // MFMA GEMM-shaped launches
 thread_local Timing g_hbm_timing;  // bandwidth-bound launches
 
 TimingRec* next_slot(Timing& t) {
-  if (!t.on) return nullptr;
+  if (!t.on || fixed_scratch_active()) return nullptr;
   if (t.used == t.pool.size()) {
     TimingRec r{};
     // timing-only events: no system-scope fence (cache writeback) at record,
@@ -694,6 +694,17 @@ static int gemm_small(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K,
   return check_launch(who);
 }
 
+// split-K partials of a planned GEMM: [batches][splits][M, N]
+static size_t split_bytes(const Plan& plan, int64_t M, int64_t N, int64_t batches) {
+  return plan.splits > 1 ? (size_t)batches * (size_t)plan.splits * (size_t)M * (size_t)N * sizeof(float) : 0;
+}
+
+size_t gemm_scratch_bytes(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, int64_t batches) {
+  if (M <= 0 || N <= 0 || K < 0 || batches <= 0) return 0;
+  if (gemm_is_small(M, N, K, batches, trans_a, trans_b)) return 0;
+  return split_bytes(plan_gemm(trans_a, trans_b, M, N, K, batches, 64), M, N, batches);
+}
+
 int gemm_f32_core(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float alpha,
                   const float* A, int64_t lda, int64_t stride_a, const float* B, int64_t ldb,
                   int64_t stride_b, float beta, float* C, int64_t ldc, int64_t stride_c,
@@ -739,8 +750,7 @@ int gemm_f32_core(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, flo
 
   if (splits > 1) {
     void* ws = nullptr;
-    const size_t bytes = (size_t)batches * (size_t)splits * (size_t)M * (size_t)N * sizeof(float);
-    CNHIP_TRY(scratch(st, kScratchGemm, bytes, &ws, who));
+    CNHIP_TRY(scratch(st, kScratchGemm, split_bytes(plan, M, N, batches), &ws, who));
     g.partial = static_cast<float*>(ws);
   }
 

@@ -6,6 +6,7 @@
 //   dW += X^T dY      db += sum_batch dY      dX = dY W^T
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdlib>
 
 #include "act_math.hpp"
@@ -247,24 +248,33 @@ void skinny_launch_o(dim3 grid, hipStream_t st, int act, bool sep, const float* 
 // The one-pass backward above, when the shape is one it serves (O one of
 // 1, 2, 4, 8, 10, 16; B % 512 == 0, F % 16 == 0, a wide input, dW wanted);
 // *done says whether it ran.  CNHIP_LINEAR_ONE_PASS=0 keeps the GEMM path.
-int linear_backward_skinny(const float* X, const float* W, const float* dY, float* dW, float* db,
-                           float* dX, const float* aux, int64_t B, int64_t F, int64_t O,
-                           int accumulate, int act, hipStream_t st, const char* who, bool* done) {
-  *done = false;
+static bool skinny_serves(int64_t B, int64_t F, int64_t O, const float* X, const float* W, const float* dY,
+                          const float* dW) {
   static const bool enabled = [] {
     const char* e = std::getenv("CNHIP_LINEAR_ONE_PASS");
     return !(e && e[0] == '0');
   }();
   const bool o_ok = O == 1 || O == 2 || O == 4 || O == 8 || O == 10 || O == 16;
-  if (!enabled || !o_ok || B % SK_RB != 0 || F % SK_FBLK != 0 || F / SK_FBLK > 65535 ||
-      B * F < ((int64_t)1 << 22) || !dW || !X || !dY || !W)
-    return CNHIP_OK;
+  return enabled && o_ok && B % SK_RB == 0 && F % SK_FBLK == 0 && F / SK_FBLK <= 65535 &&
+         B * F >= ((int64_t)1 << 22) && dW && X && dY && W;
+}
+
+// partials of the one-pass backward: per row chunk [F, O] then [O]
+static size_t skinny_bytes(int64_t B, int64_t F, int64_t O) {
+  return (size_t)((B / SK_RB) * (F * O + O)) * sizeof(float);
+}
+
+int linear_backward_skinny(const float* X, const float* W, const float* dY, float* dW, float* db,
+                           float* dX, const float* aux, int64_t B, int64_t F, int64_t O,
+                           int accumulate, int act, hipStream_t st, const char* who, bool* done) {
+  *done = false;
+  if (!skinny_serves(B, F, O, X, W, dY, dW)) return CNHIP_OK;
   CNHIP_REQUIRE(act >= 0 && act <= 2, "%s: bad activation %d", who, act);
   CNHIP_REQUIRE(act == 0 || (dX && aux), "%s: the activation derivative needs dX and its input", who);
   const int64_t chunks = B / SK_RB, FO = F * O;
   CNHIP_REQUIRE(chunks <= 0x7fffffff, "%s: too large", who);
   void* ws = nullptr;
-  CNHIP_TRY(scratch(st, kScratchGemm, (size_t)(chunks * (FO + O)) * sizeof(float), &ws, who));
+  CNHIP_TRY(scratch(st, kScratchGemm, skinny_bytes(B, F, O), &ws, who));
   float* partial = static_cast<float*>(ws);
   *done = true;
   const bool sep = act != 0 && aux != X;
@@ -290,6 +300,21 @@ int linear_backward_skinny(const float* X, const float* W, const float* dY, floa
   hipLaunchKernelGGL(skinny_reduce_kernel, dim3((unsigned)((FO + O + 255) / 256)), dim3(256), 0, st, partial, dW, db,
                      FO, (int)O, (int)chunks, accumulate);
   return check_launch(who);
+}
+
+// Largest GEMM-slot scratch request that cnhip_linear_backward_act makes for
+// these arguments (its launches run in order on one stream, so one buffer of
+// this size serves them all): the one-pass partials when that path serves
+// the shape, else the split-K partials of the dW GEMM; and those of the dX
+// GEMM unless the one-pass kernel wrote dX (it does for every act but the
+// residual sum).
+size_t linear_backward_act_scratch_bytes(const float* X, const float* W, const float* dY,
+                                         const float* grad_W, const float* dX, int64_t B, int64_t I,
+                                         int64_t O, int trainable, int act) {
+  const bool one_pass = trainable && B > 0 && skinny_serves(B, I, O, X, W, dY, grad_W);
+  size_t need = one_pass ? skinny_bytes(B, I, O) : trainable ? gemm_scratch_bytes(1, 0, I, O, B, 1) : 0;
+  if (dX && !(one_pass && act != CNHIP_ACT_RESIDUAL)) need = std::max(need, gemm_scratch_bytes(0, 1, B, I, O, 1));
+  return need;
 }
 
 int column_sum(const float* in, float* out, int64_t rows, int64_t cols, int accumulate,

@@ -90,7 +90,32 @@ int fill_bytes(void* dst, int value, size_t bytes, hipStream_t stream, const cha
   return check_launch(where);
 }
 
+namespace {
+struct FixedWs {
+  void* p = nullptr;
+  size_t cap = 0;
+};
+thread_local FixedWs t_fixed;
+}  // namespace
+
+FixedScratch::FixedScratch(void* p, size_t cap) { t_fixed = FixedWs{p, cap}; }
+FixedScratch::~FixedScratch() { t_fixed = FixedWs{}; }
+bool fixed_scratch_active() { return t_fixed.p != nullptr; }
+
 int scratch(hipStream_t stream, int slot, size_t bytes, void** ptr, const char* where) {
+  if (t_fixed.p) {
+    if (slot != kScratchGemm) {
+      set_error("%s: scratch slot %d requested inside a no-allocation call", where, slot);
+      return CNHIP_EUNSUPPORTED;
+    }
+    if (bytes > t_fixed.cap) {
+      set_error("%s: needs %zu bytes of workspace; the fixed device workspace holds %zu", where, bytes,
+                t_fixed.cap);
+      return CNHIP_EINVAL;
+    }
+    *ptr = t_fixed.p;
+    return CNHIP_OK;
+  }
   int dev = 0;
   CNHIP_TRY(check_hip(hipGetDevice(&dev), where));
   std::lock_guard<std::mutex> lock(g_scratch_mu);

@@ -84,6 +84,16 @@ def linear_backward_act(X, W, dY, grad_W, grad_b, dX, act_aux, batch: int, in_fe
                ACT[act], _stream())
 
 
+def linear_backward_act_noalloc(X, W, dY, grad_W, grad_b, dX, act_aux, batch: int, in_features: int,
+                                out_features: int, act: str, trainable: bool = True,
+                                accumulate: bool = False) -> None:
+    """linear_backward_act with its workspace in the library's fixed device
+    array (no device allocation); shapes that need more are refused."""
+    _capi.call("cnhip_linear_backward_act_noalloc", _p(X), _p(W), _p(dY), _p(grad_W), _p(grad_b), _p(dX),
+               _p(act_aux), batch, in_features, out_features, int(trainable), int(accumulate),
+               ACT[act], _stream())
+
+
 def column_sum(x, out, rows: int, cols: int, accumulate: bool = False) -> None:
     _capi.call("cnhip_column_sum", _p(x), _p(out), rows, cols, int(accumulate), _stream())
 

@@ -196,6 +196,21 @@ int cnhip_linear_backward_act(const float* X, const float* W, const float* dY,
                               float* grad_W, float* grad_b, float* dX, const float* act_aux,
                               int64_t batch, int64_t in_features, int64_t out_features,
                               int trainable, int accumulate, int act, cnhip_stream_t stream);
+/* cnhip_linear_backward_act for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference.  Same arguments, kernels and
+ * results, bit for bit; it calls no hipMalloc / hipFree and creates no
+ * events.  The kernels' workspace (split-K partials, the one-pass head's
+ * row-chunk partials) is a fixed 32 MiB device array per GPU, looked up on
+ * the first call on each device; a shape that would need more is refused
+ * with CNHIP_EINVAL before anything runs.  Nothing in the workspace has to
+ * start at zero.  Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (two streams, or two host threads) race. */
+int cnhip_linear_backward_act_noalloc(const float* X, const float* W, const float* dY,
+                                      float* grad_W, float* grad_b, float* dX,
+                                      const float* act_aux, int64_t batch, int64_t in_features,
+                                      int64_t out_features, int trainable, int accumulate,
+                                      int act, cnhip_stream_t stream);
 /* out[j] (+)= sum_r in[r + rows*j]   — column sums of a ColMajor [rows,cols]
  * ref: src/CppNet/kernels/gpu/bias_grad.cu:12-46 */
 int cnhip_column_sum(const float* in, float* out, int64_t rows, int64_t cols,

@@ -88,6 +88,13 @@ def test_linear_rejects_bad_shapes():
     st, msg = _status_and_error(lib.cnhip_linear_backward, d, d, d, None, None, None, 4, 2, 3, 1,
                                 1, None)
     assert st == 1 and "grad_W" in msg
+    # the no-allocation variant checks shape and activation before any HIP call
+    st, msg = _status_and_error(lib.cnhip_linear_backward_act_noalloc, d, d, d, d, d, d, None, -1, 2, 3, 1,
+                                0, 0, None)
+    assert st == 1 and "bad shape" in msg
+    st, msg = _status_and_error(lib.cnhip_linear_backward_act_noalloc, d, d, d, d, d, d, None, 4, 2, 3, 1,
+                                0, 9, None)
+    assert st == 1 and "bad activation" in msg
 
 
 def test_ops_refuse_host_tensors():
