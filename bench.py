@@ -407,8 +407,8 @@ def main() -> int:
                             "frac": round(gbs / PEAK_HBM_GBS, 4)})
 
     kernels = {3: "gemm_f32_kernel + conv_pixel/conv_wgrad_kernel (fp32 MFMA, all shapes of the step)",
-               4: "gemm_f32_kernel + lstm_step_fwd/bwd_kernel (fp32 MFMA; the per-timestep recurrent "
-                  "GEMM tiles with the cell update fused)"}.get(
+               4: "gemm_f32_kernel + lstm_fwd/bwd_persist_kernel (fp32 MFMA; the whole recurrence of "
+                  "each pass in one launch, W_hh slices held in registers, cell update fused)"}.get(
         args.config, "gemm_f32_kernel (fp32 MFMA GEMM, all shapes of the step)")
     result = {
         "metric": METRIC,

@@ -62,6 +62,31 @@ struct FixedScratch {
 };
 bool fixed_scratch_active();
 
+// Runs launch(), which enqueues device work on `stream` that must not run
+// at the same time as other such work of this process on the device: the
+// persistent recurrence kernels (a grid that spins until all of its blocks
+// have run a step; two such grids dispatched at once could each be left
+// partly resident) and the replay of a graph that may contain one.  The
+// stream first waits for the device's previous such launch (an event), and
+// an event recorded after launch() marks this one.  Under stream capture
+// nothing is waited for or recorded (graph replays are ordered by
+// cnhip_graph_launch itself).
+int persist_order_enter(hipStream_t stream, const char* who, int* dev);
+int persist_order_leave(hipStream_t stream, int dev, const char* who);
+void persist_order_lock();
+void persist_order_unlock();
+template <class F>
+int persist_ordered(hipStream_t stream, bool capturing, const char* who, F&& launch) {
+  if (capturing) return launch();
+  persist_order_lock();
+  int dev = 0;
+  int st = persist_order_enter(stream, who, &dev);
+  if (st == CNHIP_OK) st = launch();
+  if (st == CNHIP_OK) st = persist_order_leave(stream, dev, who);
+  persist_order_unlock();
+  return st;
+}
+
 // Bytes of GEMM scratch (split-K partials) that gemm_f32_core requests for
 // this shape: 0 when it runs without a split.
 size_t gemm_scratch_bytes(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, int64_t batches);

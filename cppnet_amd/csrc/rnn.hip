@@ -10,10 +10,13 @@
 // The reference computes x_t W_ih and every weight gradient inside its time
 // loop.  Here the parts that do not depend on the recurrence run once over
 // all B*S rows as large MFMA GEMMs:
-//   forward : G = X W_ih (all steps), then per step one launch of
-//             h_{t-1} W_hh with the LSTM cell in its epilogue
-//   backward: per step one launch of dh_t = dY_t + dG_{t+1} W_hh^T with the
-//             cell backward in its epilogue; afterwards dW_ih = X^T dG,
+//   forward : G = X W_ih (all steps), then the recurrence h_{t-1} W_hh with
+//             the LSTM cell fused, all timesteps in one persistent launch
+//             (lstm_fwd_persist_kernel) where the shape suits it, else one
+//             launch per step (lstm_step_fwd_kernel)
+//   backward: dh_t = dY_t + dG_{t+1} W_hh^T with the cell backward fused, in
+//             one persistent launch (lstm_bwd_persist_kernel) or one launch
+//             per step (lstm_step_bwd_kernel); afterwards dW_ih = X^T dG,
 //             dW_hh = Y_{t-1}^T dG, db = colsum dG, dX = dG W_ih^T, each a
 //             single GEMM over all B*S rows.
 // The cell kernels fuse every elementwise gate computation of a step into one
@@ -215,29 +218,47 @@ __global__ void __launch_bounds__(LstmCfg::NT) lstm_step_fwd_kernel(
 }
 
 // ---------------------------------------------------------------- persistent recurrence
-// All timesteps of the LSTM forward in ONE launch.  The grid is the same
-// 32-sample x 8-unit tiling as lstm_step_fwd_kernel (256 blocks at B = 128,
-// H = 512), one block per CU, every block resident for the whole sequence:
-// a block keeps its W_hh slice (H x 32, 64 KB at H = 512) in LDS for all S
-// steps and its units' cell state c in registers, so per step it reads only
-// h_{t-1} of its 32 samples and the step's x W_ih terms.  Between steps the
-// blocks of one sample tile synchronise through a counter: after writing its
-// part of h_t (agent-coherent stores, below) a block adds 1; before step t a
-// block waits until its tile's counter reaches units_tiles * t and then
-// reads h_{t-1} with agent-coherent loads.  Each wave runs exactly the MFMA sequence of the per-step
-// kernel (same k per lane per step, same order) and the four waves' partial
-// tiles are added in the same order, so both paths give identical bits.
+// All timesteps of the LSTM forward, or of its backward through time, in ONE
+// launch.  A per-timestep launch (lstm_step_fwd/bwd_kernel) costs 8-9 us at
+// B 128, H 512: launch ramp, reloading its W_hh slice and h_{t-1} through L2,
+// then ~2 us of MFMA.  Here every block keeps its W_hh slice in registers for
+// the whole sequence and the blocks hand each other the recurrent values
+// directly, which measured ~3 us per step for the hand-over on MI355X.
 //
-// Every wait is bounded: after spin_limit polls a block gives up, sets the
-// launch's fault word (device memory; every waiting block sees it at its
-// next poll and exits) and the host-visible fault word, and returns -- so the
-// grid always drains, even if the blocks were not all resident.  The host
-// reports a set fault word as an error at the next recurrent launch.
-constexpr int kPersistMaxH = 512;  // LDS: W slice + h tile of H x 32 floats each
+// Tiling.  A tile is 16 samples x 16 hidden units, i.e. those units' 4 gate
+// columns (64 columns of W_hh), computed by one block of 4 waves.  The blocks
+// of one sample tile exchange values every step, so all of them run on ONE
+// XCD and exchange through its L2.  The hardware deals a grid's blocks to
+// the 8 XCDs round robin, but from a starting XCD that depends on earlier
+// dispatches, so a block does not take its tile from blockIdx: it reads the
+// XCD it runs on (XCC_ID) and takes the next slot i of that XCD's counter;
+// XCD x then serves the sample tiles x, x + 8, x + 16, ... with H/16 blocks
+// each (tile x + 8 (i / (H/16)), units 16 (i % (H/16))).  grid = 8 (H/16)
+// ceil(nst/8) for nst = B/16 sample tiles gives every XCD as many blocks as
+// it has slots; blocks with a slot past the last sample tile exit.
+//
+// Exchange.  A value handed to another block travels as one 64-bit word
+// (float bits, step stamp) in a double-buffered exchange area zeroed before
+// the launch (stamps start at 1, so a zeroed word never matches).  The
+// writer stores the word; the reader invalidates its CU's L1 (buffer_inv
+// sc0) and loads the words (nontemporal) until each carries the stamp it
+// waits for.  A word is stored and loaded whole, so a value is never taken
+// without its own stamp: a read that comes too early only waits longer.
+// Slot t & 1 is rewritten at step t + 2 only after the writer has read every
+// block's words of step t + 1, which each block wrote after its reads of
+// step t were complete, so no word is overwritten while it may still be read.
+//
+// Every wait is bounded: after spin_limit polls a thread gives up and sets
+// the launch's fault word (which every waiting thread checks while it polls,
+// then exits) and the host-visible one; the next recurrent call reports it.
+// A negative spin limit gives up at once (the tests of the fault path).
+constexpr int kPt = 16;            // samples and hidden units per tile
+constexpr int kPersistMaxH = 512;  // W_hh slice of H x 64 floats: H/4 registers per lane
+typedef unsigned long long u64;
 
 struct PersistSync {
-  unsigned* counters;  // [sample tiles], zeroed before the launch
-  unsigned* fault;     // device word, zeroed before the launch
+  unsigned* fault;       // device word, zeroed before the launch
+  unsigned* xcd_slots;   // [8] per-XCD block counters, zeroed before the launch
   unsigned* fault_host;  // pinned host word, or null
   long long spin_limit;
 };
@@ -247,58 +268,75 @@ __device__ __forceinline__ void persist_fail(const PersistSync& ps) {
   if (ps.fault_host) __hip_atomic_store(ps.fault_host, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
-// Thread 0 of a block: wait until *ctr >= target.  false: gave up (fault).
-__device__ __forceinline__ bool persist_wait(const PersistSync& ps, unsigned* ctr, unsigned target) {
-  if (ps.spin_limit < 0) {  // a negative limit gives up at once (tests of the fault path)
+__device__ __forceinline__ unsigned xcc_id() {
+  return __builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & 0xfu;  // hwreg(HW_REG_XCC_ID, 0, 4)
+}
+
+// The block's sample tile (>= nst when it has none) and unit tile, from the
+// XCD it runs on; false (after raising the fault) when XCC_ID is not 0..7.
+__device__ __forceinline__ bool persist_place(const PersistSync& ps, int nut, int& st, int& ut, int* place) {
+  if (threadIdx.x == 0) {
+    const unsigned x = xcc_id();
+    if (x < 8u) {
+      const int i = (int)__hip_atomic_fetch_add(ps.xcd_slots + x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      place[0] = (int)x + 8 * (i / nut);
+      place[1] = i % nut;
+    } else {
+      place[0] = -1;
+      persist_fail(ps);
+    }
+  }
+  __syncthreads();
+  st = place[0];
+  ut = place[1];
+  return st >= 0;
+}
+
+__device__ __forceinline__ u64 ex_word(float v, unsigned stamp) {
+  return ((u64)stamp << 32) | (u64)__float_as_uint(v);
+}
+__device__ __forceinline__ void ex_store(u64* p, u64 w) {
+  __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));  // (value bits, stamp)
+
+// Raw buffer resource over the exchange area (32-bit byte offsets).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t ex_rsrc(const u64* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<u64*>(base), 0, 0x7fffffff, 0x00020000);
+}
+
+// One thread: w[k] = the word at byte offset voff + soff + k * STRIDE of the
+// exchange area (k < N), once every one of them carries `stamp`.  The
+// k-dependent part of the offset is uniform, so it travels in the load's
+// scalar offset.  false: the launch faulted or this wait gave up.
+template <int N, int STRIDE>
+__device__ __forceinline__ bool ex_wait(const PersistSync& ps, __amdgpu_buffer_rsrc_t rs, unsigned voff,
+                                        unsigned soff, unsigned stamp, u32x2 (&w)[N]) {
+  if (ps.spin_limit < 0) {
     persist_fail(ps);
     return false;
   }
-  // relaxed polls of the agent-coherent counter
+  asm volatile("buffer_inv sc0" ::: "memory");
+#pragma unroll
+  for (int k = 0; k < N; ++k) w[k] = __builtin_amdgcn_raw_buffer_load_b64(rs, voff, soff + k * STRIDE, 2);
   for (long long spins = 0;; ++spins) {
-    if (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= target) return true;
-    if (__hip_atomic_load(ps.fault, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) return false;
+    bool all = true;
+#pragma unroll
+    for (int k = 0; k < N; ++k) all = all && w[k].y == stamp;
+    if (all) return true;
+    if ((spins & 63) == 63 && __hip_atomic_load(ps.fault, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u)
+      return false;
     if (spins >= ps.spin_limit) {
       persist_fail(ps);
       return false;
     }
-    __builtin_amdgcn_s_sleep(2);
-  }
-}
-
-// Values one block hands to the others between steps (h_t forward, dG_t
-// backward) are written and read with agent-coherent accesses: relaxed
-// agent-scope atomic stores write through to the memory level all XCDs
-// share, and relaxed agent-scope atomic loads read from it, so a stale line
-// in an XCD's L2 is never read.  The step counter then needs no fence: a
-// wave's stores have completed (s_waitcnt) before the barrier, and thread 0
-// increments the counter after it; a reader polls the counter, passes the
-// barrier, then loads.  (An agent-scope release/acquire pair would instead
-// write back and invalidate the XCD's whole L2 for every block and step,
-// which measured several times the per-step launches' cost.)
-__device__ __forceinline__ void xstore(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ f32x4 xload4(const float* p) {
-  f32x4 v;
+    __builtin_amdgcn_s_sleep(1);
+    asm volatile("buffer_inv sc0" ::: "memory");
 #pragma unroll
-  for (int e = 0; e < 4; ++e) v[e] = __hip_atomic_load(p + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return v;
-}
-
-// All threads: wait until the tile's counter reaches target (thread 0
-// polls).  Returns false (uniformly) when the launch has faulted.
-__device__ __forceinline__ bool persist_block_wait(const PersistSync& ps, unsigned* ctr, unsigned target,
-                                                   int* flag) {
-  if (threadIdx.x == 0) *flag = persist_wait(ps, ctr, target) ? 1 : 0;
-  __syncthreads();
-  return *flag != 0;
-}
-
-// All threads: each wave's exchanged stores complete, then thread 0 counts.
-__device__ __forceinline__ void persist_block_signal(unsigned* ctr) {
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (threadIdx.x == 0) __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int k = 0; k < N; ++k)
+      if (w[k].y != stamp) w[k] = __builtin_amdgcn_raw_buffer_load_b64(rs, voff, soff + k * STRIDE, 2);
+  }
 }
 
 struct LstmFwdPersistArgs {
@@ -308,120 +346,118 @@ struct LstmFwdPersistArgs {
   float* tanh_c;
   float* Y;
   const float* W_hh;
-  int B, S, H, nbt;
+  u64* ex;  // [2 slots][nst][H][16]: h_t of (unit, sample), stamp t + 1
+  int B, S, nst;
   PersistSync sync;
 };
 
+// Forward, t = 0 .. S-1.  Per step t >= 1 a block waits for h_{t-1} of its
+// 16 samples (all H units, from the H/16 blocks of its sample tile), stages
+// it in LDS, and wave w computes gate w's 16 x 16 recurrent pre-activations
+// (v_mfma_f32_16x16x4f32 over k ascending in blocks of 16: lane (q, r)
+// supplies k = 16 kb + 4 q + e to MFMA (kb, e)); then one thread per
+// (sample, unit) runs the cell exactly as lstm_cell_fwd0_kernel /
+// lstm_step_fwd_kernel do, writes the caches and Y, and hands h_t on.
+template <int H>
 __global__ void __launch_bounds__(256) lstm_fwd_persist_kernel(LstmFwdPersistArgs a) {
-  __shared__ __align__(16) float Ws[kPersistMaxH * 32];  // [k][col], col = gate * 8 + unit
-  __shared__ __align__(16) float hs[kPersistMaxH * 32];  // [k][sample]
-  __shared__ float red[4][32 * 33];                        // per-wave partial tiles, [col][sample]
-  __shared__ int flag;
-  const int H = a.H, B = a.B;
+  constexpr int NKB = H / 16;  // k-blocks; also the words per thread of h_{t-1}
+  constexpr int NUT = H / kPt;
+  __shared__ __align__(16) f32x4 hs[H / 4 * kPt];  // h_{t-1}: [k/4][sample], k..k+3
+  __shared__ float gt[4][kPt][kPt + 1];             // [gate][sample][unit]
+  __shared__ int place[2];
+  int st, ut;
+  if (!persist_place(a.sync, NUT, st, ut, place)) return;
+  if (st >= a.nst) return;
+  const int B = a.B;
   const int64_t BS = (int64_t)B * a.S;
-  const int bt = (int)(blockIdx.x % a.nbt), ut = (int)(blockIdx.x / a.nbt);
-  const int b0 = bt * 32, j0 = ut * kLstmUnits;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  unsigned* ctr = a.sync.counters + bt;
-
-  // the block's W_hh columns gate * H + j0 + unit, k-contiguous in memory
-  for (int idx = tid; idx < H * 8; idx += 256) {  // 32 columns x H/4 float4s
-    const int col = idx / (H / 4), k = (idx % (H / 4)) * 4;
-    const float* src = a.W_hh + k + (int64_t)H * ((col / kLstmUnits) * H + j0 + col % kLstmUnits);
-    const f32x4 v = *reinterpret_cast<const f32x4*>(src);
+  const int q = lane >> 4, r = lane & 15;
+  const int b0 = st * kPt, j0 = ut * kPt;
+  // W_hh(k, column `wave` H + j0 + r) for k = 16 kb + 4 q + e, e = 0..3
+  f32x4 wv[NKB];
+  {
+    const float* wc = a.W_hh + (int64_t)H * ((int64_t)wave * H + j0 + r) + 4 * q;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) Ws[(k + e) * 32 + col] = v[e];
+    for (int kb = 0; kb < NKB; ++kb) wv[kb] = *reinterpret_cast<const f32x4*>(wc + 16 * kb);
   }
-  // thread -> (sample bl, unit u) of the cell update, as lstm_step_fwd_kernel
-  const int bl = tid % 32, u = tid / 32;
-  const int64_t n = b0 + bl, d = j0 + u;
+  // cell thread: sample m, unit u
+  const int m = tid & 15, u = tid >> 4;
+  const int64_t n = b0 + m, d = j0 + u;
+  const float bi = a.bias[d], bf = a.bias[d + H], bg = a.bias[d + 2 * H], bo = a.bias[d + 3 * H];
+  u64* const ex = a.ex + (int64_t)st * H * kPt;
+  const __amdgpu_buffer_rsrc_t rs = ex_rsrc(ex);
+  const unsigned slot_bytes = (unsigned)a.nst * H * kPt * 8u;
+  float xi, xf, xg, xo;  // this step's x W_ih terms (no dependence on the recurrence)
+  {
+    const float* g = a.gates + n;
+    xi = g[BS * d];
+    xf = g[BS * (d + H)];
+    xg = g[BS * (d + 2 * H)];
+    xo = g[BS * (d + 3 * H)];
+  }
   float c_prev = 0.0f;
-  __syncthreads();
-
+  float* hsf = reinterpret_cast<float*>(hs);
   for (int t = 0; t < a.S; ++t) {
     const int64_t row = n + (int64_t)B * t;
-    float* g = a.gates + row;
-    // this step's x W_ih terms do not depend on the recurrence
-    const float xi = g[BS * d], xf = g[BS * (d + H)], xg = g[BS * (d + 2 * H)], xo = g[BS * (d + 3 * H)];
     float ig, fg, gg, og;
     if (t == 0) {  // h_0 = c_0 = 0 (lstm_cell_fwd0_kernel's arithmetic)
-      ig = sigm(xi + a.bias[d]);
-      fg = sigm(xf + a.bias[d + H]);
-      gg = tanhf(xg + a.bias[d + 2 * H]);
-      og = sigm(xo + a.bias[d + 3 * H]);
+      ig = sigm(xi + bi);
+      fg = sigm(xf + bf);
+      gg = tanhf(xg + bg);
+      og = sigm(xo + bo);
     } else {
-      if (!persist_block_wait(a.sync, ctr, (unsigned)(a.H / kLstmUnits) * (unsigned)t, &flag)) return;
-      // h_{t-1} of the tile's 32 samples: hs[k][m] = Y[b0 + m + B (t-1) + BS k].
-      // All of a thread's loads are issued before its LDS stores, so their
-      // latencies overlap (a load-store loop waits for each load in turn).
-      const float* Yp = a.Y + b0 + (int64_t)B * (t - 1);
-      constexpr int kPer = kPersistMaxH * 8 / 256;
-      f32x4 hv[kPer];
+      // h_{t-1}: word (k, s) at [slot (t-1) & 1][k][s]; this thread takes
+      // s = tid % 16, k = tid / 16 + 16 j (byte offset tid 8 + j 2048)
+      u32x2 w[NKB];
+      const bool ok = ex_wait<NKB, 256 * 8>(a.sync, rs, (unsigned)tid * 8u, ((t - 1) & 1) * slot_bytes,
+                                            (unsigned)t, w);
+      if (__syncthreads_or(!ok)) return;
 #pragma unroll
-      for (int j = 0; j < kPer; ++j) {
-        const int idx = tid + 256 * j;
-        if (idx < H * 8) hv[j] = xload4(Yp + (idx & 7) * 4 + BS * (idx >> 3));
-      }
-#pragma unroll
-      for (int j = 0; j < kPer; ++j) {
-        const int idx = tid + 256 * j;
-        if (idx < H * 8) *reinterpret_cast<f32x4*>(hs + (idx >> 3) * 32 + (idx & 7) * 4) = hv[j];
+      for (int j = 0; j < NKB; ++j) {
+        const int k = (tid >> 4) + 16 * j;
+        hsf[((k >> 2) * kPt + m) * 4 + (k & 3)] = __uint_as_float(w[j].x);
       }
       __syncthreads();
-      // wave w: k = kt*64 + 16w + 8h + 4c + e, in lstm_step_fwd_kernel's order
-      kp::f32x16 acc;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
-      const int r32 = lane & 31, hf = lane >> 5;
-      for (int kt = 0; kt < H / 64; ++kt) {
+      for (int kb = 0; kb < NKB; ++kb) {
+        const f32x4 h4 = hs[(4 * kb + q) * kPt + r];
 #pragma unroll
-        for (int c = 0; c < 2; ++c)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int k = kt * 64 + wave * 16 + 8 * hf + 4 * c + e;
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(hs[k * 32 + r32], Ws[k * 32 + r32], acc, 0, 0, 0);
-          }
+        for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(h4[e], wv[kb][e], acc, 0, 0, 0);
       }
-      // partial tile of this wave: lane holds column r32, rows 8(r/4) + 4hf + r%4
+      // acc[i]: gate `wave`, sample 4 q + i, unit r
 #pragma unroll
-      for (int r = 0; r < 16; ++r) red[wave][r32 * 33 + 8 * (r / 4) + 4 * hf + (r % 4)] = acc[r];
+      for (int i = 0; i < 4; ++i) gt[wave][4 * q + i][r] = acc[i];
       __syncthreads();
-      // waves summed in order 0, 1, 2, 3 (reduce_wgk's order)
-      float pre[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int at = (q * kLstmUnits + u) * 33 + bl;
-        pre[q] = ((red[0][at] + red[1][at]) + red[2][at]) + red[3][at];
-      }
-      ig = sigm((pre[0] + xi) + a.bias[d]);
-      fg = sigm((pre[1] + xf) + a.bias[d + H]);
-      gg = tanhf((pre[2] + xg) + a.bias[d + 2 * H]);
-      og = sigm((pre[3] + xo) + a.bias[d + 3 * H]);
+      // as lstm_step_fwd_kernel: (recurrent + x W_ih) + bias
+      ig = sigm((gt[0][m][u] + xi) + bi);
+      fg = sigm((gt[1][m][u] + xf) + bf);
+      gg = tanhf((gt[2][m][u] + xg) + bg);
+      og = sigm((gt[3][m][u] + xo) + bo);
     }
-    const float ct = lstm_cell_c(fg, t == 0 ? 0.0f : c_prev, ig, gg);
+    const float ct = lstm_cell_c(fg, c_prev, ig, gg);
     const float tc = tanhf(ct);
+    const float h = og * tc;
+    if (t + 1 < a.S)
+      ex_store(ex + (int64_t)(t & 1) * (slot_bytes / 8) + (int64_t)d * kPt + m, ex_word(h, (unsigned)(t + 1)));
+    float* g = a.gates + row;
     g[BS * d] = ig;
     g[BS * (d + H)] = fg;
     g[BS * (d + 2 * H)] = gg;
     g[BS * (d + 3 * H)] = og;
     a.c[row + BS * d] = ct;
     a.tanh_c[row + BS * d] = tc;
-    xstore(a.Y + row + BS * d, og * tc);
+    a.Y[row + BS * d] = h;
     c_prev = ct;
-    if (t + 1 < a.S) persist_block_signal(ctr);
+    if (t + 1 < a.S) {
+      const float* gn = g + B;
+      xi = gn[BS * d];
+      xf = gn[BS * (d + H)];
+      xg = gn[BS * (d + 2 * H)];
+      xo = gn[BS * (d + 3 * H)];
+    }
   }
 }
-
-// All backward timesteps (t = S-1 .. 0) in ONE launch, the tiling of
-// lstm_step_bwd_kernel (16 samples x 16 units, 8 waves, 256 blocks at
-// B = 128, H = 512).  A block keeps its slice of W_hh^T (16 units x 4H) in
-// registers -- wave w only ever needs the k of its own slices, 64 values per
-// lane -- and its units' dc in registers; per step it stages dG_{t+1} of its
-// 16 samples (16 x 4H, [sample][k] in LDS) and runs the per-step kernel's
-// MFMA sequence and 8-way reduction, then the cell backward.  Blocks of one
-// sample tile synchronise as in lstm_fwd_persist_kernel.
-constexpr int kPersistBwdMaxG = 2048;  // 4H <= 2048
-constexpr int kPersistBwdLd = kPersistBwdMaxG + 4;
 
 struct LstmBwdPersistArgs {
   const float* gates;
@@ -430,111 +466,108 @@ struct LstmBwdPersistArgs {
   const float* dY;
   const float* W_hh;
   float* dG;
-  int B, S, H, nbt;
+  u64* ex;  // [2 slots][nst][H/16 writers][H][16]: partial dG_t W_hh^T, stamp t + 1
+  int B, S, nst;
   PersistSync sync;
 };
 
-__global__ void __launch_bounds__(512) lstm_bwd_persist_kernel(LstmBwdPersistArgs a) {
-  __shared__ __align__(16) float As[16 * kPersistBwdLd];  // dG_{t+1}: [sample][k]
-  __shared__ float red[7][4 * 64];                         // partials of waves 1..7
-  __shared__ float tile[16 * 17];                          // [unit][sample]
-  __shared__ int flag;
-  const int H = a.H, B = a.B, G = 4 * H;
-  const int64_t BS = (int64_t)B * a.S;
-  const int bt = (int)(blockIdx.x % a.nbt), ut = (int)(blockIdx.x / a.nbt);
-  const int b0 = bt * 16, j0 = ut * 16;
+// Backward through time, t = S-1 .. 0.  The recurrent term dG_{t+1} W_hh^T
+// is split by columns of W_hh: the block that computed dG_t for its 16
+// units (64 columns) multiplies it by its W_hh columns for ALL H units
+// (16 x H partial products, K = 64: wave w takes H/64 output tiles, MFMA
+// (kb, e) over local column 16 kb + 4 q + e, i.e. gate kb), and hands them
+// on; at step t-1 each block adds, for its units, the H/16 partials of its
+// sample tile in block order.  Each block only multiplies its own dG, and
+// exchanges 16 x 16 words per partner per step.  The cell backward is
+// lstm_cell_bwd_last_kernel's at t = S-1 and lstm_step_bwd_kernel's after.
+template <int H>
+__global__ void __launch_bounds__(256) lstm_bwd_persist_kernel(LstmBwdPersistArgs a) {
+  constexpr int NUT = H / kPt;  // blocks (writers) per sample tile
+  constexpr int TPW = H / 64;   // output tiles of 16 units per wave
+  __shared__ __align__(16) f32x4 dgs[64 / 4 * kPt];  // dG_t of the 64 columns: [c/4][sample]
+  __shared__ int place[2];
+  int st, ut;
+  if (!persist_place(a.sync, NUT, st, ut, place)) return;
+  if (st >= a.nst) return;
+  const int B = a.B, S = a.S;
+  const int64_t BS = (int64_t)B * S;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int q = lane >> 4, r16 = lane & 15;
-  unsigned* ctr = a.sync.counters + bt;
-  const int nkt = G / 256;  // k-tiles of 256 (G % 256 == 0)
-
-  // W_hh^T(j, k) = W_hh[j + H k] for this lane's unit j0 + r16 and the k of
-  // its MFMA steps: k = kt*256 + 32*wave + 16c + 4q + e
-  constexpr int kMaxKt = kPersistBwdMaxG / 256;
-  float wv[kMaxKt * 8];  // unrolled loops below: register-indexed only
+  const int q = lane >> 4, r = lane & 15;
+  const int b0 = st * kPt, j0 = ut * kPt;
+  // W_hh(unit 16 (wave TPW + tt) + r, column kb H + j0 + 4 q + e)
+  f32x4 wv[TPW][4];
 #pragma unroll
-  for (int kt = 0; kt < kMaxKt; ++kt)
+  for (int tt = 0; tt < TPW; ++tt)
 #pragma unroll
-    for (int c = 0; c < 2; ++c)
+    for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int k = kt * 256 + 32 * wave + 16 * c + 4 * q + e;
-        wv[(kt * 2 + c) * 4 + e] = kt < nkt ? a.W_hh[(j0 + r16) + (int64_t)H * k] : 0.0f;
-      }
-  // thread -> (sample bl, unit jl) of the cell backward (threads 0..255)
-  const int bl = tid % 16, jl = tid / 16;
-  const bool cell = tid < 256;
-  const int64_t n = b0 + bl, d = j0 + jl;
-  float dc_next = 0.0f;
-
-  for (int t = a.S - 1; t >= 0; --t) {
+      for (int e = 0; e < 4; ++e)
+        wv[tt][kb][e] = a.W_hh[(16 * (wave * TPW + tt) + r) + (int64_t)H * ((int64_t)kb * H + j0 + 4 * q + e)];
+  // cell thread: sample m, unit u
+  const int m = tid & 15, u = tid >> 4;
+  const int64_t n = b0 + m, d = j0 + u;
+  u64* const ex = a.ex + (int64_t)st * NUT * H * kPt;  // + writer * H * 16
+  const __amdgpu_buffer_rsrc_t rs = ex_rsrc(ex);
+  const unsigned slot_bytes = (unsigned)a.nst * NUT * H * kPt * 8u;
+  float* dgsf = reinterpret_cast<float*>(dgs);
+  // operands of step t (no dependence on the recurrence), loaded a step ahead
+  float ig, fg, gg, og, tc, cprev, dy;
+  auto load_step = [&](int t) {
     const int64_t row = n + (int64_t)B * t;
-    float rec = 0.0f;  // dG_{t+1} W_hh^T for (n, d)
-    if (t < a.S - 1) {
-      if (!persist_block_wait(a.sync, ctr, (unsigned)(H / 16) * (unsigned)(a.S - 1 - t), &flag)) return;
-      // As[m][k] = dG[b0 + m + B (t+1) + BS k]
-      // (loads first, then the LDS stores, as in the forward kernel)
-      const float* src = a.dG + b0 + (int64_t)B * (t + 1);
-      constexpr int kPer = kPersistBwdMaxG * 4 / 512;
-      f32x4 gv[kPer];
+    ig = a.gates[row + BS * d];
+    fg = a.gates[row + BS * (d + H)];
+    gg = a.gates[row + BS * (d + 2 * H)];
+    og = a.gates[row + BS * (d + 3 * H)];
+    tc = a.tanh_c[row + BS * d];
+    cprev = t > 0 ? a.c[row - B + BS * d] : 0.0f;
+    dy = a.dY[row + BS * d];
+  };
+  load_step(S - 1);
+  float dc_next = 0.0f;
+  for (int t = S - 1; t >= 0; --t) {
+    const int64_t row = n + (int64_t)B * t;
+    float dh = dy;
+    if (t < S - 1) {
+      // partials of step t+1: writer w's word (d, m) at [slot (t+1) & 1][w][d][m], stamp t + 2
+      u32x2 w[NUT];
+      const bool ok = ex_wait<NUT, H * kPt * 8>(a.sync, rs, (unsigned)(d * kPt + m) * 8u,
+                                               ((t + 1) & 1) * slot_bytes, (unsigned)(t + 2), w);
+      if (__syncthreads_or(!ok)) return;
+      float rec = 0.0f;
 #pragma unroll
-      for (int j = 0; j < kPer; ++j) {
-        const int idx = tid + 512 * j;
-        if (idx < G * 4) gv[j] = xload4(src + (idx & 3) * 4 + BS * (idx >> 2));
-      }
+      for (int k = 0; k < NUT; ++k) rec += __uint_as_float(w[k].x);
+      dh = dy + rec;
+    }
+    float di, df, dgg, dout;
+    lstm_cell_bwd(ig, fg, gg, og, tc, dh, t == S - 1 ? 0.0f : dc_next, cprev, di, df, dgg, dout, dc_next);
+    a.dG[row + BS * d] = di;
+    a.dG[row + BS * (d + H)] = df;
+    a.dG[row + BS * (d + 2 * H)] = dgg;
+    a.dG[row + BS * (d + 3 * H)] = dout;
+    if (t == 0) break;
+    // local column gate * 16 + u at dgs[(col / 4) * 16 + m][col % 4]
+    dgsf[(((0 * 16 + u) >> 2) * kPt + m) * 4 + (u & 3)] = di;
+    dgsf[(((1 * 16 + u) >> 2) * kPt + m) * 4 + (u & 3)] = df;
+    dgsf[(((2 * 16 + u) >> 2) * kPt + m) * 4 + (u & 3)] = dgg;
+    dgsf[(((3 * 16 + u) >> 2) * kPt + m) * 4 + (u & 3)] = dout;
+    load_step(t - 1);
+    __syncthreads();
+    u64* dst = ex + (int64_t)(t & 1) * (slot_bytes / 8) + (int64_t)ut * H * kPt;
 #pragma unroll
-      for (int j = 0; j < kPer; ++j) {
-        const int idx = tid + 512 * j;
-        if (idx < G * 4) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) As[((idx & 3) * 4 + e) * kPersistBwdLd + (idx >> 2)] = gv[j][e];
-        }
-      }
-      __syncthreads();
+    for (int tt = 0; tt < TPW; ++tt) {
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kt = 0; kt < kMaxKt; ++kt)
-        if (kt < nkt)
+      for (int kb = 0; kb < 4; ++kb) {
+        const f32x4 g4 = dgs[(4 * kb + q) * kPt + r];
 #pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          const int k = kt * 256 + 32 * wave + 16 * c + 4 * q;
-          const f32x4 av = *reinterpret_cast<const f32x4*>(As + r16 * kPersistBwdLd + k);
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[e], wv[(kt * 2 + c) * 4 + e], acc, 0, 0, 0);
-        }
-      // waves 1..7 hand their partials to wave 0, which adds them in order
-      if (wave > 0) {
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) red[wave - 1][rr * 64 + lane] = acc[rr];
+        for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(g4[e], wv[tt][kb][e], acc, 0, 0, 0);
       }
-      __syncthreads();
-      if (wave == 0) {
-        for (int g = 0; g < 7; ++g)
+      // acc[i]: sample 4 q + i, unit 16 (wave TPW + tt) + r
+      u64* o = dst + (int64_t)(16 * (wave * TPW + tt) + r) * kPt + 4 * q;
 #pragma unroll
-          for (int rr = 0; rr < 4; ++rr) acc[rr] += red[g][rr * 64 + lane];
-        // lane holds unit column r16 and samples 4q + rr
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) tile[(4 * q + rr) + 17 * r16] = acc[rr];
-      }
-      __syncthreads();
-      if (cell) rec = tile[bl + 17 * jl];
+      for (int i = 0; i < 4; ++i) ex_store(o + i, ex_word(acc[i], (unsigned)(t + 1)));
     }
-    if (cell) {
-      const float ig = a.gates[row + BS * d], fg = a.gates[row + BS * (d + H)];
-      const float gg = a.gates[row + BS * (d + 2 * H)], og = a.gates[row + BS * (d + 3 * H)];
-      const float tc = a.tanh_c[row + BS * d];
-      // the last step (lstm_cell_bwd_last_kernel) has no later step: dh = dY, dc_in = 0
-      const float dh = t == a.S - 1 ? a.dY[row + BS * d] : a.dY[row + BS * d] + rec;
-      const float cprev = t > 0 ? a.c[row - B + BS * d] : 0.0f;
-      float di, df, dgg, dout;
-      lstm_cell_bwd(ig, fg, gg, og, tc, dh, t == a.S - 1 ? 0.0f : dc_next, cprev, di, df, dgg, dout, dc_next);
-      xstore(a.dG + row + BS * d, di);
-      xstore(a.dG + row + BS * (d + H), df);
-      xstore(a.dG + row + BS * (d + 2 * H), dgg);
-      xstore(a.dG + row + BS * (d + 3 * H), dout);
-    }
-    if (t > 0) persist_block_signal(ctr);
+    // dgs is rewritten at the next step only after the wait's block-wide vote
   }
 }
 
@@ -817,7 +850,7 @@ int lstm_bwd_steps(const float* gates, const float* c, const float* tanh_c, cons
 }
 
 // ---- persistent-launch plumbing
-constexpr int kScratchRecur = 2;  // scratch slot of the counters and fault word
+constexpr int kScratchRecur = 2;  // scratch slot of the fault word and the exchange area
 
 // Pinned host fault word per device (the kernels set it when a wait gives up).
 unsigned* fault_host_word(int dev) {
@@ -856,16 +889,13 @@ long long persist_spin_limit() {
   return e ? std::atoll(e) : (1LL << 20);
 }
 
-// The persistent kernels run only with CNHIP_RECURRENCE_PERSISTENT=1: on the
-// MI355X they measure slower than the per-step launches (C4 shape: 0.85 ms
-// forward and 1.6 ms backward against 0.55 and 0.89 ms), because every step
-// re-reads each sample tile's h_{t-1} (or dG_{t+1}) from the memory level
-// all XCDs share -- the per-XCD L2s are not coherent with each other within
-// a launch -- where the per-step kernels read it through L2.  Both paths
-// compute the same bits.
+// The persistent recurrence is the default wherever the shape suits it;
+// CNHIP_RECURRENCE_PERSISTENT=0 keeps the per-step launches (which compute
+// the recurrent products in another summation order, so the two paths agree
+// to rounding, not bit for bit).
 bool persist_enabled() {
   const char* e = std::getenv("CNHIP_RECURRENCE_PERSISTENT");
-  return e && e[0] == '1';
+  return !(e && e[0] == '0');
 }
 
 // Whether `grid` blocks of `kernel` (`threads` threads) can all be resident.
@@ -903,30 +933,77 @@ bool persist_fits(const void* kernel, int64_t grid, int threads, const char* who
   return capacity > 0 && grid <= capacity;
 }
 
-// Zeroes the counters and fault word, then launches `kernel` with one
-// argument (cooperatively; a plain launch of the same kernel while the
-// stream is being captured into a graph).
+// Whether the persistent kernels are launched cooperatively
+// (CNHIP_RECURRENCE_COOPERATIVE=1: the runtime then guarantees every block
+// resident, or refuses the launch).  By default they are launched plainly,
+// as under graph capture: on this ROCm a cooperative launch costs ~23 us
+// more per launch (C4: 1.226 vs 1.180 ms per step) and rocprofv3 cannot
+// trace it (it crashes at exit without writing its results).  The grid is
+// within the device's resident capacity (persist_fits), and this process's
+// persistent launches (and graph replays) are ordered one after another
+// (persist_ordered), so no two such grids share the device; other work
+// holding CUs drains by itself while the blocks already running wait
+// (bounded), and a wait that gives up is reported as an error, never a hang.
+bool persist_cooperative() {
+  const char* e = std::getenv("CNHIP_RECURRENCE_COOPERATIVE");
+  return e && e[0] == '1';
+}
+
+// Zeroes the fault word, the XCD slot counters and the exchange area
+// (ex_bytes, after a 256-byte header), then launches
+// `kernel` with one argument (cooperatively only when asked to above, and
+// never while the stream is being captured into a graph).
 template <class Args>
-int persist_launch(const void* kernel, int64_t grid, int threads, Args& args, int tiles, hipStream_t st,
+int persist_launch(const void* kernel, int64_t grid, int threads, Args& args, size_t ex_bytes, hipStream_t st,
                    const char* who) {
   void* ws = nullptr;
-  const size_t bytes = (size_t)(tiles + 1) * sizeof(unsigned);
+  const size_t bytes = 256 + ex_bytes;
   CNHIP_TRY(scratch(st, kScratchRecur, bytes, &ws, who));
   CNHIP_TRY(fill_bytes(ws, 0, bytes, st, who));
   int dev = 0;
   CNHIP_TRY(check_hip(hipGetDevice(&dev), who));
-  args.sync.counters = static_cast<unsigned*>(ws);
-  args.sync.fault = static_cast<unsigned*>(ws) + tiles;
+  args.sync.fault = static_cast<unsigned*>(ws);
+  args.sync.xcd_slots = static_cast<unsigned*>(ws) + 16;
   args.sync.fault_host = fault_host_word(dev);
   args.sync.spin_limit = persist_spin_limit();
+  args.ex = reinterpret_cast<u64*>(static_cast<char*>(ws) + 256);
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
   CNHIP_TRY(check_hip(hipStreamIsCapturing(st, &cs), who));
+  const bool capturing = cs != hipStreamCaptureStatusNone;
   void* params[] = {&args};
-  if (cs == hipStreamCaptureStatusNone)
-    CNHIP_TRY(check_hip(hipLaunchCooperativeKernel(kernel, dim3((unsigned)grid), dim3(threads), params, 0, st), who));
-  else
-    CNHIP_TRY(check_hip(hipLaunchKernel(kernel, dim3((unsigned)grid), dim3(threads), params, 0, st), who));
-  return check_launch(who);
+  return persist_ordered(st, capturing, who, [&] {
+    if (!capturing && persist_cooperative())
+      CNHIP_TRY(check_hip(hipLaunchCooperativeKernel(kernel, dim3((unsigned)grid), dim3(threads), params, 0, st), who));
+    else
+      CNHIP_TRY(check_hip(hipLaunchKernel(kernel, dim3((unsigned)grid), dim3(threads), params, 0, st), who));
+    return check_launch(who);
+  });
+}
+
+// Shapes the persistent kernels take: 16-sample tiles, H a multiple of 64
+// up to kPersistMaxH, 32-bit row indices.  grid = 8 (H/16) ceil(nst/8).
+bool persist_shape(int64_t B, int64_t S, int64_t H, int64_t& nst, int64_t& nut, int64_t& grid) {
+  if (B % kPt != 0 || H % 64 != 0 || H > kPersistMaxH || S < 2 || B * S * 4 * H > INT32_MAX) return false;
+  nst = B / kPt;
+  nut = H / kPt;
+  grid = 8 * nut * ((nst + 7) / 8);
+  return true;
+}
+
+template <int H>
+const void* fwd_persist_kernel() { return reinterpret_cast<const void*>(&lstm_fwd_persist_kernel<H>); }
+template <int H>
+const void* bwd_persist_kernel() { return reinterpret_cast<const void*>(&lstm_bwd_persist_kernel<H>); }
+
+// The instantiated hidden sizes (W_hh slice of H/4 registers per lane).
+const void* persist_kernel(bool fwd, int64_t H) {
+  switch (H) {
+    case 64: return fwd ? fwd_persist_kernel<64>() : bwd_persist_kernel<64>();
+    case 128: return fwd ? fwd_persist_kernel<128>() : bwd_persist_kernel<128>();
+    case 256: return fwd ? fwd_persist_kernel<256>() : bwd_persist_kernel<256>();
+    case 512: return fwd ? fwd_persist_kernel<512>() : bwd_persist_kernel<512>();
+    default: return nullptr;
+  }
 }
 
 // The whole BPTT recurrence in one persistent launch when the shape suits
@@ -935,16 +1012,15 @@ int lstm_bwd_persistent(const float* gates, const float* c, const float* tanh_c,
                         const float* W_hh, float* dG, int64_t B, int64_t S, int64_t H, hipStream_t st,
                         const char* who, bool* done) {
   *done = false;
-  if (!persist_enabled() || B % 16 != 0 || H % 64 != 0 || 4 * H > kPersistBwdMaxG || (B * S) % 4 != 0 ||
-      !aligned16(dG) || B * S > INT32_MAX)
-    return CNHIP_OK;
-  const int64_t nbt = B / 16, grid = nbt * (H / 16);
-  const void* kern = reinterpret_cast<const void*>(&lstm_bwd_persist_kernel);
-  if (!persist_fits(kern, grid, 512, who)) return CNHIP_OK;
-  LstmBwdPersistArgs args{gates, c, tanh_c, dY, W_hh, dG, (int)B, (int)S, (int)H, (int)nbt, {}};
+  int64_t nst, nut, grid;
+  const void* kern = persist_kernel(false, H);
+  if (!persist_enabled() || !kern || !persist_shape(B, S, H, nst, nut, grid)) return CNHIP_OK;
+  const size_t ex_bytes = (size_t)2 * nst * nut * H * kPt * sizeof(u64);
+  if (ex_bytes > 0x7fffffffu || !persist_fits(kern, grid, 256, who)) return CNHIP_OK;
+  LstmBwdPersistArgs args{gates, c, tanh_c, dY, W_hh, dG, nullptr, (int)B, (int)S, (int)nst, {}};
   TimingRec* rec = timing_slot(2.0 * B * 4 * H * H * (double)(S - 1));
   if (rec) (void)hipEventRecord(rec->start, st);
-  CNHIP_TRY(persist_launch(kern, grid, 512, args, (int)nbt, st, who));
+  CNHIP_TRY(persist_launch(kern, grid, 256, args, ex_bytes, st, who));
   if (rec) (void)hipEventRecord(rec->stop, st);
   *done = true;
   return CNHIP_OK;
@@ -955,16 +1031,15 @@ int lstm_bwd_persistent(const float* gates, const float* c, const float* tanh_c,
 int lstm_fwd_persistent(float* gates, const float* b, float* c, float* tanh_c, float* Y, const float* W_hh,
                         int64_t B, int64_t S, int64_t H, hipStream_t st, const char* who, bool* done) {
   *done = false;
-  if (!persist_enabled() || B % 32 != 0 || H % 64 != 0 || H > kPersistMaxH || (B * S) % 4 != 0 ||
-      !aligned16(Y) || !aligned16(W_hh) || B * S > INT32_MAX)
-    return CNHIP_OK;
-  const int64_t nbt = B / 32, grid = nbt * (H / kLstmUnits);
-  const void* kern = reinterpret_cast<const void*>(&lstm_fwd_persist_kernel);
-  if (!persist_fits(kern, grid, 256, who)) return CNHIP_OK;
-  LstmFwdPersistArgs args{gates, b, c, tanh_c, Y, W_hh, (int)B, (int)S, (int)H, (int)nbt, {}};
+  int64_t nst, nut, grid;
+  const void* kern = persist_kernel(true, H);
+  if (!persist_enabled() || !kern || !persist_shape(B, S, H, nst, nut, grid) || !aligned16(W_hh)) return CNHIP_OK;
+  const size_t ex_bytes = (size_t)2 * nst * H * kPt * sizeof(u64);
+  if (ex_bytes > 0x7fffffffu || !persist_fits(kern, grid, 256, who)) return CNHIP_OK;
+  LstmFwdPersistArgs args{gates, b, c, tanh_c, Y, W_hh, nullptr, (int)B, (int)S, (int)nst, {}};
   TimingRec* rec = timing_slot(2.0 * B * 4 * H * H * (double)(S - 1));
   if (rec) (void)hipEventRecord(rec->start, st);
-  CNHIP_TRY(persist_launch(kern, grid, 256, args, (int)nbt, st, who));
+  CNHIP_TRY(persist_launch(kern, grid, 256, args, ex_bytes, st, who));
   if (rec) (void)hipEventRecord(rec->stop, st);
   *done = true;
   return CNHIP_OK;

@@ -102,6 +102,34 @@ FixedScratch::FixedScratch(void* p, size_t cap) { t_fixed = FixedWs{p, cap}; }
 FixedScratch::~FixedScratch() { t_fixed = FixedWs{}; }
 bool fixed_scratch_active() { return t_fixed.p != nullptr; }
 
+namespace {
+std::mutex g_persist_mu;
+struct PersistOrder {
+  hipEvent_t ev = nullptr;
+  bool recorded = false;
+};
+PersistOrder g_persist_order[64];  // per device
+}  // namespace
+
+void persist_order_lock() { g_persist_mu.lock(); }
+void persist_order_unlock() { g_persist_mu.unlock(); }
+
+int persist_order_enter(hipStream_t stream, const char* who, int* dev) {
+  CNHIP_TRY(check_hip(hipGetDevice(dev), who));
+  CNHIP_REQUIRE(*dev >= 0 && *dev < 64, "%s: device %d is beyond the 64 supported", who, *dev);
+  PersistOrder& o = g_persist_order[*dev];
+  if (o.recorded) CNHIP_TRY(check_hip(hipStreamWaitEvent(stream, o.ev, 0), who));
+  return CNHIP_OK;
+}
+
+int persist_order_leave(hipStream_t stream, int dev, const char* who) {
+  PersistOrder& o = g_persist_order[dev];
+  if (!o.ev) CNHIP_TRY(check_hip(hipEventCreateWithFlags(&o.ev, hipEventDisableTiming), who));
+  CNHIP_TRY(check_hip(hipEventRecord(o.ev, stream), who));
+  o.recorded = true;
+  return CNHIP_OK;
+}
+
 int scratch(hipStream_t stream, int slot, size_t bytes, void** ptr, const char* where) {
   if (t_fixed.p) {
     if (slot != kScratchGemm) {
@@ -348,7 +376,11 @@ int cnhip_graph_launch(cnhip_graph_t graph, cnhip_stream_t stream) {
   CNHIP_REQUIRE(as_stream(stream) == G->stream,
                 "cnhip_graph_launch: a graph replays on the stream it was captured on (its scratch "
                 "slots are that stream's)");
-  return check_hip(hipGraphLaunch(G->exec, as_stream(stream)), "cnhip_graph_launch");
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  CNHIP_TRY(check_hip(hipStreamIsCapturing(as_stream(stream), &cs), "cnhip_graph_launch"));
+  return cnhip::persist_ordered(as_stream(stream), cs != hipStreamCaptureStatusNone, "cnhip_graph_launch", [&] {
+    return check_hip(hipGraphLaunch(G->exec, as_stream(stream)), "cnhip_graph_launch");
+  });
 }
 
 int cnhip_graph_destroy(cnhip_graph_t graph) {
