@@ -119,7 +119,7 @@ CPU_BATCH = {1: 512, 2: 512, 3: 32, 4: 16, 5: 4}
 # PMC runs (FETCH_SIZE, WRITE_SIZE) scaled by a reference kernel of known
 # traffic; the runs, factors and per-GEMM table are in
 # profiles/gemm_f32_config2_traffic.md.  Configs not yet measured report null.
-PMC_TRAFFIC_BYTES = {2: 321.0e6}
+PMC_TRAFFIC_BYTES = {2: 388.4e6}
 
 
 def _cpu_model() -> str:
