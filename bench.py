@@ -123,14 +123,22 @@ PMC_TRAFFIC_BYTES = {2: 388.4e6}
 
 
 def _cpu_model() -> str:
+    """The host's "model name" from /proc/cpuinfo with its family, model and
+    stepping numbers (some hosts report only a family name such as "AMD EPYC")."""
+    info = {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                if ":" in line:
+                    k, v = (x.strip() for x in line.split(":", 1))
+                    info.setdefault(k, v)
+                if not line.strip() and info:
+                    break
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    name = info.get("model name", "unknown")
+    ids = [f"{k} {info[k]}" for k in ("cpu family", "model", "stepping") if k in info]
+    return f"{name} ({', '.join(ids)})" if ids else name
 
 
 def _cpu_share() -> int:
