@@ -571,10 +571,16 @@ Plan plan_gemm(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, int64_
     } else if (ts >= 512) {
       shape = Shape::S;
     } else {
-      const int64_t sm = std::min<int64_t>({(512 + tm - 1) / tm, 16, max_s});
+      // too few tiles to fill the chip: split K.  The 128 x 128 tile's split
+      // count (<= 16) is the one with the lowest dispatch-round cost: a count
+      // that leaves some CUs a block more than the others costs that block's
+      // whole duration (11 splits of 48 tiles, 528 blocks, ran at 82 TFLOP/s
+      // where 10 splits, 480 blocks, run at 92)
+      int sm = 1;
+      split_cost(Shape::M, tm / batches, M, N, K, batches, (int)std::min<int64_t>(16, max_s), true, sm);
       if (tm * sm >= 256) {
         shape = Shape::M;
-        splits = (int)sm;
+        splits = sm;
       } else {
         shape = Shape::S;
         splits = (int)std::min<int64_t>((512 + ts - 1) / ts, max_s);

@@ -121,7 +121,7 @@ def test_100_steps_full_width(gpu, oracle_mt, name):
         lg[step], lo[step] = sess.step(), ref.step(X, Y)
         if step % 20 == 19:
             _report(config=name, step=step + 1, loss_gpu=lg[step], loss_oracle=lo[step],
-                    worst_loss_rel=float((np.abs(lg - lo) / np.abs(lo))[:step + 1].max()),
+                    worst_loss_rel=float((np.abs(lg[:step + 1] - lo[:step + 1]) / np.abs(lo[:step + 1])).max()),
                     seconds=round(time.time() - t0, 1))
     got, want = sess.get_params(), ref.get_params()
     sess.close()
