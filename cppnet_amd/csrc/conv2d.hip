@@ -195,6 +195,99 @@ __global__ void __launch_bounds__(C::NT) conv_pixel_kernel(ConvArgs a) {
   });
 }
 
+// ------------------------------------------------------- short-contraction forward
+// Forward of a convolution whose contraction is short (C KS^2 <= 32, such as
+// an RGB input layer's 27): 2 C KS^2 flops per output against the 4 bytes of
+// writing it, so the layer is bound by writing Y, and the per-pixel MFMA
+// tile above spends its time staging two k-tiles through LDS.  Here the
+// operands go straight from memory into MFMA registers: a block takes one
+// output pixel and 256 samples, each of its 4 waves 64 samples x all output
+// channels in chunks of 32, over k-steps of 4 taps (v_mfma_f32_16x16x4f32;
+// taps past C KS^2 and padded taps are 0).  The weights are the row operand
+// (16 channels per row tile) and X the column operand: column tile nt holds
+// samples n0 + 4 r + nt (r = 0..15), so a lane loads its four column tiles'
+// operands at one tap as one float4 of X, and an output row (one channel)
+// comes back as float4s of 4 consecutive samples, lanes r = 0..15 covering
+// 256 contiguous bytes: every store instruction writes whole cache lines.
+// Taps are summed in ascending k = ic + C (kh + KS kw), then the bias is
+// added, then the ReLU, as in the MFMA epilogue.  The grid is 2 blocks per
+// CU (512 blocks of 256 samples), each looping over every gridDim.x-th
+// pixel: one block per pixel (1024 at config 3, 3 resident per CU) had left
+// the last third of the CUs' slots a whole extra round.
+constexpr int kDirectMaxK = 32;
+
+__global__ void __launch_bounds__(256) conv_direct_fwd_kernel(ConvArgs a) {
+  const ConvDims& d = a.d;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int q = lane >> 4, r = lane & 15;
+  const int K = (int)(d.C * d.KS * d.KS), OC = (int)d.OC, npix = (int)(d.HO * d.WO);
+  __shared__ int off[kDirectMaxK];  // element offset of X(0, tap k), or -1 (padding, k >= K)
+  const int64_t n0 = (int64_t)blockIdx.y * 256 + 64 * wave;  // N % 64 == 0
+  // the grid holds as many blocks as the CUs run at once; each takes every
+  // gridDim.x-th pixel, so every CU gets the same number of pixels
+  for (int pix = (int)blockIdx.x; pix < npix; pix += (int)gridDim.x) {
+    // 32-bit index arithmetic (the host checks that X's offsets fit): 64-bit
+    // division has no instruction and expands into long sequences
+    const int oh = pix % (int)d.HO, ow = pix / (int)d.HO;
+    __syncthreads();  // the previous pixel's offsets have been read
+    if (threadIdx.x < kDirectMaxK)
+      off[threadIdx.x] = (int)threadIdx.x < K ? gather_off<false, int>(d, oh, ow, (int)threadIdx.x) : -1;
+    __syncthreads();
+    if (n0 >= d.N) continue;
+    f32x4 xv[kDirectMaxK / 4];  // X(n0 + 4 r .. 4 r + 3, tap 4 ks + q)
+#pragma unroll
+    for (int ks = 0; ks < kDirectMaxK / 4; ++ks) {
+      const int o = off[4 * ks + q];
+      xv[ks] = o >= 0 ? *reinterpret_cast<const f32x4*>(a.src + o + n0 + 4 * r) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    const int nks = (K + 3) / 4;
+    for (int oc0 = 0; oc0 < OC; oc0 += 32) {
+      float wv[2][kDirectMaxK / 4];  // W(oc0 + 16 mt + r, tap 4 ks + q)
+#pragma unroll
+      for (int ks = 0; ks < kDirectMaxK / 4; ++ks)
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+          const int k = 4 * ks + q;
+          wv[mt][ks] = k < K ? a.wt[oc0 + 16 * mt + r + (int64_t)OC * k] : 0.f;
+        }
+      f32x4 acc[2][4];
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < kDirectMaxK / 4; ++ks)
+        if (ks < nks) {
+#pragma unroll
+          for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < 4; ++nt)
+              acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(wv[mt][ks], xv[ks][nt], acc[mt][nt], 0, 0, 0);
+        }
+      // acc[mt][nt][i]: channel oc0 + 16 mt + 4 q + i, sample n0 + 4 r + nt
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int64_t oc = oc0 + 16 * mt + 4 * q + i;
+          f32x4 o;
+#pragma unroll
+          for (int nt = 0; nt < 4; ++nt) o[nt] = acc[mt][nt][i];
+          if (a.bias) {
+            const float b = a.bias[oc];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = o[e] + b;
+          }
+          if (a.relu) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = relu_f(o[e]);
+          }
+          *reinterpret_cast<f32x4*>(a.out + n0 + 4 * r + d.N * (oc + d.OC * pix)) = o;
+        }
+    }
+  }
+}
+
 // Wd[k' + K'*ic] = W[oc + OC*(ic + C*t)], k' = oc + OC*t
 __global__ void __launch_bounds__(256) conv_relayout_w_kernel(const float* __restrict__ Wt,
                                                               float* __restrict__ Wd, int64_t OC,
@@ -513,6 +606,18 @@ int conv_forward(const float* X, const float* W, const float* b, float* Y, int64
   a.out_vec = (N % 4 == 0) && cnhip::aligned16(Y);
   a.src_vec = (N % 4 == 0) && cnhip::aligned16(X);
   a.wt_vec = (OC % 4 == 0) && cnhip::aligned16(W);
+  if (C * KS * KS <= cnhip::kDirectMaxK && OC % 32 == 0 && N % 64 == 0 && a.out_vec && a.src_vec &&
+      (N + 255) / 256 <= 65535 && N * C * H * Wd < ((int64_t)1 << 31)) {
+    // short contraction: bound by writing Y (X read once from HBM, then from cache)
+    cnhip::HbmTimer timer("conv_direct_fwd_kernel",
+                          4.0 * ((double)N * C * H * Wd + (double)N * OC * d.HO * d.WO + (double)OC * C * KS * KS),
+                          as_stream(stream));
+    // 2 blocks per CU over the 256 CUs: an even share of pixels each
+    const int64_t nb = (N + 255) / 256, px = std::min<int64_t>(d.HO * d.WO, std::max<int64_t>(1, 512 / nb));
+    hipLaunchKernelGGL(cnhip::conv_direct_fwd_kernel, dim3((unsigned)px, (unsigned)nb), dim3(256), 0,
+                       as_stream(stream), a);
+    return cnhip::check_launch(who);
+  }
   cnhip::launch_pixel<false>(a, OC, C * KS * KS, d.HO * d.WO, N * C * H * Wd, as_stream(stream));
   return cnhip::check_launch(who);
 }

@@ -37,7 +37,12 @@ CONV_CASES = [(2, 3, 8, 8, 4, 3, 1, 1), (3, 2, 7, 5, 5, 3, 2, 0), (1, 4, 6, 6, 2
               # N a multiple of the wgrad k-tile (one output pixel per k-tile):
               # 32x64 tile split over 2 wave groups with a partial OC tile, and a
               # 64x32 tile split over 2 wave groups with stride 2
-              (32, 6, 8, 8, 20, 3, 1, 1), (16, 3, 10, 10, 48, 3, 2, 1)]
+              (32, 6, 8, 8, 20, 3, 1, 1), (16, 3, 10, 10, 48, 3, 2, 1),
+              # short contractions (C*KS^2 <= 32, OC % 32 == 0, N % 64 == 0) take the
+              # direct MFMA kernel: 5x5 taps with padding 2; stride 2 with no padding on
+              # a non-square input and 64 channels; N = 320, whose second sample block
+              # has one wave's worth of samples
+              (64, 1, 12, 12, 32, 5, 1, 2), (128, 2, 9, 7, 64, 3, 2, 0), (320, 3, 6, 6, 32, 3, 1, 1)]
 
 
 @pytest.mark.parametrize("N,C,H,W,OC,KS,S,P", CONV_CASES)
