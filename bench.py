@@ -416,7 +416,8 @@ def main() -> int:
 
     kernels = {3: "gemm_f32_kernel + conv_pixel/conv_wgrad_kernel (fp32 MFMA, all shapes of the step)",
                4: "gemm_f32_kernel + lstm_fwd/bwd_persist_kernel (fp32 MFMA; the whole recurrence of "
-                  "each pass in one launch, W_hh slices held in registers, cell update fused)"}.get(
+                  "each pass in one launch, cell update fused, the backward also accumulating "
+                  "dW_hh, dW_ih and db)"}.get(
         args.config, "gemm_f32_kernel (fp32 MFMA GEMM, all shapes of the step)")
     result = {
         "metric": METRIC,

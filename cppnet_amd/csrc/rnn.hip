@@ -300,6 +300,18 @@ __device__ __forceinline__ void ex_store(u64* p, u64 w) {
 }
 
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));  // (value bits, stamp)
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+// Two adjacent words (a, stamp), (b, stamp) at byte offset voff + soff of a
+// buffer resource, in one 16-byte store (cache policy sc0, as ex_store).
+// Each 8-byte word lies inside the one store, so a reader never sees a value
+// without its stamp; the store covers half as many cache-line pieces per
+// instruction as two 8-byte stores.
+__device__ __forceinline__ void ex_store_pair(__amdgpu_buffer_rsrc_t rs, unsigned voff, unsigned soff, float a,
+                                              float b, unsigned stamp) {
+  const u32x4 v = {__float_as_uint(a), stamp, __float_as_uint(b), stamp};
+  __builtin_amdgcn_raw_buffer_store_b128(v, rs, voff, soff, 1);
+}
 
 // Raw buffer resource over the exchange area (32-bit byte offsets).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t ex_rsrc(const u64* base) {
@@ -309,17 +321,24 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t ex_rsrc(const u64* base) {
 // One thread: w[k] = the word at byte offset voff + soff + k * STRIDE of the
 // exchange area (k < N), once every one of them carries `stamp`.  The
 // k-dependent part of the offset is uniform, so it travels in the load's
-// scalar offset.  false: the launch faulted or this wait gave up.
+// scalar offset.  ex_issue sends the first round of loads; other work may
+// run before ex_finish, which waits for them, checks the stamps and polls
+// again for the words not yet written.  false: the launch faulted or this
+// wait gave up.
 template <int N, int STRIDE>
-__device__ __forceinline__ bool ex_wait(const PersistSync& ps, __amdgpu_buffer_rsrc_t rs, unsigned voff,
-                                        unsigned soff, unsigned stamp, u32x2 (&w)[N]) {
+__device__ __forceinline__ void ex_issue(__amdgpu_buffer_rsrc_t rs, unsigned voff, unsigned soff, u32x2 (&w)[N]) {
+  asm volatile("buffer_inv sc0" ::: "memory");
+#pragma unroll
+  for (int k = 0; k < N; ++k) w[k] = __builtin_amdgcn_raw_buffer_load_b64(rs, voff, soff + k * STRIDE, 2);
+}
+
+template <int N, int STRIDE>
+__device__ __forceinline__ bool ex_finish(const PersistSync& ps, __amdgpu_buffer_rsrc_t rs, unsigned voff,
+                                          unsigned soff, unsigned stamp, u32x2 (&w)[N]) {
   if (ps.spin_limit < 0) {
     persist_fail(ps);
     return false;
   }
-  asm volatile("buffer_inv sc0" ::: "memory");
-#pragma unroll
-  for (int k = 0; k < N; ++k) w[k] = __builtin_amdgcn_raw_buffer_load_b64(rs, voff, soff + k * STRIDE, 2);
   for (long long spins = 0;; ++spins) {
     bool all = true;
 #pragma unroll
@@ -337,6 +356,13 @@ __device__ __forceinline__ bool ex_wait(const PersistSync& ps, __amdgpu_buffer_r
     for (int k = 0; k < N; ++k)
       if (w[k].y != stamp) w[k] = __builtin_amdgcn_raw_buffer_load_b64(rs, voff, soff + k * STRIDE, 2);
   }
+}
+
+template <int N, int STRIDE>
+__device__ __forceinline__ bool ex_wait(const PersistSync& ps, __amdgpu_buffer_rsrc_t rs, unsigned voff,
+                                        unsigned soff, unsigned stamp, u32x2 (&w)[N]) {
+  ex_issue<N, STRIDE>(rs, voff, soff, w);
+  return ex_finish<N, STRIDE>(ps, rs, voff, soff, stamp, w);
 }
 
 struct LstmFwdPersistArgs {
@@ -469,6 +495,12 @@ struct LstmBwdPersistArgs {
   u64* ex;  // [2 slots][nst][H/16 writers][H][16]: partial dG_t W_hh^T, stamp t + 1
   int B, S, nst;
   PersistSync sync;
+  // fused weight gradients (IT > 0): X [B*S, I], Y [B*S, H] and the
+  // per-sample-tile partials [nst][H*4H | I*4H | 4H] (dW_hh, dW_ih, db)
+  const float* X;
+  const float* Y;
+  float* part;
+  int I;
 };
 
 // Backward through time, t = S-1 .. 0.  The recurrent term dG_{t+1} W_hh^T
@@ -480,11 +512,28 @@ struct LstmBwdPersistArgs {
 // sample tile in block order.  Each block only multiplies its own dG, and
 // exchanges 16 x 16 words per partner per step.  The cell backward is
 // lstm_cell_bwd_last_kernel's at t = S-1 and lstm_step_bwd_kernel's after.
-template <int H>
+//
+// IT > 0 (I = 64 IT inputs) also accumulates the block's share of the weight
+// gradients while it waits for the next step's partials: dW_hh += h_{t-1}^T
+// dG_t (t >= 1) and dW_ih += x_t^T dG_t over its 16 samples and its 64
+// columns (MFMA tiles of 16 k x 16 columns over the 16 samples; wave w takes
+// the k-tiles w H/64 .. and w IT ..), and db += dG_t per cell thread.  The
+// first poll's loads of step t's wait are sent before step t+1's
+// accumulation, so their latency and the MFMAs overlap.  The sums run over
+// t descending, then over the block's samples; at the end the block writes
+// its partials, which lstm_dw_reduce_kernel adds over the sample tiles in
+// order.  (The separate GEMMs these replace sum over all B S rows instead.)
+template <int H, int IT>
 __global__ void __launch_bounds__(256) lstm_bwd_persist_kernel(LstmBwdPersistArgs a) {
   constexpr int NUT = H / kPt;  // blocks (writers) per sample tile
-  constexpr int TPW = H / 64;   // output tiles of 16 units per wave
+  constexpr int TPW = H / 64;   // output tiles of 16 units per wave; dW_hh k-tiles per wave
+  constexpr bool FUSE = IT > 0;
+  // the W_hh slice (H 64 floats) moves to LDS when the weight-gradient
+  // accumulators would not fit beside it in registers
+  constexpr bool WLDS = FUSE && H > 256;
   __shared__ __align__(16) f32x4 dgs[64 / 4 * kPt];  // dG_t of the 64 columns: [c/4][sample]
+  __shared__ __align__(16) f32x4 wl[WLDS ? H * 64 / 4 : 1];
+  __shared__ float dbr[FUSE ? 64 * kPt : 1];  // db reduction: [column][sample]
   __shared__ int place[2];
   int st, ut;
   if (!persist_place(a.sync, NUT, st, ut, place)) return;
@@ -494,15 +543,23 @@ __global__ void __launch_bounds__(256) lstm_bwd_persist_kernel(LstmBwdPersistArg
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int q = lane >> 4, r = lane & 15;
   const int b0 = st * kPt, j0 = ut * kPt;
-  // W_hh(unit 16 (wave TPW + tt) + r, column kb H + j0 + 4 q + e)
-  f32x4 wv[TPW][4];
+  // W_hh(unit 16 (wave TPW + tt) + r, column kb H + j0 + 4 q + e), in
+  // registers, or (WLDS) in LDS at wl[((wave TPW + tt) 4 + kb) 64 + lane],
+  // read back by the lane that wrote it
+  f32x4 wv[WLDS ? 1 : TPW][4];
 #pragma unroll
   for (int tt = 0; tt < TPW; ++tt)
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
+    for (int kb = 0; kb < 4; ++kb) {
+      f32x4 w4;
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        wv[tt][kb][e] = a.W_hh[(16 * (wave * TPW + tt) + r) + (int64_t)H * ((int64_t)kb * H + j0 + 4 * q + e)];
+        w4[e] = a.W_hh[(16 * (wave * TPW + tt) + r) + (int64_t)H * ((int64_t)kb * H + j0 + 4 * q + e)];
+      if constexpr (WLDS)
+        wl[((wave * TPW + tt) * 4 + kb) * 64 + lane] = w4;
+      else
+        wv[tt][kb] = w4;
+    }
   // cell thread: sample m, unit u
   const int m = tid & 15, u = tid >> 4;
   const int64_t n = b0 + m, d = j0 + u;
@@ -510,6 +567,68 @@ __global__ void __launch_bounds__(256) lstm_bwd_persist_kernel(LstmBwdPersistArg
   const __amdgpu_buffer_rsrc_t rs = ex_rsrc(ex);
   const unsigned slot_bytes = (unsigned)a.nst * NUT * H * kPt * 8u;
   float* dgsf = reinterpret_cast<float*>(dgs);
+  // weight-gradient accumulators: [k-tile][column tile = gate]
+  f32x4 ahh[FUSE ? TPW : 1][4], aih[FUSE ? IT : 1][4];
+  float dbs[4] = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (FUSE) {
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+#pragma unroll
+      for (int kt = 0; kt < TPW; ++kt) ahh[kt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int it = 0; it < IT; ++it) aih[it][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+  // Step p's accumulation, dgs holding dG_p.  MFMA (ks) of tile (kt, ct)
+  // sums over the samples 4 q + ks of lane group q (any order of the 16
+  // samples gives the same sum up to rounding): row operands h_{p-1}(sample,
+  // k) in hA and x_p(sample, i) in xA with k, i = 16 (tile) + r, one 16-byte
+  // load of 4 samples each; column operand dG_p(sample, column 16 ct + r)
+  // from dgs.  Tile by tile, each row operand is reloaded with step p-1's
+  // rows right after its last MFMA: the loads issue while the MFMAs run (16
+  // rows apart each, they are slow to issue) and have a whole step to land.
+  f32x4 hA[FUSE ? TPW : 1], xA[FUSE ? IT : 1];
+  const int64_t smp = b0 + 4 * q;
+  auto load_h = [&](int kt, int p) {  // h_{p-1}, zero for p = 0
+    hA[kt] = p > 0 ? *reinterpret_cast<const f32x4*>(a.Y + smp + (int64_t)B * (p - 1) +
+                                                      BS * (16 * (wave * TPW + kt) + r))
+                   : f32x4{0.f, 0.f, 0.f, 0.f};
+  };
+  auto load_x = [&](int it, int p) {  // x_p
+    xA[it] = *reinterpret_cast<const f32x4*>(a.X + smp + (int64_t)B * p + BS * (16 * (wave * IT + it) + r));
+  };
+  auto dw_step = [&](int p) {
+    if constexpr (FUSE) {
+      float bv[4][4];
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) {
+        const int col = 16 * ct + r;
+        const f32x4* gp = reinterpret_cast<const f32x4*>(dgsf + ((col >> 2) * kPt + 4 * q) * 4);
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) bv[ct][ks] = reinterpret_cast<const float*>(gp + ks)[col & 3];
+      }
+#pragma unroll
+      for (int it = 0; it < IT; ++it) {
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+          for (int ks = 0; ks < 4; ++ks)
+            aih[it][ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(xA[it][ks], bv[ct][ks], aih[it][ct], 0, 0, 0);
+        if (p > 0) load_x(it, p - 1);
+      }
+#pragma unroll
+      for (int kt = 0; kt < TPW; ++kt) {
+        if (p > 0) {
+#pragma unroll
+          for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+              ahh[kt][ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(hA[kt][ks], bv[ct][ks], ahh[kt][ct], 0, 0, 0);
+          load_h(kt, p - 1);
+        }
+      }
+    }
+  };
   // operands of step t (no dependence on the recurrence), loaded a step ahead
   float ig, fg, gg, og, tc, cprev, dy;
   auto load_step = [&](int t) {
@@ -523,6 +642,12 @@ __global__ void __launch_bounds__(256) lstm_bwd_persist_kernel(LstmBwdPersistArg
     dy = a.dY[row + BS * d];
   };
   load_step(S - 1);
+  if constexpr (FUSE) {
+#pragma unroll
+    for (int kt = 0; kt < TPW; ++kt) load_h(kt, S - 1);
+#pragma unroll
+    for (int it = 0; it < IT; ++it) load_x(it, S - 1);
+  }
   float dc_next = 0.0f;
   for (int t = S - 1; t >= 0; --t) {
     const int64_t row = n + (int64_t)B * t;
@@ -530,8 +655,10 @@ __global__ void __launch_bounds__(256) lstm_bwd_persist_kernel(LstmBwdPersistArg
     if (t < S - 1) {
       // partials of step t+1: writer w's word (d, m) at [slot (t+1) & 1][w][d][m], stamp t + 2
       u32x2 w[NUT];
-      const bool ok = ex_wait<NUT, H * kPt * 8>(a.sync, rs, (unsigned)(d * kPt + m) * 8u,
-                                               ((t + 1) & 1) * slot_bytes, (unsigned)(t + 2), w);
+      const unsigned voff = (unsigned)(d * kPt + m) * 8u, soff = ((t + 1) & 1) * slot_bytes;
+      ex_issue<NUT, H * kPt * 8>(rs, voff, soff, w);
+      dw_step(t + 1);  // dgs still holds dG_{t+1}
+      const bool ok = ex_finish<NUT, H * kPt * 8>(a.sync, rs, voff, soff, (unsigned)(t + 2), w);
       if (__syncthreads_or(!ok)) return;
       float rec = 0.0f;
 #pragma unroll
@@ -544,30 +671,90 @@ __global__ void __launch_bounds__(256) lstm_bwd_persist_kernel(LstmBwdPersistArg
     a.dG[row + BS * (d + H)] = df;
     a.dG[row + BS * (d + 2 * H)] = dgg;
     a.dG[row + BS * (d + 3 * H)] = dout;
-    if (t == 0) break;
+    if constexpr (FUSE) {
+      dbs[0] += di;
+      dbs[1] += df;
+      dbs[2] += dgg;
+      dbs[3] += dout;
+    }
+    if (t == 0 && !FUSE) break;
     // local column gate * 16 + u at dgs[(col / 4) * 16 + m][col % 4]
     dgsf[(((0 * 16 + u) >> 2) * kPt + m) * 4 + (u & 3)] = di;
     dgsf[(((1 * 16 + u) >> 2) * kPt + m) * 4 + (u & 3)] = df;
     dgsf[(((2 * 16 + u) >> 2) * kPt + m) * 4 + (u & 3)] = dgg;
     dgsf[(((3 * 16 + u) >> 2) * kPt + m) * 4 + (u & 3)] = dout;
-    load_step(t - 1);
+    if (t > 0) load_step(t - 1);
     __syncthreads();
-    u64* dst = ex + (int64_t)(t & 1) * (slot_bytes / 8) + (int64_t)ut * H * kPt;
+    if (t == 0) break;
+    const unsigned so = (unsigned)(t & 1) * slot_bytes + (unsigned)ut * H * kPt * 8u;
 #pragma unroll
     for (int tt = 0; tt < TPW; ++tt) {
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) {
         const f32x4 g4 = dgs[(4 * kb + q) * kPt + r];
+        f32x4 w4;
+        if constexpr (WLDS)
+          w4 = wl[((wave * TPW + tt) * 4 + kb) * 64 + lane];
+        else
+          w4 = wv[tt][kb];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(g4[e], wv[tt][kb][e], acc, 0, 0, 0);
+        for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(g4[e], w4[e], acc, 0, 0, 0);
       }
-      // acc[i]: sample 4 q + i, unit 16 (wave TPW + tt) + r
-      u64* o = dst + (int64_t)(16 * (wave * TPW + tt) + r) * kPt + 4 * q;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) ex_store(o + i, ex_word(acc[i], (unsigned)(t + 1)));
+      // acc[i]: sample 4 q + i, unit 16 (wave TPW + tt) + r, words
+      // [slot t & 1][writer ut][unit][sample], the lane's four adjacent
+      const unsigned vo = (unsigned)((16 * (wave * TPW + tt) + r) * kPt + 4 * q) * 8u;
+      ex_store_pair(rs, vo, so, acc[0], acc[1], (unsigned)(t + 1));
+      ex_store_pair(rs, vo + 16, so, acc[2], acc[3], (unsigned)(t + 1));
     }
     // dgs is rewritten at the next step only after the wait's block-wide vote
+  }
+  if constexpr (FUSE) {
+    // step 0's accumulation (dgs holds dG_0, made visible by the barrier above)
+    dw_step(0);
+    // the block's partials: acc[i] of tile (kt, ct) is row 16 kt' + 4 q + i,
+    // column ct H + j0 + r of dW (kt' = the wave's k-tile)
+    const int64_t G = 4 * (int64_t)H, I = a.I;
+    float* phh = a.part + (int64_t)st * (H * G + I * G + G);
+    float* pih = phh + H * G;
+    float* pb = pih + I * G;
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+      const int64_t col = (int64_t)ct * H + j0 + r;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int kt = 0; kt < TPW; ++kt) phh[(16 * (wave * TPW + kt) + 4 * q + i) + H * col] = ahh[kt][ct][i];
+#pragma unroll
+        for (int it = 0; it < IT; ++it) pih[(16 * (wave * IT + it) + 4 * q + i) + I * col] = aih[it][ct][i];
+      }
+    }
+    // db: the 16 samples' running sums of each column added in sample order
+#pragma unroll
+    for (int g = 0; g < 4; ++g) dbr[(16 * g + u) * kPt + m] = dbs[g];
+    __syncthreads();
+    if (tid < 64) {
+      float v = 0.f;
+#pragma unroll
+      for (int s2 = 0; s2 < kPt; ++s2) v += dbr[tid * kPt + s2];
+      pb[(int64_t)(tid >> 4) * H + j0 + (tid & 15)] = v;
+    }
+  }
+}
+
+// out_k[e] = sum over the sample tiles s = 0 .. nst-1, in order, of
+// part[s][e] (the persistent backward's weight-gradient partials), for the
+// concatenation e of dW_hh | dW_ih | db into their three buffers.
+__global__ void __launch_bounds__(256) lstm_dw_reduce_kernel(const float* __restrict__ part, int nst, int64_t n_hh,
+                                                             int64_t n_ih, int64_t n_b, float* __restrict__ gW_hh,
+                                                             float* __restrict__ gW_ih, float* __restrict__ gb) {
+  const int64_t total = n_hh + n_ih + n_b;
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+    float v = 0.f;
+    for (int s2 = 0; s2 < nst; ++s2) v += part[(int64_t)s2 * total + e];
+    if (e < n_hh) gW_hh[e] = v;
+    else if (e < n_hh + n_ih) gW_ih[e - n_hh] = v;
+    else gb[e - n_hh - n_ih] = v;
   }
 }
 
@@ -993,36 +1180,80 @@ bool persist_shape(int64_t B, int64_t S, int64_t H, int64_t& nst, int64_t& nut, 
 template <int H>
 const void* fwd_persist_kernel() { return reinterpret_cast<const void*>(&lstm_fwd_persist_kernel<H>); }
 template <int H>
-const void* bwd_persist_kernel() { return reinterpret_cast<const void*>(&lstm_bwd_persist_kernel<H>); }
-
-// The instantiated hidden sizes (W_hh slice of H/4 registers per lane).
-const void* persist_kernel(bool fwd, int64_t H) {
-  switch (H) {
-    case 64: return fwd ? fwd_persist_kernel<64>() : bwd_persist_kernel<64>();
-    case 128: return fwd ? fwd_persist_kernel<128>() : bwd_persist_kernel<128>();
-    case 256: return fwd ? fwd_persist_kernel<256>() : bwd_persist_kernel<256>();
-    case 512: return fwd ? fwd_persist_kernel<512>() : bwd_persist_kernel<512>();
+const void* bwd_persist_kernel(int it) {
+  switch (it) {
+    case 0: return reinterpret_cast<const void*>(&lstm_bwd_persist_kernel<H, 0>);
+    case 1: return reinterpret_cast<const void*>(&lstm_bwd_persist_kernel<H, 1>);
+    case 2: return reinterpret_cast<const void*>(&lstm_bwd_persist_kernel<H, 2>);
     default: return nullptr;
   }
 }
 
+// The instantiated hidden sizes (W_hh slice of H/4 registers per lane) and,
+// for the backward, input widths I = 64 it with the weight gradients fused
+// (it = 0: not fused).
+const void* persist_kernel(bool fwd, int64_t H, int it = 0) {
+  switch (H) {
+    case 64: return fwd ? fwd_persist_kernel<64>() : bwd_persist_kernel<64>(it);
+    case 128: return fwd ? fwd_persist_kernel<128>() : bwd_persist_kernel<128>(it);
+    case 256: return fwd ? fwd_persist_kernel<256>() : bwd_persist_kernel<256>(it);
+    case 512: return fwd ? fwd_persist_kernel<512>() : bwd_persist_kernel<512>(it);
+    default: return nullptr;
+  }
+}
+
+// Whether the persistent backward can also accumulate the weight gradients
+// (CNHIP_RECURRENCE_FUSED_DW=0 turns it off): I a multiple of 64 up to 128
+// and 16-byte aligned X and Y (the kernel reads 4 samples per load).
+// Returns I / 64, or 0.
+int bwd_fused_inputs(const float* X, const float* Y, int64_t I) {
+  const char* e = std::getenv("CNHIP_RECURRENCE_FUSED_DW");
+  if (e && e[0] == '0') return 0;
+  if (I % 64 != 0 || I / 64 > 2 || !aligned16(X) || !aligned16(Y)) return 0;
+  return (int)(I / 64);
+}
+
 // The whole BPTT recurrence in one persistent launch when the shape suits
-// it (dG: [B*S, 4H], fully written); false in *done to fall back.
+// it (dG: [B*S, 4H], fully written); false in *done to fall back.  With
+// `part` (nst (4H^2 + 4HI + 4H) floats) the launch also accumulates the
+// weight gradients and a reduction writes gW_hh, gW_ih and gb (*fused).
 int lstm_bwd_persistent(const float* gates, const float* c, const float* tanh_c, const float* dY,
-                        const float* W_hh, float* dG, int64_t B, int64_t S, int64_t H, hipStream_t st,
-                        const char* who, bool* done) {
+                        const float* W_hh, float* dG, const float* X, const float* Y, float* part, int64_t I,
+                        float* gW_hh, float* gW_ih, float* gb, int64_t B, int64_t S, int64_t H, hipStream_t st,
+                        const char* who, bool* done, bool* fused) {
   *done = false;
+  *fused = false;
   int64_t nst, nut, grid;
-  const void* kern = persist_kernel(false, H);
+  int it = part ? bwd_fused_inputs(X, Y, I) : 0;
+  const void* kern = persist_kernel(false, H, it);
   if (!persist_enabled() || !kern || !persist_shape(B, S, H, nst, nut, grid)) return CNHIP_OK;
   const size_t ex_bytes = (size_t)2 * nst * nut * H * kPt * sizeof(u64);
-  if (ex_bytes > 0x7fffffffu || !persist_fits(kern, grid, 256, who)) return CNHIP_OK;
-  LstmBwdPersistArgs args{gates, c, tanh_c, dY, W_hh, dG, nullptr, (int)B, (int)S, (int)nst, {}};
-  TimingRec* rec = timing_slot(2.0 * B * 4 * H * H * (double)(S - 1));
+  if (ex_bytes > 0x7fffffffu) return CNHIP_OK;
+  if (it && !persist_fits(kern, grid, 256, who)) {
+    // the fused kernel holds fewer blocks per CU: the unfused one may fit
+    it = 0;
+    kern = persist_kernel(false, H, 0);
+  }
+  if (!persist_fits(kern, grid, 256, who)) return CNHIP_OK;
+  LstmBwdPersistArgs args{gates, c, tanh_c, dY, W_hh, dG, nullptr, (int)B, (int)S, (int)nst, {},
+                          X, Y, it ? part : nullptr, (int)I};
+  const double G = 4.0 * H;
+  double flops = 2.0 * B * G * H * (double)(S - 1);
+  if (it) flops += 2.0 * H * G * B * (double)(S - 1) + 2.0 * I * G * B * (double)S;
+  TimingRec* rec = timing_slot(flops);
   if (rec) (void)hipEventRecord(rec->start, st);
   CNHIP_TRY(persist_launch(kern, grid, 256, args, ex_bytes, st, who));
   if (rec) (void)hipEventRecord(rec->stop, st);
   *done = true;
+  if (!it) return CNHIP_OK;
+  const int64_t n_hh = H * 4 * H, n_ih = I * 4 * H, n_b = 4 * H;
+  {
+    HbmTimer timer("lstm_dw_reduce_kernel", 4.0 * (double)(n_hh + n_ih + n_b) * (nst + 1), st);
+    hipLaunchKernelGGL(lstm_dw_reduce_kernel, dim3(elementwise_grid(n_hh + n_ih + n_b, 256)), dim3(256), 0, st, part,
+                       (int)nst, n_hh, n_ih, n_b, gW_hh, gW_ih, gb);
+    CNHIP_TRY(check_launch(who));
+  }
+  *fused = true;
   return CNHIP_OK;
 }
 
@@ -1101,11 +1332,15 @@ int cnhip_lstm_backward(const float* X, const float* W_ih, const float* W_hh, co
   hipStream_t st = as_stream(stream);
   const int64_t G = 4 * H, BS = B * S;
   cnhip::Workspace ws(st);
-  CNHIP_TRY(ws.alloc((size_t)(BS * G + B * H) * sizeof(float), who));
+  // dG, dc and, for the fused weight gradients, one partial per 16-sample tile
+  const int64_t n_part = cnhip::bwd_fused_inputs(X, Y, I) ? (B / 16) * (G * H + G * I + G) : 0;
+  CNHIP_TRY(ws.alloc((size_t)(BS * G + B * H + n_part) * sizeof(float), who));
   float* dG = static_cast<float*>(ws.p);
   float* dc = dG + BS * G;
-  bool done = false;
-  CNHIP_TRY(cnhip::lstm_bwd_persistent(gates, c, tanh_c, dY, W_hh, dG, B, S, H, st, who, &done));
+  float* part = n_part ? dc + B * H : nullptr;
+  bool done = false, fused = false;
+  CNHIP_TRY(cnhip::lstm_bwd_persistent(gates, c, tanh_c, dY, W_hh, dG, X, Y, part, I, gW_hh, gW_ih, gb, B, S, H, st,
+                                       who, &done, &fused));
   if (!done) {
     // t = S-1: dh = dY only; then per step one fused launch of
     // dh_t = dY_t + dG_{t+1} W_hh^T (lstm.cpp:244) and the cell backward
@@ -1115,10 +1350,12 @@ int cnhip_lstm_backward(const float* X, const float* W_ih, const float* W_hh, co
     CNHIP_TRY(cnhip::lstm_bwd_steps<cnhip::LstmBwdCfgDefault>(gates, c, tanh_c, dY, W_hh, dc, dG, B, S,
                                                               H, st, who));
   }
-  CNHIP_TRY(cnhip::gemm_f32(1, 0, I, G, BS, 1.f, X, BS, dG, BS, 0.f, gW_ih, I, nullptr, 0, st, who));
-  CNHIP_TRY(cnhip::gemm_f32(1, 0, H, G, B * (S - 1), 1.f, Y, BS, dG + B, BS, 0.f, gW_hh, H, nullptr,
-                            0, st, who));
-  CNHIP_TRY(cnhip::column_sum(dG, gb, BS, G, 0, st, who));
+  if (!fused) {
+    CNHIP_TRY(cnhip::gemm_f32(1, 0, I, G, BS, 1.f, X, BS, dG, BS, 0.f, gW_ih, I, nullptr, 0, st, who));
+    CNHIP_TRY(cnhip::gemm_f32(1, 0, H, G, B * (S - 1), 1.f, Y, BS, dG + B, BS, 0.f, gW_hh, H, nullptr,
+                              0, st, who));
+    CNHIP_TRY(cnhip::column_sum(dG, gb, BS, G, 0, st, who));
+  }
   if (dX)
     CNHIP_TRY(cnhip::gemm_f32(0, 1, BS, I, G, 1.f, dG, BS, W_ih, I, 0.f, dX, BS, nullptr, 0, st, who));
   return CNHIP_OK;

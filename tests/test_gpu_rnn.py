@@ -39,17 +39,27 @@ RNN_CASES = [(3, 5, 4, 8), (8, 7, 16, 32), (5, 1, 3, 6), (40, 6, 12, 71), (128, 
 # 512, S >= 2): one XCD's sample tile, three of eight XCDs, all eight, two
 # sample tiles per XCD
 PERSIST_CASES = [(16, 5, 8, 64), (48, 9, 24, 128), (128, 64, 128, 512), (256, 6, 32, 256)]
+# shapes whose persistent backward also accumulates the weight gradients
+# (I = 64 or 128): each hidden size, W_hh in registers (H <= 256) and in LDS
+# (H = 512), one and two 64-wide input tiles, one and several sample tiles
+FUSED_CASES = [(32, 7, 64, 64), (48, 4, 128, 128), (64, 5, 128, 256), (16, 3, 64, 512), (128, 64, 128, 512)]
 LSTM_CASES = ([(*c, "per-step") for c in RNN_CASES if c not in PERSIST_CASES] +
-              [(*c, path) for c in PERSIST_CASES for path in ("persistent", "per-step")])
+              [(*c, path) for c in PERSIST_CASES for path in ("persistent", "per-step")] +
+              [(*c, path) for c in FUSED_CASES for path in ("persistent", "persistent-unfused")
+               if (*c, path) not in [(*p, "persistent") for p in PERSIST_CASES]])
 
 
 @pytest.mark.parametrize("B,S,I,H,path", LSTM_CASES)
 def test_lstm_vs_oracle(gpu, oracle, monkeypatch, B, S, I, H, path):
     """Both recurrence paths -- one persistent launch for all timesteps, or
     one launch per timestep -- against the oracle (they sum the recurrent
-    products in different orders, so each is held to the oracle's bars)."""
+    products in different orders, so each is held to the oracle's bars).
+    The persistent backward accumulates the weight gradients itself where I
+    is 64 or 128 ("persistent"), or leaves them to the GEMMs
+    ("persistent-unfused")."""
     print(f"[lstm] B={B} S={S} I={I} H={H} {path}", flush=True)
-    monkeypatch.setenv("CNHIP_RECURRENCE_PERSISTENT", "1" if path == "persistent" else "0")
+    monkeypatch.setenv("CNHIP_RECURRENCE_PERSISTENT", "0" if path == "per-step" else "1")
+    monkeypatch.setenv("CNHIP_RECURRENCE_FUSED_DW", "0" if path == "persistent-unfused" else "1")
     oracle.cnref_set_threads(16)
     rng = np.random.default_rng(B + S + I + H)
     X, Wih, Whh, b, dY = _inputs(rng, B, S, I, H, 4)
