@@ -299,8 +299,7 @@ __device__ __forceinline__ void ex_store(u64* p, u64 w) {
   __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
-typedef unsigned u32x2 __attribute__((ext_vector_type(2)));  // (value bits, stamp)
-typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));  // two (value bits, stamp) words
 
 // Two adjacent words (a, stamp), (b, stamp) at byte offset voff + soff of a
 // buffer resource, in one 16-byte store (cache policy sc0, as ex_store).
@@ -318,23 +317,26 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t ex_rsrc(const u64* base) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<u64*>(base), 0, 0x7fffffff, 0x00020000);
 }
 
-// One thread: w[k] = the word at byte offset voff + soff + k * STRIDE of the
-// exchange area (k < N), once every one of them carries `stamp`.  The
-// k-dependent part of the offset is uniform, so it travels in the load's
-// scalar offset.  ex_issue sends the first round of loads; other work may
-// run before ex_finish, which waits for them, checks the stamps and polls
-// again for the words not yet written.  false: the launch faulted or this
-// wait gave up.
-template <int N, int STRIDE>
-__device__ __forceinline__ void ex_issue(__amdgpu_buffer_rsrc_t rs, unsigned voff, unsigned soff, u32x2 (&w)[N]) {
+// One thread: w[k] = the two adjacent words at byte offset voff + soff +
+// k * STRIDE of the exchange area (k < N, one 16-byte load each), once every
+// one of them carries `stamp`.  The k-dependent part of the offset is
+// uniform, so it travels in the load's scalar offset.  ex_issue sends the
+// first round of loads (after `sleep` s_sleep units: the words a thread
+// has just written itself take about that long to reach the others); other
+// work may run before ex_finish, which waits for them, checks the stamps and
+// polls again for the words not yet written.  false: the launch faulted or
+// this wait gave up.
+template <int N, int STRIDE, int SLEEP = 0>
+__device__ __forceinline__ void ex_issue(__amdgpu_buffer_rsrc_t rs, unsigned voff, unsigned soff, u32x4 (&w)[N]) {
+  if constexpr (SLEEP > 0) __builtin_amdgcn_s_sleep(SLEEP);
   asm volatile("buffer_inv sc0" ::: "memory");
 #pragma unroll
-  for (int k = 0; k < N; ++k) w[k] = __builtin_amdgcn_raw_buffer_load_b64(rs, voff, soff + k * STRIDE, 2);
+  for (int k = 0; k < N; ++k) w[k] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, soff + k * STRIDE, 2);
 }
 
 template <int N, int STRIDE>
 __device__ __forceinline__ bool ex_finish(const PersistSync& ps, __amdgpu_buffer_rsrc_t rs, unsigned voff,
-                                          unsigned soff, unsigned stamp, u32x2 (&w)[N]) {
+                                          unsigned soff, unsigned stamp, u32x4 (&w)[N]) {
   if (ps.spin_limit < 0) {
     persist_fail(ps);
     return false;
@@ -342,7 +344,7 @@ __device__ __forceinline__ bool ex_finish(const PersistSync& ps, __amdgpu_buffer
   for (long long spins = 0;; ++spins) {
     bool all = true;
 #pragma unroll
-    for (int k = 0; k < N; ++k) all = all && w[k].y == stamp;
+    for (int k = 0; k < N; ++k) all = all && w[k].y == stamp && w[k].w == stamp;
     if (all) return true;
     if ((spins & 63) == 63 && __hip_atomic_load(ps.fault, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u)
       return false;
@@ -354,15 +356,9 @@ __device__ __forceinline__ bool ex_finish(const PersistSync& ps, __amdgpu_buffer
     asm volatile("buffer_inv sc0" ::: "memory");
 #pragma unroll
     for (int k = 0; k < N; ++k)
-      if (w[k].y != stamp) w[k] = __builtin_amdgcn_raw_buffer_load_b64(rs, voff, soff + k * STRIDE, 2);
+      if (w[k].y != stamp || w[k].w != stamp)
+        w[k] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, soff + k * STRIDE, 2);
   }
-}
-
-template <int N, int STRIDE>
-__device__ __forceinline__ bool ex_wait(const PersistSync& ps, __amdgpu_buffer_rsrc_t rs, unsigned voff,
-                                        unsigned soff, unsigned stamp, u32x2 (&w)[N]) {
-  ex_issue<N, STRIDE>(rs, voff, soff, w);
-  return ex_finish<N, STRIDE>(ps, rs, voff, soff, stamp, w);
 }
 
 struct LstmFwdPersistArgs {
@@ -384,6 +380,11 @@ struct LstmFwdPersistArgs {
 // supplies k = 16 kb + 4 q + e to MFMA (kb, e)); then one thread per
 // (sample, unit) runs the cell exactly as lstm_cell_fwd0_kernel /
 // lstm_step_fwd_kernel do, writes the caches and Y, and hands h_t on.
+// s_sleep units before the forward's first poll of a step (~64 clocks each):
+// sooner than that the other blocks' h_t cannot have arrived, and a poll of
+// 64 KB per block that returns stale words only delays the next one.
+constexpr int kFirstPollSleep = 12;
+
 template <int H>
 __global__ void __launch_bounds__(256) lstm_fwd_persist_kernel(LstmFwdPersistArgs a) {
   constexpr int NKB = H / 16;  // k-blocks; also the words per thread of h_{t-1}
@@ -433,15 +434,18 @@ __global__ void __launch_bounds__(256) lstm_fwd_persist_kernel(LstmFwdPersistArg
       og = sigm(xo + bo);
     } else {
       // h_{t-1}: word (k, s) at [slot (t-1) & 1][k][s]; this thread takes
-      // s = tid % 16, k = tid / 16 + 16 j (byte offset tid 8 + j 2048)
-      u32x2 w[NKB];
-      const bool ok = ex_wait<NKB, 256 * 8>(a.sync, rs, (unsigned)tid * 8u, ((t - 1) & 1) * slot_bytes,
-                                            (unsigned)t, w);
+      // s = 2 (tid % 8) and the next, k = tid / 8 + 32 j (byte offset tid 16
+      // + j 4096)
+      u32x4 w[NKB / 2];
+      const unsigned voff = (unsigned)tid * 16u, soff = ((t - 1) & 1) * slot_bytes;
+      ex_issue<NKB / 2, 256 * 16, kFirstPollSleep>(rs, voff, soff, w);
+      const bool ok = ex_finish<NKB / 2, 256 * 16>(a.sync, rs, voff, soff, (unsigned)t, w);
       if (__syncthreads_or(!ok)) return;
 #pragma unroll
-      for (int j = 0; j < NKB; ++j) {
-        const int k = (tid >> 4) + 16 * j;
-        hsf[((k >> 2) * kPt + m) * 4 + (k & 3)] = __uint_as_float(w[j].x);
+      for (int j = 0; j < NKB / 2; ++j) {
+        const int k = (tid >> 3) + 32 * j, s2 = 2 * (tid & 7);
+        hsf[((k >> 2) * kPt + s2) * 4 + (k & 3)] = __uint_as_float(w[j].x);
+        hsf[((k >> 2) * kPt + s2 + 1) * 4 + (k & 3)] = __uint_as_float(w[j].z);
       }
       __syncthreads();
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -534,6 +538,7 @@ __global__ void __launch_bounds__(256) lstm_bwd_persist_kernel(LstmBwdPersistArg
   __shared__ __align__(16) f32x4 dgs[64 / 4 * kPt];  // dG_t of the 64 columns: [c/4][sample]
   __shared__ __align__(16) f32x4 wl[WLDS ? H * 64 / 4 : 1];
   __shared__ float dbr[FUSE ? 64 * kPt : 1];  // db reduction: [column][sample]
+  __shared__ float red[2][kPt][kPt];          // half sums of the partials: [half][unit][sample]
   __shared__ int place[2];
   int st, ut;
   if (!persist_place(a.sync, NUT, st, ut, place)) return;
@@ -653,17 +658,28 @@ __global__ void __launch_bounds__(256) lstm_bwd_persist_kernel(LstmBwdPersistArg
     const int64_t row = n + (int64_t)B * t;
     float dh = dy;
     if (t < S - 1) {
-      // partials of step t+1: writer w's word (d, m) at [slot (t+1) & 1][w][d][m], stamp t + 2
-      u32x2 w[NUT];
-      const unsigned voff = (unsigned)(d * kPt + m) * 8u, soff = ((t + 1) & 1) * slot_bytes;
-      ex_issue<NUT, H * kPt * 8>(rs, voff, soff, w);
+      // partials of step t+1: writer w's word (unit, sample) at [slot (t+1)
+      // & 1][w][unit][sample], stamp t + 2.  Thread (half, u2, p2) loads the
+      // words (j0 + u2, 2 p2) and (j0 + u2, 2 p2 + 1) of writers half NUT/2
+      // .. half NUT/2 + NUT/2 - 1 and sums them in writer order; the cell
+      // thread adds its two half sums.
+      const int half = tid >> 7, u2 = (tid >> 3) & 15, p2 = tid & 7;
+      u32x4 w[NUT / 2];
+      const unsigned voff = (unsigned)((j0 + u2) * kPt + 2 * p2) * 8u;
+      const unsigned soff = ((t + 1) & 1) * slot_bytes + (unsigned)half * (NUT / 2) * H * kPt * 8u;
+      ex_issue<NUT / 2, H * kPt * 8>(rs, voff, soff, w);
       dw_step(t + 1);  // dgs still holds dG_{t+1}
-      const bool ok = ex_finish<NUT, H * kPt * 8>(a.sync, rs, voff, soff, (unsigned)(t + 2), w);
-      if (__syncthreads_or(!ok)) return;
-      float rec = 0.0f;
+      const bool ok = ex_finish<NUT / 2, H * kPt * 8>(a.sync, rs, voff, soff, (unsigned)(t + 2), w);
+      float s0 = 0.f, s1 = 0.f;
 #pragma unroll
-      for (int k = 0; k < NUT; ++k) rec += __uint_as_float(w[k].x);
-      dh = dy + rec;
+      for (int k = 0; k < NUT / 2; ++k) {
+        s0 += __uint_as_float(w[k].x);
+        s1 += __uint_as_float(w[k].z);
+      }
+      red[half][u2][2 * p2] = s0;
+      red[half][u2][2 * p2 + 1] = s1;
+      if (__syncthreads_or(!ok)) return;
+      dh = dy + (red[0][u][m] + red[1][u][m]);
     }
     float di, df, dgg, dout;
     lstm_cell_bwd(ig, fg, gg, og, tc, dh, t == S - 1 ? 0.0f : dc_next, cprev, di, df, dgg, dout, dc_next);
