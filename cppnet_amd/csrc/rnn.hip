@@ -374,23 +374,58 @@ struct LstmFwdPersistArgs {
 };
 
 // Forward, t = 0 .. S-1.  Per step t >= 1 a block waits for h_{t-1} of its
-// 16 samples (all H units, from the H/16 blocks of its sample tile), stages
-// it in LDS, and wave w computes gate w's 16 x 16 recurrent pre-activations
-// (v_mfma_f32_16x16x4f32 over k ascending in blocks of 16: lane (q, r)
-// supplies k = 16 kb + 4 q + e to MFMA (kb, e)); then one thread per
-// (sample, unit) runs the cell exactly as lstm_cell_fwd0_kernel /
-// lstm_step_fwd_kernel do, writes the caches and Y, and hands h_t on.
+// 16 samples (all H units, from the H/16 blocks of its sample tile) and
+// stages it in LDS; wave w computes the 16 x 16 recurrent pre-activations of
+// its 4 units j0 + 4 w .. j0 + 4 w + 3 for all 4 gates (column c = gate 4 +
+// unit; v_mfma_f32_16x16x4f32 over k ascending in blocks of 16: lane (q, r)
+// supplies k = 16 kb + 4 q + e to MFMA (kb, e)).  A 4 x 4 transpose between
+// lanes and accumulator registers then hands each lane the 4 gates of one
+// cell (sample 4 q + r / 4, unit 4 w + r % 4), which it runs exactly as
+// lstm_cell_fwd0_kernel / lstm_step_fwd_kernel do: it writes the caches and
+// Y, and hands h_t on.  One barrier per step (the wait's vote, which also
+// publishes the staged h_{t-1}): a wave rewrites the staging area only after
+// it has seen every wave's h_t, which each wave stores after its last read
+// of the area.
 // s_sleep units before the forward's first poll of a step (~64 clocks each):
 // sooner than that the other blocks' h_t cannot have arrived, and a poll of
 // 64 KB per block that returns stale words only delays the next one.
 constexpr int kFirstPollSleep = 12;
+
+// The transpose of a 4 x 4 block between lane bits 2..3 and the register
+// index: afterwards lane (g, j) (g = lane bits 2..3, j = bits 0..1) holds in
+// register i what lane (i, j) held in register g.  Lanes 16 apart are
+// independent.
+__device__ __forceinline__ f32x4 xpose_lanes4(f32x4 v, int lane) {
+  {  // lane bit 2 <-> register bit 0
+    const bool l = (lane >> 2) & 1;
+    const float ra = __shfl_xor(l ? v[0] : v[1], 4, 64), rb = __shfl_xor(l ? v[2] : v[3], 4, 64);
+    if (l) {
+      v[0] = ra;
+      v[2] = rb;
+    } else {
+      v[1] = ra;
+      v[3] = rb;
+    }
+  }
+  {  // lane bit 3 <-> register bit 1
+    const bool l = (lane >> 3) & 1;
+    const float ra = __shfl_xor(l ? v[0] : v[2], 8, 64), rb = __shfl_xor(l ? v[1] : v[3], 8, 64);
+    if (l) {
+      v[0] = ra;
+      v[1] = rb;
+    } else {
+      v[2] = ra;
+      v[3] = rb;
+    }
+  }
+  return v;
+}
 
 template <int H>
 __global__ void __launch_bounds__(256) lstm_fwd_persist_kernel(LstmFwdPersistArgs a) {
   constexpr int NKB = H / 16;  // k-blocks; also the words per thread of h_{t-1}
   constexpr int NUT = H / kPt;
   __shared__ __align__(16) f32x4 hs[H / 4 * kPt];  // h_{t-1}: [k/4][sample], k..k+3
-  __shared__ float gt[4][kPt][kPt + 1];             // [gate][sample][unit]
   __shared__ int place[2];
   int st, ut;
   if (!persist_place(a.sync, NUT, st, ut, place)) return;
@@ -400,15 +435,15 @@ __global__ void __launch_bounds__(256) lstm_fwd_persist_kernel(LstmFwdPersistArg
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int q = lane >> 4, r = lane & 15;
   const int b0 = st * kPt, j0 = ut * kPt;
-  // W_hh(k, column `wave` H + j0 + r) for k = 16 kb + 4 q + e, e = 0..3
+  // W_hh(k, column (r / 4) H + j0 + 4 wave + r % 4) for k = 16 kb + 4 q + e
   f32x4 wv[NKB];
   {
-    const float* wc = a.W_hh + (int64_t)H * ((int64_t)wave * H + j0 + r) + 4 * q;
+    const float* wc = a.W_hh + (int64_t)H * ((int64_t)(r >> 2) * H + j0 + 4 * wave + (r & 3)) + 4 * q;
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) wv[kb] = *reinterpret_cast<const f32x4*>(wc + 16 * kb);
   }
   // cell thread: sample m, unit u
-  const int m = tid & 15, u = tid >> 4;
+  const int m = 4 * q + (r >> 2), u = 4 * wave + (r & 3);
   const int64_t n = b0 + m, d = j0 + u;
   const float bi = a.bias[d], bf = a.bias[d + H], bg = a.bias[d + 2 * H], bo = a.bias[d + 3 * H];
   u64* const ex = a.ex + (int64_t)st * H * kPt;
@@ -440,14 +475,13 @@ __global__ void __launch_bounds__(256) lstm_fwd_persist_kernel(LstmFwdPersistArg
       const unsigned voff = (unsigned)tid * 16u, soff = ((t - 1) & 1) * slot_bytes;
       ex_issue<NKB / 2, 256 * 16, kFirstPollSleep>(rs, voff, soff, w);
       const bool ok = ex_finish<NKB / 2, 256 * 16>(a.sync, rs, voff, soff, (unsigned)t, w);
-      if (__syncthreads_or(!ok)) return;
 #pragma unroll
       for (int j = 0; j < NKB / 2; ++j) {
         const int k = (tid >> 3) + 32 * j, s2 = 2 * (tid & 7);
         hsf[((k >> 2) * kPt + s2) * 4 + (k & 3)] = __uint_as_float(w[j].x);
         hsf[((k >> 2) * kPt + s2 + 1) * 4 + (k & 3)] = __uint_as_float(w[j].z);
       }
-      __syncthreads();
+      if (__syncthreads_or(!ok)) return;
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb) {
@@ -455,15 +489,14 @@ __global__ void __launch_bounds__(256) lstm_fwd_persist_kernel(LstmFwdPersistArg
 #pragma unroll
         for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(h4[e], wv[kb][e], acc, 0, 0, 0);
       }
-      // acc[i]: gate `wave`, sample 4 q + i, unit r
-#pragma unroll
-      for (int i = 0; i < 4; ++i) gt[wave][4 * q + i][r] = acc[i];
-      __syncthreads();
+      // acc[i]: sample 4 q + i, gate r / 4, unit 4 wave + r % 4; after the
+      // transpose acc[g]: gate g of this lane's cell
+      acc = xpose_lanes4(acc, lane);
       // as lstm_step_fwd_kernel: (recurrent + x W_ih) + bias
-      ig = sigm((gt[0][m][u] + xi) + bi);
-      fg = sigm((gt[1][m][u] + xf) + bf);
-      gg = tanhf((gt[2][m][u] + xg) + bg);
-      og = sigm((gt[3][m][u] + xo) + bo);
+      ig = sigm((acc[0] + xi) + bi);
+      fg = sigm((acc[1] + xf) + bf);
+      gg = tanhf((acc[2] + xg) + bg);
+      og = sigm((acc[3] + xo) + bo);
     }
     const float ct = lstm_cell_c(fg, c_prev, ig, gg);
     const float tc = tanhf(ct);
