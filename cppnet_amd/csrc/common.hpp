@@ -46,6 +46,10 @@ int ws_alloc(void** ptr, size_t bytes, hipStream_t stream, const char* where);
 // Calls on one stream from several host threads at once are not supported.
 constexpr int kScratchGemm = 0, kScratchLayer = 1;
 int scratch(hipStream_t stream, int slot, size_t bytes, void** ptr, const char* where);
+// The same, also returning in *gen which allocation the buffer is: a number
+// unique over the process, new whenever the slot's buffer is (re)allocated
+// (its contents are then undefined).  Not for the no-allocation calls.
+int scratch(hipStream_t stream, int slot, size_t bytes, void** ptr, uint64_t* gen, const char* where);
 
 // While one is in scope on this host thread, a caller-provided device
 // buffer of `cap` bytes stands in for the GEMM scratch slot of every stream

@@ -24,6 +24,7 @@
 // reference expressions in the reference's operation order.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdlib>
 #include <mutex>
@@ -238,8 +239,14 @@ __global__ void __launch_bounds__(LstmCfg::NT) lstm_step_fwd_kernel(
 // it has slots; blocks with a slot past the last sample tile exit.
 //
 // Exchange.  A value handed to another block travels as one 64-bit word
-// (float bits, step stamp) in a double-buffered exchange area zeroed before
-// the launch (stamps start at 1, so a zeroed word never matches).  The
+// (float bits, stamp) in a double-buffered exchange area.  The stamp is the
+// launch's epoch (16 bits, from a per-device counter) times 65536 plus the
+// step, so words left by earlier launches never match: the area is zeroed
+// only when its buffer is new, when the counter wraps, and before every
+// launch recorded into a graph (whose replays all reuse epoch 0; a zeroed
+// word carries stamp 0, which no step uses).  The fault word is tagged with
+// the epoch the same way; the XCD slot counters are returned to 0 by the
+// last block placed on each XCD.  The
 // writer stores the word; the reader invalidates its CU's L1 (buffer_inv
 // sc0) and loads the words (nontemporal) until each carries the stamp it
 // waits for.  A word is stored and loaded whole, so a value is never taken
@@ -257,15 +264,22 @@ constexpr int kPersistMaxH = 512;  // W_hh slice of H x 64 floats: H/4 registers
 typedef unsigned long long u64;
 
 struct PersistSync {
-  unsigned* fault;       // device word, zeroed before the launch
-  unsigned* xcd_slots;   // [8] per-XCD block counters, zeroed before the launch
+  unsigned* fault;       // device word: fault_mark(epoch) once this launch faulted
+  unsigned* xcd_slots;   // [8] per-XCD block counters, 0 between launches
   unsigned* fault_host;  // pinned host word, or null
   long long spin_limit;
+  unsigned epoch;        // 0 .. 65535; stamps are epoch << 16 | step
 };
 
+__device__ __forceinline__ unsigned fault_mark(unsigned epoch) { return 0x80000000u | epoch; }
+__device__ __forceinline__ unsigned ex_stamp(const PersistSync& ps, int step) { return (ps.epoch << 16) | (unsigned)step; }
+
 __device__ __forceinline__ void persist_fail(const PersistSync& ps) {
-  __hip_atomic_store(ps.fault, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(ps.fault, fault_mark(ps.epoch), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if (ps.fault_host) __hip_atomic_store(ps.fault_host, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ bool persist_faulted(const PersistSync& ps) {
+  return __hip_atomic_load(ps.fault, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == fault_mark(ps.epoch);
 }
 
 __device__ __forceinline__ unsigned xcc_id() {
@@ -278,9 +292,13 @@ __device__ __forceinline__ bool persist_place(const PersistSync& ps, int nut, in
   if (threadIdx.x == 0) {
     const unsigned x = xcc_id();
     if (x < 8u) {
-      const int i = (int)__hip_atomic_fetch_add(ps.xcd_slots + x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      place[0] = (int)x + 8 * (i / nut);
-      place[1] = i % nut;
+      // every XCD receives gridDim.x / 8 blocks; the one that takes the last
+      // ticket leaves the counter at 0 for the next launch
+      unsigned* slot = ps.xcd_slots + x;
+      const unsigned i = __hip_atomic_fetch_add(slot, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (i + 1u == gridDim.x / 8u) __hip_atomic_store(slot, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      place[0] = (int)x + 8 * ((int)i / nut);
+      place[1] = (int)i % nut;
     } else {
       place[0] = -1;
       persist_fail(ps);
@@ -346,8 +364,7 @@ __device__ __forceinline__ bool ex_finish(const PersistSync& ps, __amdgpu_buffer
 #pragma unroll
     for (int k = 0; k < N; ++k) all = all && w[k].y == stamp && w[k].w == stamp;
     if (all) return true;
-    if ((spins & 63) == 63 && __hip_atomic_load(ps.fault, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u)
-      return false;
+    if ((spins & 63) == 63 && persist_faulted(ps)) return false;
     if (spins >= ps.spin_limit) {
       persist_fail(ps);
       return false;
@@ -368,7 +385,7 @@ struct LstmFwdPersistArgs {
   float* tanh_c;
   float* Y;
   const float* W_hh;
-  u64* ex;  // [2 slots][nst][H][16]: h_t of (unit, sample), stamp t + 1
+  u64* ex;  // [2 slots][nst][H][16]: h_t of (unit, sample), stamp of step t + 1
   int B, S, nst;
   PersistSync sync;
 };
@@ -474,7 +491,7 @@ __global__ void __launch_bounds__(256) lstm_fwd_persist_kernel(LstmFwdPersistArg
       u32x4 w[NKB / 2];
       const unsigned voff = (unsigned)tid * 16u, soff = ((t - 1) & 1) * slot_bytes;
       ex_issue<NKB / 2, 256 * 16, kFirstPollSleep>(rs, voff, soff, w);
-      const bool ok = ex_finish<NKB / 2, 256 * 16>(a.sync, rs, voff, soff, (unsigned)t, w);
+      const bool ok = ex_finish<NKB / 2, 256 * 16>(a.sync, rs, voff, soff, ex_stamp(a.sync, t), w);
 #pragma unroll
       for (int j = 0; j < NKB / 2; ++j) {
         const int k = (tid >> 3) + 32 * j, s2 = 2 * (tid & 7);
@@ -502,7 +519,7 @@ __global__ void __launch_bounds__(256) lstm_fwd_persist_kernel(LstmFwdPersistArg
     const float tc = tanhf(ct);
     const float h = og * tc;
     if (t + 1 < a.S)
-      ex_store(ex + (int64_t)(t & 1) * (slot_bytes / 8) + (int64_t)d * kPt + m, ex_word(h, (unsigned)(t + 1)));
+      ex_store(ex + (int64_t)(t & 1) * (slot_bytes / 8) + (int64_t)d * kPt + m, ex_word(h, ex_stamp(a.sync, t + 1)));
     float* g = a.gates + row;
     g[BS * d] = ig;
     g[BS * (d + H)] = fg;
@@ -529,7 +546,7 @@ struct LstmBwdPersistArgs {
   const float* dY;
   const float* W_hh;
   float* dG;
-  u64* ex;  // [2 slots][nst][H/16 writers][H][16]: partial dG_t W_hh^T, stamp t + 1
+  u64* ex;  // [2 slots][nst][H/16 writers][H][16]: partial dG_t W_hh^T, stamp of step t + 1
   int B, S, nst;
   PersistSync sync;
   // fused weight gradients (IT > 0): X [B*S, I], Y [B*S, H] and the
@@ -692,7 +709,7 @@ __global__ void __launch_bounds__(256) lstm_bwd_persist_kernel(LstmBwdPersistArg
     float dh = dy;
     if (t < S - 1) {
       // partials of step t+1: writer w's word (unit, sample) at [slot (t+1)
-      // & 1][w][unit][sample], stamp t + 2.  Thread (half, u2, p2) loads the
+      // & 1][w][unit][sample], stamp of step t + 2.  Thread (half, u2, p2) loads the
       // words (j0 + u2, 2 p2) and (j0 + u2, 2 p2 + 1) of writers half NUT/2
       // .. half NUT/2 + NUT/2 - 1 and sums them in writer order; the cell
       // thread adds its two half sums.
@@ -702,7 +719,7 @@ __global__ void __launch_bounds__(256) lstm_bwd_persist_kernel(LstmBwdPersistArg
       const unsigned soff = ((t + 1) & 1) * slot_bytes + (unsigned)half * (NUT / 2) * H * kPt * 8u;
       ex_issue<NUT / 2, H * kPt * 8>(rs, voff, soff, w);
       dw_step(t + 1);  // dgs still holds dG_{t+1}
-      const bool ok = ex_finish<NUT / 2, H * kPt * 8>(a.sync, rs, voff, soff, (unsigned)(t + 2), w);
+      const bool ok = ex_finish<NUT / 2, H * kPt * 8>(a.sync, rs, voff, soff, ex_stamp(a.sync, t + 2), w);
       float s0 = 0.f, s1 = 0.f;
 #pragma unroll
       for (int k = 0; k < NUT / 2; ++k) {
@@ -753,8 +770,8 @@ __global__ void __launch_bounds__(256) lstm_bwd_persist_kernel(LstmBwdPersistArg
       // acc[i]: sample 4 q + i, unit 16 (wave TPW + tt) + r, words
       // [slot t & 1][writer ut][unit][sample], the lane's four adjacent
       const unsigned vo = (unsigned)((16 * (wave * TPW + tt) + r) * kPt + 4 * q) * 8u;
-      ex_store_pair(rs, vo, so, acc[0], acc[1], (unsigned)(t + 1));
-      ex_store_pair(rs, vo + 16, so, acc[2], acc[3], (unsigned)(t + 1));
+      ex_store_pair(rs, vo, so, acc[0], acc[1], ex_stamp(a.sync, t + 1));
+      ex_store_pair(rs, vo + 16, so, acc[2], acc[3], ex_stamp(a.sync, t + 1));
     }
     // dgs is rewritten at the next step only after the wait's block-wide vote
   }
@@ -1088,6 +1105,22 @@ int lstm_bwd_steps(const float* gates, const float* c, const float* tanh_c, cons
 // ---- persistent-launch plumbing
 constexpr int kScratchRecur = 2;  // scratch slot of the fault word and the exchange area
 
+// Per device: the epoch of the next launch, and the exchange buffers
+// (scratch allocations) zeroed or run in since the counter last started
+// over.
+struct PersistEpochs {
+  unsigned next = 1;
+  std::vector<uint64_t> clean;
+};
+std::mutex g_epoch_mu;
+PersistEpochs g_epochs[64];
+
+void persist_forget_clean(int dev) {
+  if (dev < 0 || dev >= 64) return;
+  std::lock_guard<std::mutex> lock(g_epoch_mu);
+  g_epochs[dev].clean.clear();
+}
+
 // Pinned host fault word per device (the kernels set it when a wait gives up).
 unsigned* fault_host_word(int dev) {
   static std::mutex mu;
@@ -1113,6 +1146,7 @@ int persist_take_fault(const char* who) {
   CNHIP_TRY(check_hip(hipGetDevice(&dev), who));
   unsigned* w = fault_host_word(dev);
   if (w && __atomic_exchange_n(w, 0u, __ATOMIC_ACQ_REL) != 0u) {
+    persist_forget_clean(dev);  // the faulted launch may have left its counters off 0
     set_error("%s: an earlier persistent recurrence launch on this device gave up waiting for its other "
               "blocks (not all co-resident?); its outputs are invalid", who);
     return CNHIP_EHIP;
@@ -1185,29 +1219,54 @@ bool persist_cooperative() {
   return e && e[0] == '1';
 }
 
+// The epoch of the next launch on `dev`, and whether its buffer (allocation
+// `gen`) must be zeroed first: when no launch has run in it since the epoch
+// counter last started over at 1 (a new buffer holds arbitrary words; after
+// the wrap, words of earlier launches may carry the epochs to come), or
+// since a fault was reported.  A launch recorded into a graph takes epoch 0
+// and is always preceded by the zeroing (every replay reuses its stamps).
+unsigned persist_epoch(int dev, uint64_t gen, bool capturing, bool* zero) {
+  if (capturing || dev < 0 || dev >= 64) {
+    *zero = true;
+    return 0;
+  }
+  std::lock_guard<std::mutex> lock(g_epoch_mu);
+  PersistEpochs& e = g_epochs[dev];
+  if (e.next > 0xffffu) {
+    e.next = 1;
+    e.clean.clear();
+  }
+  *zero = std::find(e.clean.begin(), e.clean.end(), gen) == e.clean.end();
+  if (*zero) e.clean.push_back(gen);
+  return e.next++;
+}
+
 // Zeroes the fault word, the XCD slot counters and the exchange area
-// (ex_bytes, after a 256-byte header), then launches
-// `kernel` with one argument (cooperatively only when asked to above, and
-// never while the stream is being captured into a graph).
+// (ex_bytes, after a 256-byte header) where persist_epoch asks for it, then
+// launches `kernel` with one argument (cooperatively only when asked to
+// above, and never while the stream is being captured into a graph).
 template <class Args>
 int persist_launch(const void* kernel, int64_t grid, int threads, Args& args, size_t ex_bytes, hipStream_t st,
                    const char* who) {
   void* ws = nullptr;
+  uint64_t gen = 0;
   const size_t bytes = 256 + ex_bytes;
-  CNHIP_TRY(scratch(st, kScratchRecur, bytes, &ws, who));
-  CNHIP_TRY(fill_bytes(ws, 0, bytes, st, who));
+  CNHIP_TRY(scratch(st, kScratchRecur, bytes, &ws, &gen, who));
   int dev = 0;
   CNHIP_TRY(check_hip(hipGetDevice(&dev), who));
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  CNHIP_TRY(check_hip(hipStreamIsCapturing(st, &cs), who));
+  const bool capturing = cs != hipStreamCaptureStatusNone;
   args.sync.fault = static_cast<unsigned*>(ws);
   args.sync.xcd_slots = static_cast<unsigned*>(ws) + 16;
   args.sync.fault_host = fault_host_word(dev);
   args.sync.spin_limit = persist_spin_limit();
   args.ex = reinterpret_cast<u64*>(static_cast<char*>(ws) + 256);
-  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-  CNHIP_TRY(check_hip(hipStreamIsCapturing(st, &cs), who));
-  const bool capturing = cs != hipStreamCaptureStatusNone;
   void* params[] = {&args};
   return persist_ordered(st, capturing, who, [&] {
+    bool zero = true;
+    args.sync.epoch = persist_epoch(dev, gen, capturing, &zero);
+    if (zero) CNHIP_TRY(fill_bytes(ws, 0, bytes, st, who));
     if (!capturing && persist_cooperative())
       CNHIP_TRY(check_hip(hipLaunchCooperativeKernel(kernel, dim3((unsigned)grid), dim3(threads), params, 0, st), who));
     else
@@ -1217,9 +1276,11 @@ int persist_launch(const void* kernel, int64_t grid, int threads, Args& args, si
 }
 
 // Shapes the persistent kernels take: 16-sample tiles, H a multiple of 64
-// up to kPersistMaxH, 32-bit row indices.  grid = 8 (H/16) ceil(nst/8).
+// up to kPersistMaxH, steps below 65535 (the step part of a stamp), 32-bit
+// row indices.  grid = 8 (H/16) ceil(nst/8).
 bool persist_shape(int64_t B, int64_t S, int64_t H, int64_t& nst, int64_t& nut, int64_t& grid) {
-  if (B % kPt != 0 || H % 64 != 0 || H > kPersistMaxH || S < 2 || B * S * 4 * H > INT32_MAX) return false;
+  if (B % kPt != 0 || H % 64 != 0 || H > kPersistMaxH || S < 2 || S > 65000 || B * S * 4 * H > INT32_MAX)
+    return false;
   nst = B / kPt;
   nut = H / kPt;
   grid = 8 * nut * ((nst + 7) / 8);

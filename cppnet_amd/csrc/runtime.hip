@@ -43,7 +43,9 @@ struct ScratchEntry {
   int slot;
   void* p;
   size_t cap;
+  uint64_t gen;  // which allocation p is (unique over the process)
 };
+uint64_t g_scratch_gens = 0;
 std::mutex g_scratch_mu;
 std::vector<ScratchEntry> g_scratch;
 // Streams whose scratch slots a captured graph refers to: their buffers
@@ -131,6 +133,10 @@ int persist_order_leave(hipStream_t stream, int dev, const char* who) {
 }
 
 int scratch(hipStream_t stream, int slot, size_t bytes, void** ptr, const char* where) {
+  return scratch(stream, slot, bytes, ptr, nullptr, where);
+}
+
+int scratch(hipStream_t stream, int slot, size_t bytes, void** ptr, uint64_t* gen, const char* where) {
   if (t_fixed.p) {
     if (slot != kScratchGemm) {
       set_error("%s: scratch slot %d requested inside a no-allocation call", where, slot);
@@ -142,6 +148,7 @@ int scratch(hipStream_t stream, int slot, size_t bytes, void** ptr, const char* 
       return CNHIP_EINVAL;
     }
     *ptr = t_fixed.p;
+    if (gen) *gen = 0;
     return CNHIP_OK;
   }
   int dev = 0;
@@ -151,7 +158,7 @@ int scratch(hipStream_t stream, int slot, size_t bytes, void** ptr, const char* 
   for (auto& x : g_scratch)
     if (x.dev == dev && x.stream == stream && x.slot == slot) e = &x;
   if (!e) {
-    g_scratch.push_back(ScratchEntry{dev, stream, slot, nullptr, 0});
+    g_scratch.push_back(ScratchEntry{dev, stream, slot, nullptr, 0, 0});
     e = &g_scratch.back();
   }
   if (e->cap < bytes) {
@@ -174,8 +181,10 @@ int scratch(hipStream_t stream, int slot, size_t bytes, void** ptr, const char* 
     cap = (cap + ((size_t)2 << 20) - 1) & ~(((size_t)2 << 20) - 1);
     CNHIP_TRY(ws_alloc(&e->p, cap, stream, where));
     e->cap = cap;
+    e->gen = ++g_scratch_gens;
   }
   *ptr = e->p;
+  if (gen) *gen = e->gen;
   return CNHIP_OK;
 }
 

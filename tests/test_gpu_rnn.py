@@ -199,3 +199,18 @@ def test_lstm_persistent_wait_fault_is_reported(gpu):
     for x, y, name in zip(good[:4], ref[:4], ["Y", "gates", "c", "tanh_c"]):
         ok, msg = close(x, y, 1e-4, 2e-5)
         assert ok, f"{name}: persistent vs per-step: {msg}"
+
+
+def test_lstm_persistent_exchange_reuse_is_exact(gpu):
+    """Launch after launch the persistent kernels reuse their exchange area
+    without zeroing it (each launch stamps its words with a new epoch): runs
+    of one shape repeat bit for bit, also after a larger shape has grown the
+    area and a different layout (forward vs backward) has written over it."""
+    env = {"CNHIP_RECURRENCE_PERSISTENT": "1"}
+    print("[lstm-persist] exchange reuse", flush=True)
+    first = _lstm_run(64, 6, 64, 128, 5, env)
+    for shape in [(64, 6, 64, 128), (128, 9, 128, 256), (64, 6, 64, 128), (32, 4, 16, 64), (64, 6, 64, 128)]:
+        got = _lstm_run(*shape, 5, env)
+        if shape == (64, 6, 64, 128):
+            for x, y in zip(first, got):
+                assert np.array_equal(x.view(np.uint32), y.view(np.uint32))
