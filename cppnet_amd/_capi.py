@@ -63,10 +63,12 @@ SIGNATURES: dict[str, tuple] = {
     "cnhip_linear_backward_act_noalloc": (i32, [vp] * 7 + [i64, i64, i64, i32, i32, i32, vp]),
     "cnhip_conv2d_forward": (i32, [vp, vp, vp, vp] + [i64] * 8 + [vp]),
     "cnhip_conv2d_forward_relu": (i32, [vp, vp, vp, vp] + [i64] * 8 + [vp]),
+    "cnhip_conv2d_forward_relu_maxpool": (i32, [vp, vp, vp, vp, vp] + [i64] * 10 + [vp]),
     "cnhip_conv2d_backward": (i32, [vp, vp, vp, vp, vp, vp] + [i64] * 8 + [vp]),
     "cnhip_maxpool2d_forward": (i32, [vp, vp, vp] + [i64] * 6 + [vp]),
     "cnhip_maxpool2d_backward": (i32, [vp, vp, vp] + [i64] * 6 + [vp]),
     "cnhip_maxpool2d_backward_relu": (i32, [vp, vp, vp, vp] + [i64] * 6 + [vp]),
+    "cnhip_maxpool2d_backward_relu_pooled": (i32, [vp, vp, vp, vp] + [i64] * 6 + [vp]),
     "cnhip_lstm_forward": (i32, [vp] * 8 + [i64] * 4 + [vp]),
     "cnhip_lstm_backward": (i32, [vp] * 12 + [i64] * 4 + [vp]),
     "cnhip_gru_forward": (i32, [vp] * 7 + [i64] * 4 + [vp]),

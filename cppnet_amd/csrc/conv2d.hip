@@ -288,6 +288,117 @@ __global__ void __launch_bounds__(256) conv_direct_fwd_kernel(ConvArgs a) {
   }
 }
 
+// conv_direct_fwd_kernel with the ReLU and a MaxPool2D (window p x p,
+// stride p, windows tiling the conv output) fused in: a block takes one
+// pooled pixel and 256 samples, and each wave runs the direct kernel's MFMAs
+// (same operands, same order) for the p^2 conv pixels of the window in the
+// pool's (ph, pw) order, keeping per output the running maximum and its
+// window index ph p + pw -- strict >, from -inf and index 0, as
+// maxpool_fwd_vec_kernel compares -- so the pooled output and the argmax are
+// bit for bit those of the two launches, and the conv output is never
+// written.  The next conv pixel's X operands are loaded before the current
+// one's MFMAs.
+constexpr int kPoolMaxFused = 4;
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+__global__ void __launch_bounds__(256) conv_direct_pool_fwd_kernel(ConvArgs a, int pool, float* __restrict__ P,
+                                                                   int32_t* __restrict__ pidx) {
+  const ConvDims& d = a.d;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int q = lane >> 4, r = lane & 15;
+  const int K = (int)(d.C * d.KS * d.KS), OC = (int)d.OC;
+  const int HP = (int)d.HO / pool, npp = HP * ((int)d.WO / pool), nsub = pool * pool;
+  __shared__ int off[kPoolMaxFused * kPoolMaxFused][kDirectMaxK];  // per window tap s = ph pool + pw
+  const int64_t n0 = (int64_t)blockIdx.y * 256 + 64 * wave;  // N % 64 == 0
+  const int nks = (K + 3) / 4;
+  for (int pp = (int)blockIdx.x; pp < npp; pp += (int)gridDim.x) {
+    const int py = pp % HP, px = pp / HP;
+    __syncthreads();  // the previous window's offsets have been read
+    for (int e = (int)threadIdx.x; e < nsub * kDirectMaxK; e += 256) {
+      const int sub = e / kDirectMaxK, k = e % kDirectMaxK;
+      off[sub][k] = k < K ? gather_off<false, int>(d, py * pool + sub / pool, px * pool + sub % pool, k) : -1;
+    }
+    __syncthreads();
+    if (n0 >= d.N) continue;
+    auto load_x = [&](int sub, f32x4 (&xv)[kDirectMaxK / 4]) {  // X(n0 + 4 r .. 4 r + 3, tap 4 ks + q)
+#pragma unroll
+      for (int ks = 0; ks < kDirectMaxK / 4; ++ks) {
+        const int o = off[sub][4 * ks + q];
+        xv[ks] = o >= 0 ? *reinterpret_cast<const f32x4*>(a.src + o + n0 + 4 * r) : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    };
+    for (int oc0 = 0; oc0 < OC; oc0 += 32) {
+      float wv[2][kDirectMaxK / 4];  // W(oc0 + 16 mt + r, tap 4 ks + q)
+#pragma unroll
+      for (int ks = 0; ks < kDirectMaxK / 4; ++ks)
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+          const int k = 4 * ks + q;
+          wv[mt][ks] = k < K ? a.wt[oc0 + 16 * mt + r + (int64_t)OC * k] : 0.f;
+        }
+      float bias[2][4];
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) bias[mt][i] = a.bias ? a.bias[oc0 + 16 * mt + 4 * q + i] : 0.f;
+      // mx[mt][i][nt], mi: channel oc0 + 16 mt + 4 q + i, sample n0 + 4 r + nt
+      f32x4 mx[2][4];
+      i32x4 mi[2][4];
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          mx[mt][i] = f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+          mi[mt][i] = i32x4{0, 0, 0, 0};
+        }
+      f32x4 xv[kDirectMaxK / 4], xn[kDirectMaxK / 4];
+      load_x(0, xv);
+      for (int sub = 0; sub < nsub; ++sub) {
+        if (sub + 1 < nsub) load_x(sub + 1, xn);
+        f32x4 acc[2][4];
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+          for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < kDirectMaxK / 4; ++ks)
+          if (ks < nks) {
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+              for (int nt = 0; nt < 4; ++nt)
+                acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(wv[mt][ks], xv[ks][nt], acc[mt][nt], 0, 0, 0);
+          }
+        // as conv_direct_fwd_kernel's epilogue: + bias, then the ReLU
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int nt = 0; nt < 4; ++nt) {
+              float o = acc[mt][nt][i];
+              if (a.bias) o = o + bias[mt][i];
+              o = relu_f(o);
+              if (o > mx[mt][i][nt]) {
+                mx[mt][i][nt] = o;
+                mi[mt][i][nt] = sub;
+              }
+            }
+#pragma unroll
+        for (int ks = 0; ks < kDirectMaxK / 4; ++ks) xv[ks] = xn[ks];
+      }
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int64_t o = n0 + 4 * r + d.N * (oc0 + 16 * mt + 4 * q + i + (int64_t)d.OC * pp);
+          *reinterpret_cast<f32x4*>(P + o) = mx[mt][i];
+          *reinterpret_cast<i32x4*>(pidx + o) = mi[mt][i];
+        }
+    }
+  }
+}
+
 // Wd[k' + K'*ic] = W[oc + OC*(ic + C*t)], k' = oc + OC*t
 __global__ void __launch_bounds__(256) conv_relayout_w_kernel(const float* __restrict__ Wt,
                                                               float* __restrict__ Wd, int64_t OC,
@@ -637,6 +748,43 @@ int cnhip_conv2d_forward_relu(const float* X, const float* W, const float* b, fl
                               int64_t P, cnhip_stream_t stream) {
   return conv_forward(X, W, b, Y, N, C, H, Wd, OC, KS, S, P, 1, stream,
                       "cnhip_conv2d_forward_relu");
+}
+
+int cnhip_conv2d_forward_relu_maxpool(const float* X, const float* W, const float* b, float* Yp,
+                                      int32_t* idx, int64_t N, int64_t C, int64_t H, int64_t Wd,
+                                      int64_t OC, int64_t KS, int64_t S, int64_t P, int64_t pool,
+                                      int64_t pool_stride, cnhip_stream_t stream) {
+  const char* who = "cnhip_conv2d_forward_relu_maxpool";
+  const cnhip::ConvDims d = cnhip::make_dims(N, C, H, Wd, OC, KS, S, P);
+  CNHIP_TRY(cnhip::check_dims(d, who));
+  CNHIP_REQUIRE(X && W && Yp && idx, "%s: NULL pointer", who);
+  if (pool_stride <= 0) pool_stride = pool;  // max_pool2d.cpp:25-28
+  CNHIP_REQUIRE(pool > 0 && pool <= d.HO && pool <= d.WO, "%s: pool %lld does not fit the %lldx%lld conv output",
+                who, (long long)pool, (long long)d.HO, (long long)d.WO);
+  hipStream_t st = as_stream(stream);
+  const int64_t HP = (d.HO - pool) / pool_stride + 1, WP = (d.WO - pool) / pool_stride + 1;
+  cnhip::ConvArgs a{};
+  a.d = d; a.src = X; a.wt = W; a.bias = b; a.relu = 1;
+  a.src_vec = (N % 4 == 0) && cnhip::aligned16(X);
+  if (C * KS * KS <= cnhip::kDirectMaxK && OC % 32 == 0 && N % 64 == 0 && a.src_vec && cnhip::aligned16(Yp) &&
+      cnhip::aligned16(idx) && pool_stride == pool && pool <= cnhip::kPoolMaxFused && HP * pool == d.HO &&
+      WP * pool == d.WO && (N + 255) / 256 <= 65535 && N * C * H * Wd < ((int64_t)1 << 31) &&
+      N * OC * HP * WP < ((int64_t)1 << 31)) {
+    // X read once from HBM; the pooled output and the int32 argmax written
+    cnhip::HbmTimer timer("conv_direct_pool_fwd_kernel",
+                          4.0 * ((double)N * C * H * Wd + (double)OC * C * KS * KS) + 8.0 * (double)N * OC * HP * WP,
+                          st);
+    const int64_t nb = (N + 255) / 256, px = std::min<int64_t>(HP * WP, std::max<int64_t>(1, 512 / nb));
+    hipLaunchKernelGGL(cnhip::conv_direct_pool_fwd_kernel, dim3((unsigned)px, (unsigned)nb), dim3(256), 0, st, a,
+                       (int)pool, Yp, idx);
+    return cnhip::check_launch(who);
+  }
+  // any other shape: the conv + ReLU output in a workspace, then the pool
+  void* ws = nullptr;
+  CNHIP_TRY(cnhip::scratch(st, cnhip::kScratchLayer, (size_t)(N * OC * d.HO * d.WO) * sizeof(float), &ws, who));
+  float* Y = static_cast<float*>(ws);
+  CNHIP_TRY(conv_forward(X, W, b, Y, N, C, H, Wd, OC, KS, S, P, 1, stream, who));
+  return cnhip_maxpool2d_forward(Y, Yp, idx, N, OC, d.HO, d.WO, pool, pool_stride, stream);
 }
 
 int cnhip_conv2d_backward(const float* X, const float* W, const float* dY, float* gW, float* gb,

@@ -63,6 +63,30 @@ namespace CppNet
             return y;
         }
 
+        DeviceTensor Conv2D::forward_relu_maxpool(const DeviceTensor& x, MaxPool2D& pool)
+        {
+            if (x.rank() != 4 || x.dimension(1) != in_channels_)
+                throw std::runtime_error("Conv2D::forward: expected [N, " + std::to_string(in_channels_) +
+                                         ", H, W], got " + shape_str(x.dims()));
+            const int64_t N = x.dimension(0), H = x.dimension(2), W = x.dimension(3);
+            const int64_t HO = (H + 2 * padding_ - kernel_size_) / stride_ + 1;
+            const int64_t WO = (W + 2 * padding_ - kernel_size_) / stride_ + 1;
+            if (HO <= 0 || WO <= 0) throw std::runtime_error("Conv2D::forward: input smaller than kernel");
+            const int64_t ps = pool.get_pool_size(), pst = pool.get_stride();
+            if (HO < ps || WO < ps) throw std::runtime_error("MaxPool2D::forward: input smaller than the pool window");
+            const int64_t HP = (HO - ps) / pst + 1, WP = (WO - ps) / pst + 1;
+            in_cache_ = x;
+            DeviceTensor y = DeviceTensor::empty({N, out_channels_, HP, WP});
+            DeviceTensor idx = DeviceTensor::empty({N, out_channels_, HP, WP});  // int32 payload
+            Device::check(cnhip_conv2d_forward_relu_maxpool(x.data(), W_.data(), bias_flag_ ? b_.data() : nullptr,
+                                                            y.data(), idx.idata(), N, in_channels_, H, W,
+                                                            out_channels_, kernel_size_, stride_, padding_, ps,
+                                                            pst, Device::stream()),
+                          "Conv2D::forward_relu_maxpool");
+            pool.set_fused_forward({N, out_channels_, HO, WO}, y, idx);
+            return y;
+        }
+
         DeviceTensor Conv2D::backward(const DeviceTensor& g) { return backward(g, true); }
 
         DeviceTensor Conv2D::backward(const DeviceTensor& g, bool input_grad)
@@ -152,6 +176,7 @@ namespace CppNet
                 throw std::runtime_error("MaxPool2D::forward: input smaller than the pool window");
             const int64_t HO = (H - pool_size_) / stride_ + 1, WO = (W - pool_size_) / stride_ + 1;
             in_dims_ = x.dims();
+            fused_out_ = DeviceTensor();
             DeviceTensor y = DeviceTensor::empty({N, C, HO, WO});
             idx_ = DeviceTensor::empty({N, C, HO, WO});  // int32 payload
             Device::check(cnhip_maxpool2d_forward(x.data(), y.data(), idx_.idata(), N, C, H, W, pool_size_,
@@ -183,6 +208,27 @@ namespace CppNet
                                                         in_dims_[0], in_dims_[1], in_dims_[2], in_dims_[3],
                                                         pool_size_, stride_, Device::stream()),
                           "MaxPool2D::backward_relu");
+            return dx;
+        }
+
+        void MaxPool2D::set_fused_forward(const std::vector<int64_t>& in_dims, const DeviceTensor& out,
+                                          const DeviceTensor& idx)
+        {
+            in_dims_ = in_dims;
+            fused_out_ = out;
+            idx_ = idx;
+        }
+
+        DeviceTensor MaxPool2D::backward_relu_pooled(const DeviceTensor& g)
+        {
+            if (!idx_.defined() || !fused_out_.defined())
+                throw std::runtime_error("MaxPool2D::backward_relu_pooled without a fused forward");
+            if (g.size() != idx_.size()) throw std::runtime_error("MaxPool2D::backward: grad shape mismatch");
+            DeviceTensor dx = DeviceTensor::empty(in_dims_);
+            Device::check(cnhip_maxpool2d_backward_relu_pooled(g.data(), idx_.idata(), fused_out_.data(), dx.data(),
+                                                               in_dims_[0], in_dims_[1], in_dims_[2], in_dims_[3],
+                                                               pool_size_, stride_, Device::stream()),
+                          "MaxPool2D::backward_relu_pooled");
             return dx;
         }
 

@@ -41,6 +41,16 @@ namespace CppNet
                     }
                     if (Layers::Conv2D* conv = steps_[i]->conv2d())
                     {
+                        // Conv2D -> ReLU -> MaxPool2D: one call, the ReLU output not
+                        // kept (the pool's backward masks with its own output)
+                        Layers::MaxPool2D* mp = i + 2 < count ? steps_[i + 2]->maxpool() : nullptr;
+                        if (mp)
+                        {
+                            x = conv->forward_relu_maxpool(x, *mp);
+                            relu->set_output_cache(DeviceTensor());
+                            i += 2;
+                            continue;
+                        }
                         x = conv->forward_relu(x);
                         relu->set_output_cache(x);
                         ++i;
@@ -84,6 +94,13 @@ namespace CppNet
                 if (k == first && !input_grad) return steps_[k]->backward_no_input_grad(g);
                 Activations::Activation* prev = k > first ? steps_[k - 1]->activation() : nullptr;
                 auto* relu = dynamic_cast<Activations::ReLU*>(prev);
+                Layers::MaxPool2D* fused_mp = steps_[k]->maxpool();
+                if (relu && fused_mp && fused_mp->fused_forward())
+                {
+                    g = fused_mp->backward_relu_pooled(g);
+                    --k;
+                    continue;
+                }
                 if (relu && relu->output_cache().defined())
                 {
                     if (Layers::Linear* lin = steps_[k]->linear())

@@ -16,6 +16,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <type_traits>
 
 #include "act_math.hpp"
 #include "common.hpp"
@@ -95,8 +96,17 @@ __global__ void __launch_bounds__(256) maxpool_fwd_vec_kernel(PoolDims d, const 
   }
 }
 
+// The ReLU backward fused into the pool's backward (MASK): the pool's input
+// is a ReLU output, and a routed gradient is scaled by relu_mask of that
+// input at the argmax -- read from the input itself (kMaskIn: y is the ReLU
+// output [N, C, H, W]) or from the pool's own output (kMaskOut: y is the
+// pooled [N, C, HO, WO], whose value at a window is the input at its argmax,
+// bit for bit, so the scale is the same; the ReLU output itself then need
+// not be kept).
+constexpr int kMaskNone = 0, kMaskIn = 1, kMaskOut = 2;
+
 // maxpool_bwd_tiled_kernel for N % 4 == 0: a wave per window, float4s over n.
-template <bool MASK>
+template <int MASK>
 __global__ void __launch_bounds__(256) maxpool_bwd_tiled_vec_kernel(PoolDims d,
                                                                     const float* __restrict__ dY,
                                                                     const int32_t* __restrict__ idx,
@@ -113,14 +123,19 @@ __global__ void __launch_bounds__(256) maxpool_bwd_tiled_vec_kernel(PoolDims d,
     const int64_t base = N * c + sh * (oh * pool) + sw * (ow * pool);
     for (int64_t q = lane; q < N4; q += 64) {
       const i32x4 mi = *reinterpret_cast<const i32x4*>(idx + N * pos + 4 * q);
-      const f32x4 gy = 0.f + *reinterpret_cast<const f32x4*>(dY + N * pos + 4 * q);
+      f32x4 gy = 0.f + *reinterpret_cast<const f32x4*>(dY + N * pos + 4 * q);
+      if (MASK == kMaskOut) {
+        const f32x4 yv = *reinterpret_cast<const f32x4*>(y + N * pos + 4 * q);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) gy[e] *= relu_mask(yv[e]);
+      }
       for (int ph = 0; ph < pool; ++ph)
         for (int pw = 0; pw < pool; ++pw) {
           const int64_t o = base + sh * ph + sw * pw + 4 * q;
           f32x4 g;
 #pragma unroll
           for (int e = 0; e < 4; ++e) g[e] = mi[e] == ph * pool + pw ? gy[e] : 0.f;
-          if (MASK) {
+          if (MASK == kMaskIn) {
             const f32x4 yv = *reinterpret_cast<const f32x4*>(y + o);
 #pragma unroll
             for (int e = 0; e < 4; ++e) g[e] *= relu_mask(yv[e]);
@@ -133,9 +148,9 @@ __global__ void __launch_bounds__(256) maxpool_bwd_tiled_vec_kernel(PoolDims d,
 
 // Backward as a gather (any stride): input position (c, ih, iw) sums dY over
 // the windows that contain it and picked it, in (oh, ow) order starting from
-// 0.  MASK: the pool's input is a ReLU output y, and the result is scaled by
-// relu_mask(y) -- the ReLU backward fused in, same arithmetic as separately.
-template <bool MASK>
+// 0, then scales by the ReLU mask (kMaskIn), or scales each window's term
+// (kMaskOut; the same value wherever the mask is 1).
+template <int MASK>
 __global__ void __launch_bounds__(256) maxpool_bwd_gather_kernel(PoolDims d,
                                                                  const float* __restrict__ dY,
                                                                  const int32_t* __restrict__ idx,
@@ -158,9 +173,9 @@ __global__ void __launch_bounds__(256) maxpool_bwd_gather_kernel(PoolDims d,
         for (int ow = ow_lo; ow <= ow_hi; ++ow) {
           const int32_t want = (ih - oh * stride) * pool + (iw - ow * stride);
           const int64_t o = n + N * (c + (int64_t)C * (oh + HO * ow));
-          if (idx[o] == want) g += dY[o];
+          if (idx[o] == want) g += MASK == kMaskOut ? dY[o] * relu_mask(y[o]) : dY[o];
         }
-      if (MASK) g *= relu_mask(y[n + N * pos]);
+      if (MASK == kMaskIn) g *= relu_mask(y[n + N * pos]);
       dX[n + N * pos] = g;
     }
   }
@@ -170,7 +185,7 @@ __global__ void __launch_bounds__(256) maxpool_bwd_gather_kernel(PoolDims d,
 // multiples of pool): each input element lies in exactly one window, so a
 // block per window reads idx/dY once and writes its pool^2 inputs:
 // 0 + dY at the argmax (the reference's zero-fill then add), 0 elsewhere.
-template <bool MASK>
+template <int MASK>
 __global__ void __launch_bounds__(256) maxpool_bwd_tiled_kernel(PoolDims d,
                                                                 const float* __restrict__ dY,
                                                                 const int32_t* __restrict__ idx,
@@ -184,12 +199,13 @@ __global__ void __launch_bounds__(256) maxpool_bwd_tiled_kernel(PoolDims d,
     const int64_t base = N * c + sh * (oh * pool) + sw * (ow * pool);
     for (int64_t n = threadIdx.x; n < N; n += blockDim.x) {
       const int32_t mi = idx[n + N * pos];
-      const float gy = 0.f + dY[n + N * pos];
+      float gy = 0.f + dY[n + N * pos];
+      if (MASK == kMaskOut) gy *= relu_mask(y[n + N * pos]);
       for (int ph = 0; ph < pool; ++ph)
         for (int pw = 0; pw < pool; ++pw) {
           const int64_t o = base + n + sh * ph + sw * pw;
           float g = mi == ph * pool + pw ? gy : 0.f;
-          if (MASK) g *= relu_mask(y[o]);
+          if (MASK == kMaskIn) g *= relu_mask(y[o]);
           dX[o] = g;
         }
     }
@@ -213,7 +229,9 @@ unsigned pool_grid(int64_t positions) {
 }
 unsigned pool_threads(int64_t N) { return N >= 256 ? 256u : (unsigned)((N + 63) / 64 * 64); }
 
-int maxpool_backward(const float* dY, const int32_t* idx, const float* y, float* dX, int64_t N,
+// y: null, the pool's input (a ReLU output; mask kMaskIn) or the pool's
+// output (mask kMaskOut), see maxpool_bwd_tiled_vec_kernel.
+int maxpool_backward(const float* dY, const int32_t* idx, const float* y, int mask, float* dX, int64_t N,
                      int64_t C, int64_t H, int64_t W, int64_t pool, int64_t stride,
                      cnhip_stream_t stream, const char* who) {
   PoolDims d;
@@ -222,34 +240,36 @@ int maxpool_backward(const float* dY, const int32_t* idx, const float* y, float*
   CNHIP_REQUIRE(C * H * W < ((int64_t)1 << 31), "%s: too many input positions", who);
   const hipStream_t st = as_stream(stream);
   const unsigned threads = pool_threads(N);
-  // dY and the argmax read per output; dX written (and the ReLU output y
-  // read, when fused) per input
+  // dY and the argmax read per output; dX written per input; the mask's
+  // source read per input (kMaskIn) or per output (kMaskOut)
+  if (!y) mask = kMaskNone;
   const double outs = (double)N * C * d.HO * d.WO, ins = (double)N * C * H * W;
-  HbmTimer timer(y ? "maxpool_bwd_kernel<relu>" : "maxpool_bwd_kernel", 8.0 * outs + (y ? 8.0 : 4.0) * ins, st);
+  const double bytes = 8.0 * outs + 4.0 * ins + (mask == kMaskIn ? 4.0 * ins : mask == kMaskOut ? 4.0 * outs : 0.0);
+  HbmTimer timer(mask == kMaskIn ? "maxpool_bwd_kernel<relu>"
+                 : mask == kMaskOut ? "maxpool_bwd_kernel<relu of output>"
+                                    : "maxpool_bwd_kernel",
+                 bytes, st);
   const bool vec = N % 4 == 0 && aligned16(dY) && aligned16(idx) && aligned16(dX) && (!y || aligned16(y));
-  if (d.stride == d.pool && d.HO * d.pool == H && d.WO * d.pool == W && vec) {
-    const unsigned grid = pool_grid((C * d.HO * d.WO + 3) / 4);
-    if (y)
-      hipLaunchKernelGGL(maxpool_bwd_tiled_vec_kernel<true>, dim3(grid), dim3(256), 0, st, d, dY, idx, y, dX);
-    else
-      hipLaunchKernelGGL(maxpool_bwd_tiled_vec_kernel<false>, dim3(grid), dim3(256), 0, st, d, dY, idx, y, dX);
-  } else if (d.stride == d.pool && d.HO * d.pool == H && d.WO * d.pool == W) {
-    const unsigned grid = pool_grid(C * d.HO * d.WO);
-    if (y)
-      hipLaunchKernelGGL(maxpool_bwd_tiled_kernel<true>, dim3(grid), dim3(threads), 0, st, d, dY,
-                         idx, y, dX);
-    else
-      hipLaunchKernelGGL(maxpool_bwd_tiled_kernel<false>, dim3(grid), dim3(threads), 0, st, d, dY,
-                         idx, y, dX);
-  } else {
-    const unsigned grid = pool_grid(C * H * W);
-    if (y)
-      hipLaunchKernelGGL(maxpool_bwd_gather_kernel<true>, dim3(grid), dim3(threads), 0, st, d,
+  const bool tiled = d.stride == d.pool && d.HO * d.pool == H && d.WO * d.pool == W;
+  auto go = [&](auto mode) {
+    constexpr int M = decltype(mode)::value;
+    if (tiled && vec) {
+      const unsigned grid = pool_grid((C * d.HO * d.WO + 3) / 4);
+      hipLaunchKernelGGL(maxpool_bwd_tiled_vec_kernel<M>, dim3(grid), dim3(256), 0, st, d, dY, idx, y, dX);
+    } else if (tiled) {
+      hipLaunchKernelGGL(maxpool_bwd_tiled_kernel<M>, dim3(pool_grid(C * d.HO * d.WO)), dim3(threads), 0, st, d,
                          dY, idx, y, dX);
-    else
-      hipLaunchKernelGGL(maxpool_bwd_gather_kernel<false>, dim3(grid), dim3(threads), 0, st, d,
-                         dY, idx, y, dX);
-  }
+    } else {
+      hipLaunchKernelGGL(maxpool_bwd_gather_kernel<M>, dim3(pool_grid(C * H * W)), dim3(threads), 0, st, d, dY,
+                         idx, y, dX);
+    }
+  };
+  if (mask == kMaskIn)
+    go(std::integral_constant<int, kMaskIn>{});
+  else if (mask == kMaskOut)
+    go(std::integral_constant<int, kMaskOut>{});
+  else
+    go(std::integral_constant<int, kMaskNone>{});
   return check_launch(who);
 }
 
@@ -282,7 +302,7 @@ int cnhip_maxpool2d_forward(const float* X, float* Y, int32_t* idx, int64_t N, i
 int cnhip_maxpool2d_backward(const float* dY, const int32_t* idx, float* dX, int64_t N, int64_t C,
                              int64_t H, int64_t W, int64_t pool, int64_t stride,
                              cnhip_stream_t stream) {
-  return cnhip::maxpool_backward(dY, idx, nullptr, dX, N, C, H, W, pool, stride, stream,
+  return cnhip::maxpool_backward(dY, idx, nullptr, cnhip::kMaskNone, dX, N, C, H, W, pool, stride, stream,
                                  "cnhip_maxpool2d_backward");
 }
 
@@ -291,7 +311,15 @@ int cnhip_maxpool2d_backward_relu(const float* dY, const int32_t* idx, const flo
                                   int64_t stride, cnhip_stream_t stream) {
   const char* who = "cnhip_maxpool2d_backward_relu";
   CNHIP_REQUIRE(y, "%s: NULL ReLU output", who);
-  return cnhip::maxpool_backward(dY, idx, y, dX, N, C, H, W, pool, stride, stream, who);
+  return cnhip::maxpool_backward(dY, idx, y, cnhip::kMaskIn, dX, N, C, H, W, pool, stride, stream, who);
+}
+
+int cnhip_maxpool2d_backward_relu_pooled(const float* dY, const int32_t* idx, const float* Y, float* dX,
+                                         int64_t N, int64_t C, int64_t H, int64_t W, int64_t pool,
+                                         int64_t stride, cnhip_stream_t stream) {
+  const char* who = "cnhip_maxpool2d_backward_relu_pooled";
+  CNHIP_REQUIRE(Y, "%s: NULL pooled output", who);
+  return cnhip::maxpool_backward(dY, idx, Y, cnhip::kMaskOut, dX, N, C, H, W, pool, stride, stream, who);
 }
 
 }  // extern "C"

@@ -17,6 +17,7 @@
 
 #include "CppNet/core/tensor.hpp"
 #include "CppNet/layers/layer.hpp"
+#include "CppNet/layers/max_pool2d.hpp"
 
 namespace CppNet
 {
@@ -34,6 +35,10 @@ namespace CppNet
             /// forward() followed by ReLU, in the GEMM epilogue; returns the
             /// ReLU output (what the ReLU's backward reads).
             DeviceTensor forward_relu(const DeviceTensor& input);
+            /// forward_relu() followed by `pool`'s forward, in one call where
+            /// the shape allows: returns the pooled output and records the
+            /// forward in `pool` (MaxPool2D::set_fused_forward).
+            DeviceTensor forward_relu_maxpool(const DeviceTensor& input, MaxPool2D& pool);
             DeviceTensor backward(const DeviceTensor& grad_output);
             /// backward() with the input gradient optional: input_grad = false
             /// computes the parameter gradients only and returns an undefined

@@ -31,6 +31,15 @@ namespace CppNet
             /// is this layer's input: dX * [y > 0] in one pass, equal to the
             /// two calls.
             DeviceTensor backward_relu(const DeviceTensor& grad_output, const DeviceTensor& relu_out);
+            /// Records a forward that Conv2D::forward_relu_maxpool ran for this
+            /// layer: its input dims (the conv output's), pooled output and argmax.
+            void set_fused_forward(const std::vector<int64_t>& in_dims, const DeviceTensor& out,
+                                   const DeviceTensor& idx);
+            /// Whether the last forward was fused (no ReLU output was kept).
+            bool fused_forward() const { return fused_out_.defined(); }
+            /// backward_relu() for a fused forward: the ReLU mask from this
+            /// layer's own output.
+            DeviceTensor backward_relu_pooled(const DeviceTensor& grad_output);
             bool is_trainable() const override { return false; }
             void step(Optimizers::Optimizer&, float) override {}
             int get_pool_size() const { return pool_size_; }
@@ -43,6 +52,7 @@ namespace CppNet
             int pool_size_, stride_;
             std::string device_;
             DeviceTensor idx_;
+            DeviceTensor fused_out_;  // pooled output of a fused forward, else undefined
             std::vector<int64_t> in_dims_;
         };
     } // namespace Layers

@@ -109,6 +109,12 @@ def conv2d_forward_relu(X, W, b, Y, N, C, H, Wd, OC, KS, S=1, P=0) -> None:
                H, Wd, OC, KS, S, P, _stream())
 
 
+def conv2d_forward_relu_maxpool(X, W, b, Yp, idx, N, C, H, Wd, OC, KS, S=1, P=0, pool=2, pool_stride=-1) -> None:
+    """Conv2D forward, ReLU and MaxPool2D in one call: Yp the pooled output, idx its argmax."""
+    _capi.call("cnhip_conv2d_forward_relu_maxpool", _p(X, "X"), _p(W, "W"), _p(b, "b"), _p(Yp, "Yp"),
+               _p(idx, "idx"), N, C, H, Wd, OC, KS, S, P, pool, pool_stride, _stream())
+
+
 def conv2d_backward(X, W, dY, grad_W, grad_b, dX, N, C, H, Wd, OC, KS, S=1, P=0) -> None:
     _capi.call("cnhip_conv2d_backward", _p(X, "X"), _p(W, "W"), _p(dY, "dY"), _p(grad_W, "gW"),
                _p(grad_b, "gb"), _p(dX, "dX"), N, C, H, Wd, OC, KS, S, P, _stream())
@@ -127,6 +133,12 @@ def maxpool2d_backward(dY, idx, dX, N, C, H, W, pool=2, stride=-1) -> None:
 def maxpool2d_backward_relu(dY, idx, y, dX, N, C, H, W, pool=2, stride=-1) -> None:
     """MaxPool2D backward times the mask [y > 0] of the ReLU output y feeding the pool."""
     _capi.call("cnhip_maxpool2d_backward_relu", _p(dY, "dY"), _p(idx, "idx"), _p(y, "y"),
+               _p(dX, "dX"), N, C, H, W, pool, stride, _stream())
+
+
+def maxpool2d_backward_relu_pooled(dY, idx, Y, dX, N, C, H, W, pool=2, stride=-1) -> None:
+    """MaxPool2D backward times the ReLU mask, taken from the pool's output Y."""
+    _capi.call("cnhip_maxpool2d_backward_relu_pooled", _p(dY, "dY"), _p(idx, "idx"), _p(Y, "Y"),
                _p(dX, "dX"), N, C, H, W, pool, stride, _stream())
 
 

@@ -233,6 +233,20 @@ int cnhip_conv2d_forward(const float* X, const float* W, const float* b, float* 
 int cnhip_conv2d_forward_relu(const float* X, const float* W, const float* b, float* Y,
                               int64_t N, int64_t C, int64_t H, int64_t Wd, int64_t OC,
                               int64_t KS, int64_t S, int64_t P, cnhip_stream_t stream);
+/* Conv2D forward, ReLU and MaxPool2D in one call: Yp = maxpool(max(0,
+ * conv(X) + b)) [N,OC,HP,WP] and idx its int32 argmax, bit-identical to
+ * cnhip_conv2d_forward_relu then cnhip_maxpool2d_forward (pool_stride <= 0
+ * means pool).  The ReLU output is not kept: the pool's backward takes its
+ * mask from Yp (cnhip_maxpool2d_backward_relu_pooled).  Replaces the three
+ * forwards Conv2D::forward (conv2d.cpp:78-130), the 4-D ReLU::forward
+ * (relu.cpp:128-160) and MaxPool2D::forward (max_pool2d.cpp:32-95) of a
+ * Conv2D -> ReLU -> MaxPool2D stack.  One kernel for short contractions
+ * (C*KS*KS <= 32, OC % 32 == 0, N % 64 == 0, pool_stride == pool <= 4
+ * tiling the conv output), otherwise the two steps through a workspace. */
+int cnhip_conv2d_forward_relu_maxpool(const float* X, const float* W, const float* b, float* Yp,
+                                      int32_t* idx, int64_t N, int64_t C, int64_t H, int64_t Wd,
+                                      int64_t OC, int64_t KS, int64_t S, int64_t P, int64_t pool,
+                                      int64_t pool_stride, cnhip_stream_t stream);
 int cnhip_conv2d_backward(const float* X, const float* W, const float* dY,
                           float* grad_W, float* grad_b, float* dX, int64_t N, int64_t C,
                           int64_t H, int64_t Wd, int64_t OC, int64_t KS, int64_t S,
@@ -258,6 +272,15 @@ int cnhip_maxpool2d_backward(const float* dY, const int32_t* idx, float* dX, int
 int cnhip_maxpool2d_backward_relu(const float* dY, const int32_t* idx, const float* y, float* dX,
                                   int64_t N, int64_t C, int64_t H, int64_t W, int64_t pool,
                                   int64_t stride, cnhip_stream_t stream);
+/* The same with the ReLU mask taken from the pool's output Y [N,C,HO,WO]
+ * (whose value at a window is the ReLU output at its argmax): dX equals
+ * cnhip_maxpool2d_backward_relu's (bit for bit when the windows tile the
+ * input; where overlapping windows add several terms the masked ones are
+ * zeros).  For the output of cnhip_conv2d_forward_relu_maxpool.
+ * ref: as cnhip_maxpool2d_backward_relu. */
+int cnhip_maxpool2d_backward_relu_pooled(const float* dY, const int32_t* idx, const float* Y, float* dX,
+                                         int64_t N, int64_t C, int64_t H, int64_t W, int64_t pool,
+                                         int64_t stride, cnhip_stream_t stream);
 
 /* ---- recurrent layers ----------------------------------------------------
  * X [B,S,I], Y [B,S,H] ColMajor (row n + B*t of a [B*S, .] matrix).

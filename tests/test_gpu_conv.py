@@ -134,3 +134,49 @@ def test_maxpool_vs_oracle(gpu, oracle, N, C, H, W, p, s):
     dXr = torch.full((N * C * H * W,), 3.0, device="cuda")
     ops.maxpool2d_backward_relu(dev(dY), I, dev(X), dXr, N, C, H, W, p, s)
     np.testing.assert_array_equal(host(dXr), host(dX) * (X > 0).astype(np.float32))
+
+
+# Conv2D -> ReLU -> MaxPool2D in one call: the short-contraction fused kernel
+# (C*KS^2 <= 32, OC % 32 == 0, N % 64 == 0, pool == stride tiling the conv
+# output: config 3's first layer, 2 channel chunks, an unpadded conv, pool 3)
+# and the two-step path of every other shape (config 3's second layer, ragged
+# batch and channels, a pool that does not tile, overlapping windows)
+FUSED_POOL_CASES = [(256, 3, 32, 32, 32, 3, 1, 1, 2, -1), (64, 3, 16, 16, 64, 3, 1, 1, 2, -1),
+                    (128, 2, 12, 12, 32, 3, 1, 0, 2, -1), (64, 3, 18, 18, 32, 3, 1, 1, 3, -1),
+                    (64, 32, 16, 16, 64, 3, 1, 1, 2, -1), (20, 3, 9, 9, 8, 3, 1, 1, 2, -1),
+                    (64, 3, 11, 11, 32, 3, 1, 1, 3, 2)]
+
+
+@pytest.mark.parametrize("N,C,H,W,OC,KS,S,P,p,ps", FUSED_POOL_CASES)
+def test_conv_relu_maxpool_fused(gpu, N, C, H, W, OC, KS, S, P, p, ps):
+    """cnhip_conv2d_forward_relu_maxpool against conv + ReLU then max-pool
+    (pooled output and argmax bit for bit), and the pool's backward with the
+    mask taken from its output against the mask taken from the ReLU output."""
+    from cppnet_amd import ops
+    print(f"[conv-relu-pool] N={N} C={C} H={H} W={W} OC={OC} KS={KS} S={S} P={P} pool={p} stride={ps}", flush=True)
+    rng = np.random.default_rng(N + C + H + OC + p)
+    X = rng.standard_normal(N * C * H * W).astype(np.float32)
+    # quantised weights: exact ties and exact zeros after the ReLU
+    Wt = (rng.integers(-3, 4, OC * C * KS * KS) * 0.25).astype(np.float32)
+    b = (rng.integers(-2, 3, OC) * 0.5).astype(np.float32)
+    HO, WO = (H + 2 * P - KS) // S + 1, (W + 2 * P - KS) // S + 1
+    st = ps if ps > 0 else p
+    HP, WP = (HO - p) // st + 1, (WO - p) // st + 1
+    Y1 = torch.empty(N * OC * HO * WO, device="cuda")
+    ops.conv2d_forward_relu(dev(X), dev(Wt), dev(b), Y1, N, C, H, W, OC, KS, S, P)
+    Yp, I = torch.empty(N * OC * HP * WP, device="cuda"), torch.empty(N * OC * HP * WP, dtype=torch.int32, device="cuda")
+    ops.maxpool2d_forward(Y1, Yp, I, N, OC, HO, WO, p, ps)
+    Fp = torch.full((N * OC * HP * WP,), 7.0, device="cuda")
+    FI = torch.full((N * OC * HP * WP,), -1, dtype=torch.int32, device="cuda")
+    ops.conv2d_forward_relu_maxpool(dev(X), dev(Wt), dev(b), Fp, FI, N, C, H, W, OC, KS, S, P, p, ps)
+    assert np.array_equal(host(Fp).view(np.uint32), host(Yp).view(np.uint32))
+    assert np.array_equal(host(FI), host(I))
+    dYp = rng.standard_normal(N * OC * HP * WP).astype(np.float32)
+    dA = torch.full((N * OC * HO * WO,), 3.0, device="cuda")
+    dB = torch.full((N * OC * HO * WO,), 5.0, device="cuda")
+    ops.maxpool2d_backward_relu(dev(dYp), I, Y1, dA, N, OC, HO, WO, p, ps)
+    ops.maxpool2d_backward_relu_pooled(dev(dYp), FI, Fp, dB, N, OC, HO, WO, p, ps)
+    if st == p and HP * p == HO and WP * p == WO:
+        assert np.array_equal(host(dB).view(np.uint32), host(dA).view(np.uint32))
+    else:
+        np.testing.assert_array_equal(host(dB), host(dA))
