@@ -388,6 +388,9 @@ struct LstmFwdPersistArgs {
   u64* ex;  // [2 slots][nst][H][16]: h_t of (unit, sample), stamp of step t + 1
   int B, S, nst;
   PersistSync sync;
+  // input projection computed in the kernel (IT > 0): X [B*S, I], W_ih [I, 4H]
+  const float* X;
+  const float* W_ih;
 };
 
 // Forward, t = 0 .. S-1.  Per step t >= 1 a block waits for h_{t-1} of its
@@ -438,11 +441,22 @@ __device__ __forceinline__ f32x4 xpose_lanes4(f32x4 v, int lane) {
   return v;
 }
 
-template <int H>
+// IT > 0 (I = 64 IT inputs): the kernel also computes the input projection
+// x_t W_ih of its 16 samples and 64 columns (the GEMM it replaces wrote all
+// B S x 4H pre-activations only for this kernel to read them back).  Each
+// block holds its W_ih slice in registers like the W_hh slice; x_t is staged
+// in LDS (double-buffered, two 16-byte loads per thread) one step ahead and
+// published by the step's vote; its 4 I/16 MFMAs per wave run while the
+// block waits for h_{t-1}.  The x term has its own accumulator, so the gate
+// is still (recurrent + x W_ih) + bias.
+template <int H, int IT>
 __global__ void __launch_bounds__(256) lstm_fwd_persist_kernel(LstmFwdPersistArgs a) {
   constexpr int NKB = H / 16;  // k-blocks; also the words per thread of h_{t-1}
   constexpr int NUT = H / kPt;
+  constexpr bool FUSE = IT > 0;
+  constexpr int I = 64 * IT, NKX = I / 16;  // inputs; their k-blocks
   __shared__ __align__(16) f32x4 hs[H / 4 * kPt];  // h_{t-1}: [k/4][sample], k..k+3
+  __shared__ __align__(16) f32x4 xs[FUSE ? 2 * I / 4 * kPt : 1];  // x_t, [t & 1][i/4][sample]
   __shared__ int place[2];
   int st, ut;
   if (!persist_place(a.sync, NUT, st, ut, place)) return;
@@ -466,13 +480,63 @@ __global__ void __launch_bounds__(256) lstm_fwd_persist_kernel(LstmFwdPersistArg
   u64* const ex = a.ex + (int64_t)st * H * kPt;
   const __amdgpu_buffer_rsrc_t rs = ex_rsrc(ex);
   const unsigned slot_bytes = (unsigned)a.nst * H * kPt * 8u;
-  float xi, xf, xg, xo;  // this step's x W_ih terms (no dependence on the recurrence)
-  {
+  float xi = 0.f, xf = 0.f, xg = 0.f, xo = 0.f;  // this step's x W_ih terms
+  if constexpr (!FUSE) {
     const float* g = a.gates + n;
     xi = g[BS * d];
     xf = g[BS * (d + H)];
     xg = g[BS * (d + 2 * H)];
     xo = g[BS * (d + 3 * H)];
+  }
+  // W_ih(i, column (r / 4) H + j0 + 4 wave + r % 4) for i = 16 kb + 4 q + e
+  f32x4 wi[FUSE ? NKX : 1];
+  // staging of x_t: thread tid loads samples b0 + 4 g .. + 3 of input i,
+  // (i, g) = ((tid + 256 j) / 4, (tid + 256 j) % 4), j < IT
+  f32x4 xr[FUSE ? IT : 1];
+  float* xsf = reinterpret_cast<float*>(xs);
+  auto x_issue = [&](int t) {
+    if constexpr (FUSE) {
+#pragma unroll
+      for (int j = 0; j < IT; ++j) {
+        const int e = tid + 256 * j, i = e >> 2, g = e & 3;
+        xr[j] = *reinterpret_cast<const f32x4*>(a.X + b0 + 4 * g + (int64_t)B * t + BS * i);
+      }
+    }
+  };
+  auto x_write = [&](int buf) {
+    if constexpr (FUSE) {
+#pragma unroll
+      for (int j = 0; j < IT; ++j) {
+        const int e = tid + 256 * j, i = e >> 2, g = e & 3;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) xsf[((buf * (I / 4) + (i >> 2)) * kPt + 4 * g + v) * 4 + (i & 3)] = xr[j][v];
+      }
+    }
+  };
+  // acc[i]: x_t W_ih of sample 4 q + i, this wave's column r
+  auto x_mfma = [&](int buf) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (FUSE) {
+#pragma unroll
+      for (int kb = 0; kb < NKX; ++kb) {
+        const f32x4 x4 = xs[(buf * (I / 4) + 4 * kb + q) * kPt + r];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(x4[e], wi[kb][e], acc, 0, 0, 0);
+      }
+    }
+    return acc;
+  };
+  if constexpr (FUSE) {
+    const float* wc = a.W_ih + (int64_t)I * ((int64_t)(r >> 2) * H + j0 + 4 * wave + (r & 3)) + 4 * q;
+#pragma unroll
+    for (int kb = 0; kb < NKX; ++kb) wi[kb] = *reinterpret_cast<const f32x4*>(wc + 16 * kb);
+    x_issue(0);
+    x_write(0);
+    if (a.S > 1) {
+      x_issue(1);
+      x_write(1);
+    }
+    __syncthreads();
   }
   float c_prev = 0.0f;
   float* hsf = reinterpret_cast<float*>(hs);
@@ -480,6 +544,13 @@ __global__ void __launch_bounds__(256) lstm_fwd_persist_kernel(LstmFwdPersistArg
     const int64_t row = n + (int64_t)B * t;
     float ig, fg, gg, og;
     if (t == 0) {  // h_0 = c_0 = 0 (lstm_cell_fwd0_kernel's arithmetic)
+      if constexpr (FUSE) {
+        const f32x4 ax = xpose_lanes4(x_mfma(0), lane);
+        xi = ax[0];
+        xf = ax[1];
+        xg = ax[2];
+        xo = ax[3];
+      }
       ig = sigm(xi + bi);
       fg = sigm(xf + bf);
       gg = tanhf(xg + bg);
@@ -490,7 +561,11 @@ __global__ void __launch_bounds__(256) lstm_fwd_persist_kernel(LstmFwdPersistArg
       // + j 4096)
       u32x4 w[NKB / 2];
       const unsigned voff = (unsigned)tid * 16u, soff = ((t - 1) & 1) * slot_bytes;
+      // x_{t+1} staged while waiting: its loads go first, written to the
+      // other buffer (last read at step t - 1, before that step's vote)
+      if (t + 1 < a.S) x_issue(t + 1);
       ex_issue<NKB / 2, 256 * 16, kFirstPollSleep>(rs, voff, soff, w);
+      const f32x4 axr = x_mfma(t & 1);
       const bool ok = ex_finish<NKB / 2, 256 * 16>(a.sync, rs, voff, soff, ex_stamp(a.sync, t), w);
 #pragma unroll
       for (int j = 0; j < NKB / 2; ++j) {
@@ -498,7 +573,15 @@ __global__ void __launch_bounds__(256) lstm_fwd_persist_kernel(LstmFwdPersistArg
         hsf[((k >> 2) * kPt + s2) * 4 + (k & 3)] = __uint_as_float(w[j].x);
         hsf[((k >> 2) * kPt + s2 + 1) * 4 + (k & 3)] = __uint_as_float(w[j].z);
       }
+      if (t + 1 < a.S) x_write((t + 1) & 1);
       if (__syncthreads_or(!ok)) return;
+      if constexpr (FUSE) {
+        const f32x4 ax = xpose_lanes4(axr, lane);
+        xi = ax[0];
+        xf = ax[1];
+        xg = ax[2];
+        xo = ax[3];
+      }
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb) {
@@ -529,7 +612,7 @@ __global__ void __launch_bounds__(256) lstm_fwd_persist_kernel(LstmFwdPersistArg
     a.tanh_c[row + BS * d] = tc;
     a.Y[row + BS * d] = h;
     c_prev = ct;
-    if (t + 1 < a.S) {
+    if (!FUSE && t + 1 < a.S) {
       const float* gn = g + B;
       xi = gn[BS * d];
       xf = gn[BS * (d + H)];
@@ -1288,7 +1371,14 @@ bool persist_shape(int64_t B, int64_t S, int64_t H, int64_t& nst, int64_t& nut, 
 }
 
 template <int H>
-const void* fwd_persist_kernel() { return reinterpret_cast<const void*>(&lstm_fwd_persist_kernel<H>); }
+const void* fwd_persist_kernel(int it) {
+  switch (it) {
+    case 0: return reinterpret_cast<const void*>(&lstm_fwd_persist_kernel<H, 0>);
+    case 1: return reinterpret_cast<const void*>(&lstm_fwd_persist_kernel<H, 1>);
+    case 2: return reinterpret_cast<const void*>(&lstm_fwd_persist_kernel<H, 2>);
+    default: return nullptr;
+  }
+}
 template <int H>
 const void* bwd_persist_kernel(int it) {
   switch (it) {
@@ -1299,17 +1389,27 @@ const void* bwd_persist_kernel(int it) {
   }
 }
 
-// The instantiated hidden sizes (W_hh slice of H/4 registers per lane) and,
-// for the backward, input widths I = 64 it with the weight gradients fused
-// (it = 0: not fused).
+// The instantiated hidden sizes (W_hh slice of H/4 registers per lane) and
+// input widths I = 64 it whose input projection (forward) or weight
+// gradients (backward) the kernel computes itself (it = 0: not fused).
 const void* persist_kernel(bool fwd, int64_t H, int it = 0) {
   switch (H) {
-    case 64: return fwd ? fwd_persist_kernel<64>() : bwd_persist_kernel<64>(it);
-    case 128: return fwd ? fwd_persist_kernel<128>() : bwd_persist_kernel<128>(it);
-    case 256: return fwd ? fwd_persist_kernel<256>() : bwd_persist_kernel<256>(it);
-    case 512: return fwd ? fwd_persist_kernel<512>() : bwd_persist_kernel<512>(it);
+    case 64: return fwd ? fwd_persist_kernel<64>(it) : bwd_persist_kernel<64>(it);
+    case 128: return fwd ? fwd_persist_kernel<128>(it) : bwd_persist_kernel<128>(it);
+    case 256: return fwd ? fwd_persist_kernel<256>(it) : bwd_persist_kernel<256>(it);
+    case 512: return fwd ? fwd_persist_kernel<512>(it) : bwd_persist_kernel<512>(it);
     default: return nullptr;
   }
+}
+
+// Whether the persistent forward can compute the input projection itself
+// (CNHIP_RECURRENCE_FUSED_X=0 turns it off): I a multiple of 64 up to 128,
+// X and W_ih 16-byte aligned.  Returns I / 64, or 0.
+int fwd_fused_inputs(const float* X, const float* W_ih, int64_t I) {
+  const char* e = std::getenv("CNHIP_RECURRENCE_FUSED_X");
+  if (e && e[0] == '0') return 0;
+  if (I % 64 != 0 || I / 64 > 2 || !aligned16(X) || !aligned16(W_ih)) return 0;
+  return (int)(I / 64);
 }
 
 // Whether the persistent backward can also accumulate the weight gradients
@@ -1368,17 +1468,25 @@ int lstm_bwd_persistent(const float* gates, const float* c, const float* tanh_c,
 }
 
 // The whole forward recurrence (t = 0 .. S-1) in one persistent launch, when
-// the shape suits it: returns false to fall back to the per-step launches.
+// the shape suits it; false in *done to fall back to the per-step launches.
+// fused: the launch that also computes the input projection (the caller has
+// not run the GEMM), tried only where fwd_fused_inputs allows it; otherwise
+// the launch that reads the projection from gates.
 int lstm_fwd_persistent(float* gates, const float* b, float* c, float* tanh_c, float* Y, const float* W_hh,
-                        int64_t B, int64_t S, int64_t H, hipStream_t st, const char* who, bool* done) {
+                        const float* X, const float* W_ih, int64_t I, bool fused, int64_t B, int64_t S, int64_t H,
+                        hipStream_t st, const char* who, bool* done) {
   *done = false;
   int64_t nst, nut, grid;
-  const void* kern = persist_kernel(true, H);
+  const int it = fused ? fwd_fused_inputs(X, W_ih, I) : 0;
+  if (fused && !it) return CNHIP_OK;
+  const void* kern = persist_kernel(true, H, it);
   if (!persist_enabled() || !kern || !persist_shape(B, S, H, nst, nut, grid) || !aligned16(W_hh)) return CNHIP_OK;
   const size_t ex_bytes = (size_t)2 * nst * H * kPt * sizeof(u64);
   if (ex_bytes > 0x7fffffffu || !persist_fits(kern, grid, 256, who)) return CNHIP_OK;
-  LstmFwdPersistArgs args{gates, b, c, tanh_c, Y, W_hh, nullptr, (int)B, (int)S, (int)nst, {}};
-  TimingRec* rec = timing_slot(2.0 * B * 4 * H * H * (double)(S - 1));
+  LstmFwdPersistArgs args{gates, b, c, tanh_c, Y, W_hh, nullptr, (int)B, (int)S, (int)nst, {}, X, W_ih};
+  double flops = 2.0 * B * 4 * H * H * (double)(S - 1);
+  if (it) flops += 2.0 * B * 4 * H * I * (double)S;
+  TimingRec* rec = timing_slot(flops);
   if (rec) (void)hipEventRecord(rec->start, st);
   CNHIP_TRY(persist_launch(kern, grid, 256, args, ex_bytes, st, who));
   if (rec) (void)hipEventRecord(rec->stop, st);
@@ -1419,9 +1527,11 @@ int cnhip_lstm_forward(const float* X, const float* W_ih, const float* W_hh, con
   CNHIP_TRY(cnhip::persist_take_fault(who));
   hipStream_t st = as_stream(stream);
   const int64_t G = 4 * H, BS = B * S;
-  CNHIP_TRY(cnhip::gemm_f32(0, 0, BS, G, I, 1.f, X, BS, W_ih, I, 0.f, gates, BS, nullptr, 0, st, who));
   bool done = false;
-  CNHIP_TRY(cnhip::lstm_fwd_persistent(gates, b, c, tanh_c, Y, W_hh, B, S, H, st, who, &done));
+  CNHIP_TRY(cnhip::lstm_fwd_persistent(gates, b, c, tanh_c, Y, W_hh, X, W_ih, I, true, B, S, H, st, who, &done));
+  if (done) return CNHIP_OK;
+  CNHIP_TRY(cnhip::gemm_f32(0, 0, BS, G, I, 1.f, X, BS, W_ih, I, 0.f, gates, BS, nullptr, 0, st, who));
+  CNHIP_TRY(cnhip::lstm_fwd_persistent(gates, b, c, tanh_c, Y, W_hh, X, W_ih, I, false, B, S, H, st, who, &done));
   if (done) return CNHIP_OK;
   // t = 0: h_0 = 0, no recurrent term; then one fused GEMM + cell launch per step
   hipLaunchKernelGGL(cnhip::lstm_cell_fwd0_kernel, dim3(cnhip::cell_grid(B, H)), dim3(256), 0, st,

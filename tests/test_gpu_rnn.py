@@ -54,12 +54,13 @@ def test_lstm_vs_oracle(gpu, oracle, monkeypatch, B, S, I, H, path):
     """Both recurrence paths -- one persistent launch for all timesteps, or
     one launch per timestep -- against the oracle (they sum the recurrent
     products in different orders, so each is held to the oracle's bars).
-    The persistent backward accumulates the weight gradients itself where I
-    is 64 or 128 ("persistent"), or leaves them to the GEMMs
-    ("persistent-unfused")."""
+    Where I is 64 or 128 the persistent forward computes the input
+    projection and the persistent backward the weight gradients itself
+    ("persistent"), or leaves them to the GEMMs ("persistent-unfused")."""
     print(f"[lstm] B={B} S={S} I={I} H={H} {path}", flush=True)
     monkeypatch.setenv("CNHIP_RECURRENCE_PERSISTENT", "0" if path == "per-step" else "1")
     monkeypatch.setenv("CNHIP_RECURRENCE_FUSED_DW", "0" if path == "persistent-unfused" else "1")
+    monkeypatch.setenv("CNHIP_RECURRENCE_FUSED_X", "0" if path == "persistent-unfused" else "1")
     oracle.cnref_set_threads(16)
     rng = np.random.default_rng(B + S + I + H)
     X, Wih, Whh, b, dY = _inputs(rng, B, S, I, H, 4)
