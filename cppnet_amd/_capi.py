@@ -71,6 +71,7 @@ SIGNATURES: dict[str, tuple] = {
     "cnhip_maxpool2d_backward_relu_pooled": (i32, [vp, vp, vp, vp] + [i64] * 6 + [vp]),
     "cnhip_lstm_forward": (i32, [vp] * 8 + [i64] * 4 + [vp]),
     "cnhip_lstm_backward": (i32, [vp] * 12 + [i64] * 4 + [vp]),
+    "cnhip_lstm_backward_last": (i32, [vp] * 12 + [i64] * 4 + [vp]),
     "cnhip_gru_forward": (i32, [vp] * 7 + [i64] * 4 + [vp]),
     "cnhip_gru_backward": (i32, [vp] * 11 + [i64] * 4 + [vp]),
     "cnhip_seq_select": (i32, [vp, vp, i64, i64, i64, i64, vp]),

@@ -92,6 +92,17 @@ namespace CppNet
             for (std::size_t k = end; k-- > first;)
             {
                 if (k == first && !input_grad) return steps_[k]->backward_no_input_grad(g);
+                // LSTM -> SequenceLast: the LSTM takes the last step's gradient
+                // as it is, without the zeros of the other steps
+                Layers::LSTM* lstm = k > first && steps_[k]->sequence_last() ? steps_[k - 1]->lstm() : nullptr;
+                if (lstm)
+                {
+                    const bool dx = input_grad || k - 1 > first;
+                    g = lstm->backward_last(g, dx);
+                    if (!dx) return g;
+                    --k;
+                    continue;
+                }
                 Activations::Activation* prev = k > first ? steps_[k - 1]->activation() : nullptr;
                 auto* relu = dynamic_cast<Activations::ReLU*>(prev);
                 Layers::MaxPool2D* fused_mp = steps_[k]->maxpool();

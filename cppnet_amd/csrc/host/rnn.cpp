@@ -126,6 +126,23 @@ namespace CppNet
             return dx;
         }
 
+        DeviceTensor LSTM::backward_last(const DeviceTensor& g, bool input_grad)
+        {
+            if (!out_cache_.defined()) throw std::runtime_error("LSTM::backward before forward");
+            const int64_t B = out_cache_.dimension(0), S = out_cache_.dimension(1);
+            if (g.rank() != 2 || g.dimension(0) != B || g.dimension(1) != hidden_size_)
+                throw std::runtime_error("LSTM::backward_last: grad shape mismatch");
+            DeviceTensor dx = input_grad ? DeviceTensor::empty(in_cache_.dims()) : DeviceTensor();
+            Device::check(cnhip_lstm_backward_last(in_cache_.data(), W_ih_.data(), W_hh_.data(), out_cache_.data(),
+                                                   gates_cache_.data(), c_cache_.data(), tanh_c_cache_.data(),
+                                                   g.data(), gW_ih_.data(), gW_hh_.data(), gb_.data(),
+                                                   input_grad ? dx.data() : nullptr, B, S, input_size_, hidden_size_,
+                                                   Device::stream()),
+                          "LSTM::backward_last");
+            grads_zero_ = false;
+            return dx;
+        }
+
         Tensor<float, 3> LSTM::forward(const Tensor<float, 3>& x)
         {
             return forward(DeviceTensor::from_host(x)).to_host<float, 3>();

@@ -638,6 +638,7 @@ struct LstmBwdPersistArgs {
   const float* Y;
   float* part;
   int I;
+  int dy_last;  // dY is [B, H], the gradient of the last step only (0 at the others)
 };
 
 // Backward through time, t = S-1 .. 0.  The recurrent term dG_{t+1} W_hh^T
@@ -777,7 +778,7 @@ __global__ void __launch_bounds__(256) lstm_bwd_persist_kernel(LstmBwdPersistArg
     og = a.gates[row + BS * (d + 3 * H)];
     tc = a.tanh_c[row + BS * d];
     cprev = t > 0 ? a.c[row - B + BS * d] : 0.0f;
-    dy = a.dY[row + BS * d];
+    dy = !a.dy_last ? a.dY[row + BS * d] : t == S - 1 ? a.dY[n + (int64_t)B * d] : 0.0f;
   };
   load_step(S - 1);
   if constexpr (FUSE) {
@@ -1187,6 +1188,7 @@ int lstm_bwd_steps(const float* gates, const float* c, const float* tanh_c, cons
 
 // ---- persistent-launch plumbing
 constexpr int kScratchRecur = 2;  // scratch slot of the fault word and the exchange area
+constexpr int kScratchSeq = 3;    // scratch slot of a last-step gradient spread over all steps
 
 // Per device: the epoch of the next launch, and the exchange buffers
 // (scratch allocations) zeroed or run in since the counter last started
@@ -1427,7 +1429,7 @@ int bwd_fused_inputs(const float* X, const float* Y, int64_t I) {
 // it (dG: [B*S, 4H], fully written); false in *done to fall back.  With
 // `part` (nst (4H^2 + 4HI + 4H) floats) the launch also accumulates the
 // weight gradients and a reduction writes gW_hh, gW_ih and gb (*fused).
-int lstm_bwd_persistent(const float* gates, const float* c, const float* tanh_c, const float* dY,
+int lstm_bwd_persistent(const float* gates, const float* c, const float* tanh_c, const float* dY, bool dy_last,
                         const float* W_hh, float* dG, const float* X, const float* Y, float* part, int64_t I,
                         float* gW_hh, float* gW_ih, float* gb, int64_t B, int64_t S, int64_t H, hipStream_t st,
                         const char* who, bool* done, bool* fused) {
@@ -1446,7 +1448,7 @@ int lstm_bwd_persistent(const float* gates, const float* c, const float* tanh_c,
   }
   if (!persist_fits(kern, grid, 256, who)) return CNHIP_OK;
   LstmBwdPersistArgs args{gates, c, tanh_c, dY, W_hh, dG, nullptr, (int)B, (int)S, (int)nst, {},
-                          X, Y, it ? part : nullptr, (int)I};
+                          X, Y, it ? part : nullptr, (int)I, dy_last ? 1 : 0};
   const double G = 4.0 * H;
   double flops = 2.0 * B * G * H * (double)(S - 1);
   if (it) flops += 2.0 * H * G * B * (double)(S - 1) + 2.0 * I * G * B * (double)S;
@@ -1511,6 +1513,56 @@ struct Workspace {
   }
 };
 
+// BPTT of the LSTM (lstm.cpp:184-253).  dy_last: dY is [B, H], the
+// gradient of the last step's output only (a SequenceLast after the layer);
+// the persistent kernel reads it as such, the per-step path from a [B, S, H]
+// copy with zeros elsewhere.
+int lstm_backward(const float* X, const float* W_ih, const float* W_hh, const float* Y, const float* gates,
+                  const float* c, const float* tanh_c, const float* dY, bool dy_last, float* gW_ih, float* gW_hh,
+                  float* gb, float* dX, int64_t B, int64_t S, int64_t I, int64_t H, hipStream_t st,
+                  const char* who) {
+  CNHIP_TRY(check_rnn(B, S, I, H, who));
+  CNHIP_REQUIRE(X && W_ih && W_hh && Y && gates && c && tanh_c && dY && gW_ih && gW_hh && gb,
+                "%s: NULL pointer", who);
+  CNHIP_TRY(persist_take_fault(who));
+  const int64_t G = 4 * H, BS = B * S;
+  Workspace ws(st);
+  // dG, dc and, for the fused weight gradients, one partial per 16-sample tile
+  const int64_t n_part = bwd_fused_inputs(X, Y, I) ? (B / 16) * (G * H + G * I + G) : 0;
+  CNHIP_TRY(ws.alloc((size_t)(BS * G + B * H + n_part) * sizeof(float), who));
+  float* dG = static_cast<float*>(ws.p);
+  float* dc = dG + BS * G;
+  float* part = n_part ? dc + B * H : nullptr;
+  bool done = false, fused = false;
+  CNHIP_TRY(lstm_bwd_persistent(gates, c, tanh_c, dY, dy_last, W_hh, dG, X, Y, part, I, gW_hh, gW_ih, gb, B, S, H,
+                                st, who, &done, &fused));
+  if (!done) {
+    const float* dYs = dY;
+    if (dy_last) {
+      void* p = nullptr;
+      CNHIP_TRY(scratch(st, kScratchSeq, (size_t)BS * H * sizeof(float), &p, who));
+      float* full = static_cast<float*>(p);
+      hipLaunchKernelGGL(seq_scatter_kernel, dim3(elementwise_grid(BS * H, 256)), dim3(256), 0, st, dY, full, B,
+                         S, H, S - 1);
+      CNHIP_TRY(check_launch(who));
+      dYs = full;
+    }
+    // t = S-1: dh = dY only; then per step one fused launch of
+    // dh_t = dY_t + dG_{t+1} W_hh^T (lstm.cpp:244) and the cell backward
+    hipLaunchKernelGGL(lstm_cell_bwd_last_kernel, dim3(cell_grid(B, H)), dim3(256), 0, st, gates, c, tanh_c, dYs,
+                       dc, dG, B, S, H);
+    CNHIP_TRY(check_launch(who));
+    CNHIP_TRY(lstm_bwd_steps<LstmBwdCfgDefault>(gates, c, tanh_c, dYs, W_hh, dc, dG, B, S, H, st, who));
+  }
+  if (!fused) {
+    CNHIP_TRY(gemm_f32(1, 0, I, G, BS, 1.f, X, BS, dG, BS, 0.f, gW_ih, I, nullptr, 0, st, who));
+    CNHIP_TRY(gemm_f32(1, 0, H, G, B * (S - 1), 1.f, Y, BS, dG + B, BS, 0.f, gW_hh, H, nullptr, 0, st, who));
+    CNHIP_TRY(column_sum(dG, gb, BS, G, 0, st, who));
+  }
+  if (dX) CNHIP_TRY(gemm_f32(0, 1, BS, I, G, 1.f, dG, BS, W_ih, I, 0.f, dX, BS, nullptr, 0, st, who));
+  return CNHIP_OK;
+}
+
 }  // namespace
 }  // namespace cnhip
 
@@ -1544,41 +1596,16 @@ int cnhip_lstm_backward(const float* X, const float* W_ih, const float* W_hh, co
                         const float* gates, const float* c, const float* tanh_c, const float* dY,
                         float* gW_ih, float* gW_hh, float* gb, float* dX, int64_t B, int64_t S,
                         int64_t I, int64_t H, cnhip_stream_t stream) {
-  const char* who = "cnhip_lstm_backward";
-  CNHIP_TRY(cnhip::check_rnn(B, S, I, H, who));
-  CNHIP_REQUIRE(X && W_ih && W_hh && Y && gates && c && tanh_c && dY && gW_ih && gW_hh && gb,
-                "%s: NULL pointer", who);
-  CNHIP_TRY(cnhip::persist_take_fault(who));
-  hipStream_t st = as_stream(stream);
-  const int64_t G = 4 * H, BS = B * S;
-  cnhip::Workspace ws(st);
-  // dG, dc and, for the fused weight gradients, one partial per 16-sample tile
-  const int64_t n_part = cnhip::bwd_fused_inputs(X, Y, I) ? (B / 16) * (G * H + G * I + G) : 0;
-  CNHIP_TRY(ws.alloc((size_t)(BS * G + B * H + n_part) * sizeof(float), who));
-  float* dG = static_cast<float*>(ws.p);
-  float* dc = dG + BS * G;
-  float* part = n_part ? dc + B * H : nullptr;
-  bool done = false, fused = false;
-  CNHIP_TRY(cnhip::lstm_bwd_persistent(gates, c, tanh_c, dY, W_hh, dG, X, Y, part, I, gW_hh, gW_ih, gb, B, S, H, st,
-                                       who, &done, &fused));
-  if (!done) {
-    // t = S-1: dh = dY only; then per step one fused launch of
-    // dh_t = dY_t + dG_{t+1} W_hh^T (lstm.cpp:244) and the cell backward
-    hipLaunchKernelGGL(cnhip::lstm_cell_bwd_last_kernel, dim3(cnhip::cell_grid(B, H)), dim3(256), 0,
-                       st, gates, c, tanh_c, dY, dc, dG, B, S, H);
-    CNHIP_TRY(cnhip::check_launch(who));
-    CNHIP_TRY(cnhip::lstm_bwd_steps<cnhip::LstmBwdCfgDefault>(gates, c, tanh_c, dY, W_hh, dc, dG, B, S,
-                                                              H, st, who));
-  }
-  if (!fused) {
-    CNHIP_TRY(cnhip::gemm_f32(1, 0, I, G, BS, 1.f, X, BS, dG, BS, 0.f, gW_ih, I, nullptr, 0, st, who));
-    CNHIP_TRY(cnhip::gemm_f32(1, 0, H, G, B * (S - 1), 1.f, Y, BS, dG + B, BS, 0.f, gW_hh, H, nullptr,
-                              0, st, who));
-    CNHIP_TRY(cnhip::column_sum(dG, gb, BS, G, 0, st, who));
-  }
-  if (dX)
-    CNHIP_TRY(cnhip::gemm_f32(0, 1, BS, I, G, 1.f, dG, BS, W_ih, I, 0.f, dX, BS, nullptr, 0, st, who));
-  return CNHIP_OK;
+  return cnhip::lstm_backward(X, W_ih, W_hh, Y, gates, c, tanh_c, dY, false, gW_ih, gW_hh, gb, dX, B, S, I, H,
+                              as_stream(stream), "cnhip_lstm_backward");
+}
+
+int cnhip_lstm_backward_last(const float* X, const float* W_ih, const float* W_hh, const float* Y,
+                             const float* gates, const float* c, const float* tanh_c, const float* dY_last,
+                             float* gW_ih, float* gW_hh, float* gb, float* dX, int64_t B, int64_t S,
+                             int64_t I, int64_t H, cnhip_stream_t stream) {
+  return cnhip::lstm_backward(X, W_ih, W_hh, Y, gates, c, tanh_c, dY_last, true, gW_ih, gW_hh, gb, dX, B, S, I,
+                              H, as_stream(stream), "cnhip_lstm_backward_last");
 }
 
 int cnhip_gru_forward(const float* X, const float* W_ih, const float* W_hh, const float* b,

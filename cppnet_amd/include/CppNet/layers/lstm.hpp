@@ -78,6 +78,10 @@ namespace CppNet
             /// computes the parameter gradients only and returns an undefined
             /// tensor (a model's first layer, whose input is data).
             DeviceTensor backward(const DeviceTensor& grad_output, bool input_grad);
+            /// backward() for a gradient [B, H] of the last step's output only
+            /// (an LSTM -> SequenceLast stack): equal to SequenceLast's backward
+            /// followed by backward(), without materialising the zeros.
+            DeviceTensor backward_last(const DeviceTensor& grad_last, bool input_grad);
 
         private:
             DeviceTensor c_cache_, tanh_c_cache_;

@@ -28,7 +28,9 @@
 #include "CppNet/activations/activation.hpp"
 #include "CppNet/layers/conv2d.hpp"
 #include "CppNet/layers/linear.hpp"
+#include "CppNet/layers/lstm.hpp"
 #include "CppNet/layers/max_pool2d.hpp"
+#include "CppNet/layers/sequence_last.hpp"
 #include "CppNet/core/tensor.hpp"
 #include "CppNet/layers/layer.hpp"
 #include "CppNet/optimizers/optimizer.hpp"
@@ -50,6 +52,8 @@ namespace CppNet
             virtual Layers::Linear* linear() { return nullptr; }
             virtual Layers::MaxPool2D* maxpool() { return nullptr; }
             virtual Layers::Conv2D* conv2d() { return nullptr; }
+            virtual Layers::LSTM* lstm() { return nullptr; }
+            virtual Layers::SequenceLast* sequence_last() { return nullptr; }
             virtual Activations::Activation* activation() { return nullptr; }
             virtual ~Step() = default;
         };
@@ -84,6 +88,11 @@ namespace CppNet
             Layers::Linear* linear() override { return dynamic_cast<Layers::Linear*>(layer_.get()); }
             Layers::MaxPool2D* maxpool() override { return dynamic_cast<Layers::MaxPool2D*>(layer_.get()); }
             Layers::Conv2D* conv2d() override { return dynamic_cast<Layers::Conv2D*>(layer_.get()); }
+            Layers::LSTM* lstm() override { return dynamic_cast<Layers::LSTM*>(layer_.get()); }
+            Layers::SequenceLast* sequence_last() override
+            {
+                return dynamic_cast<Layers::SequenceLast*>(layer_.get());
+            }
 
         private:
             std::shared_ptr<LayerT> layer_;

@@ -153,6 +153,13 @@ def lstm_backward(X, W_ih, W_hh, Y, gates, c, tanh_c, dY, gW_ih, gW_hh, gb, dX, 
                _stream())
 
 
+def lstm_backward_last(X, W_ih, W_hh, Y, gates, c, tanh_c, dY_last, gW_ih, gW_hh, gb, dX, B, S, I, H):
+    """lstm_backward for a gradient dY_last [B, H] of the last step's output only."""
+    _capi.call("cnhip_lstm_backward_last", *(_p(t) for t in (X, W_ih, W_hh, Y, gates, c, tanh_c, dY_last,
+                                                             gW_ih, gW_hh, gb, dX)), B, S, I, H,
+               _stream())
+
+
 def gru_forward(X, W_ih, W_hh, b, Y, gates, rh, B, S, I, H) -> None:
     _capi.call("cnhip_gru_forward", *(_p(t) for t in (X, W_ih, W_hh, b, Y, gates, rh)), B, S, I, H,
                _stream())

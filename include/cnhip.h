@@ -298,6 +298,17 @@ int cnhip_lstm_backward(const float* X, const float* W_ih, const float* W_hh, co
                         const float* dY, float* grad_W_ih, float* grad_W_hh, float* grad_b,
                         float* dX, int64_t B, int64_t S, int64_t I, int64_t H,
                         cnhip_stream_t stream);
+/* cnhip_lstm_backward for a gradient that reaches only the last step's
+ * output: dY_last [B,H] is dY at t = S-1, dY being 0 at every other step.
+ * Results equal cnhip_lstm_backward on that dY.  Replaces the spread of the
+ * gradient over [B,S,H] (the backward of taking the last step,
+ * cnhip_seq_scatter) plus the LSTM backward (lstm.cpp:184-253) of an
+ * LSTM -> last step -> Linear model. */
+int cnhip_lstm_backward_last(const float* X, const float* W_ih, const float* W_hh, const float* Y,
+                             const float* gates, const float* c, const float* tanh_c,
+                             const float* dY_last, float* grad_W_ih, float* grad_W_hh, float* grad_b,
+                             float* dX, int64_t B, int64_t S, int64_t I, int64_t H,
+                             cnhip_stream_t stream);
 /* GRU: W_ih [I,3H], W_hh [H,3H], b [3H], gate blocks z,r,n with
  * n = tanh(x W_in + (r*h) W_hn + b_n), h = (1-z) n + z h_prev; caches gates
  * (z,r,n activations [B*S,3H]) and rh = r*h_prev [B*S,H].

@@ -215,3 +215,33 @@ def test_lstm_persistent_exchange_reuse_is_exact(gpu):
         if shape == (64, 6, 64, 128):
             for x, y in zip(first, got):
                 assert np.array_equal(x.view(np.uint32), y.view(np.uint32))
+
+
+@pytest.mark.parametrize("B,S,I,H,path", [(32, 7, 64, 64, "persistent"), (128, 64, 128, 512, "persistent"),
+                                          (48, 9, 24, 128, "persistent"), (32, 7, 64, 64, "persistent-unfused"),
+                                          (40, 6, 12, 71, "per-step")])
+def test_lstm_backward_last_step_gradient(gpu, monkeypatch, B, S, I, H, path):
+    """cnhip_lstm_backward_last (the gradient of the last step's output only,
+    as an LSTM -> SequenceLast model passes it) against the same gradient
+    spread over all steps with zeros and cnhip_lstm_backward: bit for bit."""
+    print(f"[lstm-last] B={B} S={S} I={I} H={H} {path}", flush=True)
+    monkeypatch.setenv("CNHIP_RECURRENCE_PERSISTENT", "0" if path == "per-step" else "1")
+    monkeypatch.setenv("CNHIP_RECURRENCE_FUSED_DW", "0" if path == "persistent-unfused" else "1")
+    monkeypatch.setenv("CNHIP_RECURRENCE_FUSED_X", "0" if path == "persistent-unfused" else "1")
+    rng = np.random.default_rng(B * S + H)
+    X, Wih, Whh, b, _ = _inputs(rng, B, S, I, H, 4)
+    BS, G = B * S, 4 * H
+    Y, gates = torch.empty(BS * H, device="cuda"), torch.empty(BS * G, device="cuda")
+    c, tc = torch.empty(BS * H, device="cuda"), torch.empty(BS * H, device="cuda")
+    ops.lstm_forward(dev(X), dev(Wih), dev(Whh), dev(b), Y, gates, c, tc, B, S, I, H)
+    dlast = (rng.standard_normal(B * H) * 1e-2).astype(np.float32)
+    full = np.zeros((H, S, B), np.float32)  # ColMajor [B, S, H]
+    full[:, S - 1, :] = dlast.reshape(H, B)
+    outs = []
+    for fn, dy in [(ops.lstm_backward, full.reshape(-1)), (ops.lstm_backward_last, dlast)]:
+        gWih, gWhh = torch.empty(I * G, device="cuda"), torch.empty(H * G, device="cuda")
+        gb, dX = torch.empty(G, device="cuda"), torch.empty(BS * I, device="cuda")
+        fn(dev(X), dev(Wih), dev(Whh), Y, gates, c, tc, dev(dy), gWih, gWhh, gb, dX, B, S, I, H)
+        outs.append([host(t) for t in (gWih, gWhh, gb, dX)])
+    for x, y, name in zip(outs[0], outs[1], ["grad_W_ih", "grad_W_hh", "grad_b", "dX"]):
+        assert np.array_equal(x.view(np.uint32), y.view(np.uint32)), name
