@@ -4,6 +4,7 @@
 #include <iostream>
 #include <stdexcept>
 
+#include "CppNet/layers/max_pool2d.hpp"
 #include "CppNet/optimizers/optimizer.hpp"
 #include "CppNet/utils/init.hpp"
 
@@ -132,6 +133,36 @@ namespace CppNet
                           "Linear::backward");
             if (trainable_) grads_zero_ = false;
             return dX;
+        }
+
+        bool Linear::fuses_maxpool_backward(const DeviceTensor& g, const MaxPool2D& pool) const
+        {
+            if (!trainable_ || !pool.fused_forward() || !in_cache_.defined()) return false;
+            const DeviceTensor& P = pool.pooled_output();
+            const std::vector<int64_t>& d = pool.input_dims();
+            if (in_cache_.data() != P.data() || in_cache_.size() != P.size() || d.size() != 4) return false;
+            if (g.rank() != 2 || g.dimension(0) != d[0] || g.dimension(1) != out_size_) return false;
+            return cnhip_linear_backward_maxpool_relu_fits(d[0], d[1], d[2], d[3], out_size_, pool.get_pool_size(),
+                                                           pool.get_stride()) != 0;
+        }
+
+        DeviceTensor Linear::backward_maxpool_relu(const DeviceTensor& g, const MaxPool2D& pool)
+        {
+            if (!fuses_maxpool_backward(g, pool))
+                throw std::runtime_error("Linear::backward_maxpool_relu: the input is not the pooled output of a "
+                                         "fused Conv2D -> ReLU -> MaxPool2D forward, or the shapes do not fit, "
+                                         "in layer: " + layer_name_);
+            const std::vector<int64_t>& d = pool.input_dims();
+            DeviceTensor dx = DeviceTensor::empty(d);
+            const int accumulate = grads_zero_ ? 0 : 1;
+            Device::check(cnhip_linear_backward_maxpool_relu(in_cache_.data(), pool.max_indices().idata(), W_.data(),
+                                                             g.data(), gW_.data(), bias_flag_ ? gb_.data() : nullptr,
+                                                             dx.data(), d[0], d[1], d[2], d[3], out_size_,
+                                                             pool.get_pool_size(), pool.get_stride(), accumulate,
+                                                             Device::stream()),
+                          "Linear::backward_maxpool_relu");
+            grads_zero_ = false;
+            return dx;
         }
 
         Tensor<float, 2> Linear::forward(const Tensor<float, 2>& input)

@@ -103,6 +103,21 @@ namespace CppNet
                     --k;
                     continue;
                 }
+                // Conv2D -> ReLU -> MaxPool2D -> Flatten -> Linear: the backward
+                // of the last four in one pass over the pooled output
+                if (k >= first + 3 && (k - 3 > first || input_grad))
+                {
+                    Layers::Linear* lin = steps_[k]->linear();
+                    Layers::MaxPool2D* mp = lin ? steps_[k - 2]->maxpool() : nullptr;
+                    if (mp && steps_[k - 1]->flatten() &&
+                        dynamic_cast<Activations::ReLU*>(steps_[k - 3]->activation()) &&
+                        lin->fuses_maxpool_backward(g, *mp))
+                    {
+                        g = lin->backward_maxpool_relu(g, *mp);
+                        k -= 3;
+                        continue;
+                    }
+                }
                 Activations::Activation* prev = k > first ? steps_[k - 1]->activation() : nullptr;
                 auto* relu = dynamic_cast<Activations::ReLU*>(prev);
                 Layers::MaxPool2D* fused_mp = steps_[k]->maxpool();

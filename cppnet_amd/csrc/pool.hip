@@ -15,8 +15,10 @@
 // input exactly (each element then gets exactly one term).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <type_traits>
+#include <utility>
 
 #include "act_math.hpp"
 #include "common.hpp"
@@ -212,6 +214,170 @@ __global__ void __launch_bounds__(256) maxpool_bwd_tiled_kernel(PoolDims d,
   }
 }
 
+// Backward of a classifier head Conv2D -> ReLU -> MaxPool2D -> Flatten ->
+// Linear(F -> O) from the Linear's output gradient dZ [N, O] down to the
+// ReLU's input, in one pass over the pooled output P [N, F] (the Linear's
+// input, F = C HO WO, f = c + C (oh + HO ow)):
+//   gW[f, o] (+)= sum_n P[n, f] dZ[n, o]      gb[o] (+)= sum_n dZ[n, o]
+//   dX = the pool's routing of (dZ W^T)[n, f] * [P[n, f] > 0]
+// A wave takes a feature f: lane l runs over n = l, l + 64, ... in order and
+// the lane sums meet in an xor butterfly -- the order gemm_small_wave_kernel
+// sums a weight gradient in (and its bias column sums), so gW and gb are bit
+// for bit the separate Linear backward's where that kernel serves it.  The
+// input gradient (dZ W^T)[n, f] is summed over o ascending, then masked and
+// routed as maxpool_bwd_tiled_vec_kernel<kMaskOut> does.  dZ is staged in LDS
+// per block; each P and argmax element is read once, each dX element written
+// once (the windows tile the input).
+constexpr int kLinPoolMaxO = 16, kLinPoolMaxNO = 8192;
+
+// O (outputs) and POOL (window, 0 = taken from d) are compile-time, so the
+// per-row loops unroll without guards and their LDS reads issue together.
+template <int O, int POOL>
+__global__ void __launch_bounds__(256) linear_bwd_maxpool_kernel(PoolDims d, const float* __restrict__ P,
+                                                                 const int32_t* __restrict__ idx,
+                                                                 const float* __restrict__ W,
+                                                                 const float* __restrict__ dZ, float* __restrict__ gW,
+                                                                 float* __restrict__ gb, float* __restrict__ dX,
+                                                                 int accumulate) {
+  __shared__ float dzs[kLinPoolMaxNO];
+  const int N = (int)d.N, C = (int)d.C, HO = (int)d.HO;
+  const int pool = POOL > 0 ? POOL : (int)d.pool;
+  const int F = C * HO * (int)d.WO;
+  {
+    // 16 loads in flight per thread before their LDS stores: one round trip
+    // for up to 4096 floats of dZ
+    constexpr int U = 16;
+    const int NO = N * O;
+    for (int e0 = 0; e0 < NO; e0 += 256 * U) {
+      float v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int e = e0 + (int)threadIdx.x + 256 * u;
+        v[u] = e < NO ? dZ[e] : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int e = e0 + (int)threadIdx.x + 256 * u;
+        if (e < NO) dzs[e] = v[u];
+      }
+    }
+  }
+  __syncthreads();
+  // the wave index as a wave-uniform value: a feature's W row then comes
+  // through scalar loads
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t sh = d.N * d.C, sw = d.N * d.C * d.H;
+  if (gb && blockIdx.x == 0 && w == 0) {
+#pragma unroll
+    for (int o = 0; o < O; ++o) {
+      float sum = 0.f;
+      for (int n = lane; n < N; n += 64) sum += dzs[n + N * o];
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+      if (lane == 0) gb[o] = accumulate ? gb[o] + sum : sum;
+    }
+  }
+  const int fstride = gridDim.x * 4;
+  for (int f = blockIdx.x * 4 + w; f < F; f += fstride) {
+    const int c = f % C, r = f / C, oh = r % HO, ow = r / HO;
+    const int64_t base = d.N * c + sh * (oh * pool) + sw * (ow * pool);
+    const float* pf = P + d.N * f;
+    const int32_t* xf = idx + d.N * f;
+    float wf[O], acc[O];
+#pragma unroll
+    for (int o = 0; o < O; ++o) {
+      wf[o] = W[f + (int64_t)F * o];
+      acc[o] = 0.f;
+    }
+    for (int n0 = 0; n0 < N; n0 += 256) {
+      // the lane's four rows loaded together, then all four computed, then
+      // all their stores: a store ahead of a load would make the wait for
+      // that load wait for the store as well (vmcnt counts both)
+      float x[4], g[4];
+      int mi[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int n = n0 + lane + 64 * u;
+        x[u] = n < N ? pf[n] : 0.f;
+        mi[u] = n < N ? xf[n] : -1;
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int n = n0 + lane + 64 * u;
+        const bool ok = n < N;
+        const int nr = ok ? n : N - 1;
+        float dz[O];
+#pragma unroll
+        for (int o = 0; o < O; ++o) dz[o] = dzs[nr + N * o];
+        float gv = 0.f;
+#pragma unroll
+        for (int o = 0; o < O; ++o) {
+          const float a = fmaf(x[u], dz[o], acc[o]);
+          acc[o] = ok ? a : acc[o];
+          gv = fmaf(dz[o], wf[o], gv);
+        }
+        g[u] = (0.f + gv) * relu_mask(x[u]);
+      }
+      auto store = [&](int u) {
+        const int n = n0 + lane + 64 * u;
+        if (POOL > 0) {
+#pragma unroll
+          for (int ph = 0; ph < (POOL > 0 ? POOL : 1); ++ph)
+#pragma unroll
+            for (int pw = 0; pw < (POOL > 0 ? POOL : 1); ++pw)
+              dX[base + n + sh * ph + sw * pw] = mi[u] == ph * pool + pw ? g[u] : 0.f;
+        } else {
+          for (int ph = 0; ph < pool; ++ph)
+            for (int pw = 0; pw < pool; ++pw)
+              dX[base + n + sh * ph + sw * pw] = mi[u] == ph * pool + pw ? g[u] : 0.f;
+        }
+      };
+      if (n0 + 256 <= N) {  // wave-uniform: a full set of rows, no per-row branch
+#pragma unroll
+        for (int u = 0; u < 4; ++u) store(u);
+      } else {
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          if (n0 + lane + 64 * u < N) store(u);
+      }
+    }
+#pragma unroll
+    for (int o = 0; o < O; ++o) {
+      float a = acc[o];
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) a += __shfl_xor(a, off, 64);
+      acc[o] = a;
+    }
+    if (lane == 0) {
+      float prev[O];
+#pragma unroll
+      for (int o = 0; o < O; ++o) prev[o] = accumulate ? gW[f + (int64_t)F * o] : 0.f;
+#pragma unroll
+      for (int o = 0; o < O; ++o) gW[f + (int64_t)F * o] = accumulate ? acc[o] + prev[o] : acc[o];
+    }
+  }
+}
+
+template <int O>
+void launch_linear_bwd_maxpool(unsigned grid, hipStream_t st, const PoolDims& d, const float* P,
+                               const int32_t* idx, const float* W, const float* dZ, float* gW, float* gb,
+                               float* dX, int accumulate) {
+  if (d.pool == 2)
+    hipLaunchKernelGGL((linear_bwd_maxpool_kernel<O, 2>), dim3(grid), dim3(256), 0, st, d, P, idx, W, dZ, gW, gb,
+                       dX, accumulate);
+  else
+    hipLaunchKernelGGL((linear_bwd_maxpool_kernel<O, 0>), dim3(grid), dim3(256), 0, st, d, P, idx, W, dZ, gW, gb,
+                       dX, accumulate);
+}
+
+template <int... Os>
+void dispatch_linear_bwd_maxpool(std::integer_sequence<int, Os...>, int O, unsigned grid, hipStream_t st,
+                                 const PoolDims& d, const float* P, const int32_t* idx, const float* W,
+                                 const float* dZ, float* gW, float* gb, float* dX, int accumulate) {
+  ((O == Os + 1 ? launch_linear_bwd_maxpool<Os + 1>(grid, st, d, P, idx, W, dZ, gW, gb, dX, accumulate) : void()),
+   ...);
+}
+
 int pool_dims(PoolDims& d, int64_t N, int64_t C, int64_t H, int64_t W, int64_t pool,
               int64_t stride, const char* who) {
   CNHIP_REQUIRE(N > 0 && C > 0 && H > 0 && W > 0 && pool > 0,
@@ -320,6 +486,42 @@ int cnhip_maxpool2d_backward_relu_pooled(const float* dY, const int32_t* idx, co
   const char* who = "cnhip_maxpool2d_backward_relu_pooled";
   CNHIP_REQUIRE(Y, "%s: NULL pooled output", who);
   return cnhip::maxpool_backward(dY, idx, Y, cnhip::kMaskOut, dX, N, C, H, W, pool, stride, stream, who);
+}
+
+int cnhip_linear_backward_maxpool_relu_fits(int64_t N, int64_t C, int64_t H, int64_t W, int64_t out_features,
+                                            int64_t pool, int64_t stride) {
+  if (stride <= 0) stride = pool;
+  return N > 0 && C > 0 && pool > 0 && stride == pool && H % pool == 0 && W % pool == 0 && out_features > 0 &&
+                 out_features <= cnhip::kLinPoolMaxO && N * out_features <= cnhip::kLinPoolMaxNO &&
+                 C * H * W < ((int64_t)1 << 31)
+             ? 1
+             : 0;
+}
+
+int cnhip_linear_backward_maxpool_relu(const float* P, const int32_t* idx, const float* W, const float* dZ,
+                                       float* grad_W, float* grad_b, float* dX, int64_t N, int64_t C, int64_t H,
+                                       int64_t Wd, int64_t out_features, int64_t pool, int64_t stride, int accumulate,
+                                       cnhip_stream_t stream) {
+  const char* who = "cnhip_linear_backward_maxpool_relu";
+  cnhip::PoolDims d;
+  CNHIP_TRY(cnhip::pool_dims(d, N, C, H, Wd, pool, stride, who));
+  CNHIP_REQUIRE(cnhip_linear_backward_maxpool_relu_fits(N, C, H, Wd, out_features, pool, stride),
+                "%s: needs windows that tile the input (stride == pool dividing H and W), out_features <= %d and "
+                "batch * out_features <= %d (N=%lld C=%lld H=%lld W=%lld out=%lld pool=%lld stride=%lld)",
+                who, cnhip::kLinPoolMaxO, cnhip::kLinPoolMaxNO, (long long)N, (long long)C, (long long)H,
+                (long long)Wd, (long long)out_features, (long long)pool, (long long)stride);
+  CNHIP_REQUIRE(P && idx && W && dZ && grad_W && dX, "%s: NULL pointer", who);
+  const hipStream_t st = cnhip::as_stream(stream);
+  const int64_t F = C * d.HO * d.WO;
+  // P and the argmax read once, dX written once, grad_W written (and read
+  // when accumulating); dZ and W are small
+  const double bytes = 8.0 * (double)N * F + 4.0 * (double)N * C * H * Wd +
+                       (accumulate ? 8.0 : 4.0) * (double)F * out_features + 4.0 * (double)N * out_features;
+  cnhip::HbmTimer timer("linear_bwd_maxpool_kernel", bytes, st);
+  const unsigned grid = (unsigned)std::min<int64_t>((F + 3) / 4, 1024);
+  cnhip::dispatch_linear_bwd_maxpool(std::make_integer_sequence<int, cnhip::kLinPoolMaxO>{}, (int)out_features,
+                                     grid, st, d, P, idx, W, dZ, grad_W, grad_b, dX, accumulate);
+  return cnhip::check_launch(who);
 }
 
 }  // extern "C"

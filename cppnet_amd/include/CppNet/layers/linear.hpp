@@ -25,6 +25,14 @@ namespace CppNet
 {
     namespace Layers
     {
+        class MaxPool2D;
+    }
+}
+
+namespace CppNet
+{
+    namespace Layers
+    {
         class Linear : public Layer
         {
         public:
@@ -51,6 +59,16 @@ namespace CppNet
             /// backward().
             DeviceTensor backward_act(const DeviceTensor& grad_output, int act,
                                       const DeviceTensor& act_aux);
+            /// Whether backward_maxpool_relu() serves this layer: its input is
+            /// the (flattened) pooled output of pool's last fused Conv2D ->
+            /// ReLU -> MaxPool2D forward, and the shapes fit the one-pass kernel.
+            bool fuses_maxpool_backward(const DeviceTensor& grad_output, const MaxPool2D& pool) const;
+            /// backward() followed by the Flatten's, pool's and ReLU's backward
+            /// of a Conv2D -> ReLU -> MaxPool2D -> Flatten -> this stack, in one
+            /// pass (cnhip_linear_backward_maxpool_relu): accumulates the
+            /// parameter gradients as backward() does and returns the gradient
+            /// at the ReLU's input, [N, C, H, W].
+            DeviceTensor backward_maxpool_relu(const DeviceTensor& grad_output, const MaxPool2D& pool);
             /// forward(input) + residual (a skip connection, [B, out]) in the
             /// GEMM epilogue; equals forward() followed by the add.  The
             /// matching backward is backward_act(g, CNHIP_ACT_RESIDUAL,

@@ -37,6 +37,10 @@ namespace CppNet
                                    const DeviceTensor& idx);
             /// Whether the last forward was fused (no ReLU output was kept).
             bool fused_forward() const { return fused_out_.defined(); }
+            /// Pooled output of the last fused forward (undefined otherwise).
+            const DeviceTensor& pooled_output() const { return fused_out_; }
+            /// Input dims [N, C, H, W] of the last fused forward.
+            const std::vector<int64_t>& input_dims() const { return in_dims_; }
             /// backward_relu() for a fused forward: the ReLU mask from this
             /// layer's own output.
             DeviceTensor backward_relu_pooled(const DeviceTensor& grad_output);

@@ -7,7 +7,9 @@
  * followed by ReLU runs as one GEMM with the ReLU in its epilogue, and the
  * next Linear's input-gradient GEMM -- or the backward of a MaxPool2D that
  * follows the ReLU -- applies the ReLU mask (same arithmetic as the separate
- * calls).
+ * calls).  Conv2D -> ReLU -> MaxPool2D runs as one forward call, and a
+ * Linear head on its flattened output takes the backward of the Linear,
+ * Flatten, pool and ReLU in one pass.
  * GELU is not fused: its erfc epilogue measured slower than a separate pass
  * on MI355X.  backward() returns the gradient of the model input, as the
  * reference does; backward_params() is the training step's variant: it
@@ -27,6 +29,7 @@
 
 #include "CppNet/activations/activation.hpp"
 #include "CppNet/layers/conv2d.hpp"
+#include "CppNet/layers/flatten.hpp"
 #include "CppNet/layers/linear.hpp"
 #include "CppNet/layers/lstm.hpp"
 #include "CppNet/layers/max_pool2d.hpp"
@@ -51,6 +54,7 @@ namespace CppNet
             virtual DeviceTensor backward_no_input_grad(const DeviceTensor& g) { return backward(g); }
             virtual Layers::Linear* linear() { return nullptr; }
             virtual Layers::MaxPool2D* maxpool() { return nullptr; }
+            virtual Layers::Flatten* flatten() { return nullptr; }
             virtual Layers::Conv2D* conv2d() { return nullptr; }
             virtual Layers::LSTM* lstm() { return nullptr; }
             virtual Layers::SequenceLast* sequence_last() { return nullptr; }
@@ -87,6 +91,7 @@ namespace CppNet
             void step(Optimizers::Optimizer& o, float lr) override { layer_->step(o, lr); }
             Layers::Linear* linear() override { return dynamic_cast<Layers::Linear*>(layer_.get()); }
             Layers::MaxPool2D* maxpool() override { return dynamic_cast<Layers::MaxPool2D*>(layer_.get()); }
+            Layers::Flatten* flatten() override { return dynamic_cast<Layers::Flatten*>(layer_.get()); }
             Layers::Conv2D* conv2d() override { return dynamic_cast<Layers::Conv2D*>(layer_.get()); }
             Layers::LSTM* lstm() override { return dynamic_cast<Layers::LSTM*>(layer_.get()); }
             Layers::SequenceLast* sequence_last() override

@@ -142,6 +142,20 @@ def maxpool2d_backward_relu_pooled(dY, idx, Y, dX, N, C, H, W, pool=2, stride=-1
                _p(dX, "dX"), N, C, H, W, pool, stride, _stream())
 
 
+def linear_backward_maxpool_relu(P, idx, W, dZ, gW, gb, dX, N, C, H, Wd, out_features, pool=2, stride=-1,
+                                 accumulate=0) -> None:
+    """Backward of Conv2D -> ReLU -> MaxPool2D -> Flatten -> Linear from the
+    Linear's output gradient dZ: gW (+)= P^T dZ, gb (+)= column sums of dZ, and
+    dX (the ReLU input's gradient) = the pool's routing of (dZ W^T) * [P > 0]."""
+    _capi.call("cnhip_linear_backward_maxpool_relu", _p(P, "P"), _p(idx, "idx"), _p(W, "W"), _p(dZ, "dZ"),
+               _p(gW, "gW"), _p(gb), _p(dX, "dX"), N, C, H, Wd, out_features, pool,
+               stride, accumulate, _stream())
+
+
+def linear_backward_maxpool_relu_fits(N, C, H, Wd, out_features, pool=2, stride=-1) -> bool:
+    return bool(_capi.load().cnhip_linear_backward_maxpool_relu_fits(N, C, H, Wd, out_features, pool, stride))
+
+
 def lstm_forward(X, W_ih, W_hh, b, Y, gates, c, tanh_c, B, S, I, H) -> None:
     _capi.call("cnhip_lstm_forward", *(_p(t) for t in (X, W_ih, W_hh, b, Y, gates, c, tanh_c)),
                B, S, I, H, _stream())

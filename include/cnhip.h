@@ -281,6 +281,28 @@ int cnhip_maxpool2d_backward_relu(const float* dY, const int32_t* idx, const flo
 int cnhip_maxpool2d_backward_relu_pooled(const float* dY, const int32_t* idx, const float* Y, float* dX,
                                          int64_t N, int64_t C, int64_t H, int64_t W, int64_t pool,
                                          int64_t stride, cnhip_stream_t stream);
+/* Backward of a classifier head Conv2D -> ReLU -> MaxPool2D -> Flatten ->
+ * Linear(F -> O) from the Linear's output gradient dZ [N, O] to the ReLU's
+ * input, in one pass: grad_W [F, O] (+)= P^T dZ and grad_b (+)= the column
+ * sums of dZ (accumulate as cnhip_linear_backward), and dX [N, C, H, W] =
+ * the pool's backward of (dZ W^T) with the ReLU mask from P, as
+ * cnhip_linear_backward then cnhip_maxpool2d_backward_relu_pooled compute
+ * them.  P [N, C, HO, WO] is the pooled output (the Linear's input, F =
+ * C HO WO) and idx its argmax, as cnhip_conv2d_forward_relu_maxpool writes
+ * them.  grad_W and grad_b are bit-identical to cnhip_linear_backward's
+ * when its weight gradient runs the wave-per-output SIMT kernel (batch > 64
+ * and 2 F O N <= 32 MFLOP); dX may differ from the MFMA product there in
+ * the last bits (the sum over O runs in ascending order here).  Needs
+ * windows that tile the input (stride == pool, dividing H and W), O <= 16
+ * and N O <= 8192 (cnhip_linear_backward_maxpool_relu_fits).  Replaces
+ * Linear::backward (linear.cpp:335-358) + Flatten::backward + MaxPool2D::
+ * backward (max_pool2d.cpp:96-131) + ReLU::backward (relu.cpp:194-225). */
+int cnhip_linear_backward_maxpool_relu(const float* P, const int32_t* idx, const float* W, const float* dZ,
+                                       float* grad_W, float* grad_b, float* dX, int64_t N, int64_t C,
+                                       int64_t H, int64_t Wd, int64_t out_features, int64_t pool,
+                                       int64_t stride, int accumulate, cnhip_stream_t stream);
+int cnhip_linear_backward_maxpool_relu_fits(int64_t N, int64_t C, int64_t H, int64_t W,
+                                            int64_t out_features, int64_t pool, int64_t stride);
 
 /* ---- recurrent layers ----------------------------------------------------
  * X [B,S,I], Y [B,S,H] ColMajor (row n + B*t of a [B*S, .] matrix).

@@ -180,3 +180,76 @@ def test_conv_relu_maxpool_fused(gpu, N, C, H, W, OC, KS, S, P, p, ps):
         assert np.array_equal(host(dB).view(np.uint32), host(dA).view(np.uint32))
     else:
         np.testing.assert_array_equal(host(dB), host(dA))
+
+
+# (N, C, H, W, O, pool): config 3's head; a batch that is no multiple of 64;
+# a batch of at most 64 (the separate weight gradient then sums on one thread,
+# so only the tolerance applies) with 3x3 windows and 16 outputs; the largest
+# staged dZ (N O = 8192)
+HEAD_POOL_CASES = [(256, 64, 16, 16, 10, 2), (100, 3, 6, 4, 3, 2), (32, 5, 6, 6, 16, 3), (512, 8, 4, 4, 16, 2)]
+
+
+@pytest.mark.parametrize("N,C,H,W,O,p", HEAD_POOL_CASES)
+@pytest.mark.parametrize("accumulate", [0, 1])
+def test_linear_backward_maxpool_relu(gpu, N, C, H, W, O, p, accumulate):
+    """cnhip_linear_backward_maxpool_relu (Linear + Flatten + MaxPool2D + ReLU
+    backward in one pass) against a float64 restatement (close_mag bound) and
+    against the separate calls cnhip_linear_backward then
+    cnhip_maxpool2d_backward_relu_pooled: grad_W and grad_b bit for bit where
+    the separate weight gradient runs the wave-per-output kernel (N > 64), dX
+    routed to the same elements with values within the contraction bound (the
+    separate dX is an MFMA product, summed in another order)."""
+    from cppnet_amd import ops
+    print(f"[linear-pool-bwd] N={N} C={C} H={H} W={W} O={O} pool={p} acc={accumulate}", flush=True)
+    rng = np.random.default_rng(N + C + H + W + O + p + accumulate)
+    HO, WO = H // p, W // p
+    F = C * HO * WO
+    # a ReLU output with exact zeros and ties, pooled on the GPU
+    Y = np.maximum(rng.integers(-4, 5, N * C * H * W) * 0.5, 0).astype(np.float32)
+    Pt = torch.empty(N * F, device="cuda")
+    It = torch.empty(N * F, dtype=torch.int32, device="cuda")
+    ops.maxpool2d_forward(dev(Y), Pt, It, N, C, H, W, p, -1)
+    Wt = rng.standard_normal(F * O).astype(np.float32)
+    dZ = rng.standard_normal(N * O).astype(np.float32)
+    gW0 = rng.standard_normal(F * O).astype(np.float32)
+    gb0 = rng.standard_normal(O).astype(np.float32)
+    assert ops.linear_backward_maxpool_relu_fits(N, C, H, W, O, p, -1)
+    gWa, gba = dev(gW0), dev(gb0)
+    dXa = torch.full((N * C * H * W,), 9.0, device="cuda")
+    ops.linear_backward_maxpool_relu(Pt, It, dev(Wt), dev(dZ), gWa, gba, dXa, N, C, H, W, O, p, -1, accumulate)
+    gWb, gbb = dev(gW0), dev(gb0)
+    dP = torch.empty(N * F, device="cuda")
+    dXb = torch.full((N * C * H * W,), 7.0, device="cuda")
+    ops.linear_backward(Pt, dev(Wt), dev(dZ), gWb, gbb, dP, N, F, O, True, bool(accumulate))
+    ops.maxpool2d_backward_relu_pooled(dP, It, Pt, dXb, N, C, H, W, p, -1)
+    P, I = host(Pt), host(It)
+    # float64 restatement
+    Pm, dZm, Wm = P.reshape(F, N).T.astype(np.float64), dZ.reshape(O, N).T.astype(np.float64), \
+        Wt.reshape(O, F).T.astype(np.float64)
+    gW_ref = (Pm.T @ dZm).T.reshape(-1) + (gW0 if accumulate else 0)
+    gW_mag = (np.abs(Pm).T @ np.abs(dZm)).T.reshape(-1) / np.sqrt(N)
+    gb_ref = dZm.sum(0) + (gb0 if accumulate else 0)
+    g = (dZm @ Wm.T).T.reshape(WO, HO, C, N) * (P.reshape(WO, HO, C, N) > 0)
+    gmag = (np.abs(dZm) @ np.abs(Wm).T).T.reshape(WO, HO, C, N) / np.sqrt(O)
+    I4 = I.reshape(WO, HO, C, N)
+    dX_ref = np.zeros((WO, p, HO, p, C, N))
+    dX_mag = np.zeros((WO, p, HO, p, C, N))
+    for ph in range(p):
+        for pw in range(p):
+            hit = I4 == ph * p + pw
+            dX_ref[:, pw, :, ph] = np.where(hit, g, 0.0)
+            dX_mag[:, pw, :, ph] = np.where(hit, gmag, 0.0)
+    dXa_h, dXb_h = host(dXa), host(dXb)
+    for name, a, ref, mag in (("grad_W", host(gWa), gW_ref, gW_mag), ("dX", dXa_h, dX_ref.reshape(-1), dX_mag.reshape(-1))):
+        ok, msg = close_mag(a, ref, mag)
+        assert ok, f"{name}: {msg}"
+    ok, msg = close(host(gba), gb_ref, rtol=1e-5, atol=1e-5)
+    assert ok, f"grad_b: {msg}"
+    # the separate calls: the same routing (every element written, zeros where
+    # the pool routes nothing), values within the bound
+    assert np.array_equal(dXa_h == 0, dXb_h == 0)
+    ok, msg = close_mag(dXa_h, dXb_h, dX_mag.reshape(-1))
+    assert ok, f"dX vs separate calls: {msg}"
+    if N > 64:
+        assert np.array_equal(host(gWa).view(np.uint32), host(gWb).view(np.uint32))
+        assert np.array_equal(host(gba).view(np.uint32), host(gbb).view(np.uint32))
