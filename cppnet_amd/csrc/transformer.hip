@@ -293,10 +293,18 @@ __global__ void __launch_bounds__(256) embedding_fwd_kernel(const int32_t* __res
     tok[threadIdx.x] = id;
   }
   __syncthreads();
-  for (int j = ty; j < TT; j += 4) {  // token j, feature tx: contiguous along d
+  {
+    // token j = ty + 4 jj, feature tx: contiguous along d; all TT / 4 loads
+    // of a thread in flight before its LDS stores
+    float v[TT / 4];
     const int64_t d = d0 + tx;
-    const int32_t id = tok[j];
-    tile[j][tx] = (d < D && id >= 0) ? Wt[d + D * (int64_t)id] : 0.f;
+#pragma unroll
+    for (int jj = 0; jj < TT / 4; ++jj) {
+      const int32_t id = tok[ty + 4 * jj];
+      v[jj] = (d < D && id >= 0) ? Wt[d + D * (int64_t)id] : 0.f;
+    }
+#pragma unroll
+    for (int jj = 0; jj < TT / 4; ++jj) tile[ty + 4 * jj][tx] = v[jj];
   }
   __syncthreads();
   for (int j = ty; j < TT; j += 4) {  // feature j, token tx: contiguous along p
@@ -392,13 +400,56 @@ __global__ void __launch_bounds__(128) emb_sum_kernel(const int32_t* __restrict_
                                                       int64_t S, int64_t D, int by_sample) {
   const int64_t v = blockIdx.x;
   const int32_t lo = offsets[v], hi = offsets[v + 1];
-  for (int64_t d = threadIdx.x; d < D; d += blockDim.x) {
-    float s = 0.f;
+  // four features per thread, so each bucket entry's key is read once and
+  // four independent loads are in flight per entry
+  constexpr int U = 4;
+  for (int64_t d0 = threadIdx.x; d0 < D; d0 += U * blockDim.x) {
+    float s[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) s[u] = 0.f;
     for (int32_t i = lo; i < hi; ++i) {
       const int64_t key = keys[i];
-      s += dYt[d + D * (by_sample ? key : key / S + B * (key % S))];
+      const float* src = dYt + D * (by_sample ? key : key / S + B * (key % S));
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t d = d0 + (int64_t)u * blockDim.x;
+        if (d < D) s[u] += src[d];
+      }
     }
-    gWt[d + D * v] = s;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t d = d0 + (int64_t)u * blockDim.x;
+      if (d < D) gWt[d + D * v] = s[u];
+    }
+  }
+}
+
+// emb_sum_kernel when D % 4 == 0: a wave per token, lane l summing the
+// float4 columns l, l + 64 (two in flight per bucket entry); each element's
+// sum runs over the bucket in key order, as there
+__global__ void __launch_bounds__(256) emb_sum_vec_kernel(const int32_t* __restrict__ offsets,
+                                                          const int32_t* __restrict__ keys,
+                                                          const float* __restrict__ dYt,
+                                                          float* __restrict__ gWt, int B, int S, int D,
+                                                          int V, int by_sample) {
+  const int lane = threadIdx.x & 63;
+  const int v = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (v >= V) return;
+  const int32_t lo = offsets[v], hi = offsets[v + 1];
+  const int D4 = D / 4;
+  f32x4* out = reinterpret_cast<f32x4*>(gWt + (int64_t)D * v);
+  for (int c0 = lane; c0 < D4; c0 += 128) {
+    const int c1 = c0 + 64;
+    f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = s0;
+    for (int32_t i = lo; i < hi; ++i) {
+      const int key = keys[i];
+      const int64_t row = by_sample ? key : key / S + (int64_t)B * (key % S);
+      const f32x4* src = reinterpret_cast<const f32x4*>(dYt + (int64_t)D * row);
+      s0 += src[c0];
+      if (c1 < D4) s1 += src[c1];
+    }
+    out[c0] = s0;
+    if (c1 < D4) out[c1] = s1;
   }
 }
 
@@ -938,6 +989,37 @@ __global__ void __launch_bounds__(256) meanpool_bwd_kernel(const float* __restri
   }
 }
 
+// meanpool_bwd_kernel by sample when S % 4 == 0: a wave per (b, d) fills the
+// S contiguous values of dx at S b + B S d with float4 stores of dy(b, d) / S
+__global__ void __launch_bounds__(256) meanpool_bwd_by_sample_vec_kernel(const float* __restrict__ dy,
+                                                                         float* __restrict__ dx, int B,
+                                                                         int S, int pairs, float inv_S) {
+  const int lane = threadIdx.x & 63;
+  const int pair = blockIdx.x * 4 + (threadIdx.x >> 6);  // b + B d
+  if (pair >= pairs) return;
+  const int b = pair % B, d = pair / B;
+  const float v = dy[pair] * inv_S;
+  const f32x4 v4 = {v, v, v, v};
+  f32x4* out = reinterpret_cast<f32x4*>(dx + (int64_t)S * b + (int64_t)B * S * d);
+  for (int t = lane; t < S / 4; t += 64) out[t] = v4;
+}
+
+// meanpool_bwd_kernel in the reference row order when B % 4 == 0: column s of
+// feature d, dx[b + B s + B S d] = dy(b, d) / S, as float4s along b
+__global__ void __launch_bounds__(256) meanpool_bwd_vec_kernel(const float* __restrict__ dy,
+                                                               float* __restrict__ dx, int B, int S,
+                                                               int D, float inv_S) {
+  const int B4 = B / 4;
+  const int64_t total4 = (int64_t)B4 * S * D;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total4;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int b4 = (int)(i % B4);
+    const int d = (int)(i / ((int64_t)B4 * S));
+    f32x4 v = reinterpret_cast<const f32x4*>(dy + (int64_t)B * d)[b4];
+    reinterpret_cast<f32x4*>(dx)[i] = v * inv_S;
+  }
+}
+
 __global__ void __launch_bounds__(256) add_kernel(const float* __restrict__ a,
                                                   const float* __restrict__ b,
                                                   float* __restrict__ y, int64_t n, int vec) {
@@ -1234,8 +1316,12 @@ int cnhip_embedding_backward_rows(const int32_t* ids, const float* dY, float* gW
   CNHIP_TRY(cnhip::check_launch(who));
   // every token's gradient row read once, every table row written
   cnhip::HbmTimer timer("emb_sum_kernel", 4.0 * (double)BS * (double)D + 4.0 * (double)V * (double)D, st);
-  hipLaunchKernelGGL(cnhip::emb_sum_kernel, dim3((unsigned)V), dim3(128), 0, st, offsets, pos, dYt,
-                     gWt, B, S, D, rows);
+  if (D % 4 == 0 && D < ((int64_t)1 << 31) && cnhip::aligned16(gWt))
+    hipLaunchKernelGGL(cnhip::emb_sum_vec_kernel, dim3((unsigned)((V + 3) / 4)), dim3(256), 0, st, offsets, pos,
+                       dYt, gWt, (int)B, (int)S, (int)D, (int)V, rows);
+  else
+    hipLaunchKernelGGL(cnhip::emb_sum_kernel, dim3((unsigned)V), dim3(128), 0, st, offsets, pos, dYt,
+                       gWt, B, S, D, rows);
   return cnhip::check_launch(who);
 }
 
@@ -1384,8 +1470,20 @@ int cnhip_meanpool1d_backward_rows(const float* dy, float* dx, int64_t B, int64_
   CNHIP_REQUIRE(rows == CNHIP_ROWS_REF || rows == CNHIP_ROWS_BY_SAMPLE, "%s: bad row order %d", who, rows);
   CNHIP_REQUIRE(dy && dx, "%s: NULL pointer", who);
   cnhip::HbmTimer timer("meanpool_bwd_kernel", 4.0 * (double)B * (double)D * (double)(S + 1), as_stream(s));
-  hipLaunchKernelGGL(cnhip::meanpool_bwd_kernel, dim3(cnhip::elementwise_grid(B * S * D, 256)),
-                     dim3(256), 0, as_stream(s), dy, dx, B, S, D, 1.0f / (float)S, rows);
+  const float inv_S = 1.0f / (float)S;
+  // the float4 kernels index (b, s, d) and their pair count in 32-bit integers
+  const bool fits32 = B * D < ((int64_t)1 << 31) && S < ((int64_t)1 << 31);
+  if (fits32 && rows == CNHIP_ROWS_BY_SAMPLE && S % 4 == 0 && cnhip::aligned16(dx)) {
+    const int pairs = (int)(B * D);
+    hipLaunchKernelGGL(cnhip::meanpool_bwd_by_sample_vec_kernel, dim3((unsigned)((pairs + 3) / 4)), dim3(256), 0,
+                       as_stream(s), dy, dx, (int)B, (int)S, pairs, inv_S);
+  } else if (fits32 && rows == CNHIP_ROWS_REF && B % 4 == 0 && cnhip::aligned16(dx) && cnhip::aligned16(dy)) {
+    hipLaunchKernelGGL(cnhip::meanpool_bwd_vec_kernel, dim3(cnhip::elementwise_grid(B * S * D / 4, 256)),
+                       dim3(256), 0, as_stream(s), dy, dx, (int)B, (int)S, (int)D, inv_S);
+  } else {
+    hipLaunchKernelGGL(cnhip::meanpool_bwd_kernel, dim3(cnhip::elementwise_grid(B * S * D, 256)),
+                       dim3(256), 0, as_stream(s), dy, dx, B, S, D, inv_S, rows);
+  }
   return cnhip::check_launch(who);
 }
 
