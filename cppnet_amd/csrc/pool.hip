@@ -223,7 +223,8 @@ __global__ void __launch_bounds__(256) maxpool_bwd_tiled_kernel(PoolDims d,
 // A wave takes a feature f: lane l runs over n = l, l + 64, ... in order and
 // the lane sums meet in an xor butterfly -- the order gemm_small_wave_kernel
 // sums a weight gradient in (and its bias column sums), so gW and gb are bit
-// for bit the separate Linear backward's where that kernel serves it.  The
+// for bit the separate Linear backward's where that kernel serves it (the
+// float4 form below, for N % 4 == 0, sums each lane's 4 rows first).  The
 // input gradient (dZ W^T)[n, f] is summed over o ascending, then masked and
 // routed as maxpool_bwd_tiled_vec_kernel<kMaskOut> does.  dZ is staged in LDS
 // per block; each P and argmax element is read once, each dX element written
@@ -267,16 +268,6 @@ __global__ void __launch_bounds__(256) linear_bwd_maxpool_kernel(PoolDims d, con
   // through scalar loads
   const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t sh = d.N * d.C, sw = d.N * d.C * d.H;
-  if (gb && blockIdx.x == 0 && w == 0) {
-#pragma unroll
-    for (int o = 0; o < O; ++o) {
-      float sum = 0.f;
-      for (int n = lane; n < N; n += 64) sum += dzs[n + N * o];
-#pragma unroll
-      for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
-      if (lane == 0) gb[o] = accumulate ? gb[o] + sum : sum;
-    }
-  }
   const int fstride = gridDim.x * 4;
   for (int f = blockIdx.x * 4 + w; f < F; f += fstride) {
     const int c = f % C, r = f / C, oh = r % HO, ow = r / HO;
@@ -356,13 +347,151 @@ __global__ void __launch_bounds__(256) linear_bwd_maxpool_kernel(PoolDims d, con
       for (int o = 0; o < O; ++o) gW[f + (int64_t)F * o] = accumulate ? acc[o] + prev[o] : acc[o];
     }
   }
+  // bias gradient: output o = 4 block + wave sums dZ's column o, after the
+  // features (one column per wave, so no wave's features wait for it)
+  const int o = blockIdx.x * 4 + w;
+  if (gb && o < O) {
+    float sum = 0.f;
+    for (int n = lane; n < N; n += 64) sum += dzs[n + N * o];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+    if (lane == 0) gb[o] = accumulate ? gb[o] + sum : sum;
+  }
+}
+
+// linear_bwd_maxpool_kernel for N % 4 == 0 with 16-byte accesses: lane l
+// owns rows 4 l .. 4 l + 3 (+ 256 j), so P, the argmax and dZ's LDS rows come
+// as float4 / int4 and dX leaves as float4s.  A lane sums its rows in
+// ascending order, then the lanes meet in the xor butterfly (a fixed order;
+// not the separate weight-gradient kernel's lane-strided one).
+template <int O, int POOL>
+__global__ void __launch_bounds__(256) linear_bwd_maxpool_vec_kernel(PoolDims d, const float* __restrict__ P,
+                                                                     const int32_t* __restrict__ idx,
+                                                                     const float* __restrict__ W,
+                                                                     const float* __restrict__ dZ,
+                                                                     float* __restrict__ gW, float* __restrict__ gb,
+                                                                     float* __restrict__ dX, int accumulate) {
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  typedef int i32x4 __attribute__((ext_vector_type(4)));
+  __shared__ __align__(16) float dzs[kLinPoolMaxNO];
+  const int N = (int)d.N, C = (int)d.C, HO = (int)d.HO;
+  const int pool = POOL > 0 ? POOL : (int)d.pool;
+  const int F = C * HO * (int)d.WO;
+  {
+    constexpr int U = 4;  // float4s in flight per thread: 4096 floats of dZ per round trip
+    const int NO4 = N * O / 4;
+    for (int e0 = 0; e0 < NO4; e0 += 256 * U) {
+      f32x4 v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int e = e0 + (int)threadIdx.x + 256 * u;
+        v[u] = e < NO4 ? reinterpret_cast<const f32x4*>(dZ)[e] : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int e = e0 + (int)threadIdx.x + 256 * u;
+        if (e < NO4) reinterpret_cast<f32x4*>(dzs)[e] = v[u];
+      }
+    }
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t sh = d.N * d.C, sw = d.N * d.C * d.H;
+  for (int f = blockIdx.x * 4 + w; f < F; f += gridDim.x * 4) {
+    const int c = f % C, r = f / C, oh = r % HO, ow = r / HO;
+    const int64_t base = d.N * c + sh * (oh * pool) + sw * (ow * pool);
+    const f32x4* pf = reinterpret_cast<const f32x4*>(P + d.N * f);
+    const i32x4* xf = reinterpret_cast<const i32x4*>(idx + d.N * f);
+    float wf[O], acc[O];
+#pragma unroll
+    for (int o = 0; o < O; ++o) {
+      wf[o] = W[f + (int64_t)F * o];
+      acc[o] = 0.f;
+    }
+    for (int n0 = 0; n0 < N; n0 += 256) {
+      const int q = n0 / 4 + lane;  // float4 index of rows 4 q .. 4 q + 3
+      if (4 * q < N) {
+        const f32x4 x = pf[q];
+        const i32x4 mi = xf[q];
+        f32x4 g = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int o = 0; o < O; ++o) {
+          const f32x4 dz = reinterpret_cast<const f32x4*>(dzs + N * o)[q];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            acc[o] = fmaf(x[e], dz[e], acc[o]);
+            g[e] = fmaf(dz[e], wf[o], g[e]);
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) g[e] = (0.f + g[e]) * relu_mask(x[e]);
+        f32x4* out = reinterpret_cast<f32x4*>(dX + base) + q;
+        if (POOL > 0) {
+#pragma unroll
+          for (int ph = 0; ph < (POOL > 0 ? POOL : 1); ++ph)
+#pragma unroll
+            for (int pw = 0; pw < (POOL > 0 ? POOL : 1); ++pw) {
+              f32x4 v;
+#pragma unroll
+              for (int e = 0; e < 4; ++e) v[e] = mi[e] == ph * pool + pw ? g[e] : 0.f;
+              out[(sh * ph + sw * pw) / 4] = v;
+            }
+        } else {
+          for (int ph = 0; ph < pool; ++ph)
+            for (int pw = 0; pw < pool; ++pw) {
+              f32x4 v;
+#pragma unroll
+              for (int e = 0; e < 4; ++e) v[e] = mi[e] == ph * pool + pw ? g[e] : 0.f;
+              out[(sh * ph + sw * pw) / 4] = v;
+            }
+        }
+      }
+    }
+#pragma unroll
+    for (int o = 0; o < O; ++o) {
+      float a = acc[o];
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) a += __shfl_xor(a, off, 64);
+      acc[o] = a;
+    }
+    if (lane == 0) {
+      float prev[O];
+#pragma unroll
+      for (int o = 0; o < O; ++o) prev[o] = accumulate ? gW[f + (int64_t)F * o] : 0.f;
+#pragma unroll
+      for (int o = 0; o < O; ++o) gW[f + (int64_t)F * o] = accumulate ? acc[o] + prev[o] : acc[o];
+    }
+  }
+  // bias gradient: output o = 4 block + wave sums dZ's column o (each lane
+  // its four rows in order, then the butterfly)
+  const int o = blockIdx.x * 4 + w;
+  if (gb && o < O) {
+    float sum = 0.f;
+    for (int q = lane; 4 * q < N; q += 64) {
+      const f32x4 dz = reinterpret_cast<const f32x4*>(dzs + N * o)[q];
+      sum += dz[0];
+      sum += dz[1];
+      sum += dz[2];
+      sum += dz[3];
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+    if (lane == 0) gb[o] = accumulate ? gb[o] + sum : sum;
+  }
 }
 
 template <int O>
 void launch_linear_bwd_maxpool(unsigned grid, hipStream_t st, const PoolDims& d, const float* P,
                                const int32_t* idx, const float* W, const float* dZ, float* gW, float* gb,
                                float* dX, int accumulate) {
-  if (d.pool == 2)
+  const bool vec = d.N % 4 == 0 && aligned16(P) && aligned16(idx) && aligned16(dZ) && aligned16(dX);
+  if (vec && d.pool == 2)
+    hipLaunchKernelGGL((linear_bwd_maxpool_vec_kernel<O, 2>), dim3(grid), dim3(256), 0, st, d, P, idx, W, dZ, gW,
+                       gb, dX, accumulate);
+  else if (vec)
+    hipLaunchKernelGGL((linear_bwd_maxpool_vec_kernel<O, 0>), dim3(grid), dim3(256), 0, st, d, P, idx, W, dZ, gW,
+                       gb, dX, accumulate);
+  else if (d.pool == 2)
     hipLaunchKernelGGL((linear_bwd_maxpool_kernel<O, 2>), dim3(grid), dim3(256), 0, st, d, P, idx, W, dZ, gW, gb,
                        dX, accumulate);
   else
@@ -518,7 +647,9 @@ int cnhip_linear_backward_maxpool_relu(const float* P, const int32_t* idx, const
   const double bytes = 8.0 * (double)N * F + 4.0 * (double)N * C * H * Wd +
                        (accumulate ? 8.0 : 4.0) * (double)F * out_features + 4.0 * (double)N * out_features;
   cnhip::HbmTimer timer("linear_bwd_maxpool_kernel", bytes, st);
-  const unsigned grid = (unsigned)std::min<int64_t>((F + 3) / 4, 1024);
+  // a wave per feature (up to 1024 blocks), and at least one wave per output
+  // for the bias gradient
+  const unsigned grid = (unsigned)std::max<int64_t>(std::min<int64_t>((F + 3) / 4, 1024), (out_features + 3) / 4);
   cnhip::dispatch_linear_bwd_maxpool(std::make_integer_sequence<int, cnhip::kLinPoolMaxO>{}, (int)out_features,
                                      grid, st, d, P, idx, W, dZ, grad_W, grad_b, dX, accumulate);
   return cnhip::check_launch(who);

@@ -289,10 +289,9 @@ int cnhip_maxpool2d_backward_relu_pooled(const float* dY, const int32_t* idx, co
  * cnhip_linear_backward then cnhip_maxpool2d_backward_relu_pooled compute
  * them.  P [N, C, HO, WO] is the pooled output (the Linear's input, F =
  * C HO WO) and idx its argmax, as cnhip_conv2d_forward_relu_maxpool writes
- * them.  grad_W and grad_b are bit-identical to cnhip_linear_backward's
- * when its weight gradient runs the wave-per-output SIMT kernel (batch > 64
- * and 2 F O N <= 32 MFLOP); dX may differ from the MFMA product there in
- * the last bits (the sum over O runs in ascending order here).  Needs
+ * them.  Sums run in a fixed order (a lane's rows, then an xor butterfly
+ * over the lanes; dX over O ascending), so the results can differ from
+ * the separate calls' in the last bits.  Needs
  * windows that tile the input (stride == pool, dividing H and W), O <= 16
  * and N O <= 8192 (cnhip_linear_backward_maxpool_relu_fits).  Replaces
  * Linear::backward (linear.cpp:335-358) + Flatten::backward + MaxPool2D::
