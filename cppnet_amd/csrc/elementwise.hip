@@ -333,6 +333,61 @@ __global__ void __launch_bounds__(SCE_BLOCK) softmax_ce_head_kernel(
   }
 }
 
+// softmax_ce_rows_kernel for C <= REG classes with the row in registers (all
+// of a row's loads in flight at once) and, when g is given, the gradient of
+// softmax_ce_backward_kernel written as well: the same arithmetic and the same
+// per-block partials, in one pass.
+template <int REG>
+__global__ void __launch_bounds__(SCE_BLOCK) softmax_ce_rows_reg_kernel(
+    const float* __restrict__ z, const float* __restrict__ t, float* __restrict__ sm,
+    float* __restrict__ partial, float* __restrict__ g, int64_t B, int64_t C, int mean, float inv_batch) {
+  __shared__ float smem[SCE_BLOCK / 64];
+  float row = 0.f;
+  const int64_t b = (int64_t)blockIdx.x * SCE_BLOCK + threadIdx.x;
+  if (b < B) {
+    float zr[REG], tr[REG], er[REG];
+#pragma unroll
+    for (int c = 0; c < REG; ++c) {
+      zr[c] = c < C ? z[b + B * c] : 0.f;
+      tr[c] = c < C ? t[b + B * c] : 0.f;
+    }
+    float mx = zr[0];
+#pragma unroll
+    for (int c = 1; c < REG; ++c)
+      if (c < C) mx = fmaxf(mx, zr[c]);
+    float se = 0.f;
+#pragma unroll
+    for (int c = 0; c < REG; ++c)
+      if (c < C) {
+        er[c] = expf(zr[c] - mx);
+        se += er[c];
+      }
+    const float ls = logf(se + 1e-12f);
+#pragma unroll
+    for (int c = 0; c < REG; ++c)
+      if (c < C) {
+        const float p = er[c] / se;
+        sm[b + B * c] = p;
+        row -= tr[c] * ((zr[c] - mx) - ls);
+        if (g) {
+          float v = p - tr[c];
+          if (mean) v *= inv_batch;
+          g[b + B * c] = v;
+        }
+      }
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) row += __shfl_xor(row, off, 64);
+  if (lane == 0) smem[wave] = row;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float s = 0.f;
+    for (int w = 0; w < SCE_BLOCK / 64; ++w) s += smem[w];
+    partial[blockIdx.x] = s;
+  }
+}
+
 __global__ void __launch_bounds__(RB) partial_sum_kernel(const float* __restrict__ partial,
                                                          int64_t count, float* __restrict__ out,
                                                          float divisor) {
@@ -451,6 +506,54 @@ int cnhip_mse_backward(const float* pred, const float* target, float* grad, int6
   return cnhip::check_launch(who);
 }
 
+namespace cnhip {
+namespace {
+// Softmax-CE over a batch of any size: per-block rows (+ the gradient when g
+// is given) and partial losses, then partial_sum_kernel.  The two kernels
+// give the same values; the register form serves rows of up to 32 classes.
+int softmax_ce_multi(const float* logits, const float* targets, float* softmax_out, float* loss, float* g,
+                     int64_t batch, int64_t classes, int reduction, hipStream_t st, const char* who) {
+  const int64_t blocks = (batch + SCE_BLOCK - 1) / SCE_BLOCK;
+  CNHIP_REQUIRE(blocks < ((int64_t)1 << 31), "%s: batch too large", who);
+  void* ws = nullptr;
+  CNHIP_TRY(scratch(st, kScratchLayer, (size_t)blocks * sizeof(float), &ws, who));
+  float* partial = static_cast<float*>(ws);
+  const int mean = reduction == CNHIP_REDUCE_MEAN ? 1 : 0;
+  const float inv = 1.0f / (float)batch;
+  {
+    // logits and targets read, softmax (and the gradient) and the partials written
+    HbmTimer timer("softmax_ce_rows_kernel", (g ? 16.0 : 12.0) * (double)batch * (double)classes + 4.0 * blocks,
+                   st);
+    if (classes <= 16)
+      hipLaunchKernelGGL(softmax_ce_rows_reg_kernel<16>, dim3((unsigned)blocks), dim3(SCE_BLOCK), 0, st, logits,
+                         targets, softmax_out, partial, g, batch, classes, mean, inv);
+    else if (classes <= 32)
+      hipLaunchKernelGGL(softmax_ce_rows_reg_kernel<32>, dim3((unsigned)blocks), dim3(SCE_BLOCK), 0, st, logits,
+                         targets, softmax_out, partial, g, batch, classes, mean, inv);
+    else
+      hipLaunchKernelGGL(softmax_ce_rows_kernel, dim3((unsigned)blocks), dim3(SCE_BLOCK), 0, st, logits, targets,
+                         softmax_out, partial, batch, classes);
+    CNHIP_TRY(check_launch(who));
+  }
+  {
+    // "mean" divides the summed loss by the batch size (softmax_cross_entropy.cpp:154-156)
+    const float divisor = reduction == CNHIP_REDUCE_MEAN ? (float)batch : 1.0f;
+    HbmTimer timer("partial_sum_kernel", 4.0 * blocks + 4.0, st);
+    hipLaunchKernelGGL(partial_sum_kernel, dim3(1), dim3(RB), 0, st, partial, blocks, loss, divisor);
+    CNHIP_TRY(check_launch(who));
+  }
+  if (g && classes > 32) {
+    const int64_t n = batch * classes;
+    HbmTimer timer("softmax_ce_backward_kernel", 12.0 * (double)n, st);
+    hipLaunchKernelGGL(softmax_ce_backward_kernel, dim3(elementwise_grid(n, 256)), dim3(256), 0, st, softmax_out,
+                       targets, g, n, mean, inv);
+    CNHIP_TRY(check_launch(who));
+  }
+  return CNHIP_OK;
+}
+}  // namespace
+}  // namespace cnhip
+
 int cnhip_softmax_ce_forward(const float* logits, const float* targets, float* softmax_out,
                              float* loss, int64_t batch, int64_t classes, int reduction,
                              cnhip_stream_t s) {
@@ -458,29 +561,8 @@ int cnhip_softmax_ce_forward(const float* logits, const float* targets, float* s
   CNHIP_TRY(cnhip::check_reduction(reduction, who));
   CNHIP_REQUIRE(batch > 0 && classes > 0, "%s: empty input", who);
   CNHIP_REQUIRE(logits && targets && softmax_out && loss, "%s: NULL pointer", who);
-  hipStream_t st = as_stream(s);
-  const int64_t blocks = (batch + cnhip::SCE_BLOCK - 1) / cnhip::SCE_BLOCK;
-  CNHIP_REQUIRE(blocks < ((int64_t)1 << 31), "%s: batch too large", who);
-  void* ws = nullptr;
-  CNHIP_TRY(cnhip::scratch(st, cnhip::kScratchLayer, (size_t)blocks * sizeof(float), &ws, who));
-  float* partial = static_cast<float*>(ws);
-  int status;
-  {
-    // logits and targets read, softmax and the per-block partial losses written
-    cnhip::HbmTimer timer("softmax_ce_rows_kernel", 12.0 * (double)batch * (double)classes + 4.0 * blocks, st);
-    hipLaunchKernelGGL(cnhip::softmax_ce_rows_kernel, dim3((unsigned)blocks), dim3(cnhip::SCE_BLOCK),
-                       0, st, logits, targets, softmax_out, partial, batch, classes);
-    status = cnhip::check_launch(who);
-  }
-  if (status == CNHIP_OK) {
-    // "mean" divides the summed loss by the batch size (softmax_cross_entropy.cpp:154-156)
-    const float divisor = reduction == CNHIP_REDUCE_MEAN ? (float)batch : 1.0f;
-    cnhip::HbmTimer timer("partial_sum_kernel", 4.0 * blocks + 4.0, st);
-    hipLaunchKernelGGL(cnhip::partial_sum_kernel, dim3(1), dim3(cnhip::RB), 0, st, partial, blocks,
-                       loss, divisor);
-    status = cnhip::check_launch(who);
-  }
-  return status;
+  return cnhip::softmax_ce_multi(logits, targets, softmax_out, loss, nullptr, batch, classes, reduction,
+                                 as_stream(s), who);
 }
 
 int cnhip_softmax_ce_head(const float* logits, const float* targets, float* softmax_out, float* loss,
@@ -489,10 +571,9 @@ int cnhip_softmax_ce_head(const float* logits, const float* targets, float* soft
   CNHIP_TRY(cnhip::check_reduction(reduction, who));
   CNHIP_REQUIRE(batch > 0 && classes > 0, "%s: empty input", who);
   CNHIP_REQUIRE(logits && targets && softmax_out && loss && grad, "%s: NULL pointer", who);
-  if (batch > cnhip::SCE_BLOCK) {
-    CNHIP_TRY(cnhip_softmax_ce_forward(logits, targets, softmax_out, loss, batch, classes, reduction, s));
-    return cnhip_softmax_ce_backward(softmax_out, targets, grad, batch, classes, reduction, s);
-  }
+  if (batch > cnhip::SCE_BLOCK)
+    return cnhip::softmax_ce_multi(logits, targets, softmax_out, loss, grad, batch, classes, reduction, as_stream(s),
+                                   who);
   const float divisor = reduction == CNHIP_REDUCE_MEAN ? (float)batch : 1.0f;
   cnhip::HbmTimer timer("softmax_ce_head_kernel", 20.0 * (double)batch * (double)classes + 4.0, as_stream(s));
   const int mean = reduction == CNHIP_REDUCE_MEAN ? 1 : 0;

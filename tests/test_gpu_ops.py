@@ -412,12 +412,13 @@ def test_sigmoid_bce_head_matches_separate_kernels(gpu, n, red_f, red_b):
 
 
 @pytest.mark.parametrize("B,C", [(1, 1), (32, 4), (256, 10), (200, 7), (64, 16), (100, 17), (256, 32),
-                                 (77, 33), (257, 10), (4096, 10)])
+                                 (77, 33), (257, 10), (4096, 10), (300, 40), (600, 32)])
 @pytest.mark.parametrize("red", [0, 1])
 def test_softmax_ce_head_matches_separate_kernels(gpu, B, C, red):
     """cnhip_softmax_ce_head against cnhip_softmax_ce_forward +
     cnhip_softmax_ce_backward: softmax, loss and gradient bit-identical (one
-    launch up to 256 rows, the two calls beyond)."""
+    launch up to 256 rows; beyond, per-block rows with the gradient for up
+    to 32 classes, the separate backward kernel for more)."""
     from cppnet_amd import _capi
     lib = _capi.load()
     print(f"[ops] softmax-CE head B={B} C={C} red={red}", flush=True)
