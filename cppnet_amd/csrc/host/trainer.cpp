@@ -98,7 +98,7 @@ namespace
         {
             DeviceTensor x = pool->backward(fc->backward(g));
             for (auto it = blocks.rbegin(); it != blocks.rend(); ++it) x = it->backward(x);
-            emb->backward(x);
+            emb->backward(x, false);  // the ids take no gradient
         }
 
         void update(Optimizers::Optimizer& opt, float lr)

@@ -96,7 +96,9 @@ namespace CppNet
             return out;
         }
 
-        DeviceTensor Embedding::backward(const DeviceTensor& g)
+        DeviceTensor Embedding::backward(const DeviceTensor& g) { return backward(g, true); }
+
+        DeviceTensor Embedding::backward(const DeviceTensor& g, bool input_grad)
         {
             if (!ids_cache_.defined()) throw std::runtime_error("Embedding::backward before forward");
             const int64_t B = ids_cache_.dimension(0), S = ids_cache_.dimension(1);
@@ -106,7 +108,7 @@ namespace CppNet
                                                         vocab_size_, embed_dim_, rows_, Device::stream()),
                           "Embedding::backward");
             grads_zero_ = false;
-            return DeviceTensor::zeros({B, S, embed_dim_});  // embedding.cpp:171-174
+            return input_grad ? DeviceTensor::zeros({B, S, embed_dim_}) : DeviceTensor();  // embedding.cpp:171-174
         }
 
         Tensor<float, 3> Embedding::forward(const Tensor<int, 2>& input)

@@ -42,6 +42,12 @@ namespace CppNet
             /// stays asynchronous.  Out-of-range ids still produce zero rows.
             DeviceTensor forward(const DeviceTensor& ids, bool ids_checked);
             DeviceTensor backward(const DeviceTensor& grad_output);
+            /// backward() with the input gradient optional: the ids are not
+            /// differentiable, so the reference returns zeros
+            /// (embedding.cpp:171-174); input_grad = false (a model's first
+            /// layer in a training step) skips allocating and clearing them
+            /// and returns an undefined tensor.
+            DeviceTensor backward(const DeviceTensor& grad_output, bool input_grad);
 
             bool is_trainable() const override { return trainable_; }
             void step(Optimizers::Optimizer& optimizer, float learning_rate) override;
