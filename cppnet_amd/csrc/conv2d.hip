@@ -399,18 +399,6 @@ __global__ void __launch_bounds__(256) conv_direct_pool_fwd_kernel(ConvArgs a, i
   }
 }
 
-// Wd[k' + K'*ic] = W[oc + OC*(ic + C*t)], k' = oc + OC*t
-__global__ void __launch_bounds__(256) conv_relayout_w_kernel(const float* __restrict__ Wt,
-                                                              float* __restrict__ Wd, int64_t OC,
-                                                              int64_t C, int64_t T) {
-  const int64_t total = OC * C * T, Kp = OC * T;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t oc = i % OC, ic = (i / OC) % C, t = i / (OC * C);
-    Wd[(oc + OC * t) + Kp * ic] = Wt[i];
-  }
-}
-
 // ---------------------------------------------------------------- wgrad
 // M = OC, Ng = C*T (+1 ones-column for the bias), contraction index
 // k = n + N*q over (sample, output pixel); split over blockIdx.z.
@@ -566,9 +554,15 @@ __global__ void __launch_bounds__(C::NT) conv_wgrad_kernel(ConvArgs a) {
 // block each sum one contiguous chunk of z in ascending order, and the chunk
 // sums are added in ascending order: a fixed summation order for any launch.
 constexpr int WGRAD_RW = 16;
+// With Wr set, the same launch also writes the input-gradient pass's copy of
+// W as [OC*T, C]: Wr[k' + OC*T*ic] = W[oc + OC*(ic + C*t)], k' = oc + OC*t,
+// T = CT / C.  W does not change during the backward, so the copy needs no
+// launch of its own (a separate one cost ~4.6 us for 18 K floats at config
+// 3's conv2).
 __global__ void __launch_bounds__(64 * WGRAD_RW) conv_wgrad_reduce_kernel(
     const float* __restrict__ partial, int splits, int64_t OC, int64_t CT, int has_bias,
-    float* __restrict__ gW, float* __restrict__ gb) {
+    float* __restrict__ gW, float* __restrict__ gb, const float* __restrict__ W,
+    float* __restrict__ Wr, int64_t C) {
   __shared__ float part[WGRAD_RW][64];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int64_t Ng = CT + has_bias, total = OC * Ng;
@@ -589,6 +583,14 @@ __global__ void __launch_bounds__(64 * WGRAD_RW) conv_wgrad_reduce_kernel(
     const int64_t j = e / OC;
     if (j < CT) gW[e] = t;
     else if (gb) gb[e - OC * CT] = t;
+  }
+  if (Wr) {
+    const int64_t T = CT / C, Kp = OC * T, n = OC * CT;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x) {
+      const int64_t oc = i % OC, ic = (i / OC) % C, t = i / (OC * C);
+      Wr[(oc + OC * t) + Kp * ic] = W[i];
+    }
   }
 }
 
@@ -650,7 +652,9 @@ void launch_pixel(const ConvArgs& a, int64_t Ng, int64_t K, int64_t pixels, int6
 // Weight-gradient launch for an OC x Ng tile grid: split-K partials, then a
 // fixed-order sum into gW / gb.  Small tiles split each k-tile over WGK wave
 // groups so a block has 4 or 8 waves.
-int launch_wgrad(ConvArgs a, float* gW, float* gb, hipStream_t st, const char* who) {
+// W and Wr: see conv_wgrad_reduce_kernel (both null: no relayout).
+int launch_wgrad(ConvArgs a, float* gW, float* gb, const float* W, float* Wr, hipStream_t st,
+                 const char* who) {
   const ConvDims& d = a.d;
   const int64_t CT = d.C * d.KS * d.KS, Ng = CT + a.has_bias, Kc = d.N * d.HO * d.WO;
   // target: blocks to aim for with split-K (fewer, longer blocks cut the
@@ -675,10 +679,11 @@ int launch_wgrad(ConvArgs a, float* gW, float* gb, hipStream_t st, const char* w
     int status = check_launch(who);
     if (rec) (void)hipEventRecord(rec->stop, st);
     if (status == CNHIP_OK) {
-      HbmTimer timer("conv_wgrad_reduce_kernel", 4.0 * (double)(splits + 1) * d.OC * Ng, st);
+      HbmTimer timer("conv_wgrad_reduce_kernel",
+                     4.0 * (double)(splits + 1) * d.OC * Ng + (Wr ? 8.0 * (double)d.OC * CT : 0.0), st);
       hipLaunchKernelGGL(conv_wgrad_reduce_kernel, dim3((unsigned)((d.OC * Ng + 63) / 64)),
                          dim3(64 * WGRAD_RW), 0, st, a.partial, (int)splits, d.OC, CT, a.has_bias,
-                         gW, gb);
+                         gW, gb, W, Wr, d.C);
       status = check_launch(who);
     }
     return status;
@@ -802,30 +807,26 @@ int cnhip_conv2d_backward(const float* X, const float* W, const float* dY, float
   a.d = d; a.src = X; a.dY = dY;
   a.has_bias = gb ? 1 : 0;
   a.aligned = cnhip::aligned16(X) && cnhip::aligned16(dY);  // N % KT is checked per tile shape
-  CNHIP_TRY(cnhip::launch_wgrad(a, gW, gb, st, who));
-
-  // ---- input grad: relay W out as [OC*T, C], then per-input-pixel GEMMs
+  // W relaid out as [OC*T, C] for the input gradient, written by the weight
+  // gradient's reduce launch into the GEMM scratch slot (the wgrad partials
+  // hold the layer slot; nothing on this path runs a GEMM)
+  float* Wr = nullptr;
   if (dX) {
     void* ws = nullptr;
-    CNHIP_TRY(cnhip::scratch(st, cnhip::kScratchLayer, (size_t)OC * CT * sizeof(float), &ws, who));
-    float* Wr = static_cast<float*>(ws);
-    int status;
-    {
-      cnhip::HbmTimer timer("conv_relayout_w_kernel", 8.0 * (double)OC * CT, st);
-      hipLaunchKernelGGL(cnhip::conv_relayout_w_kernel, dim3(cnhip::elementwise_grid(OC * CT, 256)),
-                         dim3(256), 0, st, W, Wr, OC, C, T);
-      status = cnhip::check_launch(who);
-    }
-    if (status == CNHIP_OK) {
-      cnhip::ConvArgs b{};
-      b.d = d; b.src = dY; b.wt = Wr; b.out = dX;
-      b.out_vec = (N % 4 == 0) && cnhip::aligned16(dX);
-      b.src_vec = (N % 4 == 0) && cnhip::aligned16(dY);
-      b.wt_vec = (OC * T) % 4 == 0;  // Wd is a scratch buffer: 256-byte aligned
-      cnhip::launch_pixel<true>(b, C, OC * T, H * Wd, N * OC * d.HO * d.WO, st);
-      status = cnhip::check_launch(who);
-    }
-    CNHIP_TRY(status);
+    CNHIP_TRY(cnhip::scratch(st, cnhip::kScratchGemm, (size_t)OC * CT * sizeof(float), &ws, who));
+    Wr = static_cast<float*>(ws);
+  }
+  CNHIP_TRY(cnhip::launch_wgrad(a, gW, gb, W, Wr, st, who));
+
+  // ---- input grad: per-input-pixel GEMMs over the relaid-out W
+  if (dX) {
+    cnhip::ConvArgs b{};
+    b.d = d; b.src = dY; b.wt = Wr; b.out = dX;
+    b.out_vec = (N % 4 == 0) && cnhip::aligned16(dX);
+    b.src_vec = (N % 4 == 0) && cnhip::aligned16(dY);
+    b.wt_vec = (OC * T) % 4 == 0;  // Wr is a scratch buffer: 256-byte aligned
+    cnhip::launch_pixel<true>(b, C, OC * T, H * Wd, N * OC * d.HO * d.WO, st);
+    CNHIP_TRY(cnhip::check_launch(who));
   }
   return CNHIP_OK;
 }
