@@ -65,55 +65,6 @@ __global__ void __launch_bounds__(256) column_sum_kernel(const float* __restrict
   if (lane == 0) out[col] = accumulate ? out[col] + s : s;
 }
 
-// column_sum_kernel's float4 form (rows % 4 == 0, 16-byte aligned) with WPC
-// waves per column and 4 / WPC columns per 256-thread block, so that few
-// columns still spread over the 256 CUs: at [8192, 512] one wave per column
-// gave 128 blocks, each lane streaming 32 KB with 4 loads in flight.  Used
-// with WPC = 4 for fewer than 1024 columns.  Wave w of a column takes
-// float4s w*64 + lane, + 64*WPC, ..: eight loads in flight per lane into
-// eight running sums, added pairwise, then across the wave, then the
-// column's waves in order.  The order is fixed for a given shape.
-template <int WPC>
-__global__ void __launch_bounds__(256) column_sum_vec_kernel(const float* __restrict__ in,
-                                                             float* __restrict__ out, int64_t rows,
-                                                             int64_t cols, int accumulate) {
-  constexpr int CPB = 4 / WPC;  // columns per block
-  __shared__ float part[4];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int64_t col = (int64_t)blockIdx.x * CPB + w / WPC;
-  const int sub = w % WPC;
-  float s = 0.f;
-  if (col < cols) {
-    const int64_t n4 = rows >> 2;
-    const f32x4* p4 = reinterpret_cast<const f32x4*>(in + rows * col);
-    constexpr int64_t STEP = 64 * WPC;
-    f32x4 a[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) a[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    int64_t i = (int64_t)sub * 64 + lane;
-    for (; i + 7 * STEP < n4; i += 8 * STEP) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) a[j] += p4[i + j * STEP];
-    }
-#pragma unroll
-    for (int j = 0; j < 7; ++j)
-      if (i + j * STEP < n4) a[j] += p4[i + j * STEP];
-    const f32x4 t = ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]));
-    s = (t[0] + t[1]) + (t[2] + t[3]);
-  }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
-  if (WPC > 1) {
-    if (lane == 0) part[w] = s;
-    __syncthreads();
-    if (sub != 0) return;
-    s = part[w];
-#pragma unroll
-    for (int j = 1; j < WPC; ++j) s += part[w + j];
-  }
-  if (lane == 0 && col < cols) out[col] = accumulate ? out[col] + s : s;
-}
-
 // Backward of a Linear with few outputs over a wide input (a classifier
 // head, O <= 16), in one pass over X instead of the dW GEMM, its split-K
 // reduce, the bias column sum and the dX GEMM:
@@ -375,15 +326,8 @@ int column_sum(const float* in, float* out, int64_t rows, int64_t cols, int accu
   const int vec = (rows % 4 == 0) && aligned16(in);
   HbmTimer timer("column_sum_kernel", 4.0 * (double)rows * (double)cols + (accumulate ? 8.0 : 4.0) * (double)cols,
                  st);
-  // fewer than 1024 columns: four waves per column, one column per block
-  // (measured on MI355X: [8192, 512] 3.8 -> 3.3 us; from 1024 columns on the
-  // one-wave form was as fast or faster, [4096, 4096] 11.2 against 12.4 us)
-  if (vec && cols < 1024)
-    hipLaunchKernelGGL(column_sum_vec_kernel<4>, dim3((unsigned)cols), dim3(256), 0, st, in, out, rows,
-                       cols, accumulate);
-  else
-    hipLaunchKernelGGL(column_sum_kernel, dim3((unsigned)((cols + 3) / 4)), dim3(256), 0, st, in, out,
-                       rows, cols, accumulate, vec);
+  hipLaunchKernelGGL(column_sum_kernel, dim3((unsigned)((cols + 3) / 4)), dim3(256), 0, st, in, out,
+                     rows, cols, accumulate, vec);
   return check_launch(who);
 }
 
