@@ -19,9 +19,13 @@ moments are resident in HBM before timing starts.  Prints ONE JSON line:
                    launch / event-timed launch duration, against 8 TB/s
   cpu_baseline     the CPU oracle (a restatement of the reference's cpu-eigen
                    semantics, oracle/) on a bounded sample of the same workload
+  other_configs    the four other configs, GPU legs only, timed the same way
+                   (20 steps each, config 1: 200): samples/s, ms/step, their
+                   roofline and their four longest bandwidth-bound kernels;
+                   --only leaves them out
 
 Usage: python bench.py [--gpus 1] [--config 2] [--steps K] [--warmup W]
-                       [--no-cpu-baseline] [--cpu-seconds S] [--graph]
+                       [--no-cpu-baseline] [--cpu-seconds S] [--graph] [--only]
 
 --graph replays the step's zero_grad + forward + loss + backward as one
 captured HIP graph (cnt_capture_step) and then runs the fused Adam update
@@ -305,56 +309,39 @@ def loader_leg(sess, cfg, B, steps, step_ms, mode):
     return out
 
 
-def main() -> int:
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
-    ap.add_argument("--steps", type=int, default=None, help="default 50 (config 1: 200)")
-    ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=20.0)
-    ap.add_argument("--graph", action="store_true",
-                    help="replay the step's zero_grad + forward + loss + backward as one captured "
-                         "HIP graph (cnt_capture_step), Adam eagerly after it; same results bit for "
-                         "bit, measured no faster on MI355X (the cost per kernel is GPU-side)")
-    ap.add_argument("--traffic-calibration", action="store_true",
-                    help="only run the known-traffic reference kernel (cnhip_add over 64 Mi floats, "
-                         "5 times: 512 MiB read + 256 MiB written per launch) that scales the PMC "
-                         "FETCH_SIZE / WRITE_SIZE counts behind roofline.traffic")
-    ap.add_argument("--loader", choices=["resident", "stream", "both"], default=None,
-                    help="also time the same steps fed by the DataLoader (configs 1-4): 'resident' "
-                         "gathers each batch in HBM, 'stream' uploads it from page-locked host "
-                         "memory on a copy stream; reported under 'loader', never as 'value'")
-    args = ap.parse_args()
-    if args.traffic_calibration:
-        return traffic_calibration()
-    if args.gpus != 1:
-        print(f"bench.py: this build runs on one GPU only (got --gpus {args.gpus}); the "
-              "multi-GPU data-parallel design is described, not built", file=sys.stderr)
-        return 2
-    steps = args.steps if args.steps is not None else (200 if args.config == 1 else 50)
+KERNEL_CLASS = {
+    3: "gemm_f32_kernel + conv_pixel/conv_wgrad_kernel (fp32 MFMA, all shapes of the step)",
+    4: "gemm_f32_kernel + lstm_fwd/bwd_persist_kernel (fp32 MFMA; the whole recurrence of "
+       "each pass in one launch, cell update fused, the backward also accumulating "
+       "dW_hh, dW_ih and db)"}
+DEFAULT_KERNEL_CLASS = "gemm_f32_kernel (fp32 MFMA GEMM, all shapes of the step)"
 
+
+def measure(config: int, steps: int, warmup: int, graph: bool = False, loader: str | None = None,
+            hbm_detail: bool = True) -> dict:
+    """Times `steps` train steps of one config after `warmup` untimed ones,
+    inputs resident in HBM, between HIP events on the session's stream; then
+    three more eager steps with per-launch events around the MFMA class and
+    three around the bandwidth-bound kernels.  Returns the per-config part of
+    the JSON line (no cpu_baseline)."""
     import ctypes as C
 
     import numpy as np
     from cppnet_amd import _capi, trainer
 
     lib = _capi.load()
-    if lib.cnhip_device_count() < 1:
-        log("bench.py: no GPU visible")
-        return 1
-    cfg, synth, _, flops_fn, desc = workload(args.config)
+    cfg, synth, _, flops_fn, desc = workload(config)
     B = cfg.batch
     params, X, Y = synth(cfg, np.random.default_rng(2024))
     sess = trainer.Session(cfg)
     sess.set_params(params)
     sess.set_batch(X, Y)           # resident in HBM from here on
     stream = sess.stream
-    log(f"bench.py: {desc}, batch {B}: {args.warmup} warmup + {steps} timed steps")
+    log(f"bench.py: {desc}, batch {B}: {warmup} warmup + {steps} timed steps")
 
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         sess.step(read_loss=False)
-    if args.graph:
+    if graph:
         # zero_grad + forward + loss + backward replayed as one HIP graph; the
         # Adam update still runs every step, eagerly, after the replay
         sess.capture()
@@ -374,12 +361,14 @@ def main() -> int:
     wall = time.perf_counter() - t0
     ms = C.c_float()
     _capi.check(lib.cnhip_event_elapsed_ms(C.byref(ms), ev0, ev1))
+    _capi.check(lib.cnhip_event_destroy(ev0))
+    _capi.check(lib.cnhip_event_destroy(ev1))
     step_ms = ms.value / steps
     loss = sess.step()  # one more step, read back: the run trained on finite numbers
     if not np.isfinite(loss):
-        log(f"bench.py: non-finite loss {loss}")
-        return 1
-    log(f"bench.py: {step_ms:.4f} ms/step, loss {loss:.6f}")
+        sess.close()
+        raise RuntimeError(f"config {config}: non-finite loss {loss}")
+    log(f"bench.py: config {config}: {step_ms:.4f} ms/step, loss {loss:.6f}")
 
     # Dominant kernel class: per-launch timing over a few extra eager steps
     # (a graph replay records no per-launch events).
@@ -414,50 +403,113 @@ def main() -> int:
                             "achieved_GBs": round(gbs, 1),
                             "frac": round(gbs / PEAK_HBM_GBS, 4)})
 
-    kernels = {3: "gemm_f32_kernel + conv_pixel/conv_wgrad_kernel (fp32 MFMA, all shapes of the step)",
-               4: "gemm_f32_kernel + lstm_fwd/bwd_persist_kernel (fp32 MFMA; the whole recurrence of "
-                  "each pass in one launch, cell update fused, the backward also accumulating "
-                  "dW_hh, dW_ih and db)"}.get(
-        args.config, "gemm_f32_kernel (fp32 MFMA GEMM, all shapes of the step)")
     result = {
-        "metric": METRIC,
         "value": round(B / (step_ms * 1e-3), 1),
         "unit": "samples/s",
-        "n_gpus": 1,
         "steps": steps,
-        "warmup": args.warmup,
+        "warmup": warmup,
         "ms_per_step": round(step_ms, 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "fp32",
-        "data": "synthetic (seeded inputs/labels, reference init distributions; resident in HBM)",
         "config": {"workload": desc, "global_batch": B, "parallelism": "single GPU",
                    "params": int(sum(p.size for p in params)),
                    "step_tflops": round(flops_fn(cfg) / (step_ms * 1e-3) / 1e12, 2),
                    "execution": ("captured fwd+bwd HIP graph replay + eager fused Adam, every step"
-                                 if args.graph else "eager launches on one stream"),
+                                 if graph else "eager launches on one stream"),
                    "wall_s_timed_region": round(wall, 3)},
-        "roofline": ({"bound": "mfma", "kernel": kernels,
+        "roofline": ({"bound": "mfma", "kernel": KERNEL_CLASS.get(config, DEFAULT_KERNEL_CLASS),
                      "achieved": round(achieved, 2), "peak": PEAK_FP32_MFMA_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4),
-                     "traffic": PMC_TRAFFIC_BYTES.get(args.config),
+                     "traffic": PMC_TRAFFIC_BYTES.get(config),
                      "traffic_unit": "bytes per launch (rocprofv3 PMC, see profiles/)",
                      "launches_per_step": launches.value // prof_steps,
                      "avg_launch_us": round(per_launch_us, 2),
                      "flops_per_launch": flops_per_launch,
                      "share_of_step": round(gemm_share, 3)}
                      if launches.value else small_roofline(hbm_kernels, step_ms)),
-        "hbm_kernels": {"peak_GBs": PEAK_HBM_GBS,
-                        "note": "algorithmic bytes (inputs read once, outputs written once) / "
-                                "event-timed launch duration, per bandwidth-bound kernel",
-                        "kernels": hbm_kernels},
-        "cpu_baseline": None,
+        "hbm_kernels": ({"peak_GBs": PEAK_HBM_GBS,
+                         "note": "algorithmic bytes (inputs read once, outputs written once) / "
+                                 "event-timed launch duration, per bandwidth-bound kernel",
+                         "kernels": hbm_kernels} if hbm_detail else
+                        {"top": [{k: r[k] for k in ("kernel", "launches_per_step", "avg_us", "frac")}
+                                 for r in hbm_kernels[:4]]}),
     }
-    if args.loader and args.config != 5:
-        modes = ["resident", "stream"] if args.loader == "both" else [args.loader]
+    if loader and config != 5:
+        modes = ["resident", "stream"] if loader == "both" else [loader]
         result["loader"] = [loader_leg(sess, cfg, B, steps, step_ms, m) for m in modes]
     sess.close()
+    return result
+
+
+EXTRA_STEPS = {1: 200, 3: 20, 4: 20, 5: 20}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
+    ap.add_argument("--steps", type=int, default=None, help="default 50 (config 1: 200)")
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--only", action="store_true",
+                    help="measure only --config; by default the other four configs are also timed "
+                         "(GPU legs only, 20 steps each after 5 warm-up steps; config 1: 200) and "
+                         "reported under 'other_configs'")
+    ap.add_argument("--graph", action="store_true",
+                    help="replay the step's zero_grad + forward + loss + backward as one captured "
+                         "HIP graph (cnt_capture_step), Adam eagerly after it; same results bit for "
+                         "bit, measured no faster on MI355X (the cost per kernel is GPU-side)")
+    ap.add_argument("--traffic-calibration", action="store_true",
+                    help="only run the known-traffic reference kernel (cnhip_add over 64 Mi floats, "
+                         "5 times: 512 MiB read + 256 MiB written per launch) that scales the PMC "
+                         "FETCH_SIZE / WRITE_SIZE counts behind roofline.traffic")
+    ap.add_argument("--loader", choices=["resident", "stream", "both"], default=None,
+                    help="also time the same steps fed by the DataLoader (configs 1-4): 'resident' "
+                         "gathers each batch in HBM, 'stream' uploads it from page-locked host "
+                         "memory on a copy stream; reported under 'loader', never as 'value'")
+    args = ap.parse_args()
+    if args.traffic_calibration:
+        return traffic_calibration()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (got --gpus {args.gpus}); the "
+              "multi-GPU data-parallel design is described, not built", file=sys.stderr)
+        return 2
+    steps = args.steps if args.steps is not None else (200 if args.config == 1 else 50)
+
+    from cppnet_amd import _capi
+
+    lib = _capi.load()
+    if lib.cnhip_device_count() < 1:
+        log("bench.py: no GPU visible")
+        return 1
+    try:
+        head = measure(args.config, steps, args.warmup, args.graph, args.loader)
+    except RuntimeError as e:
+        log(f"bench.py: {e}")
+        return 1
+    result = {"metric": METRIC, "value": head["value"], "unit": head["unit"], "n_gpus": 1,
+              "steps": steps, "warmup": args.warmup, "ms_per_step": head["ms_per_step"],
+              "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
+              "data": "synthetic (seeded inputs/labels, reference init distributions; resident in HBM)"}
+    result.update({k: v for k, v in head.items() if k not in ("value", "unit", "steps", "warmup",
+                                                                "ms_per_step")})
+    result["cpu_baseline"] = None
+    if not args.only:
+        others = {}
+        for c in (1, 2, 3, 4, 5):
+            if c == args.config:
+                continue
+            try:
+                r = measure(c, EXTRA_STEPS.get(c, 20), 5, args.graph, None, hbm_detail=False)
+            except RuntimeError as e:
+                log(f"bench.py: {e}")
+                return 1
+            others[str(c)] = {"value": r["value"], "unit": r["unit"], "ms_per_step": r["ms_per_step"],
+                              "steps": r["steps"], "warmup": r["warmup"],
+                              "workload": r["config"]["workload"],
+                              "global_batch": r["config"]["global_batch"],
+                              "step_tflops": r["config"]["step_tflops"],
+                              "roofline": r["roofline"], "hbm_kernels_top": r["hbm_kernels"]["top"]}
+        result["other_configs"] = others
     if not args.no_cpu_baseline:
         try:
             result["cpu_baseline"] = cpu_baseline(args.config, args.cpu_seconds)

@@ -407,7 +407,10 @@ namespace CppNet
                 const auto drops = dropouts(layers);
                 std::vector<std::pair<uint64_t, uint64_t>> rng;
                 int32_t tag = 0;
-                if (is.read(reinterpret_cast<char*>(&tag), 4))
+                is.read(reinterpret_cast<char*>(&tag), 4);
+                if (is.gcount() != 0 && is.gcount() != 4)
+                    throw std::runtime_error("Truncated model file: the Dropout section's tag is cut short");
+                if (is.gcount() == 4)
                 {
                     if (tag != kRngMagic) throw std::runtime_error("load_checkpoint: corrupt extension after the optimizer state");
                     const int32_t n = get_i32(is, "dropout count");

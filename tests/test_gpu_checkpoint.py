@@ -265,6 +265,20 @@ def test_checkpoint_refuses_other_optimizer_and_shapes(gpu, tmp_path):
     d.step()
     d.save_checkpoint(tmp_path / "d.ckpt")
     _refused_load_changes_nothing(cfg, tmp_path / "d.ckpt", "Dropout", X, Y)
+    # a file cut 1-3 bytes into the Dropout section's tag is a truncated file,
+    # not an older checkpoint without that section
+    raw = (tmp_path / "d.ckpt").read_bytes()
+    tag = raw.rfind(struct.pack("<i", 0x434E5253))
+    assert tag > 0
+    for cut in (1, 2, 3):
+        (tmp_path / f"cut{cut}.ckpt").write_bytes(raw[:tag + cut])
+        _refused_load_changes_nothing(_dropout_cfg(), tmp_path / f"cut{cut}.ckpt", "Truncated", X, Y)
+    # cut exactly before the tag: a checkpoint written before the section
+    # existed, which loads and leaves the generators as they are
+    (tmp_path / "cut0.ckpt").write_bytes(raw[:tag])
+    e = trainer.Session(_dropout_cfg())
+    e.load_checkpoint(tmp_path / "cut0.ckpt")
+    e.close()
     d.close()
     a.close()
 

@@ -355,6 +355,48 @@ def test_linear_fused_activation_matches_unfused(gpu, oracle, act, B, I, O):
     assert ok, msg
 
 
+@pytest.mark.parametrize("act", ["relu", "gelu", "residual"])
+@pytest.mark.parametrize("B,I,O", [(4096, 1024, 10), (8192, 512, 1), (2048, 2048, 16)])
+def test_linear_backward_one_pass_variants_vs_oracle(gpu, oracle, act, B, I, O):
+    """cnhip_linear_backward_act at shapes the one-pass few-output backward
+    serves (O in 1..16, B % 512 == 0, B*I >= 2^22), with the activation's
+    input (or the skip branch's gradient) a tensor distinct from X: ReLU and
+    GELU fold act'(aux) into the one pass's dX; the residual takes the one
+    pass for dW, db and then dX = dY W^T + G.  Held to the oracle's Linear
+    backward followed by the activation backward (or the add) under the
+    contraction bar; the accumulated dW, db start from nonzero values."""
+    print(f"[linear-one-pass] {act} B={B} I={I} O={O}", flush=True)
+    rng = np.random.default_rng(B + 3 * I + O)
+    X, W, dY = rnd(rng, B * I), rnd(rng, I * O, 1 / np.sqrt(I)), rnd(rng, B * O, 0.05)
+    aux = rnd(rng, B * I)  # ReLU output / GELU input / skip-branch gradient
+    if act == "relu":
+        aux = np.maximum(aux, 0)
+    gW0, gb0 = rnd(rng, I * O, 1e-3), rnd(rng, O, 1e-3)
+    gW, gb, dX = dev(gW0), dev(gb0), torch.empty(B * I, device="cuda")
+    ops.linear_backward_act(dev(X), dev(W), dev(dY), gW, gb, dX, dev(aux), B, I, O, act,
+                            accumulate=True)
+    rgW, rgb, rdL = gW0.copy(), gb0.copy(), np.zeros(B * I, np.float32)
+    oracle.cnref_linear_backward(fp(X), fp(W), fp(dY), fp(rgW), fp(rgb), fp(rdL), B, I, O, 1, 1)
+    rdX = np.zeros_like(rdL)
+    if act == "relu":
+        oracle.cnref_relu_backward(fp(aux), fp(rdL), fp(rdX), rdX.size)
+    elif act == "gelu":
+        oracle.cnref_gelu_backward(fp(aux), fp(rdL), fp(rdX), rdX.size)
+    else:
+        oracle.cnref_add(fp(rdL), fp(aux), fp(rdX), rdX.size)
+    mag_dx = gemm_mag(oracle, 0, 1, B, I, O, dY, B, W, I, B)
+    if act == "gelu":  # the contraction's rounding carried through gelu'(aux), |gelu'| <= 1.13
+        mag_dx = mag_dx * 1.13
+    elif act == "relu":
+        mag_dx = mag_dx * (aux > 0)
+    mags = {"grad_W": gemm_mag(oracle, 1, 0, I, O, B, X, B, dY, B, I),
+            "grad_b": gemm_mag(oracle, 1, 0, 1, O, B, np.ones(B, np.float32), B, dY, B, 1),
+            "dX": mag_dx}
+    for got, want, name in [(host(gW), rgW, "grad_W"), (host(gb), rgb, "grad_b"), (host(dX), rdX, "dX")]:
+        ok, msg = close_mag(got, want, mags[name], RTOL, ATOL)
+        assert ok, f"{act} {name}: {msg}"
+
+
 @pytest.mark.parametrize("B,I,O", [(64, 48, 40), (8192, 2048, 512), (37, 130, 19), (512, 4096, 64)])
 def test_linear_fused_residual_matches_unfused(gpu, B, I, O):
     """Y = X W + b + R and dX = dY W^T + G in the GEMM epilogue equal the
