@@ -71,6 +71,10 @@ SIGNATURES: dict[str, tuple] = {
     "cnhip_maxpool2d_backward_relu_pooled": (i32, [vp, vp, vp, vp] + [i64] * 6 + [vp]),
     "cnhip_linear_backward_maxpool_relu": (i32, [vp] * 7 + [i64] * 7 + [i32, vp]),
     "cnhip_linear_backward_maxpool_relu_fits": (i32, [i64] * 7),
+    "cnhip_recurrence_fault_check": (i32, [vp]),
+    "cnhip_update_seq_last": (i64, []),
+    "cnhip_update_faults_taken": (i64, []),
+    "cnhip_update_withheld": (i32, [i64]),
     "cnhip_lstm_forward": (i32, [vp] * 8 + [i64] * 4 + [vp]),
     "cnhip_lstm_backward": (i32, [vp] * 12 + [i64] * 4 + [vp]),
     "cnhip_lstm_backward_last": (i32, [vp] * 12 + [i64] * 4 + [vp]),

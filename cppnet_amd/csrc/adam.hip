@@ -55,7 +55,8 @@ struct AdamBatch {
 // and v (4R loads in flight), then updates them, then stores: the four
 // arrays are distinct buffers, so no store can feed a later load.
 template <int R>
-__device__ __forceinline__ void adam_range(const AdamTensor& T, int64_t begin, const AdamHyper& h) {
+__device__ __forceinline__ void adam_range(const AdamTensor& T, int64_t begin, const AdamHyper& h,
+                                           const UpdateGuard& guard) {
   if (T.vec) {
     // begin is a multiple of the chunk, hence of 4.
     f32x4 w[R], g[R], m[R], v[R];
@@ -69,6 +70,7 @@ __device__ __forceinline__ void adam_range(const AdamTensor& T, int64_t begin, c
         v[r] = *reinterpret_cast<const f32x4*>(T.v + i);
       }
     }
+    if (update_withheld(guard)) return;  // checked once the loads are in flight
 #pragma unroll
     for (int r = 0; r < R; ++r) {
 #pragma unroll
@@ -88,6 +90,7 @@ __device__ __forceinline__ void adam_range(const AdamTensor& T, int64_t begin, c
       }
     }
   } else {
+    if (update_withheld(guard)) return;
     for (int r = 0; r < 4 * R; ++r) {
       const int64_t i = begin + (int64_t)r * ADAM_BLOCK + threadIdx.x;
       if (i >= T.n) break;
@@ -99,7 +102,7 @@ __device__ __forceinline__ void adam_range(const AdamTensor& T, int64_t begin, c
 }
 
 template <int R>
-__global__ void __launch_bounds__(ADAM_BLOCK) adam_multi_kernel(AdamBatch batch, AdamHyper h) {
+__global__ void __launch_bounds__(ADAM_BLOCK) adam_multi_kernel(AdamBatch batch, AdamHyper h, UpdateGuard guard) {
   // Find the tensor owning this block (count <= 64: a linear scan of
   // uniform values is cheap and stays in scalar registers).
   int ti = 0;
@@ -107,7 +110,7 @@ __global__ void __launch_bounds__(ADAM_BLOCK) adam_multi_kernel(AdamBatch batch,
     if ((int)blockIdx.x >= batch.t[i].first_block) ti = i;
   const AdamTensor& T = batch.t[ti];
   const int64_t begin = (int64_t)((int)blockIdx.x - T.first_block) * (R * ADAM_BLOCK * 4);
-  adam_range<R>(T, begin, h);
+  adam_range<R>(T, begin, h, guard);
 }
 
 template <int R>
@@ -121,9 +124,11 @@ int adam_launch_r(AdamBatch& b, const AdamHyper& h, int64_t params, hipStream_t 
     blocks += (int)nb;
   }
   if (blocks == 0) return CNHIP_OK;
+  UpdateGuard guard;
+  CNHIP_TRY(update_guard(&guard, who));
   // read W, g, m, v and write W, m, v: 28 bytes per parameter
   HbmTimer timer("adam_multi_kernel", 28.0 * (double)params, st);
-  hipLaunchKernelGGL(adam_multi_kernel<R>, dim3(blocks), dim3(ADAM_BLOCK), 0, st, b, h);
+  hipLaunchKernelGGL(adam_multi_kernel<R>, dim3(blocks), dim3(ADAM_BLOCK), 0, st, b, h, guard);
   return check_launch(who);
 }
 

@@ -91,6 +91,37 @@ int persist_ordered(hipStream_t stream, bool capturing, const char* who, F&& lau
   return st;
 }
 
+// Optimizer guard.  A persistent recurrence launch that gives up waiting
+// sets the current device's guard word; while it is set, every optimizer
+// kernel leaves its tensors unchanged and lowers *first_withheld to its
+// launch's sequence number, so invalid recurrent outputs never reach the
+// parameters.  update_guard fills the current device's words and the next
+// sequence number (update_seq_last() returns it to the caller's thread).
+// recurrence_fault_check reports a pending fault (CNHIP_EHIP) and takes it:
+// it synchronizes the device, clears the guard and records the range of
+// sequence numbers withheld (update_withheld(seq): 1 for a launch in one;
+// update_faults_taken() counts the faults taken); without a pending fault it
+// costs one read of a host word.
+struct UpdateGuard {
+  const unsigned* withhold;
+  unsigned long long* first_withheld;
+  unsigned long long seq;
+};
+int update_guard(UpdateGuard* out, const char* who);
+int recurrence_fault_check(hipStream_t st, const char* who);
+int update_withheld(int64_t seq);
+int64_t update_faults_taken();
+int64_t update_seq_last();
+
+// In an optimizer kernel: whether this launch is withheld (the block's first
+// thread then records it).
+__device__ __forceinline__ bool update_withheld(const UpdateGuard& g) {
+  if (__builtin_expect(*g.withhold == 0u, 1)) return false;
+  if (blockIdx.x == 0 && threadIdx.x == 0)
+    __hip_atomic_fetch_min(g.first_withheld, g.seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return true;
+}
+
 // Bytes of GEMM scratch (split-K partials) that gemm_f32_core requests for
 // this shape: 0 when it runs without a split.
 size_t gemm_scratch_bytes(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, int64_t batches);

@@ -356,7 +356,9 @@ __device__ __forceinline__ void opt_one(float& w, float g, float& s, float lr, f
 }
 
 template <int KIND>
-__global__ void __launch_bounds__(OPT_BLOCK) opt_multi_kernel(OptBatch batch, float lr, float h, float eps) {
+__global__ void __launch_bounds__(OPT_BLOCK) opt_multi_kernel(OptBatch batch, float lr, float h, float eps,
+                                                               UpdateGuard guard) {
+  if (update_withheld(guard)) return;
   int ti = 0;
   for (int i = 1; i < batch.count; ++i)
     if ((int)blockIdx.x >= batch.t[i].first_block) ti = i;
@@ -614,24 +616,26 @@ int cnhip_optimizer_step_multi(int kind, int count, float* const* W, const float
   }
   if (blocks == 0) return CNHIP_OK;
   hipStream_t st = as_stream(s);
+  cnhip::UpdateGuard guard;
+  CNHIP_TRY(cnhip::update_guard(&guard, who));
   // W and g read, W written; the state read and written (not for SGD)
   cnhip::HbmTimer timer("opt_multi_kernel", (kind == CNHIP_OPT_SGD ? 12.0 : 20.0) * params, st);
   switch (kind) {
     case CNHIP_OPT_SGD:
       hipLaunchKernelGGL(cnhip::opt_multi_kernel<CNHIP_OPT_SGD>, dim3(blocks), dim3(cnhip::OPT_BLOCK), 0, st, b,
-                         lr, hyper, eps);
+                         lr, hyper, eps, guard);
       break;
     case CNHIP_OPT_MOMENTUM:
       hipLaunchKernelGGL(cnhip::opt_multi_kernel<CNHIP_OPT_MOMENTUM>, dim3(blocks), dim3(cnhip::OPT_BLOCK), 0,
-                         st, b, lr, hyper, eps);
+                         st, b, lr, hyper, eps, guard);
       break;
     case CNHIP_OPT_ADAGRAD:
       hipLaunchKernelGGL(cnhip::opt_multi_kernel<CNHIP_OPT_ADAGRAD>, dim3(blocks), dim3(cnhip::OPT_BLOCK), 0,
-                         st, b, lr, hyper, eps);
+                         st, b, lr, hyper, eps, guard);
       break;
     default:
       hipLaunchKernelGGL(cnhip::opt_multi_kernel<CNHIP_OPT_RMSPROP>, dim3(blocks), dim3(cnhip::OPT_BLOCK), 0,
-                         st, b, lr, hyper, eps);
+                         st, b, lr, hyper, eps, guard);
       break;
   }
   return cnhip::check_launch(who);

@@ -24,6 +24,7 @@ namespace CppNet
         void Adam::update(float* weights, const float* gradients, int64_t size, float learning_rate)
         {
             if (size <= 0) return;
+            if (pending_.empty()) reconcile_withheld();  // before any t of this group advances
             auto it = states_.find(weights);
             if (it == states_.end())
             {
@@ -51,6 +52,23 @@ namespace CppNet
         void Adam::end_group()
         {
             if (group_depth_ > 0 && --group_depth_ == 0) flush();
+        }
+
+        void Adam::reconcile_withheld()
+        {
+            const int64_t taken = cnhip_update_faults_taken();
+            if (taken == faults_seen_) return;
+            faults_seen_ = taken;
+            for (auto it = launched_.begin(); it != launched_.end();)
+            {
+                if (cnhip_update_withheld(it->seq))
+                {
+                    for (State* s : it->keys) --s->t;
+                    it = launched_.erase(it);
+                }
+                else
+                    ++it;
+            }
         }
 
         void Adam::flush()
@@ -81,6 +99,10 @@ namespace CppNet
                     pending_.clear();
                     Device::check(st, "Adam::update");
                 }
+                Launched l{cnhip_update_seq_last(), {}};
+                for (size_t k = i - count; k < i; ++k) l.keys.push_back(pending_[k].s);
+                launched_.push_back(std::move(l));
+                if (launched_.size() > kLaunchHistory) launched_.pop_front();
             }
             pending_.clear();
         }

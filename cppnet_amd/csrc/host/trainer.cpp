@@ -663,6 +663,33 @@ int cnt_get_grad(cnt_session* s, int index, float* host)
     });
 }
 
+int cnt_get_opt_state(cnt_session* s, int index, int k, float* host, int* t)
+{
+    return guarded("cnt_get_opt_state", [&] {
+        check_session(s);
+        StreamScope scope(s);
+        if (!host || !t) throw std::invalid_argument("NULL output");
+        if (k < 0 || k >= s->opt->state_tensors())
+            throw std::invalid_argument("state tensor " + std::to_string(k) + " of an optimizer that keeps " +
+                                        std::to_string(s->opt->state_tensors()));
+        auto& p = param_rec(s, index);
+        DeviceTensor& w = p.value();
+        std::vector<std::vector<float>> st;
+        int tt = 0;
+        if (!s->opt->get_state(w.data(), w.size(), st, tt)) st.assign(k + 1, std::vector<float>(w.size(), 0.f));
+        *t = tt;
+        const std::vector<float>& v = st[k];
+        if (p.t_rows == 0)
+        {
+            std::copy(v.begin(), v.end(), host);
+            return;
+        }
+        // the device keeps the transpose of the reference's [t_rows, t_cols]
+        for (int64_t r = 0; r < p.t_rows; ++r)
+            for (int64_t c = 0; c < p.t_cols; ++c) host[r + p.t_rows * c] = v[c + p.t_cols * r];
+    });
+}
+
 namespace
 {
     // The token ids of a batch are checked once, when the batch is uploaded
@@ -792,6 +819,33 @@ namespace
         else
             s->model.update(*s->opt, s->lr);
         s->updated = true;
+    }
+
+    // A persistent recurrence launch that gave up waiting leaves invalid
+    // outputs; the device then withholds every optimizer launch queued after
+    // it.  Taking the fault (at a sync point, or when the next recurrent call
+    // or graph replay finds it) reports it here, after the optimizer's step
+    // counts of the withheld updates are rolled back: parameters and
+    // optimizer state are then as before the faulted step.
+    void take_recurrence_fault(cnt_session* s, const char* who)
+    {
+        const int st = cnhip_recurrence_fault_check(s->stream);
+        if (s->opt) s->opt->reconcile_withheld();
+        Device::check(st, who);
+    }
+
+    // Runs f; on an error, first rolls back what a fault taken inside it withheld.
+    void reconciled(cnt_session* s, const std::function<void()>& f)
+    {
+        try
+        {
+            f();
+        }
+        catch (...)
+        {
+            if (s->opt) s->opt->reconcile_withheld();
+            throw;
+        }
     }
 } // namespace
 
@@ -1025,16 +1079,23 @@ int cnt_step(cnt_session* s, float* loss_out)
     return guarded("cnt_step", [&] {
         check_session(s);
         StreamScope scope(s);
-        if (s->graph)
+        take_recurrence_fault(s, "cnt_step");  // one left by an earlier step
+        reconciled(s, [&] {
+            if (s->graph)
+            {
+                Device::check(cnhip_graph_launch(s->graph, s->stream), "cnt_step graph replay");
+                s->last_loss = s->graph_loss;
+                for (auto& f : s->graph_flags) f.first->set_grads_pending_zero(f.second);
+            }
+            else
+                eager_forward_backward(s);
+            update(s);
+        });
+        if (loss_out)
         {
-            Device::check(cnhip_graph_launch(s->graph, s->stream), "cnt_step graph replay");
-            s->last_loss = s->graph_loss;
-            for (auto& f : s->graph_flags) f.first->set_grads_pending_zero(f.second);
+            *loss_out = s->last_loss.get();
+            take_recurrence_fault(s, "cnt_step");  // this step's, now that it has run
         }
-        else
-            eager_forward_backward(s);
-        update(s);
-        if (loss_out) *loss_out = s->last_loss.get();
     });
 }
 
@@ -1099,8 +1160,13 @@ int cnt_forward_backward(cnt_session* s, float* loss_out)
     return guarded("cnt_forward_backward", [&] {
         check_session(s);
         StreamScope scope(s);
-        eager_forward_backward(s);
-        if (loss_out) *loss_out = s->last_loss.get();
+        take_recurrence_fault(s, "cnt_forward_backward");
+        reconciled(s, [&] { eager_forward_backward(s); });
+        if (loss_out)
+        {
+            *loss_out = s->last_loss.get();
+            take_recurrence_fault(s, "cnt_forward_backward");
+        }
     });
 }
 
@@ -1109,7 +1175,8 @@ int cnt_update(cnt_session* s)
     return guarded("cnt_update", [&] {
         check_session(s);
         StreamScope scope(s);
-        update(s);
+        take_recurrence_fault(s, "cnt_update");
+        reconciled(s, [&] { update(s); });
     });
 }
 
@@ -1118,6 +1185,7 @@ int cnt_synchronize(cnt_session* s)
     return guarded("cnt_synchronize", [&] {
         check_session(s);
         Device::check(cnhip_stream_synchronize(s->stream), "sync");
+        take_recurrence_fault(s, "cnt_synchronize");
     });
 }
 

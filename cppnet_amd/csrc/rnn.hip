@@ -25,6 +25,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdlib>
 #include <mutex>
@@ -245,8 +246,14 @@ __global__ void __launch_bounds__(LstmCfg::NT) lstm_step_fwd_kernel(
 // only when its buffer is new, when the counter wraps, and before every
 // launch recorded into a graph (whose replays all reuse epoch 0; a zeroed
 // word carries stamp 0, which no step uses).  The fault word is tagged with
-// the epoch the same way; the XCD slot counters are returned to 0 by the
-// last block placed on each XCD.  The
+// the epoch the same way.  The XCD slot counters come in three sets: the
+// launches of one buffer alternate between sets 0 and 1, and the first block
+// placed on an XCD zeroes that XCD's counter of the other set for the next
+// launch (the previous launch, which used it, has finished: persistent
+// launches are ordered); a launch recorded into a graph uses set 2, zeroed
+// with the rest of the area before each replay.  A block whose slot is
+// beyond gridDim.x / 8 (an XCD dealt more blocks than that) raises the
+// fault instead of taking a tile.  The
 // writer stores the word; the reader invalidates its CU's L1 (buffer_inv
 // sc0) and loads the words (nontemporal) until each carries the stamp it
 // waits for.  A word is stored and loaded whole, so a value is never taken
@@ -257,15 +264,21 @@ __global__ void __launch_bounds__(LstmCfg::NT) lstm_step_fwd_kernel(
 //
 // Every wait is bounded: after spin_limit polls a thread gives up and sets
 // the launch's fault word (which every waiting thread checks while it polls,
-// then exits) and the host-visible one; the next recurrent call reports it.
-// A negative spin limit gives up at once (the tests of the fault path).
+// then exits), the device's optimizer guard (while it is set, every
+// optimizer launch on the device leaves its tensors as they are, so the
+// invalid outputs never reach the parameters) and the host-visible word,
+// which the next recurrent call, graph replay or training-session sync point
+// reports (cnhip_recurrence_fault_check).  A negative spin limit gives up at
+// once (the tests of the fault path).
 constexpr int kPt = 16;            // samples and hidden units per tile
 constexpr int kPersistMaxH = 512;  // W_hh slice of H x 64 floats: H/4 registers per lane
 typedef unsigned long long u64;
 
 struct PersistSync {
   unsigned* fault;       // device word: fault_mark(epoch) once this launch faulted
-  unsigned* xcd_slots;   // [8] per-XCD block counters, 0 between launches
+  unsigned* slots;       // [8] this launch's per-XCD block counters (0 at its start)
+  unsigned* slots_next;  // [8] the next launch's counters, zeroed here; null under capture
+  unsigned* guard;       // the device's optimizer guard (set with the fault)
   unsigned* fault_host;  // pinned host word, or null
   long long spin_limit;
   unsigned epoch;        // 0 .. 65535; stamps are epoch << 16 | step
@@ -276,7 +289,8 @@ __device__ __forceinline__ unsigned ex_stamp(const PersistSync& ps, int step) { 
 
 __device__ __forceinline__ void persist_fail(const PersistSync& ps) {
   __hip_atomic_store(ps.fault, fault_mark(ps.epoch), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  if (ps.fault_host) __hip_atomic_store(ps.fault_host, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  __hip_atomic_store(ps.guard, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (ps.fault_host) __hip_atomic_store(ps.fault_host, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 __device__ __forceinline__ bool persist_faulted(const PersistSync& ps) {
   return __hip_atomic_load(ps.fault, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == fault_mark(ps.epoch);
@@ -287,16 +301,16 @@ __device__ __forceinline__ unsigned xcc_id() {
 }
 
 // The block's sample tile (>= nst when it has none) and unit tile, from the
-// XCD it runs on; false (after raising the fault) when XCC_ID is not 0..7.
+// XCD it runs on; false (after raising the fault) when XCC_ID is not 0..7 or
+// the XCD was dealt more than gridDim.x / 8 blocks.
 __device__ __forceinline__ bool persist_place(const PersistSync& ps, int nut, int& st, int& ut, int* place) {
   if (threadIdx.x == 0) {
     const unsigned x = xcc_id();
-    if (x < 8u) {
-      // every XCD receives gridDim.x / 8 blocks; the one that takes the last
-      // ticket leaves the counter at 0 for the next launch
-      unsigned* slot = ps.xcd_slots + x;
-      const unsigned i = __hip_atomic_fetch_add(slot, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (i + 1u == gridDim.x / 8u) __hip_atomic_store(slot, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned i = x < 8u ? __hip_atomic_fetch_add(ps.slots + x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                              : ~0u;
+    if (i == 0u && ps.slots_next)
+      __hip_atomic_store(ps.slots_next + x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (i < gridDim.x / 8u) {
       place[0] = (int)x + 8 * ((int)i / nut);
       place[1] = (int)i % nut;
     } else {
@@ -1191,11 +1205,12 @@ constexpr int kScratchRecur = 2;  // scratch slot of the fault word and the exch
 constexpr int kScratchSeq = 3;    // scratch slot of a last-step gradient spread over all steps
 
 // Per device: the epoch of the next launch, and the exchange buffers
-// (scratch allocations) zeroed or run in since the counter last started
-// over.
+// (scratch allocations, by generation) zeroed or run in since the counter
+// last started over, each with the number of launches run in it since it
+// was zeroed (whose parity picks the launch's XCD counter set).
 struct PersistEpochs {
   unsigned next = 1;
-  std::vector<uint64_t> clean;
+  std::vector<std::pair<uint64_t, unsigned>> clean;
 };
 std::mutex g_epoch_mu;
 PersistEpochs g_epochs[64];
@@ -1224,20 +1239,118 @@ unsigned* fault_host_word(int dev) {
   return words[dev];
 }
 
-// A fault left by an earlier persistent launch on this device: reported
-// (and cleared) at the next recurrent call.
-int persist_take_fault(const char* who) {
+}  // namespace
+
+// ---- optimizer guard
+// Per GPU (each device holds its own copy of these words): g_update_guard is
+// set by a persistent launch that gave up waiting; while it is set, every
+// optimizer launch on the device leaves its tensors unchanged and lowers
+// g_first_withheld to its sequence number.  Both are reset when the host
+// takes the fault (recurrence_fault_check).
+__device__ unsigned g_update_guard = 0u;
+__device__ unsigned long long g_first_withheld = ~0ull;
+
+namespace {
+struct GuardWords {
+  unsigned* guard = nullptr;
+  unsigned long long* first = nullptr;
+};
+std::mutex g_guard_mu;
+GuardWords g_guard_words[64];
+// per device: the sequence numbers [first, last] of the optimizer launches
+// withheld by each fault taken
+std::vector<std::pair<unsigned long long, unsigned long long>> g_withheld[64];
+std::atomic<unsigned long long> g_update_seq{0};
+std::atomic<long long> g_faults_taken{0};
+thread_local long long t_last_update_seq = -1;
+
+// The device addresses of the current device's guard words, looked up once
+// per device with that device current.
+int guard_words(GuardWords* out, int* dev_out, const char* who) {
   int dev = 0;
   CNHIP_TRY(check_hip(hipGetDevice(&dev), who));
-  unsigned* w = fault_host_word(dev);
-  if (w && __atomic_exchange_n(w, 0u, __ATOMIC_ACQ_REL) != 0u) {
-    persist_forget_clean(dev);  // the faulted launch may have left its counters off 0
-    set_error("%s: an earlier persistent recurrence launch on this device gave up waiting for its other "
-              "blocks (not all co-resident?); its outputs are invalid", who);
-    return CNHIP_EHIP;
+  CNHIP_REQUIRE(dev >= 0 && dev < 64, "%s: device %d out of range", who, dev);
+  std::lock_guard<std::mutex> lock(g_guard_mu);
+  GuardWords& g = g_guard_words[dev];
+  if (!g.guard) {
+    void* a = nullptr;
+    void* b = nullptr;
+    CNHIP_TRY(check_hip(hipGetSymbolAddress(&a, HIP_SYMBOL(g_update_guard)), who));
+    CNHIP_TRY(check_hip(hipGetSymbolAddress(&b, HIP_SYMBOL(g_first_withheld)), who));
+    g.guard = static_cast<unsigned*>(a);
+    g.first = static_cast<unsigned long long*>(b);
   }
+  *out = g;
+  if (dev_out) *dev_out = dev;
   return CNHIP_OK;
 }
+}  // namespace
+
+int update_guard(UpdateGuard* out, const char* who) {
+  GuardWords g;
+  CNHIP_TRY(guard_words(&g, nullptr, who));
+  out->withhold = g.guard;
+  out->first_withheld = g.first;
+  out->seq = ++g_update_seq;
+  t_last_update_seq = (long long)out->seq;
+  return CNHIP_OK;
+}
+
+int recurrence_fault_check(hipStream_t st, const char* who) {
+  int dev = 0;
+  CNHIP_TRY(check_hip(hipGetDevice(&dev), who));
+  unsigned* w = dev >= 0 && dev < 64 ? fault_host_word(dev) : nullptr;
+  if (!w || __atomic_load_n(w, __ATOMIC_ACQUIRE) == 0u) return CNHIP_OK;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  CNHIP_TRY(check_hip(hipStreamIsCapturing(st, &cs), who));
+  if (cs != hipStreamCaptureStatusNone) {
+    set_error("%s: a persistent recurrence launch on this device gave up waiting for its other blocks; "
+              "the fault is taken outside graph capture", who);
+    return CNHIP_EHIP;
+  }
+  // every launch queued so far has run: the faulted one and the optimizer
+  // launches it withheld
+  CNHIP_TRY(check_hip(hipDeviceSynchronize(), who));
+  GuardWords g;
+  CNHIP_TRY(guard_words(&g, nullptr, who));
+  unsigned long long first = ~0ull;
+  const unsigned zero = 0u;
+  const unsigned long long none = ~0ull;
+  CNHIP_TRY(check_hip(hipMemcpy(&first, g.first, sizeof(first), hipMemcpyDeviceToHost), who));
+  CNHIP_TRY(check_hip(hipMemcpy(g.first, &none, sizeof(none), hipMemcpyHostToDevice), who));
+  CNHIP_TRY(check_hip(hipMemcpy(g.guard, &zero, sizeof(zero), hipMemcpyHostToDevice), who));
+  __atomic_store_n(w, 0u, __ATOMIC_RELEASE);
+  persist_forget_clean(dev);  // the faulted launch may have left its counters and words anywhere
+  if (first != ~0ull) {
+    // every optimizer launch from the first withheld one to the last one
+    // made so far has run (the device is synchronized) with the guard set
+    std::lock_guard<std::mutex> lock(g_guard_mu);
+    g_withheld[dev].emplace_back(first, g_update_seq.load());
+  }
+  ++g_faults_taken;
+  set_error("%s: a persistent recurrence launch on this device gave up waiting for its other blocks; its "
+            "outputs are invalid, and the optimizer updates queued after it were withheld (%s)",
+            who, first != ~0ull ? "parameters and optimizer state are as before them" : "none was queued");
+  return CNHIP_EHIP;
+}
+
+int update_withheld(int64_t seq) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  std::lock_guard<std::mutex> lock(g_guard_mu);
+  for (const auto& r : g_withheld[dev])
+    if (seq >= 0 && (unsigned long long)seq >= r.first && (unsigned long long)seq <= r.second) return 1;
+  return 0;
+}
+
+int64_t update_faults_taken() { return g_faults_taken.load(); }
+
+int64_t update_seq_last() { return t_last_update_seq; }
+
+namespace {
 
 long long persist_spin_limit() {
   const char* e = std::getenv("CNHIP_RECURRENCE_SPIN_LIMIT");
@@ -1262,7 +1375,7 @@ bool persist_fits(const void* kernel, int64_t grid, int threads, const char* who
     int dev;
     const void* kernel;
     int threads;
-    int64_t capacity;  // resident blocks, 0 when a cooperative launch is impossible
+    int64_t capacity;  // resident blocks, 0 when a cooperative launch is impossible or XCDs != 8
   };
   static std::mutex mu;
   static std::vector<Fit> cache;
@@ -1275,12 +1388,17 @@ bool persist_fits(const void* kernel, int64_t grid, int threads, const char* who
   std::lock_guard<std::mutex> lock(mu);
   for (const Fit& f : cache)
     if (f.dev == dev && f.kernel == kernel && f.threads == threads) return f.capacity > 0 && grid <= f.capacity;
-  int cus = 0, coop = 0, per_cu = 0;
+  // The tile placement takes XCC_ID 0..7 and gridDim.x / 8 blocks per XCD
+  // (the hardware's round-robin deal of a grid over the 8 XCDs of a device
+  // in SPX mode): a device partitioned into fewer XCDs runs the per-step
+  // launches instead.
+  int cus = 0, coop = 0, per_cu = 0, xccs = 0;
   int64_t capacity = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
       hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) == hipSuccess &&
+      hipDeviceGetAttribute(&xccs, hipDeviceAttributeNumberOfXccs, dev) == hipSuccess &&
       hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) == hipSuccess) {
-    if (coop != 0 && per_cu > 0) capacity = (int64_t)cus * per_cu;
+    if (coop != 0 && per_cu > 0 && xccs == 8 && cus % 8 == 0) capacity = (int64_t)cus * per_cu;
   } else {
     (void)hipGetLastError();
   }
@@ -1310,9 +1428,10 @@ bool persist_cooperative() {
 // the wrap, words of earlier launches may carry the epochs to come), or
 // since a fault was reported.  A launch recorded into a graph takes epoch 0
 // and is always preceded by the zeroing (every replay reuses its stamps).
-unsigned persist_epoch(int dev, uint64_t gen, bool capturing, bool* zero) {
+unsigned persist_epoch(int dev, uint64_t gen, bool capturing, bool* zero, int* set) {
   if (capturing || dev < 0 || dev >= 64) {
     *zero = true;
+    *set = 2;
     return 0;
   }
   std::lock_guard<std::mutex> lock(g_epoch_mu);
@@ -1321,8 +1440,10 @@ unsigned persist_epoch(int dev, uint64_t gen, bool capturing, bool* zero) {
     e.next = 1;
     e.clean.clear();
   }
-  *zero = std::find(e.clean.begin(), e.clean.end(), gen) == e.clean.end();
-  if (*zero) e.clean.push_back(gen);
+  auto it = std::find_if(e.clean.begin(), e.clean.end(), [gen](const auto& c) { return c.first == gen; });
+  *zero = it == e.clean.end();
+  if (*zero) it = e.clean.insert(e.clean.end(), {gen, 0u});
+  *set = (int)(it->second++ & 1u);
   return e.next++;
 }
 
@@ -1330,6 +1451,7 @@ unsigned persist_epoch(int dev, uint64_t gen, bool capturing, bool* zero) {
 // (ex_bytes, after a 256-byte header) where persist_epoch asks for it, then
 // launches `kernel` with one argument (cooperatively only when asked to
 // above, and never while the stream is being captured into a graph).
+// Header words: 0 the fault word, 16 + 8 k the counter set k (k = 0, 1, 2).
 template <class Args>
 int persist_launch(const void* kernel, int64_t grid, int threads, Args& args, size_t ex_bytes, hipStream_t st,
                    const char* who) {
@@ -1342,15 +1464,21 @@ int persist_launch(const void* kernel, int64_t grid, int threads, Args& args, si
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
   CNHIP_TRY(check_hip(hipStreamIsCapturing(st, &cs), who));
   const bool capturing = cs != hipStreamCaptureStatusNone;
-  args.sync.fault = static_cast<unsigned*>(ws);
-  args.sync.xcd_slots = static_cast<unsigned*>(ws) + 16;
+  GuardWords g;
+  CNHIP_TRY(guard_words(&g, nullptr, who));
+  unsigned* head = static_cast<unsigned*>(ws);
+  args.sync.fault = head;
+  args.sync.guard = g.guard;
   args.sync.fault_host = fault_host_word(dev);
   args.sync.spin_limit = persist_spin_limit();
   args.ex = reinterpret_cast<u64*>(static_cast<char*>(ws) + 256);
   void* params[] = {&args};
   return persist_ordered(st, capturing, who, [&] {
     bool zero = true;
-    args.sync.epoch = persist_epoch(dev, gen, capturing, &zero);
+    int set = 2;
+    args.sync.epoch = persist_epoch(dev, gen, capturing, &zero, &set);
+    args.sync.slots = head + 16 + 8 * set;
+    args.sync.slots_next = set == 2 ? nullptr : head + 16 + 8 * (1 - set);
     if (zero) CNHIP_TRY(fill_bytes(ws, 0, bytes, st, who));
     if (!capturing && persist_cooperative())
       CNHIP_TRY(check_hip(hipLaunchCooperativeKernel(kernel, dim3((unsigned)grid), dim3(threads), params, 0, st), who));
@@ -1524,7 +1652,7 @@ int lstm_backward(const float* X, const float* W_ih, const float* W_hh, const fl
   CNHIP_TRY(check_rnn(B, S, I, H, who));
   CNHIP_REQUIRE(X && W_ih && W_hh && Y && gates && c && tanh_c && dY && gW_ih && gW_hh && gb,
                 "%s: NULL pointer", who);
-  CNHIP_TRY(persist_take_fault(who));
+  CNHIP_TRY(recurrence_fault_check(st, who));
   const int64_t G = 4 * H, BS = B * S;
   Workspace ws(st);
   // dG, dc and, for the fused weight gradients, one partial per 16-sample tile
@@ -1570,14 +1698,24 @@ using cnhip::as_stream;
 
 extern "C" {
 
+int cnhip_recurrence_fault_check(cnhip_stream_t stream) {
+  return cnhip::recurrence_fault_check(as_stream(stream), "cnhip_recurrence_fault_check");
+}
+
+int64_t cnhip_update_faults_taken(void) { return cnhip::update_faults_taken(); }
+
+int cnhip_update_withheld(int64_t seq) { return cnhip::update_withheld(seq); }
+
+int64_t cnhip_update_seq_last(void) { return cnhip::update_seq_last(); }
+
 int cnhip_lstm_forward(const float* X, const float* W_ih, const float* W_hh, const float* b,
                        float* Y, float* gates, float* c, float* tanh_c, int64_t B, int64_t S,
                        int64_t I, int64_t H, cnhip_stream_t stream) {
   const char* who = "cnhip_lstm_forward";
   CNHIP_TRY(cnhip::check_rnn(B, S, I, H, who));
   CNHIP_REQUIRE(X && W_ih && W_hh && b && Y && gates && c && tanh_c, "%s: NULL pointer", who);
-  CNHIP_TRY(cnhip::persist_take_fault(who));
   hipStream_t st = as_stream(stream);
+  CNHIP_TRY(cnhip::recurrence_fault_check(st, who));
   const int64_t G = 4 * H, BS = B * S;
   bool done = false;
   CNHIP_TRY(cnhip::lstm_fwd_persistent(gates, b, c, tanh_c, Y, W_hh, X, W_ih, I, true, B, S, H, st, who, &done));

@@ -381,6 +381,9 @@ int cnhip_graph_end_capture(cnhip_stream_t stream, int ok, cnhip_graph_t* graph)
 
 int cnhip_graph_launch(cnhip_graph_t graph, cnhip_stream_t stream) {
   CNHIP_REQUIRE(graph, "cnhip_graph_launch: NULL graph");
+  // a persistent recurrence launch of an earlier replay that gave up is
+  // reported here, before anything is replayed on top of its outputs
+  CNHIP_TRY(cnhip::recurrence_fault_check(as_stream(stream), "cnhip_graph_launch"));
   auto* G = static_cast<Graph*>(graph);
   CNHIP_REQUIRE(as_stream(stream) == G->stream,
                 "cnhip_graph_launch: a graph replays on the stream it was captured on (its scratch "

@@ -12,6 +12,7 @@
 #ifndef CPPNET_OPTIMIZERS_ADAM_HPP
 #define CPPNET_OPTIMIZERS_ADAM_HPP
 
+#include <deque>
 #include <string>
 #include <unordered_map>
 #include <vector>
@@ -46,6 +47,7 @@ namespace CppNet
                            int& t) const override;
             void set_state(const float* weights, int64_t n, const std::vector<std::vector<float>>& tensors,
                            int t) override;
+            void reconcile_withheld() override;
 
         private:
             struct State
@@ -61,6 +63,12 @@ namespace CppNet
                 int64_t n;
                 float bc1, bc2, lr;
             };
+            // one fused launch: its sequence number and the keys whose t it advanced
+            struct Launched
+            {
+                int64_t seq;
+                std::vector<State*> keys;
+            };
             void flush();
 
             float beta1_, beta2_, epsilon_;
@@ -68,6 +76,9 @@ namespace CppNet
             std::unordered_map<const void*, State> states_;
             std::vector<Pending> pending_;
             int group_depth_ = 0;
+            std::deque<Launched> launched_;  // the last kLaunchHistory launches
+            int64_t faults_seen_ = 0;
+            static constexpr std::size_t kLaunchHistory = 4096;
         };
     } // namespace Optimizers
 } // namespace CppNet

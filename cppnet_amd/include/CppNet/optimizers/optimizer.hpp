@@ -32,6 +32,13 @@ namespace CppNet
             virtual void end_group() {}
             virtual ~Optimizer() = default;
 
+            // Undoes the host-side bookkeeping (step counts) of updates the
+            // device withheld after a persistent recurrence launch gave up
+            // (cnhip_recurrence_fault_check); the device left their tensors
+            // unchanged.  Called by the optimizer before each launch and by
+            // the training session when it reports such a fault.
+            virtual void reconcile_withheld() {}
+
             // Checkpoint support (Utils::save_checkpoint; no counterpart in the
             // reference, whose model files hold weights only).  kind_code()
             // names the algorithm in a checkpoint (-1: none saved),

@@ -69,6 +69,7 @@ def load() -> C.CDLL:
         "cnt_set_param": (i32, [vp, i32, vp]),
         "cnt_get_param": (i32, [vp, i32, vp]),
         "cnt_get_grad": (i32, [vp, i32, vp]),
+        "cnt_get_opt_state": (i32, [vp, i32, i32, vp, C.POINTER(i32)]),
         "cnt_set_batch": (i32, [vp, vp, vp]),
         "cnt_set_batch_device": (i32, [vp, vp, vp]),
         "cnt_step": (i32, [vp, C.POINTER(f32)]),
@@ -494,6 +495,18 @@ class Session:
             _check(load().cnt_get_grad(self.h, i, a.ctypes.data))
             out.append(a)
         return out
+
+    def get_opt_state(self, k: int) -> tuple[list, list]:
+        """The optimizer's state tensor k of every parameter (Adam: 0 m, 1 v)
+        in get_params' layout, and each parameter's step count t."""
+        out, ts = [], []
+        for i in range(self.num_params()):
+            a = np.empty(self.param_size(i), np.float32)
+            t = C.c_int()
+            _check(load().cnt_get_opt_state(self.h, i, k, a.ctypes.data, C.byref(t)))
+            out.append(a)
+            ts.append(t.value)
+        return out, ts
 
     def set_batch(self, X: np.ndarray, Y: np.ndarray) -> None:
         """X: float32 inputs, or int32 token ids for a transformer session."""

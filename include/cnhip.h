@@ -311,6 +311,27 @@ int cnhip_linear_backward_maxpool_relu_fits(int64_t N, int64_t C, int64_t H, int
  * (lstm.cpp:158-160); dX may be NULL.
  * ref: LSTM::forward/backward src/CppNet/layers/lstm.cpp:63-253;
  * lstm_cell.cu:21-114 */
+/* Faults of the persistent recurrence.  The LSTM recurrence runs as one
+ * launch per pass whose blocks wait for each other's values every step;
+ * every wait is bounded, and a launch that gives up leaves invalid outputs
+ * and sets a device guard: until the fault is taken, every optimizer launch
+ * on the device (cnhip_adam_step[_multi], cnhip_optimizer_step_multi)
+ * leaves its tensors unchanged, so the invalid values never reach the
+ * parameters.  cnhip_recurrence_fault_check returns CNHIP_OK when no fault
+ * is pending (one read of a pinned host word); otherwise it takes the fault
+ * (synchronizes the device, clears the guard) and returns CNHIP_EHIP.  The
+ * recurrent calls and cnhip_graph_launch check on entry; a caller that
+ * synchronizes (a loss read-back) checks after it.  Each optimizer launch
+ * gets a sequence number, increasing over the process
+ * (cnhip_update_seq_last: this thread's last one); cnhip_update_withheld(seq)
+ * is 1 when that launch (on the current device) was withheld by a fault
+ * taken so far, and cnhip_update_faults_taken counts those faults, so a
+ * caller can roll back the step counts of its withheld updates.  No
+ * counterpart in the reference (its recurrence is a host loop). */
+int cnhip_recurrence_fault_check(cnhip_stream_t stream);
+int64_t cnhip_update_seq_last(void);
+int64_t cnhip_update_faults_taken(void);
+int cnhip_update_withheld(int64_t seq);
 int cnhip_lstm_forward(const float* X, const float* W_ih, const float* W_hh, const float* b,
                        float* Y, float* gates, float* c, float* tanh_c, int64_t B, int64_t S,
                        int64_t I, int64_t H, cnhip_stream_t stream);

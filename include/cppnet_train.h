@@ -117,6 +117,12 @@ int cnt_param_size(cnt_session* s, int index, int64_t* n);
 int cnt_set_param(cnt_session* s, int index, const float* host);
 int cnt_get_param(cnt_session* s, int index, float* host);
 int cnt_get_grad(cnt_session* s, int index, float* host);
+/* Host copy of the optimizer's state tensor k of parameter `index` (Adam: 0
+ * m, 1 v; Momentum, Adagrad, RMSProp: 0 their one tensor; in the layout of
+ * cnt_get_param) and its step count *t (Adam's per-key t; 0 and zeros
+ * before the parameter's first update).  No counterpart in the reference,
+ * whose optimizer state is private (adam.hpp:40-53). */
+int cnt_get_opt_state(cnt_session* s, int index, int k, float* host, int* t);
 
 /* Uploads one batch (X: the model's input shape, Y: [batch, outputs]) that
  * every later cnt_step() trains on, until the next call. */

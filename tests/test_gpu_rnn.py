@@ -245,3 +245,70 @@ def test_lstm_backward_last_step_gradient(gpu, monkeypatch, B, S, I, H, path):
         outs.append([host(t) for t in (gWih, gWhh, gb, dX)])
     for x, y, name in zip(outs[0], outs[1], ["grad_W_ih", "grad_W_hh", "grad_b", "dX"]):
         assert np.array_equal(x.view(np.uint32), y.view(np.uint32)), name
+
+
+def _bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def _snapshot(sess):
+    m, t = sess.get_opt_state(0)
+    v, _ = sess.get_opt_state(1)
+    return sess.get_params(), m, v, t
+
+
+def _assert_same(a, b, what):
+    pa, ma, va, ta = a
+    pb, mb, vb, tb = b
+    assert ta == tb, f"{what}: Adam step counts {tb} vs {ta}"
+    for k in range(len(pa)):
+        for u, w, name in ((pa[k], pb[k], "value"), (ma[k], mb[k], "m"), (va[k], vb[k], "v")):
+            assert np.array_equal(_bits(u), _bits(w)), f"{what}: {name} of parameter {k} differs"
+
+
+@pytest.mark.parametrize("read_loss", [True, False])
+def test_lstm_fault_in_training_step_withholds_the_update(gpu, monkeypatch, read_loss):
+    """A persistent recurrence launch that gives up (forced from the host:
+    spin limit -1, so every block exits at once) inside a full config-4
+    training step (LSTM 128->512, T 64, B 128 -> Linear -> MSE -> Adam),
+    with no synchronization between the backward and the update: the device
+    withholds the step's Adam launch, the step reports the fault (at its
+    loss read-back; without one, at the next step or sync), the parameters,
+    m, v and Adam's per-key t are exactly as before the step, and training
+    continues bit for bit as a session that never faulted."""
+    from cppnet_amd import _capi, trainer
+    print(f"[lstm-fault] config-4 step, read_loss={read_loss}", flush=True)
+    monkeypatch.setenv("CNHIP_RECURRENCE_PERSISTENT", "1")
+    cfg = trainer.rnn_config(4)
+    rng = np.random.default_rng(44)
+    params, X, Y = trainer.synthetic_rnn(cfg, rng)
+    a, twin = trainer.Session(cfg), trainer.Session(cfg)
+    for s in (a, twin):
+        s.set_params(params)
+        s.set_batch(X, Y)
+        s.step()
+        s.step()
+    before = _snapshot(a)
+    _assert_same(before, _snapshot(twin), "twin sessions")
+    monkeypatch.setenv("CNHIP_RECURRENCE_SPIN_LIMIT", "-1")
+    raised = False
+    try:
+        if read_loss:
+            a.step()  # the fault surfaces at this step's own loss read-back
+        else:
+            a.step(read_loss=False)
+            monkeypatch.delenv("CNHIP_RECURRENCE_SPIN_LIMIT")
+            a.step(read_loss=False)  # either this step or the sync reports it
+            a.synchronize()
+    except _capi.CnhipError as e:
+        assert "gave up waiting" in str(e), str(e)
+        raised = True
+    monkeypatch.delenv("CNHIP_RECURRENCE_SPIN_LIMIT", raising=False)
+    assert raised, "the faulted step was not reported"
+    a.synchronize()  # nothing left pending
+    _assert_same(before, _snapshot(a), "after the faulted step")
+    la, lt = a.step(), twin.step()
+    assert _bits(la)[0] == _bits(lt)[0], f"loss after the fault {la!r} vs {lt!r}"
+    _assert_same(_snapshot(twin), _snapshot(a), "one step after the fault")
+    a.close()
+    twin.close()
