@@ -48,14 +48,40 @@ def rnn_mags(oracle, ref, cfg):
     return [m_ih, m_hh, m_b, m_w, m_bb]
 
 
-def transformer_mags(oracle, ref, cfg):
+def _demb_mag(oracle, ref, cfg, params):
+    """Per-element size of the gradient reaching the embedding, dy = dX_attn +
+    dr of the first block (oracle/transformer.py): the attention input
+    gradient is a contraction over the 3D columns of [gQp gKp gVp] with
+    [Wq Wk Wv]^T, and BatchNorm's dr = gamma/sigma (gh - mean(gh) - xhat
+    mean(gh xhat)) with gh = dy + dz1 W1^T, itself a contraction over F.
+    Each contraction contributes (|A||B|)/sqrt(K), the other terms their
+    absolute values; ColMajor [R, D]."""
+    B, S, D, F = cfg.batch, cfg.seq_len, cfg.embed_dim, cfg.ffn
+    R = B * S
+    T = ref.trace[0]
+    Wq, Wk, Wv, _, gam, _, W1 = (params[j] for j in range(1, 8))
+    dxa = sum(gemm_mag(oracle, 0, 1, R, D, D, T[g], R, W, D, R) for g, W in (("gQp", Wq), ("gKp", Wk), ("gVp", Wv)))
+    dxa /= np.float32(np.sqrt(3.0))  # three sums over D each: one over 3D
+    gh_mag = np.abs(T["gh"]) + gemm_mag(oracle, 0, 1, R, D, F, T["dz1"], R, W1, D, R)
+    gh, xh = T["gh"].reshape(D, R), T["xh"].reshape(D, R)
+    inv_sigma = 1.0 / np.sqrt(T["bv"].astype(np.float64) + 1e-5)
+    scale = (np.abs(gam) * inv_sigma)[:, None]
+    dr = scale * (gh_mag.reshape(D, R) + np.abs(gh.mean(axis=1))[:, None]
+                  + np.abs(xh) * np.abs((gh * xh).mean(axis=1))[:, None])
+    return (np.abs(ref.head_trace["demb"]) + dxa + dr.ravel()).astype(np.float32)
+
+
+def transformer_mags(oracle, ref, cfg, params=None):
+    """params: the weights the step's backward used (default: the oracle's
+    current ones, i.e. after its update, close enough for a magnitude)."""
     B, S, V, D, F, C = cfg.batch, cfg.seq_len, cfg.vocab, cfg.embed_dim, cfg.ffn, cfg.classes
     R = B * S
     ones = np.ones(R, np.float32)
     ht = ref.head_trace
-    # embedding rows: the sum over each token's positions of |dy| / sqrt(count)
+    # embedding rows: the sum over each token's positions of the size of the
+    # gradient reaching the embedding, / sqrt(count)
     ids = ht["ids"].astype(np.int64)
-    demb = np.abs(ht["demb"].reshape(D, R))
+    demb = _demb_mag(oracle, ref, cfg, ref.params if params is None else params).reshape(D, R)
     acc = np.zeros((D, V), np.float64)
     np.add.at(acc.T, ids, demb.T)
     cnt = np.bincount(ids, minlength=V).astype(np.float64)
