@@ -72,22 +72,35 @@ __global__ void __launch_bounds__(256) column_sum_kernel(const float* __restrict
 //   dX[b, f] = (sum_n dY[b, n] W[f, n]) * act'(aux[b, f])
 // with act' = [aux > 0] (ReLU below), gelu'(aux) (GELU below) or 1 (none).
 // X, dY, dX ColMajor with leading dimension B, W ColMajor [F, O]; the path
-// takes B % SK_RB == 0 and F % SK_FBLK == 0, so no access needs a guard.
+// takes B % 512 == 0, F % 16 == 0 and 16-byte aligned X, dY, dX and aux,
+// so every access is an aligned float4 and none needs a guard.
 //
-// A block covers SK_FBLK features and SK_RB rows; its rows' dY [SK_RB, O]
-// is staged in LDS once and shared by the four waves, wave w taking features
-// SK_FW w .. SK_FW (w + 1) - 1.  Lanes walk rows (coalesced: the batch is the
-// contiguous dimension), SK_U row groups per iteration so SK_U * SK_FW loads
-// of X are in flight, keep SK_FW x NP running sums of X * dY and write dX as
-// they go.  The 64 lane sums of each dW element are then added in lane order
-// through LDS into a partial [row chunk][F, O]; skinny_reduce_kernel adds the
-// row chunks in order (and the chunks' db parts).  Each element of X (and
-// aux) is read once and each element of dX written once.
-constexpr int SK_FW = 4, SK_FBLK = 4 * SK_FW, SK_RB = 512, SK_U = 2;
+// A block covers 16 features and 256 RPL rows, one short pass: wave w owns
+// features 4w .. 4w+3 of the block, a lane 4 consecutive rows in each of
+// RPL 256-row groups.  Every load of the block is issued first -- the
+// lane's float4s of its 4 columns of X (and of a separate aux) and of the
+// NP columns of dY, per row group -- then the lane forms its 4 x NP dW sums
+// (rows in order) and its dX float4s; W of the wave's features is
+// wave-uniform (scalar loads).  Short blocks keep the loads of many waves
+// in flight (measured on the MI355X at [4096, 4096] -> 10: 22.8 us against
+// 27.2 us for 1024-row blocks that prefetch one 256-row group ahead and
+// 33.1 us for lane-strided scalar loads).  The 64 lane sums of each dW
+// element are added by two DPP steps within each quad of lanes (xor 1, then
+// xor 2: the four lanes end equal), then the 16 quad sums in quad order
+// through LDS, into a partial [row chunk][F, O] (the chunk's db from wave 0
+// of the first feature block); skinny_reduce_kernel adds the row chunks in
+// order.  Each element of X (and aux) is read once and each element of dX
+// written once.
+constexpr int SK_FW = 4, SK_FBLK = 4 * SK_FW;  // features per wave, per block
+constexpr int SK_QS = 20;  // floats per value in the quad-sum area: 16 quads + pad
+__host__ __device__ constexpr int sk_rpl(int np) {  // 256-row groups per block
+  return np > 10 ? 1 : 2;
+}
 
-template <int NP>
-constexpr int sk_lds_floats() {  // dY stage, reused for the lane sums
-  return SK_RB * (NP + 1) > 4 * SK_FW * NP * 64 ? SK_RB * (NP + 1) : 4 * SK_FW * NP * 64;
+__device__ __forceinline__ float quad_sum(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+  return v;
 }
 
 template <int NP, int ACT, bool SEP_AUX>
@@ -95,110 +108,110 @@ __global__ void __launch_bounds__(256) linear_bwd_skinny_kernel(
     const float* __restrict__ X, const float* __restrict__ W, const float* __restrict__ dY,
     const float* __restrict__ aux, float* __restrict__ partial, float* __restrict__ dX, int64_t B,
     int64_t F) {
-  constexpr int O = NP;
-  __shared__ __align__(16) float lds[sk_lds_floats<NP>()];
-  __shared__ float w[SK_FBLK][NP];
-  float* dys = lds;  // [row][n], odd row stride: no bank conflicts
-  // blockIdx.x is the row chunk: consecutive blocks read consecutive 2 KB
-  // pieces of the same columns, so the blocks in flight at any time cover
-  // whole contiguous runs of X rather than one piece of every column
-  const int64_t f0 = (int64_t)blockIdx.y * SK_FBLK;
-  const int64_t r0 = (int64_t)blockIdx.x * SK_RB;
-  {
-    // all of a thread's loads issued before its LDS stores (a load-store
-    // loop would wait for each load in turn)
-    constexpr int kPer = SK_RB * O / 256;
-    float v[kPer];
+  constexpr int O = NP, FW = SK_FW, RPL = sk_rpl(NP), NV = FW * NP, NT = NV + NP;
+  __shared__ __align__(16) float red[4][NT][SK_QS];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t r0 = (int64_t)blockIdx.x * (256 * RPL);
+  const int64_t fw = (int64_t)blockIdx.y * SK_FBLK + FW * wave;  // this wave's first feature
+  const bool with_db = blockIdx.y == 0 && wave == 0;
+  const int64_t B4 = B >> 2;
+  const f32x4* X4 = reinterpret_cast<const f32x4*>(X) + (r0 >> 2) + lane + B4 * fw;
+  const f32x4* A4 = reinterpret_cast<const f32x4*>(SEP_AUX ? aux : X) + (r0 >> 2) + lane + B4 * fw;
+  const f32x4* D4 = reinterpret_cast<const f32x4*>(dY) + (r0 >> 2) + lane;
+  f32x4 x[RPL][FW], a[RPL][FW], d[RPL][NP];
 #pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-      const int i = threadIdx.x + 256 * j;
-      v[j] = dY[r0 + i % SK_RB + B * (i / SK_RB)];
+  for (int g = 0; g < RPL; ++g) {
+#pragma unroll
+    for (int fi = 0; fi < FW; ++fi) {
+      x[g][fi] = X4[64 * g + B4 * fi];
+      if (SEP_AUX) a[g][fi] = A4[64 * g + B4 * fi];
     }
 #pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-      const int i = threadIdx.x + 256 * j;
-      dys[(i % SK_RB) * (NP + 1) + i / SK_RB] = v[j];
-    }
-    if (threadIdx.x < SK_FBLK * NP) {
-      const int fi = threadIdx.x / NP, n = threadIdx.x % NP;
-      w[fi][n] = W[f0 + fi + F * n];
-    }
+    for (int n = 0; n < NP; ++n) d[g][n] = D4[64 * g + B4 * n];
   }
-  __syncthreads();
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  float* part = partial + (int64_t)blockIdx.x * (F * O + O);  // [F, O] then db[O]
-  if (blockIdx.y == 0 && wave == 0) {
-    // this row chunk's part of db: lane-strided sums, then a fixed butterfly
+  float wv[FW][NP];  // W[fw + fi, n], wave-uniform
 #pragma unroll
-    for (int n = 0; n < O; ++n) {
-      float v = 0.f;
-      for (int r = lane; r < SK_RB; r += 64) v += dys[r * (NP + 1) + n];
+  for (int fi = 0; fi < FW; ++fi)
 #pragma unroll
-      for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-      if (lane == 0) part[F * O + n] = v;
-    }
-  }
-  const int64_t fw = f0 + SK_FW * wave;  // this wave's first feature
-  float acc[SK_FW][NP];
+    for (int n = 0; n < NP; ++n) wv[fi][n] = W[fw + fi + F * n];
+
+  float acc[FW][NP], dbs[NP];
 #pragma unroll
-  for (int fi = 0; fi < SK_FW; ++fi)
+  for (int fi = 0; fi < FW; ++fi)
 #pragma unroll
     for (int n = 0; n < NP; ++n) acc[fi][n] = 0.f;
-  for (int r = lane; r < SK_RB; r += 64 * SK_U) {
-    float x[SK_U][SK_FW], a[SK_U][SK_FW];
 #pragma unroll
-    for (int u = 0; u < SK_U; ++u)
+  for (int n = 0; n < NP; ++n) dbs[n] = 0.f;
 #pragma unroll
-      for (int fi = 0; fi < SK_FW; ++fi) {
-        const int64_t i = r0 + r + 64 * u + B * (fw + fi);
-        x[u][fi] = X[i];
-        a[u][fi] = SEP_AUX ? aux[i] : x[u][fi];
+  for (int g = 0; g < RPL; ++g) {
+    if (with_db) {
+#pragma unroll
+      for (int n = 0; n < NP; ++n) dbs[n] += (d[g][n][0] + d[g][n][1]) + (d[g][n][2] + d[g][n][3]);
+    }
+#pragma unroll
+    for (int fi = 0; fi < FW; ++fi)
+#pragma unroll
+      for (int n = 0; n < NP; ++n) {
+        acc[fi][n] += x[g][fi][0] * d[g][n][0];
+        acc[fi][n] += x[g][fi][1] * d[g][n][1];
+        acc[fi][n] += x[g][fi][2] * d[g][n][2];
+        acc[fi][n] += x[g][fi][3] * d[g][n][3];
       }
+    if (dX) {
+      f32x4* dX4 = reinterpret_cast<f32x4*>(dX) + (r0 >> 2) + lane + B4 * fw;
 #pragma unroll
-    for (int u = 0; u < SK_U; ++u) {
-      const int rr = r + 64 * u;
-      float dy[NP];
+      for (int fi = 0; fi < FW; ++fi) {
+        f32x4 v = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int n = 0; n < NP; ++n) dy[n] = dys[rr * (NP + 1) + n];
+        for (int n = 0; n < NP; ++n) v += d[g][n] * wv[fi][n];
+        const f32x4 m = SEP_AUX ? a[g][fi] : x[g][fi];
 #pragma unroll
-      for (int fi = 0; fi < SK_FW; ++fi) {
-        float v = 0.f;
-#pragma unroll
-        for (int n = 0; n < NP; ++n) {
-          acc[fi][n] += x[u][fi] * dy[n];
-          v += dy[n] * w[SK_FW * wave + fi][n];
+        for (int j = 0; j < 4; ++j) {
+          if (ACT == 1) v[j] *= relu_mask(m[j]);
+          if (ACT == 2) v[j] *= gelu_grad_f(m[j]);
         }
-        if (dX) {
-          if (ACT == 1) v *= relu_mask(a[u][fi]);
-          if (ACT == 2) v *= gelu_grad_f(a[u][fi]);
-          dX[r0 + rr + B * (fw + fi)] = v;
-        }
+        dX4[64 * g + B4 * fi] = v;
       }
     }
   }
-  // lane sums through LDS (the dY stage is no longer read): value e of wave
-  // w at red[(w * SK_FW * NP + e) * 64 + lane], then lane e of the wave adds
-  // its 64 entries in lane order
-  __syncthreads();
-  float* red = lds + wave * SK_FW * NP * 64;
+
+  // quad sums by DPP; lane m of a quad stores the values e with e % 4 == m
+  // at red[wave][e][quad], then lane e of the wave adds its 16 quad sums in
+  // quad order (the wave's values e >= 64 in a second pass)
+  const int q = lane >> 2, m = lane & 3;
 #pragma unroll
-  for (int fi = 0; fi < SK_FW; ++fi)
+  for (int e = 0; e < NV; ++e) {
+    const float s = quad_sum(acc[e / NP][e % NP]);
+    if ((e & 3) == m) red[wave][e][q] = s;
+  }
+  if (with_db) {
 #pragma unroll
-    for (int n = 0; n < NP; ++n) red[(fi * NP + n) * 64 + lane] = acc[fi][n];
-  __syncthreads();
-  if (lane < SK_FW * NP) {
-    const f32x4* q = reinterpret_cast<const f32x4*>(red + lane * 64);
-    float v = 0.f;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const f32x4 t = q[j];
-      v += t[0];
-      v += t[1];
-      v += t[2];
-      v += t[3];
+    for (int n = 0; n < NP; ++n) {
+      const float s = quad_sum(dbs[n]);
+      if (((NV + n) & 3) == m) red[wave][NV + n][q] = s;
     }
-    const int fi = lane / NP, n = lane % NP;
-    part[fw + fi + F * n] = v;
+  }
+  __syncthreads();
+  float* part = partial + (int64_t)blockIdx.x * (F * O + O);  // [F, O] then db[O]
+  const int cnt = with_db ? NT : NV;
+#pragma unroll
+  for (int p = 0; p < (NT + 63) / 64; ++p) {
+    const int e = lane + 64 * p;
+    if (e < cnt) {
+      const f32x4* r = reinterpret_cast<const f32x4*>(&red[wave][e][0]);
+      float v = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const f32x4 t = r[j];
+        v += t[0];
+        v += t[1];
+        v += t[2];
+        v += t[3];
+      }
+      if (e < NV) part[fw + e / NP + F * (e % NP)] = v;
+      else part[F * O + (e - NV)] = v;
+    }
   }
 }
 
@@ -236,8 +249,9 @@ void skinny_launch(dim3 grid, hipStream_t st, const float* X, const float* W, co
 }
 
 template <int NP>
-void skinny_launch_o(dim3 grid, hipStream_t st, int act, bool sep, const float* X, const float* W,
-                     const float* dY, const float* aux, float* partial, float* dX, int64_t B, int64_t F) {
+void skinny_launch_o(hipStream_t st, int act, bool sep, const float* X, const float* W, const float* dY,
+                     const float* aux, float* partial, float* dX, int64_t B, int64_t F) {
+  const dim3 grid((unsigned)(B / (256 * sk_rpl(NP))), (unsigned)(F / SK_FBLK));
   if (act == 0) skinny_launch<NP, 0, false>(grid, st, X, W, dY, aux, partial, dX, B, F);
   else if (act == 1 && sep) skinny_launch<NP, 1, true>(grid, st, X, W, dY, aux, partial, dX, B, F);
   else if (act == 1) skinny_launch<NP, 1, false>(grid, st, X, W, dY, aux, partial, dX, B, F);
@@ -246,32 +260,37 @@ void skinny_launch_o(dim3 grid, hipStream_t st, int act, bool sep, const float* 
 }
 
 // The one-pass backward above, when the shape is one it serves (O one of
-// 1, 2, 4, 8, 10, 16; B % 512 == 0, F % 16 == 0, a wide input, dW wanted);
-// *done says whether it ran.  CNHIP_LINEAR_ONE_PASS=0 keeps the GEMM path.
+// 1, 2, 4, 8, 10, 16; B % 512 == 0, F % 16 == 0, a wide input, dW wanted,
+// X, dY, dX and a separate aux 16-byte aligned); *done says whether it ran.
+// CNHIP_LINEAR_ONE_PASS=0 keeps the GEMM path.
 static bool skinny_serves(int64_t B, int64_t F, int64_t O, const float* X, const float* W, const float* dY,
-                          const float* dW) {
+                          const float* dW, const float* dX, const float* aux) {
   static const bool enabled = [] {
     const char* e = std::getenv("CNHIP_LINEAR_ONE_PASS");
     return !(e && e[0] == '0');
   }();
   const bool o_ok = O == 1 || O == 2 || O == 4 || O == 8 || O == 10 || O == 16;
-  return enabled && o_ok && B % SK_RB == 0 && F % SK_FBLK == 0 && F / SK_FBLK <= 65535 &&
-         B * F >= ((int64_t)1 << 22) && dW && X && dY && W;
+  return enabled && o_ok && B % 512 == 0 && F % SK_FBLK == 0 && F / SK_FBLK <= 65535 &&
+         B * F >= ((int64_t)1 << 22) && dW && X && dY && W && aligned16(X) && aligned16(dY) &&
+         (!dX || aligned16(dX)) && (!aux || aligned16(aux));
 }
+
+// Rows per block (and per partial) of the one-pass backward
+static int64_t skinny_rows(int64_t O) { return 256 * sk_rpl((int)O); }
 
 // partials of the one-pass backward: per row chunk [F, O] then [O]
 static size_t skinny_bytes(int64_t B, int64_t F, int64_t O) {
-  return (size_t)((B / SK_RB) * (F * O + O)) * sizeof(float);
+  return (size_t)((B / skinny_rows(O)) * (F * O + O)) * sizeof(float);
 }
 
 int linear_backward_skinny(const float* X, const float* W, const float* dY, float* dW, float* db,
                            float* dX, const float* aux, int64_t B, int64_t F, int64_t O,
                            int accumulate, int act, hipStream_t st, const char* who, bool* done) {
   *done = false;
-  if (!skinny_serves(B, F, O, X, W, dY, dW)) return CNHIP_OK;
+  if (!skinny_serves(B, F, O, X, W, dY, dW, dX, act != 0 ? aux : nullptr)) return CNHIP_OK;
   CNHIP_REQUIRE(act >= 0 && act <= 2, "%s: bad activation %d", who, act);
   CNHIP_REQUIRE(act == 0 || (dX && aux), "%s: the activation derivative needs dX and its input", who);
-  const int64_t chunks = B / SK_RB, FO = F * O;
+  const int64_t chunks = B / skinny_rows(O), FO = F * O;
   CNHIP_REQUIRE(chunks <= 0x7fffffff, "%s: too large", who);
   void* ws = nullptr;
   CNHIP_TRY(scratch(st, kScratchGemm, skinny_bytes(B, F, O), &ws, who));
@@ -284,14 +303,13 @@ int linear_backward_skinny(const float* X, const float* W, const float* dY, floa
     HbmTimer timer("linear_bwd_skinny_kernel",
                    per * (double)B * (double)F + 4.0 * (double)B * (double)O + 4.0 * (double)(chunks * (FO + O)),
                    st);
-    const dim3 grid((unsigned)chunks, (unsigned)(F / SK_FBLK));
     switch (O) {
-      case 1: skinny_launch_o<1>(grid, st, act, sep, X, W, dY, aux, partial, dX, B, F); break;
-      case 2: skinny_launch_o<2>(grid, st, act, sep, X, W, dY, aux, partial, dX, B, F); break;
-      case 4: skinny_launch_o<4>(grid, st, act, sep, X, W, dY, aux, partial, dX, B, F); break;
-      case 8: skinny_launch_o<8>(grid, st, act, sep, X, W, dY, aux, partial, dX, B, F); break;
-      case 10: skinny_launch_o<10>(grid, st, act, sep, X, W, dY, aux, partial, dX, B, F); break;
-      default: skinny_launch_o<16>(grid, st, act, sep, X, W, dY, aux, partial, dX, B, F); break;
+      case 1: skinny_launch_o<1>(st, act, sep, X, W, dY, aux, partial, dX, B, F); break;
+      case 2: skinny_launch_o<2>(st, act, sep, X, W, dY, aux, partial, dX, B, F); break;
+      case 4: skinny_launch_o<4>(st, act, sep, X, W, dY, aux, partial, dX, B, F); break;
+      case 8: skinny_launch_o<8>(st, act, sep, X, W, dY, aux, partial, dX, B, F); break;
+      case 10: skinny_launch_o<10>(st, act, sep, X, W, dY, aux, partial, dX, B, F); break;
+      default: skinny_launch_o<16>(st, act, sep, X, W, dY, aux, partial, dX, B, F); break;
     }
     CNHIP_TRY(check_launch(who));
   }
@@ -309,11 +327,18 @@ int linear_backward_skinny(const float* X, const float* W, const float* dY, floa
 // GEMM unless the one-pass kernel wrote dX (it does for every act but the
 // residual sum).
 size_t linear_backward_act_scratch_bytes(const float* X, const float* W, const float* dY,
-                                         const float* grad_W, const float* dX, int64_t B, int64_t I,
-                                         int64_t O, int trainable, int act) {
-  const bool one_pass = trainable && B > 0 && skinny_serves(B, I, O, X, W, dY, grad_W);
+                                         const float* grad_W, const float* dX, const float* act_aux, int64_t B,
+                                         int64_t I, int64_t O, int trainable, int act) {
+  // the one pass with dX (act none, ReLU, GELU), else (act ReLU, GELU,
+  // residual) the one pass for dW and db only, followed by the dX GEMM
+  const bool run = trainable && B > 0;
+  const bool full = run && act != CNHIP_ACT_RESIDUAL &&
+                    skinny_serves(B, I, O, X, W, dY, grad_W, dX,
+                                  act == CNHIP_ACT_RELU || act == CNHIP_ACT_GELU ? act_aux : nullptr);
+  const bool one_pass =
+      full || (run && act != CNHIP_ACT_NONE && skinny_serves(B, I, O, X, W, dY, grad_W, nullptr, nullptr));
   size_t need = one_pass ? skinny_bytes(B, I, O) : trainable ? gemm_scratch_bytes(1, 0, I, O, B, 1) : 0;
-  if (dX && !(one_pass && act != CNHIP_ACT_RESIDUAL)) need = std::max(need, gemm_scratch_bytes(0, 1, B, I, O, 1));
+  if (dX && !full) need = std::max(need, gemm_scratch_bytes(0, 1, B, I, O, 1));
   return need;
 }
 

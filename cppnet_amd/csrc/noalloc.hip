@@ -21,8 +21,8 @@ static __device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(flo
 
 namespace cnhip {
 size_t linear_backward_act_scratch_bytes(const float* X, const float* W, const float* dY,
-                                         const float* grad_W, const float* dX, int64_t B, int64_t I,
-                                         int64_t O, int trainable, int act);
+                                         const float* grad_W, const float* dX, const float* act_aux, int64_t B,
+                                         int64_t I, int64_t O, int trainable, int act);
 }  // namespace cnhip
 
 namespace {
@@ -59,7 +59,7 @@ extern "C" int cnhip_linear_backward_act_noalloc(const float* X, const float* W,
   CNHIP_REQUIRE(batch >= 0 && in_features > 0 && out_features > 0, "%s: bad shape batch=%lld in=%lld out=%lld",
                 who, (long long)batch, (long long)in_features, (long long)out_features);
   CNHIP_REQUIRE(act >= CNHIP_ACT_NONE && act <= CNHIP_ACT_RESIDUAL, "%s: bad activation %d", who, act);
-  const size_t need = cnhip::linear_backward_act_scratch_bytes(X, W, dY, grad_W, dX, batch, in_features,
+  const size_t need = cnhip::linear_backward_act_scratch_bytes(X, W, dY, grad_W, dX, act_aux, batch, in_features,
                                                                out_features, trainable, act);
   CNHIP_REQUIRE(need <= kNoAllocScratchBytes,
                 "%s: batch=%lld in=%lld out=%lld needs %zu bytes of workspace; the fixed device workspace "

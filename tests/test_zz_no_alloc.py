@@ -57,7 +57,7 @@ def test_noalloc_matches_linear_backward_act(gpu, case):
 
 def test_noalloc_refuses_workspace_beyond_its_array(gpu):
     """The one-pass head backward at B = 129 x 512 rows, I = 4096, O = 16 needs
-    129 chunks x (4096 x 16 + 16) floats = 33.8 MB > 32 MiB of partials: the
+    258 row chunks of 256 x (4096 x 16 + 16) floats = 67.7 MB > 32 MiB of partials: the
     call fails with CNHIP_EINVAL and a message, and leaves every output as it
     was.  The buffers are full size, so even a call that ran would stay in
     bounds."""
