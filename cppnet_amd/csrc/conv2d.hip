@@ -12,7 +12,7 @@
 //   dgrad    dX_pix[N, C]  = A'[N, K'] * Wd      A'(n,k') = dY(n, oc, oh, ow), k' = oc + OC*t
 //   wgrad    dW[OC, K | 1] = dY^T * [X | 1]      contraction over (n, pixel) pairs; the
 //                                                extra ones-column yields the bias grad
-// Forward and dgrad run one GEMM per pixel (blockIdx.y).  With the pixel
+// Forward and dgrad run one GEMM per pixel (blocks in XCD-contiguous order, below).  With the pixel
 // fixed, A's column k is one fixed element offset of X (dY), or padding; a
 // table of those offsets is built in LDS once per block, so the K loop does
 // no index arithmetic: a 16-byte unit of A (4 samples at one k) is one table
@@ -82,6 +82,17 @@ __device__ __forceinline__ I gather_off(const ConvDims& d, I q1, I q2, I k) {
   return (I)d.N * (oc + OC * (oh + (I)d.HO * ow));
 }
 
+// Hardware dispatch deals consecutive block ids to the 8 XCDs in turn, and
+// each XCD has its own L2.  This maps a linear block id so that each XCD
+// owns a contiguous range of logical blocks: consecutive output pixels (or
+// the k-splits of neighbouring pixels), whose 3x3 neighbourhoods overlap,
+// then share that XCD's L2 instead of each XCD fetching its own copy.
+__device__ __forceinline__ int xcd_contiguous(int bid, int total) {
+  const int xcd = bid & 7, local = bid >> 3;
+  const int base = total >> 3, rem = total & 7;
+  return xcd * base + min(xcd, rem) + local;
+}
+
 // ------------------------------------------------------- forward / dgrad
 // Stage for kp::pipeline.  A(n, k) = src[n + off(k)] (rows contiguous along
 // the batch: a unit is 4 consecutive samples at one k, one table lookup and
@@ -147,9 +158,12 @@ __global__ void __launch_bounds__(C::NT) conv_pixel_kernel(ConvArgs a) {
   const int64_t Ng = DGRAD ? d.C : d.OC;
   const int64_t K = (DGRAD ? d.OC : d.C) * d.KS * d.KS;
   const int nbm = (int)((d.N + C::BM - 1) / C::BM);
-  const int64_t m0 = (int64_t)(blockIdx.x % nbm) * C::BM;
-  const int64_t n0 = (int64_t)(blockIdx.x / nbm) * C::BN;
-  const int64_t q = blockIdx.y, HQ = DGRAD ? d.H : d.HO;
+  // gridDim.x tiles per pixel, gridDim.y pixels
+  const int lb = xcd_contiguous((int)(blockIdx.x + gridDim.x * blockIdx.y), (int)(gridDim.x * gridDim.y));
+  const int tile = lb % (int)gridDim.x;
+  const int64_t m0 = (int64_t)(tile % nbm) * C::BM;
+  const int64_t n0 = (int64_t)(tile / nbm) * C::BN;
+  const int64_t q = lb / (int)gridDim.x, HQ = DGRAD ? d.H : d.HO;
   const int64_t q1 = q % HQ, q2 = q / HQ;
   const int ntiles = (int)((K + C::KT - 1) / C::KT);
   if (TBL) {  // host guarantees ntiles * KT <= KTBL and 32-bit offsets
@@ -518,9 +532,13 @@ __global__ void __launch_bounds__(C::NT) conv_wgrad_kernel(ConvArgs a) {
   const ConvDims& d = a.d;
   const int64_t CT = d.C * d.KS * d.KS, Ng = CT + a.has_bias, Kc = d.N * d.HO * d.WO;
   const int nbm = (int)((d.OC + C::BM - 1) / C::BM);
-  const int64_t m0 = (int64_t)(blockIdx.x % nbm) * C::BM;
-  const int64_t n0 = (int64_t)(blockIdx.x / nbm) * C::BN;
-  const int64_t k_begin = (int64_t)blockIdx.z * a.k_per_split;
+  // gridDim.x tiles, gridDim.z splits: the tiles of a split (which share its
+  // rows of dY) and neighbouring splits go to one XCD
+  const int lb = xcd_contiguous((int)(blockIdx.x + gridDim.x * blockIdx.z), (int)(gridDim.x * gridDim.z));
+  const int tile = lb % (int)gridDim.x, split = lb / (int)gridDim.x;
+  const int64_t m0 = (int64_t)(tile % nbm) * C::BM;
+  const int64_t n0 = (int64_t)(tile / nbm) * C::BN;
+  const int64_t k_begin = (int64_t)split * a.k_per_split;
   const int64_t k_end = min(Kc, k_begin + a.k_per_split);
   const int ntiles = k_end > k_begin ? (int)((k_end - k_begin + C::KT - 1) / C::KT) : 0;
   f32x16 acc[C::WM][C::WN];
@@ -534,7 +552,7 @@ __global__ void __launch_bounds__(C::NT) conv_wgrad_kernel(ConvArgs a) {
   }
   kp::reduce_wgk<C>(lds, acc);
 
-  float* P = a.partial + (int64_t)blockIdx.z * d.OC * Ng;
+  float* P = a.partial + (int64_t)split * d.OC * Ng;
   const bool p_vec = (d.OC & 3) == 0;
   kp::for_each_acc_run<C>(acc, [&](int ml, int nl, const f32x4& v) {
     const int64_t m = m0 + ml, j = n0 + nl;

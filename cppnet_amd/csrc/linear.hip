@@ -215,6 +215,79 @@ __global__ void __launch_bounds__(256) linear_bwd_skinny_kernel(
   }
 }
 
+// Forward of a Linear with few outputs over a wide input (a classifier head,
+// O <= 16):  Y[b, n] = sum_f X[b, f] W[f, n] + bias[n], in one pass over X
+// instead of a split-K GEMM whose 32-wide tile would spend most of its MFMA
+// work on padding.  X ColMajor with leading dimension B (16-byte aligned,
+// B % 256 == 0), W ColMajor [F, O].  A block covers 256 rows (a lane's 4
+// consecutive rows as one float4) and 4 fw features, wave w features fw w ..
+// fw (w + 1) - 1: the lane keeps a float4 of running sums per output over
+// its wave's features in ascending order (W wave-uniform: scalar loads),
+// eight features' loads in flight at a time.  The four waves' sums are added
+// in wave order through LDS into partial[feature chunk][B, O];
+// linear_fwd_reduce_kernel adds the chunks in order and the bias.
+template <int NP>
+__global__ void __launch_bounds__(256) linear_fwd_skinny_kernel(const float* __restrict__ X,
+                                                                const float* __restrict__ W,
+                                                                float* __restrict__ partial, int64_t B,
+                                                                int64_t F, int fw) {
+  __shared__ __align__(16) float red[4][NP][256];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t r0 = (int64_t)blockIdx.x * 256;
+  const int64_t f0 = (int64_t)blockIdx.y * 4 * fw + (int64_t)fw * wave;  // this wave's first feature
+  const int64_t B4 = B >> 2;
+  const f32x4* X4 = reinterpret_cast<const f32x4*>(X) + (r0 >> 2) + lane + B4 * f0;
+  f32x4 acc[NP];
+#pragma unroll
+  for (int n = 0; n < NP; ++n) acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int f = 0; f < fw; f += 8) {
+    f32x4 x[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = X4[B4 * (f + j)];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int n = 0; n < NP; ++n) acc[n] += x[j] * W[f0 + f + j + F * n];
+  }
+#pragma unroll
+  for (int n = 0; n < NP; ++n) *reinterpret_cast<f32x4*>(&red[wave][n][4 * lane]) = acc[n];
+  __syncthreads();
+  const int t = threadIdx.x;  // row r0 + t
+  float* part = partial + (int64_t)blockIdx.y * B * NP;
+#pragma unroll
+  for (int n = 0; n < NP; ++n) {
+    float v = red[0][n][t];
+    v += red[1][n][t];
+    v += red[2][n][t];
+    v += red[3][n][t];
+    part[r0 + t + B * n] = v;
+  }
+}
+
+// Y[e] = sum over the feature chunks, in order, of partial[chunk][e] (+ the
+// bias of e's column); loads issued eight chunks at a time.
+__global__ void __launch_bounds__(256) linear_fwd_reduce_kernel(const float* __restrict__ partial,
+                                                                const float* __restrict__ bias,
+                                                                float* __restrict__ Y, int64_t B, int64_t BO,
+                                                                int chunks) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= BO) return;
+  const float* p = partial + e;
+  float v = 0.f;
+  int c = 0;
+  for (; c + 8 <= chunks; c += 8) {
+    float q[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) q[j] = p[(int64_t)(c + j) * BO];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v += q[j];
+  }
+  for (; c < chunks; ++c) v += p[(int64_t)c * BO];
+  if (bias) v += bias[e / B];
+  Y[e] = v;
+}
+
 // out[e] (+)= sum over the row chunks, in order, of partial[chunk][e], each
 // chunk's partial being [F * O] (dW) followed by [O] (db).  Loads are issued
 // eight chunks at a time, then added in order.
@@ -320,6 +393,47 @@ int linear_backward_skinny(const float* X, const float* W, const float* dY, floa
   return check_launch(who);
 }
 
+// The one-pass forward above, when the shape is one it serves (O one of 1,
+// 2, 4, 8, 10, 16; B % 256 == 0, F % 64 == 0, B F >= 2^20, X 16-byte
+// aligned); *done says whether it ran.  Features per wave: the largest of
+// 64, 32, 16 that still gives 512 blocks (else 16), so the partials stay few.
+int linear_forward_skinny(const float* X, const float* W, const float* bias, float* Y, int64_t B, int64_t F,
+                          int64_t O, hipStream_t st, const char* who, bool* done) {
+  *done = false;
+  const bool o_ok = O == 1 || O == 2 || O == 4 || O == 8 || O == 10 || O == 16;
+  if (!(o_ok && B % 256 == 0 && F % 64 == 0 && B * F >= ((int64_t)1 << 20) && aligned16(X) && X && W && Y &&
+        B / 256 <= 0x7fffffff && F / 64 <= 65535))
+    return CNHIP_OK;
+  int fw = 16;
+  for (int c : {64, 32})
+    if ((B / 256) * (F / (4 * c)) >= 512) {
+      fw = c;
+      break;
+    }
+  const int64_t chunks = F / (4 * fw), BO = B * O;
+  void* ws = nullptr;
+  CNHIP_TRY(scratch(st, kScratchGemm, (size_t)(chunks * BO) * sizeof(float), &ws, who));
+  float* partial = static_cast<float*>(ws);
+  *done = true;
+  {
+    HbmTimer timer("linear_fwd_skinny_kernel", 4.0 * ((double)B * F + (double)F * O + (double)(chunks * BO)), st);
+    const dim3 grid((unsigned)(B / 256), (unsigned)chunks);
+    switch (O) {
+      case 1: hipLaunchKernelGGL(linear_fwd_skinny_kernel<1>, grid, dim3(256), 0, st, X, W, partial, B, F, fw); break;
+      case 2: hipLaunchKernelGGL(linear_fwd_skinny_kernel<2>, grid, dim3(256), 0, st, X, W, partial, B, F, fw); break;
+      case 4: hipLaunchKernelGGL(linear_fwd_skinny_kernel<4>, grid, dim3(256), 0, st, X, W, partial, B, F, fw); break;
+      case 8: hipLaunchKernelGGL(linear_fwd_skinny_kernel<8>, grid, dim3(256), 0, st, X, W, partial, B, F, fw); break;
+      case 10: hipLaunchKernelGGL(linear_fwd_skinny_kernel<10>, grid, dim3(256), 0, st, X, W, partial, B, F, fw); break;
+      default: hipLaunchKernelGGL(linear_fwd_skinny_kernel<16>, grid, dim3(256), 0, st, X, W, partial, B, F, fw); break;
+    }
+    CNHIP_TRY(check_launch(who));
+  }
+  HbmTimer timer("linear_fwd_reduce_kernel", 4.0 * (double)(chunks * BO) + 4.0 * (double)BO, st);
+  hipLaunchKernelGGL(linear_fwd_reduce_kernel, dim3((unsigned)((BO + 255) / 256)), dim3(256), 0, st, partial, bias, Y,
+                     B, BO, (int)chunks);
+  return check_launch(who);
+}
+
 // Largest GEMM-slot scratch request that cnhip_linear_backward_act makes for
 // these arguments (its launches run in order on one stream, so one buffer of
 // this size serves them all): the one-pass partials when that path serves
@@ -372,6 +486,10 @@ int cnhip_linear_forward(const float* X, const float* W, const float* b, float* 
                 "cnhip_linear_forward: bad shape batch=%lld in=%lld out=%lld", (long long)batch,
                 (long long)in_features, (long long)out_features);
   // Y[B,O] = X[B,I] * W[I,O]  (+ b)
+  bool one_pass = false;
+  CNHIP_TRY(cnhip::linear_forward_skinny(X, W, b, Y, batch, in_features, out_features, cnhip::as_stream(stream),
+                                         "cnhip_linear_forward", &one_pass));
+  if (one_pass) return CNHIP_OK;
   return cnhip::gemm_f32(0, 0, batch, out_features, in_features, 1.f, X, batch, W, in_features,
                          0.f, Y, batch, b, CNHIP_EPI_NONE, cnhip::as_stream(stream),
                          "cnhip_linear_forward");

@@ -76,11 +76,13 @@ def test_gemm_k_zero_scales_c(gpu, oracle):
 
 
 # (4096, 1024, 10) .. (8192, 512, 1) take the one-pass backward of a few-output
-# layer (O in 1, 2, 4, 8, 10, 16; B % 512 == 0, I % 16 == 0, B*I >= 2^22);
-# (4100, 1100, 3) is just outside it
+# layer (O in 1, 2, 4, 8, 10, 16; B % 512 == 0, I % 16 == 0, B*I >= 2^22) and
+# the one-pass forward (B % 256 == 0, I % 64 == 0, B*I >= 2^20), as does
+# config 3's head (256, 4096, 10) for the forward only; (4100, 1100, 3) is
+# just outside both
 @pytest.mark.parametrize("B,I,O", [(512, 30, 64), (512, 64, 1), (256, 1024, 256), (33, 17, 5),
                                    (4096, 1024, 10), (2048, 2048, 16), (1024, 4096, 8), (4096, 1024, 4),
-                                   (8192, 512, 2), (8192, 512, 1), (4100, 1100, 3)])
+                                   (8192, 512, 2), (8192, 512, 1), (256, 4096, 10), (4100, 1100, 3)])
 @pytest.mark.parametrize("trainable", [1, 0])
 def test_linear_vs_oracle(gpu, oracle, B, I, O, trainable):
     print(f"[linear] B={B} I={I} O={O} trainable={trainable}", flush=True)
