@@ -65,6 +65,8 @@ SIGNATURES: dict[str, tuple] = {
     "cnhip_conv2d_forward_relu": (i32, [vp, vp, vp, vp] + [i64] * 8 + [vp]),
     "cnhip_conv2d_forward_relu_maxpool": (i32, [vp, vp, vp, vp, vp] + [i64] * 10 + [vp]),
     "cnhip_conv2d_backward": (i32, [vp, vp, vp, vp, vp, vp] + [i64] * 8 + [vp]),
+    "cnhip_conv2d_backward_maxpool_relu": (i32, [vp] * 6 + [i64] * 10 + [vp]),
+    "cnhip_conv2d_backward_maxpool_relu_fits": (i32, [i64] * 10),
     "cnhip_maxpool2d_forward": (i32, [vp, vp, vp] + [i64] * 6 + [vp]),
     "cnhip_maxpool2d_backward": (i32, [vp, vp, vp] + [i64] * 6 + [vp]),
     "cnhip_maxpool2d_backward_relu": (i32, [vp, vp, vp, vp] + [i64] * 6 + [vp]),

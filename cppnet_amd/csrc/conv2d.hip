@@ -55,6 +55,12 @@ struct ConvArgs {
   int src_vec;        // forward / dgrad: N % 4 == 0 and src 16-byte aligned
   int wt_vec;         // forward: OC % 4 == 0, dgrad: K' % 4 == 0; weights 16-byte aligned
   int aligned;        // wgrad: N % KT == 0 and X, dY 16-byte aligned
+  // wgrad through a ReLU -> MaxPool2D (pool > 0): dY is the pooled gradient
+  // [N, OC, HP, WP], pidx its int32 argmax and pout the pooled output
+  const int32_t* pidx;
+  const float* pout;
+  int pool;
+  int64_t HP;
 };
 
 // Capacity of the per-block gather table (ints, 18 KiB of LDS).
@@ -418,7 +424,17 @@ __global__ void __launch_bounds__(256) conv_direct_pool_fwd_kernel(ConvArgs a, i
 // k = n + N*q over (sample, output pixel); split over blockIdx.z.
 // A(oc, k) = dY[n + N*(oc + OC*q)], B(j, k) = X(n, ic, ih, iw) for
 // j = ic + C*t < CT, 1 for j == CT: both contiguous along k within a pixel.
-template <class C, bool ALIGNED, bool FAST>
+// POOLED: A is the gradient at the conv output of a Conv2D -> ReLU ->
+// MaxPool2D stack (windows pool x pool, stride pool, tiling the output),
+// formed while loading from the pooled gradient dP, its argmax and the
+// pooled output P, as the pool's backward (maxpool_bwd_tiled_vec_kernel,
+// ReLU mask from the pooled output) would have written it: conv output
+// pixel (oh, ow) in window (oh / pool, ow / pool) at offset s = (oh % pool)
+// pool + ow % pool takes (0 + dP) * [P > 0] where the argmax is s, else 0.
+// The same values enter the same MFMAs, so the weight and bias gradients
+// equal those of the two launches bit for bit, and that gradient (the size
+// of the conv output) is never written.
+template <class C, bool ALIGNED, bool FAST, bool POOLED = false>
 struct WgradStage {
   using OA = kp::Operand<true, C::BM, C::NT, C::KT>;
   using OB = kp::Operand<true, C::BN, C::NT, C::KT>;
@@ -459,7 +475,32 @@ struct WgradStage {
       const int N = (int)d.N, HO = (int)d.HO;
       const int q = (int)(k0 / N), nb = (int)(k0 - (int64_t)q * N);
       const int oh = q % HO, ow = q / HO;
-      OA::template load<FAST>(a.dY + nb + d.N * d.OC * q, d.N, m0, 0, d.OC, C::KT, ra[S]);
+      if constexpr (POOLED) {
+        typedef int i32x4 __attribute__((ext_vector_type(4)));
+        const int pool = a.pool;
+        const int s = (oh % pool) * pool + ow % pool;
+        const int64_t pbase = nb + d.N * d.OC * ((int64_t)(oh / pool) + a.HP * (int64_t)(ow / pool));
+#pragma unroll
+        for (int p = 0; p < OA::PER; ++p) {
+          int r, k;
+          if (!OA::origin(p, r, k)) break;
+          f32x4 v{0.f, 0.f, 0.f, 0.f};
+          if (FAST || m0 + r < d.OC) {
+            const int64_t o = pbase + k + d.N * (m0 + r);
+            f32x4 gy = 0.f + *reinterpret_cast<const f32x4*>(a.dY + o);
+            const f32x4 yv = *reinterpret_cast<const f32x4*>(a.pout + o);
+            const i32x4 mi = *reinterpret_cast<const i32x4*>(a.pidx + o);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              gy[e] *= relu_mask(yv[e]);
+              v[e] = mi[e] == s ? gy[e] : 0.f;
+            }
+          }
+          ra[S][p] = v;
+        }
+      } else {
+        OA::template load<FAST>(a.dY + nb + d.N * d.OC * q, d.N, m0, 0, d.OC, C::KT, ra[S]);
+      }
       const int ih0 = oh * (int)d.S - (int)d.P, iw0 = ow * (int)d.S - (int)d.P;
 #pragma unroll
       for (int p = 0; p < OB::PER; ++p) {
@@ -523,9 +564,10 @@ struct WgradStage {
   }
 };
 
-template <class C, bool ALIGNED>
+template <class C, bool ALIGNED, bool POOLED = false>
 __global__ void __launch_bounds__(C::NT) conv_wgrad_kernel(ConvArgs a) {
-  constexpr int FLOATS = 2 * kp::stage_floats<WgradStage<C, ALIGNED, true>>();
+  static_assert(!POOLED || ALIGNED, "the pooled operand needs whole k-tiles within a pixel");
+  constexpr int FLOATS = 2 * kp::stage_floats<WgradStage<C, ALIGNED, true, POOLED>>();
   __shared__ __align__(16) float lds[FLOATS];
   static_assert((C::WGK - 1) * C::WGM * C::WGN * C::WM * C::WN * 1024 <= FLOATS,
                 "reduce_wgk needs more LDS than the operand buffers");
@@ -544,10 +586,10 @@ __global__ void __launch_bounds__(C::NT) conv_wgrad_kernel(ConvArgs a) {
   f32x16 acc[C::WM][C::WN];
   kp::zero_acc<C>(acc);
   if (ALIGNED && m0 + C::BM <= d.OC) {
-    WgradStage<C, ALIGNED, true> s(a, m0, n0, k_begin, k_end);
+    WgradStage<C, ALIGNED, true, POOLED> s(a, m0, n0, k_begin, k_end);
     kp::pipeline<C>(ntiles, lds, s, acc);
   } else {
-    WgradStage<C, ALIGNED, false> s(a, m0, n0, k_begin, k_end);
+    WgradStage<C, ALIGNED, false, POOLED> s(a, m0, n0, k_begin, k_end);
     kp::pipeline<C>(ntiles, lds, s, acc);
   }
   kp::reduce_wgk<C>(lds, acc);
@@ -692,7 +734,10 @@ int launch_wgrad(ConvArgs a, float* gW, float* gb, const float* W, float* Wr, hi
     a.partial = static_cast<float*>(ws);
     TimingRec* rec = timing_slot(2.0 * Kc * d.OC * CT);
     if (rec) (void)hipEventRecord(rec->start, st);
-    const auto kern = a.aligned ? &conv_wgrad_kernel<Cfg, true> : &conv_wgrad_kernel<Cfg, false>;
+    CNHIP_REQUIRE(a.pool == 0 || a.aligned, "%s: the pooled weight gradient needs N %% %d == 0 and 16-byte "
+                  "aligned tensors", who, Cfg::KT);
+    const auto kern = a.pool > 0 ? &conv_wgrad_kernel<Cfg, true, true>
+                      : a.aligned ? &conv_wgrad_kernel<Cfg, true> : &conv_wgrad_kernel<Cfg, false>;
     hipLaunchKernelGGL(kern, dim3((unsigned)tiles, 1, (unsigned)splits), dim3(Cfg::NT), 0, st, a);
     int status = check_launch(who);
     if (rec) (void)hipEventRecord(rec->stop, st);
@@ -808,6 +853,41 @@ int cnhip_conv2d_forward_relu_maxpool(const float* X, const float* W, const floa
   float* Y = static_cast<float*>(ws);
   CNHIP_TRY(conv_forward(X, W, b, Y, N, C, H, Wd, OC, KS, S, P, 1, stream, who));
   return cnhip_maxpool2d_forward(Y, Yp, idx, N, OC, d.HO, d.WO, pool, pool_stride, stream);
+}
+
+int cnhip_conv2d_backward_maxpool_relu_fits(int64_t N, int64_t C, int64_t H, int64_t Wd, int64_t OC, int64_t KS,
+                                            int64_t S, int64_t P, int64_t pool, int64_t pool_stride) {
+  const cnhip::ConvDims d = cnhip::make_dims(N, C, H, Wd, OC, KS, S, P);
+  if (pool_stride <= 0) pool_stride = pool;
+  return N > 0 && C > 0 && H > 0 && Wd > 0 && OC > 0 && KS > 0 && S > 0 && P >= 0 && d.HO > 0 && d.WO > 0 &&
+                 d.HO * d.WO <= 65535 && pool > 0 && pool_stride == pool && d.HO % pool == 0 && d.WO % pool == 0 &&
+                 N % 64 == 0 && N * OC * d.HO * d.WO < ((int64_t)1 << 31)
+             ? 1
+             : 0;
+}
+
+int cnhip_conv2d_backward_maxpool_relu(const float* X, const float* dP, const int32_t* idx, const float* Pout,
+                                       float* gW, float* gb, int64_t N, int64_t C, int64_t H, int64_t Wd,
+                                       int64_t OC, int64_t KS, int64_t S, int64_t P, int64_t pool,
+                                       int64_t pool_stride, cnhip_stream_t stream) {
+  const char* who = "cnhip_conv2d_backward_maxpool_relu";
+  const cnhip::ConvDims d = cnhip::make_dims(N, C, H, Wd, OC, KS, S, P);
+  CNHIP_TRY(cnhip::check_dims(d, who));
+  CNHIP_REQUIRE(X && dP && idx && Pout && gW, "%s: NULL pointer", who);
+  if (pool_stride <= 0) pool_stride = pool;  // max_pool2d.cpp:25-28
+  CNHIP_REQUIRE(cnhip_conv2d_backward_maxpool_relu_fits(N, C, H, Wd, OC, KS, S, P, pool, pool_stride),
+                "%s: needs pool windows that tile the %lldx%lld conv output (stride == pool), N %% 64 == 0 and "
+                "fewer than 2^31 conv outputs (N=%lld OC=%lld pool=%lld stride=%lld)",
+                who, (long long)d.HO, (long long)d.WO, (long long)N, (long long)OC, (long long)pool,
+                (long long)pool_stride);
+  CNHIP_REQUIRE(cnhip::aligned16(X) && cnhip::aligned16(dP) && cnhip::aligned16(idx) && cnhip::aligned16(Pout),
+                "%s: X, dP, idx and the pooled output must be 16-byte aligned", who);
+  cnhip::ConvArgs a{};
+  a.d = d; a.src = X; a.dY = dP;
+  a.has_bias = gb ? 1 : 0;
+  a.aligned = 1;
+  a.pidx = idx; a.pout = Pout; a.pool = (int)pool; a.HP = d.HO / pool;
+  return cnhip::launch_wgrad(a, gW, gb, nullptr, nullptr, as_stream(stream), who);
 }
 
 int cnhip_conv2d_backward(const float* X, const float* W, const float* dY, float* gW, float* gb,

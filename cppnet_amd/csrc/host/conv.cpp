@@ -104,6 +104,34 @@ namespace CppNet
             return dx;
         }
 
+        bool Conv2D::fuses_pool_backward(const DeviceTensor& g, const MaxPool2D& pool) const
+        {
+            if (!trainable_ || !in_cache_.defined() || !pool.fused_forward()) return false;
+            const std::vector<int64_t>& d = pool.input_dims();
+            const int64_t N = in_cache_.dimension(0), H = in_cache_.dimension(2), W = in_cache_.dimension(3);
+            if (d.size() != 4 || d[0] != N || d[1] != out_channels_ || g.size() != pool.pooled_output().size())
+                return false;
+            return cnhip_conv2d_backward_maxpool_relu_fits(N, in_channels_, H, W, out_channels_, kernel_size_,
+                                                           stride_, padding_, pool.get_pool_size(),
+                                                           pool.get_stride()) != 0;
+        }
+
+        void Conv2D::backward_params_maxpool_relu(const DeviceTensor& g, const MaxPool2D& pool)
+        {
+            if (!fuses_pool_backward(g, pool))
+                throw std::runtime_error("Conv2D::backward_params_maxpool_relu: the pool's forward was not fused "
+                                         "into this layer's, or the shape does not fit");
+            const int64_t N = in_cache_.dimension(0), H = in_cache_.dimension(2), W = in_cache_.dimension(3);
+            Device::check(cnhip_conv2d_backward_maxpool_relu(in_cache_.data(), g.data(), pool.max_indices().idata(),
+                                                             pool.pooled_output().data(), gW_.data(),
+                                                             bias_flag_ ? gb_.data() : nullptr, N, in_channels_, H,
+                                                             W, out_channels_, kernel_size_, stride_, padding_,
+                                                             pool.get_pool_size(), pool.get_stride(),
+                                                             Device::stream()),
+                          "Conv2D::backward_params_maxpool_relu");
+            grads_zero_ = false;
+        }
+
         Tensor<float, 4> Conv2D::forward(const Tensor<float, 4>& x)
         {
             return forward(DeviceTensor::from_host(x)).to_host<float, 4>();

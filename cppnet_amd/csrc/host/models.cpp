@@ -121,6 +121,18 @@ namespace CppNet
                 Activations::Activation* prev = k > first ? steps_[k - 1]->activation() : nullptr;
                 auto* relu = dynamic_cast<Activations::ReLU*>(prev);
                 Layers::MaxPool2D* fused_mp = steps_[k]->maxpool();
+                // Conv2D -> ReLU -> MaxPool2D as the first trainable layers with
+                // no input gradient wanted: the conv's parameter gradients
+                // straight from the pooled gradient
+                if (relu && fused_mp && fused_mp->fused_forward() && !input_grad && k == first + 2)
+                {
+                    Layers::Conv2D* conv = steps_[first]->conv2d();
+                    if (conv && conv->fuses_pool_backward(g, *fused_mp))
+                    {
+                        conv->backward_params_maxpool_relu(g, *fused_mp);
+                        return DeviceTensor();
+                    }
+                }
                 if (relu && fused_mp && fused_mp->fused_forward())
                 {
                     g = fused_mp->backward_relu_pooled(g);

@@ -44,6 +44,14 @@ namespace CppNet
             /// computes the parameter gradients only and returns an undefined
             /// tensor (a model's first layer, whose input is data).
             DeviceTensor backward(const DeviceTensor& grad_output, bool input_grad);
+            /// Whether backward_params_maxpool_relu serves `pool` (a forward
+            /// fused by forward_relu_maxpool into it, with a shape that fits).
+            bool fuses_pool_backward(const DeviceTensor& grad_pooled, const MaxPool2D& pool) const;
+            /// The parameter gradients of this layer, its ReLU and `pool`
+            /// from the pooled gradient in one pass (no input gradient, no
+            /// gradient of the conv output stored): equal to pool's
+            /// backward_relu_pooled() then backward(g, false).
+            void backward_params_maxpool_relu(const DeviceTensor& grad_pooled, const MaxPool2D& pool);
 
             bool is_trainable() const override { return trainable_; }
             void step(Optimizers::Optimizer& optimizer, float learning_rate) override;

@@ -120,6 +120,17 @@ def conv2d_backward(X, W, dY, grad_W, grad_b, dX, N, C, H, Wd, OC, KS, S=1, P=0)
                _p(grad_b, "gb"), _p(dX, "dX"), N, C, H, Wd, OC, KS, S, P, _stream())
 
 
+def conv2d_backward_maxpool_relu(X, dP, idx, Pout, grad_W, grad_b, N, C, H, Wd, OC, KS, S=1, P=0, pool=2,
+                                 pool_stride=-1) -> None:
+    """Weight and bias gradients of Conv2D -> ReLU -> MaxPool2D from the pooled gradient."""
+    _capi.call("cnhip_conv2d_backward_maxpool_relu", _p(X, "X"), _p(dP, "dP"), _p(idx, "idx"), _p(Pout, "Pout"),
+               _p(grad_W, "gW"), _p(grad_b, "gb"), N, C, H, Wd, OC, KS, S, P, pool, pool_stride, _stream())
+
+
+def conv2d_backward_maxpool_relu_fits(N, C, H, Wd, OC, KS, S=1, P=0, pool=2, pool_stride=-1) -> bool:
+    return bool(_capi.load().cnhip_conv2d_backward_maxpool_relu_fits(N, C, H, Wd, OC, KS, S, P, pool, pool_stride))
+
+
 def maxpool2d_forward(X, Y, idx, N, C, H, W, pool=2, stride=-1) -> None:
     _capi.call("cnhip_maxpool2d_forward", _p(X, "X"), _p(Y, "Y"), _p(idx, "idx"), N, C, H, W,
                pool, stride, _stream())

@@ -251,6 +251,28 @@ int cnhip_conv2d_backward(const float* X, const float* W, const float* dY,
                           float* grad_W, float* grad_b, float* dX, int64_t N, int64_t C,
                           int64_t H, int64_t Wd, int64_t OC, int64_t KS, int64_t S,
                           int64_t P, cnhip_stream_t stream);
+/* The weight and bias gradients of a Conv2D -> ReLU -> MaxPool2D stack whose
+ * forward ran as cnhip_conv2d_forward_relu_maxpool, straight from the pooled
+ * gradient dP [N,OC,HP,WP], the argmax idx and the pooled output Pout: the
+ * gradient at the conv output is formed while the weight-gradient GEMM loads
+ * it (routed to each window's argmax, masked by Pout > 0, as
+ * cnhip_maxpool2d_backward_relu_pooled writes it) and never stored, so
+ * grad_W and grad_b (overwritten) equal that call followed by
+ * cnhip_conv2d_backward bit for bit.  No input gradient: for a model's first
+ * layer, whose input is data.  Takes pool windows tiling the conv output
+ * (pool_stride == pool, or <= 0), N % 64 == 0 and 16-byte aligned X, dP, idx,
+ * Pout (cnhip_conv2d_backward_maxpool_relu_fits: 1 when the shape fits).
+ * Replaces Conv2D::backward (conv2d.cpp:131-198, weight and bias part),
+ * ReLU::backward (relu.cpp:194-225) and MaxPool2D::backward
+ * (max_pool2d.cpp:96-131) of that stack. */
+int cnhip_conv2d_backward_maxpool_relu(const float* X, const float* dP, const int32_t* idx,
+                                       const float* Pout, float* grad_W, float* grad_b, int64_t N,
+                                       int64_t C, int64_t H, int64_t Wd, int64_t OC, int64_t KS,
+                                       int64_t S, int64_t P, int64_t pool, int64_t pool_stride,
+                                       cnhip_stream_t stream);
+int cnhip_conv2d_backward_maxpool_relu_fits(int64_t N, int64_t C, int64_t H, int64_t Wd, int64_t OC,
+                                            int64_t KS, int64_t S, int64_t P, int64_t pool,
+                                            int64_t pool_stride);
 /* MaxPool2D: Y [N,C,HO,WO], HO = (H - pool)/stride + 1 (stride <= 0 means
  * pool); idx = int32 window-local ph*pool + pw of the first maximum;
  * backward writes every element of dX (no pre-zeroing needed).

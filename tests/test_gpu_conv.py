@@ -182,6 +182,64 @@ def test_conv_relu_maxpool_fused(gpu, N, C, H, W, OC, KS, S, P, p, ps):
         np.testing.assert_array_equal(host(dB), host(dA))
 
 
+# (N, C, H, W, OC, KS, S, P, pool): config 3's first layer; more channels and
+# the 64 x 64 weight-gradient tile (OC 64, 289 columns); an unpadded conv with
+# pool 3; stride 2 with padding 2; no bias
+CONV_POOL_BWD_CASES = [(256, 3, 32, 32, 32, 3, 1, 1, 2, True), (64, 32, 16, 16, 64, 3, 1, 1, 2, True),
+                       (128, 2, 14, 14, 32, 3, 1, 0, 3, True), (64, 4, 19, 19, 16, 5, 2, 2, 2, True),
+                       (64, 3, 16, 16, 32, 3, 1, 1, 2, False)]
+
+
+@pytest.mark.parametrize("N,C,H,W,OC,KS,S,P,p,bias", CONV_POOL_BWD_CASES)
+def test_conv_backward_maxpool_relu_fused(gpu, N, C, H, W, OC, KS, S, P, p, bias):
+    """cnhip_conv2d_backward_maxpool_relu (the conv's weight and bias
+    gradients formed from the pooled gradient, argmax and pooled output)
+    against cnhip_maxpool2d_backward_relu_pooled then cnhip_conv2d_backward:
+    bit for bit, on quantised weights with exact ties and exact zeros."""
+    from cppnet_amd import ops
+    print(f"[conv-pool-bwd] N={N} C={C} H={H} W={W} OC={OC} KS={KS} S={S} P={P} pool={p} bias={bias}", flush=True)
+    rng = np.random.default_rng(N + 3 * C + H + OC + p + KS)
+    X = rng.standard_normal(N * C * H * W).astype(np.float32)
+    Wt = (rng.integers(-3, 4, OC * C * KS * KS) * 0.25).astype(np.float32)
+    b = (rng.integers(-2, 3, OC) * 0.5).astype(np.float32)
+    HO, WO = (H + 2 * P - KS) // S + 1, (W + 2 * P - KS) // S + 1
+    HP, WP = HO // p, WO // p
+    assert ops.conv2d_backward_maxpool_relu_fits(N, C, H, W, OC, KS, S, P, p)
+    Fp = torch.empty(N * OC * HP * WP, device="cuda")
+    FI = torch.empty(N * OC * HP * WP, dtype=torch.int32, device="cuda")
+    ops.conv2d_forward_relu_maxpool(dev(X), dev(Wt), dev(b), Fp, FI, N, C, H, W, OC, KS, S, P, p)
+    dP = dev(rng.standard_normal(N * OC * HP * WP).astype(np.float32))
+    dZ = torch.empty(N * OC * HO * WO, device="cuda")
+    ops.maxpool2d_backward_relu_pooled(dP, FI, Fp, dZ, N, OC, HO, WO, p)
+    gW0, gb0 = torch.full((OC * C * KS * KS,), 7.0, device="cuda"), torch.full((OC,), 7.0, device="cuda")
+    ops.conv2d_backward(dev(X), dev(Wt), dZ, gW0, gb0 if bias else None, None, N, C, H, W, OC, KS, S, P)
+    gW1, gb1 = torch.full((OC * C * KS * KS,), 9.0, device="cuda"), torch.full((OC,), 9.0, device="cuda")
+    ops.conv2d_backward_maxpool_relu(dev(X), dP, FI, Fp, gW1, gb1 if bias else None, N, C, H, W, OC, KS, S, P, p)
+    assert np.array_equal(host(gW1).view(np.uint32), host(gW0).view(np.uint32))
+    if bias:
+        assert np.array_equal(host(gb1).view(np.uint32), host(gb0).view(np.uint32))
+    else:
+        assert bool((gb1 == 9.0).all())
+
+
+def test_conv_backward_maxpool_relu_refuses_unfit_shapes(gpu):
+    """Shapes the fused weight gradient does not take are reported by _fits
+    and refused by the call (a batch that is no multiple of 64; windows that
+    do not tile the conv output; overlapping windows) before any work."""
+    from cppnet_amd import _capi, ops
+    assert not ops.conv2d_backward_maxpool_relu_fits(100, 3, 16, 16, 32, 3, 1, 1, 2)
+    assert not ops.conv2d_backward_maxpool_relu_fits(64, 3, 15, 15, 32, 3, 1, 1, 2)
+    assert not ops.conv2d_backward_maxpool_relu_fits(64, 3, 16, 16, 32, 3, 1, 1, 3, 2)
+    N, C, H, W, OC = 100, 3, 16, 16, 32
+    t = torch.zeros(N * OC * 8 * 8, device="cuda")
+    ti = torch.zeros(N * OC * 8 * 8, dtype=torch.int32, device="cuda")
+    gW = torch.full((OC * C * 9,), 7.0, device="cuda")
+    with pytest.raises(_capi.CnhipError, match="N % 64"):
+        ops.conv2d_backward_maxpool_relu(torch.zeros(N * C * H * W, device="cuda"), t, ti, t, gW, None,
+                                         N, C, H, W, OC, 3, 1, 1, 2)
+    assert bool((gW == 7.0).all())
+
+
 # (N, C, H, W, O, pool): config 3's head; a batch that is no multiple of 64;
 # a batch of at most 64 (the separate weight gradient then sums on one thread,
 # so only the tolerance applies) with 3x3 windows and 16 outputs; the largest
