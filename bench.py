@@ -119,11 +119,12 @@ def workload(config: int, batch: int | None = None):
 
 CPU_BATCH = {1: 512, 2: 512, 3: 32, 4: 16, 5: 4}
 
-# HBM bytes per launch of the dominant kernel class, from the two rocprofv3
-# PMC runs (FETCH_SIZE, WRITE_SIZE) scaled by a reference kernel of known
-# traffic; the runs, factors and per-GEMM table are in
-# profiles/gemm_f32_config2_traffic.md.  Configs not yet measured report null.
-PMC_TRAFFIC_BYTES = {2: 388.4e6}
+# HBM bytes per launch of each config's dominant kernel class, from the two
+# rocprofv3 PMC runs (FETCH_SIZE, WRITE_SIZE) of that config scaled by a
+# reference kernel of known traffic (bench.py --traffic-calibration),
+# averaged over the class's launches of a step; the runs, the factors and the
+# per-kernel tables are in profiles/*_counters.md.
+PMC_TRAFFIC_BYTES = {1: 0.6e6, 2: 442.8e6, 3: 39.5e6, 4: 955.3e6, 5: 133.4e6}
 
 
 def _cpu_model() -> str:
@@ -224,7 +225,7 @@ def traffic_calibration() -> int:
     return 0
 
 
-def small_roofline(hbm_kernels, step_ms):
+def small_roofline(hbm_kernels, step_ms, config):
     """A step without MFMA launches (config 1: every GEMM is a latency-bound
     SIMT kernel): the SIMT GEMM class against HBM, its algorithmic bytes over
     its event-timed launch duration."""
@@ -234,7 +235,8 @@ def small_roofline(hbm_kernels, step_ms):
     return {"bound": "hbm", "kernel": "gemm_small_thread/wave_kernel (SIMT fp32 GEMMs of <= 2 MFLOP: the "
                                       "step is launch-latency bound)",
             "achieved": k["achieved_GBs"], "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": k["frac"],
-            "traffic": None, "launches_per_step": k["launches_per_step"], "avg_launch_us": k["avg_us"],
+            "traffic": PMC_TRAFFIC_BYTES.get(config), "traffic_unit": "bytes per launch (rocprofv3 PMC, see profiles/)",
+            "launches_per_step": k["launches_per_step"], "avg_launch_us": k["avg_us"],
             "bytes_per_launch": k["bytes_per_launch"],
             "share_of_step": round(k["avg_us"] * k["launches_per_step"] / (step_ms * 1e3), 3)}
 
@@ -424,7 +426,7 @@ def measure(config: int, steps: int, warmup: int, graph: bool = False, loader: s
                      "avg_launch_us": round(per_launch_us, 2),
                      "flops_per_launch": flops_per_launch,
                      "share_of_step": round(gemm_share, 3)}
-                     if launches.value else small_roofline(hbm_kernels, step_ms)),
+                     if launches.value else small_roofline(hbm_kernels, step_ms, config)),
         "hbm_kernels": ({"peak_GBs": PEAK_HBM_GBS,
                          "note": "algorithmic bytes (inputs read once, outputs written once) / "
                                  "event-timed launch duration, per bandwidth-bound kernel",
