@@ -225,6 +225,68 @@ def traffic_calibration() -> int:
     return 0
 
 
+PHASES = {"forward": ["wait for h_{t-1} (first poll sent, x_{t+1} staged)", "stage h_{t-1} and the block's vote",
+                     "recurrent product (MFMA), gates", "cell update, h_t handed on, caches written"],
+          "backward": ["weight-gradient MFMAs of step t+1", "wait for the partials of step t+1",
+                       "their sum and the block's vote", "cell backward, dG_t staged",
+                       "recurrent partials dG_t W_hh^T (MFMA) handed on"]}
+
+
+def phase_stamps(config: int = 4) -> int:
+    """Per-phase time of the persistent LSTM kernels' timesteps: one train
+    step of the config with cnhip_lstm_phase_stamps set, then the mean over
+    blocks and the interior timesteps of each phase's span (the kernels
+    record a 100 MHz realtime counter at every phase boundary)."""
+    import ctypes as C
+
+    import numpy as np
+    import torch
+    from cppnet_amd import _capi, trainer
+
+    lib = _capi.load()
+    cfg, synth, _, _, desc = workload(config)
+    params, X, Y = synth(cfg, np.random.default_rng(2024))
+    sess = trainer.Session(cfg)
+    sess.set_params(params)
+    sess.set_batch(X, Y)
+    for _ in range(3):
+        sess.step(read_loss=False)
+    sess.synchronize()
+    S, blocks = cfg.seq_len, (cfg.batch // 16) * (cfg.hidden // 16)
+    cap = blocks * S * 8
+    bufs = [torch.zeros(cap, dtype=torch.int64, device="cuda") for _ in range(2)]
+    torch.cuda.synchronize()
+    _capi.check(lib.cnhip_lstm_phase_stamps(C.c_void_p(bufs[0].data_ptr()), C.c_void_p(bufs[1].data_ptr()), cap))
+    try:
+        sess.step(read_loss=False)
+        sess.synchronize()
+    finally:
+        _capi.check(lib.cnhip_lstm_phase_stamps(None, None, 0))
+    out = {"workload": desc, "clock_MHz": 100, "timesteps": S, "blocks": blocks}
+    for k, (name, b) in enumerate(zip(("forward", "backward"), bufs)):
+        st = b.cpu().numpy().reshape(blocks, S, 8).astype(np.float64)
+        n = len(PHASES[name])
+        if name == "forward":  # steps 1 .. S-2, phases 0 .. n in time order
+            sl = st[:, 1:S - 1, :n + 1]
+        else:  # steps S-2 .. 1 (t descending in time)
+            sl = st[:, 1:S - 1, :n + 1]
+        d = np.diff(sl, axis=2) / 100.0  # us
+        step_us = (sl[:, :, n] - sl[:, :, 0]) / 100.0
+        if name == "forward":
+            nxt = (st[:, 2:S, 0] - st[:, 1:S - 1, 0]) / 100.0
+        else:
+            nxt = (st[:, 0:S - 2, 0] - st[:, 1:S - 1, 0]) / 100.0
+        out[name] = {"phases_us": {PHASES[name][i]: round(float(d[:, :, i].mean()), 3) for i in range(n)},
+                     "step_us": round(float(nxt.mean()), 3),
+                     "step_us_max_over_blocks": round(float(nxt.mean(axis=1).max()), 3),
+                     "span_us": round(float((st[:, :, 0].max() - st[:, :, 0].min()) / 100.0), 1)}
+        log(f"bench.py: {name}: " + ", ".join(f"{k2} {v:.2f} us" for k2, v in out[name]["phases_us"].items()) +
+            f"; step {out[name]['step_us']:.2f} us")
+    sess.close()
+    print(json.dumps({"phase_stamps": out}))
+    return 0
+
+
 def small_roofline(hbm_kernels, step_ms, config):
     """A step without MFMA launches (config 1: every GEMM is a latency-bound
     SIMT kernel): the SIMT GEMM class against HBM, its algorithmic bytes over
@@ -468,9 +530,14 @@ def main() -> int:
                     help="also time the same steps fed by the DataLoader (configs 1-4): 'resident' "
                          "gathers each batch in HBM, 'stream' uploads it from page-locked host "
                          "memory on a copy stream; reported under 'loader', never as 'value'")
+    ap.add_argument("--phase-stamps", action="store_true",
+                    help="only time the phases of config 4's persistent LSTM timesteps "
+                         "(cnhip_lstm_phase_stamps) and print them as JSON")
     args = ap.parse_args()
     if args.traffic_calibration:
         return traffic_calibration()
+    if args.phase_stamps:
+        return phase_stamps(4)
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (got --gpus {args.gpus}); the "
               "multi-GPU data-parallel design is described, not built", file=sys.stderr)

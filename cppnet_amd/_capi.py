@@ -74,6 +74,7 @@ SIGNATURES: dict[str, tuple] = {
     "cnhip_linear_backward_maxpool_relu": (i32, [vp] * 7 + [i64] * 7 + [i32, vp]),
     "cnhip_linear_backward_maxpool_relu_fits": (i32, [i64] * 7),
     "cnhip_recurrence_fault_check": (i32, [vp]),
+    "cnhip_lstm_phase_stamps": (i32, [vp, vp, i64]),
     "cnhip_update_seq_last": (i64, []),
     "cnhip_update_faults_taken": (i64, []),
     "cnhip_update_withheld": (i32, [i64]),

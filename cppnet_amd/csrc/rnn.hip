@@ -405,7 +405,16 @@ struct LstmFwdPersistArgs {
   // input projection computed in the kernel (IT > 0): X [B*S, I], W_ih [I, 4H]
   const float* X;
   const float* W_ih;
+  u64* stamps;  // measurement aid (null: off), see phase_stamp
 };
+
+// Measurement aid: thread 0 of each block records the constant-rate
+// realtime counter (100 MHz) at the phase boundaries of every timestep, at
+// stamps[((block) S + t) 8 + phase], block = sample tile * (H / 16) + unit
+// tile, when the host has set a buffer (cnhip_lstm_phase_stamps).
+__device__ __forceinline__ void phase_stamp(u64* stamps, int block, int S, int t, int phase) {
+  if (stamps && threadIdx.x == 0) stamps[((int64_t)block * S + t) * 8 + phase] = __builtin_amdgcn_s_memrealtime();
+}
 
 // Forward, t = 0 .. S-1.  Per step t >= 1 a block waits for h_{t-1} of its
 // 16 samples (all H units, from the H/16 blocks of its sample tile) and
@@ -554,9 +563,11 @@ __global__ void __launch_bounds__(256) lstm_fwd_persist_kernel(LstmFwdPersistArg
   }
   float c_prev = 0.0f;
   float* hsf = reinterpret_cast<float*>(hs);
+  const int sblk = st * NUT + ut;
   for (int t = 0; t < a.S; ++t) {
     const int64_t row = n + (int64_t)B * t;
     float ig, fg, gg, og;
+    phase_stamp(a.stamps, sblk, a.S, t, 0);  // step start
     if (t == 0) {  // h_0 = c_0 = 0 (lstm_cell_fwd0_kernel's arithmetic)
       if constexpr (FUSE) {
         const f32x4 ax = xpose_lanes4(x_mfma(0), lane);
@@ -581,6 +592,7 @@ __global__ void __launch_bounds__(256) lstm_fwd_persist_kernel(LstmFwdPersistArg
       ex_issue<NKB / 2, 256 * 16, kFirstPollSleep>(rs, voff, soff, w);
       const f32x4 axr = x_mfma(t & 1);
       const bool ok = ex_finish<NKB / 2, 256 * 16>(a.sync, rs, voff, soff, ex_stamp(a.sync, t), w);
+      phase_stamp(a.stamps, sblk, a.S, t, 1);  // h_{t-1} arrived
 #pragma unroll
       for (int j = 0; j < NKB / 2; ++j) {
         const int k = (tid >> 3) + 32 * j, s2 = 2 * (tid & 7);
@@ -589,6 +601,7 @@ __global__ void __launch_bounds__(256) lstm_fwd_persist_kernel(LstmFwdPersistArg
       }
       if (t + 1 < a.S) x_write((t + 1) & 1);
       if (__syncthreads_or(!ok)) return;
+      phase_stamp(a.stamps, sblk, a.S, t, 2);  // the block's vote
       if constexpr (FUSE) {
         const f32x4 ax = xpose_lanes4(axr, lane);
         xi = ax[0];
@@ -596,13 +609,21 @@ __global__ void __launch_bounds__(256) lstm_fwd_persist_kernel(LstmFwdPersistArg
         xg = ax[2];
         xo = ax[3];
       }
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      // two accumulation chains (even and odd k-blocks), added at the end:
+      // one chain of 4 NKB dependent MFMAs leaves the single wave of each
+      // SIMD waiting on each result
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kb = 0; kb < NKB; ++kb) {
+      for (int kb = 0; kb < NKB; kb += 2) {
         const f32x4 h4 = hs[(4 * kb + q) * kPt + r];
+        const f32x4 h5 = hs[(4 * (kb + 1) + q) * kPt + r];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(h4[e], wv[kb][e], acc, 0, 0, 0);
+        for (int e = 0; e < 4; ++e) {
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(h4[e], wv[kb][e], acc, 0, 0, 0);
+          acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(h5[e], wv[kb + 1][e], acc1, 0, 0, 0);
+        }
       }
+      acc += acc1;
       // acc[i]: sample 4 q + i, gate r / 4, unit 4 wave + r % 4; after the
       // transpose acc[g]: gate g of this lane's cell
       acc = xpose_lanes4(acc, lane);
@@ -612,6 +633,7 @@ __global__ void __launch_bounds__(256) lstm_fwd_persist_kernel(LstmFwdPersistArg
       gg = tanhf((acc[2] + xg) + bg);
       og = sigm((acc[3] + xo) + bo);
     }
+    phase_stamp(a.stamps, sblk, a.S, t, 3);  // recurrent product and gates
     const float ct = lstm_cell_c(fg, c_prev, ig, gg);
     const float tc = tanhf(ct);
     const float h = og * tc;
@@ -626,6 +648,7 @@ __global__ void __launch_bounds__(256) lstm_fwd_persist_kernel(LstmFwdPersistArg
     a.tanh_c[row + BS * d] = tc;
     a.Y[row + BS * d] = h;
     c_prev = ct;
+    phase_stamp(a.stamps, sblk, a.S, t, 4);  // cell update, h_t handed on, caches written
     if (!FUSE && t + 1 < a.S) {
       const float* gn = g + B;
       xi = gn[BS * d];
@@ -653,6 +676,7 @@ struct LstmBwdPersistArgs {
   float* part;
   int I;
   int dy_last;  // dY is [B, H], the gradient of the last step only (0 at the others)
+  u64* stamps;  // measurement aid (null: off), see phase_stamp
 };
 
 // Backward through time, t = S-1 .. 0.  The recurrent term dG_{t+1} W_hh^T
@@ -802,9 +826,11 @@ __global__ void __launch_bounds__(256) lstm_bwd_persist_kernel(LstmBwdPersistArg
     for (int it = 0; it < IT; ++it) load_x(it, S - 1);
   }
   float dc_next = 0.0f;
+  const int sblk = st * NUT + ut;
   for (int t = S - 1; t >= 0; --t) {
     const int64_t row = n + (int64_t)B * t;
     float dh = dy;
+    phase_stamp(a.stamps, sblk, S, t, 0);  // step start
     if (t < S - 1) {
       // partials of step t+1: writer w's word (unit, sample) at [slot (t+1)
       // & 1][w][unit][sample], stamp of step t + 2.  Thread (half, u2, p2) loads the
@@ -817,7 +843,9 @@ __global__ void __launch_bounds__(256) lstm_bwd_persist_kernel(LstmBwdPersistArg
       const unsigned soff = ((t + 1) & 1) * slot_bytes + (unsigned)half * (NUT / 2) * H * kPt * 8u;
       ex_issue<NUT / 2, H * kPt * 8>(rs, voff, soff, w);
       dw_step(t + 1);  // dgs still holds dG_{t+1}
+      phase_stamp(a.stamps, sblk, S, t, 1);  // weight-gradient MFMAs of step t + 1
       const bool ok = ex_finish<NUT / 2, H * kPt * 8>(a.sync, rs, voff, soff, ex_stamp(a.sync, t + 2), w);
+      phase_stamp(a.stamps, sblk, S, t, 2);  // partials of step t + 1 arrived
       float s0 = 0.f, s1 = 0.f;
 #pragma unroll
       for (int k = 0; k < NUT / 2; ++k) {
@@ -827,6 +855,7 @@ __global__ void __launch_bounds__(256) lstm_bwd_persist_kernel(LstmBwdPersistArg
       red[half][u2][2 * p2] = s0;
       red[half][u2][2 * p2 + 1] = s1;
       if (__syncthreads_or(!ok)) return;
+      phase_stamp(a.stamps, sblk, S, t, 3);  // the block's vote
       dh = dy + (red[0][u][m] + red[1][u][m]);
     }
     float di, df, dgg, dout;
@@ -849,6 +878,7 @@ __global__ void __launch_bounds__(256) lstm_bwd_persist_kernel(LstmBwdPersistArg
     dgsf[(((3 * 16 + u) >> 2) * kPt + m) * 4 + (u & 3)] = dout;
     if (t > 0) load_step(t - 1);
     __syncthreads();
+    phase_stamp(a.stamps, sblk, S, t, 4);  // cell backward, dG_t staged
     if (t == 0) break;
     const unsigned so = (unsigned)(t & 1) * slot_bytes + (unsigned)ut * H * kPt * 8u;
 #pragma unroll
@@ -871,6 +901,7 @@ __global__ void __launch_bounds__(256) lstm_bwd_persist_kernel(LstmBwdPersistArg
       ex_store_pair(rs, vo, so, acc[0], acc[1], ex_stamp(a.sync, t + 1));
       ex_store_pair(rs, vo + 16, so, acc[2], acc[3], ex_stamp(a.sync, t + 1));
     }
+    phase_stamp(a.stamps, sblk, S, t, 5);  // recurrent partials handed on
     // dgs is rewritten at the next step only after the wait's block-wide vote
   }
   if constexpr (FUSE) {
@@ -1553,6 +1584,14 @@ int bwd_fused_inputs(const float* X, const float* Y, int64_t I) {
   return (int)(I / 64);
 }
 
+// Phase-stamp buffers of the persistent launches (cnhip_lstm_phase_stamps):
+// forward, backward, and their capacity in 64-bit entries.
+u64* g_stamps[2] = {nullptr, nullptr};
+int64_t g_stamps_cap = 0;
+u64* stamps_for(bool fwd, int64_t blocks, int64_t S) {
+  return g_stamps[fwd ? 0 : 1] && blocks * S * 8 <= g_stamps_cap ? g_stamps[fwd ? 0 : 1] : nullptr;
+}
+
 // The whole BPTT recurrence in one persistent launch when the shape suits
 // it (dG: [B*S, 4H], fully written); false in *done to fall back.  With
 // `part` (nst (4H^2 + 4HI + 4H) floats) the launch also accumulates the
@@ -1576,7 +1615,7 @@ int lstm_bwd_persistent(const float* gates, const float* c, const float* tanh_c,
   }
   if (!persist_fits(kern, grid, 256, who)) return CNHIP_OK;
   LstmBwdPersistArgs args{gates, c, tanh_c, dY, W_hh, dG, nullptr, (int)B, (int)S, (int)nst, {},
-                          X, Y, it ? part : nullptr, (int)I, dy_last ? 1 : 0};
+                          X, Y, it ? part : nullptr, (int)I, dy_last ? 1 : 0, stamps_for(false, nst * nut, S)};
   const double G = 4.0 * H;
   double flops = 2.0 * B * G * H * (double)(S - 1);
   if (it) flops += 2.0 * H * G * B * (double)(S - 1) + 2.0 * I * G * B * (double)S;
@@ -1613,7 +1652,8 @@ int lstm_fwd_persistent(float* gates, const float* b, float* c, float* tanh_c, f
   if (!persist_enabled() || !kern || !persist_shape(B, S, H, nst, nut, grid) || !aligned16(W_hh)) return CNHIP_OK;
   const size_t ex_bytes = (size_t)2 * nst * H * kPt * sizeof(u64);
   if (ex_bytes > 0x7fffffffu || !persist_fits(kern, grid, 256, who)) return CNHIP_OK;
-  LstmFwdPersistArgs args{gates, b, c, tanh_c, Y, W_hh, nullptr, (int)B, (int)S, (int)nst, {}, X, W_ih};
+  LstmFwdPersistArgs args{gates, b, c, tanh_c, Y, W_hh, nullptr, (int)B, (int)S, (int)nst, {}, X, W_ih,
+                          stamps_for(true, nst * nut, S)};
   double flops = 2.0 * B * 4 * H * H * (double)(S - 1);
   if (it) flops += 2.0 * B * 4 * H * I * (double)S;
   TimingRec* rec = timing_slot(flops);
@@ -1697,6 +1737,14 @@ int lstm_backward(const float* X, const float* W_ih, const float* W_hh, const fl
 using cnhip::as_stream;
 
 extern "C" {
+
+int cnhip_lstm_phase_stamps(uint64_t* fwd, uint64_t* bwd, int64_t capacity) {
+  CNHIP_REQUIRE(capacity >= 0, "cnhip_lstm_phase_stamps: negative capacity");
+  cnhip::g_stamps[0] = reinterpret_cast<cnhip::u64*>(fwd);
+  cnhip::g_stamps[1] = reinterpret_cast<cnhip::u64*>(bwd);
+  cnhip::g_stamps_cap = capacity;
+  return CNHIP_OK;
+}
 
 int cnhip_recurrence_fault_check(cnhip_stream_t stream) {
   return cnhip::recurrence_fault_check(as_stream(stream), "cnhip_recurrence_fault_check");

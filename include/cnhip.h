@@ -351,6 +351,16 @@ int cnhip_linear_backward_maxpool_relu_fits(int64_t N, int64_t C, int64_t H, int
  * caller can roll back the step counts of its withheld updates.  No
  * counterpart in the reference (its recurrence is a host loop). */
 int cnhip_recurrence_fault_check(cnhip_stream_t stream);
+/* Measurement aid for the persistent LSTM kernels (no reference
+ * counterpart): while set, every persistent forward (backward) launch whose
+ * (B/16) (H/16) S 8 entries fit `capacity` records, per block and timestep,
+ * a 100 MHz realtime counter at its phase boundaries into fwd (bwd), a
+ * device array of uint64 [blocks][S][8] (block = sample tile H/16 + unit
+ * tile); forward phases: step start, h_{t-1} arrived, vote, gates, step
+ * end; backward: step start, weight-gradient MFMAs done, partials arrived,
+ * vote, cell backward done, partials handed on.  NULL / 0 switches it off.
+ * The buffers must outlive the launches that use them. */
+int cnhip_lstm_phase_stamps(uint64_t* fwd, uint64_t* bwd, int64_t capacity);
 int64_t cnhip_update_seq_last(void);
 int64_t cnhip_update_faults_taken(void);
 int cnhip_update_withheld(int64_t seq);
