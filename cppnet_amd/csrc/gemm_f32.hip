@@ -33,6 +33,7 @@ using kp::f32x4;
 // with 64x64 wave tiles and beat 4-wave blocks with larger wave tiles).
 using CfgXL = kp::Cfg<4, 2, 2, 2>;  // 256 x 128, 8 waves of 64x64
 using CfgXN = kp::Cfg<2, 4, 2, 2>;  // 128 x 256, 8 waves of 64x64
+using CfgXX = kp::Cfg<4, 4, 2, 2>;  // 256 x 256, 16 waves of 64x64 (one block per CU)
 using CfgM = kp::Cfg<4, 2, 1, 2>;   // 128 x 128, 8 waves of 32x64
 using CfgSN = kp::Cfg<4, 1, 1, 1>;  // 128 x 32 : N <= 32
 using CfgSM = kp::Cfg<1, 4, 1, 1>;  // 32 x 128 : M <= 32
@@ -480,7 +481,7 @@ TimingRec* hbm_timing_slot(const char* kernel, double bytes) {
 
 namespace {
 
-enum class Shape { XL, XN, M, SN, SM, S };
+enum class Shape { XX, XL, XN, M, SN, SM, S };
 
 template <class Cfg>
 int64_t tiles_of(int64_t M, int64_t N) {
@@ -510,6 +511,7 @@ double split_cost(Shape shape, int64_t tiles, int64_t M, int64_t N, int64_t K, i
   int64_t bm = 0, bn = 0;
   double eff = 1.0;
   switch (shape) {
+    case Shape::XX: bm = CfgXX::BM; bn = CfgXX::BN; break;
     case Shape::XL: bm = CfgXL::BM; bn = CfgXL::BN; break;
     case Shape::XN: bm = CfgXN::BM; bn = CfgXN::BN; break;
     case Shape::M: bm = CfgM::BM; bn = CfgM::BN; eff = 0.95; break;
@@ -517,7 +519,7 @@ double split_cost(Shape shape, int64_t tiles, int64_t M, int64_t N, int64_t K, i
     case Shape::SM: bm = CfgSM::BM; bn = CfgSM::BN; eff = 0.8; break;
     case Shape::S: bm = CfgS::BM; bn = CfgS::BN; eff = 0.8; break;
   }
-  const bool big = shape == Shape::XL || shape == Shape::XN || shape == Shape::M;
+  const bool big = shape == Shape::XX || shape == Shape::XL || shape == Shape::XN || shape == Shape::M;
   const int64_t per_cu = big ? 2 : 4;
   const int64_t slots = 256 * per_cu;
   // seconds per K-tile of 32 of one block, sharing its CU with per_cu - 1 others
@@ -547,7 +549,8 @@ Plan plan_gemm(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, int64_
   // the cost model above.  Otherwise, in order (rules fitted to measured
   // tile x split sweeps on MI355X, where the 512-thread tiles run 2 blocks
   // per CU and split-K costs more than its reduce traffic alone):
-  //   128 x 256 (256 x 128 when only A is k-contiguous) if >= 512 blocks;
+  //   128 x 256 (256 x 128 when only A is k-contiguous) if >= 512 blocks,
+  //   256 x 256 instead when that gives whole rounds of 256 blocks, K >= 1024;
   //   128 x 128 if >= 256 blocks;  64 x 64 if >= 512 blocks;
   //   else split K: 128 x 128 toward 512 blocks (<= 16 splits) if that
   //   reaches 256 blocks, otherwise 64 x 64 toward 512 blocks.
@@ -565,7 +568,11 @@ Plan plan_gemm(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, int64_
     const int64_t ts = tiles_of<CfgS>(M, N) * batches;
     const int64_t max_s = K >= 8 * KQ ? std::max<int64_t>(1, std::min<int64_t>(K / (4 * KQ), max_splits)) : 1;
     if (tb >= 512) {
-      shape = big;
+      // whole rounds of 256 x 256 tiles (one 16-wave block per CU) for a
+      // long contraction: each staged k-tile feeds 16 waves instead of 8
+      // (config 2's 4096^3 GEMMs 0.6-1.7% faster than 128 x 256)
+      const int64_t tx = tiles_of<CfgXX>(M, N) * batches;
+      shape = K >= 1024 && tx % 256 == 0 ? Shape::XX : big;
     } else if (tm >= 256) {
       shape = Shape::M;
     } else if (ts >= 512) {
@@ -589,6 +596,7 @@ Plan plan_gemm(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, int64_
   }
   int64_t tiles = 0;
   switch (shape) {
+    case Shape::XX: tiles = tiles_of<CfgXX>(M, N); break;
     case Shape::XL: tiles = tiles_of<CfgXL>(M, N); break;
     case Shape::XN: tiles = tiles_of<CfgXN>(M, N); break;
     case Shape::M: tiles = tiles_of<CfgM>(M, N); break;
@@ -611,6 +619,7 @@ int launch_plan(Shape shape, int trans_a, int trans_b, const GemmArgs& g, int64_
       timing_slot(2.0 * (double)g.M * (double)g.N * (double)g.K * (double)batches);
   if (rec) (void)hipEventRecord(rec->start, st);
   switch (shape) {
+    case Shape::XX: launch_t<CfgXX>(trans_a, trans_b, g, batches, st); break;
     case Shape::XL: launch_t<CfgXL>(trans_a, trans_b, g, batches, st); break;
     case Shape::XN: launch_t<CfgXN>(trans_a, trans_b, g, batches, st); break;
     case Shape::M: launch_t<CfgM>(trans_a, trans_b, g, batches, st); break;
