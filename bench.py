@@ -124,7 +124,7 @@ CPU_BATCH = {1: 512, 2: 512, 3: 32, 4: 16, 5: 4}
 # reference kernel of known traffic (bench.py --traffic-calibration),
 # averaged over the class's launches of a step; the runs, the factors and the
 # per-kernel tables are in profiles/*_counters.md.
-PMC_TRAFFIC_BYTES = {1: 0.6e6, 2: 442.8e6, 3: 39.5e6, 4: 955.3e6, 5: 133.4e6}
+PMC_TRAFFIC_BYTES = {1: 0.6e6, 2: 377.7e6, 3: 39.5e6, 4: 955.1e6, 5: 134.9e6}
 
 
 def _cpu_model() -> str:
