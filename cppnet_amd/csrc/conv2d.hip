@@ -25,6 +25,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "act_math.hpp"
 #include "common.hpp"
@@ -609,6 +610,178 @@ __global__ void __launch_bounds__(C::NT) conv_wgrad_kernel(ConvArgs a) {
   });
 }
 
+// Weight gradient with one output pixel per block (OC = 64, C*k^2 <= 16 CG
+// NBW, N % 32 == 0): the block's split of the contraction is exactly the N
+// samples of its pixel, so the whole [64, C*k^2] gradient of that pixel is
+// one block's tile and every block runs the chip's full MFMA rate for its
+// whole life (the 64 x 64 tiles above take C*k^2 / 64 blocks per pixel,
+// each a few k-tiles long).  The pixel fixes every tap's input pixel, so
+// each thread's gather offsets are computed once and advance by 32 samples
+// per k-tile.  Wave (rb, cg): output rows 16 rb .. (oc) and column blocks
+// cg NBW .. cg NBW + NBW - 1 (j = c + C (kh + KS kw)) on
+// v_mfma_f32_16x16x4f32, lane (q, r) supplying k = 16 s + 4 q + e to MFMA
+// (s, e) from float4 LDS reads of rows k-contiguous.  The bias column is the
+// sum of the wave's A operands (waves cg = 0).  Partials go to the same
+// [pixel][oc + OC*j] layout as conv_wgrad_kernel's splits, for the same
+// reduce.
+constexpr int PXW_KT = 32;  // samples per k-tile
+
+// j / dv and j % dv for 0 <= j < 2^20, 1 <= dv: the quotient estimated from
+// an approximate float reciprocal (off by at most one, since the product's
+// error is below 2^20 * 2^-22) and corrected by the remainder's sign and
+// size.  A 32-bit integer division by a runtime divisor is a ~40-instruction
+// sequence; the block prologues below decode several per thread.
+__device__ __forceinline__ int divmod_small(int j, int dv, float inv, int& rem) {
+  int q = (int)((float)j * inv);
+  int r = j - q * dv;
+  if (r < 0) {
+    --q;
+    r += dv;
+  } else if (r >= dv) {
+    ++q;
+    r -= dv;
+  }
+  rem = r;
+  return q;
+}
+
+template <int CG, int NBW>
+__global__ void __launch_bounds__(256 * CG, 1) conv_wgrad_px_kernel(ConvArgs a) {
+  constexpr int MB = 4, NT = 64 * MB * CG;
+  constexpr int NJ = 16 * CG * NBW;          // B rows j (columns of dW), padded
+  constexpr int LD = PXW_KT + 4;             // LDS row stride in floats
+  constexpr int AF = 64 * LD, SF = AF + NJ * LD;
+  constexpr int AU = 64 * PXW_KT / 4, BU = NJ * PXW_KT / 4;  // float4 units per k-tile
+  constexpr int APT = (AU + NT - 1) / NT, BPT = (BU + NT - 1) / NT;
+  __shared__ __align__(16) float lds[2 * SF];
+  const ConvDims& d = a.d;
+  const int N = (int)d.N, C = (int)d.C, KS = (int)d.KS, HO = (int)d.HO;
+  const int CT = C * KS * KS;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int q = lane >> 4, r = lane & 15;
+  const int rb = wave % MB, cg = wave / MB;
+  const int pix = xcd_contiguous((int)blockIdx.x, (int)gridDim.x);
+  int oh;
+  const int ow = divmod_small(pix, HO, __builtin_amdgcn_rcpf((float)HO), oh);
+  // gather offsets (sample 0 of the unit's 4) and LDS slots of this thread's units
+  int aoff[APT], boff[BPT];
+  const float inv_c = __builtin_amdgcn_rcpf((float)C), inv_ks = __builtin_amdgcn_rcpf((float)KS);
+#pragma unroll
+  for (int i = 0; i < APT; ++i) {
+    const int u = tid + NT * i;
+    aoff[i] = u < AU ? 4 * (u & 7) + N * ((u >> 3) + 64 * pix) : -1;
+  }
+#pragma unroll
+  for (int i = 0; i < BPT; ++i) {
+    const int u = tid + NT * i, j = u >> 3;
+    boff[i] = -2;  // no unit
+    if (u < BU) {
+      boff[i] = -1;  // zero: padding column or padded input pixel
+      if (j < CT) {
+        int c, kh;
+        const int t = divmod_small(j, C, inv_c, c), kw = divmod_small(t, KS, inv_ks, kh);
+        const int ih = oh * (int)d.S - (int)d.P + kh, iw = ow * (int)d.S - (int)d.P + kw;
+        if (ih >= 0 && ih < (int)d.H && iw >= 0 && iw < (int)d.W)
+          boff[i] = 4 * (u & 7) + N * (c + C * (ih + (int)d.H * iw));
+      }
+    }
+  }
+  f32x4 ra[2][APT], rbv[2][BPT];
+  auto load = [&](auto slot, int kt) {
+    constexpr int S = decltype(slot)::value;
+    const int nb = PXW_KT * kt;
+#pragma unroll
+    for (int i = 0; i < APT; ++i)
+      if (aoff[i] >= 0) ra[S][i] = *reinterpret_cast<const f32x4*>(a.dY + aoff[i] + nb);
+#pragma unroll
+    for (int i = 0; i < BPT; ++i) {
+      f32x4 v = {0.f, 0.f, 0.f, 0.f};
+      if (boff[i] >= 0) v = *reinterpret_cast<const f32x4*>(a.src + boff[i] + nb);
+      rbv[S][i] = v;
+    }
+  };
+  auto store = [&](auto slot) {
+    constexpr int S = decltype(slot)::value;
+    float* buf = lds + S * SF;
+#pragma unroll
+    for (int i = 0; i < APT; ++i) {
+      const int u = tid + NT * i;
+      if (u < AU) *reinterpret_cast<f32x4*>(buf + (u >> 3) * LD + 4 * (u & 7)) = ra[S][i];
+    }
+#pragma unroll
+    for (int i = 0; i < BPT; ++i) {
+      const int u = tid + NT * i;
+      if (u < BU) *reinterpret_cast<f32x4*>(buf + AF + (u >> 3) * LD + 4 * (u & 7)) = rbv[S][i];
+    }
+  };
+  f32x4 acc[NBW];
+#pragma unroll
+  for (int c = 0; c < NBW; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float bsum = 0.f;
+  auto compute = [&](auto slot) {
+    constexpr int S = decltype(slot)::value;
+    const float* As = lds + S * SF;
+    const float* Bs = As + AF;
+#pragma unroll
+    for (int s = 0; s < PXW_KT / 16; ++s) {
+      const f32x4 av = *reinterpret_cast<const f32x4*>(As + (16 * rb + r) * LD + 16 * s + 4 * q);
+      f32x4 bv[NBW];
+#pragma unroll
+      for (int c = 0; c < NBW; ++c)
+        bv[c] = *reinterpret_cast<const f32x4*>(Bs + (16 * (cg * NBW + c) + r) * LD + 16 * s + 4 * q);
+      // raised issue priority while this wave's MFMAs are queued (the other
+      // wave on the SIMD is then more often the one staging operands)
+      __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int c = 0; c < NBW; ++c) acc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[e], bv[c][e], acc[c], 0, 0, 0);
+      __builtin_amdgcn_s_setprio(0);
+      if (cg == 0) bsum += (av[0] + av[1]) + (av[2] + av[3]);
+    }
+  };
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  const int nkt = N / PXW_KT;
+  load(S0{}, 0);
+  if (nkt > 1) load(S1{}, 1);
+  store(S0{});
+  __syncthreads();
+  // tile kt sits in LDS buffer kt & 1; the registers of slot kt & 1 are
+  // refilled with tile kt + 2 once tile kt has been stored
+  for (int kt = 0; kt < nkt; kt += 2) {
+    if (kt + 2 < nkt) load(S0{}, kt + 2);
+    compute(S0{});
+    if (kt + 1 < nkt) store(S1{});
+    __syncthreads();
+    if (kt + 1 >= nkt) break;
+    if (kt + 3 < nkt) load(S1{}, kt + 3);
+    compute(S1{});
+    if (kt + 2 < nkt) store(S0{});
+    __syncthreads();
+  }
+  const int64_t OC = d.OC;
+  float* P = a.partial + (int64_t)pix * OC * (CT + a.has_bias);
+#pragma unroll
+  for (int c = 0; c < NBW; ++c) {
+    const int j = 16 * (cg * NBW + c) + r;
+    if (j < CT) *reinterpret_cast<f32x4*>(P + 16 * rb + 4 * q + OC * j) = acc[c];
+  }
+  if (cg == 0 && a.has_bias) {
+    bsum += __shfl_xor(bsum, 16, 64);
+    bsum += __shfl_xor(bsum, 32, 64);
+    if (q == 0) P[16 * rb + r + OC * CT] = bsum;
+  }
+}
+
+// Shapes conv_wgrad_px_kernel<CG, NBW> serves.
+bool wgrad_px_serves(const ConvArgs& a, int CG, int NBW) {
+  const ConvDims& d = a.d;
+  return a.pool == 0 && a.aligned && d.OC == 64 && d.N % PXW_KT == 0 && d.N >= 4 * PXW_KT &&
+         d.C * d.KS * d.KS <= 16 * CG * NBW && d.HO * d.WO <= 1024 &&
+         d.N * d.C * d.H * d.W < ((int64_t)1 << 31) && d.N * d.OC * d.HO * d.WO < ((int64_t)1 << 31);
+}
+
 // gW[oc + OC*j] = sum_z partial[z][oc + OC*j]; the ones-column goes to gb.
 // 64 consecutive outputs per block (coalesced along e); the RW waves of a
 // block each sum one contiguous chunk of z in ascending order, and the chunk
@@ -717,6 +890,31 @@ int launch_wgrad(ConvArgs a, float* gW, float* gb, const float* W, float* Wr, hi
                  const char* who) {
   const ConvDims& d = a.d;
   const int64_t CT = d.C * d.KS * d.KS, Ng = CT + a.has_bias, Kc = d.N * d.HO * d.WO;
+  // the fixed-order sum of the splits' partials (and W's relayout)
+  auto reduce = [&](int64_t splits, int status) -> int {
+    if (status == CNHIP_OK) {
+      HbmTimer timer("conv_wgrad_reduce_kernel",
+                     4.0 * (double)(splits + 1) * d.OC * Ng + (Wr ? 8.0 * (double)d.OC * CT : 0.0), st);
+      hipLaunchKernelGGL(conv_wgrad_reduce_kernel, dim3((unsigned)((d.OC * Ng + 63) / 64)),
+                         dim3(64 * WGRAD_RW), 0, st, a.partial, (int)splits, d.OC, CT, a.has_bias,
+                         gW, gb, W, Wr, d.C);
+      status = check_launch(who);
+    }
+    return status;
+  };
+  if (wgrad_px_serves(a, 2, 9)) {
+    // one output pixel per block: its N samples are the block's split
+    const int64_t splits = d.HO * d.WO;
+    void* ws = nullptr;
+    CNHIP_TRY(scratch(st, kScratchLayer, (size_t)splits * d.OC * Ng * sizeof(float), &ws, who));
+    a.partial = static_cast<float*>(ws);
+    TimingRec* rec = timing_slot(2.0 * Kc * d.OC * CT);
+    if (rec) (void)hipEventRecord(rec->start, st);
+    hipLaunchKernelGGL((conv_wgrad_px_kernel<2, 9>), dim3((unsigned)splits), dim3(512), 0, st, a);
+    const int status = check_launch(who);
+    if (rec) (void)hipEventRecord(rec->stop, st);
+    return reduce(splits, status);
+  }
   // target: blocks to aim for with split-K (fewer, longer blocks cut the
   // partial traffic; more hide latency), measured per tile shape
   auto go = [&](auto cfg, int64_t target) -> int {
@@ -739,17 +937,9 @@ int launch_wgrad(ConvArgs a, float* gW, float* gb, const float* W, float* Wr, hi
     const auto kern = a.pool > 0 ? &conv_wgrad_kernel<Cfg, true, true>
                       : a.aligned ? &conv_wgrad_kernel<Cfg, true> : &conv_wgrad_kernel<Cfg, false>;
     hipLaunchKernelGGL(kern, dim3((unsigned)tiles, 1, (unsigned)splits), dim3(Cfg::NT), 0, st, a);
-    int status = check_launch(who);
+    const int status = check_launch(who);
     if (rec) (void)hipEventRecord(rec->stop, st);
-    if (status == CNHIP_OK) {
-      HbmTimer timer("conv_wgrad_reduce_kernel",
-                     4.0 * (double)(splits + 1) * d.OC * Ng + (Wr ? 8.0 * (double)d.OC * CT : 0.0), st);
-      hipLaunchKernelGGL(conv_wgrad_reduce_kernel, dim3((unsigned)((d.OC * Ng + 63) / 64)),
-                         dim3(64 * WGRAD_RW), 0, st, a.partial, (int)splits, d.OC, CT, a.has_bias,
-                         gW, gb, W, Wr, d.C);
-      status = check_launch(who);
-    }
-    return status;
+    return reduce(splits, status);
   };
   const int bm = d.OC <= 32 ? 32 : d.OC <= 64 ? 64 : 128;
   const int bn = Ng <= 32 ? 32 : Ng <= 64 ? 64 : 128;

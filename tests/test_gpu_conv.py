@@ -42,7 +42,11 @@ CONV_CASES = [(2, 3, 8, 8, 4, 3, 1, 1), (3, 2, 7, 5, 5, 3, 2, 0), (1, 4, 6, 6, 2
               # direct MFMA kernel: 5x5 taps with padding 2; stride 2 with no padding on
               # a non-square input and 64 channels; N = 320, whose second sample block
               # has one wave's worth of samples
-              (64, 1, 12, 12, 32, 5, 1, 2), (128, 2, 9, 7, 64, 3, 2, 0), (320, 3, 6, 6, 32, 3, 1, 1)]
+              (64, 1, 12, 12, 32, 5, 1, 2), (128, 2, 9, 7, 64, 3, 2, 0), (320, 3, 6, 6, 32, 3, 1, 1),
+              # OC = 64, C*KS^2 <= 288, N % 32 == 0, N >= 128: the weight gradient takes one
+              # output pixel per block (config 3's conv2 above is one): the full 288 columns;
+              # 144 columns with stride 2 and no padding on a non-square input; a 1x1 kernel
+              (128, 32, 8, 8, 64, 3, 1, 1), (128, 16, 9, 7, 64, 3, 2, 0), (160, 40, 5, 5, 64, 1, 1, 0)]
 
 
 @pytest.mark.parametrize("N,C,H,W,OC,KS,S,P", CONV_CASES)
