@@ -122,6 +122,32 @@ __device__ __forceinline__ bool update_withheld(const UpdateGuard& g) {
   return true;
 }
 
+// The arguments of one GEMM (the parameters of gemm_f32_core in
+// gemm_f32.hip: op(A) is M x K, op(B) K x N, C M x N, all column-major,
+// strides between batch entries).
+struct GemmSpec {
+  int trans_a, trans_b;
+  int64_t M, N, K;
+  float alpha;
+  const float* A;
+  int64_t lda, stride_a;
+  const float* B;
+  int64_t ldb, stride_b;
+  float beta;
+  float* C;
+  int64_t ldc, stride_c, batches;
+  const float* bias;
+  int epilogue;
+  const float* aux_in;
+  float* aux_out;
+  int64_t ld_aux;
+};
+
+// x then y, in one launch where both GEMMs are of a shape that leaves half
+// of the chip's block slots empty (gemm_f32.hip); otherwise one after the
+// other.  The two must be independent: neither reads what the other writes.
+int gemm_f32_pair(const GemmSpec& x, const GemmSpec& y, hipStream_t st, const char* who);
+
 // Bytes of GEMM scratch (split-K partials) that gemm_f32_core requests for
 // this shape: 0 when it runs without a split.
 size_t gemm_scratch_bytes(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, int64_t batches);

@@ -107,9 +107,8 @@ __device__ __forceinline__ float epilogue_value(const GemmArgs& g, const float* 
 // consecutive XCDs (8 of them, each with its own L2); remap so that every XCD
 // owns a contiguous range of tiles, then walk tiles in groups of 8 tile-rows
 // so neighbouring blocks on one XCD share A rows and B columns in its L2.
-__device__ __forceinline__ void tile_of_block(int nbm, int nbn, int& tm, int& tn) {
+__device__ __forceinline__ void tile_of_block(int bid, int nbm, int nbn, int& tm, int& tn) {
   const int total = nbm * nbn;
-  const int bid = blockIdx.x;
   const int xcd = bid & 7, local = bid >> 3;
   const int base = total >> 3, rem = total & 7;
   const int tile = xcd * base + min(xcd, rem) + local;
@@ -234,21 +233,25 @@ __device__ __forceinline__ void epilogue_interior(const GemmArgs& g, float* __re
   }
 }
 
-template <bool TA, bool TB, class C, bool FUSED>
-__global__ void __launch_bounds__(C::NT, min_blocks<C>()) gemm_f32_kernel(GemmArgs g) {
-  constexpr int BM = C::BM, BN = C::BN;
-  __shared__ __align__(16) float lds[2 * kp::stage_floats<GemmStage<true, TA, TB, C>>()];
+template <bool TA, bool TB, class C>
+constexpr int gemm_lds_floats() {
+  return 2 * kp::stage_floats<GemmStage<true, TA, TB, C>>();
+}
 
+// One block of a GEMM launch: tile block `bx` (grid x), batch entry `batch`
+// (grid y) and k-split `split` (grid z).
+template <bool TA, bool TB, class C, bool FUSED>
+__device__ __forceinline__ void gemm_block(const GemmArgs& g, float* lds, int bx, int64_t batch, int split) {
+  constexpr int BM = C::BM, BN = C::BN;
   const int nbm = (int)((g.M + BM - 1) / BM);
   const int nbn = (int)((g.N + BN - 1) / BN);
   int tm, tn;
-  tile_of_block(nbm, nbn, tm, tn);
+  tile_of_block(bx, nbm, nbn, tm, tn);
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
-  const int64_t batch = blockIdx.y;
   const float* A = g.A + batch * g.stride_a;
   const float* B = g.B + batch * g.stride_b;
 
-  const int64_t k_begin = (int64_t)blockIdx.z * g.k_per_split;
+  const int64_t k_begin = (int64_t)split * g.k_per_split;
   const int64_t k_end = min(g.K, k_begin + g.k_per_split);
   const bool full_mn = (m0 + BM <= g.M) && (n0 + BN <= g.N);
   const bool fast = g.vec_ok && full_mn && ((k_end - k_begin) % C::BK == 0);
@@ -270,7 +273,7 @@ __global__ void __launch_bounds__(C::NT, min_blocks<C>()) gemm_f32_kernel(GemmAr
       return;
     }
   }
-  float* P = g.partial ? g.partial + (batch * g.splits + blockIdx.z) * g.M * g.N : nullptr;
+  float* P = g.partial ? g.partial + (batch * g.splits + split) * g.M * g.N : nullptr;
   const bool p_vec = (g.M & 3) == 0;
   kp::for_each_acc_run<C>(acc, [&](int ml, int nl, const f32x4& v) {
     const int64_t m = m0 + ml, n = n0 + nl;
@@ -296,6 +299,37 @@ __global__ void __launch_bounds__(C::NT, min_blocks<C>()) gemm_f32_kernel(GemmAr
         if (m + e < g.M) Cp[(m + e) + g.ldc * n] = epilogue_value<FUSED>(g, Cp, v[e], m + e, n);
     }
   });
+}
+
+template <bool TA, bool TB, class C, bool FUSED>
+__global__ void __launch_bounds__(C::NT, min_blocks<C>()) gemm_f32_kernel(GemmArgs g) {
+  __shared__ __align__(16) float lds[gemm_lds_floats<TA, TB, C>()];
+  gemm_block<TA, TB, C, FUSED>(g, lds, (int)blockIdx.x, (int64_t)blockIdx.y, (int)blockIdx.z);
+}
+
+// Two independent GEMMs in one launch, both on tile shape C: blocks
+// [0, n1) run the first's (tiles1 x batches1 x splits1) blocks, the rest the
+// second's, each block exactly as in its own launch (so each product is
+// bit-identical to a launch of its own with the same plan).  A GEMM whose
+// tiles fill only one of the two block slots per CU (256 tiles of 128 x 128)
+// leaves every CU's matrix pipe idle while its single block loads its first
+// k-tiles and stores its results; a second GEMM's blocks in the other slot
+// fill those gaps.
+template <bool TA1, bool TB1, bool F1, bool TA2, bool TB2, bool F2, class C>
+__global__ void __launch_bounds__(C::NT, min_blocks<C>()) gemm_pair_kernel(GemmArgs g1, GemmArgs g2, int n1,
+                                                                           int tiles1, int batches1, int tiles2,
+                                                                           int batches2) {
+  constexpr int F = gemm_lds_floats<TA1, TB1, C>() > gemm_lds_floats<TA2, TB2, C>()
+                        ? gemm_lds_floats<TA1, TB1, C>()
+                        : gemm_lds_floats<TA2, TB2, C>();
+  __shared__ __align__(16) float lds[F];
+  int b = (int)blockIdx.x;
+  if (b < n1) {
+    gemm_block<TA1, TB1, C, F1>(g1, lds, b % tiles1, (b / tiles1) % batches1, b / (tiles1 * batches1));
+  } else {
+    b -= n1;
+    gemm_block<TA2, TB2, C, F2>(g2, lds, b % tiles2, (b / tiles2) % batches2, b / (tiles2 * batches2));
+  }
 }
 
 // Sums split-K partials in split order and applies the epilogue.
@@ -720,73 +754,151 @@ size_t gemm_scratch_bytes(int trans_a, int trans_b, int64_t M, int64_t N, int64_
   return split_bytes(plan_gemm(trans_a, trans_b, M, N, K, batches, 64), M, N, batches);
 }
 
+
+static int check_spec(const GemmSpec& s, const char* who) {
+  CNHIP_REQUIRE(s.M >= 0 && s.N >= 0 && s.K >= 0 && s.batches >= 0,
+                "%s: negative GEMM size (M=%lld N=%lld K=%lld batch=%lld)", who, (long long)s.M,
+                (long long)s.N, (long long)s.K, (long long)s.batches);
+  if (s.M == 0 || s.N == 0 || s.batches == 0) return CNHIP_OK;
+  CNHIP_REQUIRE(s.C != nullptr, "%s: C is NULL", who);
+  CNHIP_REQUIRE(s.ldc >= s.M, "%s: ldc=%lld < M=%lld", who, (long long)s.ldc, (long long)s.M);
+  if (s.K > 0) {
+    CNHIP_REQUIRE(s.A && s.B, "%s: A or B is NULL", who);
+    CNHIP_REQUIRE(s.lda >= (s.trans_a ? s.K : s.M), "%s: lda=%lld too small", who, (long long)s.lda);
+    CNHIP_REQUIRE(s.ldb >= (s.trans_b ? s.N : s.K), "%s: ldb=%lld too small", who, (long long)s.ldb);
+  }
+  CNHIP_REQUIRE(s.batches <= 65535, "%s: batch count %lld exceeds 65535", who, (long long)s.batches);
+  return CNHIP_OK;
+}
+
+static GemmArgs args_of(const GemmSpec& s, const Plan& plan) {
+  GemmArgs g;
+  g.M = s.M; g.N = s.N; g.K = s.K;
+  g.A = s.A; g.lda = s.lda; g.stride_a = s.stride_a;
+  g.B = s.B; g.ldb = s.ldb; g.stride_b = s.stride_b;
+  g.C = s.C; g.ldc = s.ldc; g.stride_c = s.stride_c;
+  g.alpha = s.alpha; g.beta = s.beta; g.bias = s.bias; g.epilogue = s.epilogue;
+  g.aux_in = s.aux_in; g.aux_out = s.aux_out; g.ld_aux = s.ld_aux;
+  g.vec_ok = (s.lda % 4 == 0) && (s.ldb % 4 == 0) && (s.stride_a % 4 == 0) && (s.stride_b % 4 == 0) &&
+             aligned16(s.A) && aligned16(s.B);
+  g.c_vec_ok = (s.ldc % 4 == 0) && (s.stride_c % 4 == 0) && aligned16(s.C);
+  g.aux_vec_ok = (s.ld_aux % 4 == 0) && s.aux_in && aligned16(s.aux_in) && s.batches == 1;
+  g.partial = nullptr;
+  g.k_per_split = plan.kps;
+  g.splits = plan.splits;
+  g.colsum = nullptr;
+  g.colsum_acc = 0;
+  return g;
+}
+
+// The fixed-order sum of a split GEMM's partials into C (with its epilogue).
+static int splitk_reduce(const GemmArgs& g, int64_t batches, hipStream_t st, const char* who) {
+  // reads the partials (and C when beta != 0), writes C
+  const double mn = (double)g.M * (double)g.N * (double)batches;
+  HbmTimer timer("splitk_reduce_kernel", 4.0 * mn * (g.splits + 1 + (g.beta != 0.f ? 1 : 0)), st);
+  if (g.M % 4 == 0 && g.M * g.N * batches < ((int64_t)1 << 31))
+    hipLaunchKernelGGL(splitk_reduce_vec_kernel, dim3(elementwise_grid(g.M * g.N * batches / 4, 256)),
+                       dim3(256), 0, st, g, (int)batches);
+  else
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(elementwise_grid(g.M * g.N * batches, 256)),
+                       dim3(256), 0, st, g, batches);
+  return check_launch(who);
+}
+
+static int gemm_spec(const GemmSpec& s, hipStream_t st, const char* who) {
+  CNHIP_TRY(check_spec(s, who));
+  if (s.M == 0 || s.N == 0 || s.batches == 0) return CNHIP_OK;
+  if (gemm_is_small(s.M, s.N, s.K, s.batches, s.trans_a, s.trans_b))
+    return gemm_small(s.trans_a, s.trans_b, s.M, s.N, s.K, s.alpha, s.A, s.lda, s.B, s.ldb, s.beta, s.C,
+                      s.ldc, s.bias, s.epilogue, s.aux_in, s.aux_out, s.ld_aux, st, who);
+
+  const Plan plan = plan_gemm(s.trans_a, s.trans_b, s.M, s.N, s.K, s.batches, 64);
+  CNHIP_REQUIRE(plan.tiles < ((int64_t)1 << 30), "%s: GEMM too large", who);
+  GemmArgs g = args_of(s, plan);
+  if (plan.splits > 1) {
+    void* ws = nullptr;
+    CNHIP_TRY(scratch(st, kScratchGemm, split_bytes(plan, s.M, s.N, s.batches), &ws, who));
+    g.partial = static_cast<float*>(ws);
+  }
+  const int status = launch_plan(plan.shape, s.trans_a, s.trans_b, g, s.batches, st, who);
+  if (plan.splits > 1 && status == CNHIP_OK) return splitk_reduce(g, s.batches, st, who);
+  return status;
+}
+
 int gemm_f32_core(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float alpha,
                   const float* A, int64_t lda, int64_t stride_a, const float* B, int64_t ldb,
                   int64_t stride_b, float beta, float* C, int64_t ldc, int64_t stride_c,
                   int64_t batches, const float* bias, int epilogue, const float* aux_in,
                   float* aux_out, int64_t ld_aux, hipStream_t st, const char* who) {
-  CNHIP_REQUIRE(M >= 0 && N >= 0 && K >= 0 && batches >= 0,
-                "%s: negative GEMM size (M=%lld N=%lld K=%lld batch=%lld)", who, (long long)M,
-                (long long)N, (long long)K, (long long)batches);
-  if (M == 0 || N == 0 || batches == 0) return CNHIP_OK;
-  CNHIP_REQUIRE(C != nullptr, "%s: C is NULL", who);
-  CNHIP_REQUIRE(ldc >= M, "%s: ldc=%lld < M=%lld", who, (long long)ldc, (long long)M);
-  if (K > 0) {
-    CNHIP_REQUIRE(A && B, "%s: A or B is NULL", who);
-    CNHIP_REQUIRE(lda >= (trans_a ? K : M), "%s: lda=%lld too small", who, (long long)lda);
-    CNHIP_REQUIRE(ldb >= (trans_b ? N : K), "%s: ldb=%lld too small", who, (long long)ldb);
+  const GemmSpec s{trans_a, trans_b, M, N, K, alpha, A, lda, stride_a, B, ldb, stride_b, beta, C, ldc,
+                   stride_c, batches, bias, epilogue, aux_in, aux_out, ld_aux};
+  return gemm_spec(s, st, who);
+}
+
+// Orientation codes of the pair kernels' two GEMMs: (trans_a, trans_b, fused
+// epilogue) of the first, then of the second.
+#define CNHIP_PAIR_CODE(a1, b1, f1, a2, b2, f2) ((a1) << 5 | (b1) << 4 | (f1) << 3 | (a2) << 2 | (b2) << 1 | (f2))
+
+// x and y in one launch when both take the 128 x 128 tile, x does not split
+// K, and together they fit the chip's 512 block slots at once (y's split
+// count is lowered to fit, never raised); otherwise one after the other.
+// Pairs served: x an input gradient (NT, optionally with a fused epilogue)
+// or a TN product, y a TN weight gradient or an NN product.
+int gemm_f32_pair(const GemmSpec& x, const GemmSpec& y, hipStream_t st, const char* who) {
+  CNHIP_TRY(check_spec(x, who));
+  CNHIP_TRY(check_spec(y, who));
+  auto apart = [&]() -> int {
+    CNHIP_TRY(gemm_spec(x, st, who));
+    return gemm_spec(y, st, who);
+  };
+  auto big = [](const GemmSpec& s) {
+    return s.M > 0 && s.N > 0 && s.K > 0 && s.batches > 0 &&
+           !gemm_is_small(s.M, s.N, s.K, s.batches, s.trans_a, s.trans_b);
+  };
+  if (!big(x) || !big(y)) return apart();
+  const Plan px = plan_gemm(x.trans_a, x.trans_b, x.M, x.N, x.K, x.batches, 64);
+  Plan py = plan_gemm(y.trans_a, y.trans_b, y.M, y.N, y.K, y.batches, 64);
+  if (px.shape != Shape::M || py.shape != Shape::M || px.splits != 1) return apart();
+  constexpr int64_t kSlots = 512;  // 2 blocks of 512 threads per CU, 256 CUs
+  const int64_t nx = px.tiles * x.batches, ty = py.tiles * y.batches;
+  if (nx + ty > kSlots) return apart();
+  if (nx + ty * py.splits > kSlots) {
+    const int fit = (int)((kSlots - nx) / ty);
+    int64_t kps = (y.K + fit - 1) / fit;
+    kps = ((kps + KQ - 1) / KQ) * KQ;
+    py.kps = kps;
+    py.splits = (int)((y.K + kps - 1) / kps);
   }
-  CNHIP_REQUIRE(batches <= 65535, "%s: batch count %lld exceeds 65535", who, (long long)batches);
-
-  if (gemm_is_small(M, N, K, batches, trans_a, trans_b))
-    return gemm_small(trans_a, trans_b, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, bias, epilogue,
-                      aux_in, aux_out, ld_aux, st, who);
-
-  const Plan plan = plan_gemm(trans_a, trans_b, M, N, K, batches, 64);
-  CNHIP_REQUIRE(plan.tiles < ((int64_t)1 << 30), "%s: GEMM too large", who);
-  const Shape shape = plan.shape;
-  const int splits = plan.splits;
-
-  GemmArgs g;
-  g.M = M; g.N = N; g.K = K;
-  g.A = A; g.lda = lda; g.stride_a = stride_a;
-  g.B = B; g.ldb = ldb; g.stride_b = stride_b;
-  g.C = C; g.ldc = ldc; g.stride_c = stride_c;
-  g.alpha = alpha; g.beta = beta; g.bias = bias; g.epilogue = epilogue;
-  g.aux_in = aux_in; g.aux_out = aux_out; g.ld_aux = ld_aux;
-  g.vec_ok = (lda % 4 == 0) && (ldb % 4 == 0) && (stride_a % 4 == 0) && (stride_b % 4 == 0) &&
-             aligned16(A) && aligned16(B);
-  g.c_vec_ok = (ldc % 4 == 0) && (stride_c % 4 == 0) && aligned16(C);
-  g.aux_vec_ok = (ld_aux % 4 == 0) && aux_in && aligned16(aux_in) && batches == 1;
-  g.partial = nullptr;
-
-  g.k_per_split = plan.kps;
-  g.splits = splits;
-
-  if (splits > 1) {
+  const bool fx = !x.trans_a && x.epilogue >= EPI_GELU, fy = !y.trans_a && y.epilogue >= EPI_GELU;
+  const int code = CNHIP_PAIR_CODE(x.trans_a, x.trans_b, fx ? 1 : 0, y.trans_a, y.trans_b, fy && py.splits == 1 ? 1 : 0);
+  using C = CfgM;
+  const void* kern = nullptr;
+  switch (code) {
+    case CNHIP_PAIR_CODE(0, 1, 1, 1, 0, 0): kern = (const void*)&gemm_pair_kernel<false, true, true, true, false, false, C>; break;
+    case CNHIP_PAIR_CODE(0, 1, 0, 1, 0, 0): kern = (const void*)&gemm_pair_kernel<false, true, false, true, false, false, C>; break;
+    case CNHIP_PAIR_CODE(1, 0, 0, 0, 0, 0): kern = (const void*)&gemm_pair_kernel<true, false, false, false, false, false, C>; break;
+    default: return apart();
+  }
+  GemmArgs gx = args_of(x, px), gy = args_of(y, py);
+  if (py.splits > 1) {
     void* ws = nullptr;
-    CNHIP_TRY(scratch(st, kScratchGemm, split_bytes(plan, M, N, batches), &ws, who));
-    g.partial = static_cast<float*>(ws);
+    CNHIP_TRY(scratch(st, kScratchGemm, split_bytes(py, y.M, y.N, y.batches), &ws, who));
+    gy.partial = static_cast<float*>(ws);
   }
-
-  int status = launch_plan(shape, trans_a, trans_b, g, batches, st, who);
-
-  if (splits > 1) {
-    if (status == CNHIP_OK) {
-      // reads the partials (and C when beta != 0), writes C
-      const double mn = (double)M * (double)N * (double)batches;
-      HbmTimer timer("splitk_reduce_kernel", 4.0 * mn * (splits + 1 + (beta != 0.f ? 1 : 0)), st);
-      if (M % 4 == 0 && M * N * batches < ((int64_t)1 << 31))
-        hipLaunchKernelGGL(splitk_reduce_vec_kernel, dim3(elementwise_grid(M * N * batches / 4, 256)),
-                           dim3(256), 0, st, g, (int)batches);
-      else
-        hipLaunchKernelGGL(splitk_reduce_kernel, dim3(elementwise_grid(M * N * batches, 256)),
-                           dim3(256), 0, st, g, batches);
-      status = check_launch(who);
-    }
-  }
+  const int64_t ny = ty * py.splits;
+  TimingRec* rec = timing_slot(2.0 * (double)x.M * (double)x.N * (double)x.K * (double)x.batches +
+                               2.0 * (double)y.M * (double)y.N * (double)y.K * (double)y.batches);
+  if (rec) (void)hipEventRecord(rec->start, st);
+  const int n1 = (int)nx, t1 = (int)px.tiles, b1 = (int)x.batches, t2 = (int)py.tiles, b2 = (int)y.batches;
+  void* kargs[] = {&gx, &gy, const_cast<int*>(&n1), const_cast<int*>(&t1), const_cast<int*>(&b1),
+                   const_cast<int*>(&t2), const_cast<int*>(&b2)};
+  int status = check_hip(hipLaunchKernel(kern, dim3((unsigned)(nx + ny)), dim3(C::NT), kargs, 0, st), who);
+  if (status == CNHIP_OK) status = check_launch(who);
+  if (rec) (void)hipEventRecord(rec->stop, st);
+  if (py.splits > 1 && status == CNHIP_OK) return splitk_reduce(gy, y.batches, st, who);
   return status;
 }
+#undef CNHIP_PAIR_CODE
 
 int gemm_f32(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float alpha,
              const float* A, int64_t lda, const float* B, int64_t ldb, float beta, float* C,

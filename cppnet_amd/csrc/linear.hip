@@ -517,8 +517,20 @@ int cnhip_linear_backward(const float* X, const float* W, const float* dY, float
     CNHIP_TRY(cnhip::linear_wgrad_small(X, dY, grad_W, grad_b, batch, in_features, out_features, accumulate,
                                         st, who, &fused));
     if (!fused) {
-      CNHIP_TRY(cnhip::gemm_f32(1, 0, in_features, out_features, batch, 1.f, X, batch, dY, batch,
-                                beta, grad_W, in_features, nullptr, CNHIP_EPI_NONE, st, who));
+      const cnhip::GemmSpec wgrad{1, 0, in_features, out_features, batch, 1.f, X, batch, 0, dY, batch, 0,
+                                  beta, grad_W, in_features, 0, 1, nullptr, CNHIP_EPI_NONE, nullptr,
+                                  nullptr, 0};
+      if (dX) {
+        // dX and dW in one launch where their tiles leave half the chip's block slots empty
+        const cnhip::GemmSpec dgrad{0, 1, batch, in_features, out_features, 1.f, dY, batch, 0, W,
+                                    in_features, 0, 0.f, dX, batch, 0, 1, nullptr, CNHIP_EPI_NONE,
+                                    nullptr, nullptr, 0};
+        CNHIP_TRY(cnhip::gemm_f32_pair(dgrad, wgrad, st, who));
+        dX = nullptr;
+      } else {
+        CNHIP_TRY(cnhip::gemm_f32(1, 0, in_features, out_features, batch, 1.f, X, batch, dY, batch, beta,
+                                  grad_W, in_features, nullptr, CNHIP_EPI_NONE, st, who));
+      }
       if (grad_b) CNHIP_TRY(cnhip::column_sum(dY, grad_b, batch, out_features, accumulate, st, who));
     }
   }
@@ -562,17 +574,35 @@ int cnhip_linear_backward_act(const float* X, const float* W, const float* dY, f
                                             cnhip::as_stream(stream), who, &one_pass));
     if (one_pass) return CNHIP_OK;
   }
-  CNHIP_TRY(cnhip_linear_backward(X, W, dY, grad_W, grad_b, act == CNHIP_ACT_NONE ? dX : nullptr,
-                                  batch, in_features, out_features, trainable, accumulate, stream));
-  if (act == CNHIP_ACT_NONE || batch == 0) return CNHIP_OK;
+  if (act == CNHIP_ACT_NONE || batch == 0)
+    return cnhip_linear_backward(X, W, dY, grad_W, grad_b, act == CNHIP_ACT_NONE ? dX : nullptr, batch,
+                                 in_features, out_features, trainable, accumulate, stream);
+  hipStream_t st = cnhip::as_stream(stream);
   // dX[B,I] = (dY W^T) * act'(act_aux), the activation's backward in the
   // epilogue; for the residual, dX = dY W^T + act_aux (the skip branch's gradient)
   const int epi = act == CNHIP_ACT_RELU   ? cnhip::EPI_DRELU
                   : act == CNHIP_ACT_GELU ? cnhip::EPI_DGELU
                                           : cnhip::EPI_ADD;
+  CNHIP_REQUIRE(batch > 0 && in_features > 0 && out_features > 0, "%s: bad shape", who);
+  const cnhip::GemmSpec dgrad{0, 1, batch, in_features, out_features, 1.f, dY, batch, 0, W, in_features, 0,
+                              0.f, dX, batch, 0, 1, nullptr, epi, act_aux, nullptr, batch};
+  if (trainable) {
+    CNHIP_REQUIRE(grad_W != nullptr, "%s: trainable layer needs grad_W", who);
+    bool fused = false;
+    CNHIP_TRY(cnhip::linear_wgrad_small(X, dY, grad_W, grad_b, batch, in_features, out_features, accumulate,
+                                        st, who, &fused));
+    if (!fused) {
+      // dX and dW in one launch where their tiles leave half the chip's block slots empty
+      const cnhip::GemmSpec wgrad{1, 0, in_features, out_features, batch, 1.f, X, batch, 0, dY, batch, 0,
+                                  accumulate ? 1.f : 0.f, grad_W, in_features, 0, 1, nullptr,
+                                  CNHIP_EPI_NONE, nullptr, nullptr, 0};
+      CNHIP_TRY(cnhip::gemm_f32_pair(dgrad, wgrad, st, who));
+      if (grad_b) CNHIP_TRY(cnhip::column_sum(dY, grad_b, batch, out_features, accumulate, st, who));
+      return CNHIP_OK;
+    }
+  }
   return cnhip::gemm_f32_act(0, 1, batch, in_features, out_features, dY, batch, W, in_features, dX,
-                             batch, nullptr, epi, act_aux, nullptr, batch, cnhip::as_stream(stream),
-                             who);
+                             batch, nullptr, epi, act_aux, nullptr, batch, st, who);
 }
 
 }  // extern "C"

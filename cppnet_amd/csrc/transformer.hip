@@ -1200,8 +1200,10 @@ int cnhip_mha_backward_rows(const float* q, const float* k, const float* v, cons
     ps = gps = S;
   }
   // grad_context = dY W_o^T (535); grad_W_o = context^T dY (536)
-  CNHIP_TRY(cnhip::gemm_f32(0, 1, BS, D, D, 1.f, dY, BS, Wo, D, 0.f, gctx, BS, nullptr, 0, st, who));
-  CNHIP_TRY(cnhip::gemm_f32(1, 0, D, D, BS, 1.f, ctx, BS, dY, BS, 0.f, gWo, D, nullptr, 0, st, who));
+  CNHIP_TRY(cnhip::gemm_f32_pair(
+      cnhip::GemmSpec{0, 1, BS, D, D, 1.f, dY, BS, 0, Wo, D, 0, 0.f, gctx, BS, 0, 1, nullptr, 0, nullptr, nullptr, 0},
+      cnhip::GemmSpec{1, 0, D, D, BS, 1.f, ctx, BS, 0, dY, BS, 0, 0.f, gWo, D, 0, 1, nullptr, 0, nullptr, nullptr, 0},
+      st, who));
   if (!by_sample) CNHIP_TRY(cnhip::transpose(gctx, gcs, B, SD, st, who));
   // grad_A^T_b = Vp_b grad_ctx_b^T (538); grad_Vp_b = A_b^T grad_ctx_b (539)
   CNHIP_TRY(cnhip::gemm_f32_batched(0, 1, S, S, D, 1.f, Vb, ld, ps, gcb, ld, gps, 0.f, gAT, S, SS, B,
@@ -1211,10 +1213,10 @@ int cnhip_mha_backward_rows(const float* q, const float* k, const float* v, cons
   // softmax Jacobian rows, times scale (541-551)
   CNHIP_TRY(cnhip::softmax_rows_bwd(At, gAT, gST, BS, S, scale, st, who));
   // grad_Qp_b = gS_b Kp_b ; grad_Kp_b = gS_b^T Qp_b (553-554)
-  CNHIP_TRY(cnhip::gemm_f32_batched(1, 0, S, D, S, 1.f, gST, S, SS, Kb, ld, ps, 0.f, gQb, ld, ps, B,
-                                    nullptr, 0, st, who));
-  CNHIP_TRY(cnhip::gemm_f32_batched(0, 0, S, D, S, 1.f, gST, S, SS, Qb, ld, ps, 0.f, gKb, ld, ps, B,
-                                    nullptr, 0, st, who));
+  CNHIP_TRY(cnhip::gemm_f32_pair(
+      cnhip::GemmSpec{1, 0, S, D, S, 1.f, gST, S, SS, Kb, ld, ps, 0.f, gQb, ld, ps, B, nullptr, 0, nullptr, nullptr, 0},
+      cnhip::GemmSpec{0, 0, S, D, S, 1.f, gST, S, SS, Qb, ld, ps, 0.f, gKb, ld, ps, B, nullptr, 0, nullptr, nullptr, 0},
+      st, who));
   // reference order: per-sample [3SD, B] -> [B, 3SD] = [B*S, 3D]
   if (!by_sample) CNHIP_TRY(cnhip::transpose(gPs, G, 3 * SD, B, st, who));
   const float* gQp = G;
@@ -1224,13 +1226,14 @@ int cnhip_mha_backward_rows(const float* q, const float* k, const float* v, cons
                       gWv == gWk + DD;
   if (packed) {
     // [gW_q gW_k gW_v] = X^T [gQp gKp gVp]; grad_input = [gQp gKp gVp] [Wq Wk Wv]^T
-    CNHIP_TRY(cnhip::gemm_f32(1, 0, D, 3 * D, BS, 1.f, q, BS, G, BS, 0.f, gWq, D, nullptr, 0, st, who));
-    if (dX && residual_grad)
-      CNHIP_TRY(cnhip::gemm_f32_act(0, 1, BS, D, 3 * D, G, BS, Wq, D, dX, BS, nullptr, cnhip::EPI_ADD,
-                                    residual_grad, nullptr, BS, st, who));
-    else if (dX)
-      CNHIP_TRY(cnhip::gemm_f32(0, 1, BS, D, 3 * D, 1.f, G, BS, Wq, D, 0.f, dX, BS, nullptr, 0, st, who));
-    return CNHIP_OK;
+    const cnhip::GemmSpec wgrad{1, 0, D, 3 * D, BS, 1.f, q, BS, 0, G, BS, 0, 0.f, gWq, D, 0, 1, nullptr, 0,
+                                nullptr, nullptr, 0};
+    if (!dX) return cnhip::gemm_f32(1, 0, D, 3 * D, BS, 1.f, q, BS, G, BS, 0.f, gWq, D, nullptr, 0, st, who);
+    // the input gradient and the weight gradient in one launch
+    return cnhip::gemm_f32_pair(cnhip::GemmSpec{0, 1, BS, D, 3 * D, 1.f, G, BS, 0, Wq, D, 0, 0.f, dX, BS, 0, 1,
+                                                nullptr, residual_grad ? cnhip::EPI_ADD : 0, residual_grad,
+                                                nullptr, residual_grad ? BS : 0},
+                                wgrad, st, who);
   }
   // weight grads over all B*S rows (556-563)
   CNHIP_TRY(cnhip::gemm_f32(1, 0, D, D, BS, 1.f, q, BS, gQp, BS, 0.f, gWq, D, nullptr, 0, st, who));

@@ -79,10 +79,12 @@ def test_gemm_k_zero_scales_c(gpu, oracle):
 # layer (O in 1, 2, 4, 8, 10, 16; B % 512 == 0, I % 16 == 0, B*I >= 2^22) and
 # the one-pass forward (B % 256 == 0, I % 64 == 0, B*I >= 2^20), as does
 # config 3's head (256, 4096, 10) for the forward only; (4100, 1100, 3) is
-# just outside both
+# just outside both; (8192, 512, 2048) runs dX and dW in one launch (both on
+# 128 x 128 tiles, 256 blocks each)
 @pytest.mark.parametrize("B,I,O", [(512, 30, 64), (512, 64, 1), (256, 1024, 256), (33, 17, 5),
                                    (4096, 1024, 10), (2048, 2048, 16), (1024, 4096, 8), (4096, 1024, 4),
-                                   (8192, 512, 2), (8192, 512, 1), (256, 4096, 10), (4100, 1100, 3)])
+                                   (8192, 512, 2), (8192, 512, 1), (256, 4096, 10), (4100, 1100, 3),
+                                   (8192, 512, 2048)])
 @pytest.mark.parametrize("trainable", [1, 0])
 def test_linear_vs_oracle(gpu, oracle, B, I, O, trainable):
     print(f"[linear] B={B} I={I} O={O} trainable={trainable}", flush=True)
@@ -313,7 +315,9 @@ def test_gemm_batched_vs_oracle(gpu, oracle, ta, tb, M, N, K, batch):
 
 
 @pytest.mark.parametrize("act", ["relu", "gelu"])
-@pytest.mark.parametrize("B,I,O", [(64, 48, 40), (4096, 1024, 512), (37, 130, 19), (4096, 10, 4096)])
+# (8192, 2048, 512): the backward's dX and dW run in one launch on both paths
+@pytest.mark.parametrize("B,I,O", [(64, 48, 40), (4096, 1024, 512), (37, 130, 19), (4096, 10, 4096),
+                                   (8192, 2048, 512)])
 def test_linear_fused_activation_matches_unfused(gpu, oracle, act, B, I, O):
     """Linear + activation in one GEMM epilogue, and the next layer's input
     gradient with the activation derivative in its epilogue, equal the
