@@ -332,8 +332,19 @@ __global__ void __launch_bounds__(1024) emb_scan_kernel(const int32_t* __restric
   __shared__ int32_t wave_total[16];
   const int64_t per = (V + 1023) / 1024;
   const int64_t lo = threadIdx.x * per, hi = min(V, lo + per);
+  // up to 8 counts per thread (V <= 8192) are loaded together into
+  // registers: a loop of dependent loads waited for each one in turn
+  constexpr int R = 8;
+  int32_t c[R];
   int32_t s = 0;
-  for (int64_t v = lo; v < hi; ++v) s += counts[v];
+  if (per <= R) {
+#pragma unroll
+    for (int i = 0; i < R; ++i) c[i] = lo + i < hi ? counts[lo + i] : 0;
+#pragma unroll
+    for (int i = 0; i < R; ++i) s += c[i];
+  } else {
+    for (int64_t v = lo; v < hi; ++v) s += counts[v];
+  }
   // exclusive scan of the 1024 per-thread counts: an inclusive shuffle scan
   // within each wave, then the 16 wave totals (integer sums: exact in any order)
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -349,9 +360,17 @@ __global__ void __launch_bounds__(1024) emb_scan_kernel(const int32_t* __restric
   for (int w = 0; w < wave; ++w) before += wave_total[w];
   int32_t run = before + x - s;
   if (threadIdx.x == 1023) offsets[V] = run + s;
-  for (int64_t v = lo; v < hi; ++v) {
-    offsets[v] = run;
-    run += counts[v];
+  if (per <= R) {
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      if (lo + i < hi) offsets[lo + i] = run;
+      run += c[i];
+    }
+  } else {
+    for (int64_t v = lo; v < hi; ++v) {
+      offsets[v] = run;
+      run += counts[v];
+    }
   }
 }
 
@@ -370,6 +389,90 @@ __global__ void __launch_bounds__(256) emb_fill_kernel(const int32_t* __restrict
     if (id >= 0 && id < V)
       keys[offsets[id] + atomicAdd(&cursor[id], 1)] = (int32_t)((p % B) * S + p / B);
   }
+}
+
+// The whole bucketing above (count, scan, fill, per-bucket sort) in one
+// block for up to 8192 tokens over up to 8192 ids, with the counters, the
+// offsets and the keys in LDS: the four launches and the counters' clearing
+// it replaces each cost a launch for a few microseconds of work.  Same
+// counts, offsets and per-bucket key order, so the same outputs.
+constexpr int kEmbSmall = 8192;
+
+__global__ void __launch_bounds__(1024) emb_bucket_small_kernel(const int32_t* __restrict__ ids,
+                                                                int32_t* __restrict__ offsets,
+                                                                int32_t* __restrict__ pos, int B, int S, int V) {
+  __shared__ int32_t cnt[kEmbSmall];  // counts, then the fill cursors
+  __shared__ int32_t off[kEmbSmall + 1];
+  __shared__ int32_t key[kEmbSmall];
+  __shared__ int32_t wave_total[16];
+  constexpr int R = kEmbSmall / 1024;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, BS = B * S;
+  for (int v = tid; v < V; v += 1024) cnt[v] = 0;
+  int32_t id[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const int p = tid + 1024 * i;
+    id[i] = p < BS ? ids[p] : -1;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < R; ++i)
+    if (id[i] >= 0 && id[i] < V) atomicAdd(&cnt[id[i]], 1);
+  __syncthreads();
+  // exclusive scan: thread t owns ids 8 t .. 8 t + 7
+  int32_t c[R];
+  int32_t s = 0;
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const int v = R * tid + i;
+    c[i] = v < V ? cnt[v] : 0;
+    s += c[i];
+  }
+  int32_t x = s;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int32_t y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) wave_total[wave] = x;
+  __syncthreads();
+  int32_t run = x - s;
+  for (int w = 0; w < wave; ++w) run += wave_total[w];
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const int v = R * tid + i;
+    if (v < V) off[v] = cnt[v] = run;
+    run += c[i];
+  }
+  if (tid == 1023) off[V] = run;
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    if (id[i] >= 0 && id[i] < V) {
+      const int p = tid + 1024 * i;
+      key[atomicAdd(&cnt[id[i]], 1)] = (p % B) * S + p / B;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const int v = R * tid + i;
+    if (v >= V) break;
+    const int lo = off[v], hi = off[v + 1];
+    for (int a = lo + 1; a < hi; ++a) {
+      const int32_t k = key[a];
+      int b = a - 1;
+      while (b >= lo && key[b] > k) {
+        key[b + 1] = key[b];
+        --b;
+      }
+      key[b + 1] = k;
+    }
+  }
+  __syncthreads();
+  for (int v = tid; v <= V; v += 1024) offsets[v] = off[v];
+  const int total = off[V];
+  for (int j = tid; j < total; j += 1024) pos[j] = key[j];
 }
 
 // Sort each bucket ascending (buckets are tiny: BS/V entries on average).
@@ -1306,18 +1409,24 @@ int cnhip_embedding_backward_rows(const int32_t* ids, const float* dY, float* gW
   int32_t* offsets = cursor + V;
   int32_t* pos = offsets + (V + 1);
   float* dYt = reinterpret_cast<float*>(reinterpret_cast<char*>(ws.p) + ((ibytes + 15) & ~size_t(15)));
-  CNHIP_TRY(cnhip::fill_bytes(counts, 0, (size_t)(2 * V) * sizeof(int32_t), st, who));
   CNHIP_TRY(cnhip::transpose(dY, dYt, BS, D, st, who));
-  const unsigned g = cnhip::elementwise_grid(BS, 256);
-  hipLaunchKernelGGL(cnhip::emb_count_kernel, dim3(g), dim3(256), 0, st, ids, counts, BS, V);
-  CNHIP_TRY(cnhip::check_launch(who));
-  hipLaunchKernelGGL(cnhip::emb_scan_kernel, dim3(1), dim3(1024), 0, st, counts, offsets, V);
-  CNHIP_TRY(cnhip::check_launch(who));
-  hipLaunchKernelGGL(cnhip::emb_fill_kernel, dim3(g), dim3(256), 0, st, ids, offsets, cursor, pos, B, S, V);
-  CNHIP_TRY(cnhip::check_launch(who));
-  hipLaunchKernelGGL(cnhip::emb_sort_kernel, dim3(cnhip::elementwise_grid(V, 256)), dim3(256), 0, st,
-                     offsets, pos, V);
-  CNHIP_TRY(cnhip::check_launch(who));
+  if (V <= cnhip::kEmbSmall && BS <= cnhip::kEmbSmall) {
+    hipLaunchKernelGGL(cnhip::emb_bucket_small_kernel, dim3(1), dim3(1024), 0, st, ids, offsets, pos, (int)B,
+                       (int)S, (int)V);
+    CNHIP_TRY(cnhip::check_launch(who));
+  } else {
+    CNHIP_TRY(cnhip::fill_bytes(counts, 0, (size_t)(2 * V) * sizeof(int32_t), st, who));
+    const unsigned g = cnhip::elementwise_grid(BS, 256);
+    hipLaunchKernelGGL(cnhip::emb_count_kernel, dim3(g), dim3(256), 0, st, ids, counts, BS, V);
+    CNHIP_TRY(cnhip::check_launch(who));
+    hipLaunchKernelGGL(cnhip::emb_scan_kernel, dim3(1), dim3(1024), 0, st, counts, offsets, V);
+    CNHIP_TRY(cnhip::check_launch(who));
+    hipLaunchKernelGGL(cnhip::emb_fill_kernel, dim3(g), dim3(256), 0, st, ids, offsets, cursor, pos, B, S, V);
+    CNHIP_TRY(cnhip::check_launch(who));
+    hipLaunchKernelGGL(cnhip::emb_sort_kernel, dim3(cnhip::elementwise_grid(V, 256)), dim3(256), 0, st,
+                       offsets, pos, V);
+    CNHIP_TRY(cnhip::check_launch(who));
+  }
   // every token's gradient row read once, every table row written
   cnhip::HbmTimer timer("emb_sum_kernel", 4.0 * (double)BS * (double)D + 4.0 * (double)V * (double)D, st);
   if (D % 4 == 0 && D < ((int64_t)1 << 31) && cnhip::aligned16(gWt))

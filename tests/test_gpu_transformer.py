@@ -223,7 +223,11 @@ def test_mha_rejects_bad_heads(gpu):
 
 
 # ---------------------------------------------------------------- embedding
-@pytest.mark.parametrize("B,S,V,D", [(3, 5, 7, 4), (4, 33, 50, 70), (32, 256, 8192, 512)])
+# up to 8192 tokens over up to 8192 ids the backward buckets the tokens in one
+# block (config 5's 32 x 256 over 8192 is one such; 64 x 128 over 300 ids puts
+# ~27 tokens in each bucket); 40 x 256 over 9000 ids takes the multi-launch path
+@pytest.mark.parametrize("B,S,V,D", [(3, 5, 7, 4), (4, 33, 50, 70), (32, 256, 8192, 512), (64, 128, 300, 16),
+                                     (40, 256, 9000, 8)])
 def test_embedding_exact(gpu, oracle, B, S, V, D):
     print(f"[embedding] B={B} S={S} V={V} D={D}", flush=True)
     rng = np.random.default_rng(B + S + V + D)
