@@ -626,6 +626,16 @@ __global__ void __launch_bounds__(C::NT) conv_wgrad_kernel(ConvArgs a) {
 // reduce.
 constexpr int PXW_KT = 32;  // samples per k-tile
 
+// Unit u (a float4: 4 samples of one row) of a k-tile -> its row; its 4-sample
+// chunk is u & 7.  Rows are 36 floats apart in LDS, conflict-free for the
+// fragment reads; the 16 lanes that one ds_write_b128 cycle serves write
+// rows r and r + 8 (36 * 8 = 288 = 32 mod 64 banks apart: disjoint halves)
+// rather than r and r + 1, whose 32-bank spans overlap by 4.  Global loads
+// stay 128-byte runs per 8 lanes.
+__device__ __forceinline__ int pxw_row(int u) {
+  return ((u >> 7) << 4) | (((u >> 3) & 1) << 3) | ((u >> 4) & 7);
+}
+
 // j / dv and j % dv for 0 <= j < 2^20, 1 <= dv: the quotient estimated from
 // an approximate float reciprocal (off by at most one, since the product's
 // error is below 2^20 * 2^-22) and corrected by the remainder's sign and
@@ -649,6 +659,7 @@ template <int CG, int NBW>
 __global__ void __launch_bounds__(256 * CG, 1) conv_wgrad_px_kernel(ConvArgs a) {
   constexpr int MB = 4, NT = 64 * MB * CG;
   constexpr int NJ = 16 * CG * NBW;          // B rows j (columns of dW), padded
+  static_assert(NJ % 16 == 0, "pxw_row maps 16-row groups");
   constexpr int LD = PXW_KT + 4;             // LDS row stride in floats
   constexpr int AF = 64 * LD, SF = AF + NJ * LD;
   constexpr int AU = 64 * PXW_KT / 4, BU = NJ * PXW_KT / 4;  // float4 units per k-tile
@@ -669,11 +680,11 @@ __global__ void __launch_bounds__(256 * CG, 1) conv_wgrad_px_kernel(ConvArgs a) 
 #pragma unroll
   for (int i = 0; i < APT; ++i) {
     const int u = tid + NT * i;
-    aoff[i] = u < AU ? 4 * (u & 7) + N * ((u >> 3) + 64 * pix) : -1;
+    aoff[i] = u < AU ? 4 * (u & 7) + N * (pxw_row(u) + 64 * pix) : -1;
   }
 #pragma unroll
   for (int i = 0; i < BPT; ++i) {
-    const int u = tid + NT * i, j = u >> 3;
+    const int u = tid + NT * i, j = pxw_row(u);
     boff[i] = -2;  // no unit
     if (u < BU) {
       boff[i] = -1;  // zero: padding column or padded input pixel
@@ -706,12 +717,12 @@ __global__ void __launch_bounds__(256 * CG, 1) conv_wgrad_px_kernel(ConvArgs a) 
 #pragma unroll
     for (int i = 0; i < APT; ++i) {
       const int u = tid + NT * i;
-      if (u < AU) *reinterpret_cast<f32x4*>(buf + (u >> 3) * LD + 4 * (u & 7)) = ra[S][i];
+      if (u < AU) *reinterpret_cast<f32x4*>(buf + pxw_row(u) * LD + 4 * (u & 7)) = ra[S][i];
     }
 #pragma unroll
     for (int i = 0; i < BPT; ++i) {
       const int u = tid + NT * i;
-      if (u < BU) *reinterpret_cast<f32x4*>(buf + AF + (u >> 3) * LD + 4 * (u & 7)) = rbv[S][i];
+      if (u < BU) *reinterpret_cast<f32x4*>(buf + AF + pxw_row(u) * LD + 4 * (u & 7)) = rbv[S][i];
     }
   };
   f32x4 acc[NBW];
