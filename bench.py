@@ -124,7 +124,7 @@ CPU_BATCH = {1: 512, 2: 512, 3: 32, 4: 16, 5: 4}
 # reference kernel of known traffic (bench.py --traffic-calibration),
 # averaged over the class's launches of a step; the runs, the factors and the
 # per-kernel tables are in profiles/*_counters.md.
-PMC_TRAFFIC_BYTES = {1: 0.6e6, 2: 377.7e6, 3: 39.5e6, 4: 955.1e6, 5: 134.9e6}
+PMC_TRAFFIC_BYTES = {1: 0.6e6, 2: 374.9e6, 3: 39.3e6, 4: 955.4e6, 5: 170.5e6}
 
 
 def _cpu_model() -> str:
@@ -374,11 +374,11 @@ def loader_leg(sess, cfg, B, steps, step_ms, mode):
 
 
 KERNEL_CLASS = {
-    3: "gemm_f32_kernel + conv_pixel/conv_wgrad_kernel (fp32 MFMA, all shapes of the step)",
+    3: "gemm_f32_kernel + conv_pixel/conv_wgrad/conv_wgrad_px_kernel (fp32 MFMA, all shapes of the step)",
     4: "gemm_f32_kernel + lstm_fwd/bwd_persist_kernel (fp32 MFMA; the whole recurrence of "
        "each pass in one launch, cell update fused, the backward also accumulating "
        "dW_hh, dW_ih and db)"}
-DEFAULT_KERNEL_CLASS = "gemm_f32_kernel (fp32 MFMA GEMM, all shapes of the step)"
+DEFAULT_KERNEL_CLASS = "gemm_f32_kernel (fp32 MFMA GEMM, all shapes of the step; gemm_pair_kernel where two run in one launch)"
 
 
 def measure(config: int, steps: int, warmup: int, graph: bool = False, loader: str | None = None,
