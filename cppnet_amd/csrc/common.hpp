@@ -146,7 +146,12 @@ struct GemmSpec {
 // x then y, in one launch where both GEMMs are of a shape that leaves half
 // of the chip's block slots empty (gemm_f32.hip); otherwise one after the
 // other.  The two must be independent: neither reads what the other writes.
-int gemm_f32_pair(const GemmSpec& x, const GemmSpec& y, hipStream_t st, const char* who);
+// With cs_out set, also cs_out[c] (+)= the sum of column c of the
+// column-major [cs_rows, cs_cols] cs_in (a bias gradient), in the launch of
+// y's split-K reduce when there is one (the same bits as column_sum).
+int gemm_f32_pair(const GemmSpec& x, const GemmSpec& y, hipStream_t st, const char* who,
+                  const float* cs_in = nullptr, float* cs_out = nullptr, int64_t cs_rows = 0, int64_t cs_cols = 0,
+                  int cs_accumulate = 0);
 
 // Bytes of GEMM scratch (split-K partials) that gemm_f32_core requests for
 // this shape: 0 when it runs without a split.

@@ -20,6 +20,7 @@
 #include <vector>
 
 #include "act_math.hpp"
+#include "colsum.hpp"
 #include "common.hpp"
 #include "mfma_kpack.hpp"
 
@@ -416,11 +417,11 @@ __global__ void __launch_bounds__(256) gemm_small_wave_kernel(GemmArgs g) {
 // splitk_reduce_kernel for M % 4 == 0 and fewer than 2^31 outputs: float4
 // partial loads (four consecutive m share n), 32-bit index arithmetic; the
 // same split-order sums and epilogue per element.
-__global__ void __launch_bounds__(256) splitk_reduce_vec_kernel(GemmArgs g, int batches) {
+__device__ __forceinline__ void splitk_reduce_vec(const GemmArgs& g, int batches, uint32_t first, uint32_t stride) {
   const uint32_t M = (uint32_t)g.M, mn4 = (uint32_t)(g.M * g.N) >> 2;
   const uint32_t total4 = mn4 * (uint32_t)batches;
   const int64_t mn = g.M * g.N;
-  for (uint32_t q = blockIdx.x * blockDim.x + threadIdx.x; q < total4; q += gridDim.x * blockDim.x) {
+  for (uint32_t q = first; q < total4; q += stride) {
     const uint32_t bt = batches == 1 ? 0u : q / mn4;
     const uint32_t e = (q - bt * mn4) << 2;
     const f32x4* P = reinterpret_cast<const f32x4*>(g.partial + (int64_t)bt * g.splits * mn + e);
@@ -440,6 +441,22 @@ __global__ void __launch_bounds__(256) splitk_reduce_vec_kernel(GemmArgs g, int 
       for (int k = 0; k < 4; ++k) C[(m + k) + g.ldc * n] = o[k];
     }
   }
+}
+
+__global__ void __launch_bounds__(256) splitk_reduce_vec_kernel(GemmArgs g, int batches) {
+  splitk_reduce_vec(g, batches, blockIdx.x * blockDim.x + threadIdx.x, gridDim.x * blockDim.x);
+}
+
+// The split-K reduce above in blocks [0, rblocks) and, in the rest, the
+// column sums of an independent matrix (a Linear's bias gradient), one wave
+// per column as column_sum does: two bandwidth-bound passes of a few
+// microseconds each in one launch.
+__global__ void __launch_bounds__(256) splitk_reduce_colsum_kernel(GemmArgs g, int batches, int rblocks, ColsumJob cs) {
+  if ((int)blockIdx.x < rblocks) {
+    splitk_reduce_vec(g, batches, blockIdx.x * blockDim.x + threadIdx.x, (uint32_t)rblocks * blockDim.x);
+    return;
+  }
+  colsum_wave(cs, (int64_t)(blockIdx.x - rblocks) * 4 + (threadIdx.x >> 6), threadIdx.x & 63);
 }
 
 template <bool TA, bool TB, class Cfg>
@@ -791,12 +808,28 @@ static GemmArgs args_of(const GemmSpec& s, const Plan& plan) {
   return g;
 }
 
+int column_sum(const float* in, float* out, int64_t rows, int64_t cols, int accumulate, hipStream_t st,
+               const char* who);
+
 // The fixed-order sum of a split GEMM's partials into C (with its epilogue).
-static int splitk_reduce(const GemmArgs& g, int64_t batches, hipStream_t st, const char* who) {
+static int splitk_reduce(const GemmArgs& g, int64_t batches, hipStream_t st, const char* who,
+                         const ColsumJob* cs = nullptr) {
   // reads the partials (and C when beta != 0), writes C
   const double mn = (double)g.M * (double)g.N * (double)batches;
+  const bool vec = g.M % 4 == 0 && g.M * g.N * batches < ((int64_t)1 << 31);
+  if (vec && cs && (cs->cols + 3) / 4 < ((int64_t)1 << 30)) {
+    HbmTimer timer("splitk_reduce_colsum_kernel",
+                   4.0 * mn * (g.splits + 1 + (g.beta != 0.f ? 1 : 0)) +
+                       4.0 * (double)cs->rows * (double)cs->cols + (cs->accumulate ? 8.0 : 4.0) * (double)cs->cols,
+                   st);
+    const unsigned rblocks = elementwise_grid(g.M * g.N * batches / 4, 256);
+    hipLaunchKernelGGL(splitk_reduce_colsum_kernel, dim3(rblocks + (unsigned)((cs->cols + 3) / 4)), dim3(256), 0, st,
+                       g, (int)batches, (int)rblocks, *cs);
+    return check_launch(who);
+  }
+  if (cs) CNHIP_TRY(column_sum(cs->in, cs->out, cs->rows, cs->cols, cs->accumulate, st, who));
   HbmTimer timer("splitk_reduce_kernel", 4.0 * mn * (g.splits + 1 + (g.beta != 0.f ? 1 : 0)), st);
-  if (g.M % 4 == 0 && g.M * g.N * batches < ((int64_t)1 << 31))
+  if (vec)
     hipLaunchKernelGGL(splitk_reduce_vec_kernel, dim3(elementwise_grid(g.M * g.N * batches / 4, 256)),
                        dim3(256), 0, st, g, (int)batches);
   else
@@ -805,12 +838,19 @@ static int splitk_reduce(const GemmArgs& g, int64_t batches, hipStream_t st, con
   return check_launch(who);
 }
 
-static int gemm_spec(const GemmSpec& s, hipStream_t st, const char* who) {
+// One GEMM; with cs set, also those column sums (in the split-K reduce's
+// launch when the plan splits).
+static int gemm_spec(const GemmSpec& s, hipStream_t st, const char* who, const ColsumJob* cs = nullptr) {
   CNHIP_TRY(check_spec(s, who));
-  if (s.M == 0 || s.N == 0 || s.batches == 0) return CNHIP_OK;
-  if (gemm_is_small(s.M, s.N, s.K, s.batches, s.trans_a, s.trans_b))
-    return gemm_small(s.trans_a, s.trans_b, s.M, s.N, s.K, s.alpha, s.A, s.lda, s.B, s.ldb, s.beta, s.C,
-                      s.ldc, s.bias, s.epilogue, s.aux_in, s.aux_out, s.ld_aux, st, who);
+  auto sums = [&]() -> int {
+    return cs ? column_sum(cs->in, cs->out, cs->rows, cs->cols, cs->accumulate, st, who) : CNHIP_OK;
+  };
+  if (s.M == 0 || s.N == 0 || s.batches == 0) return sums();
+  if (gemm_is_small(s.M, s.N, s.K, s.batches, s.trans_a, s.trans_b)) {
+    CNHIP_TRY(gemm_small(s.trans_a, s.trans_b, s.M, s.N, s.K, s.alpha, s.A, s.lda, s.B, s.ldb, s.beta, s.C,
+                         s.ldc, s.bias, s.epilogue, s.aux_in, s.aux_out, s.ld_aux, st, who));
+    return sums();
+  }
 
   const Plan plan = plan_gemm(s.trans_a, s.trans_b, s.M, s.N, s.K, s.batches, 64);
   CNHIP_REQUIRE(plan.tiles < ((int64_t)1 << 30), "%s: GEMM too large", who);
@@ -821,8 +861,9 @@ static int gemm_spec(const GemmSpec& s, hipStream_t st, const char* who) {
     g.partial = static_cast<float*>(ws);
   }
   const int status = launch_plan(plan.shape, s.trans_a, s.trans_b, g, s.batches, st, who);
-  if (plan.splits > 1 && status == CNHIP_OK) return splitk_reduce(g, s.batches, st, who);
-  return status;
+  if (status != CNHIP_OK) return status;
+  if (plan.splits > 1) return splitk_reduce(g, s.batches, st, who, cs);
+  return sums();
 }
 
 int gemm_f32_core(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float alpha,
@@ -844,12 +885,18 @@ int gemm_f32_core(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, flo
 // count is lowered to fit, never raised); otherwise one after the other.
 // Pairs served: x an input gradient (NT, optionally with a fused epilogue)
 // or a TN product, y a TN weight gradient or an NN product.
-int gemm_f32_pair(const GemmSpec& x, const GemmSpec& y, hipStream_t st, const char* who) {
+int gemm_f32_pair(const GemmSpec& x, const GemmSpec& y, hipStream_t st, const char* who, const float* cs_in,
+                  float* cs_out, int64_t cs_rows, int64_t cs_cols, int cs_accumulate) {
   CNHIP_TRY(check_spec(x, who));
   CNHIP_TRY(check_spec(y, who));
+  CNHIP_REQUIRE(!cs_out || (cs_rows >= 0 && cs_cols >= 0 && (cs_rows == 0 || cs_in)), "%s: bad column-sum operands",
+                who);
+  const bool sums = cs_out && cs_cols > 0;
+  const ColsumJob cs{cs_in, cs_out, cs_rows, cs_cols, cs_accumulate,
+                     (cs_rows % 4 == 0) && aligned16(cs_in) ? 1 : 0};
   auto apart = [&]() -> int {
     CNHIP_TRY(gemm_spec(x, st, who));
-    return gemm_spec(y, st, who);
+    return gemm_spec(y, st, who, sums ? &cs : nullptr);
   };
   auto big = [](const GemmSpec& s) {
     return s.M > 0 && s.N > 0 && s.K > 0 && s.batches > 0 &&
@@ -895,8 +942,10 @@ int gemm_f32_pair(const GemmSpec& x, const GemmSpec& y, hipStream_t st, const ch
   int status = check_hip(hipLaunchKernel(kern, dim3((unsigned)(nx + ny)), dim3(C::NT), kargs, 0, st), who);
   if (status == CNHIP_OK) status = check_launch(who);
   if (rec) (void)hipEventRecord(rec->stop, st);
-  if (py.splits > 1 && status == CNHIP_OK) return splitk_reduce(gy, y.batches, st, who);
-  return status;
+  if (status != CNHIP_OK) return status;
+  // the column sums ride in the split reduce's launch when there is one
+  if (py.splits > 1) return splitk_reduce(gy, y.batches, st, who, sums ? &cs : nullptr);
+  return sums ? column_sum(cs_in, cs_out, cs_rows, cs_cols, cs_accumulate, st, who) : CNHIP_OK;
 }
 #undef CNHIP_PAIR_CODE
 

@@ -10,6 +10,7 @@
 #include <cstdlib>
 
 #include "act_math.hpp"
+#include "colsum.hpp"
 #include "common.hpp"
 
 namespace cnhip {
@@ -40,28 +41,7 @@ __global__ void __launch_bounds__(256) column_sum_kernel(const float* __restrict
   const int lane = threadIdx.x & 63;
   const int64_t col = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (col >= cols) return;
-  const float* p = in + rows * col;
-  float s = 0.f;
-  if (vec) {
-    // four float4 loads in flight per lane, four running sums added in order
-    const int64_t n4 = rows >> 2;
-    const f32x4* p4 = reinterpret_cast<const f32x4*>(p);
-    f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = a0, a2 = a0, a3 = a0;
-    int64_t i = lane;
-    for (; i + 192 < n4; i += 256) {
-      a0 += p4[i];
-      a1 += p4[i + 64];
-      a2 += p4[i + 128];
-      a3 += p4[i + 192];
-    }
-    for (; i < n4; i += 64) a0 += p4[i];
-    const f32x4 t = (a0 + a1) + (a2 + a3);
-    s = (t[0] + t[1]) + (t[2] + t[3]);
-  } else {
-    for (int64_t i = lane; i < rows; i += 64) s += p[i];
-  }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+  const float s = column_wave_sum(in + rows * col, rows, vec, lane);
   if (lane == 0) out[col] = accumulate ? out[col] + s : s;
 }
 
@@ -525,8 +505,8 @@ int cnhip_linear_backward(const float* X, const float* W, const float* dY, float
         const cnhip::GemmSpec dgrad{0, 1, batch, in_features, out_features, 1.f, dY, batch, 0, W,
                                     in_features, 0, 0.f, dX, batch, 0, 1, nullptr, CNHIP_EPI_NONE,
                                     nullptr, nullptr, 0};
-        CNHIP_TRY(cnhip::gemm_f32_pair(dgrad, wgrad, st, who));
-        dX = nullptr;
+        CNHIP_TRY(cnhip::gemm_f32_pair(dgrad, wgrad, st, who, dY, grad_b, batch, out_features, accumulate));
+        return CNHIP_OK;
       } else {
         CNHIP_TRY(cnhip::gemm_f32(1, 0, in_features, out_features, batch, 1.f, X, batch, dY, batch, beta,
                                   grad_W, in_features, nullptr, CNHIP_EPI_NONE, st, who));
@@ -596,9 +576,7 @@ int cnhip_linear_backward_act(const float* X, const float* W, const float* dY, f
       const cnhip::GemmSpec wgrad{1, 0, in_features, out_features, batch, 1.f, X, batch, 0, dY, batch, 0,
                                   accumulate ? 1.f : 0.f, grad_W, in_features, 0, 1, nullptr,
                                   CNHIP_EPI_NONE, nullptr, nullptr, 0};
-      CNHIP_TRY(cnhip::gemm_f32_pair(dgrad, wgrad, st, who));
-      if (grad_b) CNHIP_TRY(cnhip::column_sum(dY, grad_b, batch, out_features, accumulate, st, who));
-      return CNHIP_OK;
+      return cnhip::gemm_f32_pair(dgrad, wgrad, st, who, dY, grad_b, batch, out_features, accumulate);
     }
   }
   return cnhip::gemm_f32_act(0, 1, batch, in_features, out_features, dY, batch, W, in_features, dX,
