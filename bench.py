@@ -287,15 +287,21 @@ def phase_stamps(config: int = 4) -> int:
     return 0
 
 
+SMALL_CLASS = {
+    "mlp2_bce_part_kernel": "mlp2_bce_part_kernel (the fused step's forward, loss and backward with per-block "
+                            "gradient sums; the step is launch-latency bound)",
+    "gemm_small_kernel": "gemm_small_thread/wave_kernel (SIMT fp32 GEMMs of <= 2 MFLOP: the "
+                         "step is launch-latency bound)"}
+
+
 def small_roofline(hbm_kernels, step_ms, config):
-    """A step without MFMA launches (config 1: every GEMM is a latency-bound
-    SIMT kernel): the SIMT GEMM class against HBM, its algorithmic bytes over
-    its event-timed launch duration."""
-    k = next((r for r in hbm_kernels if r["kernel"] == "gemm_small_kernel"), None)
+    """A step without MFMA launches (config 1: the fused two-launch step, or
+    with it switched off, latency-bound SIMT GEMMs): the dominant kernel against
+    HBM, its algorithmic bytes over its event-timed launch duration."""
+    k = next((r for name in SMALL_CLASS for r in hbm_kernels if r["kernel"] == name), None)
     if k is None:
         return None
-    return {"bound": "hbm", "kernel": "gemm_small_thread/wave_kernel (SIMT fp32 GEMMs of <= 2 MFLOP: the "
-                                      "step is launch-latency bound)",
+    return {"bound": "hbm", "kernel": SMALL_CLASS[k["kernel"]],
             "achieved": k["achieved_GBs"], "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": k["frac"],
             "traffic": PMC_TRAFFIC_BYTES.get(config), "traffic_unit": "bytes per launch (rocprofv3 PMC, see profiles/)",
             "launches_per_step": k["launches_per_step"], "avg_launch_us": k["avg_us"],
@@ -382,7 +388,7 @@ DEFAULT_KERNEL_CLASS = "gemm_f32_kernel (fp32 MFMA GEMM, all shapes of the step;
 
 
 def measure(config: int, steps: int, warmup: int, graph: bool = False, loader: str | None = None,
-            hbm_detail: bool = True) -> dict:
+            hbm_detail: bool = True, fused: bool = True) -> dict:
     """Times `steps` train steps of one config after `warmup` untimed ones,
     inputs resident in HBM, between HIP events on the session's stream; then
     three more eager steps with per-launch events around the MFMA class and
@@ -398,6 +404,7 @@ def measure(config: int, steps: int, warmup: int, graph: bool = False, loader: s
     B = cfg.batch
     params, X, Y = synth(cfg, np.random.default_rng(2024))
     sess = trainer.Session(cfg)
+    sess.set_fused_step(fused)
     sess.set_params(params)
     sess.set_batch(X, Y)           # resident in HBM from here on
     stream = sess.stream
@@ -522,6 +529,9 @@ def main() -> int:
                     help="replay the step's zero_grad + forward + loss + backward as one captured "
                          "HIP graph (cnt_capture_step), Adam eagerly after it; same results bit for "
                          "bit, measured no faster on MI355X (the cost per kernel is GPU-side)")
+    ap.add_argument("--layer-by-layer", action="store_true",
+                    help="run config 1's step layer by layer (seven launches) instead of the fused "
+                         "two-launch step (cnt_set_fused_step off); other configs have no fused step")
     ap.add_argument("--traffic-calibration", action="store_true",
                     help="only run the known-traffic reference kernel (cnhip_add over 64 Mi floats, "
                          "5 times: 512 MiB read + 256 MiB written per launch) that scales the PMC "
@@ -551,7 +561,8 @@ def main() -> int:
         log("bench.py: no GPU visible")
         return 1
     try:
-        head = measure(args.config, steps, args.warmup, args.graph, args.loader)
+        head = measure(args.config, steps, args.warmup, args.graph, args.loader,
+                       fused=not args.layer_by_layer)
     except RuntimeError as e:
         log(f"bench.py: {e}")
         return 1
@@ -568,7 +579,8 @@ def main() -> int:
             if c == args.config:
                 continue
             try:
-                r = measure(c, EXTRA_STEPS.get(c, 20), 5, args.graph, None, hbm_detail=False)
+                r = measure(c, EXTRA_STEPS.get(c, 20), 5, args.graph, None, hbm_detail=False,
+                            fused=not args.layer_by_layer)
             except RuntimeError as e:
                 log(f"bench.py: {e}")
                 return 1

@@ -124,6 +124,9 @@ SIGNATURES: dict[str, tuple] = {
     "cnhip_softmax_ce_forward": (i32, [vp, vp, vp, vp, i64, i64, i32, vp]),
     "cnhip_softmax_ce_backward": (i32, [vp, vp, vp, i64, i64, i32, vp]),
     "cnhip_adam_step": (i32, [vp, vp, vp, vp, i64, f32, f32, f32, f32, f32, f32, vp]),
+    "cnhip_mlp2_bce_adam_step": (i32, [vp, vp, i64, i64, i64, vp, vp, vp, vp, vp, vp, vp, vp,
+                                       C.POINTER(vp), C.POINTER(vp), C.POINTER(f32), C.POINTER(f32),
+                                       f32, f32, f32, f32, i32, i32, vp, vp]),
     "cnhip_adam_step_multi": (i32, [i32, C.POINTER(vp), C.POINTER(vp), C.POINTER(vp),
                                     C.POINTER(vp), C.POINTER(i64), C.POINTER(f32),
                                     C.POINTER(f32), f32, f32, f32, f32, vp]),

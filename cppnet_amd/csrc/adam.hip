@@ -11,6 +11,7 @@
 #include <hip/hip_runtime.h>
 
 #include "common.hpp"
+#include "optim_math.hpp"
 
 namespace cnhip {
 namespace {
@@ -20,19 +21,6 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int MAX_TENSORS = 64;
 constexpr int ADAM_BLOCK = 256;
 
-struct AdamHyper {
-  float lr, b1, b2, eps;
-};
-
-__device__ __forceinline__ void adam_one(float& w, float g, float& m, float& v, float bc1,
-                                         float bc2, const AdamHyper& h) {
-#pragma clang fp contract(off)
-  m = h.b1 * m + (1.0f - h.b1) * g;
-  v = h.b2 * v + (1.0f - h.b2) * g * g;
-  const float mh = m / bc1;
-  const float vh = v / bc2;
-  w -= h.lr * mh / (sqrtf(vh) + h.eps);
-}
 
 struct AdamTensor {
   float* W;

@@ -107,6 +107,49 @@ namespace CppNet
             pending_.clear();
         }
 
+        void Adam::prepare_external(const std::vector<std::pair<float*, int64_t>>& params,
+                                    std::vector<float*>& m, std::vector<float*>& v, std::vector<float>& bc1,
+                                    std::vector<float>& bc2)
+        {
+            if (!pending_.empty() || group_depth_ != 0)
+                throw std::logic_error("Adam::prepare_external inside an update group");
+            reconcile_withheld();  // before any t advances, as update() does
+            external_.clear();
+            m.clear(); v.clear(); bc1.clear(); bc2.clear();
+            for (const auto& p : params)
+            {
+                auto it = states_.find(p.first);
+                if (it == states_.end())
+                {
+                    State s;
+                    s.m = DeviceTensor::zeros({p.second});
+                    s.v = DeviceTensor::zeros({p.second});
+                    it = states_.emplace(p.first, std::move(s)).first;
+                }
+                State& s = it->second;
+                if (s.m.size() != p.second)
+                    throw std::invalid_argument("Adam::prepare_external: parameter size changed for an existing key");
+                external_.push_back(&s);
+                m.push_back(s.m.data());
+                v.push_back(s.v.data());
+            }
+            // t advances only once every key is known to be valid
+            for (State* s : external_)
+            {
+                ++s->t;
+                bc1.push_back(1.0f - std::pow(beta1_, static_cast<float>(s->t)));
+                bc2.push_back(1.0f - std::pow(beta2_, static_cast<float>(s->t)));
+            }
+        }
+
+        void Adam::commit_external()
+        {
+            Launched l{cnhip_update_seq_last(), external_};
+            launched_.push_back(std::move(l));
+            if (launched_.size() > kLaunchHistory) launched_.pop_front();
+            external_.clear();
+        }
+
         int Adam::step_count(const float* weights) const
         {
             auto it = states_.find(weights);

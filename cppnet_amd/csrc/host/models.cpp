@@ -23,6 +23,16 @@ namespace CppNet
             return steps_.empty() ? nullptr : steps_.back()->activation();
         }
 
+        Layers::Linear* SequentialModel::step_linear(std::size_t i) const
+        {
+            return i < steps_.size() ? steps_[i]->linear() : nullptr;
+        }
+
+        Activations::Activation* SequentialModel::step_activation(std::size_t i) const
+        {
+            return i < steps_.size() ? steps_[i]->activation() : nullptr;
+        }
+
         DeviceTensor SequentialModel::forward_prefix(const DeviceTensor& input, std::size_t count)
         {
             if (count > steps_.size()) throw std::out_of_range("SequentialModel::forward_prefix: too many steps");

@@ -136,6 +136,8 @@ struct cnt_session
     std::unique_ptr<Losses::Loss> loss;
     std::unique_ptr<Optimizers::Optimizer> opt;  // Adam unless cnt_set_optimizer replaced it
     bool updated = false;                        // an optimizer update has run
+    bool fused_steps = true;                     // cnt_set_fused_step
+    bool fused_taken = false;                    // a fused step has run (cnt_capture_step)
     float lr = 1e-3f;
     DeviceTensor X, Y;
     Losses::DeviceScalar last_loss;
@@ -812,6 +814,59 @@ namespace
         s->warm = true;
     }
 
+    // The whole step of Linear(I, H) -> ReLU -> Linear(H, 1) -> Sigmoid with
+    // BinaryCrossEntropy and Adam (config 1's model) in two launches
+    // (cnhip_mlp2_bce_adam_step) instead of seven: at its sizes the host's
+    // issue time per launch exceeded the GPU's work.  Taken while no graph
+    // is captured; false where it does not apply.  The layers' forward caches
+    // are not written (nothing after a full step reads them; the split calls
+    // and a capture run their own forward); the gradients are this step's.
+    bool fused_mlp_step(cnt_session* s)
+    {
+        if (!s->fused_steps || s->encoder || s->graph || s->model.num_steps() != 4) return false;
+        auto* adam = dynamic_cast<Optimizers::Adam*>(s->opt.get());
+        auto* bce = dynamic_cast<Losses::BinaryCrossEntropy*>(s->loss.get());
+        Layers::Linear* l1 = s->model.step_linear(0);
+        Layers::Linear* l2 = s->model.step_linear(2);
+        if (!adam || !bce || !l1 || !l2 || !dynamic_cast<Activations::ReLU*>(s->model.step_activation(1)) ||
+            !dynamic_cast<Activations::Sigmoid*>(s->model.step_activation(3)) || !l1->is_trainable() ||
+            !l2->is_trainable())
+            return false;
+        const int64_t I = l1->get_input_size(), H = l1->get_output_size();
+        if (s->X.dims().size() != 2 || s->X.dimension(1) != I || l2->get_input_size() != H ||
+            l2->get_output_size() != 1 || I > 64 || H > 64)
+            return false;
+        const int64_t B = s->X.dimension(0);
+        if (B % 16 != 0 || B / 16 > 65535 || s->Y.size() != B) return false;
+        DeviceTensor& W1 = l1->weights();
+        DeviceTensor& b1 = l1->biases();
+        DeviceTensor& W2 = l2->weights();
+        DeviceTensor& b2 = l2->biases();
+        DeviceTensor& gW1 = l1->grad_weights();
+        DeviceTensor& gb1 = l1->grad_biases();
+        DeviceTensor& gW2 = l2->grad_weights();
+        DeviceTensor& gb2 = l2->grad_biases();
+        std::vector<float*> m, v;
+        std::vector<float> bc1, bc2;
+        adam->prepare_external({{W1.data(), W1.size()}, {b1.data(), b1.size()}, {W2.data(), W2.size()},
+                                {b2.data(), b2.size()}},
+                               m, v, bc1, bc2);
+        DeviceTensor loss = DeviceTensor::empty({1});
+        Device::check(cnhip_mlp2_bce_adam_step(s->X.data(), s->Y.data(), B, I, H, W1.data(), b1.data(), W2.data(),
+                                               b2.data(), gW1.data(), gb1.data(), gW2.data(), gb2.data(), m.data(),
+                                               v.data(), bc1.data(), bc2.data(), s->lr, adam->beta1(),
+                                               adam->beta2(), adam->epsilon(), bce->forward_reduction(),
+                                               bce->backward_reduction(), loss.data(), s->stream),
+                      "fused MLP step");
+        adam->commit_external();
+        s->fused_taken = true;
+        l1->set_grads_pending_zero(false);
+        l2->set_grads_pending_zero(false);
+        s->last_loss = Losses::DeviceScalar(loss);
+        s->updated = true;
+        return true;
+    }
+
     void update(cnt_session* s)
     {
         if (s->encoder)
@@ -1087,6 +1142,8 @@ int cnt_step(cnt_session* s, float* loss_out)
                 s->last_loss = s->graph_loss;
                 for (auto& f : s->graph_flags) f.first->set_grads_pending_zero(f.second);
             }
+            else if (fused_mlp_step(s))
+                return;
             else
                 eager_forward_backward(s);
             update(s);
@@ -1099,12 +1156,23 @@ int cnt_step(cnt_session* s, float* loss_out)
     });
 }
 
+int cnt_set_fused_step(cnt_session* s, int enable)
+{
+    return guarded("cnt_set_fused_step", [&] {
+        check_session(s);
+        s->fused_steps = enable != 0;
+    });
+}
+
 int cnt_capture_step(cnt_session* s)
 {
     return guarded("cnt_capture_step", [&] {
         check_session(s);
         StreamScope scope(s);
         release_graph(s);
+        // after fused steps only, one eager layer-by-layer forward + backward
+        // (no update) sizes what the graph's kernels refer to
+        if (!s->warm && s->fused_taken) eager_forward_backward(s);
         if (!s->warm)
             throw std::logic_error("run one step eagerly before capturing: it sizes the buffers and "
                                    "workspaces the graph will refer to");

@@ -148,6 +148,9 @@ namespace CppNet
             void backward_params_prefix(const DeviceTensor& grad_output, std::size_t count);
             /// the activation of the last step, or null
             Activations::Activation* last_activation() const;
+            /// step i's Linear layer / activation, or null (i < num_steps())
+            Layers::Linear* step_linear(std::size_t i) const;
+            Activations::Activation* step_activation(std::size_t i) const;
             Tensor<float, 2> forward(const Tensor<float, 2>& input);
             Tensor<float, 2> backward(const Tensor<float, 2>& grad_output);
 

@@ -15,6 +15,7 @@
 #include <deque>
 #include <string>
 #include <unordered_map>
+#include <utility>
 #include <vector>
 
 #include "CppNet/core/tensor.hpp"
@@ -49,6 +50,21 @@ namespace CppNet
                            int t) override;
             void reconcile_withheld() override;
 
+            /// An update of these tensors that a fused train-step launch
+            /// performs itself (cnhip_mlp2_bce_adam_step): the same
+            /// bookkeeping as update() for each key (state created on first
+            /// use, t advanced, bias corrections as adam.cpp:121-122),
+            /// returning each key's moments and bias corrections.  Call
+            /// commit_external() right after that launch, which records it
+            /// for the withheld-update reconciliation as flush() does.
+            void prepare_external(const std::vector<std::pair<float*, int64_t>>& params,
+                                  std::vector<float*>& m, std::vector<float*>& v, std::vector<float>& bc1,
+                                  std::vector<float>& bc2);
+            void commit_external();
+            float beta1() const { return beta1_; }
+            float beta2() const { return beta2_; }
+            float epsilon() const { return epsilon_; }
+
         private:
             struct State
             {
@@ -77,6 +93,7 @@ namespace CppNet
             std::vector<Pending> pending_;
             int group_depth_ = 0;
             std::deque<Launched> launched_;  // the last kLaunchHistory launches
+            std::vector<State*> external_;    // keys of the prepared external update
             int64_t faults_seen_ = 0;
             static constexpr std::size_t kLaunchHistory = 4096;
         };

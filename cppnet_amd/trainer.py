@@ -77,6 +77,7 @@ def load() -> C.CDLL:
         "cnt_update": (i32, [vp]),
         "cnt_synchronize": (i32, [vp]),
         "cnt_stream": (vp, [vp]),
+        "cnt_set_fused_step": (i32, [vp, i32]),
         "cnt_capture_step": (i32, [vp]),
         "cnt_release_graph": (i32, [vp]),
         "cnt_has_graph": (i32, [vp]),
@@ -553,6 +554,11 @@ class Session:
 
     def synchronize(self) -> None:
         _check(load().cnt_synchronize(self.h))
+
+    def set_fused_step(self, enable: bool) -> None:
+        """Whether steps may run the fused two-launch step of the MLP
+        benchmark model (default on; cnt_set_fused_step)."""
+        _check(load().cnt_set_fused_step(self.h, int(enable)))
 
     def capture(self) -> None:
         """Records zero_grad + forward + loss + backward into a HIP graph that

@@ -607,6 +607,28 @@ int cnhip_adam_step_multi(int count, float* const* W, const float* const* g,
                           const float* bc1, const float* bc2, float lr,
                           float beta1, float beta2, float eps,
                           cnhip_stream_t stream);
+/* One whole training step of Linear(I, H) -> ReLU -> Linear(H, 1) ->
+ * Sigmoid with BinaryCrossEntropy and Adam (the reference's MLP benchmark
+ * model, benchmarks/mlp_benchmark.cpp) in two launches: forward, loss,
+ * backward and per-block partial gradient sums (a block per 16 samples),
+ * then the gradients (partials added in block order) stored into gW1, gb1,
+ * gW2, gb2 (overwritten: the step's own gradients), the loss into *loss
+ * (loss_reduction), and Adam applied to W1, b1, W2, b2 in place with moments
+ * m[k], v[k] and bias corrections bc1[k], bc2[k] (k = W1, b1, W2, b2; the
+ * caller's per-key t).  X [B, I] and Y [B, 1] ColMajor, W1 [I, H] ColMajor.
+ * B % 16 == 0, 1 <= I, H <= 64.  Per element the layer-by-layer path's
+ * arithmetic; the batch sums in an order of their own.  The Adam update is
+ * withheld like cnhip_adam_step_multi's after a faulted recurrence.
+ * ref: Linear (linear.cpp:146-358), ReLU (relu.cpp:97-160), Sigmoid
+ * (sigmoid.cpp:97-231), BinaryCrossEntropy (binary_cross_entropy.cpp:143-225),
+ * Adam::update (adam.cpp:98-133) */
+int cnhip_mlp2_bce_adam_step(const float* X, const float* Y, int64_t B, int64_t I, int64_t H,
+                             float* W1, float* b1, float* W2, float* b2,
+                             float* gW1, float* gb1, float* gW2, float* gb2,
+                             float* const* m, float* const* v, const float* bc1, const float* bc2,
+                             float lr, float beta1, float beta2, float eps,
+                             int loss_reduction, int grad_reduction, float* loss,
+                             cnhip_stream_t stream);
 /* SGD, Momentum, Adagrad, RMSProp over up to 64 tensors in ONE launch;
  * tensor i is (W[i], g[i], state[i], n[i]), state[i] the per-key velocity,
  * squared-gradient accumulator or mean square (ignored for SGD, may be NULL).

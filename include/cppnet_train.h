@@ -140,12 +140,25 @@ int cnt_step(cnt_session* s, float* loss_out);
  * gradients inside step() (conv2d.cpp:211-212), so read grads in between. */
 int cnt_forward_backward(cnt_session* s, float* loss_out);
 int cnt_update(cnt_session* s);
+/* Fused steps (on by default): cnt_step on a session of Linear(I, H) ->
+ * ReLU -> Linear(H, 1) -> Sigmoid with BinaryCrossEntropy and Adam (the
+ * reference's MLP benchmark model; I, H <= 64, batch % 16 == 0) runs each
+ * step as two launches (cnhip_mlp2_bce_adam_step) instead of seven
+ * layer-by-layer ones (a capture after fused steps first runs one
+ * layer-by-layer forward + backward, without an update, to size its
+ * buffers).  Per element the same arithmetic; the sums
+ * over the batch are ordered per 16-sample block, so its gradients differ
+ * from the layer-by-layer step's in the last bits.  enable = 0 keeps every
+ * step layer by layer (for bitwise comparisons with a captured graph, which
+ * always replays the layer-by-layer kernels).  No counterpart in the
+ * reference. */
+int cnt_set_fused_step(cnt_session* s, int enable);
 /* Whole-step graph.  cnt_capture_step records the session's zero_grad +
  * forward + loss + backward into a HIP graph (include/cnhip.h, graphs);
  * from then on cnt_step replays it with one graph launch and then runs the
  * Adam update eagerly (its bias corrections 1 - beta^t change every step and
  * are computed on the host exactly as the eager path does), so a replayed
- * step computes what an eager step computes, bit for bit.  Needs one eager
+ * step computes what an eager layer-by-layer step computes, bit for bit.  Needs one eager
  * step (cnt_step or cnt_forward_backward) at the session's shapes first.
  * The graph reads the batch buffers in place, so cnt_set_batch* between
  * replays trains on the new batch.  cnt_forward_backward runs eagerly and

@@ -51,6 +51,9 @@ def test_graph_replay_matches_eager(gpu, name):
     params, X1, Y1 = synth(cfg, rng)
     _, X2, Y2 = synth(cfg, rng)  # a second batch, uploaded between replays
     eager, graph = trainer.Session(cfg), trainer.Session(cfg)
+    # a replay is the layer-by-layer step: compare layer-by-layer steps
+    for s in (eager, graph):
+        s.set_fused_step(False)
     try:
         for s in (eager, graph):
             s.set_params(params)
@@ -83,6 +86,7 @@ def test_capture_needs_an_eager_step_and_split_calls_drop_the_graph(gpu):
     ref = trainer.Session(cfg)
     try:
         for t in (s, ref):
+            t.set_fused_step(False)  # bitwise comparisons with the layer-by-layer replays
             t.set_params(params)
             t.set_batch(X, Y)
         with pytest.raises(trainer._capi.CnhipError, match="eagerly before capturing"):
