@@ -54,11 +54,14 @@ __device__ __forceinline__ float sigmoid_clamped(float x) {
 }
 __device__ __forceinline__ float bce_clip_p(float p) { return fmaxf(1e-7f, fminf(p, 1.0f - 1e-7f)); }
 
-// LDS row strides: XS keeps float4 reads of a sample's inputs aligned while
-// the transposing store of X spreads its 16 samples over distinct banks; AS
-// (odd) spreads the head's per-sample reads of a row of hidden outputs; the
-// staged W1 columns get an odd stride for the same reason (ld_w1).
-constexpr int kXS = kMlpMaxIn + 4, kAS = kMlpMaxHid + 1, kDS = kMlpMaxHid;
+// LDS row strides: XS and AS (4 more than a row) keep float4 reads of a row
+// aligned while the 16 rows start on distinct banks, for the transposing
+// store of X and the head's per-sample reads of hidden outputs; a staged W1
+// column gets an odd stride (ld_w1) so that a wave's 64 columns read on
+// distinct banks.  Rows and columns are zero-padded to a multiple of 4 (I4,
+// H4) so the k loops step by float4: the padded terms add +0 at the end of
+// an fma chain.
+constexpr int kXS = kMlpMaxIn + 4, kAS = kMlpMaxHid + 4, kDS = kMlpMaxHid;
 // the thread mappings below: 4 waves x 4 samples in the forward, a lane per
 // hidden unit, 16 x 16 tiles of 4 x 4 for the weight gradient
 static_assert(kMlpRows == 16 && kMlpMaxIn == 64 && kMlpMaxHid == 64, "mlp2_bce_part_kernel's thread mappings");
@@ -67,11 +70,13 @@ __global__ void __launch_bounds__(256) mlp2_bce_part_kernel(Mlp2Args a) {
   constexpr int R = kMlpRows;
   __shared__ __align__(16) float xs[R * kXS];            // x[r][i] at r XS + i
   __shared__ float w1s[(kMlpMaxIn + 1) * kMlpMaxHid];    // W1[i][j] at i + ld_w1 j
-  __shared__ float a1s[R * kAS];                         // ReLU outputs a[r][j] at r AS + j
+  __shared__ __align__(16) float a1s[R * kAS];           // ReLU outputs a[r][j] at r AS + j
   __shared__ __align__(16) float da1s[R * kDS];          // dA1[r][j] at r DS + j
-  __shared__ float b1s[kMlpMaxHid], w2s[kMlpMaxHid];
+  __shared__ float b1s[kMlpMaxHid];
+  __shared__ __align__(16) float w2s[kMlpMaxHid];
   __shared__ float dzs[R], ls[R];
-  const int I = a.I, H = a.H, IH = I * H, t = threadIdx.x, ld_w1 = I | 1;
+  const int I = a.I, H = a.H, IH = I * H, t = threadIdx.x;
+  const int I4 = (I + 3) & ~3, H4 = (H + 3) & ~3, ld_w1 = I4 + 1;
   const int64_t r0 = (int64_t)blockIdx.x * R;
   // every global load of the block issued before the first wait
   constexpr int kW = kMlpMaxIn * kMlpMaxHid / 256, kX = R * kMlpMaxIn / 256;
@@ -106,33 +111,58 @@ __global__ void __launch_bounds__(256) mlp2_bce_part_kernel(Mlp2Args a) {
     const int e = t + 256 * k;
     if (e < R * I) xs[(e & (R - 1)) * kXS + e / R] = xv[k];
   }
-  if (t < H) {
-    b1s[t] = bv;
-    w2s[t] = w2v;
+  // the zero padding: inputs I .. I4-1 of every sample and W1 rows I .. I4-1
+  // of every column; units H .. H4-1 of b1 and W2 (and of a1, written below)
+  if (t < 3 * R) {
+    const int r = t / 3, i = I + t % 3;
+    if (i < I4) xs[r * kXS + i] = 0.f;
+  }
+  if (t < 3 * kMlpMaxHid) {
+    const int j = t / 3, i = I + t % 3;
+    if (i < I4 && j < H4) w1s[i + ld_w1 * j] = 0.f;
+  }
+  if (t < H4) {
+    b1s[t] = t < H ? bv : 0.f;
+    w2s[t] = t < H ? w2v : 0.f;
   }
   __syncthreads();
   // hidden layer, a wave per 4 samples and a lane per unit:
   // z = (sum_i x_i W1[i, j] as an fma chain in i order) + b1[j], a = relu(z)
   {
     const int j = t & 63, rb = (t >> 6) * 4;
-    if (j < H) {
+    if (j < H4) {
       float acc[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 8
-      for (int i = 0; i < I; ++i) {
-        const float w = w1s[i + ld_w1 * j];
+#pragma unroll 4
+      for (int i0 = 0; i0 < I4; i0 += 4) {
+        float w[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) acc[u] = fmaf(xs[(rb + u) * kXS + i], w, acc[u]);
+        for (int q = 0; q < 4; ++q) w[q] = w1s[i0 + q + ld_w1 * j];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const float4 x4 = *reinterpret_cast<const float4*>(&xs[(rb + u) * kXS + i0]);
+          acc[u] = fmaf(x4.x, w[0], acc[u]);
+          acc[u] = fmaf(x4.y, w[1], acc[u]);
+          acc[u] = fmaf(x4.z, w[2], acc[u]);
+          acc[u] = fmaf(x4.w, w[3], acc[u]);
+        }
       }
 #pragma unroll
-      for (int u = 0; u < 4; ++u) a1s[(rb + u) * kAS + j] = relu_f(acc[u] + b1s[j]);
+      for (int u = 0; u < 4; ++u) a1s[(rb + u) * kAS + j] = j < H ? relu_f(acc[u] + b1s[j]) : 0.f;
     }
   }
   __syncthreads();
   // output, loss term and dz of each sample (the sigmoid + BCE head's arithmetic)
   if (t < R) {
     float acc = 0.f;
-#pragma unroll 8
-    for (int j = 0; j < H; ++j) acc = fmaf(a1s[t * kAS + j], w2s[j], acc);
+#pragma unroll 4
+    for (int j0 = 0; j0 < H4; j0 += 4) {
+      const float4 h4 = *reinterpret_cast<const float4*>(&a1s[t * kAS + j0]);
+      const float4 w4 = *reinterpret_cast<const float4*>(&w2s[j0]);
+      acc = fmaf(h4.x, w4.x, acc);
+      acc = fmaf(h4.y, w4.y, acc);
+      acc = fmaf(h4.z, w4.z, acc);
+      acc = fmaf(h4.w, w4.w, acc);
+    }
     const float p = sigmoid_clamped(acc + b2);
     const float pc = bce_clip_p(p);
     ls[t] = -(yv * logf(pc) + (1.0f - yv) * logf(1.0f - pc));
@@ -156,7 +186,7 @@ __global__ void __launch_bounds__(256) mlp2_bce_part_kernel(Mlp2Args a) {
     const int i0 = (t & 15) * 4, j0 = (t >> 4) * 4;
     if (i0 < I && j0 < H) {
       float acc[4][4] = {};
-#pragma unroll 4
+#pragma unroll 8
       for (int r = 0; r < R; ++r) {
         const float4 x4 = *reinterpret_cast<const float4*>(&xs[r * kXS + i0]);
         const float4 d4 = *reinterpret_cast<const float4*>(&da1s[r * kDS + j0]);
