@@ -124,7 +124,7 @@ CPU_BATCH = {1: 512, 2: 512, 3: 32, 4: 16, 5: 4}
 # reference kernel of known traffic (bench.py --traffic-calibration),
 # averaged over the class's launches of a step; the runs, the factors and the
 # per-kernel tables are in profiles/*_counters.md.
-PMC_TRAFFIC_BYTES = {1: 0.6e6, 2: 374.9e6, 3: 39.3e6, 4: 955.4e6, 5: 170.5e6}
+PMC_TRAFFIC_BYTES = {1: 0.6e6, 2: 374.4e6, 3: 39.3e6, 4: 955.2e6, 5: 170.2e6}
 
 
 def _cpu_model() -> str:
