@@ -69,6 +69,30 @@ def _check_step(sess, ref, cfg, oracle, p0, X, Y, t_before):
             f"Adam m of param {k}"
 
 
+def _two_fused_steps(cfg, oracle, params, X1, Y1, X2, Y2):
+    """Step 1 against the oracle from the same weights, then step 2 against
+    the oracle re-anchored at the session's parameters and Adam state."""
+    sess = trainer.Session(cfg)
+    try:
+        sess.set_params(params)
+        ref = OracleMLP(cfg, oracle)
+        ref.set_params(params)
+        sess.set_batch(X1, Y1)
+        _check_step(sess, ref, cfg, oracle, params, X1, Y1, [0, 0, 0, 0])
+        p1 = sess.get_params()
+        m, t = sess.get_opt_state(0)
+        v, _ = sess.get_opt_state(1)
+        ref = OracleMLP(cfg, oracle)
+        ref.set_params(p1)
+        for dst, src in zip(ref.opt.m + ref.opt.v, list(m) + list(v)):
+            np.copyto(dst, src)
+        ref.opt.t = list(t)
+        sess.set_batch(X2, Y2)
+        _check_step(sess, ref, cfg, oracle, p1, X2, Y2, t)
+    finally:
+        sess.close()
+
+
 @pytest.mark.parametrize("batch", [None, 64])
 def test_fused_mlp_step_vs_oracle(gpu, oracle_mt, batch):
     cfg = trainer.mlp_config(1, batch)
@@ -76,24 +100,40 @@ def test_fused_mlp_step_vs_oracle(gpu, oracle_mt, batch):
     rng = np.random.default_rng(31)
     params, X1, Y1 = trainer.synthetic_mlp(cfg, rng)
     _, X2, Y2 = trainer.synthetic_mlp(cfg, rng)
+    _two_fused_steps(cfg, oracle_mt, params, X1, Y1, X2, Y2)
+
+
+# layer sizes that are not multiples of 4 (the kernel's zero padding of rows
+# and columns), the largest sizes, one input, and batches of 1, 3 and 5 blocks
+@pytest.mark.parametrize("I,H,B", [(7, 50, 48), (64, 64, 32), (1, 3, 16), (33, 17, 80)])
+def test_fused_mlp_step_odd_sizes(gpu, oracle_mt, I, H, B):
+    cfg = trainer.MLPConfig(f"MLP {I}-{H}-1 sigmoid BCE", [I, H, 1], "relu", "sigmoid", "bce", B)
+    print(f"[mlp-step] {I}-{H}-1 batch {B}: two fused steps", flush=True)
+    rng = np.random.default_rng(1000 * I + H)
+    params, X1, Y1 = trainer.synthetic_mlp(cfg, rng)
+    # biases away from 0 from the first step on
+    params[1] = (0.1 * rng.standard_normal(H)).astype(np.float32)
+    params[3] = (0.1 * rng.standard_normal(1)).astype(np.float32)
+    _, X2, Y2 = trainer.synthetic_mlp(cfg, rng)
+    _two_fused_steps(cfg, oracle_mt, params, X1, Y1, X2, Y2)
+
+
+# models the fused step does not take: a layer wider than 64, or a batch that
+# is not a multiple of 16, run layer by layer
+@pytest.mark.parametrize("I,H,B", [(30, 65, 64), (65, 8, 64), (30, 64, 40)])
+def test_unfused_shapes_run_layer_by_layer(gpu, I, H, B):
+    cfg = trainer.MLPConfig(f"MLP {I}-{H}-1 sigmoid BCE", [I, H, 1], "relu", "sigmoid", "bce", B)
+    params, X, Y = trainer.synthetic_mlp(cfg, np.random.default_rng(9))
     sess = trainer.Session(cfg)
-    sess.set_params(params)
-    ref = OracleMLP(cfg, oracle_mt)
-    ref.set_params(params)
-    sess.set_batch(X1, Y1)
-    _check_step(sess, ref, cfg, oracle_mt, params, X1, Y1, [0, 0, 0, 0])
-    # step 2 re-anchored: the oracle at the session's parameters and Adam state
-    p1 = sess.get_params()
-    m, t = sess.get_opt_state(0)
-    v, _ = sess.get_opt_state(1)
-    ref = OracleMLP(cfg, oracle_mt)
-    ref.set_params(p1)
-    for dst, src in zip(ref.opt.m + ref.opt.v, list(m) + list(v)):
-        np.copyto(dst, src)
-    ref.opt.t = list(t)
-    sess.set_batch(X2, Y2)
-    _check_step(sess, ref, cfg, oracle_mt, p1, X2, Y2, t)
-    sess.close()
+    try:
+        sess.set_params(params)
+        sess.set_batch(X, Y)
+        box = []
+        ran = _kernels_run(lambda: box.append(sess.step()))
+        assert "mlp2_bce_part_kernel" not in ran and "mlp2_bce_adam_kernel" not in ran, sorted(ran)
+        assert np.isfinite(box[0])
+    finally:
+        sess.close()
 
 
 def test_capture_after_fused_steps(gpu):
