@@ -150,6 +150,12 @@ namespace CppNet
             external_.clear();
         }
 
+        void Adam::abort_external()
+        {
+            for (State* s : external_) --s->t;
+            external_.clear();
+        }
+
         int Adam::step_count(const float* weights) const
         {
             auto it = states_.find(weights);

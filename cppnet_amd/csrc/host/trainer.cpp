@@ -851,13 +851,27 @@ namespace
         adam->prepare_external({{W1.data(), W1.size()}, {b1.data(), b1.size()}, {W2.data(), W2.size()},
                                 {b2.data(), b2.size()}},
                                m, v, bc1, bc2);
-        DeviceTensor loss = DeviceTensor::empty({1});
-        Device::check(cnhip_mlp2_bce_adam_step(s->X.data(), s->Y.data(), B, I, H, W1.data(), b1.data(), W2.data(),
-                                               b2.data(), gW1.data(), gb1.data(), gW2.data(), gb2.data(), m.data(),
-                                               v.data(), bc1.data(), bc2.data(), s->lr, adam->beta1(),
-                                               adam->beta2(), adam->epsilon(), bce->forward_reduction(),
-                                               bce->backward_reduction(), loss.data(), s->stream),
-                      "fused MLP step");
+        DeviceTensor loss;
+        int st = CNHIP_OK;
+        try
+        {
+            loss = DeviceTensor::empty({1});
+            st = cnhip_mlp2_bce_adam_step(s->X.data(), s->Y.data(), B, I, H, W1.data(), b1.data(), W2.data(),
+                                          b2.data(), gW1.data(), gb1.data(), gW2.data(), gb2.data(), m.data(),
+                                          v.data(), bc1.data(), bc2.data(), s->lr, adam->beta1(), adam->beta2(),
+                                          adam->epsilon(), bce->forward_reduction(), bce->backward_reduction(),
+                                          loss.data(), s->stream);
+        }
+        catch (...)
+        {
+            adam->abort_external();
+            throw;
+        }
+        if (st != CNHIP_OK)
+        {
+            adam->abort_external();  // nothing was updated: the step counts go back
+            Device::check(st, "fused MLP step");
+        }
         adam->commit_external();
         s->fused_taken = true;
         l1->set_grads_pending_zero(false);

@@ -56,11 +56,14 @@ namespace CppNet
             /// use, t advanced, bias corrections as adam.cpp:121-122),
             /// returning each key's moments and bias corrections.  Call
             /// commit_external() right after that launch, which records it
-            /// for the withheld-update reconciliation as flush() does.
+            /// for the withheld-update reconciliation as flush() does, or
+            /// abort_external() when the launch was refused, which takes the
+            /// step counts back.
             void prepare_external(const std::vector<std::pair<float*, int64_t>>& params,
                                   std::vector<float*>& m, std::vector<float*>& v, std::vector<float>& bc1,
                                   std::vector<float>& bc2);
             void commit_external();
+            void abort_external();
             float beta1() const { return beta1_; }
             float beta2() const { return beta2_; }
             float epsilon() const { return epsilon_; }
