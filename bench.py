@@ -118,6 +118,11 @@ def workload(config: int, batch: int | None = None):
 
 
 CPU_BATCH = {1: 512, 2: 512, 3: 32, 4: 16, 5: 4}
+# Batch of the reference's "cpu" device leg (Linear as OpenMP loops over the
+# outputs, linear.cpp:196-330) for the MLP configs: those loops walk the
+# ColMajor inputs with a stride of the batch, ~40x slower than the contraction
+# at C2's widths, so C2's leg runs 64 samples a step.
+CPU_LOOPS_BATCH = {1: 512, 2: 64}
 
 # HBM bytes per launch of each config's dominant kernel class, from the two
 # rocprofv3 PMC runs (FETCH_SIZE, WRITE_SIZE) of that config scaled by a
@@ -189,12 +194,22 @@ def cpu_baseline(config: int, seconds_budget: float = 20.0):
     share = _cpu_share()
     batch = CPU_BATCH[config]
     max_steps = 20000 if config == 1 else 50
-    legs = [_time_oracle(o, config, batch, share, seconds_budget / 2, max_steps)]
+    eigen = lambda **kw: dict(device="cpu-eigen", **kw)
+    legs = [eigen(**_time_oracle(o, config, batch, share, seconds_budget / 2, max_steps))]
     if share != 4:
-        legs.append(_time_oracle(o, config, batch, 4, seconds_budget / 2, max_steps))
+        legs.append(eigen(**_time_oracle(o, config, batch, 4, seconds_budget / 2, max_steps)))
     full = workload(config)[0].batch
     if config == 2:
-        legs.append(_time_oracle(o, config, full, share, 0.0, 1))
+        legs.append(eigen(**_time_oracle(o, config, full, share, 0.0, 1)))
+    if config in CPU_LOOPS_BATCH:
+        # the reference's "cpu" device: the same step with Linear as its OpenMP loops
+        o.cnref_set_cpu_loops(1)
+        try:
+            for threads in dict.fromkeys((share, 4)):
+                legs.append(dict(device="cpu", **_time_oracle(o, config, CPU_LOOPS_BATCH[config], threads,
+                                                              seconds_budget / 4, max_steps)))
+        finally:
+            o.cnref_set_cpu_loops(0)
     main = legs[0]
     return {"value": main["samples_per_s"], "unit": "samples/s", "cores": share,
             "kind": "port", "cpu_model": _cpu_model(),
@@ -202,7 +217,10 @@ def cpu_baseline(config: int, seconds_budget: float = 20.0):
             "sample": (f"reference-semantics restatement (oracle/, plain C++ of the cpu-eigen "
                        f"semantics, OpenMP): {main['steps']} train steps of config {config} at batch "
                        f"{batch} (of {full}) on {share} threads in {main['seconds']} s; legs also "
-                       f"time 4 threads" + (" and one full-batch step" if config == 2 else ""))}
+                       f"time 4 threads" + (" and one full-batch step" if config == 2 else "") +
+                       (f", and the reference's \"cpu\" device (Linear as OpenMP loops over the outputs) "
+                        f"at batch {CPU_LOOPS_BATCH[config]} on {share} and 4 threads"
+                        if config in CPU_LOOPS_BATCH else ""))}
 
 
 def traffic_calibration() -> int:

@@ -20,6 +20,8 @@ _SIGS = {
     "cnref_get_threads": (i32, []),
     "cnref_set_accumulate_double": (None, [i32]),
     "cnref_set_sum_order": (None, [i32]),
+    "cnref_set_cpu_loops": (None, [i32]),
+    "cnref_get_cpu_loops": (i32, []),
     "cnref_set_trace": (None, [i32, _f]),
     "cnref_trace": (_f, [i32]),
     "cnref_gemm_f32": (None, [i32, i32, i64, i64, i64, f32, _f, i64, _f, i64, f32, _f, i64, _f,

@@ -23,6 +23,7 @@ namespace {
 int g_threads = 1;
 int& g_acc_double = cnref_detail::acc_double;
 int g_order = 0;
+int g_cpu_loops = 0;
 
 // dst[r + R c] = trans ? src[c + ld r] : src[r + ld c], in 64 x 64 tiles.
 void copy_tiles(float* dst, int64_t R, int64_t Cn, const float* src, int64_t ld, bool trans) {
@@ -230,6 +231,8 @@ void cnref_set_threads(int n) { g_threads = n < 1 ? 1 : n; }
 int cnref_get_threads(void) { return g_threads; }
 void cnref_set_accumulate_double(int on) { g_acc_double = on != 0; }
 void cnref_set_sum_order(int order) { g_order = order >= 0 && order <= 3 ? order : 0; }
+void cnref_set_cpu_loops(int on) { g_cpu_loops = on != 0; }
+int cnref_get_cpu_loops(void) { return g_cpu_loops; }
 
 // ---------------------------------------------------------------------------
 // GEMM.  op(A) is first materialised M-contiguous and op(B) K-contiguous;
@@ -284,6 +287,24 @@ void cnref_gemm_f32(int ta, int tb, int64_t M, int64_t N, int64_t K, float alpha
 // + bias broadcast along the batch.
 void cnref_linear_forward(const float* X, const float* W, const float* b, float* Y, int64_t B,
                           int64_t I, int64_t O) {
+  if (g_cpu_loops) {
+    // Linear::forward_cpu (linear.cpp:196-215): one task per (sample, output),
+    // the sum over the inputs; then the bias in a second pass
+#pragma omp parallel for num_threads(g_threads) schedule(static) collapse(2)
+    for (int64_t n = 0; n < B; ++n)
+      for (int64_t j = 0; j < O; ++j) {
+        float s = 0.f;
+#pragma omp simd reduction(+ : s)
+        for (int64_t i = 0; i < I; ++i) s += X[n + B * i] * W[i + I * j];
+        Y[n + B * j] = s;
+      }
+    if (b) {
+#pragma omp parallel for num_threads(g_threads) schedule(static) collapse(2)
+      for (int64_t n = 0; n < B; ++n)
+        for (int64_t j = 0; j < O; ++j) Y[n + B * j] += b[j];
+    }
+    return;
+  }
   cnref_gemm_f32(0, 0, B, O, I, 1.f, X, B, W, I, 0.f, Y, B, b, 0);
 }
 
@@ -305,6 +326,41 @@ void cnref_column_sum(const float* in, float* out, int64_t rows, int64_t cols, i
 void cnref_linear_backward(const float* X, const float* W, const float* dY, float* gW, float* gb,
                            float* dX, int64_t B, int64_t I, int64_t O, int trainable,
                            int accumulate) {
+  if (g_cpu_loops) {
+    // Linear::backward_cpu (linear.cpp:289-330): one task per weight (sum
+    // over the batch), per bias (the same), per input-gradient element (sum
+    // over the outputs)
+    if (trainable) {
+#pragma omp parallel for num_threads(g_threads) schedule(static) collapse(2)
+      for (int64_t i = 0; i < I; ++i)
+        for (int64_t j = 0; j < O; ++j) {
+          float s = 0.f;
+#pragma omp simd reduction(+ : s)
+          for (int64_t n = 0; n < B; ++n) s += X[n + B * i] * dY[n + B * j];
+          gW[i + I * j] = accumulate ? gW[i + I * j] + s : s;
+        }
+      if (gb) {
+#pragma omp parallel for num_threads(g_threads) schedule(static)
+        for (int64_t j = 0; j < O; ++j) {
+          float s = 0.f;
+#pragma omp simd reduction(+ : s)
+          for (int64_t n = 0; n < B; ++n) s += dY[n + B * j];
+          gb[j] = accumulate ? gb[j] + s : s;
+        }
+      }
+    }
+    if (dX) {
+#pragma omp parallel for num_threads(g_threads) schedule(static) collapse(2)
+      for (int64_t n = 0; n < B; ++n)
+        for (int64_t i = 0; i < I; ++i) {
+          float s = 0.f;
+#pragma omp simd reduction(+ : s)
+          for (int64_t j = 0; j < O; ++j) s += dY[n + B * j] * W[i + I * j];
+          dX[n + B * i] = s;
+        }
+    }
+    return;
+  }
   if (trainable) {
     cnref_gemm_f32(1, 0, I, O, B, 1.f, X, B, dY, B, accumulate ? 1.f : 0.f, gW, I, nullptr, 0);
     if (gb) cnref_column_sum(dY, gb, B, O, accumulate);

@@ -33,6 +33,13 @@ void cnref_set_accumulate_double(int on);
  * used, like the double accumulation, to measure how far a trajectory
  * moves under rounding alone. */
 void cnref_set_sum_order(int order);
+/* 1: Linear forward and backward run as the reference's "cpu" device does
+ * them (linear.cpp:196-215 forward_cpu, 289-330 backward_cpu: OpenMP over
+ * the outputs, each output an fp32 sum over its contraction that the
+ * compiler may vectorise), instead of the cpu-eigen contraction restated by
+ * default.  Used to time the reference's "cpu" leg beside cpu-eigen. */
+void cnref_set_cpu_loops(int on);
+int  cnref_get_cpu_loops(void);
 
 /* Optional diagnostic outputs for the tests' error bars (NULL = off).  While
  * a slot holds a buffer, the functions below also write:

@@ -21,6 +21,16 @@ from oracle_lib import close, colmajor, fp, from_colmajor
 GOLD = json.loads((Path(__file__).parent / "golden" / "known_answers.json").read_text())["cases"]
 
 
+@pytest.fixture(params=[0, 1], ids=["eigen", "cpu_loops"])
+def linear_mode(oracle, request):
+    """The oracle's Linear as the cpu-eigen contraction (default) or as the
+    reference's "cpu" device loops (cnref_set_cpu_loops, used for timing the
+    reference's "cpu" leg): both are held to the same checks."""
+    oracle.cnref_set_cpu_loops(request.param)
+    yield request.param
+    oracle.cnref_set_cpu_loops(0)
+
+
 def _cases(op):
     return [c for c in GOLD if c["op"] == op]
 
@@ -32,7 +42,7 @@ def _shape(rows):
 
 # ---------------------------------------------------------------- known answers
 @pytest.mark.parametrize("case", _cases("linear_forward"), ids=lambda c: c["source"])
-def test_known_linear_forward(oracle, case):
+def test_known_linear_forward(oracle, case, linear_mode):
     B, I = _shape(case["X"])
     O = np.asarray(case["W"]).shape[1]
     X, W = colmajor(case["X"]), colmajor(case["W"])
@@ -182,7 +192,7 @@ def _t64(a):
 
 
 @pytest.mark.parametrize("B,I,O", [(4, 3, 5), (64, 30, 17), (7, 1, 1)])
-def test_linear_backward_vs_autograd(oracle, B, I, O):
+def test_linear_backward_vs_autograd(oracle, B, I, O, linear_mode):
     rng = np.random.default_rng(B + I + O)
     Xl = rng.standard_normal((B, I)).astype(np.float32)
     Wl = rng.standard_normal((I, O)).astype(np.float32)
@@ -208,7 +218,7 @@ def test_linear_backward_vs_autograd(oracle, B, I, O):
         assert ok, f"{name}: {msg}"
 
 
-def test_linear_not_trainable_skips_param_grads(oracle):
+def test_linear_not_trainable_skips_param_grads(oracle, linear_mode):
     B, I, O = 3, 2, 4
     X = np.ones(B * I, np.float32)
     W = np.ones(I * O, np.float32)
@@ -219,6 +229,31 @@ def test_linear_not_trainable_skips_param_grads(oracle):
     oracle.cnref_linear_backward(fp(X), fp(W), fp(dY), fp(gW), fp(gb), fp(dX), B, I, O, 0, 1)
     assert np.all(gW == 7.0) and np.all(gb == 7.0)
     assert np.all(dX == O)  # dX is computed even when frozen (linear.cpp:357)
+
+
+def test_mlp_step_cpu_loops_matches_eigen(oracle):
+    """A whole MLP train step (forward, softmax-CE, backward, Adam) with the
+    Linear layers as the "cpu" device loops agrees with the cpu-eigen step to
+    fp32 rounding: the loops change only the order of the fp32 sums."""
+    from cppnet_amd import trainer
+    from oracle.mlp import OracleMLP
+    cfg = trainer.MLPConfig("MLP 33-70-48-10 softmax-CE", [33, 70, 48, 10], "relu", "none", "softmax_ce", 96)
+    params, X, Y = trainer.synthetic_mlp(cfg, np.random.default_rng(4))
+    runs = []
+    for loops in (0, 1):
+        oracle.cnref_set_cpu_loops(loops)
+        try:
+            ref = OracleMLP(cfg, oracle)
+            ref.set_params(params)
+            losses = [ref.step(X, Y) for _ in range(2)]
+            runs.append((losses, ref.get_params()))
+        finally:
+            oracle.cnref_set_cpu_loops(0)
+    (l0, p0), (l1, p1) = runs
+    assert np.allclose(l0, l1, rtol=1e-5, atol=0), (l0, l1)
+    for k, (a, b) in enumerate(zip(p0, p1)):
+        ok, msg = close(b, a, rtol=1e-4, atol=1e-6)
+        assert ok, f"parameter {k}: {msg}"
 
 
 @pytest.mark.parametrize("name", ["relu", "sigmoid", "tanh"])
