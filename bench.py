@@ -198,6 +198,10 @@ def cpu_baseline(config: int, seconds_budget: float = 20.0):
     legs = [eigen(**_time_oracle(o, config, batch, share, seconds_budget / 2, max_steps))]
     if share != 4:
         legs.append(eigen(**_time_oracle(o, config, batch, 4, seconds_budget / 2, max_steps)))
+    # one thread: the reference's cpu-eigen contractions run on the calling
+    # thread (no Eigen ThreadPoolDevice) and its Conv2D backward is a serial
+    # loop, so this leg is the closer figure for that device
+    legs.append(eigen(**_time_oracle(o, config, batch, 1, seconds_budget / 4, max_steps)))
     full = workload(config)[0].batch
     if config == 2:
         legs.append(eigen(**_time_oracle(o, config, full, share, 0.0, 1)))
@@ -217,7 +221,7 @@ def cpu_baseline(config: int, seconds_budget: float = 20.0):
             "sample": (f"reference-semantics restatement (oracle/, plain C++ of the cpu-eigen "
                        f"semantics, OpenMP): {main['steps']} train steps of config {config} at batch "
                        f"{batch} (of {full}) on {share} threads in {main['seconds']} s; legs also "
-                       f"time 4 threads" + (" and one full-batch step" if config == 2 else "") +
+                       f"time 4 threads, 1 thread" + (" and one full-batch step" if config == 2 else "") +
                        (f", and the reference's \"cpu\" device (Linear as OpenMP loops over the outputs) "
                         f"at batch {CPU_LOOPS_BATCH[config]} on {share} and 4 threads"
                         if config in CPU_LOOPS_BATCH else ""))}
