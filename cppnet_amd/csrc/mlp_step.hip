@@ -1,5 +1,6 @@
 // One training step of a two-layer perceptron with a sigmoid output, binary
-// cross-entropy and Adam in two launches: config 1's model,
+// cross-entropy and Adam in two launches: the reference's quick-start binary
+// classifier (README.md:102-125),
 //   Linear(I, H) -> ReLU -> Linear(H, 1) -> Sigmoid, BCE, Adam  (B 512, I 30, H 64).
 // Its layer-by-layer step is seven launches of a few microseconds of work
 // each (two forward GEMMs, the fused sigmoid + BCE head, the input-gradient

@@ -608,8 +608,8 @@ int cnhip_adam_step_multi(int count, float* const* W, const float* const* g,
                           float beta1, float beta2, float eps,
                           cnhip_stream_t stream);
 /* One whole training step of Linear(I, H) -> ReLU -> Linear(H, 1) ->
- * Sigmoid with BinaryCrossEntropy and Adam (the reference's MLP benchmark
- * model, benchmarks/mlp_benchmark.cpp) in two launches: forward, loss,
+ * Sigmoid with BinaryCrossEntropy and Adam (the reference's quick-start
+ * binary classifier, README.md:102-125) in two launches: forward, loss,
  * backward and per-block partial gradient sums (a block per 16 samples),
  * then the gradients (partials added in block order) stored into gW1, gb1,
  * gW2, gb2 (overwritten: the step's own gradients), the loss into *loss
