@@ -217,6 +217,21 @@ def test_lstm_persistent_exchange_reuse_is_exact(gpu):
                 assert np.array_equal(x.view(np.uint32), y.view(np.uint32))
 
 
+def test_lstm_persistent_config4_shape_repeats_bit_for_bit(gpu):
+    """At config 4's shape (8 sample tiles of 32 blocks each, W_hh in LDS,
+    the weight gradients accumulated in the backward) three runs of the
+    persistent forward and backward give the same bits: every exchanged
+    value is taken with its own step's stamp, and every sum has a fixed
+    order."""
+    env = {"CNHIP_RECURRENCE_PERSISTENT": "1", "CNHIP_RECURRENCE_FUSED_DW": "1", "CNHIP_RECURRENCE_FUSED_X": "1"}
+    print("[lstm-persist] config 4 shape, 3 runs", flush=True)
+    runs = [_lstm_run(128, 64, 128, 512, 11, env) for _ in range(3)]
+    names = ["Y", "gates", "c", "tanh_c", "grad_W_ih", "grad_W_hh", "grad_b", "dX"]
+    for other in runs[1:]:
+        for x, y, name in zip(runs[0], other, names):
+            assert np.array_equal(x.view(np.uint32), y.view(np.uint32)), f"{name} differs between runs"
+
+
 @pytest.mark.parametrize("B,S,I,H,path", [(32, 7, 64, 64, "persistent"), (128, 64, 128, 512, "persistent"),
                                           (48, 9, 24, 128, "persistent"), (32, 7, 64, 64, "persistent-unfused"),
                                           (40, 6, 12, 71, "per-step")])
