@@ -7,8 +7,9 @@
 // src[idx[b]*F + f].  One block moves a 64-sample x 64-value tile through
 // LDS: reads are whole contiguous sample segments (float4 where F and the
 // pointer allow), writes are 64 consecutive b of one f (256-byte rows), so
-// both sides coalesce whatever order the indices come in.  An index outside
-// [0, N) reads nothing and yields zeros.  HBM-bound: the
+// both sides coalesce whatever order the indices come in (small batches take
+// gather_small_kernel below).  An index outside [0, N) reads nothing and
+// yields zeros.  HBM-bound: the
 // algorithmic traffic is 2*B*F*4 bytes (+ 4*B for the indices).
 #include <hip/hip_runtime.h>
 
@@ -87,6 +88,30 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(const float* __restric
   }
 }
 
+// Small batches (B (F0 + F1) <= kSmallGather values, e.g. 512 samples of 31):
+// a thread per output value, consecutive threads on consecutive samples of
+// one value, so the stores coalesce; each thread loads its sample's index and
+// then the value.  Two dependent loads instead of the tile kernel's staged
+// passes; the same values land in the same places.
+constexpr int64_t kSmallGather = 65536;
+
+__global__ __launch_bounds__(256) void gather_small_kernel(const float* __restrict__ src0,
+                                                           float* __restrict__ dst0, int64_t F0,
+                                                           const float* __restrict__ src1,
+                                                           float* __restrict__ dst1, int64_t F1,
+                                                           const int32_t* __restrict__ idx, int64_t N,
+                                                           int64_t B) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= B * (F0 + F1)) return;
+  const int64_t f = e / B, b = e - f * B;
+  const int64_t n = idx[b];
+  const bool ok = n >= 0 && n < N;
+  if (f < F0)
+    dst0[b + B * f] = ok ? src0[n * F0 + f] : 0.f;
+  else
+    dst1[b + B * (f - F0)] = ok ? src1[n * F1 + (f - F0)] : 0.f;
+}
+
 }  // namespace
 }  // namespace cnhip
 
@@ -106,6 +131,11 @@ static int gather_launch(const char* who, const float* src0, float* dst0, int64_
                 (long long)B, (long long)(F0 + F1));
   cnhip::HbmTimer timer("gather_rows_kernel", 8.0 * (double)B * (double)(F0 + F1) + 4.0 * (double)B,
                         as_stream(s));
+  if (B * (F0 + F1) <= cnhip::kSmallGather) {
+    hipLaunchKernelGGL(cnhip::gather_small_kernel, dim3((unsigned)((B * (F0 + F1) + 255) / 256)), dim3(256), 0,
+                       as_stream(s), src0, dst0, F0, src1, dst1, F1, idx, N, B);
+    return cnhip::check_launch(who);
+  }
   hipLaunchKernelGGL(cnhip::gather_rows_kernel, dim3((unsigned)(ty0 + ty1), (unsigned)gx), dim3(256), 0,
                      as_stream(s), src0, dst0, F0, src1, dst1, F1, (int)ty0, idx, N, B);
   return cnhip::check_launch(who);
