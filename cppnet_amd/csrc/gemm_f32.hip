@@ -880,6 +880,39 @@ int gemm_f32_core(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, flo
 // epilogue) of the first, then of the second.
 #define CNHIP_PAIR_CODE(a1, b1, f1, a2, b2, f2) ((a1) << 5 | (b1) << 4 | (f1) << 3 | (a2) << 2 | (b2) << 1 | (f2))
 
+// x (an input gradient, NT) and y (a TN weight gradient) that both plan to
+// the 256 x 256 tile without split-K, in one launch of tiles_x + tiles_y
+// blocks: each CU runs one such block at a time, so the launch is the two
+// GEMMs' rounds back to back, and a CU whose block of x has finished starts
+// a block of y while the others still store x's tiles (as separate launches,
+// every CU waits for the last tile of x and for the end-of-kernel writeback).
+// Each block computes exactly as in its own launch.
+static int pair_xx(const GemmSpec& x, const GemmSpec& y, const Plan& px, const Plan& py, bool fx, hipStream_t st,
+            const char* who, const ColsumJob* cs) {
+  using C = CfgXX;
+  const void* kern = nullptr;
+  if (x.trans_a == 0 && x.trans_b == 1 && y.trans_a == 1 && y.trans_b == 0)
+    kern = fx ? (const void*)&gemm_pair_kernel<false, true, true, true, false, false, C>
+              : (const void*)&gemm_pair_kernel<false, true, false, true, false, false, C>;
+  if (!kern) {
+    CNHIP_TRY(gemm_spec(x, st, who));
+    return gemm_spec(y, st, who, cs);
+  }
+  GemmArgs gx = args_of(x, px), gy = args_of(y, py);
+  const int64_t nx = px.tiles * x.batches, ny = py.tiles * y.batches;
+  TimingRec* rec = timing_slot(2.0 * (double)x.M * (double)x.N * (double)x.K * (double)x.batches +
+                               2.0 * (double)y.M * (double)y.N * (double)y.K * (double)y.batches);
+  if (rec) (void)hipEventRecord(rec->start, st);
+  const int n1 = (int)nx, t1 = (int)px.tiles, b1 = (int)x.batches, t2 = (int)py.tiles, b2 = (int)y.batches;
+  void* kargs[] = {&gx, &gy, const_cast<int*>(&n1), const_cast<int*>(&t1), const_cast<int*>(&b1),
+                   const_cast<int*>(&t2), const_cast<int*>(&b2)};
+  int status = check_hip(hipLaunchKernel(kern, dim3((unsigned)(nx + ny)), dim3(C::NT), kargs, 0, st), who);
+  if (status == CNHIP_OK) status = check_launch(who);
+  if (rec) (void)hipEventRecord(rec->stop, st);
+  if (status != CNHIP_OK) return status;
+  return cs ? column_sum(cs->in, cs->out, cs->rows, cs->cols, cs->accumulate, st, who) : CNHIP_OK;
+}
+
 // x and y in one launch when both take the 128 x 128 tile, x does not split
 // K, and together they fit the chip's 512 block slots at once (y's split
 // count is lowered to fit, never raised); otherwise one after the other.
@@ -905,6 +938,9 @@ int gemm_f32_pair(const GemmSpec& x, const GemmSpec& y, hipStream_t st, const ch
   if (!big(x) || !big(y)) return apart();
   const Plan px = plan_gemm(x.trans_a, x.trans_b, x.M, x.N, x.K, x.batches, 64);
   Plan py = plan_gemm(y.trans_a, y.trans_b, y.M, y.N, y.K, y.batches, 64);
+  const bool fx = !x.trans_a && x.epilogue >= EPI_GELU;
+  if (px.shape == Shape::XX && py.shape == Shape::XX && px.splits == 1 && py.splits == 1)
+    return pair_xx(x, y, px, py, fx, st, who, sums ? &cs : nullptr);
   if (px.shape != Shape::M || py.shape != Shape::M || px.splits != 1) return apart();
   constexpr int64_t kSlots = 512;  // 2 blocks of 512 threads per CU, 256 CUs
   const int64_t nx = px.tiles * x.batches, ty = py.tiles * y.batches;
@@ -916,7 +952,7 @@ int gemm_f32_pair(const GemmSpec& x, const GemmSpec& y, hipStream_t st, const ch
     py.kps = kps;
     py.splits = (int)((y.K + kps - 1) / kps);
   }
-  const bool fx = !x.trans_a && x.epilogue >= EPI_GELU, fy = !y.trans_a && y.epilogue >= EPI_GELU;
+  const bool fy = !y.trans_a && y.epilogue >= EPI_GELU;
   const int code = CNHIP_PAIR_CODE(x.trans_a, x.trans_b, fx ? 1 : 0, y.trans_a, y.trans_b, fy && py.splits == 1 ? 1 : 0);
   using C = CfgM;
   const void* kern = nullptr;

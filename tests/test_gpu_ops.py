@@ -361,6 +361,42 @@ def test_linear_fused_activation_matches_unfused(gpu, oracle, act, B, I, O):
     assert ok, msg
 
 
+@pytest.mark.parametrize("act,accumulate", [("none", False), ("none", True), ("relu", False)])
+# (4096, 4096, 4096): config 2's hidden layer, 256 + 256 blocks;
+# (2048, 8192, 4096): 256 blocks of dX, then 512 of dW
+@pytest.mark.parametrize("B,I,O", [(4096, 4096, 4096), (2048, 8192, 4096)])
+def test_linear_backward_paired_256_tiles_match_separate_launches(gpu, act, accumulate, B, I, O):
+    """Where dX and dW both plan to the 256 x 256 tile without split-K, the
+    backward runs them in one launch.  Each block computes as in its own
+    launch, so dX (with the ReLU mask), dW (also accumulated) and db equal
+    separate cnhip_gemm_f32 launches and the column sum bit for bit."""
+    print(f"[linear-pair-256] {act} acc={accumulate} B={B} I={I} O={O}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(B + I + O + (7 if accumulate else 0))
+    X = torch.randn(B * I, device="cuda", generator=g)
+    W = torch.randn(I * O, device="cuda", generator=g) / np.sqrt(I)
+    dY = torch.randn(B * O, device="cuda", generator=g)
+    aux = torch.relu(torch.randn(B * I, device="cuda", generator=g))
+    gW0 = torch.randn(I * O, device="cuda", generator=g) * 1e-3
+    gb0 = torch.randn(O, device="cuda", generator=g) * 1e-3
+    gW, gb, dX = gW0.clone(), gb0.clone(), torch.empty(B * I, device="cuda")
+    if act == "none":
+        ops.linear_backward(X, W, dY, gW, gb, dX, B, I, O, True, accumulate)
+    else:
+        ops.linear_backward_act(X, W, dY, gW, gb, dX, aux, B, I, O, act)
+    dXs, gWs, gbs = torch.empty(B * I, device="cuda"), gW0.clone(), gb0.clone()
+    ops.gemm(False, True, B, I, O, dY, B, W, I, dXs, B)
+    ops.gemm(True, False, I, O, B, X, B, dY, B, gWs, I, beta=1.0 if accumulate else 0.0)
+    ops.column_sum(dY, gbs, B, O, accumulate)
+    if act == "relu":
+        dZ = torch.empty(B * I, device="cuda")
+        ops.relu_backward(aux, dXs, dZ)
+        dXs = dZ
+    torch.cuda.synchronize()
+    assert torch.equal(dX, dXs), "dX"
+    assert torch.equal(gW, gWs), "grad_W"
+    assert torch.equal(gb, gbs), "grad_b"
+
+
 @pytest.mark.parametrize("act", ["relu", "gelu", "residual"])
 @pytest.mark.parametrize("B,I,O", [(4096, 1024, 10), (8192, 512, 1), (2048, 2048, 16)])
 def test_linear_backward_one_pass_variants_vs_oracle(gpu, oracle, act, B, I, O):
