@@ -121,6 +121,7 @@ SIGNATURES: dict[str, tuple] = {
     "cnhip_bce_backward": (i32, [vp, vp, vp, i64, i32, vp]),
     "cnhip_mse_forward": (i32, [vp, vp, vp, i64, i32, vp]),
     "cnhip_mse_backward": (i32, [vp, vp, vp, i64, i32, vp]),
+    "cnhip_mse_head": (i32, [vp, vp, vp, vp, i64, i32, i32, vp]),
     "cnhip_softmax_ce_forward": (i32, [vp, vp, vp, vp, i64, i64, i32, vp]),
     "cnhip_softmax_ce_backward": (i32, [vp, vp, vp, i64, i64, i32, vp]),
     "cnhip_adam_step": (i32, [vp, vp, vp, vp, i64, f32, f32, f32, f32, f32, f32, vp]),

@@ -208,6 +208,24 @@ __global__ void __launch_bounds__(RB) mse_forward_kernel(const float* __restrict
   if (threadIdx.x == 0) *loss = (reduction == CNHIP_REDUCE_MEAN) ? tot / (float)n : tot;
 }
 
+// MSE forward and backward in one single-block launch for small outputs:
+// the loss's per-thread partial sums over the same elements as
+// mse_forward_kernel and each gradient element as mse_backward_kernel forms
+// it, so loss and gradient are bit-identical to the two launches.
+__global__ void __launch_bounds__(RB) mse_head_kernel(const float* __restrict__ p, const float* __restrict__ t,
+                                                      float* __restrict__ loss, float* __restrict__ g, int64_t n,
+                                                      int loss_reduction, float grad_scale) {
+  __shared__ float smem[RB / 64];
+  float s = 0.f;
+  for (int64_t i = threadIdx.x; i < n; i += RB) {
+    const float d = p[i] - t[i];
+    s += d * d;
+    g[i] = grad_scale * d;
+  }
+  const float tot = block_sum(s, smem);
+  if (threadIdx.x == 0) *loss = (loss_reduction == CNHIP_REDUCE_MEAN) ? tot / (float)n : tot;
+}
+
 __global__ void __launch_bounds__(256) mse_backward_kernel(const float* __restrict__ p,
                                                            const float* __restrict__ t,
                                                            float* __restrict__ g, int64_t n,
@@ -490,6 +508,20 @@ int cnhip_mse_forward(const float* pred, const float* target, float* loss, int64
   cnhip::HbmTimer timer("mse_forward_kernel", 8.0 * (double)n + 4.0, as_stream(s));
   hipLaunchKernelGGL(cnhip::mse_forward_kernel, dim3(1), dim3(cnhip::RB), 0, as_stream(s), pred,
                      target, loss, n, reduction);
+  return cnhip::check_launch(who);
+}
+
+int cnhip_mse_head(const float* pred, const float* target, float* loss, float* grad, int64_t n,
+                   int loss_reduction, int grad_reduction, cnhip_stream_t s) {
+  const char* who = "cnhip_mse_head";
+  CNHIP_TRY(cnhip::check_reduction(loss_reduction, who));
+  CNHIP_TRY(cnhip::check_reduction(grad_reduction, who));
+  CNHIP_REQUIRE(n > 0, "%s: empty input", who);
+  CNHIP_REQUIRE(pred && target && loss && grad, "%s: NULL pointer", who);
+  const float scale = (grad_reduction == CNHIP_REDUCE_MEAN) ? 2.0f / (float)n : 2.0f;
+  cnhip::HbmTimer timer("mse_head_kernel", 12.0 * (double)n + 4.0, as_stream(s));
+  hipLaunchKernelGGL(cnhip::mse_head_kernel, dim3(1), dim3(cnhip::RB), 0, as_stream(s), pred, target, loss, grad,
+                     n, loss_reduction, scale);
   return cnhip::check_launch(who);
 }
 

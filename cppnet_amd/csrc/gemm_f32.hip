@@ -371,8 +371,8 @@ __device__ __forceinline__ float op_b(const GemmArgs& g, int64_t k, int64_t n) {
 // outputs of row m = 0 also sum their op(B) column: the bias gradient in the
 // same launch.
 template <bool TA, bool TB>
-__global__ void __launch_bounds__(256) gemm_small_thread_kernel(GemmArgs g) {
-  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+__device__ __forceinline__ void small_thread_block(const GemmArgs& g, int64_t bid) {
+  const int64_t e = bid * 256 + threadIdx.x;
   if (e >= g.M * g.N) return;
   const int64_t m = e % g.M, n = e / g.M;
   const bool cs = g.colsum && m == 0;
@@ -389,8 +389,13 @@ __global__ void __launch_bounds__(256) gemm_small_thread_kernel(GemmArgs g) {
 }
 
 template <bool TA, bool TB>
-__global__ void __launch_bounds__(256) gemm_small_wave_kernel(GemmArgs g) {
-  const int64_t e = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+__global__ void __launch_bounds__(256) gemm_small_thread_kernel(GemmArgs g) {
+  small_thread_block<TA, TB>(g, blockIdx.x);
+}
+
+template <bool TA, bool TB>
+__device__ __forceinline__ void small_wave_block(const GemmArgs& g, int64_t bid) {
+  const int64_t e = bid * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (e >= g.M * g.N) return;  // uniform per wave
   const int64_t m = e % g.M, n = e / g.M;
@@ -411,6 +416,26 @@ __global__ void __launch_bounds__(256) gemm_small_wave_kernel(GemmArgs g) {
   if (lane == 0) {
     g.C[m + g.ldc * n] = epilogue_value<true>(g, g.C, acc, m, n);
     if (cs) g.colsum[n] = g.colsum_acc ? g.colsum[n] + sum : sum;
+  }
+}
+
+template <bool TA, bool TB>
+__global__ void __launch_bounds__(256) gemm_small_wave_kernel(GemmArgs g) {
+  small_wave_block<TA, TB>(g, blockIdx.x);
+}
+
+// A small Linear layer's weight gradient (with its bias sums) and input
+// gradient in one launch: blocks [0, n1) are the first's, the rest the
+// second's, each block computing exactly as in its own launch.
+template <bool W1, bool W2>
+__global__ void __launch_bounds__(256) gemm_small_pair_kernel(GemmArgs g1, GemmArgs g2, int64_t n1) {
+  const int64_t b = blockIdx.x;
+  if (b < n1) {
+    if (W1) small_wave_block<true, false>(g1, b);
+    else small_thread_block<true, false>(g1, b);
+  } else {
+    if (W2) small_wave_block<false, true>(g2, b - n1);
+    else small_thread_block<false, true>(g2, b - n1);
   }
 }
 
@@ -1002,6 +1027,50 @@ int linear_wgrad_small(const float* X, const float* dY, float* dW, float* db, in
   return gemm_small(1, 0, in_features, out_features, batch, 1.f, X, batch, dY, batch,
                     accumulate ? 1.f : 0.f, dW, in_features, nullptr, CNHIP_EPI_NONE, nullptr, nullptr, 0,
                     st, who, db, accumulate);
+}
+
+// A Linear layer's weight gradient with its bias sums and its input gradient
+// in one launch when both are small GEMMs (a small head: config 4's 512 -> 1
+// over 128 samples): the same kernels' blocks as linear_wgrad_small's launch
+// followed by the dX launch, so the same bits.
+int linear_backward_small_pair(const float* X, const float* W, const float* dY, float* dW, float* db, float* dX,
+                               int64_t batch, int64_t in_features, int64_t out_features, int accumulate,
+                               hipStream_t st, const char* who, bool* done) {
+  *done = false;
+  if (batch <= 0 || !dX || !gemm_is_small(in_features, out_features, batch, 1, 1, 0) ||
+      !gemm_is_small(batch, in_features, out_features, 1, 0, 1))
+    return CNHIP_OK;
+  CNHIP_REQUIRE(X && W && dY && dW, "%s: NULL pointer", who);
+  *done = true;
+  auto args = [](int64_t M, int64_t N, int64_t K, const float* A, int64_t lda, const float* B, int64_t ldb,
+                 float beta, float* C, int64_t ldc, float* colsum, int colsum_acc) {
+    GemmArgs g{};
+    g.colsum = colsum;
+    g.colsum_acc = colsum_acc;
+    g.M = M; g.N = N; g.K = K;
+    g.A = A; g.lda = lda; g.B = B; g.ldb = ldb;
+    g.C = C; g.ldc = ldc;
+    g.alpha = 1.f; g.beta = beta; g.bias = nullptr; g.epilogue = CNHIP_EPI_NONE;
+    g.splits = 1;
+    return g;
+  };
+  // dW[I,O] (+)= X^T dY with db (+)= the column sums of dY; dX[B,I] = dY W^T
+  const GemmArgs gw = args(in_features, out_features, batch, X, batch, dY, batch, accumulate ? 1.f : 0.f, dW,
+                           in_features, db, accumulate);
+  const GemmArgs gx = args(batch, in_features, out_features, dY, batch, W, in_features, 0.f, dX, batch, nullptr, 0);
+  const bool w1 = batch > 64, w2 = out_features > 64;  // as gemm_small chooses
+  const int64_t o1 = in_features * out_features, o2 = batch * in_features;
+  const int64_t n1 = w1 ? (o1 + 3) / 4 : (o1 + 255) / 256, n2 = w2 ? (o2 + 3) / 4 : (o2 + 255) / 256;
+  HbmTimer timer("gemm_small_kernel",
+                 4.0 * ((double)in_features * batch + (double)batch * out_features + (double)o1) +
+                     4.0 * ((double)batch * out_features + (double)out_features * in_features + (double)o2),
+                 st);
+  const dim3 grid((unsigned)(n1 + n2));
+  if (w1 && w2) hipLaunchKernelGGL((gemm_small_pair_kernel<true, true>), grid, dim3(256), 0, st, gw, gx, n1);
+  else if (w1) hipLaunchKernelGGL((gemm_small_pair_kernel<true, false>), grid, dim3(256), 0, st, gw, gx, n1);
+  else if (w2) hipLaunchKernelGGL((gemm_small_pair_kernel<false, true>), grid, dim3(256), 0, st, gw, gx, n1);
+  else hipLaunchKernelGGL((gemm_small_pair_kernel<false, false>), grid, dim3(256), 0, st, gw, gx, n1);
+  return check_launch(who);
 }
 
 int gemm_f32_act(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, const float* A,

@@ -135,6 +135,24 @@ namespace CppNet
             return g;
         }
 
+        DeviceScalar MSE::forward_backward(const DeviceTensor& p, const DeviceTensor& t, DeviceTensor& grad)
+        {
+            require_same_shape(p, t, "MSE::forward_backward");
+            if (static_cast<int64_t>(p.size()) > (int64_t{1} << 16))
+            {
+                DeviceScalar loss = forward(p, t);
+                grad = backward(p, t);
+                return loss;
+            }
+            const int red = reduction_ == "mean" ? CNHIP_REDUCE_MEAN : CNHIP_REDUCE_SUM;
+            if (!grad.defined() || grad.dims() != p.dims()) grad = DeviceTensor::empty(p.dims());
+            DeviceTensor loss = DeviceTensor::empty({1});
+            Device::check(cnhip_mse_head(p.data(), t.data(), loss.data(), grad.data(), static_cast<int64_t>(p.size()),
+                                         red, red, Device::stream()),
+                          "MSE::forward_backward");
+            return DeviceScalar(loss);
+        }
+
         // ---------------------------------------------------------------- SoftmaxCE
         SoftmaxCrossEntropy::SoftmaxCrossEntropy(const std::string& reduction, const std::string& device)
             : reduction_(reduction), device_(device)

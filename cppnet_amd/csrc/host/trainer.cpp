@@ -762,6 +762,8 @@ namespace
             DeviceTensor g;
             if (auto* sce = dynamic_cast<Losses::SoftmaxCrossEntropy*>(s->loss.get()))
                 s->last_loss = sce->forward_backward(out, s->Y, g);
+            else if (auto* mse = dynamic_cast<Losses::MSE*>(s->loss.get()))
+                s->last_loss = mse->forward_backward(out, s->Y, g);
             else
             {
                 s->last_loss = s->loss->forward(out, s->Y);
@@ -796,6 +798,8 @@ namespace
         DeviceTensor g;
         if (auto* sce = dynamic_cast<Losses::SoftmaxCrossEntropy*>(s->loss.get()))
             s->last_loss = sce->forward_backward(out, s->Y, g);  // one launch for small batches
+        else if (auto* mse = dynamic_cast<Losses::MSE*>(s->loss.get()))
+            s->last_loss = mse->forward_backward(out, s->Y, g);  // one launch for small outputs
         else
         {
             s->last_loss = s->loss->forward(out, s->Y);

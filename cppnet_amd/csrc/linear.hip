@@ -21,6 +21,9 @@ int linear_wgrad_small(const float* X, const float* dY, float* dW, float* db, in
 int gemm_f32(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float alpha,
              const float* A, int64_t lda, const float* B, int64_t ldb, float beta, float* C,
              int64_t ldc, const float* bias, int epilogue, hipStream_t st, const char* who);
+int linear_backward_small_pair(const float* X, const float* W, const float* dY, float* dW, float* db, float* dX,
+                               int64_t batch, int64_t in_features, int64_t out_features, int accumulate,
+                               hipStream_t st, const char* who, bool* done);
 int gemm_f32_act(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, const float* A,
                  int64_t lda, const float* B, int64_t ldb, float* C, int64_t ldc, const float* bias,
                  int epilogue, const float* aux_in, float* aux_out, int64_t ld_aux, hipStream_t st,
@@ -491,6 +494,11 @@ int cnhip_linear_backward(const float* X, const float* W, const float* dY, float
     CNHIP_TRY(cnhip::linear_backward_skinny(X, W, dY, grad_W, grad_b, dX, nullptr, batch, in_features,
                                             out_features, accumulate, 0, st, who, &one_pass));
     if (one_pass) return CNHIP_OK;
+    // dW, db and dX in one launch when both products are small
+    bool paired = false;
+    CNHIP_TRY(cnhip::linear_backward_small_pair(X, W, dY, grad_W, grad_b, dX, batch, in_features, out_features,
+                                                accumulate, st, who, &paired));
+    if (paired) return CNHIP_OK;
     // dW[I,O] (+)= X^T[I,B] * dY[B,O]; db (+)= the column sums of dY (one
     // launch for both when the GEMM is small enough for the SIMT kernels)
     bool fused = false;

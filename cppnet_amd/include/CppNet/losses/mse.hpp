@@ -23,6 +23,11 @@ namespace CppNet
             using Loss::backward;
             DeviceScalar forward(const DeviceTensor& predictions, const DeviceTensor& targets) override;
             DeviceTensor backward(const DeviceTensor& predictions, const DeviceTensor& targets) override;
+            /// forward() then backward() in one call: one launch for outputs of
+            /// up to 64 Ki elements, with the same loss and gradient bits as
+            /// the two calls.
+            DeviceScalar forward_backward(const DeviceTensor& predictions, const DeviceTensor& targets,
+                                          DeviceTensor& grad);
             static void set_num_threads(int) {}
 
         private:

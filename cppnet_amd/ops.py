@@ -342,6 +342,12 @@ def mse_backward(pred, target, grad, reduction="mean") -> None:
                _red(reduction), _stream())
 
 
+def mse_head(pred, target, loss, grad, reduction="mean") -> None:
+    """mse_forward and mse_backward in one launch (the same bits)."""
+    _capi.call("cnhip_mse_head", _p(pred), _p(target), _p(loss), _p(grad), pred.numel(),
+               _red(reduction), _red(reduction), _stream())
+
+
 def softmax_ce_forward(logits, targets, softmax_out, loss, batch: int, classes: int,
                        reduction="mean") -> None:
     _capi.call("cnhip_softmax_ce_forward", _p(logits), _p(targets), _p(softmax_out), _p(loss),

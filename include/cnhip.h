@@ -574,6 +574,12 @@ int cnhip_mse_forward(const float* pred, const float* target, float* loss,
                       int64_t n, int reduction, cnhip_stream_t stream);
 int cnhip_mse_backward(const float* pred, const float* target, float* grad,
                        int64_t n, int reduction, cnhip_stream_t stream);
+/* MSE forward and backward in one launch: loss (loss_reduction) and grad
+ * (grad_reduction) bit-identical to cnhip_mse_forward + cnhip_mse_backward
+ * (one block: meant for small outputs).
+ * ref: MSE::forward/backward src/CppNet/losses/mse.cpp:102-161 */
+int cnhip_mse_head(const float* pred, const float* target, float* loss, float* grad, int64_t n,
+                   int loss_reduction, int grad_reduction, cnhip_stream_t stream);
 /* SoftmaxCrossEntropy over ColMajor logits/targets [batch, classes].
  * forward writes the row softmax into softmax_out (the reference's
  * softmax_cache_) and the loss; backward: grad = (softmax - t) [/batch].

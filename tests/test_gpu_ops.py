@@ -189,7 +189,7 @@ def test_bce_vs_oracle(gpu, oracle, n, reduction):
     assert ok, msg
 
 
-@pytest.mark.parametrize("n", [1, 128, 9999])
+@pytest.mark.parametrize("n", [1, 128, 9999, 65536])
 @pytest.mark.parametrize("reduction", ["mean", "sum"])
 def test_mse_vs_oracle(gpu, oracle, n, reduction):
     rng = np.random.default_rng(n + 1)
@@ -203,6 +203,10 @@ def test_mse_vs_oracle(gpu, oracle, n, reduction):
     ok, msg = close(host(loss), [oracle.cnref_mse_forward(fp(p), fp(t), n, r)], RTOL, ATOL)
     assert ok, msg
     np.testing.assert_array_equal(host(g), rg)
+    # the one-launch form: the same loss and gradient bits
+    loss2, g2 = torch.empty(1, device="cuda"), torch.empty(n, device="cuda")
+    ops.mse_head(dev(p), dev(t), loss2, g2, reduction)
+    assert torch.equal(loss2, loss) and torch.equal(g2, g)
 
 
 @pytest.mark.parametrize("B,Cc", [(1, 3), (4096, 10), (256, 10), (32, 4), (77, 1)])
@@ -359,6 +363,31 @@ def test_linear_fused_activation_matches_unfused(gpu, oracle, act, B, I, O):
     mag = gemm_mag(oracle, 0, 0, B, O, I, X, B, W, I, B)
     ok, msg = close_mag(host(Y), ry, mag, 1e-4, 1e-5)
     assert ok, msg
+
+
+# (128, 512, 1): config 4's head; the rest cover the thread and wave kernels on each side
+@pytest.mark.parametrize("B,I,O", [(128, 512, 1), (32, 512, 10), (200, 96, 3), (64, 48, 100), (100, 64, 80)])
+@pytest.mark.parametrize("accumulate", [False, True])
+def test_linear_backward_small_pair_matches_separate_launches(gpu, B, I, O, accumulate):
+    """A small Linear's dW (with db) and dX in one launch equal the layer's
+    weight-gradient launch (its backward without dX) followed by a separate
+    dX GEMM, bit for bit."""
+    print(f"[linear-small-pair] acc={accumulate} B={B} I={I} O={O}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(B * 7 + I + O)
+    X = torch.randn(B * I, device="cuda", generator=g)
+    W = torch.randn(I * O, device="cuda", generator=g) / np.sqrt(I)
+    dY = torch.randn(B * O, device="cuda", generator=g)
+    gW0 = torch.randn(I * O, device="cuda", generator=g) * 1e-3
+    gb0 = torch.randn(O, device="cuda", generator=g) * 1e-3
+    gW, gb, dX = gW0.clone(), gb0.clone(), torch.empty(B * I, device="cuda")
+    ops.linear_backward(X, W, dY, gW, gb, dX, B, I, O, True, accumulate)
+    gWs, gbs, dXs = gW0.clone(), gb0.clone(), torch.empty(B * I, device="cuda")
+    ops.linear_backward(X, W, dY, gWs, gbs, None, B, I, O, True, accumulate)
+    ops.gemm(False, True, B, I, O, dY, B, W, I, dXs, B)
+    torch.cuda.synchronize()
+    assert torch.equal(dX, dXs), "dX"
+    assert torch.equal(gW, gWs), "grad_W"
+    assert torch.equal(gb, gbs), "grad_b"
 
 
 @pytest.mark.parametrize("act,accumulate", [("none", False), ("none", True), ("relu", False)])
