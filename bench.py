@@ -129,7 +129,7 @@ CPU_LOOPS_BATCH = {1: 512, 2: 64}
 # reference kernel of known traffic (bench.py --traffic-calibration),
 # averaged over the class's launches of a step; the runs, the factors and the
 # per-kernel tables are in profiles/*_counters.md.
-PMC_TRAFFIC_BYTES = {1: 0.6e6, 2: 471.9e6, 3: 39.3e6, 4: 955.2e6, 5: 170.2e6}
+PMC_TRAFFIC_BYTES = {1: 0.6e6, 2: 471.9e6, 3: 39.3e6, 4: 955.1e6, 5: 170.4e6}
 
 
 def _cpu_model() -> str:
